@@ -1,0 +1,144 @@
+/*
+ * rta.h -- C ABI of the MI355X (gfx950) detector path of Ray Tracing Attention.
+ *
+ * Conventions
+ *   - Every pointer named w/x/y/q/out/... is a DEVICE pointer owned by the caller.
+ *     The library never allocates device memory in these entry points; kernels
+ *     that need scratch take a caller-provided workspace (size from the matching
+ *     *_workspace_bytes query).
+ *   - All calls are stream ordered on `stream` (a hipStream_t; NULL = default
+ *     stream) and return immediately after launching.  Argument errors are
+ *     detected on the host before anything is launched.
+ *   - Return value: RTA_OK (0) or one of the RTA_ERR_* codes below.
+ *   - Quantised matrices are GGUF superblocks, byte for byte, row-major: row r of
+ *     a [rows x cols] matrix occupies cols/256 consecutive superblocks
+ *     (ray_tracing/native/shaders/resident_quant.glsl:28-30,59).
+ *
+ * Each entry point names the reference interface it replaces (paths relative to
+ * the reference repository root).
+ */
+#ifndef RTA_H
+#define RTA_H
+#include <stddef.h>
+#include <stdint.h>
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef void* rta_stream_t; /* hipStream_t */
+
+enum rta_status {
+    RTA_OK = 0,
+    RTA_ERR_NULL = 1,      /* a required pointer is NULL                         */
+    RTA_ERR_SHAPE = 2,     /* a dimension is <= 0 or not a multiple it must be    */
+    RTA_ERR_FORMAT = 3,    /* unsupported format code                             */
+    RTA_ERR_ALIGN = 4,     /* a device pointer is not aligned as required         */
+    RTA_ERR_WORKSPACE = 5, /* workspace missing or smaller than required          */
+    RTA_ERR_LAUNCH = 6,    /* the HIP runtime reported an error at launch         */
+    RTA_ERR_RANGE = 7,     /* an argument is outside the supported range          */
+    RTA_ERR_DEVICE = 8     /* the device error word is non-zero (rta_device_error) */
+};
+
+/* GGUF type codes, as the reference uses them (resident_quant.glsl:6-20). */
+enum rta_format { RTA_F32 = 0, RTA_F16 = 1, RTA_Q4_K = 12, RTA_Q6_K = 14, RTA_BF16 = 30 };
+
+/* Epilogue of a projection: y = W x, or y += W x (the residual add of the O and
+ * down projections, resident_math.comp:70). */
+enum rta_epilogue { RTA_EPI_STORE = 0, RTA_EPI_ACCUMULATE = 1 };
+
+/* Device error bits; same meanings as the reference's control[3] word
+ * (resident_ray.comp:80, resident_math.comp:152, resident_detector_ordered_scores.comp:20). */
+#define RTA_DEVERR_HITS 8u          /* visible history count mismatch          */
+#define RTA_DEVERR_VOCAB 2048u      /* vocabulary coverage != V                */
+#define RTA_DEVERR_DETECTOR 65536u  /* non-finite query / key / score          */
+
+int rta_version(void);
+const char* rta_status_string(int status);
+
+/* Reads (and optionally clears) the device error word of the current device.
+ * Synchronises the device.  Replaces the host readback of control[3]
+ * (optical_resident.cpp:837-838, :945). */
+int rta_device_error(uint32_t* bits, int clear);
+
+/* Bytes per row of a [rows x cols] matrix of format fmt, -1 if invalid. */
+int64_t rta_row_bytes(int fmt, int64_t cols);
+
+/* Dequantise n values (n % 256 == 0 for K-quants) to fp32, bit exact with the
+ * reference decoder.  Replaces ggufValue (resident_quant.glsl:6-20).
+ * Alignment: src 4 bytes (F32, Q4_K) or 2 bytes (F16, BF16, Q6_K); out 4 bytes. */
+int rta_dequant(int fmt, const void* src, int64_t n, float* out, rta_stream_t stream);
+
+/* y[b, r] (=|+=) sum_c W[r, c] x[b, c],  b < batch, r < rows.
+ *   x: [batch, cols] fp32 row-major, y: [batch, rows] fp32.
+ *   K-quants need cols % 256 == 0; W 16-byte aligned (Q4_K) / 4-byte (Q6_K).
+ * Replaces the projection detector, resident_math.comp:39-75 (op 2, indices
+ * 0/1/2/4/6/8) dispatched by Resident::launch, optical_resident.cpp:304-347. */
+int rta_gemv(int fmt, const void* w, int rows, int cols, const float* x, int batch,
+             float* y, int epilogue, rta_stream_t stream);
+
+/* SwiGLU MLP: act = sign(g) sign(u) |g| |u| sigmoid(g) with g = Wg x, u = Wu x
+ * ([batch, inter]); then y (=|+=) Wd act ([batch, hidden]).
+ *   Wg, Wu: [inter, hidden]; Wd: [hidden, inter].
+ * Replaces Resident::executeMLP (optical_resident.cpp:484-491): op 2 index 3
+ * (resident_math.comp:54-58,71) then op 2 index 4 with the residual (:70).
+ * mlpCheck (optical_resident.cpp:922-949) is epilogue STORE (state zeroed). */
+int rta_mlp_swiglu(int fmt_g, const void* wg, int fmt_u, const void* wu,
+                   int fmt_d, const void* wd, int hidden, int inter,
+                   const float* x, int batch, float* act, float* y, int epilogue,
+                   rta_stream_t stream);
+
+/* LM-head vocabulary readout with fused argmax.
+ *   logits[b, v] = sum_k W[v, k] h[b, k]   (fp32, all v < vocab)
+ *   ids[b] = lowest v with logits[b, v] >= M - margin*|M|, M = max_v logits[b, v]
+ *   (fp32, no fma; margin 0 is the reference's exact-tie rule).
+ * Replaces Resident::word (optical_resident.cpp:523-530): ops 11, 24, 16, 17, 23
+ * (resident_math.comp:99-105,117-130,152-153) and the vocabulary ray query
+ * (resident_ray.comp:91-116), which always returned every word. */
+size_t rta_lm_head_workspace_bytes(int vocab, int batch);
+int rta_lm_head(int fmt, const void* w, int vocab, int hidden, const float* h, int batch,
+                float margin, float* logits, uint32_t* ids,
+                void* workspace, size_t workspace_bytes, rta_stream_t stream);
+
+/* Rotary embedding on adjacent pairs, in place: v [rows, heads, hd];
+ * row r is at absolute position positions[r] (device int64).  Pairs p < rotary/2
+ * of each head turn by positions[r] * theta^(-p/(rotary/2)) (phase, sin, cos in
+ * fp64).  Replaces op 3's rotation (resident_math.comp:76-77,
+ * resident_common.glsl:117). */
+int rta_rope(float* v, int rows, int heads, int hd, int rotary, const int64_t* positions,
+             double theta, rta_stream_t stream);
+
+/* History packet size for a compact K/V width kvw = kv_heads * head_dim:
+ * roundup8(ceil(kvw/256) * (144 + 210)) (resident_dimensions.hpp:10). */
+int64_t rta_history_bytes(int kvw);
+
+/* Decode attention over quantised K/V history, one query token per sequence.
+ *   q         [nseq, hq, hd] fp32, already rotated
+ *   packets   history packets (stride rta_history_bytes(hkv*hd), 4-byte aligned);
+ *             field K first (format fmt_k), then field V (fmt_v); Q4_K or Q6_K each.
+ *             The reference layout is fmt_k = Q4_K, fmt_v = Q6_K
+ *             (resident_quant.glsl:123-124).
+ *   slot_base [nseq] int64, ctx_len [nseq] int32 (device): sequence s holds
+ *             positions 0..ctx_len[s]-1 in slots slot_base[s] + p % capacity; its
+ *             query is at t = ctx_len[s]-1 and sees positions t-r, r < min(t+1, capacity).
+ *   n_slots   number of packets in the array; a slot outside [0, n_slots) is not read
+ *             and sets RTA_DEVERR_HITS.
+ *   max_ctx   host upper bound of min(ctx_len[s], capacity) over s (grid sizing).
+ *   gate      [nseq, hq, hd] or NULL: out *= sigmoid(gate).
+ *   out [nseq, hq, hd]; m_out, z_out [nseq, hq]: m = max score, z = sum exp(s - m)
+ *   (the reference reports physical = (m + 20, z)).
+ * hd must be 128 and hq/hkv in {1, 2, 4, 8}.
+ * Replaces Resident::detectHistory (optical_resident.cpp:429-449): history ray
+ * trace op 0 + check op 8 (resident_ray.comp:30-53,80) and the detector op 3
+ * (resident_ray.comp:56-76) / ordered three-pass detector
+ * (resident_detector_ordered_{scores,normalize,value}.comp). */
+size_t rta_decode_attention_workspace_bytes(int nseq, int hq, int hkv, int hd, int max_ctx);
+int rta_decode_attention(const float* q, int nseq, int hq, int hkv, int hd,
+                         const void* packets, int fmt_k, int fmt_v,
+                         const int64_t* slot_base, const int32_t* ctx_len, int64_t capacity,
+                         int64_t n_slots, int max_ctx, const float* gate, float* out, float* m_out, float* z_out,
+                         void* workspace, size_t workspace_bytes, rta_stream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

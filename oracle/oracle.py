@@ -1,0 +1,149 @@
+"""ctypes wrapper of the CPU oracle (oracle/lib/librta_oracle.so).
+
+TEST INFRASTRUCTURE ONLY: imported by tests/, __graft_entry__.smoke() and the
+cpu_baseline leg of bench.py, always as the checker (or the timed CPU baseline),
+never as the product path.
+"""
+import ctypes
+import subprocess
+from pathlib import Path
+
+import numpy as np
+
+HERE = Path(__file__).resolve().parent
+LIB_PATH = HERE / "lib" / "librta_oracle.so"
+
+F32, F16, Q4_K, Q6_K, BF16 = 0, 1, 12, 14, 30
+
+_i, _i64, _f, _d, _p = ctypes.c_int, ctypes.c_int64, ctypes.c_float, ctypes.c_double, ctypes.c_void_p
+_SIG = {
+    "orc_half_to_float": (_f, [ctypes.c_uint16]),
+    "orc_float_to_half": (ctypes.c_uint16, [_f]),
+    "orc_row_bytes": (_i64, [_i, _i64]),
+    "orc_dequant": (_i, [_i, _p, _i64, _p]),
+    "orc_gemv_f64": (_i, [_i, _p, _i, _i, _p, _i, _p]),
+    "orc_gemv_f32": (_i, [_i, _p, _i, _i, _p, _i, _p, _i]),
+    "orc_sigmoid": (_d, [_d]),
+    "orc_mlp_swiglu": (_i, [_i, _p, _i, _p, _i, _p, _i, _i, _p, _i, _p, _p, _p]),
+    "orc_argmax_margin_f32": (ctypes.c_uint32, [_p, _i64, _f]),
+    "orc_argmax_margin_f64": (ctypes.c_uint32, [_p, _i64, _d]),
+    "orc_lm_head": (_i, [_i, _p, _i, _i, _p, _i, _d, _p, _p]),
+    "orc_rope": (None, [_p, _i, _i, _i, _i64, _d]),
+    "orc_history_bytes": (_i64, [_i]),
+    "orc_pack_history": (_i, [_p, _p, _i, _i, _i, _p]),
+    "orc_packet_value": (_f, [_p, _i, _i, _i, _i, _i]),
+    "orc_decode_attention": (_i, [_p, _i, _i, _i, _i, _p, _i, _i, _p, _p, _i64, _p, _p, _p, _p]),
+}
+
+_LIB = None
+
+
+def build():
+    subprocess.run(["make", "-s", "-C", str(HERE)], check=True)
+
+
+def lib():
+    global _LIB
+    if _LIB is None:
+        if not LIB_PATH.is_file():
+            build()
+        l = ctypes.CDLL(str(LIB_PATH))
+        for name, (res, args) in _SIG.items():
+            f = getattr(l, name)
+            f.restype, f.argtypes = res, args
+        _LIB = l
+    return _LIB
+
+
+def _p_(a):
+    return None if a is None else a.ctypes.data_as(_p)
+
+
+def _c(a, dtype):
+    return np.ascontiguousarray(a, dtype=dtype)
+
+
+def dequant(fmt, raw, n):
+    raw = _c(raw, np.uint8)
+    out = np.empty(n, dtype=np.float32)
+    rc = lib().orc_dequant(fmt, _p_(raw), n, _p_(out))
+    assert rc == 0, rc
+    return out
+
+
+def gemv_f64(fmt, w, rows, cols, x):
+    w, x = _c(w, np.uint8), _c(x, np.float32).reshape(-1, cols)
+    y = np.empty((x.shape[0], rows), dtype=np.float64)
+    assert lib().orc_gemv_f64(fmt, _p_(w), rows, cols, _p_(x), x.shape[0], _p_(y)) == 0
+    return y
+
+
+def gemv_f32(fmt, w, rows, cols, x, threads=0):
+    w, x = _c(w, np.uint8), _c(x, np.float32).reshape(-1, cols)
+    y = np.empty((x.shape[0], rows), dtype=np.float32)
+    assert lib().orc_gemv_f32(fmt, _p_(w), rows, cols, _p_(x), x.shape[0], _p_(y), threads) == 0
+    return y
+
+
+def mlp_swiglu(fmts, wg, wu, wd, hidden, inter, x, y_in=None):
+    x = _c(x, np.float32).reshape(-1, hidden)
+    b = x.shape[0]
+    act = np.empty((b, inter), dtype=np.float64)
+    y = np.empty((b, hidden), dtype=np.float64)
+    yi = None if y_in is None else _c(y_in, np.float32)
+    rc = lib().orc_mlp_swiglu(fmts[0], _p_(_c(wg, np.uint8)), fmts[1], _p_(_c(wu, np.uint8)), fmts[2],
+                              _p_(_c(wd, np.uint8)), hidden, inter, _p_(x), b, _p_(yi), _p_(act), _p_(y))
+    assert rc == 0, rc
+    return act, y
+
+
+def argmax_margin_f32(logits, margin):
+    logits = _c(logits, np.float32)
+    return int(lib().orc_argmax_margin_f32(_p_(logits), logits.size, margin))
+
+
+def argmax_margin_f64(logits, margin):
+    logits = _c(logits, np.float64)
+    return int(lib().orc_argmax_margin_f64(_p_(logits), logits.size, margin))
+
+
+def lm_head(fmt, w, vocab, hidden, h, margin=1e-4):
+    h = _c(h, np.float32).reshape(-1, hidden)
+    b = h.shape[0]
+    logits = np.empty((b, vocab), dtype=np.float64)
+    ids = np.empty(b, dtype=np.uint32)
+    assert lib().orc_lm_head(fmt, _p_(_c(w, np.uint8)), vocab, hidden, _p_(h), b, margin, _p_(logits), _p_(ids)) == 0
+    return logits, ids
+
+
+def rope(v, t, rotary=None, theta=1e6):
+    v = _c(v, np.float32).copy()
+    heads, hd = v.shape[-2], v.shape[-1]
+    lib().orc_rope(_p_(v), heads, hd, hd if rotary is None else rotary, int(t), theta)
+    return v
+
+
+def history_bytes(kvw):
+    return int(lib().orc_history_bytes(kvw))
+
+
+def pack_history(k, v, fmt_k=Q4_K, fmt_v=Q6_K):
+    k, v = _c(k, np.float32).ravel(), _c(v, np.float32).ravel()
+    kvw = k.size
+    out = np.zeros(history_bytes(kvw), dtype=np.uint8)
+    assert lib().orc_pack_history(_p_(k), _p_(v), kvw, fmt_k, fmt_v, _p_(out)) == 0
+    return out
+
+
+def decode_attention(q, packets, fmt_k, fmt_v, slot_base, ctx_len, capacity, hkv, gate=None):
+    q = _c(q, np.float32)
+    nseq, hq, hd = q.shape
+    out = np.empty((nseq, hq, hd), dtype=np.float64)
+    m = np.empty((nseq, hq), dtype=np.float64)
+    z = np.empty((nseq, hq), dtype=np.float64)
+    g = None if gate is None else _c(gate, np.float32)
+    rc = lib().orc_decode_attention(_p_(q), nseq, hq, hkv, hd, _p_(_c(packets, np.uint8)), fmt_k, fmt_v,
+                                    _p_(_c(slot_base, np.int64)), _p_(_c(ctx_len, np.int32)), int(capacity), _p_(g),
+                                    _p_(out), _p_(m), _p_(z))
+    assert rc == 0, rc
+    return out, m, z

@@ -1,0 +1,411 @@
+/*
+ * rta_oracle.c -- CPU restatement of the Ray Tracing Attention detector path.
+ *
+ * TEST INFRASTRUCTURE ONLY (the checker).  Only tests/, __graft_entry__.smoke()
+ * and bench.py's cpu_baseline leg load this library; the product library never
+ * does.  Compiled with -ffp-contract=off: every dequantised value is formed with
+ * the reference's fp32 op order, (d*sc)*q - (dmin*m), with no fused multiply-add.
+ *
+ * Citations are relative to the reference repository root.
+ */
+#include "rta_oracle.h"
+#include <math.h>
+#include <string.h>
+#include <stdlib.h>
+#ifdef _OPENMP
+#include <omp.h>
+#endif
+
+/* ---- binary16 ----------------------------------------------------------- */
+float orc_half_to_float(uint16_t h) {
+    uint32_t sign = (uint32_t)(h >> 15) & 1u, exp = (h >> 10) & 31u, man = h & 1023u;
+    float mag;
+    if (exp == 0) mag = ldexpf((float)man, -24);                 /* zero / subnormal */
+    else if (exp == 31) mag = man ? NAN : INFINITY;
+    else mag = ldexpf((float)(man | 1024u), (int)exp - 25);
+    return sign ? -mag : mag;
+}
+
+uint16_t orc_float_to_half(float f) {
+    uint32_t x; memcpy(&x, &f, 4);
+    uint32_t sign = (x >> 16) & 0x8000u;
+    uint32_t ax = x & 0x7fffffffu;
+    if (ax >= 0x7f800000u) return (uint16_t)(sign | 0x7c00u | (ax > 0x7f800000u ? 0x200u : 0u));
+    float a; memcpy(&a, &ax, 4);
+    if (a >= 65520.0f) return (uint16_t)(sign | 0x7c00u);        /* rounds to inf */
+    if (a < ldexpf(1.0f, -14)) {                                  /* subnormal range */
+        float s = a * 16777216.0f;                                /* exact: power of two */
+        uint32_t q = (uint32_t)rintf(s);                          /* RNE */
+        return (uint16_t)(sign | q);
+    }
+    int e; float m = frexpf(a, &e);                               /* a = m * 2^e, m in [0.5,1) */
+    float scaled = ldexpf(m, 11);                                 /* [1024, 2048) */
+    uint32_t q = (uint32_t)rintf(scaled);                         /* RNE on 11 bits */
+    int he = e - 1 + 15;
+    if (q == 2048u) { q = 1024u; he += 1; }
+    if (he >= 31) return (uint16_t)(sign | 0x7c00u);
+    return (uint16_t)(sign | ((uint32_t)he << 10) | (q & 1023u));
+}
+
+static float bf16_to_float(uint16_t b) { uint32_t x = (uint32_t)b << 16; float f; memcpy(&f, &x, 4); return f; }
+
+int64_t orc_row_bytes(int fmt, int64_t cols) {
+    switch (fmt) {
+    case ORC_F32: return cols * 4;
+    case ORC_F16: case ORC_BF16: return cols * 2;
+    case ORC_Q4_K: return (cols / 256) * 144;
+    case ORC_Q6_K: return (cols / 256) * 210;
+    default: return -1;
+    }
+}
+
+/* ---- Q4_K: resident_quant.glsl:10-15 (ggufValue type 12) ----------------- */
+static void q4k_scale_min(const uint8_t* s, int g, unsigned* sc, unsigned* m) {
+    /* s = bytes 4..15 of the superblock; resident_quant.glsl:11-12, q4ScaleMin :39-43 */
+    if (g < 4) { *sc = s[g] & 63u; *m = s[g + 4] & 63u; }
+    else {
+        int p = g - 4; unsigned mixed = s[8 + p];
+        *sc = (mixed & 15u) | ((unsigned)(s[p] >> 6) << 4);
+        *m  = (mixed >> 4)  | ((unsigned)(s[4 + p] >> 6) << 4);
+    }
+}
+
+static void dequant_q4k_block(const uint8_t* b, float* out) {
+    float d    = orc_half_to_float((uint16_t)(b[0] | (b[1] << 8)));
+    float dmin = orc_half_to_float((uint16_t)(b[2] | (b[3] << 8)));
+    for (int i = 0; i < 256; ++i) {
+        unsigned sc, m; q4k_scale_min(b + 4, i / 32, &sc, &m);
+        unsigned q = (b[16 + (i / 64) * 32 + i % 32] >> (((i % 64) / 32) * 4)) & 15u;
+        float ds = d * (float)sc;          /* (coefficientHalf(at)*float(sc)) */
+        float dq = ds * (float)q;          /*  ... *float(q) */
+        float dm = dmin * (float)m;        /* coefficientHalf(at+2)*float(minval) */
+        out[i] = dq - dm;
+    }
+}
+
+/* ---- Q6_K: resident_quant.glsl:16-19 (ggufValue type 14) ----------------- */
+static void dequant_q6k_block(const uint8_t* b, float* out) {
+    float d = orc_half_to_float((uint16_t)(b[208] | (b[209] << 8)));
+    for (int i = 0; i < 256; ++i) {
+        int h = i / 128, l = i % 128;
+        unsigned ql = (b[h * 64 + l % 64] >> ((l / 64) * 4)) & 15u;
+        unsigned qh = (b[128 + h * 32 + l % 32] >> ((l / 32) * 2)) & 3u;
+        int sc = (int8_t)b[192 + i / 16];
+        float ds = d * (float)sc;
+        out[i] = ds * (float)((int)(ql | (qh << 4)) - 32);
+    }
+}
+
+int orc_dequant(int fmt, const void* src, int64_t n, float* out) {
+    const uint8_t* p = (const uint8_t*)src;
+    if (!src || !out || n < 0) return 1;
+    switch (fmt) {
+    case ORC_F32: memcpy(out, src, (size_t)n * 4); return 0;
+    case ORC_F16: for (int64_t i = 0; i < n; ++i) out[i] = orc_half_to_float((uint16_t)(p[2*i] | (p[2*i+1] << 8))); return 0;
+    case ORC_BF16: for (int64_t i = 0; i < n; ++i) out[i] = bf16_to_float((uint16_t)(p[2*i] | (p[2*i+1] << 8))); return 0;
+    case ORC_Q4_K: if (n % 256) return 2; for (int64_t b = 0; b < n / 256; ++b) dequant_q4k_block(p + b * 144, out + b * 256); return 0;
+    case ORC_Q6_K: if (n % 256) return 2; for (int64_t b = 0; b < n / 256; ++b) dequant_q6k_block(p + b * 210, out + b * 256); return 0;
+    default: return 3;
+    }
+}
+
+static int valid_shape(int fmt, int rows, int cols) {
+    if (rows <= 0 || cols <= 0) return 0;
+    if ((fmt == ORC_Q4_K || fmt == ORC_Q6_K) && cols % 256) return 0;
+    return orc_row_bytes(fmt, cols) > 0;
+}
+
+/* ---- GEMV (resident_math.comp:39-75 op 2; fp64 closed form verify_rt_mlp.py:84-89) */
+int orc_gemv_f64(int fmt, const void* W, int rows, int cols, const float* x, int batch, double* y) {
+    if (!W || !x || !y || batch <= 0 || !valid_shape(fmt, rows, cols)) return 1;
+    int64_t rb = orc_row_bytes(fmt, cols);
+    #pragma omp parallel
+    {
+        float* w = (float*)malloc((size_t)cols * sizeof(float));
+        #pragma omp for schedule(static)
+        for (int r = 0; r < rows; ++r) {
+            orc_dequant(fmt, (const uint8_t*)W + (int64_t)r * rb, cols, w);
+            for (int b = 0; b < batch; ++b) {
+                double acc = 0.0; const float* xb = x + (int64_t)b * cols;
+                for (int c = 0; c < cols; ++c) acc += (double)w[c] * (double)xb[c];
+                y[(int64_t)b * rows + r] = acc;
+            }
+        }
+        free(w);
+    }
+    return 0;
+}
+
+int orc_gemv_f32(int fmt, const void* W, int rows, int cols, const float* x, int batch, float* y, int threads) {
+    if (!W || !x || !y || batch <= 0 || !valid_shape(fmt, rows, cols)) return 1;
+    int64_t rb = orc_row_bytes(fmt, cols);
+#ifdef _OPENMP
+    if (threads > 0) omp_set_num_threads(threads);
+#else
+    (void)threads;
+#endif
+    #pragma omp parallel
+    {
+        float* w = (float*)malloc((size_t)cols * sizeof(float));
+        #pragma omp for schedule(static)
+        for (int r = 0; r < rows; ++r) {
+            orc_dequant(fmt, (const uint8_t*)W + (int64_t)r * rb, cols, w);
+            for (int b = 0; b < batch; ++b) {
+                float acc = 0.0f; const float* xb = x + (int64_t)b * cols;
+                for (int c = 0; c < cols; ++c) acc += w[c] * xb[c];
+                y[(int64_t)b * rows + r] = acc;
+            }
+        }
+        free(w);
+    }
+    return 0;
+}
+
+/* ---- SwiGLU (resident_math.comp:71; resident_common.glsl:138) ------------- */
+double orc_sigmoid(double v) {
+    if (v >= 0) return 1.0 / (1.0 + exp(-v));
+    double light = exp(v);
+    return light / (1.0 + light);
+}
+
+static double sgn(double v) { return v > 0 ? 1.0 : (v < 0 ? -1.0 : 0.0); }
+
+int orc_mlp_swiglu(int fmt_g, const void* Wg, int fmt_u, const void* Wu, int fmt_d, const void* Wd,
+                   int hidden, int inter, const float* x, int batch, const float* y_in,
+                   double* act, double* y) {
+    if (!act || !y || batch <= 0) return 1;
+    double* g = (double*)malloc(sizeof(double) * (size_t)batch * inter);
+    double* u = (double*)malloc(sizeof(double) * (size_t)batch * inter);
+    float* a32 = (float*)malloc(sizeof(float) * (size_t)batch * inter);
+    double* d = (double*)malloc(sizeof(double) * (size_t)batch * hidden);
+    int rc = orc_gemv_f64(fmt_g, Wg, inter, hidden, x, batch, g);
+    if (!rc) rc = orc_gemv_f64(fmt_u, Wu, inter, hidden, x, batch, u);
+    if (!rc) {
+        for (int64_t i = 0; i < (int64_t)batch * inter; ++i) {
+            double gv = g[i], uv = u[i];
+            act[i] = sgn(gv) * sgn(uv) * (fabs(gv) * fabs(uv) * orc_sigmoid(gv));
+            a32[i] = (float)act[i];
+        }
+        /* The detector stores the activation as fp32 (feedForward buffer) before the
+         * down projection reads it (resident_math.comp:71 then :56). */
+        rc = orc_gemv_f64(fmt_d, Wd, hidden, inter, a32, batch, d);
+    }
+    if (!rc) for (int64_t i = 0; i < (int64_t)batch * hidden; ++i) y[i] = (y_in ? (double)y_in[i] : 0.0) + d[i];
+    free(g); free(u); free(a32); free(d);
+    return rc;
+}
+
+/* ---- argmax with margin (resident_math.comp:125-130 generalised) ---------- */
+uint32_t orc_argmax_margin_f32(const float* logits, int64_t n, float margin) {
+    float M = -INFINITY; int any = 0;
+    for (int64_t i = 0; i < n; ++i) if (logits[i] > M) { M = logits[i]; any = 1; }
+    if (!any) return 0xffffffffu;
+    float mag = fabsf(M);
+    float slack = margin * mag;            /* two separate roundings: no fma */
+    float T = M - slack;
+    for (int64_t i = 0; i < n; ++i) if (logits[i] >= T) return (uint32_t)i;
+    return 0xffffffffu;
+}
+
+uint32_t orc_argmax_margin_f64(const double* logits, int64_t n, double margin) {
+    double M = -INFINITY; int any = 0;
+    for (int64_t i = 0; i < n; ++i) if (logits[i] > M) { M = logits[i]; any = 1; }
+    if (!any) return 0xffffffffu;
+    double T = M - margin * fabs(M);
+    for (int64_t i = 0; i < n; ++i) if (logits[i] >= T) return (uint32_t)i;
+    return 0xffffffffu;
+}
+
+int orc_lm_head(int fmt, const void* W, int vocab, int hidden, const float* h, int batch, double margin,
+                double* logits, uint32_t* ids) {
+    int rc = orc_gemv_f64(fmt, W, vocab, hidden, h, batch, logits);
+    if (rc) return rc;
+    for (int b = 0; b < batch; ++b) ids[b] = orc_argmax_margin_f64(logits + (int64_t)b * vocab, vocab, margin);
+    return 0;
+}
+
+/* ---- RoPE (resident_math.comp:76-77; resident_common.glsl:117,79) --------- */
+void orc_rope(float* v, int heads, int hd, int rotary, int64_t t, double theta) {
+    int active = rotary / 2;
+    for (int h = 0; h < heads; ++h)
+        for (int p = 0; p < hd / 2; ++p) {
+            if (p >= active) continue;                    /* phase 0: unchanged */
+            double phase = (double)t * pow(theta, -(double)p / (double)active);
+            double c = cos(phase), s = sin(phase);
+            float* e = v + (int64_t)h * hd + 2 * p;
+            double x = e[0], y = e[1];
+            e[0] = (float)(x * c - y * s);
+            e[1] = (float)(x * s + y * c);
+        }
+}
+
+/* ---- history packets (resident_dimensions.hpp:10; resident_quant.glsl:123-124) */
+int64_t orc_history_bytes(int kvw) {
+    int64_t blocks = (kvw + 255) / 256;
+    return (blocks * (144 + 210) + 7) / 8 * 8;
+}
+
+static int64_t field_offset(int kvw, int fmt_k, int content) {
+    int64_t blocks = (kvw + 255) / 256;
+    return content ? blocks * (fmt_k == ORC_Q4_K ? 144 : 210) : 0;
+}
+
+static void decode_field(const uint8_t* packet, int kvw, int fmt_k, int fmt_v, int content, float* out) {
+    int fmt = content ? fmt_v : fmt_k;
+    int bb = fmt == ORC_Q4_K ? 144 : 210;
+    int64_t blocks = (kvw + 255) / 256;
+    const uint8_t* base = packet + field_offset(kvw, fmt_k, content);
+    for (int64_t b = 0; b < blocks; ++b) {
+        if (fmt == ORC_Q4_K) dequant_q4k_block(base + b * bb, out + b * 256);
+        else dequant_q6k_block(base + b * bb, out + b * 256);
+    }
+}
+
+float orc_packet_value(const uint8_t* packet, int kvw, int fmt_k, int fmt_v, int content, int c) {
+    int fmt = content ? fmt_v : fmt_k;
+    int bb = fmt == ORC_Q4_K ? 144 : 210;
+    const uint8_t* blk = packet + field_offset(kvw, fmt_k, content) + (int64_t)(c / 256) * bb;
+    float vals[256];
+    if (fmt == ORC_Q4_K) dequant_q4k_block(blk, vals); else dequant_q6k_block(blk, vals);
+    return vals[c % 256];
+}
+
+static float halfround(float v) { return orc_half_to_float(orc_float_to_half(v)); }
+
+/* fp32 round-half-to-even clamp used for codes (GLSL round(); .5 ties are
+ * implementation-defined there -- parity for exact ties is unpinned). */
+static float clampf(float v, float lo, float hi) { return v < lo ? lo : (v > hi ? hi : v); }
+
+/* Q4_K field of 256 coordinates, min/max groups of 32 (resident_history_quant.glsl:14-16,
+ * 21-23, 27-29, 31-33, 36). */
+static void pack_q4k_field(const float* x, uint8_t* blk) {
+    float gscale[8], gmin[8]; unsigned sc[8], mn[8];
+    memset(blk, 0, 144);
+    for (int g = 0; g < 8; ++g) {
+        float lo = 0.0f, hi = 0.0f;
+        for (int i = 0; i < 32; ++i) { float v = x[g * 32 + i]; lo = fminf(lo, v); hi = fmaxf(hi, v); }
+        float span = hi - lo;
+        gscale[g] = span / 15.0f; gmin[g] = -lo;
+    }
+    float maxD = 0.0f, maxMin = 0.0f;
+    for (int g = 0; g < 8; ++g) { maxD = fmaxf(maxD, gscale[g]); maxMin = fmaxf(maxMin, gmin[g]); }
+    float d = halfround(maxD / 63.0f), dm = halfround(maxMin / 63.0f);
+    uint16_t hd = orc_float_to_half(d), hm = orc_float_to_half(dm);
+    blk[0] = hd & 255; blk[1] = hd >> 8; blk[2] = hm & 255; blk[3] = hm >> 8;
+    for (int g = 0; g < 8; ++g) {
+        sc[g] = (unsigned)clampf(rintf(gscale[g] / fmaxf(d, 1e-30f)), 0.0f, 63.0f);
+        mn[g] = (unsigned)clampf(rintf(gmin[g] / fmaxf(dm, 1e-30f)), 0.0f, 63.0f);
+    }
+    for (int g = 0; g < 4; ++g) {
+        blk[4 + g]  = (uint8_t)(sc[g] | ((sc[g + 4] >> 4) << 6));
+        blk[8 + g]  = (uint8_t)(mn[g] | ((mn[g + 4] >> 4) << 6));
+        blk[12 + g] = (uint8_t)((sc[g + 4] & 15u) | ((mn[g + 4] & 15u) << 4));
+    }
+    for (int i = 0; i < 256; ++i) {
+        int g = i / 32;
+        float num = x[i] + dm * (float)mn[g];
+        float den = fmaxf(d * (float)sc[g], 1e-30f);
+        unsigned q = (unsigned)clampf(rintf(num / den), 0.0f, 15.0f);
+        blk[16 + (i / 64) * 32 + i % 32] |= (uint8_t)(q << (((i % 64) / 32) * 4));
+    }
+}
+
+/* Q6_K field of 256 coordinates, abs-max groups of 16 (resident_history_quant.glsl:15-16,
+ * 21-22, 27-28, 37-38). */
+static void pack_q6k_field(const float* x, uint8_t* blk) {
+    float gscale[16]; unsigned sc[16];
+    memset(blk, 0, 210);
+    for (int g = 0; g < 16; ++g) {
+        float hi = 0.0f;
+        for (int i = 0; i < 16; ++i) hi = fmaxf(hi, fabsf(x[g * 16 + i]));
+        gscale[g] = hi / 31.0f;
+    }
+    float maxD = 0.0f;
+    for (int g = 0; g < 16; ++g) maxD = fmaxf(maxD, gscale[g]);
+    float d = halfround(maxD / 127.0f);
+    uint16_t hd = orc_float_to_half(d);
+    blk[208] = hd & 255; blk[209] = hd >> 8;
+    for (int g = 0; g < 16; ++g) {
+        sc[g] = (unsigned)clampf(rintf(gscale[g] / fmaxf(d, 1e-30f)), 0.0f, 127.0f);
+        blk[192 + g] = (uint8_t)sc[g];
+    }
+    for (int i = 0; i < 256; ++i) {
+        float den = fmaxf(d * (float)sc[i / 16], 1e-30f);
+        unsigned q = (unsigned)((int)clampf(rintf(x[i] / den), -32.0f, 31.0f) + 32);
+        int part = i / 128, within = i % 128;
+        blk[part * 64 + within % 64] |= (uint8_t)((q & 15u) << ((within / 64) * 4));
+        blk[128 + part * 32 + within % 32] |= (uint8_t)((q >> 4) << ((within / 32) * 2));
+    }
+}
+
+int orc_pack_history(const float* k, const float* v, int kvw, int fmt_k, int fmt_v, uint8_t* packet) {
+    if (!k || !v || !packet || kvw <= 0) return 1;
+    if ((fmt_k != ORC_Q4_K && fmt_k != ORC_Q6_K) || (fmt_v != ORC_Q4_K && fmt_v != ORC_Q6_K)) return 3;
+    int64_t blocks = (kvw + 255) / 256, bytes = orc_history_bytes(kvw);
+    memset(packet, 0, (size_t)bytes);
+    float tmp[256];
+    for (int content = 0; content < 2; ++content) {
+        const float* src = content ? v : k;
+        int fmt = content ? fmt_v : fmt_k;
+        int bb = fmt == ORC_Q4_K ? 144 : 210;
+        uint8_t* base = packet + field_offset(kvw, fmt_k, content);
+        for (int64_t b = 0; b < blocks; ++b) {
+            for (int i = 0; i < 256; ++i) { int64_t c = b * 256 + i; tmp[i] = c < kvw ? src[c] : 0.0f; }
+            if (fmt == ORC_Q4_K) pack_q4k_field(tmp, base + b * bb); else pack_q6k_field(tmp, base + b * bb);
+        }
+    }
+    return 0;
+}
+
+/* ---- decode attention (resident_ray.comp:30-53,56-76; verify_attention_receipts.py:84-114) */
+int orc_decode_attention(const float* q, int nseq, int hq, int hkv, int hd,
+                         const uint8_t* packets, int fmt_k, int fmt_v,
+                         const int64_t* slot_base, const int32_t* ctx_len,
+                         int64_t capacity, const float* gate,
+                         double* out, double* m, double* z) {
+    if (!q || !packets || !slot_base || !ctx_len || !out || !m || !z) return 1;
+    if (nseq <= 0 || hq <= 0 || hkv <= 0 || hd <= 0 || hq % hkv || capacity <= 0) return 2;
+    int kvw = hkv * hd, group = hq / hkv;
+    int64_t stride = orc_history_bytes(kvw);
+    double inv = 1.0 / sqrt((double)hd);
+    #pragma omp parallel for collapse(2) schedule(dynamic)
+    for (int s = 0; s < nseq; ++s)
+        for (int h = 0; h < hq; ++h) {
+            int64_t t = (int64_t)ctx_len[s] - 1;
+            int64_t visible = t + 1 < capacity ? t + 1 : capacity;
+            int kvh = h / group;                              /* resident_common.glsl:109 */
+            const float* qh = q + ((int64_t)s * hq + h) * hd;
+            double* o = out + ((int64_t)s * hq + h) * hd;
+            double* scores = (double*)malloc(sizeof(double) * (size_t)(visible > 0 ? visible : 1));
+            int64_t padded = (kvw + 255) / 256 * 256;
+            float* field = (float*)malloc(sizeof(float) * (size_t)padded);
+            double mx = -INFINITY;
+            for (int64_t r = 0; r < visible; ++r) {
+                int64_t p = t - r;
+                const uint8_t* pk = packets + (slot_base[s] + p % capacity) * stride;
+                decode_field(pk, kvw, fmt_k, fmt_v, 0, field);
+                double acc = 0.0;
+                for (int c = 0; c < hd; ++c) acc += (double)qh[c] * (double)field[kvh * hd + c];
+                scores[r] = acc * inv;
+                if (scores[r] > mx) mx = scores[r];
+            }
+            double zz = 0.0;
+            for (int c = 0; c < hd; ++c) o[c] = 0.0;
+            for (int64_t r = 0; r < visible; ++r) {
+                int64_t p = t - r;
+                const uint8_t* pk = packets + (slot_base[s] + p % capacity) * stride;
+                double w = exp(scores[r] - mx);
+                zz += w;
+                decode_field(pk, kvw, fmt_k, fmt_v, 1, field);
+                for (int c = 0; c < hd; ++c) o[c] += w * (double)field[kvh * hd + c];
+            }
+            for (int c = 0; c < hd; ++c) {
+                double g = gate ? orc_sigmoid((double)gate[((int64_t)s * hq + h) * hd + c]) : 1.0;
+                o[c] = o[c] / (zz > 1e-30 ? zz : 1e-30) * g;
+            }
+            m[(int64_t)s * hq + h] = mx;
+            z[(int64_t)s * hq + h] = zz;
+            free(scores); free(field);
+        }
+    return 0;
+}

@@ -1,0 +1,109 @@
+/*
+ * rta_oracle.h -- CPU restatement of the Ray Tracing Attention detector path.
+ *
+ * TEST INFRASTRUCTURE ONLY.  This library is the checker: only tests/,
+ * __graft_entry__.smoke() and bench.py's cpu_baseline leg may load it.  The
+ * product path (librta.so) never links, loads or calls it.
+ *
+ * Every function cites the reference file:line it restates (paths relative to
+ * the reference repository root).  Built with -ffp-contract=off so that the
+ * dequantisation op order is exactly the reference's fp32 order.
+ */
+#ifndef RTA_ORACLE_H
+#define RTA_ORACLE_H
+#include <stdint.h>
+#include <stddef.h>
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* GGUF type codes used by the reference (resident_quant.glsl:6-20). */
+enum { ORC_F32 = 0, ORC_F16 = 1, ORC_Q4_K = 12, ORC_Q6_K = 14, ORC_BF16 = 30 };
+
+/* IEEE binary16 <-> binary32 (unpackHalf2x16 / packHalf2x16 semantics). */
+float    orc_half_to_float(uint16_t h);
+uint16_t orc_float_to_half(float f);           /* round to nearest even */
+
+/* Bytes per row of a [rows x cols] matrix in format fmt (cols % 256 == 0 for K-quants). */
+int64_t  orc_row_bytes(int fmt, int64_t cols);
+
+/* Dequantise n values (n % 256 == 0 for K-quants) -- bit exact fp32.
+ * ray_tracing/native/shaders/resident_quant.glsl:6-20 (ggufValue). */
+int orc_dequant(int fmt, const void* src, int64_t n, float* out);
+
+/* y[b*rows + r] = sum_c W[r,c] * x[b*cols + c]; W dequantised bit-exactly to fp32,
+ * products and sums in fp64 (verification/verify_rt_mlp.py:84-89 closed form). */
+int orc_gemv_f64(int fmt, const void* W, int rows, int cols,
+                 const float* x, int batch, double* y);
+
+/* Same contraction, fp32 accumulation, OpenMP over rows: the timed CPU baseline
+ * (dequant + dot as resident_math.comp:39-75 does per output channel). */
+int orc_gemv_f32(int fmt, const void* W, int rows, int cols,
+                 const float* x, int batch, float* y, int threads);
+
+/* Stable sigmoid, resident_common.glsl:138 (detectorSigmoid), in fp64. */
+double orc_sigmoid(double v);
+
+/* SwiGLU MLP, resident_math.comp:54-58,70-71 + optical_resident.cpp:484-491:
+ *   a = sign(g) sign(u) |g| |u| sigmoid(g)   (g = Wg x, u = Wu x)
+ *   y = y_in + Wd a                         (y_in may be NULL: mlpCheck zeroes state)
+ * act: [batch, inter], y: [batch, hidden]; fp64 throughout. */
+int orc_mlp_swiglu(int fmt_g, const void* Wg, int fmt_u, const void* Wu,
+                   int fmt_d, const void* Wd, int hidden, int inter,
+                   const float* x, int batch, const float* y_in,
+                   double* act, double* y);
+
+/* Argmax with the relative-margin tie rule: M = max finite logit,
+ * T = M - margin*|M|, id = lowest v with logit[v] >= T.  margin = 0 is the
+ * reference's exact rule (resident_math.comp:125-130: strict > , equal -> lower id).
+ * The f32 variant evaluates T in fp32 with two roundings (no fma). */
+uint32_t orc_argmax_margin_f32(const float* logits, int64_t n, float margin);
+uint32_t orc_argmax_margin_f64(const double* logits, int64_t n, double margin);
+
+/* LM head readout (resident_math.comp:117-130, ops 16/17/23): fp64 logits
+ * [batch, vocab] and ids [batch] under the margin rule. */
+int orc_lm_head(int fmt, const void* W, int vocab, int hidden,
+                const float* h, int batch, double margin,
+                double* logits, uint32_t* ids);
+
+/* RoPE on adjacent pairs (resident_math.comp:76-77, resident_common.glsl:117):
+ * pair p of each head, local = p < rotary/2 ? p : none;
+ * phase = t * theta^(-local/(rotary/2)); (x,y) -> (x cos - y sin, x sin + y cos).
+ * Phase, sin and cos in fp64; result rounded to fp32.  v: [heads, hd] in place. */
+void orc_rope(float* v, int heads, int hd, int rotary, int64_t t, double theta);
+
+/* History packet geometry (resident_dimensions.hpp:10, spec.py:45):
+ * bytes = roundup8(ceil(kvw/256) * (144 + 210)).  K blocks first, then V blocks. */
+int64_t orc_history_bytes(int kvw);
+
+/* Pack one token's compact K and V rows (kvw floats each) into a packet,
+ * restating resident_history_quant.glsl:9-41 (reference format: K Q4_K, V Q6_K).
+ * fmt_k/fmt_v choose the per-field format (Q4_K or Q6_K); for Q4_K the
+ * min/max group scheme and for Q6_K the abs-max scheme of that file apply. */
+int orc_pack_history(const float* k, const float* v, int kvw, int fmt_k, int fmt_v,
+                     uint8_t* packet);
+
+/* Decode coordinate c (0..kvw) of field K (content=0) or V (content=1) of a
+ * packet (resident_quant.glsl:123-124, quantizedPath). */
+float orc_packet_value(const uint8_t* packet, int kvw, int fmt_k, int fmt_v,
+                       int content, int c);
+
+/* Decode attention over quantised history for one query token per sequence
+ * (resident_ray.comp:56-76 detector; verify_attention_receipts.py:84-114 dense oracle).
+ *   q        [nseq, hq, hd] (already rotated)
+ *   packets  base of the packet array, stride orc_history_bytes(hkv*hd)
+ *   slot_base[s], ctx_len[s]: sequence s holds absolute positions 0..ctx_len-1 in
+ *            ring slots slot_base + p % capacity; the query sits at t = ctx_len-1 and
+ *            sees positions t-r, r < min(t+1, capacity) (resident_ray.comp:30-53).
+ *   gate     [nseq, hq, hd] or NULL; out *= sigmoid(gate) (resident_ray.comp:75-76)
+ * Outputs fp64: out [nseq, hq, hd], m [nseq, hq] (running max), z [nseq, hq]. */
+int orc_decode_attention(const float* q, int nseq, int hq, int hkv, int hd,
+                         const uint8_t* packets, int fmt_k, int fmt_v,
+                         const int64_t* slot_base, const int32_t* ctx_len,
+                         int64_t capacity, const float* gate,
+                         double* out, double* m, double* z);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,87 @@
+// rta_common.hpp -- device helpers shared by the gfx950 kernels.
+//
+// Quantised formats follow the reference decoder byte for byte
+// (ray_tracing/native/shaders/resident_quant.glsl:6-20):
+//   Q4_K superblock (144 B): d f16 | dmin f16 | 12 scale bytes | 128 nibble bytes
+//   Q6_K superblock (210 B): 128 ql | 64 qh | 16 int8 scales | d f16
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "../../include/rta.h"
+
+namespace rta {
+
+constexpr int kWave = 64;
+
+// Sticky device error word; bits as RTA_DEVERR_* (the reference's control[3]).
+extern __device__ uint32_t g_error_word;
+
+__device__ __forceinline__ void raise_error(uint32_t bit) { atomicOr(&g_error_word, bit); }
+
+// IEEE binary16 -> binary32 for the low / high half of a dword (exact).
+__device__ __forceinline__ float half_lo(uint32_t w) {
+    return (float)__builtin_bit_cast(_Float16, (uint16_t)(w & 0xffffu));
+}
+__device__ __forceinline__ float half_hi(uint32_t w) {
+    return (float)__builtin_bit_cast(_Float16, (uint16_t)(w >> 16));
+}
+
+typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
+
+// Reinterprets a dword whose halves hold small integer codes c (bits 0..9) as two
+// binary16 subnormals c * 2^-24.  Converting such a half to fp32 is exact, so
+// fmaf((float)h.x, x, acc) accumulates c * x * 2^-24 with one v_fma_mix_f32.
+__device__ __forceinline__ half2_t as_codes(uint32_t w) { return __builtin_bit_cast(half2_t, w); }
+
+// (hi:lo) >> (8 * shift) -- extracts a dword that starts `shift` bytes into lo.
+__device__ __forceinline__ uint32_t funnel(uint32_t lo, uint32_t hi, uint32_t shift) {
+    return __builtin_amdgcn_alignbyte(hi, lo, shift);
+}
+
+// Butterfly sum over lanes whose index differs only in the bits below `width`
+// (a power of two <= 64).  Every lane of the group ends with the group sum.
+__device__ __forceinline__ float group_sum(float v, int width) {
+    for (int off = width >> 1; off > 0; off >>= 1) v += __shfl_xor(v, off, kWave);
+    return v;
+}
+
+__device__ __forceinline__ float group_max(float v, int width) {
+    for (int off = width >> 1; off > 0; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, kWave));
+    return v;
+}
+
+// Q4_K 6-bit scale/min codes of group g (0..7) from the scale dwords
+// s0 = bytes 4..7, s1 = bytes 8..11, s2 = bytes 12..15 of the superblock
+// (resident_quant.glsl:11-12, q4ScaleMin :39-43).
+__device__ __forceinline__ void q4k_scale_min(uint32_t s0, uint32_t s1, uint32_t s2, int g,
+                                              uint32_t& sc, uint32_t& m) {
+    const uint32_t sh = 8u * (uint32_t)(g & 3);
+    const uint32_t a = (s0 >> sh) & 255u, b = (s1 >> sh) & 255u;
+    if (g < 4) {
+        sc = a & 63u;
+        m = b & 63u;
+    } else {
+        const uint32_t mixed = (s2 >> sh) & 255u;
+        sc = (mixed & 15u) | ((a >> 6) << 4);
+        m = (mixed >> 4) | ((b >> 6) << 4);
+    }
+}
+
+// Stable logistic of resident_common.glsl:138 (detectorSigmoid).
+__device__ __forceinline__ float detector_sigmoid(float v) {
+    if (v >= 0.0f) return 1.0f / (1.0f + expf(-v));
+    const float light = expf(v);
+    return light / (1.0f + light);
+}
+
+__device__ __forceinline__ float signf(float v) { return v > 0.0f ? 1.0f : (v < 0.0f ? -1.0f : 0.0f); }
+
+// sign(g) sign(u) |g| |u| sigmoid(g): the fused gate/up detector of
+// resident_math.comp:71 (equal to SiLU(g) * u).
+__device__ __forceinline__ float swiglu(float g, float u) {
+    const float amplitude = fabsf(g) * fabsf(u) * detector_sigmoid(g);
+    return signf(g) * signf(u) * amplitude;
+}
+
+}  // namespace rta

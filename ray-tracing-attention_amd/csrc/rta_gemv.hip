@@ -1,0 +1,335 @@
+// rta_gemv.hip -- C ABI for dequantisation, projections, the SwiGLU MLP and the
+// LM-head readout with fused margin argmax (gfx950).
+#include <math.h>
+
+#include "rta_gemv.hpp"
+#include "rta_host.hpp"
+
+namespace rta {
+
+__device__ uint32_t g_error_word = 0;
+
+// ---------------------------------------------------------------- dequant ----
+// One thread per value, the reference's per-value decoder with its fp32 op order
+// (resident_quant.glsl:6-20): contraction is disabled so that (d*sc)*q - dmin*m is
+// rounded exactly as the reference rounds it.
+__global__ void __launch_bounds__(256) dequant_kernel(int fmt, const uint8_t* __restrict__ src, int64_t n,
+                                                      float* __restrict__ out) {
+#pragma clang fp contract(off)
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n) return;
+    float v;
+    if (fmt == RTA_F32) {
+        v = reinterpret_cast<const float*>(src)[i];
+    } else if (fmt == RTA_F16) {
+        v = (float)reinterpret_cast<const _Float16*>(src)[i];
+    } else if (fmt == RTA_BF16) {
+        v = __builtin_bit_cast(float, (uint32_t)reinterpret_cast<const uint16_t*>(src)[i] << 16);
+    } else if (fmt == RTA_Q4_K) {
+        const uint8_t* b = src + (i >> 8) * 144;
+        const int idx = (int)(i & 255), g = idx >> 5;
+        const float d = (float)*reinterpret_cast<const _Float16*>(b);
+        const float dmin = (float)*reinterpret_cast<const _Float16*>(b + 2);
+        uint32_t sc, m;
+        const uint32_t* s = reinterpret_cast<const uint32_t*>(b + 4);
+        q4k_scale_min(s[0], s[1], s[2], g, sc, m);
+        const uint32_t q = (b[16 + (idx >> 6) * 32 + (idx & 31)] >> (((idx & 63) >> 5) * 4)) & 15u;
+        const float ds = d * (float)sc;
+        const float dq = ds * (float)q;
+        const float dm = dmin * (float)m;
+        v = dq - dm;
+    } else {  // Q6_K
+        const uint8_t* b = src + (i >> 8) * 210;
+        const int idx = (int)(i & 255), h = idx >> 7, l = idx & 127;
+        const uint32_t ql = (b[h * 64 + (l & 63)] >> ((l >> 6) * 4)) & 15u;
+        const uint32_t qh = (b[128 + h * 32 + (l & 31)] >> ((l >> 5) * 2)) & 3u;
+        const int sc = (int8_t)b[192 + (idx >> 4)];
+        const float d = (float)__builtin_bit_cast(_Float16, (uint16_t)(b[208] | (b[209] << 8)));
+        const float ds = d * (float)sc;
+        v = ds * (float)((int)(ql | (qh << 4)) - 32);
+    }
+    out[i] = v;
+}
+
+// ------------------------------------------------------------------ argmax ----
+// Phase two of the readout: M = max of the per-task maxima (exact logit values),
+// T = M - margin*|M| evaluated in fp32 without contraction, id = lowest v with
+// logit >= T.  Only tasks whose maximum reaches T are scanned.  Generalises the
+// reference's reduction (resident_math.comp:124-130: strict >, ties -> lower id).
+__global__ void __launch_bounds__(1024) argmax_margin_kernel(const float* __restrict__ logits, int vocab,
+                                                             const float* __restrict__ partial, int ntasks,
+                                                             int rows_per_task, float margin,
+                                                             uint32_t* __restrict__ ids) {
+#pragma clang fp contract(off)
+    __shared__ float red_f[32];
+    __shared__ uint32_t red_u[32];
+    const int b = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const float* pb = partial + (int64_t)b * ntasks;
+    const float* lb = logits + (int64_t)b * vocab;
+    float m = -INFINITY;
+    for (int t = tid; t < ntasks; t += blockDim.x) m = fmaxf(m, pb[t]);
+    m = group_max(m, kWave);
+    if (lane == 0) red_f[wave] = m;
+    __syncthreads();
+    if (tid < 64) {
+        float v = tid < (int)(blockDim.x >> 6) ? red_f[tid] : -INFINITY;
+        v = group_max(v, kWave);
+        if (tid == 0) red_f[0] = v;
+    }
+    __syncthreads();
+    const float M = red_f[0];
+    __syncthreads();
+    uint32_t best = 0xffffffffu;
+    if (M > -INFINITY) {
+        const float mag = fabsf(M);
+        const float slack = margin * mag;
+        const float T = M - slack;
+        for (int t = tid; t < ntasks; t += blockDim.x) {
+            if (!(pb[t] >= T)) continue;
+            const int r0 = t * rows_per_task, r1 = min(r0 + rows_per_task, vocab);
+            for (int r = r0; r < r1; ++r)
+                if (lb[r] >= T) { best = min(best, (uint32_t)r); break; }
+        }
+    }
+    for (int off = 32; off > 0; off >>= 1) best = min(best, (uint32_t)__shfl_xor((int)best, off, kWave));
+    if (lane == 0) red_u[wave] = best;
+    __syncthreads();
+    if (tid == 0) {
+        uint32_t v = 0xffffffffu;
+        for (int w = 0; w < (int)(blockDim.x >> 6); ++w) v = min(v, red_u[w]);
+        ids[b] = v;
+    }
+}
+
+// ----------------------------------------------------------- launch plumbing ----
+static int pow2ceil(int v) {
+    int p = 1;
+    while (p < v) p <<= 1;
+    return p;
+}
+
+struct Plan {
+    int nb, r, lpr, ntasks, grid;
+};
+
+// Chooses the batch tile NB and row passes R for a K-quant launch.
+static Plan plan_kquant(int rows, int cols, int batch, bool dual) {
+    Plan p;
+    p.nb = batch <= 1 ? 1 : batch <= 2 ? 2 : batch <= 4 ? 4 : 8;
+    p.r = p.nb >= 8 ? 2 : 4;
+    if (dual) p.r = p.r / 2 > 0 ? p.r / 2 : 1;
+    const int S = cols / 64;
+    p.lpr = S >= kWave ? kWave : pow2ceil(S);
+    const int rows_per_task = (kWave / p.lpr) * p.r;
+    p.ntasks = (rows + rows_per_task - 1) / rows_per_task;
+    const int wgs = (p.ntasks + 3) / 4;
+    p.grid = wgs < 2048 ? wgs : 2048;
+    return p;
+}
+
+template <int FMT, int MODE>
+static hipError_t launch_kquant_nb(int nb, const GemvArgs& a, int grid, hipStream_t s, bool dual_r) {
+    (void)dual_r;
+    switch (nb) {
+    case 1: hipLaunchKernelGGL((gemv_kquant_kernel<FMT, 1, MODE == kSwiglu ? 2 : 4, MODE>), dim3(grid), dim3(256), 0, s, a); break;
+    case 2: hipLaunchKernelGGL((gemv_kquant_kernel<FMT, 2, MODE == kSwiglu ? 2 : 4, MODE>), dim3(grid), dim3(256), 0, s, a); break;
+    case 4: hipLaunchKernelGGL((gemv_kquant_kernel<FMT, 4, MODE == kSwiglu ? 2 : 4, MODE>), dim3(grid), dim3(256), 0, s, a); break;
+    default: hipLaunchKernelGGL((gemv_kquant_kernel<FMT, 8, MODE == kSwiglu ? 1 : 2, MODE>), dim3(grid), dim3(256), 0, s, a); break;
+    }
+    return hipGetLastError();
+}
+
+template <int MODE>
+static hipError_t launch_kquant(int fmt, int nb, const GemvArgs& a, int grid, hipStream_t s) {
+    if (fmt == RTA_Q4_K) return launch_kquant_nb<RTA_Q4_K, MODE>(nb, a, grid, s, false);
+    return launch_kquant_nb<RTA_Q6_K, MODE>(nb, a, grid, s, false);
+}
+
+template <int MODE>
+static hipError_t launch_plain(int fmt, const GemvArgs& a, int grid, hipStream_t s) {
+    if (fmt == RTA_F32) hipLaunchKernelGGL((gemv_plain_kernel<RTA_F32, MODE>), dim3(grid), dim3(256), 0, s, a);
+    else if (fmt == RTA_F16) hipLaunchKernelGGL((gemv_plain_kernel<RTA_F16, MODE>), dim3(grid), dim3(256), 0, s, a);
+    else hipLaunchKernelGGL((gemv_plain_kernel<RTA_BF16, MODE>), dim3(grid), dim3(256), 0, s, a);
+    return hipGetLastError();
+}
+
+static bool is_kquant(int fmt) { return fmt == RTA_Q4_K || fmt == RTA_Q6_K; }
+
+static int check_matrix(int fmt, const void* w, int rows, int cols) {
+    if (!host::valid_format(fmt)) return RTA_ERR_FORMAT;
+    if (!w) return RTA_ERR_NULL;
+    if (rows <= 0 || cols <= 0) return RTA_ERR_SHAPE;
+    if (is_kquant(fmt) && cols % 256) return RTA_ERR_SHAPE;
+    if (!is_kquant(fmt) && cols % 4) return RTA_ERR_SHAPE;
+    const uintptr_t p = reinterpret_cast<uintptr_t>(w);
+    const uintptr_t need = fmt == RTA_Q4_K ? 16 : fmt == RTA_F32 ? 4 : 2;
+    if (p % need) return RTA_ERR_ALIGN;
+    return RTA_OK;
+}
+
+// Runs one projection over the whole batch, in batch tiles of at most 8 rows.
+template <int MODE>
+static int run_projection(int fmt, const void* w, const void* w2, int rows, int cols, const float* x, int batch,
+                          float* y, float* partial, int* ntasks_out, int* rows_per_task_out, hipStream_t s) {
+    const int64_t row_bytes = host::row_bytes(fmt, cols);
+    int b0 = 0;
+    while (b0 < batch) {
+        const int chunk = batch - b0 < 8 ? batch - b0 : 8;
+        GemvArgs a{};
+        a.w = static_cast<const uint8_t*>(w);
+        a.w2 = static_cast<const uint8_t*>(w2);
+        a.row_bytes = row_bytes;
+        a.rows = rows;
+        a.cols = cols;
+        a.x = x + (int64_t)b0 * cols;
+        a.y = y + (int64_t)b0 * rows;
+        a.batch = chunk;
+        hipError_t e;
+        if (is_kquant(fmt)) {
+            const Plan p = plan_kquant(rows, cols, chunk, MODE == kSwiglu);
+            a.lpr = p.lpr;
+            a.ntasks = p.ntasks;
+            a.partial = partial ? partial + (int64_t)b0 * p.ntasks : nullptr;
+            if (ntasks_out) *ntasks_out = p.ntasks;
+            if (rows_per_task_out) *rows_per_task_out = (kWave / p.lpr) * p.r;
+            e = launch_kquant<MODE>(fmt, p.nb, a, p.grid, s);
+        } else {
+            a.lpr = kWave;
+            a.ntasks = rows;
+            a.partial = partial ? partial + (int64_t)b0 * rows : nullptr;
+            if (ntasks_out) *ntasks_out = rows;
+            if (rows_per_task_out) *rows_per_task_out = 1;
+            const int wgs = (rows + 3) / 4;
+            e = launch_plain<MODE>(fmt, a, wgs < 2048 ? wgs : 2048, s);
+        }
+        if (e != hipSuccess) return RTA_ERR_LAUNCH;
+        b0 += chunk;
+    }
+    return RTA_OK;
+}
+
+}  // namespace rta
+
+using namespace rta;
+
+extern "C" {
+
+int rta_version(void) { return 1; }
+
+const char* rta_status_string(int status) {
+    switch (status) {
+    case RTA_OK: return "ok";
+    case RTA_ERR_NULL: return "null pointer argument";
+    case RTA_ERR_SHAPE: return "invalid shape";
+    case RTA_ERR_FORMAT: return "unsupported format";
+    case RTA_ERR_ALIGN: return "misaligned pointer";
+    case RTA_ERR_WORKSPACE: return "workspace missing or too small";
+    case RTA_ERR_LAUNCH: return "HIP launch error";
+    case RTA_ERR_RANGE: return "argument out of supported range";
+    case RTA_ERR_DEVICE: return "device error word set";
+    default: return "unknown status";
+    }
+}
+
+int rta_device_error(uint32_t* bits, int clear) {
+    if (!bits) return RTA_ERR_NULL;
+    if (hipDeviceSynchronize() != hipSuccess) return RTA_ERR_LAUNCH;
+    uint32_t v = 0;
+    if (hipMemcpyFromSymbol(&v, HIP_SYMBOL(g_error_word), sizeof(v), 0, hipMemcpyDeviceToHost) != hipSuccess)
+        return RTA_ERR_LAUNCH;
+    *bits = v;
+    if (clear) {
+        const uint32_t zero = 0;
+        if (hipMemcpyToSymbol(HIP_SYMBOL(g_error_word), &zero, sizeof(zero), 0, hipMemcpyHostToDevice) != hipSuccess)
+            return RTA_ERR_LAUNCH;
+    }
+    return RTA_OK;
+}
+
+int64_t rta_row_bytes(int fmt, int64_t cols) { return host::row_bytes(fmt, cols); }
+
+int rta_dequant(int fmt, const void* src, int64_t n, float* out, rta_stream_t stream) {
+    if (!host::valid_format(fmt)) return RTA_ERR_FORMAT;
+    if (!src || !out) return RTA_ERR_NULL;
+    if (n < 0 || (is_kquant(fmt) && n % 256)) return RTA_ERR_SHAPE;
+    if (reinterpret_cast<uintptr_t>(src) % (fmt == RTA_F32 || fmt == RTA_Q4_K ? 4 : 2) ||
+        reinterpret_cast<uintptr_t>(out) % 4)
+        return RTA_ERR_ALIGN;
+    if (n == 0) return RTA_OK;
+    const int64_t blocks = (n + 255) / 256;
+    hipLaunchKernelGGL(dequant_kernel, dim3((unsigned)blocks), dim3(256), 0, (hipStream_t)stream, fmt,
+                       static_cast<const uint8_t*>(src), n, out);
+    return hipGetLastError() == hipSuccess ? RTA_OK : RTA_ERR_LAUNCH;
+}
+
+int rta_gemv(int fmt, const void* w, int rows, int cols, const float* x, int batch, float* y, int epilogue,
+             rta_stream_t stream) {
+    int rc = check_matrix(fmt, w, rows, cols);
+    if (rc) return rc;
+    if (!x || !y) return RTA_ERR_NULL;
+    if (batch <= 0) return RTA_ERR_SHAPE;
+    if (epilogue != RTA_EPI_STORE && epilogue != RTA_EPI_ACCUMULATE) return RTA_ERR_RANGE;
+    if (reinterpret_cast<uintptr_t>(x) % 16 || reinterpret_cast<uintptr_t>(y) % 4) return RTA_ERR_ALIGN;
+    hipStream_t s = (hipStream_t)stream;
+    if (epilogue == RTA_EPI_STORE)
+        return run_projection<kStore>(fmt, w, nullptr, rows, cols, x, batch, y, nullptr, nullptr, nullptr, s);
+    return run_projection<kAccumulate>(fmt, w, nullptr, rows, cols, x, batch, y, nullptr, nullptr, nullptr, s);
+}
+
+int rta_mlp_swiglu(int fmt_g, const void* wg, int fmt_u, const void* wu, int fmt_d, const void* wd, int hidden,
+                   int inter, const float* x, int batch, float* act, float* y, int epilogue, rta_stream_t stream) {
+    int rc = check_matrix(fmt_g, wg, inter, hidden);
+    if (rc) return rc;
+    if ((rc = check_matrix(fmt_u, wu, inter, hidden))) return rc;
+    if ((rc = check_matrix(fmt_d, wd, hidden, inter))) return rc;
+    if (fmt_g != fmt_u) return RTA_ERR_FORMAT;  // the fused gate/up pass streams both in one format
+    if (!x || !act || !y) return RTA_ERR_NULL;
+    if (batch <= 0) return RTA_ERR_SHAPE;
+    if (epilogue != RTA_EPI_STORE && epilogue != RTA_EPI_ACCUMULATE) return RTA_ERR_RANGE;
+    if (reinterpret_cast<uintptr_t>(x) % 16 || reinterpret_cast<uintptr_t>(act) % 16 ||
+        reinterpret_cast<uintptr_t>(y) % 4)
+        return RTA_ERR_ALIGN;
+    hipStream_t s = (hipStream_t)stream;
+    rc = run_projection<kSwiglu>(fmt_g, wg, wu, inter, hidden, x, batch, act, nullptr, nullptr, nullptr, s);
+    if (rc) return rc;
+    if (epilogue == RTA_EPI_STORE)
+        return run_projection<kStore>(fmt_d, wd, nullptr, hidden, inter, act, batch, y, nullptr, nullptr, nullptr, s);
+    return run_projection<kAccumulate>(fmt_d, wd, nullptr, hidden, inter, act, batch, y, nullptr, nullptr, nullptr, s);
+}
+
+size_t rta_lm_head_workspace_bytes(int vocab, int batch) {
+    if (vocab <= 0 || batch <= 0) return 0;
+    return (size_t)vocab * (size_t)batch * sizeof(float);
+}
+
+int rta_lm_head(int fmt, const void* w, int vocab, int hidden, const float* h, int batch, float margin, float* logits,
+                uint32_t* ids, void* workspace, size_t workspace_bytes, rta_stream_t stream) {
+    int rc = check_matrix(fmt, w, vocab, hidden);
+    if (rc) return rc;
+    if (!h || !logits || !ids) return RTA_ERR_NULL;
+    if (batch <= 0) return RTA_ERR_SHAPE;
+    if (!(margin >= 0.0f) || !(margin < 1.0f)) return RTA_ERR_RANGE;
+    if (!workspace || workspace_bytes < rta_lm_head_workspace_bytes(vocab, batch)) return RTA_ERR_WORKSPACE;
+    if (reinterpret_cast<uintptr_t>(h) % 16 || reinterpret_cast<uintptr_t>(logits) % 4 ||
+        reinterpret_cast<uintptr_t>(ids) % 4 || reinterpret_cast<uintptr_t>(workspace) % 4)
+        return RTA_ERR_ALIGN;
+    hipStream_t s = (hipStream_t)stream;
+    float* partial = static_cast<float*>(workspace);
+    int ntasks = 0, rpt = 1;
+    // Batch tiles share one ntasks/rows_per_task plan except possibly the last tile;
+    // run the argmax per tile so each uses the plan it was written with.
+    int b0 = 0;
+    while (b0 < batch) {
+        const int chunk = batch - b0 < 8 ? batch - b0 : 8;
+        rc = run_projection<kLogits>(fmt, w, nullptr, vocab, hidden, h + (int64_t)b0 * hidden, chunk,
+                                     logits + (int64_t)b0 * vocab, partial + (int64_t)b0 * vocab, &ntasks, &rpt, s);
+        if (rc) return rc;
+        hipLaunchKernelGGL(argmax_margin_kernel, dim3(chunk), dim3(1024), 0, s, logits + (int64_t)b0 * vocab,
+                           vocab, partial + (int64_t)b0 * vocab, ntasks, rpt, margin, ids + b0);
+        if (hipGetLastError() != hipSuccess) return RTA_ERR_LAUNCH;
+        b0 += chunk;
+    }
+    return RTA_OK;
+}
+
+}  // extern "C"

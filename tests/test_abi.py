@@ -1,0 +1,85 @@
+"""CPU checks of the C ABI: the library loads, exports every symbol the header
+declares, answers the host-only queries, and rejects bad arguments on the host
+(no kernel is launched by any call in this file)."""
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+
+from rta import _lib
+
+HEADER = Path(__file__).resolve().parent.parent / "include" / "rta.h"
+FAKE = ctypes.c_void_p(0x100000)      # never dereferenced: every call below fails validation first
+FAKE_ODD = ctypes.c_void_p(0x100002)
+
+
+@pytest.fixture(scope="module")
+def lib():
+    return _lib.load()
+
+
+def declared():
+    text = HEADER.read_text()
+    body = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(rta_[a-z0-9_]+)\s*\(", body)))
+
+
+def test_every_declared_symbol_is_exported_and_bound(lib):
+    names = declared()
+    assert len(names) >= 13
+    for n in names:
+        assert hasattr(lib, n), n
+        assert n in _lib.SIGNATURES, n
+
+
+def test_host_queries(lib):
+    assert lib.rta_version() >= 1
+    assert lib.rta_status_string(0) == b"ok"
+    assert lib.rta_row_bytes(_lib.Q4_K, 4096) == 16 * 144
+    assert lib.rta_row_bytes(_lib.Q6_K, 2048) == 8 * 210
+    assert lib.rta_row_bytes(_lib.Q4_K, 100) == -1
+    assert lib.rta_row_bytes(_lib.F16, 10) == 20
+    assert lib.rta_history_bytes(512) == 712          # resident_dimensions.hpp:10
+    assert lib.rta_history_bytes(1024) == 1416
+    assert lib.rta_lm_head_workspace_bytes(151936, 4) == 151936 * 4 * 4
+    assert lib.rta_decode_attention_workspace_bytes(16, 16, 4, 128, 32768) == 16 * 4 * 128 * 4 * 130 * 4
+    assert lib.rta_decode_attention_workspace_bytes(16, 16, 4, 64, 32768) == 0
+
+
+def test_argument_errors_are_reported_before_launch(lib):
+    E = {"null": 1, "shape": 2, "format": 3, "align": 4, "ws": 5, "range": 7}
+    assert lib.rta_gemv(99, FAKE, 8, 256, FAKE, 1, FAKE, 0, None) == E["format"]
+    assert lib.rta_gemv(_lib.Q4_K, None, 8, 256, FAKE, 1, FAKE, 0, None) == E["null"]
+    assert lib.rta_gemv(_lib.Q4_K, FAKE, 8, 255, FAKE, 1, FAKE, 0, None) == E["shape"]
+    assert lib.rta_gemv(_lib.Q4_K, FAKE, 0, 256, FAKE, 1, FAKE, 0, None) == E["shape"]
+    assert lib.rta_gemv(_lib.Q4_K, FAKE, 8, 256, FAKE, 0, FAKE, 0, None) == E["shape"]
+    assert lib.rta_gemv(_lib.Q4_K, FAKE_ODD, 8, 256, FAKE, 1, FAKE, 0, None) == E["align"]
+    assert lib.rta_gemv(_lib.Q4_K, FAKE, 8, 256, FAKE_ODD, 1, FAKE, 0, None) == E["align"]
+    assert lib.rta_gemv(_lib.Q4_K, FAKE, 8, 256, FAKE, 1, FAKE, 7, None) == E["range"]
+    assert lib.rta_mlp_swiglu(_lib.Q4_K, FAKE, _lib.Q6_K, FAKE, _lib.Q6_K, FAKE, 256, 512, FAKE, 1, FAKE, FAKE, 0,
+                              None) == E["format"]
+    assert lib.rta_lm_head(_lib.Q6_K, FAKE, 300, 256, FAKE, 1, ctypes.c_float(1e-4), FAKE, FAKE, None, 0,
+                           None) == E["ws"]
+    assert lib.rta_lm_head(_lib.Q6_K, FAKE, 300, 256, FAKE, 1, ctypes.c_float(-1.0), FAKE, FAKE, FAKE, 1 << 20,
+                           None) == E["range"]
+    assert lib.rta_dequant(_lib.Q6_K, FAKE, 100, FAKE, None) == E["shape"]
+    assert lib.rta_rope(FAKE, 1, 1, 7, 7, FAKE, ctypes.c_double(1e6), None) == E["shape"]
+    assert lib.rta_rope(FAKE, 1, 1, 8, 8, FAKE, ctypes.c_double(-1.0), None) == E["range"]
+    args = [FAKE, 1, 16, 4, 64, FAKE, _lib.Q4_K, _lib.Q6_K, FAKE, FAKE, 1024, 4096, 1024, None, FAKE, FAKE, FAKE,
+            FAKE, 1 << 30, None]
+    assert lib.rta_decode_attention(*args) == E["range"]          # hd != 128
+    args[4] = 128
+    args[7] = 13
+    assert lib.rta_decode_attention(*args) == E["format"]
+    args[7] = _lib.Q6_K
+    args[18] = 16
+    assert lib.rta_decode_attention(*args) == E["ws"]
+    args[18] = 1 << 30
+    args[11] = 0
+    assert lib.rta_decode_attention(*args) == E["shape"]           # n_slots <= 0
+
+
+def test_missing_library_fails_loudly(tmp_path):
+    with pytest.raises(FileNotFoundError):
+        _lib.load(tmp_path / "librta.so")

@@ -1,0 +1,294 @@
+"""Pins the CPU oracle before it is trusted as the checker.
+
+Each oracle function is checked against something that does not restate its own
+formula: numpy's IEEE binary16 conversion; the published GGML dequantisation
+algorithm (dequantize_row_q4_K / dequantize_row_q6_K, the algorithm of the
+reference's oracle dependency `gguf`, pyproject.toml:12, gguf>=0.17, absent here)
+written in its own 64-/128-value loop structure; hand-built known-answer blocks;
+numpy float64 matmul; scipy's softmax; complex multiplication for RoPE; and
+algebraic identities (split-K merge, constant values, single position).
+"""
+import numpy as np
+import pytest
+from scipy.special import softmax
+
+import oracle as orc
+from ggml_ref import ggml_q4k, ggml_q6k
+from rta import synth
+
+
+# ---------------------------------------------------------------- binary16 ----
+def test_half_to_float_all_codes():
+    codes = np.arange(65536, dtype=np.uint16)
+    ref = codes.view(np.float16).astype(np.float32)
+    got = np.array([orc.lib().orc_half_to_float(int(c)) for c in codes], dtype=np.float32)
+    nan = np.isnan(ref)
+    assert np.array_equal(np.isnan(got), nan)
+    assert np.array_equal(got[~nan].view(np.uint32), ref[~nan].view(np.uint32))
+
+
+def test_float_to_half_round_nearest_even():
+    rng = np.random.default_rng(1)
+    vals = np.concatenate([
+        rng.standard_normal(20000).astype(np.float32) * 10.0 ** rng.integers(-9, 5, 20000),
+        np.array([0.0, -0.0, 65504.0, 65519.0, 65520.0, 1e-8, 5.96e-8, 2.98e-8, 6.1e-5, np.inf, -np.inf],
+                 dtype=np.float32)]).astype(np.float32)
+    ref = vals.astype(np.float16).view(np.uint16)
+    got = np.array([orc.lib().orc_float_to_half(float(v)) for v in vals], dtype=np.uint16)
+    assert np.array_equal(got, ref)
+
+
+def _bits(a):
+    return np.asarray(a, dtype=np.float32).view(np.uint32)
+
+
+@pytest.mark.parametrize("seed", [0, 1, 2])
+def test_q4k_dequant_matches_ggml_bitwise(seed):
+    raw = synth.random_q4k(np.random.default_rng(seed), 24)
+    got = orc.dequant(orc.Q4_K, raw, 24 * 256)
+    assert np.array_equal(_bits(got), _bits(ggml_q4k(raw)))
+
+
+@pytest.mark.parametrize("seed", [0, 1, 2])
+def test_q6k_dequant_matches_ggml_bitwise(seed):
+    raw = synth.random_q6k(np.random.default_rng(seed), 24)
+    got = orc.dequant(orc.Q6_K, raw, 24 * 256)
+    assert np.array_equal(_bits(got), _bits(ggml_q6k(raw)))
+
+
+def test_q4k_known_answers():
+    n = 1
+    q = (np.arange(256) * 7 % 16).astype(np.uint8)[None]
+    # d = dmin = 0 -> all zeros
+    raw = synth.pack_q4k(np.zeros(n), np.zeros(n), np.full((n, 8), 63), np.full((n, 8), 63), q)
+    assert not orc.dequant(orc.Q4_K, raw, 256).any()
+    # d = 1, sc = 1, m = 0 -> the quant itself
+    raw = synth.pack_q4k(np.ones(n), np.ones(n), np.ones((n, 8)), np.zeros((n, 8)), q)
+    assert np.array_equal(orc.dequant(orc.Q4_K, raw, 256), q[0].astype(np.float32))
+    # every 6-bit code in every group position, across the g<4 / g>=4 packing split
+    for code in range(64):
+        for g in range(8):
+            sc = np.zeros((1, 8), np.uint8)
+            mn = np.zeros((1, 8), np.uint8)
+            sc[0, g] = code
+            mn[0, 7 - g] = 63 - code
+            qq = np.ones((1, 256), np.uint8)
+            raw = synth.pack_q4k(np.ones(1), np.full(1, 0.5), sc, mn, qq)
+            v = orc.dequant(orc.Q4_K, raw, 256).reshape(8, 32)
+            expect = np.array([(code if gg == g else 0) - 0.5 * ((63 - code) if gg == 7 - g else 0)
+                               for gg in range(8)], dtype=np.float32)
+            assert np.array_equal(v, np.repeat(expect[:, None], 32, 1)), (code, g)
+
+
+def test_q6k_known_answers():
+    q = (np.arange(256) % 64).astype(np.uint8)[None]
+    raw = synth.pack_q6k(np.ones(1), np.ones((1, 16), np.int8), q)
+    assert np.array_equal(orc.dequant(orc.Q6_K, raw, 256), q[0].astype(np.float32) - 32)
+    sc = np.arange(-8, 8, dtype=np.int8)[None]  # negative int8 scales
+    raw = synth.pack_q6k(np.full(1, 0.25), sc, q)
+    expect = 0.25 * np.repeat(sc[0].astype(np.float32), 16) * (q[0].astype(np.float32) - 32)
+    assert np.array_equal(orc.dequant(orc.Q6_K, raw, 256), expect.astype(np.float32))
+
+
+def test_plain_formats():
+    rng = np.random.default_rng(3)
+    v = rng.standard_normal(256).astype(np.float32)
+    assert np.array_equal(orc.dequant(orc.F32, v.view(np.uint8), 256), v)
+    h = v.astype(np.float16)
+    assert np.array_equal(orc.dequant(orc.F16, h.view(np.uint8), 256), h.astype(np.float32))
+    bf = (v.view(np.uint32) >> 16).astype(np.uint16)
+    expect = (bf.astype(np.uint32) << 16).view(np.float32)
+    assert np.array_equal(orc.dequant(orc.BF16, bf.view(np.uint8), 256), expect)
+
+
+def test_golden_fixtures():
+    from pathlib import Path
+    g = np.load(Path(__file__).parent / "golden" / "dequant_golden.npz")
+    assert np.array_equal(_bits(orc.dequant(orc.Q4_K, g["q4k_raw"], g["q4k_values"].size)), _bits(g["q4k_values"]))
+    assert np.array_equal(_bits(orc.dequant(orc.Q6_K, g["q6k_raw"], g["q6k_values"].size)), _bits(g["q6k_values"]))
+
+
+# --------------------------------------------------------------------- GEMV ----
+@pytest.mark.parametrize("fmt", [orc.Q4_K, orc.Q6_K])
+def test_gemv_matches_numpy_matmul(fmt):
+    rng = np.random.default_rng(4)
+    rows, cols = 48, 512
+    w = synth.random_matrix(rng, fmt, rows, cols)
+    x = rng.standard_normal((3, cols)).astype(np.float32)
+    dense = orc.dequant(fmt, w, rows * cols).reshape(rows, cols).astype(np.float64)
+    ref = x.astype(np.float64) @ dense.T
+    got = orc.gemv_f64(fmt, w, rows, cols, x)
+    assert np.allclose(got, ref, rtol=1e-12, atol=1e-12)
+    got32 = orc.gemv_f32(fmt, w, rows, cols, x)
+    assert np.allclose(got32, ref, rtol=1e-4, atol=1e-4)
+
+
+def test_gemv_integer_exact():
+    # d = 1, sc = 1, m = 0 and integer x: the contraction is an exact integer
+    rng = np.random.default_rng(5)
+    rows, cols = 8, 256
+    q = rng.integers(0, 16, (rows, 256), dtype=np.uint8)
+    w = synth.pack_q4k(np.ones(rows), np.zeros(rows), np.ones((rows, 8)), np.zeros((rows, 8)), q)
+    x = rng.integers(-5, 6, (1, cols)).astype(np.float32)
+    got = orc.gemv_f64(orc.Q4_K, w, rows, cols, x)
+    assert np.array_equal(got[0], q.astype(np.int64) @ x[0].astype(np.int64))
+
+
+# ---------------------------------------------------------------------- MLP ----
+def test_mlp_closed_form():
+    rng = np.random.default_rng(6)
+    hidden, inter = 256, 512
+    wg = synth.random_matrix(rng, orc.Q4_K, inter, hidden)
+    wu = synth.random_matrix(rng, orc.Q4_K, inter, hidden)
+    wd = synth.random_matrix(rng, orc.Q6_K, hidden, inter)
+    x = rng.standard_normal((4, hidden)).astype(np.float32)
+    x[1] = 0.0                       # zero row (verify_rt_mlp.py:64-67)
+    x[2] = -x[0]
+    act, y = orc.mlp_swiglu((orc.Q4_K, orc.Q4_K, orc.Q6_K), wg, wu, wd, hidden, inter, x)
+    G = orc.dequant(orc.Q4_K, wg, inter * hidden).reshape(inter, hidden).astype(np.float64)
+    U = orc.dequant(orc.Q4_K, wu, inter * hidden).reshape(inter, hidden).astype(np.float64)
+    D = orc.dequant(orc.Q6_K, wd, hidden * inter).reshape(hidden, inter).astype(np.float64)
+    g, u = x @ G.T, x @ U.T
+    silu = g / (1.0 + np.exp(-g))
+    assert np.allclose(act, silu * u, rtol=1e-12, atol=1e-15)
+    assert not act[1].any() and not y[1].any()
+    assert np.allclose(y, act.astype(np.float32).astype(np.float64) @ D.T, rtol=1e-12, atol=1e-12)
+    act1, y1 = orc.mlp_swiglu((orc.Q4_K, orc.Q4_K, orc.Q6_K), wg, wu, wd, hidden, inter, x[:1])
+    assert np.array_equal(act1[0], act[0]) and np.array_equal(y1[0], y[0])   # batch-prefix invariance
+
+
+# ------------------------------------------------------------------- argmax ----
+def test_argmax_margin_rule():
+    a = np.array([1.0, 3.0, 2.0, 3.0], np.float32)
+    assert orc.argmax_margin_f32(a, 0.0) == 1                  # exact tie -> lowest id
+    b = np.array([0.0, 0.99995, 1.0], np.float32)
+    assert orc.argmax_margin_f32(b, 1e-4) == 1                 # within 1e-4 relative
+    assert orc.argmax_margin_f32(b, 0.0) == 2
+    c = np.array([-2.0, -1.00005, -1.0], np.float32)
+    assert orc.argmax_margin_f32(c, 1e-4) == 1                 # |M| for negative maxima
+    d = np.array([np.nan, 5.0, np.nan], np.float32)
+    assert orc.argmax_margin_f32(d, 1e-4) == 1
+    rng = np.random.default_rng(7)
+    for _ in range(50):
+        v = rng.standard_normal(1000).astype(np.float32)
+        assert orc.argmax_margin_f32(v, 0.0) == int(np.argmax(v))
+        assert orc.argmax_margin_f64(v.astype(np.float64), 0.0) == int(np.argmax(v))
+
+
+def test_lm_head_planted_winner():
+    rng = np.random.default_rng(8)
+    vocab, hidden = 300, 256
+    w = synth.random_matrix(rng, orc.Q6_K, vocab, hidden)
+    h = rng.standard_normal((2, hidden)).astype(np.float32)
+    logits, ids = orc.lm_head(orc.Q6_K, w, vocab, hidden, h)
+    dense = orc.dequant(orc.Q6_K, w, vocab * hidden).reshape(vocab, hidden).astype(np.float64)
+    assert np.allclose(logits, h.astype(np.float64) @ dense.T, rtol=1e-12, atol=1e-12)
+    assert list(ids) == [int(np.argmax(l)) for l in logits]
+
+
+# -------------------------------------------------------------------- RoPE ----
+def test_rope_matches_complex_rotation():
+    rng = np.random.default_rng(9)
+    heads, hd, theta = 3, 128, 1e6
+    v = rng.standard_normal((heads, hd)).astype(np.float32)
+    for t in (0, 1, 17, 32767):
+        got = orc.rope(v, t, theta=theta)
+        z = v[:, 0::2].astype(np.float64) + 1j * v[:, 1::2].astype(np.float64)
+        ang = t * theta ** (-np.arange(hd // 2) / (hd // 2))
+        r = z * np.exp(1j * ang)
+        ref = np.stack([r.real, r.imag], -1).reshape(heads, hd).astype(np.float32)
+        assert np.allclose(got, ref, rtol=1e-6, atol=1e-6)
+        if t == 0:
+            assert np.array_equal(got, v)
+    part = orc.rope(v, 5, rotary=64, theta=theta)            # pairs >= rotary/2 untouched
+    assert np.array_equal(part[:, 64:], v[:, 64:])
+
+
+# --------------------------------------------------------------- attention ----
+def _history(rng, n, hkv, hd, fmt_k, fmt_v):
+    return synth.random_packets(rng, n, hkv * hd, fmt_k, fmt_v)
+
+
+def _dense_reference(q, packets, fmt_k, fmt_v, L, hkv, hd):
+    kvw = hkv * hd
+    K = np.stack([[orc.lib().orc_packet_value(p.ctypes.data, kvw, fmt_k, fmt_v, 0, c) for c in range(kvw)]
+                  for p in packets[:L]]).reshape(L, hkv, hd).astype(np.float64)
+    V = np.stack([[orc.lib().orc_packet_value(p.ctypes.data, kvw, fmt_k, fmt_v, 1, c) for c in range(kvw)]
+                  for p in packets[:L]]).reshape(L, hkv, hd).astype(np.float64)
+    hq = q.shape[0]
+    mapping = np.arange(hq) // (hq // hkv)
+    s = np.einsum("hd,nhd->hn", q.astype(np.float64), K[:, mapping]) / np.sqrt(hd)
+    w = softmax(s, axis=1)
+    return np.einsum("hn,nhd->hd", w, V[:, mapping]), s.max(1), np.exp(s - s.max(1, keepdims=True)).sum(1)
+
+
+@pytest.mark.parametrize("fmts", [(orc.Q4_K, orc.Q6_K), (orc.Q6_K, orc.Q4_K)])
+def test_attention_matches_scipy_softmax(fmts):
+    rng = np.random.default_rng(10)
+    hq, hkv, hd, L = 8, 2, 128, 37
+    packets = _history(rng, L, hkv, hd, *fmts)
+    q = rng.standard_normal((1, hq, hd)).astype(np.float32)
+    out, m, z = orc.decode_attention(q, packets, fmts[0], fmts[1], [0], [L], 1 << 20, hkv)
+    ref, rm, rz = _dense_reference(q[0], packets, fmts[0], fmts[1], L, hkv, hd)
+    assert np.allclose(out[0], ref, rtol=1e-10, atol=1e-12)
+    assert np.allclose(m[0], rm) and np.allclose(z[0], rz)
+
+
+def test_attention_identities():
+    rng = np.random.default_rng(11)
+    hq, hkv, hd = 4, 1, 128
+    one = _history(rng, 1, hkv, hd, orc.Q4_K, orc.Q6_K)
+    const = np.repeat(one, 9, axis=0)
+    q = rng.standard_normal((1, hq, hd)).astype(np.float32)
+    v0 = np.array([orc.lib().orc_packet_value(one[0].ctypes.data, hd, orc.Q4_K, orc.Q6_K, 1, c) for c in range(hd)])
+    out, m, z = orc.decode_attention(q, one, orc.Q4_K, orc.Q6_K, [0], [1], 64, hkv)
+    assert np.allclose(out[0], v0[None], rtol=1e-12) and np.allclose(z, 1.0)       # one position -> V0
+    out, m, z = orc.decode_attention(q, const, orc.Q4_K, orc.Q6_K, [0], [9], 64, hkv)
+    assert np.allclose(out[0], v0[None], rtol=1e-12) and np.allclose(z, 9.0)       # constant V -> V
+    hist = _history(rng, 20, hkv, hd, orc.Q4_K, orc.Q6_K)
+    zq = np.zeros((1, hq, hd), np.float32)
+    out, m, z = orc.decode_attention(zq, hist, orc.Q4_K, orc.Q6_K, [0], [20], 64, hkv)
+    V = np.array([[orc.lib().orc_packet_value(p.ctypes.data, hd, orc.Q4_K, orc.Q6_K, 1, c) for c in range(hd)]
+                  for p in hist])
+    assert np.allclose(out[0], V.mean(0)[None], rtol=1e-10)                        # zero q -> uniform
+    assert np.allclose(z, 20.0) and np.allclose(m, 0.0)
+
+
+def test_attention_split_merge_identity():
+    # The split-K merge (resident_attention_runtime.inl:618-645; paper eq. 46):
+    # two halves combined with M = max, Z = sum Z_i e^(m_i - M) equal the whole.
+    rng = np.random.default_rng(12)
+    hq, hkv, hd, L = 4, 1, 128, 50
+    hist = _history(rng, L, hkv, hd, orc.Q4_K, orc.Q6_K)
+    q = rng.standard_normal((1, hq, hd)).astype(np.float32)
+    full, mf, zf = orc.decode_attention(q, hist, orc.Q4_K, orc.Q6_K, [0], [L], 1 << 20, hkv)
+    # positions 20..49 in a ring of capacity 30 (slot = p % 30); the query at t = 49
+    # sees exactly them.  Positions 0..19 are the other half.
+    a, ma, za = orc.decode_attention(q, hist[:20], orc.Q4_K, orc.Q6_K, [0], [20], 1 << 20, hkv)
+    ring = np.empty((30, hist.shape[1]), np.uint8)
+    for p in range(20, L):
+        ring[p % 30] = hist[p]
+    b, mb, zb = orc.decode_attention(q, ring, orc.Q4_K, orc.Q6_K, [0], [L], 30, hkv)
+    M = np.maximum(ma, mb)
+    Z = za * np.exp(ma - M) + zb * np.exp(mb - M)
+    merged = (a * (za * np.exp(ma - M))[..., None] + b * (zb * np.exp(mb - M))[..., None]) / Z[..., None]
+    assert np.allclose(merged, full, rtol=1e-10, atol=1e-12)
+    assert np.allclose(M, mf) and np.allclose(Z, zf)
+
+
+# ------------------------------------------------------------------ packer ----
+@pytest.mark.parametrize("fmts", [(orc.Q4_K, orc.Q6_K), (orc.Q6_K, orc.Q4_K)])
+def test_packer_round_trip(fmts):
+    rng = np.random.default_rng(13)
+    kvw = 512
+    k = rng.normal(0, 0.25, kvw).astype(np.float32)
+    v = rng.normal(0, 0.5, kvw).astype(np.float32)
+    pk = orc.pack_history(k, v, *fmts)
+    assert pk.size == 712
+    kk = np.array([orc.lib().orc_packet_value(pk.ctypes.data, kvw, fmts[0], fmts[1], 0, c) for c in range(kvw)])
+    vv = np.array([orc.lib().orc_packet_value(pk.ctypes.data, kvw, fmts[0], fmts[1], 1, c) for c in range(kvw)])
+    # error within one quantisation step of each field's 16/32-value group
+    for field, dec in ((k, kk), (v, vv)):
+        step = np.abs(field).max() / 7.0
+        assert np.max(np.abs(dec - field)) <= step, np.max(np.abs(dec - field))
+    assert not pk[708:].any()                                  # 4 pad bytes stay zero
