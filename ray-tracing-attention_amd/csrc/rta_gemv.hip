@@ -108,52 +108,98 @@ static int pow2ceil(int v) {
     return p;
 }
 
+static bool is_kquant(int fmt) { return fmt == RTA_Q4_K || fmt == RTA_Q6_K; }
+
 struct Plan {
-    int nb, r, lpr, ntasks, grid;
+    bool b1;          // batch-1 kernel
+    int nb, r, kw, lpr, ntasks, grid, block, rows_per_task;
 };
 
-// Chooses the batch tile NB and row passes R for a K-quant launch.
+// Launch plan of one K-quant projection over `batch` (<= 8) x rows.
 static Plan plan_kquant(int rows, int cols, int batch, bool dual) {
-    Plan p;
+    Plan p{};
+    const int S = cols / 64;
+    p.b1 = batch == 1 && S <= 4 * kWave;
+    if (p.b1) {
+        p.nb = 1;
+        p.r = dual ? 1 : 2;
+        p.kw = S <= kWave ? 1 : (S + kWave - 1) / kWave;
+        p.lpr = S >= kWave ? kWave : pow2ceil(S);
+        p.rows_per_task = (kWave / p.lpr) * p.r;
+        p.ntasks = (rows + p.rows_per_task - 1) / p.rows_per_task;
+        const int groups = p.kw == 3 ? 1 : 4 / p.kw;
+        p.block = p.kw == 3 ? 192 : 256;
+        const int blocks = (p.ntasks + groups - 1) / groups;
+        p.grid = blocks < 2048 ? blocks : 2048;
+        return p;
+    }
     p.nb = batch <= 1 ? 1 : batch <= 2 ? 2 : batch <= 4 ? 4 : 8;
     p.r = p.nb >= 8 ? 2 : 4;
     if (dual) p.r = p.r / 2 > 0 ? p.r / 2 : 1;
-    const int S = cols / 64;
+    p.kw = 1;
     p.lpr = S >= kWave ? kWave : pow2ceil(S);
-    const int rows_per_task = (kWave / p.lpr) * p.r;
-    p.ntasks = (rows + rows_per_task - 1) / rows_per_task;
+    p.rows_per_task = (kWave / p.lpr) * p.r;
+    p.ntasks = (rows + p.rows_per_task - 1) / p.rows_per_task;
     const int wgs = (p.ntasks + 3) / 4;
     p.grid = wgs < 2048 ? wgs : 2048;
+    p.block = 256;
     return p;
 }
 
-template <int FMT, int MODE>
-static hipError_t launch_kquant_nb(int nb, const GemvArgs& a, int grid, hipStream_t s, bool dual_r) {
-    (void)dual_r;
-    switch (nb) {
-    case 1: hipLaunchKernelGGL((gemv_kquant_kernel<FMT, 1, MODE == kSwiglu ? 2 : 4, MODE>), dim3(grid), dim3(256), 0, s, a); break;
-    case 2: hipLaunchKernelGGL((gemv_kquant_kernel<FMT, 2, MODE == kSwiglu ? 2 : 4, MODE>), dim3(grid), dim3(256), 0, s, a); break;
-    case 4: hipLaunchKernelGGL((gemv_kquant_kernel<FMT, 4, MODE == kSwiglu ? 2 : 4, MODE>), dim3(grid), dim3(256), 0, s, a); break;
-    default: hipLaunchKernelGGL((gemv_kquant_kernel<FMT, 8, MODE == kSwiglu ? 1 : 2, MODE>), dim3(grid), dim3(256), 0, s, a); break;
+struct Launch {
+    const uint8_t* w;
+    const uint8_t* w2;
+    int64_t row_bytes;
+    int rows, cols;
+    const float* x;
+    float* y;
+    float* partial;
+    int batch;
+};
+
+template <int FMT, int MODE, int R>
+static void launch_b1_kw(const Plan& p, const Launch& l, hipStream_t s) {
+    const dim3 g(p.grid), b(p.block);
+    switch (p.kw) {
+    case 1: hipLaunchKernelGGL((gemv_b1_kernel<FMT, R, MODE, 1>), g, b, 0, s, l.w, l.w2, l.row_bytes, l.rows, l.cols, l.x, l.y, l.partial, p.lpr, p.ntasks); break;
+    case 2: hipLaunchKernelGGL((gemv_b1_kernel<FMT, R, MODE, 2>), g, b, 0, s, l.w, l.w2, l.row_bytes, l.rows, l.cols, l.x, l.y, l.partial, p.lpr, p.ntasks); break;
+    case 3: hipLaunchKernelGGL((gemv_b1_kernel<FMT, R, MODE, 3>), g, b, 0, s, l.w, l.w2, l.row_bytes, l.rows, l.cols, l.x, l.y, l.partial, p.lpr, p.ntasks); break;
+    default: hipLaunchKernelGGL((gemv_b1_kernel<FMT, R, MODE, 4>), g, b, 0, s, l.w, l.w2, l.row_bytes, l.rows, l.cols, l.x, l.y, l.partial, p.lpr, p.ntasks); break;
     }
+}
+
+template <int FMT, int MODE>
+static void launch_kquant_fmt(const Plan& p, const Launch& l, hipStream_t s) {
+    if (p.b1) {
+        if (p.r == 1) launch_b1_kw<FMT, MODE, 1>(p, l, s);
+        else launch_b1_kw<FMT, MODE, 2>(p, l, s);
+        return;
+    }
+    const dim3 g(p.grid), b(256);
+    constexpr bool dual = MODE == kSwiglu;
+    switch (p.nb) {
+    case 1: hipLaunchKernelGGL((gemv_kquant_kernel<FMT, 1, dual ? 2 : 4, MODE>), g, b, 0, s, l.w, l.w2, l.row_bytes, l.rows, l.cols, l.x, l.y, l.partial, l.batch, p.lpr, p.ntasks); break;
+    case 2: hipLaunchKernelGGL((gemv_kquant_kernel<FMT, 2, dual ? 2 : 4, MODE>), g, b, 0, s, l.w, l.w2, l.row_bytes, l.rows, l.cols, l.x, l.y, l.partial, l.batch, p.lpr, p.ntasks); break;
+    case 4: hipLaunchKernelGGL((gemv_kquant_kernel<FMT, 4, dual ? 2 : 4, MODE>), g, b, 0, s, l.w, l.w2, l.row_bytes, l.rows, l.cols, l.x, l.y, l.partial, l.batch, p.lpr, p.ntasks); break;
+    default: hipLaunchKernelGGL((gemv_kquant_kernel<FMT, 8, dual ? 1 : 2, MODE>), g, b, 0, s, l.w, l.w2, l.row_bytes, l.rows, l.cols, l.x, l.y, l.partial, l.batch, p.lpr, p.ntasks); break;
+    }
+}
+
+template <int MODE>
+static hipError_t launch_kquant(int fmt, const Plan& p, const Launch& l, hipStream_t s) {
+    if (fmt == RTA_Q4_K) launch_kquant_fmt<RTA_Q4_K, MODE>(p, l, s);
+    else launch_kquant_fmt<RTA_Q6_K, MODE>(p, l, s);
     return hipGetLastError();
 }
 
 template <int MODE>
-static hipError_t launch_kquant(int fmt, int nb, const GemvArgs& a, int grid, hipStream_t s) {
-    if (fmt == RTA_Q4_K) return launch_kquant_nb<RTA_Q4_K, MODE>(nb, a, grid, s, false);
-    return launch_kquant_nb<RTA_Q6_K, MODE>(nb, a, grid, s, false);
-}
-
-template <int MODE>
-static hipError_t launch_plain(int fmt, const GemvArgs& a, int grid, hipStream_t s) {
-    if (fmt == RTA_F32) hipLaunchKernelGGL((gemv_plain_kernel<RTA_F32, MODE>), dim3(grid), dim3(256), 0, s, a);
-    else if (fmt == RTA_F16) hipLaunchKernelGGL((gemv_plain_kernel<RTA_F16, MODE>), dim3(grid), dim3(256), 0, s, a);
-    else hipLaunchKernelGGL((gemv_plain_kernel<RTA_BF16, MODE>), dim3(grid), dim3(256), 0, s, a);
+static hipError_t launch_plain(int fmt, const Launch& l, int grid, hipStream_t s) {
+    const dim3 g(grid), b(256);
+    if (fmt == RTA_F32) hipLaunchKernelGGL((gemv_plain_kernel<RTA_F32, MODE>), g, b, 0, s, l.w, l.w2, l.row_bytes, l.rows, l.cols, l.x, l.y, l.partial, l.batch);
+    else if (fmt == RTA_F16) hipLaunchKernelGGL((gemv_plain_kernel<RTA_F16, MODE>), g, b, 0, s, l.w, l.w2, l.row_bytes, l.rows, l.cols, l.x, l.y, l.partial, l.batch);
+    else hipLaunchKernelGGL((gemv_plain_kernel<RTA_BF16, MODE>), g, b, 0, s, l.w, l.w2, l.row_bytes, l.rows, l.cols, l.x, l.y, l.partial, l.batch);
     return hipGetLastError();
 }
-
-static bool is_kquant(int fmt) { return fmt == RTA_Q4_K || fmt == RTA_Q6_K; }
 
 static int check_matrix(int fmt, const void* w, int rows, int cols) {
     if (!host::valid_format(fmt)) return RTA_ERR_FORMAT;
@@ -168,6 +214,8 @@ static int check_matrix(int fmt, const void* w, int rows, int cols) {
 }
 
 // Runs one projection over the whole batch, in batch tiles of at most 8 rows.
+// For kLogits, partial receives per-task maxima laid out [tile row][ntasks] inside
+// the tile's [8 x rows] region, and *ntasks_out / *rows_per_task_out the plan.
 template <int MODE>
 static int run_projection(int fmt, const void* w, const void* w2, int rows, int cols, const float* x, int batch,
                           float* y, float* partial, int* ntasks_out, int* rows_per_task_out, hipStream_t s) {
@@ -175,32 +223,27 @@ static int run_projection(int fmt, const void* w, const void* w2, int rows, int 
     int b0 = 0;
     while (b0 < batch) {
         const int chunk = batch - b0 < 8 ? batch - b0 : 8;
-        GemvArgs a{};
-        a.w = static_cast<const uint8_t*>(w);
-        a.w2 = static_cast<const uint8_t*>(w2);
-        a.row_bytes = row_bytes;
-        a.rows = rows;
-        a.cols = cols;
-        a.x = x + (int64_t)b0 * cols;
-        a.y = y + (int64_t)b0 * rows;
-        a.batch = chunk;
+        Launch l{};
+        l.w = static_cast<const uint8_t*>(w);
+        l.w2 = static_cast<const uint8_t*>(w2);
+        l.row_bytes = row_bytes;
+        l.rows = rows;
+        l.cols = cols;
+        l.x = x + (int64_t)b0 * cols;
+        l.y = y + (int64_t)b0 * rows;
+        l.batch = chunk;
+        l.partial = partial ? partial + (int64_t)b0 * rows : nullptr;
         hipError_t e;
         if (is_kquant(fmt)) {
             const Plan p = plan_kquant(rows, cols, chunk, MODE == kSwiglu);
-            a.lpr = p.lpr;
-            a.ntasks = p.ntasks;
-            a.partial = partial ? partial + (int64_t)b0 * p.ntasks : nullptr;
             if (ntasks_out) *ntasks_out = p.ntasks;
-            if (rows_per_task_out) *rows_per_task_out = (kWave / p.lpr) * p.r;
-            e = launch_kquant<MODE>(fmt, p.nb, a, p.grid, s);
+            if (rows_per_task_out) *rows_per_task_out = p.rows_per_task;
+            e = launch_kquant<MODE>(fmt, p, l, s);
         } else {
-            a.lpr = kWave;
-            a.ntasks = rows;
-            a.partial = partial ? partial + (int64_t)b0 * rows : nullptr;
             if (ntasks_out) *ntasks_out = rows;
             if (rows_per_task_out) *rows_per_task_out = 1;
             const int wgs = (rows + 3) / 4;
-            e = launch_plain<MODE>(fmt, a, wgs < 2048 ? wgs : 2048, s);
+            e = launch_plain<MODE>(fmt, l, wgs < 2048 ? wgs : 2048, s);
         }
         if (e != hipSuccess) return RTA_ERR_LAUNCH;
         b0 += chunk;
@@ -315,12 +358,11 @@ int rta_lm_head(int fmt, const void* w, int vocab, int hidden, const float* h, i
         return RTA_ERR_ALIGN;
     hipStream_t s = (hipStream_t)stream;
     float* partial = static_cast<float*>(workspace);
-    int ntasks = 0, rpt = 1;
-    // Batch tiles share one ntasks/rows_per_task plan except possibly the last tile;
-    // run the argmax per tile so each uses the plan it was written with.
+    // Argmax per batch tile of 8, with the plan that tile was written with.
     int b0 = 0;
     while (b0 < batch) {
         const int chunk = batch - b0 < 8 ? batch - b0 : 8;
+        int ntasks = 0, rpt = 1;
         rc = run_projection<kLogits>(fmt, w, nullptr, vocab, hidden, h + (int64_t)b0 * hidden, chunk,
                                      logits + (int64_t)b0 * vocab, partial + (int64_t)b0 * vocab, &ntasks, &rpt, s);
         if (rc) return rc;

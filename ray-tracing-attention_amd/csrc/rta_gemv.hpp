@@ -5,14 +5,17 @@
 //     Q4_K slot = chunk j of a superblock: 32 nibble bytes, groups 2j and 2j+1
 //     Q6_K slot = (half h, l0 in {0,16}) of a superblock: 16 ql bytes at
 //                 64h+l0 and 64h+32+l0, 16 qh bytes at 128+32h+l0, 4 scales
-//   `lpr` lanes share one row (lpr = min(64, pow2ceil(S))); a wave therefore
-//   covers P = 64/lpr rows per pass and R passes per task (P*R consecutive rows).
-//   Each lane streams its slot's bytes straight from HBM (16-byte loads for Q4_K,
-//   4-byte loads + alignbyte for the 2-byte aligned Q6_K blocks), unpacks codes in
-//   registers and accumulates code*x with v_fma_mix_f32 (the codes are binary16
-//   subnormals, so the conversion is free and exact).  The per-group scale and
-//   minimum are applied once per slot:  sum_i (D q_i - M) x_i = D sum q_i x_i - M sum x_i.
-//   Partial sums are reduced across the row's lanes with xor shuffles.
+//   Each lane owns one slot position for the whole kernel, so its 64 x values
+//   and their per-run sums stay in registers while the lane streams that slot
+//   of row after row.  A row is covered by `lpr` lanes of one wave when
+//   S <= 64 (P = 64/lpr rows per pass), or by KW = S/64 waves of one
+//   workgroup when S > 64 (partials combined through LDS).
+//   Weights stream straight from HBM (16-byte loads for Q4_K; 4-byte loads plus
+//   alignbyte for the 2-byte aligned Q6_K blocks) one task ahead of the
+//   arithmetic (ping-pong register buffers).  Codes are unpacked in registers
+//   into binary16 subnormals c * 2^-24, so v_fma_mix_f32 converts and
+//   accumulates in one instruction; the group scale and minimum are applied once
+//   per slot:  sum_i (D q_i - M) x_i = D sum q_i x_i - M sum x_i.
 //
 // Equivalent reference: resident_math.comp:39-75 (one 32-lane subgroup per channel,
 // quantizedOctet decode of resident_quant.glsl:47-94, subgroupAdd).
@@ -23,54 +26,49 @@ namespace rta {
 
 enum GemvMode { kStore = 0, kAccumulate = 1, kSwiglu = 2, kLogits = 3 };
 
-struct GemvArgs {
-    const uint8_t* w;     // matrix (gate matrix in kSwiglu)
-    const uint8_t* w2;    // up matrix in kSwiglu
-    int64_t row_bytes;
-    int rows, cols;
-    const float* x;       // [batch, cols]
-    float* y;             // [batch, rows]
-    float* partial;       // kLogits: [batch, ntasks] maxima per task
-    int batch;            // rows of x handled by this launch (<= NB)
-    int lpr;              // lanes per matrix row
-    int ntasks;
-};
+// ------------------------------------------------------------ reductions ----
+template <int CTRL>
+__device__ __forceinline__ float dpp(float v) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), CTRL, 0xF, 0xF, true));
+}
+
+// Sum over aligned groups of `width` lanes (power of two, 4..64); every lane of
+// a group ends with the group sum.  quad_perm xor1/xor2, half-row and row
+// mirrors (DPP), then xor 16 / 32 through ds_bpermute.
+__device__ __forceinline__ float lane_group_sum(float v, int width) {
+    v += dpp<0xB1>(v);   // quad_perm [1,0,3,2]
+    v += dpp<0x4E>(v);   // quad_perm [2,3,0,1]
+    if (width == 4) return v;
+    v += dpp<0x141>(v);  // row_half_mirror
+    if (width == 8) return v;
+    v += dpp<0x140>(v);  // row_mirror
+    if (width == 16) return v;
+    v += __shfl_xor(v, 16, kWave);
+    if (width == 32) return v;
+    return v + __shfl_xor(v, 32, kWave);
+}
 
 // ---------------------------------------------------------------- Q4_K ----
 struct Q4K {
     static constexpr int kBytes = 144;
-    static constexpr int kRuns = 2;       // x runs per slot: [0,32) low nibbles, [32,64) high
+    static constexpr int kRuns = 2;  // x runs per slot: [0,32) low nibbles, [32,64) high
     static constexpr int kRunLen = 32;
     struct Raw { uint4 hdr, q0, q1; };
-    struct Scale { float d0, d1, m0, m1; };
 
     __device__ static __forceinline__ int run_col(int slot, int run) {
         return (slot >> 2) * 256 + (slot & 3) * 64 + run * 32;
     }
-    __device__ static __forceinline__ void load(const uint8_t* row, int slot, Raw& r) {
-        const uint8_t* blk = row + (int64_t)(slot >> 2) * kBytes;
+    __device__ static __forceinline__ void load(const uint8_t* __restrict__ row, int slot, Raw& r) {
+        const uint8_t* blk = row + (slot >> 2) * kBytes;
         const int j = slot & 3;
         r.hdr = *reinterpret_cast<const uint4*>(blk);
         r.q0 = *reinterpret_cast<const uint4*>(blk + 16 + 32 * j);
         r.q1 = *reinterpret_cast<const uint4*>(blk + 32 + 32 * j);
     }
-    __device__ static __forceinline__ Scale scale(const Raw& r, int slot) {
-        const int j = slot & 3;
-        uint32_t sc0, m0, sc1, m1;
-        q4k_scale_min(r.hdr.y, r.hdr.z, r.hdr.w, 2 * j, sc0, m0);
-        q4k_scale_min(r.hdr.y, r.hdr.z, r.hdr.w, 2 * j + 1, sc1, m1);
-        const float d = half_lo(r.hdr.x), dmin = half_hi(r.hdr.x);
-        Scale s;
-        s.d0 = d * (float)sc0 * 16777216.0f;  // low-nibble codes carry 2^-24
-        s.d1 = d * (float)sc1 * 1048576.0f;   // high-nibble codes carry 2^-20
-        s.m0 = dmin * (float)m0;
-        s.m1 = dmin * (float)m1;
-        return s;
-    }
-    // acc[0] += sum q_lo x[0..32) * 2^-24 ; acc[1] += sum q_hi x[32..64) * 2^-20
-    __device__ static __forceinline__ void dot(const Raw& r, const float* __restrict__ xs, float acc[kRuns]) {
+    // Contribution of one slot: D0 sum q_lo x - M0 X0 + D1 sum q_hi x - M1 X1.
+    __device__ static __forceinline__ float slot_dot(const Raw& r, int slot, const float* xs, const float* X) {
         const uint32_t q[8] = {r.q0.x, r.q0.y, r.q0.z, r.q0.w, r.q1.x, r.q1.y, r.q1.z, r.q1.w};
-        float a0 = acc[0], a1 = acc[1], b0 = 0.0f, b1 = 0.0f;
+        float a0 = 0.0f, a1 = 0.0f, b0 = 0.0f, b1 = 0.0f;
 #pragma unroll
         for (int t = 0; t < 8; ++t) {
             const uint32_t w = q[t], v = w >> 8;
@@ -85,75 +83,70 @@ struct Q4K {
             a1 = fmaf((float)h0.y, xs[32 + 4 * t + 2], a1);
             b1 = fmaf((float)h1.y, xs[32 + 4 * t + 3], b1);
         }
-        acc[0] = a0 + b0;
-        acc[1] = a1 + b1;
-    }
-    __device__ static __forceinline__ float combine(const Scale& s, const float acc[kRuns], const float X[kRuns]) {
-        float v = s.d0 * acc[0];
-        v = fmaf(-s.m0, X[0], v);
-        v = fmaf(s.d1, acc[1], v);
-        v = fmaf(-s.m1, X[1], v);
-        return v;
+        const int j = slot & 3;
+        uint32_t sc0, m0, sc1, m1;
+        q4k_scale_min(r.hdr.y, r.hdr.z, r.hdr.w, 2 * j, sc0, m0);
+        q4k_scale_min(r.hdr.y, r.hdr.z, r.hdr.w, 2 * j + 1, sc1, m1);
+        const float d = half_lo(r.hdr.x), dmin = half_hi(r.hdr.x);
+        // low-nibble codes carry 2^-24, high-nibble codes 2^-20
+        float v = (d * 16777216.0f) * (float)sc0 * (a0 + b0);
+        v = fmaf(-(dmin * (float)m0), X[0], v);
+        v = fmaf((d * 1048576.0f) * (float)sc1, a1 + b1, v);
+        return fmaf(-(dmin * (float)m1), X[1], v);
     }
 };
 
 // ---------------------------------------------------------------- Q6_K ----
 struct Q6K {
     static constexpr int kBytes = 210;
-    static constexpr int kRuns = 4;       // run k: values l0 + [0,16) + 32k of half h
+    static constexpr int kRuns = 4;  // run k: values l0 + [0,16) + 32k of half h
     static constexpr int kRunLen = 16;
-    struct Raw { uint32_t a[4], b[4], h[4]; uint32_t s; uint32_t d; };
-    struct Scale { float d[4]; };
+    // Raw dwords from the 4-byte aligned address below each run; funnelled later.
+    struct Raw { uint32_t a[5], b[5], h[5], s[3], d, mis; };
 
     __device__ static __forceinline__ int run_col(int slot, int run) {
         const int hh = (slot >> 1) & 1, l0 = (slot & 1) * 16;
         return (slot >> 2) * 256 + hh * 128 + l0 + 32 * run;
     }
-    // Loads 16 bytes that start at a 2-byte aligned address p (never beyond p + 20).
-    __device__ static __forceinline__ void load16(const uint8_t* p, uint32_t out[4]) {
-        const uintptr_t addr = reinterpret_cast<uintptr_t>(p);
+    // Every read lies inside the 210-byte block (the last dword of each run and
+    // the third scale dword are only consumed when the block is 2-byte aligned).
+    __device__ static __forceinline__ void load(const uint8_t* __restrict__ row, int slot, Raw& r) {
+        const uint8_t* blk = row + (slot >> 2) * kBytes;
+        const int hh = (slot >> 1) & 1, l0 = (slot & 1) * 16;
+        const uintptr_t addr = reinterpret_cast<uintptr_t>(blk);
         const uint32_t mis = (uint32_t)(addr & 3u);
         const uint32_t* a = reinterpret_cast<const uint32_t*>(addr - mis);
-        uint32_t w[5];
+        const int ia = (64 * hh + l0) >> 2, ib = (64 * hh + 32 + l0) >> 2, ih = (128 + 32 * hh + l0) >> 2;
+        const int is = (192 + 8 * hh) >> 2;
 #pragma unroll
-        for (int i = 0; i < 5; ++i) w[i] = a[i];
-#pragma unroll
-        for (int i = 0; i < 4; ++i) out[i] = funnel(w[i], w[i + 1], mis);
-    }
-    __device__ static __forceinline__ void load(const uint8_t* row, int slot, Raw& r) {
-        const uint8_t* blk = row + (int64_t)(slot >> 2) * kBytes;
-        const int hh = (slot >> 1) & 1, l0 = (slot & 1) * 16;
-        load16(blk + 64 * hh + l0, r.a);
-        load16(blk + 64 * hh + 32 + l0, r.b);
-        load16(blk + 128 + 32 * hh + l0, r.h);
-        // scale bytes 192 + 8h + l0/16 + {0,2,4,6}: four 2-byte aligned halfwords
-        const uint16_t* sp = reinterpret_cast<const uint16_t*>(blk + 192 + 8 * hh);
-        const uint32_t pick = (uint32_t)(l0 >> 4) * 8u;
-        uint32_t s = 0;
-#pragma unroll
-        for (int k = 0; k < 4; ++k) s |= (((uint32_t)sp[k] >> pick) & 255u) << (8 * k);
-        r.s = s;
+        for (int i = 0; i < 5; ++i) {
+            r.a[i] = a[ia + i];
+            r.b[i] = a[ib + i];
+            r.h[i] = a[ih + i];
+        }
+        r.s[0] = a[is];
+        r.s[1] = a[is + 1];
+        r.s[2] = a[is + 1 + (mis ? 1 : 0)];
         r.d = *reinterpret_cast<const uint16_t*>(blk + 208);
+        r.mis = mis;
     }
-    __device__ static __forceinline__ Scale scale(const Raw& r, int) {
-        const float d = (float)__builtin_bit_cast(_Float16, (uint16_t)r.d);
-        Scale s;
-#pragma unroll
-        for (int k = 0; k < 4; ++k) s.d[k] = d * (float)(int8_t)((r.s >> (8 * k)) & 255u);
-        return s;
-    }
-    __device__ static __forceinline__ void dot(const Raw& r, const float* __restrict__ xs, float acc[kRuns]) {
+    __device__ static __forceinline__ float slot_dot(const Raw& r, int slot, const float* xs, const float* X) {
+        float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
         for (int t = 0; t < 4; ++t) {
-            const uint32_t a = r.a[t], b = r.b[t], h = r.h[t];
+            const uint32_t a = funnel(r.a[t], r.a[t + 1], r.mis);
+            const uint32_t b = funnel(r.b[t], r.b[t + 1], r.mis);
+            const uint32_t h = funnel(r.h[t], r.h[t + 1], r.mis);
+            const uint32_t ha = h & 0x33333333u, hb = (h >> 2) & 0x33333333u;
             uint32_t c[4];
-            c[0] = (a & 0x0F0F0F0Fu) | ((h << 4) & 0x30303030u);
-            c[1] = (b & 0x0F0F0F0Fu) | ((h << 2) & 0x30303030u);
-            c[2] = ((a >> 4) & 0x0F0F0F0Fu) | (h & 0x30303030u);
-            c[3] = ((b >> 4) & 0x0F0F0F0Fu) | ((h >> 2) & 0x30303030u);
+            c[0] = (a & 0x0F0F0F0Fu) | ((ha << 4) & 0xF0F0F0F0u);
+            c[1] = (b & 0x0F0F0F0Fu) | ((hb << 4) & 0xF0F0F0F0u);
+            c[2] = ((a >> 4) & 0x0F0F0F0Fu) | (ha & 0xF0F0F0F0u);
+            c[3] = ((b >> 4) & 0x0F0F0F0Fu) | (hb & 0xF0F0F0F0u);
 #pragma unroll
             for (int k = 0; k < 4; ++k) {
-                const half2_t p = as_codes(c[k] & 0x00FF00FFu), q = as_codes((c[k] >> 8) & 0x00FF00FFu);
+                const half2_t p = as_codes(c[k] & 0x00FF00FFu);
+                const half2_t q = as_codes(__builtin_amdgcn_perm(c[k], c[k], 0x0C030C01u));
                 const float* xr = xs + 16 * k + 4 * t;
                 float v = acc[k];
                 v = fmaf((float)p.x, xr[0], v);
@@ -163,12 +156,18 @@ struct Q6K {
                 acc[k] = v;
             }
         }
-    }
-    __device__ static __forceinline__ float combine(const Scale& s, const float acc[kRuns], const float X[kRuns]) {
-        // sum (c-32) x = sum c x - 32 sum x ; codes carry 2^-24
+        // scales 8h + l0/16 + {0,2,4,6}: bytes (l0/16) + 2k of the half's 8 scale bytes
+        const uint32_t s_lo = funnel(r.s[0], r.s[1], r.mis), s_hi = funnel(r.s[1], r.s[2], r.mis);
+        const uint32_t pick = (uint32_t)(slot & 1) * 8u;
+        const float d = (float)__builtin_bit_cast(_Float16, (uint16_t)r.d);
         float v = 0.0f;
 #pragma unroll
-        for (int k = 0; k < 4; ++k) v = fmaf(s.d[k], fmaf(acc[k], 16777216.0f, -32.0f * X[k]), v);
+        for (int k = 0; k < 4; ++k) {
+            const uint32_t word = k < 2 ? s_lo : s_hi;
+            const int sc = (int)(int8_t)((word >> (16 * (k & 1) + pick)) & 255u);
+            // sum (c-32) x = sum c x - 32 sum x ; codes carry 2^-24
+            v = fmaf(d * (float)sc, fmaf(acc[k], 16777216.0f, -32.0f * X[k]), v);
+        }
         return v;
     }
 };
@@ -177,11 +176,9 @@ template <int FMT> struct FmtOf;
 template <> struct FmtOf<RTA_Q4_K> { using T = Q4K; };
 template <> struct FmtOf<RTA_Q6_K> { using T = Q6K; };
 
-// Loads the 64 x values of one slot for batch row b, and the per-run sums.
+// The 64 x values of one slot and their per-run sums.
 template <class F>
-__device__ __forceinline__ void load_x(const float* __restrict__ x, int cols, int b, int slot,
-                                       float xs[64], float X[F::kRuns]) {
-    const float* xb = x + (int64_t)b * cols;
+__device__ __forceinline__ void load_x(const float* __restrict__ xb, int slot, float xs[64], float X[F::kRuns]) {
 #pragma unroll
     for (int run = 0; run < F::kRuns; ++run) {
         const float4* p = reinterpret_cast<const float4*>(xb + F::run_col(slot, run));
@@ -199,19 +196,143 @@ __device__ __forceinline__ void load_x(const float* __restrict__ x, int cols, in
     }
 }
 
-// NB: batch rows per launch (x rows), R: row passes per task.
+// ------------------------------------------------------------ batch 1 ----
+// KW waves per row task (cols = 64*64*KW at most); 256-thread blocks run 4/KW
+// independent task groups when KW divides 4, otherwise one group of KW waves.
+// R rows per lane per task (P*R rows per task).
+template <int FMT, int R, int MODE, int KW>
+__global__ void __launch_bounds__(256) gemv_b1_kernel(const uint8_t* __restrict__ w, const uint8_t* __restrict__ w2,
+                                                      const int64_t row_bytes, const int rows, const int cols,
+                                                      const float* __restrict__ x, float* __restrict__ y,
+                                                      float* __restrict__ partial, const int lpr, const int ntasks) {
+    using F = typename FmtOf<FMT>::T;
+    using Raw = typename F::Raw;
+    constexpr bool kDual = MODE == kSwiglu;
+    constexpr int kGroups = (KW == 3) ? 1 : 4 / KW;
+    __shared__ float s_part[kGroups][KW][R][2][4];   // per wave partials (KW > 1), 4 subs max
+
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int group = wave / KW, wk = wave - group * KW;   // wave index inside its task group
+    const int S = cols >> 6, P = kWave / lpr;
+    const int sub = lane / lpr, lir = lane - sub * lpr;
+    const int slot_i = wk * 64 + lir;
+    const bool active = lir < lpr && slot_i < S && (KW == 1 || lpr == kWave);
+    const int slot = active ? slot_i : 0;
+    const int rpt = P * R;
+
+    float xs[64], X[F::kRuns];
+    if (active) {
+        load_x<F>(x, slot, xs, X);
+    } else {
+#pragma unroll
+        for (int i = 0; i < 64; ++i) xs[i] = 0.0f;
+#pragma unroll
+        for (int i = 0; i < F::kRuns; ++i) X[i] = 0.0f;
+    }
+
+    const int stride = gridDim.x * kGroups;
+    Raw bufA[R], bufB[R], bufA2[kDual ? R : 1], bufB2[kDual ? R : 1];
+
+    auto load_task = [&](int t, Raw* dst, Raw* dst2) {
+        if (!active) return;
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            const int row = min(t * rpt + sub + P * r, rows - 1);  // clamped rows are discarded
+            F::load(w + (int64_t)row * row_bytes, slot, dst[r]);
+            if constexpr (kDual) F::load(w2 + (int64_t)row * row_bytes, slot, dst2[r]);
+        }
+    };
+
+    // real == false: a task group past the end that only keeps the block's barriers
+    // matched; it computes on stale registers and writes nothing.
+    auto run_task = [&](int t, const Raw* src, const Raw* src2, bool real) {
+        float acc[R], acc2[R];
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            acc[r] = active ? F::slot_dot(src[r], slot, xs, X) : 0.0f;
+            if constexpr (kDual) acc2[r] = active ? F::slot_dot(src2[r], slot, xs, X) : 0.0f;
+        }
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            acc[r] = lane_group_sum(acc[r], lpr);
+            if constexpr (kDual) acc2[r] = lane_group_sum(acc2[r], lpr);
+        }
+        if constexpr (KW > 1) {   // lpr == 64 here: one row pass per wave
+            if (lane == 0) {
+#pragma unroll
+                for (int r = 0; r < R; ++r) {
+                    s_part[group][wk][r][0][0] = acc[r];
+                    if constexpr (kDual) s_part[group][wk][r][1][0] = acc2[r];
+                }
+            }
+            __syncthreads();
+#pragma unroll
+            for (int r = 0; r < R; ++r) {
+                float s = 0.0f, s2 = 0.0f;
+#pragma unroll
+                for (int k = 0; k < KW; ++k) {
+                    s += s_part[group][k][r][0][0];
+                    if constexpr (kDual) s2 += s_part[group][k][r][1][0];
+                }
+                acc[r] = s;
+                if constexpr (kDual) acc2[r] = s2;
+            }
+            __syncthreads();
+            if (wk != 0) return;
+        }
+        if (!real) return;
+        float local_max = -INFINITY;
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            const int row = t * rpt + sub + P * r;
+            if (row >= rows) continue;
+            const float v = acc[r];
+            if constexpr (MODE == kLogits) local_max = fmaxf(local_max, v);
+            if (lir == 0) {
+                if constexpr (MODE == kStore || MODE == kLogits) y[row] = v;
+                else if constexpr (MODE == kAccumulate) y[row] += v;
+                else y[row] = swiglu(v, acc2[r]);
+            }
+        }
+        if constexpr (MODE == kLogits) {
+            for (int off = lpr; off < kWave; off <<= 1) local_max = fmaxf(local_max, __shfl_xor(local_max, off, kWave));
+            if (lane == 0) partial[t] = local_max;
+        }
+    };
+
+    // Uniform trip count per block (KW > 1 groups synchronise inside run_task).
+    int task = blockIdx.x * kGroups + group;
+    if (task < ntasks) load_task(task, bufA, bufA2);
+    for (int base = blockIdx.x * kGroups; base < ntasks; base += 2 * stride) {
+        const int t0 = base + group, t1 = t0 + stride, t2 = t1 + stride;
+        if (t1 < ntasks) load_task(t1, bufB, bufB2);
+        if (t0 < ntasks) run_task(t0, bufA, bufA2, true);
+        else if constexpr (KW > 1) run_task(t0, bufA, bufA2, false);
+        if (base + stride >= ntasks) break;
+        if (t2 < ntasks) load_task(t2, bufA, bufA2);
+        if (t1 < ntasks) run_task(t1, bufB, bufB2, true);
+        else if constexpr (KW > 1) run_task(t1, bufB, bufB2, false);
+    }
+}
+
+// ------------------------------------------------------------ batch > 1 ----
+// NB batch rows per launch; x slices are loaded per task (L1/L2 resident).
 template <int FMT, int NB, int R, int MODE>
-__global__ void __launch_bounds__(256) gemv_kquant_kernel(const GemvArgs a) {
+__global__ void __launch_bounds__(256) gemv_kquant_kernel(const uint8_t* __restrict__ w, const uint8_t* __restrict__ w2,
+                                                          const int64_t row_bytes, const int rows, const int cols,
+                                                          const float* __restrict__ x, float* __restrict__ y,
+                                                          float* __restrict__ partial, const int batch, const int lpr,
+                                                          const int ntasks) {
     using F = typename FmtOf<FMT>::T;
     constexpr bool kDual = MODE == kSwiglu;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int S = a.cols >> 6;
-    const int lpr = a.lpr, P = kWave / lpr;
+    const int S = cols >> 6;
+    const int P = kWave / lpr;
     const int sub = lane / lpr, lir = lane - sub * lpr;
     const int ks = (S + lpr - 1) / lpr;
     const int rows_per_task = P * R;
 
-    for (int task = blockIdx.x * 4 + wave; task < a.ntasks; task += gridDim.x * 4) {
+    for (int task = blockIdx.x * 4 + wave; task < ntasks; task += gridDim.x * 4) {
         const int row0 = task * rows_per_task + sub;
         float acc[R][NB], acc2[R][NB];
 #pragma unroll
@@ -225,46 +346,30 @@ __global__ void __launch_bounds__(256) gemv_kquant_kernel(const GemvArgs a) {
                 typename F::Raw raw[R], raw2[kDual ? R : 1];
 #pragma unroll
                 for (int r = 0; r < R; ++r) {
-                    const int row = min(row0 + P * r, a.rows - 1);   // clamped rows are discarded
-                    F::load(a.w + (int64_t)row * a.row_bytes, slot, raw[r]);
-                    if constexpr (kDual) F::load(a.w2 + (int64_t)row * a.row_bytes, slot, raw2[r]);
-                }
-                typename F::Scale sc[R], sc2[kDual ? R : 1];
-#pragma unroll
-                for (int r = 0; r < R; ++r) {
-                    sc[r] = F::scale(raw[r], slot);
-                    if constexpr (kDual) sc2[r] = F::scale(raw2[r], slot);
+                    const int row = min(row0 + P * r, rows - 1);   // clamped rows are discarded
+                    F::load(w + (int64_t)row * row_bytes, slot, raw[r]);
+                    if constexpr (kDual) F::load(w2 + (int64_t)row * row_bytes, slot, raw2[r]);
                 }
 #pragma unroll
                 for (int b = 0; b < NB; ++b) {
-                    if (b < a.batch) {
+                    if (b < batch) {
                         float xs[64], X[F::kRuns];
-                        load_x<F>(a.x, a.cols, b, slot, xs, X);
+                        load_x<F>(x + (int64_t)b * cols, slot, xs, X);
 #pragma unroll
                         for (int r = 0; r < R; ++r) {
-                            float part[F::kRuns];
-#pragma unroll
-                            for (int i = 0; i < F::kRuns; ++i) part[i] = 0.0f;
-                            F::dot(raw[r], xs, part);
-                            acc[r][b] += F::combine(sc[r], part, X);
-                            if constexpr (kDual) {
-#pragma unroll
-                                for (int i = 0; i < F::kRuns; ++i) part[i] = 0.0f;
-                                F::dot(raw2[r], xs, part);
-                                acc2[r][b] += F::combine(sc2[r], part, X);
-                            }
+                            acc[r][b] += F::slot_dot(raw[r], slot, xs, X);
+                            if constexpr (kDual) acc2[r][b] += F::slot_dot(raw2[r], slot, xs, X);
                         }
                     }
                 }
             }
         }
-        // Reduce across the lpr lanes of each row; every lane of the row gets the sum.
 #pragma unroll
         for (int r = 0; r < R; ++r)
 #pragma unroll
             for (int b = 0; b < NB; ++b) {
-                acc[r][b] = group_sum(acc[r][b], lpr);
-                if constexpr (kDual) acc2[r][b] = group_sum(acc2[r][b], lpr);
+                acc[r][b] = lane_group_sum(acc[r][b], lpr);
+                if constexpr (kDual) acc2[r][b] = lane_group_sum(acc2[r][b], lpr);
             }
 
         float local_max[NB];
@@ -275,8 +380,8 @@ __global__ void __launch_bounds__(256) gemv_kquant_kernel(const GemvArgs a) {
             const int row = row0 + P * r;
 #pragma unroll
             for (int b = 0; b < NB; ++b) {
-                if (b >= a.batch || row >= a.rows) continue;
-                float* out = a.y + (int64_t)b * a.rows + row;
+                if (b >= batch || row >= rows) continue;
+                float* out = y + (int64_t)b * rows + row;
                 const float v = acc[r][b];
                 if constexpr (MODE == kLogits) local_max[b] = fmaxf(local_max[b], v);
                 if (lir == 0) {
@@ -287,12 +392,11 @@ __global__ void __launch_bounds__(256) gemv_kquant_kernel(const GemvArgs a) {
             }
         }
         if constexpr (MODE == kLogits) {
-            // max over the P rows of this pass set: lanes sub*lpr hold row partials
 #pragma unroll
             for (int b = 0; b < NB; ++b) {
                 float m = local_max[b];
                 for (int off = lpr; off < kWave; off <<= 1) m = fmaxf(m, __shfl_xor(m, off, kWave));
-                if (lane == 0 && b < a.batch) a.partial[(int64_t)b * a.ntasks + task] = m;
+                if (lane == 0 && b < batch) partial[(int64_t)b * ntasks + task] = m;
             }
         }
     }
@@ -308,27 +412,29 @@ __device__ __forceinline__ float plain_value(const uint8_t* row, int c) {
 }
 
 template <int FMT, int MODE>
-__global__ void __launch_bounds__(256) gemv_plain_kernel(const GemvArgs a) {
+__global__ void __launch_bounds__(256) gemv_plain_kernel(const uint8_t* __restrict__ w, const uint8_t* __restrict__ w2,
+                                                         const int64_t row_bytes, const int rows, const int cols,
+                                                         const float* __restrict__ x, float* __restrict__ y,
+                                                         float* __restrict__ partial, const int batch) {
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int ntasks = a.rows;  // one row per task
-    for (int row = blockIdx.x * 4 + wave; row < ntasks; row += gridDim.x * 4) {
-        const uint8_t* wr = a.w + (int64_t)row * a.row_bytes;
-        const uint8_t* wr2 = MODE == kSwiglu ? a.w2 + (int64_t)row * a.row_bytes : nullptr;
-        for (int b = 0; b < a.batch; ++b) {
-            const float* xb = a.x + (int64_t)b * a.cols;
+    for (int row = blockIdx.x * 4 + wave; row < rows; row += gridDim.x * 4) {
+        const uint8_t* wr = w + (int64_t)row * row_bytes;
+        const uint8_t* wr2 = MODE == kSwiglu ? w2 + (int64_t)row * row_bytes : nullptr;
+        for (int b = 0; b < batch; ++b) {
+            const float* xb = x + (int64_t)b * cols;
             float s = 0.0f, s2 = 0.0f;
-            for (int c = lane; c < a.cols; c += kWave) {
+            for (int c = lane; c < cols; c += kWave) {
                 s = fmaf(plain_value<FMT>(wr, c), xb[c], s);
                 if constexpr (MODE == kSwiglu) s2 = fmaf(plain_value<FMT>(wr2, c), xb[c], s2);
             }
-            s = group_sum(s, kWave);
-            if constexpr (MODE == kSwiglu) s2 = group_sum(s2, kWave);
+            s = lane_group_sum(s, kWave);
+            if constexpr (MODE == kSwiglu) s2 = lane_group_sum(s2, kWave);
             if (lane == 0) {
-                float* out = a.y + (int64_t)b * a.rows + row;
+                float* out = y + (int64_t)b * rows + row;
                 if constexpr (MODE == kStore || MODE == kLogits) *out = s;
                 else if constexpr (MODE == kAccumulate) *out += s;
                 else *out = swiglu(s, s2);
-                if constexpr (MODE == kLogits) a.partial[(int64_t)b * a.ntasks + row] = s;
+                if constexpr (MODE == kLogits) partial[(int64_t)b * rows + row] = s;
             }
         }
     }
