@@ -1,17 +1,24 @@
 """Benchmark of the MI355X detector path.
 
-python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload NAME] [--no-cpu]
+python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload NAME] [--batch B] [--no-cpu]
 
-Workloads (one JSON line each run):
-  gemv_q4k   4096x4096 Q4_K dequant-fused GEMV, batch 1, fp32 x (default)
+Workloads (one JSON line per run):
+  gemv_q4k    4096x4096 Q4_K dequant-fused GEMV, batch 1, fp32 x            (default)
+  mlp         SwiGLU MLP 2048 -> 6144 -> 2048, gate/up Q4_K, down Q6_K, --batch rows
+  lm_head     151936 x 2048 Q6_K vocabulary readout + margin argmax, --batch rows
+  attention   GQA decode attention, 16 sequences, contexts log-uniform in [512, 32768],
+              16 q / 4 kv heads, hd 128, K Q6_K / V Q4_K history, RoPE theta 1e6 on q
+  copy_calib  plain device-to-device copy of known size (PMC byte-counter calibration)
+
 A step is one pass of the hot path over one batch of synthetic input resident in
 HBM.  The timed region replays exactly K steps (captured in a HIP graph) between
-two synchronisations.  Matrices rotate through enough distinct copies to exceed
-3x the 256 MB Infinity Cache, so every step streams its weights from HBM.
+two synchronisations.  Weights (and the attention history) rotate through enough
+distinct copies to exceed 3x the 256 MB Infinity Cache, so every step streams
+them from HBM.
 
-roofline.achieved is the algorithmic bytes of one launch of the dominant kernel
-divided by that kernel's mean duration, measured live with HIP events recorded on
-the launching stream around individual launches.
+roofline.achieved = algorithmic bytes of one launch of the dominant kernel / that
+kernel's mean duration, measured with HIP events recorded on the launching
+stream around individual launches of that kernel.
 """
 import argparse
 import json
@@ -28,21 +35,25 @@ sys.path.insert(0, str(ROOT / "ray-tracing-attention_amd"))
 HBM_PEAK_GBS = 8000.0
 CACHE_BYTES = 256 << 20
 METRIC = "decode tokens/sec at batch 1/32 (9B-shape) + Q4_K GEMV GB/s, % of HBM peak"
+Q4_K, Q6_K = 12, 14
 
 
 def parse():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=2000)
-    ap.add_argument("--warmup", type=int, default=200)
-    ap.add_argument("--workload", default="gemv_q4k", choices=["gemv_q4k"])
+    ap.add_argument("--steps", type=int, default=1000)
+    ap.add_argument("--warmup", type=int, default=100)
+    ap.add_argument("--workload", default="gemv_q4k",
+                    choices=["gemv_q4k", "mlp", "lm_head", "attention", "copy_calib"])
+    ap.add_argument("--batch", type=int, default=None)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--eager", action="store_true", help="time eager launches instead of a graph replay")
     return ap.parse_args()
 
 
 def traffic_for(workload):
-    """HBM bytes per launch measured with rocprofv3 --pmc (profiles/traffic.json), if recorded."""
+    """HBM bytes per launch of the dominant kernel, from rocprofv3 --pmc (profiles/traffic.json)."""
     f = ROOT / "profiles" / "traffic.json"
     if f.is_file():
         return json.loads(f.read_text()).get(workload)
@@ -59,22 +70,21 @@ def cpu_model():
     return "unknown"
 
 
+def omp_threads():
+    return int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
+
+
+def rotation(torch, host_array, dev, min_total=3 * CACHE_BYTES, max_copies=256):
+    """Distinct device copies of host_array totalling more than min_total bytes."""
+    t0 = torch.from_numpy(np.ascontiguousarray(host_array)).to(dev)
+    n = int(min(max_copies, max(2, min_total // t0.numel() + 1)))
+    return [t0] + [t0.clone() for _ in range(n - 1)]
+
+
 def time_kernel(torch, launch, n=200):
-    """Mean duration (ms) of single launches bracketed by events on the launch stream."""
-    s = torch.cuda.current_stream()
-    starts = [torch.cuda.Event(enable_timing=True) for _ in range(n)]
-    ends = [torch.cuda.Event(enable_timing=True) for _ in range(n)]
-    for i in range(n):
-        starts[i].record(s)
-        launch(i)
-        ends[i].record(s)
-    torch.cuda.synchronize()
-    d = np.array([a.elapsed_time(b) for a, b in zip(starts, ends)])
-    return float(np.median(d)), float(d.mean())
-
-
-def timed_region(torch, launch, steps, warmup):
-    for i in range(warmup):
+    """Mean duration (ms) of one launch of the dominant kernel: n back-to-back launches captured
+    in a HIP graph, replayed between two events recorded on the launching stream."""
+    for i in range(10):
         launch(i)
     torch.cuda.synchronize()
     g = torch.cuda.CUDAGraph()
@@ -82,8 +92,38 @@ def timed_region(torch, launch, steps, warmup):
     s.wait_stream(torch.cuda.current_stream())
     with torch.cuda.stream(s):
         with torch.cuda.graph(g, stream=s):
-            for i in range(steps):
+            for i in range(n):
                 launch(i)
+    torch.cuda.synchronize()
+    g.replay()
+    torch.cuda.synchronize()
+    with torch.cuda.stream(s):
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record(s)
+        g.replay()
+        b.record(s)
+    torch.cuda.synchronize()
+    return a.elapsed_time(b) / n
+
+
+def timed_region(torch, step, steps, warmup, eager=False):
+    """Exactly `steps` steps captured in one graph; returns wall ms of one replay."""
+    for i in range(warmup):
+        step(i)
+    torch.cuda.synchronize()
+    if eager:
+        t0 = time.perf_counter()
+        for i in range(steps):
+            step(i)
+        torch.cuda.synchronize()
+        return (time.perf_counter() - t0) * 1e3
+    g = torch.cuda.CUDAGraph()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        with torch.cuda.graph(g, stream=s):
+            for i in range(steps):
+                step(i)
     torch.cuda.synchronize()
     g.replay()                      # graph warm-up (not timed)
     torch.cuda.synchronize()
@@ -93,64 +133,239 @@ def timed_region(torch, launch, steps, warmup):
     return (time.perf_counter() - t0) * 1e3
 
 
-def bench_gemv_q4k(torch, args):
+def cpu_time(fn, seconds):
+    fn()  # warm
+    n, t0 = 0, time.perf_counter()
+    while True:
+        fn()
+        n += 1
+        el = time.perf_counter() - t0
+        if el >= seconds:
+            return n, el
+
+
+def close(got, ref):
+    got, ref = np.asarray(got, np.float64), np.asarray(ref, np.float64)
+    err = float(np.max(np.abs(got - ref)))
+    peak = float(np.max(np.abs(ref)))
+    return {"max_abs_err": err, "peak": peak, "ok": bool(err <= 1e-5 + 1e-3 * peak)}
+
+
+# ------------------------------------------------------------------ workloads ----
+def w_gemv_q4k(torch, args, orc):
     from rta import ops, synth
     rows = cols = 4096
     dev = torch.device("cuda:0")
     rng = synth.rng_for(1)
-    w = synth.random_matrix(rng, 12, rows, cols)
+    w = synth.random_matrix(rng, Q4_K, rows, cols)
     x = rng.standard_normal((1, cols)).astype(np.float32)
-    wbytes = w.nbytes
-    ncopy = max(2, int(3 * CACHE_BYTES // wbytes) + 1)
-    w0 = torch.from_numpy(w).to(dev)
-    copies = [w0] + [w0.clone() for _ in range(ncopy - 1)]
+    copies = rotation(torch, w, dev)
     xd = torch.from_numpy(x).to(dev)
     y = torch.empty(1, rows, dtype=torch.float32, device=dev)
 
-    def launch(i):
-        ops.gemv(12, copies[i % ncopy], rows, cols, xd, y=y)
+    def step(i):
+        ops.gemv(Q4_K, copies[i % len(copies)], rows, cols, xd, y=y)
 
-    alg_bytes = wbytes + 4 * cols + 4 * rows
-    med, mean = time_kernel(torch, launch)
-    ms = timed_region(torch, launch, args.steps, args.warmup)
-    ms_step = ms / args.steps
-    # parity of the timed configuration against the oracle (one copy)
-    out = {
-        "value": alg_bytes / (ms_step * 1e-3) / 1e9,
-        "unit": "GB/s",
-        "ms_per_step": ms_step,
-        "dtype": "q4_k weights x fp32 activations, fp32 accumulate",
-        "config": {"workload": "Q4_K GEMV 4096x4096, batch 1 (single dequant-fused matrix-vector readout)",
-                   "rows": rows, "cols": cols, "batch": 1, "weight_copies_rotated": ncopy,
-                   "rotated_bytes": ncopy * wbytes, "seed": "20261110+1"},
-        "kernel": "gemv_kquant_kernel<Q4_K,NB=1,R=4,store>",
-        "alg_bytes_per_launch": alg_bytes,
-        "kernel_ms_median": med,
-        "kernel_ms_mean": mean,
-        "roofline": {"bound": "hbm", "achieved": alg_bytes / (med * 1e-3) / 1e9, "peak": HBM_PEAK_GBS,
-                     "unit": "GB/s", "frac": alg_bytes / (med * 1e-3) / 1e9 / HBM_PEAK_GBS,
-                     "traffic": traffic_for("gemv_q4k")},
-    }
-    host = {"w": w, "x": x, "rows": rows, "cols": cols, "alg_bytes": alg_bytes}
-    return out, host, lambda: y.cpu().numpy()
+    alg = w.nbytes + 4 * cols + 4 * rows
+    res = {"alg_bytes": alg, "kernel": "gemv_b1_kernel<Q4_K,R=2,store,KW=1>", "step": step, "kernel_launch": step,
+           "unit": "GB/s", "value_from_ms": lambda ms: alg / (ms * 1e-3) / 1e9,
+           "dtype": "q4_k weights x fp32 activations, fp32 accumulate",
+           "config": {"workload": "Q4_K GEMV 4096x4096, batch 1 (single dequant-fused matrix-vector readout)",
+                      "rows": rows, "cols": cols, "batch": 1, "weight_copies_rotated": len(copies),
+                      "seed": "20261110+1"}}
+
+    def check():
+        step(0)
+        return close(y.cpu().numpy(), orc.gemv_f64(Q4_K, w, rows, cols, x))
+
+    def cpu(seconds):
+        t = omp_threads()
+        n, el = cpu_time(lambda: orc.gemv_f32(Q4_K, w, rows, cols, x, t), seconds)
+        return {"value": alg * n / el / 1e9, "unit": "GB/s", "cores": t, "kind": "port",
+                "sample": f"{n} calls of the oracle's fp32-accumulating OpenMP Q4_K GEMV 4096x4096 batch 1 "
+                          f"in {el:.1f} s on {cpu_model()}"}
+    res["check"], res["cpu"] = check, cpu
+    return res
 
 
-def cpu_baseline_gemv(host, seconds):
-    sys.path.insert(0, str(ROOT / "oracle"))
-    import oracle as orc
-    threads = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
-    w, x = host["w"], host["x"]
-    orc.gemv_f32(12, w, host["rows"], host["cols"], x, threads)  # warm
-    n, t0 = 0, time.perf_counter()
-    while True:
-        orc.gemv_f32(12, w, host["rows"], host["cols"], x, threads)
-        n += 1
-        el = time.perf_counter() - t0
-        if el >= seconds:
-            break
-    return {"value": host["alg_bytes"] * n / el / 1e9, "unit": "GB/s", "cores": threads, "kind": "port",
-            "sample": f"{n} calls of the oracle's fp32-accumulating OpenMP Q4_K GEMV (4096x4096, batch 1) "
-                      f"in {el:.1f} s on {cpu_model()}"}
+def w_mlp(torch, args, orc):
+    from rta import ops, synth
+    hidden, inter = 2048, 6144
+    batch = args.batch or 1
+    dev = torch.device("cuda:0")
+    rng = synth.rng_for(2)
+    wg = synth.random_matrix(rng, Q4_K, inter, hidden)
+    wu = synth.random_matrix(rng, Q4_K, inter, hidden)
+    wd = synth.random_matrix(rng, Q6_K, hidden, inter)
+    x = rng.standard_normal((batch, hidden)).astype(np.float32)
+    packed = np.concatenate([wg.ravel(), wu.ravel(), wd.ravel()])
+    copies = rotation(torch, packed, dev)
+    ng, nd = wg.size, wd.size
+    xd = torch.from_numpy(x).to(dev)
+    act = torch.empty(batch, inter, dtype=torch.float32, device=dev)
+    y = torch.empty(batch, hidden, dtype=torch.float32, device=dev)
+    fm = (Q4_K, Q4_K, Q6_K)
+
+    def step(i):
+        c = copies[i % len(copies)]
+        ops.mlp_swiglu(fm, c[:ng], c[ng:2 * ng], c[2 * ng:], hidden, inter, xd, y=y, act=act)
+
+    alg = packed.nbytes + batch * (hidden * 4 + inter * 4 + hidden * 4)
+    res = {"alg_bytes": alg, "kernel": "gemv (gate+up fused SwiGLU) then gemv (down)", "step": step,
+           "kernel_launch": step, "unit": "GB/s", "value_from_ms": lambda ms: alg / (ms * 1e-3) / 1e9,
+           "dtype": "q4_k/q6_k weights x fp32 activations, fp32 accumulate",
+           "config": {"workload": f"SwiGLU MLP 2048->6144->2048 (gate/up Q4_K, down Q6_K), batch {batch}",
+                      "hidden": hidden, "intermediate": inter, "batch": batch, "weight_copies_rotated": len(copies),
+                      "seed": "20261110+2"}}
+
+    def check():
+        step(0)
+        ract, ry = orc.mlp_swiglu(fm, wg, wu, wd, hidden, inter, x)
+        a, b = close(act.cpu().numpy(), ract), close(y.cpu().numpy(), ry)
+        return {"activation": a, "output": b, "ok": a["ok"] and b["ok"]}
+
+    def cpu(seconds):
+        n, el = cpu_time(lambda: orc.mlp_swiglu(fm, wg, wu, wd, hidden, inter, x), seconds)
+        return {"value": alg * n / el / 1e9, "unit": "GB/s", "cores": omp_threads(), "kind": "port",
+                "sample": f"{n} calls of the oracle's fp64 SwiGLU MLP (batch {batch}) in {el:.1f} s on {cpu_model()}"}
+    res["check"], res["cpu"] = check, cpu
+    return res
+
+
+def w_lm_head(torch, args, orc):
+    from rta import ops, synth
+    vocab, hidden = 151936, 2048
+    batch = args.batch or 1
+    dev = torch.device("cuda:0")
+    rng = synth.rng_for(4)
+    w = synth.random_matrix(rng, Q6_K, vocab, hidden)
+    h = (rng.standard_normal((batch, hidden)) * 2.0).astype(np.float32)
+    copies = rotation(torch, w, dev)
+    hd = torch.from_numpy(h).to(dev)
+    logits = torch.empty(batch, vocab, dtype=torch.float32, device=dev)
+    ids = torch.empty(batch, dtype=torch.int32, device=dev)
+    ws = torch.empty(ops.lm_head_workspace_bytes(vocab, batch), dtype=torch.uint8, device=dev)
+
+    def step(i):
+        ops.lm_head(Q6_K, copies[i % len(copies)], vocab, hidden, hd, margin=1e-4, workspace=ws, logits=logits,
+                    ids=ids)
+
+    def readout(i):  # the dominant kernel alone: the Q6_K logits GEMV
+        ops.gemv(Q6_K, copies[i % len(copies)], vocab, hidden, hd, y=logits)
+
+    alg = w.nbytes + batch * (hidden * 4 + vocab * 4 + 4)
+    alg_k = w.nbytes + batch * (hidden * 4 + vocab * 4)
+    res = {"alg_bytes": alg, "alg_bytes_kernel": alg_k, "kernel": "Q6_K logits GEMV (gemv_b1_kernel<Q6_K,R=2,store,KW=1>)",
+           "step": step, "kernel_launch": readout, "unit": "GB/s", "value_from_ms": lambda ms: alg / (ms * 1e-3) / 1e9,
+           "dtype": "q6_k weights x fp32 activations, fp32 accumulate",
+           "config": {"workload": f"LM head 151936x2048 Q6_K + margin argmax, batch {batch}", "vocab": vocab,
+                      "hidden": hidden, "batch": batch, "weight_copies_rotated": len(copies),
+                      "seed": "20261110+4"}}
+
+    def check():
+        step(0)
+        lg = logits.cpu().numpy()
+        ref = orc.gemv_f64(Q6_K, w, vocab, hidden, h)
+        c = close(lg, ref)
+        got_ids = ids.cpu().numpy().view(np.uint32)
+        rule = [orc.argmax_margin_f32(lg[b], 1e-4) for b in range(batch)]
+        c["ids_match_rule"] = bool(list(got_ids) == rule)
+        c["ids_match_oracle"] = bool(list(got_ids) == [orc.argmax_margin_f64(ref[b], 1e-4) for b in range(batch)])
+        c["ok"] = c["ok"] and c["ids_match_rule"]
+        return c
+
+    def cpu(seconds):
+        t = omp_threads()
+        n, el = cpu_time(lambda: orc.gemv_f32(Q6_K, w, vocab, hidden, h, t), seconds)
+        return {"value": alg * n / el / 1e9, "unit": "GB/s", "cores": t, "kind": "port",
+                "sample": f"{n} calls of the oracle's fp32 OpenMP Q6_K readout 151936x2048 batch {batch} "
+                          f"in {el:.1f} s on {cpu_model()}"}
+    res["check"], res["cpu"] = check, cpu
+    return res
+
+
+def w_attention(torch, args, orc):
+    from rta import ops, synth
+    nseq, hq, hkv, hd = 16, 16, 4, 128
+    dev = torch.device("cuda:0")
+    rng = synth.rng_for(3)
+    ctx = synth.log_uniform_lengths(rng, nseq, 512, 32768)
+    base = np.concatenate([[0], np.cumsum(ctx)[:-1]]).astype(np.int64)
+    total = int(ctx.sum())
+    kvw = hkv * hd
+    packets = synth.random_packets(rng, total, kvw, Q6_K, Q4_K)
+    q = rng.standard_normal((nseq, hq, hd)).astype(np.float32)
+    copies = rotation(torch, packets, dev)
+    qd = torch.from_numpy(q).to(dev)
+    qr = torch.empty_like(qd)
+    pos = torch.from_numpy(ctx - 1).to(dev)
+    based = torch.from_numpy(base).to(dev)
+    ctxd = torch.from_numpy(ctx.astype(np.int32)).to(dev)
+    cap = int(ctx.max())
+    ws = torch.empty(ops.decode_attention_workspace_bytes(nseq, hq, hkv, hd, cap), dtype=torch.uint8, device=dev)
+    out = torch.empty_like(qd)
+
+    def attn(i):
+        ops.decode_attention(qr, copies[i % len(copies)], Q6_K, Q4_K, based, ctxd, cap, cap, hkv, workspace=ws,
+                             out=out)
+
+    def step(i):
+        qr.copy_(qd)
+        ops.rope(qr, pos, theta=1e6)
+        attn(i)
+
+    alg = total * (2 * 354) + 2 * nseq * hq * hd * 4
+    res = {"alg_bytes": alg, "kernel": "attn_chunk_kernel<Q6_K,Q4_K,G=4> + attn_merge_kernel", "step": step,
+           "kernel_launch": attn, "unit": "GB/s", "value_from_ms": lambda ms: alg / (ms * 1e-3) / 1e9,
+           "dtype": "q6_k keys / q4_k values x fp32 queries, fp32 softmax",
+           "config": {"workload": "GQA decode attention, 16 seq, ctx log-uniform [512,32768], 16q/4kv heads, "
+                                  "hd 128, K Q6_K V Q4_K, RoPE 1e6",
+                      "contexts": [int(c) for c in ctx], "sum_context": total, "history_copies_rotated": len(copies),
+                      "seed": "20261110+3"}}
+
+    def check():
+        step(0)
+        qrot = np.stack([orc.rope(q[s], ctx[s] - 1, theta=1e6) for s in range(nseq)])
+        # sampled: the oracle over all 16 sequences at full length takes minutes; check 4 of them
+        pick = [int(i) for i in np.argsort(ctx)[[0, 5, 10, 15]]]
+        sub_base = np.concatenate([[0], np.cumsum(ctx[pick])[:-1]]).astype(np.int64)
+        sub_pk = np.concatenate([packets[base[s]:base[s] + ctx[s]] for s in pick])
+        ro, rm, rz = orc.decode_attention(qrot[pick], sub_pk, Q6_K, Q4_K, sub_base, ctx[pick], cap, hkv)
+        c = close(out.cpu().numpy()[pick], ro)
+        c["sequences_checked"] = pick
+        return c
+
+    def cpu(seconds):
+        sub = int(np.argmin(ctx))
+        qrot = orc.rope(q[sub], ctx[sub] - 1, theta=1e6)[None]
+        pk = packets[base[sub]:base[sub] + ctx[sub]]
+        n, el = cpu_time(lambda: orc.decode_attention(qrot, pk, Q6_K, Q4_K, [0], [ctx[sub]], cap, hkv), seconds)
+        by = int(ctx[sub]) * 708 + 2 * hq * hd * 4
+        return {"value": by * n / el / 1e9, "unit": "GB/s", "cores": omp_threads(), "kind": "port",
+                "sample": f"{n} oracle attention calls over one sequence of {int(ctx[sub])} positions "
+                          f"(16 heads) in {el:.1f} s on {cpu_model()}"}
+    res["check"], res["cpu"] = check, cpu
+    return res
+
+
+def w_copy_calib(torch, args, orc):
+    dev = torch.device("cuda:0")
+    n = 64 << 20
+    src = [torch.empty(n, dtype=torch.uint8, device=dev).fill_(1) for _ in range(14)]
+    dst = torch.empty(n, dtype=torch.uint8, device=dev)
+
+    def step(i):
+        dst.copy_(src[i % len(src)])
+
+    res = {"alg_bytes": 2 * n, "kernel": "device-to-device copy of 64 MiB", "step": step, "kernel_launch": step,
+           "unit": "GB/s", "value_from_ms": lambda ms: 2 * n / (ms * 1e-3) / 1e9, "dtype": "u8",
+           "config": {"workload": "plain copy 64 MiB (read 64 MiB + write 64 MiB), PMC calibration"},
+           "check": lambda: {"ok": True}, "cpu": None}
+    return res
+
+
+WORKLOADS = {"gemv_q4k": w_gemv_q4k, "mlp": w_mlp, "lm_head": w_lm_head, "attention": w_attention,
+             "copy_calib": w_copy_calib}
 
 
 def main():
@@ -162,23 +377,25 @@ def main():
     import torch
     from rta import _lib
     _lib.load()
-    if args.workload == "gemv_q4k":
-        out, host, fetch = bench_gemv_q4k(torch, args)
-        sys.path.insert(0, str(ROOT / "oracle"))
-        import oracle as orc
-        ref = orc.gemv_f64(12, host["w"], host["rows"], host["cols"], host["x"])
-        got = fetch()
-        err = float(np.max(np.abs(got - ref)))
-        out["parity"] = {"max_abs_err": err, "peak": float(np.abs(ref).max()),
-                         "ok": bool(err <= 1e-5 + 1e-3 * np.abs(ref).max())}
-        cpu = None if args.no_cpu else cpu_baseline_gemv(host, args.cpu_seconds)
-    line = {"metric": METRIC, "value": out["value"], "unit": out["unit"], "n_gpus": 1, "steps": args.steps,
-            "warmup": args.warmup, "ms_per_step": out["ms_per_step"], "higher_is_better": True,
-            "scaling": "weak", "vs_baseline": None, "dtype": out["dtype"], "data": "synthetic",
-            "config": out["config"], "roofline": out["roofline"], "cpu_baseline": cpu,
-            "kernel": out["kernel"], "kernel_ms_median": out["kernel_ms_median"],
-            "kernel_ms_mean": out["kernel_ms_mean"], "alg_bytes_per_launch": out["alg_bytes_per_launch"],
-            "parity": out["parity"]}
+    sys.path.insert(0, str(ROOT / "oracle"))
+    import oracle as orc
+    wl = WORKLOADS[args.workload](torch, args, orc)
+    parity = wl["check"]()
+    k_mean = time_kernel(torch, wl["kernel_launch"])
+    ms = timed_region(torch, wl["step"], args.steps, args.warmup, args.eager)
+    ms_step = ms / args.steps
+    alg_k = wl.get("alg_bytes_kernel", wl["alg_bytes"])
+    achieved = alg_k / (k_mean * 1e-3) / 1e9
+    cpu = None if (args.no_cpu or wl["cpu"] is None) else wl["cpu"](args.cpu_seconds)
+    line = {"metric": METRIC, "value": wl["value_from_ms"](ms_step), "unit": wl["unit"], "n_gpus": 1,
+            "steps": args.steps, "warmup": args.warmup, "ms_per_step": ms_step, "higher_is_better": True,
+            "scaling": "weak", "vs_baseline": None, "dtype": wl["dtype"], "data": "synthetic",
+            "timing": "eager launches" if args.eager else "one HIP graph replay of all steps",
+            "config": wl["config"],
+            "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                         "frac": achieved / HBM_PEAK_GBS, "traffic": traffic_for(args.workload)},
+            "cpu_baseline": cpu, "kernel": wl["kernel"], "kernel_ms_mean": k_mean,
+            "alg_bytes_per_launch": alg_k, "alg_bytes_per_step": wl["alg_bytes"], "parity": parity}
     print(json.dumps(line), flush=True)
 
 
