@@ -205,10 +205,11 @@ def w_mlp(torch, args, orc):
     act = torch.empty(batch, inter, dtype=torch.float32, device=dev)
     y = torch.empty(batch, hidden, dtype=torch.float32, device=dev)
     fm = (Q4_K, Q4_K, Q6_K)
+    ws = torch.empty(max(1, ops.mlp_workspace_bytes(Q4_K, Q6_K, hidden, inter, batch)), dtype=torch.uint8, device=dev)
 
     def step(i):
         c = copies[i % len(copies)]
-        ops.mlp_swiglu(fm, c[:ng], c[ng:2 * ng], c[2 * ng:], hidden, inter, xd, y=y, act=act)
+        ops.mlp_swiglu(fm, c[:ng], c[ng:2 * ng], c[2 * ng:], hidden, inter, xd, y=y, act=act, workspace=ws)
 
     alg = packed.nbytes + batch * (hidden * 4 + inter * 4 + hidden * 4)
     res = {"alg_bytes": alg, "kernel": "gemv (gate+up fused SwiGLU) then gemv (down)", "step": step,
@@ -244,14 +245,15 @@ def w_lm_head(torch, args, orc):
     hd = torch.from_numpy(h).to(dev)
     logits = torch.empty(batch, vocab, dtype=torch.float32, device=dev)
     ids = torch.empty(batch, dtype=torch.int32, device=dev)
-    ws = torch.empty(ops.lm_head_workspace_bytes(vocab, batch), dtype=torch.uint8, device=dev)
+    ws = torch.empty(ops.lm_head_workspace_bytes(Q6_K, vocab, hidden, batch), dtype=torch.uint8, device=dev)
+    gws = torch.empty(max(1, ops.gemv_workspace_bytes(Q6_K, vocab, hidden, batch)), dtype=torch.uint8, device=dev)
 
     def step(i):
         ops.lm_head(Q6_K, copies[i % len(copies)], vocab, hidden, hd, margin=1e-4, workspace=ws, logits=logits,
                     ids=ids)
 
     def readout(i):  # the dominant kernel alone: the Q6_K logits GEMV
-        ops.gemv(Q6_K, copies[i % len(copies)], vocab, hidden, hd, y=logits)
+        ops.gemv(Q6_K, copies[i % len(copies)], vocab, hidden, hd, y=logits, workspace=gws)
 
     alg = w.nbytes + batch * (hidden * 4 + vocab * 4 + 4)
     alg_k = w.nbytes + batch * (hidden * 4 + vocab * 4)

@@ -70,31 +70,39 @@ int rta_dequant(int fmt, const void* src, int64_t n, float* out, rta_stream_t st
 
 /* y[b, r] (=|+=) sum_c W[r, c] x[b, c],  b < batch, r < rows.
  *   x: [batch, cols] fp32 row-major, y: [batch, rows] fp32.
- *   K-quants need cols % 256 == 0; W 16-byte aligned (Q4_K) / 4-byte (Q6_K).
+ *   K-quants need cols % 256 == 0; W 16-byte aligned (Q4_K) / 2-byte (Q6_K).
+ *   Batch tiles of 8 or more K-quant rows run on the matrix cores and need a
+ *   workspace of rta_gemv_workspace_bytes() (256-byte aligned); 0 bytes otherwise.
  * Replaces the projection detector, resident_math.comp:39-75 (op 2, indices
- * 0/1/2/4/6/8) dispatched by Resident::launch, optical_resident.cpp:304-347. */
+ * 0/1/2/4/6/8) dispatched by Resident::launch, optical_resident.cpp:304-347, and its
+ * batched pipelines (optical_resident.cpp:168,343; resident_batch2.comp). */
+size_t rta_gemv_workspace_bytes(int fmt, int rows, int cols, int batch);
 int rta_gemv(int fmt, const void* w, int rows, int cols, const float* x, int batch,
-             float* y, int epilogue, rta_stream_t stream);
+             float* y, int epilogue, void* workspace, size_t workspace_bytes,
+             rta_stream_t stream);
 
 /* SwiGLU MLP: act = sign(g) sign(u) |g| |u| sigmoid(g) with g = Wg x, u = Wu x
  * ([batch, inter]); then y (=|+=) Wd act ([batch, hidden]).
- *   Wg, Wu: [inter, hidden]; Wd: [hidden, inter].
+ *   Wg, Wu: [inter, hidden] (one format); Wd: [hidden, inter].
+ *   Workspace: rta_mlp_workspace_bytes() (0 for batch < 8).
  * Replaces Resident::executeMLP (optical_resident.cpp:484-491): op 2 index 3
  * (resident_math.comp:54-58,71) then op 2 index 4 with the residual (:70).
  * mlpCheck (optical_resident.cpp:922-949) is epilogue STORE (state zeroed). */
+size_t rta_mlp_workspace_bytes(int fmt_g, int fmt_d, int hidden, int inter, int batch);
 int rta_mlp_swiglu(int fmt_g, const void* wg, int fmt_u, const void* wu,
                    int fmt_d, const void* wd, int hidden, int inter,
                    const float* x, int batch, float* act, float* y, int epilogue,
-                   rta_stream_t stream);
+                   void* workspace, size_t workspace_bytes, rta_stream_t stream);
 
 /* LM-head vocabulary readout with fused argmax.
  *   logits[b, v] = sum_k W[v, k] h[b, k]   (fp32, all v < vocab)
  *   ids[b] = lowest v with logits[b, v] >= M - margin*|M|, M = max_v logits[b, v]
  *   (fp32, no fma; margin 0 is the reference's exact-tie rule).
+ *   Workspace: rta_lm_head_workspace_bytes() (always needed; 256-byte aligned).
  * Replaces Resident::word (optical_resident.cpp:523-530): ops 11, 24, 16, 17, 23
  * (resident_math.comp:99-105,117-130,152-153) and the vocabulary ray query
  * (resident_ray.comp:91-116), which always returned every word. */
-size_t rta_lm_head_workspace_bytes(int vocab, int batch);
+size_t rta_lm_head_workspace_bytes(int fmt, int vocab, int hidden, int batch);
 int rta_lm_head(int fmt, const void* w, int vocab, int hidden, const float* h, int batch,
                 float margin, float* logits, uint32_t* ids,
                 void* workspace, size_t workspace_bytes, rta_stream_t stream);

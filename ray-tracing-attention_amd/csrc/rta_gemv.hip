@@ -2,6 +2,7 @@
 // LM-head readout with fused margin argmax (gfx950).
 #include <math.h>
 
+#include "rta_gemm.hpp"
 #include "rta_gemv.hpp"
 #include "rta_host.hpp"
 
@@ -213,16 +214,94 @@ static int check_matrix(int fmt, const void* w, int rows, int cols) {
     return RTA_OK;
 }
 
-// Runs one projection over the whole batch, in batch tiles of at most 8 rows.
-// For kLogits, partial receives per-task maxima laid out [tile row][ntasks] inside
-// the tile's [8 x rows] region, and *ntasks_out / *rows_per_task_out the plan.
+// ------------------------------------------------------------ MFMA path ----
+constexpr int kMfmaMinBatch = 8;   // batch tiles from this size use the matrix cores
+constexpr int kMfmaRT = 2;         // 16-row tiles per wave: 128 rows per workgroup
+
+struct MmaPlan {
+    int total_rows, row_blocks, nslab, sb_per_slab, grid;
+    size_t x_bytes, part_bytes;
+};
+
+static MmaPlan plan_mfma(int rows, int cols, bool dual) {
+    MmaPlan p{};
+    p.total_rows = dual ? 2 * rows : rows;
+    p.row_blocks = (p.total_rows + 64 * kMfmaRT - 1) / (64 * kMfmaRT);
+    const int nsb = cols / 256;
+    int want = (512 + p.row_blocks - 1) / p.row_blocks;   // aim for >= 512 workgroups
+    if (want < 1) want = 1;
+    if (want > nsb) want = nsb;
+    p.sb_per_slab = (nsb + want - 1) / want;
+    p.nslab = (nsb + p.sb_per_slab - 1) / p.sb_per_slab;
+    p.grid = p.row_blocks * p.nslab;
+    p.x_bytes = (size_t)kMaxBatchTile * cols * 2 * 2 + (size_t)kMaxBatchTile * (cols / 32) * 2 * 2 +
+                kMaxBatchTile * sizeof(float);
+    p.x_bytes = (p.x_bytes + 255) & ~(size_t)255;
+    p.part_bytes = (size_t)p.nslab * kMaxBatchTile * p.total_rows * sizeof(float);
+    return p;
+}
+
+static GemmX carve_x(void* ws, int cols) {
+    uint8_t* b = static_cast<uint8_t*>(ws);
+    GemmX x;
+    x.hi = reinterpret_cast<_Float16*>(b);
+    x.lo = reinterpret_cast<_Float16*>(b + (size_t)kMaxBatchTile * cols * 2);
+    x.gs = reinterpret_cast<_Float16*>(b + (size_t)kMaxBatchTile * cols * 4);
+    x.inv = reinterpret_cast<float*>(b + (size_t)kMaxBatchTile * cols * 4 + (size_t)kMaxBatchTile * (cols / 32) * 4);
+    return x;
+}
+
+// Bytes of workspace one K-quant projection needs (0 when the VALU paths serve it).
+static size_t projection_ws(int fmt, int rows, int cols, int batch, bool dual) {
+    if (!(fmt == RTA_Q4_K || fmt == RTA_Q6_K) || batch < kMfmaMinBatch) return 0;
+    const MmaPlan p = plan_mfma(rows, cols, dual);
+    return p.x_bytes + p.part_bytes;
+}
+
+template <int FMT, int MODE>
+static void launch_mfma_fmt(int nbt, const MmaPlan& p, const Launch& l, const GemmX& xp, float* part, hipStream_t s) {
+    const dim3 g(p.grid), b(256);
+    if (nbt == 1)
+        hipLaunchKernelGGL((gemm_mfma_kernel<FMT, kMfmaRT, 1, 2, MODE>), g, b, 0, s, l.w, l.w2, l.row_bytes, l.rows,
+                           l.cols, xp, l.batch, l.y, part, p.row_blocks, p.sb_per_slab);
+    else
+        hipLaunchKernelGGL((gemm_mfma_kernel<FMT, kMfmaRT, 2, 2, MODE>), g, b, 0, s, l.w, l.w2, l.row_bytes, l.rows,
+                           l.cols, xp, l.batch, l.y, part, p.row_blocks, p.sb_per_slab);
+}
+
+// One batch tile (<= 32 rows) through xprep -> MFMA GEMM -> fixed-order slab reduce.
+template <int MODE>
+static hipError_t run_mfma(int fmt, const Launch& l, void* ws, float* pmax, int* ntasks_out, int* rpt_out,
+                           hipStream_t s) {
+    const MmaPlan p = plan_mfma(l.rows, l.cols, MODE == kSwiglu);
+    GemmX xp = carve_x(ws, l.cols);
+    float* part = reinterpret_cast<float*>(static_cast<uint8_t*>(ws) + p.x_bytes);
+    hipLaunchKernelGGL(xprep_kernel, dim3(kMaxBatchTile), dim3(256), 0, s, l.x, l.cols, l.batch, xp);
+    const int nbt = l.batch > 16 ? 2 : 1;
+    if (fmt == RTA_Q4_K) launch_mfma_fmt<RTA_Q4_K, MODE>(nbt, p, l, xp, part, s);
+    else launch_mfma_fmt<RTA_Q6_K, MODE>(nbt, p, l, xp, part, s);
+    const dim3 rg((l.rows + 255) / 256, l.batch);
+    hipLaunchKernelGGL((gemm_reduce_kernel<MODE>), rg, dim3(256), 0, s, part, p.nslab, l.rows, l.batch, l.y, pmax);
+    if (ntasks_out) *ntasks_out = (int)rg.x;
+    if (rpt_out) *rpt_out = 256;
+    return hipGetLastError();
+}
+
+// Runs one projection over the whole batch: K-quant tiles of >= 8 rows on the matrix
+// cores (32 rows per tile), smaller ones on the VALU kernels (8 rows per tile).
+// For kLogits, partial receives per-task maxima laid out [tile row][ntasks] inside the
+// tile's [tile x rows] region; *ntasks_out / *rows_per_task_out describe the last tile.
 template <int MODE>
 static int run_projection(int fmt, const void* w, const void* w2, int rows, int cols, const float* x, int batch,
-                          float* y, float* partial, int* ntasks_out, int* rows_per_task_out, hipStream_t s) {
+                          float* y, float* partial, int* ntasks_out, int* rows_per_task_out, void* ws,
+                          size_t ws_bytes, hipStream_t s, int path_batch = 0) {
     const int64_t row_bytes = host::row_bytes(fmt, cols);
     int b0 = 0;
+    // The path depends on the whole batch, so a row's result never depends on tiling.
+    const bool mma = is_kquant(fmt) && (path_batch > 0 ? path_batch : batch) >= kMfmaMinBatch;
     while (b0 < batch) {
-        const int chunk = batch - b0 < 8 ? batch - b0 : 8;
+        const int cap = mma ? kMaxBatchTile : 8;
+        const int chunk = batch - b0 < cap ? batch - b0 : cap;
         Launch l{};
         l.w = static_cast<const uint8_t*>(w);
         l.w2 = static_cast<const uint8_t*>(w2);
@@ -234,7 +313,10 @@ static int run_projection(int fmt, const void* w, const void* w2, int rows, int 
         l.batch = chunk;
         l.partial = partial ? partial + (int64_t)b0 * rows : nullptr;
         hipError_t e;
-        if (is_kquant(fmt)) {
+        if (mma) {
+            if (!ws || ws_bytes < projection_ws(fmt, rows, cols, chunk, MODE == kSwiglu)) return RTA_ERR_WORKSPACE;
+            e = run_mfma<MODE>(fmt, l, ws, l.partial, ntasks_out, rows_per_task_out, s);
+        } else if (is_kquant(fmt)) {
             const Plan p = plan_kquant(rows, cols, chunk, MODE == kSwiglu);
             if (ntasks_out) *ntasks_out = p.ntasks;
             if (rows_per_task_out) *rows_per_task_out = p.rows_per_task;
@@ -305,22 +387,41 @@ int rta_dequant(int fmt, const void* src, int64_t n, float* out, rta_stream_t st
     return hipGetLastError() == hipSuccess ? RTA_OK : RTA_ERR_LAUNCH;
 }
 
+size_t rta_gemv_workspace_bytes(int fmt, int rows, int cols, int batch) {
+    if (rows <= 0 || cols <= 0 || batch <= 0 || (is_kquant(fmt) && cols % 256)) return 0;
+    return projection_ws(fmt, rows, cols, batch < kMaxBatchTile ? batch : kMaxBatchTile, false);
+}
+
 int rta_gemv(int fmt, const void* w, int rows, int cols, const float* x, int batch, float* y, int epilogue,
-             rta_stream_t stream) {
+             void* workspace, size_t workspace_bytes, rta_stream_t stream) {
     int rc = check_matrix(fmt, w, rows, cols);
     if (rc) return rc;
     if (!x || !y) return RTA_ERR_NULL;
     if (batch <= 0) return RTA_ERR_SHAPE;
     if (epilogue != RTA_EPI_STORE && epilogue != RTA_EPI_ACCUMULATE) return RTA_ERR_RANGE;
-    if (reinterpret_cast<uintptr_t>(x) % 16 || reinterpret_cast<uintptr_t>(y) % 4) return RTA_ERR_ALIGN;
+    if (reinterpret_cast<uintptr_t>(x) % 16 || reinterpret_cast<uintptr_t>(y) % 4 ||
+        reinterpret_cast<uintptr_t>(workspace) % 256)
+        return RTA_ERR_ALIGN;
+    if (workspace_bytes < rta_gemv_workspace_bytes(fmt, rows, cols, batch)) return RTA_ERR_WORKSPACE;
     hipStream_t s = (hipStream_t)stream;
     if (epilogue == RTA_EPI_STORE)
-        return run_projection<kStore>(fmt, w, nullptr, rows, cols, x, batch, y, nullptr, nullptr, nullptr, s);
-    return run_projection<kAccumulate>(fmt, w, nullptr, rows, cols, x, batch, y, nullptr, nullptr, nullptr, s);
+        return run_projection<kStore>(fmt, w, nullptr, rows, cols, x, batch, y, nullptr, nullptr, nullptr, workspace,
+                                      workspace_bytes, s);
+    return run_projection<kAccumulate>(fmt, w, nullptr, rows, cols, x, batch, y, nullptr, nullptr, nullptr, workspace,
+                                       workspace_bytes, s);
+}
+
+size_t rta_mlp_workspace_bytes(int fmt_g, int fmt_d, int hidden, int inter, int batch) {
+    if (hidden <= 0 || inter <= 0 || batch <= 0) return 0;
+    const int tile = batch < kMaxBatchTile ? batch : kMaxBatchTile;
+    const size_t a = projection_ws(fmt_g, inter, hidden, tile, true);
+    const size_t b = projection_ws(fmt_d, hidden, inter, tile, false);
+    return a > b ? a : b;
 }
 
 int rta_mlp_swiglu(int fmt_g, const void* wg, int fmt_u, const void* wu, int fmt_d, const void* wd, int hidden,
-                   int inter, const float* x, int batch, float* act, float* y, int epilogue, rta_stream_t stream) {
+                   int inter, const float* x, int batch, float* act, float* y, int epilogue, void* workspace,
+                   size_t workspace_bytes, rta_stream_t stream) {
     int rc = check_matrix(fmt_g, wg, inter, hidden);
     if (rc) return rc;
     if ((rc = check_matrix(fmt_u, wu, inter, hidden))) return rc;
@@ -330,19 +431,25 @@ int rta_mlp_swiglu(int fmt_g, const void* wg, int fmt_u, const void* wu, int fmt
     if (batch <= 0) return RTA_ERR_SHAPE;
     if (epilogue != RTA_EPI_STORE && epilogue != RTA_EPI_ACCUMULATE) return RTA_ERR_RANGE;
     if (reinterpret_cast<uintptr_t>(x) % 16 || reinterpret_cast<uintptr_t>(act) % 16 ||
-        reinterpret_cast<uintptr_t>(y) % 4)
+        reinterpret_cast<uintptr_t>(y) % 4 || reinterpret_cast<uintptr_t>(workspace) % 256)
         return RTA_ERR_ALIGN;
+    if (workspace_bytes < rta_mlp_workspace_bytes(fmt_g, fmt_d, hidden, inter, batch)) return RTA_ERR_WORKSPACE;
     hipStream_t s = (hipStream_t)stream;
-    rc = run_projection<kSwiglu>(fmt_g, wg, wu, inter, hidden, x, batch, act, nullptr, nullptr, nullptr, s);
+    rc = run_projection<kSwiglu>(fmt_g, wg, wu, inter, hidden, x, batch, act, nullptr, nullptr, nullptr, workspace,
+                                 workspace_bytes, s);
     if (rc) return rc;
     if (epilogue == RTA_EPI_STORE)
-        return run_projection<kStore>(fmt_d, wd, nullptr, hidden, inter, act, batch, y, nullptr, nullptr, nullptr, s);
-    return run_projection<kAccumulate>(fmt_d, wd, nullptr, hidden, inter, act, batch, y, nullptr, nullptr, nullptr, s);
+        return run_projection<kStore>(fmt_d, wd, nullptr, hidden, inter, act, batch, y, nullptr, nullptr, nullptr,
+                                      workspace, workspace_bytes, s);
+    return run_projection<kAccumulate>(fmt_d, wd, nullptr, hidden, inter, act, batch, y, nullptr, nullptr, nullptr,
+                                       workspace, workspace_bytes, s);
 }
 
-size_t rta_lm_head_workspace_bytes(int vocab, int batch) {
-    if (vocab <= 0 || batch <= 0) return 0;
-    return (size_t)vocab * (size_t)batch * sizeof(float);
+size_t rta_lm_head_workspace_bytes(int fmt, int vocab, int hidden, int batch) {
+    if (vocab <= 0 || hidden <= 0 || batch <= 0 || !host::valid_format(fmt)) return 0;
+    // per-task maxima [batch][vocab] (upper bound), then the matrix-core scratch of one tile
+    const size_t maxima = ((size_t)vocab * (size_t)batch * sizeof(float) + 255) & ~(size_t)255;
+    return maxima + projection_ws(fmt, vocab, hidden, batch < kMaxBatchTile ? batch : kMaxBatchTile, false);
 }
 
 int rta_lm_head(int fmt, const void* w, int vocab, int hidden, const float* h, int batch, float margin, float* logits,
@@ -352,19 +459,24 @@ int rta_lm_head(int fmt, const void* w, int vocab, int hidden, const float* h, i
     if (!h || !logits || !ids) return RTA_ERR_NULL;
     if (batch <= 0) return RTA_ERR_SHAPE;
     if (!(margin >= 0.0f) || !(margin < 1.0f)) return RTA_ERR_RANGE;
-    if (!workspace || workspace_bytes < rta_lm_head_workspace_bytes(vocab, batch)) return RTA_ERR_WORKSPACE;
+    const size_t maxima = ((size_t)vocab * (size_t)batch * sizeof(float) + 255) & ~(size_t)255;
+    const size_t mma = projection_ws(fmt, vocab, hidden, batch < kMaxBatchTile ? batch : kMaxBatchTile, false);
+    if (!workspace || workspace_bytes < rta_lm_head_workspace_bytes(fmt, vocab, hidden, batch)) return RTA_ERR_WORKSPACE;
     if (reinterpret_cast<uintptr_t>(h) % 16 || reinterpret_cast<uintptr_t>(logits) % 4 ||
-        reinterpret_cast<uintptr_t>(ids) % 4 || reinterpret_cast<uintptr_t>(workspace) % 4)
+        reinterpret_cast<uintptr_t>(ids) % 4 || reinterpret_cast<uintptr_t>(workspace) % 256)
         return RTA_ERR_ALIGN;
     hipStream_t s = (hipStream_t)stream;
     float* partial = static_cast<float*>(workspace);
-    // Argmax per batch tile of 8, with the plan that tile was written with.
+    void* scratch = static_cast<uint8_t*>(workspace) + maxima;
+    // Argmax per batch tile, with the plan that tile was written with.
     int b0 = 0;
     while (b0 < batch) {
-        const int chunk = batch - b0 < 8 ? batch - b0 : 8;
+        const int cap = (is_kquant(fmt) && batch >= kMfmaMinBatch) ? kMaxBatchTile : 8;
+        const int chunk = batch - b0 < cap ? batch - b0 : cap;
         int ntasks = 0, rpt = 1;
         rc = run_projection<kLogits>(fmt, w, nullptr, vocab, hidden, h + (int64_t)b0 * hidden, chunk,
-                                     logits + (int64_t)b0 * vocab, partial + (int64_t)b0 * vocab, &ntasks, &rpt, s);
+                                     logits + (int64_t)b0 * vocab, partial + (int64_t)b0 * vocab, &ntasks, &rpt,
+                                     scratch, mma, s, batch);
         if (rc) return rc;
         hipLaunchKernelGGL(argmax_margin_kernel, dim3(chunk), dim3(1024), 0, s, logits + (int64_t)b0 * vocab,
                            vocab, partial + (int64_t)b0 * vocab, ntasks, rpt, margin, ids + b0);

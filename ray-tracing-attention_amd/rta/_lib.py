@@ -25,9 +25,11 @@ SIGNATURES = {
     "rta_device_error": (_i, [_u32p, _i]),
     "rta_row_bytes": (_i64, [_i, _i64]),
     "rta_dequant": (_i, [_i, _p, _i64, _p, _p]),
-    "rta_gemv": (_i, [_i, _p, _i, _i, _p, _i, _p, _i, _p]),
-    "rta_mlp_swiglu": (_i, [_i, _p, _i, _p, _i, _p, _i, _i, _p, _i, _p, _p, _i, _p]),
-    "rta_lm_head_workspace_bytes": (_sz, [_i, _i]),
+    "rta_gemv_workspace_bytes": (_sz, [_i, _i, _i, _i]),
+    "rta_gemv": (_i, [_i, _p, _i, _i, _p, _i, _p, _i, _p, _sz, _p]),
+    "rta_mlp_workspace_bytes": (_sz, [_i, _i, _i, _i, _i]),
+    "rta_mlp_swiglu": (_i, [_i, _p, _i, _p, _i, _p, _i, _i, _p, _i, _p, _p, _i, _p, _sz, _p]),
+    "rta_lm_head_workspace_bytes": (_sz, [_i, _i, _i, _i]),
     "rta_lm_head": (_i, [_i, _p, _i, _i, _p, _i, _f, _p, _p, _p, _sz, _p]),
     "rta_rope": (_i, [_p, _i, _i, _i, _i, _p, _d, _p]),
     "rta_history_bytes": (_i64, [_i]),

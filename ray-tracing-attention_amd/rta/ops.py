@@ -47,7 +47,17 @@ def dequant(fmt, blocks, n):
     return out
 
 
-def gemv(fmt, w, rows, cols, x, y=None, accumulate=False):
+def _workspace(nbytes, dev, given):
+    if given is not None:
+        return given
+    return torch.empty(max(int(nbytes), 1), dtype=torch.uint8, device=dev)
+
+
+def gemv_workspace_bytes(fmt, rows, cols, batch):
+    return int(_lib.load().rta_gemv_workspace_bytes(fmt, rows, cols, batch))
+
+
+def gemv(fmt, w, rows, cols, x, y=None, accumulate=False, workspace=None):
     """y[b] = W x[b] (or y += W x); x [batch, cols] fp32 -> y [batch, rows]."""
     lib = _lib.load()
     _dev(w, "w"), _dev(x, "x")
@@ -58,12 +68,17 @@ def gemv(fmt, w, rows, cols, x, y=None, accumulate=False):
             raise ValueError("accumulate needs y")
         y = torch.empty(batch, rows, dtype=torch.float32, device=x.device)
     _dev(y, "y")
+    ws = _workspace(gemv_workspace_bytes(fmt, rows, cols, batch), x.device, workspace)
     check(lib.rta_gemv(fmt, _ptr(w), rows, cols, _ptr(x2), batch, _ptr(y),
-                       EPI_ACCUMULATE if accumulate else EPI_STORE, _stream()), "rta_gemv")
+                       EPI_ACCUMULATE if accumulate else EPI_STORE, _ptr(ws), ws.numel(), _stream()), "rta_gemv")
     return y
 
 
-def mlp_swiglu(fmts, wg, wu, wd, hidden, inter, x, y=None, accumulate=False, act=None):
+def mlp_workspace_bytes(fmt_g, fmt_d, hidden, inter, batch):
+    return int(_lib.load().rta_mlp_workspace_bytes(fmt_g, fmt_d, hidden, inter, batch))
+
+
+def mlp_swiglu(fmts, wg, wu, wd, hidden, inter, x, y=None, accumulate=False, act=None, workspace=None):
     """act = sign(g)sign(u)|g||u|sigmoid(g); y (=|+=) Wd act.  Returns (act, y)."""
     lib = _lib.load()
     fg, fu, fd = fmts
@@ -75,14 +90,15 @@ def mlp_swiglu(fmts, wg, wu, wd, hidden, inter, x, y=None, accumulate=False, act
         act = torch.empty(batch, inter, dtype=torch.float32, device=x.device)
     if y is None:
         y = torch.empty(batch, hidden, dtype=torch.float32, device=x.device)
+    ws = _workspace(mlp_workspace_bytes(fg, fd, hidden, inter, batch), x.device, workspace)
     check(lib.rta_mlp_swiglu(fg, _ptr(wg), fu, _ptr(wu), fd, _ptr(wd), hidden, inter, _ptr(x2), batch,
-                             _ptr(act), _ptr(y), EPI_ACCUMULATE if accumulate else EPI_STORE, _stream()),
-          "rta_mlp_swiglu")
+                             _ptr(act), _ptr(y), EPI_ACCUMULATE if accumulate else EPI_STORE, _ptr(ws), ws.numel(),
+                             _stream()), "rta_mlp_swiglu")
     return act, y
 
 
-def lm_head_workspace_bytes(vocab, batch):
-    return int(_lib.load().rta_lm_head_workspace_bytes(vocab, batch))
+def lm_head_workspace_bytes(fmt, vocab, hidden, batch):
+    return int(_lib.load().rta_lm_head_workspace_bytes(fmt, vocab, hidden, batch))
 
 
 def lm_head(fmt, w, vocab, hidden, h, margin=1e-4, workspace=None, logits=None, ids=None):
@@ -96,12 +112,9 @@ def lm_head(fmt, w, vocab, hidden, h, margin=1e-4, workspace=None, logits=None, 
         logits = torch.empty(batch, vocab, dtype=torch.float32, device=dev)
     if ids is None:
         ids = torch.empty(batch, dtype=torch.int32, device=dev)
-    need = lm_head_workspace_bytes(vocab, batch)
-    if workspace is None:
-        workspace = torch.empty(need, dtype=torch.uint8, device=dev)
+    ws = _workspace(lm_head_workspace_bytes(fmt, vocab, hidden, batch), dev, workspace)
     check(lib.rta_lm_head(fmt, _ptr(w), vocab, hidden, _ptr(h2), batch, ctypes.c_float(margin), _ptr(logits),
-                          _ptr(ids), _ptr(workspace), workspace.numel() * workspace.element_size(), _stream()),
-          "rta_lm_head")
+                          _ptr(ids), _ptr(ws), ws.numel(), _stream()), "rta_lm_head")
     return logits, ids
 
 

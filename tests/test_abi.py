@@ -42,23 +42,28 @@ def test_host_queries(lib):
     assert lib.rta_row_bytes(_lib.F16, 10) == 20
     assert lib.rta_history_bytes(512) == 712          # resident_dimensions.hpp:10
     assert lib.rta_history_bytes(1024) == 1416
-    assert lib.rta_lm_head_workspace_bytes(151936, 4) == 151936 * 4 * 4
+    assert lib.rta_lm_head_workspace_bytes(_lib.Q6_K, 151936, 2048, 4) == 151936 * 4 * 4
+    assert lib.rta_gemv_workspace_bytes(_lib.Q4_K, 4096, 4096, 1) == 0
+    assert lib.rta_gemv_workspace_bytes(_lib.Q4_K, 4096, 4096, 32) > 0
+    assert lib.rta_mlp_workspace_bytes(_lib.Q4_K, _lib.Q6_K, 2048, 6144, 4) == 0
     assert lib.rta_decode_attention_workspace_bytes(16, 16, 4, 128, 32768) == 16 * 4 * 128 * 4 * 130 * 4
     assert lib.rta_decode_attention_workspace_bytes(16, 16, 4, 64, 32768) == 0
 
 
 def test_argument_errors_are_reported_before_launch(lib):
     E = {"null": 1, "shape": 2, "format": 3, "align": 4, "ws": 5, "range": 7}
-    assert lib.rta_gemv(99, FAKE, 8, 256, FAKE, 1, FAKE, 0, None) == E["format"]
-    assert lib.rta_gemv(_lib.Q4_K, None, 8, 256, FAKE, 1, FAKE, 0, None) == E["null"]
-    assert lib.rta_gemv(_lib.Q4_K, FAKE, 8, 255, FAKE, 1, FAKE, 0, None) == E["shape"]
-    assert lib.rta_gemv(_lib.Q4_K, FAKE, 0, 256, FAKE, 1, FAKE, 0, None) == E["shape"]
-    assert lib.rta_gemv(_lib.Q4_K, FAKE, 8, 256, FAKE, 0, FAKE, 0, None) == E["shape"]
-    assert lib.rta_gemv(_lib.Q4_K, FAKE_ODD, 8, 256, FAKE, 1, FAKE, 0, None) == E["align"]
-    assert lib.rta_gemv(_lib.Q4_K, FAKE, 8, 256, FAKE_ODD, 1, FAKE, 0, None) == E["align"]
-    assert lib.rta_gemv(_lib.Q4_K, FAKE, 8, 256, FAKE, 1, FAKE, 7, None) == E["range"]
+    G = lambda *a: lib.rta_gemv(*a, None, 0, None)
+    assert G(99, FAKE, 8, 256, FAKE, 1, FAKE, 0) == E["format"]
+    assert G(_lib.Q4_K, None, 8, 256, FAKE, 1, FAKE, 0) == E["null"]
+    assert G(_lib.Q4_K, FAKE, 8, 255, FAKE, 1, FAKE, 0) == E["shape"]
+    assert G(_lib.Q4_K, FAKE, 0, 256, FAKE, 1, FAKE, 0) == E["shape"]
+    assert G(_lib.Q4_K, FAKE, 8, 256, FAKE, 0, FAKE, 0) == E["shape"]
+    assert G(_lib.Q4_K, FAKE_ODD, 8, 256, FAKE, 1, FAKE, 0) == E["align"]
+    assert G(_lib.Q4_K, FAKE, 8, 256, FAKE_ODD, 1, FAKE, 0) == E["align"]
+    assert G(_lib.Q4_K, FAKE, 8, 256, FAKE, 1, FAKE, 7) == E["range"]
     assert lib.rta_mlp_swiglu(_lib.Q4_K, FAKE, _lib.Q6_K, FAKE, _lib.Q6_K, FAKE, 256, 512, FAKE, 1, FAKE, FAKE, 0,
-                              None) == E["format"]
+                              None, 0, None) == E["format"]
+    assert G(_lib.Q4_K, FAKE, 8, 256, FAKE, 8, FAKE, 0) == E["ws"]             # matrix-core tile needs scratch
     assert lib.rta_lm_head(_lib.Q6_K, FAKE, 300, 256, FAKE, 1, ctypes.c_float(1e-4), FAKE, FAKE, None, 0,
                            None) == E["ws"]
     assert lib.rta_lm_head(_lib.Q6_K, FAKE, 300, 256, FAKE, 1, ctypes.c_float(-1.0), FAKE, FAKE, FAKE, 1 << 20,

@@ -77,25 +77,81 @@ def test_gemv_parity(torch_dev, fmt, rows, cols):
             assert_close(got[b], ref[b], f"fmt {fmt} {rows}x{cols} batch {batch} row {b}")
 
 
+MMA_SHAPES = [(4096, 4096), (1000, 768), (37, 256), (300, 12288), (6144, 2048)]
+
+
+@pytest.mark.parametrize("fmt", [orc.Q4_K, orc.Q6_K])
+@pytest.mark.parametrize("rows,cols", MMA_SHAPES)
+def test_gemv_matrix_core_parity(torch_dev, fmt, rows, cols):
+    """Batch tiles of >= 8 rows run on the matrix cores (prepared fp16 hi/lo x, exact
+    integer weight operands, fixed-order K-slab reduce)."""
+    torch, dev = torch_dev
+    rng = np.random.default_rng(rows * 13 + cols + fmt)
+    w = synth.random_matrix(rng, fmt, rows, cols)
+    wd = to_dev(torch, w, dev)
+    for batch in (8, 9, 16, 17, 32, 33, 40):
+        x = rng.standard_normal((batch, cols)).astype(np.float32)
+        x[0] *= 1e3          # rows of very different magnitude (per-row binary16 scaling)
+        x[-1] *= 1e-3
+        got = ops.gemv(fmt, wd, rows, cols, to_dev(torch, x, dev)).cpu().numpy()
+        ref = orc.gemv_f64(fmt, w, rows, cols, x)
+        for b in range(batch):
+            assert_close(got[b], ref[b], f"fmt {fmt} {rows}x{cols} batch {batch} row {b}")
+
+
+def test_matrix_core_large_q6k_scales(torch_dev):
+    """Q6_K int8 scales beyond +-64 (products above 2048 round to 11 bits)."""
+    torch, dev = torch_dev
+    rng = np.random.default_rng(91)
+    rows, cols = 256, 1024
+    n = rows * cols // 256
+    d = (np.abs(rng.standard_normal(n)) * 0.01).astype(np.float16)
+    sc = rng.integers(-128, 128, (n, 16)).astype(np.int8)
+    q = rng.integers(0, 64, (n, 256)).astype(np.uint8)
+    w = synth.pack_q6k(d, sc, q).reshape(rows, -1)
+    x = rng.standard_normal((16, cols)).astype(np.float32)
+    got = ops.gemv(orc.Q6_K, to_dev(torch, w, dev), rows, cols, to_dev(torch, x, dev)).cpu().numpy()
+    ref = orc.gemv_f64(orc.Q6_K, w, rows, cols, x)
+    for b in range(16):
+        assert_close(got[b], ref[b], f"row {b}")
+
+
 @pytest.mark.parametrize("fmt", [orc.Q4_K, orc.Q6_K])
 def test_gemv_invariants(torch_dev, fmt):
+    """Zero row -> exact zero; batch-prefix bitwise invariance (verify_rt_mlp.py:95-98)
+    within each path: the VALU kernels (batch tiles of <= 7 rows) and the matrix-core
+    kernels (>= 8 rows) each compute a row independently of the other rows; across the
+    two paths results agree to tolerance.  x -> -x gives y -> -y exactly on the VALU
+    path; on the matrix cores only to tolerance (the MFMA's multi-operand fp32
+    accumulation is not sign-symmetric at the last bits)."""
     torch, dev = torch_dev
     rows, cols = 512, 4096
     rng = np.random.default_rng(33)
-    w = to_dev(torch, synth.random_matrix(rng, fmt, rows, cols), dev)
-    x = rng.standard_normal((8, cols)).astype(np.float32)
+    w_host = synth.random_matrix(rng, fmt, rows, cols)
+    w = to_dev(torch, w_host, dev)
+    x = rng.standard_normal((40, cols)).astype(np.float32)
     x[1] = 0.0
     x[2] = -x[0]
-    y = ops.gemv(fmt, w, rows, cols, to_dev(torch, x, dev)).cpu().numpy()
-    assert not y[1].any()                                  # zero row -> exact zero
-    assert np.array_equal(y[2], -y[0])                     # x -> -x gives y -> -y exactly
-    for prefix in (1, 2, 4):                               # batch-prefix bitwise invariance
-        yp = ops.gemv(fmt, w, rows, cols, to_dev(torch, x[:prefix], dev)).cpu().numpy()
-        assert np.array_equal(yp, y[:prefix]), prefix
-    base = rng.standard_normal((8, rows)).astype(np.float32)
-    yacc = to_dev(torch, base, dev)
-    ops.gemv(fmt, w, rows, cols, to_dev(torch, x, dev), y=yacc, accumulate=True)
-    assert np.array_equal(yacc.cpu().numpy(), (base + y).astype(np.float32))
+    for n, prefixes, exact_sign in ((7, (1, 2, 4), True), (40, (8, 16, 33), False)):
+        y = ops.gemv(fmt, w, rows, cols, to_dev(torch, x[:n], dev)).cpu().numpy()
+        assert not y[1].any()                              # zero row -> exact zero
+        if exact_sign:
+            assert np.array_equal(y[2], -y[0])             # x -> -x gives y -> -y exactly
+        else:
+            assert_close(y[2], -y[0], "sign symmetry (matrix cores)")
+        for prefix in prefixes:
+            yp = ops.gemv(fmt, w, rows, cols, to_dev(torch, x[:prefix], dev)).cpu().numpy()
+            assert np.array_equal(yp, y[:prefix]), (n, prefix)
+        base = rng.standard_normal((n, rows)).astype(np.float32)
+        yacc = to_dev(torch, base, dev)
+        ops.gemv(fmt, w, rows, cols, to_dev(torch, x[:n], dev), y=yacc, accumulate=True)
+        assert np.array_equal(yacc.cpu().numpy(), (base + y).astype(np.float32))
+    ref = orc.gemv_f64(fmt, w_host, rows, cols, x)
+    y40 = ops.gemv(fmt, w, rows, cols, to_dev(torch, x, dev)).cpu().numpy()
+    y7 = ops.gemv(fmt, w, rows, cols, to_dev(torch, x[:7], dev)).cpu().numpy()
+    for b in range(7):
+        assert_close(y40[b], ref[b], f"matrix cores row {b}")
+        assert_close(y7[b], ref[b], f"VALU row {b}")
 
 
 def test_gemv_plain_formats(torch_dev):
@@ -112,7 +168,7 @@ def test_gemv_plain_formats(torch_dev):
 
 
 # -------------------------------------------------------------------- MLP ----
-@pytest.mark.parametrize("batch", [1, 7, 8, 17, 32])
+@pytest.mark.parametrize("batch", [1, 7, 8, 17, 32, 40])
 def test_mlp_swiglu_parity(torch_dev, batch):
     torch, dev = torch_dev
     hidden, inter = 2048, 6144
@@ -151,7 +207,7 @@ def _check_ids(logits_gpu, ids_gpu, logits_ref, margin):
             assert int(ids_gpu[b]) == orc.argmax_margin_f64(ref, margin), b
 
 
-@pytest.mark.parametrize("batch", [1, 4, 16])
+@pytest.mark.parametrize("batch", [1, 4, 16, 33])
 def test_lm_head_parity(torch_dev, batch):
     torch, dev = torch_dev
     vocab, hidden = (151936 if batch == 1 else 20011), 2048
