@@ -8,6 +8,7 @@ Workloads (one JSON line per run):
   lm_head     151936 x 2048 Q6_K vocabulary readout + margin argmax, --batch rows
   attention   GQA decode attention, 16 sequences, contexts log-uniform in [512, 32768],
               16 q / 4 kv heads, hd 128, K Q6_K / V Q4_K history, RoPE theta 1e6 on q
+  proj        one projection --rows x --cols in --fmt q4k|q6k for --batch rows
   copy_calib  plain device-to-device copy of known size (PMC byte-counter calibration)
 
 A step is one pass of the hot path over one batch of synthetic input resident in
@@ -44,8 +45,11 @@ def parse():
     ap.add_argument("--steps", type=int, default=1000)
     ap.add_argument("--warmup", type=int, default=100)
     ap.add_argument("--workload", default="gemv_q4k",
-                    choices=["gemv_q4k", "mlp", "lm_head", "attention", "copy_calib"])
+                    choices=["gemv_q4k", "mlp", "lm_head", "attention", "proj", "copy_calib"])
     ap.add_argument("--batch", type=int, default=None)
+    ap.add_argument("--rows", type=int, default=12288, help="proj workload: output rows")
+    ap.add_argument("--cols", type=int, default=4096, help="proj workload: input columns")
+    ap.add_argument("--fmt", default="q4k", choices=["q4k", "q6k"], help="proj workload: weight format")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--eager", action="store_true", help="time eager launches instead of a graph replay")
@@ -350,6 +354,47 @@ def w_attention(torch, args, orc):
     return res
 
 
+def w_proj(torch, args, orc):
+    """One dequant-fused projection y = W x of --rows x --cols in --fmt (q4k / q6k) for --batch rows."""
+    from rta import ops, synth
+    fmt = {"q4k": Q4_K, "q6k": Q6_K}[args.fmt]
+    rows, cols, batch = args.rows, args.cols, args.batch or 1
+    dev = torch.device("cuda:0")
+    rng = synth.rng_for(5)
+    w = synth.random_matrix(rng, fmt, rows, cols)
+    x = rng.standard_normal((batch, cols)).astype(np.float32)
+    copies = rotation(torch, w, dev)
+    xd = torch.from_numpy(x).to(dev)
+    y = torch.empty(batch, rows, dtype=torch.float32, device=dev)
+    ws = torch.empty(max(1, ops.gemv_workspace_bytes(fmt, rows, cols, batch)), dtype=torch.uint8, device=dev)
+
+    def step(i):
+        ops.gemv(fmt, copies[i % len(copies)], rows, cols, xd, y=y, workspace=ws)
+
+    alg = w.nbytes + batch * 4 * (cols + rows)
+    res = {"alg_bytes": alg, "kernel": "dequant-fused projection (MFMA path from batch 8)", "step": step,
+           "kernel_launch": step, "unit": "GB/s", "value_from_ms": lambda ms: alg / (ms * 1e-3) / 1e9,
+           "dtype": f"{args.fmt} weights x fp32 activations, fp32 accumulate",
+           "config": {"workload": f"{args.fmt.upper()} projection {rows}x{cols}, batch {batch}", "rows": rows,
+                      "cols": cols, "batch": batch, "weight_copies_rotated": len(copies), "seed": "20261110+5"}}
+
+    def check():
+        step(0)
+        sub = min(rows, 4096)   # the fp64 oracle over the first rows
+        return close(y.cpu().numpy()[:, :sub], orc.gemv_f64(fmt, w[:sub], sub, cols, x))
+
+    def cpu(seconds):
+        t = omp_threads()
+        sub = min(rows, 4096)
+        n, el = cpu_time(lambda: orc.gemv_f32(fmt, w[:sub], sub, cols, x, t), seconds)
+        by = w[:sub].nbytes + batch * 4 * (cols + sub)
+        return {"value": by * n / el / 1e9, "unit": "GB/s", "cores": t, "kind": "port",
+                "sample": f"{n} calls of the oracle's fp32 OpenMP projection over {sub} rows x {cols}, batch {batch}"
+                          f" in {el:.1f} s on {cpu_model()}"}
+    res["check"], res["cpu"] = check, cpu
+    return res
+
+
 def w_copy_calib(torch, args, orc):
     dev = torch.device("cuda:0")
     n = 64 << 20
@@ -367,7 +412,7 @@ def w_copy_calib(torch, args, orc):
 
 
 WORKLOADS = {"gemv_q4k": w_gemv_q4k, "mlp": w_mlp, "lm_head": w_lm_head, "attention": w_attention,
-             "copy_calib": w_copy_calib}
+             "proj": w_proj, "copy_calib": w_copy_calib}
 
 
 def main():

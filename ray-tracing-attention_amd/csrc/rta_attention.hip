@@ -48,9 +48,8 @@ __device__ __forceinline__ uint32_t ld32(const uint8_t* p) { return *reinterpret
 
 // Dword that starts at the 2-byte aligned address p (reads [floor4(p), floor4(p)+8)).
 __device__ __forceinline__ uint32_t ld32_u2(const uint8_t* p) {
-    const uintptr_t a = reinterpret_cast<uintptr_t>(p);
-    const uint32_t mis = (uint32_t)(a & 3u);
-    const uint32_t* w = reinterpret_cast<const uint32_t*>(a - mis);
+    const uint32_t mis = (uint32_t)(reinterpret_cast<uintptr_t>(p) & 3u);
+    const uint32_t* w = reinterpret_cast<const uint32_t*>(p - mis);   // keeps the address space
     return mis ? funnel(w[0], w[1], mis) : w[0];
 }
 

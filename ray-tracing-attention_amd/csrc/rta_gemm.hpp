@@ -1,31 +1,45 @@
 // rta_gemm.hpp -- batched (>= 8 rows) dequant-fused readout on the gfx950 matrix cores.
 //
-// y[b, r] = sum_k W[r, k] x[b, k] for a batch of up to 32 x rows per launch, with
-// v_mfma_f32_16x16x32_f16 (fp32 accumulation):
-//   A operand  x, prepared once per call (xprep_kernel): per batch row a power-of-two
-//              scale s_b puts max|x_b s_b| in [2^13, 2^14); x s_b is split into
-//              binary16 hi + lo (22 significant bits), both multiplied in.
-//   B operand  the weights, built in registers as exact binary16 integers:
-//                Q4_K  sc_g * q          (<= 945)   = fma(1024 + q, sc, -1024 sc)
-//                Q6_K  sc * (q - 32)     = ((1024 + q) - 1056) * sc, exact for
-//                                         |product| <= 2048; beyond that (|sc| > 64)
-//                                         it rounds to 11 bits, < 2^-12 relative
-//              with packed binary16 ops on two codes at a time (1024 + q is the code
-//              OR 0x6400, an exact binary16 integer).
-//              So a superblock accumulates across all its groups and d (and the
-//              Q4_K minimum term dmin * sum_g m_g X_g, one more MFMA over the group
-//              sums) is applied once per superblock and output.
-//   Layout     lane l of a wave: weight row l%16 / k segment 8*(l/16) (B operand),
-//              batch row l%16 / k segment 8*(l/16) (A operand), and it owns outputs
-//              (batch 4*(l/16)+e, row l%16) -- the row whose header it loaded.
-// A workgroup (4 waves) covers 64*RT rows x one K slab; x for the slab is staged
-// superblock by superblock in double-buffered LDS and shared by the 4 waves; the
-// weights of the next superblock are prefetched into registers.  K slabs > 1 write
-// partial sums that gemm_reduce_kernel adds in a fixed order (deterministic).
+// y[b, r] = sum_k W[r, k] x[b, k] for up to 32 x rows per launch with
+// v_mfma_f32_16x16x32_f16 (fp32 accumulation).
+//
+//   x (A operand), prepared by xprep_kernel per (batch row, superblock of 256
+//   columns): a power-of-two scale s puts max|x s| in [2^13, 2^14); x s is split
+//   into binary16 hi + lo (22 significant bits) and both are multiplied in.  The
+//   group sums the formats need (sum x over 32 for the Q4_K minimum, over 16 for
+//   the Q6_K -32 offset) are prepared the same way, already in A-operand order.
+//
+//   Weights (B operand) are built in registers as exact binary16 values with one
+//   packed multiply per two codes: a code c in the low bits of a half is the
+//   subnormal c * 2^-24, and
+//     Q4_K  low nibble  (c 2^-24) * (sc 2^10) = c sc 2^-14   (c sc <= 945)
+//           high nibble (16 c 2^-24) * (sc 2^6) = c sc 2^-14
+//     Q6_K  (4 c 2^-24) * (sc 2^8) = c sc 2^-14  (exact for |c sc| <= 2048; beyond,
+//           |sc| > 32, it rounds to 11 bits, <= 2^-12 relative; the -32 offset is
+//           applied exactly through the group sums)
+//   so every product handed to the matrix cores is a normal binary16 (or zero).
+//   The masks deliver code pairs (k, k+2); x is stored in the same order inside
+//   every 8-value segment (slots 0..7 hold k = 0,2,1,3,4,6,5,7), and a common
+//   permutation of k leaves the contraction unchanged.
+//   Per superblock the MFMAs accumulate across all groups; the superblock's
+//   scale d, the minimum / offset terms (one more MFMA over the group sums) and
+//   the 1/s of x are applied once per superblock.
+//
+//   Lane l of a wave owns weight row l%16 / k segment 8*(l/16) (B operand), batch
+//   row l%16 / k segment (A operand), and outputs (batch 4*(l/16)+e, row l%16).
+//
+//   Work split: the K range is cut into slabs of up to 8 (16 x rows) or 4 (32 x
+//   rows) superblocks.  A workgroup (8 waves, one per CU) loads its slab of x into
+//   LDS once; after that its waves run independently over tiles of 16*RT weight
+//   rows, each loading the next superblock's weights into registers while the
+//   current one is multiplied.  With one slab the kernel applies the epilogue
+//   itself; with more it writes per-slab partial sums that gemm_reduce_kernel adds
+//   in slab order (deterministic).
 //
 // Equivalent reference: the batched projection pipelines (optical_resident.cpp:168,343,
 // matrixRows 4/8/16) and resident_batch2.comp (which accumulates in fp16; not copied).
 #pragma once
+#include <type_traits>
 #include "rta_gemv.hpp"
 
 namespace rta {
@@ -35,69 +49,88 @@ typedef float f4_t __attribute__((ext_vector_type(4)));
 typedef _Float16 h2v_t __attribute__((ext_vector_type(2)));
 
 constexpr int kMaxBatchTile = 32;  // batch rows per GEMM launch
-constexpr int kXpad = 8;           // f16 padding per staged x row (bank spread)
+constexpr int kXStride = 256 + 8;  // f16 per staged x row (8 of padding spread the LDS banks)
+constexpr int kGemmWaves = 8;      // waves per workgroup
+constexpr int kSlabRowSb = 128;    // LDS holds (x rows) * (superblocks) <= 128
 
 struct GemmX {           // prepared x (workspace), batch padded to 32
-    _Float16* hi;        // [32][cols]
+    _Float16* hi;        // [32][cols]          x s, k-permuted inside 8-segments
     _Float16* lo;        // [32][cols]
-    _Float16* gs;        // [32][cols/32][2] group sums / 32, hi and lo
-    float* inv;          // [32] 1/s_b
+    h8_t* g;             // [32][cols/256][4]   group-sum A operand per k segment
+    float* inv;          // [32][cols/256]      1/s (0 for padding rows)
 };
 
 // ---------------------------------------------------------------- x prep ----
-__global__ void __launch_bounds__(256) xprep_kernel(const float* __restrict__ x, int cols, int batch, GemmX p) {
-    __shared__ float red[4];
-    const int b = blockIdx.x, tid = threadIdx.x;
-    const float* xb = x + (int64_t)b * cols;
-    _Float16* hi = p.hi + (int64_t)b * cols;
-    _Float16* lo = p.lo + (int64_t)b * cols;
-    _Float16* gs = p.gs + (int64_t)b * (cols / 32) * 2;
-    if (b >= batch) {   // padding rows of the 32-row tile: zeros
-        for (int c = tid; c < cols; c += 256) hi[c] = lo[c] = (_Float16)0.0f;
-        for (int g = tid; g < cols / 32; g += 256) gs[2 * g] = gs[2 * g + 1] = (_Float16)0.0f;
-        if (tid == 0) p.inv[b] = 0.0f;
-        return;
+// Block: 64 threads = 2 batch rows x 32 threads; thread = 8 consecutive columns of
+// superblock blockIdx.x.  G16 selects 16-value group sums (Q6_K) over 32 (Q4_K):
+//   Q4_K  segment 0 = hi of groups 0..7, 1 = lo of groups 0..7, 2 and 3 = 0
+//   Q6_K  segment 0 = hi of groups 0..7, 1 = hi of 8..15, 2 = lo of 0..7, 3 = lo of 8..15
+template <bool G16>
+__global__ void __launch_bounds__(64) xprep_kernel(const float* __restrict__ x, int cols, int batch, GemmX p) {
+    const int lane = threadIdx.x, sb = blockIdx.x;
+    const int b = blockIdx.y * 2 + (lane >> 5), t = lane & 31;
+    const int nsb = cols >> 8;
+    const int c0 = sb * 256 + 8 * t;
+    float v[8];
+    if (b < batch) {
+        const float4* src = reinterpret_cast<const float4*>(x + (int64_t)b * cols + c0);
+        const float4 a = src[0], c = src[1];
+        v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w; v[4] = c.x; v[5] = c.y; v[6] = c.z; v[7] = c.w;
+    } else {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) v[i] = 0.0f;
     }
     float m = 0.0f;
-    for (int c = tid; c < cols; c += 256) m = fmaxf(m, fabsf(xb[c]));
-    for (int off = 32; off > 0; off >>= 1) m = fmaxf(m, __shfl_xor(m, off, kWave));
-    if ((tid & 63) == 0) red[tid >> 6] = m;
-    __syncthreads();
-    m = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+#pragma unroll
+    for (int i = 0; i < 8; ++i) m = fmaxf(m, fabsf(v[i]));
+    for (int off = 16; off > 0; off >>= 1) m = fmaxf(m, __shfl_xor(m, off, kWave));   // within 32 lanes
     int e = 0;
     if (m > 0.0f && isfinite(m)) (void)frexpf(m, &e);
-    const float s = ldexpf(1.0f, 14 - e);          // m * s in [2^13, 2^14)
-    if (tid == 0) p.inv[b] = ldexpf(1.0f, e - 14);
-    for (int c = tid; c < cols; c += 256) {
-        const float v = xb[c] * s;
-        const _Float16 h = (_Float16)v;
-        hi[c] = h;
-        lo[c] = (_Float16)(v - (float)h);
+    const float s = ldexpf(1.0f, 14 - e);        // m * s in [2^13, 2^14)
+    if (t == 0) p.inv[(int64_t)b * nsb + sb] = b < batch ? ldexpf(1.0f, e - 14) : 0.0f;
+    constexpr int perm[8] = {0, 2, 1, 3, 4, 6, 5, 7};
+    _Float16 hi[8], lo[8];
+    float sum8 = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        const float w = v[perm[i]] * s;
+        hi[i] = (_Float16)w;
+        lo[i] = (_Float16)(w - (float)hi[i]);
+        sum8 += v[i] * s;
     }
-    for (int g = tid; g < cols / 32; g += 256) {
-        float acc = 0.0f;
-        for (int i = 0; i < 32; ++i) acc += xb[32 * g + i] * s;
-        const float v = acc * (1.0f / 32.0f);      // |v| < 2^14: fits binary16
-        const _Float16 h = (_Float16)v;
-        gs[2 * g] = h;
-        gs[2 * g + 1] = (_Float16)(v - (float)h);
+    const int64_t at = (int64_t)b * cols + c0;
+    *reinterpret_cast<h8_t*>(p.hi + at) = h8_t{hi[0], hi[1], hi[2], hi[3], hi[4], hi[5], hi[6], hi[7]};
+    *reinterpret_cast<h8_t*>(p.lo + at) = h8_t{lo[0], lo[1], lo[2], lo[3], lo[4], lo[5], lo[6], lo[7]};
+    _Float16* g = reinterpret_cast<_Float16*>(p.g + ((int64_t)b * nsb + sb) * 4);   // 32 f16
+    const float s16 = sum8 + __shfl_xor(sum8, 1, kWave);
+    const float s32 = s16 + __shfl_xor(s16, 2, kWave);
+    if constexpr (G16) {
+        if ((t & 1) == 0) {   // group u = t / 2 of 16 columns
+            const int u = t >> 1;
+            const float w = s16 * (1.0f / 16.0f);
+            const _Float16 h = (_Float16)w;
+            g[8 * (u >> 3) + (u & 7)] = h;
+            g[16 + 8 * (u >> 3) + (u & 7)] = (_Float16)(w - (float)h);
+        }
+    } else {
+        const int q = t >> 2;  // group of 32 columns
+        if ((t & 3) == 0) {
+            const float w = s32 * (1.0f / 32.0f);
+            const _Float16 h = (_Float16)w;
+            g[q] = h;
+            g[8 + q] = (_Float16)(w - (float)h);
+        } else if ((t & 3) == 1) {
+            g[16 + q] = (_Float16)0.0f;
+            g[24 + q] = (_Float16)0.0f;
+        }
     }
 }
 
-__device__ __forceinline__ uint32_t pk_fma_f16(uint32_t a, uint32_t b, uint32_t c) {
-    const h2v_t r = __builtin_bit_cast(h2v_t, a) * __builtin_bit_cast(h2v_t, b) + __builtin_bit_cast(h2v_t, c);
-    return __builtin_bit_cast(uint32_t, r);
-}
-
-__device__ __forceinline__ uint32_t pk_add_f16(uint32_t a, uint32_t b) {
-    return __builtin_bit_cast(uint32_t, __builtin_bit_cast(h2v_t, a) + __builtin_bit_cast(h2v_t, b));
-}
 __device__ __forceinline__ uint32_t pk_mul_f16(uint32_t a, uint32_t b) {
     return __builtin_bit_cast(uint32_t, __builtin_bit_cast(h2v_t, a) * __builtin_bit_cast(h2v_t, b));
 }
-constexpr uint32_t kMinus1056 = 0xE420E420u;   // (-1056.0, -1056.0) in binary16
 
-// (f16(v), f16(v)) for a small exact integer v
+// (f16(v), f16(v)) for a value v exactly representable in binary16
 __device__ __forceinline__ uint32_t h2dup(float v) {
     const uint32_t h = __builtin_bit_cast(uint16_t, (_Float16)v);
     return h | (h << 16);
@@ -106,7 +139,7 @@ __device__ __forceinline__ uint32_t h2dup(float v) {
 // -------------------------------------------------------- weight operand ----
 // Per lane: row l%16 of one 16-row tile, k segment s = l/16 of every 32-value chunk.
 struct Q4KMma {
-    static constexpr int kBytes = 144;
+    static constexpr int kBlock = 144;
     struct Raw { uint4 hdr; uint2 q[4]; };   // q[j] = bytes 16+32j+8s .. +8
     __device__ static __forceinline__ void load(const uint8_t* __restrict__ blk, int s, Raw& r) {
         r.hdr = *reinterpret_cast<const uint4*>(blk);
@@ -116,14 +149,15 @@ struct Q4KMma {
 };
 
 struct Q6KMma {
-    static constexpr int kBytes = 210;
+    static constexpr int kBlock = 210;
     // half h: ql runs at 64h + 8s and 64h + 32 + 8s, qh run at 128 + 32h + 8s (8 bytes
-    // each), loaded as 3 dwords from the 4-byte aligned address below; scales 192..207; d.
+    // each), loaded as 3 dwords from the 4-byte aligned address at or below; scales; d.
+    // Every dword read overlaps the 210-byte block (blocks are 2-byte aligned).
     struct Raw { uint32_t a[2][3], b[2][3], h[2][3]; uint32_t sc[5]; uint32_t d; uint32_t mis; };
     __device__ static __forceinline__ void load(const uint8_t* __restrict__ blk, int s, Raw& r) {
-        const uintptr_t addr = reinterpret_cast<uintptr_t>(blk);
-        const uint32_t mis = (uint32_t)(addr & 3u);
-        const uint32_t* a = reinterpret_cast<const uint32_t*>(addr - mis);
+        // aligned down by pointer arithmetic, which keeps the global address space
+        const uint32_t mis = (uint32_t)(reinterpret_cast<uintptr_t>(blk) & 3u);
+        const uint32_t* a = reinterpret_cast<const uint32_t*>(blk - mis);
 #pragma unroll
         for (int hh = 0; hh < 2; ++hh) {
             const int ia = (64 * hh + 8 * s) >> 2, ib = (64 * hh + 32 + 8 * s) >> 2, ih = (128 + 32 * hh + 8 * s) >> 2;
@@ -142,67 +176,103 @@ struct Q6KMma {
     }
 };
 
-// Spreads bytes i, i+1 of w into the low bytes of the two halves.
-__device__ __forceinline__ uint32_t spread(uint32_t w, int i) {
-    return __builtin_amdgcn_perm(w, w, i == 0 ? 0x0C010C00u : 0x0C030C02u);
-}
+// Static LDS of the GEMM: the x slab (hi and lo planes), group-sum operands, 1/s.
+template <int NBT>
+struct GemmSmem {
+    static constexpr int kRows = 16 * NBT;
+    static constexpr int kSb = kSlabRowSb / kRows;   // superblocks per slab
+    _Float16 x[kSb][2][kRows][kXStride];
+    h8_t g[kSb][kRows][4];
+    float inv[kSb][kRows];
+};
 
-template <int FMT, int RT, int NBT, int XS, int MODE>
-__global__ void __launch_bounds__(256) gemm_mfma_kernel(
+template <int FMT, int RT, int NBT, int MODE>
+__global__ void __launch_bounds__(64 * kGemmWaves) gemm_mfma_kernel(
     const uint8_t* __restrict__ w, const uint8_t* __restrict__ w2, const int64_t row_bytes, const int rows,
     const int cols, const GemmX xp, const int batch, float* __restrict__ y, float* __restrict__ part,
-    const int row_blocks, const int sb_per_slab) {
+    float* __restrict__ pmax, const int sb_per_slab, const int wgs_per_slab) {
     constexpr bool kQ4 = FMT == RTA_Q4_K;
-    constexpr int kStride = 256 + kXpad;                       // staged x row, f16 elements
-    __shared__ _Float16 s_xh[2][kMaxBatchTile][kStride];
-    __shared__ _Float16 s_xl[XS == 2 ? 2 : 1][XS == 2 ? kMaxBatchTile : 1][XS == 2 ? kStride : 1];
-    __shared__ _Float16 s_gs[2][kMaxBatchTile][16];            // 8 groups x (hi, lo) per batch row
+    using Fmt = typename std::conditional<kQ4, Q4KMma, Q6KMma>::type;
+    using Raw = typename Fmt::Raw;
+    using Smem = GemmSmem<NBT>;
+    constexpr int kRows = Smem::kRows;
+    constexpr int kTile = 16 * RT;
+    __shared__ Smem sm;
 
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int rb = blockIdx.x % row_blocks, slab = blockIdx.x / row_blocks;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);   // uniform: scalar loop control
+    const int slab = blockIdx.x / wgs_per_slab, pos = blockIdx.x - slab * wgs_per_slab;
+    const int nslab = gridDim.x / wgs_per_slab;
+    const int nsbt = cols >> 8;
     const int sb0 = slab * sb_per_slab;
-    const int nsb = min(sb_per_slab, cols / 256 - sb0);
+    const int nsb = min(sb_per_slab, nsbt - sb0);
     const int s = lane >> 4, li = lane & 15;
     const int total_rows = MODE == kSwiglu ? 2 * rows : rows;
 
-    // rows of this lane's RT tiles (clamped: out-of-range rows are computed and dropped)
-    const uint8_t* rowp[RT];
-#pragma unroll
-    for (int t = 0; t < RT; ++t) {
-        int r = rb * 64 * RT + wave * 16 * RT + t * 16 + li;
-        r = min(r, total_rows - 1);
-        const uint8_t* base = (MODE == kSwiglu && r >= rows) ? w2 + (int64_t)(r - rows) * row_bytes
-                                                             : w + (int64_t)r * row_bytes;
-        rowp[t] = base;
-    }
+    // ---- this wave's tiles: tg = gw, gw + nw, ...; iteration = (tile, superblock)
+    const int gw = pos * kGemmWaves + wave, nw = wgs_per_slab * kGemmWaves;
+    const int ntg = (total_rows + kTile - 1) / kTile;
+    const int my_tiles = gw < ntg ? (ntg - 1 - gw) / nw + 1 : 0;
+    const int nit = my_tiles * nsb;
 
-    auto stage = [&](int sb, int buf) {   // x of superblock sb -> LDS buffer
-        const int k0 = sb * 256;
-        // 32 rows x 256 f16 = 32 x 32 chunks of 16 bytes per array
-        for (int i = tid; i < kMaxBatchTile * 32; i += 256) {
-            const int b = i >> 5, c = (i & 31) * 8;
-            *reinterpret_cast<uint4*>(&s_xh[buf][b][c]) = *reinterpret_cast<const uint4*>(xp.hi + (int64_t)b * cols + k0 + c);
-            if constexpr (XS == 2)
-                *reinterpret_cast<uint4*>(&s_xl[buf][b][c]) = *reinterpret_cast<const uint4*>(xp.lo + (int64_t)b * cols + k0 + c);
-        }
-        if constexpr (kQ4) {
-            if (tid < kMaxBatchTile * 4) {   // 8 groups x 2 f16 = 32 bytes per batch row
-                const int b = tid >> 2, q = tid & 3;
-                *reinterpret_cast<uint2*>(&s_gs[buf][b][4 * q]) =
-                    *reinterpret_cast<const uint2*>(xp.gs + ((int64_t)b * (cols / 32) + sb * 8) * 2 + 4 * q);
-            }
-        }
-    };
-
-    using Raw = typename std::conditional<kQ4, Q4KMma, Q6KMma>::type::Raw;
-    Raw cur[RT], nxt[RT];
-    auto load_w = [&](int sb, Raw* dst) {
+    auto load_w = [&](int it, Raw* dst) {
+        const int tgi = it / nsb, sbl = it - tgi * nsb;
+        const int tg = gw + tgi * nw;
 #pragma unroll
         for (int t = 0; t < RT; ++t) {
-            if constexpr (kQ4) Q4KMma::load(rowp[t] + (int64_t)sb * 144, s, dst[t]);
-            else Q6KMma::load(rowp[t] + (int64_t)sb * 210, s, dst[t]);
+            // In kSwiglu virtual row v is gate row v/2 (v even) or up row v/2 (v odd).
+            // Rows past the end are clamped, computed and dropped.
+            const int v = min(tg * kTile + t * 16 + li, total_rows - 1);
+            const uint8_t* rowp;
+            if constexpr (MODE == kSwiglu) rowp = ((v & 1) ? w2 : w) + (int64_t)(v >> 1) * row_bytes;
+            else rowp = w + (int64_t)v * row_bytes;
+            Fmt::load(rowp + (int64_t)(sb0 + sbl) * Fmt::kBlock, s, dst[t]);
         }
     };
+
+    // Weights are prefetched DEPTH - 1 superblocks ahead through rotating register
+    // buffers; the first loads are issued before the x slab is staged.
+    // Loads are unconditional (indices clamped to the last iteration) so that the
+    // outstanding-load counts the compiler waits on are static.
+    constexpr int DEPTH = kQ4 ? 3 : 2;
+    Raw buf[DEPTH][RT];
+    if (nit > 0) {
+#pragma unroll
+        for (int d = 0; d < DEPTH - 1; ++d) load_w(min(d, nit - 1), buf[d]);
+    }
+
+    // ---- x slab -> LDS (the only barrier of the kernel).  Every load of a thread is
+    // issued before the first LDS store, so the slab costs one memory round trip.
+    {
+        constexpr int kThreads = 64 * kGemmWaves;
+        constexpr int kPer = Smem::kSb * 2 * kRows * 32 / kThreads;   // 16-byte chunks per thread
+        const int nchunk = nsb * 2 * kRows * 32;
+        uint4 tmp[kPer];
+#pragma unroll
+        for (int k = 0; k < kPer; ++k) {   // unconditional (clamped) loads
+            const int i = min(tid + k * kThreads, nchunk - 1);
+            const int c8 = i & 31, r = (i >> 5) % kRows, plane = ((i >> 5) / kRows) & 1, sbl = i / (64 * kRows);
+            tmp[k] = *reinterpret_cast<const uint4*>((plane ? xp.lo : xp.hi) + (int64_t)r * cols +
+                                                     (int64_t)(sb0 + sbl) * 256 + 8 * c8);
+        }
+        static_assert(Smem::kSb * kRows * 4 <= kThreads && Smem::kSb * kRows <= kThreads, "one operand per thread");
+        const int gi = min(tid, nsb * kRows * 4 - 1), ii = min(tid, nsb * kRows - 1);
+        const int gq = gi & 3, gr = (gi >> 2) % kRows, gs = gi / (4 * kRows);
+        const h8_t gv = xp.g[((int64_t)gr * nsbt + sb0 + gs) * 4 + gq];
+        const int ir = ii % kRows, is = ii / kRows;
+        const float iv = xp.inv[(int64_t)ir * nsbt + sb0 + is];
+        // Stores are unconditional too (threads past the end rewrite the last chunk with
+        // the same data), so that the compiler cannot sink the loads next to them.
+#pragma unroll
+        for (int k = 0; k < kPer; ++k) {
+            const int i = min(tid + k * kThreads, nchunk - 1);
+            const int c8 = i & 31, r = (i >> 5) % kRows, plane = ((i >> 5) / kRows) & 1, sbl = i / (64 * kRows);
+            *reinterpret_cast<uint4*>(&sm.x[sbl][plane][r][8 * c8]) = tmp[k];
+        }
+        sm.g[gs][gr][gq] = gv;
+        sm.inv[is][ir] = iv;
+    }
+    __syncthreads();
 
     f4_t acc[RT][NBT];
 #pragma unroll
@@ -210,178 +280,209 @@ __global__ void __launch_bounds__(256) gemm_mfma_kernel(
 #pragma unroll
         for (int bt = 0; bt < NBT; ++bt) acc[t][bt] = f4_t{0.0f, 0.0f, 0.0f, 0.0f};
 
-    if (nsb > 0) {
-        stage(sb0, 0);
-        load_w(sb0, cur);
-    }
-    __syncthreads();
-    for (int i = 0; i < nsb; ++i) {
-        const int buf = i & 1;
-        if (i + 1 < nsb) {
-            stage(sb0 + i + 1, buf ^ 1);
-            load_w(sb0 + i + 1, nxt);
-        }
+    // One superblock of RT tiles: acc += (dC C - / + dM Cm) / s
+    auto compute = [&](int sbl, const Raw* r) {
         f4_t C[RT][NBT], Cm[RT][NBT];
 #pragma unroll
         for (int t = 0; t < RT; ++t)
 #pragma unroll
             for (int bt = 0; bt < NBT; ++bt) C[t][bt] = Cm[t][bt] = f4_t{0.0f, 0.0f, 0.0f, 0.0f};
-        float dsc[RT], dmn[RT];
-
+        float dC[RT], dM[RT];
+        h8_t bm[RT];   // B operand of the group-sum MFMA (k = 8 s + e)
         if constexpr (kQ4) {
-            uint32_t scp[RT][8], mcp[RT][8];   // (sc, sc) and (-1024 sc, -1024 sc) per group
+            uint32_t slo[RT][4], shi[RT][4];
 #pragma unroll
             for (int t = 0; t < RT; ++t) {
-                const uint4 h = cur[t].hdr;
-                dsc[t] = half_lo(h.x);
-                dmn[t] = half_hi(h.x) * 32.0f;        // group sums are staged / 32
+                const uint4 h = r[t].hdr;
+                dC[t] = half_lo(h.x) * 16384.0f;     // codes carry 2^-14
+                dM[t] = half_hi(h.x) * 32.0f;        // group sums are staged / 32
 #pragma unroll
-                for (int g = 0; g < 8; ++g) {
-                    uint32_t sc, m;
-                    q4k_scale_min(h.y, h.z, h.w, g, sc, m);
-                    scp[t][g] = h2dup((float)sc);
-                    mcp[t][g] = h2dup(-1024.0f * (float)sc);
-                    (void)m;
+                for (int j = 0; j < 4; ++j) {
+                    uint32_t sc0, m0, sc1, m1;
+                    q4k_scale_min(h.y, h.z, h.w, 2 * j, sc0, m0);
+                    q4k_scale_min(h.y, h.z, h.w, 2 * j + 1, sc1, m1);
+                    slo[t][j] = h2dup((float)sc0 * 1024.0f);
+                    shi[t][j] = h2dup((float)sc1 * 64.0f);
+                    // minimum term: segments 0 (hi sums) and 1 (lo sums) hold group e; 2, 3 zero
+                    bm[t][2 * j] = s < 2 ? (_Float16)(float)m0 : (_Float16)0.0f;
+                    bm[t][2 * j + 1] = s < 2 ? (_Float16)(float)m1 : (_Float16)0.0f;
                 }
             }
 #pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                h8_t bw[RT][2];   // weight operand for groups 2j (low nibbles), 2j+1 (high)
-#pragma unroll
-                for (int t = 0; t < RT; ++t) {
-                    const uint32_t w0 = cur[t].q[j].x, w1 = cur[t].q[j].y;
-                    const uint32_t tt[4] = {spread(w0, 0), spread(w0, 2), spread(w1, 0), spread(w1, 2)};
-                    uint32_t lo[4], hi[4];
-#pragma unroll
-                    for (int e = 0; e < 4; ++e) {
-                        const uint32_t pl = (tt[e] & 0x000F000Fu) | 0x64006400u;
-                        const uint32_t ph = ((tt[e] >> 4) & 0x000F000Fu) | 0x64006400u;
-                        lo[e] = pk_fma_f16(pl, scp[t][2 * j], mcp[t][2 * j]);
-                        hi[e] = pk_fma_f16(ph, scp[t][2 * j + 1], mcp[t][2 * j + 1]);
-                    }
-                    bw[t][0] = __builtin_bit_cast(h8_t, uint4{lo[0], lo[1], lo[2], lo[3]});
-                    bw[t][1] = __builtin_bit_cast(h8_t, uint4{hi[0], hi[1], hi[2], hi[3]});
-                }
+            for (int j = 0; j < 4; ++j)
 #pragma unroll
                 for (int half = 0; half < 2; ++half) {
-                    const int kk = (2 * j + half) * 32 + 8 * s;       // k offset inside the superblock
+                    const int kk = (2 * j + half) * 32 + 8 * s;
+                    h8_t ah[NBT], al[NBT];
 #pragma unroll
                     for (int bt = 0; bt < NBT; ++bt) {
-                        const h8_t ah = *reinterpret_cast<const h8_t*>(&s_xh[buf][bt * 16 + li][kk]);
+                        ah[bt] = *reinterpret_cast<const h8_t*>(&sm.x[sbl][0][bt * 16 + li][kk]);
+                        al[bt] = *reinterpret_cast<const h8_t*>(&sm.x[sbl][1][bt * 16 + li][kk]);
+                    }
 #pragma unroll
-                        for (int t = 0; t < RT; ++t)
-                            C[t][bt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, bw[t][half], C[t][bt], 0, 0, 0);
-                        if constexpr (XS == 2) {
-                            const h8_t al = *reinterpret_cast<const h8_t*>(&s_xl[buf][bt * 16 + li][kk]);
+                    for (int t = 0; t < RT; ++t) {
+                        const uint32_t w0 = r[t].q[j].x, w1 = r[t].q[j].y, v0 = w0 >> 8, v1 = w1 >> 8;
+                        const uint32_t M = half ? 0x00F000F0u : 0x000F000Fu;
+                        const uint32_t sp = half ? shi[t][j] : slo[t][j];
+                        const uint4 q4 = {pk_mul_f16(w0 & M, sp), pk_mul_f16(v0 & M, sp), pk_mul_f16(w1 & M, sp),
+                                          pk_mul_f16(v1 & M, sp)};
+                        const h8_t bw = __builtin_bit_cast(h8_t, q4);
 #pragma unroll
-                            for (int t = 0; t < RT; ++t)
-                                C[t][bt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(al, bw[t][half], C[t][bt], 0, 0, 0);
+                        for (int bt = 0; bt < NBT; ++bt) {
+                            C[t][bt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah[bt], bw, C[t][bt], 0, 0, 0);
+                            C[t][bt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(al[bt], bw, C[t][bt], 0, 0, 0);
                         }
                     }
                 }
-            }
-            // minimum term: sum_g m_g (X_g hi + X_g lo); k 0..7 hi, 8..15 lo, 16..31 zero
+        } else {
+            // chunk c = 32 values = half c/4, l = 32(c%4) + 8s + [0,8); scale index
+            // 8h + 2(c%4) + s/2.  Offset term k = 8 s + e: group 8(s%2) + e.
+            uint32_t A[RT][2][2], B[RT][2][2], H[RT][2][2], scw[RT][4];
 #pragma unroll
             for (int t = 0; t < RT; ++t) {
-                h8_t bm;
-                const uint4 h = cur[t].hdr;
+                const float d = (float)__builtin_bit_cast(_Float16, (uint16_t)r[t].d);
+                dC[t] = d * 16384.0f;   // codes carry 2^-14
+                dM[t] = d * 512.0f;     // -32 sc x: sums staged / 16
 #pragma unroll
-                for (int g = 0; g < 8; ++g) {
-                    uint32_t sc, m;
-                    q4k_scale_min(h.y, h.z, h.w, g, sc, m);
-                    bm[g] = s < 2 ? (_Float16)(float)m : (_Float16)0.0f;
-                    (void)sc;
+                for (int i = 0; i < 4; ++i) scw[t][i] = funnel(r[t].sc[i], r[t].sc[i + 1], r[t].mis);
+#pragma unroll
+                for (int e = 0; e < 8; ++e) {   // group 8 (s % 2) + e
+                    const uint32_t word = (s & 1) ? scw[t][2 + (e >> 2)] : scw[t][e >> 2];
+                    bm[t][e] = (_Float16)(float)(-(int)(int8_t)((word >> (8 * (e & 3))) & 255u));
                 }
 #pragma unroll
-                for (int bt = 0; bt < NBT; ++bt) {
-                    h8_t am;
-                    const _Float16* gsrow = &s_gs[buf][bt * 16 + li][0];
+                for (int hh = 0; hh < 2; ++hh)
 #pragma unroll
-                    for (int g = 0; g < 8; ++g) am[g] = s < 2 ? gsrow[2 * g + s] : (_Float16)0.0f;
-                    Cm[t][bt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(am, bm, Cm[t][bt], 0, 0, 0);
-                }
+                    for (int i = 0; i < 2; ++i) {
+                        A[t][hh][i] = funnel(r[t].a[hh][i], r[t].a[hh][i + 1], r[t].mis);
+                        B[t][hh][i] = funnel(r[t].b[hh][i], r[t].b[hh][i + 1], r[t].mis);
+                        H[t][hh][i] = funnel(r[t].h[hh][i], r[t].h[hh][i + 1], r[t].mis);
+                    }
             }
-        } else {
-            // Q6_K: chunk c (32 values) = half c/4, l = 32(c%4) + 8s + [0,8); group 16 = 2c + s/2
-#pragma unroll
-            for (int t = 0; t < RT; ++t) dsc[t] = (float)__builtin_bit_cast(_Float16, (uint16_t)cur[t].d);
 #pragma unroll
             for (int c = 0; c < 8; ++c) {
-                const int hh = c >> 2, q4 = c & 3;
-                h8_t bw[RT];
-#pragma unroll
-                for (int t = 0; t < RT; ++t) {
-                    const Raw& r = cur[t];
-                    const uint32_t* run = (q4 & 1) ? r.b[hh] : r.a[hh];
-                    const uint32_t a0 = funnel(run[0], run[1], r.mis), a1 = funnel(run[1], run[2], r.mis);
-                    const uint32_t h0 = funnel(r.h[hh][0], r.h[hh][1], r.mis), h1 = funnel(r.h[hh][1], r.h[hh][2], r.mis);
-                    const int nib = (q4 >> 1) * 4, hs = 2 * q4;
-                    const uint32_t c0 = ((a0 >> nib) & 0x0F0F0F0Fu) | (((h0 >> hs) & 0x03030303u) << 4);
-                    const uint32_t c1 = ((a1 >> nib) & 0x0F0F0F0Fu) | (((h1 >> hs) & 0x03030303u) << 4);
-                    const int gidx = 8 * hh + 2 * q4 + (s >> 1);      // scale index 0..15
-                    const uint32_t sw = funnel(r.sc[gidx >> 2], r.sc[(gidx >> 2) + 1], r.mis);
-                    const float scf = (float)(int8_t)((sw >> (8 * (gidx & 3))) & 255u);
-                    const uint32_t sp = h2dup(scf);
-                    const uint32_t tt[4] = {spread(c0, 0), spread(c0, 2), spread(c1, 0), spread(c1, 2)};
-                    uint32_t v[4];
-                    // (1024 + c) - 1056 = c - 32 exactly, then times the int8 scale
-#pragma unroll
-                    for (int e = 0; e < 4; ++e) v[e] = pk_mul_f16(pk_add_f16(tt[e] | 0x64006400u, kMinus1056), sp);
-                    bw[t] = __builtin_bit_cast(h8_t, uint4{v[0], v[1], v[2], v[3]});
-                }
+                const int hh = c >> 2, q4 = c & 3, hs = 2 * q4;
                 const int kk = c * 32 + 8 * s;
+                h8_t ah[NBT], al[NBT];
 #pragma unroll
                 for (int bt = 0; bt < NBT; ++bt) {
-                    const h8_t ah = *reinterpret_cast<const h8_t*>(&s_xh[buf][bt * 16 + li][kk]);
+                    ah[bt] = *reinterpret_cast<const h8_t*>(&sm.x[sbl][0][bt * 16 + li][kk]);
+                    al[bt] = *reinterpret_cast<const h8_t*>(&sm.x[sbl][1][bt * 16 + li][kk]);
+                }
 #pragma unroll
-                    for (int t = 0; t < RT; ++t)
-                        C[t][bt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, bw[t], C[t][bt], 0, 0, 0);
-                    if constexpr (XS == 2) {
-                        const h8_t al = *reinterpret_cast<const h8_t*>(&s_xl[buf][bt * 16 + li][kk]);
+                for (int t = 0; t < RT; ++t) {
+                    // scale 8 hh + 2 q4 + s/2: word 2 hh + q4/2, byte 2 (q4 % 2) + s/2
+                    const uint32_t word = scw[t][2 * hh + (q4 >> 1)];
+                    const float scf = (float)(int)(int8_t)((word >> (8 * (2 * (q4 & 1) + (s >> 1)))) & 255u);
+                    const uint32_t sp = h2dup(scf * 256.0f);
+                    uint32_t v[4];
 #pragma unroll
-                        for (int t = 0; t < RT; ++t)
-                            C[t][bt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(al, bw[t], C[t][bt], 0, 0, 0);
+                    for (int d2 = 0; d2 < 2; ++d2) {
+                        const uint32_t run = (q4 & 1) ? B[t][hh][d2] : A[t][hh][d2];
+                        // 4 c per byte: nibble at bits 2..5, the two high bits at 6..7
+                        const uint32_t nb = (q4 >> 1) ? (run >> 2) : (run << 2);
+                        const uint32_t code = (nb & 0x3C3C3C3Cu) | ((H[t][hh][d2] << (6 - hs)) & 0xC0C0C0C0u);
+                        v[2 * d2] = pk_mul_f16(code & 0x00FF00FFu, sp);
+                        v[2 * d2 + 1] = pk_mul_f16((code >> 8) & 0x00FF00FFu, sp);
+                    }
+                    const h8_t bw = __builtin_bit_cast(h8_t, uint4{v[0], v[1], v[2], v[3]});
+#pragma unroll
+                    for (int bt = 0; bt < NBT; ++bt) {
+                        C[t][bt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah[bt], bw, C[t][bt], 0, 0, 0);
+                        C[t][bt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(al[bt], bw, C[t][bt], 0, 0, 0);
                     }
                 }
             }
         }
-        // superblock scale: acc += d C - dmin 32 Cmin  (per lane: its own row)
+        // group-sum MFMA: A operand rows were laid out by xprep_kernel per k segment
 #pragma unroll
-        for (int t = 0; t < RT; ++t)
+        for (int bt = 0; bt < NBT; ++bt) {
+            const h8_t am = sm.g[sbl][bt * 16 + li][s];
 #pragma unroll
-            for (int bt = 0; bt < NBT; ++bt)
-#pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    float v = fmaf(dsc[t], C[t][bt][e], acc[t][bt][e]);
-                    if constexpr (kQ4) v = fmaf(-dmn[t], Cm[t][bt][e], v);
-                    acc[t][bt][e] = v;
-                }
-        if (i + 1 < nsb) {
-#pragma unroll
-            for (int t = 0; t < RT; ++t) cur[t] = nxt[t];
+            for (int t = 0; t < RT; ++t) Cm[t][bt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(am, bm[t], Cm[t][bt], 0, 0, 0);
         }
-        __syncthreads();
-    }
-
-    // outputs: batch 16 bt + 4 s + e, row (tile base) + li
-#pragma unroll
-    for (int t = 0; t < RT; ++t) {
-        const int r = rb * 64 * RT + wave * 16 * RT + t * 16 + li;
-        if (r >= total_rows) continue;
+        // Q4_K: minimum enters with -dmin; Q6_K: the -sc sign is inside bm
 #pragma unroll
         for (int bt = 0; bt < NBT; ++bt)
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
-                const int b = bt * 16 + 4 * s + e;
-                if (b >= batch) continue;
-                const float v = acc[t][bt][e] * xp.inv[b];
-                part[((int64_t)slab * kMaxBatchTile + b) * total_rows + r] = v;
+                const float inv = sm.inv[sbl][bt * 16 + 4 * s + e];
+#pragma unroll
+                for (int t = 0; t < RT; ++t) {
+                    float v = dC[t] * C[t][bt][e];
+                    v = kQ4 ? fmaf(-dM[t], Cm[t][bt][e], v) : fmaf(dM[t], Cm[t][bt][e], v);
+                    acc[t][bt][e] = fmaf(v, inv, acc[t][bt][e]);
+                }
             }
+    };
+
+    // Tile finished: epilogue (one slab) or partial sums [slab][batch][virtual row].
+    auto finish = [&](int it) {
+        const int tg = gw + (it / nsb) * nw;
+        float tmax[NBT][4];
+#pragma unroll
+        for (int bt = 0; bt < NBT; ++bt)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) tmax[bt][e] = -INFINITY;
+#pragma unroll
+        for (int t = 0; t < RT; ++t) {
+            const int v = tg * kTile + t * 16 + li;
+            const bool ok = v < total_rows;
+#pragma unroll
+            for (int bt = 0; bt < NBT; ++bt)
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const int b = bt * 16 + 4 * s + e;
+                    const float val = acc[t][bt][e];
+                    if (nslab > 1) {
+                        if (ok && b < batch) part[((int64_t)slab * kMaxBatchTile + b) * total_rows + v] = val;
+                    } else if constexpr (MODE == kSwiglu) {
+                        const float up = __shfl_xor(val, 1, kWave);   // odd lane holds the up row
+                        if (ok && b < batch && !(li & 1)) y[(int64_t)b * rows + (v >> 1)] = swiglu(val, up);
+                    } else if constexpr (MODE == kAccumulate) {
+                        if (ok && b < batch) y[(int64_t)b * rows + v] += val;
+                    } else {
+                        if (ok && b < batch) y[(int64_t)b * rows + v] = val;
+                        if (ok) tmax[bt][e] = fmaxf(tmax[bt][e], val);
+                    }
+                    acc[t][bt][e] = 0.0f;
+                }
+        }
+        if constexpr (MODE == kLogits) {
+            if (nslab == 1) {   // per-tile maxima for the argmax: pmax[b][tg]
+#pragma unroll
+                for (int bt = 0; bt < NBT; ++bt)
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        float m = tmax[bt][e];
+                        m = fmaxf(m, __shfl_xor(m, 1, kWave));
+                        m = fmaxf(m, __shfl_xor(m, 2, kWave));
+                        m = fmaxf(m, __shfl_xor(m, 4, kWave));
+                        m = fmaxf(m, __shfl_xor(m, 8, kWave));
+                        const int b = bt * 16 + 4 * s + e;
+                        if (li == 0 && b < batch) pmax[(int64_t)b * ntg + tg] = m;
+                    }
+            }
+        }
+    };
+
+    // Iteration it multiplies buffer it % DEPTH while it + DEPTH - 1 loads.
+    for (int it0 = 0; it0 < nit; it0 += DEPTH) {
+#pragma unroll
+        for (int d = 0; d < DEPTH; ++d) {
+            const int it = it0 + d;
+            load_w(min(it + DEPTH - 1, nit - 1), buf[(d + DEPTH - 1) % DEPTH]);
+            if (it < nit) {
+                compute(it % nsb, buf[d]);
+                if ((it + 1) % nsb == 0) finish(it);
+            }
+        }
     }
 }
 
-// Adds the K-slab partials in slab order and applies the epilogue.
-// kLogits also writes per-block maxima (partial[b * gridDim.x + block]) for the argmax.
+// Adds the K-slab partials in slab order and applies the epilogue.  In kSwiglu the
+// virtual rows interleave gate (even) and up (odd).  kLogits also writes per-block
+// maxima pmax[b * gridDim.x + block] for the argmax.
 template <int MODE>
 __global__ void __launch_bounds__(256) gemm_reduce_kernel(const float* __restrict__ part, int nslab, int rows,
                                                           int batch, float* __restrict__ y, float* __restrict__ pmax) {
@@ -393,8 +494,13 @@ __global__ void __launch_bounds__(256) gemm_reduce_kernel(const float* __restric
         float s = 0.0f, s2 = 0.0f;
         for (int k = 0; k < nslab; ++k) {
             const float* p = part + ((int64_t)k * kMaxBatchTile + b) * total_rows;
-            s += p[r];
-            if constexpr (MODE == kSwiglu) s2 += p[rows + r];
+            if constexpr (MODE == kSwiglu) {
+                const float2 gu = *reinterpret_cast<const float2*>(p + 2 * r);
+                s += gu.x;
+                s2 += gu.y;
+            } else {
+                s += p[r];
+            }
         }
         float* out = y + (int64_t)b * rows + r;
         if constexpr (MODE == kStore || MODE == kLogits) *out = s;

@@ -2,6 +2,7 @@
 // LM-head readout with fused margin argmax (gfx950).
 #include <math.h>
 
+#include <climits>
 #include "rta_gemm.hpp"
 #include "rta_gemv.hpp"
 #include "rta_host.hpp"
@@ -55,51 +56,56 @@ __global__ void __launch_bounds__(256) dequant_kernel(int fmt, const uint8_t* __
 // ------------------------------------------------------------------ argmax ----
 // Phase two of the readout: M = max of the per-task maxima (exact logit values),
 // T = M - margin*|M| evaluated in fp32 without contraction, id = lowest v with
-// logit >= T.  Only tasks whose maximum reaches T are scanned.  Generalises the
+// logit >= T.  The first task whose maximum reaches T holds that id, so only its
+// rows are scanned (in parallel).  Generalises the
 // reference's reduction (resident_math.comp:124-130: strict >, ties -> lower id).
-__global__ void __launch_bounds__(1024) argmax_margin_kernel(const float* __restrict__ logits, int vocab,
-                                                             const float* __restrict__ partial, int ntasks,
-                                                             int rows_per_task, float margin,
-                                                             uint32_t* __restrict__ ids) {
+__global__ void __launch_bounds__(256) argmax_margin_kernel(const float* __restrict__ logits, int vocab,
+                                                            const float* __restrict__ partial, int ntasks,
+                                                            int rows_per_task, float margin,
+                                                            uint32_t* __restrict__ ids) {
 #pragma clang fp contract(off)
-    __shared__ float red_f[32];
-    __shared__ uint32_t red_u[32];
+    __shared__ float red_f[4];
+    __shared__ int red_i[4];
     const int b = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const float* pb = partial + (int64_t)b * ntasks;
     const float* lb = logits + (int64_t)b * vocab;
+    // 1. M = max over the task maxima
     float m = -INFINITY;
-    for (int t = tid; t < ntasks; t += blockDim.x) m = fmaxf(m, pb[t]);
+#pragma unroll 8
+    for (int t = tid; t < ntasks; t += 256) m = fmaxf(m, pb[t]);
     m = group_max(m, kWave);
     if (lane == 0) red_f[wave] = m;
     __syncthreads();
-    if (tid < 64) {
-        float v = tid < (int)(blockDim.x >> 6) ? red_f[tid] : -INFINITY;
-        v = group_max(v, kWave);
-        if (tid == 0) red_f[0] = v;
+    const float M = fmaxf(fmaxf(red_f[0], red_f[1]), fmaxf(red_f[2], red_f[3]));
+    if (!(M > -INFINITY)) {
+        if (tid == 0) ids[b] = 0xffffffffu;
+        return;
     }
+    const float mag = fabsf(M);
+    const float slack = margin * mag;
+    const float T = M - slack;
+    // 2. the first task whose maximum reaches T holds the lowest index with logit >= T
+    int first = INT_MAX;   // branch-free so that the loads of a thread overlap
+#pragma unroll 8
+    for (int t = tid; t < ntasks; t += 256) first = (pb[t] >= T && t < first) ? t : first;
+    for (int off = 32; off > 0; off >>= 1) first = min(first, __shfl_xor(first, off, kWave));
+    if (lane == 0) red_i[wave] = first;
     __syncthreads();
-    const float M = red_f[0];
+    first = min(min(red_i[0], red_i[1]), min(red_i[2], red_i[3]));
     __syncthreads();
-    uint32_t best = 0xffffffffu;
-    if (M > -INFINITY) {
-        const float mag = fabsf(M);
-        const float slack = margin * mag;
-        const float T = M - slack;
-        for (int t = tid; t < ntasks; t += blockDim.x) {
-            if (!(pb[t] >= T)) continue;
-            const int r0 = t * rows_per_task, r1 = min(r0 + rows_per_task, vocab);
-            for (int r = r0; r < r1; ++r)
-                if (lb[r] >= T) { best = min(best, (uint32_t)r); break; }
-        }
+    if (first == INT_MAX) {   // only with NaN logits
+        if (tid == 0) ids[b] = 0xffffffffu;
+        return;
     }
-    for (int off = 32; off > 0; off >>= 1) best = min(best, (uint32_t)__shfl_xor((int)best, off, kWave));
-    if (lane == 0) red_u[wave] = best;
+    // 3. lowest row of that task with logit >= T
+    const int r0 = first * rows_per_task, r1 = min(r0 + rows_per_task, vocab);
+    int best = INT_MAX;
+#pragma unroll 4
+    for (int r = r0 + tid; r < r1; r += 256) best = (lb[r] >= T && r < best) ? r : best;
+    for (int off = 32; off > 0; off >>= 1) best = min(best, __shfl_xor(best, off, kWave));
+    if (lane == 0) red_i[wave] = best;
     __syncthreads();
-    if (tid == 0) {
-        uint32_t v = 0xffffffffu;
-        for (int w = 0; w < (int)(blockDim.x >> 6); ++w) v = min(v, red_u[w]);
-        ids[b] = v;
-    }
+    if (tid == 0) ids[b] = (uint32_t)min(min(red_i[0], red_i[1]), min(red_i[2], red_i[3]));
 }
 
 // ----------------------------------------------------------- launch plumbing ----
@@ -215,75 +221,99 @@ static int check_matrix(int fmt, const void* w, int rows, int cols) {
 }
 
 // ------------------------------------------------------------ MFMA path ----
-constexpr int kMfmaMinBatch = 8;   // batch tiles from this size use the matrix cores
-constexpr int kMfmaRT = 2;         // 16-row tiles per wave: 128 rows per workgroup
+constexpr int kMfmaMinBatch = 8;   // batches from this size use the matrix cores
+constexpr int kMfmaRT = 2;         // 16-row tiles per wave
+constexpr int kPlanCUs = 256;      // CUs the work split is planned for (MI355X)
 
 struct MmaPlan {
-    int total_rows, row_blocks, nslab, sb_per_slab, grid;
+    int nbt, total_rows, ntg, nslab, sb_per_slab, wgs_per_slab, grid;
     size_t x_bytes, part_bytes;
 };
 
-static MmaPlan plan_mfma(int rows, int cols, bool dual) {
+// Work split of one projection over a batch tile: K slabs that fit the LDS, doubled
+// while the (tile, slab) units would leave waves idle.  Independent of the device so
+// that workspace sizes are host queries.
+static MmaPlan plan_mfma(int rows, int cols, int nbt, bool dual) {
     MmaPlan p{};
+    p.nbt = nbt;
     p.total_rows = dual ? 2 * rows : rows;
-    p.row_blocks = (p.total_rows + 64 * kMfmaRT - 1) / (64 * kMfmaRT);
-    const int nsb = cols / 256;
-    int want = (512 + p.row_blocks - 1) / p.row_blocks;   // aim for >= 512 workgroups
-    if (want < 1) want = 1;
-    if (want > nsb) want = nsb;
-    p.sb_per_slab = (nsb + want - 1) / want;
-    p.nslab = (nsb + p.sb_per_slab - 1) / p.sb_per_slab;
-    p.grid = p.row_blocks * p.nslab;
-    p.x_bytes = (size_t)kMaxBatchTile * cols * 2 * 2 + (size_t)kMaxBatchTile * (cols / 32) * 2 * 2 +
-                kMaxBatchTile * sizeof(float);
+    p.ntg = (p.total_rows + 16 * kMfmaRT - 1) / (16 * kMfmaRT);
+    const int nsbt = cols / 256;
+    const int sbmax = kSlabRowSb / (16 * nbt);
+    int nslab = (nsbt + sbmax - 1) / sbmax;
+    while (nslab < nsbt && (int64_t)p.ntg * nslab < (int64_t)kPlanCUs * kGemmWaves) nslab *= 2;
+    if (nslab > nsbt) nslab = nsbt;
+    p.sb_per_slab = (nsbt + nslab - 1) / nslab;
+    p.nslab = (nsbt + p.sb_per_slab - 1) / p.sb_per_slab;
+    int wps = (kPlanCUs + p.nslab - 1) / p.nslab;
+    const int need = (p.ntg + kGemmWaves - 1) / kGemmWaves;
+    p.wgs_per_slab = wps < need ? wps : need;
+    p.grid = p.nslab * p.wgs_per_slab;
+    p.x_bytes = (size_t)kMaxBatchTile * cols * 2 * 2                 // hi, lo
+              + (size_t)kMaxBatchTile * nsbt * 64                    // group-sum operands
+              + (size_t)kMaxBatchTile * nsbt * sizeof(float);        // 1 / scale
     p.x_bytes = (p.x_bytes + 255) & ~(size_t)255;
-    p.part_bytes = (size_t)p.nslab * kMaxBatchTile * p.total_rows * sizeof(float);
+    p.part_bytes = p.nslab > 1 ? (size_t)p.nslab * kMaxBatchTile * p.total_rows * sizeof(float) : 0;
     return p;
 }
 
 static GemmX carve_x(void* ws, int cols) {
     uint8_t* b = static_cast<uint8_t*>(ws);
     GemmX x;
+    const size_t n = (size_t)kMaxBatchTile * cols;
+    const size_t nsbt = cols / 256;
     x.hi = reinterpret_cast<_Float16*>(b);
-    x.lo = reinterpret_cast<_Float16*>(b + (size_t)kMaxBatchTile * cols * 2);
-    x.gs = reinterpret_cast<_Float16*>(b + (size_t)kMaxBatchTile * cols * 4);
-    x.inv = reinterpret_cast<float*>(b + (size_t)kMaxBatchTile * cols * 4 + (size_t)kMaxBatchTile * (cols / 32) * 4);
+    x.lo = reinterpret_cast<_Float16*>(b + 2 * n);
+    x.g = reinterpret_cast<h8_t*>(b + 4 * n);
+    x.inv = reinterpret_cast<float*>(b + 4 * n + (size_t)kMaxBatchTile * nsbt * 64);
     return x;
 }
 
-// Bytes of workspace one K-quant projection needs (0 when the VALU paths serve it).
+// Bytes of workspace one K-quant projection needs (0 when the VALU paths serve it);
+// covers batch tiles of either width.
 static size_t projection_ws(int fmt, int rows, int cols, int batch, bool dual) {
     if (!(fmt == RTA_Q4_K || fmt == RTA_Q6_K) || batch < kMfmaMinBatch) return 0;
-    const MmaPlan p = plan_mfma(rows, cols, dual);
-    return p.x_bytes + p.part_bytes;
+    const MmaPlan a = plan_mfma(rows, cols, 1, dual), b = plan_mfma(rows, cols, 2, dual);
+    return a.x_bytes + (a.part_bytes > b.part_bytes ? a.part_bytes : b.part_bytes);
 }
 
-template <int FMT, int MODE>
-static void launch_mfma_fmt(int nbt, const MmaPlan& p, const Launch& l, const GemmX& xp, float* part, hipStream_t s) {
-    const dim3 g(p.grid), b(256);
-    if (nbt == 1)
-        hipLaunchKernelGGL((gemm_mfma_kernel<FMT, kMfmaRT, 1, 2, MODE>), g, b, 0, s, l.w, l.w2, l.row_bytes, l.rows,
-                           l.cols, xp, l.batch, l.y, part, p.row_blocks, p.sb_per_slab);
-    else
-        hipLaunchKernelGGL((gemm_mfma_kernel<FMT, kMfmaRT, 2, 2, MODE>), g, b, 0, s, l.w, l.w2, l.row_bytes, l.rows,
-                           l.cols, xp, l.batch, l.y, part, p.row_blocks, p.sb_per_slab);
+template <int FMT, int NBT, int MODE>
+static void launch_gemm(const MmaPlan& p, const Launch& l, const GemmX& xp, float* part, float* pmax,
+                        hipStream_t s) {
+    hipLaunchKernelGGL((xprep_kernel<FMT == RTA_Q6_K>), dim3(l.cols / 256, 8 * NBT), dim3(64), 0, s, l.x, l.cols,
+                       l.batch, xp);
+    hipLaunchKernelGGL((gemm_mfma_kernel<FMT, kMfmaRT, NBT, MODE>), dim3(p.grid), dim3(64 * kGemmWaves), 0, s, l.w,
+                       l.w2, l.row_bytes, l.rows, l.cols, xp, l.batch, l.y, part, pmax, p.sb_per_slab,
+                       p.wgs_per_slab);
 }
 
-// One batch tile (<= 32 rows) through xprep -> MFMA GEMM -> fixed-order slab reduce.
+// One batch tile (<= 32 rows): xprep -> MFMA GEMM (-> fixed-order slab reduce).
+// For kLogits, pmax receives per-task maxima [batch][*ntasks_out], tasks of
+// *rpt_out rows.
 template <int MODE>
 static hipError_t run_mfma(int fmt, const Launch& l, void* ws, float* pmax, int* ntasks_out, int* rpt_out,
                            hipStream_t s) {
-    const MmaPlan p = plan_mfma(l.rows, l.cols, MODE == kSwiglu);
+    const int nbt = l.batch > 16 ? 2 : 1;
+    const MmaPlan p = plan_mfma(l.rows, l.cols, nbt, MODE == kSwiglu);
     GemmX xp = carve_x(ws, l.cols);
     float* part = reinterpret_cast<float*>(static_cast<uint8_t*>(ws) + p.x_bytes);
-    hipLaunchKernelGGL(xprep_kernel, dim3(kMaxBatchTile), dim3(256), 0, s, l.x, l.cols, l.batch, xp);
-    const int nbt = l.batch > 16 ? 2 : 1;
-    if (fmt == RTA_Q4_K) launch_mfma_fmt<RTA_Q4_K, MODE>(nbt, p, l, xp, part, s);
-    else launch_mfma_fmt<RTA_Q6_K, MODE>(nbt, p, l, xp, part, s);
-    const dim3 rg((l.rows + 255) / 256, l.batch);
-    hipLaunchKernelGGL((gemm_reduce_kernel<MODE>), rg, dim3(256), 0, s, part, p.nslab, l.rows, l.batch, l.y, pmax);
-    if (ntasks_out) *ntasks_out = (int)rg.x;
-    if (rpt_out) *rpt_out = 256;
+    if (fmt == RTA_Q4_K) {
+        if (nbt == 1) launch_gemm<RTA_Q4_K, 1, MODE>(p, l, xp, part, pmax, s);
+        else launch_gemm<RTA_Q4_K, 2, MODE>(p, l, xp, part, pmax, s);
+    } else {
+        if (nbt == 1) launch_gemm<RTA_Q6_K, 1, MODE>(p, l, xp, part, pmax, s);
+        else launch_gemm<RTA_Q6_K, 2, MODE>(p, l, xp, part, pmax, s);
+    }
+    if (p.nslab > 1) {
+        const dim3 rg((l.rows + 255) / 256, l.batch);
+        hipLaunchKernelGGL((gemm_reduce_kernel<MODE>), rg, dim3(256), 0, s, part, p.nslab, l.rows, l.batch, l.y,
+                           pmax);
+        if (ntasks_out) *ntasks_out = (int)rg.x;
+        if (rpt_out) *rpt_out = 256;
+    } else {
+        if (ntasks_out) *ntasks_out = p.ntg;
+        if (rpt_out) *rpt_out = 16 * kMfmaRT;
+    }
     return hipGetLastError();
 }
 
@@ -478,7 +508,7 @@ int rta_lm_head(int fmt, const void* w, int vocab, int hidden, const float* h, i
                                      logits + (int64_t)b0 * vocab, partial + (int64_t)b0 * vocab, &ntasks, &rpt,
                                      scratch, mma, s, batch);
         if (rc) return rc;
-        hipLaunchKernelGGL(argmax_margin_kernel, dim3(chunk), dim3(1024), 0, s, logits + (int64_t)b0 * vocab,
+        hipLaunchKernelGGL(argmax_margin_kernel, dim3(chunk), dim3(256), 0, s, logits + (int64_t)b0 * vocab,
                            vocab, partial + (int64_t)b0 * vocab, ntasks, rpt, margin, ids + b0);
         if (hipGetLastError() != hipSuccess) return RTA_ERR_LAUNCH;
         b0 += chunk;

@@ -113,9 +113,9 @@ struct Q6K {
     __device__ static __forceinline__ void load(const uint8_t* __restrict__ row, int slot, Raw& r) {
         const uint8_t* blk = row + (slot >> 2) * kBytes;
         const int hh = (slot >> 1) & 1, l0 = (slot & 1) * 16;
-        const uintptr_t addr = reinterpret_cast<uintptr_t>(blk);
-        const uint32_t mis = (uint32_t)(addr & 3u);
-        const uint32_t* a = reinterpret_cast<const uint32_t*>(addr - mis);
+        // aligned down by pointer arithmetic, which keeps the global address space
+        const uint32_t mis = (uint32_t)(reinterpret_cast<uintptr_t>(blk) & 3u);
+        const uint32_t* a = reinterpret_cast<const uint32_t*>(blk - mis);
         const int ia = (64 * hh + l0) >> 2, ib = (64 * hh + 32 + l0) >> 2, ih = (128 + 32 * hh + l0) >> 2;
         const int is = (192 + 8 * hh) >> 2;
 #pragma unroll
