@@ -50,6 +50,8 @@ def parse():
     ap.add_argument("--rows", type=int, default=12288, help="proj workload: output rows")
     ap.add_argument("--cols", type=int, default=4096, help="proj workload: input columns")
     ap.add_argument("--fmt", default="q4k", choices=["q4k", "q6k"], help="proj workload: weight format")
+    ap.add_argument("--packed", action="store_true",
+                    help="proj / mlp / lm_head: weights packed once by rta_pack (tiled layout, matrix cores)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--eager", action="store_true", help="time eager launches instead of a graph replay")
@@ -205,22 +207,31 @@ def w_mlp(torch, args, orc):
     packed = np.concatenate([wg.ravel(), wu.ravel(), wd.ravel()])
     copies = rotation(torch, packed, dev)
     ng, nd = wg.size, wd.size
+    fm = (Q4_K, Q4_K, Q6_K)
+    mats = [(c[:ng], c[ng:2 * ng], c[2 * ng:]) for c in copies]
+    kfm = fm
+    if args.packed:
+        mats = [(ops.pack(Q4_K, g_, inter, hidden), ops.pack(Q4_K, u_, inter, hidden), ops.pack(Q6_K, d_, hidden, inter))
+                for g_, u_, d_ in mats]
+        kfm = tuple(f | ops.TILED for f in fm)
+        del copies
     xd = torch.from_numpy(x).to(dev)
     act = torch.empty(batch, inter, dtype=torch.float32, device=dev)
     y = torch.empty(batch, hidden, dtype=torch.float32, device=dev)
-    fm = (Q4_K, Q4_K, Q6_K)
-    ws = torch.empty(max(1, ops.mlp_workspace_bytes(Q4_K, Q6_K, hidden, inter, batch)), dtype=torch.uint8, device=dev)
+    ws = torch.empty(max(1, ops.mlp_workspace_bytes(kfm[0], kfm[2], hidden, inter, batch)), dtype=torch.uint8,
+                     device=dev)
 
     def step(i):
-        c = copies[i % len(copies)]
-        ops.mlp_swiglu(fm, c[:ng], c[ng:2 * ng], c[2 * ng:], hidden, inter, xd, y=y, act=act, workspace=ws)
+        g_, u_, d_ = mats[i % len(mats)]
+        ops.mlp_swiglu(kfm, g_, u_, d_, hidden, inter, xd, y=y, act=act, workspace=ws)
 
     alg = packed.nbytes + batch * (hidden * 4 + inter * 4 + hidden * 4)
     res = {"alg_bytes": alg, "kernel": "gemv (gate+up fused SwiGLU) then gemv (down)", "step": step,
            "kernel_launch": step, "unit": "GB/s", "value_from_ms": lambda ms: alg / (ms * 1e-3) / 1e9,
            "dtype": "q4_k/q6_k weights x fp32 activations, fp32 accumulate",
-           "config": {"workload": f"SwiGLU MLP 2048->6144->2048 (gate/up Q4_K, down Q6_K), batch {batch}",
-                      "hidden": hidden, "intermediate": inter, "batch": batch, "weight_copies_rotated": len(copies),
+           "config": {"workload": f"SwiGLU MLP 2048->6144->2048 (gate/up Q4_K, down Q6_K), batch {batch}"
+                                  + (" (packed tiles)" if args.packed else ""),
+                      "hidden": hidden, "intermediate": inter, "batch": batch, "weight_copies_rotated": len(mats),
                       "seed": "20261110+2"}}
 
     def check():
@@ -246,25 +257,30 @@ def w_lm_head(torch, args, orc):
     w = synth.random_matrix(rng, Q6_K, vocab, hidden)
     h = (rng.standard_normal((batch, hidden)) * 2.0).astype(np.float32)
     copies = rotation(torch, w, dev)
+    kfmt = Q6_K
+    if args.packed:
+        copies = [ops.pack(Q6_K, c, vocab, hidden) for c in copies]
+        kfmt = Q6_K | ops.TILED
     hd = torch.from_numpy(h).to(dev)
     logits = torch.empty(batch, vocab, dtype=torch.float32, device=dev)
     ids = torch.empty(batch, dtype=torch.int32, device=dev)
-    ws = torch.empty(ops.lm_head_workspace_bytes(Q6_K, vocab, hidden, batch), dtype=torch.uint8, device=dev)
-    gws = torch.empty(max(1, ops.gemv_workspace_bytes(Q6_K, vocab, hidden, batch)), dtype=torch.uint8, device=dev)
+    ws = torch.empty(ops.lm_head_workspace_bytes(kfmt, vocab, hidden, batch), dtype=torch.uint8, device=dev)
+    gws = torch.empty(max(1, ops.gemv_workspace_bytes(kfmt, vocab, hidden, batch)), dtype=torch.uint8, device=dev)
 
     def step(i):
-        ops.lm_head(Q6_K, copies[i % len(copies)], vocab, hidden, hd, margin=1e-4, workspace=ws, logits=logits,
+        ops.lm_head(kfmt, copies[i % len(copies)], vocab, hidden, hd, margin=1e-4, workspace=ws, logits=logits,
                     ids=ids)
 
     def readout(i):  # the dominant kernel alone: the Q6_K logits GEMV
-        ops.gemv(Q6_K, copies[i % len(copies)], vocab, hidden, hd, y=logits, workspace=gws)
+        ops.gemv(kfmt, copies[i % len(copies)], vocab, hidden, hd, y=logits, workspace=gws)
 
     alg = w.nbytes + batch * (hidden * 4 + vocab * 4 + 4)
     alg_k = w.nbytes + batch * (hidden * 4 + vocab * 4)
     res = {"alg_bytes": alg, "alg_bytes_kernel": alg_k, "kernel": "Q6_K logits GEMV (gemv_b1_kernel<Q6_K,R=2,store,KW=1>)",
            "step": step, "kernel_launch": readout, "unit": "GB/s", "value_from_ms": lambda ms: alg / (ms * 1e-3) / 1e9,
            "dtype": "q6_k weights x fp32 activations, fp32 accumulate",
-           "config": {"workload": f"LM head 151936x2048 Q6_K + margin argmax, batch {batch}", "vocab": vocab,
+           "config": {"workload": f"LM head 151936x2048 Q6_K + margin argmax, batch {batch}"
+                                  + (" (packed tiles)" if args.packed else ""), "vocab": vocab,
                       "hidden": hidden, "batch": batch, "weight_copies_rotated": len(copies),
                       "seed": "20261110+4"}}
 
@@ -364,18 +380,23 @@ def w_proj(torch, args, orc):
     w = synth.random_matrix(rng, fmt, rows, cols)
     x = rng.standard_normal((batch, cols)).astype(np.float32)
     copies = rotation(torch, w, dev)
+    kfmt = fmt
+    if args.packed:
+        copies = [ops.pack(fmt, c, rows, cols) for c in copies]
+        kfmt = fmt | ops.TILED
     xd = torch.from_numpy(x).to(dev)
     y = torch.empty(batch, rows, dtype=torch.float32, device=dev)
-    ws = torch.empty(max(1, ops.gemv_workspace_bytes(fmt, rows, cols, batch)), dtype=torch.uint8, device=dev)
+    ws = torch.empty(max(1, ops.gemv_workspace_bytes(kfmt, rows, cols, batch)), dtype=torch.uint8, device=dev)
 
     def step(i):
-        ops.gemv(fmt, copies[i % len(copies)], rows, cols, xd, y=y, workspace=ws)
+        ops.gemv(kfmt, copies[i % len(copies)], rows, cols, xd, y=y, workspace=ws)
 
     alg = w.nbytes + batch * 4 * (cols + rows)
     res = {"alg_bytes": alg, "kernel": "dequant-fused projection (MFMA path from batch 8)", "step": step,
            "kernel_launch": step, "unit": "GB/s", "value_from_ms": lambda ms: alg / (ms * 1e-3) / 1e9,
            "dtype": f"{args.fmt} weights x fp32 activations, fp32 accumulate",
-           "config": {"workload": f"{args.fmt.upper()} projection {rows}x{cols}, batch {batch}", "rows": rows,
+           "config": {"workload": f"{args.fmt.upper()} projection {rows}x{cols}, batch {batch}"
+                                  + (" (packed tiles)" if args.packed else ""), "rows": rows,
                       "cols": cols, "batch": batch, "weight_copies_rotated": len(copies), "seed": "20261110+5"}}
 
     def check():

@@ -39,8 +39,12 @@ enum rta_status {
     RTA_ERR_DEVICE = 8     /* the device error word is non-zero (rta_device_error) */
 };
 
-/* GGUF type codes, as the reference uses them (resident_quant.glsl:6-20). */
-enum rta_format { RTA_F32 = 0, RTA_F16 = 1, RTA_Q4_K = 12, RTA_Q6_K = 14, RTA_BF16 = 30 };
+/* GGUF type codes, as the reference uses them (resident_quant.glsl:6-20).
+ * RTA_TILED marks a K-quant matrix repacked by rta_pack (no counterpart in the
+ * reference, which streams GGUF rows as uploaded); every projection entry point
+ * accepts RTA_Q4_K | RTA_TILED and RTA_Q6_K | RTA_TILED and then runs on the matrix
+ * cores at every batch size. */
+enum rta_format { RTA_F32 = 0, RTA_F16 = 1, RTA_Q4_K = 12, RTA_Q6_K = 14, RTA_BF16 = 30, RTA_TILED = 0x100 };
 
 /* Epilogue of a projection: y = W x, or y += W x (the residual add of the O and
  * down projections, resident_math.comp:70). */
@@ -68,11 +72,25 @@ int64_t rta_row_bytes(int fmt, int64_t cols);
  * Alignment: src 4 bytes (F32, Q4_K) or 2 bytes (F16, BF16, Q6_K); out 4 bytes. */
 int rta_dequant(int fmt, const void* src, int64_t n, float* out, rta_stream_t stream);
 
+/* Bytes of the packed (tiled) form of a [rows x cols] Q4_K or Q6_K matrix, -1 if
+ * invalid: ceil(rows/16) * (cols/256) tiles of 16 GGUF blocks (2304 / 3360 bytes).
+ * No reference counterpart: the packed layout is this library's own. */
+int64_t rta_pack_bytes(int fmt, int rows, int cols);
+
+/* Repacks a device-resident GGUF Q4_K / Q6_K matrix (rows of cols/256 blocks, as
+ * the reference uploads it, optical_resident.cpp:213-252) into tiles of 16 rows x 1
+ * superblock whose bytes are ordered the way the matrix-core readout loads them
+ * (each load instruction reads whole cache lines).  One-time, at load; the result
+ * is used with fmt | RTA_TILED.  dst: rta_pack_bytes() bytes, 16-byte aligned; src
+ * aligned as for rta_gemv.  No reference counterpart. */
+int rta_pack(int fmt, const void* src, int rows, int cols, void* dst, rta_stream_t stream);
+
 /* y[b, r] (=|+=) sum_c W[r, c] x[b, c],  b < batch, r < rows.
  *   x: [batch, cols] fp32 row-major, y: [batch, rows] fp32.
  *   K-quants need cols % 256 == 0; W 16-byte aligned (Q4_K) / 2-byte (Q6_K).
- *   Batch tiles of 8 or more K-quant rows run on the matrix cores and need a
- *   workspace of rta_gemv_workspace_bytes() (256-byte aligned); 0 bytes otherwise.
+ *   Batch tiles of 8 or more K-quant rows, and packed matrices (fmt | RTA_TILED)
+ *   at every batch, run on the matrix cores and need a workspace of
+ *   rta_gemv_workspace_bytes() (256-byte aligned); 0 bytes otherwise.
  * Replaces the projection detector, resident_math.comp:39-75 (op 2, indices
  * 0/1/2/4/6/8) dispatched by Resident::launch, optical_resident.cpp:304-347, and its
  * batched pipelines (optical_resident.cpp:168,343; resident_batch2.comp). */

@@ -61,11 +61,16 @@ struct GemmX {           // prepared x (workspace), batch padded to 32
 };
 
 // ---------------------------------------------------------------- x prep ----
+// Group-sum operand layouts (8 f16 per lane segment s = 0..3 of the superblock):
+//   kXpQ4Row   s0 = hi of 32-groups 0..7, s1 = lo of 0..7, s2 = s3 = 0
+//   kXpQ6Row   s0 = hi of 16-groups 0..7, s1 = hi of 8..15, s2 = lo of 0..7, s3 = lo of 8..15
+//   kXpQ4Tile  s = [hi, lo of 32-group 2s, hi, lo of 2s+1, 0, 0, 0, 0]
+//   kXpQ6Tile  s = [hi, lo of 16-group g(q)] for q = 0..3, g(q) = 8 (s/2) + 2 q + s%2
+enum { kXpQ4Row = 0, kXpQ6Row = 1, kXpQ4Tile = 2, kXpQ6Tile = 3 };
+
 // Block: 64 threads = 2 batch rows x 32 threads; thread = 8 consecutive columns of
-// superblock blockIdx.x.  G16 selects 16-value group sums (Q6_K) over 32 (Q4_K):
-//   Q4_K  segment 0 = hi of groups 0..7, 1 = lo of groups 0..7, 2 and 3 = 0
-//   Q6_K  segment 0 = hi of groups 0..7, 1 = hi of 8..15, 2 = lo of 0..7, 3 = lo of 8..15
-template <bool G16>
+// superblock blockIdx.x.
+template <int LAYOUT>
 __global__ void __launch_bounds__(64) xprep_kernel(const float* __restrict__ x, int cols, int batch, GemmX p) {
     const int lane = threadIdx.x, sb = blockIdx.x;
     const int b = blockIdx.y * 2 + (lane >> 5), t = lane & 31;
@@ -104,24 +109,40 @@ __global__ void __launch_bounds__(64) xprep_kernel(const float* __restrict__ x, 
     _Float16* g = reinterpret_cast<_Float16*>(p.g + ((int64_t)b * nsb + sb) * 4);   // 32 f16
     const float s16 = sum8 + __shfl_xor(sum8, 1, kWave);
     const float s32 = s16 + __shfl_xor(s16, 2, kWave);
-    if constexpr (G16) {
-        if ((t & 1) == 0) {   // group u = t / 2 of 16 columns
+    if constexpr (LAYOUT == kXpQ6Row || LAYOUT == kXpQ6Tile) {
+        if ((t & 1) == 0) {   // 16-group u = t / 2
             const int u = t >> 1;
             const float w = s16 * (1.0f / 16.0f);
-            const _Float16 h = (_Float16)w;
-            g[8 * (u >> 3) + (u & 7)] = h;
-            g[16 + 8 * (u >> 3) + (u & 7)] = (_Float16)(w - (float)h);
+            const _Float16 h = (_Float16)w, l = (_Float16)(w - (float)h);
+            if constexpr (LAYOUT == kXpQ6Row) {
+                g[8 * (u >> 3) + (u & 7)] = h;
+                g[16 + 8 * (u >> 3) + (u & 7)] = l;
+            } else {   // u = 8 hh + 2 q + sg -> segment 2 hh + sg, slot 2 q
+                const int seg = 2 * (u >> 3) + (u & 1), q = (u >> 1) & 3;
+                g[8 * seg + 2 * q] = h;
+                g[8 * seg + 2 * q + 1] = l;
+            }
         }
     } else {
-        const int q = t >> 2;  // group of 32 columns
+        const int q = t >> 2;  // 32-group
         if ((t & 3) == 0) {
             const float w = s32 * (1.0f / 32.0f);
-            const _Float16 h = (_Float16)w;
-            g[q] = h;
-            g[8 + q] = (_Float16)(w - (float)h);
-        } else if ((t & 3) == 1) {
-            g[16 + q] = (_Float16)0.0f;
-            g[24 + q] = (_Float16)0.0f;
+            const _Float16 h = (_Float16)w, l = (_Float16)(w - (float)h);
+            if constexpr (LAYOUT == kXpQ4Row) {
+                g[q] = h;
+                g[8 + q] = l;
+            } else {
+                g[8 * (q >> 1) + 2 * (q & 1)] = h;
+                g[8 * (q >> 1) + 2 * (q & 1) + 1] = l;
+            }
+        } else if ((t & 3) == 1) {   // the zero slots
+            if constexpr (LAYOUT == kXpQ4Row) {
+                g[16 + q] = (_Float16)0.0f;
+                g[24 + q] = (_Float16)0.0f;
+            } else {
+                g[8 * (q >> 1) + 4 + 2 * (q & 1)] = (_Float16)0.0f;
+                g[8 * (q >> 1) + 5 + 2 * (q & 1)] = (_Float16)0.0f;
+            }
         }
     }
 }

@@ -4,6 +4,7 @@
 
 #include <climits>
 #include "rta_gemm.hpp"
+#include "rta_tiled.hpp"
 #include "rta_gemv.hpp"
 #include "rta_host.hpp"
 
@@ -208,7 +209,14 @@ static hipError_t launch_plain(int fmt, const Launch& l, int grid, hipStream_t s
     return hipGetLastError();
 }
 
+static bool is_tiled(int fmt) { return fmt == (RTA_Q4_K | kTiled) || fmt == (RTA_Q6_K | kTiled); }
+
 static int check_matrix(int fmt, const void* w, int rows, int cols) {
+    if (is_tiled(fmt)) {   // packed by rta_pack: 16-byte aligned tiles
+        if (!w) return RTA_ERR_NULL;
+        if (rows <= 0 || cols <= 0 || cols % 256) return RTA_ERR_SHAPE;
+        return reinterpret_cast<uintptr_t>(w) % 16 ? RTA_ERR_ALIGN : RTA_OK;
+    }
     if (!host::valid_format(fmt)) return RTA_ERR_FORMAT;
     if (!w) return RTA_ERR_NULL;
     if (rows <= 0 || cols <= 0) return RTA_ERR_SHAPE;
@@ -269,9 +277,41 @@ static GemmX carve_x(void* ws, int cols) {
     return x;
 }
 
-// Bytes of workspace one K-quant projection needs (0 when the VALU paths serve it);
-// covers batch tiles of either width.
+// Work split of a projection over packed tiles: 16-row tiles are shared out to the
+// waves of each K slab in balanced contiguous ranges and multiplied in pairs (the
+// gate and up tiles of one row range in kSwiglu).
+static MmaPlan plan_tiled(int rows, int cols, int nbt, bool dual) {
+    MmaPlan p{};
+    p.nbt = nbt;
+    p.total_rows = dual ? 2 * rows : rows;
+    const int ntile = (rows + 15) / 16;
+    const int units = dual ? ntile : (ntile + 1) / 2;
+    p.ntg = ntile;
+    const int nsbt = cols / 256;
+    const int sbmax = kSlabRowSb / (16 * nbt);
+    int nslab = (nsbt + sbmax - 1) / sbmax;
+    while (nslab < nsbt && (int64_t)units * nslab < (int64_t)kPlanCUs * kGemmWaves) nslab *= 2;
+    if (nslab > nsbt) nslab = nsbt;
+    p.sb_per_slab = (nsbt + nslab - 1) / nslab;
+    p.nslab = (nsbt + p.sb_per_slab - 1) / p.sb_per_slab;
+    const int wps = (kPlanCUs + p.nslab - 1) / p.nslab;
+    const int need = (units + kGemmWaves - 1) / kGemmWaves;
+    p.wgs_per_slab = wps < need ? wps : need;
+    p.grid = p.nslab * p.wgs_per_slab;
+    p.x_bytes = (size_t)kMaxBatchTile * cols * 2 * 2 + (size_t)kMaxBatchTile * nsbt * 64 +
+                (size_t)kMaxBatchTile * nsbt * sizeof(float);
+    p.x_bytes = (p.x_bytes + 255) & ~(size_t)255;
+    p.part_bytes = p.nslab > 1 ? (size_t)p.nslab * kMaxBatchTile * p.total_rows * sizeof(float) : 0;
+    return p;
+}
+
+// Bytes of workspace one projection needs (0 when the VALU paths serve it); covers
+// batch tiles of either width.
 static size_t projection_ws(int fmt, int rows, int cols, int batch, bool dual) {
+    if (is_tiled(fmt)) {
+        const MmaPlan a = plan_tiled(rows, cols, 1, dual), b = plan_tiled(rows, cols, 2, dual);
+        return a.x_bytes + (a.part_bytes > b.part_bytes ? a.part_bytes : b.part_bytes);
+    }
     if (!(fmt == RTA_Q4_K || fmt == RTA_Q6_K) || batch < kMfmaMinBatch) return 0;
     const MmaPlan a = plan_mfma(rows, cols, 1, dual), b = plan_mfma(rows, cols, 2, dual);
     return a.x_bytes + (a.part_bytes > b.part_bytes ? a.part_bytes : b.part_bytes);
@@ -280,7 +320,7 @@ static size_t projection_ws(int fmt, int rows, int cols, int batch, bool dual) {
 template <int FMT, int NBT, int MODE>
 static void launch_gemm(const MmaPlan& p, const Launch& l, const GemmX& xp, float* part, float* pmax,
                         hipStream_t s) {
-    hipLaunchKernelGGL((xprep_kernel<FMT == RTA_Q6_K>), dim3(l.cols / 256, 8 * NBT), dim3(64), 0, s, l.x, l.cols,
+    hipLaunchKernelGGL((xprep_kernel<FMT == RTA_Q6_K ? kXpQ6Row : kXpQ4Row>), dim3(l.cols / 256, 8 * NBT), dim3(64), 0, s, l.x, l.cols,
                        l.batch, xp);
     hipLaunchKernelGGL((gemm_mfma_kernel<FMT, kMfmaRT, NBT, MODE>), dim3(p.grid), dim3(64 * kGemmWaves), 0, s, l.w,
                        l.w2, l.row_bytes, l.rows, l.cols, xp, l.batch, l.y, part, pmax, p.sb_per_slab,
@@ -317,6 +357,43 @@ static hipError_t run_mfma(int fmt, const Launch& l, void* ws, float* pmax, int*
     return hipGetLastError();
 }
 
+template <int FMT, int NBT, int MODE>
+static void launch_tiled(const MmaPlan& p, const Launch& l, const GemmX& xp, float* part, float* pmax,
+                         hipStream_t s) {
+    hipLaunchKernelGGL((xprep_kernel<FMT == RTA_Q6_K ? kXpQ6Tile : kXpQ4Tile>), dim3(l.cols / 256, 8 * NBT), dim3(64),
+                       0, s, l.x, l.cols, l.batch, xp);
+    hipLaunchKernelGGL((gemm_tiled_kernel<FMT, NBT, MODE>), dim3(p.grid), dim3(64 * kGemmWaves), 0, s, l.w, l.w2,
+                       l.rows, l.cols, xp, l.batch, l.y, part, pmax, p.sb_per_slab, p.wgs_per_slab);
+}
+
+// One batch tile (<= 32 rows) over packed weights: xprep -> tiled GEMM (-> slab reduce).
+template <int MODE>
+static hipError_t run_tiled(int fmt, const Launch& l, void* ws, float* pmax, int* ntasks_out, int* rpt_out,
+                            hipStream_t s) {
+    const int nbt = l.batch > 16 ? 2 : 1;
+    const MmaPlan p = plan_tiled(l.rows, l.cols, nbt, MODE == kSwiglu);
+    GemmX xp = carve_x(ws, l.cols);
+    float* part = reinterpret_cast<float*>(static_cast<uint8_t*>(ws) + p.x_bytes);
+    if ((fmt & 0xff) == RTA_Q4_K) {
+        if (nbt == 1) launch_tiled<RTA_Q4_K, 1, MODE>(p, l, xp, part, pmax, s);
+        else launch_tiled<RTA_Q4_K, 2, MODE>(p, l, xp, part, pmax, s);
+    } else {
+        if (nbt == 1) launch_tiled<RTA_Q6_K, 1, MODE>(p, l, xp, part, pmax, s);
+        else launch_tiled<RTA_Q6_K, 2, MODE>(p, l, xp, part, pmax, s);
+    }
+    if (p.nslab > 1) {
+        const dim3 rg((l.rows + 255) / 256, l.batch);
+        hipLaunchKernelGGL((gemm_reduce_kernel<MODE>), rg, dim3(256), 0, s, part, p.nslab, l.rows, l.batch, l.y,
+                           pmax);
+        if (ntasks_out) *ntasks_out = (int)rg.x;
+        if (rpt_out) *rpt_out = 256;
+    } else {
+        if (ntasks_out) *ntasks_out = p.ntg;
+        if (rpt_out) *rpt_out = 16;
+    }
+    return hipGetLastError();
+}
+
 // Runs one projection over the whole batch: K-quant tiles of >= 8 rows on the matrix
 // cores (32 rows per tile), smaller ones on the VALU kernels (8 rows per tile).
 // For kLogits, partial receives per-task maxima laid out [tile row][ntasks] inside the
@@ -325,12 +402,13 @@ template <int MODE>
 static int run_projection(int fmt, const void* w, const void* w2, int rows, int cols, const float* x, int batch,
                           float* y, float* partial, int* ntasks_out, int* rows_per_task_out, void* ws,
                           size_t ws_bytes, hipStream_t s, int path_batch = 0) {
-    const int64_t row_bytes = host::row_bytes(fmt, cols);
+    const bool tiled = is_tiled(fmt);
+    const int64_t row_bytes = tiled ? 0 : host::row_bytes(fmt, cols);
     int b0 = 0;
     // The path depends on the whole batch, so a row's result never depends on tiling.
     const bool mma = is_kquant(fmt) && (path_batch > 0 ? path_batch : batch) >= kMfmaMinBatch;
     while (b0 < batch) {
-        const int cap = mma ? kMaxBatchTile : 8;
+        const int cap = (mma || tiled) ? kMaxBatchTile : 8;
         const int chunk = batch - b0 < cap ? batch - b0 : cap;
         Launch l{};
         l.w = static_cast<const uint8_t*>(w);
@@ -343,7 +421,10 @@ static int run_projection(int fmt, const void* w, const void* w2, int rows, int 
         l.batch = chunk;
         l.partial = partial ? partial + (int64_t)b0 * rows : nullptr;
         hipError_t e;
-        if (mma) {
+        if (tiled) {
+            if (!ws || ws_bytes < projection_ws(fmt, rows, cols, chunk, MODE == kSwiglu)) return RTA_ERR_WORKSPACE;
+            e = run_tiled<MODE>(fmt, l, ws, l.partial, ntasks_out, rows_per_task_out, s);
+        } else if (mma) {
             if (!ws || ws_bytes < projection_ws(fmt, rows, cols, chunk, MODE == kSwiglu)) return RTA_ERR_WORKSPACE;
             e = run_mfma<MODE>(fmt, l, ws, l.partial, ntasks_out, rows_per_task_out, s);
         } else if (is_kquant(fmt)) {
@@ -418,7 +499,7 @@ int rta_dequant(int fmt, const void* src, int64_t n, float* out, rta_stream_t st
 }
 
 size_t rta_gemv_workspace_bytes(int fmt, int rows, int cols, int batch) {
-    if (rows <= 0 || cols <= 0 || batch <= 0 || (is_kquant(fmt) && cols % 256)) return 0;
+    if (rows <= 0 || cols <= 0 || batch <= 0 || ((is_kquant(fmt) || is_tiled(fmt)) && cols % 256)) return 0;
     return projection_ws(fmt, rows, cols, batch < kMaxBatchTile ? batch : kMaxBatchTile, false);
 }
 
@@ -476,7 +557,7 @@ int rta_mlp_swiglu(int fmt_g, const void* wg, int fmt_u, const void* wu, int fmt
 }
 
 size_t rta_lm_head_workspace_bytes(int fmt, int vocab, int hidden, int batch) {
-    if (vocab <= 0 || hidden <= 0 || batch <= 0 || !host::valid_format(fmt)) return 0;
+    if (vocab <= 0 || hidden <= 0 || batch <= 0 || !(host::valid_format(fmt) || is_tiled(fmt))) return 0;
     // per-task maxima [batch][vocab] (upper bound), then the matrix-core scratch of one tile
     const size_t maxima = ((size_t)vocab * (size_t)batch * sizeof(float) + 255) & ~(size_t)255;
     return maxima + projection_ws(fmt, vocab, hidden, batch < kMaxBatchTile ? batch : kMaxBatchTile, false);
@@ -501,7 +582,7 @@ int rta_lm_head(int fmt, const void* w, int vocab, int hidden, const float* h, i
     // Argmax per batch tile, with the plan that tile was written with.
     int b0 = 0;
     while (b0 < batch) {
-        const int cap = (is_kquant(fmt) && batch >= kMfmaMinBatch) ? kMaxBatchTile : 8;
+        const int cap = ((is_kquant(fmt) && batch >= kMfmaMinBatch) || is_tiled(fmt)) ? kMaxBatchTile : 8;
         const int chunk = batch - b0 < cap ? batch - b0 : cap;
         int ntasks = 0, rpt = 1;
         rc = run_projection<kLogits>(fmt, w, nullptr, vocab, hidden, h + (int64_t)b0 * hidden, chunk,
@@ -514,6 +595,32 @@ int rta_lm_head(int fmt, const void* w, int vocab, int hidden, const float* h, i
         b0 += chunk;
     }
     return RTA_OK;
+}
+
+int64_t rta_pack_bytes(int fmt, int rows, int cols) {
+    if (rows <= 0 || cols <= 0 || cols % 256) return -1;
+    const int64_t tiles = (int64_t)((rows + 15) / 16) * (cols / 256);
+    if (fmt == RTA_Q4_K) return tiles * TileFmt<RTA_Q4_K>::kBytes;
+    if (fmt == RTA_Q6_K) return tiles * TileFmt<RTA_Q6_K>::kBytes;
+    return -1;
+}
+
+int rta_pack(int fmt, const void* src, int rows, int cols, void* dst, rta_stream_t stream) {
+    if (fmt != RTA_Q4_K && fmt != RTA_Q6_K) return RTA_ERR_FORMAT;
+    int rc = check_matrix(fmt, src, rows, cols);
+    if (rc) return rc;
+    if (!dst) return RTA_ERR_NULL;
+    if (reinterpret_cast<uintptr_t>(dst) % 16) return RTA_ERR_ALIGN;
+    const int64_t n2 = rta_pack_bytes(fmt, rows, cols) / 2;
+    const dim3 g((unsigned)((n2 + 255) / 256)), b(256);
+    hipStream_t s = (hipStream_t)stream;
+    if (fmt == RTA_Q4_K)
+        hipLaunchKernelGGL(pack_kernel<RTA_Q4_K>, g, b, 0, s, static_cast<const uint8_t*>(src), rows, cols,
+                           static_cast<uint8_t*>(dst), n2);
+    else
+        hipLaunchKernelGGL(pack_kernel<RTA_Q6_K>, g, b, 0, s, static_cast<const uint8_t*>(src), rows, cols,
+                           static_cast<uint8_t*>(dst), n2);
+    return hipGetLastError() == hipSuccess ? RTA_OK : RTA_ERR_LAUNCH;
 }
 
 }  // extern "C"

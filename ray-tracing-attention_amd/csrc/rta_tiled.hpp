@@ -1,0 +1,396 @@
+// rta_tiled.hpp -- packed ("tiled") K-quant weights and their matrix-core readout.
+//
+// The GGUF row layout spreads the 16 rows a matrix-core tile multiplies over 16
+// separate blocks per superblock, so every load instruction touches 16 short
+// pieces of as many cache lines, and each line is read piecewise by several
+// instructions.  rta_pack rewrites a matrix once (at load time, same size) into
+// tiles of 16 rows x 1 superblock whose bytes are laid out in the order the 64
+// lanes of a wave consume them: every load instruction of the readout then reads
+// whole contiguous lines that no other instruction needs.
+//
+//   Q4_K tile, 2304 bytes (16 x 144):
+//     [0, 256)      row r's 16-byte block header (d, dmin, 12 scale bytes) at 16 r
+//     [256, 1280)   lane l = 16 s + r: bytes [32 s, 32 s + 16) of row r's 128 quant bytes
+//     [1280, 2304)  lane l: bytes [32 s + 16, 32 s + 32)
+//   Q6_K tile, 3360 bytes (16 x 210):
+//     [0, 256)      row r's 16 int8 scales at 16 r
+//     [256, 288)    row r's f16 d at 256 + 2 r
+//     [288, 1312)   lane l = 16 s + r, h = s / 2, o = 16 (s % 2): ql[64 h + o, +16)
+//     [1312, 2336)  lane l: ql[64 h + 32 + o, +16)
+//     [2336, 3360)  lane l: qh[32 h + o, +16)
+//   Tiles are ordered [row tile][superblock]; a last partial row tile is padded
+//   with zero rows (d = 0: they contribute nothing and are never written).
+//
+// Lane (r, s) of a tile thus holds 64 of the superblock's 256 values, 8 per matrix
+// core instruction m = 0..7, each 8 from one scale group:
+//   Q4_K  columns 64 s + 8 m + [0, 8): low nibbles (group 2 s) for m < 4, high
+//         nibbles (group 2 s + 1) for m >= 4
+//   Q6_K  columns 128 (s/2) + 32 (m/2) + 16 (s%2) + 8 (m%2) + [0, 8): group
+//         8 (s/2) + 2 (m/2) + s%2
+// and x is read from LDS at exactly those columns (k-permuted inside each 8 as in
+// the row-layout path).  The minimum (Q4_K) / -32 offset (Q6_K) terms use group
+// sums of x that xprep_kernel lays out per lane segment to match.
+#pragma once
+#include "rta_gemm.hpp"
+
+namespace rta {
+
+constexpr int kTiled = 0x100;   // format flag: RTA_Q4_K | kTiled, RTA_Q6_K | kTiled
+
+template <int FMT>
+struct TileFmt;
+
+template <>
+struct TileFmt<RTA_Q4_K> {
+    static constexpr int kBytes = 2304, kBlock = 144;
+    struct Raw { uint4 hdr, q0, q1; };
+    __device__ static __forceinline__ void load(const uint8_t* __restrict__ c, int lane, Raw& r) {
+        r.hdr = *reinterpret_cast<const uint4*>(c + 16 * (lane & 15));
+        r.q0 = *reinterpret_cast<const uint4*>(c + 256 + 16 * lane);
+        r.q1 = *reinterpret_cast<const uint4*>(c + 1280 + 16 * lane);
+    }
+    // byte offset, inside row r's GGUF block, of tile byte o (o even)
+    __host__ __device__ static inline int source(int o, int& r) {
+        if (o < 256) { r = o >> 4; return o & 15; }
+        const int k = o < 1280 ? 0 : 1, p = o - (k ? 1280 : 256), l = p >> 4;
+        r = l & 15;
+        return 16 + 32 * (l >> 4) + 16 * k + (p & 15);
+    }
+};
+
+template <>
+struct TileFmt<RTA_Q6_K> {
+    static constexpr int kBytes = 3360, kBlock = 210;
+    struct Raw { uint4 sc, a, b, h; uint32_t d; };
+    __device__ static __forceinline__ void load(const uint8_t* __restrict__ c, int lane, Raw& r) {
+        r.sc = *reinterpret_cast<const uint4*>(c + 16 * (lane & 15));
+        r.d = *reinterpret_cast<const uint16_t*>(c + 256 + 2 * (lane & 15));
+        r.a = *reinterpret_cast<const uint4*>(c + 288 + 16 * lane);
+        r.b = *reinterpret_cast<const uint4*>(c + 1312 + 16 * lane);
+        r.h = *reinterpret_cast<const uint4*>(c + 2336 + 16 * lane);
+    }
+    __host__ __device__ static inline int source(int o, int& r) {
+        if (o < 256) { r = o >> 4; return 192 + (o & 15); }
+        if (o < 288) { r = (o - 256) >> 1; return 208 + (o & 1); }
+        const int k = o < 1312 ? 0 : o < 2336 ? 1 : 2;
+        const int p = o - (k == 0 ? 288 : k == 1 ? 1312 : 2336), l = p >> 4, s = l >> 4;
+        r = l & 15;
+        const int h = s >> 1, ofs = 16 * (s & 1) + (p & 15);
+        return k == 0 ? 64 * h + ofs : k == 1 ? 64 * h + 32 + ofs : 128 + 32 * h + ofs;
+    }
+};
+
+// One thread per 2 bytes of the packed matrix.
+template <int FMT>
+__global__ void __launch_bounds__(256) pack_kernel(const uint8_t* __restrict__ src, int rows, int cols,
+                                                   uint8_t* __restrict__ dst, int64_t n2) {
+    using F = TileFmt<FMT>;
+    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (i >= n2) return;
+    const int64_t o = 2 * i;
+    const int nsb = cols >> 8;
+    const int64_t chunk = o / F::kBytes;
+    const int within = (int)(o - chunk * F::kBytes);
+    const int64_t tile = chunk / nsb;
+    const int sb = (int)(chunk - tile * nsb);
+    int r;
+    const int off = F::source(within, r);
+    const int64_t row = tile * 16 + r;
+    uint16_t v = 0;
+    if (row < rows) {
+        const uint8_t* p = src + row * (int64_t)nsb * F::kBlock + (int64_t)sb * F::kBlock + off;
+        v = (uint16_t)(p[0] | (p[1] << 8));
+    }
+    *reinterpret_cast<uint16_t*>(dst + o) = v;
+}
+
+// Scale and minimum of Q4_K group g (0..7, may differ between lanes).
+__device__ __forceinline__ void q4k_scale_min_lane(uint32_t s0, uint32_t s1, uint32_t s2, int g, uint32_t& sc,
+                                                   uint32_t& m) {
+    const uint32_t sh = 8u * (uint32_t)(g & 3);
+    const uint32_t a = (s0 >> sh) & 255u, b = (s1 >> sh) & 255u, mixed = (s2 >> sh) & 255u;
+    const bool lo = g < 4;
+    sc = lo ? (a & 63u) : ((mixed & 15u) | ((a >> 6) << 4));
+    m = lo ? (b & 63u) : ((mixed >> 4) | ((b >> 6) << 4));
+}
+
+__device__ __forceinline__ uint32_t word_of(const uint4& v, int i) {
+    return i == 0 ? v.x : i == 1 ? v.y : i == 2 ? v.z : v.w;
+}
+
+// Units of work: pairs of 16-row tiles (t = 0, 1).  In kSwiglu the pair is (gate
+// tile T, up tile T) of one unit T; otherwise tiles (a + 2u, a + 2u + 1) of the
+// wave's contiguous tile range [a, b), the second one absent at an odd end.
+template <int FMT, int NBT, int MODE>
+__global__ void __launch_bounds__(64 * kGemmWaves) gemm_tiled_kernel(
+    const uint8_t* __restrict__ w, const uint8_t* __restrict__ w2, const int rows, const int cols, const GemmX xp,
+    const int batch, float* __restrict__ y, float* __restrict__ part, float* __restrict__ pmax,
+    const int sb_per_slab, const int wgs_per_slab) {
+    constexpr bool kQ4 = FMT == RTA_Q4_K;
+    using F = TileFmt<FMT>;
+    using Raw = typename F::Raw;
+    using Smem = GemmSmem<NBT>;
+    constexpr int kRows = Smem::kRows;
+    __shared__ Smem sm;
+
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int slab = blockIdx.x / wgs_per_slab, pos = blockIdx.x - slab * wgs_per_slab;
+    const int nslab = gridDim.x / wgs_per_slab;
+    const int nsbt = cols >> 8;
+    const int sb0 = slab * sb_per_slab;
+    const int nsb = min(sb_per_slab, nsbt - sb0);
+    const int s = lane >> 4, li = lane & 15;
+    const int total_rows = MODE == kSwiglu ? 2 * rows : rows;
+    const int ntile = (rows + 15) >> 4;
+
+    // ---- balanced contiguous tile range of this wave
+    const int gw = pos * kGemmWaves + wave, nw = wgs_per_slab * kGemmWaves;
+    const int ta = (int)((int64_t)gw * ntile / nw), tb = (int)((int64_t)(gw + 1) * ntile / nw);
+    const int nunit = MODE == kSwiglu ? tb - ta : (tb - ta + 1) >> 1;
+    const int nit = nunit * nsb;
+
+    auto tiles_of = [&](int u, int& t0, int& t1) {
+        if constexpr (MODE == kSwiglu) { t0 = t1 = ta + u; }
+        else { t0 = ta + 2 * u; t1 = min(t0 + 1, tb - 1); }
+    };
+    auto load_w = [&](int it, Raw* dst) {
+        const int u = it / nsb, sbl = it - u * nsb;
+        int t0, t1;
+        tiles_of(u, t0, t1);
+        const int64_t sb = sb0 + sbl;
+        F::load(w + ((int64_t)t0 * nsbt + sb) * F::kBytes, lane, dst[0]);
+        F::load((MODE == kSwiglu ? w2 : w) + ((int64_t)t1 * nsbt + sb) * F::kBytes, lane, dst[1]);
+    };
+
+    constexpr int DEPTH = 2;   // the next superblock loads while the current one multiplies
+    Raw buf[DEPTH][2];
+    if (nit > 0) {
+#pragma unroll
+        for (int d = 0; d < DEPTH - 1; ++d) load_w(min(d, nit - 1), buf[d]);
+    }
+
+    // ---- x slab -> LDS, every load of a thread issued before its first store
+    {
+        constexpr int kThreads = 64 * kGemmWaves;
+        constexpr int kPer = Smem::kSb * 2 * kRows * 32 / kThreads;
+        const int nchunk = nsb * 2 * kRows * 32;
+        uint4 tmp[kPer];
+#pragma unroll
+        for (int k = 0; k < kPer; ++k) {
+            const int i = min(tid + k * kThreads, nchunk - 1);
+            const int c8 = i & 31, r = (i >> 5) % kRows, plane = ((i >> 5) / kRows) & 1, sbl = i / (64 * kRows);
+            tmp[k] = *reinterpret_cast<const uint4*>((plane ? xp.lo : xp.hi) + (int64_t)r * cols +
+                                                     (int64_t)(sb0 + sbl) * 256 + 8 * c8);
+        }
+        const int gi = min(tid, nsb * kRows * 4 - 1), ii = min(tid, nsb * kRows - 1);
+        const int gq = gi & 3, gr = (gi >> 2) % kRows, gs = gi / (4 * kRows);
+        const h8_t gv = xp.g[((int64_t)gr * nsbt + sb0 + gs) * 4 + gq];
+        const int ir = ii % kRows, is = ii / kRows;
+        const float iv = xp.inv[(int64_t)ir * nsbt + sb0 + is];
+#pragma unroll
+        for (int k = 0; k < kPer; ++k) {
+            const int i = min(tid + k * kThreads, nchunk - 1);
+            const int c8 = i & 31, r = (i >> 5) % kRows, plane = ((i >> 5) / kRows) & 1, sbl = i / (64 * kRows);
+            *reinterpret_cast<uint4*>(&sm.x[sbl][plane][r][8 * c8]) = tmp[k];
+        }
+        sm.g[gs][gr][gq] = gv;
+        sm.inv[is][ir] = iv;
+    }
+    __syncthreads();
+
+    f4_t acc[2][NBT];
+#pragma unroll
+    for (int t = 0; t < 2; ++t)
+#pragma unroll
+        for (int bt = 0; bt < NBT; ++bt) acc[t][bt] = f4_t{0.0f, 0.0f, 0.0f, 0.0f};
+
+    // One superblock of the unit's tiles (the second only when has2).
+    auto compute = [&](int sbl, const Raw* r, bool has2) {
+        f4_t C[2][NBT], Cm[2][NBT];
+#pragma unroll
+        for (int t = 0; t < 2; ++t)
+#pragma unroll
+            for (int bt = 0; bt < NBT; ++bt) C[t][bt] = Cm[t][bt] = f4_t{0.0f, 0.0f, 0.0f, 0.0f};
+        float dC[2], dM[2];
+        h8_t bm[2];
+        // x operands of column offset kk, read once and used by both tiles
+        auto xload = [&](int kk, h8_t* ah, h8_t* al) {
+#pragma unroll
+            for (int bt = 0; bt < NBT; ++bt) {
+                ah[bt] = *reinterpret_cast<const h8_t*>(&sm.x[sbl][0][bt * 16 + li][kk]);
+                al[bt] = *reinterpret_cast<const h8_t*>(&sm.x[sbl][1][bt * 16 + li][kk]);
+            }
+        };
+        auto mma = [&](int t, const h8_t* ah, const h8_t* al, const h8_t& bw) {
+#pragma unroll
+            for (int bt = 0; bt < NBT; ++bt) {
+                C[t][bt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah[bt], bw, C[t][bt], 0, 0, 0);
+                C[t][bt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(al[bt], bw, C[t][bt], 0, 0, 0);
+            }
+        };
+        if constexpr (kQ4) {
+            uint32_t slo[2], shi[2];
+#pragma unroll
+            for (int t = 0; t < 2; ++t) {
+                if (t == 1 && !has2) break;
+                const uint4 h = r[t].hdr;
+                dC[t] = half_lo(h.x) * 16384.0f;     // codes carry 2^-14
+                dM[t] = half_hi(h.x) * 32.0f;        // group sums are staged / 32
+                uint32_t sc0, m0, sc1, m1;
+                q4k_scale_min_lane(h.y, h.z, h.w, 2 * s, sc0, m0);
+                q4k_scale_min_lane(h.y, h.z, h.w, 2 * s + 1, sc1, m1);
+                slo[t] = h2dup((float)sc0 * 1024.0f);
+                shi[t] = h2dup((float)sc1 * 64.0f);
+                const _Float16 fm0 = (_Float16)(float)m0, fm1 = (_Float16)(float)m1, z = (_Float16)0.0f;
+                bm[t] = h8_t{fm0, fm0, fm1, fm1, z, z, z, z};
+            }
+#pragma unroll
+            for (int m = 0; m < 8; ++m) {
+                h8_t ah[NBT], al[NBT];
+                xload(64 * s + 8 * m, ah, al);
+#pragma unroll
+                for (int t = 0; t < 2; ++t) {
+                    if (t == 1 && !has2) break;
+                    const int mq = m & 3;
+                    const uint32_t w0 = word_of(mq < 2 ? r[t].q0 : r[t].q1, 2 * (mq & 1));
+                    const uint32_t w1 = word_of(mq < 2 ? r[t].q0 : r[t].q1, 2 * (mq & 1) + 1);
+                    const uint32_t M = m < 4 ? 0x000F000Fu : 0x00F000F0u;
+                    const uint32_t sp = m < 4 ? slo[t] : shi[t];
+                    const uint4 q4 = {pk_mul_f16(w0 & M, sp), pk_mul_f16((w0 >> 8) & M, sp), pk_mul_f16(w1 & M, sp),
+                                      pk_mul_f16((w1 >> 8) & M, sp)};
+                    mma(t, ah, al, __builtin_bit_cast(h8_t, q4));
+                }
+            }
+        } else {
+            const int hh = s >> 1, sg = s & 1;
+            float scq[2][4];
+#pragma unroll
+            for (int t = 0; t < 2; ++t) {
+                if (t == 1 && !has2) break;
+                const float d = (float)__builtin_bit_cast(_Float16, (uint16_t)r[t].d);
+                dC[t] = d * 16384.0f;   // codes carry 2^-14
+                dM[t] = d * 512.0f;     // -32 sc x: sums staged / 16
+                // scales of groups 8 hh + 2 q + sg, q = 0..3: words 2 hh (q < 2) and 2 hh + 1
+                const uint32_t wa = hh ? r[t].sc.z : r[t].sc.x, wb = hh ? r[t].sc.w : r[t].sc.y;
+#pragma unroll
+                for (int q = 0; q < 4; ++q)
+                    scq[t][q] = (float)(int)(int8_t)(((q < 2 ? wa : wb) >> (8 * (2 * (q & 1) + sg))) & 255u);
+                bm[t] = h8_t{(_Float16)-scq[t][0], (_Float16)-scq[t][0], (_Float16)-scq[t][1], (_Float16)-scq[t][1],
+                             (_Float16)-scq[t][2], (_Float16)-scq[t][2], (_Float16)-scq[t][3], (_Float16)-scq[t][3]};
+            }
+#pragma unroll
+            for (int m = 0; m < 8; ++m) {
+                const int q = m >> 1, half = m & 1;
+                h8_t ah[NBT], al[NBT];
+                xload(128 * hh + 32 * q + 16 * sg + 8 * half, ah, al);
+#pragma unroll
+                for (int t = 0; t < 2; ++t) {
+                    if (t == 1 && !has2) break;
+                    const uint4& run = (q & 1) ? r[t].b : r[t].a;
+                    const uint32_t sp = h2dup(scq[t][q] * 256.0f);
+                    uint32_t v[4];
+#pragma unroll
+                    for (int d2 = 0; d2 < 2; ++d2) {
+                        const uint32_t rw = word_of(run, 2 * half + d2), hw = word_of(r[t].h, 2 * half + d2);
+                        // 4 c per byte: nibble at bits 2..5, the two high bits at 6..7
+                        const uint32_t nb = (q >> 1) ? (rw >> 2) : (rw << 2);
+                        const uint32_t code = (nb & 0x3C3C3C3Cu) | ((hw << (6 - 2 * q)) & 0xC0C0C0C0u);
+                        v[2 * d2] = pk_mul_f16(code & 0x00FF00FFu, sp);
+                        v[2 * d2 + 1] = pk_mul_f16((code >> 8) & 0x00FF00FFu, sp);
+                    }
+                    mma(t, ah, al, __builtin_bit_cast(h8_t, uint4{v[0], v[1], v[2], v[3]}));
+                }
+            }
+        }
+        // group-sum MFMA (A operand laid out per lane segment by xprep_kernel)
+#pragma unroll
+        for (int bt = 0; bt < NBT; ++bt) {
+            const h8_t am = sm.g[sbl][bt * 16 + li][s];
+            Cm[0][bt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(am, bm[0], Cm[0][bt], 0, 0, 0);
+            if (has2) Cm[1][bt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(am, bm[1], Cm[1][bt], 0, 0, 0);
+        }
+#pragma unroll
+        for (int bt = 0; bt < NBT; ++bt)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const float inv = sm.inv[sbl][bt * 16 + 4 * s + e];
+#pragma unroll
+                for (int t = 0; t < 2; ++t) {
+                    if (t == 1 && !has2) break;
+                    float v = dC[t] * C[t][bt][e];
+                    v = kQ4 ? fmaf(-dM[t], Cm[t][bt][e], v) : fmaf(dM[t], Cm[t][bt][e], v);
+                    acc[t][bt][e] = fmaf(v, inv, acc[t][bt][e]);
+                }
+            }
+    };
+
+    // Unit finished: epilogue (one slab) or partial sums [slab][batch][virtual row].
+    auto finish = [&](int u) {
+        int t0, t1;
+        tiles_of(u, t0, t1);
+        const bool has2 = MODE == kSwiglu || t1 != t0;
+#pragma unroll
+        for (int t = 0; t < 2; ++t) {
+            if (t == 1 && !has2) break;
+            const int row = 16 * (t == 0 ? t0 : t1) + li;
+            const bool ok = row < rows;
+            float tmax[NBT][4];
+#pragma unroll
+            for (int bt = 0; bt < NBT; ++bt)
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const int b = bt * 16 + 4 * s + e;
+                    const float val = acc[t][bt][e];
+                    tmax[bt][e] = ok ? val : -INFINITY;
+                    if (nslab > 1) {
+                        const int v = MODE == kSwiglu ? 2 * row + t : row;
+                        if (ok && b < batch) part[((int64_t)slab * kMaxBatchTile + b) * total_rows + v] = val;
+                    } else if constexpr (MODE == kSwiglu) {
+                        if (t == 1 && ok && b < batch) y[(int64_t)b * rows + row] = swiglu(acc[0][bt][e], val);
+                    } else if constexpr (MODE == kAccumulate) {
+                        if (ok && b < batch) y[(int64_t)b * rows + row] += val;
+                    } else {
+                        if (ok && b < batch) y[(int64_t)b * rows + row] = val;
+                    }
+                }
+            if constexpr (MODE == kLogits) {
+                if (nslab == 1) {   // per-tile maxima for the argmax: pmax[b][tile]
+#pragma unroll
+                    for (int bt = 0; bt < NBT; ++bt)
+#pragma unroll
+                        for (int e = 0; e < 4; ++e) {
+                            float m = tmax[bt][e];
+                            m = fmaxf(m, __shfl_xor(m, 1, kWave));
+                            m = fmaxf(m, __shfl_xor(m, 2, kWave));
+                            m = fmaxf(m, __shfl_xor(m, 4, kWave));
+                            m = fmaxf(m, __shfl_xor(m, 8, kWave));
+                            const int b = bt * 16 + 4 * s + e;
+                            if (li == 0 && b < batch) pmax[(int64_t)b * ntile + (t == 0 ? t0 : t1)] = m;
+                        }
+                }
+            }
+        }
+#pragma unroll
+        for (int t = 0; t < 2; ++t)
+#pragma unroll
+            for (int bt = 0; bt < NBT; ++bt) acc[t][bt] = f4_t{0.0f, 0.0f, 0.0f, 0.0f};
+    };
+
+    for (int it0 = 0; it0 < nit; it0 += DEPTH) {
+#pragma unroll
+        for (int d = 0; d < DEPTH; ++d) {
+            const int it = it0 + d;
+            load_w(min(it + DEPTH - 1, nit - 1), buf[(d + DEPTH - 1) % DEPTH]);
+            if (it < nit) {
+                const int u = it / nsb;
+                int t0, t1;
+                tiles_of(u, t0, t1);
+                compute(it - u * nsb, buf[d], MODE == kSwiglu || t1 != t0);
+                if (it - u * nsb == nsb - 1) finish(u);
+            }
+        }
+    }
+}
+
+}  // namespace rta

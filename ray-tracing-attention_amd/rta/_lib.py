@@ -12,6 +12,7 @@ LIB_PATH = PKG_ROOT / "lib" / "librta.so"
 
 # GGUF type codes (resident_quant.glsl:6-20)
 F32, F16, Q4_K, Q6_K, BF16 = 0, 1, 12, 14, 30
+TILED = 0x100   # fmt | TILED: a K-quant matrix packed by rta_pack
 EPI_STORE, EPI_ACCUMULATE = 0, 1
 DEVERR_HITS, DEVERR_VOCAB, DEVERR_DETECTOR = 8, 2048, 65536
 
@@ -25,6 +26,8 @@ SIGNATURES = {
     "rta_device_error": (_i, [_u32p, _i]),
     "rta_row_bytes": (_i64, [_i, _i64]),
     "rta_dequant": (_i, [_i, _p, _i64, _p, _p]),
+    "rta_pack_bytes": (_i64, [_i, _i, _i]),
+    "rta_pack": (_i, [_i, _p, _i, _i, _p, _p]),
     "rta_gemv_workspace_bytes": (_sz, [_i, _i, _i, _i]),
     "rta_gemv": (_i, [_i, _p, _i, _i, _p, _i, _p, _i, _p, _sz, _p]),
     "rta_mlp_workspace_bytes": (_sz, [_i, _i, _i, _i, _i]),

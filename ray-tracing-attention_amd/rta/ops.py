@@ -9,7 +9,7 @@ import ctypes
 import torch
 
 from . import _lib
-from ._lib import BF16, F16, F32, Q4_K, Q6_K, EPI_ACCUMULATE, EPI_STORE, check
+from ._lib import BF16, F16, F32, Q4_K, Q6_K, TILED, EPI_ACCUMULATE, EPI_STORE, check
 
 KQUANT_BYTES = {Q4_K: 144, Q6_K: 210}
 
@@ -44,6 +44,22 @@ def dequant(fmt, blocks, n):
     _dev(blocks, "blocks")
     out = torch.empty(n, dtype=torch.float32, device=blocks.device)
     check(lib.rta_dequant(fmt, _ptr(blocks), n, _ptr(out), _stream()), "rta_dequant")
+    return out
+
+
+def pack_bytes(fmt, rows, cols):
+    return int(_lib.load().rta_pack_bytes(fmt, rows, cols))
+
+
+def pack(fmt, w, rows, cols):
+    """Packed (tiled) copy of a device GGUF Q4_K / Q6_K matrix, for use with fmt | TILED."""
+    lib = _lib.load()
+    _dev(w, "w")
+    n = pack_bytes(fmt, rows, cols)
+    if n < 0:
+        raise ValueError(f"cannot pack format {fmt} of shape {rows}x{cols}")
+    out = torch.empty(n, dtype=torch.uint8, device=w.device)
+    check(lib.rta_pack(fmt, _ptr(w), rows, cols, _ptr(out), _stream()), "rta_pack")
     return out
 
 

@@ -48,6 +48,12 @@ def test_host_queries(lib):
     assert lib.rta_mlp_workspace_bytes(_lib.Q4_K, _lib.Q6_K, 2048, 6144, 4) == 0
     assert lib.rta_decode_attention_workspace_bytes(16, 16, 4, 128, 32768) == 16 * 4 * 128 * 4 * 130 * 4
     assert lib.rta_decode_attention_workspace_bytes(16, 16, 4, 64, 32768) == 0
+    # packed (tiled) matrices: ceil(rows/16) * (cols/256) tiles of 16 blocks
+    assert lib.rta_pack_bytes(_lib.Q4_K, 4096, 4096) == 256 * 16 * 2304
+    assert lib.rta_pack_bytes(_lib.Q6_K, 37, 512) == 3 * 2 * 3360
+    assert lib.rta_pack_bytes(_lib.Q4_K, 8, 100) == -1
+    assert lib.rta_pack_bytes(_lib.F16, 8, 256) == -1
+    assert lib.rta_gemv_workspace_bytes(_lib.Q4_K | _lib.TILED, 4096, 4096, 1) > 0   # matrix cores at any batch
 
 
 def test_argument_errors_are_reported_before_launch(lib):
@@ -69,6 +75,11 @@ def test_argument_errors_are_reported_before_launch(lib):
     assert lib.rta_lm_head(_lib.Q6_K, FAKE, 300, 256, FAKE, 1, ctypes.c_float(-1.0), FAKE, FAKE, FAKE, 1 << 20,
                            None) == E["range"]
     assert lib.rta_dequant(_lib.Q6_K, FAKE, 100, FAKE, None) == E["shape"]
+    assert lib.rta_pack(_lib.F32, FAKE, 8, 256, FAKE, None) == E["format"]
+    assert lib.rta_pack(_lib.Q4_K, FAKE, 8, 256, FAKE_ODD, None) == E["align"]
+    assert lib.rta_pack(_lib.Q4_K, FAKE, 8, 200, FAKE, None) == E["shape"]
+    assert G(_lib.Q4_K | _lib.TILED, FAKE_ODD, 8, 256, FAKE, 1, FAKE, 0) == E["align"]
+    assert G(_lib.Q4_K | _lib.TILED, FAKE, 8, 256, FAKE, 1, FAKE, 0) == E["ws"]     # tiled always needs scratch
     assert lib.rta_rope(FAKE, 1, 1, 7, 7, FAKE, ctypes.c_double(1e6), None) == E["shape"]
     assert lib.rta_rope(FAKE, 1, 1, 8, 8, FAKE, ctypes.c_double(-1.0), None) == E["range"]
     args = [FAKE, 1, 16, 4, 64, FAKE, _lib.Q4_K, _lib.Q6_K, FAKE, FAKE, 1024, 4096, 1024, None, FAKE, FAKE, FAKE,
