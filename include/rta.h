@@ -55,6 +55,7 @@ enum rta_epilogue { RTA_EPI_STORE = 0, RTA_EPI_ACCUMULATE = 1 };
 #define RTA_DEVERR_HITS 8u          /* visible history count mismatch          */
 #define RTA_DEVERR_VOCAB 2048u      /* vocabulary coverage != V                */
 #define RTA_DEVERR_DETECTOR 65536u  /* non-finite query / key / score          */
+#define RTA_DEVERR_TOKEN 4096u      /* token id >= vocabulary (rta_embed); no reference bit */
 
 int rta_version(void);
 const char* rta_status_string(int status);
@@ -163,6 +164,60 @@ int rta_decode_attention(const float* q, int nseq, int hq, int hkv, int hd,
                          const int64_t* slot_base, const int32_t* ctx_len, int64_t capacity,
                          int64_t n_slots, int max_ctx, const float* gate, float* out, float* m_out, float* z_out,
                          void* workspace, size_t workspace_bytes, rta_stream_t stream);
+
+/* ---------------- the rest of a decoder step (resident_math.comp ops 0, 1, 14, 15,
+ * 18-21, 34); every call is stream ordered, allocates nothing, validates on the host. */
+
+/* op 0, token embedding (resident_math.comp:30-32; optical_resident.cpp generation
+ * feeds control[0]): out[b, :] = decoded row ids[b] of table [vocab x hidden] in fmt
+ * (bit exact with rta_dequant).  Ids >= vocab give zeros and set RTA_DEVERR_TOKEN. */
+int rta_embed(int fmt, const void* table, int vocab, int hidden, const uint32_t* ids, int batch, float* out,
+              rta_stream_t stream);
+
+/* op 1, RMSNorm (resident_math.comp:33-38; Resident::layer, optical_resident.cpp:456,481):
+ * out[r, :] = x[r, :] * w / sqrt(mean(x[r, :]^2) + eps).  width % 4 == 0; x, w, out
+ * 16-byte aligned; out may equal x (op 1 index 2 normalises in place). */
+int rta_rmsnorm(const float* x, const float* w, int rows, int width, float eps, float* out, rta_stream_t stream);
+
+/* ops 14 (QK-norm), 15 (gated norm) and the L2 norm of op 20
+ * (resident_math.comp:113-115,139-140), in place over heads of hd (64/128/256) values:
+ *   x = x * w[h*hd + c] / sqrt(sum(x^2) / (mean ? hd : 1) + eps) * (gate ? g*sigmoid(g) : 1)
+ * w may be NULL (no weight); gate NULL for ops 14 and 20.  Row strides in floats. */
+int rta_head_norm(float* x, int x_stride, const float* w, const float* gate, int gate_stride, int rows, int heads,
+                  int hd, int mean, float eps, rta_stream_t stream);
+
+/* op 18 after its two projections (resident_math.comp:131-133):
+ *   decay[b, h] = exp(-exp(a_log[h]) * softplus(a[b, h] + dt_bias[h])),  beta = sigmoid(b[b, h]);
+ * a, b: [batch, >= heads] with row stride `stride`. */
+int rta_delta_gates(const float* a, const float* b, int stride, const float* a_log, const float* dt_bias, int batch,
+                    int heads, float* decay, float* beta, rta_stream_t stream);
+
+/* ops 19 + 20 for one new token per sequence (resident_math.comp:134-140): causal
+ * depthwise convolution of 4 taps + SiLU over the q | k | v projections (3 W values,
+ * W = heads * hd, hd = 128), then per-head L2 normalisation of q and k.
+ *   raw [batch, >= 3W] (stride raw_stride); state [batch, 3W, 3] the three previous raw
+ *   values, oldest first, shifted in place; w [3W, 4] (16-byte aligned); out [batch, 3W]. */
+int rta_short_conv(const float* raw, int raw_stride, float* state, const float* w, int batch, int heads, int hd,
+                   float eps, float* out, rta_stream_t stream);
+
+/* op 21 / resident_state.comp, one token per sequence: the gated delta rule on the
+ * fp32 state [batch, heads, hd, hd] ([value][key], updated in place), hd = 128:
+ *   S = decay S;  u = S k;  S += beta (v - u) k^T;  o = S q / sqrt(hd)
+ * qkv: [batch, >= 3 heads hd] (q | k | v as rta_short_conv writes them).  With norm_w,
+ * op 15 is fused: o = rmsnorm_hd(o) * norm_w[h hd + c] * g sigmoid(g), g = gate[b, h hd + c].
+ * out [batch, >= heads hd] with row stride out_stride. */
+int rta_delta_rule(float* state, const float* qkv, int qkv_stride, const float* decay, const float* beta, int batch,
+                   int heads, int hd, const float* norm_w, const float* gate, int gate_stride, float eps, float* out,
+                   int out_stride, rta_stream_t stream);
+
+/* op 34, history packer (resident_history_quant.glsl:9-41; Resident::layer,
+ * optical_resident.cpp:461): the new key and value rows of each sequence, k[b, :kvw]
+ * and v[b, :kvw], quantised into one packet (one Q4_K and one Q6_K field, fmt_k !=
+ * fmt_v, rta_history_bytes(kvw) bytes) written to packet slot[b] of `packets`
+ * (n_slots slots; a slot outside sets RTA_DEVERR_HITS).  Bit exact with the
+ * reference's fp32 op order; exact .5 ties of the code rounding resolve to even. */
+int rta_pack_history(const float* k, int k_stride, const float* v, int v_stride, int batch, int kvw, int fmt_k,
+                     int fmt_v, const int64_t* slot, int64_t n_slots, void* packets, rta_stream_t stream);
 
 #ifdef __cplusplus
 }

@@ -33,6 +33,12 @@ _SIG = {
     "orc_pack_history": (_i, [_p, _p, _i, _i, _i, _p]),
     "orc_packet_value": (_f, [_p, _i, _i, _i, _i, _i]),
     "orc_decode_attention": (_i, [_p, _i, _i, _i, _i, _p, _i, _i, _p, _p, _i64, _p, _p, _p, _p]),
+    "orc_embed": (_i, [_i, _p, _i, _i, _p, _i, _p]),
+    "orc_rmsnorm": (None, [_p, _p, _i, _i, _d, _p]),
+    "orc_head_norm": (None, [_p, _i, _p, _p, _i, _i, _i, _i, _i, _d, _p]),
+    "orc_delta_gates": (None, [_p, _p, _i, _p, _p, _i, _i, _p, _p]),
+    "orc_short_conv": (None, [_p, _i, _p, _p, _i, _i, _i, _d, _p, _p]),
+    "orc_delta_rule": (None, [_p, _p, _p, _p, _i, _p, _p, _i, _i, _i, _p]),
 }
 
 _LIB = None
@@ -147,3 +153,67 @@ def decode_attention(q, packets, fmt_k, fmt_v, slot_base, ctx_len, capacity, hkv
                                     _p_(out), _p_(m), _p_(z))
     assert rc == 0, rc
     return out, m, z
+
+
+# ---- the rest of a decoder step ----
+def embed(fmt, table, vocab, hidden, ids):
+    ids = _c(ids, np.uint32)
+    out = np.empty((ids.size, hidden), dtype=np.float32)
+    rc = lib().orc_embed(fmt, _p_(_c(table, np.uint8)), vocab, hidden, _p_(ids), ids.size, _p_(out))
+    assert rc == 0, rc
+    return out
+
+
+def rmsnorm(x, w, eps=1e-6):
+    x = _c(x, np.float32)
+    rows, width = x.reshape(-1, x.shape[-1]).shape
+    out = np.empty((rows, width), dtype=np.float64)
+    lib().orc_rmsnorm(_p_(x), _p_(_c(w, np.float32)), rows, width, eps, _p_(out))
+    return out.reshape(x.shape)
+
+
+def head_norm(x, heads, hd, w=None, gate=None, mean=True, eps=1e-6):
+    """x [rows, >= heads*hd] (row stride = x.shape[1]); gate likewise or None."""
+    x = _c(x, np.float32)
+    rows = x.shape[0]
+    g = None if gate is None else _c(gate, np.float32)
+    out = np.empty((rows, heads * hd), dtype=np.float64)
+    lib().orc_head_norm(_p_(x), x.shape[1], _p_(None if w is None else _c(w, np.float32)), _p_(g),
+                        0 if g is None else g.shape[1], rows, heads, hd, int(bool(mean)), eps, _p_(out))
+    return out
+
+
+def delta_gates(a, b, a_log, dt_bias):
+    a, b = _c(a, np.float32), _c(b, np.float32)
+    batch, heads = a.shape
+    decay = np.empty((batch, heads), dtype=np.float64)
+    beta = np.empty((batch, heads), dtype=np.float64)
+    bb = np.ascontiguousarray(b)
+    assert bb.shape == a.shape
+    # a and b are passed as separate [batch, heads] arrays with the same row stride
+    lib().orc_delta_gates(_p_(a), _p_(bb), heads, _p_(_c(a_log, np.float32)), _p_(_c(dt_bias, np.float32)), batch,
+                          heads, _p_(decay), _p_(beta))
+    return decay, beta
+
+
+def short_conv(raw, state, w, heads, hd, eps=1e-6):
+    """raw [batch, >= 3*heads*hd]; state [batch, 3*heads*hd, 3]; w [3*heads*hd, 4]."""
+    raw = _c(raw, np.float32)
+    batch = raw.shape[0]
+    W3 = 3 * heads * hd
+    out = np.empty((batch, W3), dtype=np.float64)
+    new_state = np.empty((batch, W3, 3), dtype=np.float32)
+    lib().orc_short_conv(_p_(raw), raw.shape[1], _p_(_c(state, np.float32)), _p_(_c(w, np.float32)), batch, heads,
+                         hd, eps, _p_(out), _p_(new_state))
+    return out, new_state
+
+
+def delta_rule(state, q, k, v, decay, beta):
+    """state [batch, heads, hd, hd] fp64 (updated copy returned); q, k, v [batch, heads*hd]."""
+    state = np.array(state, dtype=np.float64, order="C", copy=True)
+    batch, heads, hd, _ = state.shape
+    q, k, v = (_c(a, np.float64) for a in (q, k, v))
+    out = np.empty((batch, heads * hd), dtype=np.float64)
+    lib().orc_delta_rule(_p_(state), _p_(q), _p_(k), _p_(v), q.shape[1], _p_(_c(decay, np.float64)),
+                         _p_(_c(beta, np.float64)), batch, heads, hd, _p_(out))
+    return state, out

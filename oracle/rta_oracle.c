@@ -276,6 +276,12 @@ static float halfround(float v) { return orc_half_to_float(orc_float_to_half(v))
  * implementation-defined there -- parity for exact ties is unpinned). */
 static float clampf(float v, float lo, float hi) { return v < lo ? lo : (v > hi ? hi : v); }
 
+/* GLSL min / max (returns x unless y is strictly smaller / larger): decides the sign of
+ * zero where the packer compares +0 with -0 (a group minimum -min(0, x) of an all-zero
+ * group is -0). */
+static float glsl_min(float x, float y) { return y < x ? y : x; }
+static float glsl_max(float x, float y) { return x < y ? y : x; }
+
 /* Q4_K field of 256 coordinates, min/max groups of 32 (resident_history_quant.glsl:14-16,
  * 21-23, 27-29, 31-33, 36). */
 static void pack_q4k_field(const float* x, uint8_t* blk) {
@@ -283,12 +289,12 @@ static void pack_q4k_field(const float* x, uint8_t* blk) {
     memset(blk, 0, 144);
     for (int g = 0; g < 8; ++g) {
         float lo = 0.0f, hi = 0.0f;
-        for (int i = 0; i < 32; ++i) { float v = x[g * 32 + i]; lo = fminf(lo, v); hi = fmaxf(hi, v); }
+        for (int i = 0; i < 32; ++i) { float v = x[g * 32 + i]; lo = glsl_min(lo, v); hi = glsl_max(hi, v); }
         float span = hi - lo;
         gscale[g] = span / 15.0f; gmin[g] = -lo;
     }
     float maxD = 0.0f, maxMin = 0.0f;
-    for (int g = 0; g < 8; ++g) { maxD = fmaxf(maxD, gscale[g]); maxMin = fmaxf(maxMin, gmin[g]); }
+    for (int g = 0; g < 8; ++g) { maxD = glsl_max(maxD, gscale[g]); maxMin = glsl_max(maxMin, gmin[g]); }
     float d = halfround(maxD / 63.0f), dm = halfround(maxMin / 63.0f);
     uint16_t hd = orc_float_to_half(d), hm = orc_float_to_half(dm);
     blk[0] = hd & 255; blk[1] = hd >> 8; blk[2] = hm & 255; blk[3] = hm >> 8;
@@ -317,11 +323,11 @@ static void pack_q6k_field(const float* x, uint8_t* blk) {
     memset(blk, 0, 210);
     for (int g = 0; g < 16; ++g) {
         float hi = 0.0f;
-        for (int i = 0; i < 16; ++i) hi = fmaxf(hi, fabsf(x[g * 16 + i]));
+        for (int i = 0; i < 16; ++i) hi = glsl_max(hi, fabsf(x[g * 16 + i]));
         gscale[g] = hi / 31.0f;
     }
     float maxD = 0.0f;
-    for (int g = 0; g < 16; ++g) maxD = fmaxf(maxD, gscale[g]);
+    for (int g = 0; g < 16; ++g) maxD = glsl_max(maxD, gscale[g]);
     float d = halfround(maxD / 127.0f);
     uint16_t hd = orc_float_to_half(d);
     blk[208] = hd & 255; blk[209] = hd >> 8;
@@ -408,4 +414,110 @@ int orc_decode_attention(const float* q, int nseq, int hq, int hkv, int hd,
             free(scores); free(field);
         }
     return 0;
+}
+
+/* ---- the rest of a decoder step ---- */
+
+/* resident_math.comp:30-32 (op 0): the embedding row, decoded like every weight. */
+int orc_embed(int fmt, const void* table, int vocab, int hidden, const uint32_t* ids, int batch, float* out) {
+    int64_t rb = orc_row_bytes(fmt, hidden);
+    if (rb <= 0 || !table || !ids || !out) return 2;
+    for (int b = 0; b < batch; ++b) {
+        if (ids[b] >= (uint32_t)vocab) return 7;
+        int rc = orc_dequant(fmt, (const uint8_t*)table + (int64_t)ids[b] * rb, hidden, out + (int64_t)b * hidden);
+        if (rc) return rc;
+    }
+    return 0;
+}
+
+/* resident_math.comp:33-38 (op 1). */
+void orc_rmsnorm(const float* x, const float* w, int rows, int width, double eps, double* out) {
+    for (int r = 0; r < rows; ++r) {
+        const float* xr = x + (int64_t)r * width;
+        double ss = 0.0;
+        for (int c = 0; c < width; ++c) ss += (double)xr[c] * xr[c];
+        double inv = 1.0 / sqrt(ss / width + eps);
+        for (int c = 0; c < width; ++c) out[(int64_t)r * width + c] = xr[c] * inv * (double)w[c];
+    }
+}
+
+/* resident_math.comp:113-115 (ops 14, 15) and :139-140 (op 20). */
+void orc_head_norm(const float* x, int x_stride, const float* w, const float* gate, int gate_stride, int rows,
+                   int heads, int hd, int mean, double eps, double* out) {
+    for (int r = 0; r < rows; ++r)
+        for (int h = 0; h < heads; ++h) {
+            const float* xh = x + (int64_t)r * x_stride + (int64_t)h * hd;
+            double ss = 0.0;
+            for (int c = 0; c < hd; ++c) ss += (double)xh[c] * xh[c];
+            double inv = 1.0 / sqrt(ss / (mean ? hd : 1) + eps);
+            for (int c = 0; c < hd; ++c) {
+                double v = xh[c] * inv * (w ? (double)w[h * hd + c] : 1.0);
+                if (gate) {
+                    double g = gate[(int64_t)r * gate_stride + (int64_t)h * hd + c];
+                    v *= g * orc_sigmoid(g);
+                }
+                out[((int64_t)r * heads + h) * hd + c] = v;
+            }
+        }
+}
+
+static double softplus_d(double v) { return (v > 0 ? v : 0.0) + log1p(exp(-fabs(v))); }
+
+/* resident_math.comp:131-133 (op 18); softplus as resident_common.glsl:80. */
+void orc_delta_gates(const float* a, const float* b, int stride, const float* a_log, const float* dt_bias,
+                     int batch, int heads, double* decay, double* beta) {
+    for (int r = 0; r < batch; ++r)
+        for (int h = 0; h < heads; ++h) {
+            double av = a[(int64_t)r * stride + h], bv = b[(int64_t)r * stride + h];
+            decay[(int64_t)r * heads + h] = exp(-exp((double)a_log[h]) * softplus_d(av + dt_bias[h]));
+            beta[(int64_t)r * heads + h] = orc_sigmoid(bv);
+        }
+}
+
+/* resident_math.comp:134-140 (ops 19, 20) for one new token. */
+void orc_short_conv(const float* raw, int raw_stride, const float* state, const float* w, int batch, int heads,
+                    int hd, double eps, double* out, float* new_state) {
+    int W = heads * hd, W3 = 3 * W;
+    for (int b = 0; b < batch; ++b) {
+        double* o = out + (int64_t)b * W3;
+        for (int c = 0; c < W3; ++c) {
+            const float* st = state + ((int64_t)b * W3 + c) * 3;
+            double s = 0.0;
+            for (int j = 0; j < 3; ++j) s += (double)w[c * 4 + j] * st[j];
+            s += (double)w[c * 4 + 3] * raw[(int64_t)b * raw_stride + c];
+            o[c] = s * orc_sigmoid(s);
+            float* ns = new_state + ((int64_t)b * W3 + c) * 3;
+            ns[0] = st[1]; ns[1] = st[2]; ns[2] = raw[(int64_t)b * raw_stride + c];
+        }
+        for (int part = 0; part < 2; ++part)
+            for (int h = 0; h < heads; ++h) {
+                double* y = o + part * W + h * hd;
+                double ss = 0.0;
+                for (int c = 0; c < hd; ++c) ss += y[c] * y[c];
+                double inv = 1.0 / sqrt(ss + eps);
+                for (int c = 0; c < hd; ++c) y[c] *= inv;
+            }
+    }
+}
+
+/* resident_math.comp:141-147 (op 21) and resident_state.comp:16-33. */
+void orc_delta_rule(double* state, const double* q, const double* k, const double* v, int stride,
+                    const double* decay, const double* beta, int batch, int heads, int hd, double* out) {
+    double scale = 1.0 / sqrt((double)hd);
+    for (int b = 0; b < batch; ++b)
+        for (int h = 0; h < heads; ++h) {
+            double* S = state + ((int64_t)b * heads + h) * hd * hd;
+            const double* qh = q + (int64_t)b * stride + (int64_t)h * hd;
+            const double* kh = k + (int64_t)b * stride + (int64_t)h * hd;
+            const double* vh = v + (int64_t)b * stride + (int64_t)h * hd;
+            double dc = decay[(int64_t)b * heads + h], bt = beta[(int64_t)b * heads + h];
+            for (int row = 0; row < hd; ++row) {
+                double* s = S + (int64_t)row * hd;
+                double u = 0.0;
+                for (int c = 0; c < hd; ++c) { s[c] *= dc; u += s[c] * kh[c]; }
+                double delta = bt * (vh[row] - u), o = 0.0;
+                for (int c = 0; c < hd; ++c) { s[c] += delta * kh[c]; o += s[c] * qh[c]; }
+                out[((int64_t)b * heads + h) * hd + row] = o * scale;
+            }
+        }
 }

@@ -103,6 +103,42 @@ int orc_decode_attention(const float* q, int nseq, int hq, int hkv, int hd,
                          int64_t capacity, const float* gate,
                          double* out, double* m, double* z);
 
+/* ---- the rest of a decoder step (resident_math.comp ops 0, 1, 14, 15, 18-21) ----
+ * Test infrastructure: restatements in fp64 (fp32 inputs, fp32 embedding values). */
+
+/* op 0 (resident_math.comp:30-32): out[b, c] = dequant(table row ids[b])[c], bit exact. */
+int orc_embed(int fmt, const void* table, int vocab, int hidden, const uint32_t* ids, int batch, float* out);
+
+/* op 1 (resident_math.comp:33-38): out = x * w / sqrt(sum(x^2)/width + eps) per row. */
+void orc_rmsnorm(const float* x, const float* w, int rows, int width, double eps, double* out);
+
+/* ops 14 / 15 / 20 (resident_math.comp:113-115,139-140): per head of hd values,
+ *   out = x * w[h*hd + c] / sqrt(sum(x^2)/(mean ? hd : 1) + eps) * (gate ? g*sigmoid(g) : 1)
+ * w may be NULL (1).  x, gate: [rows, heads*hd] with row strides x_stride, gate_stride. */
+void orc_head_norm(const float* x, int x_stride, const float* w, const float* gate, int gate_stride, int rows,
+                   int heads, int hd, int mean, double eps, double* out);
+
+/* op 18 (resident_math.comp:131-133): decay = exp(-exp(a_log[h]) * softplus(a + dt_bias[h])),
+ * beta = sigmoid(b); a, b: [batch, heads] with row stride `stride`. */
+void orc_delta_gates(const float* a, const float* b, int stride, const float* a_log, const float* dt_bias,
+                     int batch, int heads, double* decay, double* beta);
+
+/* ops 19 + 20 for one new token per sequence (resident_math.comp:134-140):
+ *   raw [batch, 3W] (q | k | v projections, W = heads*hd, row stride raw_stride),
+ *   state [batch, 3W, 3] the three previous raw values (oldest first), w [3W, 4]:
+ *   s = sum_j<3 w[c][j] state[c][j] + w[c][3] raw[c];  y = s * sigmoid(s);
+ *   q and k parts then L2-normalised per head: y / sqrt(sum(y^2) + eps).
+ * out [batch, 3W]; new_state receives the shifted window (state[1], state[2], raw). */
+void orc_short_conv(const float* raw, int raw_stride, const float* state, const float* w, int batch, int heads,
+                    int hd, double eps, double* out, float* new_state);
+
+/* op 21 / resident_state.comp, one token per sequence (the gated delta rule): per
+ * sequence b and head h with S = state[b][h] ([value][key], hd x hd):
+ *   S = decay S;  u = S k;  S += beta (v - u) k^T;  o = S q / sqrt(hd)
+ * q, k, v: [batch, heads*hd] with row stride `stride`; state fp64 in/out; out [batch, heads*hd]. */
+void orc_delta_rule(double* state, const double* q, const double* k, const double* v, int stride,
+                    const double* decay, const double* beta, int batch, int heads, int hd, double* out);
+
 #ifdef __cplusplus
 }
 #endif

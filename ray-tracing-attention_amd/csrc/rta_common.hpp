@@ -68,6 +68,38 @@ __device__ __forceinline__ void q4k_scale_min(uint32_t s0, uint32_t s1, uint32_t
     }
 }
 
+// Value i of a GGUF-encoded array, with the reference decoder's fp32 op order
+// (resident_quant.glsl:6-20); contraction is disabled so that (d*sc)*q - dmin*m is
+// rounded exactly as the reference rounds it.
+__device__ __forceinline__ float dequant_value(int fmt, const uint8_t* __restrict__ src, int64_t i) {
+#pragma clang fp contract(off)
+    if (fmt == RTA_F32) return reinterpret_cast<const float*>(src)[i];
+    if (fmt == RTA_F16) return (float)reinterpret_cast<const _Float16*>(src)[i];
+    if (fmt == RTA_BF16) return __builtin_bit_cast(float, (uint32_t)reinterpret_cast<const uint16_t*>(src)[i] << 16);
+    if (fmt == RTA_Q4_K) {
+        const uint8_t* b = src + (i >> 8) * 144;
+        const int idx = (int)(i & 255), g = idx >> 5;
+        const float d = (float)*reinterpret_cast<const _Float16*>(b);
+        const float dmin = (float)*reinterpret_cast<const _Float16*>(b + 2);
+        uint32_t sc, m;
+        const uint32_t* s = reinterpret_cast<const uint32_t*>(b + 4);
+        q4k_scale_min(s[0], s[1], s[2], g, sc, m);
+        const uint32_t q = (b[16 + (idx >> 6) * 32 + (idx & 31)] >> (((idx & 63) >> 5) * 4)) & 15u;
+        const float ds = d * (float)sc;
+        const float dq = ds * (float)q;
+        const float dm = dmin * (float)m;
+        return dq - dm;
+    }
+    const uint8_t* b = src + (i >> 8) * 210;   // Q6_K
+    const int idx = (int)(i & 255), h = idx >> 7, l = idx & 127;
+    const uint32_t ql = (b[h * 64 + (l & 63)] >> ((l >> 6) * 4)) & 15u;
+    const uint32_t qh = (b[128 + h * 32 + (l & 31)] >> ((l >> 5) * 2)) & 3u;
+    const int sc = (int8_t)b[192 + (idx >> 4)];
+    const float d = (float)__builtin_bit_cast(_Float16, (uint16_t)(b[208] | (b[209] << 8)));
+    const float ds = d * (float)sc;
+    return ds * (float)((int)(ql | (qh << 4)) - 32);
+}
+
 // Stable logistic of resident_common.glsl:138 (detectorSigmoid).
 __device__ __forceinline__ float detector_sigmoid(float v) {
     if (v >= 0.0f) return 1.0f / (1.0f + expf(-v));

@@ -18,40 +18,9 @@ __device__ uint32_t g_error_word = 0;
 // rounded exactly as the reference rounds it.
 __global__ void __launch_bounds__(256) dequant_kernel(int fmt, const uint8_t* __restrict__ src, int64_t n,
                                                       float* __restrict__ out) {
-#pragma clang fp contract(off)
     const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (i >= n) return;
-    float v;
-    if (fmt == RTA_F32) {
-        v = reinterpret_cast<const float*>(src)[i];
-    } else if (fmt == RTA_F16) {
-        v = (float)reinterpret_cast<const _Float16*>(src)[i];
-    } else if (fmt == RTA_BF16) {
-        v = __builtin_bit_cast(float, (uint32_t)reinterpret_cast<const uint16_t*>(src)[i] << 16);
-    } else if (fmt == RTA_Q4_K) {
-        const uint8_t* b = src + (i >> 8) * 144;
-        const int idx = (int)(i & 255), g = idx >> 5;
-        const float d = (float)*reinterpret_cast<const _Float16*>(b);
-        const float dmin = (float)*reinterpret_cast<const _Float16*>(b + 2);
-        uint32_t sc, m;
-        const uint32_t* s = reinterpret_cast<const uint32_t*>(b + 4);
-        q4k_scale_min(s[0], s[1], s[2], g, sc, m);
-        const uint32_t q = (b[16 + (idx >> 6) * 32 + (idx & 31)] >> (((idx & 63) >> 5) * 4)) & 15u;
-        const float ds = d * (float)sc;
-        const float dq = ds * (float)q;
-        const float dm = dmin * (float)m;
-        v = dq - dm;
-    } else {  // Q6_K
-        const uint8_t* b = src + (i >> 8) * 210;
-        const int idx = (int)(i & 255), h = idx >> 7, l = idx & 127;
-        const uint32_t ql = (b[h * 64 + (l & 63)] >> ((l >> 6) * 4)) & 15u;
-        const uint32_t qh = (b[128 + h * 32 + (l & 31)] >> ((l >> 5) * 2)) & 3u;
-        const int sc = (int8_t)b[192 + (idx >> 4)];
-        const float d = (float)__builtin_bit_cast(_Float16, (uint16_t)(b[208] | (b[209] << 8)));
-        const float ds = d * (float)sc;
-        v = ds * (float)((int)(ql | (qh << 4)) - 32);
-    }
-    out[i] = v;
+    out[i] = dequant_value(fmt, src, i);
 }
 
 // ------------------------------------------------------------------ argmax ----

@@ -1,0 +1,443 @@
+// rta_step.hip -- the rest of a decoder step around the projections and attention:
+// embedding gather, RMSNorm, per-head norms, the gated delta-net recurrent layer
+// (gates, short convolution, state update) and the history packer (gfx950).
+#include <math.h>
+
+#include "rta_common.hpp"
+#include "rta_host.hpp"
+
+namespace rta {
+
+__device__ __forceinline__ float wave_sum(float v) {
+    for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, kWave);
+    return v;
+}
+
+// Sum over a block of NW waves through LDS red[NW]; every thread gets the total.
+template <int NW>
+__device__ __forceinline__ float block_sum(float v, float* red) {
+    v = wave_sum(v);
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    __syncthreads();
+    if (lane == 0) red[wave] = v;
+    __syncthreads();
+    float t = 0.0f;
+#pragma unroll
+    for (int i = 0; i < NW; ++i) t += red[i];
+    return t;
+}
+
+__device__ __forceinline__ float silu(float v) { return v * detector_sigmoid(v); }
+
+// ------------------------------------------------------------- embedding ----
+// op 0 (resident_math.comp:30-32): out[b, c] = decoded table row ids[b].  Ids past
+// the vocabulary give zeros and raise RTA_DEVERR_TOKEN.
+__global__ void __launch_bounds__(256) embed_kernel(int fmt, const uint8_t* __restrict__ table, int64_t row_bytes,
+                                                    int vocab, int hidden, const uint32_t* __restrict__ ids,
+                                                    float* __restrict__ out) {
+    const int b = blockIdx.y, c = blockIdx.x * 256 + threadIdx.x;
+    if (c >= hidden) return;
+    const uint32_t id = ids[b];
+    float v = 0.0f;
+    if (id < (uint32_t)vocab) v = dequant_value(fmt, table + (int64_t)id * row_bytes, c);
+    else if (c == 0) raise_error(RTA_DEVERR_TOKEN);
+    out[(int64_t)b * hidden + c] = v;
+}
+
+// --------------------------------------------------------------- RMSNorm ----
+// op 1 (resident_math.comp:33-38): out = x * w / sqrt(mean(x^2) + eps), one block per row.
+__global__ void __launch_bounds__(256) rmsnorm_kernel(const float* __restrict__ x, const float* __restrict__ w,
+                                                      int width, float eps, float* __restrict__ out) {
+    __shared__ float red[4];
+    const float4* xr = reinterpret_cast<const float4*>(x + (int64_t)blockIdx.x * width);
+    const int n4 = width >> 2;
+    float ss = 0.0f;
+    for (int i = threadIdx.x; i < n4; i += 256) {
+        const float4 v = xr[i];
+        ss += v.x * v.x + v.y * v.y + v.z * v.z + v.w * v.w;
+    }
+    ss = block_sum<4>(ss, red);
+    const float inv = 1.0f / sqrtf(ss / (float)width + eps);
+    float4* o = reinterpret_cast<float4*>(out + (int64_t)blockIdx.x * width);
+    const float4* w4 = reinterpret_cast<const float4*>(w);
+    for (int i = threadIdx.x; i < n4; i += 256) {
+        const float4 v = xr[i], g = w4[i];
+        o[i] = float4{v.x * inv * g.x, v.y * inv * g.y, v.z * inv * g.z, v.w * inv * g.w};
+    }
+}
+
+// ------------------------------------------------------------- head norms ----
+// ops 14 / 15 / 20 (resident_math.comp:113-115,139-140), in place: one wave per
+// (row, head) of hd = 64 * VPL values:
+//   x = x * w[h*hd+c] / sqrt(sum(x^2) / (mean ? hd : 1) + eps) * (gate ? g*sigmoid(g) : 1)
+template <int VPL>
+__global__ void __launch_bounds__(256) head_norm_kernel(float* __restrict__ x, int x_stride,
+                                                        const float* __restrict__ w, const float* __restrict__ gate,
+                                                        int gate_stride, int heads, int mean, float eps) {
+    const int lane = threadIdx.x & 63;
+    const int h = blockIdx.x * 4 + (threadIdx.x >> 6), r = blockIdx.y;
+    if (h >= heads) return;
+    constexpr int hd = 64 * VPL;
+    float* xh = x + (int64_t)r * x_stride + (int64_t)h * hd;
+    float v[VPL];
+    float ss = 0.0f;
+#pragma unroll
+    for (int i = 0; i < VPL; ++i) {
+        v[i] = xh[lane + 64 * i];
+        ss += v[i] * v[i];
+    }
+    ss = wave_sum(ss);
+    const float inv = 1.0f / sqrtf((mean ? ss / (float)hd : ss) + eps);
+#pragma unroll
+    for (int i = 0; i < VPL; ++i) {
+        const int c = lane + 64 * i;
+        float o = v[i] * inv;
+        if (w) o *= w[h * hd + c];
+        if (gate) o *= silu(gate[(int64_t)r * gate_stride + (int64_t)h * hd + c]);
+        xh[c] = o;
+    }
+}
+
+// -------------------------------------------------------- delta-net gates ----
+// op 18 (resident_math.comp:131-133) after its two projections:
+// decay = exp(-exp(a_log[h]) * softplus(a + dt_bias[h])), beta = sigmoid(b).
+__global__ void __launch_bounds__(256) delta_gates_kernel(const float* __restrict__ a, const float* __restrict__ b,
+                                                          int stride, const float* __restrict__ a_log,
+                                                          const float* __restrict__ dt_bias, int batch, int heads,
+                                                          float* __restrict__ decay, float* __restrict__ beta) {
+    const int i = blockIdx.x * 256 + threadIdx.x;
+    if (i >= batch * heads) return;
+    const int r = i / heads, h = i - r * heads;
+    const float av = a[(int64_t)r * stride + h] + dt_bias[h];
+    const float sp = fmaxf(av, 0.0f) + log1pf(expf(-fabsf(av)));   // softplus, resident_common.glsl:80
+    decay[i] = expf(-expf(a_log[h]) * sp);
+    beta[i] = detector_sigmoid(b[(int64_t)r * stride + h]);
+}
+
+// ---------------------------------------------------- short convolution ----
+// ops 19 + 20 (resident_math.comp:134-140) for one new token per sequence: block
+// (head, sequence), thread c of hd.  For each part (q, k, v) coordinate
+// p = part*W + h*hd + c:  s = sum_j<3 w[p][j] state[p][j] + w[p][3] raw[p];
+// y = s * sigmoid(s); the window shifts by one; q and k are L2-normalised per head.
+__global__ void __launch_bounds__(128) short_conv_kernel(const float* __restrict__ raw, int raw_stride,
+                                                         float* __restrict__ state, const float* __restrict__ w,
+                                                         int heads, float eps, float* __restrict__ out) {
+    __shared__ float red[2];
+    const int h = blockIdx.x, b = blockIdx.y, c = threadIdx.x, hd = 128;
+    const int W = heads * hd, W3 = 3 * W;
+    float y[3];
+#pragma unroll
+    for (int part = 0; part < 3; ++part) {
+        const int p = part * W + h * hd + c;
+        float* st = state + ((int64_t)b * W3 + p) * 3;
+        const float4 wp = *reinterpret_cast<const float4*>(w + (int64_t)p * 4);
+        const float x = raw[(int64_t)b * raw_stride + p];
+        const float s0 = st[0], s1 = st[1], s2 = st[2];
+        const float s = wp.x * s0 + wp.y * s1 + wp.z * s2 + wp.w * x;
+        y[part] = silu(s);
+        st[0] = s1;
+        st[1] = s2;
+        st[2] = x;
+    }
+#pragma unroll
+    for (int part = 0; part < 2; ++part) {
+        float ss = wave_sum(y[part] * y[part]);
+        __syncthreads();
+        if ((c & 63) == 0) red[c >> 6] = ss;
+        __syncthreads();
+        y[part] *= 1.0f / sqrtf(red[0] + red[1] + eps);
+    }
+#pragma unroll
+    for (int part = 0; part < 3; ++part) out[(int64_t)b * W3 + part * W + h * hd + c] = y[part];
+}
+
+// ---------------------------------------------------------- delta rule ----
+// op 21 / resident_state.comp, one token per sequence: block (head, sequence), 4
+// waves x 32 value rows of the hd x hd state ([value][key]); lane l holds keys 2l,
+// 2l+1.  Per row:  s = decay s;  u = s.k;  s += beta (v - u) k;  o = s.q / sqrt(hd).
+// With norm_w the gated RMSNorm of op 15 (resident_math.comp:115) is applied to o.
+__global__ void __launch_bounds__(256) delta_rule_kernel(float* __restrict__ state, const float* __restrict__ qkv,
+                                                         int qkv_stride, const float* __restrict__ decay,
+                                                         const float* __restrict__ beta, int heads,
+                                                         const float* __restrict__ norm_w,
+                                                         const float* __restrict__ gate, int gate_stride, float eps,
+                                                         float* __restrict__ out, int out_stride) {
+    constexpr int hd = 128;
+    __shared__ float o_s[hd];
+    __shared__ float red[4];
+    const int h = blockIdx.x, b = blockIdx.y, lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int W = heads * hd;
+    const float* row = qkv + (int64_t)b * qkv_stride;
+    const float2 q = *reinterpret_cast<const float2*>(row + h * hd + 2 * lane);
+    const float2 k = *reinterpret_cast<const float2*>(row + W + h * hd + 2 * lane);
+    const float dc = decay[(int64_t)b * heads + h], bt = beta[(int64_t)b * heads + h];
+    const float scale = 1.0f / sqrtf((float)hd);
+    float2* S = reinterpret_cast<float2*>(state + ((int64_t)b * heads + h) * hd * hd);
+    constexpr int kRows = hd / 4, kUnroll = 8;
+    for (int r0 = 0; r0 < kRows; r0 += kUnroll) {
+        float2 s[kUnroll];
+#pragma unroll
+        for (int i = 0; i < kUnroll; ++i) s[i] = S[(wave * kRows + r0 + i) * (hd / 2) + lane];
+#pragma unroll
+        for (int i = 0; i < kUnroll; ++i) {
+            const int v = wave * kRows + r0 + i;
+            s[i].x *= dc;
+            s[i].y *= dc;
+            const float u = wave_sum(s[i].x * k.x + s[i].y * k.y);
+            const float delta = bt * (row[2 * W + h * hd + v] - u);
+            s[i].x += delta * k.x;
+            s[i].y += delta * k.y;
+            const float o = wave_sum(s[i].x * q.x + s[i].y * q.y) * scale;
+            if (lane == 0) o_s[v] = o;
+            S[v * (hd / 2) + lane] = s[i];
+        }
+    }
+    __syncthreads();
+    float* o = out + (int64_t)b * out_stride + h * hd;
+    if (!norm_w) {
+        if (threadIdx.x < hd) o[threadIdx.x] = o_s[threadIdx.x];
+        return;
+    }
+    const float v = threadIdx.x < hd ? o_s[threadIdx.x] : 0.0f;
+    const float ss = block_sum<4>(v * v, red);
+    const float inv = 1.0f / sqrtf(ss / (float)hd + eps);
+    if (threadIdx.x < hd) {
+        const float g = gate[(int64_t)b * gate_stride + h * hd + threadIdx.x];
+        o[threadIdx.x] = v * inv * norm_w[h * hd + threadIdx.x] * silu(g);
+    }
+}
+
+// --------------------------------------------------------- history packer ----
+// op 34 (resident_history_quant.glsl:9-41): one block per sequence quantises its new
+// key and value rows into a history packet (a Q4_K or Q6_K field each) in LDS and
+// writes it to packet slot slot[b].  Every step follows the reference's fp32 order
+// (contraction off, IEEE division, round-half-even codes, fp16 block scales):
+//   Q4_K field: 32-value groups, span (max(0,x) - min(0,x)) / 15, minimum -min(0,x),
+//               d = fp16(max span / 63), dmin = fp16(max minimum / 63), 6-bit codes
+//   Q6_K field: 16-value groups, max|x| / 31, d = fp16(max / 127), 8-bit codes
+constexpr int kPackMaxBlocks = 16;   // kvw <= 4096
+
+// GLSL min / max: x unless y is strictly smaller / larger.  They fix the sign of
+// zero where the packer compares +0 with -0 (the minimum -min(0, x) of an all-zero
+// group is -0), which the fp16 block minimum keeps.
+__device__ __forceinline__ float glsl_min(float x, float y) { return y < x ? y : x; }
+__device__ __forceinline__ float glsl_max(float x, float y) { return x < y ? y : x; }
+
+__global__ void __launch_bounds__(256) pack_history_kernel(const float* __restrict__ kin, int k_stride,
+                                                           const float* __restrict__ vin, int v_stride, int kvw,
+                                                           int fmt_k, int fmt_v, const int64_t* __restrict__ slot,
+                                                           int64_t n_slots, int64_t stride,
+                                                           uint8_t* __restrict__ packets) {
+#pragma clang fp contract(off)
+    __shared__ uint32_t pkt[kPackMaxBlocks * 2 * 210 / 4 + 4];
+    __shared__ float gscale[2][kPackMaxBlocks * 16], gmin[2][kPackMaxBlocks * 16];
+    __shared__ float bd[2][kPackMaxBlocks], bdm[2][kPackMaxBlocks];
+    __shared__ uint32_t sc[2][kPackMaxBlocks * 16], mn[2][kPackMaxBlocks * 16];
+    uint8_t* pb = reinterpret_cast<uint8_t*>(pkt);
+    const int b = blockIdx.x, tid = threadIdx.x;
+    const int blocks = (kvw + 255) / 256;
+    const float* src[2] = {kin + (int64_t)b * k_stride, vin + (int64_t)b * v_stride};
+    const int fmt[2] = {fmt_k, fmt_v};
+    const int field_off[2] = {0, blocks * (fmt_k == RTA_Q4_K ? 144 : 210)};
+    auto value = [&](int f, int i) { return i < kvw ? src[f][i] : 0.0f; };
+    for (int i = tid; i < (int)(stride / 4); i += 256) pkt[i] = 0u;
+    // 1. group statistics
+    for (int f = 0; f < 2; ++f) {
+        const bool q4 = fmt[f] == RTA_Q4_K;
+        const int ng = blocks * (q4 ? 8 : 16), width = q4 ? 32 : 16;
+        for (int g = tid; g < ng; g += 256) {
+            float lo = 0.0f, hi = 0.0f;
+            for (int i = 0; i < width; ++i) {
+                const float v = value(f, g * width + i);
+                if (q4) { lo = glsl_min(lo, v); hi = glsl_max(hi, v); }
+                else hi = glsl_max(hi, fabsf(v));
+            }
+            gscale[f][g] = q4 ? (hi - lo) / 15.0f : hi / 31.0f;
+            gmin[f][g] = q4 ? -lo : 0.0f;
+        }
+    }
+    __syncthreads();
+    // 2. block scales (fp16) and their header bytes
+    if (tid < 2 * blocks) {
+        const int f = tid / blocks, blk = tid - f * blocks;
+        const bool q4 = fmt[f] == RTA_Q4_K;
+        const int ng = q4 ? 8 : 16;
+        float maxD = 0.0f, maxMin = 0.0f;
+        for (int g = 0; g < ng; ++g) {
+            maxD = glsl_max(maxD, gscale[f][blk * ng + g]);
+            maxMin = glsl_max(maxMin, gmin[f][blk * ng + g]);
+        }
+        const _Float16 hd16 = (_Float16)(maxD / (q4 ? 63.0f : 127.0f));
+        bd[f][blk] = (float)hd16;
+        const uint16_t hb = __builtin_bit_cast(uint16_t, hd16);
+        uint8_t* base = pb + field_off[f] + blk * (q4 ? 144 : 210);
+        if (q4) {
+            const _Float16 hm16 = (_Float16)(maxMin / 63.0f);
+            bdm[f][blk] = (float)hm16;
+            const uint16_t hm = __builtin_bit_cast(uint16_t, hm16);
+            base[0] = hb & 255; base[1] = hb >> 8; base[2] = hm & 255; base[3] = hm >> 8;
+        } else {
+            base[208] = hb & 255; base[209] = hb >> 8;
+        }
+    }
+    __syncthreads();
+    // 3. group codes
+    for (int f = 0; f < 2; ++f) {
+        const bool q4 = fmt[f] == RTA_Q4_K;
+        const int ng = blocks * (q4 ? 8 : 16);
+        for (int g = tid; g < ng; g += 256) {
+            const int blk = g / (q4 ? 8 : 16);
+            const float d = bd[f][blk];
+            sc[f][g] = (uint32_t)fminf(fmaxf(rintf(gscale[f][g] / fmaxf(d, 1e-30f)), 0.0f), q4 ? 63.0f : 127.0f);
+            if (q4) mn[f][g] = (uint32_t)fminf(fmaxf(rintf(gmin[f][g] / fmaxf(bdm[f][blk], 1e-30f)), 0.0f), 63.0f);
+            else pb[field_off[f] + blk * 210 + 192 + (g & 15)] = (uint8_t)sc[f][g];
+        }
+    }
+    __syncthreads();
+    // 4. packed 6-bit Q4_K scales, then the quantised values, one output byte per thread
+    for (int f = 0; f < 2; ++f) {
+        if (fmt[f] != RTA_Q4_K) continue;
+        for (int t = tid; t < blocks * 4; t += 256) {
+            const int blk = t >> 2, g = t & 3, o = blk * 8;
+            uint8_t* base = pb + field_off[f] + blk * 144;
+            base[4 + g] = (uint8_t)(sc[f][o + g] | ((sc[f][o + g + 4] >> 4) << 6));
+            base[8 + g] = (uint8_t)(mn[f][o + g] | ((mn[f][o + g + 4] >> 4) << 6));
+            base[12 + g] = (uint8_t)((sc[f][o + g + 4] & 15u) | ((mn[f][o + g + 4] & 15u) << 4));
+        }
+    }
+    auto q4code = [&](int f, int i) {
+#pragma clang fp contract(off)
+        const int blk = i >> 8, g = i >> 5;
+        const float num = value(f, i) + bdm[f][blk] * (float)mn[f][g];
+        const float den = fmaxf(bd[f][blk] * (float)sc[f][g], 1e-30f);
+        return (uint32_t)fminf(fmaxf(rintf(num / den), 0.0f), 15.0f);
+    };
+    auto q6code = [&](int f, int i) {
+#pragma clang fp contract(off)
+        const int blk = i >> 8, g = i >> 4;
+        const float den = fmaxf(bd[f][blk] * (float)sc[f][g], 1e-30f);
+        return (uint32_t)((int)fminf(fmaxf(rintf(value(f, i) / den), -32.0f), 31.0f) + 32);
+    };
+    for (int f = 0; f < 2; ++f) {
+        const bool q4 = fmt[f] == RTA_Q4_K;
+        const int per = q4 ? 128 : 192;   // quant bytes per block
+        for (int t = tid; t < blocks * per; t += 256) {
+            const int blk = t / per, j = t - blk * per, v0 = blk * 256;
+            uint8_t byte;
+            if (q4) {   // qs byte j: value 64 (j/32) + j%32 (low nibble) and +32 (high)
+                const int i = v0 + 64 * (j >> 5) + (j & 31);
+                byte = (uint8_t)(q4code(f, i) | (q4code(f, i + 32) << 4));
+            } else if (j < 128) {   // ql byte: value 128 (j/64) + j%64 (low) and +64 (high)
+                const int i = v0 + 128 * (j >> 6) + (j & 63);
+                byte = (uint8_t)((q6code(f, i) & 15u) | ((q6code(f, i + 64) & 15u) << 4));
+            } else {                // qh byte: values 128 part + l + 32 k, two bits each
+                const int jj = j - 128, i = v0 + 128 * (jj >> 5) + (jj & 31);
+                byte = (uint8_t)(((q6code(f, i) >> 4) & 3u) | (((q6code(f, i + 32) >> 4) & 3u) << 2) |
+                                 (((q6code(f, i + 64) >> 4) & 3u) << 4) | (((q6code(f, i + 96) >> 4) & 3u) << 6));
+            }
+            pb[field_off[f] + blk * (q4 ? 144 : 210) + (q4 ? 16 + j : j)] = byte;
+        }
+    }
+    __syncthreads();
+    const int64_t s = slot[b];
+    if (s < 0 || s >= n_slots) {
+        if (tid == 0) raise_error(RTA_DEVERR_HITS);
+        return;
+    }
+    uint32_t* dst = reinterpret_cast<uint32_t*>(packets + s * stride);
+    for (int i = tid; i < (int)(stride / 4); i += 256) dst[i] = pkt[i];
+}
+
+}  // namespace rta
+
+using namespace rta;
+
+extern "C" {
+
+int rta_embed(int fmt, const void* table, int vocab, int hidden, const uint32_t* ids, int batch, float* out,
+              rta_stream_t stream) {
+    if (!host::valid_format(fmt)) return RTA_ERR_FORMAT;
+    if (!table || !ids || !out) return RTA_ERR_NULL;
+    const int64_t rb = host::row_bytes(fmt, hidden);
+    if (vocab <= 0 || hidden <= 0 || batch <= 0 || rb <= 0) return RTA_ERR_SHAPE;
+    if (!host::aligned(table, fmt == RTA_F32 || fmt == RTA_Q4_K ? 4 : 2) || !host::aligned(out, 4) ||
+        !host::aligned(ids, 4))
+        return RTA_ERR_ALIGN;
+    hipLaunchKernelGGL(embed_kernel, dim3((hidden + 255) / 256, batch), dim3(256), 0, (hipStream_t)stream, fmt,
+                       static_cast<const uint8_t*>(table), rb, vocab, hidden, ids, out);
+    return hipGetLastError() == hipSuccess ? RTA_OK : RTA_ERR_LAUNCH;
+}
+
+int rta_rmsnorm(const float* x, const float* w, int rows, int width, float eps, float* out, rta_stream_t stream) {
+    if (!x || !w || !out) return RTA_ERR_NULL;
+    if (rows <= 0 || width <= 0 || width % 4) return RTA_ERR_SHAPE;
+    if (!(eps >= 0.0f)) return RTA_ERR_RANGE;
+    if (!host::aligned(x, 16) || !host::aligned(w, 16) || !host::aligned(out, 16)) return RTA_ERR_ALIGN;
+    hipLaunchKernelGGL(rmsnorm_kernel, dim3(rows), dim3(256), 0, (hipStream_t)stream, x, w, width, eps, out);
+    return hipGetLastError() == hipSuccess ? RTA_OK : RTA_ERR_LAUNCH;
+}
+
+int rta_head_norm(float* x, int x_stride, const float* w, const float* gate, int gate_stride, int rows, int heads,
+                  int hd, int mean, float eps, rta_stream_t stream) {
+    if (!x) return RTA_ERR_NULL;
+    if (rows <= 0 || heads <= 0 || x_stride < heads * hd || (gate && gate_stride < heads * hd)) return RTA_ERR_SHAPE;
+    if ((hd != 64 && hd != 128 && hd != 256) || !(eps >= 0.0f)) return RTA_ERR_RANGE;
+    const dim3 g((heads + 3) / 4, rows), bl(256);
+    hipStream_t s = (hipStream_t)stream;
+    if (hd == 64) hipLaunchKernelGGL(head_norm_kernel<1>, g, bl, 0, s, x, x_stride, w, gate, gate_stride, heads, mean, eps);
+    else if (hd == 128) hipLaunchKernelGGL(head_norm_kernel<2>, g, bl, 0, s, x, x_stride, w, gate, gate_stride, heads, mean, eps);
+    else hipLaunchKernelGGL(head_norm_kernel<4>, g, bl, 0, s, x, x_stride, w, gate, gate_stride, heads, mean, eps);
+    return hipGetLastError() == hipSuccess ? RTA_OK : RTA_ERR_LAUNCH;
+}
+
+int rta_delta_gates(const float* a, const float* b, int stride, const float* a_log, const float* dt_bias, int batch,
+                    int heads, float* decay, float* beta, rta_stream_t stream) {
+    if (!a || !b || !a_log || !dt_bias || !decay || !beta) return RTA_ERR_NULL;
+    if (batch <= 0 || heads <= 0 || stride < heads) return RTA_ERR_SHAPE;
+    const int n = batch * heads;
+    hipLaunchKernelGGL(delta_gates_kernel, dim3((n + 255) / 256), dim3(256), 0, (hipStream_t)stream, a, b, stride,
+                       a_log, dt_bias, batch, heads, decay, beta);
+    return hipGetLastError() == hipSuccess ? RTA_OK : RTA_ERR_LAUNCH;
+}
+
+int rta_short_conv(const float* raw, int raw_stride, float* state, const float* w, int batch, int heads, int hd,
+                   float eps, float* out, rta_stream_t stream) {
+    if (!raw || !state || !w || !out) return RTA_ERR_NULL;
+    if (batch <= 0 || heads <= 0 || raw_stride < 3 * heads * hd) return RTA_ERR_SHAPE;
+    if (hd != 128 || !(eps >= 0.0f)) return RTA_ERR_RANGE;
+    if (!host::aligned(w, 16)) return RTA_ERR_ALIGN;
+    hipLaunchKernelGGL(short_conv_kernel, dim3(heads, batch), dim3(128), 0, (hipStream_t)stream, raw, raw_stride,
+                       state, w, heads, eps, out);
+    return hipGetLastError() == hipSuccess ? RTA_OK : RTA_ERR_LAUNCH;
+}
+
+int rta_delta_rule(float* state, const float* qkv, int qkv_stride, const float* decay, const float* beta, int batch,
+                   int heads, int hd, const float* norm_w, const float* gate, int gate_stride, float eps, float* out,
+                   int out_stride, rta_stream_t stream) {
+    if (!state || !qkv || !decay || !beta || !out || (norm_w && !gate)) return RTA_ERR_NULL;
+    if (batch <= 0 || heads <= 0 || qkv_stride < 3 * heads * hd || out_stride < heads * hd ||
+        (gate && gate_stride < heads * hd))
+        return RTA_ERR_SHAPE;
+    if (hd != 128 || !(eps >= 0.0f)) return RTA_ERR_RANGE;
+    if (!host::aligned(state, 16) || !host::aligned(qkv, 8) || qkv_stride % 2) return RTA_ERR_ALIGN;
+    hipLaunchKernelGGL(delta_rule_kernel, dim3(heads, batch), dim3(256), 0, (hipStream_t)stream, state, qkv,
+                       qkv_stride, decay, beta, heads, norm_w, gate, gate_stride, eps, out, out_stride);
+    return hipGetLastError() == hipSuccess ? RTA_OK : RTA_ERR_LAUNCH;
+}
+
+int rta_pack_history(const float* k, int k_stride, const float* v, int v_stride, int batch, int kvw, int fmt_k,
+                     int fmt_v, const int64_t* slot, int64_t n_slots, void* packets, rta_stream_t stream) {
+    if (!k || !v || !slot || !packets) return RTA_ERR_NULL;
+    // a packet holds one Q4_K and one Q6_K field (354 bytes per 256 coordinates)
+    if ((fmt_k != RTA_Q4_K && fmt_k != RTA_Q6_K) || (fmt_v != RTA_Q4_K && fmt_v != RTA_Q6_K) || fmt_k == fmt_v)
+        return RTA_ERR_FORMAT;
+    if (batch <= 0 || kvw <= 0 || k_stride < kvw || v_stride < kvw || n_slots <= 0) return RTA_ERR_SHAPE;
+    if (kvw > 256 * kPackMaxBlocks) return RTA_ERR_RANGE;
+    const int64_t stride = host::history_bytes(kvw);
+    if (!host::aligned(packets, 8)) return RTA_ERR_ALIGN;
+    hipLaunchKernelGGL(pack_history_kernel, dim3(batch), dim3(256), 0, (hipStream_t)stream, k, k_stride, v, v_stride,
+                       kvw, fmt_k, fmt_v, slot, n_slots, stride, static_cast<uint8_t*>(packets));
+    return hipGetLastError() == hipSuccess ? RTA_OK : RTA_ERR_LAUNCH;
+}
+
+}  // extern "C"

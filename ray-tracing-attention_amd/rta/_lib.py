@@ -26,6 +26,13 @@ SIGNATURES = {
     "rta_device_error": (_i, [_u32p, _i]),
     "rta_row_bytes": (_i64, [_i, _i64]),
     "rta_dequant": (_i, [_i, _p, _i64, _p, _p]),
+    "rta_embed": (_i, [_i, _p, _i, _i, _p, _i, _p, _p]),
+    "rta_rmsnorm": (_i, [_p, _p, _i, _i, _f, _p, _p]),
+    "rta_head_norm": (_i, [_p, _i, _p, _p, _i, _i, _i, _i, _i, _f, _p]),
+    "rta_delta_gates": (_i, [_p, _p, _i, _p, _p, _i, _i, _p, _p, _p]),
+    "rta_short_conv": (_i, [_p, _i, _p, _p, _i, _i, _i, _f, _p, _p]),
+    "rta_delta_rule": (_i, [_p, _p, _i, _p, _p, _i, _i, _i, _p, _p, _i, _f, _p, _i, _p]),
+    "rta_pack_history": (_i, [_p, _i, _p, _i, _i, _i, _i, _i, _p, _i64, _p, _p]),
     "rta_pack_bytes": (_i64, [_i, _i, _i]),
     "rta_pack": (_i, [_i, _p, _i, _i, _p, _p]),
     "rta_gemv_workspace_bytes": (_sz, [_i, _i, _i, _i]),

@@ -175,3 +175,108 @@ def device_error(clear=True):
     bits = ctypes.c_uint32(0)
     check(_lib.load().rta_device_error(ctypes.byref(bits), 1 if clear else 0), "rta_device_error")
     return bits.value
+
+
+# ---------------------------------------------------- the rest of a decoder step ----
+def _rows(t, name):
+    """A 2-D float32 CUDA tensor whose rows may be strided views (unit column stride)."""
+    if not isinstance(t, torch.Tensor) or not t.is_cuda or t.dim() != 2 or t.stride(1) != 1:
+        raise ValueError(f"{name} must be a 2-D CUDA tensor with unit column stride")
+    return t
+
+
+def embed(fmt, table, vocab, hidden, ids, out=None):
+    """op 0: decoded embedding rows of `ids` (uint32/int32 device tensor)."""
+    lib = _lib.load()
+    _dev(table, "table")
+    _dev(ids, "ids")
+    batch = ids.numel()
+    if out is None:
+        out = torch.empty(batch, hidden, dtype=torch.float32, device=table.device)
+    check(lib.rta_embed(fmt, _ptr(table), vocab, hidden, _ptr(ids), batch, _ptr(out), _stream()), "rta_embed")
+    return out
+
+
+def rmsnorm(x, w, eps=1e-6, out=None):
+    """op 1: x * w / sqrt(mean(x^2) + eps) per row (out may be x)."""
+    lib = _lib.load()
+    _dev(x, "x")
+    if out is None:
+        out = torch.empty_like(x)
+    rows, width = x.reshape(-1, x.shape[-1]).shape
+    check(lib.rta_rmsnorm(_ptr(x), _ptr(w), rows, width, ctypes.c_float(eps), _ptr(out), _stream()), "rta_rmsnorm")
+    return out
+
+
+def head_norm(x, heads, hd, w=None, gate=None, mean=True, eps=1e-6):
+    """ops 14 / 15 / 20, in place on x [rows, >= heads*hd] (rows may be strided)."""
+    lib = _lib.load()
+    _rows(x, "x")
+    gs = 0
+    if gate is not None:
+        _rows(gate, "gate")
+        gs = gate.stride(0)
+    check(lib.rta_head_norm(_ptr(x), x.stride(0), _ptr(w), _ptr(gate), gs, x.shape[0], heads, hd, int(bool(mean)),
+                            ctypes.c_float(eps), _stream()), "rta_head_norm")
+    return x
+
+
+def delta_gates(a, b, a_log, dt_bias, decay=None, beta=None):
+    """op 18 after its projections: a, b [batch, heads] views with one row stride."""
+    lib = _lib.load()
+    _rows(a, "a")
+    _rows(b, "b")
+    if a.stride(0) != b.stride(0):
+        raise ValueError("a and b must share a row stride")
+    batch, heads = a.shape
+    decay = torch.empty(batch, heads, dtype=torch.float32, device=a.device) if decay is None else decay
+    beta = torch.empty(batch, heads, dtype=torch.float32, device=a.device) if beta is None else beta
+    check(lib.rta_delta_gates(_ptr(a), _ptr(b), a.stride(0), _ptr(a_log), _ptr(dt_bias), batch, heads, _ptr(decay),
+                              _ptr(beta), _stream()), "rta_delta_gates")
+    return decay, beta
+
+
+def short_conv(raw, state, w, heads, hd=128, eps=1e-6, out=None):
+    """ops 19 + 20 for one token: raw [batch, >= 3*heads*hd] (strided rows), state
+    [batch, 3*heads*hd, 3] shifted in place, w [3*heads*hd, 4]; returns out [batch, 3*heads*hd]."""
+    lib = _lib.load()
+    _rows(raw, "raw")
+    _dev(state, "state")
+    batch = raw.shape[0]
+    if out is None:
+        out = torch.empty(batch, 3 * heads * hd, dtype=torch.float32, device=raw.device)
+    check(lib.rta_short_conv(_ptr(raw), raw.stride(0), _ptr(state), _ptr(w), batch, heads, hd, ctypes.c_float(eps),
+                             _ptr(out), _stream()), "rta_short_conv")
+    return out
+
+
+def delta_rule(state, qkv, decay, beta, heads, hd=128, norm_w=None, gate=None, eps=1e-6, out=None):
+    """op 21 (+ op 15 when norm_w is given): state [batch, heads, hd, hd] updated in place."""
+    lib = _lib.load()
+    _dev(state, "state")
+    _rows(qkv, "qkv")
+    batch = qkv.shape[0]
+    if out is None:
+        out = torch.empty(batch, heads * hd, dtype=torch.float32, device=qkv.device)
+    gs = 0
+    if gate is not None:
+        _rows(gate, "gate")
+        gs = gate.stride(0)
+    check(lib.rta_delta_rule(_ptr(state), _ptr(qkv), qkv.stride(0), _ptr(decay), _ptr(beta), batch, heads, hd,
+                             _ptr(norm_w), _ptr(gate), gs, ctypes.c_float(eps), _ptr(out), out.stride(0), _stream()),
+          "rta_delta_rule")
+    return out
+
+
+def pack_history(k, v, slot, packets, fmt_k=Q4_K, fmt_v=Q6_K):
+    """op 34: quantise k[b], v[b] ([batch, kvw] strided rows) into packet slot[b] of packets."""
+    lib = _lib.load()
+    _rows(k, "k")
+    _rows(v, "v")
+    _dev(slot, "slot")
+    _dev(packets, "packets")
+    batch, kvw = k.shape
+    n_slots = packets.numel() // history_bytes(kvw)
+    check(lib.rta_pack_history(_ptr(k), k.stride(0), _ptr(v), v.stride(0), batch, kvw, fmt_k, fmt_v, _ptr(slot),
+                               n_slots, _ptr(packets), _stream()), "rta_pack_history")
+    return packets

@@ -292,3 +292,102 @@ def test_packer_round_trip(fmts):
         step = np.abs(field).max() / 7.0
         assert np.max(np.abs(dec - field)) <= step, np.max(np.abs(dec - field))
     assert not pk[708:].any()                                  # 4 pad bytes stay zero
+
+
+# ------------------------------------------------------- decoder-step ops ----
+def test_embed_rows_match_ggml_rows():
+    rng = np.random.default_rng(14)
+    vocab, hidden = 50, 512
+    for fmt, ref in ((orc.Q4_K, ggml_q4k), (orc.Q6_K, ggml_q6k)):
+        table = synth.random_matrix(rng, fmt, vocab, hidden)
+        ids = np.array([3, 0, 49, 3], np.uint32)
+        got = orc.embed(fmt, table, vocab, hidden, ids)
+        for b, t in enumerate(ids):
+            assert np.array_equal(_bits(got[b]), _bits(ref(table[t]))), (fmt, t)
+
+
+def test_rmsnorm_known_answers():
+    x = np.array([[3.0, 4.0], [-2.0, 0.0]], np.float32)
+    out = orc.rmsnorm(x, np.array([1.0, 2.0], np.float32), eps=0.0)
+    assert np.allclose(out[0], [3 / np.sqrt(12.5), 8 / np.sqrt(12.5)], rtol=1e-15)
+    assert np.allclose(out[1], [-np.sqrt(2.0), 0.0], rtol=1e-15)
+    rng = np.random.default_rng(15)
+    y = rng.standard_normal((3, 4096)).astype(np.float32)
+    o1 = orc.rmsnorm(y, np.ones(4096, np.float32), eps=0.0)
+    assert np.allclose(np.mean(o1 ** 2, axis=1), 1.0, rtol=1e-12)          # unit RMS
+    o2 = orc.rmsnorm(y * np.float32(8.0), np.ones(4096, np.float32), eps=0.0)
+    assert np.allclose(o1, o2, rtol=1e-12)                                 # scale invariance
+
+
+def test_head_norm_modes_and_gate():
+    rng = np.random.default_rng(16)
+    heads, hd = 3, 128
+    x = rng.standard_normal((2, heads * hd)).astype(np.float32)
+    rms = orc.head_norm(x, heads, hd, mean=True, eps=0.0).reshape(2, heads, hd)
+    l2 = orc.head_norm(x, heads, hd, mean=False, eps=0.0).reshape(2, heads, hd)
+    assert np.allclose(np.mean(rms ** 2, axis=2), 1.0, rtol=1e-12)
+    assert np.allclose(np.sum(l2 ** 2, axis=2), 1.0, rtol=1e-12)
+    assert np.allclose(rms, l2 * np.sqrt(hd), rtol=1e-12)
+    g0 = np.zeros_like(x)
+    assert not orc.head_norm(x, heads, hd, gate=g0).any()                  # silu(0) = 0
+    g = np.full_like(x, 40.0)                                              # silu(40) = 40 (to 1e-17)
+    assert np.allclose(orc.head_norm(x, heads, hd, gate=g), 40.0 * orc.head_norm(x, heads, hd), rtol=1e-15)
+
+
+def test_delta_gates_closed_forms():
+    z = np.zeros((1, 3), np.float32)
+    a_log = np.array([0.0, np.log(2.0), 0.0], np.float32)
+    b = np.array([[0.0, np.log(3.0), -np.log(3.0)]], np.float32)
+    decay, beta = orc.delta_gates(z, b, a_log, np.zeros(3, np.float32))
+    # softplus(0) = ln 2: exp(-1 * ln 2) = 1/2, exp(-2 ln 2) = 1/4
+    assert np.allclose(decay, [[0.5, 0.25, 0.5]], rtol=1e-7)
+    assert np.allclose(beta, [[0.5, 0.75, 0.25]], rtol=1e-7)
+
+
+def test_short_conv_taps_and_state():
+    rng = np.random.default_rng(17)
+    heads, hd, batch = 2, 128, 2
+    W3 = 3 * heads * hd
+    raw = rng.standard_normal((batch, W3 + 5)).astype(np.float32)          # extra columns: row stride
+    state = rng.standard_normal((batch, W3, 3)).astype(np.float32)
+    silu = lambda s: s / (1.0 + np.exp(-s))
+    for tap in range(4):
+        w = np.zeros((W3, 4), np.float32)
+        w[:, tap] = 1.0
+        out, ns = orc.short_conv(raw, state, w, heads, hd, eps=0.0)
+        src = (raw[:, :W3] if tap == 3 else state[:, :, tap]).astype(np.float64)
+        y = silu(src)
+        for part in range(2):                                              # q, k: unit L2 per head
+            blk = y[:, part * heads * hd:(part + 1) * heads * hd].reshape(batch, heads, hd)
+            y[:, part * heads * hd:(part + 1) * heads * hd] = (blk / np.sqrt((blk ** 2).sum(-1, keepdims=True))
+                                                                ).reshape(batch, -1)
+        assert np.allclose(out, y, rtol=1e-12, atol=1e-15), tap
+        assert np.array_equal(ns[:, :, :2], state[:, :, 1:]) and np.array_equal(ns[:, :, 2], raw[:, :W3])
+
+
+def test_delta_rule_recall_and_decay():
+    rng = np.random.default_rng(18)
+    heads, hd = 2, 128
+    # orthonormal keys: writing (k_i, v_i) from S = 0 with decay 1, beta 1 stores
+    # S = sum v_i k_i^T; querying k_j * sqrt(hd) returns v_j
+    basis = np.linalg.qr(rng.standard_normal((hd, hd)))[0]
+    S = np.zeros((1, heads, hd, hd))
+    vs = []
+    for i in range(5):
+        k = np.tile(basis[:, i], heads)[None]
+        v = rng.standard_normal((1, heads * hd))
+        vs.append(v)
+        S, _ = orc.delta_rule(S, np.zeros_like(v), k, v, np.ones((1, heads)), np.ones((1, heads)))
+    for j in range(5):
+        q = np.tile(basis[:, j], heads)[None] * np.sqrt(hd)
+        zero = np.zeros((1, heads))
+        _, o = orc.delta_rule(S, q, np.zeros_like(q), np.zeros_like(q), np.ones((1, heads)), zero)
+        assert np.allclose(o, vs[j], atol=1e-12), j
+    # beta = 0: the state only decays and the read is decay * S q / sqrt(hd)
+    S0 = rng.standard_normal((1, heads, hd, hd))
+    q = rng.standard_normal((1, heads * hd))
+    S1, o = orc.delta_rule(S0, q, rng.standard_normal((1, heads * hd)), rng.standard_normal((1, heads * hd)),
+                           np.full((1, heads), 0.9), np.zeros((1, heads)))
+    assert np.allclose(S1, 0.9 * S0, rtol=1e-15)
+    ref = np.einsum("hvk,hk->hv", 0.9 * S0[0], q.reshape(heads, hd)).reshape(1, -1) / np.sqrt(hd)
+    assert np.allclose(o, ref, rtol=1e-12)
