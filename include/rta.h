@@ -151,8 +151,8 @@ int64_t rta_history_bytes(int kvw);
  *             and sets RTA_DEVERR_HITS.
  *   max_ctx   host upper bound of min(ctx_len[s], capacity) over s (grid sizing).
  *   gate      [nseq, hq, hd] or NULL: out *= sigmoid(gate).
- *   out [nseq, hq, hd]; m_out, z_out [nseq, hq]: m = max score, z = sum exp(s - m)
- *   (the reference reports physical = (m + 20, z)).
+ *   out [nseq, hq, hd]; m_out, z_out [nseq, hq] (each may be NULL): m = max score,
+ *   z = sum exp(s - m) (the reference reports physical = (m + 20, z)).
  * hd must be 128 and hq/hkv in {1, 2, 4, 8}.
  * Replaces Resident::detectHistory (optical_resident.cpp:429-449): history ray
  * trace op 0 + check op 8 (resident_ray.comp:30-53,80) and the detector op 3
@@ -218,6 +218,85 @@ int rta_delta_rule(float* state, const float* qkv, int qkv_stride, const float* 
  * reference's fp32 op order; exact .5 ties of the code rounding resolve to even. */
 int rta_pack_history(const float* k, int k_stride, const float* v, int v_stride, int batch, int kvw, int fmt_k,
                      int fmt_v, const int64_t* slot, int64_t n_slots, void* packets, rta_stream_t stream);
+
+/* ---------------- one greedy decode step of a hybrid decoder (gated delta-net
+ * recurrent layers and full-attention layers, 128-wide heads), for a batch of
+ * independent sequences.  The host sequencing of Resident::forward / layer / word
+ * (optical_resident.cpp:455-530): per layer RMSNorm, the fused in-projection, then
+ *   full layers:      QK-norm + RoPE (ops 14, 3), history pack (op 34), attention,
+ *   recurrent layers: gates (op 18), short conv + L2 norm (ops 19, 20), delta rule
+ *                     with the gated norm (ops 21, 15),
+ * the O projection with the residual add, RMSNorm and the SwiGLU MLP (executeMLP),
+ * and finally RMSNorm, the LM head and the margin argmax.  Tokens, positions and
+ * ring slots stay on the device and are advanced there, so one step can be
+ * captured in a HIP graph and replayed. */
+typedef struct rta_hybrid_shape {
+    int hidden, layers;
+    int full_every;                   /* layer l is full attention when l % full_every == full_every - 1 */
+    int q_heads, kv_heads, head_dim;  /* head_dim must be 128 */
+    int rec_heads;                    /* delta-net heads, each with a head_dim x head_dim fp32 state */
+    int ff, vocab;
+    int capacity;                     /* history ring slots per sequence and full layer */
+    int fmt_embed, fmt_proj, fmt_lm;  /* GGUF codes; fmt_proj / fmt_lm may carry RTA_TILED */
+    int fmt_k, fmt_v;                 /* history packet fields (the reference: K Q4_K, V Q6_K) */
+    int rope_rotary;                  /* rotated dimensions per head (even, <= head_dim) */
+    float eps;                        /* RMSNorm epsilon */
+    float margin;                     /* argmax tie margin (relative), as rta_lm_head */
+    double rope_theta;
+} rta_hybrid_shape;
+
+typedef struct rta_hybrid_layer {   /* device pointers; fmt_proj matrices [rows x cols] */
+    const float* norm_in;            /* [hidden] */
+    const float* norm_post;          /* [hidden] */
+    const void* w_in;                /* full: (q_heads + 2 kv_heads) * 128 rows [q | k | v];
+                                        recurrent: 4 S + 2 rec_heads rows [q | k | v | z | a | b],
+                                        S = rec_heads * 128; cols = hidden */
+    const void* w_o;                 /* [hidden x (q_heads * 128 or S)] */
+    const void* w_gate;              /* [ff x hidden] */
+    const void* w_up;                /* [ff x hidden] */
+    const void* w_down;              /* [hidden x ff] */
+    const float* q_norm;             /* full: [q_heads * 128] or NULL (no QK-norm) */
+    const float* k_norm;             /* full: [kv_heads * 128] or NULL */
+    const float* conv_w;             /* recurrent: [3 S][4] */
+    const float* a_log;              /* recurrent: [rec_heads] */
+    const float* dt_bias;            /* recurrent: [rec_heads] */
+    const float* out_norm;           /* recurrent: [S] gated-norm weight */
+} rta_hybrid_layer;
+
+typedef struct rta_hybrid_weights {
+    const void* embed;               /* [vocab x hidden] fmt_embed */
+    const rta_hybrid_layer* layers;  /* host array of `layers` entries */
+    const float* norm_final;         /* [hidden] */
+    const void* lm_head;             /* [vocab x hidden] fmt_lm */
+} rta_hybrid_weights;
+
+typedef struct rta_hybrid_views {   /* where the state buffer keeps each part */
+    float* recurrent;                /* [recurrent layer][batch][rec_heads][128 value][128 key] */
+    float* conv;                     /* [recurrent layer][batch][3 S][3] previous raw q|k|v, oldest first */
+    uint8_t* packets;                /* [full layer][batch][capacity] history packets */
+    int64_t* slot_base;              /* [full layer][batch] first ring slot of each sequence */
+    int32_t* ctx;                    /* [batch] tokens already in the history = next position */
+    int64_t recurrent_per_layer, conv_per_layer, packet_bytes, slots_per_layer;
+} rta_hybrid_views;
+
+/* Device bytes of the persistent state and of the per-step workspace; 0 if invalid. */
+size_t rta_hybrid_state_bytes(const rta_hybrid_shape* shape, int batch);
+size_t rta_hybrid_workspace_bytes(const rta_hybrid_shape* shape, int batch);
+
+/* Pointers into a state buffer (256-byte aligned) for filling or reading it. */
+int rta_hybrid_layout(const rta_hybrid_shape* shape, int batch, void* state, rta_hybrid_views* views);
+
+/* Sets the ring bases and the starting positions ctx[batch] (device int32) of a state
+ * buffer; the recurrent, conv and packet parts are left as the caller filled them. */
+int rta_hybrid_init(const rta_hybrid_shape* shape, int batch, void* state, const int32_t* ctx, rta_stream_t stream);
+
+/* One decode step: reads tokens[batch] (device uint32; the embedding of each
+ * sequence's newest token), writes the greedy next tokens into the same array, and
+ * optionally the logits [batch x vocab] (logits_out may be NULL).  Positions advance
+ * by one on the device. */
+int rta_hybrid_decode_step(const rta_hybrid_shape* shape, const rta_hybrid_weights* weights, int batch, void* state,
+                           uint32_t* tokens, float* logits_out, void* workspace, size_t workspace_bytes,
+                           rta_stream_t stream);
 
 #ifdef __cplusplus
 }

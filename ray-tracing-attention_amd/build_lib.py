@@ -9,7 +9,7 @@ import sys
 from pathlib import Path
 
 HERE = Path(__file__).resolve().parent
-SOURCES = ["csrc/rta_gemv.hip", "csrc/rta_attention.hip", "csrc/rta_step.hip"]
+SOURCES = ["csrc/rta_gemv.hip", "csrc/rta_attention.hip", "csrc/rta_step.hip", "csrc/rta_model.hip"]
 LIB = HERE / "lib" / "librta.so"
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 

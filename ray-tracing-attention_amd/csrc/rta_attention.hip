@@ -317,8 +317,8 @@ __global__ void __launch_bounds__(kHd) attn_merge_kernel(const AttnArgs a) {
     if (visible <= 0) {
         out[dd] = 0.0f;
         if (dd == 0) {
-            a.m_out[sh] = -INFINITY;
-            a.z_out[sh] = 0.0f;
+            if (a.m_out) a.m_out[sh] = -INFINITY;
+            if (a.z_out) a.z_out[sh] = 0.0f;
             raise_error(RTA_DEVERR_HITS);
         }
         return;
@@ -341,10 +341,8 @@ __global__ void __launch_bounds__(kHd) attn_merge_kernel(const AttnArgs a) {
     float o = U / fmaxf(Z, 1e-30f);
     if (a.gate) o *= detector_sigmoid(a.gate[(int64_t)sh * kHd + dd]);
     out[dd] = o;
-    if (dd == 0) {
-        a.m_out[sh] = M;
-        a.z_out[sh] = Z;
-    }
+    if (dd == 0 && a.m_out) a.m_out[sh] = M;
+    if (dd == 0 && a.z_out) a.z_out[sh] = Z;
 }
 
 // ---- RoPE -------------------------------------------------------------------
@@ -409,7 +407,7 @@ int rta_decode_attention(const float* q, int nseq, int hq, int hkv, int hd, cons
                          const int64_t* slot_base, const int32_t* ctx_len, int64_t capacity, int64_t n_slots,
                          int max_ctx, const float* gate, float* out, float* m_out, float* z_out, void* workspace,
                          size_t workspace_bytes, rta_stream_t stream) {
-    if (!q || !packets || !slot_base || !ctx_len || !out || !m_out || !z_out) return RTA_ERR_NULL;
+    if (!q || !packets || !slot_base || !ctx_len || !out) return RTA_ERR_NULL;   // m_out, z_out optional
     if (nseq <= 0 || hq <= 0 || hkv <= 0 || hd <= 0 || hq % hkv || capacity <= 0 || max_ctx <= 0 || n_slots <= 0)
         return RTA_ERR_SHAPE;
     if ((fmt_k != RTA_Q4_K && fmt_k != RTA_Q6_K) || (fmt_v != RTA_Q4_K && fmt_v != RTA_Q6_K)) return RTA_ERR_FORMAT;

@@ -1,0 +1,336 @@
+// rta_model.hip -- one greedy decode step of a hybrid (gated delta-net + full
+// attention) decoder, sequenced on the host over the library's kernels; the role of
+// Resident::forward / Resident::layer / Resident::word (optical_resident.cpp:455-530)
+// for a batch of independent sequences.
+//
+// Everything a step reads per sequence (token, position, ring slots) lives in device
+// memory and is advanced on the device, so a caller may capture one step in a HIP
+// graph and replay it.
+#include <math.h>
+#include <string.h>
+
+#include <algorithm>
+
+#include "rta_common.hpp"
+#include "rta_host.hpp"
+
+namespace rta {
+
+// Step prologue: the new token of sequence b sits at position pos = ctx[b]; it is
+// written to ring slot base[l][b] + pos % capacity of every full layer l and sees
+// min(pos + 1, capacity) history entries.  ctx advances by one.
+__global__ void __launch_bounds__(256) step_prologue_kernel(int32_t* __restrict__ ctx, int batch, int n_full,
+                                                            int64_t capacity, const int64_t* __restrict__ base,
+                                                            int64_t* __restrict__ pos64, int32_t* __restrict__ visible,
+                                                            int64_t* __restrict__ slots) {
+    const int b = blockIdx.x * 256 + threadIdx.x;
+    if (b >= batch) return;
+    const int32_t pos = ctx[b];
+    pos64[b] = pos;
+    visible[b] = pos + 1;
+    for (int l = 0; l < n_full; ++l) slots[(int64_t)l * batch + b] = base[(int64_t)l * batch + b] + pos % capacity;
+    ctx[b] = pos + 1;
+}
+
+// Fused QK-norm (op 14, resident_math.comp:113-114) and RoPE (op 3,
+// resident_math.comp:76-77; phase resident_common.glsl:117) over the q and k heads
+// of the [q | k | v] projection rows; one wave per (row, head), lane l holds the
+// adjacent pair (2l, 2l+1) of a 128-wide head.  q goes to q_out (contiguous), k is
+// rotated in place.  wq / wk NULL: RoPE only.
+__global__ void __launch_bounds__(256) qk_norm_rope_kernel(float* __restrict__ qkv, int stride, int hq, int hkv,
+                                                           const float* __restrict__ wq,
+                                                           const float* __restrict__ wk, float eps,
+                                                           const int64_t* __restrict__ positions, int rotary,
+                                                           double theta, float* __restrict__ q_out) {
+    constexpr int hd = 128;
+    const int lane = threadIdx.x & 63, head = blockIdx.x * 4 + (threadIdx.x >> 6), b = blockIdx.y;
+    if (head >= hq + hkv) return;
+    const bool isq = head < hq;
+    float* x = qkv + (int64_t)b * stride + (int64_t)head * hd;   // k heads follow the q heads
+    float2 v = reinterpret_cast<float2*>(x)[lane];
+    const float* w = isq ? (wq ? wq + head * hd : nullptr) : (wk ? wk + (head - hq) * hd : nullptr);
+    if (w) {
+        float ss = v.x * v.x + v.y * v.y;
+        for (int off = 32; off > 0; off >>= 1) ss += __shfl_xor(ss, off, kWave);
+        const float inv = 1.0f / sqrtf(ss / (float)hd + eps);
+        v.x = v.x * inv * w[2 * lane];
+        v.y = v.y * inv * w[2 * lane + 1];
+    }
+    const int active = rotary / 2;
+    if (lane < active) {
+        const double phase = (double)positions[b] * pow(theta, -(double)lane / (double)active);
+        double sn, cs;
+        sincos(phase, &sn, &cs);
+        const double a = v.x, c = v.y;
+        v.x = (float)(a * cs - c * sn);
+        v.y = (float)(a * sn + c * cs);
+    }
+    if (isq) reinterpret_cast<float2*>(q_out + ((int64_t)b * hq + head) * hd)[lane] = v;
+    else reinterpret_cast<float2*>(x)[lane] = v;
+}
+
+// Ring bases (sequence b owns slots [b * capacity, (b + 1) * capacity) of every
+// full layer's packet array) and the starting positions.
+__global__ void __launch_bounds__(256) state_init_kernel(const int32_t* __restrict__ ctx_in, int batch, int n_full,
+                                                         int64_t capacity, int64_t* __restrict__ base,
+                                                         int32_t* __restrict__ ctx) {
+    const int b = blockIdx.x * 256 + threadIdx.x;
+    if (b >= batch) return;
+    for (int l = 0; l < n_full; ++l) base[(int64_t)l * batch + b] = (int64_t)b * capacity;
+    ctx[b] = ctx_in[b];
+}
+
+namespace {
+
+struct Carve {
+    uint8_t* p;
+    size_t off = 0;
+    explicit Carve(void* base) : p(static_cast<uint8_t*>(base)) {}
+    template <class T>
+    T* take(size_t n) {
+        off = (off + 255) & ~(size_t)255;
+        T* r = p ? reinterpret_cast<T*>(p + off) : nullptr;
+        off += n * sizeof(T);
+        return r;
+    }
+};
+
+struct Dims {
+    int D, L, nfull, nrec, hq, hkv, hd, H, S, FF, V, cap, B;
+    int rows_full, rows_rec, kvw;
+    int64_t stride;
+};
+
+Dims dims_of(const rta_hybrid_shape* s, int batch) {
+    Dims d{};
+    d.D = s->hidden;
+    d.L = s->layers;
+    d.nfull = s->full_every > 0 ? s->layers / s->full_every : 0;
+    d.nrec = d.L - d.nfull;
+    d.hq = s->q_heads;
+    d.hkv = s->kv_heads;
+    d.hd = s->head_dim;
+    d.H = s->rec_heads;
+    d.S = s->rec_heads * s->head_dim;
+    d.FF = s->ff;
+    d.V = s->vocab;
+    d.cap = s->capacity;
+    d.B = batch;
+    d.rows_full = (d.hq + 2 * d.hkv) * d.hd;
+    d.rows_rec = 4 * d.S + 2 * d.H;
+    d.kvw = d.hkv * d.hd;
+    d.stride = host::history_bytes(d.kvw);
+    return d;
+}
+
+bool is_full(const rta_hybrid_shape* s, int l) { return s->full_every > 0 && l % s->full_every == s->full_every - 1; }
+
+int check_shape(const rta_hybrid_shape* s, int batch) {
+    if (!s) return RTA_ERR_NULL;
+    if (batch <= 0 || batch > 4096 || s->layers <= 0 || s->full_every < 0 || s->hidden <= 0 ||
+        s->hidden % 256 || s->ff <= 0 || s->ff % 256 || s->vocab <= 0 || s->capacity <= 0)
+        return RTA_ERR_SHAPE;
+    if (s->head_dim != 128 || (s->full_every > 0 && (s->q_heads <= 0 || s->kv_heads <= 0 || s->q_heads % s->kv_heads)) ||
+        (s->full_every != 1 && s->rec_heads <= 0) || s->rope_rotary <= 0 || s->rope_rotary > 128 || s->rope_rotary % 2 ||
+        !(s->eps >= 0.0f) || !(s->rope_theta > 0.0))
+        return RTA_ERR_RANGE;
+    if ((s->full_every > 0 && (s->q_heads * 128) % 256) || (s->rec_heads * 128) % 256) return RTA_ERR_SHAPE;
+    return RTA_OK;
+}
+
+struct State {
+    float* rec;        // [nrec][B][H][hd][hd]
+    float* conv;       // [nrec][B][3S][3]
+    uint8_t* packets;  // [nfull][B][cap][stride]
+    int64_t* base;     // [nfull][B]
+    int32_t* ctx;      // [B]
+};
+
+State carve_state(const Dims& d, void* p, size_t* bytes) {
+    Carve c(p);
+    State s;
+    s.rec = c.take<float>((size_t)d.nrec * d.B * d.H * d.hd * d.hd);
+    s.conv = c.take<float>((size_t)d.nrec * d.B * 3 * d.S * 3);
+    s.packets = c.take<uint8_t>((size_t)d.nfull * d.B * d.cap * d.stride);
+    s.base = c.take<int64_t>((size_t)d.nfull * d.B);
+    s.ctx = c.take<int32_t>((size_t)d.B);
+    if (bytes) *bytes = (c.off + 255) & ~(size_t)255;
+    return s;
+}
+
+struct Work {
+    float *hidden, *normed, *proj, *q, *conv, *decay, *beta, *mix, *act, *logits;
+    int64_t *pos, *slots;
+    int32_t* visible;
+    void *attn_ws, *lm_ws, *gemm_ws;
+    size_t attn_bytes, lm_bytes, gemm_bytes;
+};
+
+size_t gemm_ws_bytes(const rta_hybrid_shape* s, const Dims& d) {
+    size_t m = 0;
+    auto up = [&](size_t v) { m = std::max(m, v); };
+    if (d.nfull) up(rta_gemv_workspace_bytes(s->fmt_proj, d.rows_full, d.D, d.B));
+    if (d.nrec) up(rta_gemv_workspace_bytes(s->fmt_proj, d.rows_rec, d.D, d.B));
+    if (d.nfull) up(rta_gemv_workspace_bytes(s->fmt_proj, d.D, d.hq * d.hd, d.B));
+    if (d.nrec) up(rta_gemv_workspace_bytes(s->fmt_proj, d.D, d.S, d.B));
+    up(rta_mlp_workspace_bytes(s->fmt_proj, s->fmt_proj, d.D, d.FF, d.B));
+    return m;
+}
+
+Work carve_work(const rta_hybrid_shape* s, const Dims& d, void* p, size_t* bytes) {
+    Carve c(p);
+    Work w{};
+    const size_t B = d.B;
+    w.hidden = c.take<float>(B * d.D);
+    w.normed = c.take<float>(B * d.D);
+    w.proj = c.take<float>(B * std::max(d.nfull ? d.rows_full : 0, d.nrec ? d.rows_rec : 0));
+    w.q = c.take<float>(B * std::max(1, d.hq * d.hd));
+    w.conv = c.take<float>(B * std::max(1, 3 * d.S));
+    w.decay = c.take<float>(B * std::max(1, d.H));
+    w.beta = c.take<float>(B * std::max(1, d.H));
+    w.mix = c.take<float>(B * std::max(d.hq * d.hd, d.S));
+    w.act = c.take<float>(B * d.FF);
+    w.logits = c.take<float>(B * d.V);
+    w.pos = c.take<int64_t>(B);
+    w.slots = c.take<int64_t>(B * std::max(1, d.nfull));
+    w.visible = c.take<int32_t>(B);
+    w.attn_bytes = d.nfull ? rta_decode_attention_workspace_bytes(d.B, d.hq, d.hkv, d.hd, d.cap) : 0;
+    w.attn_ws = c.take<uint8_t>(std::max<size_t>(w.attn_bytes, 1));
+    w.lm_bytes = rta_lm_head_workspace_bytes(s->fmt_lm, d.V, d.D, d.B);
+    w.lm_ws = c.take<uint8_t>(std::max<size_t>(w.lm_bytes, 1));
+    w.gemm_bytes = gemm_ws_bytes(s, d);
+    w.gemm_ws = c.take<uint8_t>(std::max<size_t>(w.gemm_bytes, 1));
+    if (bytes) *bytes = (c.off + 255) & ~(size_t)255;
+    return w;
+}
+
+}  // namespace
+}  // namespace rta
+
+using namespace rta;
+
+extern "C" {
+
+size_t rta_hybrid_state_bytes(const rta_hybrid_shape* shape, int batch) {
+    if (check_shape(shape, batch)) return 0;
+    size_t bytes = 0;
+    carve_state(dims_of(shape, batch), nullptr, &bytes);
+    return bytes;
+}
+
+size_t rta_hybrid_workspace_bytes(const rta_hybrid_shape* shape, int batch) {
+    if (check_shape(shape, batch)) return 0;
+    size_t bytes = 0;
+    carve_work(shape, dims_of(shape, batch), nullptr, &bytes);
+    return bytes;
+}
+
+int rta_hybrid_layout(const rta_hybrid_shape* shape, int batch, void* state, rta_hybrid_views* views) {
+    int rc = check_shape(shape, batch);
+    if (rc) return rc;
+    if (!state || !views) return RTA_ERR_NULL;
+    const Dims d = dims_of(shape, batch);
+    const State s = carve_state(d, state, nullptr);
+    views->recurrent = s.rec;
+    views->conv = s.conv;
+    views->packets = s.packets;
+    views->slot_base = s.base;
+    views->ctx = s.ctx;
+    views->recurrent_per_layer = (int64_t)d.B * d.H * d.hd * d.hd;
+    views->conv_per_layer = (int64_t)d.B * 3 * d.S * 3;
+    views->packet_bytes = d.stride;
+    views->slots_per_layer = (int64_t)d.B * d.cap;
+    return RTA_OK;
+}
+
+int rta_hybrid_init(const rta_hybrid_shape* shape, int batch, void* state, const int32_t* ctx, rta_stream_t stream) {
+    int rc = check_shape(shape, batch);
+    if (rc) return rc;
+    if (!state || !ctx) return RTA_ERR_NULL;
+    if (!host::aligned(state, 256)) return RTA_ERR_ALIGN;
+    const Dims d = dims_of(shape, batch);
+    const State st = carve_state(d, state, nullptr);
+    hipLaunchKernelGGL(state_init_kernel, dim3((batch + 255) / 256), dim3(256), 0, (hipStream_t)stream, ctx, batch,
+                       d.nfull, (int64_t)d.cap, st.base, st.ctx);
+    return hipGetLastError() == hipSuccess ? RTA_OK : RTA_ERR_LAUNCH;
+}
+
+int rta_hybrid_decode_step(const rta_hybrid_shape* shape, const rta_hybrid_weights* weights, int batch, void* state,
+                           uint32_t* tokens, float* logits_out, void* workspace, size_t workspace_bytes,
+                           rta_stream_t stream) {
+    int rc = check_shape(shape, batch);
+    if (rc) return rc;
+    if (!weights || !weights->layers || !weights->embed || !weights->lm_head || !weights->norm_final || !state ||
+        !tokens || !workspace)
+        return RTA_ERR_NULL;
+    if (workspace_bytes < rta_hybrid_workspace_bytes(shape, batch)) return RTA_ERR_WORKSPACE;
+    if (!host::aligned(state, 256) || !host::aligned(workspace, 256)) return RTA_ERR_ALIGN;
+    const Dims d = dims_of(shape, batch);
+    const State st = carve_state(d, state, nullptr);
+    Work w = carve_work(shape, d, workspace, nullptr);
+    hipStream_t s = (hipStream_t)stream;
+    const int pf = shape->fmt_proj;
+    const float eps = shape->eps;
+    const int B = d.B;
+#define RTA_TRY(call)            \
+    do {                         \
+        const int e_ = (call);   \
+        if (e_) return e_;       \
+    } while (0)
+
+    // prologue: positions, visible counts, ring slots; the token embedding (op 0)
+    hipLaunchKernelGGL(step_prologue_kernel, dim3((B + 255) / 256), dim3(256), 0, s, st.ctx, B, d.nfull,
+                       (int64_t)d.cap, st.base, w.pos, w.visible, w.slots);
+    if (hipGetLastError() != hipSuccess) return RTA_ERR_LAUNCH;
+    RTA_TRY(rta_embed(shape->fmt_embed, weights->embed, d.V, d.D, tokens, B, w.hidden, stream));
+
+    int lf = 0, lr = 0;
+    for (int l = 0; l < d.L; ++l) {
+        const rta_hybrid_layer& lw = weights->layers[l];
+        RTA_TRY(rta_rmsnorm(w.hidden, lw.norm_in, B, d.D, eps, w.normed, stream));
+        if (is_full(shape, l)) {
+            // op 2 index 5 (q | k | v), ops 14 + 3, op 34, attention, op 2 index 2
+            RTA_TRY(rta_gemv(pf, lw.w_in, d.rows_full, d.D, w.normed, B, w.proj, RTA_EPI_STORE, w.gemm_ws,
+                             w.gemm_bytes, stream));
+            hipLaunchKernelGGL(qk_norm_rope_kernel, dim3((d.hq + d.hkv + 3) / 4, B), dim3(256), 0, s, w.proj,
+                               d.rows_full, d.hq, d.hkv, lw.q_norm, lw.k_norm, eps, w.pos, shape->rope_rotary,
+                               shape->rope_theta, w.q);
+            if (hipGetLastError() != hipSuccess) return RTA_ERR_LAUNCH;
+            uint8_t* packets = st.packets + (size_t)lf * B * d.cap * d.stride;
+            RTA_TRY(rta_pack_history(w.proj + d.hq * d.hd, d.rows_full, w.proj + (d.hq + d.hkv) * d.hd, d.rows_full,
+                                     B, d.kvw, shape->fmt_k, shape->fmt_v, w.slots + (size_t)lf * B,
+                                     (int64_t)B * d.cap, packets, stream));
+            RTA_TRY(rta_decode_attention(w.q, B, d.hq, d.hkv, d.hd, packets, shape->fmt_k, shape->fmt_v,
+                                         st.base + (size_t)lf * B, w.visible, d.cap, (int64_t)B * d.cap, d.cap,
+                                         nullptr, w.mix, nullptr, nullptr, w.attn_ws, w.attn_bytes, stream));
+            RTA_TRY(rta_gemv(pf, lw.w_o, d.D, d.hq * d.hd, w.mix, B, w.hidden, RTA_EPI_ACCUMULATE, w.gemm_ws,
+                             w.gemm_bytes, stream));
+            ++lf;
+        } else {
+            // op 2 index 5 (q | k | v | z | a | b), ops 18-21 and 15, op 2 index 2
+            RTA_TRY(rta_gemv(pf, lw.w_in, d.rows_rec, d.D, w.normed, B, w.proj, RTA_EPI_STORE, w.gemm_ws,
+                             w.gemm_bytes, stream));
+            RTA_TRY(rta_delta_gates(w.proj + 4 * d.S, w.proj + 4 * d.S + d.H, d.rows_rec, lw.a_log, lw.dt_bias, B,
+                                    d.H, w.decay, w.beta, stream));
+            RTA_TRY(rta_short_conv(w.proj, d.rows_rec, st.conv + (size_t)lr * B * 3 * d.S * 3, lw.conv_w, B, d.H,
+                                   d.hd, eps, w.conv, stream));
+            RTA_TRY(rta_delta_rule(st.rec + (size_t)lr * B * d.H * d.hd * d.hd, w.conv, 3 * d.S, w.decay, w.beta,
+                                   B, d.H, d.hd, lw.out_norm, w.proj + 3 * d.S, d.rows_rec, eps, w.mix, d.S, stream));
+            RTA_TRY(rta_gemv(pf, lw.w_o, d.D, d.S, w.mix, B, w.hidden, RTA_EPI_ACCUMULATE, w.gemm_ws, w.gemm_bytes,
+                             stream));
+            ++lr;
+        }
+        // op 1 index 1, then the SwiGLU MLP with the residual add (executeMLP)
+        RTA_TRY(rta_rmsnorm(w.hidden, lw.norm_post, B, d.D, eps, w.normed, stream));
+        RTA_TRY(rta_mlp_swiglu(pf, lw.w_gate, pf, lw.w_up, pf, lw.w_down, d.D, d.FF, w.normed, B, w.act, w.hidden,
+                               RTA_EPI_ACCUMULATE, w.gemm_ws, w.gemm_bytes, stream));
+    }
+    // op 1 index 2, then the readout (Resident::word): logits and the next tokens
+    RTA_TRY(rta_rmsnorm(w.hidden, weights->norm_final, B, d.D, eps, w.normed, stream));
+    RTA_TRY(rta_lm_head(shape->fmt_lm, weights->lm_head, d.V, d.D, w.normed, B, shape->margin,
+                        logits_out ? logits_out : w.logits, tokens, w.lm_ws, w.lm_bytes, stream));
+#undef RTA_TRY
+    return RTA_OK;
+}
+
+}  // extern "C"

@@ -34,6 +34,12 @@ SIGNATURES = {
     "rta_delta_rule": (_i, [_p, _p, _i, _p, _p, _i, _i, _i, _p, _p, _i, _f, _p, _i, _p]),
     "rta_pack_history": (_i, [_p, _i, _p, _i, _i, _i, _i, _i, _p, _i64, _p, _p]),
     "rta_pack_bytes": (_i64, [_i, _i, _i]),
+    # struct-pointer arguments as void*; rta.model rebinds them with typed pointers
+    "rta_hybrid_state_bytes": (_sz, [_p, _i]),
+    "rta_hybrid_workspace_bytes": (_sz, [_p, _i]),
+    "rta_hybrid_layout": (_i, [_p, _i, _p, _p]),
+    "rta_hybrid_init": (_i, [_p, _i, _p, _p, _p]),
+    "rta_hybrid_decode_step": (_i, [_p, _p, _i, _p, _p, _p, _p, _sz, _p]),
     "rta_pack": (_i, [_i, _p, _i, _i, _p, _p]),
     "rta_gemv_workspace_bytes": (_sz, [_i, _i, _i, _i]),
     "rta_gemv": (_i, [_i, _p, _i, _i, _p, _i, _p, _i, _p, _sz, _p]),

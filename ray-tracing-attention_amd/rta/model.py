@@ -1,0 +1,254 @@
+"""Hybrid decoder (gated delta-net recurrent layers + full attention) over
+librta.so's rta_hybrid_* entry points: ctypes mirrors of the C structs, synthetic
+random-init weights and states of a given shape, and one greedy decode step.
+
+The C driver (rta_hybrid_decode_step) sequences the layers the way the reference's
+worker does (optical_resident.cpp:455-530); this module only owns device memory.
+"""
+import ctypes
+import math
+
+import torch
+
+from . import _lib
+from ._lib import Q4_K, Q6_K, TILED, check
+from . import ops
+
+_i, _f, _d, _p, _i64 = ctypes.c_int, ctypes.c_float, ctypes.c_double, ctypes.c_void_p, ctypes.c_int64
+
+
+class HybridShape(ctypes.Structure):
+    _fields_ = [("hidden", _i), ("layers", _i), ("full_every", _i), ("q_heads", _i), ("kv_heads", _i),
+                ("head_dim", _i), ("rec_heads", _i), ("ff", _i), ("vocab", _i), ("capacity", _i),
+                ("fmt_embed", _i), ("fmt_proj", _i), ("fmt_lm", _i), ("fmt_k", _i), ("fmt_v", _i),
+                ("rope_rotary", _i), ("eps", _f), ("margin", _f), ("rope_theta", _d)]
+
+
+class HybridLayer(ctypes.Structure):
+    _fields_ = [(n, _p) for n in ("norm_in", "norm_post", "w_in", "w_o", "w_gate", "w_up", "w_down", "q_norm",
+                                  "k_norm", "conv_w", "a_log", "dt_bias", "out_norm")]
+
+
+class HybridWeights(ctypes.Structure):
+    _fields_ = [("embed", _p), ("layers", ctypes.POINTER(HybridLayer)), ("norm_final", _p), ("lm_head", _p)]
+
+
+class HybridViews(ctypes.Structure):
+    _fields_ = [("recurrent", _p), ("conv", _p), ("packets", _p), ("slot_base", _p), ("ctx", _p),
+                ("recurrent_per_layer", _i64), ("conv_per_layer", _i64), ("packet_bytes", _i64),
+                ("slots_per_layer", _i64)]
+
+
+_SIGS = {
+    "rta_hybrid_state_bytes": (ctypes.c_size_t, [ctypes.POINTER(HybridShape), _i]),
+    "rta_hybrid_workspace_bytes": (ctypes.c_size_t, [ctypes.POINTER(HybridShape), _i]),
+    "rta_hybrid_layout": (_i, [ctypes.POINTER(HybridShape), _i, _p, ctypes.POINTER(HybridViews)]),
+    "rta_hybrid_init": (_i, [ctypes.POINTER(HybridShape), _i, _p, _p, _p]),
+    "rta_hybrid_decode_step": (_i, [ctypes.POINTER(HybridShape), ctypes.POINTER(HybridWeights), _i, _p, _p, _p, _p,
+                                    ctypes.c_size_t, _p]),
+}
+
+
+def _lib_h():
+    lib = _lib.load()
+    for name, (res, args) in _SIGS.items():
+        f = getattr(lib, name)
+        f.restype, f.argtypes = res, args
+    return lib
+
+
+def shape_9b(capacity, packed=True):
+    """The 9B-like shape: 32 layers (3 recurrent : 1 full), hidden 4096, 32/8 heads x 128,
+    32 delta-net heads, FF 12288, vocab 151936, Q4_K projections, Q6_K LM head."""
+    return HybridShape(hidden=4096, layers=32, full_every=4, q_heads=32, kv_heads=8, head_dim=128, rec_heads=32,
+                       ff=12288, vocab=151936, capacity=capacity, fmt_embed=Q4_K,
+                       fmt_proj=Q4_K | (TILED if packed else 0), fmt_lm=Q6_K | (TILED if packed else 0),
+                       fmt_k=Q4_K, fmt_v=Q6_K, rope_rotary=128, eps=1e-6, margin=1e-4, rope_theta=1e6)
+
+
+# ------------------------------------------------------------- synthetic data ----
+def random_kquant(fmt, rows, cols, gen, dev, d_scale=0.01):
+    """A [rows x cols] GGUF matrix with the fields of the benchmark configs: Q4_K 6-bit
+    scale / min codes and 4-bit quants uniform, d and dmin = |N(0,1)| * d_scale;
+    Q6_K int8 scales uniform in [-32, 31], 6-bit quants uniform, d = |N(0,1)| * d_scale."""
+    nsb = cols // 256
+    blk = 144 if fmt == Q4_K else 210
+    w = torch.randint(0, 256, (rows * nsb, blk), dtype=torch.uint8, device=dev, generator=gen)
+    n = rows * nsb
+    half = lambda: (torch.randn(n, device=dev, generator=gen).abs() * d_scale).to(torch.float16).view(torch.uint8)
+    if fmt == Q4_K:
+        w[:, 0:2] = half().view(n, 2)
+        w[:, 2:4] = half().view(n, 2)
+    else:
+        w[:, 192:208] = torch.randint(-32, 32, (n, 16), dtype=torch.int8, device=dev, generator=gen).view(torch.uint8)
+        w[:, 208:210] = half().view(n, 2)
+    return w.view(rows, nsb * blk)
+
+
+def _near_one(n, gen, dev, spread=0.05):
+    return (1.0 + spread * torch.randn(n, device=dev, generator=gen)).float()
+
+
+class DecodeModel:
+    """Device weights + state of a hybrid decoder and its graph-replayable decode step."""
+
+    def __init__(self, shape, batch, ctx, seed=20261115, dev="cuda:0", keep_gguf=False):
+        self.lib = _lib_h()
+        self.shape = shape
+        self.batch = batch
+        self.dev = torch.device(dev)
+        gen = torch.Generator(device=self.dev)
+        gen.manual_seed(seed)
+        s = shape
+        self._keep = []
+        self.gguf = {} if keep_gguf else None   # name -> GGUF matrix (tests feed these to the oracle)
+        base_fmt = lambda f: f & 0xff
+
+        def mat(fmt, rows, cols, d_scale=0.01, small_rows=0, name=None):
+            w = random_kquant(base_fmt(fmt), rows, cols, gen, self.dev, d_scale)
+            if small_rows:   # the delta-net a / b rows: tiny, so decay stays near its target
+                nsb = cols // 256
+                tail = w.view(rows, nsb, -1)[rows - small_rows:]
+                hv = (torch.randn(small_rows * nsb, device=self.dev, generator=gen).abs() * 1e-6).to(torch.float16)
+                hv = hv.view(torch.uint8).view(small_rows, nsb, 2)
+                if base_fmt(fmt) == Q4_K:
+                    tail[:, :, 0:2] = hv
+                    tail[:, :, 2:4] = 0
+                else:
+                    tail[:, :, 208:210] = hv
+            if self.gguf is not None and name:
+                self.gguf[name] = w.cpu().numpy()
+            if fmt & TILED:
+                w = ops.pack(base_fmt(fmt), w, rows, cols)
+            self._keep.append(w)
+            return w
+
+        def vec(t, name=None):
+            self._keep.append(t)
+            if self.gguf is not None and name:
+                self.gguf[name] = t.cpu().numpy()
+            return t.data_ptr()
+
+        hd, S, H = s.head_dim, s.rec_heads * s.head_dim, s.rec_heads
+        self.layers = (HybridLayer * s.layers)()
+        for l in range(s.layers):
+            L = self.layers[l]
+            L.norm_in = vec(_near_one(s.hidden, gen, self.dev), f"{l}.norm_in")
+            L.norm_post = vec(_near_one(s.hidden, gen, self.dev), f"{l}.norm_post")
+            full = s.full_every > 0 and l % s.full_every == s.full_every - 1
+            if full:
+                L.w_in = mat(s.fmt_proj, (s.q_heads + 2 * s.kv_heads) * hd, s.hidden, name=f"{l}.w_in").data_ptr()
+                L.w_o = mat(s.fmt_proj, s.hidden, s.q_heads * hd, name=f"{l}.w_o").data_ptr()
+                L.q_norm = vec(_near_one(s.q_heads * hd, gen, self.dev), f"{l}.q_norm")
+                L.k_norm = vec(_near_one(s.kv_heads * hd, gen, self.dev), f"{l}.k_norm")
+            else:
+                L.w_in = mat(s.fmt_proj, 4 * S + 2 * H, s.hidden, small_rows=2 * H, name=f"{l}.w_in").data_ptr()
+                L.w_o = mat(s.fmt_proj, s.hidden, S, name=f"{l}.w_o").data_ptr()
+                L.conv_w = vec((0.5 * torch.randn(3 * S, 4, device=self.dev, generator=gen)).float(), f"{l}.conv_w")
+                # decay ~ U(0.9, 0.999) at a = 0: exp(a_log) softplus(dt_bias) = -ln(decay)
+                target = 0.9 + 0.099 * torch.rand(H, device=self.dev, generator=gen)
+                dt = 2.0 * torch.rand(H, device=self.dev, generator=gen) - 1.0
+                sp = torch.nn.functional.softplus(dt)
+                L.a_log = vec(torch.log(-torch.log(target) / sp).float(), f"{l}.a_log")
+                L.dt_bias = vec(dt.float(), f"{l}.dt_bias")
+                L.out_norm = vec(_near_one(S, gen, self.dev), f"{l}.out_norm")
+            L.w_gate = mat(s.fmt_proj, s.ff, s.hidden, name=f"{l}.w_gate").data_ptr()
+            L.w_up = mat(s.fmt_proj, s.ff, s.hidden, name=f"{l}.w_up").data_ptr()
+            L.w_down = mat(s.fmt_proj, s.hidden, s.ff, name=f"{l}.w_down").data_ptr()
+        self.embed = random_kquant(s.fmt_embed, s.vocab, s.hidden, gen, self.dev)
+        self.norm_final = _near_one(s.hidden, gen, self.dev)
+        if self.gguf is not None:
+            self.gguf["embed"] = self.embed.cpu().numpy()
+            self.gguf["norm_final"] = self.norm_final.cpu().numpy()
+        self.lm_head = mat(s.fmt_lm, s.vocab, s.hidden, name="lm_head")
+        self.weights = HybridWeights(embed=self.embed.data_ptr(), layers=self.layers,
+                                     norm_final=self.norm_final.data_ptr(), lm_head=self.lm_head.data_ptr())
+        # state: recurrent N(0, 0.1), conv window N(0, 1), history packets random with
+        # sane block scales, positions = ctx
+        nbytes = self.lib.rta_hybrid_state_bytes(ctypes.byref(s), batch)
+        assert nbytes > 0, "invalid hybrid shape"
+        self.state = torch.empty(nbytes, dtype=torch.uint8, device=self.dev)
+        v = HybridViews()
+        check(self.lib.rta_hybrid_layout(ctypes.byref(s), batch, self.state.data_ptr(), ctypes.byref(v)),
+              "rta_hybrid_layout")
+        self.views = v
+        nrec = s.layers - (s.layers // s.full_every if s.full_every else 0)
+        nfull = s.layers - nrec
+        off = lambda p: p - self.state.data_ptr()
+        st = self.state
+        if nrec:
+            rec = st[off(v.recurrent):off(v.recurrent) + 4 * nrec * v.recurrent_per_layer].view(torch.float32)
+            rec.normal_(0.0, 0.1, generator=gen)
+            conv = st[off(v.conv):off(v.conv) + 4 * nrec * v.conv_per_layer].view(torch.float32)
+            conv.normal_(0.0, 1.0, generator=gen)
+        if nfull:
+            pk = st[off(v.packets):off(v.packets) + nfull * v.slots_per_layer * v.packet_bytes]
+            self._random_packets(pk.view(-1, v.packet_bytes), gen)
+        self.ctx = torch.as_tensor(ctx, dtype=torch.int32, device=self.dev)
+        check(self.lib.rta_hybrid_init(ctypes.byref(s), batch, self.state.data_ptr(), self.ctx.data_ptr(),
+                                       ops._stream()), "rta_hybrid_init")
+        self.ws_bytes = self.lib.rta_hybrid_workspace_bytes(ctypes.byref(s), batch)
+        self.workspace = torch.empty(self.ws_bytes, dtype=torch.uint8, device=self.dev)
+        self.tokens = torch.randint(0, s.vocab, (batch,), dtype=torch.int32, device=self.dev, generator=gen)
+        self.logits = None
+
+    def _random_packets(self, pk, gen):
+        """K (Q4_K) / V (Q6_K) history fields with random quants and sane block scales."""
+        s = self.shape
+        kvw = s.kv_heads * s.head_dim
+        nb = (kvw + 255) // 256
+        pk.random_(0, 256, generator=gen)
+        n = pk.shape[0]
+        half = lambda: (torch.rand(n, device=self.dev, generator=gen) * 0.01 + 1e-3).to(torch.float16).view(
+            torch.uint8).view(n, 2)
+        koff, kb = 0, (144 if s.fmt_k == Q4_K else 210)
+        voff, vb = nb * kb, (144 if s.fmt_v == Q4_K else 210)
+        for fld_off, bb, fmt in ((koff, kb, s.fmt_k), (voff, vb, s.fmt_v)):
+            for b in range(nb):
+                o = fld_off + b * bb
+                if fmt == Q4_K:
+                    pk[:, o:o + 2] = half()
+                    pk[:, o + 2:o + 4] = half()
+                else:
+                    pk[:, o + 192:o + 208] = torch.randint(-32, 32, (n, 16), dtype=torch.int8, device=self.dev,
+                                                           generator=gen).view(torch.uint8)
+                    pk[:, o + 208:o + 210] = half()
+        pk[:, nb * (kb + vb):] = 0   # the packet's padding to 8 bytes
+
+    def step(self, logits=False):
+        """One greedy decode step for every sequence (tokens and positions advance on the device)."""
+        if logits and self.logits is None:
+            self.logits = torch.empty(self.batch, self.shape.vocab, dtype=torch.float32, device=self.dev)
+        check(self.lib.rta_hybrid_decode_step(ctypes.byref(self.shape), ctypes.byref(self.weights), self.batch,
+                                              self.state.data_ptr(), self.tokens.data_ptr(),
+                                              self.logits.data_ptr() if logits else None,
+                                              self.workspace.data_ptr(), self.ws_bytes, ops._stream()),
+              "rta_hybrid_decode_step")
+        return self.tokens
+
+    def weight_bytes(self):
+        """HBM bytes of the weights one step streams (embedding rows excluded)."""
+        return sum(t.numel() * t.element_size() for t in self._keep)
+
+    def state_view(self, kind):
+        """numpy copy of one part of the state: 'recurrent' [nrec, B, H, hd, hd], 'conv'
+        [nrec, B, 3S, 3], 'packets' [nfull, B, capacity, packet_bytes], 'ctx' [B]."""
+        import numpy as np
+        s, v = self.shape, self.views
+        nfull = s.layers // s.full_every if s.full_every else 0
+        nrec = s.layers - nfull
+        off = lambda p: p - self.state.data_ptr()
+        raw = self.state.cpu().numpy()
+        B, hd, S = self.batch, s.head_dim, s.rec_heads * s.head_dim
+        if kind == "recurrent":
+            n = nrec * v.recurrent_per_layer * 4
+            return raw[off(v.recurrent):off(v.recurrent) + n].view(np.float32).reshape(nrec, B, s.rec_heads, hd, hd)
+        if kind == "conv":
+            n = nrec * v.conv_per_layer * 4
+            return raw[off(v.conv):off(v.conv) + n].view(np.float32).reshape(nrec, B, 3 * S, 3)
+        if kind == "packets":
+            n = nfull * v.slots_per_layer * v.packet_bytes
+            return raw[off(v.packets):off(v.packets) + n].reshape(nfull, B, s.capacity, v.packet_bytes)
+        if kind == "ctx":
+            return raw[off(v.ctx):off(v.ctx) + 4 * B].view(np.int32).copy()
+        raise ValueError(kind)
