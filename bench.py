@@ -9,6 +9,8 @@ Workloads (one JSON line per run):
   attention   GQA decode attention, 16 sequences, contexts log-uniform in [512, 32768],
               16 q / 4 kv heads, hd 128, K Q6_K / V Q4_K history, RoPE theta 1e6 on q
   proj        one projection --rows x --cols in --fmt q4k|q6k for --batch rows
+  decode      9B-shape hybrid decode step (24 delta-net + 8 attention layers), --batch sequences
+              (default 32), tokens/s
   copy_calib  plain device-to-device copy of known size (PMC byte-counter calibration)
 
 A step is one pass of the hot path over one batch of synthetic input resident in
@@ -42,10 +44,10 @@ Q4_K, Q6_K = 12, 14
 def parse():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=1000)
-    ap.add_argument("--warmup", type=int, default=100)
+    ap.add_argument("--steps", type=int, default=None, help="timed steps (default 64 for decode, else 1000)")
+    ap.add_argument("--warmup", type=int, default=None, help="untimed steps (default 4 for decode, else 100)")
     ap.add_argument("--workload", default="gemv_q4k",
-                    choices=["gemv_q4k", "mlp", "lm_head", "attention", "proj", "copy_calib"])
+                    choices=["gemv_q4k", "mlp", "lm_head", "attention", "proj", "decode", "copy_calib"])
     ap.add_argument("--batch", type=int, default=None)
     ap.add_argument("--rows", type=int, default=12288, help="proj workload: output rows")
     ap.add_argument("--cols", type=int, default=4096, help="proj workload: input columns")
@@ -135,6 +137,27 @@ def timed_region(torch, step, steps, warmup, eager=False):
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     g.replay()
+    torch.cuda.synchronize()
+    return (time.perf_counter() - t0) * 1e3
+
+
+def timed_replays(torch, step, steps, warmup):
+    """One step captured in a graph and replayed `steps` times; returns wall ms of all replays."""
+    for i in range(warmup):
+        step(i)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        with torch.cuda.graph(g, stream=s):
+            step(0)
+    torch.cuda.synchronize()
+    g.replay()                      # graph warm-up (not timed)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        g.replay()
     torch.cuda.synchronize()
     return (time.perf_counter() - t0) * 1e3
 
@@ -416,6 +439,74 @@ def w_proj(torch, args, orc):
     return res
 
 
+def w_decode(torch, args, orc):
+    """The 9B-shape hybrid decode step: 32 layers (3 gated delta-net : 1 full attention),
+    hidden 4096, 32/8 heads x 128, 32 delta-net heads, FF 12288, Q4_K projections (packed
+    tiles), Q6_K LM head 151936 x 4096; a batch of sequences with contexts U[256, 8192]."""
+    from rta import model, ops
+    batch = args.batch or 32
+    dev = torch.device("cuda:0")
+    rng = np.random.default_rng(20261110 + 5)
+    ctx = rng.integers(256, 8193, batch).astype(np.int32)
+    capacity = 8192 + 256
+    shape = model.shape_9b(capacity, packed=True)
+    m = model.DecodeModel(shape, batch, ctx, seed=20261115)
+    gates = [m.mats[f"{l}.w_gate"] for l in range(shape.layers)]        # 32 x 28.3 MB: streams from HBM
+    x = torch.randn(batch, shape.hidden, device=dev)
+    y = torch.empty(batch, shape.ff, device=dev)
+    gws = torch.empty(max(1, ops.gemv_workspace_bytes(Q4_K | ops.TILED, shape.ff, shape.hidden, batch)),
+                      dtype=torch.uint8, device=dev)
+
+    def step(i):
+        m.step()
+
+    def gate_proj(i):   # the dominant kernel: one 12288 x 4096 Q4_K projection of the batch
+        ops.gemv(Q4_K | ops.TILED, gates[i % len(gates)], shape.ff, shape.hidden, x, y=y, workspace=gws)
+
+    nfull = shape.layers // shape.full_every
+    nrec = shape.layers - nfull
+    w_bytes = m.weight_bytes() - m.lm_head.numel()                       # projections + small vectors
+    hist = int(sum(min(int(c), capacity) for c in ctx)) * nfull * 1416    # history read per step (approx.)
+    state = 2 * nrec * batch * shape.rec_heads * 128 * 128 * 4          # recurrent state read + write
+    step_bytes = w_bytes + m.lm_head.numel() + hist + state
+    alg_k = gates[0].numel() + batch * 4 * (shape.hidden + shape.ff)
+    res = {"alg_bytes": step_bytes, "alg_bytes_kernel": alg_k, "graph_per_step": True,
+           "kernel": "gemm_tiled_kernel<Q4_K> (12288x4096 gate projection, packed tiles)", "step": step,
+           "kernel_launch": gate_proj, "unit": "tok/s", "value_from_ms": lambda ms: batch / (ms * 1e-3),
+           "dtype": "q4_k/q6_k weights x fp32 activations and state, fp32 accumulate",
+           "config": {"workload": f"9B-shape hybrid decode step, batch {batch} (32 layers: 24 gated delta-net + 8 "
+                                  "full attention; hidden 4096, 32/8 heads x 128, FF 12288, Q4_K projections, "
+                                  "Q6_K LM head 151936x4096; contexts U[256, 8192], greedy)",
+                      "batch": batch, "layers": 32, "hidden": 4096, "ff": 12288, "vocab": 151936,
+                      "sum_context": int(ctx.sum()), "history_capacity": capacity,
+                      "bytes_per_step": int(step_bytes), "weight_bytes_per_step": int(w_bytes + m.lm_head.numel()),
+                      "seed": "20261110+5"}}
+
+    def check():
+        m.step(logits=True)
+        lg = m.logits.cpu().numpy()
+        toks = m.tokens.cpu().numpy().view(np.uint32)
+        ok = bool(np.isfinite(lg).all()) and all(int(toks[b]) == orc.argmax_margin_f32(lg[b], 1e-4)
+                                                 for b in range(batch))
+        return {"tokens_follow_margin_rule": ok, "logits_finite": bool(np.isfinite(lg).all()), "ok": ok,
+                "note": "end-to-end step parity vs the fp64 oracle: tests/test_gpu_model.py (small shape)"}
+
+    def cpu(seconds):
+        from rta import synth
+        t = omp_threads()
+        rows = 1024
+        wq = synth.random_matrix(np.random.default_rng(3), Q4_K, rows, 4096)
+        xs = np.random.default_rng(4).standard_normal((batch, 4096)).astype(np.float32)
+        n, el = cpu_time(lambda: orc.gemv_f32(Q4_K, wq, rows, 4096, xs, t), seconds)
+        gbs = wq.nbytes * n / el / 1e9
+        return {"value": batch / (step_bytes / (gbs * 1e9)), "unit": "tok/s", "cores": t, "kind": "port",
+                "sample": f"{n} calls of the oracle's fp32 OpenMP Q4_K projection {rows}x4096 at batch {batch} "
+                          f"({gbs:.2f} GB/s of weights) in {el:.1f} s on {cpu_model()}, scaled to the step's "
+                          f"{step_bytes / 1e9:.2f} GB"}
+    res["check"], res["cpu"] = check, cpu
+    return res
+
+
 def w_copy_calib(torch, args, orc):
     dev = torch.device("cuda:0")
     n = 64 << 20
@@ -433,7 +524,7 @@ def w_copy_calib(torch, args, orc):
 
 
 WORKLOADS = {"gemv_q4k": w_gemv_q4k, "mlp": w_mlp, "lm_head": w_lm_head, "attention": w_attention,
-             "proj": w_proj, "copy_calib": w_copy_calib}
+             "proj": w_proj, "decode": w_decode, "copy_calib": w_copy_calib}
 
 
 def main():
@@ -447,10 +538,17 @@ def main():
     _lib.load()
     sys.path.insert(0, str(ROOT / "oracle"))
     import oracle as orc
+    if args.steps is None:
+        args.steps = 64 if args.workload == "decode" else 1000
+    if args.warmup is None:
+        args.warmup = 4 if args.workload == "decode" else 100
     wl = WORKLOADS[args.workload](torch, args, orc)
     parity = wl["check"]()
     k_mean = time_kernel(torch, wl["kernel_launch"])
-    ms = timed_region(torch, wl["step"], args.steps, args.warmup, args.eager)
+    if wl.get("graph_per_step") and not args.eager:
+        ms = timed_replays(torch, wl["step"], args.steps, args.warmup)
+    else:
+        ms = timed_region(torch, wl["step"], args.steps, args.warmup, args.eager)
     ms_step = ms / args.steps
     alg_k = wl.get("alg_bytes_kernel", wl["alg_bytes"])
     achieved = alg_k / (k_mean * 1e-3) / 1e9
@@ -458,7 +556,9 @@ def main():
     line = {"metric": METRIC, "value": wl["value_from_ms"](ms_step), "unit": wl["unit"], "n_gpus": 1,
             "steps": args.steps, "warmup": args.warmup, "ms_per_step": ms_step, "higher_is_better": True,
             "scaling": "weak", "vs_baseline": None, "dtype": wl["dtype"], "data": "synthetic",
-            "timing": "eager launches" if args.eager else "one HIP graph replay of all steps",
+            "timing": "eager launches" if args.eager else ("one HIP graph of a step, replayed per step"
+                                                            if wl.get("graph_per_step") else
+                                                            "one HIP graph replay of all steps"),
             "config": wl["config"],
             "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
                          "frac": achieved / HBM_PEAK_GBS, "traffic": traffic_for(args.workload)},

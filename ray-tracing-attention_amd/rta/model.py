@@ -102,6 +102,7 @@ class DecodeModel:
         s = shape
         self._keep = []
         self.gguf = {} if keep_gguf else None   # name -> GGUF matrix (tests feed these to the oracle)
+        self.mats = {}                            # name -> device matrix as the step reads it
         base_fmt = lambda f: f & 0xff
 
         def mat(fmt, rows, cols, d_scale=0.01, small_rows=0, name=None):
@@ -121,6 +122,8 @@ class DecodeModel:
             if fmt & TILED:
                 w = ops.pack(base_fmt(fmt), w, rows, cols)
             self._keep.append(w)
+            if name:
+                self.mats[name] = w
             return w
 
         def vec(t, name=None):
