@@ -141,7 +141,8 @@ int64_t rta_history_bytes(int kvw);
 /* Decode attention over quantised K/V history, one query token per sequence.
  *   q         [nseq, hq, hd] fp32, already rotated
  *   packets   history packets (stride rta_history_bytes(hkv*hd), 4-byte aligned);
- *             field K first (format fmt_k), then field V (fmt_v); Q4_K or Q6_K each.
+ *             field K first (format fmt_k), then field V (fmt_v); Q4_K or Q6_K each,
+ *             not both Q6_K (two Q6_K fields do not fit the packet size).
  *             The reference layout is fmt_k = Q4_K, fmt_v = Q6_K
  *             (resident_quant.glsl:123-124).
  *   slot_base [nseq] int64, ctx_len [nseq] int32 (device): sequence s holds

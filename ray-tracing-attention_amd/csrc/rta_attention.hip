@@ -5,17 +5,24 @@
 // resident_detector_ordered_*.comp) walks every visible history slot -- its ray
 // query returns all of them and checks the count (resident_ray.comp:30-53,80).
 // Here the visible slots are enumerated in closed form, slot = base + p % capacity
-// for p in [t+1-visible, t], and cut into 256-position chunks.  One workgroup
-// handles one (sequence, kv head, chunk):
-//   pass A  one lane per position: decode the position's K half-superblock once
-//           and score it against the G query heads sharing that kv head (GQA);
-//           chunk maximum m and Z = sum exp(s - m) per head.
-//   pass B  eight position groups x 32 lanes of 4 coordinates: decode V once and
-//           accumulate U[g] += w * V for all G heads; reduce the groups in LDS.
-// A merge kernel combines the per-chunk (m, Z, U) records,
-//   M = max m_c, Z = sum Z_c e^(m_c-M), o = sum U_c e^(m_c-M) / Z,
-// which is the receipt merge of the grouped backends
-// (resident_attention_runtime.inl:618-645).
+// for p in [t+1-visible, t], and cut into chunks of nt tiles of 64 positions.
+// One workgroup (4 waves) owns one (sequence, chunk) and every head of it, so each
+// history packet is read from HBM by exactly one workgroup.  Per tile:
+//   phase A  lane = position.  Each wave scores the K half-superblocks of its kv
+//            heads against the G query heads sharing them (GQA); q stays uniform,
+//            so the compiler keeps it in SGPRs and every code costs one
+//            v_fma_mix_f32 per head.  In the same pass the lanes copy their
+//            position's V superblocks into LDS (dword aligned), so the V loads are
+//            in flight while the K arithmetic runs.
+//   softmax  per head over the tile, folded into running (m, Z) with the online
+//            rescale exp(m_old - m_new).
+//   phase B  thread = (kv head, 16 or 8 coordinates, position group): V codes
+//            from LDS, one v_fma_mix_f32 per code and head; the per-position
+//            factor w * d * sc is applied once per sub-block run, and the Q4_K
+//            minimum / Q6_K -32 offset is accumulated separately.
+// Each chunk writes one (m, Z, U[128]) record per head; a merge kernel combines
+// them:  M = max m_c, Z = sum Z_c e^(m_c-M), o = sum U_c e^(m_c-M) / Z, which is the
+// receipt merge of the grouped backends (resident_attention_runtime.inl:618-645).
 #include <math.h>
 
 #include "rta_common.hpp"
@@ -23,9 +30,10 @@
 
 namespace rta {
 
-constexpr int kHd = 128;     // head dimension supported by these kernels
-constexpr int kChunk = 256;  // positions per workgroup (the reference's tile, ordered_scores.comp:17)
-constexpr int kRec = 2 + kHd; // per-head record: m, Z, U[128]
+constexpr int kHd = 128;       // head dimension supported by these kernels
+constexpr int kTile = 64;      // positions per tile: one per lane in phase A
+constexpr int kRec = 2 + kHd;  // per-head record: m, Z, U[128]
+constexpr int kMaxLds = 160 * 1024;
 
 struct AttnArgs {
     const float* q;
@@ -42,307 +50,490 @@ struct AttnArgs {
     int64_t stride;     // packet bytes
     int64_t v_offset;   // byte offset of the V field inside a packet
     int nseq, hq, hkv, nchunk;
+    int nt;             // tiles per chunk
+    int nblk;           // superblocks per field: ceil(hkv / 2)
 };
 
-__device__ __forceinline__ uint32_t ld32(const uint8_t* p) { return *reinterpret_cast<const uint32_t*>(p); }
+template <int FMT> struct Fmt;
+template <> struct Fmt<RTA_Q4_K> { static constexpr int kBytes = 144, kRow = 37; };  // LDS row: 36 dwords + pad
+template <> struct Fmt<RTA_Q6_K> { static constexpr int kBytes = 210, kRow = 53; };  // 52.5 dwords
 
-// Dword that starts at the 2-byte aligned address p (reads [floor4(p), floor4(p)+8)).
-__device__ __forceinline__ uint32_t ld32_u2(const uint8_t* p) {
-    const uint32_t mis = (uint32_t)(reinterpret_cast<uintptr_t>(p) & 3u);
-    const uint32_t* w = reinterpret_cast<const uint32_t*>(p - mis);   // keeps the address space
-    return mis ? funnel(w[0], w[1], mis) : w[0];
-}
+// LDS carve-up of the chunk kernel (dynamic shared memory), in floats.
+struct AttnLds {
+    int sc, w, qs, m, z, scale, ok, v, total;
+    __host__ __device__ AttnLds(int hq, int nblk, int vrow) {
+        sc = 0;                       // [hq][64] scores of the tile   } reused after the tiles
+        w = sc + hq * kTile;          // [64][hq] weights x 2^24       } as U[hq][128]
+        qs = w + hq * kTile;          // [hq][8] 16-dim sums of q
+        m = qs + hq * 8;              // [hq] running max
+        z = m + hq;                   // [hq] running sum
+        scale = z + hq;               // [hq] rescale of this tile
+        ok = scale + hq;              // [64] position valid (int)
+        v = (ok + kTile + 3) & ~3;    // [nblk][64][vrow] V superblocks, dword aligned
+        total = v + nblk * kTile * vrow;
+    }
+};
 
-// ---- pass A: K scores ------------------------------------------------------
-// Q4_K key half-superblock (head hh of the block): groups 4hh..4hh+3.
+// ---- phase A: K scores --------------------------------------------------------
+// Q4_K key, head half hh of the superblock at blk (4-byte aligned).  Dims of the head:
+// chunk jc (bytes 16 + 32(2hh+jc) ..), dword t: low nibbles are dims 64jc + 4t + b,
+// high nibbles 64jc + 32 + 4t + b (resident_quant.glsl:10-15).
 template <int G>
-__device__ __forceinline__ void score_q4k(const uint8_t* blk, int hh, const float* __restrict__ qg,
-                                          const float qs32[G][4], float score[G]) {
-    const uint32_t h0 = ld32(blk), s0 = ld32(blk + 4), s1 = ld32(blk + 8), s2 = ld32(blk + 12);
-    const float d = half_lo(h0), dmin = half_hi(h0);
+__device__ __forceinline__ void score_q4k(const uint8_t* __restrict__ blk, int hh, const float* __restrict__ qg,
+                                          const float* qs, float score[G]) {
+    const uint32_t* bw = reinterpret_cast<const uint32_t*>(blk);
+    uint32_t hdr[4], w[16];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) hdr[i] = bw[i];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) w[i] = bw[4 + 16 * hh + i];
+    const float d = half_lo(hdr[0]), dmin = half_hi(hdr[0]);
 #pragma unroll
     for (int g = 0; g < G; ++g) score[g] = 0.0f;
 #pragma unroll
-    for (int u = 0; u < 2; ++u) {
-        const int jj = 2 * hh + u;
-        const uint8_t* qsb = blk + 16 + 32 * jj;
+    for (int jc = 0; jc < 2; ++jc) {
         float alo[G], ahi[G];
 #pragma unroll
         for (int g = 0; g < G; ++g) alo[g] = ahi[g] = 0.0f;
 #pragma unroll
         for (int t = 0; t < 8; ++t) {
-            const uint32_t w = ld32(qsb + 4 * t), v = w >> 8;
-            const half2_t p0 = as_codes(w & 0x000F000Fu), p1 = as_codes(v & 0x000F000Fu);
-            const half2_t c0 = as_codes(w & 0x00F000F0u), c1 = as_codes(v & 0x00F000F0u);
+            const uint32_t x = w[8 * jc + t], v = x >> 8;
+            const half2_t p0 = as_codes(x & 0x000F000Fu), p1 = as_codes(v & 0x000F000Fu);
+            const half2_t h0 = as_codes(x & 0x00F000F0u), h1 = as_codes(v & 0x00F000F0u);
 #pragma unroll
             for (int g = 0; g < G; ++g) {
-                const float* qa = qg + g * kHd + 64 * u + 4 * t;
-                alo[g] = fmaf((float)p0.x, qa[0], alo[g]);
-                alo[g] = fmaf((float)p1.x, qa[1], alo[g]);
-                alo[g] = fmaf((float)p0.y, qa[2], alo[g]);
-                alo[g] = fmaf((float)p1.y, qa[3], alo[g]);
-                ahi[g] = fmaf((float)c0.x, qa[32], ahi[g]);
-                ahi[g] = fmaf((float)c1.x, qa[33], ahi[g]);
-                ahi[g] = fmaf((float)c0.y, qa[34], ahi[g]);
-                ahi[g] = fmaf((float)c1.y, qa[35], ahi[g]);
+                const float* qa = qg + g * kHd + 64 * jc + 4 * t;
+                float a = alo[g], b = ahi[g];
+                a = fmaf((float)p0.x, qa[0], a);
+                a = fmaf((float)p1.x, qa[1], a);
+                a = fmaf((float)p0.y, qa[2], a);
+                a = fmaf((float)p1.y, qa[3], a);
+                b = fmaf((float)h0.x, qa[32], b);
+                b = fmaf((float)h1.x, qa[33], b);
+                b = fmaf((float)h0.y, qa[34], b);
+                b = fmaf((float)h1.y, qa[35], b);
+                alo[g] = a;
+                ahi[g] = b;
             }
         }
+        const int jj = 2 * hh + jc;
         uint32_t sc0, m0, sc1, m1;
-        q4k_scale_min(s0, s1, s2, 2 * jj, sc0, m0);
-        q4k_scale_min(s0, s1, s2, 2 * jj + 1, sc1, m1);
+        q4k_scale_min(hdr[1], hdr[2], hdr[3], 2 * jj, sc0, m0);
+        q4k_scale_min(hdr[1], hdr[2], hdr[3], 2 * jj + 1, sc1, m1);
+        // low-nibble codes carry 2^-24, high-nibble codes 2^-20
         const float D0 = d * (float)sc0 * 16777216.0f, D1 = d * (float)sc1 * 1048576.0f;
         const float M0 = dmin * (float)m0, M1 = dmin * (float)m1;
 #pragma unroll
         for (int g = 0; g < G; ++g) {
+            const float* qsg = qs + g * 8 + 4 * jc;
             float v2 = fmaf(D0, alo[g], score[g]);
-            v2 = fmaf(-M0, qs32[g][2 * u], v2);
+            v2 = fmaf(-M0, qsg[0] + qsg[1], v2);
             v2 = fmaf(D1, ahi[g], v2);
-            score[g] = fmaf(-M1, qs32[g][2 * u + 1], v2);
+            score[g] = fmaf(-M1, qsg[2] + qsg[3], v2);
         }
     }
 }
 
-// Q6_K key half-superblock: dims l = 4t + 32k + e use ql byte 64hh + (l%64)
-// (nibble l/64), qh byte 128 + 32hh + l%32 (bits 2(l/32)), scale 8hh + l/16.
+// Q6_K key, head half hh of the superblock at blk (2-byte aligned).  Reads stay
+// inside the 210-byte block: dwords from the 4-byte aligned address below, joined
+// with alignbyte.  16-byte run c of ql (bytes 64hh + 16c ..) holds dims 16c + i in
+// its low nibbles and 64 + 16c + i in its high nibbles; their two top bits come
+// from qh bytes 128 + 32hh + 16(c & 1) + i at bit 2(c >> 1) and 2(2 + (c >> 1))
+// (resident_quant.glsl:16-19).
 template <int G>
-__device__ __forceinline__ void score_q6k(const uint8_t* blk, int hh, const float* __restrict__ qg,
-                                          const float qs16[G][8], float score[G]) {
+__device__ __forceinline__ void score_q6k(const uint8_t* __restrict__ blk, int hh, const float* __restrict__ qg,
+                                          const float* qs, float score[G]) {
+    const uint32_t mis = (uint32_t)(reinterpret_cast<uintptr_t>(blk) & 3u);
+    const uint32_t* a = reinterpret_cast<const uint32_t*>(blk - mis);
+    uint32_t ql[17], qh[9];
+#pragma unroll
+    for (int i = 0; i < 17; ++i) ql[i] = a[16 * hh + i];
+#pragma unroll
+    for (int i = 0; i < 9; ++i) qh[i] = a[32 + 8 * hh + i];
+    const uint32_t s0 = a[48 + 2 * hh], s1 = a[49 + 2 * hh];
+    const uint32_t s2 = mis ? a[50 + 2 * hh] : s1;   // the third dword only exists when misaligned
+    const uint32_t sc_lo = funnel(s0, s1, mis), sc_hi = funnel(s1, s2, mis);
     const float d = (float)__builtin_bit_cast(_Float16, *reinterpret_cast<const uint16_t*>(blk + 208));
-    const uint32_t sc_lo = ld32_u2(blk + 192 + 8 * hh), sc_hi = ld32_u2(blk + 196 + 8 * hh);
-    float acc[G][8];
 #pragma unroll
-    for (int g = 0; g < G; ++g)
+    for (int g = 0; g < G; ++g) score[g] = 0.0f;
 #pragma unroll
-        for (int i = 0; i < 8; ++i) acc[g][i] = 0.0f;
+    for (int c = 0; c < 4; ++c) {
+        float alo[G], ahi[G];
 #pragma unroll
-    for (int t = 0; t < 8; ++t) {
-        const uint32_t a = ld32_u2(blk + 64 * hh + 4 * t), b = ld32_u2(blk + 64 * hh + 32 + 4 * t);
-        const uint32_t h = ld32_u2(blk + 128 + 32 * hh + 4 * t);
-        uint32_t c[4];
-        c[0] = (a & 0x0F0F0F0Fu) | ((h << 4) & 0x30303030u);
-        c[1] = (b & 0x0F0F0F0Fu) | ((h << 2) & 0x30303030u);
-        c[2] = ((a >> 4) & 0x0F0F0F0Fu) | (h & 0x30303030u);
-        c[3] = ((b >> 4) & 0x0F0F0F0Fu) | ((h >> 2) & 0x30303030u);
+        for (int g = 0; g < G; ++g) alo[g] = ahi[g] = 0.0f;
+        const uint32_t shl = 2u * (uint32_t)(c >> 1), shh = shl + 4u;
 #pragma unroll
-        for (int k = 0; k < 4; ++k) {
-            const half2_t p = as_codes(c[k] & 0x00FF00FFu), r = as_codes((c[k] >> 8) & 0x00FF00FFu);
-            const int grp = 2 * k + (t >> 2);
+        for (int t = 0; t < 4; ++t) {
+            const uint32_t A = funnel(ql[4 * c + t], ql[4 * c + t + 1], mis);
+            const uint32_t H = funnel(qh[4 * (c & 1) + t], qh[4 * (c & 1) + t + 1], mis);
+            const uint32_t lo = (A & 0x0F0F0F0Fu) | (((H >> shl) & 0x03030303u) << 4);
+            const uint32_t hi = ((A >> 4) & 0x0F0F0F0Fu) | (((H >> shh) & 0x03030303u) << 4);
+            const half2_t l0 = as_codes(lo & 0x00FF00FFu), l1 = as_codes((lo >> 8) & 0x00FF00FFu);
+            const half2_t h0 = as_codes(hi & 0x00FF00FFu), h1 = as_codes((hi >> 8) & 0x00FF00FFu);
 #pragma unroll
             for (int g = 0; g < G; ++g) {
-                const float* qa = qg + g * kHd + 32 * k + 4 * t;
-                float v = acc[g][grp];
-                v = fmaf((float)p.x, qa[0], v);
-                v = fmaf((float)r.x, qa[1], v);
-                v = fmaf((float)p.y, qa[2], v);
-                v = fmaf((float)r.y, qa[3], v);
-                acc[g][grp] = v;
+                const float* qa = qg + g * kHd + 16 * c + 4 * t;
+                float x = alo[g], y = ahi[g];
+                x = fmaf((float)l0.x, qa[0], x);
+                x = fmaf((float)l1.x, qa[1], x);
+                x = fmaf((float)l0.y, qa[2], x);
+                x = fmaf((float)l1.y, qa[3], x);
+                y = fmaf((float)h0.x, qa[64], y);
+                y = fmaf((float)h1.x, qa[65], y);
+                y = fmaf((float)h0.y, qa[66], y);
+                y = fmaf((float)h1.y, qa[67], y);
+                alo[g] = x;
+                ahi[g] = y;
             }
         }
-    }
+        // sub-block scales c (low run) and 4 + c (high run) of this half
+        const float Dl = d * (float)(int8_t)((sc_lo >> (8 * c)) & 255u);
+        const float Dh = d * (float)(int8_t)((sc_hi >> (8 * c)) & 255u);
 #pragma unroll
-    for (int g = 0; g < G; ++g) {
-        float s = 0.0f;
-#pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            const uint32_t sb = ((i < 4 ? sc_lo : sc_hi) >> (8 * (i & 3))) & 255u;
-            const float D = d * (float)(int8_t)sb;
-            s = fmaf(D, fmaf(acc[g][i], 16777216.0f, -32.0f * qs16[g][i]), s);
+        for (int g = 0; g < G; ++g) {
+            // sum (c - 32) q = sum c q - 32 sum q ; codes carry 2^-24
+            float v = fmaf(Dl, fmaf(alo[g], 16777216.0f, -32.0f * qs[g * 8 + c]), score[g]);
+            score[g] = fmaf(Dh, fmaf(ahi[g], 16777216.0f, -32.0f * qs[g * 8 + 4 + c]), v);
         }
-        score[g] = s;
     }
 }
 
-// ---- pass B: V values for coordinates 4e..4e+3 of the head half -------------
-__device__ __forceinline__ void values_q4k(const uint8_t* blk, int hh, int e, float v[4]) {
-    const uint32_t h0 = ld32(blk);
-    const int l = 4 * e, jj = 2 * hh + (l >> 6), hi = (l & 63) >> 5, g = 2 * jj + hi;
-    uint32_t sc, m;
-    q4k_scale_min(ld32(blk + 4), ld32(blk + 8), ld32(blk + 12), g, sc, m);
-    const uint32_t w = ld32(blk + 16 + 32 * jj + (l & 31));
-    const float D = half_lo(h0) * (float)sc, M = half_hi(h0) * (float)m;
+// Copies the V superblock at blk (2-byte aligned, `bytes` long) into an LDS row whose
+// dword i holds block bytes 4i..4i+3.  Reads stay inside [blk, blk + bytes).
+template <int FMT>
+struct VStage {
+    static constexpr int kRaw = (Fmt<FMT>::kBytes + 2 + 3) / 4;   // dwords covering a misaligned block
+    uint32_t raw[kRaw];
+    uint32_t mis;
+    __device__ __forceinline__ void load(const uint8_t* __restrict__ blk) {
+        constexpr int kB = Fmt<FMT>::kBytes;
+        mis = (uint32_t)(reinterpret_cast<uintptr_t>(blk) & 3u);   // 0 or 2
+        const uint32_t* a = reinterpret_cast<const uint32_t*>(blk - mis);
+        const uint32_t tail = (uint32_t)*reinterpret_cast<const uint16_t*>(blk + kB - 2);
+        // (kB + mis) / 4 whole dwords, then the last 2 bytes when (kB + mis) % 4 == 2
 #pragma unroll
-    for (int i = 0; i < 4; ++i) v[i] = fmaf(D, (float)((w >> (8 * i + 4 * hi)) & 15u), -M);
-}
+        for (int i = 0; i < kRaw - 1; ++i) raw[i] = a[i];
+        if constexpr (FMT == RTA_Q4_K) {   // 36 dwords aligned; 36 + 2 bytes misaligned
+            raw[kRaw - 1] = mis ? tail : 0u;
+        } else {                           // 52 + 2 bytes aligned; 53 dwords misaligned
+            if (mis) raw[kRaw - 1] = a[kRaw - 1];
+            else raw[kRaw - 1] = tail;
+        }
+    }
+    __device__ __forceinline__ void store(uint32_t* row) const {
+        constexpr int kOut = (Fmt<FMT>::kBytes + 3) / 4;
+#pragma unroll
+        for (int i = 0; i < kOut; ++i) row[i] = funnel(raw[i], i + 1 < kRaw ? raw[i + 1] : 0u, mis);
+    }
+};
 
-__device__ __forceinline__ void values_q6k(const uint8_t* blk, int hh, int e, float v[4]) {
-    const int l = 4 * e;
-    const uint32_t a = ld32_u2(blk + 64 * hh + (l & 63));
-    const uint32_t h = ld32_u2(blk + 128 + 32 * hh + (l & 31));
-    const uint32_t sh = 8u * (uint32_t)((l >> 4) & 1);
-    const uint32_t sb = ((uint32_t)*reinterpret_cast<const uint16_t*>(blk + 192 + 8 * hh + ((l >> 4) & ~1)) >> sh) & 255u;
-    const float d = (float)__builtin_bit_cast(_Float16, *reinterpret_cast<const uint16_t*>(blk + 208));
-    const float D = d * (float)(int8_t)sb;
-    const uint32_t nib = (a >> (4 * (l >> 6))) & 0x0F0F0F0Fu;
-    const uint32_t top = ((h >> (2 * (l >> 5))) & 0x03030303u) << 4;
-    const uint32_t c = nib | top;
+// ---- phase B: V accumulation from an LDS row -----------------------------------
+// Dims l0 .. l0 + DPT - 1 of head half hh, all inside one sub-block.  Returns the
+// codes as DPT/4 dwords of bytes, and the sub-block factors: value = D * code - M.
+template <int FMT, int DPT>
+__device__ __forceinline__ void v_codes(const uint32_t* row, int hh, int l0, uint32_t c[DPT / 4], float& D,
+                                        float& M) {
+    if constexpr (FMT == RTA_Q4_K) {
+        const int jj = 2 * hh + (l0 >> 6), hi = (l0 >> 5) & 1;
+        const int base = 4 + 8 * jj + ((l0 & 31) >> 2);
 #pragma unroll
-    for (int i = 0; i < 4; ++i) v[i] = D * (float)((int)((c >> (8 * i)) & 255u) - 32);
+        for (int k = 0; k < DPT / 4; ++k) c[k] = (row[base + k] >> (4 * hi)) & 0x0F0F0F0Fu;
+        uint32_t sc, m;
+        q4k_scale_min(row[1], row[2], row[3], 2 * jj + hi, sc, m);
+        D = half_lo(row[0]) * (float)sc;
+        M = half_hi(row[0]) * (float)m;
+    } else {
+        const int bl = (64 * hh + (l0 & 63)) >> 2, bh = (128 + 32 * hh + (l0 & 31)) >> 2;
+        const uint32_t sl = 4u * (uint32_t)(l0 >> 6), sh = 2u * (uint32_t)(l0 >> 5);
+#pragma unroll
+        for (int k = 0; k < DPT / 4; ++k)
+            c[k] = ((row[bl + k] >> sl) & 0x0F0F0F0Fu) | (((row[bh + k] >> sh) & 0x03030303u) << 4);
+        const int si = 192 + 8 * hh + (l0 >> 4);
+        const int sc = (int)(int8_t)((row[si >> 2] >> (8 * (si & 3))) & 255u);
+        D = half_lo(row[52]) * (float)sc;
+        M = 0.0f;
+    }
 }
 
 template <int KF, int VF, int G>
-__global__ void __launch_bounds__(256) attn_chunk_kernel(const AttnArgs a) {
-    __shared__ float s_w[kChunk][G];          // weights exp(s - m) per position
-    __shared__ float s_red[4][G];
-    __shared__ float s_u[8][G][kHd];          // per position-group partial U
+__global__ void __launch_bounds__(256, 2) attn_chunk_kernel(const AttnArgs a) {
+    extern __shared__ __align__(16) float lds[];
+    constexpr int DPT = G == 8 ? 8 : 16;      // phase B dims per thread
+    constexpr int TPK = kHd / DPT;            // threads per kv head
+    constexpr int VROW = Fmt<VF>::kRow;
+    const AttnLds L(a.hq, a.nblk, VROW);
+    float* s_sc = lds + L.sc;
+    float* s_w = lds + L.w;
+    float* s_qs = lds + L.qs;
+    float* s_m = lds + L.m;
+    float* s_z = lds + L.z;
+    float* s_scale = lds + L.scale;
+    int* s_ok = reinterpret_cast<int*>(lds + L.ok);
+    uint32_t* s_v = reinterpret_cast<uint32_t*>(lds + L.v);
 
-    const int c = blockIdx.x, sk = blockIdx.y;
-    const int s = sk / a.hkv, kvh = sk - s * a.hkv;
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int64_t L = a.ctx_len[s];
-    const int64_t t = L - 1;
-    const int64_t visible = L < a.capacity ? L : a.capacity;
-    const int64_t first = (int64_t)c * kChunk;
+    const int c = blockIdx.x, s = blockIdx.y;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int hq = a.hq, hkv = a.hkv;
+    const int64_t Lc = a.ctx_len[s];
+    const int64_t visible = Lc < a.capacity ? Lc : a.capacity;
+    const int64_t chunk = (int64_t)a.nt * kTile;
+    const int64_t first = (int64_t)c * chunk;
     if (visible <= 0 || first >= visible) return;
-    const int n = (int)(visible - first < kChunk ? visible - first : kChunk);
-    const int64_t p0 = t + 1 - visible + first;     // oldest position of this chunk
+    const int n_all = (int)(visible - first < chunk ? visible - first : chunk);
+    const int64_t p0 = Lc - visible + first;   // oldest position of this chunk
     const int64_t base = a.slot_base[s];
-    const int hh = kvh & 1;
-    const int64_t kblk = (int64_t)(kvh >> 1) * (KF == RTA_Q4_K ? 144 : 210);
-    const int64_t vblk = a.v_offset + (int64_t)(kvh >> 1) * (VF == RTA_Q4_K ? 144 : 210);
-    const float* qg = a.q + ((int64_t)s * a.hq + (int64_t)kvh * G) * kHd;
+    const float* qs_seq = a.q + (int64_t)s * hq * kHd;
 
-    // Group sums of q used by the minimum / centring terms (uniform per wave).
-    float qs32[G][4], qs16[G][8];
-#pragma unroll
-    for (int g = 0; g < G; ++g) {
-#pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            float acc = 0.0f;
-#pragma unroll
-            for (int e = 0; e < 16; ++e) acc += qg[g * kHd + 16 * i + e];
-            qs16[g][i] = acc;
-        }
-#pragma unroll
-        for (int i = 0; i < 4; ++i) qs32[g][i] = qs16[g][2 * i] + qs16[g][2 * i + 1];
-    }
-
-    // ---- pass A
-    float score[G];
-    bool live = tid < n;
-    if (live) {
-        const int64_t slot = base + (p0 + tid) % a.capacity;
-        if (slot < 0 || slot >= a.n_slots) {
-            raise_error(RTA_DEVERR_HITS);
-            live = false;
-        }
-    }
-    if (live) {
-        const int64_t p = p0 + tid;
-        const uint8_t* pk = a.packets + (base + p % a.capacity) * a.stride;
-        if constexpr (KF == RTA_Q4_K) score_q4k<G>(pk + kblk, hh, qg, qs32, score);
-        else score_q6k<G>(pk + kblk, hh, qg, qs16, score);
-        const float inv = 1.0f / sqrtf((float)kHd);
-        bool bad = false;
-#pragma unroll
-        for (int g = 0; g < G; ++g) {
-            score[g] *= inv;
-            bad |= !isfinite(score[g]);
-        }
-        if (bad) raise_error(RTA_DEVERR_DETECTOR);
-    } else {
-#pragma unroll
-        for (int g = 0; g < G; ++g) score[g] = -INFINITY;
-    }
-    float m[G], z[G];
-#pragma unroll
-    for (int g = 0; g < G; ++g) {
-        const float v = group_max(score[g], kWave);
-        if (lane == 0) s_red[wave][g] = v;
-    }
-    __syncthreads();
-#pragma unroll
-    for (int g = 0; g < G; ++g) m[g] = fmaxf(fmaxf(s_red[0][g], s_red[1][g]), fmaxf(s_red[2][g], s_red[3][g]));
-    __syncthreads();
-#pragma unroll
-    for (int g = 0; g < G; ++g) {
-        const float w = live ? expf(score[g] - m[g]) : 0.0f;
-        s_w[tid][g] = w;
-        const float v = group_sum(w, kWave);
-        if (lane == 0) s_red[wave][g] = v;
-    }
-    __syncthreads();
-#pragma unroll
-    for (int g = 0; g < G; ++g) z[g] = (s_red[0][g] + s_red[1][g]) + (s_red[2][g] + s_red[3][g]);
-
-    // ---- pass B
-    const int grp = tid >> 5, e = tid & 31;
-    float u[G][4];
-#pragma unroll
-    for (int g = 0; g < G; ++g)
-#pragma unroll
-        for (int i = 0; i < 4; ++i) u[g][i] = 0.0f;
-    for (int j = grp; j < n; j += 8) {
-        const int64_t p = p0 + j;
-        const int64_t slot = base + p % a.capacity;
-        if (slot < 0 || slot >= a.n_slots) continue;   // flagged in pass A
-        const uint8_t* pk = a.packets + slot * a.stride;
-        float v[4];
-        if constexpr (VF == RTA_Q4_K) values_q4k(pk + vblk, hh, e, v);
-        else values_q6k(pk + vblk, hh, e, v);
-#pragma unroll
-        for (int g = 0; g < G; ++g) {
-            const float w = s_w[j][g];
-#pragma unroll
-            for (int i = 0; i < 4; ++i) u[g][i] = fmaf(w, v[i], u[g][i]);
-        }
-    }
-#pragma unroll
-    for (int g = 0; g < G; ++g)
-#pragma unroll
-        for (int i = 0; i < 4; ++i) s_u[grp][g][4 * e + i] = u[g][i];
-    __syncthreads();
-    float* rec = a.ws + ((int64_t)sk * a.nchunk + c) * G * kRec;
-    for (int idx = tid; idx < G * kHd; idx += 256) {
-        const int g = idx / kHd, dd = idx - g * kHd;
+    // prologue: 16-dim sums of q (the minimum / centring terms), running (m, Z)
+    for (int i = tid; i < hq * 8; i += 256) {
+        const float* p = qs_seq + (int64_t)i * 16;
         float acc = 0.0f;
 #pragma unroll
-        for (int k = 0; k < 8; ++k) acc += s_u[k][g][dd];
-        rec[g * kRec + 2 + dd] = acc;
+        for (int e = 0; e < 16; ++e) acc += p[e];
+        s_qs[i] = acc;
     }
-    if (tid < G) {
-        rec[tid * kRec + 0] = m[tid];
-        rec[tid * kRec + 1] = z[tid];
+    for (int h = tid; h < hq; h += 256) {
+        s_m[h] = -INFINITY;
+        s_z[h] = 0.0f;
     }
+    __syncthreads();
+
+    // phase B role
+    const int kvl = hkv * TPK, PG = 256 / kvl;
+    const int pg = tid / kvl, rr = tid - pg * kvl;
+    const int bkvh = rr / TPK, part = rr - bkvh * TPK;
+    const bool bact = pg < PG;
+    const int l0 = part * DPT, bhh = bkvh & 1;
+    float acc[G][DPT], off[G];
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+        off[g] = 0.0f;
+#pragma unroll
+        for (int i = 0; i < DPT; ++i) acc[g][i] = 0.0f;
+    }
+
+    // error bits are raised once at the end: a global atomic inside the loop would
+    // keep the compiler from reading q through the scalar cache
+    uint32_t err = 0;
+    const float inv = 1.0f / sqrtf((float)kHd);
+    const int ntile = (n_all + kTile - 1) / kTile;
+    for (int tile = 0; tile < ntile; ++tile) {
+        const int n = min(kTile, n_all - tile * kTile);
+        // ---- phase A: lane = position j
+        const int j = lane;
+        bool ok = j < n;
+        const uint8_t* pk = a.packets;
+        if (ok) {
+            const int64_t slot = base + (p0 + tile * kTile + j) % a.capacity;
+            if (slot < 0 || slot >= a.n_slots) {
+                err |= RTA_DEVERR_HITS;
+                ok = false;
+            } else {
+                pk = a.packets + slot * a.stride;
+            }
+        }
+        if (wave == 0) s_ok[j] = ok ? 1 : 0;
+        VStage<VF> vst;
+        const bool stage = ok && wave < a.nblk;
+        if (stage) vst.load(pk + a.v_offset + (int64_t)wave * Fmt<VF>::kBytes);
+        for (int kvh = wave; kvh < hkv; kvh += 4) {
+            float score[G];
+            if (ok) {
+                const float* qg = qs_seq + (int64_t)kvh * G * kHd;
+                const uint8_t* kb = pk + (int64_t)(kvh >> 1) * Fmt<KF>::kBytes;
+                if constexpr (KF == RTA_Q4_K) score_q4k<G>(kb, kvh & 1, qg, s_qs + kvh * G * 8, score);
+                else score_q6k<G>(kb, kvh & 1, qg, s_qs + kvh * G * 8, score);
+                bool bad = false;
+#pragma unroll
+                for (int g = 0; g < G; ++g) {
+                    score[g] *= inv;
+                    bad |= !isfinite(score[g]);
+                }
+                if (bad) err |= RTA_DEVERR_DETECTOR;
+            } else {
+#pragma unroll
+                for (int g = 0; g < G; ++g) score[g] = -INFINITY;
+            }
+#pragma unroll
+            for (int g = 0; g < G; ++g) s_sc[(kvh * G + g) * kTile + j] = score[g];
+        }
+        if (stage) vst.store(s_v + ((int64_t)wave * kTile + j) * VROW);
+        for (int vb = wave + 4; vb < a.nblk; vb += 4) {   // more than 8 kv heads
+            if (ok) {
+                vst.load(pk + a.v_offset + (int64_t)vb * Fmt<VF>::kBytes);
+                vst.store(s_v + ((int64_t)vb * kTile + j) * VROW);
+            }
+        }
+        __syncthreads();
+
+        // ---- softmax of the tile, folded into the running (m, Z)
+        for (int h = wave; h < hq; h += 4) {
+            const float v = s_sc[h * kTile + lane];
+            const float mt = group_max(v, kWave);
+            const float m_old = s_m[h];
+            const float m_new = fmaxf(m_old, mt);
+            float w, scale;
+            if (m_new == -INFINITY) {
+                w = 0.0f;
+                scale = 1.0f;
+            } else {
+                w = expf(v - m_new);
+                scale = expf(m_old - m_new);
+            }
+            const float zt = group_sum(w, kWave);
+            s_w[lane * hq + h] = w * 16777216.0f;
+            if (lane == 0) {
+                s_z[h] = s_z[h] * scale + zt;
+                s_m[h] = m_new;
+                s_scale[h] = scale;
+            }
+        }
+        __syncthreads();
+
+        // ---- phase B: U[g][l0 + i] += w * V over this group's positions
+        if (bact) {
+#pragma unroll
+            for (int g = 0; g < G; ++g) {
+                const float f = s_scale[bkvh * G + g];
+                off[g] *= f;
+#pragma unroll
+                for (int i = 0; i < DPT; ++i) acc[g][i] *= f;
+            }
+            const uint32_t* vrows = s_v + (int64_t)(bkvh >> 1) * kTile * VROW;
+            for (int jj = pg; jj < n; jj += PG) {
+                if (!s_ok[jj]) continue;
+                uint32_t cw[DPT / 4];
+                float D, M;
+                v_codes<VF, DPT>(vrows + jj * VROW, bhh, l0, cw, D, M);
+                const float* wr = s_w + jj * hq + bkvh * G;
+                float wD[G];
+#pragma unroll
+                for (int g = 0; g < G; ++g) {
+                    const float wg = wr[g];
+                    wD[g] = wg * D;
+                    off[g] = (VF == RTA_Q4_K) ? fmaf(wg, M, off[g]) : off[g] + wD[g];
+                }
+#pragma unroll
+                for (int k = 0; k < DPT / 4; ++k) {
+                    const half2_t lo = as_codes(cw[k] & 0x00FF00FFu), hi = as_codes((cw[k] >> 8) & 0x00FF00FFu);
+#pragma unroll
+                    for (int g = 0; g < G; ++g) {
+                        acc[g][4 * k + 0] = fmaf((float)lo.x, wD[g], acc[g][4 * k + 0]);
+                        acc[g][4 * k + 1] = fmaf((float)hi.x, wD[g], acc[g][4 * k + 1]);
+                        acc[g][4 * k + 2] = fmaf((float)lo.y, wD[g], acc[g][4 * k + 2]);
+                        acc[g][4 * k + 3] = fmaf((float)hi.y, wD[g], acc[g][4 * k + 3]);
+                    }
+                }
+            }
+        }
+        __syncthreads();
+    }
+
+    // ---- combine the position groups (deterministic order) and write the records
+    float* s_u = lds + L.sc;   // [hq][128], over the scores and weights of the last tile
+    // Q4_K: U = acc - 2^-24 sum w' M ;  Q6_K: U = acc - 32 * 2^-24 sum w' D
+    const float corr = (VF == RTA_Q4_K) ? (1.0f / 16777216.0f) : (32.0f / 16777216.0f);
+    for (int r = 0; r < PG; ++r) {
+        if (bact && pg == r) {
+#pragma unroll
+            for (int g = 0; g < G; ++g) {
+                float* u = s_u + (bkvh * G + g) * kHd + l0;
+#pragma unroll
+                for (int i = 0; i < DPT; ++i) {
+                    const float v = fmaf(-corr, off[g], acc[g][i]);
+                    u[i] = r == 0 ? v : u[i] + v;
+                }
+            }
+        }
+        __syncthreads();
+    }
+    float* rec = a.ws + ((int64_t)s * a.nchunk + c) * hq * kRec;
+    for (int i = tid; i < hq * kHd; i += 256) {
+        const int h = i / kHd, dd = i - h * kHd;
+        rec[h * kRec + 2 + dd] = s_u[i];
+    }
+    for (int h = tid; h < hq; h += 256) {
+        rec[h * kRec + 0] = s_m[h];
+        rec[h * kRec + 1] = s_z[h];
+    }
+    if (err) raise_error(err);
 }
 
-// One workgroup per (sequence, query head); thread = coordinate.
-__global__ void __launch_bounds__(kHd) attn_merge_kernel(const AttnArgs a) {
+// One workgroup per (sequence, query head): 2 halves x 128 coordinates.
+__global__ void __launch_bounds__(256) attn_merge_kernel(const AttnArgs a) {
+    __shared__ float s_red[4];
+    __shared__ float s_part[kHd + 1];
     const int sh = blockIdx.x;
     const int s = sh / a.hq, h = sh - s * a.hq;
-    const int G = a.hq / a.hkv, kvh = h / G, g = h - kvh * G;
-    const int dd = threadIdx.x;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int dd = tid & (kHd - 1), half = tid >> 7;
     const int64_t L = a.ctx_len[s];
     const int64_t visible = L < a.capacity ? L : a.capacity;
     float* out = a.out + (int64_t)sh * kHd;
     if (visible <= 0) {
-        out[dd] = 0.0f;
-        if (dd == 0) {
+        if (half == 0) out[dd] = 0.0f;
+        if (tid == 0) {
             if (a.m_out) a.m_out[sh] = -INFINITY;
             if (a.z_out) a.z_out[sh] = 0.0f;
             raise_error(RTA_DEVERR_HITS);
         }
         return;
     }
-    int nch = (int)((visible + kChunk - 1) / kChunk);
+    const int64_t chunk = (int64_t)a.nt * kTile;
+    int nch = (int)((visible + chunk - 1) / chunk);
     if (nch > a.nchunk) {  // max_ctx was below this sequence's visible count
         nch = a.nchunk;
-        if (dd == 0) raise_error(RTA_DEVERR_HITS);
+        if (tid == 0) raise_error(RTA_DEVERR_HITS);
     }
-    const float* rec0 = a.ws + ((int64_t)(s * a.hkv + kvh) * a.nchunk) * G * kRec + g * kRec;
-    float M = -INFINITY;
-    for (int c = 0; c < nch; ++c) M = fmaxf(M, rec0[(int64_t)c * G * kRec]);
+    const int64_t cstride = (int64_t)a.hq * kRec;
+    const float* rec0 = a.ws + (int64_t)s * a.nchunk * cstride + (int64_t)h * kRec;
+    float mx = -INFINITY;
+    for (int ci = tid; ci < nch; ci += 256) mx = fmaxf(mx, rec0[ci * cstride]);
+    mx = group_max(mx, kWave);
+    if (lane == 0) s_red[wave] = mx;
+    __syncthreads();
+    const float M = fmaxf(fmaxf(s_red[0], s_red[1]), fmaxf(s_red[2], s_red[3]));
     float Z = 0.0f, U = 0.0f;
-    for (int c = 0; c < nch; ++c) {
-        const float* rec = rec0 + (int64_t)c * G * kRec;
-        const float f = expf(rec[0] - M);
-        Z = fmaf(rec[1], f, Z);
-        U = fmaf(rec[2 + dd], f, U);
+    if (M != -INFINITY) {
+        int ci = half;
+        for (; ci + 6 < nch; ci += 8) {   // four chunks in flight per thread
+            float mm[4], zz[4], uu[4];
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                const float* r = rec0 + (int64_t)(ci + 2 * k) * cstride;
+                mm[k] = r[0];
+                zz[k] = r[1];
+                uu[k] = r[2 + dd];
+            }
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                const float f = expf(mm[k] - M);
+                Z = fmaf(zz[k], f, Z);
+                U = fmaf(uu[k], f, U);
+            }
+        }
+        for (; ci < nch; ci += 2) {
+            const float* r = rec0 + (int64_t)ci * cstride;
+            const float f = expf(r[0] - M);
+            Z = fmaf(r[1], f, Z);
+            U = fmaf(r[2 + dd], f, U);
+        }
     }
-    float o = U / fmaxf(Z, 1e-30f);
-    if (a.gate) o *= detector_sigmoid(a.gate[(int64_t)sh * kHd + dd]);
-    out[dd] = o;
-    if (dd == 0 && a.m_out) a.m_out[sh] = M;
-    if (dd == 0 && a.z_out) a.z_out[sh] = Z;
+    if (half == 1) {
+        s_part[dd] = U;
+        if (dd == 0) s_part[kHd] = Z;
+    }
+    __syncthreads();
+    if (half == 0) {
+        U += s_part[dd];
+        Z += s_part[kHd];
+        float o = U / fmaxf(Z, 1e-30f);
+        if (a.gate) o *= detector_sigmoid(a.gate[(int64_t)sh * kHd + dd]);
+        out[dd] = o;
+        if (dd == 0 && a.m_out) a.m_out[sh] = M;
+        if (dd == 0 && a.z_out) a.z_out[sh] = Z;
+    }
 }
 
 // ---- RoPE -------------------------------------------------------------------
@@ -365,16 +556,38 @@ __global__ void __launch_bounds__(256) rope_kernel(float* __restrict__ v, int ro
     e[1] = (float)(x * sn + y * cs);
 }
 
-template <int KF, int VF>
-static hipError_t launch_chunks(int G, const AttnArgs& a, hipStream_t s) {
-    const dim3 grid(a.nchunk, a.nseq * a.hkv);
-    switch (G) {
-    case 1: hipLaunchKernelGGL((attn_chunk_kernel<KF, VF, 1>), grid, dim3(256), 0, s, a); break;
-    case 2: hipLaunchKernelGGL((attn_chunk_kernel<KF, VF, 2>), grid, dim3(256), 0, s, a); break;
-    case 4: hipLaunchKernelGGL((attn_chunk_kernel<KF, VF, 4>), grid, dim3(256), 0, s, a); break;
-    default: hipLaunchKernelGGL((attn_chunk_kernel<KF, VF, 8>), grid, dim3(256), 0, s, a); break;
+// Tiles per chunk: long histories use 2-4 tiles per workgroup so that the per-chunk
+// records stay small next to the history they summarise.
+static int attn_tiles(int nseq, int max_ctx) {
+    const int64_t tiles = (int64_t)nseq * ((max_ctx + kTile - 1) / kTile);
+    return tiles >= 16384 ? 4 : tiles >= 8192 ? 2 : 1;
+}
+
+static int attn_lds_bytes(int hq, int nblk, int fmt_v) {
+    return AttnLds(hq, nblk, fmt_v == RTA_Q4_K ? Fmt<RTA_Q4_K>::kRow : Fmt<RTA_Q6_K>::kRow).total * 4;
+}
+
+template <int KF, int VF, int G>
+static hipError_t launch_chunk(const AttnArgs& a, int lds, hipStream_t s) {
+    static int configured = 64 * 1024;   // raise the dynamic LDS limit when a launch needs more
+    if (lds > configured) {
+        const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&attn_chunk_kernel<KF, VF, G>),
+                                                 hipFuncAttributeMaxDynamicSharedMemorySize, lds);
+        if (e != hipSuccess) return e;
+        configured = lds;
     }
+    hipLaunchKernelGGL((attn_chunk_kernel<KF, VF, G>), dim3(a.nchunk, a.nseq), dim3(256), lds, s, a);
     return hipGetLastError();
+}
+
+template <int KF, int VF>
+static hipError_t launch_chunks(int G, const AttnArgs& a, int lds, hipStream_t s) {
+    switch (G) {
+    case 1: return launch_chunk<KF, VF, 1>(a, lds, s);
+    case 2: return launch_chunk<KF, VF, 2>(a, lds, s);
+    case 4: return launch_chunk<KF, VF, 4>(a, lds, s);
+    default: return launch_chunk<KF, VF, 8>(a, lds, s);
+    }
 }
 
 }  // namespace rta
@@ -399,8 +612,9 @@ int rta_rope(float* v, int rows, int heads, int hd, int rotary, const int64_t* p
 
 size_t rta_decode_attention_workspace_bytes(int nseq, int hq, int hkv, int hd, int max_ctx) {
     if (nseq <= 0 || hq <= 0 || hkv <= 0 || hd != kHd || max_ctx <= 0 || hq % hkv) return 0;
-    const int64_t nchunk = ((int64_t)max_ctx + kChunk - 1) / kChunk;
-    return (size_t)nseq * (size_t)hkv * (size_t)nchunk * (size_t)(hq / hkv) * kRec * sizeof(float);
+    const int64_t chunk = (int64_t)attn_tiles(nseq, max_ctx) * kTile;
+    const int64_t nchunk = ((int64_t)max_ctx + chunk - 1) / chunk;
+    return (size_t)nseq * (size_t)nchunk * (size_t)hq * kRec * sizeof(float);
 }
 
 int rta_decode_attention(const float* q, int nseq, int hq, int hkv, int hd, const void* packets, int fmt_k, int fmt_v,
@@ -411,13 +625,21 @@ int rta_decode_attention(const float* q, int nseq, int hq, int hkv, int hd, cons
     if (nseq <= 0 || hq <= 0 || hkv <= 0 || hd <= 0 || hq % hkv || capacity <= 0 || max_ctx <= 0 || n_slots <= 0)
         return RTA_ERR_SHAPE;
     if ((fmt_k != RTA_Q4_K && fmt_k != RTA_Q6_K) || (fmt_v != RTA_Q4_K && fmt_v != RTA_Q6_K)) return RTA_ERR_FORMAT;
+    // a packet holds 354 bytes per 256 values (resident_dimensions.hpp:10): one Q4_K and one
+    // Q6_K field, or two Q4_K fields; two Q6_K fields would overrun it
+    if (fmt_k == RTA_Q6_K && fmt_v == RTA_Q6_K) return RTA_ERR_FORMAT;
     const int G = hq / hkv;
     if (hd != kHd || (G != 1 && G != 2 && G != 4 && G != 8)) return RTA_ERR_RANGE;
+    // phase B spreads every kv head over 128 / (8 or 16) threads of one 256-thread workgroup
+    if (hkv * (G == 8 ? 16 : 8) > 256) return RTA_ERR_RANGE;
+    const int nblk = (hkv * kHd + 255) / 256;
+    const int lds = attn_lds_bytes(hq, nblk, fmt_v);
+    if (lds > kMaxLds) return RTA_ERR_RANGE;
     if (!host::aligned(q, 4) || !host::aligned(packets, 4) || !host::aligned(slot_base, 8) ||
         !host::aligned(ctx_len, 4) || !host::aligned(out, 4) || (gate && !host::aligned(gate, 4)))
         return RTA_ERR_ALIGN;
     const size_t need = rta_decode_attention_workspace_bytes(nseq, hq, hkv, hd, max_ctx);
-    if (!workspace || workspace_bytes < need) return RTA_ERR_WORKSPACE;
+    if (!workspace || workspace_bytes < need || !host::aligned(workspace, 4)) return RTA_ERR_WORKSPACE;
     AttnArgs a{};
     a.q = q;
     a.packets = static_cast<const uint8_t*>(packets);
@@ -432,19 +654,20 @@ int rta_decode_attention(const float* q, int nseq, int hq, int hkv, int hd, cons
     a.n_slots = n_slots;
     const int kvw = hkv * kHd;
     a.stride = host::history_bytes(kvw);
-    a.v_offset = (int64_t)((kvw + 255) / 256) * (fmt_k == RTA_Q4_K ? 144 : 210);
+    a.v_offset = (int64_t)nblk * (fmt_k == RTA_Q4_K ? 144 : 210);
     a.nseq = nseq;
     a.hq = hq;
     a.hkv = hkv;
-    a.nchunk = (int)((max_ctx + kChunk - 1) / kChunk);
+    a.nt = attn_tiles(nseq, max_ctx);
+    a.nchunk = (int)((max_ctx + a.nt * kTile - 1) / (a.nt * kTile));
+    a.nblk = nblk;
     hipStream_t s = (hipStream_t)stream;
     hipError_t e;
-    if (fmt_k == RTA_Q4_K && fmt_v == RTA_Q6_K) e = launch_chunks<RTA_Q4_K, RTA_Q6_K>(G, a, s);
-    else if (fmt_k == RTA_Q6_K && fmt_v == RTA_Q4_K) e = launch_chunks<RTA_Q6_K, RTA_Q4_K>(G, a, s);
-    else if (fmt_k == RTA_Q4_K) e = launch_chunks<RTA_Q4_K, RTA_Q4_K>(G, a, s);
-    else e = launch_chunks<RTA_Q6_K, RTA_Q6_K>(G, a, s);
+    if (fmt_k == RTA_Q4_K && fmt_v == RTA_Q6_K) e = launch_chunks<RTA_Q4_K, RTA_Q6_K>(G, a, lds, s);
+    else if (fmt_k == RTA_Q6_K && fmt_v == RTA_Q4_K) e = launch_chunks<RTA_Q6_K, RTA_Q4_K>(G, a, lds, s);
+    else e = launch_chunks<RTA_Q4_K, RTA_Q4_K>(G, a, lds, s);
     if (e != hipSuccess) return RTA_ERR_LAUNCH;
-    hipLaunchKernelGGL(attn_merge_kernel, dim3(nseq * hq), dim3(kHd), 0, s, a);
+    hipLaunchKernelGGL(attn_merge_kernel, dim3(nseq * hq), dim3(256), 0, s, a);
     return hipGetLastError() == hipSuccess ? RTA_OK : RTA_ERR_LAUNCH;
 }
 

@@ -46,7 +46,11 @@ def test_host_queries(lib):
     assert lib.rta_gemv_workspace_bytes(_lib.Q4_K, 4096, 4096, 1) == 0
     assert lib.rta_gemv_workspace_bytes(_lib.Q4_K, 4096, 4096, 32) > 0
     assert lib.rta_mlp_workspace_bytes(_lib.Q4_K, _lib.Q6_K, 2048, 6144, 4) == 0
-    assert lib.rta_decode_attention_workspace_bytes(16, 16, 4, 128, 32768) == 16 * 4 * 128 * 4 * 130 * 4
+    # one (m, Z, U[128]) record per (sequence, chunk, q head); chunks of 64 * nt positions with
+    # nt = 1, 2, 4 as nseq * ceil(max_ctx / 64) crosses 8192 and 16384
+    assert lib.rta_decode_attention_workspace_bytes(16, 16, 4, 128, 32768) == 16 * 256 * 16 * 130 * 4
+    assert lib.rta_decode_attention_workspace_bytes(32, 32, 8, 128, 8448) == 32 * 132 * 32 * 130 * 4
+    assert lib.rta_decode_attention_workspace_bytes(64, 32, 8, 128, 16384) == 64 * 64 * 32 * 130 * 4
     assert lib.rta_decode_attention_workspace_bytes(16, 16, 4, 64, 32768) == 0
     # packed (tiled) matrices: ceil(rows/16) * (cols/256) tiles of 16 blocks
     assert lib.rta_pack_bytes(_lib.Q4_K, 4096, 4096) == 256 * 16 * 2304
@@ -88,6 +92,9 @@ def test_argument_errors_are_reported_before_launch(lib):
     args[4] = 128
     args[7] = 13
     assert lib.rta_decode_attention(*args) == E["format"]
+    args[6] = args[7] = _lib.Q6_K                                 # two Q6_K fields overrun a packet
+    assert lib.rta_decode_attention(*args) == E["format"]
+    args[6] = _lib.Q4_K
     args[7] = _lib.Q6_K
     args[18] = 16
     assert lib.rta_decode_attention(*args) == E["ws"]

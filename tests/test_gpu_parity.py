@@ -278,10 +278,34 @@ def test_attention_boundaries(torch_dev, fmts):
     _attention_case(torch, dev, 5, ctx, 16, 4, fmts)
 
 
-@pytest.mark.parametrize("hq,hkv", [(4, 4), (8, 4), (16, 4), (32, 4)])
+@pytest.mark.parametrize("hq,hkv", [(4, 4), (8, 4), (16, 4), (32, 4), (32, 8), (8, 2), (4, 1), (24, 6)])
 def test_attention_gqa_groups(torch_dev, hq, hkv):
     torch, dev = torch_dev
     _attention_case(torch, dev, 6, [700, 3, 1500], hq, hkv, (orc.Q4_K, orc.Q6_K), gate=True)
+
+
+@pytest.mark.parametrize("fmts", [(orc.Q4_K, orc.Q6_K), (orc.Q6_K, orc.Q4_K), (orc.Q4_K, orc.Q4_K)])
+@pytest.mark.parametrize("max_ctx", [2100, 9000, 17000])
+def test_attention_multi_tile_chunks(torch_dev, fmts, max_ctx):
+    """64 sequences: the grid bound max_ctx (a host upper bound, above every context here) sets
+    the tiles per chunk to 1, 2 and 4; contexts cover one to several chunks and partial tiles."""
+    torch, dev = torch_dev
+    rng = np.random.default_rng(max_ctx)
+    ctx = rng.integers(1, 700, 64)
+    ctx[:4] = [2047, 1025, 511, 64]
+    rng2 = np.random.default_rng(11)
+    nseq, hq, hkv, hd = 64, 8, 2, 128
+    ctx = ctx.astype(np.int32)
+    base = np.concatenate([[0], np.cumsum(ctx)[:-1]]).astype(np.int64)
+    packets = synth.random_packets(rng2, int(ctx.sum()), hkv * hd, *fmts)
+    q = rng2.standard_normal((nseq, hq, hd)).astype(np.float32)
+    out, m, z = ops.decode_attention(to_dev(torch, q, dev), to_dev(torch, packets, dev), fmts[0], fmts[1],
+                                     to_dev(torch, base, dev), to_dev(torch, ctx, dev), 1 << 20, max_ctx, hkv)
+    rout, rm, rz = orc.decode_attention(q, packets, fmts[0], fmts[1], base, ctx, 1 << 20, hkv)
+    assert ops.device_error() == 0
+    assert_close(out.cpu().numpy(), rout, "attention output")
+    assert_close(m.cpu().numpy(), rm, "attention max")
+    assert_close(z.cpu().numpy(), rz, "attention Z")
 
 
 def test_attention_ring_capacity(torch_dev):
