@@ -154,7 +154,8 @@ int64_t rta_history_bytes(int kvw);
  *   gate      [nseq, hq, hd] or NULL: out *= sigmoid(gate).
  *   out [nseq, hq, hd]; m_out, z_out [nseq, hq] (each may be NULL): m = max score,
  *   z = sum exp(s - m) (the reference reports physical = (m + 20, z)).
- * hd must be 128 and hq/hkv in {1, 2, 4, 8}.
+ *   workspace: rta_decode_attention_workspace_bytes() bytes, 16-byte aligned.
+ * hd must be 128, hq/hkv in {1, 2, 4, 8} and hkv * 128 / (16 if hq/hkv < 8, else 8) <= 256.
  * Replaces Resident::detectHistory (optical_resident.cpp:429-449): history ray
  * trace op 0 + check op 8 (resident_ray.comp:30-53,80) and the detector op 3
  * (resident_ray.comp:56-76) / ordered three-pass detector

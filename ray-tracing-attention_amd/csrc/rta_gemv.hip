@@ -263,13 +263,12 @@ static MmaPlan plan_tiled(int rows, int cols, int nbt, bool dual) {
     if (nslab > nsbt) nslab = nsbt;
     p.sb_per_slab = (nsbt + nslab - 1) / nslab;
     p.nslab = (nsbt + p.sb_per_slab - 1) / p.sb_per_slab;
-    const int wps = (kPlanCUs + p.nslab - 1) / p.nslab;
+    // one workgroup per CU (the LDS slab fills a CU): never plan a second round
+    const int wps = kPlanCUs / p.nslab > 0 ? kPlanCUs / p.nslab : 1;
     const int need = (units + kGemmWaves - 1) / kGemmWaves;
     p.wgs_per_slab = wps < need ? wps : need;
     p.grid = p.nslab * p.wgs_per_slab;
-    p.x_bytes = (size_t)kMaxBatchTile * cols * 2 * 2 + (size_t)kMaxBatchTile * nsbt * 64 +
-                (size_t)kMaxBatchTile * nsbt * sizeof(float);
-    p.x_bytes = (p.x_bytes + 255) & ~(size_t)255;
+    p.x_bytes = 0;   // x is prepared in LDS by the kernel
     p.part_bytes = p.nslab > 1 ? (size_t)p.nslab * kMaxBatchTile * p.total_rows * sizeof(float) : 0;
     return p;
 }
@@ -327,28 +326,25 @@ static hipError_t run_mfma(int fmt, const Launch& l, void* ws, float* pmax, int*
 }
 
 template <int FMT, int NBT, int MODE>
-static void launch_tiled(const MmaPlan& p, const Launch& l, const GemmX& xp, float* part, float* pmax,
-                         hipStream_t s) {
-    hipLaunchKernelGGL((xprep_kernel<FMT == RTA_Q6_K ? kXpQ6Tile : kXpQ4Tile>), dim3(l.cols / 256, 8 * NBT), dim3(64),
-                       0, s, l.x, l.cols, l.batch, xp);
+static void launch_tiled(const MmaPlan& p, const Launch& l, float* part, float* pmax, hipStream_t s) {
     hipLaunchKernelGGL((gemm_tiled_kernel<FMT, NBT, MODE>), dim3(p.grid), dim3(64 * kGemmWaves), 0, s, l.w, l.w2,
-                       l.rows, l.cols, xp, l.batch, l.y, part, pmax, p.sb_per_slab, p.wgs_per_slab);
+                       l.rows, l.cols, l.x, l.batch, l.y, part, pmax, p.sb_per_slab, p.wgs_per_slab);
 }
 
-// One batch tile (<= 32 rows) over packed weights: xprep -> tiled GEMM (-> slab reduce).
+// One batch tile (<= 32 rows) over packed weights: the tiled GEMM prepares x in LDS
+// itself; with several K slabs, gemm_reduce_kernel adds the partials in slab order.
 template <int MODE>
 static hipError_t run_tiled(int fmt, const Launch& l, void* ws, float* pmax, int* ntasks_out, int* rpt_out,
                             hipStream_t s) {
     const int nbt = l.batch > 16 ? 2 : 1;
     const MmaPlan p = plan_tiled(l.rows, l.cols, nbt, MODE == kSwiglu);
-    GemmX xp = carve_x(ws, l.cols);
-    float* part = reinterpret_cast<float*>(static_cast<uint8_t*>(ws) + p.x_bytes);
+    float* part = static_cast<float*>(ws);
     if ((fmt & 0xff) == RTA_Q4_K) {
-        if (nbt == 1) launch_tiled<RTA_Q4_K, 1, MODE>(p, l, xp, part, pmax, s);
-        else launch_tiled<RTA_Q4_K, 2, MODE>(p, l, xp, part, pmax, s);
+        if (nbt == 1) launch_tiled<RTA_Q4_K, 1, MODE>(p, l, part, pmax, s);
+        else launch_tiled<RTA_Q4_K, 2, MODE>(p, l, part, pmax, s);
     } else {
-        if (nbt == 1) launch_tiled<RTA_Q6_K, 1, MODE>(p, l, xp, part, pmax, s);
-        else launch_tiled<RTA_Q6_K, 2, MODE>(p, l, xp, part, pmax, s);
+        if (nbt == 1) launch_tiled<RTA_Q6_K, 1, MODE>(p, l, part, pmax, s);
+        else launch_tiled<RTA_Q6_K, 2, MODE>(p, l, part, pmax, s);
     }
     if (p.nslab > 1) {
         const dim3 rg((l.rows + 255) / 256, l.batch);
@@ -357,7 +353,7 @@ static hipError_t run_tiled(int fmt, const Launch& l, void* ws, float* pmax, int
         if (ntasks_out) *ntasks_out = (int)rg.x;
         if (rpt_out) *rpt_out = 256;
     } else {
-        if (ntasks_out) *ntasks_out = p.ntg;
+        if (ntasks_out) *ntasks_out = (l.rows + 15) / 16;
         if (rpt_out) *rpt_out = 16;
     }
     return hipGetLastError();

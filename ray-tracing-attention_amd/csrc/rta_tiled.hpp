@@ -118,14 +118,103 @@ __device__ __forceinline__ uint32_t word_of(const uint4& v, int i) {
     return i == 0 ? v.x : i == 1 ? v.y : i == 2 ? v.z : v.w;
 }
 
+// Prepares x rows [0, 16 NBT) over superblocks [sb0, sb0 + nsb) straight into LDS,
+// in the tiled-readout layouts (kXpQ4Tile / kXpQ6Tile of xprep_kernel): per (row,
+// superblock) a power-of-two scale s with max|x s| in [2^13, 2^14), x s as binary16
+// hi + lo (k-permuted inside each 8-value segment), the group sums of x s (/32 for
+// Q4_K, /16 for Q6_K) as hi + lo, and 1/s (0 for rows >= batch).  32 threads per
+// (row, superblock), 8 columns each.  load() issues every x load; store() (after the
+// weight prefetch has been issued behind them) prepares and writes LDS.
+template <int FMT, int NBT>
+struct XStage {
+    using Smem = GemmSmem<NBT>;
+    static constexpr int kRows = Smem::kRows;
+    static constexpr int kGroups = 64 * kGemmWaves / 32;            // (row, superblock) pairs per round
+    static constexpr int kRounds = Smem::kSb * kRows / kGroups;
+    float v[kRounds][8];
+
+    __device__ __forceinline__ void load(const float* __restrict__ x, int cols, int batch, int sb0, int nsb) {
+        const int grp = threadIdx.x >> 5, t = threadIdx.x & 31;
+        const int npairs = nsb * kRows;                           // a multiple of kGroups
+#pragma unroll
+        for (int k = 0; k < kRounds; ++k) {
+            const int pr = grp + k * kGroups, sbl = pr / kRows, r = pr - sbl * kRows;
+            if (pr < npairs && r < batch) {
+                const float4* src =
+                    reinterpret_cast<const float4*>(x + (int64_t)r * cols + (int64_t)(sb0 + sbl) * 256 + 8 * t);
+                const float4 a = src[0], c = src[1];
+                v[k][0] = a.x; v[k][1] = a.y; v[k][2] = a.z; v[k][3] = a.w;
+                v[k][4] = c.x; v[k][5] = c.y; v[k][6] = c.z; v[k][7] = c.w;
+            } else {
+#pragma unroll
+                for (int i = 0; i < 8; ++i) v[k][i] = 0.0f;
+            }
+        }
+    }
+
+    __device__ __forceinline__ void store(Smem& sm, int batch, int nsb) const {
+        const int grp = threadIdx.x >> 5, t = threadIdx.x & 31;
+        const int npairs = nsb * kRows;
+#pragma unroll
+        for (int k = 0; k < kRounds; ++k) {
+            const int pr = grp + k * kGroups, sbl = pr / kRows, r = pr - sbl * kRows;
+            if (pr >= npairs) break;                              // uniform over the workgroup
+            float m = 0.0f;
+#pragma unroll
+            for (int i = 0; i < 8; ++i) m = fmaxf(m, fabsf(v[k][i]));
+            for (int off = 16; off > 0; off >>= 1) m = fmaxf(m, __shfl_xor(m, off, kWave));   // within 32 lanes
+            int e = 0;
+            if (m > 0.0f && isfinite(m)) (void)frexpf(m, &e);
+            const float sc = ldexpf(1.0f, 14 - e);
+            if (t == 0) sm.inv[sbl][r] = r < batch ? ldexpf(1.0f, e - 14) : 0.0f;
+            constexpr int perm[8] = {0, 2, 1, 3, 4, 6, 5, 7};
+            _Float16 hi[8], lo[8];
+            float sum8 = 0.0f;
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                const float w = v[k][perm[i]] * sc;
+                hi[i] = (_Float16)w;
+                lo[i] = (_Float16)(w - (float)hi[i]);
+                sum8 += v[k][i] * sc;
+            }
+            *reinterpret_cast<h8_t*>(&sm.x[sbl][0][r][8 * t]) = h8_t{hi[0], hi[1], hi[2], hi[3], hi[4], hi[5], hi[6], hi[7]};
+            *reinterpret_cast<h8_t*>(&sm.x[sbl][1][r][8 * t]) = h8_t{lo[0], lo[1], lo[2], lo[3], lo[4], lo[5], lo[6], lo[7]};
+            _Float16* g = reinterpret_cast<_Float16*>(&sm.g[sbl][r][0]);   // 4 segments x 8
+            const float s16 = sum8 + __shfl_xor(sum8, 1, kWave);
+            const float s32 = s16 + __shfl_xor(s16, 2, kWave);
+            if constexpr (FMT == RTA_Q6_K) {
+                if ((t & 1) == 0) {   // 16-group u = 8 hh + 2 q + sg -> segment 2 hh + sg, slot 2 q
+                    const int u = t >> 1;
+                    const float w = s16 * (1.0f / 16.0f);
+                    const _Float16 h = (_Float16)w, l = (_Float16)(w - (float)h);
+                    const int seg = 2 * (u >> 3) + (u & 1), q = (u >> 1) & 3;
+                    g[8 * seg + 2 * q] = h;
+                    g[8 * seg + 2 * q + 1] = l;
+                }
+            } else {
+                const int q = t >> 2;  // 32-group: segment q / 2, slots 2 (q % 2), +1; zeros at +4, +5
+                if ((t & 3) == 0) {
+                    const float w = s32 * (1.0f / 32.0f);
+                    const _Float16 h = (_Float16)w, l = (_Float16)(w - (float)h);
+                    g[8 * (q >> 1) + 2 * (q & 1)] = h;
+                    g[8 * (q >> 1) + 2 * (q & 1) + 1] = l;
+                } else if ((t & 3) == 1) {
+                    g[8 * (q >> 1) + 4 + 2 * (q & 1)] = (_Float16)0.0f;
+                    g[8 * (q >> 1) + 5 + 2 * (q & 1)] = (_Float16)0.0f;
+                }
+            }
+        }
+    }
+};
+
 // Units of work: pairs of 16-row tiles (t = 0, 1).  In kSwiglu the pair is (gate
 // tile T, up tile T) of one unit T; otherwise tiles (a + 2u, a + 2u + 1) of the
 // wave's contiguous tile range [a, b), the second one absent at an odd end.
 template <int FMT, int NBT, int MODE>
 __global__ void __launch_bounds__(64 * kGemmWaves) gemm_tiled_kernel(
-    const uint8_t* __restrict__ w, const uint8_t* __restrict__ w2, const int rows, const int cols, const GemmX xp,
-    const int batch, float* __restrict__ y, float* __restrict__ part, float* __restrict__ pmax,
-    const int sb_per_slab, const int wgs_per_slab) {
+    const uint8_t* __restrict__ w, const uint8_t* __restrict__ w2, const int rows, const int cols,
+    const float* __restrict__ x, const int batch, float* __restrict__ y, float* __restrict__ part,
+    float* __restrict__ pmax, const int sb_per_slab, const int wgs_per_slab) {
     constexpr bool kQ4 = FMT == RTA_Q4_K;
     using F = TileFmt<FMT>;
     using Raw = typename F::Raw;
@@ -163,40 +252,17 @@ __global__ void __launch_bounds__(64 * kGemmWaves) gemm_tiled_kernel(
         F::load((MODE == kSwiglu ? w2 : w) + ((int64_t)t1 * nsbt + sb) * F::kBytes, lane, dst[1]);
     };
 
-    constexpr int DEPTH = 2;   // the next superblock loads while the current one multiplies
+    // x loads first (vector-memory loads complete in order, so the x slab is not held
+    // up behind the weights), then DEPTH - 1 superblocks of weights, then the x prep.
+    XStage<FMT, NBT> xs;
+    xs.load(x, cols, batch, sb0, nsb);
+    constexpr int DEPTH = 3;   // two superblocks load while the current one multiplies
     Raw buf[DEPTH][2];
     if (nit > 0) {
 #pragma unroll
         for (int d = 0; d < DEPTH - 1; ++d) load_w(min(d, nit - 1), buf[d]);
     }
-
-    // ---- x slab -> LDS, every load of a thread issued before its first store
-    {
-        constexpr int kThreads = 64 * kGemmWaves;
-        constexpr int kPer = Smem::kSb * 2 * kRows * 32 / kThreads;
-        const int nchunk = nsb * 2 * kRows * 32;
-        uint4 tmp[kPer];
-#pragma unroll
-        for (int k = 0; k < kPer; ++k) {
-            const int i = min(tid + k * kThreads, nchunk - 1);
-            const int c8 = i & 31, r = (i >> 5) % kRows, plane = ((i >> 5) / kRows) & 1, sbl = i / (64 * kRows);
-            tmp[k] = *reinterpret_cast<const uint4*>((plane ? xp.lo : xp.hi) + (int64_t)r * cols +
-                                                     (int64_t)(sb0 + sbl) * 256 + 8 * c8);
-        }
-        const int gi = min(tid, nsb * kRows * 4 - 1), ii = min(tid, nsb * kRows - 1);
-        const int gq = gi & 3, gr = (gi >> 2) % kRows, gs = gi / (4 * kRows);
-        const h8_t gv = xp.g[((int64_t)gr * nsbt + sb0 + gs) * 4 + gq];
-        const int ir = ii % kRows, is = ii / kRows;
-        const float iv = xp.inv[(int64_t)ir * nsbt + sb0 + is];
-#pragma unroll
-        for (int k = 0; k < kPer; ++k) {
-            const int i = min(tid + k * kThreads, nchunk - 1);
-            const int c8 = i & 31, r = (i >> 5) % kRows, plane = ((i >> 5) / kRows) & 1, sbl = i / (64 * kRows);
-            *reinterpret_cast<uint4*>(&sm.x[sbl][plane][r][8 * c8]) = tmp[k];
-        }
-        sm.g[gs][gr][gq] = gv;
-        sm.inv[is][ir] = iv;
-    }
+    xs.store(sm, batch, nsb);
     __syncthreads();
 
     f4_t acc[2][NBT];
@@ -206,7 +272,12 @@ __global__ void __launch_bounds__(64 * kGemmWaves) gemm_tiled_kernel(
         for (int bt = 0; bt < NBT; ++bt) acc[t][bt] = f4_t{0.0f, 0.0f, 0.0f, 0.0f};
 
     // One superblock of the unit's tiles (the second only when has2).
-    auto compute = [&](int sbl, const Raw* r, bool has2) {
+    // One superblock of the unit's two tiles.  Both tiles are always multiplied (at an
+    // odd end of the wave's range the second repeats the first and finish() skips it),
+    // so the loop body has no branches and the x operands of the next column offset
+    // can be read while the current MFMAs run.  Per column offset the eight MFMAs go
+    // hi planes first, then lo planes, so an accumulator's two MFMAs are four apart.
+    auto compute = [&](int sbl, const Raw* r) {
         f4_t C[2][NBT], Cm[2][NBT];
 #pragma unroll
         for (int t = 0; t < 2; ++t)
@@ -222,18 +293,22 @@ __global__ void __launch_bounds__(64 * kGemmWaves) gemm_tiled_kernel(
                 al[bt] = *reinterpret_cast<const h8_t*>(&sm.x[sbl][1][bt * 16 + li][kk]);
             }
         };
-        auto mma = [&](int t, const h8_t* ah, const h8_t* al, const h8_t& bw) {
+        auto mma8 = [&](const h8_t* ah, const h8_t* al, const h8_t* bw) {
 #pragma unroll
-            for (int bt = 0; bt < NBT; ++bt) {
-                C[t][bt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah[bt], bw, C[t][bt], 0, 0, 0);
-                C[t][bt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(al[bt], bw, C[t][bt], 0, 0, 0);
-            }
+            for (int t = 0; t < 2; ++t)
+#pragma unroll
+                for (int bt = 0; bt < NBT; ++bt)
+                    C[t][bt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah[bt], bw[t], C[t][bt], 0, 0, 0);
+#pragma unroll
+            for (int t = 0; t < 2; ++t)
+#pragma unroll
+                for (int bt = 0; bt < NBT; ++bt)
+                    C[t][bt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(al[bt], bw[t], C[t][bt], 0, 0, 0);
         };
         if constexpr (kQ4) {
             uint32_t slo[2], shi[2];
 #pragma unroll
             for (int t = 0; t < 2; ++t) {
-                if (t == 1 && !has2) break;
                 const uint4 h = r[t].hdr;
                 dC[t] = half_lo(h.x) * 16384.0f;     // codes carry 2^-14
                 dM[t] = half_hi(h.x) * 32.0f;        // group sums are staged / 32
@@ -245,13 +320,13 @@ __global__ void __launch_bounds__(64 * kGemmWaves) gemm_tiled_kernel(
                 const _Float16 fm0 = (_Float16)(float)m0, fm1 = (_Float16)(float)m1, z = (_Float16)0.0f;
                 bm[t] = h8_t{fm0, fm0, fm1, fm1, z, z, z, z};
             }
+            h8_t ah[NBT], al[NBT];
+            xload(64 * s, ah, al);
 #pragma unroll
             for (int m = 0; m < 8; ++m) {
-                h8_t ah[NBT], al[NBT];
-                xload(64 * s + 8 * m, ah, al);
+                h8_t bw[2];
 #pragma unroll
                 for (int t = 0; t < 2; ++t) {
-                    if (t == 1 && !has2) break;
                     const int mq = m & 3;
                     const uint32_t w0 = word_of(mq < 2 ? r[t].q0 : r[t].q1, 2 * (mq & 1));
                     const uint32_t w1 = word_of(mq < 2 ? r[t].q0 : r[t].q1, 2 * (mq & 1) + 1);
@@ -259,7 +334,17 @@ __global__ void __launch_bounds__(64 * kGemmWaves) gemm_tiled_kernel(
                     const uint32_t sp = m < 4 ? slo[t] : shi[t];
                     const uint4 q4 = {pk_mul_f16(w0 & M, sp), pk_mul_f16((w0 >> 8) & M, sp), pk_mul_f16(w1 & M, sp),
                                       pk_mul_f16((w1 >> 8) & M, sp)};
-                    mma(t, ah, al, __builtin_bit_cast(h8_t, q4));
+                    bw[t] = __builtin_bit_cast(h8_t, q4);
+                }
+                h8_t nh[NBT], nl[NBT];
+                if (m < 7) xload(64 * s + 8 * (m + 1), nh, nl);
+                mma8(ah, al, bw);
+                if (m < 7) {
+#pragma unroll
+                    for (int bt = 0; bt < NBT; ++bt) {
+                        ah[bt] = nh[bt];
+                        al[bt] = nl[bt];
+                    }
                 }
             }
         } else {
@@ -267,7 +352,6 @@ __global__ void __launch_bounds__(64 * kGemmWaves) gemm_tiled_kernel(
             float scq[2][4];
 #pragma unroll
             for (int t = 0; t < 2; ++t) {
-                if (t == 1 && !has2) break;
                 const float d = (float)__builtin_bit_cast(_Float16, (uint16_t)r[t].d);
                 dC[t] = d * 16384.0f;   // codes carry 2^-14
                 dM[t] = d * 512.0f;     // -32 sc x: sums staged / 16
@@ -279,14 +363,15 @@ __global__ void __launch_bounds__(64 * kGemmWaves) gemm_tiled_kernel(
                 bm[t] = h8_t{(_Float16)-scq[t][0], (_Float16)-scq[t][0], (_Float16)-scq[t][1], (_Float16)-scq[t][1],
                              (_Float16)-scq[t][2], (_Float16)-scq[t][2], (_Float16)-scq[t][3], (_Float16)-scq[t][3]};
             }
+            auto col = [&](int m) { return 128 * hh + 32 * (m >> 1) + 16 * sg + 8 * (m & 1); };
+            h8_t ah[NBT], al[NBT];
+            xload(col(0), ah, al);
 #pragma unroll
             for (int m = 0; m < 8; ++m) {
                 const int q = m >> 1, half = m & 1;
-                h8_t ah[NBT], al[NBT];
-                xload(128 * hh + 32 * q + 16 * sg + 8 * half, ah, al);
+                h8_t bw[2];
 #pragma unroll
                 for (int t = 0; t < 2; ++t) {
-                    if (t == 1 && !has2) break;
                     const uint4& run = (q & 1) ? r[t].b : r[t].a;
                     const uint32_t sp = h2dup(scq[t][q] * 256.0f);
                     uint32_t v[4];
@@ -299,16 +384,26 @@ __global__ void __launch_bounds__(64 * kGemmWaves) gemm_tiled_kernel(
                         v[2 * d2] = pk_mul_f16(code & 0x00FF00FFu, sp);
                         v[2 * d2 + 1] = pk_mul_f16((code >> 8) & 0x00FF00FFu, sp);
                     }
-                    mma(t, ah, al, __builtin_bit_cast(h8_t, uint4{v[0], v[1], v[2], v[3]}));
+                    bw[t] = __builtin_bit_cast(h8_t, uint4{v[0], v[1], v[2], v[3]});
+                }
+                h8_t nh[NBT], nl[NBT];
+                if (m < 7) xload(col(m + 1), nh, nl);
+                mma8(ah, al, bw);
+                if (m < 7) {
+#pragma unroll
+                    for (int bt = 0; bt < NBT; ++bt) {
+                        ah[bt] = nh[bt];
+                        al[bt] = nl[bt];
+                    }
                 }
             }
         }
-        // group-sum MFMA (A operand laid out per lane segment by xprep_kernel)
+        // group-sum MFMA (A operand laid out per lane segment by the x staging)
 #pragma unroll
         for (int bt = 0; bt < NBT; ++bt) {
             const h8_t am = sm.g[sbl][bt * 16 + li][s];
             Cm[0][bt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(am, bm[0], Cm[0][bt], 0, 0, 0);
-            if (has2) Cm[1][bt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(am, bm[1], Cm[1][bt], 0, 0, 0);
+            Cm[1][bt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(am, bm[1], Cm[1][bt], 0, 0, 0);
         }
 #pragma unroll
         for (int bt = 0; bt < NBT; ++bt)
@@ -317,7 +412,6 @@ __global__ void __launch_bounds__(64 * kGemmWaves) gemm_tiled_kernel(
                 const float inv = sm.inv[sbl][bt * 16 + 4 * s + e];
 #pragma unroll
                 for (int t = 0; t < 2; ++t) {
-                    if (t == 1 && !has2) break;
                     float v = dC[t] * C[t][bt][e];
                     v = kQ4 ? fmaf(-dM[t], Cm[t][bt][e], v) : fmaf(dM[t], Cm[t][bt][e], v);
                     acc[t][bt][e] = fmaf(v, inv, acc[t][bt][e]);
@@ -386,7 +480,7 @@ __global__ void __launch_bounds__(64 * kGemmWaves) gemm_tiled_kernel(
                 const int u = it / nsb;
                 int t0, t1;
                 tiles_of(u, t0, t1);
-                compute(it - u * nsb, buf[d], MODE == kSwiglu || t1 != t0);
+                compute(it - u * nsb, buf[d]);
                 if (it - u * nsb == nsb - 1) finish(u);
             }
         }
