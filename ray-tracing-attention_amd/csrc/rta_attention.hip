@@ -20,7 +20,7 @@
 //            from LDS, one v_fma_mix_f32 per code and head; the per-position
 //            factor w * d * sc is applied once per sub-block run, and the Q4_K
 //            minimum / Q6_K -32 offset is accumulated separately.
-// Each chunk writes one (m, Z, U[128]) record per head; a merge kernel combines
+// Each chunk writes one (U[128], m, Z) record per head; a merge kernel combines
 // them:  M = max m_c, Z = sum Z_c e^(m_c-M), o = sum U_c e^(m_c-M) / Z, which is the
 // receipt merge of the grouped backends (resident_attention_runtime.inl:618-645).
 #include <math.h>
@@ -32,7 +32,7 @@ namespace rta {
 
 constexpr int kHd = 128;       // head dimension supported by these kernels
 constexpr int kTile = 64;      // positions per tile: one per lane in phase A
-constexpr int kRec = 2 + kHd;  // per-head record: m, Z, U[128]
+constexpr int kRec = kHd + 4;  // per-head record: U[128], m, Z, 2 pad (16-byte multiple)
 constexpr int kMaxLds = 160 * 1024;
 
 struct AttnArgs {
@@ -57,6 +57,23 @@ struct AttnArgs {
 template <int FMT> struct Fmt;
 template <> struct Fmt<RTA_Q4_K> { static constexpr int kBytes = 144, kRow = 37; };  // LDS row: 36 dwords + pad
 template <> struct Fmt<RTA_Q6_K> { static constexpr int kBytes = 210, kRow = 53; };  // 52.5 dwords
+
+// N consecutive dwords from a 4-byte aligned address, in 16-byte loads (each lane of a
+// wave reads a different packet, so wide loads cut the cache-line requests per byte).
+template <int N>
+__device__ __forceinline__ void load_dwords(const uint32_t* __restrict__ p, uint32_t* r) {
+#pragma unroll
+    for (int i = 0; i < N / 4; ++i) {
+        uint4 v;
+        __builtin_memcpy(&v, p + 4 * i, 16);
+        r[4 * i] = v.x;
+        r[4 * i + 1] = v.y;
+        r[4 * i + 2] = v.z;
+        r[4 * i + 3] = v.w;
+    }
+#pragma unroll
+    for (int i = (N / 4) * 4; i < N; ++i) r[i] = p[i];
+}
 
 // LDS carve-up of the chunk kernel (dynamic shared memory), in floats.
 struct AttnLds {
@@ -83,10 +100,8 @@ __device__ __forceinline__ void score_q4k(const uint8_t* __restrict__ blk, int h
                                           const float* qs, float score[G]) {
     const uint32_t* bw = reinterpret_cast<const uint32_t*>(blk);
     uint32_t hdr[4], w[16];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) hdr[i] = bw[i];
-#pragma unroll
-    for (int i = 0; i < 16; ++i) w[i] = bw[4 + 16 * hh + i];
+    load_dwords<4>(bw, hdr);
+    load_dwords<16>(bw + 4 + 16 * hh, w);
     const float d = half_lo(hdr[0]), dmin = half_hi(hdr[0]);
 #pragma unroll
     for (int g = 0; g < G; ++g) score[g] = 0.0f;
@@ -145,12 +160,11 @@ __device__ __forceinline__ void score_q6k(const uint8_t* __restrict__ blk, int h
                                           const float* qs, float score[G]) {
     const uint32_t mis = (uint32_t)(reinterpret_cast<uintptr_t>(blk) & 3u);
     const uint32_t* a = reinterpret_cast<const uint32_t*>(blk - mis);
-    uint32_t ql[17], qh[9];
-#pragma unroll
-    for (int i = 0; i < 17; ++i) ql[i] = a[16 * hh + i];
-#pragma unroll
-    for (int i = 0; i < 9; ++i) qh[i] = a[32 + 8 * hh + i];
-    const uint32_t s0 = a[48 + 2 * hh], s1 = a[49 + 2 * hh];
+    uint32_t ql[17], qh[9], sw[2];
+    load_dwords<17>(a + 16 * hh, ql);
+    load_dwords<9>(a + 32 + 8 * hh, qh);
+    __builtin_memcpy(sw, a + 48 + 2 * hh, 8);
+    const uint32_t s0 = sw[0], s1 = sw[1];
     const uint32_t s2 = mis ? a[50 + 2 * hh] : s1;   // the third dword only exists when misaligned
     const uint32_t sc_lo = funnel(s0, s1, mis), sc_hi = funnel(s1, s2, mis);
     const float d = (float)__builtin_bit_cast(_Float16, *reinterpret_cast<const uint16_t*>(blk + 208));
@@ -211,8 +225,7 @@ struct VStage {
         const uint32_t* a = reinterpret_cast<const uint32_t*>(blk - mis);
         const uint32_t tail = (uint32_t)*reinterpret_cast<const uint16_t*>(blk + kB - 2);
         // (kB + mis) / 4 whole dwords, then the last 2 bytes when (kB + mis) % 4 == 2
-#pragma unroll
-        for (int i = 0; i < kRaw - 1; ++i) raw[i] = a[i];
+        load_dwords<kRaw - 1>(a, raw);
         if constexpr (FMT == RTA_Q4_K) {   // 36 dwords aligned; 36 + 2 bytes misaligned
             raw[kRaw - 1] = mis ? tail : 0u;
         } else {                           // 52 + 2 bytes aligned; 53 dwords misaligned
@@ -451,28 +464,31 @@ __global__ void __launch_bounds__(256, 2) attn_chunk_kernel(const AttnArgs a) {
     float* rec = a.ws + ((int64_t)s * a.nchunk + c) * hq * kRec;
     for (int i = tid; i < hq * kHd; i += 256) {
         const int h = i / kHd, dd = i - h * kHd;
-        rec[h * kRec + 2 + dd] = s_u[i];
+        rec[h * kRec + dd] = s_u[i];
     }
     for (int h = tid; h < hq; h += 256) {
-        rec[h * kRec + 0] = s_m[h];
-        rec[h * kRec + 1] = s_z[h];
+        rec[h * kRec + kHd] = s_m[h];
+        rec[h * kRec + kHd + 1] = s_z[h];
     }
     if (err) raise_error(err);
 }
 
-// One workgroup per (sequence, query head): 2 halves x 128 coordinates.
+// One workgroup per (sequence, query head): 8 chunk groups x 32 lanes of 4
+// coordinates; every thread keeps 8 chunk records in flight.
 __global__ void __launch_bounds__(256) attn_merge_kernel(const AttnArgs a) {
+    constexpr int kGroups = 8, kAhead = 8;
     __shared__ float s_red[4];
-    __shared__ float s_part[kHd + 1];
+    __shared__ float4 s_u[kGroups][kHd / 4];
+    __shared__ float s_zp[kGroups];
     const int sh = blockIdx.x;
     const int s = sh / a.hq, h = sh - s * a.hq;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int dd = tid & (kHd - 1), half = tid >> 7;
+    const int grp = tid >> 5, e = tid & 31;
     const int64_t L = a.ctx_len[s];
     const int64_t visible = L < a.capacity ? L : a.capacity;
     float* out = a.out + (int64_t)sh * kHd;
     if (visible <= 0) {
-        if (half == 0) out[dd] = 0.0f;
+        if (tid < kHd) out[tid] = 0.0f;
         if (tid == 0) {
             if (a.m_out) a.m_out[sh] = -INFINITY;
             if (a.z_out) a.z_out[sh] = 0.0f;
@@ -482,57 +498,65 @@ __global__ void __launch_bounds__(256) attn_merge_kernel(const AttnArgs a) {
     }
     const int64_t chunk = (int64_t)a.nt * kTile;
     int nch = (int)((visible + chunk - 1) / chunk);
-    if (nch > a.nchunk) {  // max_ctx was below this sequence's visible count
-        nch = a.nchunk;
-        if (tid == 0) raise_error(RTA_DEVERR_HITS);
-    }
+    const bool short_grid = nch > a.nchunk;   // max_ctx was below this sequence's visible count
+    if (short_grid) nch = a.nchunk;
     const int64_t cstride = (int64_t)a.hq * kRec;
     const float* rec0 = a.ws + (int64_t)s * a.nchunk * cstride + (int64_t)h * kRec;
     float mx = -INFINITY;
-    for (int ci = tid; ci < nch; ci += 256) mx = fmaxf(mx, rec0[ci * cstride]);
+    for (int ci = tid; ci < nch; ci += 256) mx = fmaxf(mx, rec0[ci * cstride + kHd]);
     mx = group_max(mx, kWave);
     if (lane == 0) s_red[wave] = mx;
     __syncthreads();
     const float M = fmaxf(fmaxf(s_red[0], s_red[1]), fmaxf(s_red[2], s_red[3]));
-    float Z = 0.0f, U = 0.0f;
+    float Z = 0.0f;
+    float4 U = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
     if (M != -INFINITY) {
-        int ci = half;
-        for (; ci + 6 < nch; ci += 8) {   // four chunks in flight per thread
-            float mm[4], zz[4], uu[4];
+        for (int c0 = grp; c0 < nch; c0 += kGroups * kAhead) {
+            float mm[kAhead], zz[kAhead];
+            float4 uu[kAhead];
 #pragma unroll
-            for (int k = 0; k < 4; ++k) {
-                const float* r = rec0 + (int64_t)(ci + 2 * k) * cstride;
-                mm[k] = r[0];
-                zz[k] = r[1];
-                uu[k] = r[2 + dd];
+            for (int k = 0; k < kAhead; ++k) {
+                const int ci = c0 + kGroups * k;
+                if (ci < nch) {
+                    const float* r = rec0 + (int64_t)ci * cstride;
+                    mm[k] = r[kHd];
+                    zz[k] = r[kHd + 1];
+                    uu[k] = *reinterpret_cast<const float4*>(r + 4 * e);
+                } else {
+                    mm[k] = -INFINITY;
+                    zz[k] = 0.0f;
+                    uu[k] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+                }
             }
 #pragma unroll
-            for (int k = 0; k < 4; ++k) {
+            for (int k = 0; k < kAhead; ++k) {
                 const float f = expf(mm[k] - M);
                 Z = fmaf(zz[k], f, Z);
-                U = fmaf(uu[k], f, U);
+                U.x = fmaf(uu[k].x, f, U.x);
+                U.y = fmaf(uu[k].y, f, U.y);
+                U.z = fmaf(uu[k].z, f, U.z);
+                U.w = fmaf(uu[k].w, f, U.w);
             }
         }
-        for (; ci < nch; ci += 2) {
-            const float* r = rec0 + (int64_t)ci * cstride;
-            const float f = expf(r[0] - M);
-            Z = fmaf(r[1], f, Z);
-            U = fmaf(r[2 + dd], f, U);
-        }
     }
-    if (half == 1) {
-        s_part[dd] = U;
-        if (dd == 0) s_part[kHd] = Z;
-    }
+    s_u[grp][e] = U;
+    if (e == 0) s_zp[grp] = Z;
     __syncthreads();
-    if (half == 0) {
-        U += s_part[dd];
-        Z += s_part[kHd];
-        float o = U / fmaxf(Z, 1e-30f);
-        if (a.gate) o *= detector_sigmoid(a.gate[(int64_t)sh * kHd + dd]);
-        out[dd] = o;
-        if (dd == 0 && a.m_out) a.m_out[sh] = M;
-        if (dd == 0 && a.z_out) a.z_out[sh] = Z;
+    if (tid < kHd) {
+        float u = 0.0f, z = 0.0f;
+#pragma unroll
+        for (int g = 0; g < kGroups; ++g) {
+            u += reinterpret_cast<const float*>(&s_u[g][0])[tid];
+            z += s_zp[g];
+        }
+        float o = u / fmaxf(z, 1e-30f);
+        if (a.gate) o *= detector_sigmoid(a.gate[(int64_t)sh * kHd + tid]);
+        out[tid] = o;
+        if (tid == 0) {
+            if (a.m_out) a.m_out[sh] = M;
+            if (a.z_out) a.z_out[sh] = z;
+            if (short_grid) raise_error(RTA_DEVERR_HITS);
+        }
     }
 }
 
@@ -639,7 +663,7 @@ int rta_decode_attention(const float* q, int nseq, int hq, int hkv, int hd, cons
         !host::aligned(ctx_len, 4) || !host::aligned(out, 4) || (gate && !host::aligned(gate, 4)))
         return RTA_ERR_ALIGN;
     const size_t need = rta_decode_attention_workspace_bytes(nseq, hq, hkv, hd, max_ctx);
-    if (!workspace || workspace_bytes < need || !host::aligned(workspace, 4)) return RTA_ERR_WORKSPACE;
+    if (!workspace || workspace_bytes < need || !host::aligned(workspace, 16)) return RTA_ERR_WORKSPACE;
     AttnArgs a{};
     a.q = q;
     a.packets = static_cast<const uint8_t*>(packets);

@@ -7,6 +7,7 @@
 #include "rta_tiled.hpp"
 #include "rta_gemv.hpp"
 #include "rta_host.hpp"
+#include "rta_internal.hpp"
 
 namespace rta {
 
@@ -407,6 +408,37 @@ static int run_projection(int fmt, const void* w, const void* w2, int rows, int 
         b0 += chunk;
     }
     return RTA_OK;
+}
+
+int tiled_accumulate_partials(int fmt, const void* w, int rows, int cols, const float* x, int batch, float* y,
+                              void* ws, size_t ws_bytes, hipStream_t s, int* nslab) {
+    if (!is_tiled(fmt) || batch <= 0 || batch > kMaxBatchTile || !nslab) return RTA_ERR_RANGE;
+    if (!ws || ws_bytes < projection_ws(fmt, rows, cols, batch, false)) return RTA_ERR_WORKSPACE;
+    const int nbt = batch > 16 ? 2 : 1;
+    const MmaPlan p = plan_tiled(rows, cols, nbt, false);
+    Launch l{};
+    l.w = static_cast<const uint8_t*>(w);
+    l.rows = rows;
+    l.cols = cols;
+    l.x = x;
+    l.y = y;
+    l.batch = batch;
+    float* part = static_cast<float*>(ws);
+    if ((fmt & 0xff) == RTA_Q4_K) {
+        if (nbt == 1) launch_tiled<RTA_Q4_K, 1, kAccumulate>(p, l, part, nullptr, s);
+        else launch_tiled<RTA_Q4_K, 2, kAccumulate>(p, l, part, nullptr, s);
+    } else {
+        if (nbt == 1) launch_tiled<RTA_Q6_K, 1, kAccumulate>(p, l, part, nullptr, s);
+        else launch_tiled<RTA_Q6_K, 2, kAccumulate>(p, l, part, nullptr, s);
+    }
+    *nslab = p.nslab;
+    return hipGetLastError() == hipSuccess ? RTA_OK : RTA_ERR_LAUNCH;
+}
+
+int swiglu_activation(int fmt, const void* wg, const void* wu, int inter, int hidden, const float* x, int batch,
+                      float* act, void* ws, size_t ws_bytes, hipStream_t s) {
+    return run_projection<kSwiglu>(fmt, wg, wu, inter, hidden, x, batch, act, nullptr, nullptr, nullptr, ws, ws_bytes,
+                                   s);
 }
 
 }  // namespace rta

@@ -1,0 +1,26 @@
+// rta_internal.hpp -- library-internal entry points shared between translation units
+// (no C ABI): the pieces the decode step fuses across kernel boundaries.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+
+namespace rta {
+
+// Packed-tile projection y += W x for batch <= 32 rows whose K slabs are left in the
+// workspace for the caller to add: partials [slab][32][rows] fp32 at ws.  *nslab = 1
+// means the kernel added into y itself and nothing is pending.  ws_bytes must cover
+// rta_gemv_workspace_bytes(fmt, rows, cols, batch).
+int tiled_accumulate_partials(int fmt, const void* w, int rows, int cols, const float* x, int batch, float* y,
+                              void* ws, size_t ws_bytes, hipStream_t s, int* nslab);
+
+// The fused gate/up projection of the SwiGLU MLP alone: act = swiglu(Wg x, Wu x).
+int swiglu_activation(int fmt, const void* wg, const void* wu, int inter, int hidden, const float* x, int batch,
+                      float* act, void* ws, size_t ws_bytes, hipStream_t s);
+
+// hidden[b, :] += sum over slabs k < nslab of part[(k * 32 + b) * width + :] (slab order),
+// then out[b, :] = hidden[b, :] * w / sqrt(mean(hidden[b, :]^2) + eps).  nslab may be 0.
+// width % 4 == 0; pointers 16-byte aligned.
+int residual_rmsnorm(float* hidden, const float* part, int nslab, const float* w, int batch, int width, float eps,
+                     float* out, hipStream_t s);
+
+}  // namespace rta

@@ -13,6 +13,7 @@
 
 #include "rta_common.hpp"
 #include "rta_host.hpp"
+#include "rta_internal.hpp"
 
 namespace rta {
 
@@ -284,10 +285,31 @@ int rta_hybrid_decode_step(const rta_hybrid_shape* shape, const rta_hybrid_weigh
     if (hipGetLastError() != hipSuccess) return RTA_ERR_LAUNCH;
     RTA_TRY(rta_embed(shape->fmt_embed, weights->embed, d.V, d.D, tokens, B, w.hidden, stream));
 
+    // With packed projections and one batch tile, the residual projections (O and
+    // down) leave their K slabs in the GEMM workspace and the next RMSNorm adds them
+    // into the residual stream (one kernel instead of a reduce and a norm).
+    const bool fuse = (pf & RTA_TILED) != 0 && B <= 32;
+    int pending = 0;   // K slabs of the last residual projection still in gemm_ws
+    auto residual_proj = [&](const void* wm, int cols, const float* x) -> int {
+        if (!fuse) return rta_gemv(pf, wm, d.D, cols, x, B, w.hidden, RTA_EPI_ACCUMULATE, w.gemm_ws, w.gemm_bytes,
+                                   stream);
+        int ns = 1;
+        const int rc = tiled_accumulate_partials(pf, wm, d.D, cols, x, B, w.hidden, w.gemm_ws, w.gemm_bytes, s, &ns);
+        pending = ns > 1 ? ns : 0;
+        return rc;
+    };
+    auto norm = [&](const float* nw) -> int {
+        if (!fuse) return rta_rmsnorm(w.hidden, nw, B, d.D, eps, w.normed, stream);
+        const int rc = residual_rmsnorm(w.hidden, static_cast<const float*>(w.gemm_ws), pending, nw, B, d.D, eps,
+                                        w.normed, s);
+        pending = 0;
+        return rc;
+    };
+
     int lf = 0, lr = 0;
     for (int l = 0; l < d.L; ++l) {
         const rta_hybrid_layer& lw = weights->layers[l];
-        RTA_TRY(rta_rmsnorm(w.hidden, lw.norm_in, B, d.D, eps, w.normed, stream));
+        RTA_TRY(norm(lw.norm_in));
         if (is_full(shape, l)) {
             // op 2 index 5 (q | k | v), ops 14 + 3, op 34, attention, op 2 index 2
             RTA_TRY(rta_gemv(pf, lw.w_in, d.rows_full, d.D, w.normed, B, w.proj, RTA_EPI_STORE, w.gemm_ws,
@@ -303,8 +325,7 @@ int rta_hybrid_decode_step(const rta_hybrid_shape* shape, const rta_hybrid_weigh
             RTA_TRY(rta_decode_attention(w.q, B, d.hq, d.hkv, d.hd, packets, shape->fmt_k, shape->fmt_v,
                                          st.base + (size_t)lf * B, w.visible, d.cap, (int64_t)B * d.cap, d.cap,
                                          nullptr, w.mix, nullptr, nullptr, w.attn_ws, w.attn_bytes, stream));
-            RTA_TRY(rta_gemv(pf, lw.w_o, d.D, d.hq * d.hd, w.mix, B, w.hidden, RTA_EPI_ACCUMULATE, w.gemm_ws,
-                             w.gemm_bytes, stream));
+            RTA_TRY(residual_proj(lw.w_o, d.hq * d.hd, w.mix));
             ++lf;
         } else {
             // op 2 index 5 (q | k | v | z | a | b), ops 18-21 and 15, op 2 index 2
@@ -316,17 +337,21 @@ int rta_hybrid_decode_step(const rta_hybrid_shape* shape, const rta_hybrid_weigh
                                    d.hd, eps, w.conv, stream));
             RTA_TRY(rta_delta_rule(st.rec + (size_t)lr * B * d.H * d.hd * d.hd, w.conv, 3 * d.S, w.decay, w.beta,
                                    B, d.H, d.hd, lw.out_norm, w.proj + 3 * d.S, d.rows_rec, eps, w.mix, d.S, stream));
-            RTA_TRY(rta_gemv(pf, lw.w_o, d.D, d.S, w.mix, B, w.hidden, RTA_EPI_ACCUMULATE, w.gemm_ws, w.gemm_bytes,
-                             stream));
+            RTA_TRY(residual_proj(lw.w_o, d.S, w.mix));
             ++lr;
         }
         // op 1 index 1, then the SwiGLU MLP with the residual add (executeMLP)
-        RTA_TRY(rta_rmsnorm(w.hidden, lw.norm_post, B, d.D, eps, w.normed, stream));
-        RTA_TRY(rta_mlp_swiglu(pf, lw.w_gate, pf, lw.w_up, pf, lw.w_down, d.D, d.FF, w.normed, B, w.act, w.hidden,
-                               RTA_EPI_ACCUMULATE, w.gemm_ws, w.gemm_bytes, stream));
+        RTA_TRY(norm(lw.norm_post));
+        if (fuse) {
+            RTA_TRY(swiglu_activation(pf, lw.w_gate, lw.w_up, d.FF, d.D, w.normed, B, w.act, w.gemm_ws, w.gemm_bytes, s));
+            RTA_TRY(residual_proj(lw.w_down, d.FF, w.act));
+        } else {
+            RTA_TRY(rta_mlp_swiglu(pf, lw.w_gate, pf, lw.w_up, pf, lw.w_down, d.D, d.FF, w.normed, B, w.act, w.hidden,
+                                   RTA_EPI_ACCUMULATE, w.gemm_ws, w.gemm_bytes, stream));
+        }
     }
     // op 1 index 2, then the readout (Resident::word): logits and the next tokens
-    RTA_TRY(rta_rmsnorm(w.hidden, weights->norm_final, B, d.D, eps, w.normed, stream));
+    RTA_TRY(norm(weights->norm_final));
     RTA_TRY(rta_lm_head(shape->fmt_lm, weights->lm_head, d.V, d.D, w.normed, B, shape->margin,
                         logits_out ? logits_out : w.logits, tokens, w.lm_ws, w.lm_bytes, stream));
 #undef RTA_TRY

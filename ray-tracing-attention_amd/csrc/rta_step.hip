@@ -5,6 +5,7 @@
 
 #include "rta_common.hpp"
 #include "rta_host.hpp"
+#include "rta_internal.hpp"
 
 namespace rta {
 
@@ -64,6 +65,61 @@ __global__ void __launch_bounds__(256) rmsnorm_kernel(const float* __restrict__ 
         const float4 v = xr[i], g = w4[i];
         o[i] = float4{v.x * inv * g.x, v.y * inv * g.y, v.z * inv * g.z, v.w * inv * g.w};
     }
+}
+
+// Split-K residual add fused with the next RMSNorm (decode step): one 1024-thread
+// block per row; every thread keeps its float4 of the row in registers.
+__global__ void __launch_bounds__(1024) residual_rmsnorm_kernel(float* __restrict__ hidden,
+                                                                const float* __restrict__ part, int nslab,
+                                                                const float* __restrict__ w, int width, float eps,
+                                                                float* __restrict__ out) {
+    __shared__ float red[16];
+    constexpr int kMaxPer = 4;   // float4s per thread: width <= 16384
+    const int b = blockIdx.x, n4 = width >> 2;
+    float4* hr = reinterpret_cast<float4*>(hidden + (int64_t)b * width);
+    float4 h[kMaxPer];
+    float ss = 0.0f;
+#pragma unroll
+    for (int j = 0; j < kMaxPer; ++j) {
+        const int i = threadIdx.x + 1024 * j;
+        if (i < n4) {
+            float4 v = hr[i];
+#pragma unroll 4
+            for (int k = 0; k < nslab; ++k) {
+                const float4 p = reinterpret_cast<const float4*>(part + ((int64_t)k * 32 + b) * width)[i];
+                v.x += p.x;
+                v.y += p.y;
+                v.z += p.z;
+                v.w += p.w;
+            }
+            if (nslab > 0) hr[i] = v;
+            h[j] = v;
+            ss += v.x * v.x + v.y * v.y + v.z * v.z + v.w * v.w;
+        }
+    }
+    ss = block_sum<16>(ss, red);
+    const float inv = 1.0f / sqrtf(ss / (float)width + eps);
+    float4* o = reinterpret_cast<float4*>(out + (int64_t)b * width);
+    const float4* w4 = reinterpret_cast<const float4*>(w);
+#pragma unroll
+    for (int j = 0; j < kMaxPer; ++j) {
+        const int i = threadIdx.x + 1024 * j;
+        if (i < n4) {
+            const float4 v = h[j], g = w4[i];
+            o[i] = float4{v.x * inv * g.x, v.y * inv * g.y, v.z * inv * g.z, v.w * inv * g.w};
+        }
+    }
+}
+
+int residual_rmsnorm(float* hidden, const float* part, int nslab, const float* w, int batch, int width, float eps,
+                     float* out, hipStream_t s) {
+    if (!hidden || !w || !out || (nslab > 0 && !part)) return RTA_ERR_NULL;
+    if (batch <= 0 || batch > 32 || width <= 0 || width % 4 || width > 4 * 1024 * 4 || nslab < 0) return RTA_ERR_SHAPE;
+    if (!host::aligned(hidden, 16) || !host::aligned(w, 16) || !host::aligned(out, 16) ||
+        (part && !host::aligned(part, 16)))
+        return RTA_ERR_ALIGN;
+    hipLaunchKernelGGL(residual_rmsnorm_kernel, dim3(batch), dim3(1024), 0, s, hidden, part, nslab, w, width, eps, out);
+    return hipGetLastError() == hipSuccess ? RTA_OK : RTA_ERR_LAUNCH;
 }
 
 // ------------------------------------------------------------- head norms ----
