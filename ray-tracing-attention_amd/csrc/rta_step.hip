@@ -211,47 +211,73 @@ __global__ void __launch_bounds__(128) short_conv_kernel(const float* __restrict
 // op 21 / resident_state.comp, one token per sequence: block (head, sequence), 4
 // waves x 32 value rows of the hd x hd state ([value][key]); lane l holds keys 2l,
 // 2l+1.  Per row:  s = decay s;  u = s.k;  s += beta (v - u) k;  o = s.q / sqrt(hd).
-// With norm_w the gated RMSNorm of op 15 (resident_math.comp:115) is applied to o.
+// A wave issues the loads of all its 32 rows at once (one memory round trip per
+// block), and the 64 row sums go through DPP steps inside each 16-lane row plus two
+// cross-row shuffles.  With norm_w the gated RMSNorm of op 15 (resident_math.comp:115)
+// is applied to o.
+template <int CTRL>
+__device__ __forceinline__ float dpp_mov(float v) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), CTRL, 0xF, 0xF, true));
+}
+
+// Sum over the 64 lanes of a wave; every lane gets the total.
+__device__ __forceinline__ float wave_sum_dpp(float v) {
+    v += dpp_mov<0xB1>(v);    // quad_perm [1,0,3,2]
+    v += dpp_mov<0x4E>(v);    // quad_perm [2,3,0,1]
+    v += dpp_mov<0x141>(v);   // row_half_mirror
+    v += dpp_mov<0x140>(v);   // row_mirror
+    v += __shfl_xor(v, 16, kWave);
+    return v + __shfl_xor(v, 32, kWave);
+}
+
 __global__ void __launch_bounds__(256) delta_rule_kernel(float* __restrict__ state, const float* __restrict__ qkv,
                                                          int qkv_stride, const float* __restrict__ decay,
                                                          const float* __restrict__ beta, int heads,
                                                          const float* __restrict__ norm_w,
                                                          const float* __restrict__ gate, int gate_stride, float eps,
                                                          float* __restrict__ out, int out_stride) {
-    constexpr int hd = 128;
+    constexpr int hd = 128, kRows = hd / 4;
     __shared__ float o_s[hd];
     __shared__ float red[4];
-    const int h = blockIdx.x, b = blockIdx.y, lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int h = blockIdx.x, b = blockIdx.y, lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int W = heads * hd;
     const float* row = qkv + (int64_t)b * qkv_stride;
+    float2* S = reinterpret_cast<float2*>(state + ((int64_t)b * heads + h) * hd * hd) + wave * kRows * (hd / 2) + lane;
+    float2 s[kRows];
+#pragma unroll
+    for (int i = 0; i < kRows; ++i) s[i] = S[i * (hd / 2)];
     const float2 q = *reinterpret_cast<const float2*>(row + h * hd + 2 * lane);
     const float2 k = *reinterpret_cast<const float2*>(row + W + h * hd + 2 * lane);
+    const float* vv = row + 2 * W + h * hd + wave * kRows;   // this wave's value coordinates (uniform)
     const float dc = decay[(int64_t)b * heads + h], bt = beta[(int64_t)b * heads + h];
     const float scale = 1.0f / sqrtf((float)hd);
-    float2* S = reinterpret_cast<float2*>(state + ((int64_t)b * heads + h) * hd * hd);
-    constexpr int kRows = hd / 4, kUnroll = 8;
-    for (int r0 = 0; r0 < kRows; r0 += kUnroll) {
-        float2 s[kUnroll];
+    float u[kRows];
 #pragma unroll
-        for (int i = 0; i < kUnroll; ++i) s[i] = S[(wave * kRows + r0 + i) * (hd / 2) + lane];
+    for (int i = 0; i < kRows; ++i) {
+        s[i].x *= dc;
+        s[i].y *= dc;
+        u[i] = wave_sum_dpp(s[i].x * k.x + s[i].y * k.y);
+    }
+    float o[kRows];
 #pragma unroll
-        for (int i = 0; i < kUnroll; ++i) {
-            const int v = wave * kRows + r0 + i;
-            s[i].x *= dc;
-            s[i].y *= dc;
-            const float u = wave_sum(s[i].x * k.x + s[i].y * k.y);
-            const float delta = bt * (row[2 * W + h * hd + v] - u);
-            s[i].x += delta * k.x;
-            s[i].y += delta * k.y;
-            const float o = wave_sum(s[i].x * q.x + s[i].y * q.y) * scale;
-            if (lane == 0) o_s[v] = o;
-            S[v * (hd / 2) + lane] = s[i];
-        }
+    for (int i = 0; i < kRows; ++i) {
+        const float delta = bt * (vv[i] - u[i]);
+        s[i].x += delta * k.x;
+        s[i].y += delta * k.y;
+        S[i * (hd / 2)] = s[i];
+        o[i] = s[i].x * q.x + s[i].y * q.y;
+    }
+#pragma unroll
+    for (int i = 0; i < kRows; ++i) o[i] = wave_sum_dpp(o[i]);
+    if (lane == 0) {
+#pragma unroll
+        for (int i = 0; i < kRows; ++i) o_s[wave * kRows + i] = o[i] * scale;
     }
     __syncthreads();
-    float* o = out + (int64_t)b * out_stride + h * hd;
+    float* op = out + (int64_t)b * out_stride + h * hd;
     if (!norm_w) {
-        if (threadIdx.x < hd) o[threadIdx.x] = o_s[threadIdx.x];
+        if (threadIdx.x < hd) op[threadIdx.x] = o_s[threadIdx.x];
         return;
     }
     const float v = threadIdx.x < hd ? o_s[threadIdx.x] : 0.0f;
@@ -259,7 +285,7 @@ __global__ void __launch_bounds__(256) delta_rule_kernel(float* __restrict__ sta
     const float inv = 1.0f / sqrtf(ss / (float)hd + eps);
     if (threadIdx.x < hd) {
         const float g = gate[(int64_t)b * gate_stride + h * hd + threadIdx.x];
-        o[threadIdx.x] = v * inv * norm_w[h * hd + threadIdx.x] * silu(g);
+        op[threadIdx.x] = v * inv * norm_w[h * hd + threadIdx.x] * silu(g);
     }
 }
 
