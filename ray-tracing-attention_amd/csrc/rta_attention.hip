@@ -79,15 +79,15 @@ __device__ __forceinline__ void load_dwords(const uint32_t* __restrict__ p, uint
 struct AttnLds {
     int sc, w, qs, m, z, scale, ok, v, total;
     __host__ __device__ AttnLds(int hq, int nblk, int vrow) {
-        sc = 0;                       // [hq][64] scores of the tile   } reused after the tiles
-        w = sc + hq * kTile;          // [64][hq] weights x 2^24       } as U[hq][128]
-        qs = w + hq * kTile;          // [hq][8] 16-dim sums of q
+        sc = 0;                       // [hq][64] scores of the tile      } reused after the
+        w = sc + hq * kTile;          // [hq][65] weights x 2^24 (padded) } tiles as U[hq][128]
+        qs = w + hq * (kTile + 1);    // [hq][8] 16-dim sums of q
         m = qs + hq * 8;              // [hq] running max
         z = m + hq;                   // [hq] running sum
         scale = z + hq;               // [hq] rescale of this tile
         ok = scale + hq;              // [64] position valid (int)
-        v = (ok + kTile + 3) & ~3;    // [nblk][64][vrow] V superblocks, dword aligned
-        total = v + nblk * kTile * vrow;
+        v = (ok + kTile + 3) & ~3;    // [nblk][64 vrow + 1] V superblocks, dword aligned; the
+        total = v + nblk * (kTile * vrow + 1);   // +1 puts the superblock regions on different banks
     }
 };
 
@@ -371,11 +371,11 @@ __global__ void __launch_bounds__(256, 2) attn_chunk_kernel(const AttnArgs a) {
 #pragma unroll
             for (int g = 0; g < G; ++g) s_sc[(kvh * G + g) * kTile + j] = score[g];
         }
-        if (stage) vst.store(s_v + ((int64_t)wave * kTile + j) * VROW);
+        if (stage) vst.store(s_v + (int64_t)wave * (kTile * VROW + 1) + j * VROW);
         for (int vb = wave + 4; vb < a.nblk; vb += 4) {   // more than 8 kv heads
             if (ok) {
                 vst.load(pk + a.v_offset + (int64_t)vb * Fmt<VF>::kBytes);
-                vst.store(s_v + ((int64_t)vb * kTile + j) * VROW);
+                vst.store(s_v + (int64_t)vb * (kTile * VROW + 1) + j * VROW);
             }
         }
         __syncthreads();
@@ -395,7 +395,7 @@ __global__ void __launch_bounds__(256, 2) attn_chunk_kernel(const AttnArgs a) {
                 scale = expf(m_old - m_new);
             }
             const float zt = group_sum(w, kWave);
-            s_w[lane * hq + h] = w * 16777216.0f;
+            s_w[h * (kTile + 1) + lane] = w * 16777216.0f;
             if (lane == 0) {
                 s_z[h] = s_z[h] * scale + zt;
                 s_m[h] = m_new;
@@ -413,17 +413,17 @@ __global__ void __launch_bounds__(256, 2) attn_chunk_kernel(const AttnArgs a) {
 #pragma unroll
                 for (int i = 0; i < DPT; ++i) acc[g][i] *= f;
             }
-            const uint32_t* vrows = s_v + (int64_t)(bkvh >> 1) * kTile * VROW;
+            const uint32_t* vrows = s_v + (int64_t)(bkvh >> 1) * (kTile * VROW + 1);
             for (int jj = pg; jj < n; jj += PG) {
                 if (!s_ok[jj]) continue;
                 uint32_t cw[DPT / 4];
                 float D, M;
                 v_codes<VF, DPT>(vrows + jj * VROW, bhh, l0, cw, D, M);
-                const float* wr = s_w + jj * hq + bkvh * G;
+                const float* wr = s_w + bkvh * G * (kTile + 1) + jj;
                 float wD[G];
 #pragma unroll
                 for (int g = 0; g < G; ++g) {
-                    const float wg = wr[g];
+                    const float wg = wr[g * (kTile + 1)];
                     wD[g] = wg * D;
                     off[g] = (VF == RTA_Q4_K) ? fmaf(wg, M, off[g]) : off[g] + wD[g];
                 }
@@ -443,7 +443,10 @@ __global__ void __launch_bounds__(256, 2) attn_chunk_kernel(const AttnArgs a) {
         __syncthreads();
     }
 
-    // ---- combine the position groups (deterministic order) and write the records
+    // ---- combine the position groups (deterministic order) and write the records.
+    // U[h] sits in LDS with its coordinates permuted so that the 8 threads of a row
+    // write 8 adjacent 16-byte chunks: coordinates l0 + 4k + e (l0 = DPT part) at
+    // 4 (k TPK + part) + e, which keeps the stores free of bank conflicts.
     float* s_u = lds + L.sc;   // [hq][128], over the scores and weights of the last tile
     // Q4_K: U = acc - 2^-24 sum w' M ;  Q6_K: U = acc - 32 * 2^-24 sum w' D
     const float corr = (VF == RTA_Q4_K) ? (1.0f / 16777216.0f) : (32.0f / 16777216.0f);
@@ -451,11 +454,17 @@ __global__ void __launch_bounds__(256, 2) attn_chunk_kernel(const AttnArgs a) {
         if (bact && pg == r) {
 #pragma unroll
             for (int g = 0; g < G; ++g) {
-                float* u = s_u + (bkvh * G + g) * kHd + l0;
+                float* u = s_u + (bkvh * G + g) * kHd;
 #pragma unroll
-                for (int i = 0; i < DPT; ++i) {
-                    const float v = fmaf(-corr, off[g], acc[g][i]);
-                    u[i] = r == 0 ? v : u[i] + v;
+                for (int k = 0; k < DPT / 4; ++k) {
+                    float4* u4 = reinterpret_cast<float4*>(u + 4 * (k * TPK + part));
+                    float4 v = float4{fmaf(-corr, off[g], acc[g][4 * k + 0]), fmaf(-corr, off[g], acc[g][4 * k + 1]),
+                                      fmaf(-corr, off[g], acc[g][4 * k + 2]), fmaf(-corr, off[g], acc[g][4 * k + 3])};
+                    if (r > 0) {
+                        const float4 o = *u4;
+                        v = float4{v.x + o.x, v.y + o.y, v.z + o.z, v.w + o.w};
+                    }
+                    *u4 = v;
                 }
             }
         }
@@ -464,7 +473,8 @@ __global__ void __launch_bounds__(256, 2) attn_chunk_kernel(const AttnArgs a) {
     float* rec = a.ws + ((int64_t)s * a.nchunk + c) * hq * kRec;
     for (int i = tid; i < hq * kHd; i += 256) {
         const int h = i / kHd, dd = i - h * kHd;
-        rec[h * kRec + dd] = s_u[i];
+        const int p = dd / DPT, k = (dd % DPT) >> 2, e = dd & 3;
+        rec[h * kRec + dd] = s_u[h * kHd + 4 * (k * TPK + p) + e];
     }
     for (int h = tid; h < hq; h += 256) {
         rec[h * kRec + kHd] = s_m[h];
