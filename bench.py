@@ -46,7 +46,7 @@ def parse():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=None, help="timed steps (default 64 for decode, else 1000)")
     ap.add_argument("--warmup", type=int, default=None, help="untimed steps (default 4 for decode, else 100)")
-    ap.add_argument("--workload", default="gemv_q4k",
+    ap.add_argument("--workload", default="decode",
                     choices=["gemv_q4k", "mlp", "lm_head", "attention", "proj", "decode", "copy_calib"])
     ap.add_argument("--batch", type=int, default=None)
     ap.add_argument("--rows", type=int, default=12288, help="proj workload: output rows")
@@ -57,6 +57,8 @@ def parse():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--eager", action="store_true", help="time eager launches instead of a graph replay")
+    ap.add_argument("--no-companions", action="store_true",
+                    help="decode: skip the batch-1 step and the Q4_K GEMV figures reported beside it")
     return ap.parse_args()
 
 
@@ -451,28 +453,39 @@ def w_decode(torch, args, orc):
     capacity = 8192 + 256
     shape = model.shape_9b(capacity, packed=True)
     m = model.DecodeModel(shape, batch, ctx, seed=20261115)
-    gates = [m.mats[f"{l}.w_gate"] for l in range(shape.layers)]        # 32 x 28.3 MB: streams from HBM
-    x = torch.randn(batch, shape.hidden, device=dev)
-    y = torch.empty(batch, shape.ff, device=dev)
-    gws = torch.empty(max(1, ops.gemv_workspace_bytes(Q4_K | ops.TILED, shape.ff, shape.hidden, batch)),
-                      dtype=torch.uint8, device=dev)
+    nfull = shape.layers // shape.full_every
+    nrec = shape.layers - nfull
+    # the dominant kernel: decode attention of the batch over one full-attention layer's
+    # history, rotated over the 8 layers' distinct histories (8 x 191 MB)
+    v = m.views
+    per_layer = v.slots_per_layer * v.packet_bytes
+    p0 = v.packets - m.state.data_ptr()
+    hist_layers = [m.state[p0 + l * per_layer:p0 + (l + 1) * per_layer] for l in range(nfull)]
+    hq, hkv, hd = shape.q_heads, shape.kv_heads, shape.head_dim
+    qa = torch.randn(batch, hq, hd, device=dev)
+    oa = torch.empty_like(qa)
+    base = torch.arange(batch, dtype=torch.int64, device=dev) * capacity
+    ctx_d = torch.from_numpy(ctx).to(dev)
+    aws = torch.empty(ops.decode_attention_workspace_bytes(batch, hq, hkv, hd, capacity), dtype=torch.uint8,
+                      device=dev)
 
     def step(i):
         m.step()
 
-    def gate_proj(i):   # the dominant kernel: one 12288 x 4096 Q4_K projection of the batch
-        ops.gemv(Q4_K | ops.TILED, gates[i % len(gates)], shape.ff, shape.hidden, x, y=y, workspace=gws)
+    def attention(i):
+        ops.decode_attention(qa, hist_layers[i % nfull], shape.fmt_k, shape.fmt_v, base, ctx_d, capacity, capacity,
+                             hkv, workspace=aws, out=oa)
 
-    nfull = shape.layers // shape.full_every
-    nrec = shape.layers - nfull
     w_bytes = m.weight_bytes() - m.lm_head.numel()                       # projections + small vectors
-    hist = int(sum(min(int(c), capacity) for c in ctx)) * nfull * 1416    # history read per step (approx.)
+    sum_ctx = int(sum(min(int(c), capacity) for c in ctx))
+    hist = sum_ctx * nfull * v.packet_bytes                             # history read per step (approx.)
     state = 2 * nrec * batch * shape.rec_heads * 128 * 128 * 4          # recurrent state read + write
     step_bytes = w_bytes + m.lm_head.numel() + hist + state
-    alg_k = gates[0].numel() + batch * 4 * (shape.hidden + shape.ff)
+    alg_k = sum_ctx * v.packet_bytes + 2 * batch * hq * hd * 4
     res = {"alg_bytes": step_bytes, "alg_bytes_kernel": alg_k, "graph_per_step": True,
-           "kernel": "gemm_tiled_kernel<Q4_K> (12288x4096 gate projection, packed tiles)", "step": step,
-           "kernel_launch": gate_proj, "unit": "tok/s", "value_from_ms": lambda ms: batch / (ms * 1e-3),
+           "kernel": f"attn_chunk_kernel<Q4_K,Q6_K,G=4> + attn_merge_kernel (one layer: {batch} sequences, "
+                     f"{hq}/{hkv} heads, {sum_ctx} positions of {v.packet_bytes}-byte K/V packets)",
+           "step": step, "kernel_launch": attention, "unit": "tok/s", "value_from_ms": lambda ms: batch / (ms * 1e-3),
            "dtype": "q4_k/q6_k weights x fp32 activations and state, fp32 accumulate",
            "config": {"workload": f"9B-shape hybrid decode step, batch {batch} (32 layers: 24 gated delta-net + 8 "
                                   "full attention; hidden 4096, 32/8 heads x 128, FF 12288, Q4_K projections, "
@@ -523,6 +536,32 @@ def w_copy_calib(torch, args, orc):
     return res
 
 
+def companions(torch, args, orc):
+    """The metric's other two figures, measured in the same run as the batch-32 decode step:
+    the same step at batch 1 (tok/s) and the single Q4_K GEMV 4096x4096 (GB/s, HBM fraction)."""
+    import argparse as ap
+    a1 = ap.Namespace(**vars(args))
+    a1.batch = 1
+    d1 = w_decode(torch, a1, orc)
+    p1 = d1["check"]()
+    ms1 = timed_replays(torch, d1["step"], args.steps, args.warmup) / args.steps
+    out = {"decode_batch1": {"value": d1["value_from_ms"](ms1), "unit": "tok/s", "ms_per_step": ms1,
+                             "steps": args.steps, "parity": p1, "config": d1["config"]}}
+    del d1
+    g = w_gemv_q4k(torch, args, orc)
+    pg = g["check"]()
+    k = time_kernel(torch, g["kernel_launch"])
+    ms = timed_region(torch, g["step"], 1000, 100) / 1000
+    gbs = g["value_from_ms"](ms)
+    ach = g["alg_bytes"] / (k * 1e-3) / 1e9
+    out["gemv_q4k"] = {"value": gbs, "unit": "GB/s", "steps": 1000, "ms_per_step": ms, "frac_of_hbm_peak":
+                       gbs / HBM_PEAK_GBS, "roofline": {"bound": "hbm", "achieved": ach, "peak": HBM_PEAK_GBS,
+                                                       "unit": "GB/s", "frac": ach / HBM_PEAK_GBS,
+                                                       "traffic": traffic_for("gemv_q4k")},
+                       "kernel": g["kernel"], "kernel_ms_mean": k, "parity": pg, "config": g["config"]}
+    return out
+
+
 WORKLOADS = {"gemv_q4k": w_gemv_q4k, "mlp": w_mlp, "lm_head": w_lm_head, "attention": w_attention,
              "proj": w_proj, "decode": w_decode, "copy_calib": w_copy_calib}
 
@@ -564,6 +603,8 @@ def main():
                          "frac": achieved / HBM_PEAK_GBS, "traffic": traffic_for(args.workload)},
             "cpu_baseline": cpu, "kernel": wl["kernel"], "kernel_ms_mean": k_mean,
             "alg_bytes_per_launch": alg_k, "alg_bytes_per_step": wl["alg_bytes"], "parity": parity}
+    if args.workload == "decode" and not args.no_companions:
+        line["companions"] = companions(torch, args, orc)
     print(json.dumps(line), flush=True)
 
 

@@ -135,14 +135,26 @@ struct Launch {
     int batch;
 };
 
+template <int FMT, int R, int MODE, int KW>
+static void launch_b1(const Plan& p, const Launch& l, hipStream_t s) {
+    const size_t lds = b1_lds_bytes(l.cols / 64);
+    if (lds > 65536) {   // above the default dynamic LDS limit (at most 16384 columns: 68 KB)
+        static const hipError_t attr = hipFuncSetAttribute(
+            reinterpret_cast<const void*>(&gemv_b1_kernel<FMT, R, MODE, KW>),
+            hipFuncAttributeMaxDynamicSharedMemorySize, b1_lds_bytes(4 * kWave));
+        (void)attr;   // a failure surfaces as the launch error
+    }
+    hipLaunchKernelGGL((gemv_b1_kernel<FMT, R, MODE, KW>), dim3(p.grid), dim3(p.block), lds, s, l.w, l.w2,
+                       l.row_bytes, l.rows, l.cols, l.x, l.y, l.partial, p.lpr, p.ntasks);
+}
+
 template <int FMT, int MODE, int R>
 static void launch_b1_kw(const Plan& p, const Launch& l, hipStream_t s) {
-    const dim3 g(p.grid), b(p.block);
     switch (p.kw) {
-    case 1: hipLaunchKernelGGL((gemv_b1_kernel<FMT, R, MODE, 1>), g, b, 0, s, l.w, l.w2, l.row_bytes, l.rows, l.cols, l.x, l.y, l.partial, p.lpr, p.ntasks); break;
-    case 2: hipLaunchKernelGGL((gemv_b1_kernel<FMT, R, MODE, 2>), g, b, 0, s, l.w, l.w2, l.row_bytes, l.rows, l.cols, l.x, l.y, l.partial, p.lpr, p.ntasks); break;
-    case 3: hipLaunchKernelGGL((gemv_b1_kernel<FMT, R, MODE, 3>), g, b, 0, s, l.w, l.w2, l.row_bytes, l.rows, l.cols, l.x, l.y, l.partial, p.lpr, p.ntasks); break;
-    default: hipLaunchKernelGGL((gemv_b1_kernel<FMT, R, MODE, 4>), g, b, 0, s, l.w, l.w2, l.row_bytes, l.rows, l.cols, l.x, l.y, l.partial, p.lpr, p.ntasks); break;
+    case 1: launch_b1<FMT, R, MODE, 1>(p, l, s); break;
+    case 2: launch_b1<FMT, R, MODE, 2>(p, l, s); break;
+    case 3: launch_b1<FMT, R, MODE, 3>(p, l, s); break;
+    default: launch_b1<FMT, R, MODE, 4>(p, l, s); break;
     }
 }
 

@@ -58,6 +58,8 @@ struct Q4K {
     __device__ static __forceinline__ int run_col(int slot, int run) {
         return (slot >> 2) * 256 + (slot & 3) * 64 + run * 32;
     }
+    // Inverse of run_col: slot * 64 + position of column col inside its slot's x values.
+    __device__ static __forceinline__ int place(int col) { return col; }
     __device__ static __forceinline__ void load(const uint8_t* __restrict__ row, int slot, Raw& r) {
         const uint8_t* blk = row + (slot >> 2) * kBytes;
         const int j = slot & 3;
@@ -107,6 +109,10 @@ struct Q6K {
     __device__ static __forceinline__ int run_col(int slot, int run) {
         const int hh = (slot >> 1) & 1, l0 = (slot & 1) * 16;
         return (slot >> 2) * 256 + hh * 128 + l0 + 32 * run;
+    }
+    __device__ static __forceinline__ int place(int col) {
+        const int cc = col & 255, hh = cc >> 7, run = (cc & 127) >> 5, l = cc & 31;
+        return ((col >> 8) * 4 + hh * 2 + (l >> 4)) * 64 + run * 16 + (l & 15);
     }
     // Every read lies inside the 210-byte block (the last dword of each run and
     // the third scale dword are only consumed when the block is 2-byte aligned).
@@ -197,6 +203,12 @@ __device__ __forceinline__ void load_x(const float* __restrict__ xb, int slot, f
 }
 
 // ------------------------------------------------------------ batch 1 ----
+// x float4s each thread stages into LDS (at most).  Blocks are 256 threads (KW = 1, 2,
+// 4: at most 4096, 8192, 16384 columns) or 192 (KW = 3: at most 12288), so cols / 4 is
+// at most 4, 8, 16, 16 times blockDim.
+constexpr int kXPerThread = 16;
+__host__ __device__ constexpr int b1_lds_bytes(int slots) { return slots * 17 * 16; }
+
 // KW waves per row task (cols = 64*64*KW at most); 256-thread blocks run 4/KW
 // independent task groups when KW divides 4, otherwise one group of KW waves.
 // R rows per lane per task (P*R rows per task).
@@ -220,21 +232,14 @@ __global__ void __launch_bounds__(256) gemv_b1_kernel(const uint8_t* __restrict_
     const int slot = active ? slot_i : 0;
     const int rpt = P * R;
 
+    extern __shared__ float4 s_x[];   // slot s's 64 x values at float4 17 s (+1 pad: no bank conflicts)
     float xs[64], X[F::kRuns];
-    if (active) {
-        load_x<F>(x, slot, xs, X);
-    } else {
-#pragma unroll
-        for (int i = 0; i < 64; ++i) xs[i] = 0.0f;
-#pragma unroll
-        for (int i = 0; i < F::kRuns; ++i) X[i] = 0.0f;
-    }
-
     const int stride = gridDim.x * kGroups;
     Raw bufA[R], bufB[R], bufA2[kDual ? R : 1], bufB2[kDual ? R : 1];
 
+    // Every address is valid (inactive lanes read slot 0, rows clamp), so loads need no
+    // guard: results of inactive lanes and of tasks past the end are discarded.
     auto load_task = [&](int t, Raw* dst, Raw* dst2) {
-        if (!active) return;
 #pragma unroll
         for (int r = 0; r < R; ++r) {
             const int row = min(t * rpt + sub + P * r, rows - 1);  // clamped rows are discarded
@@ -301,8 +306,39 @@ __global__ void __launch_bounds__(256) gemv_b1_kernel(const uint8_t* __restrict_
     };
 
     // Uniform trip count per block (KW > 1 groups synchronise inside run_task).
-    int task = blockIdx.x * kGroups + group;
-    if (task < ntasks) load_task(task, bufA, bufA2);
+    // x goes through LDS: a lane's 64 values span 256 bytes, so direct per-lane loads
+    // touch 64 cache lines per instruction.  The coalesced loads are issued first and
+    // land in LDS while the first task's weights are in flight.
+    // Loads and stores are unconditional, clamped to the last float4 (rewritten with its
+    // own value): a guarded load becomes a branch that waits for it on the spot.
+    constexpr int kXPer = KW == 1 ? 4 : KW == 2 ? 8 : kXPerThread;
+    const int nf = cols >> 2;
+    int xf[kXPer];
+    float4 xg[kXPer];
+#pragma unroll
+    for (int k = 0; k < kXPer; ++k) {
+        xf[k] = min((int)threadIdx.x + k * (int)blockDim.x, nf - 1);
+        xg[k] = reinterpret_cast<const float4*>(x)[xf[k]];
+    }
+    const int task = blockIdx.x * kGroups + group;
+    load_task(task, bufA, bufA2);
+#pragma unroll
+    for (int k = 0; k < kXPer; ++k) {
+        const int pl = F::place(4 * xf[k]);
+        s_x[(pl >> 6) * 17 + ((pl & 63) >> 2)] = xg[k];
+    }
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < F::kRuns; ++i) X[i] = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+        const float4 v = active ? s_x[slot * 17 + i] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        xs[4 * i + 0] = v.x;
+        xs[4 * i + 1] = v.y;
+        xs[4 * i + 2] = v.z;
+        xs[4 * i + 3] = v.w;
+        X[(4 * i) / F::kRunLen] += (v.x + v.y) + (v.z + v.w);
+    }
     for (int base = blockIdx.x * kGroups; base < ntasks; base += 2 * stride) {
         const int t0 = base + group, t1 = t0 + stride, t2 = t1 + stride;
         if (t1 < ntasks) load_task(t1, bufB, bufB2);

@@ -59,7 +59,8 @@ def test_dequant_golden_and_plain(torch_dev):
 
 
 # ------------------------------------------------------------------- GEMV ----
-GEMV_SHAPES = [(4096, 4096), (6144, 2048), (2048, 6144), (1000, 768), (37, 256), (5, 12288), (300, 1024)]
+GEMV_SHAPES = [(4096, 4096), (6144, 2048), (2048, 6144), (1000, 768), (37, 256), (5, 12288), (300, 1024), (64, 8192),
+               (7, 16384)]
 
 
 @pytest.mark.parametrize("fmt", [orc.Q4_K, orc.Q6_K])
