@@ -212,6 +212,123 @@ __device__ __forceinline__ void score_q6k(const uint8_t* __restrict__ blk, int h
     }
 }
 
+// ---- phase A on the matrix cores (K = Q4_K) --------------------------------------
+// Per 16 positions and kv head, S^T = Q K^T with v_mfma_f32_16x16x32_f16:
+//   A (16 x 32)  q: row 2g + part holds binary16 hi (part 0) / lo (part 1) of q_g * s_g,
+//                s_g a power of two with max|q_g s_g| in [2^13, 2^14) (22 bits of q);
+//   B (32 x 16)  K codes * sub-block scale as exact binary16 (a code c in the low
+//                bits of a half is the subnormal c 2^-24; (c 2^-24)(sc 2^10) =
+//                (16c 2^-24)(sc 2^6) = c sc 2^-14, c sc <= 945); column = position.
+// k block kb (0..3) covers dims 64 (kb >> 1) + 32 (kb & 1) + [0, 32) of the head,
+// i.e. Q4_K group 4 hh + kb; lane segment u holds k = 8u + perm[i] in slot i (the
+// code-pair masks deliver dims (k, k + 2)).  A second MFMA takes the minimum term:
+// A = 32-dim sums of q (scaled by s_g / 32) in slots kb, B = the 6-bit minimum codes.
+// The lane that loads position p (column p % 16, segment u) receives its scores in
+// output rows 4u .. 4u + 3: heads 2u and 2u + 1, hi and lo.
+struct QOp {
+    h8_t a[4];    // k blocks of q
+    h8_t am;      // minimum-term operand (lanes of segment 0)
+    float rs[2];  // 1 / s of heads 2u and 2u + 1
+};
+
+template <int G>
+__device__ __forceinline__ QOp make_qop(const float* __restrict__ qg, int lane) {
+    constexpr int perm[8] = {0, 2, 1, 3, 4, 6, 5, 7};
+    const int row = lane & 15, g = row >> 1, part = row & 1, u = lane >> 4;
+    const bool live = g < G;
+    const float* qh = qg + (live ? g : 0) * kHd;
+    float v[4][8], sum[4];
+    float mx = 0.0f;
+#pragma unroll
+    for (int kb = 0; kb < 4; ++kb) {
+        const float4* p = reinterpret_cast<const float4*>(qh + 64 * (kb >> 1) + 32 * (kb & 1) + 8 * u);
+        const float4 x0 = p[0], x1 = p[1];
+        const float t[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
+        sum[kb] = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            v[kb][i] = live ? t[i] : 0.0f;
+            mx = fmaxf(mx, fabsf(v[kb][i]));
+            sum[kb] += v[kb][i];
+        }
+    }
+    mx = fmaxf(mx, __shfl_xor(mx, 16, kWave));
+    mx = fmaxf(mx, __shfl_xor(mx, 32, kWave));
+#pragma unroll
+    for (int kb = 0; kb < 4; ++kb) {   // fixed order: ((u0 + u1) + (u2 + u3))
+        sum[kb] += __shfl_xor(sum[kb], 16, kWave);
+        sum[kb] += __shfl_xor(sum[kb], 32, kWave);
+    }
+    int e = 0;
+    if (mx > 0.0f && isfinite(mx)) (void)frexpf(mx, &e);
+    const float sg = ldexpf(1.0f, 14 - e);
+    QOp o;
+#pragma unroll
+    for (int kb = 0; kb < 4; ++kb) {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const float x = v[kb][perm[i]] * sg;
+            const _Float16 hi = (_Float16)x;
+            o.a[kb][i] = part ? (_Float16)(x - (float)hi) : hi;
+        }
+    }
+    const _Float16 z = (_Float16)0.0f;
+    o.am = h8_t{z, z, z, z, z, z, z, z};
+#pragma unroll
+    for (int kb = 0; kb < 4; ++kb) {
+        const float x = sum[kb] * (sg * 0.03125f);
+        const _Float16 hi = (_Float16)x;
+        o.am[kb] = u == 0 ? (part ? (_Float16)(x - (float)hi) : hi) : z;
+    }
+    // rows 4u and 4u + 2 are heads 2u and 2u + 1 (their s lives in every segment)
+    o.rs[0] = 1.0f / __shfl(sg, 4 * u, kWave);
+    o.rs[1] = 1.0f / __shfl(sg, 4 * u + 2, kWave);
+    return o;
+}
+
+struct KRaw {        // one lane's share of a Q4_K key: header and its two 8-byte segments
+    uint4 hdr;
+    uint2 c[2];      // chunk 2hh + jc, bytes 8u .. 8u + 7
+};
+
+__device__ __forceinline__ void load_key_q4k(const uint8_t* __restrict__ blk, int hh, int u, KRaw& r) {
+    __builtin_memcpy(&r.hdr, blk, 16);
+#pragma unroll
+    for (int jc = 0; jc < 2; ++jc) __builtin_memcpy(&r.c[jc], blk + 16 + 32 * (2 * hh + jc) + 8 * u, 8);
+}
+
+// Scores (times 1/sqrt(hd)) of the 16 positions of one key tile against the G heads of
+// one kv head.  Returns them for heads 2u and 2u + 1 of this lane's position.
+template <int G>
+__device__ __forceinline__ void score_q4k_mma(const QOp& qo, const KRaw& r, int hh, int u, float inv,
+                                              float out[2]) {
+    uint32_t sc[4], mn[4];
+#pragma unroll
+    for (int kb = 0; kb < 4; ++kb) q4k_scale_min_lane(r.hdr.y, r.hdr.z, r.hdr.w, 4 * hh + kb, sc[kb], mn[kb]);
+    f4_t D = f4_t{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int kb = 0; kb < 4; ++kb) {
+        const uint2 c = r.c[kb >> 1];
+        const uint32_t M = (kb & 1) ? 0x00F000F0u : 0x000F000Fu;
+        const uint32_t sp = h2dup((float)sc[kb] * ((kb & 1) ? 64.0f : 1024.0f));
+        const uint4 q4 = {pk_mul_f16(c.x & M, sp), pk_mul_f16((c.x >> 8) & M, sp), pk_mul_f16(c.y & M, sp),
+                          pk_mul_f16((c.y >> 8) & M, sp)};
+        D = __builtin_amdgcn_mfma_f32_16x16x32_f16(qo.a[kb], __builtin_bit_cast(h8_t, q4), D, 0, 0, 0);
+    }
+    const _Float16 z = (_Float16)0.0f;
+    h8_t bm = h8_t{z, z, z, z, z, z, z, z};
+    if (u == 0) {
+#pragma unroll
+        for (int kb = 0; kb < 4; ++kb) bm[kb] = (_Float16)(float)mn[kb];
+    }
+    const f4_t Dm = __builtin_amdgcn_mfma_f32_16x16x32_f16(qo.am, bm, f4_t{0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0);
+    // sum_k (d sc c - dmin m) q = (d 2^14 (hi + lo) - dmin 2^5 (mhi + mlo)) / s
+    const float dC = half_lo(r.hdr.x) * 16384.0f, dM = half_hi(r.hdr.x) * 32.0f;
+#pragma unroll
+    for (int eh = 0; eh < 2; ++eh)
+        out[eh] = fmaf(dC, D[2 * eh] + D[2 * eh + 1], -dM * (Dm[2 * eh] + Dm[2 * eh + 1])) * qo.rs[eh] * inv;
+}
+
 // Copies the V superblock at blk (2-byte aligned, `bytes` long) into an LDS row whose
 // dword i holds block bytes 4i..4i+3.  Reads stay inside [blk, blk + bytes).
 template <int FMT>
@@ -229,8 +346,10 @@ struct VStage {
         if constexpr (FMT == RTA_Q4_K) {   // 36 dwords aligned; 36 + 2 bytes misaligned
             raw[kRaw - 1] = mis ? tail : 0u;
         } else {                           // 52 + 2 bytes aligned; 53 dwords misaligned
-            if (mis) raw[kRaw - 1] = a[kRaw - 1];
-            else raw[kRaw - 1] = tail;
+            // the load is unconditional (a guarded load would wait on the spot); when
+            // aligned it rereads an in-block dword and the tail is used instead
+            const uint32_t extra = a[mis ? kRaw - 1 : kRaw - 2];
+            raw[kRaw - 1] = mis ? extra : tail;
         }
     }
     __device__ __forceinline__ void store(uint32_t* row) const {
@@ -268,8 +387,11 @@ __device__ __forceinline__ void v_codes(const uint32_t* row, int hh, int l0, uin
     }
 }
 
-template <int KF, int VF, int G>
+// KPW > 0: K = Q4_K scored on the matrix cores, KPW (1 or 2) kv heads per wave
+// (hkv <= 4 KPW); KPW == 0: scored on the vector ALUs, any hkv.
+template <int KF, int VF, int G, int KPW>
 __global__ void __launch_bounds__(256, 2) attn_chunk_kernel(const AttnArgs a) {
+    static_assert(KPW == 0 || KF == RTA_Q4_K, "matrix-core scoring reads Q4_K keys");
     extern __shared__ __align__(16) float lds[];
     constexpr int DPT = G == 8 ? 8 : 16;      // phase B dims per thread
     constexpr int TPK = kHd / DPT;            // threads per kv head
@@ -326,6 +448,14 @@ __global__ void __launch_bounds__(256, 2) attn_chunk_kernel(const AttnArgs a) {
         for (int i = 0; i < DPT; ++i) acc[g][i] = 0.0f;
     }
 
+    // q of this wave's kv heads as matrix-core operands (clamped heads are never used)
+    QOp qo[KPW > 0 ? KPW : 1];
+    if constexpr (KPW > 0) {
+#pragma unroll
+        for (int kl = 0; kl < KPW; ++kl)
+            qo[kl] = make_qop<G>(qs_seq + (int64_t)min(wave + 4 * kl, hkv - 1) * G * kHd, lane);
+    }
+
     // error bits are raised once at the end: a global atomic inside the loop would
     // keep the compiler from reading q through the scalar cache
     uint32_t err = 0;
@@ -349,6 +479,54 @@ __global__ void __launch_bounds__(256, 2) attn_chunk_kernel(const AttnArgs a) {
         if (wave == 0) s_ok[j] = ok ? 1 : 0;
         VStage<VF> vst;
         const bool stage = ok && wave < a.nblk;
+        if constexpr (KPW > 0) {
+            // keys of the wave's kv heads for the 4 x 16 positions (lane: position
+            // 16 rt + lane % 16, segment u), then this lane's V superblock; every
+            // address is valid (invalid positions read slot 0, heads clamp)
+            const int u = lane >> 4;
+            const uint64_t pv = reinterpret_cast<uint64_t>(pk);
+            const uint8_t* kp[4];
+            bool okr[4];
+#pragma unroll
+            for (int rt = 0; rt < 4; ++rt) {
+                const int src = 16 * rt + (lane & 15);
+                const uint32_t lo = (uint32_t)__shfl((int)(uint32_t)pv, src, kWave);
+                const uint32_t hi = (uint32_t)__shfl((int)(uint32_t)(pv >> 32), src, kWave);
+                kp[rt] = reinterpret_cast<const uint8_t*>(((uint64_t)hi << 32) | lo);
+                okr[rt] = __shfl(ok ? 1 : 0, src, kWave) != 0;
+            }
+            // order: V, first head's keys, V into LDS (V returns first), second head's
+            // keys, then the scores; this keeps at most two key sets in registers
+            vst.load(pk + a.v_offset + (int64_t)min(wave, a.nblk - 1) * Fmt<VF>::kBytes);
+            KRaw kr[KPW][4];
+            auto load_keys = [&](int kl) {
+                const int kvh = min(wave + 4 * kl, hkv - 1);
+#pragma unroll
+                for (int rt = 0; rt < 4; ++rt)
+                    load_key_q4k(kp[rt] + (int64_t)(kvh >> 1) * Fmt<RTA_Q4_K>::kBytes, kvh & 1, u, kr[kl][rt]);
+            };
+            load_keys(0);
+            if (stage) vst.store(s_v + (int64_t)wave * (kTile * VROW + 1) + j * VROW);
+            if constexpr (KPW > 1) load_keys(1);
+#pragma unroll
+            for (int kl = 0; kl < KPW; ++kl) {
+                const int kvh = wave + 4 * kl;
+                if (kvh >= hkv) break;
+#pragma unroll
+                for (int rt = 0; rt < 4; ++rt) {
+                    float sc2[2];
+                    score_q4k_mma<G>(qo[kl], kr[kl][rt], kvh & 1, u, inv, sc2);
+#pragma unroll
+                    for (int eh = 0; eh < 2; ++eh) {
+                        const int g = 2 * u + eh;
+                        if (g < G) {
+                            if (okr[rt] && !isfinite(sc2[eh])) err |= RTA_DEVERR_DETECTOR;
+                            s_sc[(kvh * G + g) * kTile + 16 * rt + (lane & 15)] = okr[rt] ? sc2[eh] : -INFINITY;
+                        }
+                    }
+                }
+            }
+        } else {
         if (stage) vst.load(pk + a.v_offset + (int64_t)wave * Fmt<VF>::kBytes);
         for (int kvh = wave; kvh < hkv; kvh += 4) {
             float score[G];
@@ -372,6 +550,7 @@ __global__ void __launch_bounds__(256, 2) attn_chunk_kernel(const AttnArgs a) {
             for (int g = 0; g < G; ++g) s_sc[(kvh * G + g) * kTile + j] = score[g];
         }
         if (stage) vst.store(s_v + (int64_t)wave * (kTile * VROW + 1) + j * VROW);
+        }
         for (int vb = wave + 4; vb < a.nblk; vb += 4) {   // more than 8 kv heads
             if (ok) {
                 vst.load(pk + a.v_offset + (int64_t)vb * Fmt<VF>::kBytes);
@@ -601,26 +780,36 @@ static int attn_lds_bytes(int hq, int nblk, int fmt_v) {
     return AttnLds(hq, nblk, fmt_v == RTA_Q4_K ? Fmt<RTA_Q4_K>::kRow : Fmt<RTA_Q6_K>::kRow).total * 4;
 }
 
-template <int KF, int VF, int G>
+template <int KF, int VF, int G, int KPW>
 static hipError_t launch_chunk(const AttnArgs& a, int lds, hipStream_t s) {
     static int configured = 64 * 1024;   // raise the dynamic LDS limit when a launch needs more
     if (lds > configured) {
-        const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&attn_chunk_kernel<KF, VF, G>),
+        const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&attn_chunk_kernel<KF, VF, G, KPW>),
                                                  hipFuncAttributeMaxDynamicSharedMemorySize, lds);
         if (e != hipSuccess) return e;
         configured = lds;
     }
-    hipLaunchKernelGGL((attn_chunk_kernel<KF, VF, G>), dim3(a.nchunk, a.nseq), dim3(256), lds, s, a);
+    hipLaunchKernelGGL((attn_chunk_kernel<KF, VF, G, KPW>), dim3(a.nchunk, a.nseq), dim3(256), lds, s, a);
     return hipGetLastError();
+}
+
+// Q4_K keys of at most 8 kv heads are scored on the matrix cores.
+template <int KF, int VF, int G>
+static hipError_t launch_chunk_k(const AttnArgs& a, int lds, hipStream_t s) {
+    if constexpr (KF == RTA_Q4_K) {
+        if (a.hkv <= 4) return launch_chunk<KF, VF, G, 1>(a, lds, s);
+        if (a.hkv <= 8) return launch_chunk<KF, VF, G, 2>(a, lds, s);
+    }
+    return launch_chunk<KF, VF, G, 0>(a, lds, s);
 }
 
 template <int KF, int VF>
 static hipError_t launch_chunks(int G, const AttnArgs& a, int lds, hipStream_t s) {
     switch (G) {
-    case 1: return launch_chunk<KF, VF, 1>(a, lds, s);
-    case 2: return launch_chunk<KF, VF, 2>(a, lds, s);
-    case 4: return launch_chunk<KF, VF, 4>(a, lds, s);
-    default: return launch_chunk<KF, VF, 8>(a, lds, s);
+    case 1: return launch_chunk_k<KF, VF, 1>(a, lds, s);
+    case 2: return launch_chunk_k<KF, VF, 2>(a, lds, s);
+    case 4: return launch_chunk_k<KF, VF, 4>(a, lds, s);
+    default: return launch_chunk_k<KF, VF, 8>(a, lds, s);
     }
 }
 

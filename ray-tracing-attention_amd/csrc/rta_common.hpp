@@ -68,6 +68,32 @@ __device__ __forceinline__ void q4k_scale_min(uint32_t s0, uint32_t s1, uint32_t
     }
 }
 
+// Scale and minimum of Q4_K group g (0..7, may differ between lanes).
+__device__ __forceinline__ void q4k_scale_min_lane(uint32_t s0, uint32_t s1, uint32_t s2, int g, uint32_t& sc,
+                                                   uint32_t& m) {
+    const uint32_t sh = 8u * (uint32_t)(g & 3);
+    const uint32_t a = (s0 >> sh) & 255u, b = (s1 >> sh) & 255u, mixed = (s2 >> sh) & 255u;
+    const bool lo = g < 4;
+    sc = lo ? (a & 63u) : ((mixed & 15u) | ((a >> 6) << 4));
+    m = lo ? (b & 63u) : ((mixed >> 4) | ((b >> 6) << 4));
+}
+
+// ---- matrix-core operand helpers (v_mfma_f32_16x16x32_f16) ----
+typedef _Float16 h8_t __attribute__((ext_vector_type(8)));
+typedef float f4_t __attribute__((ext_vector_type(4)));
+typedef _Float16 h2v_t __attribute__((ext_vector_type(2)));
+
+// Two binary16 products in one v_pk_mul_f16 (a code pair times a duplicated scale).
+__device__ __forceinline__ uint32_t pk_mul_f16(uint32_t a, uint32_t b) {
+    return __builtin_bit_cast(uint32_t, __builtin_bit_cast(h2v_t, a) * __builtin_bit_cast(h2v_t, b));
+}
+
+// (f16(v), f16(v)) for a value v exactly representable in binary16
+__device__ __forceinline__ uint32_t h2dup(float v) {
+    const uint32_t h = __builtin_bit_cast(uint16_t, (_Float16)v);
+    return h | (h << 16);
+}
+
 // Value i of a GGUF-encoded array, with the reference decoder's fp32 op order
 // (resident_quant.glsl:6-20); contraction is disabled so that (d*sc)*q - dmin*m is
 // rounded exactly as the reference rounds it.

@@ -44,9 +44,6 @@
 
 namespace rta {
 
-typedef _Float16 h8_t __attribute__((ext_vector_type(8)));
-typedef float f4_t __attribute__((ext_vector_type(4)));
-typedef _Float16 h2v_t __attribute__((ext_vector_type(2)));
 
 constexpr int kMaxBatchTile = 32;  // batch rows per GEMM launch
 constexpr int kXStride = 256 + 8;  // f16 per staged x row (8 of padding spread the LDS banks)
@@ -147,15 +144,6 @@ __global__ void __launch_bounds__(64) xprep_kernel(const float* __restrict__ x, 
     }
 }
 
-__device__ __forceinline__ uint32_t pk_mul_f16(uint32_t a, uint32_t b) {
-    return __builtin_bit_cast(uint32_t, __builtin_bit_cast(h2v_t, a) * __builtin_bit_cast(h2v_t, b));
-}
-
-// (f16(v), f16(v)) for a value v exactly representable in binary16
-__device__ __forceinline__ uint32_t h2dup(float v) {
-    const uint32_t h = __builtin_bit_cast(uint16_t, (_Float16)v);
-    return h | (h << 16);
-}
 
 // -------------------------------------------------------- weight operand ----
 // Per lane: row l%16 of one 16-row tile, k segment s = l/16 of every 32-value chunk.

@@ -104,15 +104,6 @@ __global__ void __launch_bounds__(256) pack_kernel(const uint8_t* __restrict__ s
     *reinterpret_cast<uint16_t*>(dst + o) = v;
 }
 
-// Scale and minimum of Q4_K group g (0..7, may differ between lanes).
-__device__ __forceinline__ void q4k_scale_min_lane(uint32_t s0, uint32_t s1, uint32_t s2, int g, uint32_t& sc,
-                                                   uint32_t& m) {
-    const uint32_t sh = 8u * (uint32_t)(g & 3);
-    const uint32_t a = (s0 >> sh) & 255u, b = (s1 >> sh) & 255u, mixed = (s2 >> sh) & 255u;
-    const bool lo = g < 4;
-    sc = lo ? (a & 63u) : ((mixed & 15u) | ((a >> 6) << 4));
-    m = lo ? (b & 63u) : ((mixed >> 4) | ((b >> 6) << 4));
-}
 
 __device__ __forceinline__ uint32_t word_of(const uint4& v, int i) {
     return i == 0 ? v.x : i == 1 ? v.y : i == 2 ? v.z : v.w;
