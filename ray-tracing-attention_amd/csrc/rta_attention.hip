@@ -45,6 +45,7 @@ struct AttnArgs {
     float* m_out;
     float* z_out;
     float* ws;
+    uint4* qop;         // matrix-core q operands [nseq][hkv][6][64] (Q4_K keys)
     int64_t capacity;
     int64_t n_slots;    // packets in the array
     int64_t stride;     // packet bytes
@@ -76,18 +77,25 @@ __device__ __forceinline__ void load_dwords(const uint32_t* __restrict__ p, uint
 }
 
 // LDS carve-up of the chunk kernel (dynamic shared memory), in floats.
+// Phase B split: threads per kv head (128 coordinates, 16 or 8 per thread) and the
+// number of position groups that share the workgroup's 256 threads.
+__host__ __device__ constexpr int attn_tpk(int G) { return G == 8 ? 16 : 8; }
+__host__ __device__ constexpr int attn_pg(int hkv, int G) { return 256 / (hkv * attn_tpk(G)); }
+
 struct AttnLds {
-    int sc, w, qs, m, z, scale, ok, v, total;
-    __host__ __device__ AttnLds(int hq, int nblk, int vrow) {
-        sc = 0;                       // [hq][64] scores of the tile      } reused after the
-        w = sc + hq * kTile;          // [hq][65] weights x 2^24 (padded) } tiles as U[hq][128]
-        qs = w + hq * (kTile + 1);    // [hq][8] 16-dim sums of q
-        m = qs + hq * 8;              // [hq] running max
+    int m, z, scale, ok, qs, sc, w, v, total;
+    __host__ __device__ AttnLds(int hq, int hkv, int nblk, int vrow) {
+        m = 0;                        // [hq] running max
         z = m + hq;                   // [hq] running sum
         scale = z + hq;               // [hq] rescale of this tile
         ok = scale + hq;              // [64] position valid (int)
-        v = (ok + kTile + 3) & ~3;    // [nblk][64 vrow + 1] V superblocks, dword aligned; the
-        total = v + nblk * (kTile * vrow + 1);   // +1 puts the superblock regions on different banks
+        qs = ok + kTile;              // [hq][8] 16-dim sums of q
+        sc = (qs + hq * 8 + 3) & ~3;  // [hq][64] scores of the tile             } after the tiles:
+        w = sc + hq * kTile;          // [hq][65] weights x 2^24 (padded)        } U partials
+        v = (w + hq * (kTile + 1) + 3) & ~3;   // [nblk][64 vrow + 1] V superblocks } [PG][hq][128]
+        const int vend = v + nblk * (kTile * vrow + 1);   // +1: superblock regions on different banks
+        const int uend = sc + attn_pg(hkv, hq / hkv) * hq * kHd;
+        total = vend > uend ? vend : uend;
     }
 };
 
@@ -286,6 +294,31 @@ __device__ __forceinline__ QOp make_qop(const float* __restrict__ qg, int lane) 
     return o;
 }
 
+// q operands of one (sequence, kv head), built once and read by every chunk: six
+// 16-byte words per lane (a[0..3], am, rs).
+template <int G>
+__global__ void __launch_bounds__(64) attn_qprep_kernel(const AttnArgs a) {
+    const int kvh = blockIdx.x, s = blockIdx.y, lane = threadIdx.x;
+    const QOp o = make_qop<G>(a.q + ((int64_t)s * a.hq + (int64_t)kvh * G) * kHd, lane);
+    uint4* dst = a.qop + ((int64_t)s * a.hkv + kvh) * 6 * kWave + lane;
+#pragma unroll
+    for (int kb = 0; kb < 4; ++kb) dst[kb * kWave] = __builtin_bit_cast(uint4, o.a[kb]);
+    dst[4 * kWave] = __builtin_bit_cast(uint4, o.am);
+    dst[5 * kWave] = uint4{__builtin_bit_cast(uint32_t, o.rs[0]), __builtin_bit_cast(uint32_t, o.rs[1]), 0u, 0u};
+}
+
+__device__ __forceinline__ QOp load_qop(const uint4* __restrict__ src, int lane) {
+    QOp o;
+    src += lane;
+#pragma unroll
+    for (int kb = 0; kb < 4; ++kb) o.a[kb] = __builtin_bit_cast(h8_t, src[kb * kWave]);
+    o.am = __builtin_bit_cast(h8_t, src[4 * kWave]);
+    const uint4 r = src[5 * kWave];
+    o.rs[0] = __builtin_bit_cast(float, r.x);
+    o.rs[1] = __builtin_bit_cast(float, r.y);
+    return o;
+}
+
 struct KRaw {        // one lane's share of a Q4_K key: header and its two 8-byte segments
     uint4 hdr;
     uint2 c[2];      // chunk 2hh + jc, bytes 8u .. 8u + 7
@@ -393,10 +426,10 @@ template <int KF, int VF, int G, int KPW>
 __global__ void __launch_bounds__(256, 2) attn_chunk_kernel(const AttnArgs a) {
     static_assert(KPW == 0 || KF == RTA_Q4_K, "matrix-core scoring reads Q4_K keys");
     extern __shared__ __align__(16) float lds[];
-    constexpr int DPT = G == 8 ? 8 : 16;      // phase B dims per thread
-    constexpr int TPK = kHd / DPT;            // threads per kv head
+    constexpr int TPK = attn_tpk(G);          // threads per kv head
+    constexpr int DPT = kHd / TPK;            // phase B dims per thread
     constexpr int VROW = Fmt<VF>::kRow;
-    const AttnLds L(a.hq, a.nblk, VROW);
+    const AttnLds L(a.hq, a.hkv, a.nblk, VROW);
     float* s_sc = lds + L.sc;
     float* s_w = lds + L.w;
     float* s_qs = lds + L.qs;
@@ -420,8 +453,9 @@ __global__ void __launch_bounds__(256, 2) attn_chunk_kernel(const AttnArgs a) {
     const int64_t base = a.slot_base[s];
     const float* qs_seq = a.q + (int64_t)s * hq * kHd;
 
-    // prologue: 16-dim sums of q (the minimum / centring terms), running (m, Z)
-    for (int i = tid; i < hq * 8; i += 256) {
+    // prologue: 16-dim sums of q (the minimum / centring terms of vector-ALU scoring),
+    // running (m, Z)
+    for (int i = tid; i < (KPW > 0 ? 0 : hq * 8); i += 256) {
         const float* p = qs_seq + (int64_t)i * 16;
         float acc = 0.0f;
 #pragma unroll
@@ -448,12 +482,13 @@ __global__ void __launch_bounds__(256, 2) attn_chunk_kernel(const AttnArgs a) {
         for (int i = 0; i < DPT; ++i) acc[g][i] = 0.0f;
     }
 
-    // q of this wave's kv heads as matrix-core operands (clamped heads are never used)
+    // q of this wave's kv heads as matrix-core operands, prepared by attn_qprep_kernel
+    // (clamped heads are never used)
     QOp qo[KPW > 0 ? KPW : 1];
     if constexpr (KPW > 0) {
 #pragma unroll
         for (int kl = 0; kl < KPW; ++kl)
-            qo[kl] = make_qop<G>(qs_seq + (int64_t)min(wave + 4 * kl, hkv - 1) * G * kHd, lane);
+            qo[kl] = load_qop(a.qop + ((int64_t)s * hkv + min(wave + 4 * kl, hkv - 1)) * 6 * kWave, lane);
     }
 
     // error bits are raised once at the end: a global atomic inside the loop would
@@ -559,26 +594,44 @@ __global__ void __launch_bounds__(256, 2) attn_chunk_kernel(const AttnArgs a) {
         }
         __syncthreads();
 
-        // ---- softmax of the tile, folded into the running (m, Z)
-        for (int h = wave; h < hq; h += 4) {
-            const float v = s_sc[h * kTile + lane];
-            const float mt = group_max(v, kWave);
-            const float m_old = s_m[h];
-            const float m_new = fmaxf(m_old, mt);
-            float w, scale;
-            if (m_new == -INFINITY) {
-                w = 0.0f;
-                scale = 1.0f;
-            } else {
-                w = expf(v - m_new);
-                scale = expf(m_old - m_new);
+        // ---- softmax of the tile, folded into the running (m, Z).  A wave takes heads
+        // wave + 4i eight at a time so that their reductions interleave.
+        for (int h0 = wave; h0 < hq; h0 += 32) {
+            constexpr int kH = 8;
+            float v[kH], mt[kH];
+#pragma unroll
+            for (int i = 0; i < kH; ++i) {
+                const int h = h0 + 4 * i;
+                v[i] = h < hq ? s_sc[h * kTile + lane] : -INFINITY;
             }
-            const float zt = group_sum(w, kWave);
-            s_w[h * (kTile + 1) + lane] = w * 16777216.0f;
-            if (lane == 0) {
-                s_z[h] = s_z[h] * scale + zt;
-                s_m[h] = m_new;
-                s_scale[h] = scale;
+#pragma unroll
+            for (int i = 0; i < kH; ++i) mt[i] = wave_max_dpp(v[i]);
+            float w[kH], scale[kH], m_new[kH];
+#pragma unroll
+            for (int i = 0; i < kH; ++i) {
+                const int h = h0 + 4 * i;
+                const float m_old = h < hq ? s_m[h] : -INFINITY;
+                m_new[i] = fmaxf(m_old, mt[i]);
+                if (m_new[i] == -INFINITY) {
+                    w[i] = 0.0f;
+                    scale[i] = 1.0f;
+                } else {
+                    w[i] = expf(v[i] - m_new[i]);
+                    scale[i] = expf(m_old - m_new[i]);
+                }
+            }
+#pragma unroll
+            for (int i = 0; i < kH; ++i) {
+                const int h = h0 + 4 * i;
+                const float zt = wave_sum_dpp(w[i]);
+                if (h < hq) {
+                    s_w[h * (kTile + 1) + lane] = w[i] * 16777216.0f;
+                    if (lane == 0) {
+                        s_z[h] = s_z[h] * scale[i] + zt;
+                        s_m[h] = m_new[i];
+                        s_scale[h] = scale[i];
+                    }
+                }
             }
         }
         __syncthreads();
@@ -622,38 +675,47 @@ __global__ void __launch_bounds__(256, 2) attn_chunk_kernel(const AttnArgs a) {
         __syncthreads();
     }
 
-    // ---- combine the position groups (deterministic order) and write the records.
-    // U[h] sits in LDS with its coordinates permuted so that the 8 threads of a row
-    // write 8 adjacent 16-byte chunks: coordinates l0 + 4k + e (l0 = DPT part) at
-    // 4 (k TPK + part) + e, which keeps the stores free of bank conflicts.
-    float* s_u = lds + L.sc;   // [hq][128], over the scores and weights of the last tile
+    // ---- combine the position groups and write the records.  Every group writes its
+    // U to a slot of its own (over the scores, weights and V rows of the last tile);
+    // after one barrier each thread adds the groups of its coordinates in group order.
+    // Coordinates l0 + 4k + e (l0 = DPT part) sit at 4 (k TPK + part) + e, which keeps
+    // the float4 stores free of bank conflicts.
+    float* s_u = lds + L.sc;   // [PG][hq][128]
     // Q4_K: U = acc - 2^-24 sum w' M ;  Q6_K: U = acc - 32 * 2^-24 sum w' D
     const float corr = (VF == RTA_Q4_K) ? (1.0f / 16777216.0f) : (32.0f / 16777216.0f);
-    for (int r = 0; r < PG; ++r) {
-        if (bact && pg == r) {
+    if (bact) {
 #pragma unroll
-            for (int g = 0; g < G; ++g) {
-                float* u = s_u + (bkvh * G + g) * kHd;
+        for (int g = 0; g < G; ++g) {
+            float* u = s_u + ((int64_t)pg * hq + bkvh * G + g) * kHd;
 #pragma unroll
-                for (int k = 0; k < DPT / 4; ++k) {
-                    float4* u4 = reinterpret_cast<float4*>(u + 4 * (k * TPK + part));
-                    float4 v = float4{fmaf(-corr, off[g], acc[g][4 * k + 0]), fmaf(-corr, off[g], acc[g][4 * k + 1]),
-                                      fmaf(-corr, off[g], acc[g][4 * k + 2]), fmaf(-corr, off[g], acc[g][4 * k + 3])};
-                    if (r > 0) {
-                        const float4 o = *u4;
-                        v = float4{v.x + o.x, v.y + o.y, v.z + o.z, v.w + o.w};
-                    }
-                    *u4 = v;
-                }
-            }
+            for (int k = 0; k < DPT / 4; ++k)
+                *reinterpret_cast<float4*>(u + 4 * (k * TPK + part)) =
+                    float4{fmaf(-corr, off[g], acc[g][4 * k + 0]), fmaf(-corr, off[g], acc[g][4 * k + 1]),
+                           fmaf(-corr, off[g], acc[g][4 * k + 2]), fmaf(-corr, off[g], acc[g][4 * k + 3])};
         }
-        __syncthreads();
     }
+    __syncthreads();
     float* rec = a.ws + ((int64_t)s * a.nchunk + c) * hq * kRec;
-    for (int i = tid; i < hq * kHd; i += 256) {
-        const int h = i / kHd, dd = i - h * kHd;
-        const int p = dd / DPT, k = (dd % DPT) >> 2, e = dd & 3;
-        rec[h * kRec + dd] = s_u[h * kHd + 4 * (k * TPK + p) + e];
+    const int64_t gstride = (int64_t)hq * kHd;
+    // two coordinates per thread and round, their loads issued together (the second is
+    // clamped onto the first past the end)
+    const int ncoord = hq * kHd;
+    for (int i0 = tid; i0 < ncoord; i0 += 512) {
+        float v[2];
+        int dst[2];
+#pragma unroll
+        for (int t = 0; t < 2; ++t) {
+            const int i = (i0 + 256 * t < ncoord) ? i0 + 256 * t : i0;
+            const int h = i / kHd, dd = i - h * kHd;
+            const int p = dd / DPT, k = (dd % DPT) >> 2, e = dd & 3;
+            const float* src = s_u + h * kHd + 4 * (k * TPK + p) + e;
+            dst[t] = h * kRec + dd;
+            v[t] = src[0];
+#pragma unroll 4
+            for (int r = 1; r < PG; ++r) v[t] += src[r * gstride];
+        }
+#pragma unroll
+        for (int t = 0; t < 2; ++t) rec[dst[t]] = v[t];
     }
     for (int h = tid; h < hq; h += 256) {
         rec[h * kRec + kHd] = s_m[h];
@@ -776,8 +838,8 @@ static int attn_tiles(int nseq, int max_ctx) {
     return tiles >= 16384 ? 4 : tiles >= 8192 ? 2 : 1;
 }
 
-static int attn_lds_bytes(int hq, int nblk, int fmt_v) {
-    return AttnLds(hq, nblk, fmt_v == RTA_Q4_K ? Fmt<RTA_Q4_K>::kRow : Fmt<RTA_Q6_K>::kRow).total * 4;
+static int attn_lds_bytes(int hq, int hkv, int nblk, int fmt_v) {
+    return AttnLds(hq, hkv, nblk, fmt_v == RTA_Q4_K ? Fmt<RTA_Q4_K>::kRow : Fmt<RTA_Q6_K>::kRow).total * 4;
 }
 
 template <int KF, int VF, int G, int KPW>
@@ -793,12 +855,16 @@ static hipError_t launch_chunk(const AttnArgs& a, int lds, hipStream_t s) {
     return hipGetLastError();
 }
 
-// Q4_K keys of at most 8 kv heads are scored on the matrix cores.
+// Q4_K keys of at most 8 kv heads are scored on the matrix cores, with q operands
+// prepared once per (sequence, kv head).
 template <int KF, int VF, int G>
 static hipError_t launch_chunk_k(const AttnArgs& a, int lds, hipStream_t s) {
     if constexpr (KF == RTA_Q4_K) {
-        if (a.hkv <= 4) return launch_chunk<KF, VF, G, 1>(a, lds, s);
-        if (a.hkv <= 8) return launch_chunk<KF, VF, G, 2>(a, lds, s);
+        if (a.hkv <= 8) {
+            hipLaunchKernelGGL((attn_qprep_kernel<G>), dim3(a.hkv, a.nseq), dim3(kWave), 0, s, a);
+            if (a.hkv <= 4) return launch_chunk<KF, VF, G, 1>(a, lds, s);
+            return launch_chunk<KF, VF, G, 2>(a, lds, s);
+        }
     }
     return launch_chunk<KF, VF, G, 0>(a, lds, s);
 }
@@ -833,11 +899,17 @@ int rta_rope(float* v, int rows, int heads, int hd, int rotary, const int64_t* p
     return hipGetLastError() == hipSuccess ? RTA_OK : RTA_ERR_LAUNCH;
 }
 
-size_t rta_decode_attention_workspace_bytes(int nseq, int hq, int hkv, int hd, int max_ctx) {
-    if (nseq <= 0 || hq <= 0 || hkv <= 0 || hd != kHd || max_ctx <= 0 || hq % hkv) return 0;
+// Chunk records [nseq][nchunk][hq][kRec] floats, then the matrix-core q operands
+// [nseq][hkv][6][64] 16-byte words.
+static size_t attn_record_bytes(int nseq, int hq, int max_ctx) {
     const int64_t chunk = (int64_t)attn_tiles(nseq, max_ctx) * kTile;
     const int64_t nchunk = ((int64_t)max_ctx + chunk - 1) / chunk;
     return (size_t)nseq * (size_t)nchunk * (size_t)hq * kRec * sizeof(float);
+}
+
+size_t rta_decode_attention_workspace_bytes(int nseq, int hq, int hkv, int hd, int max_ctx) {
+    if (nseq <= 0 || hq <= 0 || hkv <= 0 || hd != kHd || max_ctx <= 0 || hq % hkv) return 0;
+    return attn_record_bytes(nseq, hq, max_ctx) + (size_t)nseq * hkv * 6 * kWave * sizeof(uint4);
 }
 
 int rta_decode_attention(const float* q, int nseq, int hq, int hkv, int hd, const void* packets, int fmt_k, int fmt_v,
@@ -856,7 +928,7 @@ int rta_decode_attention(const float* q, int nseq, int hq, int hkv, int hd, cons
     // phase B spreads every kv head over 128 / (8 or 16) threads of one 256-thread workgroup
     if (hkv * (G == 8 ? 16 : 8) > 256) return RTA_ERR_RANGE;
     const int nblk = (hkv * kHd + 255) / 256;
-    const int lds = attn_lds_bytes(hq, nblk, fmt_v);
+    const int lds = attn_lds_bytes(hq, hkv, nblk, fmt_v);
     if (lds > kMaxLds) return RTA_ERR_RANGE;
     if (!host::aligned(q, 4) || !host::aligned(packets, 4) || !host::aligned(slot_base, 8) ||
         !host::aligned(ctx_len, 4) || !host::aligned(out, 4) || (gate && !host::aligned(gate, 4)))
@@ -873,6 +945,7 @@ int rta_decode_attention(const float* q, int nseq, int hq, int hkv, int hd, cons
     a.m_out = m_out;
     a.z_out = z_out;
     a.ws = static_cast<float*>(workspace);
+    a.qop = reinterpret_cast<uint4*>(static_cast<uint8_t*>(workspace) + attn_record_bytes(nseq, hq, max_ctx));
     a.capacity = capacity;
     a.n_slots = n_slots;
     const int kvw = hkv * kHd;

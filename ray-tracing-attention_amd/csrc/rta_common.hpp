@@ -51,6 +51,31 @@ __device__ __forceinline__ float group_max(float v, int width) {
     return v;
 }
 
+template <int CTRL>
+__device__ __forceinline__ float dpp_mov(float v) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), CTRL, 0xF, 0xF, true));
+}
+
+// Sum / max over the 64 lanes of a wave, every lane getting the same result: DPP
+// steps inside each 16-lane row (quad_perm [1,0,3,2], [2,3,0,1], row_half_mirror,
+// row_mirror), then two cross-row shuffles.
+__device__ __forceinline__ float wave_sum_dpp(float v) {
+    v += dpp_mov<0xB1>(v);
+    v += dpp_mov<0x4E>(v);
+    v += dpp_mov<0x141>(v);
+    v += dpp_mov<0x140>(v);
+    v += __shfl_xor(v, 16, kWave);
+    return v + __shfl_xor(v, 32, kWave);
+}
+__device__ __forceinline__ float wave_max_dpp(float v) {
+    v = fmaxf(v, dpp_mov<0xB1>(v));
+    v = fmaxf(v, dpp_mov<0x4E>(v));
+    v = fmaxf(v, dpp_mov<0x141>(v));
+    v = fmaxf(v, dpp_mov<0x140>(v));
+    v = fmaxf(v, __shfl_xor(v, 16, kWave));
+    return fmaxf(v, __shfl_xor(v, 32, kWave));
+}
+
 // Q4_K 6-bit scale/min codes of group g (0..7) from the scale dwords
 // s0 = bytes 4..7, s1 = bytes 8..11, s2 = bytes 12..15 of the superblock
 // (resident_quant.glsl:11-12, q4ScaleMin :39-43).

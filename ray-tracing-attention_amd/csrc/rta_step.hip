@@ -215,21 +215,6 @@ __global__ void __launch_bounds__(128) short_conv_kernel(const float* __restrict
 // block), and the 64 row sums go through DPP steps inside each 16-lane row plus two
 // cross-row shuffles.  With norm_w the gated RMSNorm of op 15 (resident_math.comp:115)
 // is applied to o.
-template <int CTRL>
-__device__ __forceinline__ float dpp_mov(float v) {
-    return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), CTRL, 0xF, 0xF, true));
-}
-
-// Sum over the 64 lanes of a wave; every lane gets the total.
-__device__ __forceinline__ float wave_sum_dpp(float v) {
-    v += dpp_mov<0xB1>(v);    // quad_perm [1,0,3,2]
-    v += dpp_mov<0x4E>(v);    // quad_perm [2,3,0,1]
-    v += dpp_mov<0x141>(v);   // row_half_mirror
-    v += dpp_mov<0x140>(v);   // row_mirror
-    v += __shfl_xor(v, 16, kWave);
-    return v + __shfl_xor(v, 32, kWave);
-}
-
 __global__ void __launch_bounds__(256) delta_rule_kernel(float* __restrict__ state, const float* __restrict__ qkv,
                                                          int qkv_stride, const float* __restrict__ decay,
                                                          const float* __restrict__ beta, int heads,
