@@ -422,8 +422,10 @@ static int run_projection(int fmt, const void* w, const void* w2, int rows, int 
     return RTA_OK;
 }
 
-int tiled_accumulate_partials(int fmt, const void* w, int rows, int cols, const float* x, int batch, float* y,
-                              void* ws, size_t ws_bytes, hipStream_t s, int* nslab) {
+static_assert(kSlabBatch == kMaxBatchTile, "partial blocks hold one batch tile");
+
+int tiled_partials(int fmt, const void* w, int rows, int cols, const float* x, int batch, float* y, bool accumulate,
+                   void* ws, size_t ws_bytes, hipStream_t s, int* nslab) {
     if (!is_tiled(fmt) || batch <= 0 || batch > kMaxBatchTile || !nslab) return RTA_ERR_RANGE;
     if (!ws || ws_bytes < projection_ws(fmt, rows, cols, batch, false)) return RTA_ERR_WORKSPACE;
     const int nbt = batch > 16 ? 2 : 1;
@@ -436,12 +438,22 @@ int tiled_accumulate_partials(int fmt, const void* w, int rows, int cols, const 
     l.y = y;
     l.batch = batch;
     float* part = static_cast<float*>(ws);
-    if ((fmt & 0xff) == RTA_Q4_K) {
-        if (nbt == 1) launch_tiled<RTA_Q4_K, 1, kAccumulate>(p, l, part, nullptr, s);
-        else launch_tiled<RTA_Q4_K, 2, kAccumulate>(p, l, part, nullptr, s);
+    if (accumulate) {
+        if ((fmt & 0xff) == RTA_Q4_K) {
+            if (nbt == 1) launch_tiled<RTA_Q4_K, 1, kAccumulate>(p, l, part, nullptr, s);
+            else launch_tiled<RTA_Q4_K, 2, kAccumulate>(p, l, part, nullptr, s);
+        } else {
+            if (nbt == 1) launch_tiled<RTA_Q6_K, 1, kAccumulate>(p, l, part, nullptr, s);
+            else launch_tiled<RTA_Q6_K, 2, kAccumulate>(p, l, part, nullptr, s);
+        }
     } else {
-        if (nbt == 1) launch_tiled<RTA_Q6_K, 1, kAccumulate>(p, l, part, nullptr, s);
-        else launch_tiled<RTA_Q6_K, 2, kAccumulate>(p, l, part, nullptr, s);
+        if ((fmt & 0xff) == RTA_Q4_K) {
+            if (nbt == 1) launch_tiled<RTA_Q4_K, 1, kStore>(p, l, part, nullptr, s);
+            else launch_tiled<RTA_Q4_K, 2, kStore>(p, l, part, nullptr, s);
+        } else {
+            if (nbt == 1) launch_tiled<RTA_Q6_K, 1, kStore>(p, l, part, nullptr, s);
+            else launch_tiled<RTA_Q6_K, 2, kStore>(p, l, part, nullptr, s);
+        }
     }
     *nslab = p.nslab;
     return hipGetLastError() == hipSuccess ? RTA_OK : RTA_ERR_LAUNCH;

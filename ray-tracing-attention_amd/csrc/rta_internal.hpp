@@ -6,16 +6,26 @@
 
 namespace rta {
 
-// Packed-tile projection y += W x for batch <= 32 rows whose K slabs are left in the
-// workspace for the caller to add: partials [slab][32][rows] fp32 at ws.  *nslab = 1
-// means the kernel added into y itself and nothing is pending.  ws_bytes must cover
-// rta_gemv_workspace_bytes(fmt, rows, cols, batch).
-int tiled_accumulate_partials(int fmt, const void* w, int rows, int cols, const float* x, int batch, float* y,
-                              void* ws, size_t ws_bytes, hipStream_t s, int* nslab);
+constexpr int kSlabBatch = 32;   // batch rows of one K-slab partial block [slab][32][rows]
+
+// Packed-tile projection y (+)= W x for batch <= 32 rows whose K slabs are left in
+// the workspace for the caller to add: partials [slab][32][rows] fp32 at ws.  *nslab = 1
+// means the kernel wrote (accumulate: added into) y itself and nothing is pending.
+// ws_bytes must cover rta_gemv_workspace_bytes(fmt, rows, cols, batch).
+int tiled_partials(int fmt, const void* w, int rows, int cols, const float* x, int batch, float* y, bool accumulate,
+                   void* ws, size_t ws_bytes, hipStream_t s, int* nslab);
 
 // The fused gate/up projection of the SwiGLU MLP alone: act = swiglu(Wg x, Wu x).
 int swiglu_activation(int fmt, const void* wg, const void* wu, int inter, int hidden, const float* x, int batch,
                       float* act, void* ws, size_t ws_bytes, hipStream_t s);
+
+// The middle of a recurrent layer (ops 18-21 and 15) for every (head, sequence):
+// in-projection row r of sequence b = sum_k proj[k * slab_stride + b * row_stride + r]
+// over k < nslab (q | k | v | z | a | b, 4 heads 128 + 2 heads rows), conv window and
+// recurrent state updated in place, gated-norm output to out (row stride out_stride).
+int recurrent_mix(const float* proj, int64_t slab_stride, int row_stride, int nslab, float* conv_state,
+                  const float* conv_w, const float* a_log, const float* dt_bias, float* state, const float* norm_w,
+                  int batch, int heads, float eps, float* out, int out_stride, hipStream_t s);
 
 // hidden[b, :] += sum over slabs k < nslab of part[(k * 32 + b) * width + :] (slab order),
 // then out[b, :] = hidden[b, :] * w / sqrt(mean(hidden[b, :]^2) + eps).  nslab may be 0.

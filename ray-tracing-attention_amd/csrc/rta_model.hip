@@ -294,7 +294,7 @@ int rta_hybrid_decode_step(const rta_hybrid_shape* shape, const rta_hybrid_weigh
         if (!fuse) return rta_gemv(pf, wm, d.D, cols, x, B, w.hidden, RTA_EPI_ACCUMULATE, w.gemm_ws, w.gemm_bytes,
                                    stream);
         int ns = 1;
-        const int rc = tiled_accumulate_partials(pf, wm, d.D, cols, x, B, w.hidden, w.gemm_ws, w.gemm_bytes, s, &ns);
+        const int rc = tiled_partials(pf, wm, d.D, cols, x, B, w.hidden, true, w.gemm_ws, w.gemm_bytes, s, &ns);
         pending = ns > 1 ? ns : 0;
         return rc;
     };
@@ -329,14 +329,27 @@ int rta_hybrid_decode_step(const rta_hybrid_shape* shape, const rta_hybrid_weigh
             ++lf;
         } else {
             // op 2 index 5 (q | k | v | z | a | b), ops 18-21 and 15, op 2 index 2
-            RTA_TRY(rta_gemv(pf, lw.w_in, d.rows_rec, d.D, w.normed, B, w.proj, RTA_EPI_STORE, w.gemm_ws,
-                             w.gemm_bytes, stream));
-            RTA_TRY(rta_delta_gates(w.proj + 4 * d.S, w.proj + 4 * d.S + d.H, d.rows_rec, lw.a_log, lw.dt_bias, B,
-                                    d.H, w.decay, w.beta, stream));
-            RTA_TRY(rta_short_conv(w.proj, d.rows_rec, st.conv + (size_t)lr * B * 3 * d.S * 3, lw.conv_w, B, d.H,
-                                   d.hd, eps, w.conv, stream));
-            RTA_TRY(rta_delta_rule(st.rec + (size_t)lr * B * d.H * d.hd * d.hd, w.conv, 3 * d.S, w.decay, w.beta,
-                                   B, d.H, d.hd, lw.out_norm, w.proj + 3 * d.S, d.rows_rec, eps, w.mix, d.S, stream));
+            if (fuse) {   // the fused middle reads the in-projection's K slabs itself
+                int ns = 1;
+                RTA_TRY(tiled_partials(pf, lw.w_in, d.rows_rec, d.D, w.normed, B, w.proj, false, w.gemm_ws,
+                                       w.gemm_bytes, s, &ns));
+                const bool slabs = ns > 1;
+                RTA_TRY(recurrent_mix(slabs ? static_cast<const float*>(w.gemm_ws) : w.proj,
+                                      (int64_t)kSlabBatch * d.rows_rec, d.rows_rec, slabs ? ns : 1,
+                                      st.conv + (size_t)lr * B * 3 * d.S * 3, lw.conv_w, lw.a_log, lw.dt_bias,
+                                      st.rec + (size_t)lr * B * d.H * d.hd * d.hd, lw.out_norm, B, d.H, eps, w.mix,
+                                      d.S, s));
+            } else {
+                RTA_TRY(rta_gemv(pf, lw.w_in, d.rows_rec, d.D, w.normed, B, w.proj, RTA_EPI_STORE, w.gemm_ws,
+                                 w.gemm_bytes, stream));
+                RTA_TRY(rta_delta_gates(w.proj + 4 * d.S, w.proj + 4 * d.S + d.H, d.rows_rec, lw.a_log, lw.dt_bias, B,
+                                        d.H, w.decay, w.beta, stream));
+                RTA_TRY(rta_short_conv(w.proj, d.rows_rec, st.conv + (size_t)lr * B * 3 * d.S * 3, lw.conv_w, B, d.H,
+                                       d.hd, eps, w.conv, stream));
+                RTA_TRY(rta_delta_rule(st.rec + (size_t)lr * B * d.H * d.hd * d.hd, w.conv, 3 * d.S, w.decay, w.beta,
+                                       B, d.H, d.hd, lw.out_norm, w.proj + 3 * d.S, d.rows_rec, eps, w.mix, d.S,
+                                       stream));
+            }
             RTA_TRY(residual_proj(lw.w_o, d.S, w.mix));
             ++lr;
         }

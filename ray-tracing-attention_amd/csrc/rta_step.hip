@@ -274,6 +274,165 @@ __global__ void __launch_bounds__(256) delta_rule_kernel(float* __restrict__ sta
     }
 }
 
+// ------------------------------------------- recurrent layer, fused middle ----
+// The middle of a recurrent layer for one (head, sequence) in one block, with the
+// arithmetic of delta_gates_kernel, short_conv_kernel and delta_rule_kernel:
+//   the head's in-projection rows (q | k | v | z | a | b of the layer) summed over
+//   the packed readout's K slabs in slab order (as gemm_reduce_kernel adds them);
+//   gates (op 18); short convolution + SiLU + L2 norm of q and k (ops 19, 20); the
+//   delta rule (op 21) and the gated RMSNorm (op 15).
+// Row r of sequence b is sum_k proj[k * slab_stride + b * row_stride + r], k < nslab.
+template <int NS>
+__global__ void __launch_bounds__(256) recurrent_mix_kernel(
+    const float* __restrict__ proj, int64_t slab_stride, int row_stride, int nslab, float* __restrict__ conv_state,
+    const float* __restrict__ conv_w, const float* __restrict__ a_log, const float* __restrict__ dt_bias,
+    float* __restrict__ state, const float* __restrict__ norm_w, int heads, float eps, float* __restrict__ out,
+    int out_stride) {
+    constexpr int hd = 128, kRows = hd / 4;
+    __shared__ float qkv_s[3][hd];
+    __shared__ float z_s[hd];
+    __shared__ float gates_s[2];
+    __shared__ float o_s[hd];
+    __shared__ float red[4];
+    const int h = blockIdx.x, b = blockIdx.y, tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int W = heads * hd, W3 = 3 * W;
+    const float* src = proj + (int64_t)b * row_stride;
+    // in-projection rows: every slab load is issued at once (indices clamped to the
+    // last slab, which is not added twice), then summed in slab order
+    auto load_row = [&](int r, float t[NS]) {
+#pragma unroll
+        for (int k = 0; k < NS; ++k) t[k] = src[(int64_t)min(k, nslab - 1) * slab_stride + r];
+    };
+    auto sum_row = [&](const float t[NS]) {
+        float v = 0.0f;
+#pragma unroll
+        for (int k = 0; k < NS; ++k)
+            if (k < nslab) v += t[k];
+        return v;
+    };
+    // threads 0..127: coordinate c of q, k, v (ops 19, 20); 128..255: the gate z, and
+    // thread 128 the decay / beta inputs (op 18).  Their loads go out before the
+    // recurrent state's, which take the longest and complete in order behind them.
+    const int c = tid & (hd - 1);
+    const bool conv = tid < hd;
+    float raw[3][NS], ab[2][NS];
+    float4 wp[3];
+    float sv[3][3];
+    if (conv) {
+#pragma unroll
+        for (int part = 0; part < 3; ++part) {
+            const int pc = part * W + h * hd + c;
+            load_row(pc, raw[part]);
+            wp[part] = *reinterpret_cast<const float4*>(conv_w + (int64_t)pc * 4);
+            const float* st = conv_state + ((int64_t)b * W3 + pc) * 3;
+            sv[part][0] = st[0];
+            sv[part][1] = st[1];
+            sv[part][2] = st[2];
+        }
+    } else {
+        load_row(W3 + h * hd + c, raw[0]);
+        load_row(4 * W + h, ab[0]);
+        load_row(4 * W + heads + h, ab[1]);
+    }
+    asm volatile("" ::: "memory");   // the state loads stay behind the loads above
+    float2* S = reinterpret_cast<float2*>(state + ((int64_t)b * heads + h) * hd * hd) + wave * kRows * (hd / 2) + lane;
+    float2 s[kRows];
+#pragma unroll
+    for (int i = 0; i < kRows; ++i) s[i] = S[i * (hd / 2)];
+
+    float y[3] = {0.0f, 0.0f, 0.0f};
+    if (conv) {
+#pragma unroll
+        for (int part = 0; part < 3; ++part) {
+            const int pc = part * W + h * hd + c;
+            const float x = sum_row(raw[part]);
+            const float v = wp[part].x * sv[part][0] + wp[part].y * sv[part][1] + wp[part].z * sv[part][2] +
+                            wp[part].w * x;
+            y[part] = silu(v);
+            float* st = conv_state + ((int64_t)b * W3 + pc) * 3;
+            st[0] = sv[part][1];
+            st[1] = sv[part][2];
+            st[2] = x;
+        }
+    } else {
+        z_s[c] = sum_row(raw[0]);
+        if (c == 0) {
+            const float av = sum_row(ab[0]) + dt_bias[h];
+            const float sp = fmaxf(av, 0.0f) + log1pf(expf(-fabsf(av)));   // softplus, resident_common.glsl:80
+            gates_s[0] = expf(-expf(a_log[h]) * sp);
+            gates_s[1] = detector_sigmoid(sum_row(ab[1]));
+        }
+    }
+    // L2 norm of q and k over the head (waves 0 and 1 hold its 128 coordinates)
+#pragma unroll
+    for (int part = 0; part < 2; ++part) {
+        const float ss = wave_sum(y[part] * y[part]);
+        __syncthreads();
+        if (lane == 0 && wave < 2) red[wave] = ss;
+        __syncthreads();
+        y[part] *= 1.0f / sqrtf(red[0] + red[1] + eps);
+    }
+    if (tid < hd) {
+#pragma unroll
+        for (int part = 0; part < 3; ++part) qkv_s[part][tid] = y[part];
+    }
+    __syncthreads();
+
+    // op 21: 4 waves x 32 value rows; lane l holds keys 2l, 2l + 1
+    const float2 q = *reinterpret_cast<const float2*>(&qkv_s[0][2 * lane]);
+    const float2 k = *reinterpret_cast<const float2*>(&qkv_s[1][2 * lane]);
+    const float* vv = &qkv_s[2][wave * kRows];
+    const float dc = gates_s[0], bt = gates_s[1];
+    const float scale = 1.0f / sqrtf((float)hd);
+    float u[kRows];
+#pragma unroll
+    for (int i = 0; i < kRows; ++i) {
+        s[i].x *= dc;
+        s[i].y *= dc;
+        u[i] = wave_sum_dpp(s[i].x * k.x + s[i].y * k.y);
+    }
+    float o[kRows];
+#pragma unroll
+    for (int i = 0; i < kRows; ++i) {
+        const float delta = bt * (vv[i] - u[i]);
+        s[i].x += delta * k.x;
+        s[i].y += delta * k.y;
+        S[i * (hd / 2)] = s[i];
+        o[i] = s[i].x * q.x + s[i].y * q.y;
+    }
+#pragma unroll
+    for (int i = 0; i < kRows; ++i) o[i] = wave_sum_dpp(o[i]);
+    if (lane == 0) {
+#pragma unroll
+        for (int i = 0; i < kRows; ++i) o_s[wave * kRows + i] = o[i] * scale;
+    }
+    __syncthreads();
+    // op 15: gated RMSNorm of o
+    const float v = tid < hd ? o_s[tid] : 0.0f;
+    const float ss = block_sum<4>(v * v, red);
+    const float inv = 1.0f / sqrtf(ss / (float)hd + eps);
+    if (tid < hd) out[(int64_t)b * out_stride + h * hd + tid] = v * inv * norm_w[h * hd + tid] * silu(z_s[tid]);
+}
+
+int recurrent_mix(const float* proj, int64_t slab_stride, int row_stride, int nslab, float* conv_state,
+                  const float* conv_w, const float* a_log, const float* dt_bias, float* state, const float* norm_w,
+                  int batch, int heads, float eps, float* out, int out_stride, hipStream_t s) {
+    if (!proj || !conv_state || !conv_w || !a_log || !dt_bias || !state || !norm_w || !out) return RTA_ERR_NULL;
+    if (batch <= 0 || heads <= 0 || nslab <= 0 || row_stride < 4 * heads * 128 + 2 * heads) return RTA_ERR_SHAPE;
+    if (nslab > 16) return RTA_ERR_RANGE;
+    const dim3 g(heads, batch), blk(256);
+#define RTA_MIX(NS) hipLaunchKernelGGL(recurrent_mix_kernel<NS>, g, blk, 0, s, proj, slab_stride, row_stride, nslab, \
+                                       conv_state, conv_w, a_log, dt_bias, state, norm_w, heads, eps, out, out_stride)
+    if (nslab == 1) RTA_MIX(1);
+    else if (nslab == 2) RTA_MIX(2);
+    else if (nslab <= 4) RTA_MIX(4);
+    else if (nslab <= 8) RTA_MIX(8);
+    else RTA_MIX(16);
+#undef RTA_MIX
+    return hipGetLastError() == hipSuccess ? RTA_OK : RTA_ERR_LAUNCH;
+}
+
 // --------------------------------------------------------- history packer ----
 // op 34 (resident_history_quant.glsl:9-41): one block per sequence quantises its new
 // key and value rows into a history packet (a Q4_K or Q6_K field each) in LDS and
