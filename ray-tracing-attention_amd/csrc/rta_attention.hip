@@ -831,11 +831,11 @@ __global__ void __launch_bounds__(256) rope_kernel(float* __restrict__ v, int ro
     e[1] = (float)(x * sn + y * cs);
 }
 
-// Tiles per chunk: long histories use 2-4 tiles per workgroup so that the per-chunk
-// records stay small next to the history they summarise.
+// Tiles per chunk: 2, and 4 once the grid would cover 16384 tiles, so that the
+// per-chunk records and prologue stay small next to the history they summarise.
 static int attn_tiles(int nseq, int max_ctx) {
     const int64_t tiles = (int64_t)nseq * ((max_ctx + kTile - 1) / kTile);
-    return tiles >= 16384 ? 4 : tiles >= 8192 ? 2 : 1;
+    return tiles >= 16384 ? 4 : 2;
 }
 
 static int attn_lds_bytes(int hq, int hkv, int nblk, int fmt_v) {
