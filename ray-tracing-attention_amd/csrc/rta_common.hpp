@@ -119,6 +119,20 @@ __device__ __forceinline__ uint32_t h2dup(float v) {
     return h | (h << 16);
 }
 
+// A deferred RMSNorm for the readouts: x was written as h * w without the row factor;
+// the readout multiplies row r's result by 1 / sqrt((p.x + p.y + p.z + p.w) / width + eps),
+// p = part[r] the row's four column-chunk sums of squares (16-byte aligned, unused
+// chunks zero).  part == nullptr: no factor.
+struct RowNorm {
+    const float4* part = nullptr;
+    float width = 0.0f;
+    float eps = 0.0f;
+};
+
+__device__ __forceinline__ float row_norm_factor(const RowNorm& rn, float4 p) {
+    return 1.0f / sqrtf((((p.x + p.y) + p.z) + p.w) / rn.width + rn.eps);
+}
+
 // Value i of a GGUF-encoded array, with the reference decoder's fp32 op order
 // (resident_quant.glsl:6-20); contraction is disabled so that (d*sc)*q - dmin*m is
 // rounded exactly as the reference rounds it.

@@ -133,6 +133,7 @@ struct Launch {
     float* y;
     float* partial;
     int batch;
+    RowNorm rn;   // packed readouts only
 };
 
 template <int FMT, int R, int MODE, int KW>
@@ -341,7 +342,7 @@ static hipError_t run_mfma(int fmt, const Launch& l, void* ws, float* pmax, int*
 template <int FMT, int NBT, int MODE>
 static void launch_tiled(const MmaPlan& p, const Launch& l, float* part, float* pmax, hipStream_t s) {
     hipLaunchKernelGGL((gemm_tiled_kernel<FMT, NBT, MODE>), dim3(p.grid), dim3(64 * kGemmWaves), 0, s, l.w, l.w2,
-                       l.rows, l.cols, l.x, l.batch, l.y, part, pmax, p.sb_per_slab, p.wgs_per_slab);
+                       l.rows, l.cols, l.x, l.batch, l.y, part, pmax, p.sb_per_slab, p.wgs_per_slab, l.rn);
 }
 
 // One batch tile (<= 32 rows) over packed weights: the tiled GEMM prepares x in LDS
@@ -379,7 +380,8 @@ static hipError_t run_tiled(int fmt, const Launch& l, void* ws, float* pmax, int
 template <int MODE>
 static int run_projection(int fmt, const void* w, const void* w2, int rows, int cols, const float* x, int batch,
                           float* y, float* partial, int* ntasks_out, int* rows_per_task_out, void* ws,
-                          size_t ws_bytes, hipStream_t s, int path_batch = 0) {
+                          size_t ws_bytes, hipStream_t s, int path_batch = 0, const RowNorm& rn = RowNorm{}) {
+    if (rn.part && !is_tiled(fmt)) return RTA_ERR_FORMAT;   // only the packed readout applies it
     const bool tiled = is_tiled(fmt);
     const int64_t row_bytes = tiled ? 0 : host::row_bytes(fmt, cols);
     int b0 = 0;
@@ -398,6 +400,8 @@ static int run_projection(int fmt, const void* w, const void* w2, int rows, int 
         l.y = y + (int64_t)b0 * rows;
         l.batch = chunk;
         l.partial = partial ? partial + (int64_t)b0 * rows : nullptr;
+        l.rn = rn;
+        if (rn.part) l.rn.part = rn.part + b0;
         hipError_t e;
         if (tiled) {
             if (!ws || ws_bytes < projection_ws(fmt, rows, cols, chunk, MODE == kSwiglu)) return RTA_ERR_WORKSPACE;
@@ -425,7 +429,7 @@ static int run_projection(int fmt, const void* w, const void* w2, int rows, int 
 static_assert(kSlabBatch == kMaxBatchTile, "partial blocks hold one batch tile");
 
 int tiled_partials(int fmt, const void* w, int rows, int cols, const float* x, int batch, float* y, bool accumulate,
-                   void* ws, size_t ws_bytes, hipStream_t s, int* nslab) {
+                   void* ws, size_t ws_bytes, hipStream_t s, int* nslab, const RowNorm& rn) {
     if (!is_tiled(fmt) || batch <= 0 || batch > kMaxBatchTile || !nslab) return RTA_ERR_RANGE;
     if (!ws || ws_bytes < projection_ws(fmt, rows, cols, batch, false)) return RTA_ERR_WORKSPACE;
     const int nbt = batch > 16 ? 2 : 1;
@@ -437,6 +441,7 @@ int tiled_partials(int fmt, const void* w, int rows, int cols, const float* x, i
     l.x = x;
     l.y = y;
     l.batch = batch;
+    l.rn = rn;
     float* part = static_cast<float*>(ws);
     if (accumulate) {
         if ((fmt & 0xff) == RTA_Q4_K) {
@@ -460,9 +465,17 @@ int tiled_partials(int fmt, const void* w, int rows, int cols, const float* x, i
 }
 
 int swiglu_activation(int fmt, const void* wg, const void* wu, int inter, int hidden, const float* x, int batch,
-                      float* act, void* ws, size_t ws_bytes, hipStream_t s) {
+                      float* act, void* ws, size_t ws_bytes, hipStream_t s, const RowNorm& rn) {
     return run_projection<kSwiglu>(fmt, wg, wu, inter, hidden, x, batch, act, nullptr, nullptr, nullptr, ws, ws_bytes,
-                                   s);
+                                   s, 0, rn);
+}
+
+int projection_store(int fmt, const void* w, int rows, int cols, const float* x, int batch, float* y, void* ws,
+                     size_t ws_bytes, hipStream_t s, const RowNorm& rn) {
+    const int rc = check_matrix(fmt, w, rows, cols);
+    if (rc) return rc;
+    return run_projection<kStore>(fmt, w, nullptr, rows, cols, x, batch, y, nullptr, nullptr, nullptr, ws, ws_bytes, s,
+                                  0, rn);
 }
 
 }  // namespace rta
@@ -586,6 +599,17 @@ size_t rta_lm_head_workspace_bytes(int fmt, int vocab, int hidden, int batch) {
 
 int rta_lm_head(int fmt, const void* w, int vocab, int hidden, const float* h, int batch, float margin, float* logits,
                 uint32_t* ids, void* workspace, size_t workspace_bytes, rta_stream_t stream) {
+    return lm_head_rownorm(fmt, w, vocab, hidden, h, batch, margin, logits, ids, workspace, workspace_bytes,
+                           (hipStream_t)stream, RowNorm{});
+}
+
+}  // extern "C"
+
+namespace rta {
+
+int lm_head_rownorm(int fmt, const void* w, int vocab, int hidden, const float* h, int batch, float margin,
+                    float* logits, uint32_t* ids, void* workspace, size_t workspace_bytes, hipStream_t s,
+                    const RowNorm& rn) {
     int rc = check_matrix(fmt, w, vocab, hidden);
     if (rc) return rc;
     if (!h || !logits || !ids) return RTA_ERR_NULL;
@@ -597,7 +621,6 @@ int rta_lm_head(int fmt, const void* w, int vocab, int hidden, const float* h, i
     if (reinterpret_cast<uintptr_t>(h) % 16 || reinterpret_cast<uintptr_t>(logits) % 4 ||
         reinterpret_cast<uintptr_t>(ids) % 4 || reinterpret_cast<uintptr_t>(workspace) % 256)
         return RTA_ERR_ALIGN;
-    hipStream_t s = (hipStream_t)stream;
     float* partial = static_cast<float*>(workspace);
     void* scratch = static_cast<uint8_t*>(workspace) + maxima;
     // Argmax per batch tile, with the plan that tile was written with.
@@ -606,9 +629,11 @@ int rta_lm_head(int fmt, const void* w, int vocab, int hidden, const float* h, i
         const int cap = ((is_kquant(fmt) && batch >= kMfmaMinBatch) || is_tiled(fmt)) ? kMaxBatchTile : 8;
         const int chunk = batch - b0 < cap ? batch - b0 : cap;
         int ntasks = 0, rpt = 1;
+        RowNorm rc_rn = rn;
+        if (rn.part) rc_rn.part = rn.part + b0;
         rc = run_projection<kLogits>(fmt, w, nullptr, vocab, hidden, h + (int64_t)b0 * hidden, chunk,
                                      logits + (int64_t)b0 * vocab, partial + (int64_t)b0 * vocab, &ntasks, &rpt,
-                                     scratch, mma, s, batch);
+                                     scratch, mma, s, batch, rc_rn);
         if (rc) return rc;
         hipLaunchKernelGGL(argmax_margin_kernel, dim3(chunk), dim3(256), 0, s, logits + (int64_t)b0 * vocab,
                            vocab, partial + (int64_t)b0 * vocab, ntasks, rpt, margin, ids + b0);
@@ -617,6 +642,10 @@ int rta_lm_head(int fmt, const void* w, int vocab, int hidden, const float* h, i
     }
     return RTA_OK;
 }
+
+}  // namespace rta
+
+extern "C" {
 
 int64_t rta_pack_bytes(int fmt, int rows, int cols) {
     if (rows <= 0 || cols <= 0 || cols % 256) return -1;

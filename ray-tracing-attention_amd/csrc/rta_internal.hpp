@@ -3,6 +3,9 @@
 #pragma once
 #include <hip/hip_runtime.h>
 #include <stddef.h>
+#include <stdint.h>
+
+#include "rta_common.hpp"
 
 namespace rta {
 
@@ -12,12 +15,22 @@ constexpr int kSlabBatch = 32;   // batch rows of one K-slab partial block [slab
 // the workspace for the caller to add: partials [slab][32][rows] fp32 at ws.  *nslab = 1
 // means the kernel wrote (accumulate: added into) y itself and nothing is pending.
 // ws_bytes must cover rta_gemv_workspace_bytes(fmt, rows, cols, batch).
+// rn (packed readouts only): a deferred RMSNorm factor per batch row, see RowNorm.
 int tiled_partials(int fmt, const void* w, int rows, int cols, const float* x, int batch, float* y, bool accumulate,
-                   void* ws, size_t ws_bytes, hipStream_t s, int* nslab);
+                   void* ws, size_t ws_bytes, hipStream_t s, int* nslab, const RowNorm& rn = RowNorm{});
+
+// y = W x (rta_gemv with the STORE epilogue) with a deferred RMSNorm factor.
+int projection_store(int fmt, const void* w, int rows, int cols, const float* x, int batch, float* y, void* ws,
+                     size_t ws_bytes, hipStream_t s, const RowNorm& rn);
+
+// rta_lm_head with a deferred RMSNorm factor per batch row.
+int lm_head_rownorm(int fmt, const void* w, int vocab, int hidden, const float* h, int batch, float margin,
+                    float* logits, uint32_t* ids, void* workspace, size_t workspace_bytes, hipStream_t s,
+                    const RowNorm& rn);
 
 // The fused gate/up projection of the SwiGLU MLP alone: act = swiglu(Wg x, Wu x).
 int swiglu_activation(int fmt, const void* wg, const void* wu, int inter, int hidden, const float* x, int batch,
-                      float* act, void* ws, size_t ws_bytes, hipStream_t s);
+                      float* act, void* ws, size_t ws_bytes, hipStream_t s, const RowNorm& rn = RowNorm{});
 
 // The middle of a recurrent layer (ops 18-21 and 15) for every (head, sequence):
 // in-projection row r of sequence b = sum_k proj[k * slab_stride + b * row_stride + r]
@@ -32,5 +45,12 @@ int recurrent_mix(const float* proj, int64_t slab_stride, int row_stride, int ns
 // width % 4 == 0; pointers 16-byte aligned.
 int residual_rmsnorm(float* hidden, const float* part, int nslab, const float* w, int batch, int width, float eps,
                      float* out, hipStream_t s);
+
+// The same residual add, but the normalisation is left to the readouts that take out:
+// out[b, :] = hidden[b, :] * w (no row factor) and ss[4 b + c] = sum of hidden^2 over
+// column chunk c of 1024 (unused entries zero), for a RowNorm {ss, width, eps}.
+// width <= 4096; ss 16-byte aligned, 4 batch floats.
+int residual_norm_deferred(float* hidden, const float* part, int nslab, const float* w, int batch, int width,
+                           float* out, float* ss, hipStream_t s);
 
 }  // namespace rta

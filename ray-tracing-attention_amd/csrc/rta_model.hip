@@ -160,7 +160,7 @@ State carve_state(const Dims& d, void* p, size_t* bytes) {
 }
 
 struct Work {
-    float *hidden, *normed, *proj, *q, *conv, *decay, *beta, *mix, *act, *logits;
+    float *hidden, *normed, *proj, *q, *conv, *decay, *beta, *mix, *act, *logits, *rms;
     int64_t *pos, *slots;
     int32_t* visible;
     void *attn_ws, *lm_ws, *gemm_ws;
@@ -192,6 +192,7 @@ Work carve_work(const rta_hybrid_shape* s, const Dims& d, void* p, size_t* bytes
     w.mix = c.take<float>(B * std::max(d.hq * d.hd, d.S));
     w.act = c.take<float>(B * d.FF);
     w.logits = c.take<float>(B * d.V);
+    w.rms = c.take<float>(B * 4);   // per-chunk sums of squares of the deferred norms
     w.pos = c.take<int64_t>(B);
     w.slots = c.take<int64_t>(B * std::max(1, d.nfull));
     w.visible = c.take<int32_t>(B);
@@ -298,10 +299,22 @@ int rta_hybrid_decode_step(const rta_hybrid_shape* shape, const rta_hybrid_weigh
         pending = ns > 1 ? ns : 0;
         return rc;
     };
-    auto norm = [&](const float* nw) -> int {
+    // With packed readouts the RMSNorm factor of each row is applied by the readout that
+    // takes w.normed (h * w is written and rn describes the factor): the residual add
+    // then spreads over several blocks per row.  deferred = false: w.normed is final.
+    RowNorm rn{};
+    auto norm = [&](const float* nw, bool deferred) -> int {
+        rn = RowNorm{};
+        deferred = deferred && d.D <= 4096;
         if (!fuse) return rta_rmsnorm(w.hidden, nw, B, d.D, eps, w.normed, stream);
-        const int rc = residual_rmsnorm(w.hidden, static_cast<const float*>(w.gemm_ws), pending, nw, B, d.D, eps,
-                                        w.normed, s);
+        const float* part = static_cast<const float*>(w.gemm_ws);
+        int rc;
+        if (deferred) {
+            rc = residual_norm_deferred(w.hidden, part, pending, nw, B, d.D, w.normed, w.rms, s);
+            rn = RowNorm{reinterpret_cast<const float4*>(w.rms), (float)d.D, eps};
+        } else {
+            rc = residual_rmsnorm(w.hidden, part, pending, nw, B, d.D, eps, w.normed, s);
+        }
         pending = 0;
         return rc;
     };
@@ -309,11 +322,11 @@ int rta_hybrid_decode_step(const rta_hybrid_shape* shape, const rta_hybrid_weigh
     int lf = 0, lr = 0;
     for (int l = 0; l < d.L; ++l) {
         const rta_hybrid_layer& lw = weights->layers[l];
-        RTA_TRY(norm(lw.norm_in));
+        RTA_TRY(norm(lw.norm_in, fuse));
         if (is_full(shape, l)) {
             // op 2 index 5 (q | k | v), ops 14 + 3, op 34, attention, op 2 index 2
-            RTA_TRY(rta_gemv(pf, lw.w_in, d.rows_full, d.D, w.normed, B, w.proj, RTA_EPI_STORE, w.gemm_ws,
-                             w.gemm_bytes, stream));
+            RTA_TRY(projection_store(pf, lw.w_in, d.rows_full, d.D, w.normed, B, w.proj, w.gemm_ws, w.gemm_bytes, s,
+                                     rn));
             hipLaunchKernelGGL(qk_norm_rope_kernel, dim3((d.hq + d.hkv + 3) / 4, B), dim3(256), 0, s, w.proj,
                                d.rows_full, d.hq, d.hkv, lw.q_norm, lw.k_norm, eps, w.pos, shape->rope_rotary,
                                shape->rope_theta, w.q);
@@ -332,7 +345,7 @@ int rta_hybrid_decode_step(const rta_hybrid_shape* shape, const rta_hybrid_weigh
             if (fuse) {   // the fused middle reads the in-projection's K slabs itself
                 int ns = 1;
                 RTA_TRY(tiled_partials(pf, lw.w_in, d.rows_rec, d.D, w.normed, B, w.proj, false, w.gemm_ws,
-                                       w.gemm_bytes, s, &ns));
+                                       w.gemm_bytes, s, &ns, rn));
                 const bool slabs = ns > 1;
                 RTA_TRY(recurrent_mix(slabs ? static_cast<const float*>(w.gemm_ws) : w.proj,
                                       (int64_t)kSlabBatch * d.rows_rec, d.rows_rec, slabs ? ns : 1,
@@ -354,9 +367,10 @@ int rta_hybrid_decode_step(const rta_hybrid_shape* shape, const rta_hybrid_weigh
             ++lr;
         }
         // op 1 index 1, then the SwiGLU MLP with the residual add (executeMLP)
-        RTA_TRY(norm(lw.norm_post));
+        RTA_TRY(norm(lw.norm_post, fuse));
         if (fuse) {
-            RTA_TRY(swiglu_activation(pf, lw.w_gate, lw.w_up, d.FF, d.D, w.normed, B, w.act, w.gemm_ws, w.gemm_bytes, s));
+            RTA_TRY(swiglu_activation(pf, lw.w_gate, lw.w_up, d.FF, d.D, w.normed, B, w.act, w.gemm_ws, w.gemm_bytes, s,
+                                      rn));
             RTA_TRY(residual_proj(lw.w_down, d.FF, w.act));
         } else {
             RTA_TRY(rta_mlp_swiglu(pf, lw.w_gate, pf, lw.w_up, pf, lw.w_down, d.D, d.FF, w.normed, B, w.act, w.hidden,
@@ -364,9 +378,9 @@ int rta_hybrid_decode_step(const rta_hybrid_shape* shape, const rta_hybrid_weigh
         }
     }
     // op 1 index 2, then the readout (Resident::word): logits and the next tokens
-    RTA_TRY(norm(weights->norm_final));
-    RTA_TRY(rta_lm_head(shape->fmt_lm, weights->lm_head, d.V, d.D, w.normed, B, shape->margin,
-                        logits_out ? logits_out : w.logits, tokens, w.lm_ws, w.lm_bytes, stream));
+    RTA_TRY(norm(weights->norm_final, fuse && (shape->fmt_lm & RTA_TILED) && B <= 32));
+    RTA_TRY(lm_head_rownorm(shape->fmt_lm, weights->lm_head, d.V, d.D, w.normed, B, shape->margin,
+                            logits_out ? logits_out : w.logits, tokens, w.lm_ws, w.lm_bytes, s, rn));
 #undef RTA_TRY
     return RTA_OK;
 }

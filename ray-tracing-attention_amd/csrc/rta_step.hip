@@ -122,6 +122,59 @@ int residual_rmsnorm(float* hidden, const float* part, int nslab, const float* w
     return hipGetLastError() == hipSuccess ? RTA_OK : RTA_ERR_LAUNCH;
 }
 
+// The residual add of residual_rmsnorm_kernel with the normalisation deferred to the
+// readouts: block (column chunk c of 1024, row b) adds the K slabs, writes hidden and
+// out = hidden * w, and the chunk's sum of squares to ss[4 b + c] (the four entries of
+// a row, unused ones zero).  The row total is never needed here, so a row of up to
+// 4096 columns spreads over up to 4 blocks.
+constexpr int kNormChunk = 1024;
+
+__global__ void __launch_bounds__(256) residual_norm_deferred_kernel(float* __restrict__ hidden,
+                                                                     const float* __restrict__ part, int nslab,
+                                                                     const float* __restrict__ w, int width,
+                                                                     float* __restrict__ out, float* __restrict__ ss) {
+    __shared__ float red[4];
+    const int c = blockIdx.x, b = blockIdx.y, n4 = width >> 2;
+    const int i = c * (kNormChunk / 4) + threadIdx.x;
+    float sq = 0.0f;
+    if (i < n4) {
+        float4* hr = reinterpret_cast<float4*>(hidden + (int64_t)b * width);
+        float4 v = hr[i];
+#pragma unroll 4
+        for (int k = 0; k < nslab; ++k) {
+            const float4 p = reinterpret_cast<const float4*>(part + ((int64_t)k * 32 + b) * width)[i];
+            v.x += p.x;
+            v.y += p.y;
+            v.z += p.z;
+            v.w += p.w;
+        }
+        if (nslab > 0) hr[i] = v;
+        sq = v.x * v.x + v.y * v.y + v.z * v.z + v.w * v.w;
+        const float4 g = reinterpret_cast<const float4*>(w)[i];
+        reinterpret_cast<float4*>(out + (int64_t)b * width)[i] = float4{v.x * g.x, v.y * g.y, v.z * g.z, v.w * g.w};
+    }
+    sq = block_sum<4>(sq, red);
+    if (threadIdx.x == 0) {
+        ss[4 * b + c] = sq;
+        if (c == 0)
+            for (int z = gridDim.x; z < 4; ++z) ss[4 * b + z] = 0.0f;
+    }
+}
+
+int residual_norm_deferred(float* hidden, const float* part, int nslab, const float* w, int batch, int width,
+                           float* out, float* ss, hipStream_t s) {
+    if (!hidden || !w || !out || !ss || (nslab > 0 && !part)) return RTA_ERR_NULL;
+    if (batch <= 0 || batch > 32 || width <= 0 || width % 4 || width > 4 * kNormChunk || nslab < 0)
+        return RTA_ERR_SHAPE;
+    if (!host::aligned(ss, 16)) return RTA_ERR_ALIGN;
+    if (!host::aligned(hidden, 16) || !host::aligned(w, 16) || !host::aligned(out, 16) ||
+        (part && !host::aligned(part, 16)))
+        return RTA_ERR_ALIGN;
+    hipLaunchKernelGGL(residual_norm_deferred_kernel, dim3((width + kNormChunk - 1) / kNormChunk, batch),
+                       dim3(kNormChunk / 4), 0, s, hidden, part, nslab, w, width, out, ss);
+    return hipGetLastError() == hipSuccess ? RTA_OK : RTA_ERR_LAUNCH;
+}
+
 // ------------------------------------------------------------- head norms ----
 // ops 14 / 15 / 20 (resident_math.comp:113-115,139-140), in place: one wave per
 // (row, head) of hd = 64 * VPL values:

@@ -123,13 +123,18 @@ struct XStage {
     static constexpr int kGroups = 64 * kGemmWaves / 32;            // (row, superblock) pairs per round
     static constexpr int kRounds = Smem::kSb * kRows / kGroups;
     float v[kRounds][8];
+    float4 rnp[kRounds];   // deferred-norm sums of the round's row
 
-    __device__ __forceinline__ void load(const float* __restrict__ x, int cols, int batch, int sb0, int nsb) {
+    __device__ __forceinline__ void load(const float* __restrict__ x, int cols, int batch, int sb0, int nsb,
+                                         const RowNorm& rn) {
         const int grp = threadIdx.x >> 5, t = threadIdx.x & 31;
         const int npairs = nsb * kRows;                           // a multiple of kGroups
 #pragma unroll
         for (int k = 0; k < kRounds; ++k) {
             const int pr = grp + k * kGroups, sbl = pr / kRows, r = pr - sbl * kRows;
+            // unconditional (x's first float4 stands in when there is no deferred norm):
+            // a guarded load would wait on the spot
+            rnp[k] = rn.part ? rn.part[r < batch ? r : batch - 1] : *reinterpret_cast<const float4*>(x);
             if (pr < npairs && r < batch) {
                 const float4* src =
                     reinterpret_cast<const float4*>(x + (int64_t)r * cols + (int64_t)(sb0 + sbl) * 256 + 8 * t);
@@ -143,7 +148,7 @@ struct XStage {
         }
     }
 
-    __device__ __forceinline__ void store(Smem& sm, int batch, int nsb) const {
+    __device__ __forceinline__ void store(Smem& sm, int batch, int nsb, const RowNorm& rn) const {
         const int grp = threadIdx.x >> 5, t = threadIdx.x & 31;
         const int npairs = nsb * kRows;
 #pragma unroll
@@ -157,7 +162,10 @@ struct XStage {
             int e = 0;
             if (m > 0.0f && isfinite(m)) (void)frexpf(m, &e);
             const float sc = ldexpf(1.0f, 14 - e);
-            if (t == 0) sm.inv[sbl][r] = r < batch ? ldexpf(1.0f, e - 14) : 0.0f;
+            if (t == 0) {
+                const float f = rn.part ? row_norm_factor(rn, rnp[k]) : 1.0f;
+                sm.inv[sbl][r] = r < batch ? ldexpf(1.0f, e - 14) * f : 0.0f;
+            }
             constexpr int perm[8] = {0, 2, 1, 3, 4, 6, 5, 7};
             _Float16 hi[8], lo[8];
             float sum8 = 0.0f;
@@ -205,7 +213,7 @@ template <int FMT, int NBT, int MODE>
 __global__ void __launch_bounds__(64 * kGemmWaves) gemm_tiled_kernel(
     const uint8_t* __restrict__ w, const uint8_t* __restrict__ w2, const int rows, const int cols,
     const float* __restrict__ x, const int batch, float* __restrict__ y, float* __restrict__ part,
-    float* __restrict__ pmax, const int sb_per_slab, const int wgs_per_slab) {
+    float* __restrict__ pmax, const int sb_per_slab, const int wgs_per_slab, const RowNorm rn) {
     constexpr bool kQ4 = FMT == RTA_Q4_K;
     using F = TileFmt<FMT>;
     using Raw = typename F::Raw;
@@ -246,14 +254,14 @@ __global__ void __launch_bounds__(64 * kGemmWaves) gemm_tiled_kernel(
     // x loads first (vector-memory loads complete in order, so the x slab is not held
     // up behind the weights), then DEPTH - 1 superblocks of weights, then the x prep.
     XStage<FMT, NBT> xs;
-    xs.load(x, cols, batch, sb0, nsb);
+    xs.load(x, cols, batch, sb0, nsb, rn);
     constexpr int DEPTH = 3;   // two superblocks load while the current one multiplies
     Raw buf[DEPTH][2];
     if (nit > 0) {
 #pragma unroll
         for (int d = 0; d < DEPTH - 1; ++d) load_w(min(d, nit - 1), buf[d]);
     }
-    xs.store(sm, batch, nsb);
+    xs.store(sm, batch, nsb, rn);
     __syncthreads();
 
     f4_t acc[2][NBT];
