@@ -724,6 +724,357 @@ __global__ void __launch_bounds__(256, 2) attn_chunk_kernel(const AttnArgs a) {
     if (err) raise_error(err);
 }
 
+// ---- matrix-core attention for Q4_K keys and Q6_K values -------------------------
+// One wave owns one K/V superblock of the (sequence, chunk): both of its kv heads
+// (KPW = 2, hkv > 4), or one half of it (KPW = 1: kv head `wave`, superblock wave / 2),
+// with all G query heads of each, from the loads through the scores, the softmax (in
+// registers) and P V to the records, so the waves of a workgroup never wait for one
+// another.  Per tile of 64 positions:
+//   scores   S^T = Q K^T on the matrix cores (score_q4k_mma), lane = position in the
+//            loads; the key header is read once for both halves.
+//   staging  the lane's V superblock is written to the wave's LDS region transposed,
+//            dword i of position p at [i][p], so that a lane reads one dword of 8
+//            consecutive positions with two 16-byte reads.
+//   softmax  per query head over the tile's 64 positions (4 per lane, 16-lane rows),
+//            folded into the running (m, Z) held in registers.
+//   P V      U^T = V^T P^T on the matrix cores, k = 32 positions per instruction:
+//     A (16 x 32)  row r, position p: e = sc (c - 32), code times 8-bit sub-block
+//                  scale (an integer, |e| <= 4096), as binary16 hi = f16(e) and
+//                  lo = e - hi (exact: one fma), one instruction each.  Lane r reads
+//                  ql dword r and qh dword r & 7 of the head half, which hold the
+//                  codes of 8 dims per position: tile (b, nib), row r is head dim
+//                  32 q + 4 (r & 7) + b with q = 2 nib + (r >= 8)
+//                  (resident_quant.glsl:16-19).
+//     B (32 x 16)  column 2g + part, position p: x = w_g(p) d(p) 2^S as binary16 hi
+//                  (part 0) / lo (part 1): w the softmax weight exp(s - m), d the
+//                  superblock scale, S a per-tile power of two with max |d| 2^S in
+//                  [2^13, 2^14).
+//     D (16 x 16)  row r, column 2g + part: sum_p e x, so U_g = (D_2g + D_2g+1) 2^-S.
+//   The online rescale exp(m_old - m_new) 2^(S_new - S_old) is applied to D before
+//   the tile's products.  The records are those of attn_chunk_kernel.
+constexpr int kVtStride = kTile + 4;                        // dwords per transposed row
+constexpr int kVtRows = (Fmt<RTA_Q6_K>::kBytes + 3) / 4;    // 53 dwords of a superblock
+struct MmaWaveLds {                                         // one wave's region, dwords
+    static constexpr int vt = 0;                            // [53][68] V, transposed
+    static constexpr int w = kVtRows * kVtStride;           // [2][8][68] softmax weights
+    static constexpr int f = w + 2 * 8 * kVtStride;         // [2][8] rescale factors
+    static constexpr int total = f + 16;
+};
+static_assert(MmaWaveLds::w % 4 == 0 && MmaWaveLds::total % 4 == 0, "16-byte aligned rows");
+constexpr int kMmaLdsBytes = 4 * MmaWaveLds::total * 4;
+
+// max / sum over the 16 lanes of each row (quad_perm [1,0,3,2], [2,3,0,1],
+// row_half_mirror, row_mirror)
+__device__ __forceinline__ float row16_max(float v) {
+    v = fmaxf(v, dpp_mov<0xB1>(v));
+    v = fmaxf(v, dpp_mov<0x4E>(v));
+    v = fmaxf(v, dpp_mov<0x141>(v));
+    return fmaxf(v, dpp_mov<0x140>(v));
+}
+__device__ __forceinline__ float row16_sum(float v) {
+    v += dpp_mov<0xB1>(v);
+    v += dpp_mov<0x4E>(v);
+    v += dpp_mov<0x141>(v);
+    return v + dpp_mov<0x140>(v);
+}
+
+__device__ __forceinline__ uint32_t pk_add_f16(uint32_t a, uint32_t b) {
+    return __builtin_bit_cast(uint32_t, __builtin_bit_cast(h2v_t, a) + __builtin_bit_cast(h2v_t, b));
+}
+__device__ __forceinline__ uint32_t pk_fma_f16(uint32_t a, uint32_t b, uint32_t c) {
+    return __builtin_bit_cast(uint32_t, __builtin_elementwise_fma(__builtin_bit_cast(h2v_t, a),
+                                                                  __builtin_bit_cast(h2v_t, b),
+                                                                  __builtin_bit_cast(h2v_t, c)));
+}
+
+template <int G, int KPW>
+__global__ void __launch_bounds__(256, 2) attn_chunk_mma_kernel(const AttnArgs a) {
+    extern __shared__ __align__(16) float lds[];
+    const int c = blockIdx.x, s = blockIdx.y;
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int hkv = a.hkv;
+    const int kv0 = KPW == 2 ? 2 * wave : wave;    // first kv head of the wave
+    const int blk = KPW == 2 ? wave : wave >> 1;    // its K/V superblock
+    if (kv0 >= hkv) return;                         // no workgroup barrier in this kernel
+    const bool two = KPW == 2 && kv0 + 1 < hkv;     // uniform
+    const int64_t Lc = a.ctx_len[s];
+    const int64_t visible = Lc < a.capacity ? Lc : a.capacity;
+    const int64_t chunk = (int64_t)a.nt * kTile;
+    const int64_t first = (int64_t)c * chunk;
+    if (visible <= 0 || first >= visible) return;
+    const int n_all = (int)(visible - first < chunk ? visible - first : chunk);
+    const int64_t p0 = Lc - visible + first;
+    const int64_t base = a.slot_base[s];
+    uint32_t* vt = reinterpret_cast<uint32_t*>(lds) + wave * MmaWaveLds::total;
+    float* s_w = lds + wave * MmaWaveLds::total + MmaWaveLds::w;
+    float* s_f = lds + wave * MmaWaveLds::total + MmaWaveLds::f;
+    auto hh_of = [&](int kl) { return KPW == 2 ? kl : (wave & 1); };
+
+    const int u = lane >> 4, col = lane & 15;   // row of 16 lanes, column in it
+
+    float m_run[KPW][2], z_run[KPW][2];         // heads 2u + eh of each kv head
+    f4_t D[KPW][8];
+#pragma unroll
+    for (int kl = 0; kl < KPW; ++kl) {
+#pragma unroll
+        for (int eh = 0; eh < 2; ++eh) {
+            m_run[kl][eh] = -INFINITY;
+            z_run[kl][eh] = 0.0f;
+        }
+#pragma unroll
+        for (int t = 0; t < 8; ++t) D[kl][t] = f4_t{0.0f, 0.0f, 0.0f, 0.0f};
+    }
+    int S_cur = 0;
+
+    // per-lane constants of the P V operands (A row r = col)
+    const int qsel = col >= 8 ? 1 : 0;
+    const uint32_t sbyte = (uint32_t)(((col & 7) >> 2) + 2 * qsel);   // sub-block scale byte
+    const uint32_t sc_sel = sbyte | (0x0Cu << 8) | ((4u + sbyte) << 16) | (0x0Cu << 24);
+    // qh bits 2q, 2q + 1 to bits 4, 5: rotate left by 4 - 2q (alignbit rotates right)
+    const uint32_t rot[2] = {(32u - (uint32_t)((4 - 2 * qsel) & 31)) & 31u,
+                             (32u - (uint32_t)((4 - 2 * (2 + qsel)) & 31)) & 31u};
+
+    uint32_t err = 0;
+    const float inv = 1.0f / sqrtf((float)kHd);
+    const int ntile = (n_all + kTile - 1) / kTile;
+    for (int tile = 0; tile < ntile; ++tile) {
+        const int n = min(kTile, n_all - tile * kTile);
+        // slot of the lane's position; past the tile's end the tile's last position
+        // (its lines are read anyway), out of range slot 0
+        const int j = lane;
+        bool ok = j < n;
+        int64_t slot = base + (p0 + tile * kTile + min(j, n - 1)) % a.capacity;
+        if (slot < 0 || slot >= a.n_slots) {
+            if (ok) err |= RTA_DEVERR_HITS;
+            ok = false;
+            slot = 0;
+        }
+        // V superblock first (it is needed first), then the keys of the 4 x 16
+        // positions (lane: position 16 rt + col, segment u)
+        VStage<RTA_Q6_K> vst;
+        vst.load(a.packets + slot * a.stride + a.v_offset + (int64_t)blk * Fmt<RTA_Q6_K>::kBytes);
+        uint4 hdr[4];
+        uint2 kc[KPW][4][2];
+        bool okr[4];
+#pragma unroll
+        for (int rt = 0; rt < 4; ++rt) {
+            const int src = 16 * rt + col;
+            const uint32_t lo = (uint32_t)__shfl((int)(uint32_t)slot, src, kWave);
+            const uint32_t hi = (uint32_t)__shfl((int)(uint32_t)((uint64_t)slot >> 32), src, kWave);
+            okr[rt] = __shfl(ok ? 1 : 0, src, kWave) != 0;
+            const uint8_t* kp = a.packets + (int64_t)(((uint64_t)hi << 32) | lo) * a.stride +
+                                (int64_t)blk * Fmt<RTA_Q4_K>::kBytes;
+            __builtin_memcpy(&hdr[rt], kp, 16);
+#pragma unroll
+            for (int kl = 0; kl < KPW; ++kl)
+#pragma unroll
+                for (int jc = 0; jc < 2; ++jc)
+                    __builtin_memcpy(&kc[kl][rt][jc], kp + 16 + 32 * (2 * hh_of(kl) + jc) + 8 * u, 8);
+        }
+        // stage V transposed; the lane's d for the tile's scale 2^S
+        float dabs;
+        {
+#pragma unroll
+            for (int i = 0; i < kVtRows; ++i)
+                vt[i * kVtStride + j] = funnel(vst.raw[i], i + 1 < VStage<RTA_Q6_K>::kRaw ? vst.raw[i + 1] : 0u, vst.mis);
+            dabs = ok ? fabsf(half_lo(funnel(vst.raw[kVtRows - 1], 0u, vst.mis))) : 0.0f;
+        }
+        // q operands of the wave's kv heads (prepared by attn_qprep_kernel), reread per
+        // tile from the cache once the V registers are free
+        asm volatile("" ::: "memory");
+        QOp qo[KPW];
+#pragma unroll
+        for (int kl = 0; kl < KPW; ++kl)
+            qo[kl] = load_qop(a.qop + ((int64_t)s * hkv + min(kv0 + kl, hkv - 1)) * 6 * kWave, lane);
+        // scores of the wave's kv heads, heads 2u + eh, positions 16 rt + col
+        float sv[KPW][4][2];
+#pragma unroll
+        for (int kl = 0; kl < KPW; ++kl) {
+            if (kl == 1 && !two) break;
+#pragma unroll
+            for (int rt = 0; rt < 4; ++rt) {
+                KRaw kr;
+                kr.hdr = hdr[rt];
+                kr.c[0] = kc[kl][rt][0];
+                kr.c[1] = kc[kl][rt][1];
+                float sc2[2];
+                score_q4k_mma<G>(qo[kl], kr, hh_of(kl), u, inv, sc2);
+#pragma unroll
+                for (int eh = 0; eh < 2; ++eh) {
+                    const bool live = okr[rt] && 2 * u + eh < G;
+                    if (live && !isfinite(sc2[eh])) err |= RTA_DEVERR_DETECTOR;
+                    sv[kl][rt][eh] = live ? sc2[eh] : -INFINITY;
+                }
+            }
+        }
+        // the tile's power of two: max |d| 2^S in [2^13, 2^14) (kept when every d is 0)
+        const float dmax = wave_max_dpp(dabs);
+        int S_new = S_cur;
+        if (dmax > 0.0f && isfinite(dmax)) {
+            int e;
+            (void)frexpf(dmax, &e);
+            S_new = 14 - e;
+        }
+        if (tile == 0) S_cur = S_new;
+        // softmax over the tile, folded into (m, Z); weights and rescale factors to LDS
+#pragma unroll
+        for (int kl = 0; kl < KPW; ++kl) {
+            if (kl == 1 && !two) break;
+#pragma unroll
+            for (int eh = 0; eh < 2; ++eh) {
+                const int g = 2 * u + eh;
+                float mx = fmaxf(fmaxf(sv[kl][0][eh], sv[kl][1][eh]), fmaxf(sv[kl][2][eh], sv[kl][3][eh]));
+                mx = row16_max(mx);
+                const float m_new = fmaxf(m_run[kl][eh], mx);
+                float w[4], sf;
+                if (m_new == -INFINITY) {
+                    sf = 1.0f;
+#pragma unroll
+                    for (int rt = 0; rt < 4; ++rt) w[rt] = 0.0f;
+                } else {
+                    sf = expf(m_run[kl][eh] - m_new);
+#pragma unroll
+                    for (int rt = 0; rt < 4; ++rt) w[rt] = expf(sv[kl][rt][eh] - m_new);
+                }
+                const float zt = row16_sum((w[0] + w[1]) + (w[2] + w[3]));
+                z_run[kl][eh] = z_run[kl][eh] * sf + zt;
+                m_run[kl][eh] = m_new;
+                if (g < G) {
+#pragma unroll
+                    for (int rt = 0; rt < 4; ++rt) s_w[(kl * 8 + g) * kVtStride + 16 * rt + col] = w[rt];
+                    if (col == 0) s_f[kl * 8 + g] = ldexpf(sf, S_new - S_cur);
+                }
+            }
+        }
+        __builtin_amdgcn_wave_barrier();
+        // rescale D (column 2g + part: head g)
+        const int gcol = col >> 1;
+#pragma unroll
+        for (int kl = 0; kl < KPW; ++kl) {
+            if (kl == 1 && !two) break;
+            const float fl = s_f[kl * 8 + gcol];
+#pragma unroll
+            for (int t = 0; t < 8; ++t) D[kl][t] *= fl;
+        }
+        S_cur = S_new;
+        // P V, 32 positions per step: this lane's positions 32 ks + 8 u + i
+#pragma unroll 1
+        for (int ks = 0; ks < 2; ++ks) {
+            const int pk0 = 32 * ks + 8 * u;
+            float dS[8];
+            {
+                const uint4 d0 = *reinterpret_cast<const uint4*>(vt + 52 * kVtStride + pk0);
+                const uint4 d1 = *reinterpret_cast<const uint4*>(vt + 52 * kVtStride + pk0 + 4);
+                const uint32_t dw[8] = {d0.x, d0.y, d0.z, d0.w, d1.x, d1.y, d1.z, d1.w};
+#pragma unroll
+                for (int i = 0; i < 8; ++i) dS[i] = ldexpf(half_lo(dw[i]), S_cur);
+            }
+#pragma unroll
+            for (int kl = 0; kl < KPW; ++kl) {
+                if (kl == 1 && !two) break;
+                const int hh = hh_of(kl);
+                // B: column col = head gcol, part col & 1
+                h8_t bop;
+                {
+                    const float* wr = s_w + (kl * 8 + gcol) * kVtStride + pk0;
+                    const float4 w0 = *reinterpret_cast<const float4*>(wr);
+                    const float4 w1 = *reinterpret_cast<const float4*>(wr + 4);
+                    const float wv[8] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
+                    const bool live = gcol < G, part = (col & 1) != 0;
+#pragma unroll
+                    for (int i = 0; i < 8; ++i) {
+                        const float x = wv[i] * dS[i];
+                        const _Float16 h = (_Float16)x;
+                        const _Float16 l = (_Float16)(x - (float)h);
+                        bop[i] = live ? (part ? l : h) : (_Float16)0.0f;
+                    }
+                }
+                // A: ql dword col, qh dword col & 7, sub-block scale dwords of nib 0 / 1
+                uint32_t ql[8], qh[8], sw[2][8];
+                {
+                    auto rd8 = [&](int row, uint32_t* dst) {
+                        const uint4 x0 = *reinterpret_cast<const uint4*>(vt + row * kVtStride + pk0);
+                        const uint4 x1 = *reinterpret_cast<const uint4*>(vt + row * kVtStride + pk0 + 4);
+                        dst[0] = x0.x; dst[1] = x0.y; dst[2] = x0.z; dst[3] = x0.w;
+                        dst[4] = x1.x; dst[5] = x1.y; dst[6] = x1.z; dst[7] = x1.w;
+                    };
+                    rd8(16 * hh + col, ql);
+                    rd8(32 + 8 * hh + (col & 7), qh);
+                    rd8(48 + 2 * hh, sw[0]);
+                    rd8(49 + 2 * hh, sw[1]);
+                }
+#pragma unroll
+                for (int nib = 0; nib < 2; ++nib) {
+                    uint32_t code4[8], scp[4];
+#pragma unroll
+                    for (int i = 0; i < 8; ++i) {
+                        const uint32_t lo4 = nib ? (ql[i] >> 4) : ql[i];
+                        const uint32_t hi2 = __builtin_amdgcn_alignbit(qh[i], qh[i], rot[nib]) & 0x30303030u;
+                        code4[i] = (lo4 & 0x0F0F0F0Fu) | hi2;
+                    }
+#pragma unroll
+                    for (int k = 0; k < 4; ++k) {   // int8 scales of positions 2k, 2k+1 as binary16
+                        const uint32_t pr = __builtin_amdgcn_perm(sw[nib][2 * k + 1], sw[nib][2 * k], sc_sel);
+                        scp[k] = pk_add_f16((pr ^ 0x00800080u) | 0x64006400u, 0xE480E480u);   // - 1152
+                    }
+#pragma unroll
+                    for (int b = 0; b < 4; ++b) {
+                        const uint32_t sel = (uint32_t)b | (0x0Cu << 8) | ((4u + b) << 16) | (0x0Cu << 24);
+                        uint32_t ah[4], al[4];
+#pragma unroll
+                        for (int k = 0; k < 4; ++k) {
+                            const uint32_t pr = __builtin_amdgcn_perm(code4[2 * k + 1], code4[2 * k], sel);
+                            const uint32_t cp = pk_add_f16(pr | 0x64006400u, 0xE420E420u);   // c - 32
+                            ah[k] = pk_mul_f16(cp, scp[k]);
+                            al[k] = pk_fma_f16(cp, scp[k], ah[k] ^ 0x80008000u);   // e - hi, exact
+                        }
+                        const int t = 4 * nib + b;
+                        D[kl][t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
+                            __builtin_bit_cast(h8_t, uint4{ah[0], ah[1], ah[2], ah[3]}), bop, D[kl][t], 0, 0, 0);
+                        D[kl][t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
+                            __builtin_bit_cast(h8_t, uint4{al[0], al[1], al[2], al[3]}), bop, D[kl][t], 0, 0, 0);
+                    }
+                }
+            }
+        }
+        __builtin_amdgcn_wave_barrier();   // the next tile's staging overwrites vt and s_w
+    }
+
+    // records: U_g[dim] = (D_2g + D_2g+1) 2^-S, then m and Z
+    float* rec = a.ws + ((int64_t)s * a.nchunk + c) * a.hq * kRec;
+    const float unit = ldexpf(1.0f, -S_cur);
+    const int gcol = col >> 1;
+    const bool writer = (col & 1) == 0 && gcol < G;
+#pragma unroll
+    for (int kl = 0; kl < KPW; ++kl) {
+        if (kl == 1 && !two) break;
+        const int kvh = kv0 + kl;
+        float* rh = rec + (int64_t)(kvh * G + (gcol < G ? gcol : 0)) * kRec;
+#pragma unroll
+        for (int t = 0; t < 8; ++t) {
+            const int nib = t >> 2, b = t & 3;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                float v = D[kl][t][e];
+                v += dpp_mov<0xB1>(v);                  // + the other part of the head
+                const int rr = 4 * u + e;
+                const int dim = 32 * (2 * nib + (rr >= 8 ? 1 : 0)) + 4 * (rr & 7) + b;
+                if (writer) rh[dim] = v * unit;
+            }
+        }
+#pragma unroll
+        for (int eh = 0; eh < 2; ++eh) {
+            const int g = 2 * u + eh;
+            if (col == 0 && g < G) {
+                rec[(int64_t)(kvh * G + g) * kRec + kHd] = m_run[kl][eh];
+                rec[(int64_t)(kvh * G + g) * kRec + kHd + 1] = z_run[kl][eh];
+            }
+        }
+    }
+    if (err) raise_error(err);
+}
+
 // One workgroup per (sequence, query head): 8 chunk groups x 32 lanes of 4
 // coordinates; every thread keeps 8 chunk records in flight.
 __global__ void __launch_bounds__(256) attn_merge_kernel(const AttnArgs a) {
@@ -857,11 +1208,28 @@ static hipError_t launch_chunk(const AttnArgs& a, int lds, hipStream_t s) {
 
 // Q4_K keys of at most 8 kv heads are scored on the matrix cores, with q operands
 // prepared once per (sequence, kv head).
+template <int G, int KPW>
+static hipError_t launch_chunk_mma(const AttnArgs& a, hipStream_t s) {
+    static bool configured = false;
+    if (!configured) {
+        const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&attn_chunk_mma_kernel<G, KPW>),
+                                                 hipFuncAttributeMaxDynamicSharedMemorySize, kMmaLdsBytes);
+        if (e != hipSuccess) return e;
+        configured = true;
+    }
+    hipLaunchKernelGGL((attn_chunk_mma_kernel<G, KPW>), dim3(a.nchunk, a.nseq), dim3(256), kMmaLdsBytes, s, a);
+    return hipGetLastError();
+}
+
 template <int KF, int VF, int G>
 static hipError_t launch_chunk_k(const AttnArgs& a, int lds, hipStream_t s) {
     if constexpr (KF == RTA_Q4_K) {
         if (a.hkv <= 8) {
             hipLaunchKernelGGL((attn_qprep_kernel<G>), dim3(a.hkv, a.nseq), dim3(kWave), 0, s, a);
+            if constexpr (VF == RTA_Q6_K) {   // scores and P V on the matrix cores
+                if (a.hkv <= 4) return launch_chunk_mma<G, 1>(a, s);
+                return launch_chunk_mma<G, 2>(a, s);
+            }
             if (a.hkv <= 4) return launch_chunk<KF, VF, G, 1>(a, lds, s);
             return launch_chunk<KF, VF, G, 2>(a, lds, s);
         }
