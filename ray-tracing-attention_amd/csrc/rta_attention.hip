@@ -781,10 +781,11 @@ __device__ __forceinline__ float row16_sum(float v) {
 __device__ __forceinline__ uint32_t pk_add_f16(uint32_t a, uint32_t b) {
     return __builtin_bit_cast(uint32_t, __builtin_bit_cast(h2v_t, a) + __builtin_bit_cast(h2v_t, b));
 }
-__device__ __forceinline__ uint32_t pk_fma_f16(uint32_t a, uint32_t b, uint32_t c) {
+// a * b - c with one rounding (v_pk_fma_f16 with a negated addend)
+__device__ __forceinline__ uint32_t pk_fms_f16(uint32_t a, uint32_t b, uint32_t c) {
     return __builtin_bit_cast(uint32_t, __builtin_elementwise_fma(__builtin_bit_cast(h2v_t, a),
                                                                   __builtin_bit_cast(h2v_t, b),
-                                                                  __builtin_bit_cast(h2v_t, c)));
+                                                                  -__builtin_bit_cast(h2v_t, c)));
 }
 
 template <int G, int KPW>
@@ -798,6 +799,7 @@ __global__ void __launch_bounds__(256, 2) attn_chunk_mma_kernel(const AttnArgs a
     const int blk = KPW == 2 ? wave : wave >> 1;    // its K/V superblock
     if (kv0 >= hkv) return;                         // no workgroup barrier in this kernel
     const bool two = KPW == 2 && kv0 + 1 < hkv;     // uniform
+    const int64_t base = a.slot_base[s];            // both loads issued before either is used
     const int64_t Lc = a.ctx_len[s];
     const int64_t visible = Lc < a.capacity ? Lc : a.capacity;
     const int64_t chunk = (int64_t)a.nt * kTile;
@@ -805,7 +807,10 @@ __global__ void __launch_bounds__(256, 2) attn_chunk_mma_kernel(const AttnArgs a
     if (visible <= 0 || first >= visible) return;
     const int n_all = (int)(visible - first < chunk ? visible - first : chunk);
     const int64_t p0 = Lc - visible + first;
-    const int64_t base = a.slot_base[s];
+    // ring slot of chunk position off: base + (p0 + off) % capacity, with the modulo
+    // taken once (one conditional subtraction per position when capacity >= the chunk)
+    const int64_t r0 = p0 % a.capacity;
+    const bool small_ring = a.capacity < chunk;     // uniform
     uint32_t* vt = reinterpret_cast<uint32_t*>(lds) + wave * MmaWaveLds::total;
     float* s_w = lds + wave * MmaWaveLds::total + MmaWaveLds::w;
     float* s_f = lds + wave * MmaWaveLds::total + MmaWaveLds::f;
@@ -836,7 +841,9 @@ __global__ void __launch_bounds__(256, 2) attn_chunk_mma_kernel(const AttnArgs a
                              (32u - (uint32_t)((4 - 2 * (2 + qsel)) & 31)) & 31u};
 
     uint32_t err = 0;
-    const float inv = 1.0f / sqrtf((float)kHd);
+    // scores in log2 units, s log2(e) / sqrt(hd), so that the softmax takes exp2 (one
+    // v_exp_f32); m is converted back (times ln 2) for the records
+    const float inv2 = 1.4426950408889634f / sqrtf((float)kHd);
     const int ntile = (n_all + kTile - 1) / kTile;
     for (int tile = 0; tile < ntile; ++tile) {
         const int n = min(kTile, n_all - tile * kTile);
@@ -844,7 +851,11 @@ __global__ void __launch_bounds__(256, 2) attn_chunk_mma_kernel(const AttnArgs a
         // (its lines are read anyway), out of range slot 0
         const int j = lane;
         bool ok = j < n;
-        int64_t slot = base + (p0 + tile * kTile + min(j, n - 1)) % a.capacity;
+        int64_t slot;
+        {
+            const int64_t q = r0 + tile * kTile + min(j, n - 1);
+            slot = base + (small_ring ? q % a.capacity : (q >= a.capacity ? q - a.capacity : q));
+        }
         if (slot < 0 || slot >= a.n_slots) {
             if (ok) err |= RTA_DEVERR_HITS;
             ok = false;
@@ -885,8 +896,11 @@ __global__ void __launch_bounds__(256, 2) attn_chunk_mma_kernel(const AttnArgs a
         asm volatile("" ::: "memory");
         QOp qo[KPW];
 #pragma unroll
-        for (int kl = 0; kl < KPW; ++kl)
+        for (int kl = 0; kl < KPW; ++kl) {
             qo[kl] = load_qop(a.qop + ((int64_t)s * hkv + min(kv0 + kl, hkv - 1)) * 6 * kWave, lane);
+            qo[kl].rs[0] *= inv2;
+            qo[kl].rs[1] *= inv2;
+        }
         // scores of the wave's kv heads, heads 2u + eh, positions 16 rt + col
         float sv[KPW][4][2];
 #pragma unroll
@@ -899,7 +913,7 @@ __global__ void __launch_bounds__(256, 2) attn_chunk_mma_kernel(const AttnArgs a
                 kr.c[0] = kc[kl][rt][0];
                 kr.c[1] = kc[kl][rt][1];
                 float sc2[2];
-                score_q4k_mma<G>(qo[kl], kr, hh_of(kl), u, inv, sc2);
+                score_q4k_mma<G>(qo[kl], kr, hh_of(kl), u, 1.0f, sc2);
 #pragma unroll
                 for (int eh = 0; eh < 2; ++eh) {
                     const bool live = okr[rt] && 2 * u + eh < G;
@@ -908,13 +922,18 @@ __global__ void __launch_bounds__(256, 2) attn_chunk_mma_kernel(const AttnArgs a
                 }
             }
         }
-        // the tile's power of two: max |d| 2^S in [2^13, 2^14) (kept when every d is 0)
+        // the power of two S: set on the first tile to put max |d| 2^S in [2^13, 2^14),
+        // then kept while the tile's max |d| 2^S stays in [2^-4, 2^14) (no f16 overflow,
+        // hi/lo still carrying 22 bits of the large terms), so D is rarely rescaled for it
         const float dmax = wave_max_dpp(dabs);
         int S_new = S_cur;
         if (dmax > 0.0f && isfinite(dmax)) {
-            int e;
-            (void)frexpf(dmax, &e);
-            S_new = 14 - e;
+            const float scaled = ldexpf(dmax, S_cur);
+            if (tile == 0 || !(scaled < 16384.0f && scaled >= 0.0625f)) {
+                int e;
+                (void)frexpf(dmax, &e);
+                S_new = 14 - e;
+            }
         }
         if (tile == 0) S_cur = S_new;
         // softmax over the tile, folded into (m, Z); weights and rescale factors to LDS
@@ -933,9 +952,9 @@ __global__ void __launch_bounds__(256, 2) attn_chunk_mma_kernel(const AttnArgs a
 #pragma unroll
                     for (int rt = 0; rt < 4; ++rt) w[rt] = 0.0f;
                 } else {
-                    sf = expf(m_run[kl][eh] - m_new);
+                    sf = __builtin_amdgcn_exp2f(m_run[kl][eh] - m_new);
 #pragma unroll
-                    for (int rt = 0; rt < 4; ++rt) w[rt] = expf(sv[kl][rt][eh] - m_new);
+                    for (int rt = 0; rt < 4; ++rt) w[rt] = __builtin_amdgcn_exp2f(sv[kl][rt][eh] - m_new);
                 }
                 const float zt = row16_sum((w[0] + w[1]) + (w[2] + w[3]));
                 z_run[kl][eh] = z_run[kl][eh] * sf + zt;
@@ -948,14 +967,16 @@ __global__ void __launch_bounds__(256, 2) attn_chunk_mma_kernel(const AttnArgs a
             }
         }
         __builtin_amdgcn_wave_barrier();
-        // rescale D (column 2g + part: head g)
+        // rescale D (column 2g + part: head g), skipped when no running max and not S moved
         const int gcol = col >> 1;
 #pragma unroll
         for (int kl = 0; kl < KPW; ++kl) {
             if (kl == 1 && !two) break;
-            const float fl = s_f[kl * 8 + gcol];
+            const float fl = gcol < G ? s_f[kl * 8 + gcol] : 1.0f;   // unused columns stay 0
+            if (__builtin_amdgcn_ballot_w64(fl != 1.0f) != 0) {
 #pragma unroll
-            for (int t = 0; t < 8; ++t) D[kl][t] *= fl;
+                for (int t = 0; t < 8; ++t) D[kl][t] *= fl;
+            }
         }
         S_cur = S_new;
         // P V, 32 positions per step: this lane's positions 32 ks + 8 u + i
@@ -974,20 +995,25 @@ __global__ void __launch_bounds__(256, 2) attn_chunk_mma_kernel(const AttnArgs a
             for (int kl = 0; kl < KPW; ++kl) {
                 if (kl == 1 && !two) break;
                 const int hh = hh_of(kl);
-                // B: column col = head gcol, part col & 1
+                // B: column col = head gcol, part col & 1: x = w d 2^S as hi + lo, both
+                // rounded toward zero (|x - hi - lo| < 2^-21 |x|); columns of heads >= G
+                // are never read
                 h8_t bop;
                 {
                     const float* wr = s_w + (kl * 8 + gcol) * kVtStride + pk0;
                     const float4 w0 = *reinterpret_cast<const float4*>(wr);
                     const float4 w1 = *reinterpret_cast<const float4*>(wr + 4);
                     const float wv[8] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
-                    const bool live = gcol < G, part = (col & 1) != 0;
+                    const bool part = (col & 1) != 0;
 #pragma unroll
-                    for (int i = 0; i < 8; ++i) {
-                        const float x = wv[i] * dS[i];
-                        const _Float16 h = (_Float16)x;
-                        const _Float16 l = (_Float16)(x - (float)h);
-                        bop[i] = live ? (part ? l : h) : (_Float16)0.0f;
+                    for (int i = 0; i < 8; i += 2) {
+                        const float x0 = wv[i] * dS[i], x1 = wv[i + 1] * dS[i + 1];
+                        const h2v_t h = __builtin_bit_cast(h2v_t, __builtin_amdgcn_cvt_pkrtz(x0, x1));
+                        const h2v_t l =
+                            __builtin_bit_cast(h2v_t, __builtin_amdgcn_cvt_pkrtz(x0 - (float)h.x, x1 - (float)h.y));
+                        const h2v_t v = part ? l : h;
+                        bop[i] = v.x;
+                        bop[i + 1] = v.y;
                     }
                 }
                 // A: ql dword col, qh dword col & 7, sub-block scale dwords of nib 0 / 1
@@ -1004,9 +1030,14 @@ __global__ void __launch_bounds__(256, 2) attn_chunk_mma_kernel(const AttnArgs a
                     rd8(48 + 2 * hh, sw[0]);
                     rd8(49 + 2 * hh, sw[1]);
                 }
+                // e 2^-14 = c sc 2^-14 - 32 sc 2^-14: the code pair shifted to c 2^-20
+                // (binary16 subnormals) times sc 2^6 gives c sc 2^-14 as hi plus the exact
+                // remainder lo (|c sc| < 2^13, every nonzero product >= 2^-14, so the
+                // matrix-core operands are normal), and -sc 2^-9 (exact) goes in a third
+                // instruction; D is then in units of 2^(S - 14)
 #pragma unroll
                 for (int nib = 0; nib < 2; ++nib) {
-                    uint32_t code4[8], scp[4];
+                    uint32_t code4[8], sc6[4], corr[4];
 #pragma unroll
                     for (int i = 0; i < 8; ++i) {
                         const uint32_t lo4 = nib ? (ql[i] >> 4) : ql[i];
@@ -1016,24 +1047,27 @@ __global__ void __launch_bounds__(256, 2) attn_chunk_mma_kernel(const AttnArgs a
 #pragma unroll
                     for (int k = 0; k < 4; ++k) {   // int8 scales of positions 2k, 2k+1 as binary16
                         const uint32_t pr = __builtin_amdgcn_perm(sw[nib][2 * k + 1], sw[nib][2 * k], sc_sel);
-                        scp[k] = pk_add_f16((pr ^ 0x00800080u) | 0x64006400u, 0xE480E480u);   // - 1152
+                        const uint32_t sc = pk_add_f16((pr ^ 0x00800080u) | 0x64006400u, 0xE480E480u);   // - 1152
+                        sc6[k] = pk_mul_f16(sc, 0x54005400u);    // sc 2^6
+                        corr[k] = pk_mul_f16(sc, 0x98009800u);    // -sc 2^-9
                     }
+                    const h8_t ac = __builtin_bit_cast(h8_t, uint4{corr[0], corr[1], corr[2], corr[3]});
 #pragma unroll
                     for (int b = 0; b < 4; ++b) {
                         const uint32_t sel = (uint32_t)b | (0x0Cu << 8) | ((4u + b) << 16) | (0x0Cu << 24);
                         uint32_t ah[4], al[4];
 #pragma unroll
                         for (int k = 0; k < 4; ++k) {
-                            const uint32_t pr = __builtin_amdgcn_perm(code4[2 * k + 1], code4[2 * k], sel);
-                            const uint32_t cp = pk_add_f16(pr | 0x64006400u, 0xE420E420u);   // c - 32
-                            ah[k] = pk_mul_f16(cp, scp[k]);
-                            al[k] = pk_fma_f16(cp, scp[k], ah[k] ^ 0x80008000u);   // e - hi, exact
+                            const uint32_t cp = __builtin_amdgcn_perm(code4[2 * k + 1], code4[2 * k], sel) << 4;
+                            ah[k] = pk_mul_f16(cp, sc6[k]);
+                            al[k] = pk_fms_f16(cp, sc6[k], ah[k]);   // remainder, exact
                         }
                         const int t = 4 * nib + b;
                         D[kl][t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
                             __builtin_bit_cast(h8_t, uint4{ah[0], ah[1], ah[2], ah[3]}), bop, D[kl][t], 0, 0, 0);
                         D[kl][t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
                             __builtin_bit_cast(h8_t, uint4{al[0], al[1], al[2], al[3]}), bop, D[kl][t], 0, 0, 0);
+                        D[kl][t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ac, bop, D[kl][t], 0, 0, 0);
                     }
                 }
             }
@@ -1043,7 +1077,7 @@ __global__ void __launch_bounds__(256, 2) attn_chunk_mma_kernel(const AttnArgs a
 
     // records: U_g[dim] = (D_2g + D_2g+1) 2^-S, then m and Z
     float* rec = a.ws + ((int64_t)s * a.nchunk + c) * a.hq * kRec;
-    const float unit = ldexpf(1.0f, -S_cur);
+    const float unit = ldexpf(1.0f, 14 - S_cur);   // D is in units of 2^(S - 14)
     const int gcol = col >> 1;
     const bool writer = (col & 1) == 0 && gcol < G;
 #pragma unroll
@@ -1067,7 +1101,7 @@ __global__ void __launch_bounds__(256, 2) attn_chunk_mma_kernel(const AttnArgs a
         for (int eh = 0; eh < 2; ++eh) {
             const int g = 2 * u + eh;
             if (col == 0 && g < G) {
-                rec[(int64_t)(kvh * G + g) * kRec + kHd] = m_run[kl][eh];
+                rec[(int64_t)(kvh * G + g) * kRec + kHd] = m_run[kl][eh] * 0.6931471805599453f;
                 rec[(int64_t)(kvh * G + g) * kRec + kHd + 1] = z_run[kl][eh];
             }
         }
