@@ -53,7 +53,15 @@ struct AttnArgs {
     int nseq, hq, hkv, nchunk;
     int nt;             // tiles per chunk
     int nblk;           // superblocks per field: ceil(hkv / 2)
+    // tile-list split (matrix-core kernel): plan = [S[0..nseq]] tile prefix over the
+    // sequences, then [nwg] the sequence holding each workgroup's first tile; records
+    // [nseq][rstride][hq][kRec]; null for the chunk-grid kernels
+    int32_t* plan;
+    int nwg;
+    int64_t max_tiles;  // tiles per sequence at most: ceil(max_ctx / 64)
+    int64_t rstride;    // records per sequence in the workspace
 };
+constexpr int kMaxWg = 2048;   // plan entries for workgroups
 
 template <int FMT> struct Fmt;
 template <> struct Fmt<RTA_Q4_K> { static constexpr int kBytes = 144, kRow = 37; };  // LDS row: 36 dwords + pad
@@ -369,26 +377,32 @@ struct VStage {
     static constexpr int kRaw = (Fmt<FMT>::kBytes + 2 + 3) / 4;   // dwords covering a misaligned block
     uint32_t raw[kRaw];
     uint32_t mis;
+    uint32_t tail;   // the block's last 2 bytes; the last word is chosen when stored, so
+                     // that no arithmetic waits on the loads before they are needed
     __device__ __forceinline__ void load(const uint8_t* __restrict__ blk) {
         constexpr int kB = Fmt<FMT>::kBytes;
         mis = (uint32_t)(reinterpret_cast<uintptr_t>(blk) & 3u);   // 0 or 2
         const uint32_t* a = reinterpret_cast<const uint32_t*>(blk - mis);
-        const uint32_t tail = (uint32_t)*reinterpret_cast<const uint16_t*>(blk + kB - 2);
+        tail = (uint32_t)*reinterpret_cast<const uint16_t*>(blk + kB - 2);
         // (kB + mis) / 4 whole dwords, then the last 2 bytes when (kB + mis) % 4 == 2
         load_dwords<kRaw - 1>(a, raw);
-        if constexpr (FMT == RTA_Q4_K) {   // 36 dwords aligned; 36 + 2 bytes misaligned
-            raw[kRaw - 1] = mis ? tail : 0u;
-        } else {                           // 52 + 2 bytes aligned; 53 dwords misaligned
+        if constexpr (FMT == RTA_Q6_K) {   // 52 + 2 bytes aligned; 53 dwords misaligned
             // the load is unconditional (a guarded load would wait on the spot); when
             // aligned it rereads an in-block dword and the tail is used instead
-            const uint32_t extra = a[mis ? kRaw - 1 : kRaw - 2];
-            raw[kRaw - 1] = mis ? extra : tail;
+            raw[kRaw - 1] = a[mis ? kRaw - 1 : kRaw - 2];
         }
+    }
+    // raw word i, the last one resolved: Q4_K 36 dwords aligned, 36 + 2 bytes
+    // misaligned; Q6_K 52 + 2 bytes aligned, 53 dwords misaligned
+    __device__ __forceinline__ uint32_t word(int i) const {
+        if (i < kRaw - 1) return raw[i];
+        if constexpr (FMT == RTA_Q4_K) return mis ? tail : 0u;
+        return mis ? raw[kRaw - 1] : tail;
     }
     __device__ __forceinline__ void store(uint32_t* row) const {
         constexpr int kOut = (Fmt<FMT>::kBytes + 3) / 4;
 #pragma unroll
-        for (int i = 0; i < kOut; ++i) row[i] = funnel(raw[i], i + 1 < kRaw ? raw[i + 1] : 0u, mis);
+        for (int i = 0; i < kOut; ++i) row[i] = funnel(word(i), i + 1 < kRaw ? word(i + 1) : 0u, mis);
     }
 };
 
@@ -791,7 +805,6 @@ __device__ __forceinline__ uint32_t pk_fms_f16(uint32_t a, uint32_t b, uint32_t 
 template <int G, int KPW>
 __global__ void __launch_bounds__(256, 2) attn_chunk_mma_kernel(const AttnArgs a) {
     extern __shared__ __align__(16) float lds[];
-    const int c = blockIdx.x, s = blockIdx.y;
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int hkv = a.hkv;
@@ -799,38 +812,28 @@ __global__ void __launch_bounds__(256, 2) attn_chunk_mma_kernel(const AttnArgs a
     const int blk = KPW == 2 ? wave : wave >> 1;    // its K/V superblock
     if (kv0 >= hkv) return;                         // no workgroup barrier in this kernel
     const bool two = KPW == 2 && kv0 + 1 < hkv;     // uniform
-    const int64_t base = a.slot_base[s];            // both loads issued before either is used
-    const int64_t Lc = a.ctx_len[s];
-    const int64_t visible = Lc < a.capacity ? Lc : a.capacity;
-    const int64_t chunk = (int64_t)a.nt * kTile;
-    const int64_t first = (int64_t)c * chunk;
-    if (visible <= 0 || first >= visible) return;
-    const int n_all = (int)(visible - first < chunk ? visible - first : chunk);
-    const int64_t p0 = Lc - visible + first;
-    // ring slot of chunk position off: base + (p0 + off) % capacity, with the modulo
-    // taken once (one conditional subtraction per position when capacity >= the chunk)
-    const int64_t r0 = p0 % a.capacity;
-    const bool small_ring = a.capacity < chunk;     // uniform
+    // this workgroup's share [ta, tb) of the tile list, which runs through the
+    // sequences in order (plan: S[s] = first tile of sequence s, S[nseq] = T, then the
+    // sequence holding each workgroup's first tile)
+    // (values read from memory that every lane shares are moved to scalar registers)
+    auto uni = [](int v) { return __builtin_amdgcn_readfirstlane(v); };
+    auto uni64 = [](int64_t v) {
+        const uint32_t lo = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)v);
+        const uint32_t hi = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)((uint64_t)v >> 32));
+        return (int64_t)(((uint64_t)hi << 32) | lo);
+    };
+    const int32_t* S = a.plan;
+    const int64_t T = uni(S[a.nseq]);
+    const int64_t P = a.nwg < T ? a.nwg : T;   // every workgroup below P has a tile
+    if (blockIdx.x >= P) return;   // (all of them when T = 0)
+    const int64_t ta = (int64_t)blockIdx.x * T / P, tb = ((int64_t)blockIdx.x + 1) * T / P;
+    int s = uni(S[a.nseq + 1 + blockIdx.x]);
     uint32_t* vt = reinterpret_cast<uint32_t*>(lds) + wave * MmaWaveLds::total;
     float* s_w = lds + wave * MmaWaveLds::total + MmaWaveLds::w;
     float* s_f = lds + wave * MmaWaveLds::total + MmaWaveLds::f;
     auto hh_of = [&](int kl) { return KPW == 2 ? kl : (wave & 1); };
 
     const int u = lane >> 4, col = lane & 15;   // row of 16 lanes, column in it
-
-    float m_run[KPW][2], z_run[KPW][2];         // heads 2u + eh of each kv head
-    f4_t D[KPW][8];
-#pragma unroll
-    for (int kl = 0; kl < KPW; ++kl) {
-#pragma unroll
-        for (int eh = 0; eh < 2; ++eh) {
-            m_run[kl][eh] = -INFINITY;
-            z_run[kl][eh] = 0.0f;
-        }
-#pragma unroll
-        for (int t = 0; t < 8; ++t) D[kl][t] = f4_t{0.0f, 0.0f, 0.0f, 0.0f};
-    }
-    int S_cur = 0;
 
     // per-lane constants of the P V operands (A row r = col)
     const int qsel = col >= 8 ? 1 : 0;
@@ -844,269 +847,358 @@ __global__ void __launch_bounds__(256, 2) attn_chunk_mma_kernel(const AttnArgs a
     // scores in log2 units, s log2(e) / sqrt(hd), so that the softmax takes exp2 (one
     // v_exp_f32); m is converted back (times ln 2) for the records
     const float inv2 = 1.4426950408889634f / sqrtf((float)kHd);
-    const int ntile = (n_all + kTile - 1) / kTile;
-    for (int tile = 0; tile < ntile; ++tile) {
-        const int n = min(kTile, n_all - tile * kTile);
-        // slot of the lane's position; past the tile's end the tile's last position
-        // (its lines are read anyway), out of range slot 0
-        const int j = lane;
-        bool ok = j < n;
-        int64_t slot;
-        {
-            const int64_t q = r0 + tile * kTile + min(j, n - 1);
-            slot = base + (small_ring ? q % a.capacity : (q >= a.capacity ? q - a.capacity : q));
+    for (int64_t x = ta; x < tb;) {   // uniform: one sequence segment per pass
+        const int64_t s_first = uni(S[s]), s_end = uni(S[s + 1]);
+        if (s_end <= x) {
+            ++s;
+            continue;
         }
-        if (slot < 0 || slot >= a.n_slots) {
-            if (ok) err |= RTA_DEVERR_HITS;
-            ok = false;
-            slot = 0;
-        }
-        // V superblock first (it is needed first), then the keys of the 4 x 16
-        // positions (lane: position 16 rt + col, segment u)
-        VStage<RTA_Q6_K> vst;
-        vst.load(a.packets + slot * a.stride + a.v_offset + (int64_t)blk * Fmt<RTA_Q6_K>::kBytes);
-        uint4 hdr[4];
-        uint2 kc[KPW][4][2];
-        bool okr[4];
-#pragma unroll
-        for (int rt = 0; rt < 4; ++rt) {
-            const int src = 16 * rt + col;
-            const uint32_t lo = (uint32_t)__shfl((int)(uint32_t)slot, src, kWave);
-            const uint32_t hi = (uint32_t)__shfl((int)(uint32_t)((uint64_t)slot >> 32), src, kWave);
-            okr[rt] = __shfl(ok ? 1 : 0, src, kWave) != 0;
-            const uint8_t* kp = a.packets + (int64_t)(((uint64_t)hi << 32) | lo) * a.stride +
-                                (int64_t)blk * Fmt<RTA_Q4_K>::kBytes;
-            __builtin_memcpy(&hdr[rt], kp, 16);
-#pragma unroll
-            for (int kl = 0; kl < KPW; ++kl)
-#pragma unroll
-                for (int jc = 0; jc < 2; ++jc)
-                    __builtin_memcpy(&kc[kl][rt][jc], kp + 16 + 32 * (2 * hh_of(kl) + jc) + 8 * u, 8);
-        }
-        // stage V transposed; the lane's d for the tile's scale 2^S
-        float dabs;
-        {
-#pragma unroll
-            for (int i = 0; i < kVtRows; ++i)
-                vt[i * kVtStride + j] = funnel(vst.raw[i], i + 1 < VStage<RTA_Q6_K>::kRaw ? vst.raw[i + 1] : 0u, vst.mis);
-            dabs = ok ? fabsf(half_lo(funnel(vst.raw[kVtRows - 1], 0u, vst.mis))) : 0.0f;
-        }
-        // q operands of the wave's kv heads (prepared by attn_qprep_kernel), reread per
-        // tile from the cache once the V registers are free
-        asm volatile("" ::: "memory");
-        QOp qo[KPW];
+        const int64_t seg_end = s_end < tb ? s_end : tb;
+        const int64_t base = uni64(a.slot_base[s]);     // both loads issued before either is used
+        const int64_t Lc = uni(a.ctx_len[s]);
+        const int64_t visible = Lc < a.capacity ? Lc : a.capacity;
+        const int64_t n_vis = visible < a.max_tiles * kTile ? visible : a.max_tiles * kTile;
+        // ring slot of sequence position off (< visible <= capacity): base + (p + off) %
+        // capacity for the oldest visible position p, the modulo taken once
+        const int64_t r0 = (Lc - visible) % a.capacity;
+        float m_run[KPW][2], z_run[KPW][2];         // heads 2u + eh of each kv head
+        f4_t D[KPW][8];
 #pragma unroll
         for (int kl = 0; kl < KPW; ++kl) {
-            qo[kl] = load_qop(a.qop + ((int64_t)s * hkv + min(kv0 + kl, hkv - 1)) * 6 * kWave, lane);
-            qo[kl].rs[0] *= inv2;
-            qo[kl].rs[1] *= inv2;
-        }
-        // scores of the wave's kv heads, heads 2u + eh, positions 16 rt + col
-        float sv[KPW][4][2];
-#pragma unroll
-        for (int kl = 0; kl < KPW; ++kl) {
-            if (kl == 1 && !two) break;
-#pragma unroll
-            for (int rt = 0; rt < 4; ++rt) {
-                KRaw kr;
-                kr.hdr = hdr[rt];
-                kr.c[0] = kc[kl][rt][0];
-                kr.c[1] = kc[kl][rt][1];
-                float sc2[2];
-                score_q4k_mma<G>(qo[kl], kr, hh_of(kl), u, 1.0f, sc2);
-#pragma unroll
-                for (int eh = 0; eh < 2; ++eh) {
-                    const bool live = okr[rt] && 2 * u + eh < G;
-                    if (live && !isfinite(sc2[eh])) err |= RTA_DEVERR_DETECTOR;
-                    sv[kl][rt][eh] = live ? sc2[eh] : -INFINITY;
-                }
-            }
-        }
-        // the power of two S: set on the first tile to put max |d| 2^S in [2^13, 2^14),
-        // then kept while the tile's max |d| 2^S stays in [2^-4, 2^14) (no f16 overflow,
-        // hi/lo still carrying 22 bits of the large terms), so D is rarely rescaled for it
-        const float dmax = wave_max_dpp(dabs);
-        int S_new = S_cur;
-        if (dmax > 0.0f && isfinite(dmax)) {
-            const float scaled = ldexpf(dmax, S_cur);
-            if (tile == 0 || !(scaled < 16384.0f && scaled >= 0.0625f)) {
-                int e;
-                (void)frexpf(dmax, &e);
-                S_new = 14 - e;
-            }
-        }
-        if (tile == 0) S_cur = S_new;
-        // softmax over the tile, folded into (m, Z); weights and rescale factors to LDS
-#pragma unroll
-        for (int kl = 0; kl < KPW; ++kl) {
-            if (kl == 1 && !two) break;
 #pragma unroll
             for (int eh = 0; eh < 2; ++eh) {
-                const int g = 2 * u + eh;
-                float mx = fmaxf(fmaxf(sv[kl][0][eh], sv[kl][1][eh]), fmaxf(sv[kl][2][eh], sv[kl][3][eh]));
-                mx = row16_max(mx);
-                const float m_new = fmaxf(m_run[kl][eh], mx);
-                float w[4], sf;
-                if (m_new == -INFINITY) {
-                    sf = 1.0f;
-#pragma unroll
-                    for (int rt = 0; rt < 4; ++rt) w[rt] = 0.0f;
-                } else {
-                    sf = __builtin_amdgcn_exp2f(m_run[kl][eh] - m_new);
-#pragma unroll
-                    for (int rt = 0; rt < 4; ++rt) w[rt] = __builtin_amdgcn_exp2f(sv[kl][rt][eh] - m_new);
-                }
-                const float zt = row16_sum((w[0] + w[1]) + (w[2] + w[3]));
-                z_run[kl][eh] = z_run[kl][eh] * sf + zt;
-                m_run[kl][eh] = m_new;
-                if (g < G) {
-#pragma unroll
-                    for (int rt = 0; rt < 4; ++rt) s_w[(kl * 8 + g) * kVtStride + 16 * rt + col] = w[rt];
-                    if (col == 0) s_f[kl * 8 + g] = ldexpf(sf, S_new - S_cur);
-                }
+                m_run[kl][eh] = -INFINITY;
+                z_run[kl][eh] = 0.0f;
             }
-        }
-        __builtin_amdgcn_wave_barrier();
-        // rescale D (column 2g + part: head g), skipped when no running max and not S moved
-        const int gcol = col >> 1;
 #pragma unroll
-        for (int kl = 0; kl < KPW; ++kl) {
-            if (kl == 1 && !two) break;
-            const float fl = gcol < G ? s_f[kl * 8 + gcol] : 1.0f;   // unused columns stay 0
-            if (__builtin_amdgcn_ballot_w64(fl != 1.0f) != 0) {
-#pragma unroll
-                for (int t = 0; t < 8; ++t) D[kl][t] *= fl;
-            }
+            for (int t = 0; t < 8; ++t) D[kl][t] = f4_t{0.0f, 0.0f, 0.0f, 0.0f};
         }
-        S_cur = S_new;
-        // P V, 32 positions per step: this lane's positions 32 ks + 8 u + i
-#pragma unroll 1
-        for (int ks = 0; ks < 2; ++ks) {
-            const int pk0 = 32 * ks + 8 * u;
-            float dS[8];
+        int S_cur = 0;
+        for (int64_t tile = x - s_first; tile < seg_end - s_first; ++tile) {
+            const bool first_tile = tile == x - s_first;
+            const int n = (int)(n_vis - tile * kTile < kTile ? n_vis - tile * kTile : kTile);
+            // slot of the lane's position; past the tile's end the tile's last position
+            // (its lines are read anyway), out of range slot 0
+            const int j = lane;
+            bool ok = j < n;
+            int64_t slot;
             {
-                const uint4 d0 = *reinterpret_cast<const uint4*>(vt + 52 * kVtStride + pk0);
-                const uint4 d1 = *reinterpret_cast<const uint4*>(vt + 52 * kVtStride + pk0 + 4);
-                const uint32_t dw[8] = {d0.x, d0.y, d0.z, d0.w, d1.x, d1.y, d1.z, d1.w};
-#pragma unroll
-                for (int i = 0; i < 8; ++i) dS[i] = ldexpf(half_lo(dw[i]), S_cur);
+                const int64_t q = r0 + tile * kTile + min(j, n - 1);
+                slot = base + (q >= a.capacity ? q - a.capacity : q);
             }
+            if (slot < 0 || slot >= a.n_slots) {
+                if (ok) err |= RTA_DEVERR_HITS;
+                ok = false;
+                slot = 0;
+            }
+            // V superblock first (it is needed first), then the keys of the 4 x 16
+            // positions (lane: position 16 rt + col, segment u)
+            VStage<RTA_Q6_K> vst;
+            vst.load(a.packets + slot * a.stride + a.v_offset + (int64_t)blk * Fmt<RTA_Q6_K>::kBytes);
+            uint4 hdr[4];
+            uint2 kc[KPW][4][2];
+            bool okr[4];
+#pragma unroll
+            for (int rt = 0; rt < 4; ++rt) {
+                const int src = 16 * rt + col;
+                const uint32_t lo = (uint32_t)__shfl((int)(uint32_t)slot, src, kWave);
+                const uint32_t hi = (uint32_t)__shfl((int)(uint32_t)((uint64_t)slot >> 32), src, kWave);
+                okr[rt] = __shfl(ok ? 1 : 0, src, kWave) != 0;
+                const uint8_t* kp = a.packets + (int64_t)(((uint64_t)hi << 32) | lo) * a.stride +
+                                    (int64_t)blk * Fmt<RTA_Q4_K>::kBytes;
+                __builtin_memcpy(&hdr[rt], kp, 16);
+#pragma unroll
+                for (int kl = 0; kl < KPW; ++kl)
+#pragma unroll
+                    for (int jc = 0; jc < 2; ++jc)
+                        __builtin_memcpy(&kc[kl][rt][jc], kp + 16 + 32 * (2 * hh_of(kl) + jc) + 8 * u, 8);
+            }
+            // stage V transposed; the lane's d for the tile's scale 2^S
+            float dabs;
+            {
+#pragma unroll
+                for (int i = 0; i < kVtRows; ++i)
+                    vt[i * kVtStride + j] = funnel(vst.word(i), i + 1 < VStage<RTA_Q6_K>::kRaw ? vst.word(i + 1) : 0u, vst.mis);
+                dabs = ok ? fabsf(half_lo(funnel(vst.word(kVtRows - 1), 0u, vst.mis))) : 0.0f;
+            }
+            // q operands of the wave's kv heads (prepared by attn_qprep_kernel), reread per
+            // tile from the cache once the V registers are free
+            asm volatile("" ::: "memory");
+            QOp qo[KPW];
+#pragma unroll
+            for (int kl = 0; kl < KPW; ++kl) {
+                qo[kl] = load_qop(a.qop + ((int64_t)s * hkv + min(kv0 + kl, hkv - 1)) * 6 * kWave, lane);
+                qo[kl].rs[0] *= inv2;
+                qo[kl].rs[1] *= inv2;
+            }
+            // scores of the wave's kv heads, heads 2u + eh, positions 16 rt + col
+            float sv[KPW][4][2];
 #pragma unroll
             for (int kl = 0; kl < KPW; ++kl) {
                 if (kl == 1 && !two) break;
-                const int hh = hh_of(kl);
-                // B: column col = head gcol, part col & 1: x = w d 2^S as hi + lo, both
-                // rounded toward zero (|x - hi - lo| < 2^-21 |x|); columns of heads >= G
-                // are never read
-                h8_t bop;
-                {
-                    const float* wr = s_w + (kl * 8 + gcol) * kVtStride + pk0;
-                    const float4 w0 = *reinterpret_cast<const float4*>(wr);
-                    const float4 w1 = *reinterpret_cast<const float4*>(wr + 4);
-                    const float wv[8] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
-                    const bool part = (col & 1) != 0;
 #pragma unroll
-                    for (int i = 0; i < 8; i += 2) {
-                        const float x0 = wv[i] * dS[i], x1 = wv[i + 1] * dS[i + 1];
-                        const h2v_t h = __builtin_bit_cast(h2v_t, __builtin_amdgcn_cvt_pkrtz(x0, x1));
-                        const h2v_t l =
-                            __builtin_bit_cast(h2v_t, __builtin_amdgcn_cvt_pkrtz(x0 - (float)h.x, x1 - (float)h.y));
-                        const h2v_t v = part ? l : h;
-                        bop[i] = v.x;
-                        bop[i + 1] = v.y;
+                for (int rt = 0; rt < 4; ++rt) {
+                    KRaw kr;
+                    kr.hdr = hdr[rt];
+                    kr.c[0] = kc[kl][rt][0];
+                    kr.c[1] = kc[kl][rt][1];
+                    float sc2[2];
+                    score_q4k_mma<G>(qo[kl], kr, hh_of(kl), u, 1.0f, sc2);
+#pragma unroll
+                    for (int eh = 0; eh < 2; ++eh) {
+                        const bool live = okr[rt] && 2 * u + eh < G;
+                        if (live && !isfinite(sc2[eh])) err |= RTA_DEVERR_DETECTOR;
+                        sv[kl][rt][eh] = live ? sc2[eh] : -INFINITY;
                     }
                 }
-                // A: ql dword col, qh dword col & 7, sub-block scale dwords of nib 0 / 1
-                uint32_t ql[8], qh[8], sw[2][8];
-                {
-                    auto rd8 = [&](int row, uint32_t* dst) {
-                        const uint4 x0 = *reinterpret_cast<const uint4*>(vt + row * kVtStride + pk0);
-                        const uint4 x1 = *reinterpret_cast<const uint4*>(vt + row * kVtStride + pk0 + 4);
-                        dst[0] = x0.x; dst[1] = x0.y; dst[2] = x0.z; dst[3] = x0.w;
-                        dst[4] = x1.x; dst[5] = x1.y; dst[6] = x1.z; dst[7] = x1.w;
-                    };
-                    rd8(16 * hh + col, ql);
-                    rd8(32 + 8 * hh + (col & 7), qh);
-                    rd8(48 + 2 * hh, sw[0]);
-                    rd8(49 + 2 * hh, sw[1]);
+            }
+            // the power of two S: set on the first tile to put max |d| 2^S in [2^13, 2^14),
+            // then kept while the tile's max |d| 2^S stays in [2^-4, 2^14) (no f16 overflow,
+            // hi/lo still carrying 22 bits of the large terms), so D is rarely rescaled for it
+            const float dmax = wave_max_dpp(dabs);
+            int S_new = S_cur;
+            if (dmax > 0.0f && isfinite(dmax)) {
+                const float scaled = ldexpf(dmax, S_cur);
+                if (first_tile || !(scaled < 16384.0f && scaled >= 0.0625f)) {
+                    int e;
+                    (void)frexpf(dmax, &e);
+                    S_new = 14 - e;
                 }
-                // e 2^-14 = c sc 2^-14 - 32 sc 2^-14: the code pair shifted to c 2^-20
-                // (binary16 subnormals) times sc 2^6 gives c sc 2^-14 as hi plus the exact
-                // remainder lo (|c sc| < 2^13, every nonzero product >= 2^-14, so the
-                // matrix-core operands are normal), and -sc 2^-9 (exact) goes in a third
-                // instruction; D is then in units of 2^(S - 14)
+            }
+            if (first_tile) S_cur = S_new;
+            // softmax over the tile, folded into (m, Z); weights and rescale factors to LDS
 #pragma unroll
-                for (int nib = 0; nib < 2; ++nib) {
-                    uint32_t code4[8], sc6[4], corr[4];
+            for (int kl = 0; kl < KPW; ++kl) {
+                if (kl == 1 && !two) break;
 #pragma unroll
-                    for (int i = 0; i < 8; ++i) {
-                        const uint32_t lo4 = nib ? (ql[i] >> 4) : ql[i];
-                        const uint32_t hi2 = __builtin_amdgcn_alignbit(qh[i], qh[i], rot[nib]) & 0x30303030u;
-                        code4[i] = (lo4 & 0x0F0F0F0Fu) | hi2;
+                for (int eh = 0; eh < 2; ++eh) {
+                    const int g = 2 * u + eh;
+                    float mx = fmaxf(fmaxf(sv[kl][0][eh], sv[kl][1][eh]), fmaxf(sv[kl][2][eh], sv[kl][3][eh]));
+                    mx = row16_max(mx);
+                    const float m_new = fmaxf(m_run[kl][eh], mx);
+                    float w[4], sf;
+                    if (m_new == -INFINITY) {
+                        sf = 1.0f;
+#pragma unroll
+                        for (int rt = 0; rt < 4; ++rt) w[rt] = 0.0f;
+                    } else {
+                        sf = __builtin_amdgcn_exp2f(m_run[kl][eh] - m_new);
+#pragma unroll
+                        for (int rt = 0; rt < 4; ++rt) w[rt] = __builtin_amdgcn_exp2f(sv[kl][rt][eh] - m_new);
                     }
+                    const float zt = row16_sum((w[0] + w[1]) + (w[2] + w[3]));
+                    z_run[kl][eh] = z_run[kl][eh] * sf + zt;
+                    m_run[kl][eh] = m_new;
+                    if (g < G) {
 #pragma unroll
-                    for (int k = 0; k < 4; ++k) {   // int8 scales of positions 2k, 2k+1 as binary16
-                        const uint32_t pr = __builtin_amdgcn_perm(sw[nib][2 * k + 1], sw[nib][2 * k], sc_sel);
-                        const uint32_t sc = pk_add_f16((pr ^ 0x00800080u) | 0x64006400u, 0xE480E480u);   // - 1152
-                        sc6[k] = pk_mul_f16(sc, 0x54005400u);    // sc 2^6
-                        corr[k] = pk_mul_f16(sc, 0x98009800u);    // -sc 2^-9
+                        for (int rt = 0; rt < 4; ++rt) s_w[(kl * 8 + g) * kVtStride + 16 * rt + col] = w[rt];
+                        if (col == 0) s_f[kl * 8 + g] = ldexpf(sf, S_new - S_cur);
                     }
-                    const h8_t ac = __builtin_bit_cast(h8_t, uint4{corr[0], corr[1], corr[2], corr[3]});
+                }
+            }
+            __builtin_amdgcn_wave_barrier();
+            // rescale D (column 2g + part: head g), skipped when no running max and not S moved
+            const int gcol = col >> 1;
 #pragma unroll
-                    for (int b = 0; b < 4; ++b) {
-                        const uint32_t sel = (uint32_t)b | (0x0Cu << 8) | ((4u + b) << 16) | (0x0Cu << 24);
-                        uint32_t ah[4], al[4];
+            for (int kl = 0; kl < KPW; ++kl) {
+                if (kl == 1 && !two) break;
+                const float fl = gcol < G ? s_f[kl * 8 + gcol] : 1.0f;   // unused columns stay 0
+                if (__builtin_amdgcn_ballot_w64(fl != 1.0f) != 0) {
 #pragma unroll
-                        for (int k = 0; k < 4; ++k) {
-                            const uint32_t cp = __builtin_amdgcn_perm(code4[2 * k + 1], code4[2 * k], sel) << 4;
-                            ah[k] = pk_mul_f16(cp, sc6[k]);
-                            al[k] = pk_fms_f16(cp, sc6[k], ah[k]);   // remainder, exact
+                    for (int t = 0; t < 8; ++t) D[kl][t] *= fl;
+                }
+            }
+            S_cur = S_new;
+            // P V, 32 positions per step: this lane's positions 32 ks + 8 u + i
+#pragma unroll 1
+            for (int ks = 0; ks < 2; ++ks) {
+                const int pk0 = 32 * ks + 8 * u;
+                float dS[8];
+                {
+                    const uint4 d0 = *reinterpret_cast<const uint4*>(vt + 52 * kVtStride + pk0);
+                    const uint4 d1 = *reinterpret_cast<const uint4*>(vt + 52 * kVtStride + pk0 + 4);
+                    const uint32_t dw[8] = {d0.x, d0.y, d0.z, d0.w, d1.x, d1.y, d1.z, d1.w};
+#pragma unroll
+                    for (int i = 0; i < 8; ++i) dS[i] = ldexpf(half_lo(dw[i]), S_cur);
+                }
+#pragma unroll
+                for (int kl = 0; kl < KPW; ++kl) {
+                    if (kl == 1 && !two) break;
+                    const int hh = hh_of(kl);
+                    // B: column col = head gcol, part col & 1: x = w d 2^S as hi + lo, both
+                    // rounded toward zero (|x - hi - lo| < 2^-21 |x|); columns of heads >= G
+                    // are never read
+                    h8_t bop;
+                    {
+                        const float* wr = s_w + (kl * 8 + gcol) * kVtStride + pk0;
+                        const float4 w0 = *reinterpret_cast<const float4*>(wr);
+                        const float4 w1 = *reinterpret_cast<const float4*>(wr + 4);
+                        const float wv[8] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
+                        const bool part = (col & 1) != 0;
+#pragma unroll
+                        for (int i = 0; i < 8; i += 2) {
+                            const float x0 = wv[i] * dS[i], x1 = wv[i + 1] * dS[i + 1];
+                            const h2v_t h = __builtin_bit_cast(h2v_t, __builtin_amdgcn_cvt_pkrtz(x0, x1));
+                            const h2v_t l =
+                                __builtin_bit_cast(h2v_t, __builtin_amdgcn_cvt_pkrtz(x0 - (float)h.x, x1 - (float)h.y));
+                            const h2v_t v = part ? l : h;
+                            bop[i] = v.x;
+                            bop[i + 1] = v.y;
                         }
-                        const int t = 4 * nib + b;
-                        D[kl][t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
-                            __builtin_bit_cast(h8_t, uint4{ah[0], ah[1], ah[2], ah[3]}), bop, D[kl][t], 0, 0, 0);
-                        D[kl][t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
-                            __builtin_bit_cast(h8_t, uint4{al[0], al[1], al[2], al[3]}), bop, D[kl][t], 0, 0, 0);
-                        D[kl][t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ac, bop, D[kl][t], 0, 0, 0);
+                    }
+                    // A: ql dword col, qh dword col & 7, sub-block scale dwords of nib 0 / 1
+                    uint32_t ql[8], qh[8], sw[2][8];
+                    {
+                        auto rd8 = [&](int row, uint32_t* dst) {
+                            const uint4 x0 = *reinterpret_cast<const uint4*>(vt + row * kVtStride + pk0);
+                            const uint4 x1 = *reinterpret_cast<const uint4*>(vt + row * kVtStride + pk0 + 4);
+                            dst[0] = x0.x; dst[1] = x0.y; dst[2] = x0.z; dst[3] = x0.w;
+                            dst[4] = x1.x; dst[5] = x1.y; dst[6] = x1.z; dst[7] = x1.w;
+                        };
+                        rd8(16 * hh + col, ql);
+                        rd8(32 + 8 * hh + (col & 7), qh);
+                        rd8(48 + 2 * hh, sw[0]);
+                        rd8(49 + 2 * hh, sw[1]);
+                    }
+                    // e 2^-14 = c sc 2^-14 - 32 sc 2^-14: the code pair shifted to c 2^-20
+                    // (binary16 subnormals) times sc 2^6 gives c sc 2^-14 as hi plus the exact
+                    // remainder lo (|c sc| < 2^13, every nonzero product >= 2^-14, so the
+                    // matrix-core operands are normal), and -sc 2^-9 (exact) goes in a third
+                    // instruction; D is then in units of 2^(S - 14)
+#pragma unroll
+                    for (int nib = 0; nib < 2; ++nib) {
+                        uint32_t code4[8], sc6[4], corr[4];
+#pragma unroll
+                        for (int i = 0; i < 8; ++i) {
+                            const uint32_t lo4 = nib ? (ql[i] >> 4) : ql[i];
+                            const uint32_t hi2 = __builtin_amdgcn_alignbit(qh[i], qh[i], rot[nib]) & 0x30303030u;
+                            code4[i] = (lo4 & 0x0F0F0F0Fu) | hi2;
+                        }
+#pragma unroll
+                        for (int k = 0; k < 4; ++k) {   // int8 scales of positions 2k, 2k+1 as binary16
+                            const uint32_t pr = __builtin_amdgcn_perm(sw[nib][2 * k + 1], sw[nib][2 * k], sc_sel);
+                            const uint32_t sc = pk_add_f16((pr ^ 0x00800080u) | 0x64006400u, 0xE480E480u);   // - 1152
+                            sc6[k] = pk_mul_f16(sc, 0x54005400u);    // sc 2^6
+                            corr[k] = pk_mul_f16(sc, 0x98009800u);    // -sc 2^-9
+                        }
+                        const h8_t ac = __builtin_bit_cast(h8_t, uint4{corr[0], corr[1], corr[2], corr[3]});
+#pragma unroll
+                        for (int b = 0; b < 4; ++b) {
+                            const uint32_t sel = (uint32_t)b | (0x0Cu << 8) | ((4u + b) << 16) | (0x0Cu << 24);
+                            uint32_t ah[4], al[4];
+#pragma unroll
+                            for (int k = 0; k < 4; ++k) {
+                                const uint32_t cp = __builtin_amdgcn_perm(code4[2 * k + 1], code4[2 * k], sel) << 4;
+                                ah[k] = pk_mul_f16(cp, sc6[k]);
+                                al[k] = pk_fms_f16(cp, sc6[k], ah[k]);   // remainder, exact
+                            }
+                            const int t = 4 * nib + b;
+                            D[kl][t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
+                                __builtin_bit_cast(h8_t, uint4{ah[0], ah[1], ah[2], ah[3]}), bop, D[kl][t], 0, 0, 0);
+                            D[kl][t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
+                                __builtin_bit_cast(h8_t, uint4{al[0], al[1], al[2], al[3]}), bop, D[kl][t], 0, 0, 0);
+                            D[kl][t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ac, bop, D[kl][t], 0, 0, 0);
+                        }
                     }
                 }
             }
+            __builtin_amdgcn_wave_barrier();   // the next tile's staging overwrites vt and s_w
         }
-        __builtin_amdgcn_wave_barrier();   // the next tile's staging overwrites vt and s_w
-    }
 
-    // records: U_g[dim] = (D_2g + D_2g+1) 2^-S, then m and Z
-    float* rec = a.ws + ((int64_t)s * a.nchunk + c) * a.hq * kRec;
-    const float unit = ldexpf(1.0f, 14 - S_cur);   // D is in units of 2^(S - 14)
-    const int gcol = col >> 1;
-    const bool writer = (col & 1) == 0 && gcol < G;
+        // records: U_g[dim] = (D_2g + D_2g+1) 2^-S, then m and Z
+        // record k of the sequence: k = this workgroup - the one holding its first tile
+        const int64_t w_lo = ((s_first + 1) * P - 1) / T;
+        float* rec = a.ws + ((int64_t)s * a.rstride + ((int64_t)blockIdx.x - w_lo)) * a.hq * kRec;
+        const float unit = ldexpf(1.0f, 14 - S_cur);   // D is in units of 2^(S - 14)
+        const int gcol = col >> 1;
+        const bool writer = (col & 1) == 0 && gcol < G;
 #pragma unroll
-    for (int kl = 0; kl < KPW; ++kl) {
-        if (kl == 1 && !two) break;
-        const int kvh = kv0 + kl;
-        float* rh = rec + (int64_t)(kvh * G + (gcol < G ? gcol : 0)) * kRec;
+        for (int kl = 0; kl < KPW; ++kl) {
+            if (kl == 1 && !two) break;
+            const int kvh = kv0 + kl;
+            float* rh = rec + (int64_t)(kvh * G + (gcol < G ? gcol : 0)) * kRec;
 #pragma unroll
-        for (int t = 0; t < 8; ++t) {
-            const int nib = t >> 2, b = t & 3;
+            for (int t = 0; t < 8; ++t) {
+                const int nib = t >> 2, b = t & 3;
 #pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                float v = D[kl][t][e];
-                v += dpp_mov<0xB1>(v);                  // + the other part of the head
-                const int rr = 4 * u + e;
-                const int dim = 32 * (2 * nib + (rr >= 8 ? 1 : 0)) + 4 * (rr & 7) + b;
-                if (writer) rh[dim] = v * unit;
+                for (int e = 0; e < 4; ++e) {
+                    float v = D[kl][t][e];
+                    v += dpp_mov<0xB1>(v);                  // + the other part of the head
+                    const int rr = 4 * u + e;
+                    const int dim = 32 * (2 * nib + (rr >= 8 ? 1 : 0)) + 4 * (rr & 7) + b;
+                    if (writer) rh[dim] = v * unit;
+                }
+            }
+#pragma unroll
+            for (int eh = 0; eh < 2; ++eh) {
+                const int g = 2 * u + eh;
+                if (col == 0 && g < G) {
+                    rec[(int64_t)(kvh * G + g) * kRec + kHd] = m_run[kl][eh] * 0.6931471805599453f;
+                    rec[(int64_t)(kvh * G + g) * kRec + kHd + 1] = z_run[kl][eh];
+                }
             }
         }
-#pragma unroll
-        for (int eh = 0; eh < 2; ++eh) {
-            const int g = 2 * u + eh;
-            if (col == 0 && g < G) {
-                rec[(int64_t)(kvh * G + g) * kRec + kHd] = m_run[kl][eh] * 0.6931471805599453f;
-                rec[(int64_t)(kvh * G + g) * kRec + kHd + 1] = z_run[kl][eh];
-            }
-        }
+        x = seg_end;
+        ++s;
     }
     if (err) raise_error(err);
+}
+
+// The tile list of the matrix-core kernel: sequence s holds tiles
+// [S[s], S[s + 1]) (min(ceil(visible / 64), max_tiles) of them, the oldest positions
+// first), and workgroup w of P = min(workgroups, T) takes tiles [floor(w T / P),
+// floor((w + 1) T / P)), T = S[nseq], at least one.  Also records, per workgroup, the sequence holding its first tile: the
+// workgroups whose first tile lies in s are w in [ceil(S[s] P / T), ceil(S[s + 1] P / T)).
+__global__ void __launch_bounds__(256) attn_plan_kernel(const AttnArgs a) {
+    __shared__ int s_tot[4];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    auto tiles_of = [&](int s) {
+        int64_t t = 0;
+        if (s < a.nseq) {
+            const int64_t L = a.ctx_len[s];
+            const int64_t vis = L < a.capacity ? L : a.capacity;
+            if (vis > 0) t = (vis + kTile - 1) / kTile;
+            if (t > a.max_tiles) t = a.max_tiles;
+        }
+        return (int)t;
+    };
+    auto block_scan = [&](int t, int& before, int& total) {   // exclusive prefix over the block
+        int x = t;
+        for (int off = 1; off < kWave; off <<= 1) {
+            const int y = __shfl_up(x, off, kWave);
+            if (lane >= off) x += y;
+        }
+        if (lane == kWave - 1) s_tot[wave] = x;
+        __syncthreads();
+        before = x - t;
+        for (int w2 = 0; w2 < wave; ++w2) before += s_tot[w2];
+        total = s_tot[0] + s_tot[1] + s_tot[2] + s_tot[3];
+        __syncthreads();
+    };
+    int64_t T = 0;
+    for (int s0 = 0; s0 < a.nseq; s0 += 256) {
+        int before, total;
+        block_scan(tiles_of(s0 + tid), before, total);
+        T += total;
+    }
+    int64_t carry = 0;
+    const int64_t P = a.nwg < T ? a.nwg : T;   // workgroups in use: each gets a tile
+    for (int s0 = 0; s0 < a.nseq; s0 += 256) {
+        const int s = s0 + tid;
+        const int t = tiles_of(s);
+        int before, total;
+        block_scan(t, before, total);
+        if (s < a.nseq) {
+            const int64_t first = carry + before, end = first + t;
+            a.plan[s] = (int32_t)first;
+            if (T > 0 && t > 0) {
+                for (int64_t w = (first * P + T - 1) / T; w < (end * P + T - 1) / T && w < P; ++w)
+                    a.plan[a.nseq + 1 + w] = s;
+            }
+        }
+        carry += total;
+    }
+    if (tid == 0) a.plan[a.nseq] = (int32_t)T;
 }
 
 // One workgroup per (sequence, query head): 8 chunk groups x 32 lanes of 4
@@ -1132,12 +1224,23 @@ __global__ void __launch_bounds__(256) attn_merge_kernel(const AttnArgs a) {
         }
         return;
     }
-    const int64_t chunk = (int64_t)a.nt * kTile;
-    int nch = (int)((visible + chunk - 1) / chunk);
-    const bool short_grid = nch > a.nchunk;   // max_ctx was below this sequence's visible count
-    if (short_grid) nch = a.nchunk;
     const int64_t cstride = (int64_t)a.hq * kRec;
-    const float* rec0 = a.ws + (int64_t)s * a.nchunk * cstride + (int64_t)h * kRec;
+    int nch;
+    bool short_grid;   // max_ctx was below this sequence's visible count
+    const float* rec0;
+    if (a.plan) {   // one record per workgroup that covered tiles of the sequence
+        const int64_t T = a.plan[a.nseq], P = a.nwg < T ? a.nwg : T;
+        const int64_t first = a.plan[s], end = a.plan[s + 1];
+        nch = (int)(((end * P - 1) / T) - (((first + 1) * P - 1) / T) + 1);
+        short_grid = visible > a.max_tiles * kTile;
+        rec0 = a.ws + (int64_t)s * a.rstride * cstride + (int64_t)h * kRec;
+    } else {        // one record per chunk
+        const int64_t chunk = (int64_t)a.nt * kTile;
+        nch = (int)((visible + chunk - 1) / chunk);
+        short_grid = nch > a.nchunk;
+        if (short_grid) nch = a.nchunk;
+        rec0 = a.ws + (int64_t)s * a.nchunk * cstride + (int64_t)h * kRec;
+    }
     float mx = -INFINITY;
     for (int ci = tid; ci < nch; ci += 256) mx = fmaxf(mx, rec0[ci * cstride + kHd]);
     mx = group_max(mx, kWave);
@@ -1251,8 +1354,23 @@ static hipError_t launch_chunk_mma(const AttnArgs& a, hipStream_t s) {
         if (e != hipSuccess) return e;
         configured = true;
     }
-    hipLaunchKernelGGL((attn_chunk_mma_kernel<G, KPW>), dim3(a.nchunk, a.nseq), dim3(256), kMmaLdsBytes, s, a);
+    hipLaunchKernelGGL(attn_plan_kernel, dim3(1), dim3(256), 0, s, a);
+    hipLaunchKernelGGL((attn_chunk_mma_kernel<G, KPW>), dim3(a.nwg), dim3(256), kMmaLdsBytes, s, a);
     return hipGetLastError();
+}
+
+// Workgroups of the matrix-core kernel: two per compute unit (its LDS and registers
+// admit two), all resident at once.
+static int attn_mma_workgroups() {
+    static int n = 0;
+    if (n == 0) {
+        int dev = 0, cus = 0;
+        if (hipGetDevice(&dev) != hipSuccess ||
+            hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
+            cus = 256;
+        n = 2 * cus < kMaxWg ? 2 * cus : kMaxWg;
+    }
+    return n;
 }
 
 template <int KF, int VF, int G>
@@ -1304,14 +1422,16 @@ int rta_rope(float* v, int rows, int heads, int hd, int rotary, const int64_t* p
 // Chunk records [nseq][nchunk][hq][kRec] floats, then the matrix-core q operands
 // [nseq][hkv][6][64] 16-byte words.
 static size_t attn_record_bytes(int nseq, int hq, int max_ctx) {
-    const int64_t chunk = (int64_t)attn_tiles(nseq, max_ctx) * kTile;
-    const int64_t nchunk = ((int64_t)max_ctx + chunk - 1) / chunk;
-    return (size_t)nseq * (size_t)nchunk * (size_t)hq * kRec * sizeof(float);
+    // room for one record per tile (the chunk grid needs one per chunk, the tile-list
+    // split at most one per tile of the sequence)
+    const int64_t tiles = ((int64_t)max_ctx + kTile - 1) / kTile;
+    return (size_t)nseq * (size_t)tiles * (size_t)hq * kRec * sizeof(float);
 }
 
 size_t rta_decode_attention_workspace_bytes(int nseq, int hq, int hkv, int hd, int max_ctx) {
     if (nseq <= 0 || hq <= 0 || hkv <= 0 || hd != kHd || max_ctx <= 0 || hq % hkv) return 0;
-    return attn_record_bytes(nseq, hq, max_ctx) + (size_t)nseq * hkv * 6 * kWave * sizeof(uint4);
+    return attn_record_bytes(nseq, hq, max_ctx) + (size_t)nseq * hkv * 6 * kWave * sizeof(uint4) +
+           (((size_t)nseq + 1 + kMaxWg) * sizeof(int32_t) + 15) / 16 * 16;
 }
 
 int rta_decode_attention(const float* q, int nseq, int hq, int hkv, int hd, const void* packets, int fmt_k, int fmt_v,
@@ -1359,6 +1479,12 @@ int rta_decode_attention(const float* q, int nseq, int hq, int hkv, int hd, cons
     a.nt = attn_tiles(nseq, max_ctx);
     a.nchunk = (int)((max_ctx + a.nt * kTile - 1) / (a.nt * kTile));
     a.nblk = nblk;
+    a.max_tiles = ((int64_t)max_ctx + kTile - 1) / kTile;
+    if (fmt_k == RTA_Q4_K && fmt_v == RTA_Q6_K && hkv <= 8) {   // the matrix-core kernel's tile-list split
+        a.plan = reinterpret_cast<int32_t*>(reinterpret_cast<uint8_t*>(a.qop) + (size_t)nseq * hkv * 6 * kWave * sizeof(uint4));
+        a.nwg = attn_mma_workgroups();
+        a.rstride = a.max_tiles;
+    }
     hipStream_t s = (hipStream_t)stream;
     hipError_t e;
     if (fmt_k == RTA_Q4_K && fmt_v == RTA_Q6_K) e = launch_chunks<RTA_Q4_K, RTA_Q6_K>(G, a, lds, s);

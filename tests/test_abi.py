@@ -46,13 +46,17 @@ def test_host_queries(lib):
     assert lib.rta_gemv_workspace_bytes(_lib.Q4_K, 4096, 4096, 1) == 0
     assert lib.rta_gemv_workspace_bytes(_lib.Q4_K, 4096, 4096, 32) > 0
     assert lib.rta_mlp_workspace_bytes(_lib.Q4_K, _lib.Q6_K, 2048, 6144, 4) == 0
-    # one (U[128], m, Z, 2 pad) record per (sequence, chunk, q head); chunks of 64 * nt positions
-    # with nt = 2, 4 as nseq * ceil(max_ctx / 64) crosses 16384; then 6 x 64
-    # 16-byte q-operand words per (sequence, kv head)
+    # room for one (U[128], m, Z, 2 pad) record per (sequence, 64-position tile, q head);
+    # then 6 x 64 16-byte q-operand words per (sequence, kv head); then the tile-list
+    # plan, nseq + 1 + 2048 int32 rounded up to 16 bytes
     q = lambda nseq, hkv: nseq * hkv * 6 * 64 * 16
-    assert lib.rta_decode_attention_workspace_bytes(16, 16, 4, 128, 32768) == 16 * 256 * 16 * 132 * 4 + q(16, 4)
-    assert lib.rta_decode_attention_workspace_bytes(32, 32, 8, 128, 8448) == 32 * 66 * 32 * 132 * 4 + q(32, 8)
-    assert lib.rta_decode_attention_workspace_bytes(64, 32, 8, 128, 16384) == 64 * 64 * 32 * 132 * 4 + q(64, 8)
+    plan = lambda nseq: ((nseq + 1 + 2048) * 4 + 15) // 16 * 16
+    assert lib.rta_decode_attention_workspace_bytes(16, 16, 4, 128, 32768) == \
+        16 * 512 * 16 * 132 * 4 + q(16, 4) + plan(16)
+    assert lib.rta_decode_attention_workspace_bytes(32, 32, 8, 128, 8448) == \
+        32 * 132 * 32 * 132 * 4 + q(32, 8) + plan(32)
+    assert lib.rta_decode_attention_workspace_bytes(64, 32, 8, 128, 16384) == \
+        64 * 256 * 32 * 132 * 4 + q(64, 8) + plan(64)
     assert lib.rta_decode_attention_workspace_bytes(16, 16, 4, 64, 32768) == 0
     # packed (tiled) matrices: ceil(rows/16) * (cols/256) tiles of 16 blocks
     assert lib.rta_pack_bytes(_lib.Q4_K, 4096, 4096) == 256 * 16 * 2304
