@@ -302,11 +302,69 @@ __device__ __forceinline__ QOp make_qop(const float* __restrict__ qg, int lane) 
     return o;
 }
 
+// The tile list of the matrix-core kernel, built by one wave: sequence s holds tiles
+// [S[s], S[s + 1]) (min(ceil(visible / 64), max_tiles) of them, the oldest positions
+// first), and workgroup w of P = min(workgroups, T) takes tiles [floor(w T / P),
+// floor((w + 1) T / P)), T = S[nseq], at least one.  Also records, per workgroup, the
+// sequence holding its first tile: the workgroups whose first tile lies in s are w in
+// [ceil(S[s] P / T), ceil(S[s + 1] P / T)).
+__device__ __forceinline__ void attn_plan_wave(const AttnArgs& a) {
+    const int lane = threadIdx.x & 63;
+    auto tiles_of = [&](int s) {
+        int64_t t = 0;
+        if (s < a.nseq) {
+            const int64_t L = a.ctx_len[s];
+            const int64_t vis = L < a.capacity ? L : a.capacity;
+            if (vis > 0) t = (vis + kTile - 1) / kTile;
+            if (t > a.max_tiles) t = a.max_tiles;
+        }
+        return (int)t;
+    };
+    auto scan = [&](int t, int& before, int& total) {   // exclusive prefix over the wave
+        int x = t;
+        for (int off = 1; off < kWave; off <<= 1) {
+            const int y = __shfl_up(x, off, kWave);
+            if (lane >= off) x += y;
+        }
+        before = x - t;
+        total = __shfl(x, kWave - 1, kWave);
+    };
+    int64_t T = 0;
+    for (int s0 = 0; s0 < a.nseq; s0 += kWave) {
+        int before, total;
+        scan(tiles_of(s0 + lane), before, total);
+        T += total;
+    }
+    int64_t carry = 0;
+    const int64_t P = a.nwg < T ? a.nwg : T;   // workgroups in use: each gets a tile
+    for (int s0 = 0; s0 < a.nseq; s0 += kWave) {
+        const int s = s0 + lane;
+        const int t = tiles_of(s);
+        int before, total;
+        scan(t, before, total);
+        if (s < a.nseq) {
+            const int64_t first = carry + before, end = first + t;
+            a.plan[s] = (int32_t)first;
+            if (T > 0 && t > 0) {
+                for (int64_t w = (first * P + T - 1) / T; w < (end * P + T - 1) / T && w < P; ++w)
+                    a.plan[a.nseq + 1 + w] = s;
+            }
+        }
+        carry += total;
+    }
+    if (lane == 0) a.plan[a.nseq] = (int32_t)T;
+}
+
 // q operands of one (sequence, kv head), built once and read by every chunk: six
-// 16-byte words per lane (a[0..3], am, rs).
+// 16-byte words per lane (a[0..3], am, rs).  With a plan (the matrix-core kernel), the
+// extra block (hkv, 0) builds the tile list.
 template <int G>
 __global__ void __launch_bounds__(64) attn_qprep_kernel(const AttnArgs a) {
     const int kvh = blockIdx.x, s = blockIdx.y, lane = threadIdx.x;
+    if (kvh == a.hkv) {
+        if (s == 0 && a.plan) attn_plan_wave(a);
+        return;
+    }
     const QOp o = make_qop<G>(a.q + ((int64_t)s * a.hq + (int64_t)kvh * G) * kHd, lane);
     uint4* dst = a.qop + ((int64_t)s * a.hkv + kvh) * 6 * kWave + lane;
 #pragma unroll
@@ -1144,63 +1202,6 @@ __global__ void __launch_bounds__(256, 2) attn_chunk_mma_kernel(const AttnArgs a
     if (err) raise_error(err);
 }
 
-// The tile list of the matrix-core kernel: sequence s holds tiles
-// [S[s], S[s + 1]) (min(ceil(visible / 64), max_tiles) of them, the oldest positions
-// first), and workgroup w of P = min(workgroups, T) takes tiles [floor(w T / P),
-// floor((w + 1) T / P)), T = S[nseq], at least one.  Also records, per workgroup, the sequence holding its first tile: the
-// workgroups whose first tile lies in s are w in [ceil(S[s] P / T), ceil(S[s + 1] P / T)).
-__global__ void __launch_bounds__(256) attn_plan_kernel(const AttnArgs a) {
-    __shared__ int s_tot[4];
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    auto tiles_of = [&](int s) {
-        int64_t t = 0;
-        if (s < a.nseq) {
-            const int64_t L = a.ctx_len[s];
-            const int64_t vis = L < a.capacity ? L : a.capacity;
-            if (vis > 0) t = (vis + kTile - 1) / kTile;
-            if (t > a.max_tiles) t = a.max_tiles;
-        }
-        return (int)t;
-    };
-    auto block_scan = [&](int t, int& before, int& total) {   // exclusive prefix over the block
-        int x = t;
-        for (int off = 1; off < kWave; off <<= 1) {
-            const int y = __shfl_up(x, off, kWave);
-            if (lane >= off) x += y;
-        }
-        if (lane == kWave - 1) s_tot[wave] = x;
-        __syncthreads();
-        before = x - t;
-        for (int w2 = 0; w2 < wave; ++w2) before += s_tot[w2];
-        total = s_tot[0] + s_tot[1] + s_tot[2] + s_tot[3];
-        __syncthreads();
-    };
-    int64_t T = 0;
-    for (int s0 = 0; s0 < a.nseq; s0 += 256) {
-        int before, total;
-        block_scan(tiles_of(s0 + tid), before, total);
-        T += total;
-    }
-    int64_t carry = 0;
-    const int64_t P = a.nwg < T ? a.nwg : T;   // workgroups in use: each gets a tile
-    for (int s0 = 0; s0 < a.nseq; s0 += 256) {
-        const int s = s0 + tid;
-        const int t = tiles_of(s);
-        int before, total;
-        block_scan(t, before, total);
-        if (s < a.nseq) {
-            const int64_t first = carry + before, end = first + t;
-            a.plan[s] = (int32_t)first;
-            if (T > 0 && t > 0) {
-                for (int64_t w = (first * P + T - 1) / T; w < (end * P + T - 1) / T && w < P; ++w)
-                    a.plan[a.nseq + 1 + w] = s;
-            }
-        }
-        carry += total;
-    }
-    if (tid == 0) a.plan[a.nseq] = (int32_t)T;
-}
-
 // One workgroup per (sequence, query head): 8 chunk groups x 32 lanes of 4
 // coordinates; every thread keeps 8 chunk records in flight.
 __global__ void __launch_bounds__(256) attn_merge_kernel(const AttnArgs a) {
@@ -1354,7 +1355,6 @@ static hipError_t launch_chunk_mma(const AttnArgs& a, hipStream_t s) {
         if (e != hipSuccess) return e;
         configured = true;
     }
-    hipLaunchKernelGGL(attn_plan_kernel, dim3(1), dim3(256), 0, s, a);
     hipLaunchKernelGGL((attn_chunk_mma_kernel<G, KPW>), dim3(a.nwg), dim3(256), kMmaLdsBytes, s, a);
     return hipGetLastError();
 }
@@ -1377,7 +1377,8 @@ template <int KF, int VF, int G>
 static hipError_t launch_chunk_k(const AttnArgs& a, int lds, hipStream_t s) {
     if constexpr (KF == RTA_Q4_K) {
         if (a.hkv <= 8) {
-            hipLaunchKernelGGL((attn_qprep_kernel<G>), dim3(a.hkv, a.nseq), dim3(kWave), 0, s, a);
+            // (one more column of blocks builds the tile list of the matrix-core kernel)
+            hipLaunchKernelGGL((attn_qprep_kernel<G>), dim3(a.hkv + (a.plan ? 1 : 0), a.nseq), dim3(kWave), 0, s, a);
             if constexpr (VF == RTA_Q6_K) {   // scores and P V on the matrix cores
                 if (a.hkv <= 4) return launch_chunk_mma<G, 1>(a, s);
                 return launch_chunk_mma<G, 2>(a, s);
