@@ -218,7 +218,6 @@ __global__ void __launch_bounds__(64 * kGemmWaves) gemm_tiled_kernel(
     using F = TileFmt<FMT>;
     using Raw = typename F::Raw;
     using Smem = GemmSmem<NBT>;
-    constexpr int kRows = Smem::kRows;
     __shared__ Smem sm;
 
     const int tid = threadIdx.x, lane = tid & 63;
