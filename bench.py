@@ -483,7 +483,7 @@ def w_decode(torch, args, orc):
     step_bytes = w_bytes + m.lm_head.numel() + hist + state
     alg_k = sum_ctx * v.packet_bytes + 2 * batch * hq * hd * 4
     res = {"alg_bytes": step_bytes, "alg_bytes_kernel": alg_k, "graph_per_step": True,
-           "kernel": f"attn_chunk_kernel<Q4_K,Q6_K,G=4> + attn_merge_kernel (one layer: {batch} sequences, "
+           "kernel": f"attn_qprep_kernel (with the tile-list plan) + attn_chunk_mma_kernel<G=4,KPW=2> + attn_merge_kernel (one layer: {batch} sequences, "
                      f"{hq}/{hkv} heads, {sum_ctx} positions of {v.packet_bytes}-byte K/V packets)",
            "step": step, "kernel_launch": attention, "unit": "tok/s", "value_from_ms": lambda ms: batch / (ms * 1e-3),
            "dtype": "q4_k/q6_k weights x fp32 activations and state, fp32 accumulate",
