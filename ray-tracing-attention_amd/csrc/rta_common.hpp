@@ -93,14 +93,18 @@ __device__ __forceinline__ void q4k_scale_min(uint32_t s0, uint32_t s1, uint32_t
     }
 }
 
-// Scale and minimum of Q4_K group g (0..7, may differ between lanes).
+// Scale and minimum of Q4_K group g (0..7, may differ between lanes), without a
+// branch: both forms are computed and one is kept by a bit mask (a lane-dependent
+// ternary compiles to two exec-masked paths).
 __device__ __forceinline__ void q4k_scale_min_lane(uint32_t s0, uint32_t s1, uint32_t s2, int g, uint32_t& sc,
                                                    uint32_t& m) {
     const uint32_t sh = 8u * (uint32_t)(g & 3);
-    const uint32_t a = (s0 >> sh) & 255u, b = (s1 >> sh) & 255u, mixed = (s2 >> sh) & 255u;
-    const bool lo = g < 4;
-    sc = lo ? (a & 63u) : ((mixed & 15u) | ((a >> 6) << 4));
-    m = lo ? (b & 63u) : ((mixed >> 4) | ((b >> 6) << 4));
+    const uint32_t a = s0 >> sh, b = s1 >> sh, mixed = s2 >> sh;
+    const uint32_t sc_lo = a & 63u, m_lo = b & 63u;
+    const uint32_t sc_hi = (mixed & 15u) | ((a >> 2) & 0x30u), m_hi = ((mixed >> 4) & 15u) | ((b >> 2) & 0x30u);
+    const uint32_t keep_lo = g < 4 ? 0xFFFFFFFFu : 0u;
+    sc = (sc_lo & keep_lo) | (sc_hi & ~keep_lo);
+    m = (m_lo & keep_lo) | (m_hi & ~keep_lo);
 }
 
 // ---- matrix-core operand helpers (v_mfma_f32_16x16x32_f16) ----

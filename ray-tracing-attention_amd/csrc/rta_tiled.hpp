@@ -241,13 +241,22 @@ __global__ void __launch_bounds__(64 * kGemmWaves) gemm_tiled_kernel(
         if constexpr (MODE == kSwiglu) { t0 = t1 = ta + u; }
         else { t0 = ta + 2 * u; t1 = min(t0 + 1, tb - 1); }
     };
-    auto load_w = [&](int it, Raw* dst) {
-        const int u = it / nsb, sbl = it - u * nsb;
+    // (unit, superblock) of the next weight load, advanced one iteration at a time and
+    // held at the last iteration (no division in the loop)
+    int lu = 0, lsb = 0, lit = 0;
+    auto load_next = [&](Raw* dst) {
         int t0, t1;
-        tiles_of(u, t0, t1);
-        const int64_t sb = sb0 + sbl;
+        tiles_of(lu, t0, t1);
+        const int64_t sb = sb0 + lsb;
         F::load(w + ((int64_t)t0 * nsbt + sb) * F::kBytes, lane, dst[0]);
         F::load((MODE == kSwiglu ? w2 : w) + ((int64_t)t1 * nsbt + sb) * F::kBytes, lane, dst[1]);
+        if (lit < nit - 1) {
+            ++lit;
+            if (++lsb == nsb) {
+                lsb = 0;
+                ++lu;
+            }
+        }
     };
 
     // x loads first (vector-memory loads complete in order, so the x slab is not held
@@ -258,7 +267,7 @@ __global__ void __launch_bounds__(64 * kGemmWaves) gemm_tiled_kernel(
     Raw buf[DEPTH][2];
     if (nit > 0) {
 #pragma unroll
-        for (int d = 0; d < DEPTH - 1; ++d) load_w(min(d, nit - 1), buf[d]);
+        for (int d = 0; d < DEPTH - 1; ++d) load_next(buf[d]);
     }
     xs.store(sm, batch, nsb, rn);
     __syncthreads();
@@ -469,17 +478,19 @@ __global__ void __launch_bounds__(64 * kGemmWaves) gemm_tiled_kernel(
             for (int bt = 0; bt < NBT; ++bt) acc[t][bt] = f4_t{0.0f, 0.0f, 0.0f, 0.0f};
     };
 
+    int cu = 0, csb = 0;   // (unit, superblock) being multiplied
     for (int it0 = 0; it0 < nit; it0 += DEPTH) {
 #pragma unroll
         for (int d = 0; d < DEPTH; ++d) {
             const int it = it0 + d;
-            load_w(min(it + DEPTH - 1, nit - 1), buf[(d + DEPTH - 1) % DEPTH]);
+            load_next(buf[(d + DEPTH - 1) % DEPTH]);
             if (it < nit) {
-                const int u = it / nsb;
-                int t0, t1;
-                tiles_of(u, t0, t1);
-                compute(it - u * nsb, buf[d]);
-                if (it - u * nsb == nsb - 1) finish(u);
+                compute(csb, buf[d]);
+                if (csb == nsb - 1) finish(cu);
+                if (++csb == nsb) {
+                    csb = 0;
+                    ++cu;
+                }
             }
         }
     }
