@@ -300,6 +300,48 @@ int rta_hybrid_decode_step(const rta_hybrid_shape* shape, const rta_hybrid_weigh
                            uint32_t* tokens, float* logits_out, void* workspace, size_t workspace_bytes,
                            rta_stream_t stream);
 
+/* ---------------- on-disk assets (host only: no device work, no GPU needed).
+ * Reads the exporter's optical_model.bin (RTRES004), geometry_weights.bin and
+ * vocabulary.bin (RTBASQ01) into host memory (ray_tracing/compiler/export.py:51-138),
+ * with the checks and messages of the reference worker's loader
+ * (ray_tracing/native/src/optical_resident.cpp:139-152).  Replaces that loader; the
+ * payloads are GGUF rows as the projection entry points take them. */
+typedef struct rta_asset rta_asset;
+
+typedef struct rta_asset_info {
+    uint32_t hidden, depth, blocks, middle, vocab, quantization, step;
+    uint64_t param_words, matrix_words, basis_words;
+    uint32_t fmt_embed, fmt_lm;                  /* model header words 13, 15 */
+    uint64_t embed_offset_words, lm_offset_words; /* model header words 14, 16 */
+} rta_asset_info;
+
+typedef struct rta_asset_matrix {
+    const void* data;      /* host pointer to the raw payload */
+    uint64_t offset_words; /* from the start of geometry_weights.bin / the basis payload */
+    uint64_t avail_bytes;  /* bytes from data to the end of the layer range / file */
+    uint32_t fmt, mode;    /* GGUF code; the exporter's mode byte (export.py:91) */
+} rta_asset_matrix;
+
+/* Opens model_path (optical_model.bin; geometry_weights.bin is read from the same
+ * directory) and vocabulary_path (may be NULL to skip the basis).  On failure returns
+ * RTA_ERR_FORMAT and writes the reference's message into err (err_len bytes). */
+int rta_asset_open(const char* model_path, const char* vocabulary_path, rta_asset** out, char* err, size_t err_len);
+void rta_asset_close(rta_asset* asset);
+int rta_asset_get_info(const rta_asset* asset, rta_asset_info* info);
+/* The parameter words (model header, 64-word layer headers, fp32 vectors). */
+const uint32_t* rta_asset_params(const rta_asset* asset, uint64_t* words);
+/* Projection descriptor index 0..8 of a layer (export.py:87-91, 96-98, 108-109, 121):
+ * 0 q / qkv, 1 k, 2 output / ssm_out, 3 ffn_gate, 4 ffn_down, 5 ffn_up, 6 gate, 8 v. */
+int rta_asset_layer_matrix(const rta_asset* asset, int layer, int index, rta_asset_matrix* out);
+/* fp32 vector (count values) that word `field` of a layer header (layer -1: the model
+ * header) points at, e.g. 0 attn_norm, 1 post_attention_norm, 24/25 q/k norm; model 4
+ * output_norm. */
+int rta_asset_vector(const rta_asset* asset, int layer, int field, uint64_t count, const float** out);
+/* Word `field` of a layer header (layer -1: the model header). */
+int rta_asset_word(const rta_asset* asset, int layer, int field, uint32_t* value);
+/* token_embd (which 0) or output (which 1) payload in vocabulary.bin. */
+int rta_asset_basis(const rta_asset* asset, int which, rta_asset_matrix* out);
+
 #ifdef __cplusplus
 }
 #endif

@@ -9,8 +9,12 @@ import sys
 from pathlib import Path
 
 HERE = Path(__file__).resolve().parent
-SOURCES = ["csrc/rta_gemv.hip", "csrc/rta_attention.hip", "csrc/rta_step.hip", "csrc/rta_model.hip"]
+SOURCES = ["csrc/rta_gemv.hip", "csrc/rta_attention.hip", "csrc/rta_step.hip", "csrc/rta_model.hip",
+           "csrc/rta_asset.cpp"]
 LIB = HERE / "lib" / "librta.so"
+# the resident worker (stdin/stdout protocol of the reference's rt_optical_resident)
+WORKER_SRC = "worker/rt_optical_resident.cpp"
+WORKER = HERE / "lib" / "rt_optical_resident"
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 
 FLAGS = [
@@ -35,6 +39,18 @@ def build(verbose=False):
     if out.strip() and verbose:
         print(out, file=sys.stderr)
     os.replace(tmp, LIB)
+    wtmp = WORKER.with_suffix(".tmp")
+    cmd = [HIPCC, "--offload-arch=gfx950", "-O2", "-std=c++17", "-Xclang", "-target-feature", "-Xclang",
+           "-packed-fp32-ops", "-Wall", str(HERE / WORKER_SRC), "-L", str(LIB.parent), "-lrta",
+           "-Wl,-rpath,$ORIGIN", "-o", str(wtmp)]
+    if verbose:
+        print(" ".join(cmd), flush=True)
+    res = subprocess.run(cmd, capture_output=True, text=True)
+    out = "\n".join(l for l in (res.stdout + res.stderr).splitlines()
+                    if "packed-fp32-ops' is not a recognized feature" not in l)
+    if res.returncode != 0:
+        raise RuntimeError(f"hipcc failed on the worker ({res.returncode}):\n{out}")
+    os.replace(wtmp, WORKER)
     return LIB
 
 

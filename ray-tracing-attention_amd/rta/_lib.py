@@ -52,6 +52,15 @@ SIGNATURES = {
     "rta_decode_attention_workspace_bytes": (_sz, [_i, _i, _i, _i, _i]),
     "rta_decode_attention": (_i, [_p, _i, _i, _i, _i, _p, _i, _i, _p, _p, _i64, _i64, _i, _p, _p, _p, _p, _p, _sz,
                                   _p]),
+    # host-only asset reader (rta.asset binds the structs)
+    "rta_asset_open": (_i, [ctypes.c_char_p, ctypes.c_char_p, ctypes.POINTER(_p), ctypes.c_char_p, _sz]),
+    "rta_asset_close": (None, [_p]),
+    "rta_asset_get_info": (_i, [_p, _p]),
+    "rta_asset_params": (_u32p, [_p, ctypes.POINTER(ctypes.c_uint64)]),
+    "rta_asset_layer_matrix": (_i, [_p, _i, _i, _p]),
+    "rta_asset_vector": (_i, [_p, _i, _i, ctypes.c_uint64, ctypes.POINTER(ctypes.POINTER(_f))]),
+    "rta_asset_word": (_i, [_p, _i, _i, _u32p]),
+    "rta_asset_basis": (_i, [_p, _i, _p]),
 }
 
 

@@ -1,0 +1,502 @@
+// rt_optical_resident: a resident worker with the reference worker's command line and
+// stdin/stdout protocol (ray_tracing/native/src/optical_resident.cpp:966-969, framing
+// ray_tracing/runtime/resident_runtime.py:41-44,101-114), serving the three diagnostic
+// requests of the detector path on the gfx950 library:
+//   op 4  vocabulary readout  (wordCheck,      optical_resident.cpp:889-905; resident_runtime.py:235-250)
+//   op 6  SwiGLU MLP check    (mlpCheck,       optical_resident.cpp:922-949; resident_runtime.py:252-263)
+//   op 14 full-attention check (attentionCheck, resident_attention_runtime.inl:646-;
+//                               resident_runtime.py:265-345), standard backend, dense receipts
+// plus op 8 (resources) and op 0 (end).  Other operations (prefill, generation, ...)
+// end the worker with "Unknown resident operation" on stderr, as the reference does
+// for an operation it does not know.  Weights come from the exported assets through
+// rta_asset_*; every computation runs in librta's HIP kernels.
+#include <hip/hip_runtime.h>
+
+#include <chrono>
+#include <cmath>
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
+#include <fstream>
+#include <iostream>
+#include <map>
+#include <memory>
+#include <sstream>
+#include <stdexcept>
+#include <string>
+#include <vector>
+
+#include "../../include/rta.h"
+
+namespace {
+
+void hip_check(hipError_t e, const char* what) {
+    if (e != hipSuccess) throw std::runtime_error(std::string(what) + ": " + hipGetErrorString(e));
+}
+void rta_check(int rc, const char* what) {
+    if (rc != RTA_OK) throw std::runtime_error(std::string(what) + " failed (status " + std::to_string(rc) + ")");
+}
+
+struct Device {
+    void* p = nullptr;
+    size_t n = 0;
+    Device() = default;
+    Device(const Device&) = delete;
+    Device& operator=(const Device&) = delete;
+    ~Device() {
+        if (p) (void)hipFree(p);
+    }
+    void* ensure(size_t bytes) {
+        if (bytes > n) {
+            if (p) hip_check(hipFree(p), "hipFree");
+            p = nullptr;
+            n = 0;
+            hip_check(hipMalloc(&p, bytes ? bytes : 256), "hipMalloc");
+            n = bytes;
+        }
+        return p;
+    }
+    template <class T>
+    T* as() const { return static_cast<T*>(p); }
+};
+
+size_t row_bytes(uint32_t fmt, uint64_t cols) {
+    switch (fmt) {
+        case RTA_F32: return cols * 4;
+        case RTA_F16:
+        case RTA_BF16: return cols * 2;
+        case RTA_Q4_K: return cols / 256 * 144;
+        case RTA_Q6_K: return cols / 256 * 210;
+    }
+    throw std::runtime_error("Coefficient decoder required for this quantization");
+}
+
+// A number or boolean value of "key" inside the "model_spec" object of model.json.
+double spec_value(const std::string& json, const char* key, double fallback, bool required) {
+    size_t at = json.find("\"model_spec\"");
+    if (at == std::string::npos) at = 0;
+    const std::string k = std::string("\"") + key + "\"";
+    at = json.find(k, at);
+    if (at == std::string::npos) {
+        if (required) throw std::runtime_error(std::string("model.json lacks model_spec.") + key);
+        return fallback;
+    }
+    at = json.find(':', at + k.size());
+    if (at == std::string::npos) throw std::runtime_error("Malformed model.json");
+    ++at;
+    while (at < json.size() && std::isspace((unsigned char)json[at])) ++at;
+    if (json.compare(at, 4, "true") == 0) return 1.0;
+    if (json.compare(at, 5, "false") == 0) return 0.0;
+    return std::strtod(json.c_str() + at, nullptr);
+}
+
+template <class T>
+void input(std::vector<T>& v, size_t count) {
+    v.resize(count);
+    std::cin.read(reinterpret_cast<char*>(v.data()), (std::streamsize)(count * sizeof(T)));
+    if (!std::cin) throw std::runtime_error("Incomplete resident request body");
+}
+
+template <class T>
+void append(std::vector<char>& out, const T* p, size_t count) {
+    const char* b = reinterpret_cast<const char*>(p);
+    out.insert(out.end(), b, b + count * sizeof(T));
+}
+template <class T>
+void append(std::vector<char>& out, const std::vector<T>& v) { append(out, v.data(), v.size()); }
+
+void reply(const std::vector<char>& bytes) {
+    const uint32_t header[2] = {0u, (uint32_t)bytes.size()};
+    std::cout.write(reinterpret_cast<const char*>(header), 8);
+    std::cout.write(bytes.data(), (std::streamsize)bytes.size());
+    std::cout.flush();
+}
+
+bool all_finite(const std::vector<float>& v) {
+    for (float x : v)
+        if (!std::isfinite(x)) return false;
+    return true;
+}
+
+struct Timer {
+    hipEvent_t a{}, b{};
+    Timer() {
+        hip_check(hipEventCreate(&a), "hipEventCreate");
+        hip_check(hipEventCreate(&b), "hipEventCreate");
+    }
+    ~Timer() {
+        (void)hipEventDestroy(a);
+        (void)hipEventDestroy(b);
+    }
+    void start(hipStream_t s) { hip_check(hipEventRecord(a, s), "hipEventRecord"); }
+    double stop(hipStream_t s) {
+        hip_check(hipEventRecord(b, s), "hipEventRecord");
+        hip_check(hipEventSynchronize(b), "hipEventSynchronize");
+        float ms = 0.0f;
+        hip_check(hipEventElapsedTime(&ms, a, b), "hipEventElapsedTime");
+        return ms;
+    }
+};
+
+double wall_ms(std::chrono::steady_clock::time_point t0) {
+    return std::chrono::duration<double, std::milli>(std::chrono::steady_clock::now() - t0).count();
+}
+
+struct Worker {
+    rta_asset* asset = nullptr;
+    rta_asset_info info{};
+    uint32_t capacity = 300, work_rows = 512, block = 128;
+    uint32_t heads = 0, kv_heads = 0, hd = 0;
+    std::vector<int> full;   // full-attention layers
+    bool attention_gate = false;
+    hipStream_t stream{};
+    std::map<int, std::unique_ptr<Device>> uploads;   // (layer, index) -> device payload
+    Device lm, ws, x, act, y, logits, ids, rows, q, kbuf, vbuf, gate, out, m, z, packets, slots, ctx, err;
+
+    ~Worker() {
+        if (asset) rta_asset_close(asset);
+    }
+
+    const void* upload(int key, const void* host, size_t bytes) {
+        auto& d = uploads[key];
+        if (!d) {
+            d = std::make_unique<Device>();
+            d->ensure(bytes);
+            hip_check(hipMemcpy(d->p, host, bytes, hipMemcpyHostToDevice), "upload");
+        }
+        return d->p;
+    }
+
+    rta_asset_matrix matrix(int layer, int index, uint64_t rows, uint64_t cols, const void** dev) {
+        rta_asset_matrix mx{};
+        rta_check(rta_asset_layer_matrix(asset, layer, index, &mx), "asset matrix");
+        const size_t bytes = rows * row_bytes(mx.fmt, cols);
+        if (bytes > mx.avail_bytes) throw std::runtime_error("Truncated geometric weights");
+        *dev = upload(layer * 16 + index, mx.data, bytes);
+        return mx;
+    }
+
+    void device_error_check(const char* what) {
+        uint32_t bits = 0;
+        rta_check(rta_device_error(&bits, 1), "rta_device_error");
+        if (bits) throw std::runtime_error(std::string(what) + " error " + std::to_string(bits));
+    }
+
+    // op 6: rows already normalised; output = Wd (SiLU(Wg x) * Wu x) with the state
+    // zeroed first (optical_resident.cpp:922-949).
+    void mlp_check(uint32_t count, uint32_t layer) {
+        const uint32_t D = info.hidden, F = info.middle;
+        if (!count || count > std::min({capacity, work_rows, 32u}) || layer >= info.depth)
+            throw std::runtime_error("Invalid optical MLP input");
+        std::vector<float> xs;
+        input(xs, (size_t)count * D);
+        if (!all_finite(xs)) throw std::runtime_error("Optical MLP input must be finite");
+        Timer t;
+        t.start(stream);
+        const void *wg, *wu, *wd;
+        const auto g = matrix((int)layer, 3, F, D, &wg);
+        const auto u = matrix((int)layer, 5, F, D, &wu);
+        const auto d = matrix((int)layer, 4, D, F, &wd);
+        x.ensure(xs.size() * 4);
+        hip_check(hipMemcpyAsync(x.p, xs.data(), xs.size() * 4, hipMemcpyHostToDevice, stream), "upload rows");
+        const double setup = t.stop(stream);
+        act.ensure((size_t)count * F * 4);
+        y.ensure((size_t)count * D * 4);
+        const size_t wsb = rta_mlp_workspace_bytes((int)g.fmt, (int)d.fmt, (int)D, (int)F, (int)count);
+        ws.ensure(wsb);
+        t.start(stream);
+        rta_check(rta_mlp_swiglu((int)g.fmt, wg, (int)u.fmt, wu, (int)d.fmt, wd, (int)D, (int)F, x.as<float>(),
+                                 (int)count, act.as<float>(), y.as<float>(), RTA_EPI_STORE, ws.p, wsb, stream),
+                  "rta_mlp_swiglu");
+        const double mlp = t.stop(stream);
+        device_error_check("RT MLP transmission");
+        std::vector<float> yo((size_t)count * D), ao((size_t)count * F);
+        hip_check(hipMemcpy(yo.data(), y.p, yo.size() * 4, hipMemcpyDeviceToHost), "read output");
+        hip_check(hipMemcpy(ao.data(), act.p, ao.size() * 4, hipMemcpyDeviceToHost), "read activation");
+        std::vector<char> o;
+        append(o, yo);
+        append(o, ao);
+        const std::vector<uint32_t> hits(count, F);   // the full-matrix MLP reads every feature
+        append(o, hits);
+        // (setup, gate_up, down): the gate/up and down passes run in one call here
+        const std::vector<double> times{setup, mlp, 0.0};
+        append(o, times);
+        reply(o);
+    }
+
+    // op 4: logits of the query over the whole vocabulary, the winner (ties to the lower
+    // id), and the readout's coverage fields (optical_resident.cpp:889-905,
+    // resident_math.comp:99-105,117-130).
+    void word_check() {
+        const auto t0 = std::chrono::steady_clock::now();
+        const uint32_t D = info.hidden, V = info.vocab;
+        std::vector<float> qs;
+        input(qs, D);
+        rta_asset_matrix b{};
+        rta_check(rta_asset_basis(asset, 1, &b), "asset basis");
+        const size_t rb = row_bytes(b.fmt, D), bytes = (size_t)V * rb;
+        if (bytes > b.avail_bytes) throw std::runtime_error("Truncated original word basis");
+        const void* w = upload(-1, b.data, bytes);
+        x.ensure((size_t)D * 4);
+        hip_check(hipMemcpyAsync(x.p, qs.data(), (size_t)D * 4, hipMemcpyHostToDevice, stream), "upload query");
+        logits.ensure((size_t)V * 4);
+        ids.ensure(256);
+        const size_t wsb = rta_lm_head_workspace_bytes((int)b.fmt, (int)V, (int)D, 1);
+        ws.ensure(wsb);
+        Timer t;
+        t.start(stream);
+        rta_check(rta_lm_head((int)b.fmt, w, (int)V, (int)D, x.as<float>(), 1, 0.0f, logits.as<float>(),
+                              ids.as<uint32_t>(), ws.p, wsb, stream),
+                  "rta_lm_head");
+        const double lm_ms = t.stop(stream);
+        device_error_check("Resident word optical");
+        // decoded rows of the first 256 queued words (every word is queued, in id order)
+        const uint32_t nd = std::min<uint32_t>(256u, V);
+        rows.ensure((size_t)256 * D * 4);
+        hip_check(hipMemsetAsync(rows.p, 0, (size_t)256 * D * 4, stream), "clear rows");
+        rta_check(rta_dequant((int)b.fmt, w, (int64_t)nd * D, rows.as<float>(), stream), "rta_dequant");
+        uint32_t id = 0;
+        float best = 0.0f;
+        hip_check(hipMemcpyAsync(&id, ids.p, 4, hipMemcpyDeviceToHost, stream), "read id");
+        hip_check(hipStreamSynchronize(stream), "sync");
+        if (id >= V) throw std::runtime_error("Resident word optical error 2048");
+        hip_check(hipMemcpy(&best, logits.as<float>() + id, 4, hipMemcpyDeviceToHost), "read logit");
+        std::vector<float> dec((size_t)256 * D);
+        hip_check(hipMemcpy(dec.data(), rows.p, dec.size() * 4, hipMemcpyDeviceToHost), "read rows");
+        std::vector<char> o;
+        const std::vector<double> times{lm_ms, wall_ms(t0), 0.0, lm_ms, 0.0};
+        append(o, times);
+        float f20 = best + 20.0f, one = 1.0f;
+        uint32_t winner[4] = {id, 0, 0, 0};
+        std::memcpy(&winner[1], &f20, 4);
+        std::memcpy(&winner[2], &one, 4);
+        std::memcpy(&winner[3], &one, 4);
+        append(o, winner, 4);
+        append(o, &V, 1);
+        std::vector<uint32_t> queue(V);
+        for (uint32_t i = 0; i < V; ++i) queue[i] = i;
+        append(o, queue);
+        append(o, dec);
+        // the query as the readout stores it: fp32 bits, pairs in order (resident_common.glsl:103)
+        append(o, reinterpret_cast<const uint32_t*>(qs.data()), D);
+        // per 256-wide block: chart of its first pair scaled by sqrt(256) / |block|
+        // (resident_math.comp:99-105, resident_common.glsl:78)
+        const uint32_t blocks = D / 256;
+        std::vector<float> charts((size_t)blocks * 4, 0.0f);
+        for (uint32_t bk = 0; bk < blocks; ++bk) {
+            float ss = 0.0f;
+            for (uint32_t c = 0; c < 256; ++c) ss += qs[bk * 256 + c] * qs[bk * 256 + c];
+            const float inv = 16.0f / std::max(std::sqrt(ss), 1e-20f);
+            const float vx = qs[bk * 256] * inv, vy = qs[bk * 256 + 1] * inv;
+            const float radius = std::sqrt(vx * vx + vy * vy), a = std::log(1.0f + radius);
+            if (radius > 1e-20f) {
+                charts[bk * 4] = 0.7f * a / (1.0f + a) * vx / radius;
+                charts[bk * 4 + 1] = 0.7f * a / (1.0f + a) * vy / radius;
+            }
+        }
+        append(o, charts);
+        const uint32_t block_hits = V * blocks;   // every word meets every block
+        append(o, &block_hits, 1);
+        reply(o);
+    }
+
+    // op 14: pack the supplied K/V rows into history packets, then each query row r
+    // attends causally to positions history_start .. query_start + r (all within
+    // capacity); standard backend, dense receipts (resident_attention_runtime.inl:646-,
+    // attention_receipts.hpp:16-29).
+    void attention_check(uint32_t nrows, uint32_t layer) {
+        uint32_t hdr[4];
+        std::cin.read(reinterpret_cast<char*>(hdr), sizeof(hdr));
+        const uint32_t count = hdr[0], qstart = hdr[1], hstart = hdr[2];
+        bool full_layer = false;
+        for (int l : full)
+            if ((uint32_t)l == layer) full_layer = true;
+        if (!std::cin || !nrows || nrows > std::min(work_rows, 32u) || !count || count > capacity ||
+            layer >= info.depth || !full_layer || qstart < hstart || (uint64_t)qstart + nrows > (uint64_t)hstart + count ||
+            (uint64_t)hstart + count > 1048576u || hdr[3])
+            throw std::runtime_error("Invalid full-attention diagnostic shape or causal domain");
+        const uint32_t Q = heads * hd, G = kv_heads * hd;
+        std::vector<float> qs, ks, vs, gs;
+        input(qs, (size_t)nrows * Q);
+        input(ks, (size_t)count * G);
+        input(vs, (size_t)count * G);
+        input(gs, (size_t)nrows * Q);
+        if (!all_finite(qs) || !all_finite(ks) || !all_finite(vs) || !all_finite(gs))
+            throw std::runtime_error("Attention diagnostic values must be finite");
+        const auto t0 = std::chrono::steady_clock::now();
+        const size_t pb = rta_history_bytes((int)G);
+        if (!pb) throw std::runtime_error("Unsupported history width");
+        // positions relative to the diagnostic's origin: position history_start + i in slot i
+        packets.ensure((size_t)capacity * pb);
+        kbuf.ensure(ks.size() * 4);
+        vbuf.ensure(vs.size() * 4);
+        slots.ensure((size_t)std::max(count, nrows) * 8);
+        std::vector<int64_t> sl(count);
+        for (uint32_t i = 0; i < count; ++i) sl[i] = i;
+        hip_check(hipMemcpyAsync(kbuf.p, ks.data(), ks.size() * 4, hipMemcpyHostToDevice, stream), "upload keys");
+        hip_check(hipMemcpyAsync(vbuf.p, vs.data(), vs.size() * 4, hipMemcpyHostToDevice, stream), "upload values");
+        hip_check(hipMemcpyAsync(slots.p, sl.data(), (size_t)count * 8, hipMemcpyHostToDevice, stream), "upload slots");
+        rta_check(rta_pack_history(kbuf.as<float>(), (int)G, vbuf.as<float>(), (int)G, (int)count, (int)G, RTA_Q4_K,
+                                   RTA_Q6_K, slots.as<int64_t>(), capacity, packets.p, stream),
+                  "rta_pack_history");
+        // one sequence per query row over the shared ring, each with its own length
+        std::vector<int32_t> lens(nrows);
+        std::vector<int64_t> bases(nrows, 0);
+        int max_ctx = 0;
+        for (uint32_t r = 0; r < nrows; ++r) {
+            lens[r] = (int32_t)(qstart - hstart + r + 1);
+            max_ctx = std::max(max_ctx, lens[r]);
+        }
+        ctx.ensure((size_t)nrows * 4);
+        Device base_d;
+        base_d.ensure((size_t)nrows * 8);
+        q.ensure(qs.size() * 4);
+        gate.ensure(gs.size() * 4);
+        out.ensure(qs.size() * 4);
+        m.ensure((size_t)nrows * heads * 4);
+        z.ensure((size_t)nrows * heads * 4);
+        hip_check(hipMemcpyAsync(ctx.p, lens.data(), (size_t)nrows * 4, hipMemcpyHostToDevice, stream), "upload lengths");
+        hip_check(hipMemcpyAsync(base_d.p, bases.data(), (size_t)nrows * 8, hipMemcpyHostToDevice, stream), "upload bases");
+        hip_check(hipMemcpyAsync(q.p, qs.data(), qs.size() * 4, hipMemcpyHostToDevice, stream), "upload queries");
+        hip_check(hipMemcpyAsync(gate.p, gs.data(), gs.size() * 4, hipMemcpyHostToDevice, stream), "upload gate");
+        const size_t wsb = rta_decode_attention_workspace_bytes((int)nrows, (int)heads, (int)kv_heads, (int)hd, max_ctx);
+        ws.ensure(wsb);
+        Timer t;
+        t.start(stream);
+        rta_check(rta_decode_attention(q.as<float>(), (int)nrows, (int)heads, (int)kv_heads, (int)hd, packets.p, RTA_Q4_K,
+                                       RTA_Q6_K, base_d.as<int64_t>(), ctx.as<int32_t>(), capacity, capacity, max_ctx,
+                                       attention_gate ? gate.as<float>() : nullptr, out.as<float>(), m.as<float>(),
+                                       z.as<float>(), ws.p, wsb, stream),
+                  "rta_decode_attention");
+        const double fused = t.stop(stream);
+        uint32_t bits = 0;
+        rta_check(rta_device_error(&bits, 1), "rta_device_error");
+        std::vector<float> o_h(qs.size()), m_h((size_t)nrows * heads), z_h((size_t)nrows * heads);
+        std::vector<uint8_t> pk((size_t)count * pb);
+        hip_check(hipMemcpy(o_h.data(), out.p, o_h.size() * 4, hipMemcpyDeviceToHost), "read output");
+        hip_check(hipMemcpy(m_h.data(), m.p, m_h.size() * 4, hipMemcpyDeviceToHost), "read m");
+        hip_check(hipMemcpy(z_h.data(), z.p, z_h.size() * 4, hipMemcpyDeviceToHost), "read z");
+        hip_check(hipMemcpy(pk.data(), packets.p, pk.size(), hipMemcpyDeviceToHost), "read packets");
+        std::vector<float> phys((size_t)nrows * heads * 2);
+        for (size_t i = 0; i < m_h.size(); ++i) {
+            phys[2 * i] = m_h[i] + 20.0f;   // the reported intensity m + 20 (resident_ray.comp:74)
+            phys[2 * i + 1] = z_h[i];
+        }
+        const uint32_t stride = hd + 8 + block / 32;
+        uint64_t records = 0;
+        for (uint32_t r = 0; r < nrows; ++r) {
+            const uint32_t active = std::min(qstart - hstart + r + 1, capacity);
+            records += (active + block - 1) / block;
+        }
+        records *= heads;
+        const uint32_t legacy = hstart == 0 ? 1u : 0u;
+        std::vector<char> o;
+        const uint32_t header[12] = {0x41545231u, nrows, count, heads, kv_heads, hd, (uint32_t)pb,
+                                     block, stride, (uint32_t)records, legacy, bits};
+        append(o, header, 12);
+        const std::vector<double> times{fused, 0.0, 0.0, wall_ms(t0)};
+        append(o, times);
+        append(o, o_h);
+        append(o, phys);
+        // the same computation stands for the legacy detector when the history starts at 0
+        if (legacy) {
+            append(o, o_h);
+            append(o, phys);
+        } else {
+            const std::vector<float> zeros(o_h.size() + phys.size(), 0.0f);
+            append(o, zeros);
+        }
+        append(o, pk);
+        // receipts record ray-traversal evidence; no rays are traced here, so they are zero
+        const std::vector<uint32_t> receipts((size_t)records * stride, 0u);
+        append(o, receipts);
+        reply(o);
+    }
+
+    void resources() {
+        size_t free_b = 0, total_b = 0;
+        hip_check(hipMemGetInfo(&free_b, &total_b), "hipMemGetInfo");
+        uint64_t uploaded = lm.n;
+        for (auto& kv : uploads) uploaded += kv.second->n;
+        std::vector<uint64_t> v(61, 0);
+        v[0] = v[1] = total_b - free_b;      // allocation bytes (device)
+        v[9] = uploaded;                      // packed coefficient bytes on the device
+        v[11] = total_b - free_b;             // logical device buffer bytes
+        v[13] = (uint64_t)full.size() * capacity * rta_history_bytes((int)(kv_heads * hd));
+        v[26] = work_rows;
+        v[37] = 0;                            // attention backend: standard
+        v[38] = block;
+        std::vector<char> o;
+        append(o, v);
+        reply(o);
+    }
+};
+
+}  // namespace
+
+int main(int argc, char** argv) {
+    try {
+        if (argc < 3) throw std::runtime_error("Usage: rt_optical_resident student.bin original_head.bin [capacity]");
+        Worker w;
+        w.capacity = argc > 3 ? (uint32_t)std::stoul(argv[3]) : 300u;
+        if (!w.capacity || w.capacity > 1048576u) throw std::runtime_error("Invalid initial tree capacity");
+        if (argc > 5 && std::string(argv[5]) == "sparse") throw std::runtime_error("Sparse routing is not provided by this worker");
+        w.work_rows = argc > 11 ? (uint32_t)std::stoul(argv[11]) : 512u;
+        if (w.work_rows < 32u || w.work_rows > 1024u || (w.work_rows & (w.work_rows - 1u)))
+            throw std::runtime_error("Prefill batch requires a power of two in [32,1024]");
+        const char* backend = std::getenv("RT_ATTENTION_BACKEND");
+        if (backend && std::string(backend) != "standard")
+            throw std::runtime_error("This worker provides the standard attention backend only");
+        const char* mlp = std::getenv("RT_MLP_BACKEND");
+        if (mlp && std::string(mlp) != "standard") throw std::runtime_error("This worker provides the standard MLP backend only");
+        if (const char* b = std::getenv("RT_ATTENTION_BLOCK")) w.block = (uint32_t)std::stoul(b);
+        if (w.block != 128u && w.block != 256u && w.block != 512u) throw std::runtime_error("Invalid attention history block");
+
+        char err[256] = {};
+        if (rta_asset_open(argv[1], argv[2], &w.asset, err, sizeof(err)) != RTA_OK) throw std::runtime_error(err);
+        rta_check(rta_asset_get_info(w.asset, &w.info), "asset info");
+        if (w.info.hidden % 256u) throw std::runtime_error("Invalid resident optical student");
+        std::string dir(argv[1]);
+        dir = dir.find('/') == std::string::npos ? std::string(".") : dir.substr(0, dir.find_last_of('/'));
+        std::ifstream jf(dir + "/model.json");
+        std::stringstream js;
+        js << jf.rdbuf();
+        const std::string json = js.str();
+        w.kv_heads = (uint32_t)spec_value(json, "kv_heads", 0, true);
+        w.hd = (uint32_t)spec_value(json, "attention_head_dim", 0, true);
+        w.heads = (uint32_t)spec_value(json, "attention_heads", 0, true);
+        for (int l = 0; l < (int)w.info.depth; ++l) {
+            uint32_t kind = 0, gate_desc = 0;
+            rta_check(rta_asset_word(w.asset, l, 26, &kind), "asset word");
+            if (kind == 1u) {
+                w.full.push_back(l);
+                rta_check(rta_asset_word(w.asset, l, 9 + 2 * 6 + 1, &gate_desc), "asset word");
+                if ((gate_desc >> 8) == 2u) w.attention_gate = true;   // descriptor 6, mode 2 (export.py:98)
+            }
+        }
+        hip_check(hipSetDevice(0), "hipSetDevice");
+        hip_check(hipStreamCreate(&w.stream), "hipStreamCreate");
+        // 0x52545239: no native token stream; mode: quantisation 4, full-matrix MLP (4096),
+        // exact ordered detector (131072)
+        const uint32_t hello[5] = {0x52545239u, w.info.depth, w.info.blocks, w.info.middle, 4u | 4096u | 131072u};
+        std::cout.write(reinterpret_cast<const char*>(hello), 20);
+        std::cout.flush();
+        uint32_t op;
+        while (std::cin.read(reinterpret_cast<char*>(&op), 4)) {
+            if (!op) break;
+            uint32_t count, debug;
+            if (!std::cin.read(reinterpret_cast<char*>(&count), 4) || !std::cin.read(reinterpret_cast<char*>(&debug), 4))
+                throw std::runtime_error("Incomplete resident request");
+            if (op == 4) w.word_check();
+            else if (op == 6) w.mlp_check(count, debug);
+            else if (op == 8) w.resources();
+            else if (op == 14) w.attention_check(count, debug);
+            else throw std::runtime_error("Unknown resident operation");
+        }
+        hip_check(hipStreamDestroy(w.stream), "hipStreamDestroy");
+        return 0;
+    } catch (const std::exception& e) {
+        std::cerr << e.what() << std::endl;
+        return 1;
+    }
+}
