@@ -51,7 +51,10 @@ class Worker:
                 pass
         code = self.p.wait(timeout=60)
         for s in (self.p.stdin, self.p.stdout):
-            s.close()
+            try:
+                s.close()   # flushes what a dead worker never read
+            except OSError:
+                pass
         return code
 
     # op 6
