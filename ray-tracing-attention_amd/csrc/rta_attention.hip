@@ -883,9 +883,15 @@ __global__ void __launch_bounds__(256, 2) attn_chunk_mma_kernel(const AttnArgs a
     const int32_t* S = a.plan;
     const int64_t T = uni(S[a.nseq]);
     const int64_t P = a.nwg < T ? a.nwg : T;   // every workgroup below P has a tile
-    if (blockIdx.x >= P) return;   // (all of them when T = 0)
-    const int64_t ta = (int64_t)blockIdx.x * T / P, tb = ((int64_t)blockIdx.x + 1) * T / P;
-    int s = uni(S[a.nseq + 1 + blockIdx.x]);
+    // v: this workgroup's place in the split.  Workgroups b and b + nwg / 2 are the two
+    // resident on one compute unit (dispatched in that order), so they take adjacent
+    // shares and every compute unit gets floor or ceil of 2 T / P tiles; the plain order
+    // would give both the same floor or ceil of T / P
+    const int b = blockIdx.x, half = a.nwg / 2;
+    const int64_t v = (P == a.nwg && (a.nwg & 1) == 0) ? 2 * (b % half) + b / half : b;
+    if (v >= P) return;   // (all of them when T = 0)
+    const int64_t ta = v * T / P, tb = (v + 1) * T / P;
+    int s = uni(S[a.nseq + 1 + v]);
     uint32_t* vt = reinterpret_cast<uint32_t*>(lds) + wave * MmaWaveLds::total;
     float* s_w = lds + wave * MmaWaveLds::total + MmaWaveLds::w;
     float* s_f = lds + wave * MmaWaveLds::total + MmaWaveLds::f;
@@ -1164,9 +1170,10 @@ __global__ void __launch_bounds__(256, 2) attn_chunk_mma_kernel(const AttnArgs a
         }
 
         // records: U_g[dim] = (D_2g + D_2g+1) 2^-S, then m and Z
-        // record k of the sequence: k = this workgroup - the one holding its first tile
+        // record k of the sequence: k = this workgroup's place in the split - that of the
+        // one holding its first tile
         const int64_t w_lo = ((s_first + 1) * P - 1) / T;
-        float* rec = a.ws + ((int64_t)s * a.rstride + ((int64_t)blockIdx.x - w_lo)) * a.hq * kRec;
+        float* rec = a.ws + ((int64_t)s * a.rstride + (v - w_lo)) * a.hq * kRec;
         const float unit = ldexpf(1.0f, 14 - S_cur);   // D is in units of 2^(S - 14)
         const int gcol = col >> 1;
         const bool writer = (col & 1) == 0 && gcol < G;
