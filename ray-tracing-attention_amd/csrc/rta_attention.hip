@@ -903,9 +903,9 @@ __global__ void __launch_bounds__(256, 2) attn_chunk_mma_kernel(const AttnArgs a
     const int qsel = col >= 8 ? 1 : 0;
     const uint32_t sbyte = (uint32_t)(((col & 7) >> 2) + 2 * qsel);   // sub-block scale byte
     const uint32_t sc_sel = sbyte | (0x0Cu << 8) | ((4u + sbyte) << 16) | (0x0Cu << 24);
-    // qh bits 2q, 2q + 1 to bits 4, 5: rotate left by 4 - 2q (alignbit rotates right)
-    const uint32_t rot[2] = {(32u - (uint32_t)((4 - 2 * qsel) & 31)) & 31u,
-                             (32u - (uint32_t)((4 - 2 * (2 + qsel)) & 31)) & 31u};
+    // qh bits 2q, 2q + 1 to bits 6, 7: rotate left by 6 - 2q (alignbit rotates right)
+    const uint32_t rot[2] = {(32u - (uint32_t)((6 - 2 * qsel) & 31)) & 31u,
+                             (32u - (uint32_t)((6 - 2 * (2 + qsel)) & 31)) & 31u};
 
     uint32_t err = 0;
     // scores in log2 units, s log2(e) / sqrt(hd), so that the softmax takes exp2 (one
@@ -1124,8 +1124,9 @@ __global__ void __launch_bounds__(256, 2) attn_chunk_mma_kernel(const AttnArgs a
                         rd8(48 + 2 * hh, sw[0]);
                         rd8(49 + 2 * hh, sw[1]);
                     }
-                    // e 2^-14 = c sc 2^-14 - 32 sc 2^-14: the code pair shifted to c 2^-20
-                    // (binary16 subnormals) times sc 2^6 gives c sc 2^-14 as hi plus the exact
+                    // e 2^-14 = c sc 2^-14 - 32 sc 2^-14: the codes are built as 4 c in their
+                    // bytes, so a code pair moved into 16-bit halves reads as c 2^-22 (binary16
+                    // subnormals); times sc 2^8 that gives c sc 2^-14 as hi plus the exact
                     // remainder lo (|c sc| < 2^13, every nonzero product >= 2^-14, so the
                     // matrix-core operands are normal), and -sc 2^-9 (exact) goes in a third
                     // instruction; D is then in units of 2^(S - 14)
@@ -1134,15 +1135,15 @@ __global__ void __launch_bounds__(256, 2) attn_chunk_mma_kernel(const AttnArgs a
                         uint32_t code4[8], sc6[4], corr[4];
 #pragma unroll
                         for (int i = 0; i < 8; ++i) {
-                            const uint32_t lo4 = nib ? (ql[i] >> 4) : ql[i];
-                            const uint32_t hi2 = __builtin_amdgcn_alignbit(qh[i], qh[i], rot[nib]) & 0x30303030u;
-                            code4[i] = (lo4 & 0x0F0F0F0Fu) | hi2;
+                            const uint32_t lo4 = nib ? (ql[i] >> 2) : (ql[i] << 2);
+                            const uint32_t hi2 = __builtin_amdgcn_alignbit(qh[i], qh[i], rot[nib]) & 0xC0C0C0C0u;
+                            code4[i] = (lo4 & 0x3C3C3C3Cu) | hi2;
                         }
 #pragma unroll
                         for (int k = 0; k < 4; ++k) {   // int8 scales of positions 2k, 2k+1 as binary16
                             const uint32_t pr = __builtin_amdgcn_perm(sw[nib][2 * k + 1], sw[nib][2 * k], sc_sel);
                             const uint32_t sc = pk_add_f16((pr ^ 0x00800080u) | 0x64006400u, 0xE480E480u);   // - 1152
-                            sc6[k] = pk_mul_f16(sc, 0x54005400u);    // sc 2^6
+                            sc6[k] = pk_mul_f16(sc, 0x5C005C00u);    // sc 2^8
                             corr[k] = pk_mul_f16(sc, 0x98009800u);    // -sc 2^-9
                         }
                         const h8_t ac = __builtin_bit_cast(h8_t, uint4{corr[0], corr[1], corr[2], corr[3]});
@@ -1152,7 +1153,7 @@ __global__ void __launch_bounds__(256, 2) attn_chunk_mma_kernel(const AttnArgs a
                             uint32_t ah[4], al[4];
 #pragma unroll
                             for (int k = 0; k < 4; ++k) {
-                                const uint32_t cp = __builtin_amdgcn_perm(code4[2 * k + 1], code4[2 * k], sel) << 4;
+                                const uint32_t cp = __builtin_amdgcn_perm(code4[2 * k + 1], code4[2 * k], sel);
                                 ah[k] = pk_mul_f16(cp, sc6[k]);
                                 al[k] = pk_fms_f16(cp, sc6[k], ah[k]);   // remainder, exact
                             }
