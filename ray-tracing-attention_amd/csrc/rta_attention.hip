@@ -1211,15 +1211,16 @@ __global__ void __launch_bounds__(256, 2) attn_chunk_mma_kernel(const AttnArgs a
 }
 
 // One workgroup per (sequence, query head): 8 chunk groups x 32 lanes of 4
-// coordinates; every thread keeps 8 chunk records in flight.
+// coordinates; every thread keeps 8 chunk records in flight.  One pass: each group
+// folds its records into a running (m, Z, U), rescaled when m grows, and the groups
+// are combined at the end (the same sums as max-then-accumulate, in another order).
 __global__ void __launch_bounds__(256) attn_merge_kernel(const AttnArgs a) {
     constexpr int kGroups = 8, kAhead = 8;
-    __shared__ float s_red[4];
     __shared__ float4 s_u[kGroups][kHd / 4];
-    __shared__ float s_zp[kGroups];
+    __shared__ float s_zp[kGroups], s_mp[kGroups];
     const int sh = blockIdx.x;
     const int s = sh / a.hq, h = sh - s * a.hq;
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int tid = threadIdx.x;
     const int grp = tid >> 5, e = tid & 31;
     const int64_t L = a.ctx_len[s];
     const int64_t visible = L < a.capacity ? L : a.capacity;
@@ -1250,15 +1251,9 @@ __global__ void __launch_bounds__(256) attn_merge_kernel(const AttnArgs a) {
         if (short_grid) nch = a.nchunk;
         rec0 = a.ws + (int64_t)s * a.nchunk * cstride + (int64_t)h * kRec;
     }
-    float mx = -INFINITY;
-    for (int ci = tid; ci < nch; ci += 256) mx = fmaxf(mx, rec0[ci * cstride + kHd]);
-    mx = group_max(mx, kWave);
-    if (lane == 0) s_red[wave] = mx;
-    __syncthreads();
-    const float M = fmaxf(fmaxf(s_red[0], s_red[1]), fmaxf(s_red[2], s_red[3]));
-    float Z = 0.0f;
+    float Mg = -INFINITY, Z = 0.0f;   // the group's running max, sum and vector
     float4 U = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-    if (M != -INFINITY) {
+    {
         for (int c0 = grp; c0 < nch; c0 += kGroups * kAhead) {
             float mm[kAhead], zz[kAhead];
             float4 uu[kAhead];
@@ -1276,9 +1271,23 @@ __global__ void __launch_bounds__(256) attn_merge_kernel(const AttnArgs a) {
                     uu[k] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
                 }
             }
+            float mb = Mg;
+#pragma unroll
+            for (int k = 0; k < kAhead; ++k) mb = fmaxf(mb, mm[k]);
+            if (mb != -INFINITY) {   // uniform over the group's lanes
+                if (mb != Mg) {
+                    const float r = Mg == -INFINITY ? 0.0f : expf(Mg - mb);
+                    Z *= r;
+                    U.x *= r;
+                    U.y *= r;
+                    U.z *= r;
+                    U.w *= r;
+                    Mg = mb;
+                }
+            }
 #pragma unroll
             for (int k = 0; k < kAhead; ++k) {
-                const float f = expf(mm[k] - M);
+                const float f = mm[k] == -INFINITY ? 0.0f : expf(mm[k] - Mg);
                 Z = fmaf(zz[k], f, Z);
                 U.x = fmaf(uu[k].x, f, U.x);
                 U.y = fmaf(uu[k].y, f, U.y);
@@ -1288,14 +1297,21 @@ __global__ void __launch_bounds__(256) attn_merge_kernel(const AttnArgs a) {
         }
     }
     s_u[grp][e] = U;
-    if (e == 0) s_zp[grp] = Z;
+    if (e == 0) {
+        s_zp[grp] = Z;
+        s_mp[grp] = Mg;
+    }
     __syncthreads();
     if (tid < kHd) {
+        float M = -INFINITY;
+#pragma unroll
+        for (int g = 0; g < kGroups; ++g) M = fmaxf(M, s_mp[g]);
         float u = 0.0f, z = 0.0f;
 #pragma unroll
         for (int g = 0; g < kGroups; ++g) {
-            u += reinterpret_cast<const float*>(&s_u[g][0])[tid];
-            z += s_zp[g];
+            const float f = s_mp[g] == -INFINITY ? 0.0f : expf(s_mp[g] - M);
+            u = fmaf(reinterpret_cast<const float*>(&s_u[g][0])[tid], f, u);
+            z = fmaf(s_zp[g], f, z);
         }
         float o = u / fmaxf(z, 1e-30f);
         if (a.gate) o *= detector_sigmoid(a.gate[(int64_t)sh * kHd + tid]);
