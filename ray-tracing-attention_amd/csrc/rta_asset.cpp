@@ -13,7 +13,9 @@
 // the caller, who compares rta_asset_info with its own model spec.
 #include <cstdio>
 #include <cstring>
+#include <exception>
 #include <fstream>
+#include <memory>
 #include <string>
 #include <vector>
 
@@ -47,23 +49,38 @@ bool read_all(std::ifstream& f, void* dst, size_t bytes) {
     return true;
 }
 
+uint64_t file_bytes(const char* path) {
+    std::ifstream f(path, std::ios::binary | std::ios::ate);
+    return f ? (uint64_t)f.tellg() : 0;
+}
+
 std::string sibling(const char* path, const char* name) {
     std::string s(path);
     const size_t cut = s.find_last_of('/');
     return (cut == std::string::npos ? std::string() : s.substr(0, cut + 1)) + name;
 }
 
+int asset_open(const char* model_path, const char* vocabulary_path, rta_asset** out, char* err, size_t err_len);
+
 }  // namespace
 
+// No exception leaves the C ABI: a header whose sizes cannot be allocated is reported
+// like any other damaged file.
 extern "C" int rta_asset_open(const char* model_path, const char* vocabulary_path, rta_asset** out, char* err,
                               size_t err_len) {
     if (!model_path || !out) return RTA_ERR_NULL;
     *out = nullptr;
-    auto a = new rta_asset();
-    auto bad = [&](const char* msg) {
-        delete a;
-        return fail(err, err_len, msg);
-    };
+    try {
+        return asset_open(model_path, vocabulary_path, out, err, err_len);
+    } catch (const std::exception&) {
+        return fail(err, err_len, "Invalid resident optical student");
+    }
+}
+
+namespace {
+int asset_open(const char* model_path, const char* vocabulary_path, rta_asset** out, char* err, size_t err_len) {
+    std::unique_ptr<rta_asset> a(new rta_asset());
+    auto bad = [&](const char* msg) { return fail(err, err_len, msg); };
     std::ifstream in(model_path, std::ios::binary);
     char magic[8];
     in.read(magic, 8);
@@ -74,10 +91,14 @@ extern "C" int rta_asset_open(const char* model_path, const char* vocabulary_pat
         !h[0] || !h[4])
         return bad("Invalid resident optical student");
     if (h[6] < kModelWords + uint64_t(h[1]) * kLayerWords) return bad("Invalid resident optical student");
+    // sizes are checked against the files before anything is allocated
+    if (file_bytes(model_path) < 44 + uint64_t(h[6]) * 4) return bad("Truncated resident parameters");
     a->params.resize(h[6]);
     if (!read_all(in, a->params.data(), a->params.size() * 4)) return bad("Truncated resident parameters");
     {
-        std::ifstream mf(sibling(model_path, "geometry_weights.bin"), std::ios::binary);
+        const std::string geo = sibling(model_path, "geometry_weights.bin");
+        if (file_bytes(geo.c_str()) < uint64_t(h[7]) * 4) return bad("Truncated geometric weights");
+        std::ifstream mf(geo, std::ios::binary);
         a->matrices.resize(h[7]);
         if (!mf || !read_all(mf, a->matrices.data(), a->matrices.size() * 4)) return bad("Truncated geometric weights");
     }
@@ -101,9 +122,10 @@ extern "C" int rta_asset_open(const char* model_path, const char* vocabulary_pat
         a->basis.resize((size - 16) / 4);
         if (!read_all(vf, a->basis.data(), a->basis.size() * 4)) return bad("Truncated original word basis");
     }
-    *out = a;
+    *out = a.release();
     return RTA_OK;
 }
+}  // namespace
 
 extern "C" void rta_asset_close(rta_asset* a) { delete a; }
 

@@ -137,3 +137,14 @@ def test_damaged_assets_fail_with_the_loaders_messages(tmp_path, case, message):
         _patch(voc, 8, struct.pack("<I", 999))
     with pytest.raises(ValueError, match=message):
         ra.open_dir(tmp_path)
+
+
+def test_header_sizes_beyond_memory_are_reported(tmp_path):
+    """A parameter-word count no allocation can hold fails with the loader's message
+    instead of an exception escaping the C ABI."""
+    _model(tmp_path)
+    model = tmp_path / "optical_model.bin"
+    _patch(model, 8 + 28, struct.pack("<I", 0xFFFFFFFF))   # parameter words
+    _patch(model, 8 + 32, struct.pack("<I", 0xFFFFFFFF))   # matrix words
+    with pytest.raises(ValueError, match="Invalid resident optical student|Truncated"):
+        ra.open_dir(tmp_path)
