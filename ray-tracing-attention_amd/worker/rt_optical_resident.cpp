@@ -151,7 +151,7 @@ struct Worker {
     bool attention_gate = false;
     hipStream_t stream{};
     std::map<int, std::unique_ptr<Device>> uploads;   // (layer, index) -> device payload
-    Device lm, ws, x, act, y, logits, ids, rows, q, kbuf, vbuf, gate, out, m, z, packets, slots, ctx, err;
+    Device ws, x, act, y, logits, ids, rows, q, kbuf, vbuf, gate, out, m, z, packets, slots, ctx;
 
     ~Worker() {
         if (asset) rta_asset_close(asset);
@@ -416,7 +416,7 @@ struct Worker {
     void resources() {
         size_t free_b = 0, total_b = 0;
         hip_check(hipMemGetInfo(&free_b, &total_b), "hipMemGetInfo");
-        uint64_t uploaded = lm.n;
+        uint64_t uploaded = 0;
         for (auto& kv : uploads) uploaded += kv.second->n;
         std::vector<uint64_t> v(61, 0);
         v[0] = v[1] = total_b - free_b;      // allocation bytes (device)
