@@ -428,6 +428,44 @@ __device__ __forceinline__ void score_q4k_mma(const QOp& qo, const KRaw& r, int 
         out[eh] = fmaf(dC, D[2 * eh] + D[2 * eh + 1], -dM * (Dm[2 * eh] + Dm[2 * eh + 1])) * qo.rs[eh] * inv;
 }
 
+// Scores of the two kv heads of one Q4_K superblock (head halves 0 and 1) in one output,
+// for G <= 4: q0 holds kv head 0's q in A rows 0-7 (its rows 8-15 are zero, heads >= G),
+// q1 kv head 1's in rows 8-15 (rows 0-7 zero), so that lane segment u receives heads
+// 2 (u & 1) + eh of kv head u >> 1.  Both heads share the superblock's d and dmin.
+__device__ __forceinline__ void score_q4k_mma_pair(const QOp& q0, const QOp& q1, const uint4 hdr, const uint2 c0[2],
+                                                   const uint2 c1[2], int u, const float rs[2], float out[2]) {
+    f4_t D = f4_t{0.0f, 0.0f, 0.0f, 0.0f};
+    const _Float16 z = (_Float16)0.0f;
+    h8_t bm0 = h8_t{z, z, z, z, z, z, z, z}, bm1 = bm0;
+#pragma unroll
+    for (int hh = 0; hh < 2; ++hh) {
+        const QOp& qo = hh ? q1 : q0;
+        const uint2* c2 = hh ? c1 : c0;
+        uint32_t sc[4], mn[4];
+#pragma unroll
+        for (int kb = 0; kb < 4; ++kb) q4k_scale_min_lane(hdr.y, hdr.z, hdr.w, 4 * hh + kb, sc[kb], mn[kb]);
+#pragma unroll
+        for (int kb = 0; kb < 4; ++kb) {
+            const uint2 c = c2[kb >> 1];
+            const uint32_t M = (kb & 1) ? 0x00F000F0u : 0x000F000Fu;
+            const uint32_t sp = h2dup((float)sc[kb] * ((kb & 1) ? 64.0f : 1024.0f));
+            const uint4 q4 = {pk_mul_f16(c.x & M, sp), pk_mul_f16((c.x >> 8) & M, sp), pk_mul_f16(c.y & M, sp),
+                              pk_mul_f16((c.y >> 8) & M, sp)};
+            D = __builtin_amdgcn_mfma_f32_16x16x32_f16(qo.a[kb], __builtin_bit_cast(h8_t, q4), D, 0, 0, 0);
+        }
+        if (u == 0) {
+#pragma unroll
+            for (int kb = 0; kb < 4; ++kb) (hh ? bm1 : bm0)[kb] = (_Float16)(float)mn[kb];
+        }
+    }
+    f4_t Dm = __builtin_amdgcn_mfma_f32_16x16x32_f16(q0.am, bm0, f4_t{0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0);
+    Dm = __builtin_amdgcn_mfma_f32_16x16x32_f16(q1.am, bm1, Dm, 0, 0, 0);
+    const float dC = half_lo(hdr.x) * 16384.0f, dM = half_hi(hdr.x) * 32.0f;
+#pragma unroll
+    for (int eh = 0; eh < 2; ++eh)
+        out[eh] = fmaf(dC, D[2 * eh] + D[2 * eh + 1], -dM * (Dm[2 * eh] + Dm[2 * eh + 1])) * rs[eh];
+}
+
 // Copies the V superblock at blk (2-byte aligned, `bytes` long) into an LDS row whose
 // dword i holds block bytes 4i..4i+3.  Reads stay inside [blk, blk + bytes).
 template <int FMT>
@@ -870,6 +908,7 @@ __global__ void __launch_bounds__(256, 2) attn_chunk_mma_kernel(const AttnArgs a
     const int blk = KPW == 2 ? wave : wave >> 1;    // its K/V superblock
     if (kv0 >= hkv) return;                         // no workgroup barrier in this kernel
     const bool two = KPW == 2 && kv0 + 1 < hkv;     // uniform
+    constexpr bool kPair = KPW == 2 && G <= 4;      // both kv heads' scores in one output
     // this workgroup's share [ta, tb) of the tile list, which runs through the
     // sequences in order (plan: S[s] = first tile of sequence s, S[nseq] = T, then the
     // sequence holding each workgroup's first tile)
@@ -989,16 +1028,50 @@ __global__ void __launch_bounds__(256, 2) attn_chunk_mma_kernel(const AttnArgs a
             // tile from the cache once the V registers are free
             asm volatile("" ::: "memory");
             QOp qo[KPW];
+            // paired scores (both kv heads in one output): kv head 1's operand rows move to
+            // A rows 8-15 (lane - 8) and its 1 / s to segments 2, 3 (lane - 32)
+            float rs_pair[2];
 #pragma unroll
             for (int kl = 0; kl < KPW; ++kl) {
-                qo[kl] = load_qop(a.qop + ((int64_t)s * hkv + min(kv0 + kl, hkv - 1)) * 6 * kWave, lane);
+                const uint4* qsrc = a.qop + ((int64_t)s * hkv + min(kv0 + kl, hkv - 1)) * 6 * kWave;
+                if (kPair && kl == 1) {
+                    qo[kl] = load_qop(qsrc, col >= 8 ? lane - 8 : lane);
+                    if (col < 8) {
+                        const _Float16 z = (_Float16)0.0f;
+#pragma unroll
+                        for (int kb = 0; kb < 4; ++kb) qo[kl].a[kb] = h8_t{z, z, z, z, z, z, z, z};
+                        qo[kl].am = h8_t{z, z, z, z, z, z, z, z};
+                    }
+                    const uint4 r = qsrc[5 * kWave + (u >= 2 ? lane - 32 : lane)];
+                    // (qo[0].rs is already scaled by inv2)
+                    rs_pair[0] = u >= 2 ? __builtin_bit_cast(float, r.x) * inv2 : qo[0].rs[0];
+                    rs_pair[1] = u >= 2 ? __builtin_bit_cast(float, r.y) * inv2 : qo[0].rs[1];
+                } else {
+                    qo[kl] = load_qop(qsrc, lane);
+                }
                 qo[kl].rs[0] *= inv2;
                 qo[kl].rs[1] *= inv2;
             }
-            // scores of the wave's kv heads, heads 2u + eh, positions 16 rt + col
+            // scores of the wave's kv heads, heads 2u + eh, positions 16 rt + col (paired:
+            // heads 2 (u & 1) + eh of kv head u >> 1, kept in sv[0])
             float sv[KPW][4][2];
+            if constexpr (kPair) {
+                const int klu = u >> 1, gu = 2 * (u & 1);
+#pragma unroll
+                for (int rt = 0; rt < 4; ++rt) {
+                    float sc2[2];
+                    score_q4k_mma_pair(qo[0], qo[1], hdr[rt], kc[0][rt], kc[1][rt], u, rs_pair, sc2);
+#pragma unroll
+                    for (int eh = 0; eh < 2; ++eh) {
+                        const bool live = okr[rt] && gu + eh < G && (klu == 0 || two);
+                        if (live && !isfinite(sc2[eh])) err |= RTA_DEVERR_DETECTOR;
+                        sv[0][rt][eh] = live ? sc2[eh] : -INFINITY;
+                    }
+                }
+            }
 #pragma unroll
             for (int kl = 0; kl < KPW; ++kl) {
+                if (kPair) break;
                 if (kl == 1 && !two) break;
 #pragma unroll
                 for (int rt = 0; rt < 4; ++rt) {
@@ -1031,12 +1104,15 @@ __global__ void __launch_bounds__(256, 2) attn_chunk_mma_kernel(const AttnArgs a
             }
             if (first_tile) S_cur = S_new;
             // softmax over the tile, folded into (m, Z); weights and rescale factors to LDS
+            // (paired: one pass, lane segment u holding kv head u >> 1)
 #pragma unroll
-            for (int kl = 0; kl < KPW; ++kl) {
+            for (int kl = 0; kl < (kPair ? 1 : KPW); ++kl) {
                 if (kl == 1 && !two) break;
 #pragma unroll
                 for (int eh = 0; eh < 2; ++eh) {
-                    const int g = 2 * u + eh;
+                    const int klw = kPair ? (u >> 1) : kl;   // the kv head whose weights this lane writes
+                    const int g = kPair ? 2 * (u & 1) + eh : 2 * u + eh;
+                    const bool writes = g < G && (!kPair || klw == 0 || two);
                     float mx = fmaxf(fmaxf(sv[kl][0][eh], sv[kl][1][eh]), fmaxf(sv[kl][2][eh], sv[kl][3][eh]));
                     mx = row16_max(mx);
                     const float m_new = fmaxf(m_run[kl][eh], mx);
@@ -1053,10 +1129,10 @@ __global__ void __launch_bounds__(256, 2) attn_chunk_mma_kernel(const AttnArgs a
                     const float zt = row16_sum((w[0] + w[1]) + (w[2] + w[3]));
                     z_run[kl][eh] = z_run[kl][eh] * sf + zt;
                     m_run[kl][eh] = m_new;
-                    if (g < G) {
+                    if (writes) {
 #pragma unroll
-                        for (int rt = 0; rt < 4; ++rt) s_w[(kl * 8 + g) * kVtStride + 16 * rt + col] = w[rt];
-                        if (col == 0) s_f[kl * 8 + g] = ldexpf(sf, S_new - S_cur);
+                        for (int rt = 0; rt < 4; ++rt) s_w[(klw * 8 + g) * kVtStride + 16 * rt + col] = w[rt];
+                        if (col == 0) s_f[klw * 8 + g] = ldexpf(sf, S_new - S_cur);
                     }
                 }
             }
@@ -1197,10 +1273,19 @@ __global__ void __launch_bounds__(256, 2) attn_chunk_mma_kernel(const AttnArgs a
             }
 #pragma unroll
             for (int eh = 0; eh < 2; ++eh) {
-                const int g = 2 * u + eh;
-                if (col == 0 && g < G) {
-                    rec[(int64_t)(kvh * G + g) * kRec + kHd] = m_run[kl][eh] * 0.6931471805599453f;
-                    rec[(int64_t)(kvh * G + g) * kRec + kHd + 1] = z_run[kl][eh];
+                if (kPair) {   // lane segment u holds kv head u >> 1, heads 2 (u & 1) + eh
+                    const int g = 2 * (u & 1) + eh, klw = u >> 1;
+                    if (kl == 0 && col == 0 && g < G && (klw == 0 || two)) {
+                        const int kvw = kv0 + klw;
+                        rec[(int64_t)(kvw * G + g) * kRec + kHd] = m_run[0][eh] * 0.6931471805599453f;
+                        rec[(int64_t)(kvw * G + g) * kRec + kHd + 1] = z_run[0][eh];
+                    }
+                } else {
+                    const int g = 2 * u + eh;
+                    if (col == 0 && g < G) {
+                        rec[(int64_t)(kvh * G + g) * kRec + kHd] = m_run[kl][eh] * 0.6931471805599453f;
+                        rec[(int64_t)(kvh * G + g) * kRec + kHd + 1] = z_run[kl][eh];
+                    }
                 }
             }
         }
