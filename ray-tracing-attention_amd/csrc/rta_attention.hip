@@ -1138,9 +1138,22 @@ __global__ void __launch_bounds__(256, 2) attn_chunk_mma_kernel(const AttnArgs a
             }
             __builtin_amdgcn_wave_barrier();
             // rescale D (column 2g + part: head g), skipped when no running max and not S moved
+            // (paired: columns 8 klc + 2g + part, kv head klc = col >> 3; each D[kl] is read
+            // only in its own columns, so one factor per lane serves both)
             const int gcol = col >> 1;
+            const int klc = kPair ? col >> 3 : 0, gp = kPair ? (col & 7) >> 1 : gcol;
+            if constexpr (kPair) {
+                const float fl = gp < G && (klc == 0 || two) ? s_f[klc * 8 + gp] : 1.0f;
+                if (__builtin_amdgcn_ballot_w64(fl != 1.0f) != 0) {
+#pragma unroll
+                    for (int kl = 0; kl < KPW; ++kl)
+#pragma unroll
+                        for (int t = 0; t < 8; ++t) D[kl][t] *= fl;
+                }
+            }
 #pragma unroll
             for (int kl = 0; kl < KPW; ++kl) {
+                if (kPair) break;
                 if (kl == 1 && !two) break;
                 const float fl = gcol < G ? s_f[kl * 8 + gcol] : 1.0f;   // unused columns stay 0
                 if (__builtin_amdgcn_ballot_w64(fl != 1.0f) != 0) {
@@ -1161,16 +1174,13 @@ __global__ void __launch_bounds__(256, 2) attn_chunk_mma_kernel(const AttnArgs a
 #pragma unroll
                     for (int i = 0; i < 8; ++i) dS[i] = ldexpf(half_lo(dw[i]), S_cur);
                 }
-#pragma unroll
-                for (int kl = 0; kl < KPW; ++kl) {
-                    if (kl == 1 && !two) break;
-                    const int hh = hh_of(kl);
-                    // B: column col = head gcol, part col & 1: x = w d 2^S as hi + lo, both
-                    // rounded toward zero (|x - hi - lo| < 2^-21 |x|); columns of heads >= G
-                    // are never read
+                // B: column col = head gcol, part col & 1 (paired: kv head col >> 3, head
+                // (col & 7) >> 1, one operand for both): x = w d 2^S as hi + lo, both rounded
+                // toward zero (|x - hi - lo| < 2^-21 |x|); columns of heads >= G are never read
+                auto build_b = [&](int kl) {
                     h8_t bop;
                     {
-                        const float* wr = s_w + (kl * 8 + gcol) * kVtStride + pk0;
+                        const float* wr = s_w + (kPair ? klc * 8 + gp : kl * 8 + gcol) * kVtStride + pk0;
                         const float4 w0 = *reinterpret_cast<const float4*>(wr);
                         const float4 w1 = *reinterpret_cast<const float4*>(wr + 4);
                         const float wv[8] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
@@ -1186,6 +1196,15 @@ __global__ void __launch_bounds__(256, 2) attn_chunk_mma_kernel(const AttnArgs a
                             bop[i + 1] = v.y;
                         }
                     }
+                    return bop;
+                };
+                h8_t bop_pair;
+                if constexpr (kPair) bop_pair = build_b(0);
+#pragma unroll
+                for (int kl = 0; kl < KPW; ++kl) {
+                    if (kl == 1 && !two) break;
+                    const int hh = hh_of(kl);
+                    const h8_t bop = kPair ? bop_pair : build_b(kl);
                     // A: ql dword col, qh dword col & 7, sub-block scale dwords of nib 0 / 1
                     uint32_t ql[8], qh[8], sw[2][8];
                     {
@@ -1252,11 +1271,11 @@ __global__ void __launch_bounds__(256, 2) attn_chunk_mma_kernel(const AttnArgs a
         const int64_t w_lo = ((s_first + 1) * P - 1) / T;
         float* rec = a.ws + ((int64_t)s * a.rstride + (v - w_lo)) * a.hq * kRec;
         const float unit = ldexpf(1.0f, 14 - S_cur);   // D is in units of 2^(S - 14)
-        const int gcol = col >> 1;
-        const bool writer = (col & 1) == 0 && gcol < G;
+        const int gcol = kPair ? (col & 7) >> 1 : col >> 1;   // the lane's head (paired: of kv head col >> 3)
 #pragma unroll
         for (int kl = 0; kl < KPW; ++kl) {
             if (kl == 1 && !two) break;
+            const bool writer = (col & 1) == 0 && gcol < G && (!kPair || (col >> 3) == kl);
             const int kvh = kv0 + kl;
             float* rh = rec + (int64_t)(kvh * G + (gcol < G ? gcol : 0)) * kRec;
 #pragma unroll
