@@ -272,8 +272,10 @@ float orc_packet_value(const uint8_t* packet, int kvw, int fmt_k, int fmt_v, int
 
 static float halfround(float v) { return orc_half_to_float(orc_float_to_half(v)); }
 
-/* fp32 round-half-to-even clamp used for codes (GLSL round(); .5 ties are
- * implementation-defined there -- parity for exact ties is unpinned). */
+/* Codes are rintf() (round to nearest, ties to even) then clamped.  GLSL round() leaves
+ * the direction of exact .5 ties to the implementation; both vendors' native rounding
+ * instruction (AMD v_rndne_f32, NVIDIA cvt.rni) resolves them to even, and the known-answer
+ * packets of tests/test_oracle.py pin that choice. */
 static float clampf(float v, float lo, float hi) { return v < lo ? lo : (v > hi ? hi : v); }
 
 /* GLSL min / max (returns x unless y is strictly smaller / larger): decides the sign of

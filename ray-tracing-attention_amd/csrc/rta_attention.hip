@@ -107,6 +107,11 @@ struct AttnLds {
     }
 };
 
+// Two binary16 sums in one v_pk_add_f16.
+__device__ __forceinline__ uint32_t pk_add_f16(uint32_t a, uint32_t b) {
+    return __builtin_bit_cast(uint32_t, __builtin_bit_cast(h2v_t, a) + __builtin_bit_cast(h2v_t, b));
+}
+
 // ---- phase A: K scores --------------------------------------------------------
 // Q4_K key, head half hh of the superblock at blk (4-byte aligned).  Dims of the head:
 // chunk jc (bytes 16 + 32(2hh+jc) ..), dword t: low nibbles are dims 64jc + 4t + b,
@@ -198,8 +203,12 @@ __device__ __forceinline__ void score_q6k(const uint8_t* __restrict__ blk, int h
             const uint32_t H = funnel(qh[4 * (c & 1) + t], qh[4 * (c & 1) + t + 1], mis);
             const uint32_t lo = (A & 0x0F0F0F0Fu) | (((H >> shl) & 0x03030303u) << 4);
             const uint32_t hi = ((A >> 4) & 0x0F0F0F0Fu) | (((H >> shh) & 0x03030303u) << 4);
-            const half2_t l0 = as_codes(lo & 0x00FF00FFu), l1 = as_codes((lo >> 8) & 0x00FF00FFu);
-            const half2_t h0 = as_codes(hi & 0x00FF00FFu), h1 = as_codes((hi >> 8) & 0x00FF00FFu);
+            // (c - 32) 2^-24 per code, exact binary16 subnormals: each element whole (a
+            // -32 sum q term apart would cancel against the code term for small scores)
+            const half2_t l0 = as_codes(pk_add_f16(lo & 0x00FF00FFu, 0x80208020u));
+            const half2_t l1 = as_codes(pk_add_f16((lo >> 8) & 0x00FF00FFu, 0x80208020u));
+            const half2_t h0 = as_codes(pk_add_f16(hi & 0x00FF00FFu, 0x80208020u));
+            const half2_t h1 = as_codes(pk_add_f16((hi >> 8) & 0x00FF00FFu, 0x80208020u));
 #pragma unroll
             for (int g = 0; g < G; ++g) {
                 const float* qa = qg + g * kHd + 16 * c + 4 * t;
@@ -220,10 +229,9 @@ __device__ __forceinline__ void score_q6k(const uint8_t* __restrict__ blk, int h
         const float Dl = d * (float)(int8_t)((sc_lo >> (8 * c)) & 255u);
         const float Dh = d * (float)(int8_t)((sc_hi >> (8 * c)) & 255u);
 #pragma unroll
-        for (int g = 0; g < G; ++g) {
-            // sum (c - 32) q = sum c q - 32 sum q ; codes carry 2^-24
-            float v = fmaf(Dl, fmaf(alo[g], 16777216.0f, -32.0f * qs[g * 8 + c]), score[g]);
-            score[g] = fmaf(Dh, fmaf(ahi[g], 16777216.0f, -32.0f * qs[g * 8 + 4 + c]), v);
+        for (int g = 0; g < G; ++g) {   // the codes carry 2^-24
+            const float v = fmaf(Dl * 16777216.0f, alo[g], score[g]);
+            score[g] = fmaf(Dh * 16777216.0f, ahi[g], v);
         }
     }
 }
@@ -275,8 +283,7 @@ __device__ __forceinline__ QOp make_qop(const float* __restrict__ qg, int lane) 
         sum[kb] += __shfl_xor(sum[kb], 16, kWave);
         sum[kb] += __shfl_xor(sum[kb], 32, kWave);
     }
-    int e = 0;
-    if (mx > 0.0f && isfinite(mx)) (void)frexpf(mx, &e);
+    const int e = operand_exponent(mx);
     const float sg = ldexpf(1.0f, 14 - e);
     QOp o;
 #pragma unroll
@@ -762,22 +769,46 @@ __global__ void __launch_bounds__(256, 2) attn_chunk_kernel(const AttnArgs a) {
                 float D, M;
                 v_codes<VF, DPT>(vrows + jj * VROW, bhh, l0, cw, D, M);
                 const float* wr = s_w + bkvh * G * (kTile + 1) + jj;
-                float wD[G];
+                // every element enters the sum whole, w D (c - mu) with value = D (c - mu):
+                // a minimum (Q4_K, mu = M / D) or -32 offset (Q6_K) summed apart over the
+                // history would cancel against the code term and lose the bits of small
+                // results.  A Q4_K sub-block with D = 0 holds -M in every element; that
+                // term goes to off.
+                float wD[G], mu24 = 0.0f;
+                if constexpr (VF == RTA_Q4_K) {
+                    const bool dz = D == 0.0f;
+                    mu24 = dz ? 0.0f : (M / D) * (1.0f / 16777216.0f);
 #pragma unroll
-                for (int g = 0; g < G; ++g) {
-                    const float wg = wr[g * (kTile + 1)];
-                    wD[g] = wg * D;
-                    off[g] = (VF == RTA_Q4_K) ? fmaf(wg, M, off[g]) : off[g] + wD[g];
+                    for (int g = 0; g < G; ++g) {
+                        const float wg = wr[g * (kTile + 1)];
+                        wD[g] = wg * D;
+                        if (dz) off[g] = fmaf(wg, M, off[g]);
+                    }
+                } else {
+#pragma unroll
+                    for (int g = 0; g < G; ++g) wD[g] = wr[g * (kTile + 1)] * D;
                 }
 #pragma unroll
                 for (int k = 0; k < DPT / 4; ++k) {
-                    const half2_t lo = as_codes(cw[k] & 0x00FF00FFu), hi = as_codes((cw[k] >> 8) & 0x00FF00FFu);
+                    float e[4];   // (c - mu) 2^-24 of the four codes in dword k
+                    if constexpr (VF == RTA_Q4_K) {
+                        const half2_t lo = as_codes(cw[k] & 0x00FF00FFu), hi = as_codes((cw[k] >> 8) & 0x00FF00FFu);
+                        e[0] = (float)lo.x - mu24;
+                        e[1] = (float)hi.x - mu24;
+                        e[2] = (float)lo.y - mu24;
+                        e[3] = (float)hi.y - mu24;
+                    } else {   // c 2^-24 - 32 2^-24, exact in binary16 (subnormals)
+                        const half2_t lo = as_codes(pk_add_f16(cw[k] & 0x00FF00FFu, 0x80208020u));
+                        const half2_t hi = as_codes(pk_add_f16((cw[k] >> 8) & 0x00FF00FFu, 0x80208020u));
+                        e[0] = (float)lo.x;
+                        e[1] = (float)hi.x;
+                        e[2] = (float)lo.y;
+                        e[3] = (float)hi.y;
+                    }
 #pragma unroll
                     for (int g = 0; g < G; ++g) {
-                        acc[g][4 * k + 0] = fmaf((float)lo.x, wD[g], acc[g][4 * k + 0]);
-                        acc[g][4 * k + 1] = fmaf((float)hi.x, wD[g], acc[g][4 * k + 1]);
-                        acc[g][4 * k + 2] = fmaf((float)lo.y, wD[g], acc[g][4 * k + 2]);
-                        acc[g][4 * k + 3] = fmaf((float)hi.y, wD[g], acc[g][4 * k + 3]);
+#pragma unroll
+                        for (int i = 0; i < 4; ++i) acc[g][4 * k + i] = fmaf(e[i], wD[g], acc[g][4 * k + i]);
                     }
                 }
             }
@@ -791,8 +822,8 @@ __global__ void __launch_bounds__(256, 2) attn_chunk_kernel(const AttnArgs a) {
     // Coordinates l0 + 4k + e (l0 = DPT part) sit at 4 (k TPK + part) + e, which keeps
     // the float4 stores free of bank conflicts.
     float* s_u = lds + L.sc;   // [PG][hq][128]
-    // Q4_K: U = acc - 2^-24 sum w' M ;  Q6_K: U = acc - 32 * 2^-24 sum w' D
-    const float corr = (VF == RTA_Q4_K) ? (1.0f / 16777216.0f) : (32.0f / 16777216.0f);
+    // Q4_K: U = acc - 2^-24 sum w' M over the sub-blocks with D = 0 (off is 0 for Q6_K)
+    const float corr = 1.0f / 16777216.0f;
     if (bact) {
 #pragma unroll
         for (int g = 0; g < G; ++g) {
@@ -888,9 +919,6 @@ __device__ __forceinline__ float row16_sum(float v) {
     return v + dpp_mov<0x140>(v);
 }
 
-__device__ __forceinline__ uint32_t pk_add_f16(uint32_t a, uint32_t b) {
-    return __builtin_bit_cast(uint32_t, __builtin_bit_cast(h2v_t, a) + __builtin_bit_cast(h2v_t, b));
-}
 // a * b - c with one rounding (v_pk_fma_f16 with a negated addend)
 __device__ __forceinline__ uint32_t pk_fms_f16(uint32_t a, uint32_t b, uint32_t c) {
     return __builtin_bit_cast(uint32_t, __builtin_elementwise_fma(__builtin_bit_cast(h2v_t, a),
@@ -1219,15 +1247,17 @@ __global__ void __launch_bounds__(256, 2) attn_chunk_mma_kernel(const AttnArgs a
                         rd8(48 + 2 * hh, sw[0]);
                         rd8(49 + 2 * hh, sw[1]);
                     }
-                    // e 2^-14 = c sc 2^-14 - 32 sc 2^-14: the codes are built as 4 c in their
-                    // bytes, so a code pair moved into 16-bit halves reads as c 2^-22 (binary16
-                    // subnormals); times sc 2^8 that gives c sc 2^-14 as hi plus the exact
-                    // remainder lo (|c sc| < 2^13, every nonzero product >= 2^-14, so the
-                    // matrix-core operands are normal), and -sc 2^-9 (exact) goes in a third
-                    // instruction; D is then in units of 2^(S - 14)
+                    // e 2^-14 = (c - 32) sc 2^-14, each element whole (a separate -32 sc term
+                    // summed over the history would cancel against the code term and lose
+                    // the bits of small results): the codes are built as 4 c in their bytes,
+                    // so a code pair moved into 16-bit halves reads as c 2^-22 (binary16
+                    // subnormals); minus 2^-17 that is (c - 32) 2^-22 (exact), and times
+                    // sc 2^8 it gives (c - 32) sc 2^-14 as hi plus the exact remainder lo
+                    // (|(c - 32) sc| <= 4096, every nonzero product >= 2^-14, so the
+                    // matrix-core operands are normal); D is then in units of 2^(S - 14)
 #pragma unroll
                     for (int nib = 0; nib < 2; ++nib) {
-                        uint32_t code4[8], sc6[4], corr[4];
+                        uint32_t code4[8], sc6[4];
 #pragma unroll
                         for (int i = 0; i < 8; ++i) {
                             const uint32_t lo4 = nib ? (ql[i] >> 2) : (ql[i] << 2);
@@ -1239,9 +1269,7 @@ __global__ void __launch_bounds__(256, 2) attn_chunk_mma_kernel(const AttnArgs a
                             const uint32_t pr = __builtin_amdgcn_perm(sw[nib][2 * k + 1], sw[nib][2 * k], sc_sel);
                             const uint32_t sc = pk_add_f16((pr ^ 0x00800080u) | 0x64006400u, 0xE480E480u);   // - 1152
                             sc6[k] = pk_mul_f16(sc, 0x5C005C00u);    // sc 2^8
-                            corr[k] = pk_mul_f16(sc, 0x98009800u);    // -sc 2^-9
                         }
-                        const h8_t ac = __builtin_bit_cast(h8_t, uint4{corr[0], corr[1], corr[2], corr[3]});
 #pragma unroll
                         for (int b = 0; b < 4; ++b) {
                             const uint32_t sel = (uint32_t)b | (0x0Cu << 8) | ((4u + b) << 16) | (0x0Cu << 24);
@@ -1249,15 +1277,15 @@ __global__ void __launch_bounds__(256, 2) attn_chunk_mma_kernel(const AttnArgs a
 #pragma unroll
                             for (int k = 0; k < 4; ++k) {
                                 const uint32_t cp = __builtin_amdgcn_perm(code4[2 * k + 1], code4[2 * k], sel);
-                                ah[k] = pk_mul_f16(cp, sc6[k]);
-                                al[k] = pk_fms_f16(cp, sc6[k], ah[k]);   // remainder, exact
+                                const uint32_t cs = pk_add_f16(cp, 0x80808080u);   // - 2^-17 per half
+                                ah[k] = pk_mul_f16(cs, sc6[k]);
+                                al[k] = pk_fms_f16(cs, sc6[k], ah[k]);   // remainder, exact
                             }
                             const int t = 4 * nib + b;
                             D[kl][t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
                                 __builtin_bit_cast(h8_t, uint4{ah[0], ah[1], ah[2], ah[3]}), bop, D[kl][t], 0, 0, 0);
                             D[kl][t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
                                 __builtin_bit_cast(h8_t, uint4{al[0], al[1], al[2], al[3]}), bop, D[kl][t], 0, 0, 0);
-                            D[kl][t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ac, bop, D[kl][t], 0, 0, 0);
                         }
                     }
                 }

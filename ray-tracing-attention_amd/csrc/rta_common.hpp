@@ -108,6 +108,19 @@ __device__ __forceinline__ void q4k_scale_min_lane(uint32_t s0, uint32_t s1, uin
 }
 
 // ---- matrix-core operand helpers (v_mfma_f32_16x16x32_f16) ----
+
+// Exponent e of a block maximum mx = f 2^e (f in [0.5, 1)) for the power-of-two operand
+// scale 2^(14 - e) that puts the block's largest value in [2^13, 2^14): 0 for a zero or
+// non-finite maximum, and never below -110, so that the scale (<= 2^124) and its inverse
+// (>= 2^-124) stay finite normal fp32 numbers.  A block whose maximum is below 2^-111
+// (fp32 subnormals among them) is scaled by 2^124 only; it loses relative precision,
+// never finiteness.
+__device__ __forceinline__ int operand_exponent(float mx) {
+    int e = 0;
+    if (mx > 0.0f && isfinite(mx)) (void)frexpf(mx, &e);
+    return e < -110 ? -110 : e;
+}
+
 typedef _Float16 h8_t __attribute__((ext_vector_type(8)));
 typedef float f4_t __attribute__((ext_vector_type(4)));
 typedef _Float16 h2v_t __attribute__((ext_vector_type(2)));

@@ -86,8 +86,7 @@ __global__ void __launch_bounds__(64) xprep_kernel(const float* __restrict__ x, 
 #pragma unroll
     for (int i = 0; i < 8; ++i) m = fmaxf(m, fabsf(v[i]));
     for (int off = 16; off > 0; off >>= 1) m = fmaxf(m, __shfl_xor(m, off, kWave));   // within 32 lanes
-    int e = 0;
-    if (m > 0.0f && isfinite(m)) (void)frexpf(m, &e);
+    const int e = operand_exponent(m);
     const float s = ldexpf(1.0f, 14 - e);        // m * s in [2^13, 2^14)
     if (t == 0) p.inv[(int64_t)b * nsb + sb] = b < batch ? ldexpf(1.0f, e - 14) : 0.0f;
     constexpr int perm[8] = {0, 2, 1, 3, 4, 6, 5, 7};

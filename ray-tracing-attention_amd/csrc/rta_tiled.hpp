@@ -159,8 +159,7 @@ struct XStage {
 #pragma unroll
             for (int i = 0; i < 8; ++i) m = fmaxf(m, fabsf(v[k][i]));
             for (int off = 16; off > 0; off >>= 1) m = fmaxf(m, __shfl_xor(m, off, kWave));   // within 32 lanes
-            int e = 0;
-            if (m > 0.0f && isfinite(m)) (void)frexpf(m, &e);
+            const int e = operand_exponent(m);
             const float sc = ldexpf(1.0f, 14 - e);
             if (t == 0) {
                 const float f = rn.part ? row_norm_factor(rn, rnp[k]) : 1.0f;

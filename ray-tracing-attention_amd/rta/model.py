@@ -240,18 +240,21 @@ class DecodeModel:
         s, v = self.shape, self.views
         nfull = s.layers // s.full_every if s.full_every else 0
         nrec = s.layers - nfull
-        off = lambda p: p - self.state.data_ptr()
-        raw = self.state.cpu().numpy()
         B, hd, S = self.batch, s.head_dim, s.rec_heads * s.head_dim
+
+        def part(ptr, n):   # copies only the bytes of that part to the host
+            at = ptr - self.state.data_ptr()
+            return self.state[at:at + n].cpu().numpy()
+
         if kind == "recurrent":
-            n = nrec * v.recurrent_per_layer * 4
-            return raw[off(v.recurrent):off(v.recurrent) + n].view(np.float32).reshape(nrec, B, s.rec_heads, hd, hd)
+            raw = part(v.recurrent, nrec * v.recurrent_per_layer * 4)
+            return raw.view(np.float32).reshape(nrec, B, s.rec_heads, hd, hd)
         if kind == "conv":
-            n = nrec * v.conv_per_layer * 4
-            return raw[off(v.conv):off(v.conv) + n].view(np.float32).reshape(nrec, B, 3 * S, 3)
+            raw = part(v.conv, nrec * v.conv_per_layer * 4)
+            return raw.view(np.float32).reshape(nrec, B, 3 * S, 3)
         if kind == "packets":
-            n = nfull * v.slots_per_layer * v.packet_bytes
-            return raw[off(v.packets):off(v.packets) + n].reshape(nfull, B, s.capacity, v.packet_bytes)
+            raw = part(v.packets, nfull * v.slots_per_layer * v.packet_bytes)
+            return raw.reshape(nfull, B, s.capacity, v.packet_bytes)
         if kind == "ctx":
-            return raw[off(v.ctx):off(v.ctx) + 4 * B].view(np.int32).copy()
+            return part(v.ctx, 4 * B).view(np.int32).copy()
         raise ValueError(kind)

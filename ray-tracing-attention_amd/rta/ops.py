@@ -185,6 +185,12 @@ def _rows(t, name):
     return t
 
 
+def _rs(t):
+    """Row stride in elements as the C ABI takes it: a tensor of one row may carry any
+    stride for its single row (torch gives 0 or 1), which stands for the row width."""
+    return t.stride(0) if t.shape[0] > 1 else max(t.stride(0), t.shape[1])
+
+
 def embed(fmt, table, vocab, hidden, ids, out=None):
     """op 0: decoded embedding rows of `ids` (uint32/int32 device tensor)."""
     lib = _lib.load()
@@ -215,8 +221,8 @@ def head_norm(x, heads, hd, w=None, gate=None, mean=True, eps=1e-6):
     gs = 0
     if gate is not None:
         _rows(gate, "gate")
-        gs = gate.stride(0)
-    check(lib.rta_head_norm(_ptr(x), x.stride(0), _ptr(w), _ptr(gate), gs, x.shape[0], heads, hd, int(bool(mean)),
+        gs = _rs(gate)
+    check(lib.rta_head_norm(_ptr(x), _rs(x), _ptr(w), _ptr(gate), gs, x.shape[0], heads, hd, int(bool(mean)),
                             ctypes.c_float(eps), _stream()), "rta_head_norm")
     return x
 
@@ -226,12 +232,12 @@ def delta_gates(a, b, a_log, dt_bias, decay=None, beta=None):
     lib = _lib.load()
     _rows(a, "a")
     _rows(b, "b")
-    if a.stride(0) != b.stride(0):
+    if _rs(a) != _rs(b):
         raise ValueError("a and b must share a row stride")
     batch, heads = a.shape
     decay = torch.empty(batch, heads, dtype=torch.float32, device=a.device) if decay is None else decay
     beta = torch.empty(batch, heads, dtype=torch.float32, device=a.device) if beta is None else beta
-    check(lib.rta_delta_gates(_ptr(a), _ptr(b), a.stride(0), _ptr(a_log), _ptr(dt_bias), batch, heads, _ptr(decay),
+    check(lib.rta_delta_gates(_ptr(a), _ptr(b), _rs(a), _ptr(a_log), _ptr(dt_bias), batch, heads, _ptr(decay),
                               _ptr(beta), _stream()), "rta_delta_gates")
     return decay, beta
 
@@ -245,7 +251,7 @@ def short_conv(raw, state, w, heads, hd=128, eps=1e-6, out=None):
     batch = raw.shape[0]
     if out is None:
         out = torch.empty(batch, 3 * heads * hd, dtype=torch.float32, device=raw.device)
-    check(lib.rta_short_conv(_ptr(raw), raw.stride(0), _ptr(state), _ptr(w), batch, heads, hd, ctypes.c_float(eps),
+    check(lib.rta_short_conv(_ptr(raw), _rs(raw), _ptr(state), _ptr(w), batch, heads, hd, ctypes.c_float(eps),
                              _ptr(out), _stream()), "rta_short_conv")
     return out
 
@@ -261,9 +267,9 @@ def delta_rule(state, qkv, decay, beta, heads, hd=128, norm_w=None, gate=None, e
     gs = 0
     if gate is not None:
         _rows(gate, "gate")
-        gs = gate.stride(0)
-    check(lib.rta_delta_rule(_ptr(state), _ptr(qkv), qkv.stride(0), _ptr(decay), _ptr(beta), batch, heads, hd,
-                             _ptr(norm_w), _ptr(gate), gs, ctypes.c_float(eps), _ptr(out), out.stride(0), _stream()),
+        gs = _rs(gate)
+    check(lib.rta_delta_rule(_ptr(state), _ptr(qkv), _rs(qkv), _ptr(decay), _ptr(beta), batch, heads, hd,
+                             _ptr(norm_w), _ptr(gate), gs, ctypes.c_float(eps), _ptr(out), _rs(out), _stream()),
           "rta_delta_rule")
     return out
 
@@ -277,6 +283,6 @@ def pack_history(k, v, slot, packets, fmt_k=Q4_K, fmt_v=Q6_K):
     _dev(packets, "packets")
     batch, kvw = k.shape
     n_slots = packets.numel() // history_bytes(kvw)
-    check(lib.rta_pack_history(_ptr(k), k.stride(0), _ptr(v), v.stride(0), batch, kvw, fmt_k, fmt_v, _ptr(slot),
+    check(lib.rta_pack_history(_ptr(k), _rs(k), _ptr(v), _rs(v), batch, kvw, fmt_k, fmt_v, _ptr(slot),
                                n_slots, _ptr(packets), _stream()), "rta_pack_history")
     return packets

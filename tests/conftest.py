@@ -40,3 +40,20 @@ def tolerance_ok(actual, expected, rel=1e-3, abs_=1e-5):
     err = float(np.max(np.abs(a - e), initial=0.0))
     peak = float(np.max(np.abs(e), initial=0.0))
     return err <= abs_ + rel * peak, err / max(peak, 1e-30)
+
+
+def check_margin_ids(logits_gpu, ids_gpu, logits_ref, margin):
+    """ids equal the margin rule on the kernel's own logits, and the fp64 oracle's id unless
+    a logit sits within rounding of the threshold."""
+    import numpy as np
+    import oracle as orc
+    for b in range(logits_gpu.shape[0]):
+        # the kernel's id is exactly the margin rule applied to its own logits
+        assert int(ids_gpu[b]) == orc.argmax_margin_f32(logits_gpu[b], margin), b
+        # and the oracle's id, unless a logit sits within rounding of the threshold
+        ref = logits_ref[b]
+        M = ref.max()
+        T = M - margin * abs(M)
+        ambiguous = np.any(np.abs(ref - T) <= 1e-5 * max(1.0, abs(M)))
+        if not ambiguous:
+            assert int(ids_gpu[b]) == orc.argmax_margin_f64(ref, margin), b

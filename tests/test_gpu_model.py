@@ -1,70 +1,11 @@
 """End-to-end parity of rta_hybrid_decode_step (a small hybrid decoder: delta-net
 recurrent layers and full-attention layers) against an fp64 step composed from the
-oracle's restatements of every op.  Each step's reference starts from the GPU's
-state before that step, so float drift does not compound across steps; the new
-history packets are checked against the reference's keys and values to one
-quantisation step, the shifted conv windows bit exactly, the recurrent state, the
-new window entries, logits and next tokens to the float bar / the margin rule."""
-import numpy as np
+oracle's restatements of every op (step_reference.check_steps), over two steps."""
 import pytest
 
-import oracle as orc
-from conftest import tolerance_ok
+from step_reference import check_steps
 
 pytestmark = pytest.mark.gpu
-REL, ABS = 1e-3, 1e-5
-f32 = np.float32
-
-
-def assert_close(got, ref, what):
-    ok, frac = tolerance_ok(got, ref, REL, ABS)
-    assert ok, f"{what}: max|err|/peak = {frac:.3e}"
-
-
-def reference_step(m, tokens, ctx, rec, conv, packets_after):
-    s, g = m.shape, m.gguf
-    hq, hkv, hd, H, D, B, cap = s.q_heads, s.kv_heads, s.head_dim, s.rec_heads, s.hidden, m.batch, s.capacity
-    S = H * hd
-    Q4, Q6 = orc.Q4_K, orc.Q6_K
-    x = orc.embed(s.fmt_embed, g["embed"], s.vocab, D, tokens).astype(np.float64)
-    new_rec, new_conv = rec.astype(np.float64).copy(), conv.copy()
-    kv_new = []
-    lf = lr = 0
-    for l in range(s.layers):
-        n = orc.rmsnorm(x.astype(f32), g[f"{l}.norm_in"], s.eps)
-        if l % s.full_every == s.full_every - 1:
-            p = orc.gemv_f64(Q4, g[f"{l}.w_in"], (hq + 2 * hkv) * hd, D, n.astype(f32))
-            q = orc.head_norm(p[:, :hq * hd].astype(f32), hq, hd, w=g[f"{l}.q_norm"], eps=s.eps)
-            k = orc.head_norm(p[:, hq * hd:(hq + hkv) * hd].astype(f32), hkv, hd, w=g[f"{l}.k_norm"], eps=s.eps)
-            q = np.stack([orc.rope(q[b].reshape(hq, hd).astype(f32), ctx[b], s.rope_rotary, s.rope_theta)
-                          for b in range(B)])
-            k = np.stack([orc.rope(k[b].reshape(hkv, hd).astype(f32), ctx[b], s.rope_rotary, s.rope_theta)
-                          for b in range(B)]).reshape(B, -1)
-            kv_new.append((k, p[:, (hq + hkv) * hd:]))
-            flat = packets_after[lf].reshape(B * cap, -1)
-            attn, _, _ = orc.decode_attention(q.astype(f32), flat, s.fmt_k, s.fmt_v, [b * cap for b in range(B)],
-                                              [c + 1 for c in ctx], cap, hkv)
-            x = x + orc.gemv_f64(Q4, g[f"{l}.w_o"], D, hq * hd, attn.reshape(B, -1).astype(f32))
-            lf += 1
-        else:
-            p = orc.gemv_f64(Q4, g[f"{l}.w_in"], 4 * S + 2 * H, D, n.astype(f32))
-            decay, beta = orc.delta_gates(p[:, 4 * S:4 * S + H].astype(f32), p[:, 4 * S + H:].astype(f32),
-                                          g[f"{l}.a_log"], g[f"{l}.dt_bias"])
-            y, ns = orc.short_conv(p[:, :3 * S].astype(f32), conv[lr], g[f"{l}.conv_w"], H, hd, s.eps)
-            new_conv[lr] = ns
-            st, o = orc.delta_rule(rec[lr].astype(np.float64), y[:, :S], y[:, S:2 * S], y[:, 2 * S:], decay, beta)
-            new_rec[lr] = st
-            o = orc.head_norm(o.astype(f32), H, hd, w=g[f"{l}.out_norm"], gate=p[:, 3 * S:4 * S].astype(f32),
-                              eps=s.eps)
-            x = x + orc.gemv_f64(Q4, g[f"{l}.w_o"], D, S, o.astype(f32))
-            lr += 1
-        n = orc.rmsnorm(x.astype(f32), g[f"{l}.norm_post"], s.eps)
-        _, y = orc.mlp_swiglu((Q4, Q4, Q4), g[f"{l}.w_gate"], g[f"{l}.w_up"], g[f"{l}.w_down"], D, s.ff,
-                              n.astype(f32))
-        x = x + y
-    n = orc.rmsnorm(x.astype(f32), g["norm_final"], s.eps)
-    logits = orc.gemv_f64(Q6, g["lm_head"], s.vocab, D, n.astype(f32))
-    return logits, new_rec, new_conv, kv_new
 
 
 # hidden 256 puts every packed in-projection in one K slab (written straight to the
@@ -79,32 +20,4 @@ def test_hybrid_decode_steps(packed, hidden):
                               fmt_k=Q4_K, fmt_v=Q6_K, rope_rotary=128, eps=1e-6, margin=1e-4, rope_theta=1e6)
     ctx = [5, 17, 70]                                      # 70 > capacity: the ring has wrapped
     m = model.DecodeModel(shape, 3, ctx, seed=7, keep_gguf=True)
-    cap = shape.capacity
-    for step in range(2):
-        tokens = m.tokens.cpu().numpy().view(np.uint32).copy()
-        pos = m.state_view("ctx")
-        rec, conv = m.state_view("recurrent"), m.state_view("conv")
-        m.step(logits=True)
-        got_tokens = m.tokens.cpu().numpy().view(np.uint32)
-        got_logits = m.logits.cpu().numpy()
-        packets = m.state_view("packets")
-        ref_logits, ref_rec, ref_conv, kv_new = reference_step(m, tokens, pos, rec, conv, packets)
-        assert np.array_equal(m.state_view("ctx"), pos + 1)
-        for b in range(3):
-            assert_close(got_logits[b], ref_logits[b], f"step {step} logits row {b}")
-            assert int(got_tokens[b]) == orc.argmax_margin_f32(got_logits[b], 1e-4), (step, b)
-        got_conv = m.state_view("conv")
-        assert np.array_equal(got_conv[..., :2], ref_conv[..., :2]), step     # shifted window: exact
-        assert_close(got_conv[..., 2], ref_conv[..., 2], f"step {step} conv window (new raw value)")
-        assert_close(m.state_view("recurrent"), ref_rec, f"step {step} recurrent state")
-        # the new token's packet of each full layer holds the reference's k / v to one
-        # quantisation step of its group
-        kvw = shape.kv_heads * 128
-        for lf, (k, v) in enumerate(kv_new):
-            for b in range(3):
-                pk = np.ascontiguousarray(packets[lf, b, pos[b] % cap])
-                kk = np.array([orc.lib().orc_packet_value(pk.ctypes.data, kvw, Q4_K, Q6_K, 0, c) for c in range(kvw)])
-                vv = np.array([orc.lib().orc_packet_value(pk.ctypes.data, kvw, Q4_K, Q6_K, 1, c) for c in range(kvw)])
-                for field, dec, q in ((k[b], kk, 15.0), (v[b], vv, 31.0)):
-                    step_ = 2.0 * np.abs(field).max() / q
-                    assert np.max(np.abs(dec - field)) <= step_ * 1.01, (step, lf, b)
+    check_steps(m, 2)

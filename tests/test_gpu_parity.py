@@ -6,7 +6,7 @@ import numpy as np
 import pytest
 
 import oracle as orc
-from conftest import tolerance_ok
+from conftest import check_margin_ids, tolerance_ok
 from rta import ops, synth
 
 pytestmark = pytest.mark.gpu
@@ -155,6 +155,37 @@ def test_gemv_invariants(torch_dev, fmt):
         assert_close(y7[b], ref[b], f"VALU row {b}")
 
 
+@pytest.mark.parametrize("fmt", [orc.Q4_K, orc.Q6_K])
+@pytest.mark.parametrize("packed", [False, True])
+@pytest.mark.parametrize("batch", [4, 8, 32])
+def test_readouts_tiny_and_huge_inputs(torch_dev, fmt, packed, batch):
+    """Input rows whose superblocks hold fp32 subnormals only, or values near 1e30, beside
+    ordinary rows: every path (vector ALUs below 8 rows, matrix cores from 8 rows and on
+    packed weights) stays finite and within the bar per row."""
+    from rta._lib import TILED
+    torch, dev = torch_dev
+    rows, cols = 320, 2048
+    rng = np.random.default_rng(61 + batch + 2 * fmt)
+    w = synth.random_matrix(rng, fmt, rows, cols)
+    x = rng.standard_normal((batch, cols)).astype(np.float32)
+    sub = (rng.standard_normal(cols) * 1e-40).astype(np.float32)     # fp32 subnormals
+    x[0] = sub                                                      # a whole row of subnormals
+    x[1, 256:512] = sub[:256]                                       # one subnormal superblock
+    x[2, :256] *= np.float32(1e30)                                  # one superblock near 1e30
+    x[3] = np.float32(-1e30) * np.sign(x[3])                        # a whole row at -+1e30
+    assert np.all(np.abs(x[0][x[0] != 0]) < np.finfo(np.float32).tiny)
+    wd = to_dev(torch, w, dev)
+    f = fmt
+    if packed:
+        wd, f = ops.pack(fmt, wd, rows, cols), fmt | TILED
+    got = ops.gemv(f, wd, rows, cols, to_dev(torch, x, dev)).cpu().numpy()
+    ref = orc.gemv_f64(fmt, w, rows, cols, x)
+    assert np.isfinite(got).all()
+    for b in range(batch):
+        assert_close(got[b], ref[b], f"row {b}")
+    assert ops.device_error() == 0
+
+
 def test_gemv_plain_formats(torch_dev):
     torch, dev = torch_dev
     rng = np.random.default_rng(44)
@@ -195,19 +226,6 @@ def test_mlp_swiglu_parity(torch_dev, batch):
 
 
 # --------------------------------------------------------------- LM head ----
-def _check_ids(logits_gpu, ids_gpu, logits_ref, margin):
-    for b in range(logits_gpu.shape[0]):
-        # the kernel's id is exactly the margin rule applied to its own logits
-        assert int(ids_gpu[b]) == orc.argmax_margin_f32(logits_gpu[b], margin), b
-        # and the oracle's id, unless a logit sits within rounding of the threshold
-        ref = logits_ref[b]
-        M = ref.max()
-        T = M - margin * abs(M)
-        ambiguous = np.any(np.abs(ref - T) <= 1e-5 * max(1.0, abs(M)))
-        if not ambiguous:
-            assert int(ids_gpu[b]) == orc.argmax_margin_f64(ref, margin), b
-
-
 @pytest.mark.parametrize("batch", [1, 4, 16, 33])
 def test_lm_head_parity(torch_dev, batch):
     torch, dev = torch_dev
@@ -220,7 +238,7 @@ def test_lm_head_parity(torch_dev, batch):
     ref = orc.gemv_f64(orc.Q6_K, w, vocab, hidden, h)
     for b in range(batch):
         assert_close(logits[b], ref[b], f"logits row {b}")
-    _check_ids(logits, ids, ref, 1e-4)
+    check_margin_ids(logits, ids, ref, 1e-4)
 
 
 def test_lm_head_planted_winner_and_ties(torch_dev):
@@ -312,14 +330,6 @@ def test_attention_multi_tile_chunks(torch_dev, fmts, max_ctx):
 def test_attention_ring_capacity(torch_dev):
     torch, dev = torch_dev
     _attention_case(torch, dev, 7, [600, 1000, 90], 16, 4, (orc.Q6_K, orc.Q4_K), capacity=300)
-
-
-def test_attention_config3_sized(torch_dev):
-    torch, dev = torch_dev
-    rng = np.random.default_rng(20261112)
-    ctx = synth.log_uniform_lengths(rng, 16, 512, 32768)
-    ctx = np.minimum(ctx, 4096)   # full 32k contexts are exercised by the bench's checks
-    _attention_case(torch, dev, 8, ctx.tolist(), 16, 4, (orc.Q6_K, orc.Q4_K))
 
 
 # ------------------------------------------------------------------- RoPE ----

@@ -173,3 +173,22 @@ def test_pack_history_bad_slot(torch_dev):
     assert ops.device_error(clear=True) & 8
     got = packets.cpu().numpy().reshape(3, -1)
     assert got[1].any() and not got[0].any() and not got[2].any()
+
+
+@pytest.mark.parametrize("fmts", [(orc.Q4_K, orc.Q6_K), (orc.Q6_K, orc.Q4_K)])
+def test_pack_history_known_answer(torch_dev, fmts):
+    """The HIP packer writes the hand-built packet bytes (exact d / dmin from /63 and /127,
+    scale code 127, round to nearest with .5 ties to even) in both field orders."""
+    from known_answers import known_answer_fields
+    torch, dev = torch_dev
+    k, v, expected = known_answer_fields()
+    if fmts[0] == orc.Q6_K:   # swapped: the Q6_K row is the K field
+        k, v = v, k
+        expected = np.concatenate([expected[144:354], expected[:144], expected[354:]])
+    packets = torch.zeros(2 * 360, dtype=torch.uint8, device=dev)
+    ops.pack_history(to_dev(torch, k[None], dev), to_dev(torch, v[None], dev),
+                     to_dev(torch, np.array([1], np.int64), dev), packets, *fmts)
+    got = packets.cpu().numpy().reshape(2, 360)
+    assert not got[0].any()
+    diff = np.nonzero(got[1] != expected)[0]
+    assert diff.size == 0, f"bytes differ at {diff[:16]}"

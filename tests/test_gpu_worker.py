@@ -150,6 +150,21 @@ def test_invalid_requests_end_the_worker(tmp_path_factory, served):
     with pytest.raises(RuntimeError, match="Unknown resident operation"):
         w.request(2, 1, 0)
     assert w.close() == 1
+    # non-finite MLP input is refused (verify_rt_mlp.py:103-109; optical_resident.cpp:925)
+    for bad in (np.nan, np.inf):
+        w = Worker(EXE, d, CAPACITY, env=dict(os.environ))
+        with pytest.raises(RuntimeError, match="Optical MLP input must be finite"):
+            w.mlp(np.full((1, spec["hidden_size"]), bad, np.float32), 0, spec["hidden_size"], spec["middle_size"])
+        assert w.close() == 1
+    # and so is a non-finite attention query
+    hd, heads, kv = spec["attention_head_dim"], spec["attention_heads"], spec["kv_heads"]
+    w = Worker(EXE, d, CAPACITY, env=dict(os.environ))
+    q = np.zeros((1, heads, hd), np.float32)
+    q[0, 0, 0] = np.inf
+    k = np.zeros((4, kv, hd), np.float32)
+    with pytest.raises(RuntimeError, match="Attention diagnostic values must be finite"):
+        w.attention(q, k, k, None, spec["layer_types"].index("full"), 3, 0, heads, kv, hd)
+    assert w.close() == 1
 
 
 def test_unsupported_backend_is_refused(served, tmp_path_factory):

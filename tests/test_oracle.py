@@ -14,6 +14,7 @@ from scipy.special import softmax
 
 import oracle as orc
 from ggml_ref import ggml_q4k, ggml_q6k
+from known_answers import known_answer_fields
 from rta import synth
 
 
@@ -294,6 +295,36 @@ def test_packer_round_trip(fmts):
     assert not pk[708:].any()                                  # 4 pad bytes stay zero
 
 
+def test_packer_known_answer_bytes():
+    """Packet bytes equal the hand-built GGUF blocks: d / dmin from /63 and /127 (a /64 or
+    /128 changes the binary16 bytes), scale code 127 kept (no 63 clamp on Q6_K), codes
+    rounded to nearest (not truncated), .5 ties to even, and the pad bytes zero."""
+    k, v, expected = known_answer_fields()
+    got = orc.pack_history(k, v, orc.Q4_K, orc.Q6_K)
+    assert got.size == expected.size == 360
+    diff = np.nonzero(got != expected)[0]
+    assert diff.size == 0, f"bytes differ at {diff[:16]}"
+    # the swapped field order puts V's Q6_K block first and K's Q4_K block second
+    sw = orc.pack_history(v, k, orc.Q6_K, orc.Q4_K)
+    assert np.array_equal(sw[:210], expected[144:354]) and np.array_equal(sw[210:354], expected[:144])
+
+
+def test_packer_rounds_d_to_binary16_before_the_codes():
+    """The block scale is rounded to binary16 before the group codes are formed
+    (resident_history_quant.glsl:22 then :27): group ranges 1.0 and 0.5 give
+    maxD / 63 = 0.0010582 -> binary16 0.00105857849, so the second group's code is
+    round(0.5/15 / 0.00105857849) = round(31.489) = 31 (with the unrounded scale it
+    would be round(31.500002) = 32)."""
+    k = np.zeros(256, np.float32)
+    k[0:32] = np.linspace(0.0, 1.0, 32, dtype=np.float32)
+    k[32:64] = np.linspace(0.0, 0.5, 32, dtype=np.float32)
+    pk = orc.pack_history(k, np.zeros(256, np.float32), orc.Q4_K, orc.Q6_K)
+    assert pk[0:2].view(np.float16)[0] == np.float16(0.0010585784912109375)
+    assert pk[2:4].view(np.uint16)[0] == 0                     # dmin = 0: every minimum is 0
+    assert pk[4] & 63 == 63 and pk[5] & 63 == 31
+    assert pk[6] & 63 == 0 and pk[8] & 63 == 0                  # empty groups, zero minima
+
+
 # ------------------------------------------------------- decoder-step ops ----
 def test_embed_rows_match_ggml_rows():
     rng = np.random.default_rng(14)
@@ -391,3 +422,24 @@ def test_delta_rule_recall_and_decay():
     assert np.allclose(S1, 0.9 * S0, rtol=1e-15)
     ref = np.einsum("hvk,hk->hv", 0.9 * S0[0], q.reshape(heads, hd)).reshape(1, -1) / np.sqrt(hd)
     assert np.allclose(o, ref, rtol=1e-12)
+
+
+def test_delta_rule_rank_one_closed_form():
+    """Decay, then predict, then write (resident_math.comp:144-146): from a rank-1 state
+    S0 = a b^T ([value][key]) with decay l and beta t,
+      S1 = l a b^T + t (v - l a (b.k)) k^T,   o = S1 q / sqrt(hd)
+         = (l a (b.q) + t (v - l a (b.k)) (k.q)) / sqrt(hd).
+    Predicting from the undecayed state (u = a (b.k)), a transposed state or a dropped
+    decay each change the result."""
+    rng = np.random.default_rng(19)
+    hd = 128
+    a, b, k, q, v = (rng.standard_normal(hd) for _ in range(5))
+    lam, beta = 0.5, 0.75
+    S0 = np.outer(a, b)[None, None]
+    S1, o = orc.delta_rule(S0, q[None], k[None], v[None], np.array([[lam]]), np.array([[beta]]))
+    err = v - lam * a * (b @ k)
+    assert np.allclose(S1[0, 0], lam * np.outer(a, b) + beta * np.outer(err, k), rtol=1e-13, atol=1e-13)
+    want = (lam * a * (b @ q) + beta * err * (k @ q)) / np.sqrt(hd)
+    assert np.allclose(o[0], want, rtol=1e-12, atol=1e-13)
+    wrong = (lam * a * (b @ q) + beta * (v - a * (b @ k)) * (k @ q)) / np.sqrt(hd)   # predict before decay
+    assert not np.allclose(o[0], wrong, rtol=1e-6)
