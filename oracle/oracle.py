@@ -217,3 +217,63 @@ def delta_rule(state, q, k, v, decay, beta):
     lib().orc_delta_rule(_p_(state), _p_(q), _p_(k), _p_(v), q.shape[1], _p_(_c(decay, np.float64)),
                          _p_(_c(beta, np.float64)), batch, heads, hd, _p_(out))
     return state, out
+
+
+# ---- one whole decode step on the CPU (fp32, OpenMP; rta_cpu_step.c) ----
+class StepLayer(ctypes.Structure):
+    _fields_ = [(n, _p) for n in ("norm_in", "norm_post", "w_in", "w_o", "w_gate", "w_up", "w_down", "q_norm",
+                                  "k_norm", "conv_w", "a_log", "dt_bias", "out_norm")]
+
+
+class StepModel(ctypes.Structure):
+    _fields_ = [(n, _i) for n in ("hidden", "layers", "full_every", "q_heads", "kv_heads", "head_dim", "rec_heads",
+                                  "ff", "vocab", "capacity", "fmt_embed", "fmt_proj", "fmt_lm", "fmt_k", "fmt_v",
+                                  "rope_rotary")] + \
+        [("eps", _f), ("margin", _f), ("rope_theta", _d), ("embed", _p), ("layers_ptr", ctypes.POINTER(StepLayer)),
+         ("norm_final", _p), ("lm_head", _p)]
+
+
+class CpuStep:
+    """The hybrid decoder's weights as GGUF rows in host memory (names as in the product's
+    test models: "embed", "norm_final", "lm_head", "{l}.norm_in", "{l}.w_in", ...), and
+    the fp32 CPU step over a state laid out as the product's."""
+
+    def __init__(self, shape, gguf):
+        self.shape = shape
+        self._keep = []
+
+        def ptr(name):
+            a = gguf.get(name)
+            if a is None:
+                return None
+            a = np.ascontiguousarray(a)
+            self._keep.append(a)
+            return a.ctypes.data
+
+        s = shape
+        self.layers = (StepLayer * s.layers)()
+        for l in range(s.layers):
+            L = self.layers[l]
+            for n, _ in StepLayer._fields_:
+                setattr(L, n, ptr(f"{l}.{n}"))
+        self.model = StepModel(hidden=s.hidden, layers=s.layers, full_every=s.full_every, q_heads=s.q_heads,
+                               kv_heads=s.kv_heads, head_dim=s.head_dim, rec_heads=s.rec_heads, ff=s.ff,
+                               vocab=s.vocab, capacity=s.capacity, fmt_embed=s.fmt_embed & 0xff,
+                               fmt_proj=s.fmt_proj & 0xff, fmt_lm=s.fmt_lm & 0xff, fmt_k=s.fmt_k, fmt_v=s.fmt_v,
+                               rope_rotary=s.rope_rotary, eps=s.eps, margin=s.margin, rope_theta=s.rope_theta,
+                               embed=ptr("embed"), layers_ptr=self.layers, norm_final=ptr("norm_final"),
+                               lm_head=ptr("lm_head"))
+        f = lib().orc_step_f32
+        f.restype = _i
+        f.argtypes = [ctypes.POINTER(StepModel), _i, _p, _p, _p, _p, _p, _p, _i]
+
+    def step(self, batch, rec, conv, packets, ctx, tokens, logits=None, threads=0):
+        """Updates rec [nrec,B,H,128,128] f32, conv [nrec,B,3S,3] f32, packets [nfull,B,cap,pb] u8,
+        ctx [B] i32 and tokens [B] u32 in place; logits [B, vocab] f32 or None."""
+        for a, dt in ((rec, np.float32), (conv, np.float32), (packets, np.uint8), (ctx, np.int32),
+                      (tokens, np.uint32)):
+            assert a.dtype == dt and a.flags.c_contiguous
+        assert logits is None or (logits.dtype == np.float32 and logits.flags.c_contiguous)
+        rc = lib().orc_step_f32(ctypes.byref(self.model), batch, _p_(rec), _p_(conv), _p_(packets), _p_(ctx),
+                                _p_(tokens), _p_(logits), threads)
+        assert rc == 0, rc

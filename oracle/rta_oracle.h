@@ -139,6 +139,37 @@ void orc_short_conv(const float* raw, int raw_stride, const float* state, const 
 void orc_delta_rule(double* state, const double* q, const double* k, const double* v, int stride,
                     const double* decay, const double* beta, int batch, int heads, int hd, double* out);
 
+
+/* ---- one whole decode step on the CPU (rta_cpu_step.c) ----
+ * fp32, OpenMP: the timed CPU baseline of the decode-step benchmark and a second
+ * composition of the step for the tests.  Shapes and state layout as the product's
+ * hybrid decode step: per recurrent layer the state [batch][rec_heads][128][128]
+ * ([value][key]) and the conv window [batch][3 S][3] (S = rec_heads * 128); per full
+ * layer the packet ring [batch][capacity] (sequence b owns slots b*capacity ..);
+ * ctx[b] = tokens already in the history = the new token's position.  The step reads
+ * tokens[b], writes the greedy next tokens and logits [batch][vocab] (may be NULL),
+ * and advances ctx. */
+typedef struct orc_step_layer {
+    const float *norm_in, *norm_post;               /* [hidden] */
+    const void *w_in, *w_o, *w_gate, *w_up, *w_down; /* GGUF rows of fmt_proj */
+    const float *q_norm, *k_norm;                   /* full layers */
+    const float *conv_w, *a_log, *dt_bias, *out_norm; /* recurrent layers */
+} orc_step_layer;
+
+typedef struct orc_step_model {
+    int hidden, layers, full_every, q_heads, kv_heads, head_dim, rec_heads, ff, vocab, capacity;
+    int fmt_embed, fmt_proj, fmt_lm, fmt_k, fmt_v, rope_rotary;
+    float eps, margin;
+    double rope_theta;
+    const void* embed;
+    const orc_step_layer* layers_ptr;
+    const float* norm_final;
+    const void* lm_head;
+} orc_step_model;
+
+int orc_step_f32(const orc_step_model* m, int batch, float* rec, float* conv, uint8_t* packets, int32_t* ctx,
+                 uint32_t* tokens, float* logits, int threads);
+
 #ifdef __cplusplus
 }
 #endif
