@@ -36,7 +36,8 @@ enum rta_status {
     RTA_ERR_WORKSPACE = 5, /* workspace missing or smaller than required          */
     RTA_ERR_LAUNCH = 6,    /* the HIP runtime reported an error at launch         */
     RTA_ERR_RANGE = 7,     /* an argument is outside the supported range          */
-    RTA_ERR_DEVICE = 8     /* the device error word is non-zero (rta_device_error) */
+    RTA_ERR_DEVICE = 8,    /* the device error word is non-zero (rta_device_error) */
+    RTA_ERR_SCRATCH = 9    /* the call needs more than RTA_NOALLOC_SCRATCH_BYTES of scratch */
 };
 
 /* GGUF type codes, as the reference uses them (resident_quant.glsl:6-20).
@@ -166,6 +167,25 @@ int rta_decode_attention(const float* q, int nseq, int hq, int hkv, int hd,
                          const int64_t* slot_base, const int32_t* ctx_len, int64_t capacity,
                          int64_t n_slots, int max_ctx, const float* gate, float* out, float* m_out, float* z_out,
                          void* workspace, size_t workspace_bytes, rta_stream_t stream);
+
+/* The same decode attention for callers that cannot allocate device memory (code under
+ * HIP graph capture, tight serving loops, harnesses that forbid hipMalloc): no workspace
+ * argument; the library's own scratch, a device array of RTA_NOALLOC_SCRATCH_BYTES per
+ * GPU held until the process ends, stands in for it.  The call allocates nothing (no
+ * hipMalloc / hipFree, no allocating library routine).  A call whose
+ * rta_decode_attention_workspace_bytes() exceeds RTA_NOALLOC_SCRATCH_BYTES returns
+ * RTA_ERR_SCRATCH and launches nothing.  Every call on one GPU shares that GPU's
+ * scratch: calls that overlap on one GPU (concurrent streams, threads) race.
+ * No counterpart in the reference, whose worker owns every buffer itself
+ * (vulkan_engine.hpp:41); it exists for the callers above.
+ * 96 MiB holds the decode step's attention at batch 32 (32 / 8 heads, contexts up to
+ * 8192) and the GQA workload (16 sequences, 16 / 4 heads, contexts up to 32768). */
+#define RTA_NOALLOC_SCRATCH_BYTES ((size_t)96 << 20)
+int rta_decode_attention_noalloc(const float* q, int nseq, int hq, int hkv, int hd,
+                                 const void* packets, int fmt_k, int fmt_v,
+                                 const int64_t* slot_base, const int32_t* ctx_len, int64_t capacity,
+                                 int64_t n_slots, int max_ctx, const float* gate, float* out, float* m_out,
+                                 float* z_out, rta_stream_t stream);
 
 /* ---------------- the rest of a decoder step (resident_math.comp ops 0, 1, 14, 15,
  * 18-21, 34); every call is stream ordered, allocates nothing, validates on the host. */

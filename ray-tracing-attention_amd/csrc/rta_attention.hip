@@ -25,6 +25,8 @@
 // receipt merge of the grouped backends (resident_attention_runtime.inl:618-645).
 #include <math.h>
 
+#include <mutex>
+
 #include "rta_common.hpp"
 #include "rta_host.hpp"
 
@@ -1556,6 +1558,34 @@ static hipError_t launch_chunks(int G, const AttnArgs& a, int lds, hipStream_t s
     }
 }
 
+// ---- scratch of rta_decode_attention_noalloc ----------------------------------------
+// The workspace of rta_decode_attention held in a file-scope device array, for callers
+// that cannot allocate.  Each GPU the library runs on holds its own copy of the array
+// (RTA_NOALLOC_SCRATCH_BYTES) until the process ends.  Every call on a GPU shares that
+// GPU's copy, which keeps the last call's records: calls that overlap on one GPU race.
+// Host code never uses the array's name as an address (on the host it is a stand-in):
+// the device address comes from hipGetSymbolAddress, once per device.
+static __device__ __align__(256) uint8_t scratch[RTA_NOALLOC_SCRATCH_BYTES];
+
+constexpr int kMaxDevices = 64;
+
+// Device address of the current device's scratch, looked up once per device with that
+// device current.  RTA_OK or RTA_ERR_LAUNCH (no current device / the lookup failed).
+static int scratch_address(void** out) {
+    static std::mutex mu;
+    static void* addr[kMaxDevices] = {};
+    int dev = -1;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return RTA_ERR_LAUNCH;
+    std::lock_guard<std::mutex> lock(mu);
+    if (!addr[dev]) {
+        void* p = nullptr;
+        if (hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)) != hipSuccess || !p) return RTA_ERR_LAUNCH;
+        addr[dev] = p;
+    }
+    *out = addr[dev];
+    return RTA_OK;
+}
+
 }  // namespace rta
 
 using namespace rta;
@@ -1650,6 +1680,20 @@ int rta_decode_attention(const float* q, int nseq, int hq, int hkv, int hd, cons
     if (e != hipSuccess) return RTA_ERR_LAUNCH;
     hipLaunchKernelGGL(attn_merge_kernel, dim3(nseq * hq), dim3(256), 0, s, a);
     return hipGetLastError() == hipSuccess ? RTA_OK : RTA_ERR_LAUNCH;
+}
+
+int rta_decode_attention_noalloc(const float* q, int nseq, int hq, int hkv, int hd, const void* packets, int fmt_k,
+                                 int fmt_v, const int64_t* slot_base, const int32_t* ctx_len, int64_t capacity,
+                                 int64_t n_slots, int max_ctx, const float* gate, float* out, float* m_out,
+                                 float* z_out, rta_stream_t stream) {
+    const size_t need = rta_decode_attention_workspace_bytes(nseq, hq, hkv, hd, max_ctx);
+    // need == 0: an invalid shape, reported by rta_decode_attention's own checks
+    if (need > RTA_NOALLOC_SCRATCH_BYTES) return RTA_ERR_SCRATCH;
+    void* ws = nullptr;
+    const int rc = scratch_address(&ws);
+    if (rc) return rc;
+    return rta_decode_attention(q, nseq, hq, hkv, hd, packets, fmt_k, fmt_v, slot_base, ctx_len, capacity, n_slots,
+                                max_ctx, gate, out, m_out, z_out, ws, RTA_NOALLOC_SCRATCH_BYTES, stream);
 }
 
 }  // extern "C"

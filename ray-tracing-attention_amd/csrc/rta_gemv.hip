@@ -497,6 +497,7 @@ const char* rta_status_string(int status) {
     case RTA_ERR_LAUNCH: return "HIP launch error";
     case RTA_ERR_RANGE: return "argument out of supported range";
     case RTA_ERR_DEVICE: return "device error word set";
+    case RTA_ERR_SCRATCH: return "call needs more scratch than the no-alloc variant holds (RTA_NOALLOC_SCRATCH_BYTES)";
     default: return "unknown status";
     }
 }

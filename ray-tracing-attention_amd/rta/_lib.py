@@ -15,6 +15,8 @@ F32, F16, Q4_K, Q6_K, BF16 = 0, 1, 12, 14, 30
 TILED = 0x100   # fmt | TILED: a K-quant matrix packed by rta_pack
 EPI_STORE, EPI_ACCUMULATE = 0, 1
 DEVERR_HITS, DEVERR_VOCAB, DEVERR_DETECTOR = 8, 2048, 65536
+NOALLOC_SCRATCH_BYTES = 96 << 20   # RTA_NOALLOC_SCRATCH_BYTES
+ERR_SCRATCH = 9                    # RTA_ERR_SCRATCH
 
 _i, _i64, _sz, _f, _d, _p, _u32p = (ctypes.c_int, ctypes.c_int64, ctypes.c_size_t, ctypes.c_float,
                                     ctypes.c_double, ctypes.c_void_p, ctypes.POINTER(ctypes.c_uint32))
@@ -52,6 +54,8 @@ SIGNATURES = {
     "rta_decode_attention_workspace_bytes": (_sz, [_i, _i, _i, _i, _i]),
     "rta_decode_attention": (_i, [_p, _i, _i, _i, _i, _p, _i, _i, _p, _p, _i64, _i64, _i, _p, _p, _p, _p, _p, _sz,
                                   _p]),
+    "rta_decode_attention_noalloc": (_i, [_p, _i, _i, _i, _i, _p, _i, _i, _p, _p, _i64, _i64, _i, _p, _p, _p, _p,
+                                          _p]),
     # host-only asset reader (rta.asset binds the structs)
     "rta_asset_open": (_i, [ctypes.c_char_p, ctypes.c_char_p, ctypes.POINTER(_p), ctypes.c_char_p, _sz]),
     "rta_asset_close": (None, [_p]),

@@ -170,6 +170,26 @@ def decode_attention(q, packets, fmt_k, fmt_v, slot_base, ctx_len, capacity, max
     return out, m, z
 
 
+def decode_attention_noalloc(q, packets, fmt_k, fmt_v, slot_base, ctx_len, capacity, max_ctx, hkv, gate=None,
+                             out=None):
+    """decode_attention on the library's own scratch (rta_decode_attention_noalloc): no
+    workspace; raises RtaError (status RTA_ERR_SCRATCH) when the call would need more
+    than RTA_NOALLOC_SCRATCH_BYTES."""
+    lib = _lib.load()
+    for t, n in ((q, "q"), (packets, "packets"), (slot_base, "slot_base"), (ctx_len, "ctx_len")):
+        _dev(t, n)
+    nseq, hq, hd = q.shape
+    if out is None:
+        out = torch.empty_like(q)
+    m = torch.empty(nseq, hq, dtype=torch.float32, device=q.device)
+    z = torch.empty(nseq, hq, dtype=torch.float32, device=q.device)
+    n_slots = packets.numel() // history_bytes(hkv * hd)
+    check(lib.rta_decode_attention_noalloc(_ptr(q), nseq, hq, hkv, hd, _ptr(packets), fmt_k, fmt_v, _ptr(slot_base),
+                                           _ptr(ctx_len), capacity, n_slots, max_ctx, _ptr(gate), _ptr(out), _ptr(m),
+                                           _ptr(z), _stream()), "rta_decode_attention_noalloc")
+    return out, m, z
+
+
 def device_error(clear=True):
     """Sticky device error bits (RTA_DEVERR_*); synchronises the device."""
     bits = ctypes.c_uint32(0)
