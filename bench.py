@@ -21,7 +21,9 @@ them from HBM.
 
 roofline.achieved = algorithmic bytes of one launch of the dominant kernel / that
 kernel's mean duration, measured with HIP events recorded on the launching
-stream around individual launches of that kernel.
+stream around a graph of back-to-back launches of that kernel.  For the decode
+step the dominant kernel is the one with the largest share of a step (calls per
+step x mean duration); every timed kernel is listed under "kernels".
 """
 import argparse
 import json
@@ -62,11 +64,12 @@ def parse():
     return ap.parse_args()
 
 
-def traffic_for(workload):
-    """HBM bytes per launch of the dominant kernel, from rocprofv3 --pmc (profiles/traffic.json)."""
+def traffic_for(key):
+    """HBM bytes per launch of a kernel (key: the workload, or the workload and the kernel's
+    short name, "decode/gate/up"), from rocprofv3 --pmc runs (profiles/traffic.json)."""
     f = ROOT / "profiles" / "traffic.json"
     if f.is_file():
-        return json.loads(f.read_text()).get(workload)
+        return json.loads(f.read_text()).get(key)
     return None
 
 
@@ -441,6 +444,59 @@ def w_proj(torch, args, orc):
     return res
 
 
+def step_kernels(torch, shape, batch, dev):
+    """The decode step's readouts and its attention as separate calls of the C ABI, at the
+    step's shapes, each over enough distinct (rotated) weight copies that every call
+    streams its weights from HBM.  Returns [(name, calls per step, alg bytes, launch)]."""
+    from rta import model, ops
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(20261116)
+    D, FF, hq, hkv, hd = shape.hidden, shape.ff, shape.q_heads, shape.kv_heads, shape.head_dim
+    S = shape.rec_heads * hd
+    nfull = shape.layers // shape.full_every
+    nrec = shape.layers - nfull
+    P4, P6 = Q4_K | ops.TILED, Q6_K | ops.TILED
+    qb = lambda fmt, rows, cols: rows * cols // 256 * (144 if fmt == Q4_K else 210)  # noqa: E731
+
+    def copies(fmt, rows, cols, per=1):
+        n = max(2, 3 * CACHE_BYTES // (per * qb(fmt, rows, cols)) + 1)
+        return [[ops.pack(fmt, model.random_kquant(fmt, rows, cols, gen, dev), rows, cols) for _ in range(per)]
+                for _ in range(n)]
+
+    x_d = torch.randn(batch, D, device=dev, generator=gen)
+    x_ff = torch.randn(batch, FF, device=dev, generator=gen) * 0.1
+    act = torch.empty(batch, FF, device=dev)
+    y_d = torch.zeros(batch, D, device=dev)
+    y_in = torch.empty(batch, 4 * S + 2 * shape.rec_heads, device=dev)
+    y_full = torch.empty(batch, (hq + 2 * hkv) * hd, device=dev)
+    ws = torch.empty(max(ops.mlp_workspace_bytes(P4, P4, D, FF, batch),
+                         ops.gemv_workspace_bytes(P4, 4 * S + 2 * shape.rec_heads, D, batch)),
+                     dtype=torch.uint8, device=dev)
+    gu = copies(Q4_K, FF, D, per=2)
+    dn = copies(Q4_K, D, FF)
+    op = copies(Q4_K, D, hq * hd)
+    rin = copies(Q4_K, 4 * S + 2 * shape.rec_heads, D)
+    fin = copies(Q4_K, (hq + 2 * hkv) * hd, D)
+    out = []
+    out.append(("gate/up: gemm_tiled_kernel<Q4_K,SwiGLU> (rta_swiglu, packed 2 x 12288x4096)", shape.layers,
+                2 * qb(Q4_K, FF, D) + 4 * batch * (D + FF),
+                lambda i: ops.swiglu(P4, gu[i % len(gu)][0], gu[i % len(gu)][1], D, FF, x_d, act=act, workspace=ws)))
+    out.append(("down: gemm_tiled_kernel<Q4_K,accumulate> + slab reduce (rta_gemv, packed 4096x12288)", shape.layers,
+                qb(Q4_K, D, FF) + 4 * batch * (FF + 2 * D),
+                lambda i: ops.gemv(P4, dn[i % len(dn)][0], D, FF, x_ff, y=y_d, accumulate=True, workspace=ws)))
+    out.append(("O projection: gemm_tiled_kernel<Q4_K,accumulate> + slab reduce (rta_gemv, packed 4096x4096)",
+                shape.layers, qb(Q4_K, D, hq * hd) + 4 * batch * (hq * hd + 2 * D),
+                lambda i: ops.gemv(P4, op[i % len(op)][0], D, hq * hd, x_d, y=y_d, accumulate=True, workspace=ws)))
+    out.append(("recurrent in-projection: gemm_tiled_kernel<Q4_K,store> + slab reduce (rta_gemv, packed 16448x4096)",
+                nrec, qb(Q4_K, 4 * S + 2 * shape.rec_heads, D) + 4 * batch * (D + 4 * S + 2 * shape.rec_heads),
+                lambda i: ops.gemv(P4, rin[i % len(rin)][0], 4 * S + 2 * shape.rec_heads, D, x_d, y=y_in,
+                                   workspace=ws)))
+    out.append(("full in-projection: gemm_tiled_kernel<Q4_K,store> + slab reduce (rta_gemv, packed 6144x4096)", nfull,
+                qb(Q4_K, (hq + 2 * hkv) * hd, D) + 4 * batch * (D + (hq + 2 * hkv) * hd),
+                lambda i: ops.gemv(P4, fin[i % len(fin)][0], (hq + 2 * hkv) * hd, D, x_d, y=y_full, workspace=ws)))
+    return out
+
+
 def w_decode(torch, args, orc):
     """The 9B-shape hybrid decode step: 32 layers (3 gated delta-net : 1 full attention),
     hidden 4096, 32/8 heads x 128, 32 delta-net heads, FF 12288, Q4_K projections (packed
@@ -452,11 +508,12 @@ def w_decode(torch, args, orc):
     ctx = rng.integers(256, 8193, batch).astype(np.int32)
     capacity = 8192 + 256
     shape = model.shape_9b(capacity, packed=True)
-    m = model.DecodeModel(shape, batch, ctx, seed=20261115)
+    want_cpu = not args.no_cpu and batch == 32
+    m = model.DecodeModel(shape, batch, ctx, seed=20261115, keep_gguf=want_cpu)
     nfull = shape.layers // shape.full_every
     nrec = shape.layers - nfull
-    # the dominant kernel: decode attention of the batch over one full-attention layer's
-    # history, rotated over the 8 layers' distinct histories (8 x 191 MB)
+    # decode attention of the batch over one full-attention layer's history, rotated over
+    # the 8 layers' distinct histories (8 x 383 MB)
     v = m.views
     per_layer = v.slots_per_layer * v.packet_bytes
     p0 = v.packets - m.state.data_ptr()
@@ -476,16 +533,33 @@ def w_decode(torch, args, orc):
         ops.decode_attention(qa, hist_layers[i % nfull], shape.fmt_k, shape.fmt_v, base, ctx_d, capacity, capacity,
                              hkv, workspace=aws, out=oa)
 
+    # the LM head (510 MB, two copies rotate past the cache)
+    lm_copies = [m.lm_head, ops.pack(Q6_K, model.random_kquant(Q6_K, shape.vocab, shape.hidden,
+                                                               torch.Generator(device=dev), dev),
+                                     shape.vocab, shape.hidden)]
+    hn = torch.randn(batch, shape.hidden, device=dev)
+    lg = torch.empty(batch, shape.vocab, device=dev)
+    ids = torch.empty(batch, dtype=torch.int32, device=dev)
+    lws = torch.empty(ops.lm_head_workspace_bytes(Q6_K | ops.TILED, shape.vocab, shape.hidden, batch),
+                      dtype=torch.uint8, device=dev)
+
+    def lm_head(i):
+        ops.lm_head(Q6_K | ops.TILED, lm_copies[i % 2], shape.vocab, shape.hidden, hn, workspace=lws, logits=lg,
+                    ids=ids)
+
     w_bytes = m.weight_bytes() - m.lm_head.numel()                       # projections + small vectors
     sum_ctx = int(sum(min(int(c), capacity) for c in ctx))
     hist = sum_ctx * nfull * v.packet_bytes                             # history read per step (approx.)
     state = 2 * nrec * batch * shape.rec_heads * 128 * 128 * 4          # recurrent state read + write
     step_bytes = w_bytes + m.lm_head.numel() + hist + state
-    alg_k = sum_ctx * v.packet_bytes + 2 * batch * hq * hd * 4
-    res = {"alg_bytes": step_bytes, "alg_bytes_kernel": alg_k, "graph_per_step": True,
-           "kernel": f"attn_qprep_kernel (with the tile-list plan) + attn_chunk_mma_kernel<G=4,KPW=2> + attn_merge_kernel (one layer: {batch} sequences, "
-                     f"{hq}/{hkv} heads, {sum_ctx} positions of {v.packet_bytes}-byte K/V packets)",
-           "step": step, "kernel_launch": attention, "unit": "tok/s", "value_from_ms": lambda ms: batch / (ms * 1e-3),
+    kernels = step_kernels(torch, shape, batch, dev) if batch == 32 else []
+    kernels.append((f"attention: attn_qprep_kernel + attn_chunk_mma_kernel<G=4,KPW=2> + attn_merge_kernel ({batch} "
+                    f"sequences, {hq}/{hkv} heads, {sum_ctx} positions of {v.packet_bytes}-byte packets)", nfull,
+                    sum_ctx * v.packet_bytes + 2 * batch * hq * hd * 4, attention))
+    kernels.append(("LM head: gemm_tiled_kernel<Q6_K,logits> + argmax_margin_kernel (rta_lm_head, packed "
+                    "151936x4096)", 1, m.lm_head.numel() + 4 * batch * (shape.hidden + shape.vocab), lm_head))
+    res = {"alg_bytes": step_bytes, "graph_per_step": True, "kernels": kernels,
+           "step": step, "unit": "tok/s", "value_from_ms": lambda ms: batch / (ms * 1e-3),
            "dtype": "q4_k/q6_k weights x fp32 activations and state, fp32 accumulate",
            "config": {"workload": f"9B-shape hybrid decode step, batch {batch} (32 layers: 24 gated delta-net + 8 "
                                   "full attention; hidden 4096, 32/8 heads x 128, FF 12288, Q4_K projections, "
@@ -494,28 +568,46 @@ def w_decode(torch, args, orc):
                       "sum_context": int(ctx.sum()), "history_capacity": capacity,
                       "bytes_per_step": int(step_bytes), "weight_bytes_per_step": int(w_bytes + m.lm_head.numel()),
                       "seed": "20261110+5"}}
+    snap = {}
 
     def check():
+        # the state before this step, for the CPU step that runs from the same point
+        if want_cpu:
+            snap.update(rec=np.ascontiguousarray(m.state_view("recurrent")),
+                        conv=np.ascontiguousarray(m.state_view("conv")),
+                        packets=np.ascontiguousarray(m.state_view("packets")), ctx=m.state_view("ctx"),
+                        tokens=m.tokens.cpu().numpy().view(np.uint32).copy())
         m.step(logits=True)
-        lg = m.logits.cpu().numpy()
+        lgt = m.logits.cpu().numpy()
         toks = m.tokens.cpu().numpy().view(np.uint32)
-        ok = bool(np.isfinite(lg).all()) and all(int(toks[b]) == orc.argmax_margin_f32(lg[b], 1e-4)
-                                                 for b in range(batch))
-        return {"tokens_follow_margin_rule": ok, "logits_finite": bool(np.isfinite(lg).all()), "ok": ok,
-                "note": "end-to-end step parity vs the fp64 oracle: tests/test_gpu_model.py (small shape)"}
+        snap.update(gpu_logits=lgt.copy(), gpu_tokens=toks.copy())
+        ok = bool(np.isfinite(lgt).all()) and all(int(toks[b]) == orc.argmax_margin_f32(lgt[b], 1e-4)
+                                                  for b in range(batch))
+        return {"tokens_follow_margin_rule": ok, "logits_finite": bool(np.isfinite(lgt).all()), "ok": ok,
+                "note": "the 9B step at 4 layers against the fp64 composition: tests/test_gpu_sizes.py; "
+                        "cpu_baseline.parity: this step against the fp32 CPU step from the same state"}
 
     def cpu(seconds):
-        from rta import synth
         t = omp_threads()
-        rows = 1024
-        wq = synth.random_matrix(np.random.default_rng(3), Q4_K, rows, 4096)
-        xs = np.random.default_rng(4).standard_normal((batch, 4096)).astype(np.float32)
-        n, el = cpu_time(lambda: orc.gemv_f32(Q4_K, wq, rows, 4096, xs, t), seconds)
-        gbs = wq.nbytes * n / el / 1e9
-        return {"value": batch / (step_bytes / (gbs * 1e9)), "unit": "tok/s", "cores": t, "kind": "port",
-                "sample": f"{n} calls of the oracle's fp32 OpenMP Q4_K projection {rows}x4096 at batch {batch} "
-                          f"({gbs:.2f} GB/s of weights) in {el:.1f} s on {cpu_model()}, scaled to the step's "
-                          f"{step_bytes / 1e9:.2f} GB"}
+        cs = orc.CpuStep(shape, m.gguf)
+        st = {k: snap[k].copy() for k in ("rec", "conv", "packets", "ctx", "tokens")}
+        lg_cpu = np.empty((batch, shape.vocab), np.float32)
+        n, t0 = 0, time.perf_counter()
+        while True:
+            cs.step(batch, st["rec"], st["conv"], st["packets"], st["ctx"], st["tokens"],
+                    lg_cpu if n == 0 else None, threads=t)
+            if n == 0:
+                par = close(snap["gpu_logits"], lg_cpu)
+                same = int(np.sum(st["tokens"] == snap["gpu_tokens"]))
+            n += 1
+            el = time.perf_counter() - t0
+            if el >= seconds:
+                break
+        return {"value": batch * n / el, "unit": "tok/s", "cores": t, "kind": "port",
+                "sample": f"{n} whole decode step(s) of the 9B shape at batch {batch} (all 32 layers, LM head and "
+                          f"argmax) by the oracle's fp32 OpenMP CPU step (oracle/rta_cpu_step.c, -O3 AVX2/FMA) "
+                          f"in {el:.1f} s on {t} threads of {cpu_model()}",
+                "parity": {"logits_vs_gpu_step": par, "tokens_equal": f"{same}/{batch}"}}
     res["check"], res["cpu"] = check, cpu
     return res
 
@@ -583,13 +675,28 @@ def main():
         args.warmup = 4 if args.workload == "decode" else 100
     wl = WORKLOADS[args.workload](torch, args, orc)
     parity = wl["check"]()
-    k_mean = time_kernel(torch, wl["kernel_launch"])
     if wl.get("graph_per_step") and not args.eager:
         ms = timed_replays(torch, wl["step"], args.steps, args.warmup)
     else:
         ms = timed_region(torch, wl["step"], args.steps, args.warmup, args.eager)
     ms_step = ms / args.steps
-    alg_k = wl.get("alg_bytes_kernel", wl["alg_bytes"])
+    # the dominant kernel: the one with the largest share of a step (calls per step x mean
+    # duration) when the workload lists several, else the workload's own
+    table = []
+    for name, calls, alg, launch in wl.get("kernels", []):
+        km = time_kernel(torch, launch)
+        ach = alg / (km * 1e-3) / 1e9
+        key = f"{args.workload}/{name.split(':')[0]}"
+        table.append({"kernel": name, "calls_per_step": calls, "ms_mean": km, "alg_bytes": alg,
+                      "achieved_gbs": ach, "frac": ach / HBM_PEAK_GBS, "ms_per_step": calls * km,
+                      "traffic": traffic_for(key)})
+    if table:
+        dom = max(table, key=lambda r: r["ms_per_step"])
+        kernel_name, k_mean, alg_k, traffic = dom["kernel"], dom["ms_mean"], dom["alg_bytes"], dom["traffic"]
+    else:
+        k_mean = time_kernel(torch, wl["kernel_launch"])
+        kernel_name, alg_k = wl["kernel"], wl.get("alg_bytes_kernel", wl["alg_bytes"])
+        traffic = traffic_for(args.workload)
     achieved = alg_k / (k_mean * 1e-3) / 1e9
     cpu = None if (args.no_cpu or wl["cpu"] is None) else wl["cpu"](args.cpu_seconds)
     line = {"metric": METRIC, "value": wl["value_from_ms"](ms_step), "unit": wl["unit"], "n_gpus": 1,
@@ -600,9 +707,11 @@ def main():
                                                             "one HIP graph replay of all steps"),
             "config": wl["config"],
             "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                         "frac": achieved / HBM_PEAK_GBS, "traffic": traffic_for(args.workload)},
-            "cpu_baseline": cpu, "kernel": wl["kernel"], "kernel_ms_mean": k_mean,
+                         "frac": achieved / HBM_PEAK_GBS, "traffic": traffic},
+            "cpu_baseline": cpu, "kernel": kernel_name, "kernel_ms_mean": k_mean,
             "alg_bytes_per_launch": alg_k, "alg_bytes_per_step": wl["alg_bytes"], "parity": parity}
+    if table:
+        line["kernels"] = table
     if args.workload == "decode" and not args.no_companions:
         line["companions"] = companions(torch, args, orc)
     print(json.dumps(line), flush=True)

@@ -114,6 +114,14 @@ int rta_mlp_swiglu(int fmt_g, const void* wg, int fmt_u, const void* wu,
                    const float* x, int batch, float* act, float* y, int epilogue,
                    void* workspace, size_t workspace_bytes, rta_stream_t stream);
 
+/* The fused gate/up stage alone: act = sign(g) sign(u) |g| |u| sigmoid(g), g = Wg x,
+ * u = Wu x ([batch, inter]), both matrices streamed in one pass.  Workspace:
+ * rta_mlp_workspace_bytes(fmt, fmt, hidden, inter, batch).  Replaces op 2 index 3
+ * (resident_math.comp:54-58,71) as Resident::executeMLP launches it
+ * (optical_resident.cpp:484-491). */
+int rta_swiglu(int fmt, const void* wg, const void* wu, int hidden, int inter, const float* x, int batch,
+               float* act, void* workspace, size_t workspace_bytes, rta_stream_t stream);
+
 /* LM-head vocabulary readout with fused argmax.
  *   logits[b, v] = sum_k W[v, k] h[b, k]   (fp32, all v < vocab)
  *   ids[b] = lowest v with logits[b, v] >= M - margin*|M|, M = max_v logits[b, v]

@@ -591,6 +591,21 @@ int rta_mlp_swiglu(int fmt_g, const void* wg, int fmt_u, const void* wu, int fmt
                                        workspace, workspace_bytes, s);
 }
 
+int rta_swiglu(int fmt, const void* wg, const void* wu, int hidden, int inter, const float* x, int batch, float* act,
+               void* workspace, size_t workspace_bytes, rta_stream_t stream) {
+    int rc = check_matrix(fmt, wg, inter, hidden);
+    if (rc) return rc;
+    if ((rc = check_matrix(fmt, wu, inter, hidden))) return rc;
+    if (!x || !act) return RTA_ERR_NULL;
+    if (batch <= 0) return RTA_ERR_SHAPE;
+    if (reinterpret_cast<uintptr_t>(x) % 16 || reinterpret_cast<uintptr_t>(act) % 16 ||
+        reinterpret_cast<uintptr_t>(workspace) % 256)
+        return RTA_ERR_ALIGN;
+    if (workspace_bytes < rta_mlp_workspace_bytes(fmt, fmt, hidden, inter, batch)) return RTA_ERR_WORKSPACE;
+    return run_projection<kSwiglu>(fmt, wg, wu, inter, hidden, x, batch, act, nullptr, nullptr, nullptr, workspace,
+                                   workspace_bytes, (hipStream_t)stream);
+}
+
 size_t rta_lm_head_workspace_bytes(int fmt, int vocab, int hidden, int batch) {
     if (vocab <= 0 || hidden <= 0 || batch <= 0 || !(host::valid_format(fmt) || is_tiled(fmt))) return 0;
     // per-task maxima [batch][vocab] (upper bound), then the matrix-core scratch of one tile

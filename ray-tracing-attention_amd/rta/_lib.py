@@ -47,6 +47,7 @@ SIGNATURES = {
     "rta_gemv": (_i, [_i, _p, _i, _i, _p, _i, _p, _i, _p, _sz, _p]),
     "rta_mlp_workspace_bytes": (_sz, [_i, _i, _i, _i, _i]),
     "rta_mlp_swiglu": (_i, [_i, _p, _i, _p, _i, _p, _i, _i, _p, _i, _p, _p, _i, _p, _sz, _p]),
+    "rta_swiglu": (_i, [_i, _p, _p, _i, _i, _p, _i, _p, _p, _sz, _p]),
     "rta_lm_head_workspace_bytes": (_sz, [_i, _i, _i, _i]),
     "rta_lm_head": (_i, [_i, _p, _i, _i, _p, _i, _f, _p, _p, _p, _sz, _p]),
     "rta_rope": (_i, [_p, _i, _i, _i, _i, _p, _d, _p]),

@@ -113,6 +113,21 @@ def mlp_swiglu(fmts, wg, wu, wd, hidden, inter, x, y=None, accumulate=False, act
     return act, y
 
 
+def swiglu(fmt, wg, wu, hidden, inter, x, act=None, workspace=None):
+    """The fused gate/up stage alone (op 2 index 3): act = swiglu(Wg x, Wu x) [batch, inter]."""
+    lib = _lib.load()
+    for t, n in ((wg, "wg"), (wu, "wu"), (x, "x")):
+        _dev(t, n)
+    batch = x.shape[0]
+    if act is None:
+        act = torch.empty(batch, inter, dtype=torch.float32, device=x.device)
+    need = mlp_workspace_bytes(fmt, fmt, hidden, inter, batch)
+    ws = _workspace(need, x.device, workspace)
+    check(lib.rta_swiglu(fmt, _ptr(wg), _ptr(wu), hidden, inter, _ptr(x), batch, _ptr(act), _ptr(ws), ws.numel(),
+                         _stream()), "rta_swiglu")
+    return act
+
+
 def lm_head_workspace_bytes(fmt, vocab, hidden, batch):
     return int(_lib.load().rta_lm_head_workspace_bytes(fmt, vocab, hidden, batch))
 

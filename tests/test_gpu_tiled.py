@@ -167,3 +167,30 @@ def test_tiled_lm_head_parity(torch_dev, vocab, hidden, batch):
     for b in range(batch):
         assert_close(logits[b], ref[b], f"logits row {b}")
         assert int(ids[b]) == orc.argmax_margin_f32(logits[b], 1e-4), b
+
+
+@pytest.mark.parametrize("packed", [False, True])
+@pytest.mark.parametrize("batch", [1, 5, 32])
+def test_swiglu_stage_alone(torch_dev, packed, batch):
+    """rta_swiglu (the fused gate/up stage) equals rta_mlp_swiglu's activation bit for bit
+    and meets the oracle's bar."""
+    torch, dev = torch_dev
+    hidden, inter = 4096, 1536
+    rng = np.random.default_rng(20261130 + batch)
+    wg, wu = (synth.random_matrix(rng, orc.Q4_K, inter, hidden) for _ in range(2))
+    wd = synth.random_matrix(rng, orc.Q4_K, hidden, inter)
+    x = rng.standard_normal((batch, hidden)).astype(np.float32)
+    dg, du, dd = (to_dev(torch, w, dev) for w in (wg, wu, wd))
+    f = orc.Q4_K
+    if packed:
+        dg, du, dd = ops.pack(f, dg, inter, hidden), ops.pack(f, du, inter, hidden), ops.pack(f, dd, hidden, inter)
+        f |= TILED
+    xd = to_dev(torch, x, dev)
+    act = ops.swiglu(f, dg, du, hidden, inter, xd)
+    act_mlp, _ = ops.mlp_swiglu((f, f, f), dg, du, dd, hidden, inter, xd)
+    assert torch.equal(act, act_mlp)
+    ract, _ = orc.mlp_swiglu((orc.Q4_K, orc.Q4_K, orc.Q4_K), wg, wu, wd, hidden, inter, x)
+    act = act.cpu().numpy()
+    for b in range(batch):
+        assert_close(act[b], ract[b], f"activation row {b}")
+
