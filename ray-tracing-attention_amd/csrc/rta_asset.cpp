@@ -183,7 +183,8 @@ extern "C" int rta_asset_vector(const rta_asset* a, int layer, int field, uint64
         return RTA_ERR_RANGE;
     const uint32_t base = layer < 0 ? 0u : kModelWords + (uint32_t)layer * kLayerWords;
     const uint64_t off = a->params[base + (uint32_t)field];
-    if (off + count > a->params.size()) return RTA_ERR_RANGE;
+    const uint64_t words = a->params.size();
+    if (off > words || count > words - off) return RTA_ERR_RANGE;   // no wrap for any count
     *out = reinterpret_cast<const float*>(a->params.data() + off);
     return RTA_OK;
 }

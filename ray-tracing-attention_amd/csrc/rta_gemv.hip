@@ -559,6 +559,8 @@ int rta_gemv(int fmt, const void* w, int rows, int cols, const float* x, int bat
 
 size_t rta_mlp_workspace_bytes(int fmt_g, int fmt_d, int hidden, int inter, int batch) {
     if (hidden <= 0 || inter <= 0 || batch <= 0) return 0;
+    if (((is_kquant(fmt_g) || is_tiled(fmt_g)) && hidden % 256) || ((is_kquant(fmt_d) || is_tiled(fmt_d)) && inter % 256))
+        return 0;
     const int tile = batch < kMaxBatchTile ? batch : kMaxBatchTile;
     const size_t a = projection_ws(fmt_g, inter, hidden, tile, true);
     const size_t b = projection_ws(fmt_d, hidden, inter, tile, false);
@@ -608,6 +610,7 @@ int rta_swiglu(int fmt, const void* wg, const void* wu, int hidden, int inter, c
 
 size_t rta_lm_head_workspace_bytes(int fmt, int vocab, int hidden, int batch) {
     if (vocab <= 0 || hidden <= 0 || batch <= 0 || !(host::valid_format(fmt) || is_tiled(fmt))) return 0;
+    if ((is_kquant(fmt) || is_tiled(fmt)) && hidden % 256) return 0;
     // per-task maxima [batch][vocab] (upper bound), then the matrix-core scratch of one tile
     const size_t maxima = ((size_t)vocab * (size_t)batch * sizeof(float) + 255) & ~(size_t)255;
     return maxima + projection_ws(fmt, vocab, hidden, batch < kMaxBatchTile ? batch : kMaxBatchTile, false);

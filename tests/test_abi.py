@@ -64,6 +64,13 @@ def test_host_queries(lib):
     assert lib.rta_pack_bytes(_lib.Q4_K, 8, 100) == -1
     assert lib.rta_pack_bytes(_lib.F16, 8, 256) == -1
     assert lib.rta_gemv_workspace_bytes(_lib.Q4_K | _lib.TILED, 4096, 4096, 1) > 0   # matrix cores at any batch
+    # size queries answer 0 for shapes the K-quant formats cannot hold (no division by zero)
+    T = _lib.TILED
+    assert lib.rta_mlp_workspace_bytes(_lib.Q4_K | T, _lib.Q4_K | T, 512, 37, 32) == 0
+    assert lib.rta_mlp_workspace_bytes(_lib.Q4_K | T, _lib.Q4_K | T, 300, 512, 32) == 0
+    assert lib.rta_lm_head_workspace_bytes(_lib.Q6_K | T, 1000, 300, 1) == 0
+    assert lib.rta_lm_head_workspace_bytes(_lib.Q6_K, 1000, 100, 1) == 0
+    assert lib.rta_gemv_workspace_bytes(_lib.Q6_K | T, 300, 100, 32) == 0
 
 
 def test_argument_errors_are_reported_before_launch(lib):

@@ -93,6 +93,9 @@ def test_out_of_range_requests(tmp_path):
             a.matrix(0, 9, 16)
         with pytest.raises(Exception):
             a.vector(0, 0, a.info.param_words + 1)
+        for count in (2 ** 64 - 1, 2 ** 64 - 8, 2 ** 63):     # off + count would wrap past the check
+            with pytest.raises(Exception, match="rta_asset_vector"):
+                a.vector(0, 0, count)
         with pytest.raises(ValueError, match="Truncated geometric weights"):
             a.matrix(0, ra.FFN_GATE, 1 << 30)
 
