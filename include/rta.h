@@ -101,6 +101,46 @@ int rta_gemv(int fmt, const void* w, int rows, int cols, const float* x, int bat
              float* y, int epilogue, void* workspace, size_t workspace_bytes,
              rta_stream_t stream);
 
+/* Row/axis remap of a projection matrix: the descriptor mode (metadata >> 8) of
+ * quantizedWeight / quantizedOctet, resident_quant.glsl:20-31,53-58, as
+ * compiler/export.py:96-98,108 assigns it.  Logical row r reads GGUF row src(r),
+ * logical axis a reads GGUF column src(a), with rot(i) = i < R ? (i % 2)(R / 2) + i / 2
+ * : i (originalRotaryAxis, resident_quant.glsl:20), hd = head_dim, R = rotary_dim:
+ *   RTA_REMAP_QUERY      1  src(r) = (r / hd) 2 hd + rot(r % hd)       (Q of Q|gate rows)
+ *   RTA_REMAP_GATE       2  src(r) = (r / hd) 2 hd + hd + rot(r % hd)  (its gate)
+ *   RTA_REMAP_ROTARY     3  src(r) = (r / hd) hd + rot(r % hd)         (Q / K / V rows)
+ *   RTA_REMAP_AXES       4  src(a) = (a / hd) hd + rot(a % hd)         (O columns)
+ *   RTA_REMAP_KEY_REPEAT 5  src(r) = r % key_rows                      (recurrent q / k)
+ * head_dim > 0; 0 <= rotary_dim <= head_dim, even; key_rows > 0 for mode 5. */
+enum rta_remap_mode {
+    RTA_REMAP_NONE = 0, RTA_REMAP_QUERY = 1, RTA_REMAP_GATE = 2, RTA_REMAP_ROTARY = 3,
+    RTA_REMAP_AXES = 4, RTA_REMAP_KEY_REPEAT = 5
+};
+typedef struct rta_remap { int mode, head_dim, rotary_dim, key_rows; } rta_remap;
+
+/* rta_gemv over the remapped matrix: y[b, r] (=|+=) sum_a W[src(r), src(a)] x[b, a],
+ * r < rows, a < cols, for a GGUF (or rta_pack-ed, fmt | RTA_TILED) matrix w of
+ * src_rows rows.  Modes 1-3 need rows % head_dim == 0 and src_rows >= 2 rows (1, 2)
+ * or rows (3); mode 4 cols % head_dim == 0; mode 5 src_rows >= min(rows, key_rows).
+ * Row modes read each source row once into the workspace and gather the rows;
+ * mode 4 permutes x into the workspace.  Workspace: rta_gemv_remap_workspace_bytes().
+ * Replaces op 2 with a descriptor mode != 0 (resident_math.comp:39-75 reading
+ * through quantizedOctet, resident_quant.glsl:44-58). */
+size_t rta_gemv_remap_workspace_bytes(int fmt, const rta_remap* remap, int rows, int cols, int batch);
+int rta_gemv_remap(int fmt, const void* w, int src_rows, int rows, int cols, const rta_remap* remap,
+                   const float* x, int batch, float* y, int epilogue, void* workspace,
+                   size_t workspace_bytes, rta_stream_t stream);
+
+/* rta_pack of the row-remapped matrix: tile rows are the logical rows r < rows, read
+ * from GGUF row src(r) of src (src_rows rows); modes 0, 1, 2, 3, 5 (mode 4 moves
+ * columns inside superblocks, which no repacking can express: use rta_gemv_remap
+ * on the packed matrix).  dst: rta_pack_bytes(fmt, rows, cols) bytes.  A packed
+ * matrix of several parts (Q | gate | K | V) is packed part by part at row offsets
+ * that are multiples of 16: part p starts rta_pack_bytes(fmt, offset_p, cols) bytes
+ * into dst.  The remap is then free at run time.  No reference counterpart. */
+int rta_pack_remap(int fmt, const void* src, int src_rows, int cols, const rta_remap* remap, int rows,
+                   void* dst, rta_stream_t stream);
+
 /* SwiGLU MLP: act = sign(g) sign(u) |g| |u| sigmoid(g) with g = Wg x, u = Wu x
  * ([batch, inter]); then y (=|+=) Wd act ([batch, hidden]).
  *   Wg, Wu: [inter, hidden] (one format); Wd: [hidden, inter].

@@ -23,6 +23,10 @@ _SIG = {
     "orc_dequant": (_i, [_i, _p, _i64, _p]),
     "orc_gemv_f64": (_i, [_i, _p, _i, _i, _p, _i, _p]),
     "orc_gemv_f32": (_i, [_i, _p, _i, _i, _p, _i, _p, _i]),
+    "orc_rotary_source": (_i64, [_i64, _i]),
+    "orc_remap_row": (_i64, [_i, _i, _i, _i, _i64]),
+    "orc_remap_axis": (_i64, [_i, _i, _i, _i64]),
+    "orc_gemv_remap_f64": (_i, [_i, _p, _i, _i, _i, _i, _i, _i, _i, _p, _i, _p]),
     "orc_sigmoid": (_d, [_d]),
     "orc_mlp_swiglu": (_i, [_i, _p, _i, _p, _i, _p, _i, _i, _p, _i, _p, _p, _p]),
     "orc_argmax_margin_f32": (ctypes.c_uint32, [_p, _i64, _f]),
@@ -82,6 +86,23 @@ def gemv_f64(fmt, w, rows, cols, x):
     y = np.empty((x.shape[0], rows), dtype=np.float64)
     assert lib().orc_gemv_f64(fmt, _p_(w), rows, cols, _p_(x), x.shape[0], _p_(y)) == 0
     return y
+
+
+def gemv_remap_f64(fmt, w, src_rows, rows, cols, mode, hd, rotary, key_rows, x):
+    w, x = _c(w, np.uint8), _c(x, np.float32).reshape(-1, cols)
+    y = np.empty((x.shape[0], rows), dtype=np.float64)
+    rc = lib().orc_gemv_remap_f64(fmt, _p_(w), src_rows, rows, cols, mode, hd, rotary, key_rows, _p_(x),
+                                  x.shape[0], _p_(y))
+    assert rc == 0, rc
+    return y
+
+
+def remap_row(mode, hd, rotary, key_rows, row):
+    return int(lib().orc_remap_row(mode, hd, rotary, key_rows, row))
+
+
+def remap_axis(mode, hd, rotary, axis):
+    return int(lib().orc_remap_axis(mode, hd, rotary, axis))
 
 
 def gemv_f32(fmt, w, rows, cols, x, threads=0):

@@ -136,6 +136,53 @@ int orc_gemv_f64(int fmt, const void* W, int rows, int cols, const float* x, int
     return 0;
 }
 
+/* ---- row / axis remap (resident_quant.glsl:20-31 quantizedWeight; the mode is the
+ * descriptor's metadata >> 8, assigned by compiler/export.py:96-98,108) ---------- */
+/* originalRotaryAxis, resident_quant.glsl:20 */
+int64_t orc_rotary_source(int64_t axis, int rotary) {
+    return axis < rotary ? (axis % 2) * (rotary / 2) + axis / 2 : axis;
+}
+
+/* resident_quant.glsl:23-26: the row a detector row reads (modes 1, 2, 3, 5) */
+int64_t orc_remap_row(int mode, int hd, int rotary, int key_rows, int64_t row) {
+    if (mode == 1 || mode == 2)
+        return (row / hd) * (2 * (int64_t)hd) + (mode == 2 ? hd : 0) + orc_rotary_source(row % hd, rotary);
+    if (mode == 3) return (row / hd) * hd + orc_rotary_source(row % hd, rotary);
+    if (mode == 5) return row % key_rows;
+    return row;
+}
+
+/* resident_quant.glsl:25: the column a detector axis reads (mode 4) */
+int64_t orc_remap_axis(int mode, int hd, int rotary, int64_t axis) {
+    return mode == 4 ? (axis / hd) * hd + orc_rotary_source(axis % hd, rotary) : axis;
+}
+
+/* y[b, r] = sum_a quantizedWeight(row r, axis a) x[b, a] in fp64, each weight taken
+ * from the remapped (row, axis) of W (src_rows rows) as resident_quant.glsl:27-30 does. */
+int orc_gemv_remap_f64(int fmt, const void* W, int src_rows, int rows, int cols, int mode, int hd, int rotary,
+                       int key_rows, const float* x, int batch, double* y) {
+    if (!W || !x || !y || batch <= 0 || !valid_shape(fmt, src_rows, cols) || rows <= 0) return 1;
+    if (mode < 0 || mode > 5 || (mode >= 1 && mode <= 4 && (hd <= 0 || rotary < 0 || rotary > hd)) ||
+        (mode == 5 && key_rows <= 0) || (mode == 4 && cols % hd))
+        return 2;
+    for (int r = 0; r < rows; ++r) {
+        int64_t sr = orc_remap_row(mode, hd, rotary, key_rows, r);
+        if (sr < 0 || sr >= src_rows) return 3;
+    }
+    int64_t rb = orc_row_bytes(fmt, cols);
+    float* w = (float*)malloc((size_t)cols * sizeof(float));
+    for (int r = 0; r < rows; ++r) {
+        orc_dequant(fmt, (const uint8_t*)W + orc_remap_row(mode, hd, rotary, key_rows, r) * rb, cols, w);
+        for (int b = 0; b < batch; ++b) {
+            double acc = 0.0; const float* xb = x + (int64_t)b * cols;
+            for (int a = 0; a < cols; ++a) acc += (double)w[orc_remap_axis(mode, hd, rotary, a)] * (double)xb[a];
+            y[(int64_t)b * rows + r] = acc;
+        }
+    }
+    free(w);
+    return 0;
+}
+
 int orc_gemv_f32(int fmt, const void* W, int rows, int cols, const float* x, int batch, float* y, int threads) {
     if (!W || !x || !y || batch <= 0 || !valid_shape(fmt, rows, cols)) return 1;
     int64_t rb = orc_row_bytes(fmt, cols);

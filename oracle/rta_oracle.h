@@ -38,6 +38,12 @@ int orc_gemv_f64(int fmt, const void* W, int rows, int cols,
 
 /* Same contraction, fp32 accumulation, OpenMP over rows: the timed CPU baseline
  * (dequant + dot as resident_math.comp:39-75 does per output channel). */
+/* row / axis remap of a projection (resident_quant.glsl:20-31) */
+int64_t orc_rotary_source(int64_t axis, int rotary);
+int64_t orc_remap_row(int mode, int hd, int rotary, int key_rows, int64_t row);
+int64_t orc_remap_axis(int mode, int hd, int rotary, int64_t axis);
+int orc_gemv_remap_f64(int fmt, const void* W, int src_rows, int rows, int cols, int mode, int hd, int rotary,
+                       int key_rows, const float* x, int batch, double* y);
 int orc_gemv_f32(int fmt, const void* W, int rows, int cols,
                  const float* x, int batch, float* y, int threads);
 

@@ -5,6 +5,7 @@
 #include <climits>
 #include "rta_gemm.hpp"
 #include "rta_tiled.hpp"
+#include "rta_remap.hpp"
 #include "rta_gemv.hpp"
 #include "rta_host.hpp"
 #include "rta_internal.hpp"
@@ -80,6 +81,30 @@ __global__ void __launch_bounds__(256) argmax_margin_kernel(const float* __restr
 }
 
 // ----------------------------------------------------------- launch plumbing ----
+// y[b, r] (=|+=) ys[b, m.source_row(r)]: the gather epilogue of a row-remapped
+// projection, ys [batch, ld] holding the readout of every source row once.
+template <bool ACC>
+__global__ void __launch_bounds__(256) remap_gather_kernel(const float* __restrict__ ys, int ld, int rows, int batch,
+                                                           const Remap m, float* __restrict__ y) {
+    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (i >= (int64_t)rows * batch) return;
+    const int64_t b = i / rows, r = i - b * rows;
+    const float v = ys[b * ld + m.source_row(r)];
+    if (ACC) y[i] += v;
+    else y[i] = v;
+}
+
+// xp[b, j] = x[b, a] for the logical axis a whose source column is j (mode 4):
+// sum_a W[r, src(a)] x[a] = sum_j W[r, j] xp[j].
+__global__ void __launch_bounds__(256) remap_axes_kernel(const float* __restrict__ x, int cols, int batch,
+                                                         const Remap m, float* __restrict__ xp) {
+    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (i >= (int64_t)cols * batch) return;
+    const int64_t b = i / cols;
+    const int j = (int)(i - b * cols), h = j / m.hd;
+    xp[i] = x[b * cols + (int64_t)h * m.hd + m.rot_inv(j - h * m.hd)];
+}
+
 static int pow2ceil(int v) {
     int p = 1;
     while (p < v) p <<= 1;
@@ -478,6 +503,34 @@ int projection_store(int fmt, const void* w, int rows, int cols, const float* x,
                                   0, rn);
 }
 
+// Validates a remap against the matrix and gives the source rows one readout covers
+// (rows of ys for the row modes).
+static int check_remap(const rta_remap* rp, int src_rows, int rows, int cols, Remap* m, int* need) {
+    if (!rp) return RTA_ERR_NULL;
+    if (rp->mode < RTA_REMAP_NONE || rp->mode > RTA_REMAP_KEY_REPEAT) return RTA_ERR_RANGE;
+    Remap r;
+    r.mode = rp->mode;
+    r.hd = rp->head_dim;
+    r.rotary = rp->rotary_dim;
+    r.key_rows = rp->key_rows;
+    if (rows <= 0 || cols <= 0 || src_rows <= 0) return RTA_ERR_SHAPE;
+    int64_t n = rows;
+    if (r.mode >= RTA_REMAP_QUERY && r.mode <= RTA_REMAP_AXES) {
+        if (r.hd <= 0 || r.rotary < 0 || r.rotary > r.hd || r.rotary % 2) return RTA_ERR_RANGE;
+        if (r.mode == RTA_REMAP_AXES ? cols % r.hd : rows % r.hd) return RTA_ERR_SHAPE;
+        if (r.mode == RTA_REMAP_QUERY || r.mode == RTA_REMAP_GATE) n = 2 * (int64_t)rows;
+    } else if (r.mode == RTA_REMAP_KEY_REPEAT) {
+        if (r.key_rows <= 0) return RTA_ERR_RANGE;
+        n = rows < r.key_rows ? rows : r.key_rows;
+    }
+    if (n > src_rows) return RTA_ERR_SHAPE;
+    *m = r;
+    *need = (int)n;
+    return RTA_OK;
+}
+
+static size_t floats256(int64_t n) { return ((size_t)n * sizeof(float) + 255) & ~(size_t)255; }
+
 }  // namespace rta
 
 using namespace rta;
@@ -555,6 +608,60 @@ int rta_gemv(int fmt, const void* w, int rows, int cols, const float* x, int bat
                                       workspace_bytes, s);
     return run_projection<kAccumulate>(fmt, w, nullptr, rows, cols, x, batch, y, nullptr, nullptr, nullptr, workspace,
                                        workspace_bytes, s);
+}
+
+size_t rta_gemv_remap_workspace_bytes(int fmt, const rta_remap* remap, int rows, int cols, int batch) {
+    Remap m;
+    int need = 0;
+    if (batch <= 0 || check_remap(remap, INT_MAX, rows, cols, &m, &need)) return 0;
+    const size_t inner = rta_gemv_workspace_bytes(fmt, need, cols, batch);
+    if (m.mode == RTA_REMAP_NONE) return inner;
+    if ((is_kquant(fmt) || is_tiled(fmt)) && cols % 256) return 0;
+    return (m.moves_rows() ? floats256((int64_t)batch * need) : floats256((int64_t)batch * cols)) + inner;
+}
+
+int rta_gemv_remap(int fmt, const void* w, int src_rows, int rows, int cols, const rta_remap* remap, const float* x,
+                   int batch, float* y, int epilogue, void* workspace, size_t workspace_bytes, rta_stream_t stream) {
+    Remap m;
+    int need = 0;
+    int rc = check_remap(remap, src_rows, rows, cols, &m, &need);
+    if (rc) return rc;
+    if (m.mode == RTA_REMAP_NONE)
+        return rta_gemv(fmt, w, rows, cols, x, batch, y, epilogue, workspace, workspace_bytes, stream);
+    rc = check_matrix(fmt, w, need, cols);
+    if (rc) return rc;
+    if (!x || !y) return RTA_ERR_NULL;
+    if (batch <= 0) return RTA_ERR_SHAPE;
+    if (epilogue != RTA_EPI_STORE && epilogue != RTA_EPI_ACCUMULATE) return RTA_ERR_RANGE;
+    if (reinterpret_cast<uintptr_t>(x) % 16 || reinterpret_cast<uintptr_t>(y) % 4 ||
+        reinterpret_cast<uintptr_t>(workspace) % 256)
+        return RTA_ERR_ALIGN;
+    if (workspace_bytes < rta_gemv_remap_workspace_bytes(fmt, remap, rows, cols, batch)) return RTA_ERR_WORKSPACE;
+    if (!workspace) return RTA_ERR_WORKSPACE;
+    hipStream_t s = (hipStream_t)stream;
+    uint8_t* ws = static_cast<uint8_t*>(workspace);
+    if (!m.moves_rows()) {   // mode 4: the permuted x, then the plain readout with the caller's epilogue
+        float* xp = reinterpret_cast<float*>(ws);
+        const size_t xb = floats256((int64_t)batch * cols);
+        const int64_t n = (int64_t)batch * cols;
+        hipLaunchKernelGGL(remap_axes_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, x, cols, batch, m,
+                           xp);
+        if (hipGetLastError() != hipSuccess) return RTA_ERR_LAUNCH;
+        return rta_gemv(fmt, w, rows, cols, xp, batch, y, epilogue, ws + xb, workspace_bytes - xb, stream);
+    }
+    // row modes: every source row read once into ys, then gathered into y
+    float* ys = reinterpret_cast<float*>(ws);
+    const size_t yb = floats256((int64_t)batch * need);
+    rc = rta_gemv(fmt, w, need, cols, x, batch, ys, RTA_EPI_STORE, ws + yb, workspace_bytes - yb, stream);
+    if (rc) return rc;
+    const int64_t n = (int64_t)batch * rows;
+    if (epilogue == RTA_EPI_STORE)
+        hipLaunchKernelGGL(remap_gather_kernel<false>, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, ys, need,
+                           rows, batch, m, y);
+    else
+        hipLaunchKernelGGL(remap_gather_kernel<true>, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, ys, need,
+                           rows, batch, m, y);
+    return hipGetLastError() == hipSuccess ? RTA_OK : RTA_ERR_LAUNCH;
 }
 
 size_t rta_mlp_workspace_bytes(int fmt_g, int fmt_d, int hidden, int inter, int batch) {
@@ -674,22 +781,38 @@ int64_t rta_pack_bytes(int fmt, int rows, int cols) {
     return -1;
 }
 
-int rta_pack(int fmt, const void* src, int rows, int cols, void* dst, rta_stream_t stream) {
-    if (fmt != RTA_Q4_K && fmt != RTA_Q6_K) return RTA_ERR_FORMAT;
-    int rc = check_matrix(fmt, src, rows, cols);
-    if (rc) return rc;
+static int pack_rows(int fmt, const void* src, int rows, int cols, const Remap& m, void* dst, hipStream_t s) {
     if (!dst) return RTA_ERR_NULL;
     if (reinterpret_cast<uintptr_t>(dst) % 16) return RTA_ERR_ALIGN;
     const int64_t n2 = rta_pack_bytes(fmt, rows, cols) / 2;
     const dim3 g((unsigned)((n2 + 255) / 256)), b(256);
-    hipStream_t s = (hipStream_t)stream;
     if (fmt == RTA_Q4_K)
         hipLaunchKernelGGL(pack_kernel<RTA_Q4_K>, g, b, 0, s, static_cast<const uint8_t*>(src), rows, cols,
-                           static_cast<uint8_t*>(dst), n2);
+                           static_cast<uint8_t*>(dst), n2, m);
     else
         hipLaunchKernelGGL(pack_kernel<RTA_Q6_K>, g, b, 0, s, static_cast<const uint8_t*>(src), rows, cols,
-                           static_cast<uint8_t*>(dst), n2);
+                           static_cast<uint8_t*>(dst), n2, m);
     return hipGetLastError() == hipSuccess ? RTA_OK : RTA_ERR_LAUNCH;
+}
+
+int rta_pack(int fmt, const void* src, int rows, int cols, void* dst, rta_stream_t stream) {
+    if (fmt != RTA_Q4_K && fmt != RTA_Q6_K) return RTA_ERR_FORMAT;
+    int rc = check_matrix(fmt, src, rows, cols);
+    if (rc) return rc;
+    return pack_rows(fmt, src, rows, cols, Remap{}, dst, (hipStream_t)stream);
+}
+
+int rta_pack_remap(int fmt, const void* src, int src_rows, int cols, const rta_remap* remap, int rows, void* dst,
+                   rta_stream_t stream) {
+    if (fmt != RTA_Q4_K && fmt != RTA_Q6_K) return RTA_ERR_FORMAT;
+    Remap m;
+    int need = 0;
+    int rc = check_remap(remap, src_rows, rows, cols, &m, &need);
+    if (rc) return rc;
+    if (m.mode == RTA_REMAP_AXES) return RTA_ERR_RANGE;
+    rc = check_matrix(fmt, src, need, cols);
+    if (rc) return rc;
+    return pack_rows(fmt, src, rows, cols, m, dst, (hipStream_t)stream);
 }
 
 }  // extern "C"

@@ -32,6 +32,7 @@
 // sums of x that xprep_kernel lays out per lane segment to match.
 #pragma once
 #include "rta_gemm.hpp"
+#include "rta_remap.hpp"
 
 namespace rta {
 
@@ -80,10 +81,10 @@ struct TileFmt<RTA_Q6_K> {
     }
 };
 
-// One thread per 2 bytes of the packed matrix.
+// One thread per 2 bytes of the packed matrix; tile row r holds GGUF row m.source_row(r).
 template <int FMT>
 __global__ void __launch_bounds__(256) pack_kernel(const uint8_t* __restrict__ src, int rows, int cols,
-                                                   uint8_t* __restrict__ dst, int64_t n2) {
+                                                   uint8_t* __restrict__ dst, int64_t n2, const Remap m) {
     using F = TileFmt<FMT>;
     const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
     if (i >= n2) return;
@@ -98,7 +99,7 @@ __global__ void __launch_bounds__(256) pack_kernel(const uint8_t* __restrict__ s
     const int64_t row = tile * 16 + r;
     uint16_t v = 0;
     if (row < rows) {
-        const uint8_t* p = src + row * (int64_t)nsb * F::kBlock + (int64_t)sb * F::kBlock + off;
+        const uint8_t* p = src + m.source_row(row) * (int64_t)nsb * F::kBlock + (int64_t)sb * F::kBlock + off;
         v = (uint16_t)(p[0] | (p[1] << 8));
     }
     *reinterpret_cast<uint16_t*>(dst + o) = v;

@@ -21,6 +21,18 @@ ERR_SCRATCH = 9                    # RTA_ERR_SCRATCH
 _i, _i64, _sz, _f, _d, _p, _u32p = (ctypes.c_int, ctypes.c_int64, ctypes.c_size_t, ctypes.c_float,
                                     ctypes.c_double, ctypes.c_void_p, ctypes.POINTER(ctypes.c_uint32))
 
+# row/axis remap modes (resident_quant.glsl:21-31): rta_remap.mode
+REMAP_NONE, REMAP_QUERY, REMAP_GATE, REMAP_ROTARY, REMAP_AXES, REMAP_KEY_REPEAT = 0, 1, 2, 3, 4, 5
+
+
+class Remap(ctypes.Structure):
+    """struct rta_remap {mode, head_dim, rotary_dim, key_rows}."""
+    _fields_ = [("mode", ctypes.c_int), ("head_dim", ctypes.c_int), ("rotary_dim", ctypes.c_int),
+                ("key_rows", ctypes.c_int)]
+
+
+_remap_p = ctypes.POINTER(Remap)
+
 # name -> (restype, argtypes); must match include/rta.h
 SIGNATURES = {
     "rta_version": (_i, []),
@@ -45,6 +57,9 @@ SIGNATURES = {
     "rta_pack": (_i, [_i, _p, _i, _i, _p, _p]),
     "rta_gemv_workspace_bytes": (_sz, [_i, _i, _i, _i]),
     "rta_gemv": (_i, [_i, _p, _i, _i, _p, _i, _p, _i, _p, _sz, _p]),
+    "rta_gemv_remap_workspace_bytes": (_sz, [_i, _remap_p, _i, _i, _i]),
+    "rta_gemv_remap": (_i, [_i, _p, _i, _i, _i, _remap_p, _p, _i, _p, _i, _p, _sz, _p]),
+    "rta_pack_remap": (_i, [_i, _p, _i, _i, _remap_p, _i, _p, _p]),
     "rta_mlp_workspace_bytes": (_sz, [_i, _i, _i, _i, _i]),
     "rta_mlp_swiglu": (_i, [_i, _p, _i, _p, _i, _p, _i, _i, _p, _i, _p, _p, _i, _p, _sz, _p]),
     "rta_swiglu": (_i, [_i, _p, _p, _i, _i, _p, _i, _p, _p, _sz, _p]),

@@ -63,6 +63,29 @@ def pack(fmt, w, rows, cols):
     return out
 
 
+def remap(mode, head_dim=0, rotary_dim=0, key_rows=0):
+    """An rta_remap: the reference's descriptor mode with the geometry it reads."""
+    return _lib.Remap(mode, head_dim, rotary_dim, key_rows)
+
+
+def pack_remap(fmt, w, src_rows, cols, rm, rows, out=None):
+    """Packed copy of the row-remapped matrix (logical row r = GGUF row src(r)).
+
+    out: optional uint8 view to pack into (e.g. a part of a larger packed matrix)."""
+    lib = _lib.load()
+    _dev(w, "w")
+    n = pack_bytes(fmt, rows, cols)
+    if n < 0:
+        raise ValueError(f"cannot pack format {fmt} of shape {rows}x{cols}")
+    if out is None:
+        out = torch.empty(n, dtype=torch.uint8, device=w.device)
+    elif out.numel() < n:
+        raise ValueError("out is smaller than the packed matrix")
+    check(lib.rta_pack_remap(fmt, _ptr(w), src_rows, cols, ctypes.byref(rm), rows, _ptr(out), _stream()),
+          "rta_pack_remap")
+    return out
+
+
 def _workspace(nbytes, dev, given):
     if given is not None:
         return given
@@ -87,6 +110,28 @@ def gemv(fmt, w, rows, cols, x, y=None, accumulate=False, workspace=None):
     ws = _workspace(gemv_workspace_bytes(fmt, rows, cols, batch), x.device, workspace)
     check(lib.rta_gemv(fmt, _ptr(w), rows, cols, _ptr(x2), batch, _ptr(y),
                        EPI_ACCUMULATE if accumulate else EPI_STORE, _ptr(ws), ws.numel(), _stream()), "rta_gemv")
+    return y
+
+
+def gemv_remap_workspace_bytes(fmt, rm, rows, cols, batch):
+    return int(_lib.load().rta_gemv_remap_workspace_bytes(fmt, ctypes.byref(rm), rows, cols, batch))
+
+
+def gemv_remap(fmt, w, src_rows, rows, cols, rm, x, y=None, accumulate=False, workspace=None):
+    """y[b, r] (=|+=) sum_a W[src(r), src(a)] x[b, a] for the remap rm."""
+    lib = _lib.load()
+    _dev(w, "w"), _dev(x, "x")
+    x2 = x.reshape(-1, cols)
+    batch = x2.shape[0]
+    if y is None:
+        if accumulate:
+            raise ValueError("accumulate needs y")
+        y = torch.empty(batch, rows, dtype=torch.float32, device=x.device)
+    _dev(y, "y")
+    ws = _workspace(gemv_remap_workspace_bytes(fmt, rm, rows, cols, batch), x.device, workspace)
+    check(lib.rta_gemv_remap(fmt, _ptr(w), src_rows, rows, cols, ctypes.byref(rm), _ptr(x2), batch, _ptr(y),
+                             EPI_ACCUMULATE if accumulate else EPI_STORE, _ptr(ws), ws.numel(), _stream()),
+          "rta_gemv_remap")
     return y
 
 
