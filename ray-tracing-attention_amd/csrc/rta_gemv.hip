@@ -4,7 +4,7 @@
 
 #include <climits>
 #include "rta_gemm.hpp"
-#include "rta_tiled.hpp"
+#include "rta_packed.hpp"
 #include "rta_remap.hpp"
 #include "rta_gemv.hpp"
 #include "rta_host.hpp"
@@ -449,6 +449,128 @@ static int run_projection(int fmt, const void* w, const void* w2, int rows, int 
         b0 += chunk;
     }
     return RTA_OK;
+}
+
+// ---- readouts of a staged x image (rta_packed.hpp), used by the decode step -------
+// Kernel shape: tiles per wave and superblock, waves per workgroup, superblocks of
+// weights in flight per wave.
+constexpr int kPkTpw = 2, kPkWaves = 8, kPkDepth = 3;
+
+// Work split: units of kPkTpw tiles (kSwiglu: gate and up tiles of the same rows) are
+// shared out to the waves of each K slab in balanced contiguous ranges.  The K range is
+// cut into as few slabs as the LDS image capacity allows, and into more (up to one per
+// superblock) while the units of all slabs would not occupy every wave once.
+static MmaPlan plan_packed(int rows, int cols, int nbt, bool dual) {
+    MmaPlan p{};
+    p.nbt = nbt;
+    p.total_rows = dual ? 2 * rows : rows;
+    const int ntile = (rows + 15) / 16;
+    const int tpu = dual ? kPkTpw / 2 : kPkTpw;
+    const int units = (ntile + tpu - 1) / tpu;
+    p.ntg = ntile;
+    const int nsbt = cols / 256;
+    const int cap = nbt == 1 ? slab_capacity<1>() : slab_capacity<2>();
+    int nslab = (nsbt + cap - 1) / cap;
+    while (nslab < nsbt && (int64_t)units * nslab < (int64_t)kPlanCUs * kPkWaves) ++nslab;
+    p.sb_per_slab = (nsbt + nslab - 1) / nslab;
+    p.nslab = (nsbt + p.sb_per_slab - 1) / p.sb_per_slab;
+    const int wps = kPlanCUs / p.nslab > 0 ? kPlanCUs / p.nslab : 1;   // one workgroup per CU
+    const int need = (units + kPkWaves - 1) / kPkWaves;
+    p.wgs_per_slab = wps < need ? wps : need;
+    p.grid = p.nslab * p.wgs_per_slab;
+    p.x_bytes = 0;
+    p.part_bytes = p.nslab > 1 ? (size_t)p.nslab * kMaxBatchTile * p.total_rows * sizeof(float) : 0;
+    return p;
+}
+
+size_t image_bytes(int cols, int batch) {
+    if (cols <= 0 || cols % 256 || batch <= 0 || batch > kMaxBatchTile) return 0;
+    const size_t one = batch > 16 ? sizeof(XImage<2>) : sizeof(XImage<1>);
+    return ((size_t)(cols / 256) * one + 255) & ~(size_t)255;
+}
+
+size_t image_readout_ws_bytes(int rows, int cols, bool dual) {
+    const MmaPlan a = plan_packed(rows, cols, 1, dual), b = plan_packed(rows, cols, 2, dual);
+    return a.part_bytes > b.part_bytes ? a.part_bytes : b.part_bytes;
+}
+
+static bool image_format(int fmt) { return fmt == (RTA_Q4_K | kTiled) || fmt == (RTA_Q6_K | kTiled); }
+
+int residual_norm_image(int fmt, float* hidden, const float* part, int nslab, const float* w, int batch, int width,
+                        float* ss, void* img, hipStream_t s) {
+    if (!image_format(fmt)) return RTA_ERR_FORMAT;
+    if (!hidden || !w || !ss || !img || (nslab > 0 && !part)) return RTA_ERR_NULL;
+    if (batch <= 0 || batch > kMaxBatchTile || width <= 0 || width % 256 || width > 4096 || nslab < 0)
+        return RTA_ERR_SHAPE;
+    if (!host::aligned(hidden, 16) || !host::aligned(w, 16) || !host::aligned(ss, 16) || !host::aligned(img, 16) ||
+        (part && !host::aligned(part, 16)))
+        return RTA_ERR_ALIGN;
+    const int nbt = batch > 16 ? 2 : 1;
+    const dim3 g((width + 1023) / 1024, 16 * nbt), b(256);
+    const bool q4 = (fmt & 0xff) == RTA_Q4_K;
+    if (nbt == 1) {
+        if (q4) hipLaunchKernelGGL((residual_norm_image_kernel<RTA_Q4_K, 1>), g, b, 0, s, hidden, part, nslab, w,
+                                   width, batch, ss, static_cast<XImage<1>*>(img));
+        else hipLaunchKernelGGL((residual_norm_image_kernel<RTA_Q6_K, 1>), g, b, 0, s, hidden, part, nslab, w, width,
+                                batch, ss, static_cast<XImage<1>*>(img));
+    } else {
+        if (q4) hipLaunchKernelGGL((residual_norm_image_kernel<RTA_Q4_K, 2>), g, b, 0, s, hidden, part, nslab, w,
+                                   width, batch, ss, static_cast<XImage<2>*>(img));
+        else hipLaunchKernelGGL((residual_norm_image_kernel<RTA_Q6_K, 2>), g, b, 0, s, hidden, part, nslab, w, width,
+                                batch, ss, static_cast<XImage<2>*>(img));
+    }
+    return hipGetLastError() == hipSuccess ? RTA_OK : RTA_ERR_LAUNCH;
+}
+
+template <int FMT, int NBT, int MODE>
+static void launch_packed(const MmaPlan& p, const uint8_t* w, const uint8_t* w2, int rows, int cols, const void* img,
+                          int batch, float* y, float* part, const RowNorm& rn, hipStream_t s) {
+    hipLaunchKernelGGL((gemm_packed_kernel<FMT, NBT, MODE, kPkTpw, kPkWaves, kPkDepth>), dim3(p.grid),
+                       dim3(64 * kPkWaves), 0, s, w, w2, rows, cols, static_cast<const XImage<NBT>*>(img), batch, y,
+                       part, p.sb_per_slab, p.wgs_per_slab, rn);
+}
+
+template <int MODE>
+static int image_readout_mode(int fmt, const void* w, const void* w2, int rows, int cols, const void* img, int batch,
+                              float* y, bool reduce, void* ws, size_t ws_bytes, hipStream_t s, int* nslab,
+                              const RowNorm& rn) {
+    if (!image_format(fmt)) return RTA_ERR_FORMAT;
+    if (!w || !img || !y || (MODE == kSwiglu && !w2)) return RTA_ERR_NULL;
+    if (batch <= 0 || batch > kMaxBatchTile || rows <= 0 || cols <= 0 || cols % 256) return RTA_ERR_SHAPE;
+    const int nbt = batch > 16 ? 2 : 1;
+    const MmaPlan p = plan_packed(rows, cols, nbt, MODE == kSwiglu);
+    if (p.part_bytes && (!ws || ws_bytes < p.part_bytes)) return RTA_ERR_WORKSPACE;
+    float* part = static_cast<float*>(ws);
+    const uint8_t* a = static_cast<const uint8_t*>(w);
+    const uint8_t* a2 = static_cast<const uint8_t*>(w2);
+    if ((fmt & 0xff) == RTA_Q4_K) {
+        if (nbt == 1) launch_packed<RTA_Q4_K, 1, MODE>(p, a, a2, rows, cols, img, batch, y, part, rn, s);
+        else launch_packed<RTA_Q4_K, 2, MODE>(p, a, a2, rows, cols, img, batch, y, part, rn, s);
+    } else {
+        if (nbt == 1) launch_packed<RTA_Q6_K, 1, MODE>(p, a, a2, rows, cols, img, batch, y, part, rn, s);
+        else launch_packed<RTA_Q6_K, 2, MODE>(p, a, a2, rows, cols, img, batch, y, part, rn, s);
+    }
+    if (reduce && p.nslab > 1)
+        hipLaunchKernelGGL((gemm_reduce_kernel<MODE>), dim3((rows + 255) / 256, batch), dim3(256), 0, s, part, p.nslab,
+                           rows, batch, y, nullptr);
+    if (nslab) *nslab = reduce ? 1 : p.nslab;
+    return hipGetLastError() == hipSuccess ? RTA_OK : RTA_ERR_LAUNCH;
+}
+
+static_assert(kReadStore == kStore && kReadAccumulate == kAccumulate && kReadSwiglu == kSwiglu, "readout modes");
+
+int image_readout(int fmt, int mode, const void* w, const void* w2, int rows, int cols, const void* img, int batch,
+                  float* y, bool reduce, void* ws, size_t ws_bytes, hipStream_t s, int* nslab, const RowNorm& rn) {
+    switch (mode) {
+    case kStore:
+        return image_readout_mode<kStore>(fmt, w, w2, rows, cols, img, batch, y, reduce, ws, ws_bytes, s, nslab, rn);
+    case kAccumulate:
+        return image_readout_mode<kAccumulate>(fmt, w, w2, rows, cols, img, batch, y, reduce, ws, ws_bytes, s, nslab,
+                                               rn);
+    case kSwiglu:
+        return image_readout_mode<kSwiglu>(fmt, w, w2, rows, cols, img, batch, y, reduce, ws, ws_bytes, s, nslab, rn);
+    default: return RTA_ERR_RANGE;
+    }
 }
 
 static_assert(kSlabBatch == kMaxBatchTile, "partial blocks hold one batch tile");

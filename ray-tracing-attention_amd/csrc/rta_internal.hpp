@@ -53,4 +53,24 @@ int residual_rmsnorm(float* hidden, const float* part, int nslab, const float* w
 int residual_norm_deferred(float* hidden, const float* part, int nslab, const float* w, int batch, int width,
                            float* out, float* ss, hipStream_t s);
 
+// ---- the decode step's readouts of a staged x image (rta_packed.hpp) ----
+constexpr int kReadStore = 0, kReadAccumulate = 1, kReadSwiglu = 2;   // image_readout modes
+// Bytes of the image of x [batch <= 32, cols] (cols % 256 == 0); 0 for other shapes.
+size_t image_bytes(int cols, int batch);
+// Workspace of image_readout's K-slab partials, either batch-tile width.
+size_t image_readout_ws_bytes(int rows, int cols, bool dual);
+
+// residual_norm_deferred writing x = hidden * w as the readout image of a packed
+// format (fmt | RTA_TILED, which fixes the group-sum layout) instead of fp32; ss as
+// there, for a RowNorm {ss, width, eps}.  width % 256 == 0, <= 4096; batch <= 32.
+int residual_norm_image(int fmt, float* hidden, const float* part, int nslab, const float* w, int batch, int width,
+                        float* ss, void* img, hipStream_t s);
+
+// y (=|+=) W x (mode kStore / kAccumulate) or act = swiglu(Wg x, Wu x) (kSwiglu, w2 the up
+// matrix) from the image of x, each result times the row's RMSNorm factor rn.  reduce:
+// K slabs are added into y here; else *nslab > 1 leaves them in ws as [slab][32][rows]
+// (kSwiglu: 2 rows, gate and up interleaved) for the caller.
+int image_readout(int fmt, int mode, const void* w, const void* w2, int rows, int cols, const void* img, int batch,
+                  float* y, bool reduce, void* ws, size_t ws_bytes, hipStream_t s, int* nslab, const RowNorm& rn);
+
 }  // namespace rta

@@ -163,7 +163,7 @@ struct Work {
     float *hidden, *normed, *proj, *q, *conv, *decay, *beta, *mix, *act, *logits, *rms;
     int64_t *pos, *slots;
     int32_t* visible;
-    void *attn_ws, *lm_ws, *gemm_ws;
+    void *attn_ws, *lm_ws, *gemm_ws, *ximg;
     size_t attn_bytes, lm_bytes, gemm_bytes;
 };
 
@@ -175,6 +175,9 @@ size_t gemm_ws_bytes(const rta_hybrid_shape* s, const Dims& d) {
     if (d.nfull) up(rta_gemv_workspace_bytes(s->fmt_proj, d.D, d.hq * d.hd, d.B));
     if (d.nrec) up(rta_gemv_workspace_bytes(s->fmt_proj, d.D, d.S, d.B));
     up(rta_mlp_workspace_bytes(s->fmt_proj, s->fmt_proj, d.D, d.FF, d.B));
+    if (d.nfull) up(image_readout_ws_bytes(d.rows_full, d.D, false));
+    if (d.nrec) up(image_readout_ws_bytes(d.rows_rec, d.D, false));
+    up(image_readout_ws_bytes(d.FF, d.D, true));
     return m;
 }
 
@@ -202,6 +205,7 @@ Work carve_work(const rta_hybrid_shape* s, const Dims& d, void* p, size_t* bytes
     w.lm_ws = c.take<uint8_t>(std::max<size_t>(w.lm_bytes, 1));
     w.gemm_bytes = gemm_ws_bytes(s, d);
     w.gemm_ws = c.take<uint8_t>(std::max<size_t>(w.gemm_bytes, 1));
+    w.ximg = c.take<uint8_t>(std::max<size_t>(image_bytes(d.D, std::min(d.B, 32)), 1));
     if (bytes) *bytes = (c.off + 255) & ~(size_t)255;
     return w;
 }
@@ -303,6 +307,16 @@ int rta_hybrid_decode_step(const rta_hybrid_shape* shape, const rta_hybrid_weigh
     // takes w.normed (h * w is written and rn describes the factor): the residual add
     // then spreads over several blocks per row.  deferred = false: w.normed is final.
     RowNorm rn{};
+    // With packed Q4_K / Q6_K projections the norm in front of the in-projection and the
+    // gate/up pair writes x straight into the readout's matrix-core image (w.ximg).
+    const bool img = fuse && d.D <= 4096 && (pf == (RTA_Q4_K | RTA_TILED) || pf == (RTA_Q6_K | RTA_TILED));
+    auto norm_image = [&](const float* nw) -> int {
+        const int rc = residual_norm_image(pf, w.hidden, static_cast<const float*>(w.gemm_ws), pending, nw, B, d.D,
+                                           w.rms, w.ximg, s);
+        rn = RowNorm{reinterpret_cast<const float4*>(w.rms), (float)d.D, eps};
+        pending = 0;
+        return rc;
+    };
     auto norm = [&](const float* nw, bool deferred) -> int {
         rn = RowNorm{};
         deferred = deferred && d.D <= 4096;
@@ -322,11 +336,15 @@ int rta_hybrid_decode_step(const rta_hybrid_shape* shape, const rta_hybrid_weigh
     int lf = 0, lr = 0;
     for (int l = 0; l < d.L; ++l) {
         const rta_hybrid_layer& lw = weights->layers[l];
-        RTA_TRY(norm(lw.norm_in, fuse));
+        RTA_TRY(img ? norm_image(lw.norm_in) : norm(lw.norm_in, fuse));
         if (is_full(shape, l)) {
             // op 2 index 5 (q | k | v), ops 14 + 3, op 34, attention, op 2 index 2
-            RTA_TRY(projection_store(pf, lw.w_in, d.rows_full, d.D, w.normed, B, w.proj, w.gemm_ws, w.gemm_bytes, s,
-                                     rn));
+            if (img)
+                RTA_TRY(image_readout(pf, kReadStore, lw.w_in, nullptr, d.rows_full, d.D, w.ximg, B, w.proj, true,
+                                      w.gemm_ws, w.gemm_bytes, s, nullptr, rn));
+            else
+                RTA_TRY(projection_store(pf, lw.w_in, d.rows_full, d.D, w.normed, B, w.proj, w.gemm_ws, w.gemm_bytes,
+                                         s, rn));
             hipLaunchKernelGGL(qk_norm_rope_kernel, dim3((d.hq + d.hkv + 3) / 4, B), dim3(256), 0, s, w.proj,
                                d.rows_full, d.hq, d.hkv, lw.q_norm, lw.k_norm, eps, w.pos, shape->rope_rotary,
                                shape->rope_theta, w.q);
@@ -344,8 +362,12 @@ int rta_hybrid_decode_step(const rta_hybrid_shape* shape, const rta_hybrid_weigh
             // op 2 index 5 (q | k | v | z | a | b), ops 18-21 and 15, op 2 index 2
             if (fuse) {   // the fused middle reads the in-projection's K slabs itself
                 int ns = 1;
-                RTA_TRY(tiled_partials(pf, lw.w_in, d.rows_rec, d.D, w.normed, B, w.proj, false, w.gemm_ws,
-                                       w.gemm_bytes, s, &ns, rn));
+                if (img)
+                    RTA_TRY(image_readout(pf, kReadStore, lw.w_in, nullptr, d.rows_rec, d.D, w.ximg, B, w.proj, false,
+                                          w.gemm_ws, w.gemm_bytes, s, &ns, rn));
+                else
+                    RTA_TRY(tiled_partials(pf, lw.w_in, d.rows_rec, d.D, w.normed, B, w.proj, false, w.gemm_ws,
+                                           w.gemm_bytes, s, &ns, rn));
                 const bool slabs = ns > 1;
                 RTA_TRY(recurrent_mix(slabs ? static_cast<const float*>(w.gemm_ws) : w.proj,
                                       (int64_t)kSlabBatch * d.rows_rec, d.rows_rec, slabs ? ns : 1,
@@ -367,8 +389,12 @@ int rta_hybrid_decode_step(const rta_hybrid_shape* shape, const rta_hybrid_weigh
             ++lr;
         }
         // op 1 index 1, then the SwiGLU MLP with the residual add (executeMLP)
-        RTA_TRY(norm(lw.norm_post, fuse));
-        if (fuse) {
+        RTA_TRY(img ? norm_image(lw.norm_post) : norm(lw.norm_post, fuse));
+        if (img) {
+            RTA_TRY(image_readout(pf, kReadSwiglu, lw.w_gate, lw.w_up, d.FF, d.D, w.ximg, B, w.act, true, w.gemm_ws,
+                                  w.gemm_bytes, s, nullptr, rn));
+            RTA_TRY(residual_proj(lw.w_down, d.FF, w.act));
+        } else if (fuse) {
             RTA_TRY(swiglu_activation(pf, lw.w_gate, lw.w_up, d.FF, d.D, w.normed, B, w.act, w.gemm_ws, w.gemm_bytes, s,
                                       rn));
             RTA_TRY(residual_proj(lw.w_down, d.FF, w.act));
