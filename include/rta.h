@@ -313,14 +313,24 @@ typedef struct rta_hybrid_shape {
     float eps;                        /* RMSNorm epsilon */
     float margin;                     /* argmax tie margin (relative), as rta_lm_head */
     double rope_theta;
+    /* What compiler/export.py emits beyond the plain layout (zero: not used): */
+    int attn_gate;      /* 1: full layers' w_in holds q_heads * 128 gate rows after [q | k | v], and the
+                           attention output is times sigmoid(gate) (export.py:98,103;
+                           resident_ray.comp:75-76) */
+    int rec_key_heads;  /* q and k heads of the recurrent in-projection, 0 < rec_key_heads <= rec_heads
+                           (0: rec_heads); delta-net head h reads q / k head h % rec_key_heads, the
+                           key repeat of export.py:107-112 / resident_quant.glsl:26 */
+    int layer_formats;  /* 1: each layer's fmt_* fields give its matrices' formats (else fmt_proj) */
 } rta_hybrid_shape;
 
 typedef struct rta_hybrid_layer {   /* device pointers; fmt_proj matrices [rows x cols] */
     const float* norm_in;            /* [hidden] */
     const float* norm_post;          /* [hidden] */
-    const void* w_in;                /* full: (q_heads + 2 kv_heads) * 128 rows [q | k | v];
-                                        recurrent: 4 S + 2 rec_heads rows [q | k | v | z | a | b],
-                                        S = rec_heads * 128; cols = hidden */
+    const void* w_in;                /* full: (q_heads + 2 kv_heads) * 128 rows [q | k | v] (+ q_heads *
+                                        128 gate rows with attn_gate);
+                                        recurrent: [q | k | v | z | a | b], q and k KH * 128 rows each
+                                        (KH = rec_key_heads), v and z S rows, a and b rec_heads rows
+                                        (not with w_a), S = rec_heads * 128; cols = hidden */
     const void* w_o;                 /* [hidden x (q_heads * 128 or S)] */
     const void* w_gate;              /* [ff x hidden] */
     const void* w_up;                /* [ff x hidden] */
@@ -331,6 +341,12 @@ typedef struct rta_hybrid_layer {   /* device pointers; fmt_proj matrices [rows 
     const float* a_log;              /* recurrent: [rec_heads] */
     const float* dt_bias;            /* recurrent: [rec_heads] */
     const float* out_norm;           /* recurrent: [S] gated-norm weight */
+    int fmt_in, fmt_o, fmt_gate_up, fmt_down;   /* with shape->layer_formats: GGUF codes, | RTA_TILED */
+    const void* w_a;                 /* recurrent: the a (decay) and b (beta) rows [rec_heads x hidden]
+                                        as matrices of their own (format fmt_ab), as export.py:113 keeps
+                                        ssm_alpha / ssm_beta; NULL: the last 2 rec_heads rows of w_in */
+    const void* w_b;
+    int fmt_ab;
 } rta_hybrid_layer;
 
 typedef struct rta_hybrid_weights {

@@ -29,6 +29,7 @@
 
 #include "rta_common.hpp"
 #include "rta_host.hpp"
+#include "rta_internal.hpp"
 
 namespace rta {
 
@@ -43,6 +44,7 @@ struct AttnArgs {
     const int64_t* slot_base;
     const int32_t* ctx_len;
     const float* gate;
+    int64_t gate_stride;   // floats from one sequence's gate row to the next (head h at + h hd)
     float* out;
     float* m_out;
     float* z_out;
@@ -1448,7 +1450,7 @@ __global__ void __launch_bounds__(256) attn_merge_kernel(const AttnArgs a) {
             z = fmaf(s_zp[g], f, z);
         }
         float o = u / fmaxf(z, 1e-30f);
-        if (a.gate) o *= detector_sigmoid(a.gate[(int64_t)sh * kHd + tid]);
+        if (a.gate) o *= detector_sigmoid(a.gate[(int64_t)(sh / a.hq) * a.gate_stride + (sh % a.hq) * kHd + tid]);
         out[tid] = o;
         if (tid == 0) {
             if (a.m_out) a.m_out[sh] = M;
@@ -1625,6 +1627,20 @@ int rta_decode_attention(const float* q, int nseq, int hq, int hkv, int hd, cons
                          const int64_t* slot_base, const int32_t* ctx_len, int64_t capacity, int64_t n_slots,
                          int max_ctx, const float* gate, float* out, float* m_out, float* z_out, void* workspace,
                          size_t workspace_bytes, rta_stream_t stream) {
+    return decode_attention_gate_stride(q, nseq, hq, hkv, hd, packets, fmt_k, fmt_v, slot_base, ctx_len, capacity,
+                                        n_slots, max_ctx, gate, (int64_t)hq * hd, out, m_out, z_out, workspace,
+                                        workspace_bytes, stream);
+}
+
+}  // extern "C"
+
+namespace rta {
+
+int decode_attention_gate_stride(const float* q, int nseq, int hq, int hkv, int hd, const void* packets, int fmt_k,
+                                 int fmt_v, const int64_t* slot_base, const int32_t* ctx_len, int64_t capacity,
+                                 int64_t n_slots, int max_ctx, const float* gate, int64_t gate_stride, float* out,
+                                 float* m_out, float* z_out, void* workspace, size_t workspace_bytes,
+                                 rta_stream_t stream) {
     if (!q || !packets || !slot_base || !ctx_len || !out) return RTA_ERR_NULL;   // m_out, z_out optional
     if (nseq <= 0 || hq <= 0 || hkv <= 0 || hd <= 0 || hq % hkv || capacity <= 0 || max_ctx <= 0 || n_slots <= 0)
         return RTA_ERR_SHAPE;
@@ -1642,6 +1658,7 @@ int rta_decode_attention(const float* q, int nseq, int hq, int hkv, int hd, cons
     if (!host::aligned(q, 4) || !host::aligned(packets, 4) || !host::aligned(slot_base, 8) ||
         !host::aligned(ctx_len, 4) || !host::aligned(out, 4) || (gate && !host::aligned(gate, 4)))
         return RTA_ERR_ALIGN;
+    if (gate && gate_stride < (int64_t)hq * hd) return RTA_ERR_SHAPE;
     const size_t need = rta_decode_attention_workspace_bytes(nseq, hq, hkv, hd, max_ctx);
     if (!workspace || workspace_bytes < need || !host::aligned(workspace, 16)) return RTA_ERR_WORKSPACE;
     AttnArgs a{};
@@ -1650,6 +1667,7 @@ int rta_decode_attention(const float* q, int nseq, int hq, int hkv, int hd, cons
     a.slot_base = slot_base;
     a.ctx_len = ctx_len;
     a.gate = gate;
+    a.gate_stride = gate_stride;
     a.out = out;
     a.m_out = m_out;
     a.z_out = z_out;
@@ -1681,6 +1699,10 @@ int rta_decode_attention(const float* q, int nseq, int hq, int hkv, int hd, cons
     hipLaunchKernelGGL(attn_merge_kernel, dim3(nseq * hq), dim3(256), 0, s, a);
     return hipGetLastError() == hipSuccess ? RTA_OK : RTA_ERR_LAUNCH;
 }
+
+}  // namespace rta
+
+extern "C" {
 
 int rta_decode_attention_noalloc(const float* q, int nseq, int hq, int hkv, int hd, const void* packets, int fmt_k,
                                  int fmt_v, const int64_t* slot_base, const int32_t* ctx_len, int64_t capacity,

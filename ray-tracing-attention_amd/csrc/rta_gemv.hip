@@ -497,27 +497,27 @@ size_t image_readout_ws_bytes(int rows, int cols, bool dual) {
 static bool image_format(int fmt) { return fmt == (RTA_Q4_K | kTiled) || fmt == (RTA_Q6_K | kTiled); }
 
 int residual_norm_image(int fmt, float* hidden, const float* part, int nslab, const float* w, int batch, int width,
-                        float* ss, void* img, hipStream_t s) {
+                        float* ss, float* out, void* img, hipStream_t s) {
     if (!image_format(fmt)) return RTA_ERR_FORMAT;
     if (!hidden || !w || !ss || !img || (nslab > 0 && !part)) return RTA_ERR_NULL;
     if (batch <= 0 || batch > kMaxBatchTile || width <= 0 || width % 256 || width > 4096 || nslab < 0)
         return RTA_ERR_SHAPE;
     if (!host::aligned(hidden, 16) || !host::aligned(w, 16) || !host::aligned(ss, 16) || !host::aligned(img, 16) ||
-        (part && !host::aligned(part, 16)))
+        (part && !host::aligned(part, 16)) || (out && !host::aligned(out, 16)))
         return RTA_ERR_ALIGN;
     const int nbt = batch > 16 ? 2 : 1;
     const dim3 g((width + 1023) / 1024, 16 * nbt), b(256);
     const bool q4 = (fmt & 0xff) == RTA_Q4_K;
     if (nbt == 1) {
         if (q4) hipLaunchKernelGGL((residual_norm_image_kernel<RTA_Q4_K, 1>), g, b, 0, s, hidden, part, nslab, w,
-                                   width, batch, ss, static_cast<XImage<1>*>(img));
+                                   width, batch, ss, out, static_cast<XImage<1>*>(img));
         else hipLaunchKernelGGL((residual_norm_image_kernel<RTA_Q6_K, 1>), g, b, 0, s, hidden, part, nslab, w, width,
-                                batch, ss, static_cast<XImage<1>*>(img));
+                                batch, ss, out, static_cast<XImage<1>*>(img));
     } else {
         if (q4) hipLaunchKernelGGL((residual_norm_image_kernel<RTA_Q4_K, 2>), g, b, 0, s, hidden, part, nslab, w,
-                                   width, batch, ss, static_cast<XImage<2>*>(img));
+                                   width, batch, ss, out, static_cast<XImage<2>*>(img));
         else hipLaunchKernelGGL((residual_norm_image_kernel<RTA_Q6_K, 2>), g, b, 0, s, hidden, part, nslab, w, width,
-                                batch, ss, static_cast<XImage<2>*>(img));
+                                batch, ss, out, static_cast<XImage<2>*>(img));
     }
     return hipGetLastError() == hipSuccess ? RTA_OK : RTA_ERR_LAUNCH;
 }

@@ -34,11 +34,15 @@ int swiglu_activation(int fmt, const void* wg, const void* wu, int inter, int hi
 
 // The middle of a recurrent layer (ops 18-21 and 15) for every (head, sequence):
 // in-projection row r of sequence b = sum_k proj[k * slab_stride + b * row_stride + r]
-// over k < nslab (q | k | v | z | a | b, 4 heads 128 + 2 heads rows), conv window and
-// recurrent state updated in place, gated-norm output to out (row stride out_stride).
-int recurrent_mix(const float* proj, int64_t slab_stride, int row_stride, int nslab, float* conv_state,
-                  const float* conv_w, const float* a_log, const float* dt_bias, float* state, const float* norm_w,
-                  int batch, int heads, float eps, float* out, int out_stride, hipStream_t s);
+// over k < nslab (q | k | v | z | a | b: q and k key_heads heads of 128 rows each, v and
+// z heads * 128, a and b heads rows; head h reads q / k head h % key_heads), conv window
+// and recurrent state updated in place, gated-norm output to out (row stride
+// out_stride).  With ext_a / ext_b ([batch] rows of stride ext_stride) a and b come from
+// there, times the row factor rn, and the projection rows end after z.
+int recurrent_mix(const float* proj, int64_t slab_stride, int row_stride, int nslab, int key_heads, const float* ext_a,
+                  const float* ext_b, int ext_stride, const RowNorm& rn, float* conv_state, const float* conv_w,
+                  const float* a_log, const float* dt_bias, float* state, const float* norm_w, int batch, int heads,
+                  float eps, float* out, int out_stride, hipStream_t s);
 
 // hidden[b, :] += sum over slabs k < nslab of part[(k * 32 + b) * width + :] (slab order),
 // then out[b, :] = hidden[b, :] * w / sqrt(mean(hidden[b, :]^2) + eps).  nslab may be 0.
@@ -53,6 +57,14 @@ int residual_rmsnorm(float* hidden, const float* part, int nslab, const float* w
 int residual_norm_deferred(float* hidden, const float* part, int nslab, const float* w, int batch, int width,
                            float* out, float* ss, hipStream_t s);
 
+// rta_decode_attention with the gate of sequence s at gate + s gate_stride (head h at
+// + h hd), gate_stride >= hq hd: the gate rows of a fused in-projection.
+int decode_attention_gate_stride(const float* q, int nseq, int hq, int hkv, int hd, const void* packets, int fmt_k,
+                                 int fmt_v, const int64_t* slot_base, const int32_t* ctx_len, int64_t capacity,
+                                 int64_t n_slots, int max_ctx, const float* gate, int64_t gate_stride, float* out,
+                                 float* m_out, float* z_out, void* workspace, size_t workspace_bytes,
+                                 rta_stream_t stream);
+
 // ---- the decode step's readouts of a staged x image (rta_packed.hpp) ----
 constexpr int kReadStore = 0, kReadAccumulate = 1, kReadSwiglu = 2;   // image_readout modes
 // Bytes of the image of x [batch <= 32, cols] (cols % 256 == 0); 0 for other shapes.
@@ -61,10 +73,11 @@ size_t image_bytes(int cols, int batch);
 size_t image_readout_ws_bytes(int rows, int cols, bool dual);
 
 // residual_norm_deferred writing x = hidden * w as the readout image of a packed
-// format (fmt | RTA_TILED, which fixes the group-sum layout) instead of fp32; ss as
-// there, for a RowNorm {ss, width, eps}.  width % 256 == 0, <= 4096; batch <= 32.
+// format (fmt | RTA_TILED, which fixes the group-sum layout), and in fp32 to out (may
+// be null); ss as there, for a RowNorm {ss, width, eps}.  width % 256 == 0, <= 4096;
+// batch <= 32.
 int residual_norm_image(int fmt, float* hidden, const float* part, int nslab, const float* w, int batch, int width,
-                        float* ss, void* img, hipStream_t s);
+                        float* ss, float* out, void* img, hipStream_t s);
 
 // y (=|+=) W x (mode kStore / kAccumulate) or act = swiglu(Wg x, Wu x) (kSwiglu, w2 the up
 // matrix) from the image of x, each result times the row's RMSNorm factor rn.  reduce:

@@ -98,7 +98,10 @@ struct Carve {
 
 struct Dims {
     int D, L, nfull, nrec, hq, hkv, hd, H, S, FF, V, cap, B;
-    int rows_full, rows_rec, kvw;
+    int KH;              // q / k heads of the recurrent in-projection
+    int rows_full;       // full in-projection rows: q | k | v (| gate)
+    int rows_rec;        // recurrent in-projection rows with a | b (without: rows_rec - 2 H)
+    int kvw;
     int64_t stride;
 };
 
@@ -117,8 +120,9 @@ Dims dims_of(const rta_hybrid_shape* s, int batch) {
     d.V = s->vocab;
     d.cap = s->capacity;
     d.B = batch;
-    d.rows_full = (d.hq + 2 * d.hkv) * d.hd;
-    d.rows_rec = 4 * d.S + 2 * d.H;
+    d.KH = s->rec_key_heads > 0 ? s->rec_key_heads : s->rec_heads;
+    d.rows_full = (d.hq + 2 * d.hkv + (s->attn_gate ? d.hq : 0)) * d.hd;
+    d.rows_rec = 2 * d.KH * d.hd + 2 * d.S + 2 * d.H;
     d.kvw = d.hkv * d.hd;
     d.stride = host::history_bytes(d.kvw);
     return d;
@@ -136,6 +140,9 @@ int check_shape(const rta_hybrid_shape* s, int batch) {
         !(s->eps >= 0.0f) || !(s->rope_theta > 0.0))
         return RTA_ERR_RANGE;
     if ((s->full_every > 0 && (s->q_heads * 128) % 256) || (s->rec_heads * 128) % 256) return RTA_ERR_SHAPE;
+    if (s->attn_gate < 0 || s->attn_gate > 1 || s->layer_formats < 0 || s->layer_formats > 1 ||
+        s->rec_key_heads < 0 || s->rec_key_heads > s->rec_heads)
+        return RTA_ERR_RANGE;
     return RTA_OK;
 }
 
@@ -160,24 +167,38 @@ State carve_state(const Dims& d, void* p, size_t* bytes) {
 }
 
 struct Work {
-    float *hidden, *normed, *proj, *q, *conv, *decay, *beta, *mix, *act, *logits, *rms;
+    float *hidden, *normed, *proj, *q, *ext_a, *ext_b, *mix, *act, *logits, *rms;
     int64_t *pos, *slots;
     int32_t* visible;
     void *attn_ws, *lm_ws, *gemm_ws, *ximg;
     size_t attn_bytes, lm_bytes, gemm_bytes;
 };
 
+// The projection workspace: enough for every format a layer may use (the shape alone
+// fixes the size), the K-quant and packed ones being the only that need any.
 size_t gemm_ws_bytes(const rta_hybrid_shape* s, const Dims& d) {
     size_t m = 0;
     auto up = [&](size_t v) { m = std::max(m, v); };
-    if (d.nfull) up(rta_gemv_workspace_bytes(s->fmt_proj, d.rows_full, d.D, d.B));
-    if (d.nrec) up(rta_gemv_workspace_bytes(s->fmt_proj, d.rows_rec, d.D, d.B));
-    if (d.nfull) up(rta_gemv_workspace_bytes(s->fmt_proj, d.D, d.hq * d.hd, d.B));
-    if (d.nrec) up(rta_gemv_workspace_bytes(s->fmt_proj, d.D, d.S, d.B));
-    up(rta_mlp_workspace_bytes(s->fmt_proj, s->fmt_proj, d.D, d.FF, d.B));
+    const int fmts[5] = {s->fmt_proj, RTA_Q4_K, RTA_Q6_K, RTA_Q4_K | RTA_TILED, RTA_Q6_K | RTA_TILED};
+    for (int i = s->layer_formats ? 0 : 4; i < 5; ++i) {
+        const int f = s->layer_formats ? fmts[i] : s->fmt_proj;
+        if (d.nfull) up(rta_gemv_workspace_bytes(f, d.rows_full, d.D, d.B));
+        if (d.nrec) up(rta_gemv_workspace_bytes(f, d.rows_rec, d.D, d.B));
+        if (d.nrec) up(rta_gemv_workspace_bytes(f, d.H, d.D, d.B));
+        if (d.nfull) up(rta_gemv_workspace_bytes(f, d.D, d.hq * d.hd, d.B));
+        if (d.nrec) up(rta_gemv_workspace_bytes(f, d.D, d.S, d.B));
+        up(rta_mlp_workspace_bytes(f, f, d.D, d.FF, d.B));
+    }
     if (d.nfull) up(image_readout_ws_bytes(d.rows_full, d.D, false));
     if (d.nrec) up(image_readout_ws_bytes(d.rows_rec, d.D, false));
     up(image_readout_ws_bytes(d.FF, d.D, true));
+    if (d.nrec && s->layer_formats) {   // separate a / b readouts behind a layer's pending K slabs
+        size_t ab = 0;
+        for (int f : {RTA_Q4_K, RTA_Q6_K}) ab = std::max(ab, rta_gemv_workspace_bytes(f, d.H, d.D, d.B));
+        const size_t slabs = std::max(image_readout_ws_bytes(d.rows_rec, d.D, false),
+                                      rta_gemv_workspace_bytes(RTA_Q6_K | RTA_TILED, d.rows_rec, d.D, d.B));
+        up(((slabs + 255) & ~(size_t)255) + ab);
+    }
     return m;
 }
 
@@ -189,9 +210,8 @@ Work carve_work(const rta_hybrid_shape* s, const Dims& d, void* p, size_t* bytes
     w.normed = c.take<float>(B * d.D);
     w.proj = c.take<float>(B * std::max(d.nfull ? d.rows_full : 0, d.nrec ? d.rows_rec : 0));
     w.q = c.take<float>(B * std::max(1, d.hq * d.hd));
-    w.conv = c.take<float>(B * std::max(1, 3 * d.S));
-    w.decay = c.take<float>(B * std::max(1, d.H));
-    w.beta = c.take<float>(B * std::max(1, d.H));
+    w.ext_a = c.take<float>(B * std::max(1, d.H));
+    w.ext_b = c.take<float>(B * std::max(1, d.H));
     w.mix = c.take<float>(B * std::max(d.hq * d.hd, d.S));
     w.act = c.take<float>(B * d.FF);
     w.logits = c.take<float>(B * d.V);
@@ -290,44 +310,44 @@ int rta_hybrid_decode_step(const rta_hybrid_shape* shape, const rta_hybrid_weigh
     if (hipGetLastError() != hipSuccess) return RTA_ERR_LAUNCH;
     RTA_TRY(rta_embed(shape->fmt_embed, weights->embed, d.V, d.D, tokens, B, w.hidden, stream));
 
-    // With packed projections and one batch tile, the residual projections (O and
-    // down) leave their K slabs in the GEMM workspace and the next RMSNorm adds them
-    // into the residual stream (one kernel instead of a reduce and a norm).
-    const bool fuse = (pf & RTA_TILED) != 0 && B <= 32;
+    // Per matrix: packed formats at one batch tile run on the fused paths.  The residual
+    // projections (O and down) then leave their K slabs in the GEMM workspace and the
+    // next norm adds them into the residual stream; the norm in front of a packed
+    // in-projection or gate/up pair writes x as the readout's matrix-core image
+    // (w.ximg), the one in front of the packed LM head h * w with the row factor
+    // deferred to the readout (rn).
+    auto fmt_of = [&](int f) { return shape->layer_formats ? f : pf; };
+    auto fused = [&](int f) { return (f & RTA_TILED) != 0 && B <= 32; };
+    auto imaged = [&](int f) {
+        return fused(f) && d.D <= 4096 && (f == (RTA_Q4_K | RTA_TILED) || f == (RTA_Q6_K | RTA_TILED));
+    };
     int pending = 0;   // K slabs of the last residual projection still in gemm_ws
-    auto residual_proj = [&](const void* wm, int cols, const float* x) -> int {
-        if (!fuse) return rta_gemv(pf, wm, d.D, cols, x, B, w.hidden, RTA_EPI_ACCUMULATE, w.gemm_ws, w.gemm_bytes,
-                                   stream);
+    auto residual_proj = [&](int f, const void* wm, int cols, const float* x) -> int {
+        if (!fused(f))
+            return rta_gemv(f, wm, d.D, cols, x, B, w.hidden, RTA_EPI_ACCUMULATE, w.gemm_ws, w.gemm_bytes, stream);
         int ns = 1;
-        const int rc = tiled_partials(pf, wm, d.D, cols, x, B, w.hidden, true, w.gemm_ws, w.gemm_bytes, s, &ns);
+        const int rc = tiled_partials(f, wm, d.D, cols, x, B, w.hidden, true, w.gemm_ws, w.gemm_bytes, s, &ns);
         pending = ns > 1 ? ns : 0;
         return rc;
     };
-    // With packed readouts the RMSNorm factor of each row is applied by the readout that
-    // takes w.normed (h * w is written and rn describes the factor): the residual add
-    // then spreads over several blocks per row.  deferred = false: w.normed is final.
+    // The norm in front of a consumer of format f.  keep_fp32: w.normed must hold x in
+    // fp32 as well (a separate readout reads it), h * w when rn is set.
     RowNorm rn{};
-    // With packed Q4_K / Q6_K projections the norm in front of the in-projection and the
-    // gate/up pair writes x straight into the readout's matrix-core image (w.ximg).
-    const bool img = fuse && d.D <= 4096 && (pf == (RTA_Q4_K | RTA_TILED) || pf == (RTA_Q6_K | RTA_TILED));
-    auto norm_image = [&](const float* nw) -> int {
-        const int rc = residual_norm_image(pf, w.hidden, static_cast<const float*>(w.gemm_ws), pending, nw, B, d.D,
-                                           w.rms, w.ximg, s);
-        rn = RowNorm{reinterpret_cast<const float4*>(w.rms), (float)d.D, eps};
-        pending = 0;
-        return rc;
-    };
-    auto norm = [&](const float* nw, bool deferred) -> int {
+    auto norm = [&](const float* nw, int f, bool keep_fp32) -> int {
         rn = RowNorm{};
-        deferred = deferred && d.D <= 4096;
-        if (!fuse) return rta_rmsnorm(w.hidden, nw, B, d.D, eps, w.normed, stream);
         const float* part = static_cast<const float*>(w.gemm_ws);
         int rc;
-        if (deferred) {
+        if (imaged(f)) {
+            rc = residual_norm_image(f, w.hidden, part, pending, nw, B, d.D, w.rms, keep_fp32 ? w.normed : nullptr,
+                                     w.ximg, s);
+            rn = RowNorm{reinterpret_cast<const float4*>(w.rms), (float)d.D, eps};
+        } else if (fused(f) && d.D <= 4096) {
             rc = residual_norm_deferred(w.hidden, part, pending, nw, B, d.D, w.normed, w.rms, s);
             rn = RowNorm{reinterpret_cast<const float4*>(w.rms), (float)d.D, eps};
-        } else {
+        } else if (pending) {
             rc = residual_rmsnorm(w.hidden, part, pending, nw, B, d.D, eps, w.normed, s);
+        } else {
+            rc = rta_rmsnorm(w.hidden, nw, B, d.D, eps, w.normed, stream);
         }
         pending = 0;
         return rc;
@@ -336,15 +356,20 @@ int rta_hybrid_decode_step(const rta_hybrid_shape* shape, const rta_hybrid_weigh
     int lf = 0, lr = 0;
     for (int l = 0; l < d.L; ++l) {
         const rta_hybrid_layer& lw = weights->layers[l];
-        RTA_TRY(img ? norm_image(lw.norm_in) : norm(lw.norm_in, fuse));
+        const int fi = fmt_of(lw.fmt_in), fo = fmt_of(lw.fmt_o), fgu = fmt_of(lw.fmt_gate_up),
+                  fd = fmt_of(lw.fmt_down);
         if (is_full(shape, l)) {
-            // op 2 index 5 (q | k | v), ops 14 + 3, op 34, attention, op 2 index 2
-            if (img)
-                RTA_TRY(image_readout(pf, kReadStore, lw.w_in, nullptr, d.rows_full, d.D, w.ximg, B, w.proj, true,
+            // op 2 index 5 (q | k | v | gate), ops 14 + 3, op 34, attention, op 2 index 2
+            RTA_TRY(norm(lw.norm_in, fi, false));
+            if (imaged(fi))
+                RTA_TRY(image_readout(fi, kReadStore, lw.w_in, nullptr, d.rows_full, d.D, w.ximg, B, w.proj, true,
                                       w.gemm_ws, w.gemm_bytes, s, nullptr, rn));
-            else
-                RTA_TRY(projection_store(pf, lw.w_in, d.rows_full, d.D, w.normed, B, w.proj, w.gemm_ws, w.gemm_bytes,
+            else if (rn.part)
+                RTA_TRY(projection_store(fi, lw.w_in, d.rows_full, d.D, w.normed, B, w.proj, w.gemm_ws, w.gemm_bytes,
                                          s, rn));
+            else
+                RTA_TRY(rta_gemv(fi, lw.w_in, d.rows_full, d.D, w.normed, B, w.proj, RTA_EPI_STORE, w.gemm_ws,
+                                 w.gemm_bytes, stream));
             hipLaunchKernelGGL(qk_norm_rope_kernel, dim3((d.hq + d.hkv + 3) / 4, B), dim3(256), 0, s, w.proj,
                                d.rows_full, d.hq, d.hkv, lw.q_norm, lw.k_norm, eps, w.pos, shape->rope_rotary,
                                shape->rope_theta, w.q);
@@ -353,58 +378,80 @@ int rta_hybrid_decode_step(const rta_hybrid_shape* shape, const rta_hybrid_weigh
             RTA_TRY(rta_pack_history(w.proj + d.hq * d.hd, d.rows_full, w.proj + (d.hq + d.hkv) * d.hd, d.rows_full,
                                      B, d.kvw, shape->fmt_k, shape->fmt_v, w.slots + (size_t)lf * B,
                                      (int64_t)B * d.cap, packets, stream));
-            RTA_TRY(rta_decode_attention(w.q, B, d.hq, d.hkv, d.hd, packets, shape->fmt_k, shape->fmt_v,
-                                         st.base + (size_t)lf * B, w.visible, d.cap, (int64_t)B * d.cap, d.cap,
-                                         nullptr, w.mix, nullptr, nullptr, w.attn_ws, w.attn_bytes, stream));
-            RTA_TRY(residual_proj(lw.w_o, d.hq * d.hd, w.mix));
+            const float* gate = shape->attn_gate ? w.proj + (d.hq + 2 * d.hkv) * d.hd : nullptr;
+            RTA_TRY(decode_attention_gate_stride(w.q, B, d.hq, d.hkv, d.hd, packets, shape->fmt_k, shape->fmt_v,
+                                                 st.base + (size_t)lf * B, w.visible, d.cap, (int64_t)B * d.cap,
+                                                 d.cap, gate, d.rows_full, w.mix, nullptr, nullptr, w.attn_ws,
+                                                 w.attn_bytes, stream));
+            RTA_TRY(residual_proj(fo, lw.w_o, d.hq * d.hd, w.mix));
             ++lf;
         } else {
             // op 2 index 5 (q | k | v | z | a | b), ops 18-21 and 15, op 2 index 2
-            if (fuse) {   // the fused middle reads the in-projection's K slabs itself
-                int ns = 1;
-                if (img)
-                    RTA_TRY(image_readout(pf, kReadStore, lw.w_in, nullptr, d.rows_rec, d.D, w.ximg, B, w.proj, false,
-                                          w.gemm_ws, w.gemm_bytes, s, &ns, rn));
-                else
-                    RTA_TRY(tiled_partials(pf, lw.w_in, d.rows_rec, d.D, w.normed, B, w.proj, false, w.gemm_ws,
-                                           w.gemm_bytes, s, &ns, rn));
-                const bool slabs = ns > 1;
-                RTA_TRY(recurrent_mix(slabs ? static_cast<const float*>(w.gemm_ws) : w.proj,
-                                      (int64_t)kSlabBatch * d.rows_rec, d.rows_rec, slabs ? ns : 1,
-                                      st.conv + (size_t)lr * B * 3 * d.S * 3, lw.conv_w, lw.a_log, lw.dt_bias,
-                                      st.rec + (size_t)lr * B * d.H * d.hd * d.hd, lw.out_norm, B, d.H, eps, w.mix,
-                                      d.S, s));
-            } else {
-                RTA_TRY(rta_gemv(pf, lw.w_in, d.rows_rec, d.D, w.normed, B, w.proj, RTA_EPI_STORE, w.gemm_ws,
+            const bool ext = lw.w_a != nullptr;
+            if (ext && !lw.w_b) return RTA_ERR_NULL;
+            const int rows = d.rows_rec - (ext ? 2 * d.H : 0);
+            RTA_TRY(norm(lw.norm_in, fi, ext));
+            int ns = 1;   // K slabs the middle adds (1: the rows are final in w.proj)
+            if (imaged(fi))
+                RTA_TRY(image_readout(fi, kReadStore, lw.w_in, nullptr, rows, d.D, w.ximg, B, w.proj, false,
+                                      w.gemm_ws, w.gemm_bytes, s, &ns, rn));
+            else if (rn.part)
+                RTA_TRY(tiled_partials(fi, lw.w_in, rows, d.D, w.normed, B, w.proj, false, w.gemm_ws, w.gemm_bytes,
+                                       s, &ns, rn));
+            else
+                RTA_TRY(rta_gemv(fi, lw.w_in, rows, d.D, w.normed, B, w.proj, RTA_EPI_STORE, w.gemm_ws,
                                  w.gemm_bytes, stream));
-                RTA_TRY(rta_delta_gates(w.proj + 4 * d.S, w.proj + 4 * d.S + d.H, d.rows_rec, lw.a_log, lw.dt_bias, B,
-                                        d.H, w.decay, w.beta, stream));
-                RTA_TRY(rta_short_conv(w.proj, d.rows_rec, st.conv + (size_t)lr * B * 3 * d.S * 3, lw.conv_w, B, d.H,
-                                       d.hd, eps, w.conv, stream));
-                RTA_TRY(rta_delta_rule(st.rec + (size_t)lr * B * d.H * d.hd * d.hd, w.conv, 3 * d.S, w.decay, w.beta,
-                                       B, d.H, d.hd, lw.out_norm, w.proj + 3 * d.S, d.rows_rec, eps, w.mix, d.S,
-                                       stream));
+            const bool slabs = ns > 1;
+            // the a / b readouts into the slabs' place are done before the middle reads them;
+            // with slabs pending they use the workspace after them
+            if (ext) {
+                const int fab = fmt_of(lw.fmt_ab);
+                if (fab & RTA_TILED) return RTA_ERR_FORMAT;   // (x is not staged for them)
+                uint8_t* ws2 = static_cast<uint8_t*>(w.gemm_ws);
+                size_t ws2_bytes = w.gemm_bytes;
+                if (slabs) {
+                    const size_t used = ((size_t)ns * kSlabBatch * rows * sizeof(float) + 255) & ~(size_t)255;
+                    if (used > ws2_bytes) return RTA_ERR_WORKSPACE;
+                    ws2 += used;
+                    ws2_bytes -= used;
+                }
+                RTA_TRY(rta_gemv(fab, lw.w_a, d.H, d.D, w.normed, B, w.ext_a, RTA_EPI_STORE, ws2, ws2_bytes, stream));
+                RTA_TRY(rta_gemv(fab, lw.w_b, d.H, d.D, w.normed, B, w.ext_b, RTA_EPI_STORE, ws2, ws2_bytes, stream));
             }
-            RTA_TRY(residual_proj(lw.w_o, d.S, w.mix));
+            RTA_TRY(recurrent_mix(slabs ? static_cast<const float*>(w.gemm_ws) : w.proj, (int64_t)kSlabBatch * rows,
+                                  rows, slabs ? ns : 1, d.KH, ext ? w.ext_a : nullptr, ext ? w.ext_b : nullptr, d.H,
+                                  rn, st.conv + (size_t)lr * B * 3 * d.S * 3, lw.conv_w, lw.a_log, lw.dt_bias,
+                                  st.rec + (size_t)lr * B * d.H * d.hd * d.hd, lw.out_norm, B, d.H, eps, w.mix, d.S,
+                                  s));
+            RTA_TRY(residual_proj(fo, lw.w_o, d.S, w.mix));
             ++lr;
         }
         // op 1 index 1, then the SwiGLU MLP with the residual add (executeMLP)
-        RTA_TRY(img ? norm_image(lw.norm_post) : norm(lw.norm_post, fuse));
-        if (img) {
-            RTA_TRY(image_readout(pf, kReadSwiglu, lw.w_gate, lw.w_up, d.FF, d.D, w.ximg, B, w.act, true, w.gemm_ws,
+        RTA_TRY(norm(lw.norm_post, fgu, false));
+        if (imaged(fgu))
+            RTA_TRY(image_readout(fgu, kReadSwiglu, lw.w_gate, lw.w_up, d.FF, d.D, w.ximg, B, w.act, true, w.gemm_ws,
                                   w.gemm_bytes, s, nullptr, rn));
-            RTA_TRY(residual_proj(lw.w_down, d.FF, w.act));
-        } else if (fuse) {
-            RTA_TRY(swiglu_activation(pf, lw.w_gate, lw.w_up, d.FF, d.D, w.normed, B, w.act, w.gemm_ws, w.gemm_bytes, s,
-                                      rn));
-            RTA_TRY(residual_proj(lw.w_down, d.FF, w.act));
-        } else {
-            RTA_TRY(rta_mlp_swiglu(pf, lw.w_gate, pf, lw.w_up, pf, lw.w_down, d.D, d.FF, w.normed, B, w.act, w.hidden,
-                                   RTA_EPI_ACCUMULATE, w.gemm_ws, w.gemm_bytes, stream));
-        }
+        else
+            RTA_TRY(swiglu_activation(fgu, lw.w_gate, lw.w_up, d.FF, d.D, w.normed, B, w.act, w.gemm_ws, w.gemm_bytes,
+                                      s, rn));
+        RTA_TRY(residual_proj(fd, lw.w_down, d.FF, w.act));
     }
-    // op 1 index 2, then the readout (Resident::word): logits and the next tokens
-    RTA_TRY(norm(weights->norm_final, fuse && (shape->fmt_lm & RTA_TILED) && B <= 32));
+    // op 1 index 2, then the readout (Resident::word): logits and the next tokens; the
+    // packed LM head takes the row factor itself (never an image: it is read once)
+    {
+        const int fl = shape->fmt_lm;
+        rn = RowNorm{};
+        const float* part = static_cast<const float*>(w.gemm_ws);
+        if (fused(fl) && d.D <= 4096) {
+            RTA_TRY(residual_norm_deferred(w.hidden, part, pending, weights->norm_final, B, d.D, w.normed, w.rms, s));
+            rn = RowNorm{reinterpret_cast<const float4*>(w.rms), (float)d.D, eps};
+        } else if (pending) {
+            RTA_TRY(residual_rmsnorm(w.hidden, part, pending, weights->norm_final, B, d.D, eps, w.normed, s));
+        } else {
+            RTA_TRY(rta_rmsnorm(w.hidden, weights->norm_final, B, d.D, eps, w.normed, stream));
+        }
+        pending = 0;
+    }
     RTA_TRY(lm_head_rownorm(shape->fmt_lm, weights->lm_head, d.V, d.D, w.normed, B, shape->margin,
                             logits_out ? logits_out : w.logits, tokens, w.lm_ws, w.lm_bytes, s, rn));
 #undef RTA_TRY

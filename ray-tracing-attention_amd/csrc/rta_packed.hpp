@@ -44,12 +44,12 @@ constexpr int slab_capacity() {
 // the block = superblock 4c + k.  Rows b >= batch (up to the image's 16 NBT rows) write
 // zeros.  For b < batch: hidden[b] += the K-slab partials [slab][32][width] (slab order)
 // and ss[4 b + c] = the chunk's sum of hidden^2 (entries past the chunks zero), as
-// residual_norm_deferred_kernel.
+// residual_norm_deferred_kernel; out (may be null) = hidden * w in fp32 as well.
 template <int FMT, int NBT>
 __global__ void __launch_bounds__(256) residual_norm_image_kernel(float* __restrict__ hidden,
                                                                   const float* __restrict__ part, int nslab,
                                                                   const float* __restrict__ w, int width, int batch,
-                                                                  float* __restrict__ ss,
+                                                                  float* __restrict__ ss, float* __restrict__ out,
                                                                   XImage<NBT>* __restrict__ img) {
     __shared__ float red[4];
     const int c = blockIdx.x, b = blockIdx.y, lane = threadIdx.x & 63;
@@ -74,6 +74,7 @@ __global__ void __launch_bounds__(256) residual_norm_image_kernel(float* __restr
         sq = v.x * v.x + v.y * v.y + v.z * v.z + v.w * v.w;
         const float4 g = reinterpret_cast<const float4*>(w)[i];
         v = float4{v.x * g.x, v.y * g.y, v.z * g.z, v.w * g.w};
+        if (out) reinterpret_cast<float4*>(out + (int64_t)b * width)[i] = v;
     }
     if (live) {
         // the block sum over every thread (threads past the row hold 0)

@@ -335,12 +335,17 @@ __global__ void __launch_bounds__(256) delta_rule_kernel(float* __restrict__ sta
 //   gates (op 18); short convolution + SiLU + L2 norm of q and k (ops 19, 20); the
 //   delta rule (op 21) and the gated RMSNorm (op 15).
 // Row r of sequence b is sum_k proj[k * slab_stride + b * row_stride + r], k < nslab.
+// q and k hold key_heads heads (KW = key_heads hd rows each): head h reads head
+// h % key_heads, while the convolution runs over the heads' own channels (weights and
+// window of channel part W + h hd + c).  With ext_a, the gate inputs are ext_a[b
+// ext_stride + h] and ext_b[...] times the row's RMSNorm factor rn (1 without rn).
 template <int NS>
 __global__ void __launch_bounds__(256) recurrent_mix_kernel(
-    const float* __restrict__ proj, int64_t slab_stride, int row_stride, int nslab, float* __restrict__ conv_state,
-    const float* __restrict__ conv_w, const float* __restrict__ a_log, const float* __restrict__ dt_bias,
-    float* __restrict__ state, const float* __restrict__ norm_w, int heads, float eps, float* __restrict__ out,
-    int out_stride) {
+    const float* __restrict__ proj, int64_t slab_stride, int row_stride, int nslab, int key_heads,
+    const float* __restrict__ ext_a, const float* __restrict__ ext_b, int ext_stride, const RowNorm rn,
+    float* __restrict__ conv_state, const float* __restrict__ conv_w, const float* __restrict__ a_log,
+    const float* __restrict__ dt_bias, float* __restrict__ state, const float* __restrict__ norm_w, int heads,
+    float eps, float* __restrict__ out, int out_stride) {
     constexpr int hd = 128, kRows = hd / 4;
     __shared__ float qkv_s[3][hd];
     __shared__ float z_s[hd];
@@ -349,7 +354,8 @@ __global__ void __launch_bounds__(256) recurrent_mix_kernel(
     __shared__ float red[4];
     const int h = blockIdx.x, b = blockIdx.y, tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int W = heads * hd, W3 = 3 * W;
+    const int W = heads * hd, W3 = 3 * W, KW = key_heads * hd, hk = h % key_heads;
+    const int row_v = 2 * KW, row_z = row_v + W, row_a = row_z + W;
     const float* src = proj + (int64_t)b * row_stride;
     // in-projection rows: every slab load is issued at once (indices clamped to the
     // last slab, which is not added twice), then summed in slab order
@@ -375,8 +381,8 @@ __global__ void __launch_bounds__(256) recurrent_mix_kernel(
     if (conv) {
 #pragma unroll
         for (int part = 0; part < 3; ++part) {
-            const int pc = part * W + h * hd + c;
-            load_row(pc, raw[part]);
+            const int pc = part * W + h * hd + c;   // the channel; its input row:
+            load_row(part < 2 ? part * KW + hk * hd + c : row_v + h * hd + c, raw[part]);
             wp[part] = *reinterpret_cast<const float4*>(conv_w + (int64_t)pc * 4);
             const float* st = conv_state + ((int64_t)b * W3 + pc) * 3;
             sv[part][0] = st[0];
@@ -384,9 +390,11 @@ __global__ void __launch_bounds__(256) recurrent_mix_kernel(
             sv[part][2] = st[2];
         }
     } else {
-        load_row(W3 + h * hd + c, raw[0]);
-        load_row(4 * W + h, ab[0]);
-        load_row(4 * W + heads + h, ab[1]);
+        load_row(row_z + h * hd + c, raw[0]);
+        if (!ext_a) {
+            load_row(row_a + h, ab[0]);
+            load_row(row_a + heads + h, ab[1]);
+        }
     }
     asm volatile("" ::: "memory");   // the state loads stay behind the loads above
     float2* S = reinterpret_cast<float2*>(state + ((int64_t)b * heads + h) * hd * hd) + wave * kRows * (hd / 2) + lane;
@@ -411,10 +419,19 @@ __global__ void __launch_bounds__(256) recurrent_mix_kernel(
     } else {
         z_s[c] = sum_row(raw[0]);
         if (c == 0) {
-            const float av = sum_row(ab[0]) + dt_bias[h];
+            float ga, gb;
+            if (ext_a) {
+                const float f = rn.part ? row_norm_factor(rn, rn.part[b]) : 1.0f;
+                ga = ext_a[(int64_t)b * ext_stride + h] * f;
+                gb = ext_b[(int64_t)b * ext_stride + h] * f;
+            } else {
+                ga = sum_row(ab[0]);
+                gb = sum_row(ab[1]);
+            }
+            const float av = ga + dt_bias[h];
             const float sp = fmaxf(av, 0.0f) + log1pf(expf(-fabsf(av)));   // softplus, resident_common.glsl:80
             gates_s[0] = expf(-expf(a_log[h]) * sp);
-            gates_s[1] = detector_sigmoid(sum_row(ab[1]));
+            gates_s[1] = detector_sigmoid(gb);
         }
     }
     // L2 norm of q and k over the head (waves 0 and 1 hold its 128 coordinates)
@@ -468,15 +485,21 @@ __global__ void __launch_bounds__(256) recurrent_mix_kernel(
     if (tid < hd) out[(int64_t)b * out_stride + h * hd + tid] = v * inv * norm_w[h * hd + tid] * silu(z_s[tid]);
 }
 
-int recurrent_mix(const float* proj, int64_t slab_stride, int row_stride, int nslab, float* conv_state,
-                  const float* conv_w, const float* a_log, const float* dt_bias, float* state, const float* norm_w,
-                  int batch, int heads, float eps, float* out, int out_stride, hipStream_t s) {
+int recurrent_mix(const float* proj, int64_t slab_stride, int row_stride, int nslab, int key_heads, const float* ext_a,
+                  const float* ext_b, int ext_stride, const RowNorm& rn, float* conv_state, const float* conv_w,
+                  const float* a_log, const float* dt_bias, float* state, const float* norm_w, int batch, int heads,
+                  float eps, float* out, int out_stride, hipStream_t s) {
     if (!proj || !conv_state || !conv_w || !a_log || !dt_bias || !state || !norm_w || !out) return RTA_ERR_NULL;
-    if (batch <= 0 || heads <= 0 || nslab <= 0 || row_stride < 4 * heads * 128 + 2 * heads) return RTA_ERR_SHAPE;
+    if ((ext_a == nullptr) != (ext_b == nullptr)) return RTA_ERR_NULL;
+    if (key_heads <= 0 || key_heads > heads) return RTA_ERR_RANGE;
+    const int rows = 2 * key_heads * 128 + 2 * heads * 128 + (ext_a ? 0 : 2 * heads);
+    if (batch <= 0 || heads <= 0 || nslab <= 0 || row_stride < rows || (ext_a && ext_stride < heads))
+        return RTA_ERR_SHAPE;
     if (nslab > 16) return RTA_ERR_RANGE;
     const dim3 g(heads, batch), blk(256);
 #define RTA_MIX(NS) hipLaunchKernelGGL(recurrent_mix_kernel<NS>, g, blk, 0, s, proj, slab_stride, row_stride, nslab, \
-                                       conv_state, conv_w, a_log, dt_bias, state, norm_w, heads, eps, out, out_stride)
+                                       key_heads, ext_a, ext_b, ext_stride, rn, conv_state, conv_w, a_log, dt_bias,  \
+                                       state, norm_w, heads, eps, out, out_stride)
     if (nslab == 1) RTA_MIX(1);
     else if (nslab == 2) RTA_MIX(2);
     else if (nslab <= 4) RTA_MIX(4);

@@ -21,12 +21,15 @@ class HybridShape(ctypes.Structure):
     _fields_ = [("hidden", _i), ("layers", _i), ("full_every", _i), ("q_heads", _i), ("kv_heads", _i),
                 ("head_dim", _i), ("rec_heads", _i), ("ff", _i), ("vocab", _i), ("capacity", _i),
                 ("fmt_embed", _i), ("fmt_proj", _i), ("fmt_lm", _i), ("fmt_k", _i), ("fmt_v", _i),
-                ("rope_rotary", _i), ("eps", _f), ("margin", _f), ("rope_theta", _d)]
+                ("rope_rotary", _i), ("eps", _f), ("margin", _f), ("rope_theta", _d),
+                ("attn_gate", _i), ("rec_key_heads", _i), ("layer_formats", _i)]
 
 
 class HybridLayer(ctypes.Structure):
     _fields_ = [(n, _p) for n in ("norm_in", "norm_post", "w_in", "w_o", "w_gate", "w_up", "w_down", "q_norm",
-                                  "k_norm", "conv_w", "a_log", "dt_bias", "out_norm")]
+                                  "k_norm", "conv_w", "a_log", "dt_bias", "out_norm")] + \
+               [("fmt_in", _i), ("fmt_o", _i), ("fmt_gate_up", _i), ("fmt_down", _i), ("w_a", _p), ("w_b", _p),
+                ("fmt_ab", _i)]
 
 
 class HybridWeights(ctypes.Structure):
@@ -89,10 +92,25 @@ def _near_one(n, gen, dev, spread=0.05):
     return (1.0 + spread * torch.randn(n, device=dev, generator=gen)).float()
 
 
-class DecodeModel:
-    """Device weights + state of a hybrid decoder and its graph-replayable decode step."""
+def random_float_matrix(fmt, rows, cols, gen, dev, scale=0.02):
+    """A [rows x cols] F32 / F16 / BF16 matrix (as row bytes) of N(0, scale^2) values."""
+    v = torch.randn(rows, cols, device=dev, generator=gen) * scale
+    if fmt == _lib.F32:
+        return v.contiguous().view(torch.uint8).view(rows, -1)
+    if fmt == _lib.F16:
+        return v.half().contiguous().view(torch.uint8).view(rows, -1)
+    return (v.contiguous().view(torch.int32) >> 16).to(torch.int16).view(torch.uint8).view(rows, -1)
 
-    def __init__(self, shape, batch, ctx, seed=20261115, dev="cuda:0", keep_gguf=False):
+
+class DecodeModel:
+    """Device weights + state of a hybrid decoder and its graph-replayable decode step.
+
+    With shape.layer_formats, layer_fmts(l, full) gives each layer's formats as a dict
+    {"in", "o", "gate_up", "down", "ab"}; separate_ab keeps the delta-net a / b rows as
+    matrices of their own (w_a, w_b).  self.fmts names each matrix's format."""
+
+    def __init__(self, shape, batch, ctx, seed=20261115, dev="cuda:0", keep_gguf=False, layer_fmts=None,
+                 separate_ab=False):
         self.lib = _lib_h()
         self.shape = shape
         self.batch = batch
@@ -103,9 +121,20 @@ class DecodeModel:
         self._keep = []
         self.gguf = {} if keep_gguf else None   # name -> GGUF matrix (tests feed these to the oracle)
         self.mats = {}                            # name -> device matrix as the step reads it
+        self.fmts = {}                            # name -> its format code
         base_fmt = lambda f: f & 0xff
 
         def mat(fmt, rows, cols, d_scale=0.01, small_rows=0, name=None):
+            if name:
+                self.fmts[name] = fmt
+            if base_fmt(fmt) not in (Q4_K, Q6_K):
+                w = random_float_matrix(fmt, rows, cols, gen, self.dev, 1e-4 if small_rows else 0.02)
+                if self.gguf is not None and name:
+                    self.gguf[name] = w.cpu().numpy()
+                self._keep.append(w)
+                if name:
+                    self.mats[name] = w
+                return w
             w = random_kquant(base_fmt(fmt), rows, cols, gen, self.dev, d_scale)
             if small_rows:   # the delta-net a / b rows: tiny, so decay stays near its target
                 nsb = cols // 256
@@ -133,20 +162,32 @@ class DecodeModel:
             return t.data_ptr()
 
         hd, S, H = s.head_dim, s.rec_heads * s.head_dim, s.rec_heads
+        KH = s.rec_key_heads or H
+        self.separate_ab = separate_ab
         self.layers = (HybridLayer * s.layers)()
         for l in range(s.layers):
             L = self.layers[l]
             L.norm_in = vec(_near_one(s.hidden, gen, self.dev), f"{l}.norm_in")
             L.norm_post = vec(_near_one(s.hidden, gen, self.dev), f"{l}.norm_post")
             full = s.full_every > 0 and l % s.full_every == s.full_every - 1
+            lf = layer_fmts(l, full) if (s.layer_formats and layer_fmts) else {}
+            f_in, f_o = lf.get("in", s.fmt_proj), lf.get("o", s.fmt_proj)
+            f_gu, f_d, f_ab = lf.get("gate_up", s.fmt_proj), lf.get("down", s.fmt_proj), lf.get("ab", s.fmt_proj)
+            L.fmt_in, L.fmt_o, L.fmt_gate_up, L.fmt_down, L.fmt_ab = f_in, f_o, f_gu, f_d, f_ab
             if full:
-                L.w_in = mat(s.fmt_proj, (s.q_heads + 2 * s.kv_heads) * hd, s.hidden, name=f"{l}.w_in").data_ptr()
-                L.w_o = mat(s.fmt_proj, s.hidden, s.q_heads * hd, name=f"{l}.w_o").data_ptr()
+                rows = (s.q_heads * (2 if s.attn_gate else 1) + 2 * s.kv_heads) * hd
+                L.w_in = mat(f_in, rows, s.hidden, name=f"{l}.w_in").data_ptr()
+                L.w_o = mat(f_o, s.hidden, s.q_heads * hd, name=f"{l}.w_o").data_ptr()
                 L.q_norm = vec(_near_one(s.q_heads * hd, gen, self.dev), f"{l}.q_norm")
                 L.k_norm = vec(_near_one(s.kv_heads * hd, gen, self.dev), f"{l}.k_norm")
             else:
-                L.w_in = mat(s.fmt_proj, 4 * S + 2 * H, s.hidden, small_rows=2 * H, name=f"{l}.w_in").data_ptr()
-                L.w_o = mat(s.fmt_proj, s.hidden, S, name=f"{l}.w_o").data_ptr()
+                rows = 2 * KH * hd + 2 * S + (0 if separate_ab else 2 * H)
+                L.w_in = mat(f_in, rows, s.hidden, small_rows=0 if separate_ab else 2 * H,
+                             name=f"{l}.w_in").data_ptr()
+                if separate_ab:
+                    L.w_a = mat(f_ab, H, s.hidden, small_rows=H, name=f"{l}.w_a").data_ptr()
+                    L.w_b = mat(f_ab, H, s.hidden, small_rows=H, name=f"{l}.w_b").data_ptr()
+                L.w_o = mat(f_o, s.hidden, S, name=f"{l}.w_o").data_ptr()
                 L.conv_w = vec((0.5 * torch.randn(3 * S, 4, device=self.dev, generator=gen)).float(), f"{l}.conv_w")
                 # decay ~ U(0.9, 0.999) at a = 0: exp(a_log) softplus(dt_bias) = -ln(decay)
                 target = 0.9 + 0.099 * torch.rand(H, device=self.dev, generator=gen)
@@ -155,9 +196,9 @@ class DecodeModel:
                 L.a_log = vec(torch.log(-torch.log(target) / sp).float(), f"{l}.a_log")
                 L.dt_bias = vec(dt.float(), f"{l}.dt_bias")
                 L.out_norm = vec(_near_one(S, gen, self.dev), f"{l}.out_norm")
-            L.w_gate = mat(s.fmt_proj, s.ff, s.hidden, name=f"{l}.w_gate").data_ptr()
-            L.w_up = mat(s.fmt_proj, s.ff, s.hidden, name=f"{l}.w_up").data_ptr()
-            L.w_down = mat(s.fmt_proj, s.hidden, s.ff, name=f"{l}.w_down").data_ptr()
+            L.w_gate = mat(f_gu, s.ff, s.hidden, name=f"{l}.w_gate").data_ptr()
+            L.w_up = mat(f_gu, s.ff, s.hidden, name=f"{l}.w_up").data_ptr()
+            L.w_down = mat(f_d, s.hidden, s.ff, name=f"{l}.w_down").data_ptr()
         self.embed = random_kquant(s.fmt_embed, s.vocab, s.hidden, gen, self.dev)
         self.norm_final = _near_one(s.hidden, gen, self.dev)
         if self.gguf is not None:

@@ -24,7 +24,9 @@ def reference_step(m, tokens, ctx, rec, conv, packets_after):
     s, g = m.shape, m.gguf
     hq, hkv, hd, H, D, B, cap = s.q_heads, s.kv_heads, s.head_dim, s.rec_heads, s.hidden, m.batch, s.capacity
     S = H * hd
-    Q4, Q6 = orc.Q4_K, orc.Q6_K
+    KH = s.rec_key_heads or H
+    fmt = lambda name: m.fmts[name] & 0xff   # the GGUF format a (possibly packed) matrix came from
+    gemv = lambda name, rows, cols, x: orc.gemv_f64(fmt(name), g[name], rows, cols, x.astype(f32))
     x = orc.embed(s.fmt_embed, g["embed"], s.vocab, D, tokens).astype(np.float64)
     new_rec, new_conv = rec.astype(np.float64).copy(), conv.copy()
     kv_new = []
@@ -32,37 +34,49 @@ def reference_step(m, tokens, ctx, rec, conv, packets_after):
     for l in range(s.layers):
         n = orc.rmsnorm(x.astype(f32), g[f"{l}.norm_in"], s.eps)
         if l % s.full_every == s.full_every - 1:
-            p = orc.gemv_f64(Q4, g[f"{l}.w_in"], (hq + 2 * hkv) * hd, D, n.astype(f32))
+            rows = (hq * (2 if s.attn_gate else 1) + 2 * hkv) * hd
+            p = gemv(f"{l}.w_in", rows, D, n)
             q = orc.head_norm(p[:, :hq * hd].astype(f32), hq, hd, w=g[f"{l}.q_norm"], eps=s.eps)
             k = orc.head_norm(p[:, hq * hd:(hq + hkv) * hd].astype(f32), hkv, hd, w=g[f"{l}.k_norm"], eps=s.eps)
             q = np.stack([orc.rope(q[b].reshape(hq, hd).astype(f32), ctx[b], s.rope_rotary, s.rope_theta)
                           for b in range(B)])
             k = np.stack([orc.rope(k[b].reshape(hkv, hd).astype(f32), ctx[b], s.rope_rotary, s.rope_theta)
                           for b in range(B)]).reshape(B, -1)
-            kv_new.append((k, p[:, (hq + hkv) * hd:]))
+            kv_new.append((k, p[:, (hq + hkv) * hd:(hq + 2 * hkv) * hd]))
+            # the output gate (resident_ray.comp:75-76): rows after q | k | v
+            gate = p[:, (hq + 2 * hkv) * hd:].reshape(B, hq, hd).astype(f32) if s.attn_gate else None
             flat = packets_after[lf].reshape(B * cap, -1)
             attn, _, _ = orc.decode_attention(q.astype(f32), flat, s.fmt_k, s.fmt_v, [b * cap for b in range(B)],
-                                              [c + 1 for c in ctx], cap, hkv)
-            x = x + orc.gemv_f64(Q4, g[f"{l}.w_o"], D, hq * hd, attn.reshape(B, -1).astype(f32))
+                                              [c + 1 for c in ctx], cap, hkv, gate=gate)
+            x = x + gemv(f"{l}.w_o", D, hq * hd, attn.reshape(B, -1))
             lf += 1
         else:
-            p = orc.gemv_f64(Q4, g[f"{l}.w_in"], 4 * S + 2 * H, D, n.astype(f32))
-            decay, beta = orc.delta_gates(p[:, 4 * S:4 * S + H].astype(f32), p[:, 4 * S + H:].astype(f32),
-                                          g[f"{l}.a_log"], g[f"{l}.dt_bias"])
-            y, ns = orc.short_conv(p[:, :3 * S].astype(f32), conv[lr], g[f"{l}.conv_w"], H, hd, s.eps)
+            sep = f"{l}.w_a" in g
+            rows = 2 * KH * hd + 2 * S + (0 if sep else 2 * H)
+            p = gemv(f"{l}.w_in", rows, D, n)
+            # q and k of delta-net head h are rows of key head h % KH: the key repeat of
+            # resident_quant.glsl:26 (mode 5) over the logical rows
+            rep = np.array([orc.remap_row(5, 0, 0, KH * hd, r) for r in range(S)])
+            qkv = np.concatenate((p[:, rep], p[:, KH * hd + rep], p[:, 2 * KH * hd:2 * KH * hd + S]), axis=1)
+            z = p[:, 2 * KH * hd + S:2 * KH * hd + 2 * S]
+            if sep:
+                a_in, b_in = gemv(f"{l}.w_a", H, D, n), gemv(f"{l}.w_b", H, D, n)
+            else:
+                a_in, b_in = p[:, 2 * KH * hd + 2 * S:2 * KH * hd + 2 * S + H], p[:, 2 * KH * hd + 2 * S + H:]
+            decay, beta = orc.delta_gates(a_in.astype(f32), b_in.astype(f32), g[f"{l}.a_log"], g[f"{l}.dt_bias"])
+            y, ns = orc.short_conv(qkv.astype(f32), conv[lr], g[f"{l}.conv_w"], H, hd, s.eps)
             new_conv[lr] = ns
             st, o = orc.delta_rule(rec[lr].astype(np.float64), y[:, :S], y[:, S:2 * S], y[:, 2 * S:], decay, beta)
             new_rec[lr] = st
-            o = orc.head_norm(o.astype(f32), H, hd, w=g[f"{l}.out_norm"], gate=p[:, 3 * S:4 * S].astype(f32),
-                              eps=s.eps)
-            x = x + orc.gemv_f64(Q4, g[f"{l}.w_o"], D, S, o.astype(f32))
+            o = orc.head_norm(o.astype(f32), H, hd, w=g[f"{l}.out_norm"], gate=z.astype(f32), eps=s.eps)
+            x = x + gemv(f"{l}.w_o", D, S, o)
             lr += 1
         n = orc.rmsnorm(x.astype(f32), g[f"{l}.norm_post"], s.eps)
-        _, y = orc.mlp_swiglu((Q4, Q4, Q4), g[f"{l}.w_gate"], g[f"{l}.w_up"], g[f"{l}.w_down"], D, s.ff,
-                              n.astype(f32))
+        _, y = orc.mlp_swiglu((fmt(f"{l}.w_gate"), fmt(f"{l}.w_up"), fmt(f"{l}.w_down")), g[f"{l}.w_gate"],
+                              g[f"{l}.w_up"], g[f"{l}.w_down"], D, s.ff, n.astype(f32))
         x = x + y
     n = orc.rmsnorm(x.astype(f32), g["norm_final"], s.eps)
-    logits = orc.gemv_f64(Q6, g["lm_head"], s.vocab, D, n.astype(f32))
+    logits = gemv("lm_head", s.vocab, D, n)
     return logits, new_rec, new_conv, kv_new
 
 

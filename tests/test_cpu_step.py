@@ -15,7 +15,7 @@ def small_model(rng, hidden=512, layers=4, full_every=2, hq=4, hkv=2, H=2, ff=51
     shape = SimpleNamespace(hidden=hidden, layers=layers, full_every=full_every, q_heads=hq, kv_heads=hkv,
                             head_dim=128, rec_heads=H, ff=ff, vocab=vocab, capacity=capacity, fmt_embed=orc.Q4_K,
                             fmt_proj=orc.Q4_K, fmt_lm=orc.Q6_K, fmt_k=orc.Q4_K, fmt_v=orc.Q6_K, rope_rotary=128,
-                            eps=1e-6, margin=1e-4, rope_theta=1e6)
+                            eps=1e-6, margin=1e-4, rope_theta=1e6, attn_gate=0, rec_key_heads=0, layer_formats=0)
     S = H * 128
     near1 = lambda n: (1.0 + 0.05 * rng.standard_normal(n)).astype(np.float32)  # noqa: E731
     g = {"embed": synth.random_matrix(rng, orc.Q4_K, vocab, hidden), "norm_final": near1(hidden),
@@ -59,7 +59,8 @@ def test_cpu_step_matches_fp64_composition():
     ctx = np.array([5, 17, 70], np.int32)                 # 70 > capacity: the ring has wrapped
     tokens = rng.integers(0, shape.vocab, B).astype(np.uint32)
     cpu = orc.CpuStep(shape, g)
-    m = SimpleNamespace(shape=shape, gguf=g, batch=B)
+    fmts = {k: (orc.Q6_K if k == "lm_head" else orc.Q4_K) for k in g}
+    m = SimpleNamespace(shape=shape, gguf=g, batch=B, fmts=fmts)
     for step in range(2):
         rec0, conv0, ctx0, tok0 = rec.copy(), conv.copy(), ctx.copy(), tokens.copy()
         logits = np.empty((B, shape.vocab), np.float32)

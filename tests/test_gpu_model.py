@@ -21,3 +21,31 @@ def test_hybrid_decode_steps(packed, hidden):
     ctx = [5, 17, 70]                                      # 70 > capacity: the ring has wrapped
     m = model.DecodeModel(shape, 3, ctx, seed=7, keep_gguf=True)
     check_steps(m, 2)
+
+
+# What the exporter emits beyond the plain layout (compiler/export.py:96-113): the
+# attention output gate, fewer delta-net key heads than heads (repeated), the a / b rows
+# as matrices of their own (F32, as ssm_alpha / ssm_beta), and a format per matrix --
+# packed, GGUF rows and float mixed within and across layers.  Batch 3 and 20 run the
+# fused paths (one batch tile of 16 and 32 rows), 40 the plain ones.
+def _exporter_fmts(l, full):
+    from rta._lib import BF16, F16, Q4_K, Q6_K, TILED
+    if full:
+        return {"in": Q4_K | TILED, "o": Q6_K, "gate_up": Q4_K | TILED, "down": Q6_K | TILED}
+    if l % 2:
+        return {"in": Q6_K | TILED, "o": Q4_K | TILED, "gate_up": Q4_K, "down": BF16, "ab": 0}
+    return {"in": Q4_K, "o": F16, "gate_up": Q6_K | TILED, "down": Q4_K | TILED, "ab": 0}
+
+
+@pytest.mark.parametrize("batch", [3, 20, 40])
+def test_hybrid_decode_steps_exported_layout(batch):
+    from rta import model
+    from rta._lib import Q4_K, Q6_K, TILED
+    shape = model.HybridShape(hidden=512, layers=4, full_every=2, q_heads=4, kv_heads=2, head_dim=128, rec_heads=4,
+                              ff=512, vocab=3001, capacity=64, fmt_embed=Q4_K, fmt_proj=Q4_K | TILED,
+                              fmt_lm=Q6_K | TILED, fmt_k=Q4_K, fmt_v=Q6_K, rope_rotary=64, eps=1e-6, margin=1e-4,
+                              rope_theta=1e6, attn_gate=1, rec_key_heads=2, layer_formats=1)
+    ctx = [(5 + 13 * b) % 90 for b in range(batch)]
+    m = model.DecodeModel(shape, batch, ctx, seed=11 + batch, keep_gguf=True, layer_fmts=_exporter_fmts,
+                          separate_ab=True)
+    check_steps(m, 2)
