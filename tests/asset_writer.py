@@ -1,10 +1,11 @@
 """Writes a synthetic model in the exporter's on-disk layout (test infrastructure).
 
-Restates ray_tracing/compiler/export.py:51-149 for given tensors instead of a GGUF /
-safetensors source: optical_model.bin (RTRES004 + 9 words + parameter words),
-geometry_weights.bin (raw payloads per layer, word padded), vocabulary.bin
-(RTBASQ01 + vocab, hidden + payloads) and model.json (the model_spec the worker
-reads).  Norm vectors are fp32; packed matrices are raw GGUF rows.
+The files and the meaning of each word are those compiler/export.py:51-149 produces
+(optical_model.bin: RTRES004, 9 words, then the parameter words; geometry_weights.bin:
+every layer's matrix payloads, word padded; vocabulary.bin: RTBASQ01, vocab, hidden,
+then the embedding and LM-head payloads; model.json with the model_spec the worker
+reads), written here from the word map below for given tensors instead of a GGUF /
+safetensors source.  Norm vectors are fp32; matrices are raw GGUF rows.
 """
 import json
 import struct
@@ -12,7 +13,40 @@ from pathlib import Path
 
 import numpy as np
 
-STRIDE = 64
+# ---- the word map of the parameter region (export.py:87-123) ----------------------
+STRIDE = 64          # words per layer record, after 32 global words
+GLOBAL_WORDS = 32
+G_DEPTH, G_BLOCKS, G_MIDDLE, G_FOUR = 0, 1, 2, 3
+G_OUTPUT_NORM, G_SPARE_VECTOR = 4, 7
+G_FLAGS = (11, 12)                     # both 1
+G_EMBED_CODE, G_EMBED_AT, G_LM_CODE, G_LM_AT = 13, 14, 15, 16
+L_NORM_IN, L_NORM_POST, L_ROTARY_ZERO, L_SPARE_VECTOR = 0, 1, 2, 5
+L_HEADS, L_NORM_A, L_NORM_B, L_KIND_A, L_MATRIX_START, L_MATRIX_WORDS, L_ROTARY, L_KIND_B = 23, 24, 25, 26, 27, 28, 29, 30
+L_OUT_NORM, L_CONV, L_DT_BIAS, L_A = 31, 34, 37, 38
+L_BETA, L_ALPHA = (35, 39), (36, 40)   # (payload word offset, format code) of a separate matrix
+
+
+def descriptor_word(index):
+    """First of the two words (offset, format | mode << 8) of projection descriptor index."""
+    return 32 if index == 8 else 9 + 2 * index
+
+
+# projections per layer kind: (descriptor index, tensor, mode, first row) -- the modes
+# and row offsets export.py:96-108 gives them
+def _full_projections(spec):
+    gate = spec.get("attention_gate", False)
+    rows = [(0, "attn_q.weight", 1 if gate else 3, 0), (1, "attn_k.weight", 3, 0), (8, "attn_v.weight", 3, 0),
+            (2, "attn_output.weight", 4, 0)]
+    return rows + ([(6, "attn_q.weight", 2, 0)] if gate else [])
+
+
+def _recurrent_projections(spec):
+    key = spec["state_key_heads"] * 128
+    return [(0, "attn_qkv.weight", 5, 0), (1, "attn_qkv.weight", 5, key), (8, "attn_qkv.weight", 0, 2 * key),
+            (2, "ssm_out.weight", 0, 0), (6, "attn_gate.weight", 0, 0)]
+
+
+_MLP = [(3, "ffn_gate.weight", 0, 0), (4, "ffn_down.weight", 0, 0), (5, "ffn_up.weight", 0, 0)]
 ROW = {0: 4.0, 1: 2.0, 30: 2.0, 12: 144 / 256, 14: 210 / 256}
 
 
@@ -20,118 +54,111 @@ def row_bytes(fmt, cols):
     return int(cols * ROW[fmt])
 
 
+class _Words:
+    """An append-only run of little-endian 32-bit words; add() returns where a block starts."""
+
+    def __init__(self, first=0):
+        self.blocks, self.size = [], first
+
+    def add(self, words):
+        at = self.size
+        self.blocks.append(words)
+        self.size += len(words)
+        return at
+
+    def add_floats(self, values):
+        return self.add(np.ascontiguousarray(values, dtype="<f4").ravel().view("<u4"))
+
+    def add_bytes(self, raw):
+        raw = np.ascontiguousarray(raw, np.uint8).ravel()
+        return self.add(np.concatenate((raw, np.zeros((-raw.size) % 4, np.uint8))).view("<u4"))
+
+    def array(self):
+        return np.concatenate(self.blocks) if self.blocks else np.zeros(0, "<u4")
+
+
+def _rotary_pairs(hd, r):
+    """The norm order of the detector's rotary-pair layout: exported index of axis i."""
+    order = np.arange(hd)
+    order[:r] = np.arange(r).reshape(2, r // 2).T.ravel()
+    return order
+
+
 def write(dest, spec, packed, floats):
     """spec: model_spec dict; packed: name -> (fmt, uint8 [rows, row_bytes]);
-    floats: name -> fp32 array (norms, conv, dt bias, a).  Returns the header words."""
+    floats: name -> fp32 array (norms, conv, dt bias, a).  Returns the parameter words."""
     dest = Path(dest)
     dest.mkdir(parents=True, exist_ok=True)
-    d, middle, vocab = spec["hidden_size"], spec["middle_size"], spec["vocabulary_size"]
-    types = spec["layer_types"]
-    depth = len(types)
-    hd, heads, kvh = spec["attention_head_dim"], spec["attention_heads"], spec["kv_heads"]
-    header = np.zeros(32 + depth * STRIDE, np.uint32)
-    header[:4] = [depth, depth, middle, 4]
-    header[11:13] = [1, 1]
-    parts, count = [], [len(header)]
+    d, middle, vocab, kinds = spec["hidden_size"], spec["middle_size"], spec["vocabulary_size"], spec["layer_types"]
+    hd, heads = spec["attention_head_dim"], spec["attention_heads"]
+    depth = len(kinds)
+    head = np.zeros(GLOBAL_WORDS + depth * STRIDE, "<u4")
+    vectors = _Words(first=len(head))          # parameter words after the header
+    matrices = _Words()                         # geometry_weights.bin
+    head[[G_DEPTH, G_BLOCKS, G_MIDDLE, G_FOUR]] = [depth, depth, middle, 4]
+    head[list(G_FLAGS)] = 1
+    head[G_OUTPUT_NORM] = vectors.add_floats(floats["output_norm.weight"])
+    head[G_SPARE_VECTOR] = vectors.add_floats(np.zeros(8))
+    for layer, kind in enumerate(kinds):
+        rec = head[GLOBAL_WORDS + layer * STRIDE:GLOBAL_WORDS + (layer + 1) * STRIDE]   # a view
+        name = lambda t: f"blk.{layer}.{t}"   # noqa: E731
+        first_word, placed = matrices.size, {}
 
-    def add(value):
-        v = np.ascontiguousarray(value, dtype="<f4").ravel().view("<u4")
-        start = count[0]
-        parts.append(v)
-        count[0] += len(v)
-        return start
+        def place(tensor):   # a payload once per layer, at its word offset inside the layer
+            if tensor not in placed:
+                fmt, raw = packed[name(tensor)]
+                placed[tensor] = (matrices.add_bytes(raw) - first_word, fmt)
+            return placed[tensor]
 
-    header[4] = add(floats["output_norm.weight"])
-    header[7] = add(np.zeros(8))
-    matrix_words = 0
-    with open(dest / "geometry_weights.bin", "wb") as stream:
-        for layer, kind in enumerate(types):
-            base, prefix, start, written = 32 + layer * STRIDE, f"blk.{layer}.", matrix_words, {}
+        rec[L_NORM_IN] = vectors.add_floats(floats[name("attn_norm.weight")])
+        rec[L_NORM_POST] = vectors.add_floats(floats[name("post_attention_norm.weight")])
+        rec[L_SPARE_VECTOR] = vectors.add_floats(np.zeros(8))
+        full = kind == "full"
 
-            def put(name):
-                nonlocal matrix_words
-                if name in written:
-                    return written[name]
-                fmt, raw = packed[prefix + name]
-                raw = np.ascontiguousarray(raw, np.uint8)
-                at = matrix_words - start
-                stream.write(raw.tobytes())
-                pad = (-raw.nbytes) % 4
-                stream.write(bytes(pad))
-                matrix_words += (raw.nbytes + pad) // 4
-                written[name] = (at, fmt)
-                return written[name]
+        def describe(projections):
+            for index, tensor, mode, row0 in projections:
+                at, fmt = place(tensor)
+                skip = row0 * row_bytes(fmt, d)
+                assert skip % 4 == 0, "a row offset must be whole words"
+                w = descriptor_word(index)
+                rec[w], rec[w + 1] = at + skip // 4, fmt | (mode << 8)
 
-            def descriptor(index, name, mode=0, offset_rows=0):
-                at, fmt = put(name)
-                rb = row_bytes(fmt, d)
-                assert offset_rows * rb % 4 == 0
-                off = base + 32 if index == 8 else base + 9 + index * 2
-                header[off] = at + offset_rows * rb // 4
-                header[off + 1] = fmt | (mode << 8)
-
-            header[base] = add(floats[prefix + "attn_norm.weight"])
-            header[base + 1] = add(floats[prefix + "post_attention_norm.weight"])
-            header[base + 5] = add(np.zeros(8))
-            if kind == "full":
-                gate = spec.get("attention_gate", False)
-                descriptor(0, "attn_q.weight", 1 if gate else 3)
-                descriptor(1, "attn_k.weight", 3)
-                descriptor(8, "attn_v.weight", 3)
-                descriptor(2, "attn_output.weight", 4)
-                if gate:
-                    descriptor(6, "attn_q.weight", 2)
-                r = spec["rotary_dim"]
-                perm = np.arange(hd)
-                perm[:r] = np.stack((np.arange(r // 2), np.arange(r // 2) + r // 2), -1).ravel()
-                header[base + 2] = add(np.zeros(heads * hd // 2))
-                for name, field in (("attn_q_norm.weight", 24), ("attn_k_norm.weight", 25)):
-                    norm = floats[prefix + name][perm] if spec.get("qk_norm", True) else np.ones(hd)
-                    header[base + field] = add(np.tile(norm, heads))
-                header[base + 23] = heads
-                header[base + 29] = r
-            else:
-                key, s = spec["state_key_heads"] * 128, spec["state_heads"] * 128
-                descriptor(0, "attn_qkv.weight", 5)
-                descriptor(1, "attn_qkv.weight", 5, key)
-                descriptor(8, "attn_qkv.weight", 0, 2 * key)
-                descriptor(2, "ssm_out.weight")
-                descriptor(6, "attn_gate.weight")
-                header[base + 34] = add(floats[prefix + "ssm_conv1d.weight"])
-                header[base + 35], header[base + 39] = put("ssm_beta.weight")
-                header[base + 36], header[base + 40] = put("ssm_alpha.weight")
-                header[base + 37] = add(floats[prefix + "ssm_dt.bias"])
-                header[base + 38] = add(floats[prefix + "ssm_a"])
-                header[base + 24] = add(np.ones(s))
-                header[base + 25] = add(np.ones(s))
-                header[base + 31] = add(np.tile(floats[prefix + "ssm_norm.weight"], spec["state_heads"]))
-                header[base + 23] = spec["state_heads"]
-            descriptor(3, "ffn_gate.weight")
-            descriptor(4, "ffn_down.weight")
-            descriptor(5, "ffn_up.weight")
-            header[base + 26] = header[base + 30] = 1 if kind == "full" else 2
-            header[base + 27] = start
-            header[base + 28] = matrix_words - start
-    basis_words, seen = 0, {}
-    with open(dest / "vocabulary.bin", "wb") as stream:
-        stream.write(b"RTBASQ01")
-        stream.write(struct.pack("<2I", vocab, d))
-        for name, kind, offset in (("token_embd.weight", 13, 14), ("output.weight", 15, 16)):
-            fmt, raw = packed[name]
-            ident = id(raw)
-            header[kind] = fmt
-            header[offset] = seen.get(ident, basis_words)
-            if ident not in seen:
-                seen[ident] = basis_words
-                stream.write(np.ascontiguousarray(raw, np.uint8).tobytes())
-                pad = (-raw.nbytes) % 4
-                stream.write(bytes(pad))
-                basis_words += (raw.nbytes + pad) // 4
-    params = np.concatenate((header, *parts))
-    with open(dest / "optical_model.bin", "wb") as stream:
-        stream.write(b"RTRES004")
-        stream.write(struct.pack("<9I", d, depth, depth, middle, vocab, 4, len(params), matrix_words, 0))
-        stream.write(params.astype("<u4").tobytes())
+        describe(_full_projections(spec) if full else _recurrent_projections(spec))
+        if full:
+            r = spec["rotary_dim"]
+            order = _rotary_pairs(hd, r)
+            rec[L_ROTARY_ZERO] = vectors.add_floats(np.zeros(heads * hd // 2))
+            for field, tensor in ((L_NORM_A, "attn_q_norm.weight"), (L_NORM_B, "attn_k_norm.weight")):
+                norm = floats[name(tensor)][order] if spec.get("qk_norm", True) else np.ones(hd)
+                rec[field] = vectors.add_floats(np.tile(norm, heads))
+            rec[L_HEADS], rec[L_ROTARY] = heads, r
+        else:
+            sh = spec["state_heads"]
+            rec[L_CONV] = vectors.add_floats(floats[name("ssm_conv1d.weight")])
+            for (w_at, w_code), tensor in ((L_BETA, "ssm_beta.weight"), (L_ALPHA, "ssm_alpha.weight")):
+                rec[w_at], rec[w_code] = place(tensor)
+            rec[L_DT_BIAS] = vectors.add_floats(floats[name("ssm_dt.bias")])
+            rec[L_A] = vectors.add_floats(floats[name("ssm_a")])
+            rec[L_NORM_A] = vectors.add_floats(np.ones(sh * 128))
+            rec[L_NORM_B] = vectors.add_floats(np.ones(sh * 128))
+            rec[L_OUT_NORM] = vectors.add_floats(np.tile(floats[name("ssm_norm.weight")], sh))
+            rec[L_HEADS] = sh
+        describe(_MLP)   # (after the delta-net's beta / alpha payloads, in the exporter's order)
+        rec[L_KIND_A] = rec[L_KIND_B] = 1 if full else 2
+        rec[L_MATRIX_START], rec[L_MATRIX_WORDS] = first_word, matrices.size - first_word
+    (dest / "geometry_weights.bin").write_bytes(matrices.array().tobytes())
+    basis, where = _Words(), {}
+    for tensor, code_word, at_word in (("token_embd.weight", G_EMBED_CODE, G_EMBED_AT),
+                                       ("output.weight", G_LM_CODE, G_LM_AT)):
+        fmt, raw = packed[tensor]
+        if id(raw) not in where:   # a tied LM head shares the embedding's payload
+            where[id(raw)] = basis.add_bytes(raw)
+        head[code_word], head[at_word] = fmt, where[id(raw)]
+    (dest / "vocabulary.bin").write_bytes(b"RTBASQ01" + struct.pack("<2I", vocab, d) + basis.array().tobytes())
+    params = np.concatenate((head, vectors.array()))
+    (dest / "optical_model.bin").write_bytes(
+        b"RTRES004" + struct.pack("<9I", d, depth, depth, middle, vocab, 4, len(params), matrices.size, 0) +
+        params.astype("<u4").tobytes())
     meta = {"architecture": "synthetic", "model_spec": spec, "depth": depth, "hidden_size": d, "middle": middle,
             "vocabulary": vocab, "precision": "original coefficient formats"}
     (dest / "model.json").write_text(json.dumps(meta, indent=2))
