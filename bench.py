@@ -499,15 +499,19 @@ def step_kernels(torch, shape, batch, dev):
 
 def w_decode(torch, args, orc):
     """The 9B-shape hybrid decode step: 32 layers (3 gated delta-net : 1 full attention),
-    hidden 4096, 32/8 heads x 128, 32 delta-net heads, FF 12288, Q4_K projections (packed
-    tiles), Q6_K LM head 151936 x 4096; a batch of sequences with contexts U[256, 8192]."""
+    hidden 4096, 32/8 heads x 128, 32 delta-net heads, FF 12288, Q4_K projections, Q6_K LM
+    head 151936 x 4096 (packed tiles from batch 8, GGUF rows below); a batch of sequences
+    with contexts U[256, 8192]."""
     from rta import model, ops
     batch = args.batch or 32
     dev = torch.device("cuda:0")
     rng = np.random.default_rng(20261110 + 5)
     ctx = rng.integers(256, 8193, batch).astype(np.int32)
     capacity = 8192 + 256
-    shape = model.shape_9b(capacity, packed=True)
+    # the weight layout each batch runs fastest on (measured): packed tiles on the matrix
+    # cores from 8 rows up, GGUF rows on the batch-1 vector-ALU readouts below
+    packed = batch >= 8
+    shape = model.shape_9b(capacity, packed=packed)
     want_cpu = not args.no_cpu and batch == 32
     m = model.DecodeModel(shape, batch, ctx, seed=20261115, keep_gguf=want_cpu)
     nfull = shape.layers // shape.full_every
@@ -534,18 +538,16 @@ def w_decode(torch, args, orc):
                              hkv, workspace=aws, out=oa)
 
     # the LM head (510 MB, two copies rotate past the cache)
-    lm_copies = [m.lm_head, ops.pack(Q6_K, model.random_kquant(Q6_K, shape.vocab, shape.hidden,
-                                                               torch.Generator(device=dev), dev),
-                                     shape.vocab, shape.hidden)]
+    lm2 = model.random_kquant(Q6_K, shape.vocab, shape.hidden, torch.Generator(device=dev), dev)
+    lm_copies = [m.lm_head, ops.pack(Q6_K, lm2, shape.vocab, shape.hidden) if packed else lm2]
     hn = torch.randn(batch, shape.hidden, device=dev)
     lg = torch.empty(batch, shape.vocab, device=dev)
     ids = torch.empty(batch, dtype=torch.int32, device=dev)
-    lws = torch.empty(ops.lm_head_workspace_bytes(Q6_K | ops.TILED, shape.vocab, shape.hidden, batch),
+    lws = torch.empty(ops.lm_head_workspace_bytes(shape.fmt_lm, shape.vocab, shape.hidden, batch),
                       dtype=torch.uint8, device=dev)
 
     def lm_head(i):
-        ops.lm_head(Q6_K | ops.TILED, lm_copies[i % 2], shape.vocab, shape.hidden, hn, workspace=lws, logits=lg,
-                    ids=ids)
+        ops.lm_head(shape.fmt_lm, lm_copies[i % 2], shape.vocab, shape.hidden, hn, workspace=lws, logits=lg, ids=ids)
 
     w_bytes = m.weight_bytes() - m.lm_head.numel()                       # projections + small vectors
     sum_ctx = int(sum(min(int(c), capacity) for c in ctx))
@@ -564,6 +566,7 @@ def w_decode(torch, args, orc):
            "config": {"workload": f"9B-shape hybrid decode step, batch {batch} (32 layers: 24 gated delta-net + 8 "
                                   "full attention; hidden 4096, 32/8 heads x 128, FF 12288, Q4_K projections, "
                                   "Q6_K LM head 151936x4096; contexts U[256, 8192], greedy)",
+                      "weight_layout": "packed tiles" if packed else "GGUF rows",
                       "batch": batch, "layers": 32, "hidden": 4096, "ff": 12288, "vocab": 151936,
                       "sum_context": int(ctx.sum()), "history_capacity": capacity,
                       "bytes_per_step": int(step_bytes), "weight_bytes_per_step": int(w_bytes + m.lm_head.numel()),
