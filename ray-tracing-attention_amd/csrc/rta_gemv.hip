@@ -169,6 +169,7 @@ struct Launch {
     float* partial;
     int batch;
     RowNorm rn;   // packed readouts only
+    XNorm xn;     // batch-1 readouts only
 };
 
 template <int FMT, int R, int MODE, int KW>
@@ -181,7 +182,7 @@ static void launch_b1(const Plan& p, const Launch& l, hipStream_t s) {
         (void)attr;   // a failure surfaces as the launch error
     }
     hipLaunchKernelGGL((gemv_b1_kernel<FMT, R, MODE, KW>), dim3(p.grid), dim3(p.block), lds, s, l.w, l.w2,
-                       l.row_bytes, l.rows, l.cols, l.x, l.y, l.partial, p.lpr, p.ntasks);
+                       l.row_bytes, l.rows, l.cols, l.x, l.y, l.partial, p.lpr, p.ntasks, l.xn.w, l.xn.eps);
 }
 
 template <int FMT, int MODE, int R>
@@ -414,8 +415,10 @@ static hipError_t run_tiled(int fmt, const Launch& l, void* ws, float* pmax, int
 template <int MODE>
 static int run_projection(int fmt, const void* w, const void* w2, int rows, int cols, const float* x, int batch,
                           float* y, float* partial, int* ntasks_out, int* rows_per_task_out, void* ws,
-                          size_t ws_bytes, hipStream_t s, int path_batch = 0, const RowNorm& rn = RowNorm{}) {
+                          size_t ws_bytes, hipStream_t s, int path_batch = 0, const RowNorm& rn = RowNorm{},
+                          const XNorm& xn = XNorm{}) {
     if (rn.part && !is_tiled(fmt)) return RTA_ERR_FORMAT;   // only the packed readout applies it
+    if (xn.w && !b1_norm_fusable(fmt, cols, batch)) return RTA_ERR_FORMAT;   // only the batch-1 readout
     const bool tiled = is_tiled(fmt);
     const int64_t row_bytes = tiled ? 0 : host::row_bytes(fmt, cols);
     int b0 = 0;
@@ -436,6 +439,7 @@ static int run_projection(int fmt, const void* w, const void* w2, int rows, int 
         l.partial = partial ? partial + (int64_t)b0 * rows : nullptr;
         l.rn = rn;
         if (rn.part) l.rn.part = rn.part + b0;
+        l.xn = xn;
         hipError_t e;
         if (tiled) {
             if (!ws || ws_bytes < projection_ws(fmt, rows, cols, chunk, MODE == kSwiglu)) return RTA_ERR_WORKSPACE;
@@ -621,17 +625,21 @@ int tiled_partials(int fmt, const void* w, int rows, int cols, const float* x, i
 }
 
 int swiglu_activation(int fmt, const void* wg, const void* wu, int inter, int hidden, const float* x, int batch,
-                      float* act, void* ws, size_t ws_bytes, hipStream_t s, const RowNorm& rn) {
+                      float* act, void* ws, size_t ws_bytes, hipStream_t s, const RowNorm& rn, const XNorm& xn) {
     return run_projection<kSwiglu>(fmt, wg, wu, inter, hidden, x, batch, act, nullptr, nullptr, nullptr, ws, ws_bytes,
-                                   s, 0, rn);
+                                   s, 0, rn, xn);
 }
 
 int projection_store(int fmt, const void* w, int rows, int cols, const float* x, int batch, float* y, void* ws,
-                     size_t ws_bytes, hipStream_t s, const RowNorm& rn) {
+                     size_t ws_bytes, hipStream_t s, const RowNorm& rn, const XNorm& xn) {
     const int rc = check_matrix(fmt, w, rows, cols);
     if (rc) return rc;
     return run_projection<kStore>(fmt, w, nullptr, rows, cols, x, batch, y, nullptr, nullptr, nullptr, ws, ws_bytes, s,
-                                  0, rn);
+                                  0, rn, xn);
+}
+
+bool b1_norm_fusable(int fmt, int cols, int batch) {
+    return batch == 1 && is_kquant(fmt) && cols > 0 && cols % 256 == 0 && cols / 64 <= 4 * kWave;
 }
 
 // Validates a remap against the matrix and gives the source rows one readout covers
@@ -866,7 +874,7 @@ namespace rta {
 
 int lm_head_rownorm(int fmt, const void* w, int vocab, int hidden, const float* h, int batch, float margin,
                     float* logits, uint32_t* ids, void* workspace, size_t workspace_bytes, hipStream_t s,
-                    const RowNorm& rn) {
+                    const RowNorm& rn, const XNorm& xn) {
     int rc = check_matrix(fmt, w, vocab, hidden);
     if (rc) return rc;
     if (!h || !logits || !ids) return RTA_ERR_NULL;
@@ -890,7 +898,7 @@ int lm_head_rownorm(int fmt, const void* w, int vocab, int hidden, const float* 
         if (rn.part) rc_rn.part = rn.part + b0;
         rc = run_projection<kLogits>(fmt, w, nullptr, vocab, hidden, h + (int64_t)b0 * hidden, chunk,
                                      logits + (int64_t)b0 * vocab, partial + (int64_t)b0 * vocab, &ntasks, &rpt,
-                                     scratch, mma, s, batch, rc_rn);
+                                     scratch, mma, s, batch, rc_rn, xn);
         if (rc) return rc;
         hipLaunchKernelGGL(argmax_margin_kernel, dim3(chunk), dim3(256), 0, s, logits + (int64_t)b0 * vocab,
                            vocab, partial + (int64_t)b0 * vocab, ntasks, rpt, margin, ids + b0);

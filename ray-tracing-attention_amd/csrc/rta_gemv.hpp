@@ -216,12 +216,14 @@ template <int FMT, int R, int MODE, int KW>
 __global__ void __launch_bounds__(256) gemv_b1_kernel(const uint8_t* __restrict__ w, const uint8_t* __restrict__ w2,
                                                       const int64_t row_bytes, const int rows, const int cols,
                                                       const float* __restrict__ x, float* __restrict__ y,
-                                                      float* __restrict__ partial, const int lpr, const int ntasks) {
+                                                      float* __restrict__ partial, const int lpr, const int ntasks,
+                                                      const float* __restrict__ nw, const float eps) {
     using F = typename FmtOf<FMT>::T;
     using Raw = typename F::Raw;
     constexpr bool kDual = MODE == kSwiglu;
     constexpr int kGroups = (KW == 3) ? 1 : 4 / KW;
     __shared__ float s_part[kGroups][KW][R][2][4];   // per wave partials (KW > 1), 4 subs max
+    __shared__ float s_ss[4];                        // the fused RMSNorm's wave sums
 
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int group = wave / KW, wk = wave - group * KW;   // wave index inside its task group
@@ -322,6 +324,30 @@ __global__ void __launch_bounds__(256) gemv_b1_kernel(const uint8_t* __restrict_
     }
     const int task = blockIdx.x * kGroups + group;
     load_task(task, bufA, bufA2);
+    // With nw, x is a residual row and the readout takes its RMSNorm (op 1): x w /
+    // sqrt(mean(x^2) + eps), the sum of squares over the row's own float4s (clamped
+    // duplicates excluded), per element in rmsnorm_kernel's order.
+    if (nw) {
+        float4 wg[kXPer];
+        float ss = 0.0f;
+#pragma unroll
+        for (int k = 0; k < kXPer; ++k) {
+            wg[k] = reinterpret_cast<const float4*>(nw)[xf[k]];
+            const float4 v = xg[k];
+            if ((int)threadIdx.x + k * (int)blockDim.x < nf) ss += v.x * v.x + v.y * v.y + v.z * v.z + v.w * v.w;
+        }
+        for (int off = 32; off > 0; off >>= 1) ss += __shfl_xor(ss, off, kWave);
+        if (lane == 0) s_ss[wave] = ss;
+        __syncthreads();
+        float tot = 0.0f;
+        for (int i = 0; i < (int)(blockDim.x >> 6); ++i) tot += s_ss[i];
+        const float inv = 1.0f / sqrtf(tot / (float)cols + eps);
+#pragma unroll
+        for (int k = 0; k < kXPer; ++k) {
+            const float4 v = xg[k], g = wg[k];
+            xg[k] = make_float4(v.x * inv * g.x, v.y * inv * g.y, v.z * inv * g.z, v.w * inv * g.w);
+        }
+    }
 #pragma unroll
     for (int k = 0; k < kXPer; ++k) {
         const int pl = F::place(4 * xf[k]);

@@ -19,18 +19,28 @@ constexpr int kSlabBatch = 32;   // batch rows of one K-slab partial block [slab
 int tiled_partials(int fmt, const void* w, int rows, int cols, const float* x, int batch, float* y, bool accumulate,
                    void* ws, size_t ws_bytes, hipStream_t s, int* nslab, const RowNorm& rn = RowNorm{});
 
-// y = W x (rta_gemv with the STORE epilogue) with a deferred RMSNorm factor.
+// The RMSNorm taken by a batch-1 readout itself: x is the residual row and the readout
+// multiplies it by w / sqrt(mean(x^2) + eps) while staging it (b1_norm_fusable shapes).
+struct XNorm {
+    const float* w = nullptr;
+    float eps = 0.0f;
+};
+bool b1_norm_fusable(int fmt, int cols, int batch);
+
+// y = W x (rta_gemv with the STORE epilogue) with a deferred RMSNorm factor (rn) or the
+// batch-1 readout's own RMSNorm (xn).
 int projection_store(int fmt, const void* w, int rows, int cols, const float* x, int batch, float* y, void* ws,
-                     size_t ws_bytes, hipStream_t s, const RowNorm& rn);
+                     size_t ws_bytes, hipStream_t s, const RowNorm& rn, const XNorm& xn = XNorm{});
 
 // rta_lm_head with a deferred RMSNorm factor per batch row.
 int lm_head_rownorm(int fmt, const void* w, int vocab, int hidden, const float* h, int batch, float margin,
                     float* logits, uint32_t* ids, void* workspace, size_t workspace_bytes, hipStream_t s,
-                    const RowNorm& rn);
+                    const RowNorm& rn, const XNorm& xn = XNorm{});
 
 // The fused gate/up projection of the SwiGLU MLP alone: act = swiglu(Wg x, Wu x).
 int swiglu_activation(int fmt, const void* wg, const void* wu, int inter, int hidden, const float* x, int batch,
-                      float* act, void* ws, size_t ws_bytes, hipStream_t s, const RowNorm& rn = RowNorm{});
+                      float* act, void* ws, size_t ws_bytes, hipStream_t s, const RowNorm& rn = RowNorm{},
+                      const XNorm& xn = XNorm{});
 
 // The middle of a recurrent layer (ops 18-21 and 15) for every (head, sequence):
 // in-projection row r of sequence b = sum_k proj[k * slab_stride + b * row_stride + r]

@@ -331,12 +331,19 @@ int rta_hybrid_decode_step(const rta_hybrid_shape* shape, const rta_hybrid_weigh
         return rc;
     };
     // The norm in front of a consumer of format f.  keep_fp32: w.normed must hold x in
-    // fp32 as well (a separate readout reads it), h * w when rn is set.
+    // fp32 as well (a separate readout reads it), h * w when rn is set.  At batch 1 a
+    // GGUF-row K-quant readout takes the norm itself (xn; its x is then w.hidden).
     RowNorm rn{};
+    XNorm xn{};
     auto norm = [&](const float* nw, int f, bool keep_fp32) -> int {
         rn = RowNorm{};
+        xn = XNorm{};
         const float* part = static_cast<const float*>(w.gemm_ws);
         int rc;
+        if (!keep_fp32 && !pending && b1_norm_fusable(f, d.D, B)) {
+            xn = XNorm{nw, eps};
+            return RTA_OK;
+        }
         if (imaged(f)) {
             rc = residual_norm_image(f, w.hidden, part, pending, nw, B, d.D, w.rms, keep_fp32 ? w.normed : nullptr,
                                      w.ximg, s);
@@ -364,9 +371,9 @@ int rta_hybrid_decode_step(const rta_hybrid_shape* shape, const rta_hybrid_weigh
             if (imaged(fi))
                 RTA_TRY(image_readout(fi, kReadStore, lw.w_in, nullptr, d.rows_full, d.D, w.ximg, B, w.proj, true,
                                       w.gemm_ws, w.gemm_bytes, s, nullptr, rn));
-            else if (rn.part)
-                RTA_TRY(projection_store(fi, lw.w_in, d.rows_full, d.D, w.normed, B, w.proj, w.gemm_ws, w.gemm_bytes,
-                                         s, rn));
+            else if (rn.part || xn.w)
+                RTA_TRY(projection_store(fi, lw.w_in, d.rows_full, d.D, xn.w ? w.hidden : w.normed, B, w.proj,
+                                         w.gemm_ws, w.gemm_bytes, s, rn, xn));
             else
                 RTA_TRY(rta_gemv(fi, lw.w_in, d.rows_full, d.D, w.normed, B, w.proj, RTA_EPI_STORE, w.gemm_ws,
                                  w.gemm_bytes, stream));
@@ -398,6 +405,9 @@ int rta_hybrid_decode_step(const rta_hybrid_shape* shape, const rta_hybrid_weigh
             else if (rn.part)
                 RTA_TRY(tiled_partials(fi, lw.w_in, rows, d.D, w.normed, B, w.proj, false, w.gemm_ws, w.gemm_bytes,
                                        s, &ns, rn));
+            else if (xn.w)
+                RTA_TRY(projection_store(fi, lw.w_in, rows, d.D, w.hidden, B, w.proj, w.gemm_ws, w.gemm_bytes, s, rn,
+                                         xn));
             else
                 RTA_TRY(rta_gemv(fi, lw.w_in, rows, d.D, w.normed, B, w.proj, RTA_EPI_STORE, w.gemm_ws,
                                  w.gemm_bytes, stream));
@@ -432,8 +442,8 @@ int rta_hybrid_decode_step(const rta_hybrid_shape* shape, const rta_hybrid_weigh
             RTA_TRY(image_readout(fgu, kReadSwiglu, lw.w_gate, lw.w_up, d.FF, d.D, w.ximg, B, w.act, true, w.gemm_ws,
                                   w.gemm_bytes, s, nullptr, rn));
         else
-            RTA_TRY(swiglu_activation(fgu, lw.w_gate, lw.w_up, d.FF, d.D, w.normed, B, w.act, w.gemm_ws, w.gemm_bytes,
-                                      s, rn));
+            RTA_TRY(swiglu_activation(fgu, lw.w_gate, lw.w_up, d.FF, d.D, xn.w ? w.hidden : w.normed, B, w.act,
+                                      w.gemm_ws, w.gemm_bytes, s, rn, xn));
         RTA_TRY(residual_proj(fd, lw.w_down, d.FF, w.act));
     }
     // op 1 index 2, then the readout (Resident::word): logits and the next tokens; the
@@ -441,8 +451,11 @@ int rta_hybrid_decode_step(const rta_hybrid_shape* shape, const rta_hybrid_weigh
     {
         const int fl = shape->fmt_lm;
         rn = RowNorm{};
+        xn = XNorm{};
         const float* part = static_cast<const float*>(w.gemm_ws);
-        if (fused(fl) && d.D <= 4096) {
+        if (!pending && b1_norm_fusable(fl, d.D, B)) {
+            xn = XNorm{weights->norm_final, eps};
+        } else if (fused(fl) && d.D <= 4096) {
             RTA_TRY(residual_norm_deferred(w.hidden, part, pending, weights->norm_final, B, d.D, w.normed, w.rms, s));
             rn = RowNorm{reinterpret_cast<const float4*>(w.rms), (float)d.D, eps};
         } else if (pending) {
@@ -452,8 +465,8 @@ int rta_hybrid_decode_step(const rta_hybrid_shape* shape, const rta_hybrid_weigh
         }
         pending = 0;
     }
-    RTA_TRY(lm_head_rownorm(shape->fmt_lm, weights->lm_head, d.V, d.D, w.normed, B, shape->margin,
-                            logits_out ? logits_out : w.logits, tokens, w.lm_ws, w.lm_bytes, s, rn));
+    RTA_TRY(lm_head_rownorm(shape->fmt_lm, weights->lm_head, d.V, d.D, xn.w ? w.hidden : w.normed, B, shape->margin,
+                            logits_out ? logits_out : w.logits, tokens, w.lm_ws, w.lm_bytes, s, rn, xn));
 #undef RTA_TRY
     return RTA_OK;
 }

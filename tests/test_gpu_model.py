@@ -23,6 +23,20 @@ def test_hybrid_decode_steps(packed, hidden):
     check_steps(m, 2)
 
 
+# Batch 1: the GGUF-row readouts take the RMSNorm in front of them themselves (x is the
+# residual row), the packed ones run the matrix-core paths with one real row.
+@pytest.mark.parametrize("packed", [False, True])
+def test_hybrid_decode_steps_batch1(packed):
+    from rta import model
+    from rta._lib import Q4_K, Q6_K, TILED
+    shape = model.HybridShape(hidden=512, layers=4, full_every=2, q_heads=4, kv_heads=2, head_dim=128, rec_heads=2,
+                              ff=768, vocab=3001, capacity=64, fmt_embed=Q4_K,
+                              fmt_proj=Q4_K | (TILED if packed else 0), fmt_lm=Q6_K | (TILED if packed else 0),
+                              fmt_k=Q4_K, fmt_v=Q6_K, rope_rotary=128, eps=1e-6, margin=1e-4, rope_theta=1e6)
+    m = model.DecodeModel(shape, 1, [70], seed=9, keep_gguf=True)
+    check_steps(m, 3)
+
+
 # What the exporter emits beyond the plain layout (compiler/export.py:96-113): the
 # attention output gate, fewer delta-net key heads than heads (repeated), the a / b rows
 # as matrices of their own (F32, as ssm_alpha / ssm_beta), and a format per matrix --
@@ -37,7 +51,7 @@ def _exporter_fmts(l, full):
     return {"in": Q4_K, "o": F16, "gate_up": Q6_K | TILED, "down": Q4_K | TILED, "ab": 0}
 
 
-@pytest.mark.parametrize("batch", [3, 20, 40])
+@pytest.mark.parametrize("batch", [1, 3, 20, 40])
 def test_hybrid_decode_steps_exported_layout(batch):
     from rta import model
     from rta._lib import Q4_K, Q6_K, TILED
