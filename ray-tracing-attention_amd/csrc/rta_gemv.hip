@@ -31,24 +31,29 @@ __global__ void __launch_bounds__(256) dequant_kernel(int fmt, const uint8_t* __
 // logit >= T.  The first task whose maximum reaches T holds that id, so only its
 // rows are scanned (in parallel).  Generalises the
 // reference's reduction (resident_math.comp:124-130: strict >, ties -> lower id).
-__global__ void __launch_bounds__(256) argmax_margin_kernel(const float* __restrict__ logits, int vocab,
+constexpr int kArgmaxThreads = 1024;   // one block per batch row scans the task maxima
+
+__global__ void __launch_bounds__(kArgmaxThreads) argmax_margin_kernel(const float* __restrict__ logits, int vocab,
                                                             const float* __restrict__ partial, int ntasks,
                                                             int rows_per_task, float margin,
                                                             uint32_t* __restrict__ ids) {
 #pragma clang fp contract(off)
-    __shared__ float red_f[4];
-    __shared__ int red_i[4];
+    constexpr int kW = kArgmaxThreads / 64;
+    __shared__ float red_f[kW];
+    __shared__ int red_i[kW];
     const int b = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const float* pb = partial + (int64_t)b * ntasks;
     const float* lb = logits + (int64_t)b * vocab;
     // 1. M = max over the task maxima
     float m = -INFINITY;
 #pragma unroll 8
-    for (int t = tid; t < ntasks; t += 256) m = fmaxf(m, pb[t]);
+    for (int t = tid; t < ntasks; t += kArgmaxThreads) m = fmaxf(m, pb[t]);
     m = group_max(m, kWave);
     if (lane == 0) red_f[wave] = m;
     __syncthreads();
-    const float M = fmaxf(fmaxf(red_f[0], red_f[1]), fmaxf(red_f[2], red_f[3]));
+    float M = red_f[0];
+#pragma unroll
+    for (int i = 1; i < kW; ++i) M = fmaxf(M, red_f[i]);
     if (!(M > -INFINITY)) {
         if (tid == 0) ids[b] = 0xffffffffu;
         return;
@@ -59,11 +64,13 @@ __global__ void __launch_bounds__(256) argmax_margin_kernel(const float* __restr
     // 2. the first task whose maximum reaches T holds the lowest index with logit >= T
     int first = INT_MAX;   // branch-free so that the loads of a thread overlap
 #pragma unroll 8
-    for (int t = tid; t < ntasks; t += 256) first = (pb[t] >= T && t < first) ? t : first;
+    for (int t = tid; t < ntasks; t += kArgmaxThreads) first = (pb[t] >= T && t < first) ? t : first;
     for (int off = 32; off > 0; off >>= 1) first = min(first, __shfl_xor(first, off, kWave));
     if (lane == 0) red_i[wave] = first;
     __syncthreads();
-    first = min(min(red_i[0], red_i[1]), min(red_i[2], red_i[3]));
+    first = red_i[0];
+#pragma unroll
+    for (int i = 1; i < kW; ++i) first = min(first, red_i[i]);
     __syncthreads();
     if (first == INT_MAX) {   // only with NaN logits
         if (tid == 0) ids[b] = 0xffffffffu;
@@ -73,11 +80,14 @@ __global__ void __launch_bounds__(256) argmax_margin_kernel(const float* __restr
     const int r0 = first * rows_per_task, r1 = min(r0 + rows_per_task, vocab);
     int best = INT_MAX;
 #pragma unroll 4
-    for (int r = r0 + tid; r < r1; r += 256) best = (lb[r] >= T && r < best) ? r : best;
+    for (int r = r0 + tid; r < r1; r += kArgmaxThreads) best = (lb[r] >= T && r < best) ? r : best;
     for (int off = 32; off > 0; off >>= 1) best = min(best, __shfl_xor(best, off, kWave));
     if (lane == 0) red_i[wave] = best;
     __syncthreads();
-    if (tid == 0) ids[b] = (uint32_t)min(min(red_i[0], red_i[1]), min(red_i[2], red_i[3]));
+    if (tid == 0) {
+        for (int i = 1; i < kW; ++i) best = min(best, red_i[i]);
+        ids[b] = (uint32_t)min(best, red_i[0]);
+    }
 }
 
 // ----------------------------------------------------------- launch plumbing ----
@@ -900,7 +910,7 @@ int lm_head_rownorm(int fmt, const void* w, int vocab, int hidden, const float* 
                                      logits + (int64_t)b0 * vocab, partial + (int64_t)b0 * vocab, &ntasks, &rpt,
                                      scratch, mma, s, batch, rc_rn, xn);
         if (rc) return rc;
-        hipLaunchKernelGGL(argmax_margin_kernel, dim3(chunk), dim3(256), 0, s, logits + (int64_t)b0 * vocab,
+        hipLaunchKernelGGL(argmax_margin_kernel, dim3(chunk), dim3(kArgmaxThreads), 0, s, logits + (int64_t)b0 * vocab,
                            vocab, partial + (int64_t)b0 * vocab, ntasks, rpt, margin, ids + b0);
         if (hipGetLastError() != hipSuccess) return RTA_ERR_LAUNCH;
         b0 += chunk;

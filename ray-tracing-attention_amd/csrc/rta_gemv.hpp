@@ -328,11 +328,9 @@ __global__ void __launch_bounds__(256) gemv_b1_kernel(const uint8_t* __restrict_
     // sqrt(mean(x^2) + eps), the sum of squares over the row's own float4s (clamped
     // duplicates excluded), per element in rmsnorm_kernel's order.
     if (nw) {
-        float4 wg[kXPer];
         float ss = 0.0f;
 #pragma unroll
         for (int k = 0; k < kXPer; ++k) {
-            wg[k] = reinterpret_cast<const float4*>(nw)[xf[k]];
             const float4 v = xg[k];
             if ((int)threadIdx.x + k * (int)blockDim.x < nf) ss += v.x * v.x + v.y * v.y + v.z * v.z + v.w * v.w;
         }
@@ -344,7 +342,7 @@ __global__ void __launch_bounds__(256) gemv_b1_kernel(const uint8_t* __restrict_
         const float inv = 1.0f / sqrtf(tot / (float)cols + eps);
 #pragma unroll
         for (int k = 0; k < kXPer; ++k) {
-            const float4 v = xg[k], g = wg[k];
+            const float4 v = xg[k], g = reinterpret_cast<const float4*>(nw)[xf[k]];
             xg[k] = make_float4(v.x * inv * g.x, v.y * inv * g.y, v.z * inv * g.z, v.w * inv * g.w);
         }
     }

@@ -535,14 +535,33 @@ __global__ void __launch_bounds__(256) pack_history_kernel(const float* __restri
     __shared__ float gscale[2][kPackMaxBlocks * 16], gmin[2][kPackMaxBlocks * 16];
     __shared__ float bd[2][kPackMaxBlocks], bdm[2][kPackMaxBlocks];
     __shared__ uint32_t sc[2][kPackMaxBlocks * 16], mn[2][kPackMaxBlocks * 16];
+    __shared__ float xs[2][kPackMaxBlocks * 256];   // the K and V rows, zero past kvw
     uint8_t* pb = reinterpret_cast<uint8_t*>(pkt);
     const int b = blockIdx.x, tid = threadIdx.x;
     const int blocks = (kvw + 255) / 256;
     const float* src[2] = {kin + (int64_t)b * k_stride, vin + (int64_t)b * v_stride};
     const int fmt[2] = {fmt_k, fmt_v};
     const int field_off[2] = {0, blocks * (fmt_k == RTA_Q4_K ? 144 : 210)};
-    auto value = [&](int f, int i) { return i < kvw ? src[f][i] : 0.0f; };
+    // both rows into LDS once (every load issued before the first is used); the steps
+    // below read each value several times
+    {
+        float t[2][kPackMaxBlocks];
+#pragma unroll
+        for (int f = 0; f < 2; ++f)
+#pragma unroll
+            for (int k = 0; k < kPackMaxBlocks; ++k) {
+                const int i = tid + 256 * k;
+                t[f][k] = (k < blocks && i < kvw) ? src[f][i] : 0.0f;
+            }
+#pragma unroll
+        for (int f = 0; f < 2; ++f)
+#pragma unroll
+            for (int k = 0; k < kPackMaxBlocks; ++k)
+                if (k < blocks) xs[f][tid + 256 * k] = t[f][k];
+    }
+    auto value = [&](int f, int i) { return xs[f][i]; };
     for (int i = tid; i < (int)(stride / 4); i += 256) pkt[i] = 0u;
+    __syncthreads();
     // 1. group statistics
     for (int f = 0; f < 2; ++f) {
         const bool q4 = fmt[f] == RTA_Q4_K;
