@@ -321,6 +321,10 @@ typedef struct rta_hybrid_shape {
                            (0: rec_heads); delta-net head h reads q / k head h % rec_key_heads, the
                            key repeat of export.py:107-112 / resident_quant.glsl:26 */
     int layer_formats;  /* 1: each layer's fmt_* fields give its matrices' formats (else fmt_proj) */
+    int o_axis_remap;   /* 1: q, k, v and gate rows of full layers are in the rotary-pair order of
+                           modes 1-3 and w_o's columns in the exporter's order (descriptor 2 mode
+                           4, export.py:97): the attention output goes back to the exporter's
+                           order before w_o, so w_o is used as exported */
 } rta_hybrid_shape;
 
 typedef struct rta_hybrid_layer {   /* device pointers; fmt_proj matrices [rows x cols] */
@@ -347,6 +351,16 @@ typedef struct rta_hybrid_layer {   /* device pointers; fmt_proj matrices [rows 
                                         ssm_alpha / ssm_beta; NULL: the last 2 rec_heads rows of w_in */
     const void* w_b;
     int fmt_ab;
+    /* The in-projection as up to 4 matrices of their own formats (compiler/export.py keeps
+       attn_q, attn_k, attn_v / attn_qkv and attn_gate as tensors of their own GGUF types,
+       export.py:96-109): with in_parts > 0 the rows of w_in are those of in_w[0] (in_rows[0]
+       rows, format in_fmt[0]), then of in_w[1], ..., and w_in / fmt_in are not read.  The
+       row counts must add up to w_in's; parts need shape->layer_formats.  0: w_in holds
+       every row. */
+    int in_parts;
+    const void* in_w[4];
+    int in_rows[4];
+    int in_fmt[4];
 } rta_hybrid_layer;
 
 typedef struct rta_hybrid_weights {
@@ -415,7 +429,9 @@ int rta_asset_get_info(const rta_asset* asset, rta_asset_info* info);
 /* The parameter words (model header, 64-word layer headers, fp32 vectors). */
 const uint32_t* rta_asset_params(const rta_asset* asset, uint64_t* words);
 /* Projection descriptor index 0..8 of a layer (export.py:87-91, 96-98, 108-109, 121):
- * 0 q / qkv, 1 k, 2 output / ssm_out, 3 ffn_gate, 4 ffn_down, 5 ffn_up, 6 gate, 8 v. */
+ * 0 q / qkv, 1 k, 2 output / ssm_out, 3 ffn_gate, 4 ffn_down, 5 ffn_up, 6 gate, 8 v;
+ * and the delta-net's separate payloads (export.py:113; offset and code words 35 / 39,
+ * 36 / 40, no mode): 9 ssm_beta, 10 ssm_alpha. */
 int rta_asset_layer_matrix(const rta_asset* asset, int layer, int index, rta_asset_matrix* out);
 /* fp32 vector (count values) that word `field` of a layer header (layer -1: the model
  * header) points at, e.g. 0 attn_norm, 1 post_attention_norm, 24/25 q/k norm; model 4

@@ -157,19 +157,23 @@ extern "C" const uint32_t* rta_asset_params(const rta_asset* a, uint64_t* words)
 
 // Descriptor `index` of a layer: words base+9+2i, base+10+2i (index 8: base+32, base+33),
 // the first a word offset into the layer's matrix range, the second code | mode << 8
-// (export.py:87-91).  An index the exporter never set reads code 0 at offset 0.
+// (export.py:87-91).  Indices 9 and 10 are the delta-net's ssm_beta / ssm_alpha payloads,
+// whose offset and code sit in words 35 / 39 and 36 / 40 (export.py:113), with no mode.
+// An index the exporter never set reads code 0 at offset 0.
 extern "C" int rta_asset_layer_matrix(const rta_asset* a, int layer, int index, rta_asset_matrix* out) {
     if (!a || !out) return RTA_ERR_NULL;
-    if (layer < 0 || (uint32_t)layer >= a->hdr[1] || index < 0 || index > 8) return RTA_ERR_RANGE;
+    if (layer < 0 || (uint32_t)layer >= a->hdr[1] || index < 0 || index > 10) return RTA_ERR_RANGE;
     const uint32_t* lh = a->params.data() + kModelWords + (uint32_t)layer * kLayerWords;
-    const uint32_t at = index == 8 ? 32u : 9u + 2u * (uint32_t)index;
+    const bool separate = index >= 9;
+    const uint32_t at = separate ? 26u + (uint32_t)index : index == 8 ? 32u : 9u + 2u * (uint32_t)index;
+    const uint32_t code = separate ? lh[at + 4] : lh[at + 1];
     const uint64_t start = lh[27], words = lh[28], off = lh[at];
     if (off > words) return RTA_ERR_RANGE;
     out->data = a->matrices.data() + start + off;
     out->offset_words = start + off;
     out->avail_bytes = (words - off) * 4;
-    out->fmt = lh[at + 1] & 0xFFu;
-    out->mode = lh[at + 1] >> 8;
+    out->fmt = separate ? code : code & 0xFFu;
+    out->mode = separate ? 0u : code >> 8;
     return RTA_OK;
 }
 

@@ -45,6 +45,7 @@ struct AttnArgs {
     const int32_t* ctx_len;
     const float* gate;
     int64_t gate_stride;   // floats from one sequence's gate row to the next (head h at + h hd)
+    int out_rotary;        // > 0: dim d < out_rotary of each head goes to column rot(d) of out
     float* out;
     float* m_out;
     float* z_out;
@@ -1451,7 +1452,11 @@ __global__ void __launch_bounds__(256) attn_merge_kernel(const AttnArgs a) {
         }
         float o = u / fmaxf(z, 1e-30f);
         if (a.gate) o *= detector_sigmoid(a.gate[(int64_t)(sh / a.hq) * a.gate_stride + (sh % a.hq) * kHd + tid]);
-        out[tid] = o;
+        // with out_rotary R the head's rotary-pair order goes back to the exporter's
+        // half-split column order (originalRotaryAxis), the columns the O projection's
+        // axis remap reads (resident_quant.glsl:20,25)
+        const int R = a.out_rotary;
+        out[tid < R ? (tid & 1) * (R >> 1) + (tid >> 1) : tid] = o;
         if (tid == 0) {
             if (a.m_out) a.m_out[sh] = M;
             if (a.z_out) a.z_out[sh] = z;
@@ -1640,7 +1645,7 @@ int decode_attention_gate_stride(const float* q, int nseq, int hq, int hkv, int 
                                  int fmt_v, const int64_t* slot_base, const int32_t* ctx_len, int64_t capacity,
                                  int64_t n_slots, int max_ctx, const float* gate, int64_t gate_stride, float* out,
                                  float* m_out, float* z_out, void* workspace, size_t workspace_bytes,
-                                 rta_stream_t stream) {
+                                 rta_stream_t stream, int out_rotary) {
     if (!q || !packets || !slot_base || !ctx_len || !out) return RTA_ERR_NULL;   // m_out, z_out optional
     if (nseq <= 0 || hq <= 0 || hkv <= 0 || hd <= 0 || hq % hkv || capacity <= 0 || max_ctx <= 0 || n_slots <= 0)
         return RTA_ERR_SHAPE;
@@ -1668,6 +1673,8 @@ int decode_attention_gate_stride(const float* q, int nseq, int hq, int hkv, int 
     a.ctx_len = ctx_len;
     a.gate = gate;
     a.gate_stride = gate_stride;
+    if (out_rotary < 0 || out_rotary > hd || out_rotary % 2) return RTA_ERR_RANGE;
+    a.out_rotary = out_rotary;
     a.out = out;
     a.m_out = m_out;
     a.z_out = z_out;

@@ -68,12 +68,13 @@ int residual_norm_deferred(float* hidden, const float* part, int nslab, const fl
                            float* out, float* ss, hipStream_t s);
 
 // rta_decode_attention with the gate of sequence s at gate + s gate_stride (head h at
-// + h hd), gate_stride >= hq hd: the gate rows of a fused in-projection.
+// + h hd), gate_stride >= hq hd: the gate rows of a fused in-projection.  out_rotary R > 0:
+// output dim d < R of each head is written to column (d % 2)(R / 2) + d / 2 of the head.
 int decode_attention_gate_stride(const float* q, int nseq, int hq, int hkv, int hd, const void* packets, int fmt_k,
                                  int fmt_v, const int64_t* slot_base, const int32_t* ctx_len, int64_t capacity,
                                  int64_t n_slots, int max_ctx, const float* gate, int64_t gate_stride, float* out,
                                  float* m_out, float* z_out, void* workspace, size_t workspace_bytes,
-                                 rta_stream_t stream);
+                                 rta_stream_t stream, int out_rotary = 0);
 
 // ---- the decode step's readouts of a staged x image (rta_packed.hpp) ----
 constexpr int kReadStore = 0, kReadAccumulate = 1, kReadSwiglu = 2;   // image_readout modes

@@ -141,6 +141,7 @@ int check_shape(const rta_hybrid_shape* s, int batch) {
         return RTA_ERR_RANGE;
     if ((s->full_every > 0 && (s->q_heads * 128) % 256) || (s->rec_heads * 128) % 256) return RTA_ERR_SHAPE;
     if (s->attn_gate < 0 || s->attn_gate > 1 || s->layer_formats < 0 || s->layer_formats > 1 ||
+        s->o_axis_remap < 0 || s->o_axis_remap > 1 ||
         s->rec_key_heads < 0 || s->rec_key_heads > s->rec_heads)
         return RTA_ERR_RANGE;
     return RTA_OK;
@@ -167,7 +168,7 @@ State carve_state(const Dims& d, void* p, size_t* bytes) {
 }
 
 struct Work {
-    float *hidden, *normed, *proj, *q, *ext_a, *ext_b, *mix, *act, *logits, *rms;
+    float *hidden, *normed, *proj, *part, *q, *ext_a, *ext_b, *mix, *act, *logits, *rms;
     int64_t *pos, *slots;
     int32_t* visible;
     void *attn_ws, *lm_ws, *gemm_ws, *ximg;
@@ -209,6 +210,8 @@ Work carve_work(const rta_hybrid_shape* s, const Dims& d, void* p, size_t* bytes
     w.hidden = c.take<float>(B * d.D);
     w.normed = c.take<float>(B * d.D);
     w.proj = c.take<float>(B * std::max(d.nfull ? d.rows_full : 0, d.nrec ? d.rows_rec : 0));
+    // one in-projection part's rows before they are laid into w.proj (batch > 1)
+    w.part = c.take<float>(B > 1 ? B * std::max(d.nfull ? d.rows_full : 0, d.nrec ? d.rows_rec : 0) : 1);
     w.q = c.take<float>(B * std::max(1, d.hq * d.hd));
     w.ext_a = c.take<float>(B * std::max(1, d.H));
     w.ext_b = c.take<float>(B * std::max(1, d.H));
@@ -360,6 +363,39 @@ int rta_hybrid_decode_step(const rta_hybrid_shape* shape, const rta_hybrid_weigh
         return rc;
     };
 
+    // An in-projection given in parts (formats of their own): each part is read into its
+    // rows of w.proj; at batch 1 every K-quant row-layout part takes the norm itself.
+    auto in_parts = [&](const rta_hybrid_layer& lw, int rows, bool keep_fp32) -> int {
+        if (lw.in_parts > 4) return RTA_ERR_RANGE;
+        if (!shape->layer_formats) return RTA_ERR_FORMAT;   // (the workspace covers every format then)
+        int sum = 0;
+        bool fusable = !keep_fp32;
+        for (int i = 0; i < lw.in_parts; ++i) {
+            if (!lw.in_w[i]) return RTA_ERR_NULL;
+            if (lw.in_rows[i] <= 0) return RTA_ERR_SHAPE;
+            sum += lw.in_rows[i];
+            fusable = fusable && b1_norm_fusable(lw.in_fmt[i], d.D, B);
+        }
+        if (sum != rows) return RTA_ERR_SHAPE;
+        RTA_TRY(norm(lw.norm_in, fusable ? lw.in_fmt[0] : RTA_F32, keep_fp32));
+        int off = 0;
+        for (int i = 0; i < lw.in_parts; ++i) {
+            const int n = lw.in_rows[i], f = lw.in_fmt[i];
+            float* y = B == 1 ? w.proj + off : w.part;
+            if (xn.w)
+                RTA_TRY(projection_store(f, lw.in_w[i], n, d.D, w.hidden, B, y, w.gemm_ws, w.gemm_bytes, s, RowNorm{},
+                                         xn));
+            else
+                RTA_TRY(rta_gemv(f, lw.in_w[i], n, d.D, w.normed, B, y, RTA_EPI_STORE, w.gemm_ws, w.gemm_bytes,
+                                 stream));
+            if (B > 1 && hipMemcpy2DAsync(w.proj + off, (size_t)rows * sizeof(float), w.part, (size_t)n * sizeof(float),
+                                          (size_t)n * sizeof(float), B, hipMemcpyDeviceToDevice, s) != hipSuccess)
+                return RTA_ERR_LAUNCH;
+            off += n;
+        }
+        return RTA_OK;
+    };
+
     int lf = 0, lr = 0;
     for (int l = 0; l < d.L; ++l) {
         const rta_hybrid_layer& lw = weights->layers[l];
@@ -367,16 +403,20 @@ int rta_hybrid_decode_step(const rta_hybrid_shape* shape, const rta_hybrid_weigh
                   fd = fmt_of(lw.fmt_down);
         if (is_full(shape, l)) {
             // op 2 index 5 (q | k | v | gate), ops 14 + 3, op 34, attention, op 2 index 2
-            RTA_TRY(norm(lw.norm_in, fi, false));
-            if (imaged(fi))
-                RTA_TRY(image_readout(fi, kReadStore, lw.w_in, nullptr, d.rows_full, d.D, w.ximg, B, w.proj, true,
-                                      w.gemm_ws, w.gemm_bytes, s, nullptr, rn));
-            else if (rn.part || xn.w)
-                RTA_TRY(projection_store(fi, lw.w_in, d.rows_full, d.D, xn.w ? w.hidden : w.normed, B, w.proj,
-                                         w.gemm_ws, w.gemm_bytes, s, rn, xn));
-            else
-                RTA_TRY(rta_gemv(fi, lw.w_in, d.rows_full, d.D, w.normed, B, w.proj, RTA_EPI_STORE, w.gemm_ws,
-                                 w.gemm_bytes, stream));
+            if (lw.in_parts > 0) {
+                RTA_TRY(in_parts(lw, d.rows_full, false));
+            } else {
+                RTA_TRY(norm(lw.norm_in, fi, false));
+                if (imaged(fi))
+                    RTA_TRY(image_readout(fi, kReadStore, lw.w_in, nullptr, d.rows_full, d.D, w.ximg, B, w.proj,
+                                          true, w.gemm_ws, w.gemm_bytes, s, nullptr, rn));
+                else if (rn.part || xn.w)
+                    RTA_TRY(projection_store(fi, lw.w_in, d.rows_full, d.D, xn.w ? w.hidden : w.normed, B, w.proj,
+                                             w.gemm_ws, w.gemm_bytes, s, rn, xn));
+                else
+                    RTA_TRY(rta_gemv(fi, lw.w_in, d.rows_full, d.D, w.normed, B, w.proj, RTA_EPI_STORE,
+                                     w.gemm_ws, w.gemm_bytes, stream));
+            }
             hipLaunchKernelGGL(qk_norm_rope_kernel, dim3((d.hq + d.hkv + 3) / 4, B), dim3(256), 0, s, w.proj,
                                d.rows_full, d.hq, d.hkv, lw.q_norm, lw.k_norm, eps, w.pos, shape->rope_rotary,
                                shape->rope_theta, w.q);
@@ -389,7 +429,7 @@ int rta_hybrid_decode_step(const rta_hybrid_shape* shape, const rta_hybrid_weigh
             RTA_TRY(decode_attention_gate_stride(w.q, B, d.hq, d.hkv, d.hd, packets, shape->fmt_k, shape->fmt_v,
                                                  st.base + (size_t)lf * B, w.visible, d.cap, (int64_t)B * d.cap,
                                                  d.cap, gate, d.rows_full, w.mix, nullptr, nullptr, w.attn_ws,
-                                                 w.attn_bytes, stream));
+                                                 w.attn_bytes, stream, shape->o_axis_remap ? shape->rope_rotary : 0));
             RTA_TRY(residual_proj(fo, lw.w_o, d.hq * d.hd, w.mix));
             ++lf;
         } else {
@@ -397,20 +437,24 @@ int rta_hybrid_decode_step(const rta_hybrid_shape* shape, const rta_hybrid_weigh
             const bool ext = lw.w_a != nullptr;
             if (ext && !lw.w_b) return RTA_ERR_NULL;
             const int rows = d.rows_rec - (ext ? 2 * d.H : 0);
-            RTA_TRY(norm(lw.norm_in, fi, ext));
             int ns = 1;   // K slabs the middle adds (1: the rows are final in w.proj)
-            if (imaged(fi))
-                RTA_TRY(image_readout(fi, kReadStore, lw.w_in, nullptr, rows, d.D, w.ximg, B, w.proj, false,
-                                      w.gemm_ws, w.gemm_bytes, s, &ns, rn));
-            else if (rn.part)
-                RTA_TRY(tiled_partials(fi, lw.w_in, rows, d.D, w.normed, B, w.proj, false, w.gemm_ws, w.gemm_bytes,
-                                       s, &ns, rn));
-            else if (xn.w)
-                RTA_TRY(projection_store(fi, lw.w_in, rows, d.D, w.hidden, B, w.proj, w.gemm_ws, w.gemm_bytes, s, rn,
-                                         xn));
-            else
-                RTA_TRY(rta_gemv(fi, lw.w_in, rows, d.D, w.normed, B, w.proj, RTA_EPI_STORE, w.gemm_ws,
-                                 w.gemm_bytes, stream));
+            if (lw.in_parts > 0) {
+                RTA_TRY(in_parts(lw, rows, ext));
+            } else {
+                RTA_TRY(norm(lw.norm_in, fi, ext));
+                if (imaged(fi))
+                    RTA_TRY(image_readout(fi, kReadStore, lw.w_in, nullptr, rows, d.D, w.ximg, B, w.proj, false,
+                                          w.gemm_ws, w.gemm_bytes, s, &ns, rn));
+                else if (rn.part)
+                    RTA_TRY(tiled_partials(fi, lw.w_in, rows, d.D, w.normed, B, w.proj, false, w.gemm_ws,
+                                           w.gemm_bytes, s, &ns, rn));
+                else if (xn.w)
+                    RTA_TRY(projection_store(fi, lw.w_in, rows, d.D, w.hidden, B, w.proj, w.gemm_ws, w.gemm_bytes,
+                                             s, rn, xn));
+                else
+                    RTA_TRY(rta_gemv(fi, lw.w_in, rows, d.D, w.normed, B, w.proj, RTA_EPI_STORE, w.gemm_ws,
+                                     w.gemm_bytes, stream));
+            }
             const bool slabs = ns > 1;
             // the a / b readouts into the slabs' place are done before the middle reads them;
             // with slabs pending they use the workspace after them

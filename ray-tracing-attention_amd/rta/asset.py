@@ -26,8 +26,10 @@ class AssetMatrix(ctypes.Structure):
                 ("mode", _u32)]
 
 
-# descriptor indices (export.py:96-98, 108-109, 121)
+# descriptor indices (export.py:96-98, 108-109, 121); the delta-net's separate ssm_beta /
+# ssm_alpha payloads (export.py:113)
 Q, K, OUT, FFN_GATE, FFN_DOWN, FFN_UP, GATE, V = 0, 1, 2, 3, 4, 5, 6, 8
+BETA, ALPHA = 9, 10
 
 
 class Asset:

@@ -22,14 +22,14 @@ class HybridShape(ctypes.Structure):
                 ("head_dim", _i), ("rec_heads", _i), ("ff", _i), ("vocab", _i), ("capacity", _i),
                 ("fmt_embed", _i), ("fmt_proj", _i), ("fmt_lm", _i), ("fmt_k", _i), ("fmt_v", _i),
                 ("rope_rotary", _i), ("eps", _f), ("margin", _f), ("rope_theta", _d),
-                ("attn_gate", _i), ("rec_key_heads", _i), ("layer_formats", _i)]
+                ("attn_gate", _i), ("rec_key_heads", _i), ("layer_formats", _i), ("o_axis_remap", _i)]
 
 
 class HybridLayer(ctypes.Structure):
     _fields_ = [(n, _p) for n in ("norm_in", "norm_post", "w_in", "w_o", "w_gate", "w_up", "w_down", "q_norm",
                                   "k_norm", "conv_w", "a_log", "dt_bias", "out_norm")] + \
                [("fmt_in", _i), ("fmt_o", _i), ("fmt_gate_up", _i), ("fmt_down", _i), ("w_a", _p), ("w_b", _p),
-                ("fmt_ab", _i)]
+                ("fmt_ab", _i), ("in_parts", _i), ("in_w", _p * 4), ("in_rows", _i * 4), ("in_fmt", _i * 4)]
 
 
 class HybridWeights(ctypes.Structure):
@@ -107,10 +107,12 @@ class DecodeModel:
 
     With shape.layer_formats, layer_fmts(l, full) gives each layer's formats as a dict
     {"in", "o", "gate_up", "down", "ab"}; separate_ab keeps the delta-net a / b rows as
-    matrices of their own (w_a, w_b).  self.fmts names each matrix's format."""
+    matrices of their own (w_a, w_b); in_parts(l, full), when it returns a list of
+    formats, splits the in-projection into that many parts of equal row counts
+    (matrices "<l>.w_in.<i>", each in its format).  self.fmts names each matrix's format."""
 
     def __init__(self, shape, batch, ctx, seed=20261115, dev="cuda:0", keep_gguf=False, layer_fmts=None,
-                 separate_ab=False):
+                 separate_ab=False, in_parts=None):
         self.lib = _lib_h()
         self.shape = shape
         self.batch = batch
@@ -174,16 +176,24 @@ class DecodeModel:
             f_in, f_o = lf.get("in", s.fmt_proj), lf.get("o", s.fmt_proj)
             f_gu, f_d, f_ab = lf.get("gate_up", s.fmt_proj), lf.get("down", s.fmt_proj), lf.get("ab", s.fmt_proj)
             L.fmt_in, L.fmt_o, L.fmt_gate_up, L.fmt_down, L.fmt_ab = f_in, f_o, f_gu, f_d, f_ab
+            split = in_parts(l, full) if in_parts else None
             if full:
                 rows = (s.q_heads * (2 if s.attn_gate else 1) + 2 * s.kv_heads) * hd
-                L.w_in = mat(f_in, rows, s.hidden, name=f"{l}.w_in").data_ptr()
+                if split:
+                    self._parts(L, l, split, rows, mat)
+                else:
+                    L.w_in = mat(f_in, rows, s.hidden, name=f"{l}.w_in").data_ptr()
                 L.w_o = mat(f_o, s.hidden, s.q_heads * hd, name=f"{l}.w_o").data_ptr()
                 L.q_norm = vec(_near_one(s.q_heads * hd, gen, self.dev), f"{l}.q_norm")
                 L.k_norm = vec(_near_one(s.kv_heads * hd, gen, self.dev), f"{l}.k_norm")
             else:
                 rows = 2 * KH * hd + 2 * S + (0 if separate_ab else 2 * H)
-                L.w_in = mat(f_in, rows, s.hidden, small_rows=0 if separate_ab else 2 * H,
-                             name=f"{l}.w_in").data_ptr()
+                if split:
+                    assert separate_ab, "in-projection parts hold no a / b rows"
+                    self._parts(L, l, split, rows, mat)
+                else:
+                    L.w_in = mat(f_in, rows, s.hidden, small_rows=0 if separate_ab else 2 * H,
+                                 name=f"{l}.w_in").data_ptr()
                 if separate_ab:
                     L.w_a = mat(f_ab, H, s.hidden, small_rows=H, name=f"{l}.w_a").data_ptr()
                     L.w_b = mat(f_ab, H, s.hidden, small_rows=H, name=f"{l}.w_b").data_ptr()
@@ -235,6 +245,16 @@ class DecodeModel:
         self.workspace = torch.empty(self.ws_bytes, dtype=torch.uint8, device=self.dev)
         self.tokens = torch.randint(0, s.vocab, (batch,), dtype=torch.int32, device=self.dev, generator=gen)
         self.logits = None
+
+    def _parts(self, L, l, fmts, rows, mat):
+        n = len(fmts)
+        assert 0 < n <= 4 and rows % (16 * n) == 0, (rows, n)
+        L.in_parts = n
+        self.parts = getattr(self, "parts", {})
+        self.parts[l] = [(rows // n, f) for f in fmts]
+        for i, f in enumerate(fmts):
+            L.in_w[i] = mat(f, rows // n, self.shape.hidden, name=f"{l}.w_in.{i}").data_ptr()
+            L.in_rows[i], L.in_fmt[i] = rows // n, f
 
     def _random_packets(self, pk, gen):
         """K (Q4_K) / V (Q6_K) history fields with random quants and sane block scales."""

@@ -27,6 +27,13 @@ def reference_step(m, tokens, ctx, rec, conv, packets_after):
     KH = s.rec_key_heads or H
     fmt = lambda name: m.fmts[name] & 0xff   # the GGUF format a (possibly packed) matrix came from
     gemv = lambda name, rows, cols, x: orc.gemv_f64(fmt(name), g[name], rows, cols, x.astype(f32))
+    parts = getattr(m, "parts", {})
+
+    def in_projection(l, rows, x):   # w_in, or its parts side by side
+        if l not in parts:
+            return gemv(f"{l}.w_in", rows, D, x)
+        assert sum(r for r, _ in parts[l]) == rows
+        return np.concatenate([gemv(f"{l}.w_in.{i}", r, D, x) for i, (r, _) in enumerate(parts[l])], axis=1)
     x = orc.embed(s.fmt_embed, g["embed"], s.vocab, D, tokens).astype(np.float64)
     new_rec, new_conv = rec.astype(np.float64).copy(), conv.copy()
     kv_new = []
@@ -35,7 +42,7 @@ def reference_step(m, tokens, ctx, rec, conv, packets_after):
         n = orc.rmsnorm(x.astype(f32), g[f"{l}.norm_in"], s.eps)
         if l % s.full_every == s.full_every - 1:
             rows = (hq * (2 if s.attn_gate else 1) + 2 * hkv) * hd
-            p = gemv(f"{l}.w_in", rows, D, n)
+            p = in_projection(l, rows, n)
             q = orc.head_norm(p[:, :hq * hd].astype(f32), hq, hd, w=g[f"{l}.q_norm"], eps=s.eps)
             k = orc.head_norm(p[:, hq * hd:(hq + hkv) * hd].astype(f32), hkv, hd, w=g[f"{l}.k_norm"], eps=s.eps)
             q = np.stack([orc.rope(q[b].reshape(hq, hd).astype(f32), ctx[b], s.rope_rotary, s.rope_theta)
@@ -48,12 +55,17 @@ def reference_step(m, tokens, ctx, rec, conv, packets_after):
             flat = packets_after[lf].reshape(B * cap, -1)
             attn, _, _ = orc.decode_attention(q.astype(f32), flat, s.fmt_k, s.fmt_v, [b * cap for b in range(B)],
                                               [c + 1 for c in ctx], cap, hkv, gate=gate)
+            if getattr(s, "o_axis_remap", 0):   # dim d of a head back to the exporter's column rot(d)
+                to = [orc.remap_row(3, hd, s.rope_rotary, 0, r) for r in range(hq * hd)]
+                out = np.empty_like(attn.reshape(B, -1))
+                out[:, to] = attn.reshape(B, -1)
+                attn = out
             x = x + gemv(f"{l}.w_o", D, hq * hd, attn.reshape(B, -1))
             lf += 1
         else:
             sep = f"{l}.w_a" in g
             rows = 2 * KH * hd + 2 * S + (0 if sep else 2 * H)
-            p = gemv(f"{l}.w_in", rows, D, n)
+            p = in_projection(l, rows, n)
             # q and k of delta-net head h are rows of key head h % KH: the key repeat of
             # resident_quant.glsl:26 (mode 5) over the logical rows
             rep = np.array([orc.remap_row(5, 0, 0, KH * hd, r) for r in range(S)])

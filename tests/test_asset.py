@@ -65,6 +65,11 @@ def test_reader_returns_every_tensor(tmp_path):
                     assert (got_fmt, got_mode) == (fmt, mode)
                     np.testing.assert_array_equal(got, raw[r0:r0 + 16].ravel())
                 np.testing.assert_array_equal(a.vector(layer, 37, spec["state_heads"]), floats[p + "ssm_dt.bias"])
+                for idx, name in ((ra.BETA, "ssm_beta"), (ra.ALPHA, "ssm_alpha")):
+                    fmt, raw = packed[p + name + ".weight"]
+                    got_fmt, got_mode, got = a.matrix(layer, idx, raw.nbytes)
+                    assert (got_fmt, got_mode) == (fmt, 0), name
+                    np.testing.assert_array_equal(got, raw.ravel())
         for which, name in ((0, "token_embd.weight"), (1, "output.weight")):
             fmt, raw = packed[name]
             got_fmt, got = a.basis(which, raw.nbytes)
@@ -90,7 +95,7 @@ def test_out_of_range_requests(tmp_path):
         with pytest.raises(Exception):
             a.matrix(2, 0, 16)
         with pytest.raises(Exception):
-            a.matrix(0, 9, 16)
+            a.matrix(0, 11, 16)
         with pytest.raises(Exception):
             a.vector(0, 0, a.info.param_words + 1)
         for count in (2 ** 64 - 1, 2 ** 64 - 8, 2 ** 63):     # off + count would wrap past the check

@@ -51,6 +51,30 @@ def _exporter_fmts(l, full):
     return {"in": Q4_K, "o": F16, "gate_up": Q6_K | TILED, "down": Q4_K | TILED, "ab": 0}
 
 
+def _part_fmts(l, full):
+    from rta._lib import F32, Q4_K, Q6_K, TILED
+    return [Q4_K, Q6_K] if full else [Q4_K, Q6_K | TILED, F32]
+
+
+@pytest.mark.parametrize("batch", [1, 5, 32])
+def test_hybrid_decode_steps_in_projection_parts(batch):
+    """In-projections as matrices of their own formats (the exporter's attn_q / attn_k /
+    attn_v / attn_qkv / attn_gate), and the attention output in the exporter's column
+    order in front of w_o (o_axis_remap)."""
+    from rta import model
+    from rta._lib import Q4_K, Q6_K, TILED
+    shape = model.HybridShape(hidden=512, layers=4, full_every=2, q_heads=4, kv_heads=2, head_dim=128, rec_heads=4,
+                              ff=512, vocab=3001, capacity=64, fmt_embed=Q4_K, fmt_proj=Q4_K,
+                              fmt_lm=Q6_K, fmt_k=Q4_K, fmt_v=Q6_K, rope_rotary=64, eps=1e-6, margin=1e-4,
+                              rope_theta=1e6, attn_gate=1, rec_key_heads=2, layer_formats=1, o_axis_remap=1)
+    ctx = [(7 + 11 * b) % 90 for b in range(batch)]
+    fmts = lambda l, full: {"in": Q4_K, "o": Q4_K, "gate_up": Q4_K, "down": Q6_K | (TILED if batch > 1 else 0),  # noqa
+                            "ab": 0}
+    m = model.DecodeModel(shape, batch, ctx, seed=31 + batch, keep_gguf=True, layer_fmts=fmts, separate_ab=True,
+                          in_parts=_part_fmts)
+    check_steps(m, 2)
+
+
 @pytest.mark.parametrize("batch", [1, 3, 20, 40])
 def test_hybrid_decode_steps_exported_layout(batch):
     from rta import model
