@@ -1,17 +1,25 @@
 // rt_optical_resident: a resident worker with the reference worker's command line and
 // stdin/stdout protocol (ray_tracing/native/src/optical_resident.cpp:966-969, framing
-// ray_tracing/runtime/resident_runtime.py:41-44,101-114), serving the three diagnostic
-// requests of the detector path on the gfx950 library:
+// ray_tracing/runtime/resident_runtime.py:41-44,101-114) on the gfx950 library:
+//   op 1 / 11 / 12  prefill        (prefill,        optical_resident.cpp:609-; resident_runtime.py:116-162)
+//   op 2            generate       (generate,       optical_resident.cpp:872-885; resident_runtime.py:171-173)
+//   op 9            token stream   (streamGenerate, optical_resident.cpp:886; resident_runtime.py:174-188)
+//   op 10           history growth (growTree,       optical_resident.cpp:232-271; resident_runtime.py:91-99)
+//   op 13           finish history (finishHistory,  optical_resident.cpp:743-757; resident_runtime.py:164-169)
 //   op 4  vocabulary readout  (wordCheck,      optical_resident.cpp:889-905; resident_runtime.py:235-250)
 //   op 6  SwiGLU MLP check    (mlpCheck,       optical_resident.cpp:922-949; resident_runtime.py:252-263)
 //   op 14 full-attention check (attentionCheck, resident_attention_runtime.inl:646-;
 //                               resident_runtime.py:265-345), standard backend, dense receipts
-// plus op 8 (resources) and op 0 (end).  Other operations (prefill, generation, ...)
-// end the worker with "Unknown resident operation" on stderr, as the reference does
-// for an operation it does not know.  Weights come from the exported assets through
-// rta_asset_*; every computation runs in librta's HIP kernels.
+// plus op 8 (resources) and op 0 (end).  Other operations end the worker with "Unknown
+// resident operation" on stderr, as the reference does for an operation it does not
+// know.  Weights come from the exported assets through rta_asset_*; every computation
+// runs in librta's HIP kernels.  Generation runs rta_hybrid_decode_step on one
+// sequence: the prompt one token per step, then one step per generated token.  The
+// reference's shared-history and reply caches are not kept (every prefill computes
+// its whole prompt; replies report no cache hits).
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <chrono>
 #include <cmath>
 #include <cstdio>
@@ -27,6 +35,7 @@
 #include <vector>
 
 #include "../../include/rta.h"
+#include "../csrc/rta_remap.hpp"
 
 namespace {
 
@@ -142,6 +151,295 @@ double wall_ms(std::chrono::steady_clock::time_point t0) {
     return std::chrono::duration<double, std::milli>(std::chrono::steady_clock::now() - t0).count();
 }
 
+template <class T>
+void input_value(T& v) {
+    std::cin.read(reinterpret_cast<char*>(&v), sizeof(T));
+}
+
+// The asset laid out as rta_hybrid_decode_step reads it, for one sequence in GGUF row
+// layout: each projection's rows gathered on the host with the exporter's row mode
+// (resident_quant.glsl:20-31) applied, the in-projection sections [q | k | v | gate] /
+// [q | k | v | z] of equal formats joined into one matrix, and the O projection's axis
+// mode 4 kept as the step's o_axis_remap.
+struct Decoder {
+    rta_hybrid_shape shape{};
+    std::vector<rta_hybrid_layer> layers;
+    rta_hybrid_weights weights{};
+    std::vector<std::unique_ptr<Device>> mem;
+    std::unique_ptr<Device> state;
+    Device ws, tokens, prompt, zero_ctx;
+    size_t ws_bytes = 0;
+
+    const void* put(const void* host, size_t bytes) {
+        mem.push_back(std::make_unique<Device>());
+        Device& d = *mem.back();
+        d.ensure(bytes);
+        hip_check(hipMemcpy(d.p, host, bytes, hipMemcpyHostToDevice), "upload");
+        return d.p;
+    }
+
+    struct Section {
+        std::vector<uint8_t> rows;   // gathered GGUF rows
+        uint32_t fmt;
+        int count;
+    };
+
+    // `rows` logical rows of descriptor (layer, index), source row r of the payload for
+    // logical row r given by the remap (src_rows rows in the payload)
+    static Section gather(rta_asset* a, int layer, int index, int rows, int cols, int src_rows, const rta::Remap& m,
+                          const char* what) {
+        rta_asset_matrix mx{};
+        rta_check(rta_asset_layer_matrix(a, layer, index, &mx), "asset matrix");
+        const size_t rb = row_bytes(mx.fmt, (uint64_t)cols);
+        if ((uint64_t)src_rows * rb > mx.avail_bytes) throw std::runtime_error("Truncated geometric weights");
+        Section out{std::vector<uint8_t>((size_t)rows * rb), mx.fmt, rows};
+        const uint8_t* src = static_cast<const uint8_t*>(mx.data);
+        for (int r = 0; r < rows; ++r) {
+            const int64_t sr = m.source_row(r);
+            if (sr < 0 || sr >= src_rows) throw std::runtime_error(std::string("Invalid row mode of ") + what);
+            std::memcpy(out.rows.data() + (size_t)r * rb, src + (size_t)sr * rb, rb);
+        }
+        return out;
+    }
+
+    static uint32_t mode_of(rta_asset* a, int layer, int index) {
+        rta_asset_matrix mx{};
+        rta_check(rta_asset_layer_matrix(a, layer, index, &mx), "asset matrix");
+        return mx.mode;
+    }
+
+    // a mode-0 matrix as it lies in the payload: (device pointer, format)
+    std::pair<const void*, int> plain(rta_asset* a, int layer, int index, int rows, int cols, const char* what) {
+        rta_asset_matrix mx{};
+        rta_check(rta_asset_layer_matrix(a, layer, index, &mx), "asset matrix");
+        if (mx.mode != 0) throw std::runtime_error(std::string("Unsupported projection mode of ") + what);
+        const size_t bytes = (size_t)rows * row_bytes(mx.fmt, (uint64_t)cols);
+        if (bytes > mx.avail_bytes) throw std::runtime_error("Truncated geometric weights");
+        return {put(mx.data, bytes), (int)mx.fmt};
+    }
+
+    // joins adjacent sections of one format into one matrix each (at most 4 parts)
+    void in_projection(rta_hybrid_layer& L, const std::vector<Section>& sec) {
+        std::vector<Section> parts;
+        for (const Section& s : sec) {
+            if (!parts.empty() && parts.back().fmt == s.fmt) {
+                parts.back().rows.insert(parts.back().rows.end(), s.rows.begin(), s.rows.end());
+                parts.back().count += s.count;
+            } else {
+                parts.push_back(s);
+            }
+        }
+        if (parts.size() > 4) throw std::runtime_error("Too many in-projection formats");
+        if (parts.size() == 1) {
+            L.w_in = put(parts[0].rows.data(), parts[0].rows.size());
+            L.fmt_in = (int)parts[0].fmt;
+            return;
+        }
+        L.in_parts = (int)parts.size();
+        L.fmt_in = (int)parts[0].fmt;
+        for (size_t i = 0; i < parts.size(); ++i) {
+            L.in_w[i] = put(parts[i].rows.data(), parts[i].rows.size());
+            L.in_rows[i] = parts[i].count;
+            L.in_fmt[i] = (int)parts[i].fmt;
+        }
+    }
+
+    const float* vec(rta_asset* a, int layer, int field, uint64_t count) {
+        const float* v = nullptr;
+        rta_check(rta_asset_vector(a, layer, field, count, &v), "asset vector");
+        return static_cast<const float*>(put(v, count * 4));
+    }
+
+    void build(rta_asset* a, const rta_asset_info& info, const std::string& json, uint32_t capacity) {
+        const int D = (int)info.hidden, L = (int)info.depth, hd = (int)spec_value(json, "attention_head_dim", 0, true);
+        const int kvh = (int)spec_value(json, "kv_heads", 0, true);
+        if (hd != 128) throw std::runtime_error("This worker requires 128-wide attention heads");
+        std::vector<int> kind(L);
+        int first_full = -1, heads = 0, rec_heads = 0, rotary = 0;
+        for (int l = 0; l < L; ++l) {
+            uint32_t k = 0, h = 0;
+            rta_check(rta_asset_word(a, l, 26, &k), "asset word");
+            rta_check(rta_asset_word(a, l, 23, &h), "asset word");
+            if (k != 1u && k != 2u) throw std::runtime_error("Unknown resident layer kind");
+            kind[l] = (int)k;
+            if (k == 1u) {
+                uint32_t r = 0;
+                rta_check(rta_asset_word(a, l, 29, &r), "asset word");
+                if (first_full < 0) {
+                    first_full = l;
+                    heads = (int)h;
+                    rotary = (int)r;
+                } else if ((int)h != heads || (int)r != rotary) {
+                    throw std::runtime_error("Full layers of different shapes");
+                }
+            } else if (rec_heads && (int)h != rec_heads) {
+                throw std::runtime_error("Recurrent layers of different shapes");
+            } else {
+                rec_heads = (int)h;
+            }
+        }
+        const int every = first_full < 0 ? 0 : first_full + 1;
+        for (int l = 0; l < L; ++l)
+            if ((kind[l] == 1) != (every > 0 && l % every == every - 1))
+                throw std::runtime_error("Full layers must repeat with one period");
+        const int key_heads = (int)spec_value(json, "state_key_heads", rec_heads ? rec_heads : 1, false);
+        shape.hidden = D;
+        shape.layers = L;
+        shape.full_every = every;
+        shape.q_heads = heads;
+        shape.kv_heads = kvh;
+        shape.head_dim = hd;
+        shape.rec_heads = rec_heads;
+        shape.ff = (int)info.middle;
+        shape.vocab = (int)info.vocab;
+        shape.capacity = (int)capacity;
+        shape.fmt_embed = (int)info.fmt_embed;
+        shape.fmt_proj = RTA_Q4_K;
+        shape.fmt_lm = (int)info.fmt_lm;
+        shape.fmt_k = RTA_Q4_K;   // the history quantisation (resident_history_quant.glsl)
+        shape.fmt_v = RTA_Q6_K;
+        shape.rope_rotary = rotary ? rotary : hd;
+        shape.eps = (float)spec_value(json, "norm_epsilon", 1e-6, false);
+        shape.margin = 0.0f;      // the plain argmax, ties to the lower id (resident_math.comp:117-130)
+        shape.rope_theta = spec_value(json, "rope_theta", 1e7, false);
+        shape.rec_key_heads = rec_heads ? key_heads : 0;
+        shape.layer_formats = 1;
+        const int S = rec_heads * hd, KW = key_heads * hd;
+        layers.assign(L, rta_hybrid_layer{});
+        int o_remap = -1;
+        for (int l = 0; l < L; ++l) {
+            rta_hybrid_layer& Lw = layers[l];
+            Lw.norm_in = vec(a, l, 0, D);
+            Lw.norm_post = vec(a, l, 1, D);
+            if (kind[l] == 1) {
+                const uint32_t mq = mode_of(a, l, 0), mk = mode_of(a, l, 1), mv = mode_of(a, l, 8),
+                               mo = mode_of(a, l, 2), mg = mode_of(a, l, 6);
+                const bool gate = mg == RTA_REMAP_GATE;
+                if ((mq != 0 && mq != RTA_REMAP_QUERY && mq != RTA_REMAP_ROTARY) || (mk != 0 && mk != RTA_REMAP_ROTARY) ||
+                    (mv != 0 && mv != RTA_REMAP_ROTARY) || (mo != 0 && mo != RTA_REMAP_AXES) || (gate && mq != RTA_REMAP_QUERY))
+                    throw std::runtime_error("Unsupported attention projection modes");
+                if (o_remap >= 0 && o_remap != (mo == RTA_REMAP_AXES)) throw std::runtime_error("Unsupported attention projection modes");
+                o_remap = mo == RTA_REMAP_AXES;
+                shape.attn_gate = gate;
+                auto remap = [&](uint32_t mode) { return rta::Remap{(int)mode, hd, rotary, 0}; };
+                const int qw = heads * hd, gw = kvh * hd;
+                std::vector<Section> sec;
+                sec.push_back(gather(a, l, 0, qw, D, mq == RTA_REMAP_QUERY ? 2 * qw : qw, remap(mq), "attn_q"));
+                sec.push_back(gather(a, l, 1, gw, D, gw, remap(mk), "attn_k"));
+                sec.push_back(gather(a, l, 8, gw, D, gw, remap(mv), "attn_v"));
+                if (gate) sec.push_back(gather(a, l, 6, qw, D, 2 * qw, remap(mg), "attention gate"));
+                in_projection(Lw, sec);
+                rta_asset_matrix mx{};
+                rta_check(rta_asset_layer_matrix(a, l, 2, &mx), "asset matrix");
+                const size_t ob = (size_t)D * row_bytes(mx.fmt, (uint64_t)qw);
+                if (ob > mx.avail_bytes) throw std::runtime_error("Truncated geometric weights");
+                Lw.w_o = put(mx.data, ob);
+                Lw.fmt_o = (int)mx.fmt;
+                Lw.q_norm = vec(a, l, 24, (uint64_t)qw);
+                Lw.k_norm = vec(a, l, 25, (uint64_t)gw);
+            } else {
+                const uint32_t mq = mode_of(a, l, 0), mk = mode_of(a, l, 1);
+                for (uint32_t m : {mq, mk})
+                    if (m != RTA_REMAP_KEY_REPEAT && !(m == 0 && key_heads == rec_heads))
+                        throw std::runtime_error("Unsupported recurrent projection modes");
+                const rta::Remap id{};
+                std::vector<Section> sec;
+                sec.push_back(gather(a, l, 0, KW, D, KW, id, "attn_qkv"));
+                sec.push_back(gather(a, l, 1, KW, D, KW, id, "attn_qkv"));
+                for (int idx : {8, 6}) {
+                    if (mode_of(a, l, idx) != 0) throw std::runtime_error("Unsupported recurrent projection modes");
+                    sec.push_back(gather(a, l, idx, S, D, S, id, idx == 8 ? "attn_qkv" : "attn_gate"));
+                }
+                in_projection(Lw, sec);
+                auto o = plain(a, l, 2, D, S, "ssm_out");
+                Lw.w_o = o.first;
+                Lw.fmt_o = o.second;
+                auto beta = plain(a, l, 9, rec_heads, D, "ssm_beta");
+                auto alpha = plain(a, l, 10, rec_heads, D, "ssm_alpha");
+                if (beta.second != alpha.second) throw std::runtime_error("ssm_alpha and ssm_beta differ in format");
+                Lw.w_a = alpha.first;
+                Lw.w_b = beta.first;
+                Lw.fmt_ab = alpha.second;
+                Lw.conv_w = vec(a, l, 34, (uint64_t)3 * S * 4);
+                Lw.dt_bias = vec(a, l, 37, (uint64_t)rec_heads);
+                Lw.a_log = vec(a, l, 38, (uint64_t)rec_heads);
+                Lw.out_norm = vec(a, l, 31, (uint64_t)S);
+            }
+            auto g = plain(a, l, 3, (int)info.middle, D, "ffn_gate");
+            auto u = plain(a, l, 5, (int)info.middle, D, "ffn_up");
+            auto dn = plain(a, l, 4, D, (int)info.middle, "ffn_down");
+            if (g.second != u.second) throw std::runtime_error("ffn_gate and ffn_up differ in format");
+            Lw.w_gate = g.first;
+            Lw.w_up = u.first;
+            Lw.fmt_gate_up = g.second;
+            Lw.w_down = dn.first;
+            Lw.fmt_down = dn.second;
+        }
+        shape.o_axis_remap = o_remap > 0;
+        rta_asset_matrix e{}, h{};
+        rta_check(rta_asset_basis(a, 0, &e), "asset basis");
+        rta_check(rta_asset_basis(a, 1, &h), "asset basis");
+        const size_t eb = (size_t)info.vocab * row_bytes(e.fmt, D), hb = (size_t)info.vocab * row_bytes(h.fmt, D);
+        if (eb > e.avail_bytes || hb > h.avail_bytes) throw std::runtime_error("Truncated original word basis");
+        weights.embed = put(e.data, eb);
+        weights.lm_head = e.offset_words == h.offset_words && e.fmt == h.fmt ? weights.embed : put(h.data, hb);
+        weights.norm_final = vec(a, -1, 4, D);
+        weights.layers = layers.data();
+        tokens.ensure(256);
+        int32_t zero = 0;
+        zero_ctx.ensure(256);
+        hip_check(hipMemcpy(zero_ctx.p, &zero, 4, hipMemcpyHostToDevice), "upload");
+        allocate(capacity);
+    }
+
+    void allocate(uint32_t capacity) {
+        shape.capacity = (int)capacity;
+        const size_t sb = rta_hybrid_state_bytes(&shape, 1), wb = rta_hybrid_workspace_bytes(&shape, 1);
+        if (!sb || !wb) throw std::runtime_error("Unsupported resident model shape");
+        state = std::make_unique<Device>();
+        state->ensure(sb);
+        ws.ensure(wb);
+        ws_bytes = wb;
+    }
+
+    // a fresh sequence at position 0: zero recurrent and conv states
+    void reset(hipStream_t s) {
+        hip_check(hipMemsetAsync(state->p, 0, state->n, s), "clear state");
+        rta_check(rta_hybrid_init(&shape, 1, state->p, zero_ctx.as<int32_t>(), s), "rta_hybrid_init");
+    }
+
+    // one step: tokens[0] in, the greedy next token out
+    void step(hipStream_t s) {
+        rta_check(rta_hybrid_decode_step(&shape, &weights, 1, state->p, tokens.as<uint32_t>(), nullptr, ws.p, ws_bytes, s),
+                  "rta_hybrid_decode_step");
+    }
+
+    // the history ring grows to `next` slots; recurrent, conv and packet state are kept
+    void grow(uint32_t next, hipStream_t s) {
+        std::unique_ptr<Device> old = std::move(state);
+        const uint32_t previous = (uint32_t)shape.capacity;
+        rta_hybrid_views ov{}, nv{};
+        rta_check(rta_hybrid_layout(&shape, 1, old->p, &ov), "rta_hybrid_layout");
+        allocate(next);
+        rta_check(rta_hybrid_layout(&shape, 1, state->p, &nv), "rta_hybrid_layout");
+        const int nfull = shape.full_every > 0 ? shape.layers / shape.full_every : 0, nrec = shape.layers - nfull;
+        hip_check(hipMemsetAsync(state->p, 0, state->n, s), "clear state");
+        if (nrec) {
+            hip_check(hipMemcpyAsync(nv.recurrent, ov.recurrent, (size_t)nrec * ov.recurrent_per_layer * 4,
+                                     hipMemcpyDeviceToDevice, s), "copy state");
+            hip_check(hipMemcpyAsync(nv.conv, ov.conv, (size_t)nrec * ov.conv_per_layer * 4, hipMemcpyDeviceToDevice, s),
+                      "copy state");
+        }
+        for (int l = 0; l < nfull; ++l)
+            hip_check(hipMemcpyAsync(nv.packets + (size_t)l * nv.slots_per_layer * nv.packet_bytes,
+                                     ov.packets + (size_t)l * ov.slots_per_layer * ov.packet_bytes,
+                                     (size_t)previous * ov.packet_bytes, hipMemcpyDeviceToDevice, s),
+                      "copy history");
+        rta_check(rta_hybrid_init(&shape, 1, state->p, ov.ctx, s), "rta_hybrid_init");
+        hip_check(hipStreamSynchronize(s), "sync");
+    }
+};
+
 struct Worker {
     rta_asset* asset = nullptr;
     rta_asset_info info{};
@@ -150,6 +448,11 @@ struct Worker {
     std::vector<int> full;   // full-attention layers
     bool attention_gate = false;
     hipStream_t stream{};
+    std::string json;                                 // model.json
+    std::unique_ptr<Decoder> dec;                     // built by the first prefill / growth
+    bool prefilled = false, diagnostic_dirty = false;
+    uint32_t control[8] = {0, 0, 1, 0, 0xffffffffu, 0xffffffffu, 0, 0};   // (resident_math.comp:130)
+    uint64_t position = 0;                            // absolute position (emitted tokens count)
     std::map<int, std::unique_ptr<Device>> uploads;   // (layer, index) -> device payload
     Device ws, x, act, y, logits, ids, rows, q, kbuf, vbuf, gate, out, m, z, packets, slots, ctx;
 
@@ -413,6 +716,156 @@ struct Worker {
         reply(o);
     }
 
+    Decoder& decoder() {
+        if (!dec) {
+            dec = std::make_unique<Decoder>();
+            dec->build(asset, info, json, capacity);
+        }
+        return *dec;
+    }
+
+    // op 1 / 11 / 12: the prompt (at most capacity ids) from position 0, one decode step
+    // per token; the last step leaves the first generated token pending on the device.
+    void prefill(uint32_t count, uint32_t debug, uint32_t checkpoint_mode) {
+        if (debug == 1u) throw std::runtime_error("Layer capture is not provided by this worker");
+        if (debug > 2u || !count || count > capacity) throw std::runtime_error("Invalid resident prefix");
+        std::vector<uint32_t> ids;
+        input(ids, count);
+        uint32_t stops[2];
+        std::cin.read(reinterpret_cast<char*>(stops), 8);
+        uint32_t boundary = count;
+        if (checkpoint_mode == 1u) input_value(boundary);
+        if (checkpoint_mode == 2u) {
+            uint32_t n = 0;
+            input_value(n);
+            if (n > 4096u) throw std::runtime_error("Too many history boundaries");
+            uint32_t stable = 0;
+            for (uint32_t i = 0; i < n; ++i) {
+                uint32_t v[2];
+                std::cin.read(reinterpret_cast<char*>(v), 8);
+                if (!v[0] || v[0] > count || !(v[1] & 15u) || v[1] > 15u) throw std::runtime_error("Invalid history boundary");
+                if (v[1] & 1u) stable = std::max(stable, v[0]);
+            }
+            if (stable) boundary = stable;
+        }
+        if (!std::cin || !boundary || boundary > count || *std::max_element(ids.begin(), ids.end()) >= info.vocab)
+            throw std::runtime_error("Invalid prefix word IDs or boundary");
+        const auto t0 = std::chrono::steady_clock::now();
+        Decoder& d = decoder();
+        d.prompt.ensure((size_t)count * 4);
+        hip_check(hipMemcpyAsync(d.prompt.p, ids.data(), (size_t)count * 4, hipMemcpyHostToDevice, stream), "upload prompt");
+        Timer t;
+        t.start(stream);
+        d.reset(stream);
+        for (uint32_t i = 0; i < count; ++i) {
+            hip_check(hipMemcpyAsync(d.tokens.p, d.prompt.as<uint32_t>() + i, 4, hipMemcpyDeviceToDevice, stream),
+                      "prompt token");
+            d.step(stream);
+        }
+        const double gpu = t.stop(stream);
+        uint32_t bits = 0;
+        rta_check(rta_device_error(&bits, 1), "rta_device_error");
+        if (bits) throw std::runtime_error("Resident prefix optical error " + std::to_string(bits));
+        const uint32_t initial[8] = {0, 0, 1, 0, stops[0], stops[1], 0, 0};
+        std::memcpy(control, initial, sizeof(control));
+        prefilled = true;
+        diagnostic_dirty = false;
+        position = count;
+        std::vector<char> o;
+        const std::vector<double> times{0.0, gpu, 0.0, wall_ms(t0), 0.0, 0.0};
+        append(o, times);
+        append(o, control, 8);
+        // (tokens per compute batch, batches, tree updates, query positions)
+        const std::vector<uint64_t> footer{1u, count, 0u, count};
+        append(o, footer);
+        reply(o);
+    }
+
+    // Up to count tokens (resident_math.comp:130: each readout's id is emitted, and a stop
+    // id ends the stream without a forward of it); returns whether the stream goes on.
+    bool generate(uint32_t count, uint32_t debug) {
+        if (diagnostic_dirty) throw std::runtime_error("Attention diagnostics replace history; prefill again before generation");
+        if (!prefilled || !count || count > 64) throw std::runtime_error("Resident generation expects 1..64 tokens after prefill");
+        if (debug == 1u) throw std::runtime_error("Layer capture is not provided by this worker");
+        const auto t0 = std::chrono::steady_clock::now();
+        Decoder& d = *dec;
+        uint32_t ids[64] = {};
+        uint32_t emitted = 0, computed = 0;
+        Timer t;
+        t.start(stream);
+        while (emitted < count && control[2]) {
+            uint32_t id = 0;
+            hip_check(hipMemcpyAsync(&id, d.tokens.p, 4, hipMemcpyDeviceToHost, stream), "read token");
+            hip_check(hipStreamSynchronize(stream), "sync");
+            if (id >= info.vocab) throw std::runtime_error("Resident decode optical error 2048");
+            ids[emitted++] = id;
+            control[0] = id;
+            ++position;
+            if (id == control[4] || id == control[5]) {
+                control[2] = 0;
+                break;
+            }
+            d.step(stream);   // reads the pending id, leaves the next one
+            ++computed;
+        }
+        const double gpu = t.stop(stream);
+        uint32_t bits = 0;
+        rta_check(rta_device_error(&bits, 1), "rta_device_error");
+        if (bits) throw std::runtime_error("Resident decode optical error " + std::to_string(bits));
+        control[1] = emitted;
+        // GenerationPacket (optical_resident.cpp:57-71): timing, control, ids, hits, then
+        // the telemetry / cache / recovery fields, here all zero
+        std::vector<double> timing(18, 0.0);
+        timing[0] = gpu;
+        timing[1] = wall_ms(t0);
+        timing[2] = timing[3] = (double)std::max(computed, 1u);
+        timing[6] = (double)position;
+        std::vector<char> o;
+        append(o, timing);
+        append(o, control, 8);
+        append(o, ids, 64);
+        const uint32_t mlp = computed * info.depth * info.middle;
+        const uint32_t hits[5] = {mlp, mlp, emitted * info.vocab, 0u, 0xffffffffu};
+        append(o, hits, 5);
+        append(o, std::vector<double>(4, 0.0));    // RT query time per kind
+        append(o, std::vector<uint32_t>(4, 0u));   // cached tokens, cache queries, nodes, capacity
+        append(o, std::vector<double>(2 + 3, 0.0));  // cache time; cached-state recovery
+        append(o, std::vector<uint32_t>(2, 0u));   // cache candidates, rejected
+        append(o, std::vector<uint64_t>(2, 0u));   // MLP route rows
+        if (debug == 2u) append(o, std::vector<double>(2, 0.0));   // detector time (attention, recurrent)
+        reply(o);
+        return control[2] != 0;
+    }
+
+    void stream_generate(uint32_t count, uint32_t debug) {
+        if (!count || count > 64) throw std::runtime_error("Resident stream expects 1..64 tokens");
+        for (uint32_t i = 0; i < count; ++i)
+            if (!generate(1u, debug)) break;
+    }
+
+    // op 10: the history ring grows to `next` slots, the live history kept
+    void grow(uint32_t next) {
+        if (next <= capacity || next > 1048576u || capacity < 32u) throw std::runtime_error("Invalid tree growth request");
+        const auto t0 = std::chrono::steady_clock::now();
+        const uint32_t previous = capacity;
+        if (dec) {
+            if (prefilled) dec->grow(next, stream);
+            else dec->allocate(next);
+        }
+        capacity = next;
+        std::vector<char> o;
+        append(o, std::vector<double>{(double)previous, (double)next, wall_ms(t0)});
+        reply(o);
+    }
+
+    // op 13: no shared history cache is kept, so nothing is saved
+    void finish_history() {
+        std::vector<char> o;
+        append(o, std::vector<uint64_t>{0u, 0u, 0u});
+        append(o, std::vector<double>{0.0});
+        reply(o);
+    }
+
     void resources() {
         size_t free_b = 0, total_b = 0;
         hip_check(hipMemGetInfo(&free_b, &total_b), "hipMemGetInfo");
@@ -461,7 +914,8 @@ int main(int argc, char** argv) {
         std::ifstream jf(dir + "/model.json");
         std::stringstream js;
         js << jf.rdbuf();
-        const std::string json = js.str();
+        w.json = js.str();
+        const std::string& json = w.json;
         w.kv_heads = (uint32_t)spec_value(json, "kv_heads", 0, true);
         w.hd = (uint32_t)spec_value(json, "attention_head_dim", 0, true);
         w.heads = (uint32_t)spec_value(json, "attention_heads", 0, true);
@@ -476,9 +930,9 @@ int main(int argc, char** argv) {
         }
         hip_check(hipSetDevice(0), "hipSetDevice");
         hip_check(hipStreamCreate(&w.stream), "hipStreamCreate");
-        // 0x52545239: no native token stream; mode: quantisation 4, full-matrix MLP (4096),
-        // exact ordered detector (131072)
-        const uint32_t hello[5] = {0x52545239u, w.info.depth, w.info.blocks, w.info.middle, 4u | 4096u | 131072u};
+        // 0x5254523a: native token stream (op 9); mode: quantisation 4, full-matrix MLP
+        // (4096), exact ordered detector (131072)
+        const uint32_t hello[5] = {0x5254523au, w.info.depth, w.info.blocks, w.info.middle, 4u | 4096u | 131072u};
         std::cout.write(reinterpret_cast<const char*>(hello), 20);
         std::cout.flush();
         uint32_t op;
@@ -487,11 +941,20 @@ int main(int argc, char** argv) {
             uint32_t count, debug;
             if (!std::cin.read(reinterpret_cast<char*>(&count), 4) || !std::cin.read(reinterpret_cast<char*>(&debug), 4))
                 throw std::runtime_error("Incomplete resident request");
-            if (op == 4) w.word_check();
+            if (op == 1 || op == 11 || op == 12) w.prefill(count, debug, op == 12 ? 2u : op == 11 ? 1u : 0u);
+            else if (op == 2) w.generate(count, debug);
+            else if (op == 4) w.word_check();
             else if (op == 6) w.mlp_check(count, debug);
             else if (op == 8) w.resources();
-            else if (op == 14) w.attention_check(count, debug);
-            else throw std::runtime_error("Unknown resident operation");
+            else if (op == 9) w.stream_generate(count, debug);
+            else if (op == 10) w.grow(count);
+            else if (op == 13) w.finish_history();
+            else if (op == 14) {
+                w.diagnostic_dirty = true;   // (resident_attention_runtime.inl:657)
+                w.attention_check(count, debug);
+            } else {
+                throw std::runtime_error("Unknown resident operation");
+            }
         }
         hip_check(hipStreamDestroy(w.stream), "hipStreamDestroy");
         return 0;

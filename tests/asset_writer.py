@@ -133,8 +133,12 @@ def write(dest, spec, packed, floats):
                 rec[field] = vectors.add_floats(np.tile(norm, heads))
             rec[L_HEADS], rec[L_ROTARY] = heads, r
         else:
-            sh = spec["state_heads"]
-            rec[L_CONV] = vectors.add_floats(floats[name("ssm_conv1d.weight")])
+            sh, key = spec["state_heads"], spec["state_key_heads"] * 128
+            # the q and k channels' conv taps repeated over the key repeat, like their rows
+            conv = floats[name("ssm_conv1d.weight")].reshape(-1, 4)
+            rep = sh // spec["state_key_heads"]
+            rec[L_CONV] = vectors.add_floats(np.concatenate((np.tile(conv[:key], (rep, 1)),
+                                                             np.tile(conv[key:2 * key], (rep, 1)), conv[2 * key:])))
             for (w_at, w_code), tensor in ((L_BETA, "ssm_beta.weight"), (L_ALPHA, "ssm_alpha.weight")):
                 rec[w_at], rec[w_code] = place(tensor)
             rec[L_DT_BIAS] = vectors.add_floats(floats[name("ssm_dt.bias")])

@@ -2,6 +2,7 @@
 
 Restates the frame layouts the reference runtime reads
 (ray_tracing/runtime/resident_runtime.py:41-44 hello, 110-114 request/reply,
+116-162 prefill, 91-99 growth, 164-169 finish, 171-233 generation / stream replies,
 235-250 vocabulary, 252-263 mlp, 265-305 attention, 358-379 resources, 386-389 end).
 """
 import struct
@@ -121,3 +122,61 @@ class Worker:
     # op 8
     def resources(self):
         return np.frombuffer(self.request(8, 0), "<u8")
+
+    # op 1 / 11 / 12
+    def prefill(self, ids, stops=(), checkpoint_tokens=None, boundaries=None, debug=0):
+        ids = np.asarray(ids, "<u4")
+        stop = list(stops)[:2] + [0xFFFFFFFF] * 2
+        body = ids.tobytes() + struct.pack("<2I", *stop[:2])
+        op = 1
+        if checkpoint_tokens is not None:
+            body += struct.pack("<I", checkpoint_tokens)
+            op = 11
+        if boundaries is not None:
+            body += struct.pack("<I", len(boundaries)) + b"".join(struct.pack("<2I", p, k) for p, k in boundaries)
+            op = 12
+        pay = self.request(op, len(ids), debug, body)
+        r = dict(times=np.frombuffer(pay, "<f8", count=6), control=np.frombuffer(pay, "<u4", count=8, offset=48))
+        if len(pay) >= 112:
+            r["footer"] = np.frombuffer(pay, "<u8", count=4, offset=80)
+        return r
+
+    @staticmethod
+    def generation(pay, profile=False):
+        """A GenerationPacket reply (resident_runtime.py:190-233)."""
+        r = dict(timing=np.frombuffer(pay, "<f8", count=18), control=np.frombuffer(pay, "<u4", count=8, offset=144))
+        r["ids"] = np.frombuffer(pay, "<u4", count=64, offset=176)[:int(r["control"][1])].copy()
+        r["hits"] = np.frombuffer(pay, "<u4", count=5, offset=432)
+        off = 452
+        r["cache"] = np.frombuffer(pay, "<u4", count=4, offset=off + 32)
+        r["size"] = len(pay)
+        assert len(pay) == off + 112 + (16 if profile else 0), len(pay)
+        return r
+
+    # op 2
+    def generate(self, count, debug=0):
+        return self.generation(self.request(2, count, debug), debug == 2)
+
+    # op 9: one reply per token until the count or a stop
+    def stream(self, count, debug=0):
+        self.p.stdin.write(struct.pack("<3I", 9, count, debug))
+        self.p.stdin.flush()
+        out = []
+        for _ in range(count):
+            status, size = struct.unpack("<2I", self.read(8))
+            pay = self.read(size)
+            if status:
+                raise RuntimeError("Resident stream failed")
+            out.append(self.generation(pay, debug == 2))
+            if not out[-1]["control"][2]:
+                break
+        return out
+
+    # op 10
+    def grow(self, capacity):
+        return np.frombuffer(self.request(10, capacity), "<f8", count=3)
+
+    # op 13
+    def finish(self):
+        pay = self.request(13, 0)
+        return np.frombuffer(pay, "<u8", count=3), np.frombuffer(pay, "<f8", count=1, offset=24)

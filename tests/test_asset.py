@@ -65,6 +65,13 @@ def test_reader_returns_every_tensor(tmp_path):
                     assert (got_fmt, got_mode) == (fmt, mode)
                     np.testing.assert_array_equal(got, raw[r0:r0 + 16].ravel())
                 np.testing.assert_array_equal(a.vector(layer, 37, spec["state_heads"]), floats[p + "ssm_dt.bias"])
+                # conv taps of the q / k channels tiled over the key repeat (export.py:115-116)
+                s_w, rep = spec["state_heads"] * 128, spec["state_heads"] // spec["state_key_heads"]
+                conv = floats[p + "ssm_conv1d.weight"].reshape(-1, 4)
+                got = a.vector(layer, 34, 3 * s_w * 4).reshape(3 * s_w, 4)
+                for c in (0, key - 1, key, s_w - 1, s_w, s_w + key, 2 * s_w, 3 * s_w - 1):
+                    src = c % key if c < s_w else key + (c - s_w) % key if c < 2 * s_w else 2 * key + c - 2 * s_w
+                    np.testing.assert_array_equal(got[c], conv[src])
                 for idx, name in ((ra.BETA, "ssm_beta"), (ra.ALPHA, "ssm_alpha")):
                     fmt, raw = packed[p + name + ".weight"]
                     got_fmt, got_mode, got = a.matrix(layer, idx, raw.nbytes)

@@ -148,7 +148,7 @@ def test_invalid_requests_end_the_worker(tmp_path_factory, served):
     assert w.close() == 1
     w = Worker(EXE, d, CAPACITY, env=dict(os.environ))
     with pytest.raises(RuntimeError, match="Unknown resident operation"):
-        w.request(2, 1, 0)
+        w.request(7, 1, 0)   # aperture update: not served
     assert w.close() == 1
     # non-finite MLP input is refused (verify_rt_mlp.py:103-109; optical_resident.cpp:925)
     for bad in (np.nan, np.inf):
