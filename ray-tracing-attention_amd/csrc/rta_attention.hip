@@ -63,6 +63,7 @@ struct AttnArgs {
     // [nseq][rstride][hq][kRec]; null for the chunk-grid kernels
     int32_t* plan;
     int nwg;
+    int per_cu;         // workgroups resident on one compute unit (nwg = per_cu x compute units)
     int64_t max_tiles;  // tiles per sequence at most: ceil(max_ctx / 64)
     int64_t rstride;    // records per sequence in the workspace
 };
@@ -1347,6 +1348,475 @@ __global__ void __launch_bounds__(256, 2) attn_chunk_mma_kernel(const AttnArgs a
     if (err) raise_error(err);
 }
 
+// ---- matrix-core attention for Q6_K keys and Q4_K values (hkv <= 4) ----------------
+// attn_chunk_mma_kernel's structure (tile-list split, softmax in registers, the same
+// records) for the other field pair, one kv head per wave.  Per tile of 64 positions:
+//   scores   per 16 positions, one v_mfma_f32_16x16x16_f16 per 16-dim Q6_K sub-block s:
+//            A (16 x 16) q of the G heads, rows 2g + part (binary16 hi / lo of q_g 2^e_g,
+//            QOp16), k = dims 16 s + 4 u + (0, 2, 1, 3) in lane segment u;
+//            B (16 x 16) the codes c - 32 as exact binary16 integers, column = position.
+//            sc (c - 32) can exceed binary16's exact integers, so the int8 sub-block
+//            scale multiplies the sub-block's product on the vector ALUs and the 8
+//            sub-blocks are summed there (one fma per output per sub-block).
+//   P V      U^T = V^T P^T, k = 32 positions per instruction:
+//            A (16 x 32) row r, position p: sc c of the Q4_K code (an integer <= 945,
+//                        exact): qs dword r & 7 of chunk 2 hh + jc, nibble r >> 3, byte b,
+//                        so a row's 8 positions share one sub-block 2 jc + (r >> 3);
+//            B (32 x 16) column 2g + part: w_g(p) d(p) 2^S hi / lo as attn_chunk_mma_kernel;
+//            the minimum term sum_p w dmin m 2^S takes one more product per 32
+//            positions (A rows 0..3 = the head's 4 sub-blocks, 6-bit m; B = w dmin 2^S
+//            hi / lo), and the record is U = (D - Dm of the dim's sub-block) 2^-S.  2^S
+//            puts the tile's max(|d|, |dmin|) 2^S in [2^13, 2^14) (kept as in
+//            attn_chunk_mma_kernel while it stays in [2^-4, 2^14)).
+typedef _Float16 h4_t __attribute__((ext_vector_type(4)));
+
+struct QOp16 {
+    h4_t a[8];    // sub-block s of the head
+    float rs[2];  // 1 / 2^e of heads 2u and 2u + 1
+};
+
+template <int G>
+__device__ __forceinline__ QOp16 make_qop16(const float* __restrict__ qg, int lane) {
+    const int row = lane & 15, g = row >> 1, part = row & 1, u = lane >> 4;
+    const bool live = g < G;
+    const float* qh = qg + (live ? g : 0) * kHd;
+    float v[8][4];
+    float mx = 0.0f;
+#pragma unroll
+    for (int s = 0; s < 8; ++s) {
+        const float4 x = *reinterpret_cast<const float4*>(qh + 16 * s + 4 * u);
+        const float t[4] = {x.x, x.z, x.y, x.w};   // the codes' pair order
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            v[s][i] = live ? t[i] : 0.0f;
+            mx = fmaxf(mx, fabsf(v[s][i]));
+        }
+    }
+    mx = fmaxf(mx, __shfl_xor(mx, 16, kWave));
+    mx = fmaxf(mx, __shfl_xor(mx, 32, kWave));
+    const float sg = ldexpf(1.0f, 14 - operand_exponent(mx));
+    QOp16 o;
+#pragma unroll
+    for (int s = 0; s < 8; ++s) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const float x = v[s][i] * sg;
+            const _Float16 hi = (_Float16)x;
+            o.a[s][i] = part ? (_Float16)(x - (float)hi) : hi;
+        }
+    }
+    o.rs[0] = 1.0f / __shfl(sg, 4 * u, kWave);
+    o.rs[1] = 1.0f / __shfl(sg, 4 * u + 2, kWave);
+    return o;
+}
+
+// The tile list in memory, for more sequences than one wave's lanes (one wave).
+__global__ void __launch_bounds__(64) attn_plan_kernel(const AttnArgs a) { attn_plan_wave(a); }
+
+// The tile list of attn_plan_wave for at most 64 sequences, held by a wave: lane s has
+// sequence s's first tile and tile count, T the total.
+struct WavePlan {
+    int first, count;
+    int64_t T;
+};
+
+__device__ __forceinline__ WavePlan wave_plan(const AttnArgs& a, int lane) {
+    int t = 0;
+    if (lane < a.nseq) {
+        const int64_t L = a.ctx_len[lane];
+        const int64_t vis = L < a.capacity ? L : a.capacity;
+        int64_t n = vis > 0 ? (vis + kTile - 1) / kTile : 0;
+        t = (int)(n > a.max_tiles ? a.max_tiles : n);
+    }
+    int x = t;
+    for (int off = 1; off < kWave; off <<= 1) {
+        const int y = __shfl_up(x, off, kWave);
+        if (lane >= off) x += y;
+    }
+    return WavePlan{x - t, t, (int64_t)__shfl(x, kWave - 1, kWave)};
+}
+
+// One lane's share of a Q6_K key (head half hh of the superblock at sb, 2-byte
+// aligned): dims 4u .. 4u + 3 of every 16-dim sub-block.  Element l of the half is
+// quarter l / 32, r = l % 32: ql byte 64 hh + 32 (quarter & 1) + r (high nibble for
+// quarters 2, 3), qh byte 128 + 32 hh + r at bit 2 quarter, scale byte 192 + 8 hh + l / 16
+// (resident_quant.glsl:16-19).  Reads stay inside the block: dwords from the aligned
+// address below, joined with alignbyte.
+struct K6Raw {
+    uint32_t ql[4];   // run k = 2 (quarter & 1) + (s & 1): ql bytes 64 hh + 16 k + 4 u ..
+    uint32_t qh[2];   // qh bytes 128 + 32 hh + 16 (s & 1) + 4 u ..
+    uint32_t sc[2];   // the half's 8 int8 scales
+    float d;
+};
+
+__device__ __forceinline__ void load_key_q6k(const uint8_t* __restrict__ sb, int hh, int u, K6Raw& r) {
+    const uint32_t mis = (uint32_t)(reinterpret_cast<uintptr_t>(sb) & 3u);
+    const uint32_t* A = reinterpret_cast<const uint32_t*>(sb - mis);
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        const int i = 16 * hh + 4 * k + u;
+        r.ql[k] = funnel(A[i], A[i + 1], mis);
+    }
+#pragma unroll
+    for (int k = 0; k < 2; ++k) {
+        const int i = 32 + 8 * hh + 4 * k + u;
+        r.qh[k] = funnel(A[i], A[i + 1], mis);
+    }
+    const uint32_t s0 = A[48 + 2 * hh], s1 = A[49 + 2 * hh], s2 = A[50 + 2 * hh];
+    r.sc[0] = funnel(s0, s1, mis);
+    r.sc[1] = funnel(s1, s2, mis);
+    const uint32_t dw = A[52];   // bytes 208, 209 of the block
+    r.d = mis ? half_hi(dw) : half_lo(dw);
+}
+
+// Scores (times 1 / 2^e, with qo.rs folded in) of the lane's position against heads 2u
+// and 2u + 1 (rows 4u .. 4u + 3 of the output: head 2u hi, lo, head 2u + 1 hi, lo).
+__device__ __forceinline__ void score_q6k_mma16(const QOp16& qo, const K6Raw& r, float out[2]) {
+    f4_t D = f4_t{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int s = 0; s < 8; ++s) {
+        const int quarter = s >> 1, odd = s & 1;
+        const uint32_t lo4 = (r.ql[2 * (quarter & 1) + odd] >> (4 * (quarter >> 1))) & 0x0F0F0F0Fu;
+        const uint32_t c = lo4 | (((r.qh[odd] >> (2 * quarter)) & 0x03030303u) << 4);
+        // c - 32 as binary16: (1024 + c) - 1056, exact
+        const uint32_t p02 = pk_add_f16((c & 0x00FF00FFu) | 0x64006400u, 0xE420E420u);
+        const uint32_t p13 = pk_add_f16(((c >> 8) & 0x00FF00FFu) | 0x64006400u, 0xE420E420u);
+        const f4_t P = __builtin_amdgcn_mfma_f32_16x16x16f16(qo.a[s], __builtin_bit_cast(h4_t, uint2{p02, p13}),
+                                                            f4_t{0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0);
+        const float sc = (float)(int8_t)((r.sc[s >> 2] >> (8 * (s & 3))) & 255u);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) D[e] = fmaf(sc, P[e], D[e]);
+    }
+#pragma unroll
+    for (int eh = 0; eh < 2; ++eh) out[eh] = r.d * (D[2 * eh] + D[2 * eh + 1]) * qo.rs[eh];
+}
+
+constexpr int kVt4Rows = Fmt<RTA_Q4_K>::kBytes / 4;   // 36 dwords of a Q4_K superblock
+struct Mma6WaveLds {                                   // one wave's region, dwords
+    static constexpr int vt = 0;                       // [36][68] V, transposed
+    static constexpr int w = kVt4Rows * kVtStride;     // [8][68] softmax weights
+    static constexpr int f = w + 8 * kVtStride;        // [8] rescale factors
+    static constexpr int q = f + 8;                    // [18][64] the segment's q operands
+    static constexpr int total = q + 18 * kWave;
+};
+static_assert(Mma6WaveLds::w % 4 == 0 && Mma6WaveLds::total % 4 == 0, "16-byte aligned rows");
+constexpr int kMma6LdsBytes = 4 * Mma6WaveLds::total * 4;
+constexpr int kMma6PerCu = 2;   // (registers admit two workgroups per compute unit)
+
+template <int G>
+__global__ void __launch_bounds__(256, 2) attn_chunk_mma6_kernel(const AttnArgs a) {
+    extern __shared__ __align__(16) float lds[];
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int hkv = a.hkv;
+    const int kvh = wave, blk = wave >> 1, hh = wave & 1;
+    if (kvh >= hkv) return;   // no workgroup barrier in this kernel
+    auto uni = [](int v) { return __builtin_amdgcn_readfirstlane(v); };
+    auto uni64 = [](int64_t v) {
+        const uint32_t lo = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)v);
+        const uint32_t hi = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)((uint64_t)v >> 32));
+        return (int64_t)(((uint64_t)hi << 32) | lo);
+    };
+    // the tile-list share and compute-unit pairing of attn_chunk_mma_kernel; the list
+    // is built by every wave for at most 64 sequences (workgroup 0 leaves it in memory
+    // for the merge), else read from memory
+    const int32_t* S = a.plan;
+    const bool in_reg = a.nseq <= kWave;
+    WavePlan wp{0, 0, 0};
+    if (in_reg) wp = wave_plan(a, lane);
+    const int64_t T = in_reg ? wp.T : (int64_t)uni(S[a.nseq]);
+    if (in_reg && blockIdx.x == 0 && wave == 0) {
+        if (lane < a.nseq) a.plan[lane] = wp.first;
+        if (lane == 0) a.plan[a.nseq] = (int32_t)T;
+    }
+    auto seq_first = [&](int q) { return in_reg ? (int64_t)uni(__shfl(wp.first, q, kWave)) : (int64_t)uni(S[q]); };
+    auto seq_end = [&](int q) {
+        return in_reg ? (int64_t)uni(__shfl(wp.first + wp.count, q, kWave)) : (int64_t)uni(S[q + 1]);
+    };
+    const int64_t P = a.nwg < T ? a.nwg : T;
+    // (per_cu workgroups resident on one compute unit take adjacent shares)
+    const int b = blockIdx.x, group = a.nwg / a.per_cu;
+    const int64_t v = (P == a.nwg && a.nwg % a.per_cu == 0) ? a.per_cu * (b % group) + b / group : b;
+    if (v >= P) return;
+    const int64_t ta = v * T / P, tb = (v + 1) * T / P;
+    int s;   // the sequence holding tile ta
+    if (in_reg) {
+        const uint64_t hit = __builtin_amdgcn_ballot_w64(lane < a.nseq && wp.count > 0 && wp.first <= ta &&
+                                                         ta < (int64_t)wp.first + wp.count);
+        s = uni(hit ? (int)__builtin_ctzll(hit) : 0);
+    } else {
+        s = uni(S[a.nseq + 1 + v]);
+    }
+    uint32_t* vt = reinterpret_cast<uint32_t*>(lds) + wave * Mma6WaveLds::total;
+    uint32_t* s_q = vt + Mma6WaveLds::q;
+    float* s_w = lds + wave * Mma6WaveLds::total + Mma6WaveLds::w;
+    float* s_f = lds + wave * Mma6WaveLds::total + Mma6WaveLds::f;
+    const int u = lane >> 4, col = lane & 15;
+    const int nib = col >> 3, gcol = col >> 1;
+    uint32_t err = 0;
+    const float inv2 = 1.4426950408889634f / sqrtf((float)kHd);   // scores in log2 units
+    for (int64_t x = ta; x < tb;) {
+        const int64_t s_first = seq_first(s), s_end = seq_end(s);
+        if (s_end <= x) {
+            ++s;
+            continue;
+        }
+        const int64_t seg_end = s_end < tb ? s_end : tb;
+        const int64_t base = uni64(a.slot_base[s]);
+        const int64_t Lc = uni(a.ctx_len[s]);
+        const int64_t visible = Lc < a.capacity ? Lc : a.capacity;
+        const int64_t n_vis = visible < a.max_tiles * kTile ? visible : a.max_tiles * kTile;
+        const int64_t r0 = (Lc - visible) % a.capacity;
+        {   // the q operands of (s, kvh), kept in the wave's LDS for the segment
+            const QOp16 o = make_qop16<G>(a.q + ((int64_t)s * a.hq + (int64_t)kvh * G) * kHd, lane);
+#pragma unroll
+            for (int k = 0; k < 8; ++k) {
+                const uint2 w2 = __builtin_bit_cast(uint2, o.a[k]);
+                s_q[(2 * k) * kWave + lane] = w2.x;
+                s_q[(2 * k + 1) * kWave + lane] = w2.y;
+            }
+            s_q[16 * kWave + lane] = __builtin_bit_cast(uint32_t, o.rs[0] * inv2);
+            s_q[17 * kWave + lane] = __builtin_bit_cast(uint32_t, o.rs[1] * inv2);
+        }
+        float m_run[2] = {-INFINITY, -INFINITY}, z_run[2] = {0.0f, 0.0f};
+        f4_t D[8], Dm = f4_t{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int t = 0; t < 8; ++t) D[t] = f4_t{0.0f, 0.0f, 0.0f, 0.0f};
+        int S_cur = 0;
+        for (int64_t tile = x - s_first; tile < seg_end - s_first; ++tile) {
+            const bool first_tile = tile == x - s_first;
+            const int n = (int)(n_vis - tile * kTile < kTile ? n_vis - tile * kTile : kTile);
+            const int j = lane;
+            bool ok = j < n;
+            int64_t slot;
+            {
+                const int64_t q = r0 + tile * kTile + min(j, n - 1);
+                slot = base + (q >= a.capacity ? q - a.capacity : q);
+            }
+            if (slot < 0 || slot >= a.n_slots) {
+                if (ok) err |= RTA_DEVERR_HITS;
+                ok = false;
+                slot = 0;
+            }
+            // the V superblock, staged transposed (the lane's max(|d|, |dmin|) for the
+            // tile's 2^S); then the keys of the 4 x 16 positions (lane: position 16 rt +
+            // col, segment u), each row's loads issued while the previous row is scored
+            float dabs;
+            {
+                VStage<RTA_Q4_K> vst;
+                vst.load(a.packets + slot * a.stride + a.v_offset + (int64_t)blk * Fmt<RTA_Q4_K>::kBytes);
+#pragma unroll
+                for (int i = 0; i < kVt4Rows; ++i)
+                    vt[i * kVtStride + j] = funnel(vst.word(i), vst.word(i + 1), vst.mis);
+                const uint32_t w0 = funnel(vst.word(0), vst.word(1), vst.mis);
+                dabs = ok ? fmaxf(fabsf(half_lo(w0)), fabsf(half_hi(w0))) : 0.0f;
+            }
+            bool okr[4];
+            auto load_row = [&](int rt, K6Raw& kr) {
+                const int src = 16 * rt + col;
+                const uint32_t lo = (uint32_t)__shfl((int)(uint32_t)slot, src, kWave);
+                const uint32_t hi = (uint32_t)__shfl((int)(uint32_t)((uint64_t)slot >> 32), src, kWave);
+                okr[rt] = __shfl(ok ? 1 : 0, src, kWave) != 0;
+                const uint8_t* kp = a.packets + (int64_t)(((uint64_t)hi << 32) | lo) * a.stride +
+                                    (int64_t)blk * Fmt<RTA_Q6_K>::kBytes;
+                load_key_q6k(kp, hh, u, kr);
+            };
+            __builtin_amdgcn_sched_barrier(0);
+            K6Raw kcur;
+            load_row(0, kcur);
+            QOp16 qo;
+#pragma unroll
+            for (int k = 0; k < 8; ++k)
+                qo.a[k] = __builtin_bit_cast(h4_t, uint2{s_q[(2 * k) * kWave + lane], s_q[(2 * k + 1) * kWave + lane]});
+            qo.rs[0] = __builtin_bit_cast(float, s_q[16 * kWave + lane]);
+            qo.rs[1] = __builtin_bit_cast(float, s_q[17 * kWave + lane]);
+            float sv[4][2];
+#pragma unroll
+            for (int rt = 0; rt < 4; ++rt) {
+                float sc2[2];
+                K6Raw knext;
+                __builtin_amdgcn_sched_barrier(0);
+                if (rt < 3) load_row(rt + 1, knext);
+                score_q6k_mma16(qo, kcur, sc2);
+                kcur = knext;
+#pragma unroll
+                for (int eh = 0; eh < 2; ++eh) {
+                    const bool live = okr[rt] && 2 * u + eh < G;
+                    if (live && !isfinite(sc2[eh])) err |= RTA_DEVERR_DETECTOR;
+                    sv[rt][eh] = live ? sc2[eh] : -INFINITY;
+                }
+            }
+            const float dmax = wave_max_dpp(dabs);
+            int S_new = S_cur;
+            if (dmax > 0.0f && isfinite(dmax)) {
+                const float scaled = ldexpf(dmax, S_cur);
+                if (first_tile || !(scaled < 16384.0f && scaled >= 0.0625f)) {
+                    int e;
+                    (void)frexpf(dmax, &e);
+                    S_new = 14 - e;
+                }
+            }
+            if (first_tile) S_cur = S_new;
+            // softmax over the tile, folded into (m, Z); weights and rescale factors to LDS
+#pragma unroll
+            for (int eh = 0; eh < 2; ++eh) {
+                const int g = 2 * u + eh;
+                float mx = fmaxf(fmaxf(sv[0][eh], sv[1][eh]), fmaxf(sv[2][eh], sv[3][eh]));
+                mx = row16_max(mx);
+                const float m_new = fmaxf(m_run[eh], mx);
+                float w[4], sf;
+                if (m_new == -INFINITY) {
+                    sf = 1.0f;
+#pragma unroll
+                    for (int rt = 0; rt < 4; ++rt) w[rt] = 0.0f;
+                } else {
+                    sf = __builtin_amdgcn_exp2f(m_run[eh] - m_new);
+#pragma unroll
+                    for (int rt = 0; rt < 4; ++rt) w[rt] = __builtin_amdgcn_exp2f(sv[rt][eh] - m_new);
+                }
+                const float zt = row16_sum((w[0] + w[1]) + (w[2] + w[3]));
+                z_run[eh] = z_run[eh] * sf + zt;
+                m_run[eh] = m_new;
+                if (g < G) {
+#pragma unroll
+                    for (int rt = 0; rt < 4; ++rt) s_w[g * kVtStride + 16 * rt + col] = w[rt];
+                    if (col == 0) s_f[g] = ldexpf(sf, S_new - S_cur);
+                }
+            }
+            __builtin_amdgcn_wave_barrier();
+            {   // rescale D and Dm (column 2g + part: head g); unused columns stay 0
+                const float fl = gcol < G ? s_f[gcol] : 1.0f;
+                if (__builtin_amdgcn_ballot_w64(fl != 1.0f) != 0) {
+#pragma unroll
+                    for (int t = 0; t < 8; ++t) D[t] *= fl;
+                    Dm *= fl;
+                }
+            }
+            S_cur = S_new;
+            // P V, 32 positions per step: this lane's positions 32 ks + 8 u + i
+#pragma unroll 1
+            for (int ks = 0; ks < 2; ++ks) {
+                const int pk0 = 32 * ks + 8 * u;
+                auto rd8 = [&](int row, uint32_t* dst) {
+                    const uint4 x0 = *reinterpret_cast<const uint4*>(vt + row * kVtStride + pk0);
+                    const uint4 x1 = *reinterpret_cast<const uint4*>(vt + row * kVtStride + pk0 + 4);
+                    dst[0] = x0.x; dst[1] = x0.y; dst[2] = x0.z; dst[3] = x0.w;
+                    dst[4] = x1.x; dst[5] = x1.y; dst[6] = x1.z; dst[7] = x1.w;
+                };
+                uint32_t hd8[8], s0[8], s1[8], s2[8];
+                rd8(0, hd8);
+                rd8(1, s0);
+                rd8(2, s1);
+                rd8(3, s2);
+                // B: x = w f 2^S as hi + lo (f = d, or dmin for the minimum term), both
+                // rounded toward zero; column col = head gcol, part col & 1
+                auto build_b = [&](bool use_min) {
+                    const float* wr = s_w + gcol * kVtStride + pk0;
+                    const float4 w0 = *reinterpret_cast<const float4*>(wr);
+                    const float4 w1 = *reinterpret_cast<const float4*>(wr + 4);
+                    const float wv[8] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
+                    const bool part = (col & 1) != 0;
+                    h8_t bop;
+#pragma unroll
+                    for (int i = 0; i < 8; i += 2) {
+                        const float f0 = ldexpf(use_min ? half_hi(hd8[i]) : half_lo(hd8[i]), S_cur);
+                        const float f1 = ldexpf(use_min ? half_hi(hd8[i + 1]) : half_lo(hd8[i + 1]), S_cur);
+                        const float x0 = wv[i] * f0, x1 = wv[i + 1] * f1;
+                        const h2v_t h = __builtin_bit_cast(h2v_t, __builtin_amdgcn_cvt_pkrtz(x0, x1));
+                        const h2v_t l =
+                            __builtin_bit_cast(h2v_t, __builtin_amdgcn_cvt_pkrtz(x0 - (float)h.x, x1 - (float)h.y));
+                        const h2v_t vv = part ? l : h;
+                        bop[i] = vv.x;
+                        bop[i + 1] = vv.y;
+                    }
+                    return bop;
+                };
+                const h8_t bop = build_b(false);
+#pragma unroll
+                for (int jc = 0; jc < 2; ++jc) {
+                    // the row's sub-block 4 hh + 2 jc + nib: sc of the 8 positions as binary16 pairs
+                    const int g8 = 4 * hh + 2 * jc + nib;
+                    uint32_t scp[4];
+#pragma unroll
+                    for (int k = 0; k < 4; ++k) {
+                        uint32_t sa, ma, sb, mb;
+                        q4k_scale_min_lane(s0[2 * k], s1[2 * k], s2[2 * k], g8, sa, ma);
+                        q4k_scale_min_lane(s0[2 * k + 1], s1[2 * k + 1], s2[2 * k + 1], g8, sb, mb);
+                        scp[k] = pk_add_f16((sa | (sb << 16)) | 0x64006400u, 0xE400E400u);   // - 1024
+                    }
+                    uint32_t qw[8];
+                    rd8(4 + 8 * (2 * hh + jc) + (col & 7), qw);
+#pragma unroll
+                    for (int i = 0; i < 8; ++i) qw[i] = (qw[i] >> (4 * nib)) & 0x0F0F0F0Fu;
+#pragma unroll
+                    for (int bb = 0; bb < 4; ++bb) {
+                        const uint32_t sel = (uint32_t)bb | (0x0Cu << 8) | ((4u + bb) << 16) | (0x0Cu << 24);
+                        uint32_t ah[4];
+#pragma unroll
+                        for (int k = 0; k < 4; ++k) {
+                            const uint32_t cp = __builtin_amdgcn_perm(qw[2 * k + 1], qw[2 * k], sel);
+                            ah[k] = pk_mul_f16(pk_add_f16(cp | 0x64006400u, 0xE400E400u), scp[k]);   // sc c
+                        }
+                        const int t = 4 * jc + bb;
+                        D[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
+                            __builtin_bit_cast(h8_t, uint4{ah[0], ah[1], ah[2], ah[3]}), bop, D[t], 0, 0, 0);
+                    }
+                }
+                // the minimum term: A row r < 4 = the head's sub-block 4 hh + r (6-bit m)
+                const h8_t bopm = build_b(true);
+                uint32_t am[4] = {0u, 0u, 0u, 0u};
+                if (col < 4) {
+#pragma unroll
+                    for (int k = 0; k < 4; ++k) {
+                        uint32_t sa, ma, sb, mb;
+                        q4k_scale_min_lane(s0[2 * k], s1[2 * k], s2[2 * k], 4 * hh + col, sa, ma);
+                        q4k_scale_min_lane(s0[2 * k + 1], s1[2 * k + 1], s2[2 * k + 1], 4 * hh + col, sb, mb);
+                        am[k] = pk_add_f16((ma | (mb << 16)) | 0x64006400u, 0xE400E400u);
+                    }
+                }
+                Dm = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(h8_t, uint4{am[0], am[1], am[2], am[3]}),
+                                                            bopm, Dm, 0, 0, 0);
+            }
+            __builtin_amdgcn_wave_barrier();   // the next tile's staging overwrites vt and s_w
+        }
+
+        // records: U_g[dim] = (D - Dm of the dim's sub-block, both parts) 2^-S, then m, Z
+        const int64_t w_lo = ((s_first + 1) * P - 1) / T;
+        float* rec = a.ws + ((int64_t)s * a.rstride + (v - w_lo)) * a.hq * kRec;
+        const float unit = ldexpf(1.0f, -S_cur);
+        const bool writer = (col & 1) == 0 && gcol < G;
+        float* rh = rec + (int64_t)(kvh * G + (gcol < G ? gcol : 0)) * kRec;
+        float dm4[4];   // Dm rows 0..3 (sub-blocks) of this lane's column
+#pragma unroll
+        for (int e = 0; e < 4; ++e) dm4[e] = __shfl(Dm[e], col, kWave);
+#pragma unroll
+        for (int t = 0; t < 8; ++t) {
+            const int jc = t >> 2, bb = t & 3;
+            const int sbk = 2 * jc + (u >> 1);   // sub-block of rows 4u .. 4u + 3
+            const float dm = sbk == 0 ? dm4[0] : sbk == 1 ? dm4[1] : sbk == 2 ? dm4[2] : dm4[3];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                float val = D[t][e] - dm;
+                val += dpp_mov<0xB1>(val);   // + the other part of the head
+                const int rr = 4 * u + e;
+                const int dim = 64 * jc + 32 * (rr >> 3) + 4 * (rr & 7) + bb;
+                if (writer) rh[dim] = val * unit;
+            }
+        }
+#pragma unroll
+        for (int eh = 0; eh < 2; ++eh) {
+            const int g = 2 * u + eh;
+            if (col == 0 && g < G) {
+                rec[(int64_t)(kvh * G + g) * kRec + kHd] = m_run[eh] * 0.6931471805599453f;
+                rec[(int64_t)(kvh * G + g) * kRec + kHd + 1] = z_run[eh];
+            }
+        }
+        x = seg_end;
+        ++s;
+    }
+    if (err) raise_error(err);
+}
+
 // One workgroup per (sequence, query head): 8 chunk groups x 32 lanes of 4
 // coordinates; every thread keeps 8 chunk records in flight.  One pass: each group
 // folds its records into a running (m, Z, U), rescaled when m grows, and the groups
@@ -1526,20 +1996,38 @@ static hipError_t launch_chunk_mma(const AttnArgs& a, hipStream_t s) {
 
 // Workgroups of the matrix-core kernel: two per compute unit (its LDS and registers
 // admit two), all resident at once.
-static int attn_mma_workgroups() {
-    static int n = 0;
-    if (n == 0) {
-        int dev = 0, cus = 0;
+static int attn_mma_workgroups(int per_cu) {
+    static int cus = 0;
+    if (cus == 0) {
+        int dev = 0, n = 0;
         if (hipGetDevice(&dev) != hipSuccess ||
-            hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
-            cus = 256;
-        n = 2 * cus < kMaxWg ? 2 * cus : kMaxWg;
+            hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0)
+            n = 256;
+        cus = n;
     }
-    return n;
+    return per_cu * cus < kMaxWg ? per_cu * cus : kMaxWg;
+}
+
+// Q6_K keys with Q4_K values of at most 4 kv heads: scores and P V on the matrix cores.
+template <int G>
+static hipError_t launch_chunk_mma6(const AttnArgs& a, hipStream_t s) {
+    static bool configured = false;
+    if (!configured) {
+        const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&attn_chunk_mma6_kernel<G>),
+                                                 hipFuncAttributeMaxDynamicSharedMemorySize, kMma6LdsBytes);
+        if (e != hipSuccess) return e;
+        configured = true;
+    }
+    if (a.nseq > kWave) hipLaunchKernelGGL(attn_plan_kernel, dim3(1), dim3(kWave), 0, s, a);
+    hipLaunchKernelGGL((attn_chunk_mma6_kernel<G>), dim3(a.nwg), dim3(256), kMma6LdsBytes, s, a);
+    return hipGetLastError();
 }
 
 template <int KF, int VF, int G>
 static hipError_t launch_chunk_k(const AttnArgs& a, int lds, hipStream_t s) {
+    if constexpr (KF == RTA_Q6_K && VF == RTA_Q4_K) {
+        if (a.hkv <= 4) return launch_chunk_mma6<G>(a, s);
+    }
     if constexpr (KF == RTA_Q4_K) {
         if (a.hkv <= 8) {
             // (one more column of blocks builds the tile list of the matrix-core kernel)
@@ -1692,9 +2180,11 @@ int decode_attention_gate_stride(const float* q, int nseq, int hq, int hkv, int 
     a.nchunk = (int)((max_ctx + a.nt * kTile - 1) / (a.nt * kTile));
     a.nblk = nblk;
     a.max_tiles = ((int64_t)max_ctx + kTile - 1) / kTile;
-    if (fmt_k == RTA_Q4_K && fmt_v == RTA_Q6_K && hkv <= 8) {   // the matrix-core kernel's tile-list split
+    if ((fmt_k == RTA_Q4_K && fmt_v == RTA_Q6_K && hkv <= 8) ||
+        (fmt_k == RTA_Q6_K && fmt_v == RTA_Q4_K && hkv <= 4)) {   // the matrix-core kernels' tile-list split
         a.plan = reinterpret_cast<int32_t*>(reinterpret_cast<uint8_t*>(a.qop) + (size_t)nseq * hkv * 6 * kWave * sizeof(uint4));
-        a.nwg = attn_mma_workgroups();
+        a.per_cu = fmt_k == RTA_Q6_K ? kMma6PerCu : 2;
+        a.nwg = attn_mma_workgroups(a.per_cu);
         a.rstride = a.max_tiles;
     }
     hipStream_t s = (hipStream_t)stream;
