@@ -1491,9 +1491,12 @@ __device__ __forceinline__ void score_q6k_mma16(const QOp16& qo, const K6Raw& r,
     for (int eh = 0; eh < 2; ++eh) out[eh] = r.d * (D[2 * eh] + D[2 * eh + 1]) * qo.rs[eh];
 }
 
-constexpr int kVt4Rows = Fmt<RTA_Q4_K>::kBytes / 4;   // 36 dwords of a Q4_K superblock
+// The V rows a wave stages per position (transposed, [row][position]): row 0 the
+// superblock's d | dmin, rows 1..4 its head half's sub-blocks 4 hh + l as binary16
+// (sc | m << 16), rows 5..20 the half's 16 code dwords (chunks 2 hh, 2 hh + 1).
+constexpr int kVt4Rows = 21;
 struct Mma6WaveLds {                                   // one wave's region, dwords
-    static constexpr int vt = 0;                       // [36][68] V, transposed
+    static constexpr int vt = 0;                       // [21][68] V, transposed
     static constexpr int w = kVt4Rows * kVtStride;     // [8][68] softmax weights
     static constexpr int f = w + 8 * kVtStride;        // [8] rescale factors
     static constexpr int q = f + 8;                    // [18][64] the segment's q operands
@@ -1501,6 +1504,27 @@ struct Mma6WaveLds {                                   // one wave's region, dwo
 };
 static_assert(Mma6WaveLds::w % 4 == 0 && Mma6WaveLds::total % 4 == 0, "16-byte aligned rows");
 constexpr int kMma6LdsBytes = 4 * Mma6WaveLds::total * 4;
+
+// The dwords of a Q4_K value superblock (at blk, 2-byte aligned) one head half needs:
+// the header (d | dmin, 12 scale bytes) and the half's 16 code dwords.  An aligned block
+// rereads an in-block dword instead of the one past it; a misaligned one (the only V
+// superblock of a packet with one kv-head pair, at byte 210) reads its last dword
+// whole, 2 bytes into the packet's padding to 8 bytes.
+struct V4Half {
+    uint32_t raw[22];
+    uint32_t mis;
+    __device__ __forceinline__ void load(const uint8_t* __restrict__ blk, int hh) {
+        mis = (uint32_t)(reinterpret_cast<uintptr_t>(blk) & 3u);
+        const uint32_t* A = reinterpret_cast<const uint32_t*>(blk - mis);
+#pragma unroll
+        for (int i = 0; i < 5; ++i) raw[i] = A[i];
+#pragma unroll
+        for (int i = 0; i < 16; ++i) raw[5 + i] = A[4 + 16 * hh + i];
+        raw[21] = A[mis ? 20 + 16 * hh : 19 + 16 * hh];
+    }
+    __device__ __forceinline__ uint32_t hdr(int i) const { return funnel(raw[i], raw[i + 1], mis); }
+    __device__ __forceinline__ uint32_t code(int i) const { return funnel(raw[5 + i], raw[6 + i], mis); }
+};
 constexpr int kMma6PerCu = 2;   // (registers admit two workgroups per compute unit)
 
 template <int G>
@@ -1583,47 +1607,68 @@ __global__ void __launch_bounds__(256, 2) attn_chunk_mma6_kernel(const AttnArgs 
 #pragma unroll
         for (int t = 0; t < 8; ++t) D[t] = f4_t{0.0f, 0.0f, 0.0f, 0.0f};
         int S_cur = 0;
+        const int j = lane;
+        // slot of the lane's position in a tile; past the tile's end its last position
+        // (its lines are read anyway), out of range slot 0
+        auto slot_of = [&](int64_t tile, bool& okp) {
+            const int n = (int)(n_vis - tile * kTile < kTile ? n_vis - tile * kTile : kTile);
+            okp = j < n;
+            const int64_t q = r0 + tile * kTile + min(j, n - 1);
+            int64_t sl = base + (q >= a.capacity ? q - a.capacity : q);
+            if (sl < 0 || sl >= a.n_slots) {
+                if (okp) err |= RTA_DEVERR_HITS;
+                okp = false;
+                sl = 0;
+            }
+            return sl;
+        };
+        auto v_block = [&](int64_t sl) {
+            return a.packets + sl * a.stride + a.v_offset + (int64_t)blk * Fmt<RTA_Q4_K>::kBytes;
+        };
+        // keys of row rt of a tile (lane: position 16 rt + col, segment u) and whether
+        // that position is valid
+        auto load_row = [&](int rt, int64_t sl, bool okp, K6Raw& kr) {
+            const int src = 16 * rt + col;
+            const uint32_t lo = (uint32_t)__shfl((int)(uint32_t)sl, src, kWave);
+            const uint32_t hi = (uint32_t)__shfl((int)(uint32_t)((uint64_t)sl >> 32), src, kWave);
+            const uint8_t* kp = a.packets + (int64_t)(((uint64_t)hi << 32) | lo) * a.stride +
+                                (int64_t)blk * Fmt<RTA_Q6_K>::kBytes;
+            load_key_q6k(kp, hh, u, kr);
+            return __shfl(okp ? 1 : 0, src, kWave) != 0;
+        };
+        // the V superblock and first key row of a tile are loaded while the tile before
+        // it is multiplied
+        bool ok_next;
+        int64_t slot_next = slot_of(x - s_first, ok_next);
+        V4Half vst;
+        vst.load(v_block(slot_next), hh);
+        K6Raw k_first;
+        bool ok_first = load_row(0, slot_next, ok_next, k_first);
         for (int64_t tile = x - s_first; tile < seg_end - s_first; ++tile) {
             const bool first_tile = tile == x - s_first;
-            const int n = (int)(n_vis - tile * kTile < kTile ? n_vis - tile * kTile : kTile);
-            const int j = lane;
-            bool ok = j < n;
-            int64_t slot;
-            {
-                const int64_t q = r0 + tile * kTile + min(j, n - 1);
-                slot = base + (q >= a.capacity ? q - a.capacity : q);
-            }
-            if (slot < 0 || slot >= a.n_slots) {
-                if (ok) err |= RTA_DEVERR_HITS;
-                ok = false;
-                slot = 0;
-            }
+            const bool ok = ok_next;
+            const int64_t slot = slot_next;
             // the V superblock, staged transposed (the lane's max(|d|, |dmin|) for the
             // tile's 2^S); then the keys of the 4 x 16 positions (lane: position 16 rt +
             // col, segment u), each row's loads issued while the previous row is scored
             float dabs;
             {
-                VStage<RTA_Q4_K> vst;
-                vst.load(a.packets + slot * a.stride + a.v_offset + (int64_t)blk * Fmt<RTA_Q4_K>::kBytes);
+                const uint32_t w0 = vst.hdr(0), h1 = vst.hdr(1), h2 = vst.hdr(2), h3 = vst.hdr(3);
+                vt[j] = w0;
 #pragma unroll
-                for (int i = 0; i < kVt4Rows; ++i)
-                    vt[i * kVtStride + j] = funnel(vst.word(i), vst.word(i + 1), vst.mis);
-                const uint32_t w0 = funnel(vst.word(0), vst.word(1), vst.mis);
+                for (int l = 0; l < 4; ++l) {   // (uniform sub-block: no lane select)
+                    uint32_t sc, m;
+                    q4k_scale_min(h1, h2, h3, 4 * hh + l, sc, m);
+                    vt[(1 + l) * kVtStride + j] = pk_add_f16((sc | (m << 16)) | 0x64006400u, 0xE400E400u);
+                }
+#pragma unroll
+                for (int c = 0; c < 16; ++c) vt[(5 + c) * kVtStride + j] = vst.code(c);
                 dabs = ok ? fmaxf(fabsf(half_lo(w0)), fabsf(half_hi(w0))) : 0.0f;
             }
             bool okr[4];
-            auto load_row = [&](int rt, K6Raw& kr) {
-                const int src = 16 * rt + col;
-                const uint32_t lo = (uint32_t)__shfl((int)(uint32_t)slot, src, kWave);
-                const uint32_t hi = (uint32_t)__shfl((int)(uint32_t)((uint64_t)slot >> 32), src, kWave);
-                okr[rt] = __shfl(ok ? 1 : 0, src, kWave) != 0;
-                const uint8_t* kp = a.packets + (int64_t)(((uint64_t)hi << 32) | lo) * a.stride +
-                                    (int64_t)blk * Fmt<RTA_Q6_K>::kBytes;
-                load_key_q6k(kp, hh, u, kr);
-            };
             __builtin_amdgcn_sched_barrier(0);
-            K6Raw kcur;
-            load_row(0, kcur);
+            K6Raw kcur = k_first;
+            okr[0] = ok_first;
             QOp16 qo;
 #pragma unroll
             for (int k = 0; k < 8; ++k)
@@ -1636,7 +1681,7 @@ __global__ void __launch_bounds__(256, 2) attn_chunk_mma6_kernel(const AttnArgs 
                 float sc2[2];
                 K6Raw knext;
                 __builtin_amdgcn_sched_barrier(0);
-                if (rt < 3) load_row(rt + 1, knext);
+                if (rt < 3) okr[rt + 1] = load_row(rt + 1, slot, ok, knext);
                 score_q6k_mma16(qo, kcur, sc2);
                 kcur = knext;
 #pragma unroll
@@ -1693,6 +1738,11 @@ __global__ void __launch_bounds__(256, 2) attn_chunk_mma6_kernel(const AttnArgs 
                 }
             }
             S_cur = S_new;
+            if (tile + 1 < seg_end - s_first) {   // the next tile's V and first key row, during P V
+                slot_next = slot_of(tile + 1, ok_next);
+                vst.load(v_block(slot_next), hh);
+                ok_first = load_row(0, slot_next, ok_next, k_first);
+            }
             // P V, 32 positions per step: this lane's positions 32 ks + 8 u + i
 #pragma unroll 1
             for (int ks = 0; ks < 2; ++ks) {
@@ -1703,11 +1753,8 @@ __global__ void __launch_bounds__(256, 2) attn_chunk_mma6_kernel(const AttnArgs 
                     dst[0] = x0.x; dst[1] = x0.y; dst[2] = x0.z; dst[3] = x0.w;
                     dst[4] = x1.x; dst[5] = x1.y; dst[6] = x1.z; dst[7] = x1.w;
                 };
-                uint32_t hd8[8], s0[8], s1[8], s2[8];
+                uint32_t hd8[8];
                 rd8(0, hd8);
-                rd8(1, s0);
-                rd8(2, s1);
-                rd8(3, s2);
                 // B: x = w f 2^S as hi + lo (f = d, or dmin for the minimum term), both
                 // rounded toward zero; column col = head gcol, part col & 1
                 auto build_b = [&](bool use_min) {
@@ -1734,18 +1781,14 @@ __global__ void __launch_bounds__(256, 2) attn_chunk_mma6_kernel(const AttnArgs 
                 const h8_t bop = build_b(false);
 #pragma unroll
                 for (int jc = 0; jc < 2; ++jc) {
-                    // the row's sub-block 4 hh + 2 jc + nib: sc of the 8 positions as binary16 pairs
-                    const int g8 = 4 * hh + 2 * jc + nib;
-                    uint32_t scp[4];
+                    // the row's sub-block 2 jc + nib of the half: sc of the 8 positions as
+                    // binary16 pairs (the low halves of its staged row)
+                    uint32_t scw[8], scp[4];
+                    rd8(1 + 2 * jc + nib, scw);
 #pragma unroll
-                    for (int k = 0; k < 4; ++k) {
-                        uint32_t sa, ma, sb, mb;
-                        q4k_scale_min_lane(s0[2 * k], s1[2 * k], s2[2 * k], g8, sa, ma);
-                        q4k_scale_min_lane(s0[2 * k + 1], s1[2 * k + 1], s2[2 * k + 1], g8, sb, mb);
-                        scp[k] = pk_add_f16((sa | (sb << 16)) | 0x64006400u, 0xE400E400u);   // - 1024
-                    }
+                    for (int k = 0; k < 4; ++k) scp[k] = __builtin_amdgcn_perm(scw[2 * k + 1], scw[2 * k], 0x05040100u);
                     uint32_t qw[8];
-                    rd8(4 + 8 * (2 * hh + jc) + (col & 7), qw);
+                    rd8(5 + 8 * jc + (col & 7), qw);
 #pragma unroll
                     for (int i = 0; i < 8; ++i) qw[i] = (qw[i] >> (4 * nib)) & 0x0F0F0F0Fu;
 #pragma unroll
@@ -1764,15 +1807,13 @@ __global__ void __launch_bounds__(256, 2) attn_chunk_mma6_kernel(const AttnArgs 
                 }
                 // the minimum term: A row r < 4 = the head's sub-block 4 hh + r (6-bit m)
                 const h8_t bopm = build_b(true);
-                uint32_t am[4] = {0u, 0u, 0u, 0u};
-                if (col < 4) {
+                uint32_t am[4];
+                {
+                    uint32_t mw[8];
+                    rd8(1 + (col & 3), mw);   // (rows of lanes col >= 4 are zeroed)
 #pragma unroll
-                    for (int k = 0; k < 4; ++k) {
-                        uint32_t sa, ma, sb, mb;
-                        q4k_scale_min_lane(s0[2 * k], s1[2 * k], s2[2 * k], 4 * hh + col, sa, ma);
-                        q4k_scale_min_lane(s0[2 * k + 1], s1[2 * k + 1], s2[2 * k + 1], 4 * hh + col, sb, mb);
-                        am[k] = pk_add_f16((ma | (mb << 16)) | 0x64006400u, 0xE400E400u);
-                    }
+                    for (int k = 0; k < 4; ++k)
+                        am[k] = col < 4 ? __builtin_amdgcn_perm(mw[2 * k + 1], mw[2 * k], 0x07060302u) : 0u;
                 }
                 Dm = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(h8_t, uint4{am[0], am[1], am[2], am[3]}),
                                                             bopm, Dm, 0, 0, 0);
