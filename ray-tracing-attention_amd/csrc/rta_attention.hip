@@ -1351,13 +1351,12 @@ __global__ void __launch_bounds__(256, 2) attn_chunk_mma_kernel(const AttnArgs a
 // ---- matrix-core attention for Q6_K keys and Q4_K values (hkv <= 4) ----------------
 // attn_chunk_mma_kernel's structure (tile-list split, softmax in registers, the same
 // records) for the other field pair, one kv head per wave.  Per tile of 64 positions:
-//   scores   per 16 positions, one v_mfma_f32_16x16x16_f16 per 16-dim Q6_K sub-block s:
-//            A (16 x 16) q of the G heads, rows 2g + part (binary16 hi / lo of q_g 2^e_g,
-//            QOp16), k = dims 16 s + 4 u + (0, 2, 1, 3) in lane segment u;
-//            B (16 x 16) the codes c - 32 as exact binary16 integers, column = position.
-//            sc (c - 32) can exceed binary16's exact integers, so the int8 sub-block
-//            scale multiplies the sub-block's product on the vector ALUs and the 8
-//            sub-blocks are summed there (one fma per output per sub-block).
+//   scores   per 16 positions and k block of 32 dims (a quarter of the Q6_K head half):
+//            A (16 x 32) q of the G heads as in score_q4k_mma (QOp, rows 2g + part hi /
+//            lo), B (32 x 16) e = (c - 32) sc, column = position, lane segment u = dims
+//            8u .. 8u + 7 of the quarter (one 16-dim sub-block, one scale); |e| <= 4096
+//            is not always a binary16 integer, so B is its rounding hi plus the exact
+//            remainder lo, one product each (score_q6k_mma).
 //   P V      U^T = V^T P^T, k = 32 positions per instruction:
 //            A (16 x 32) row r, position p: sc c of the Q4_K code (an integer <= 945,
 //                        exact): qs dword r & 7 of chunk 2 hh + jc, nibble r >> 3, byte b,
@@ -1368,48 +1367,6 @@ __global__ void __launch_bounds__(256, 2) attn_chunk_mma_kernel(const AttnArgs a
 //            hi / lo), and the record is U = (D - Dm of the dim's sub-block) 2^-S.  2^S
 //            puts the tile's max(|d|, |dmin|) 2^S in [2^13, 2^14) (kept as in
 //            attn_chunk_mma_kernel while it stays in [2^-4, 2^14)).
-typedef _Float16 h4_t __attribute__((ext_vector_type(4)));
-
-struct QOp16 {
-    h4_t a[8];    // sub-block s of the head
-    float rs[2];  // 1 / 2^e of heads 2u and 2u + 1
-};
-
-template <int G>
-__device__ __forceinline__ QOp16 make_qop16(const float* __restrict__ qg, int lane) {
-    const int row = lane & 15, g = row >> 1, part = row & 1, u = lane >> 4;
-    const bool live = g < G;
-    const float* qh = qg + (live ? g : 0) * kHd;
-    float v[8][4];
-    float mx = 0.0f;
-#pragma unroll
-    for (int s = 0; s < 8; ++s) {
-        const float4 x = *reinterpret_cast<const float4*>(qh + 16 * s + 4 * u);
-        const float t[4] = {x.x, x.z, x.y, x.w};   // the codes' pair order
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            v[s][i] = live ? t[i] : 0.0f;
-            mx = fmaxf(mx, fabsf(v[s][i]));
-        }
-    }
-    mx = fmaxf(mx, __shfl_xor(mx, 16, kWave));
-    mx = fmaxf(mx, __shfl_xor(mx, 32, kWave));
-    const float sg = ldexpf(1.0f, 14 - operand_exponent(mx));
-    QOp16 o;
-#pragma unroll
-    for (int s = 0; s < 8; ++s) {
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const float x = v[s][i] * sg;
-            const _Float16 hi = (_Float16)x;
-            o.a[s][i] = part ? (_Float16)(x - (float)hi) : hi;
-        }
-    }
-    o.rs[0] = 1.0f / __shfl(sg, 4 * u, kWave);
-    o.rs[1] = 1.0f / __shfl(sg, 4 * u + 2, kWave);
-    return o;
-}
-
 // The tile list in memory, for more sequences than one wave's lanes (one wave).
 __global__ void __launch_bounds__(64) attn_plan_kernel(const AttnArgs a) { attn_plan_wave(a); }
 
@@ -1437,15 +1394,17 @@ __device__ __forceinline__ WavePlan wave_plan(const AttnArgs& a, int lane) {
 }
 
 // One lane's share of a Q6_K key (head half hh of the superblock at sb, 2-byte
-// aligned): dims 4u .. 4u + 3 of every 16-dim sub-block.  Element l of the half is
-// quarter l / 32, r = l % 32: ql byte 64 hh + 32 (quarter & 1) + r (high nibble for
-// quarters 2, 3), qh byte 128 + 32 hh + r at bit 2 quarter, scale byte 192 + 8 hh + l / 16
-// (resident_quant.glsl:16-19).  Reads stay inside the block: dwords from the aligned
+// aligned) for the products of k block kb = quarter kb of the half: elements r =
+// 8u + i of each quarter (lane segment u).  Element l of the half is quarter l / 32,
+// r = l % 32: ql byte 64 hh + 32 (quarter & 1) + r (high nibble for quarters 2, 3), qh
+// byte 128 + 32 hh + r at bit 2 quarter, scale byte 192 + 8 hh + l / 16
+// (resident_quant.glsl:16-19); the lane's 8 elements of a quarter share the scale of
+// sub-block 2 kb + (u >> 1).  Reads stay inside the block: dwords from the aligned
 // address below, joined with alignbyte.
 struct K6Raw {
-    uint32_t ql[4];   // run k = 2 (quarter & 1) + (s & 1): ql bytes 64 hh + 16 k + 4 u ..
-    uint32_t qh[2];   // qh bytes 128 + 32 hh + 16 (s & 1) + 4 u ..
-    uint32_t sc[2];   // the half's 8 int8 scales
+    uint32_t ql[4];   // ql bytes 64 hh + 8u .. + 7 (quarters 0, 2), 64 hh + 32 + 8u .. (1, 3)
+    uint32_t qh[2];   // qh bytes 128 + 32 hh + 8u .. + 7
+    uint32_t sc;      // byte kb: the int8 scale of sub-block 2 kb + (u >> 1)
     float d;
 };
 
@@ -1453,39 +1412,55 @@ __device__ __forceinline__ void load_key_q6k(const uint8_t* __restrict__ sb, int
     const uint32_t mis = (uint32_t)(reinterpret_cast<uintptr_t>(sb) & 3u);
     const uint32_t* A = reinterpret_cast<const uint32_t*>(sb - mis);
 #pragma unroll
-    for (int k = 0; k < 4; ++k) {
-        const int i = 16 * hh + 4 * k + u;
-        r.ql[k] = funnel(A[i], A[i + 1], mis);
-    }
-#pragma unroll
     for (int k = 0; k < 2; ++k) {
-        const int i = 32 + 8 * hh + 4 * k + u;
-        r.qh[k] = funnel(A[i], A[i + 1], mis);
+        const int i = 16 * hh + 8 * k + 2 * u;
+        const uint32_t a0 = A[i], a1 = A[i + 1], a2 = A[i + 2];
+        r.ql[2 * k] = funnel(a0, a1, mis);
+        r.ql[2 * k + 1] = funnel(a1, a2, mis);
+    }
+    {
+        const int i = 32 + 8 * hh + 2 * u;
+        const uint32_t a0 = A[i], a1 = A[i + 1], a2 = A[i + 2];
+        r.qh[0] = funnel(a0, a1, mis);
+        r.qh[1] = funnel(a1, a2, mis);
     }
     const uint32_t s0 = A[48 + 2 * hh], s1 = A[49 + 2 * hh], s2 = A[50 + 2 * hh];
-    r.sc[0] = funnel(s0, s1, mis);
-    r.sc[1] = funnel(s1, s2, mis);
+    const uint32_t h = (uint32_t)(u >> 1);
+    r.sc = __builtin_amdgcn_perm(funnel(s1, s2, mis), funnel(s0, s1, mis),
+                                 h | ((2u + h) << 8) | ((4u + h) << 16) | ((6u + h) << 24));
     const uint32_t dw = A[52];   // bytes 208, 209 of the block
     r.d = mis ? half_hi(dw) : half_lo(dw);
 }
 
 // Scores (times 1 / 2^e, with qo.rs folded in) of the lane's position against heads 2u
 // and 2u + 1 (rows 4u .. 4u + 3 of the output: head 2u hi, lo, head 2u + 1 hi, lo).
-__device__ __forceinline__ void score_q6k_mma16(const QOp16& qo, const K6Raw& r, float out[2]) {
+// B = (c - 32) sc, an integer of up to 4096 in magnitude, as binary16 hi (rounded) plus
+// lo (the exact remainder, one fma), one product each.
+__device__ __forceinline__ void score_q6k_mma(const QOp& qo, const K6Raw& r, float out[2]) {
     f4_t D = f4_t{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-    for (int s = 0; s < 8; ++s) {
-        const int quarter = s >> 1, odd = s & 1;
-        const uint32_t lo4 = (r.ql[2 * (quarter & 1) + odd] >> (4 * (quarter >> 1))) & 0x0F0F0F0Fu;
-        const uint32_t c = lo4 | (((r.qh[odd] >> (2 * quarter)) & 0x03030303u) << 4);
-        // c - 32 as binary16: (1024 + c) - 1056, exact
-        const uint32_t p02 = pk_add_f16((c & 0x00FF00FFu) | 0x64006400u, 0xE420E420u);
-        const uint32_t p13 = pk_add_f16(((c >> 8) & 0x00FF00FFu) | 0x64006400u, 0xE420E420u);
-        const f4_t P = __builtin_amdgcn_mfma_f32_16x16x16f16(qo.a[s], __builtin_bit_cast(h4_t, uint2{p02, p13}),
-                                                            f4_t{0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0);
-        const float sc = (float)(int8_t)((r.sc[s >> 2] >> (8 * (s & 3))) & 255u);
+    for (int kb = 0; kb < 4; ++kb) {
+        const uint32_t nsh = 4u * (uint32_t)(kb >> 1), hsh = 2u * (uint32_t)kb;
+        uint32_t p[4];
 #pragma unroll
-        for (int e = 0; e < 4; ++e) D[e] = fmaf(sc, P[e], D[e]);
+        for (int w = 0; w < 2; ++w) {
+            const uint32_t c = ((r.ql[2 * (kb & 1) + w] >> nsh) & 0x0F0F0F0Fu) |
+                               (((r.qh[w] >> hsh) & 0x03030303u) << 4);
+            // c - 32 as binary16: (1024 + c) - 1056, exact; pairs of elements (0, 2), (1, 3)
+            p[2 * w] = pk_add_f16((c & 0x00FF00FFu) | 0x64006400u, 0xE420E420u);
+            p[2 * w + 1] = pk_add_f16(((c >> 8) & 0x00FF00FFu) | 0x64006400u, 0xE420E420u);
+        }
+        const uint32_t sp = h2dup((float)(int8_t)((r.sc >> (8 * kb)) & 255u));
+        uint32_t bh[4], bl[4];
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            bh[k] = pk_mul_f16(p[k], sp);
+            bl[k] = pk_fms_f16(p[k], sp, bh[k]);   // remainder, exact
+        }
+        D = __builtin_amdgcn_mfma_f32_16x16x32_f16(qo.a[kb], __builtin_bit_cast(h8_t, uint4{bh[0], bh[1], bh[2], bh[3]}),
+                                                   D, 0, 0, 0);
+        D = __builtin_amdgcn_mfma_f32_16x16x32_f16(qo.a[kb], __builtin_bit_cast(h8_t, uint4{bl[0], bl[1], bl[2], bl[3]}),
+                                                   D, 0, 0, 0);
     }
 #pragma unroll
     for (int eh = 0; eh < 2; ++eh) out[eh] = r.d * (D[2 * eh] + D[2 * eh + 1]) * qo.rs[eh];
@@ -1592,12 +1567,14 @@ __global__ void __launch_bounds__(256, 2) attn_chunk_mma6_kernel(const AttnArgs 
         const int64_t n_vis = visible < a.max_tiles * kTile ? visible : a.max_tiles * kTile;
         const int64_t r0 = (Lc - visible) % a.capacity;
         {   // the q operands of (s, kvh), kept in the wave's LDS for the segment
-            const QOp16 o = make_qop16<G>(a.q + ((int64_t)s * a.hq + (int64_t)kvh * G) * kHd, lane);
+            const QOp o = make_qop<G>(a.q + ((int64_t)s * a.hq + (int64_t)kvh * G) * kHd, lane);
 #pragma unroll
-            for (int k = 0; k < 8; ++k) {
-                const uint2 w2 = __builtin_bit_cast(uint2, o.a[k]);
-                s_q[(2 * k) * kWave + lane] = w2.x;
-                s_q[(2 * k + 1) * kWave + lane] = w2.y;
+            for (int k = 0; k < 4; ++k) {
+                const uint4 w4 = __builtin_bit_cast(uint4, o.a[k]);
+                s_q[(4 * k) * kWave + lane] = w4.x;
+                s_q[(4 * k + 1) * kWave + lane] = w4.y;
+                s_q[(4 * k + 2) * kWave + lane] = w4.z;
+                s_q[(4 * k + 3) * kWave + lane] = w4.w;
             }
             s_q[16 * kWave + lane] = __builtin_bit_cast(uint32_t, o.rs[0] * inv2);
             s_q[17 * kWave + lane] = __builtin_bit_cast(uint32_t, o.rs[1] * inv2);
@@ -1669,10 +1646,11 @@ __global__ void __launch_bounds__(256, 2) attn_chunk_mma6_kernel(const AttnArgs 
             __builtin_amdgcn_sched_barrier(0);
             K6Raw kcur = k_first;
             okr[0] = ok_first;
-            QOp16 qo;
+            QOp qo;
 #pragma unroll
-            for (int k = 0; k < 8; ++k)
-                qo.a[k] = __builtin_bit_cast(h4_t, uint2{s_q[(2 * k) * kWave + lane], s_q[(2 * k + 1) * kWave + lane]});
+            for (int k = 0; k < 4; ++k)
+                qo.a[k] = __builtin_bit_cast(h8_t, uint4{s_q[(4 * k) * kWave + lane], s_q[(4 * k + 1) * kWave + lane],
+                                                         s_q[(4 * k + 2) * kWave + lane], s_q[(4 * k + 3) * kWave + lane]});
             qo.rs[0] = __builtin_bit_cast(float, s_q[16 * kWave + lane]);
             qo.rs[1] = __builtin_bit_cast(float, s_q[17 * kWave + lane]);
             float sv[4][2];
@@ -1682,7 +1660,7 @@ __global__ void __launch_bounds__(256, 2) attn_chunk_mma6_kernel(const AttnArgs 
                 K6Raw knext;
                 __builtin_amdgcn_sched_barrier(0);
                 if (rt < 3) okr[rt + 1] = load_row(rt + 1, slot, ok, knext);
-                score_q6k_mma16(qo, kcur, sc2);
+                score_q6k_mma(qo, kcur, sc2);
                 kcur = knext;
 #pragma unroll
                 for (int eh = 0; eh < 2; ++eh) {
