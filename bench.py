@@ -365,7 +365,7 @@ def w_attention(torch, args, orc):
         attn(i)
 
     alg = total * (2 * 354) + 2 * nseq * hq * hd * 4
-    res = {"alg_bytes": alg, "kernel": "attn_chunk_kernel<Q6_K,Q4_K,G=4> + attn_merge_kernel", "step": step,
+    res = {"alg_bytes": alg, "kernel": "attn_chunk_mma6_kernel<G=4> (Q6_K keys, Q4_K values, matrix cores) + attn_merge_kernel", "step": step,
            "kernel_launch": attn, "unit": "GB/s", "value_from_ms": lambda ms: alg / (ms * 1e-3) / 1e9,
            "dtype": "q6_k keys / q4_k values x fp32 queries, fp32 softmax",
            "config": {"workload": "GQA decode attention, 16 seq, ctx log-uniform [512,32768], 16q/4kv heads, "
