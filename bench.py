@@ -55,7 +55,7 @@ def parse():
     ap.add_argument("--cols", type=int, default=4096, help="proj workload: input columns")
     ap.add_argument("--fmt", default="q4k", choices=["q4k", "q6k"], help="proj workload: weight format")
     ap.add_argument("--packed", action="store_true",
-                    help="proj / mlp / lm_head: weights packed once by rta_pack (tiled layout, matrix cores)")
+                    help="proj / mlp / lm_head / decode: weights packed once by rta_pack (tiled layout, matrix cores)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--eager", action="store_true", help="time eager launches instead of a graph replay")
@@ -509,8 +509,9 @@ def w_decode(torch, args, orc):
     ctx = rng.integers(256, 8193, batch).astype(np.int32)
     capacity = 8192 + 256
     # the weight layout each batch runs fastest on (measured): packed tiles on the matrix
-    # cores from 8 rows up, GGUF rows on the batch-1 vector-ALU readouts below
-    packed = batch >= 8
+    # cores from 8 rows up, GGUF rows on the batch-1 vector-ALU readouts below (--packed:
+    # packed tiles at any batch, for the comparison)
+    packed = batch >= 8 or args.packed
     shape = model.shape_9b(capacity, packed=packed)
     want_cpu = not args.no_cpu and batch == 32
     m = model.DecodeModel(shape, batch, ctx, seed=20261115, keep_gguf=want_cpu)

@@ -33,10 +33,23 @@ __global__ void __launch_bounds__(256) dequant_kernel(int fmt, const uint8_t* __
 // reference's reduction (resident_math.comp:124-130: strict >, ties -> lower id).
 constexpr int kArgmaxThreads = 1024;   // one block per batch row scans the task maxima
 
+// Maxima of groups of 64 task maxima (wave g of the grid: group g of batch row
+// blockIdx.y), so that the argmax over many small tasks scans 64 times fewer values.
+__global__ void __launch_bounds__(256) group_max_kernel(const float* __restrict__ partial, int ntasks, int ngroups,
+                                                        float* __restrict__ gmax) {
+    const int g = blockIdx.x * 4 + (threadIdx.x >> 6), b = blockIdx.y, lane = threadIdx.x & 63;
+    if (g >= ngroups) return;   // uniform per wave
+    const int t = g * kWave + lane;
+    float m = t < ntasks ? partial[(int64_t)b * ntasks + t] : -INFINITY;
+    m = group_max(m, kWave);
+    if (lane == 0) gmax[(int64_t)b * ngroups + g] = m;
+}
+
 __global__ void __launch_bounds__(kArgmaxThreads) argmax_margin_kernel(const float* __restrict__ logits, int vocab,
                                                             const float* __restrict__ partial, int ntasks,
                                                             int rows_per_task, float margin,
-                                                            uint32_t* __restrict__ ids) {
+                                                            uint32_t* __restrict__ ids,
+                                                            const float* __restrict__ gmax, int ngroups) {
 #pragma clang fp contract(off)
     constexpr int kW = kArgmaxThreads / 64;
     __shared__ float red_f[kW];
@@ -44,10 +57,14 @@ __global__ void __launch_bounds__(kArgmaxThreads) argmax_margin_kernel(const flo
     const int b = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const float* pb = partial + (int64_t)b * ntasks;
     const float* lb = logits + (int64_t)b * vocab;
-    // 1. M = max over the task maxima
+    // with group maxima (gmax), steps 1 and 2 run over the groups and step 2 then picks
+    // the first task of the first group reaching T: the same task
+    const float* gb = gmax ? gmax + (int64_t)b * ngroups : pb;
+    const int nscan = gmax ? ngroups : ntasks;
+    // 1. M = max over the task (group) maxima
     float m = -INFINITY;
 #pragma unroll 8
-    for (int t = tid; t < ntasks; t += kArgmaxThreads) m = fmaxf(m, pb[t]);
+    for (int t = tid; t < nscan; t += kArgmaxThreads) m = fmaxf(m, gb[t]);
     m = group_max(m, kWave);
     if (lane == 0) red_f[wave] = m;
     __syncthreads();
@@ -64,7 +81,7 @@ __global__ void __launch_bounds__(kArgmaxThreads) argmax_margin_kernel(const flo
     // 2. the first task whose maximum reaches T holds the lowest index with logit >= T
     int first = INT_MAX;   // branch-free so that the loads of a thread overlap
 #pragma unroll 8
-    for (int t = tid; t < ntasks; t += kArgmaxThreads) first = (pb[t] >= T && t < first) ? t : first;
+    for (int t = tid; t < nscan; t += kArgmaxThreads) first = (gb[t] >= T && t < first) ? t : first;
     for (int off = 32; off > 0; off >>= 1) first = min(first, __shfl_xor(first, off, kWave));
     if (lane == 0) red_i[wave] = first;
     __syncthreads();
@@ -75,6 +92,12 @@ __global__ void __launch_bounds__(kArgmaxThreads) argmax_margin_kernel(const flo
     if (first == INT_MAX) {   // only with NaN logits
         if (tid == 0) ids[b] = 0xffffffffu;
         return;
+    }
+    if (gmax) {   // the first task of group `first` reaching T (the group's maximum does)
+        const int t = first * kWave + lane;
+        const bool hit = t < ntasks && pb[t] >= T;
+        const uint64_t mask = __builtin_amdgcn_ballot_w64(hit);
+        first = first * kWave + (mask ? (int)__builtin_ctzll(mask) : 0);
     }
     // 3. lowest row of that task with logit >= T
     const int r0 = first * rows_per_task, r1 = min(r0 + rows_per_task, vocab);
@@ -910,8 +933,17 @@ int lm_head_rownorm(int fmt, const void* w, int vocab, int hidden, const float* 
                                      logits + (int64_t)b0 * vocab, partial + (int64_t)b0 * vocab, &ntasks, &rpt,
                                      scratch, mma, s, batch, rc_rn, xn);
         if (rc) return rc;
+        // many small tasks: their group maxima go into the maxima region after the tasks'
+        // (the chunk's [chunk][ntasks] task maxima leave chunk x (vocab - ntasks) floats)
+        const int ngroups = (ntasks + kWave - 1) / kWave;
+        float* gm = nullptr;
+        if (ntasks > 4 * kArgmaxThreads && (int64_t)chunk * (ntasks + ngroups) <= (int64_t)chunk * vocab) {
+            gm = partial + (int64_t)b0 * vocab + (int64_t)chunk * ntasks;
+            hipLaunchKernelGGL(group_max_kernel, dim3((ngroups + 3) / 4, chunk), dim3(256), 0, s,
+                               partial + (int64_t)b0 * vocab, ntasks, ngroups, gm);
+        }
         hipLaunchKernelGGL(argmax_margin_kernel, dim3(chunk), dim3(kArgmaxThreads), 0, s, logits + (int64_t)b0 * vocab,
-                           vocab, partial + (int64_t)b0 * vocab, ntasks, rpt, margin, ids + b0);
+                           vocab, partial + (int64_t)b0 * vocab, ntasks, rpt, margin, ids + b0, gm, ngroups);
         if (hipGetLastError() != hipSuccess) return RTA_ERR_LAUNCH;
         b0 += chunk;
     }
