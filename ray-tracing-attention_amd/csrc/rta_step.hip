@@ -339,19 +339,19 @@ __global__ void __launch_bounds__(256) delta_rule_kernel(float* __restrict__ sta
 // h % key_heads, while the convolution runs over the heads' own channels (weights and
 // window of channel part W + h hd + c).  With ext_a, the gate inputs are ext_a[b
 // ext_stride + h] and ext_b[...] times the row's RMSNorm factor rn (1 without rn).
-template <int NS>
-__global__ void __launch_bounds__(256) recurrent_mix_kernel(
+template <int NS, int NW>
+__global__ void __launch_bounds__(64 * NW) recurrent_mix_kernel(
     const float* __restrict__ proj, int64_t slab_stride, int row_stride, int nslab, int key_heads,
     const float* __restrict__ ext_a, const float* __restrict__ ext_b, int ext_stride, const RowNorm rn,
     float* __restrict__ conv_state, const float* __restrict__ conv_w, const float* __restrict__ a_log,
     const float* __restrict__ dt_bias, float* __restrict__ state, const float* __restrict__ norm_w, int heads,
     float eps, float* __restrict__ out, int out_stride) {
-    constexpr int hd = 128, kRows = hd / 4;
+    constexpr int hd = 128, kRows = hd / NW;   // state rows per wave
     __shared__ float qkv_s[3][hd];
     __shared__ float z_s[hd];
     __shared__ float gates_s[2];
     __shared__ float o_s[hd];
-    __shared__ float red[4];
+    __shared__ float red[NW];
     const int h = blockIdx.x, b = blockIdx.y, tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int W = heads * hd, W3 = 3 * W, KW = key_heads * hd, hk = h % key_heads;
@@ -371,7 +371,7 @@ __global__ void __launch_bounds__(256) recurrent_mix_kernel(
         return v;
     };
     // threads 0..127: coordinate c of q, k, v (ops 19, 20); 128..255: the gate z, and
-    // thread 128 the decay / beta inputs (op 18).  Their loads go out before the
+    // thread 128 the decay / beta inputs (op 18); threads from 256 on only hold state.  Their loads go out before the
     // recurrent state's, which take the longest and complete in order behind them.
     const int c = tid & (hd - 1);
     const bool conv = tid < hd;
@@ -389,7 +389,7 @@ __global__ void __launch_bounds__(256) recurrent_mix_kernel(
             sv[part][1] = st[1];
             sv[part][2] = st[2];
         }
-    } else {
+    } else if (tid < 2 * hd) {
         load_row(row_z + h * hd + c, raw[0]);
         if (!ext_a) {
             load_row(row_a + h, ab[0]);
@@ -416,7 +416,7 @@ __global__ void __launch_bounds__(256) recurrent_mix_kernel(
             st[1] = sv[part][2];
             st[2] = x;
         }
-    } else {
+    } else if (tid < 2 * hd) {
         z_s[c] = sum_row(raw[0]);
         if (c == 0) {
             float ga, gb;
@@ -449,7 +449,7 @@ __global__ void __launch_bounds__(256) recurrent_mix_kernel(
     }
     __syncthreads();
 
-    // op 21: 4 waves x 32 value rows; lane l holds keys 2l, 2l + 1
+    // op 21: NW waves x 128 / NW value rows; lane l holds keys 2l, 2l + 1
     const float2 q = *reinterpret_cast<const float2*>(&qkv_s[0][2 * lane]);
     const float2 k = *reinterpret_cast<const float2*>(&qkv_s[1][2 * lane]);
     const float* vv = &qkv_s[2][wave * kRows];
@@ -480,7 +480,7 @@ __global__ void __launch_bounds__(256) recurrent_mix_kernel(
     __syncthreads();
     // op 15: gated RMSNorm of o
     const float v = tid < hd ? o_s[tid] : 0.0f;
-    const float ss = block_sum<4>(v * v, red);
+    const float ss = block_sum<NW>(v * v, red);
     const float inv = 1.0f / sqrtf(ss / (float)hd + eps);
     if (tid < hd) out[(int64_t)b * out_stride + h * hd + tid] = v * inv * norm_w[h * hd + tid] * silu(z_s[tid]);
 }
@@ -496,15 +496,26 @@ int recurrent_mix(const float* proj, int64_t slab_stride, int row_stride, int ns
     if (batch <= 0 || heads <= 0 || nslab <= 0 || row_stride < rows || (ext_a && ext_stride < heads))
         return RTA_ERR_SHAPE;
     if (nslab > 16) return RTA_ERR_RANGE;
-    const dim3 g(heads, batch), blk(256);
-#define RTA_MIX(NS) hipLaunchKernelGGL(recurrent_mix_kernel<NS>, g, blk, 0, s, proj, slab_stride, row_stride, nslab, \
-                                       key_heads, ext_a, ext_b, ext_stride, rn, conv_state, conv_w, a_log, dt_bias,  \
-                                       state, norm_w, heads, eps, out, out_stride)
-    if (nslab == 1) RTA_MIX(1);
-    else if (nslab == 2) RTA_MIX(2);
-    else if (nslab <= 4) RTA_MIX(4);
-    else if (nslab <= 8) RTA_MIX(8);
-    else RTA_MIX(16);
+    // few (sequence, head) blocks: 16 waves per head, 8 state rows each, so that the
+    // per-row reductions of a head run in parallel; many: 4 waves, 32 rows each
+    const bool wide = (int64_t)heads * batch < 256;
+    const dim3 g(heads, batch), blk(wide ? 1024 : 256);
+#define RTA_MIX(NS, NW) hipLaunchKernelGGL((recurrent_mix_kernel<NS, NW>), g, blk, 0, s, proj, slab_stride, row_stride, \
+                                           nslab, key_heads, ext_a, ext_b, ext_stride, rn, conv_state, conv_w, a_log, \
+                                           dt_bias, state, norm_w, heads, eps, out, out_stride)
+    if (wide) {
+        if (nslab == 1) RTA_MIX(1, 16);
+        else if (nslab == 2) RTA_MIX(2, 16);
+        else if (nslab <= 4) RTA_MIX(4, 16);
+        else if (nslab <= 8) RTA_MIX(8, 16);
+        else RTA_MIX(16, 16);
+    } else {
+        if (nslab == 1) RTA_MIX(1, 4);
+        else if (nslab == 2) RTA_MIX(2, 4);
+        else if (nslab <= 4) RTA_MIX(4, 4);
+        else if (nslab <= 8) RTA_MIX(8, 4);
+        else RTA_MIX(16, 4);
+    }
 #undef RTA_MIX
     return hipGetLastError() == hipSuccess ? RTA_OK : RTA_ERR_LAUNCH;
 }
