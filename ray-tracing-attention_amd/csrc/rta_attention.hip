@@ -64,6 +64,7 @@ struct AttnArgs {
     int32_t* plan;
     int nwg;
     int per_cu;         // workgroups resident on one compute unit (nwg = per_cu x compute units)
+    bool prepared;      // q operands and plan already written (full_layer_middle)
     int64_t max_tiles;  // tiles per sequence at most: ceil(max_ctx / 64)
     int64_t rstride;    // records per sequence in the workspace
 };
@@ -1836,6 +1837,311 @@ __global__ void __launch_bounds__(256, 2) attn_chunk_mma6_kernel(const AttnArgs 
     if (err) raise_error(err);
 }
 
+// ---- the middle of a full-attention layer of the decode step --------------------------
+// In-projection row r of sequence b = sum over k < nslab of proj[k slab_stride +
+// b row_stride + r] in slab order (rows q | k | v | gate: hq, hkv, hkv and hq heads of
+// 128).  Blocks (x, b), 256 threads:
+//   x < nqb          query heads 4x .. 4x + 3, a wave each: QK-norm (op 14,
+//                    resident_math.comp:113-114) and RoPE (op 3, resident_math.comp:76-77;
+//                    phase resident_common.glsl:117; lane = the pair 2l, 2l + 1) to
+//                    q_out; with qop the head's rows of its kv head's matrix-core q
+//                    operands (make_qop's values); with a gate its summed rows to gate_out
+//   x < nqb + nkv2   kv heads 2j, 2j + 1 (j = x - nqb): K norm and RoPE (waves 0, 1), V
+//                    (waves 2, 3), then one superblock of each history field quantised with
+//                    pack_history_kernel's arithmetic and written to packet slot[b]
+//   x == nqb + nkv2  (b = 0, with a plan) the attention's tile plan.
+struct MiddleArgs {
+    const float* proj;
+    int64_t slab_stride;
+    int row_stride, nslab, hq, hkv, G;
+    const float *q_norm, *k_norm;
+    float eps;
+    const int64_t* positions;
+    int rotary;
+    double theta;
+    float* q_out;
+    uint4* qop;          // [nseq][hkv][6][64] or null
+    float* gate_out;     // row b at gate_out + b gate_stride (head h at + 128 h), or null
+    int64_t gate_stride;
+    int fmt_k, fmt_v;
+    const int64_t* slot;
+    int64_t n_slots, stride, v_offset;
+    uint8_t* packets;
+    int nqb, nkv2;
+    AttnArgs plan;       // plan.plan null: no tile plan
+};
+
+__device__ __forceinline__ float mid_glsl_min(float x, float y) { return y < x ? y : x; }
+__device__ __forceinline__ float mid_glsl_max(float x, float y) { return x < y ? y : x; }
+
+// One history field superblock (256 values in xs) quantised into out (144 or 210 bytes
+// in LDS) as pack_history_kernel quantises a field: 256 threads, LDS scratch st.
+struct FieldScratch {
+    float gscale[16], gmin[16], bd, bdm;
+    uint32_t sc[16], mn[16];
+};
+
+__device__ __forceinline__ void mid_stats(const float* xs, bool q4, FieldScratch& st, int t) {
+#pragma clang fp contract(off)
+    const int ng = q4 ? 8 : 16, width = q4 ? 32 : 16;
+    if (t < ng) {
+        float lo = 0.0f, hi = 0.0f;
+        for (int i = 0; i < width; ++i) {
+            const float v = xs[t * width + i];
+            if (q4) {
+                lo = mid_glsl_min(lo, v);
+                hi = mid_glsl_max(hi, v);
+            } else {
+                hi = mid_glsl_max(hi, fabsf(v));
+            }
+        }
+        st.gscale[t] = q4 ? (hi - lo) / 15.0f : hi / 31.0f;
+        st.gmin[t] = q4 ? -lo : 0.0f;
+    }
+}
+
+__device__ __forceinline__ void mid_scales(bool q4, FieldScratch& st, uint8_t* out) {
+#pragma clang fp contract(off)
+    const int ng = q4 ? 8 : 16;
+    float maxD = 0.0f, maxMin = 0.0f;
+    for (int g = 0; g < ng; ++g) {
+        maxD = mid_glsl_max(maxD, st.gscale[g]);
+        maxMin = mid_glsl_max(maxMin, st.gmin[g]);
+    }
+    const _Float16 hd16 = (_Float16)(maxD / (q4 ? 63.0f : 127.0f));
+    st.bd = (float)hd16;
+    const uint16_t hb = __builtin_bit_cast(uint16_t, hd16);
+    if (q4) {
+        const _Float16 hm16 = (_Float16)(maxMin / 63.0f);
+        st.bdm = (float)hm16;
+        const uint16_t hm = __builtin_bit_cast(uint16_t, hm16);
+        out[0] = hb & 255;
+        out[1] = hb >> 8;
+        out[2] = hm & 255;
+        out[3] = hm >> 8;
+    } else {
+        out[208] = hb & 255;
+        out[209] = hb >> 8;
+    }
+}
+
+__device__ __forceinline__ void mid_codes(bool q4, FieldScratch& st, uint8_t* out, int t) {
+#pragma clang fp contract(off)
+    const int ng = q4 ? 8 : 16;
+    if (t < ng) {
+        st.sc[t] = (uint32_t)fminf(fmaxf(rintf(st.gscale[t] / fmaxf(st.bd, 1e-30f)), 0.0f), q4 ? 63.0f : 127.0f);
+        if (q4) st.mn[t] = (uint32_t)fminf(fmaxf(rintf(st.gmin[t] / fmaxf(st.bdm, 1e-30f)), 0.0f), 63.0f);
+        else out[192 + t] = (uint8_t)st.sc[t];
+    }
+}
+
+__device__ __forceinline__ void mid_values(const float* xs, bool q4, const FieldScratch& st, uint8_t* out, int t) {
+#pragma clang fp contract(off)
+    if (q4 && t < 4) {
+        out[4 + t] = (uint8_t)(st.sc[t] | ((st.sc[t + 4] >> 4) << 6));
+        out[8 + t] = (uint8_t)(st.mn[t] | ((st.mn[t + 4] >> 4) << 6));
+        out[12 + t] = (uint8_t)((st.sc[t + 4] & 15u) | ((st.mn[t + 4] & 15u) << 4));
+    }
+    auto q4code = [&](int i) {
+        const int g = i >> 5;
+        const float num = xs[i] + st.bdm * (float)st.mn[g];
+        const float den = fmaxf(st.bd * (float)st.sc[g], 1e-30f);
+        return (uint32_t)fminf(fmaxf(rintf(num / den), 0.0f), 15.0f);
+    };
+    auto q6code = [&](int i) {
+        const int g = i >> 4;
+        const float den = fmaxf(st.bd * (float)st.sc[g], 1e-30f);
+        return (uint32_t)((int)fminf(fmaxf(rintf(xs[i] / den), -32.0f), 31.0f) + 32);
+    };
+    if (q4) {
+        if (t < 128) {   // qs byte t: value 64 (t/32) + t%32 (low nibble) and +32 (high)
+            const int i = 64 * (t >> 5) + (t & 31);
+            out[16 + t] = (uint8_t)(q4code(i) | (q4code(i + 32) << 4));
+        }
+    } else if (t < 128) {   // ql byte: value 128 (t/64) + t%64 (low) and +64 (high)
+        const int i = 128 * (t >> 6) + (t & 63);
+        out[t] = (uint8_t)((q6code(i) & 15u) | ((q6code(i + 64) & 15u) << 4));
+    } else if (t < 192) {   // qh byte: values 128 part + l + 32 k, two bits each
+        const int jj = t - 128, i = 128 * (jj >> 5) + (jj & 31);
+        out[t] = (uint8_t)(((q6code(i) >> 4) & 3u) | (((q6code(i + 32) >> 4) & 3u) << 2) |
+                           (((q6code(i + 64) >> 4) & 3u) << 4) | (((q6code(i + 96) >> 4) & 3u) << 6));
+    }
+}
+
+template <int NS>
+__global__ void __launch_bounds__(256) full_middle_kernel(const MiddleArgs p) {
+    constexpr int hd = 128;
+    __shared__ float xs[2][256];
+    __shared__ float qsv[4][hd];
+    __shared__ FieldScratch st[2];
+    __shared__ uint8_t fb[2][212];
+    const int x = blockIdx.x, b = blockIdx.y, tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const float* src = p.proj + (int64_t)b * p.row_stride;
+    auto load2 = [&](int r) {   // rows r, r + 1 summed over the slabs in slab order
+        float2 t[NS];
+#pragma unroll
+        for (int k = 0; k < NS; ++k)
+            t[k] = *reinterpret_cast<const float2*>(src + (int64_t)min(k, p.nslab - 1) * p.slab_stride + r);
+        float2 v = t[0];
+#pragma unroll
+        for (int k = 1; k < NS; ++k)
+            if (k < p.nslab) {
+                v.x += t[k].x;
+                v.y += t[k].y;
+            }
+        return v;
+    };
+    // QK-norm and RoPE of the pair a lane holds, the phase and its sine / cosine in fp64
+    auto norm_rope = [&](float2 v, const float* w) {
+        if (w) {
+            float ss = v.x * v.x + v.y * v.y;
+            for (int off = 32; off > 0; off >>= 1) ss += __shfl_xor(ss, off, kWave);
+            const float inv = 1.0f / sqrtf(ss / (float)hd + p.eps);
+            v.x = v.x * inv * w[2 * lane];
+            v.y = v.y * inv * w[2 * lane + 1];
+        }
+        const int active = p.rotary / 2;
+        if (lane < active) {
+            const double phase = (double)p.positions[b] * pow(p.theta, -(double)lane / (double)active);
+            double sn, cs;
+            sincos(phase, &sn, &cs);
+            const double a0 = v.x, c0 = v.y;
+            v.x = (float)(a0 * cs - c0 * sn);
+            v.y = (float)(a0 * sn + c0 * cs);
+        }
+        return v;
+    };
+    if (x < p.nqb) {
+        const int h = 4 * x + wave;
+        if (h >= p.hq) return;   // uniform per wave; no block barrier below
+        float2 v = load2(h * hd + 2 * lane);
+        v = norm_rope(v, p.q_norm ? p.q_norm + h * hd : nullptr);
+        *reinterpret_cast<float2*>(p.q_out + ((int64_t)b * p.hq + h) * hd + 2 * lane) = v;
+        if (p.gate_out)
+            *reinterpret_cast<float2*>(p.gate_out + (int64_t)b * p.gate_stride + h * hd + 2 * lane) =
+                load2((p.hq + 2 * p.hkv + h) * hd + 2 * lane);
+        if (!p.qop) return;
+        // this head's rows 2g, 2g + 1 of its kv head's q operands (make_qop)
+        const int G = p.G, kvh = h / G, g = h - kvh * G;
+        qsv[wave][2 * lane] = v.x;
+        qsv[wave][2 * lane + 1] = v.y;
+        float mx = fmaxf(fabsf(v.x), fabsf(v.y));
+        for (int off = 32; off > 0; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off, kWave));
+        const float sg = ldexpf(1.0f, 14 - operand_exponent(mx));
+        __builtin_amdgcn_wave_barrier();
+        uint4* dst = p.qop + ((int64_t)b * p.hkv + kvh) * 6 * kWave;
+        const float* qv = qsv[wave];
+        constexpr int perm[8] = {0, 2, 1, 3, 4, 6, 5, 7};
+        if (lane < 32) {   // word kb of lane (2g + part) + 16u
+            const int part = lane & 1, u = (lane >> 1) & 3, kb = lane >> 3;
+            const float* base = qv + 64 * (kb >> 1) + 32 * (kb & 1) + 8 * u;
+            h8_t a;
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                const float xv = base[perm[i]] * sg;
+                const _Float16 hi = (_Float16)xv;
+                a[i] = part ? (_Float16)(xv - (float)hi) : hi;
+            }
+            dst[kb * kWave + 2 * g + part + 16 * u] = __builtin_bit_cast(uint4, a);
+        } else if (lane < 40) {   // the minimum-term word of lanes of segment 0
+            const int part = lane & 1, u = (lane >> 1) & 3;
+            const _Float16 z = (_Float16)0.0f;
+            h8_t am = h8_t{z, z, z, z, z, z, z, z};
+            if (u == 0) {
+#pragma unroll
+                for (int kb = 0; kb < 4; ++kb) {
+                    float s[4];   // (u0 + u1) + (u2 + u3), each the in-order sum of its 8 dims
+#pragma unroll
+                    for (int uu = 0; uu < 4; ++uu) {
+                        const float* bb = qv + 64 * (kb >> 1) + 32 * (kb & 1) + 8 * uu;
+                        float acc = 0.0f;
+#pragma unroll
+                        for (int i = 0; i < 8; ++i) acc += bb[i];
+                        s[uu] = acc;
+                    }
+                    const float xv = ((s[0] + s[1]) + (s[2] + s[3])) * (sg * 0.03125f);
+                    const _Float16 hi = (_Float16)xv;
+                    am[kb] = part ? (_Float16)(xv - (float)hi) : hi;
+                }
+            }
+            dst[4 * kWave + 2 * g + part + 16 * u] = __builtin_bit_cast(uint4, am);
+        } else if (lane < 56) {   // 1 / s of this head in the rs word of segment g / 2
+            float* rs = reinterpret_cast<float*>(dst + 5 * kWave + (lane - 40) + 16 * (g >> 1));
+            rs[g & 1] = 1.0f / sg;
+            if ((g & 1) == 0) {
+                rs[2] = 0.0f;
+                rs[3] = 0.0f;
+            }
+        }
+        if (g == G - 1 && G < 8) {   // rows of heads >= G: zero operands, 1 / s = 2^-14
+            const _Float16 z = (_Float16)0.0f;
+            const uint4 zero = __builtin_bit_cast(uint4, h8_t{z, z, z, z, z, z, z, z});
+            const int rows = 16 - 2 * G;
+            for (int i = lane; i < rows * 4 * 5; i += kWave) {
+                const int w = i / (rows * 4), rem = i - w * rows * 4;
+                dst[w * kWave + 2 * G + rem % rows + 16 * (rem / rows)] = zero;
+            }
+            for (int gd = G + (G & 1); gd < 8; gd += 2)
+                if (lane < 16) {
+                    float* rs = reinterpret_cast<float*>(dst + 5 * kWave + lane + 16 * (gd >> 1));
+                    rs[0] = 1.0f / 16384.0f;
+                    rs[1] = 1.0f / 16384.0f;
+                    rs[2] = 0.0f;
+                    rs[3] = 0.0f;
+                }
+            if (G & 1 && lane < 16)   // the odd head count's partner: component 1 of segment G / 2
+                reinterpret_cast<float*>(dst + 5 * kWave + lane + 16 * (G >> 1))[1] = 1.0f / 16384.0f;
+        }
+        return;
+    }
+    if (x < p.nqb + p.nkv2) {
+        const int j = x - p.nqb;
+        const int kh = 2 * j + (wave & 1);   // kv head of this wave
+        const bool live = kh < p.hkv;       // uniform
+        float2 v = float2{0.0f, 0.0f};
+        if (wave < 2) {
+            if (live) v = norm_rope(load2((p.hq + kh) * hd + 2 * lane), p.k_norm ? p.k_norm + kh * hd : nullptr);
+            xs[0][(wave & 1) * hd + 2 * lane] = v.x;
+            xs[0][(wave & 1) * hd + 2 * lane + 1] = v.y;
+        } else {
+            if (live) v = load2((p.hq + p.hkv + kh) * hd + 2 * lane);
+            xs[1][(wave & 1) * hd + 2 * lane] = v.x;
+            xs[1][(wave & 1) * hd + 2 * lane + 1] = v.y;
+        }
+        const bool q4[2] = {p.fmt_k == RTA_Q4_K, p.fmt_v == RTA_Q4_K};
+        for (int i = tid; i < 2 * 212; i += 256) fb[i / 212][i % 212] = 0;
+        __syncthreads();
+        mid_stats(xs[0], q4[0], st[0], tid);
+        if (tid >= 64 && tid < 128) mid_stats(xs[1], q4[1], st[1], tid - 64);
+        __syncthreads();
+        if (tid == 0) mid_scales(q4[0], st[0], fb[0]);
+        if (tid == 64) mid_scales(q4[1], st[1], fb[1]);
+        __syncthreads();
+        mid_codes(q4[0], st[0], fb[0], tid);
+        if (tid >= 64 && tid < 128) mid_codes(q4[1], st[1], fb[1], tid - 64);
+        __syncthreads();
+        mid_values(xs[0], q4[0], st[0], fb[0], tid);
+        mid_values(xs[1], q4[1], st[1], fb[1], tid);
+        __syncthreads();
+        const int64_t sl = p.slot[b];
+        if (sl < 0 || sl >= p.n_slots) {
+            if (tid == 0) raise_error(RTA_DEVERR_HITS);
+            return;
+        }
+        uint8_t* pk = p.packets + sl * p.stride;
+        const int kb = q4[0] ? 144 : 210, vb = q4[1] ? 144 : 210;
+        for (int i = tid; i < kb; i += 256) pk[(int64_t)j * kb + i] = fb[0][i];
+        for (int i = tid; i < vb; i += 256) pk[p.v_offset + (int64_t)j * vb + i] = fb[1][i];
+        if (j == 0) {   // the packet's padding
+            const int64_t end = p.v_offset + (int64_t)p.nkv2 * vb;
+            for (int64_t i = end + tid; i < p.stride; i += 256) pk[i] = 0;
+        }
+        return;
+    }
+    if (b == 0 && wave == 0 && p.plan.plan) attn_plan_wave(p.plan);
+}
+
 // One workgroup per (sequence, query head): 8 chunk groups x 32 lanes of 4
 // coordinates; every thread keeps 8 chunk records in flight.  One pass: each group
 // folds its records into a running (m, Z, U), rescaled when m grows, and the groups
@@ -2050,7 +2356,8 @@ static hipError_t launch_chunk_k(const AttnArgs& a, int lds, hipStream_t s) {
     if constexpr (KF == RTA_Q4_K) {
         if (a.hkv <= 8) {
             // (one more column of blocks builds the tile list of the matrix-core kernel)
-            hipLaunchKernelGGL((attn_qprep_kernel<G>), dim3(a.hkv + (a.plan ? 1 : 0), a.nseq), dim3(kWave), 0, s, a);
+            if (!a.prepared)
+                hipLaunchKernelGGL((attn_qprep_kernel<G>), dim3(a.hkv + (a.plan ? 1 : 0), a.nseq), dim3(kWave), 0, s, a);
             if constexpr (VF == RTA_Q6_K) {   // scores and P V on the matrix cores
                 if (a.hkv <= 4) return launch_chunk_mma<G, 1>(a, s);
                 return launch_chunk_mma<G, 2>(a, s);
@@ -2152,7 +2459,7 @@ int decode_attention_gate_stride(const float* q, int nseq, int hq, int hkv, int 
                                  int fmt_v, const int64_t* slot_base, const int32_t* ctx_len, int64_t capacity,
                                  int64_t n_slots, int max_ctx, const float* gate, int64_t gate_stride, float* out,
                                  float* m_out, float* z_out, void* workspace, size_t workspace_bytes,
-                                 rta_stream_t stream, int out_rotary) {
+                                 rta_stream_t stream, int out_rotary, bool prepared) {
     if (!q || !packets || !slot_base || !ctx_len || !out) return RTA_ERR_NULL;   // m_out, z_out optional
     if (nseq <= 0 || hq <= 0 || hkv <= 0 || hd <= 0 || hq % hkv || capacity <= 0 || max_ctx <= 0 || n_slots <= 0)
         return RTA_ERR_SHAPE;
@@ -2182,6 +2489,7 @@ int decode_attention_gate_stride(const float* q, int nseq, int hq, int hkv, int 
     a.gate_stride = gate_stride;
     if (out_rotary < 0 || out_rotary > hd || out_rotary % 2) return RTA_ERR_RANGE;
     a.out_rotary = out_rotary;
+    a.prepared = prepared;
     a.out = out;
     a.m_out = m_out;
     a.z_out = z_out;
@@ -2213,6 +2521,70 @@ int decode_attention_gate_stride(const float* q, int nseq, int hq, int hkv, int 
     else e = launch_chunks<RTA_Q4_K, RTA_Q4_K>(G, a, lds, s);
     if (e != hipSuccess) return RTA_ERR_LAUNCH;
     hipLaunchKernelGGL(attn_merge_kernel, dim3(nseq * hq), dim3(256), 0, s, a);
+    return hipGetLastError() == hipSuccess ? RTA_OK : RTA_ERR_LAUNCH;
+}
+
+int full_layer_middle(const float* proj, int64_t slab_stride, int row_stride, int nslab, int batch, int hq, int hkv,
+                      const float* q_norm, const float* k_norm, float eps, const int64_t* positions, int rotary,
+                      double theta, float* q_out, float* gate_out, int64_t gate_stride, int fmt_k, int fmt_v,
+                      const int64_t* slots, int64_t n_slots, void* packets, const int32_t* ctx_len, int64_t capacity,
+                      int max_ctx, void* attn_ws, hipStream_t s) {
+    if (!proj || !positions || !q_out || !slots || !packets || !ctx_len || !attn_ws) return RTA_ERR_NULL;
+    if (batch <= 0 || hq <= 0 || hkv <= 0 || hq % hkv || row_stride < (2 * hq + 2 * hkv) * kHd - (gate_out ? 0 : hq * kHd))
+        return RTA_ERR_SHAPE;
+    if (nslab <= 0 || nslab > 16 || rotary < 0 || rotary > kHd || rotary % 2) return RTA_ERR_RANGE;
+    if ((fmt_k != RTA_Q4_K && fmt_k != RTA_Q6_K) || (fmt_v != RTA_Q4_K && fmt_v != RTA_Q6_K) ||
+        (fmt_k == RTA_Q6_K && fmt_v == RTA_Q6_K))
+        return RTA_ERR_FORMAT;
+    const int G = hq / hkv;
+    MiddleArgs p{};
+    p.proj = proj;
+    p.slab_stride = slab_stride;
+    p.row_stride = row_stride;
+    p.nslab = nslab;
+    p.hq = hq;
+    p.hkv = hkv;
+    p.G = G;
+    p.q_norm = q_norm;
+    p.k_norm = k_norm;
+    p.eps = eps;
+    p.positions = positions;
+    p.rotary = rotary;
+    p.theta = theta;
+    p.q_out = q_out;
+    p.gate_out = gate_out;
+    p.gate_stride = gate_stride;
+    p.fmt_k = fmt_k;
+    p.fmt_v = fmt_v;
+    p.slot = slots;
+    p.n_slots = n_slots;
+    p.stride = host::history_bytes(hkv * kHd);
+    p.nkv2 = (hkv * kHd + 255) / 256;
+    p.v_offset = (int64_t)p.nkv2 * (fmt_k == RTA_Q4_K ? 144 : 210);
+    p.packets = static_cast<uint8_t*>(packets);
+    p.nqb = (hq + 3) / 4;
+    // the attention kernels for Q4_K keys of at most 8 kv heads read matrix-core q operands
+    // (and, with Q6_K values, a tile plan) that rta_decode_attention keeps in its
+    // workspace: written here instead
+    const bool qops = fmt_k == RTA_Q4_K && hkv <= 8 && (G == 1 || G == 2 || G == 4 || G == 8);
+    if (qops) p.qop = reinterpret_cast<uint4*>(static_cast<uint8_t*>(attn_ws) + attn_record_bytes(batch, hq, max_ctx));
+    if (qops && fmt_v == RTA_Q6_K) {
+        AttnArgs& a = p.plan;
+        a.nseq = batch;
+        a.ctx_len = ctx_len;
+        a.capacity = capacity;
+        a.max_tiles = ((int64_t)max_ctx + kTile - 1) / kTile;
+        a.per_cu = 2;
+        a.nwg = attn_mma_workgroups(a.per_cu);
+        a.plan = reinterpret_cast<int32_t*>(reinterpret_cast<uint8_t*>(p.qop) +
+                                            (size_t)batch * hkv * 6 * kWave * sizeof(uint4));
+    }
+    const dim3 g(p.nqb + p.nkv2 + (p.plan.plan ? 1 : 0), batch), blk(256);
+    if (nslab == 1) hipLaunchKernelGGL((full_middle_kernel<1>), g, blk, 0, s, p);
+    else if (nslab == 2) hipLaunchKernelGGL((full_middle_kernel<2>), g, blk, 0, s, p);
+    else if (nslab <= 4) hipLaunchKernelGGL((full_middle_kernel<4>), g, blk, 0, s, p);
+    else if (nslab <= 8) hipLaunchKernelGGL((full_middle_kernel<8>), g, blk, 0, s, p);
+    else hipLaunchKernelGGL((full_middle_kernel<16>), g, blk, 0, s, p);
     return hipGetLastError() == hipSuccess ? RTA_OK : RTA_ERR_LAUNCH;
 }
 

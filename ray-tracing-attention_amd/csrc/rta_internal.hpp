@@ -74,7 +74,22 @@ int decode_attention_gate_stride(const float* q, int nseq, int hq, int hkv, int 
                                  int fmt_v, const int64_t* slot_base, const int32_t* ctx_len, int64_t capacity,
                                  int64_t n_slots, int max_ctx, const float* gate, int64_t gate_stride, float* out,
                                  float* m_out, float* z_out, void* workspace, size_t workspace_bytes,
-                                 rta_stream_t stream, int out_rotary = 0);
+                                 rta_stream_t stream, int out_rotary = 0, bool prepared = false);
+
+// The middle of a full-attention layer in one kernel, between its in-projection and the
+// attention: in-projection rows (q | k | v | gate, hq / hkv / hkv / hq heads of 128) of
+// sequence b summed over nslab K slabs, proj[k slab_stride + b row_stride + r];
+// QK-norm + RoPE of q (to q_out, [batch][hq][128]) and k; k and v quantised into packet
+// slots[b] (fmt_k / fmt_v fields, as rta_pack_history); gate rows summed into gate_out
+// (row b at + b gate_stride; null: no gate).  For the layout whose attention runs on the
+// Q4_K-key matrix-core kernel it also writes that kernel's q operands and tile plan into
+// attn_ws (the workspace of the decode_attention_gate_stride call that follows with
+// prepared = true, same batch, heads, ctx_len, capacity and max_ctx).
+int full_layer_middle(const float* proj, int64_t slab_stride, int row_stride, int nslab, int batch, int hq, int hkv,
+                      const float* q_norm, const float* k_norm, float eps, const int64_t* positions, int rotary,
+                      double theta, float* q_out, float* gate_out, int64_t gate_stride, int fmt_k, int fmt_v,
+                      const int64_t* slots, int64_t n_slots, void* packets, const int32_t* ctx_len, int64_t capacity,
+                      int max_ctx, void* attn_ws, hipStream_t s);
 
 // ---- the decode step's readouts of a staged x image (rta_packed.hpp) ----
 constexpr int kReadStore = 0, kReadAccumulate = 1, kReadSwiglu = 2;   // image_readout modes

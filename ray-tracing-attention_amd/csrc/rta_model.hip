@@ -33,43 +33,6 @@ __global__ void __launch_bounds__(256) step_prologue_kernel(int32_t* __restrict_
     ctx[b] = pos + 1;
 }
 
-// Fused QK-norm (op 14, resident_math.comp:113-114) and RoPE (op 3,
-// resident_math.comp:76-77; phase resident_common.glsl:117) over the q and k heads
-// of the [q | k | v] projection rows; one wave per (row, head), lane l holds the
-// adjacent pair (2l, 2l+1) of a 128-wide head.  q goes to q_out (contiguous), k is
-// rotated in place.  wq / wk NULL: RoPE only.
-__global__ void __launch_bounds__(256) qk_norm_rope_kernel(float* __restrict__ qkv, int stride, int hq, int hkv,
-                                                           const float* __restrict__ wq,
-                                                           const float* __restrict__ wk, float eps,
-                                                           const int64_t* __restrict__ positions, int rotary,
-                                                           double theta, float* __restrict__ q_out) {
-    constexpr int hd = 128;
-    const int lane = threadIdx.x & 63, head = blockIdx.x * 4 + (threadIdx.x >> 6), b = blockIdx.y;
-    if (head >= hq + hkv) return;
-    const bool isq = head < hq;
-    float* x = qkv + (int64_t)b * stride + (int64_t)head * hd;   // k heads follow the q heads
-    float2 v = reinterpret_cast<float2*>(x)[lane];
-    const float* w = isq ? (wq ? wq + head * hd : nullptr) : (wk ? wk + (head - hq) * hd : nullptr);
-    if (w) {
-        float ss = v.x * v.x + v.y * v.y;
-        for (int off = 32; off > 0; off >>= 1) ss += __shfl_xor(ss, off, kWave);
-        const float inv = 1.0f / sqrtf(ss / (float)hd + eps);
-        v.x = v.x * inv * w[2 * lane];
-        v.y = v.y * inv * w[2 * lane + 1];
-    }
-    const int active = rotary / 2;
-    if (lane < active) {
-        const double phase = (double)positions[b] * pow(theta, -(double)lane / (double)active);
-        double sn, cs;
-        sincos(phase, &sn, &cs);
-        const double a = v.x, c = v.y;
-        v.x = (float)(a * cs - c * sn);
-        v.y = (float)(a * sn + c * cs);
-    }
-    if (isq) reinterpret_cast<float2*>(q_out + ((int64_t)b * hq + head) * hd)[lane] = v;
-    else reinterpret_cast<float2*>(x)[lane] = v;
-}
-
 // Ring bases (sequence b owns slots [b * capacity, (b + 1) * capacity) of every
 // full layer's packet array) and the starting positions.
 __global__ void __launch_bounds__(256) state_init_kernel(const int32_t* __restrict__ ctx_in, int batch, int n_full,
@@ -402,14 +365,16 @@ int rta_hybrid_decode_step(const rta_hybrid_shape* shape, const rta_hybrid_weigh
         const int fi = fmt_of(lw.fmt_in), fo = fmt_of(lw.fmt_o), fgu = fmt_of(lw.fmt_gate_up),
                   fd = fmt_of(lw.fmt_down);
         if (is_full(shape, l)) {
-            // op 2 index 5 (q | k | v | gate), ops 14 + 3, op 34, attention, op 2 index 2
+            // op 2 index 5 (q | k | v | gate); ops 14 + 3 and 34 with the slab sum in one
+            // kernel (full_layer_middle); attention; op 2 index 2
+            int ns = 1;   // K slabs of the in-projection left in gemm_ws (1: rows final in w.proj)
             if (lw.in_parts > 0) {
                 RTA_TRY(in_parts(lw, d.rows_full, false));
             } else {
                 RTA_TRY(norm(lw.norm_in, fi, false));
                 if (imaged(fi))
                     RTA_TRY(image_readout(fi, kReadStore, lw.w_in, nullptr, d.rows_full, d.D, w.ximg, B, w.proj,
-                                          true, w.gemm_ws, w.gemm_bytes, s, nullptr, rn));
+                                          false, w.gemm_ws, w.gemm_bytes, s, &ns, rn));
                 else if (rn.part || xn.w)
                     RTA_TRY(projection_store(fi, lw.w_in, d.rows_full, d.D, xn.w ? w.hidden : w.normed, B, w.proj,
                                              w.gemm_ws, w.gemm_bytes, s, rn, xn));
@@ -417,19 +382,18 @@ int rta_hybrid_decode_step(const rta_hybrid_shape* shape, const rta_hybrid_weigh
                     RTA_TRY(rta_gemv(fi, lw.w_in, d.rows_full, d.D, w.normed, B, w.proj, RTA_EPI_STORE,
                                      w.gemm_ws, w.gemm_bytes, stream));
             }
-            hipLaunchKernelGGL(qk_norm_rope_kernel, dim3((d.hq + d.hkv + 3) / 4, B), dim3(256), 0, s, w.proj,
-                               d.rows_full, d.hq, d.hkv, lw.q_norm, lw.k_norm, eps, w.pos, shape->rope_rotary,
-                               shape->rope_theta, w.q);
-            if (hipGetLastError() != hipSuccess) return RTA_ERR_LAUNCH;
             uint8_t* packets = st.packets + (size_t)lf * B * d.cap * d.stride;
-            RTA_TRY(rta_pack_history(w.proj + d.hq * d.hd, d.rows_full, w.proj + (d.hq + d.hkv) * d.hd, d.rows_full,
-                                     B, d.kvw, shape->fmt_k, shape->fmt_v, w.slots + (size_t)lf * B,
-                                     (int64_t)B * d.cap, packets, stream));
-            const float* gate = shape->attn_gate ? w.proj + (d.hq + 2 * d.hkv) * d.hd : nullptr;
+            float* gate = shape->attn_gate ? w.proj + (d.hq + 2 * d.hkv) * d.hd : nullptr;
+            RTA_TRY(full_layer_middle(ns > 1 ? static_cast<const float*>(w.gemm_ws) : w.proj,
+                                      (int64_t)kSlabBatch * d.rows_full, d.rows_full, ns, B, d.hq, d.hkv, lw.q_norm,
+                                      lw.k_norm, eps, w.pos, shape->rope_rotary, shape->rope_theta, w.q, gate,
+                                      d.rows_full, shape->fmt_k, shape->fmt_v, w.slots + (size_t)lf * B,
+                                      (int64_t)B * d.cap, packets, w.visible, d.cap, d.cap, w.attn_ws, s));
             RTA_TRY(decode_attention_gate_stride(w.q, B, d.hq, d.hkv, d.hd, packets, shape->fmt_k, shape->fmt_v,
                                                  st.base + (size_t)lf * B, w.visible, d.cap, (int64_t)B * d.cap,
                                                  d.cap, gate, d.rows_full, w.mix, nullptr, nullptr, w.attn_ws,
-                                                 w.attn_bytes, stream, shape->o_axis_remap ? shape->rope_rotary : 0));
+                                                 w.attn_bytes, stream, shape->o_axis_remap ? shape->rope_rotary : 0,
+                                                 true));
             RTA_TRY(residual_proj(fo, lw.w_o, d.hq * d.hd, w.mix));
             ++lf;
         } else {
