@@ -496,26 +496,19 @@ int recurrent_mix(const float* proj, int64_t slab_stride, int row_stride, int ns
     if (batch <= 0 || heads <= 0 || nslab <= 0 || row_stride < rows || (ext_a && ext_stride < heads))
         return RTA_ERR_SHAPE;
     if (nslab > 16) return RTA_ERR_RANGE;
-    // few (sequence, head) blocks: 16 waves per head, 8 state rows each, so that the
-    // per-row reductions of a head run in parallel; many: 4 waves, 32 rows each
-    const bool wide = (int64_t)heads * batch < 256;
-    const dim3 g(heads, batch), blk(wide ? 1024 : 256);
-#define RTA_MIX(NS, NW) hipLaunchKernelGGL((recurrent_mix_kernel<NS, NW>), g, blk, 0, s, proj, slab_stride, row_stride, \
-                                           nslab, key_heads, ext_a, ext_b, ext_stride, rn, conv_state, conv_w, a_log, \
-                                           dt_bias, state, norm_w, heads, eps, out, out_stride)
-    if (wide) {
-        if (nslab == 1) RTA_MIX(1, 16);
-        else if (nslab == 2) RTA_MIX(2, 16);
-        else if (nslab <= 4) RTA_MIX(4, 16);
-        else if (nslab <= 8) RTA_MIX(8, 16);
-        else RTA_MIX(16, 16);
-    } else {
-        if (nslab == 1) RTA_MIX(1, 4);
-        else if (nslab == 2) RTA_MIX(2, 4);
-        else if (nslab <= 4) RTA_MIX(4, 4);
-        else if (nslab <= 8) RTA_MIX(8, 4);
-        else RTA_MIX(16, 4);
-    }
+    // 16 waves per (sequence, head) block, 8 state rows each: the per-row reductions of
+    // a head run in parallel, and at large batches the state reads of one block overlap
+    // the state writes of another (measured faster than 4 waves x 32 rows at batch 1 and 32)
+    constexpr int kWaves = 16;
+    const dim3 g(heads, batch), blk(64 * kWaves);
+#define RTA_MIX(NS) hipLaunchKernelGGL((recurrent_mix_kernel<NS, kWaves>), g, blk, 0, s, proj, slab_stride, \
+                                       row_stride, nslab, key_heads, ext_a, ext_b, ext_stride, rn, conv_state, conv_w, \
+                                       a_log, dt_bias, state, norm_w, heads, eps, out, out_stride)
+    if (nslab == 1) RTA_MIX(1);
+    else if (nslab == 2) RTA_MIX(2);
+    else if (nslab <= 4) RTA_MIX(4);
+    else if (nslab <= 8) RTA_MIX(8);
+    else RTA_MIX(16);
 #undef RTA_MIX
     return hipGetLastError() == hipSuccess ? RTA_OK : RTA_ERR_LAUNCH;
 }
