@@ -444,10 +444,12 @@ def w_proj(torch, args, orc):
     return res
 
 
-def step_kernels(torch, shape, batch, dev):
+def step_kernels(torch, shape, batch, dev, packed):
     """The decode step's readouts and its attention as separate calls of the C ABI, at the
     step's shapes, each over enough distinct (rotated) weight copies that every call
-    streams its weights from HBM.  Returns [(name, calls per step, alg bytes, launch)]."""
+    streams its weights from HBM, on the weight layout the step runs (packed tiles read by
+    the matrix-core readout, or GGUF rows read by the vector-ALU one).  Returns [(name,
+    calls per step, alg bytes, launch)]."""
     from rta import model, ops
     gen = torch.Generator(device=dev)
     gen.manual_seed(20261116)
@@ -455,13 +457,15 @@ def step_kernels(torch, shape, batch, dev):
     S = shape.rec_heads * hd
     nfull = shape.layers // shape.full_every
     nrec = shape.layers - nfull
-    P4, P6 = Q4_K | ops.TILED, Q6_K | ops.TILED
+    P4 = Q4_K | ops.TILED if packed else Q4_K
+    kern = "gemm_tiled_kernel" if packed else "gemv_b1_kernel"
+    lay = "packed" if packed else "GGUF rows"
     qb = lambda fmt, rows, cols: rows * cols // 256 * (144 if fmt == Q4_K else 210)  # noqa: E731
 
     def copies(fmt, rows, cols, per=1):
         n = max(2, 3 * CACHE_BYTES // (per * qb(fmt, rows, cols)) + 1)
-        return [[ops.pack(fmt, model.random_kquant(fmt, rows, cols, gen, dev), rows, cols) for _ in range(per)]
-                for _ in range(n)]
+        make = lambda: model.random_kquant(fmt, rows, cols, gen, dev)  # noqa: E731
+        return [[ops.pack(fmt, make(), rows, cols) if packed else make() for _ in range(per)] for _ in range(n)]
 
     x_d = torch.randn(batch, D, device=dev, generator=gen)
     x_ff = torch.randn(batch, FF, device=dev, generator=gen) * 0.1
@@ -469,7 +473,7 @@ def step_kernels(torch, shape, batch, dev):
     y_d = torch.zeros(batch, D, device=dev)
     y_in = torch.empty(batch, 4 * S + 2 * shape.rec_heads, device=dev)
     y_full = torch.empty(batch, (hq + 2 * hkv) * hd, device=dev)
-    ws = torch.empty(max(ops.mlp_workspace_bytes(P4, P4, D, FF, batch),
+    ws = torch.empty(max(1, ops.mlp_workspace_bytes(P4, P4, D, FF, batch),
                          ops.gemv_workspace_bytes(P4, 4 * S + 2 * shape.rec_heads, D, batch)),
                      dtype=torch.uint8, device=dev)
     gu = copies(Q4_K, FF, D, per=2)
@@ -478,20 +482,20 @@ def step_kernels(torch, shape, batch, dev):
     rin = copies(Q4_K, 4 * S + 2 * shape.rec_heads, D)
     fin = copies(Q4_K, (hq + 2 * hkv) * hd, D)
     out = []
-    out.append(("gate/up: gemm_tiled_kernel<Q4_K,SwiGLU> (rta_swiglu, packed 2 x 12288x4096)", shape.layers,
+    out.append((f"gate/up: {kern}<Q4_K,SwiGLU> (rta_swiglu, {lay} 2 x 12288x4096)", shape.layers,
                 2 * qb(Q4_K, FF, D) + 4 * batch * (D + FF),
                 lambda i: ops.swiglu(P4, gu[i % len(gu)][0], gu[i % len(gu)][1], D, FF, x_d, act=act, workspace=ws)))
-    out.append(("down: gemm_tiled_kernel<Q4_K,accumulate> + slab reduce (rta_gemv, packed 4096x12288)", shape.layers,
+    out.append((f"down: {kern}<Q4_K,accumulate> + slab reduce (rta_gemv, {lay} 4096x12288)", shape.layers,
                 qb(Q4_K, D, FF) + 4 * batch * (FF + 2 * D),
                 lambda i: ops.gemv(P4, dn[i % len(dn)][0], D, FF, x_ff, y=y_d, accumulate=True, workspace=ws)))
-    out.append(("O projection: gemm_tiled_kernel<Q4_K,accumulate> + slab reduce (rta_gemv, packed 4096x4096)",
+    out.append((f"O projection: {kern}<Q4_K,accumulate> + slab reduce (rta_gemv, {lay} 4096x4096)",
                 shape.layers, qb(Q4_K, D, hq * hd) + 4 * batch * (hq * hd + 2 * D),
                 lambda i: ops.gemv(P4, op[i % len(op)][0], D, hq * hd, x_d, y=y_d, accumulate=True, workspace=ws)))
-    out.append(("recurrent in-projection: gemm_tiled_kernel<Q4_K,store> + slab reduce (rta_gemv, packed 16448x4096)",
+    out.append((f"recurrent in-projection: {kern}<Q4_K,store> + slab reduce (rta_gemv, {lay} 16448x4096)",
                 nrec, qb(Q4_K, 4 * S + 2 * shape.rec_heads, D) + 4 * batch * (D + 4 * S + 2 * shape.rec_heads),
                 lambda i: ops.gemv(P4, rin[i % len(rin)][0], 4 * S + 2 * shape.rec_heads, D, x_d, y=y_in,
                                    workspace=ws)))
-    out.append(("full in-projection: gemm_tiled_kernel<Q4_K,store> + slab reduce (rta_gemv, packed 6144x4096)", nfull,
+    out.append((f"full in-projection: {kern}<Q4_K,store> + slab reduce (rta_gemv, {lay} 6144x4096)", nfull,
                 qb(Q4_K, (hq + 2 * hkv) * hd, D) + 4 * batch * (D + (hq + 2 * hkv) * hd),
                 lambda i: ops.gemv(P4, fin[i % len(fin)][0], (hq + 2 * hkv) * hd, D, x_d, y=y_full, workspace=ws)))
     return out
@@ -555,13 +559,15 @@ def w_decode(torch, args, orc):
     hist = sum_ctx * nfull * v.packet_bytes                             # history read per step (approx.)
     state = 2 * nrec * batch * shape.rec_heads * 128 * 128 * 4          # recurrent state read + write
     step_bytes = w_bytes + m.lm_head.numel() + hist + state
-    kernels = step_kernels(torch, shape, batch, dev) if batch == 32 else []
+    kernels = step_kernels(torch, shape, batch, dev, packed)
     kernels.append((f"attention: attn_qprep_kernel + attn_chunk_mma_kernel<G=4,KPW=2> + attn_merge_kernel ({batch} "
                     f"sequences, {hq}/{hkv} heads, {sum_ctx} positions of {v.packet_bytes}-byte packets)", nfull,
                     sum_ctx * v.packet_bytes + 2 * batch * hq * hd * 4, attention))
-    kernels.append(("LM head: gemm_tiled_kernel<Q6_K,logits> + argmax_margin_kernel (rta_lm_head, packed "
-                    "151936x4096)", 1, m.lm_head.numel() + 4 * batch * (shape.hidden + shape.vocab), lm_head))
+    kernels.append((f"LM head: {'gemm_tiled_kernel' if packed else 'gemv_b1_kernel'}<Q6_K,logits> + group max + "
+                    f"argmax_margin_kernel (rta_lm_head, {'packed' if packed else 'GGUF rows'} 151936x4096)", 1, m.lm_head.numel() + 4 * batch * (shape.hidden + shape.vocab), lm_head))
+    # HBM bytes measured per launch at this batch (the batch-32 figures under "decode/...")
     res = {"alg_bytes": step_bytes, "graph_per_step": True, "kernels": kernels,
+           "traffic_prefix": "decode" if batch == 32 else f"decode_b{batch}",
            "step": step, "unit": "tok/s", "value_from_ms": lambda ms: batch / (ms * 1e-3),
            "dtype": "q4_k/q6_k weights x fp32 activations and state, fp32 accumulate",
            "config": {"workload": f"9B-shape hybrid decode step, batch {batch} (32 layers: 24 gated delta-net + 8 "
@@ -690,7 +696,7 @@ def main():
     for name, calls, alg, launch in wl.get("kernels", []):
         km = time_kernel(torch, launch)
         ach = alg / (km * 1e-3) / 1e9
-        key = f"{args.workload}/{name.split(':')[0]}"
+        key = f"{wl.get('traffic_prefix', args.workload)}/{name.split(':')[0]}"
         table.append({"kernel": name, "calls_per_step": calls, "ms_mean": km, "alg_bytes": alg,
                       "achieved_gbs": ach, "frac": ach / HBM_PEAK_GBS, "ms_per_step": calls * km,
                       "traffic": traffic_for(key)})
