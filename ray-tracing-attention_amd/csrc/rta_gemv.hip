@@ -568,6 +568,28 @@ int residual_norm_image(int fmt, float* hidden, const float* part, int nslab, co
     return hipGetLastError() == hipSuccess ? RTA_OK : RTA_ERR_LAUNCH;
 }
 
+int swiglu_image(int fmt, const float* part, int nslab, int width, int batch, void* img, hipStream_t s) {
+    if (!image_format(fmt)) return RTA_ERR_FORMAT;
+    if (!part || !img) return RTA_ERR_NULL;
+    if (batch <= 0 || batch > kMaxBatchTile || width <= 0 || width % 256 || nslab <= 0) return RTA_ERR_SHAPE;
+    if (!host::aligned(part, 16) || !host::aligned(img, 16)) return RTA_ERR_ALIGN;
+    const int nbt = batch > 16 ? 2 : 1;
+    const dim3 g((width + 1023) / 1024, 16 * nbt), b(256);
+    const bool q4 = (fmt & 0xff) == RTA_Q4_K;
+    if (nbt == 1) {
+        if (q4) hipLaunchKernelGGL((swiglu_image_kernel<RTA_Q4_K, 1>), g, b, 0, s, part, nslab, width, batch,
+                                   static_cast<XImage<1>*>(img));
+        else hipLaunchKernelGGL((swiglu_image_kernel<RTA_Q6_K, 1>), g, b, 0, s, part, nslab, width, batch,
+                                static_cast<XImage<1>*>(img));
+    } else {
+        if (q4) hipLaunchKernelGGL((swiglu_image_kernel<RTA_Q4_K, 2>), g, b, 0, s, part, nslab, width, batch,
+                                   static_cast<XImage<2>*>(img));
+        else hipLaunchKernelGGL((swiglu_image_kernel<RTA_Q6_K, 2>), g, b, 0, s, part, nslab, width, batch,
+                                static_cast<XImage<2>*>(img));
+    }
+    return hipGetLastError() == hipSuccess ? RTA_OK : RTA_ERR_LAUNCH;
+}
+
 template <int FMT, int NBT, int MODE>
 static void launch_packed(const MmaPlan& p, const uint8_t* w, const uint8_t* w2, int rows, int cols, const void* img,
                           int batch, float* y, float* part, const RowNorm& rn, hipStream_t s) {

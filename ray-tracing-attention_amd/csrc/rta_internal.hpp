@@ -105,6 +105,11 @@ size_t image_readout_ws_bytes(int rows, int cols, bool dual);
 int residual_norm_image(int fmt, float* hidden, const float* part, int nslab, const float* w, int batch, int width,
                         float* ss, float* out, void* img, hipStream_t s);
 
+// The SwiGLU of a kSwiglu readout's nslab K-slab partials (left by image_readout with
+// reduce = false) written as the readout image of x = act [batch <= 32, width] for a
+// packed format fmt (the down projection's); width % 256 == 0.
+int swiglu_image(int fmt, const float* part, int nslab, int width, int batch, void* img, hipStream_t s);
+
 // y (=|+=) W x (mode kStore / kAccumulate) or act = swiglu(Wg x, Wu x) (kSwiglu, w2 the up
 // matrix) from the image of x, each result times the row's RMSNorm factor rn.  reduce:
 // K slabs are added into y here; else *nslab > 1 leaves them in ws as [slab][32][rows]

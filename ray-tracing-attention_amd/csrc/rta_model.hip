@@ -156,6 +156,7 @@ size_t gemm_ws_bytes(const rta_hybrid_shape* s, const Dims& d) {
     if (d.nfull) up(image_readout_ws_bytes(d.rows_full, d.D, false));
     if (d.nrec) up(image_readout_ws_bytes(d.rows_rec, d.D, false));
     up(image_readout_ws_bytes(d.FF, d.D, true));
+    up(image_readout_ws_bytes(d.D, d.FF, false));
     if (d.nrec && s->layer_formats) {   // separate a / b readouts behind a layer's pending K slabs
         size_t ab = 0;
         for (int f : {RTA_Q4_K, RTA_Q6_K}) ab = std::max(ab, rta_gemv_workspace_bytes(f, d.H, d.D, d.B));
@@ -191,7 +192,10 @@ Work carve_work(const rta_hybrid_shape* s, const Dims& d, void* p, size_t* bytes
     w.lm_ws = c.take<uint8_t>(std::max<size_t>(w.lm_bytes, 1));
     w.gemm_bytes = gemm_ws_bytes(s, d);
     w.gemm_ws = c.take<uint8_t>(std::max<size_t>(w.gemm_bytes, 1));
-    w.ximg = c.take<uint8_t>(std::max<size_t>(image_bytes(d.D, std::min(d.B, 32)), 1));
+    // x images: in front of the in-projections and gate/up (D columns) and of the down
+    // projection (FF columns), one at a time
+    const int bi = std::min(d.B, 32);
+    w.ximg = c.take<uint8_t>(std::max<size_t>(std::max(image_bytes(d.D, bi), image_bytes(d.FF, bi)), 1));
     if (bytes) *bytes = (c.off + 255) & ~(size_t)255;
     return w;
 }
@@ -446,13 +450,27 @@ int rta_hybrid_decode_step(const rta_hybrid_shape* shape, const rta_hybrid_weigh
         }
         // op 1 index 1, then the SwiGLU MLP with the residual add (executeMLP)
         RTA_TRY(norm(lw.norm_post, fgu, false));
-        if (imaged(fgu))
-            RTA_TRY(image_readout(fgu, kReadSwiglu, lw.w_gate, lw.w_up, d.FF, d.D, w.ximg, B, w.act, true, w.gemm_ws,
-                                  w.gemm_bytes, s, nullptr, rn));
-        else
+        bool down_done = false;
+        if (imaged(fgu)) {
+            // a packed down projection reads the SwiGLU of the gate/up K slabs as its x
+            // image (no fp32 act); it leaves its own K slabs for the next norm
+            const bool down_img = imaged(fd);
+            int ns = 1;
+            RTA_TRY(image_readout(fgu, kReadSwiglu, lw.w_gate, lw.w_up, d.FF, d.D, w.ximg, B, w.act, !down_img,
+                                  w.gemm_ws, w.gemm_bytes, s, &ns, rn));
+            if (down_img && ns > 1) {
+                RTA_TRY(swiglu_image(fd, static_cast<const float*>(w.gemm_ws), ns, d.FF, B, w.ximg, s));
+                int nd = 1;
+                RTA_TRY(image_readout(fd, kReadAccumulate, lw.w_down, nullptr, d.D, d.FF, w.ximg, B, w.hidden, false,
+                                      w.gemm_ws, w.gemm_bytes, s, &nd, RowNorm{}));
+                pending = nd > 1 ? nd : 0;
+                down_done = true;
+            }
+        } else {
             RTA_TRY(swiglu_activation(fgu, lw.w_gate, lw.w_up, d.FF, d.D, xn.w ? w.hidden : w.normed, B, w.act,
                                       w.gemm_ws, w.gemm_bytes, s, rn, xn));
-        RTA_TRY(residual_proj(fd, lw.w_down, d.FF, w.act));
+        }
+        if (!down_done) RTA_TRY(residual_proj(fd, lw.w_down, d.FF, w.act));
     }
     // op 1 index 2, then the readout (Resident::word): logits and the next tokens; the
     // packed LM head takes the row factor itself (never an image: it is read once)

@@ -40,6 +40,55 @@ constexpr int slab_capacity() {
     return (int)(kLdsBytes / sizeof(XImage<NBT>)) < 8 ? (int)(kLdsBytes / sizeof(XImage<NBT>)) : 8;
 }
 
+// Row b of one superblock image from the wave's 64 x 4 values v (lane l: columns 4 l ..
+// 4 l + 3 of the superblock; zeros for a row past the batch, live false): scale, hi / lo
+// planes, group sums and 1 / s, in the layout described at the top of this file.
+template <int FMT, int NBT>
+__device__ __forceinline__ void image_row(XImage<NBT>& im, int b, bool live, float4 v, int lane) {
+    float m = fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
+    for (int off = 32; off > 0; off >>= 1) m = fmaxf(m, __shfl_xor(m, off, kWave));
+    const int e = operand_exponent(m);
+    const float sc = live ? ldexpf(1.0f, 14 - e) : 0.0f;
+    if (lane == 0) im.inv[b] = live ? ldexpf(1.0f, e - 14) : 0.0f;
+    // stored order inside each 8 columns: 0 2 1 3 4 6 5 7, i.e. (x, z, y, w) per float4
+    const float t[4] = {v.x * sc, v.z * sc, v.y * sc, v.w * sc};
+    _Float16 hi[4], lo[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        hi[k] = (_Float16)t[k];
+        lo[k] = (_Float16)(t[k] - (float)hi[k]);
+    }
+    using h4 = _Float16 __attribute__((ext_vector_type(4)));
+    *reinterpret_cast<h4*>(&im.x[0][b][4 * lane]) = h4{hi[0], hi[1], hi[2], hi[3]};
+    *reinterpret_cast<h4*>(&im.x[1][b][4 * lane]) = h4{lo[0], lo[1], lo[2], lo[3]};
+    const float s4 = (t[0] + t[1]) + (t[2] + t[3]);
+    const float s8 = s4 + __shfl_xor(s4, 1, kWave);
+    const float s16 = s8 + __shfl_xor(s8, 2, kWave);
+    _Float16* g = reinterpret_cast<_Float16*>(&im.g[b][0]);   // 4 segments x 8
+    if constexpr (FMT == RTA_Q6_K) {
+        if ((lane & 3) == 0) {   // 16-group u = 8 hh + 2 q + sg -> segment 2 hh + sg, slot 2 q
+            const int u = lane >> 2;
+            const float wv = s16 * (1.0f / 16.0f);
+            const _Float16 h = (_Float16)wv, l = (_Float16)(wv - (float)h);
+            const int seg = 2 * (u >> 3) + (u & 1), q = (u >> 1) & 3;
+            g[8 * seg + 2 * q] = h;
+            g[8 * seg + 2 * q + 1] = l;
+        }
+    } else {
+        const float s32 = s16 + __shfl_xor(s16, 4, kWave);
+        const int q = lane >> 3;   // 32-group: segment q / 2, slots 2 (q % 2), +1; zeros at +4, +5
+        if ((lane & 7) == 0) {
+            const float wv = s32 * (1.0f / 32.0f);
+            const _Float16 h = (_Float16)wv, l = (_Float16)(wv - (float)h);
+            g[8 * (q >> 1) + 2 * (q & 1)] = h;
+            g[8 * (q >> 1) + 2 * (q & 1) + 1] = l;
+        } else if ((lane & 7) == 1) {
+            g[8 * (q >> 1) + 4 + 2 * (q & 1)] = (_Float16)0.0f;
+            g[8 * (q >> 1) + 5 + 2 * (q & 1)] = (_Float16)0.0f;
+        }
+    }
+}
+
 // Block (column chunk c of 1024, row b), 256 threads, thread = 4 columns; wave k of
 // the block = superblock 4c + k.  Rows b >= batch (up to the image's 16 NBT rows) write
 // zeros.  For b < batch: hidden[b] += the K-slab partials [slab][32][width] (slab order)
@@ -88,49 +137,39 @@ __global__ void __launch_bounds__(256) residual_norm_image_kernel(float* __restr
         }
     }
     if (sb >= nsbt) return;   // uniform per wave
-    XImage<NBT>& im = img[sb];
-    float m = fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
-    for (int off = 32; off > 0; off >>= 1) m = fmaxf(m, __shfl_xor(m, off, kWave));
-    const int e = operand_exponent(m);
-    const float sc = live ? ldexpf(1.0f, 14 - e) : 0.0f;
-    if (lane == 0) im.inv[b] = live ? ldexpf(1.0f, e - 14) : 0.0f;
-    // stored order inside each 8 columns: 0 2 1 3 4 6 5 7, i.e. (x, z, y, w) per float4
-    const float t[4] = {v.x * sc, v.z * sc, v.y * sc, v.w * sc};
-    _Float16 hi[4], lo[4];
-#pragma unroll
-    for (int k = 0; k < 4; ++k) {
-        hi[k] = (_Float16)t[k];
-        lo[k] = (_Float16)(t[k] - (float)hi[k]);
-    }
-    using h4 = _Float16 __attribute__((ext_vector_type(4)));
-    *reinterpret_cast<h4*>(&im.x[0][b][4 * lane]) = h4{hi[0], hi[1], hi[2], hi[3]};
-    *reinterpret_cast<h4*>(&im.x[1][b][4 * lane]) = h4{lo[0], lo[1], lo[2], lo[3]};
-    const float s4 = (t[0] + t[1]) + (t[2] + t[3]);
-    const float s8 = s4 + __shfl_xor(s4, 1, kWave);
-    const float s16 = s8 + __shfl_xor(s8, 2, kWave);
-    _Float16* g = reinterpret_cast<_Float16*>(&im.g[b][0]);   // 4 segments x 8
-    if constexpr (FMT == RTA_Q6_K) {
-        if ((lane & 3) == 0) {   // 16-group u = 8 hh + 2 q + sg -> segment 2 hh + sg, slot 2 q
-            const int u = lane >> 2;
-            const float wv = s16 * (1.0f / 16.0f);
-            const _Float16 h = (_Float16)wv, l = (_Float16)(wv - (float)h);
-            const int seg = 2 * (u >> 3) + (u & 1), q = (u >> 1) & 3;
-            g[8 * seg + 2 * q] = h;
-            g[8 * seg + 2 * q + 1] = l;
+    image_row<FMT, NBT>(img[sb], b, live, v, lane);
+}
+
+// The SwiGLU of the gate/up K-slab partials [slab][32][2 rows] (gate at 2 r, up at 2 r + 1,
+// added in slab order as gemm_reduce_kernel adds them) written as the x image of the down
+// projection: block (c, b) as residual_norm_image_kernel, wave k = superblock 4 c + k of
+// row b (zeros past the batch), lane = 4 consecutive columns.
+template <int FMT, int NBT>
+__global__ void __launch_bounds__(256) swiglu_image_kernel(const float* __restrict__ part, int nslab, int width,
+                                                           int batch, XImage<NBT>* __restrict__ img) {
+    const int c = blockIdx.x, b = blockIdx.y, lane = threadIdx.x & 63;
+    const int sb = 4 * c + (threadIdx.x >> 6), nsbt = width >> 8;
+    if (sb >= nsbt) return;   // uniform per wave
+    const bool live = b < batch;   // uniform
+    float4 v = float4{0.0f, 0.0f, 0.0f, 0.0f};
+    if (live) {
+        const int i = c * 256 + threadIdx.x;   // columns 4 i .. 4 i + 3
+        float g[4] = {0.0f, 0.0f, 0.0f, 0.0f}, u[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+        for (int k = 0; k < nslab; ++k) {
+            const float4* p = reinterpret_cast<const float4*>(part + ((int64_t)k * 32 + b) * 2 * width) + 2 * i;
+            const float4 a = p[0], e = p[1];
+            g[0] += a.x;
+            u[0] += a.y;
+            g[1] += a.z;
+            u[1] += a.w;
+            g[2] += e.x;
+            u[2] += e.y;
+            g[3] += e.z;
+            u[3] += e.w;
         }
-    } else {
-        const float s32 = s16 + __shfl_xor(s16, 4, kWave);
-        const int q = lane >> 3;   // 32-group: segment q / 2, slots 2 (q % 2), +1; zeros at +4, +5
-        if ((lane & 7) == 0) {
-            const float wv = s32 * (1.0f / 32.0f);
-            const _Float16 h = (_Float16)wv, l = (_Float16)(wv - (float)h);
-            g[8 * (q >> 1) + 2 * (q & 1)] = h;
-            g[8 * (q >> 1) + 2 * (q & 1) + 1] = l;
-        } else if ((lane & 7) == 1) {
-            g[8 * (q >> 1) + 4 + 2 * (q & 1)] = (_Float16)0.0f;
-            g[8 * (q >> 1) + 5 + 2 * (q & 1)] = (_Float16)0.0f;
-        }
+        v = float4{swiglu(g[0], u[0]), swiglu(g[1], u[1]), swiglu(g[2], u[2]), swiglu(g[3], u[3])};
     }
+    image_row<FMT, NBT>(img[sb], b, live, v, lane);
 }
 
 template <int FMT, int NBT, int MODE, int TPW, int NWAVES, int DEPTH>
