@@ -3,14 +3,14 @@
 python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload NAME] [--batch B] [--no-cpu]
 
 Workloads (one JSON line per run):
-  gemv_q4k    4096x4096 Q4_K dequant-fused GEMV, batch 1, fp32 x            (default)
+  gemv_q4k    4096x4096 Q4_K dequant-fused GEMV, batch 1, fp32 x
   mlp         SwiGLU MLP 2048 -> 6144 -> 2048, gate/up Q4_K, down Q6_K, --batch rows
   lm_head     151936 x 2048 Q6_K vocabulary readout + margin argmax, --batch rows
   attention   GQA decode attention, 16 sequences, contexts log-uniform in [512, 32768],
               16 q / 4 kv heads, hd 128, K Q6_K / V Q4_K history, RoPE theta 1e6 on q
   proj        one projection --rows x --cols in --fmt q4k|q6k for --batch rows
   decode      9B-shape hybrid decode step (24 delta-net + 8 attention layers), --batch sequences
-              (default 32), tokens/s
+              (default 32), tokens/s                                          (default)
   copy_calib  plain device-to-device copy of known size (PMC byte-counter calibration)
 
 A step is one pass of the hot path over one batch of synthetic input resident in
@@ -24,6 +24,8 @@ kernel's mean duration, measured with HIP events recorded on the launching
 stream around a graph of back-to-back launches of that kernel.  For the decode
 step the dominant kernel is the one with the largest share of a step (calls per
 step x mean duration); every timed kernel is listed under "kernels".
+read_ceiling: the achievable HBM read rate (a streaming-read kernel over 1 GiB);
+roofline.frac_of_ceiling = achieved / that rate, beside frac = achieved / 8 TB/s.
 """
 import argparse
 import json
@@ -71,6 +73,46 @@ def traffic_for(key):
     if f.is_file():
         return json.loads(f.read_text()).get(key)
     return None
+
+
+def read_ceiling(torch, n_bytes=1 << 30):
+    """Achievable HBM read rate: the streaming-read kernels of lib/librta_ceiling.so over one
+    1 GiB buffer (4x the 256 MB last-level cache), 20 back-to-back launches between HIP
+    events on one stream, for each variant and a few grid sizes; the best rate is the
+    ceiling."""
+    import ctypes
+    path = ROOT / "ray-tracing-attention_amd" / "lib" / "librta_ceiling.so"
+    if not path.is_file():
+        return None
+    lib = ctypes.CDLL(str(path))
+    lib.rta_ceiling_stream_read.argtypes = [ctypes.c_void_p, ctypes.c_int64, ctypes.c_void_p, ctypes.c_int,
+                                            ctypes.c_int, ctypes.c_void_p]
+    lib.rta_ceiling_stream_read.restype = ctypes.c_int
+    dev = torch.device("cuda:0")
+    buf = torch.empty(n_bytes, dtype=torch.uint8, device=dev).fill_(7)
+    out = torch.empty(65536, dtype=torch.int32, device=dev)
+    s = torch.cuda.current_stream()
+    names = ["4 loads per trip", "8 loads per trip", "4 non-temporal loads", "8 non-temporal loads"]
+    best = (0.0, 0, 0)
+    for variant in range(4):
+        for blocks in (2048, 8192, 32768):
+            def launch():
+                rc = lib.rta_ceiling_stream_read(buf.data_ptr(), n_bytes, out.data_ptr(), blocks, variant,
+                                                 s.cuda_stream)
+                if rc:
+                    raise RuntimeError(f"rta_ceiling_stream_read failed: {rc}")
+            for _ in range(3):
+                launch()
+            a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            a.record(s)
+            for _ in range(20):
+                launch()
+            b.record(s)
+            torch.cuda.synchronize()
+            best = max(best, (n_bytes / (a.elapsed_time(b) / 20 * 1e-3) / 1e9, blocks, variant))
+    del buf
+    return {"kernel": f"stream_read_kernel, {names[best[2]]} (lib/librta_ceiling.so)", "bytes": n_bytes,
+            "gbs": best[0], "frac_of_peak": best[0] / HBM_PEAK_GBS, "blocks": best[1]}
 
 
 def cpu_model():
@@ -722,6 +764,11 @@ def main():
             "alg_bytes_per_launch": alg_k, "alg_bytes_per_step": wl["alg_bytes"], "parity": parity}
     if table:
         line["kernels"] = table
+    ceil = read_ceiling(torch)
+    if ceil:
+        line["read_ceiling"] = ceil
+        line["roofline"]["ceiling"] = ceil["gbs"]
+        line["roofline"]["frac_of_ceiling"] = achieved / ceil["gbs"]
     if args.workload == "decode" and not args.no_companions:
         line["companions"] = companions(torch, args, orc)
     print(json.dumps(line), flush=True)

@@ -15,6 +15,9 @@ LIB = HERE / "lib" / "librta.so"
 # the resident worker (stdin/stdout protocol of the reference's rt_optical_resident)
 WORKER_SRC = "worker/rt_optical_resident.cpp"
 WORKER = HERE / "lib" / "rt_optical_resident"
+# measurement support for the benchmark (the HBM read ceiling), not part of the path
+CEILING_SRC = "csrc/rta_ceiling.hip"
+CEILING = HERE / "lib" / "librta_ceiling.so"
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 
 FLAGS = [
@@ -51,6 +54,15 @@ def build(verbose=False):
     if res.returncode != 0:
         raise RuntimeError(f"hipcc failed on the worker ({res.returncode}):\n{out}")
     os.replace(wtmp, WORKER)
+    ctmp = CEILING.with_suffix(".so.tmp")
+    cmd = [HIPCC, "--offload-arch=gfx950", "-O3", "-std=c++17", "-fPIC", "-shared", "-Xclang", "-target-feature",
+           "-Xclang", "-packed-fp32-ops", "-Wall", str(HERE / CEILING_SRC), "-o", str(ctmp)]
+    if verbose:
+        print(" ".join(cmd), flush=True)
+    res = subprocess.run(cmd, capture_output=True, text=True)
+    if res.returncode != 0:
+        raise RuntimeError(f"hipcc failed on the ceiling probe ({res.returncode}):\n{res.stdout + res.stderr}")
+    os.replace(ctmp, CEILING)
     return LIB
 
 

@@ -119,3 +119,19 @@ def test_argument_errors_are_reported_before_launch(lib):
 def test_missing_library_fails_loudly(tmp_path):
     with pytest.raises(FileNotFoundError):
         _lib.load(tmp_path / "librta.so")
+
+
+def test_read_ceiling_probe_loads_and_checks_arguments():
+    """The benchmark's HBM read-ceiling probe (lib/librta_ceiling.so, not part of the C ABI)
+    exports its one entry point and refuses bad arguments before any launch."""
+    path = Path(_lib.__file__).resolve().parent.parent / "lib" / "librta_ceiling.so"
+    assert path.is_file(), "build() compiles lib/librta_ceiling.so"
+    probe = ctypes.CDLL(str(path))
+    f = probe.rta_ceiling_stream_read
+    f.argtypes = [ctypes.c_void_p, ctypes.c_int64, ctypes.c_void_p, ctypes.c_int, ctypes.c_int, ctypes.c_void_p]
+    f.restype = ctypes.c_int
+    assert f(None, 1024, FAKE, 16, 0, None) == 2        # no buffer
+    assert f(FAKE, 1000, FAKE, 16, 0, None) == 2        # not a multiple of 16 bytes
+    assert f(FAKE_ODD, 1024, FAKE, 16, 0, None) == 2    # misaligned
+    assert f(FAKE, 1024, FAKE, 0, 0, None) == 2         # no blocks
+    assert f(FAKE, 1024, FAKE, 16, 4, None) == 2        # unknown variant
