@@ -500,7 +500,7 @@ static int run_projection(int fmt, const void* w, const void* w2, int rows, int 
 // ---- readouts of a staged x image (rta_packed.hpp), used by the decode step -------
 // Kernel shape: tiles per wave and superblock, waves per workgroup, superblocks of
 // weights in flight per wave.
-constexpr int kPkTpw = 2, kPkWaves = 8, kPkDepth = 3;
+constexpr int kPkTpw = 2, kPkWaves = 8, kPkDepth = 2;
 
 // Work split: units of kPkTpw tiles (kSwiglu: gate and up tiles of the same rows) are
 // shared out to the waves of each K slab in balanced contiguous ranges.  The K range is

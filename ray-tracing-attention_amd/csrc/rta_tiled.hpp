@@ -263,7 +263,7 @@ __global__ void __launch_bounds__(64 * kGemmWaves) gemm_tiled_kernel(
     // up behind the weights), then DEPTH - 1 superblocks of weights, then the x prep.
     XStage<FMT, NBT> xs;
     xs.load(x, cols, batch, sb0, nsb, rn);
-    constexpr int DEPTH = 3;   // two superblocks load while the current one multiplies
+    constexpr int DEPTH = 2;   // one superblock loads while the current one multiplies
     Raw buf[DEPTH][2];
     if (nit > 0) {
 #pragma unroll
