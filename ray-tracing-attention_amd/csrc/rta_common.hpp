@@ -8,6 +8,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <type_traits>
+
 #include "../../include/rta.h"
 
 namespace rta {
@@ -196,6 +198,18 @@ __device__ __forceinline__ float signf(float v) { return v > 0.0f ? 1.0f : (v < 
 __device__ __forceinline__ float swiglu(float g, float u) {
     const float amplitude = fabsf(g) * fabsf(u) * detector_sigmoid(g);
     return signf(g) * signf(u) * amplitude;
+}
+
+// Host: calls f(std::integral_constant<int, NS>{}) with the smallest NS in {1, 2, 4, 8,
+// 16} that covers nslab, or NS = 0 (plain loop) above 16.
+template <class F>
+inline void with_slab_count(int nslab, F&& f) {
+    if (nslab <= 1) f(std::integral_constant<int, 1>{});
+    else if (nslab <= 2) f(std::integral_constant<int, 2>{});
+    else if (nslab <= 4) f(std::integral_constant<int, 4>{});
+    else if (nslab <= 8) f(std::integral_constant<int, 8>{});
+    else if (nslab <= 16) f(std::integral_constant<int, 16>{});
+    else f(std::integral_constant<int, 0>{});
 }
 
 }  // namespace rta

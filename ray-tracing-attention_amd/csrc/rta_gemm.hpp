@@ -491,7 +491,7 @@ __global__ void __launch_bounds__(64 * kGemmWaves) gemm_mfma_kernel(
 // Adds the K-slab partials in slab order and applies the epilogue.  In kSwiglu the
 // virtual rows interleave gate (even) and up (odd).  kLogits also writes per-block
 // maxima pmax[b * gridDim.x + block] for the argmax.
-template <int MODE>
+template <int MODE, int NS>
 __global__ void __launch_bounds__(256) gemm_reduce_kernel(const float* __restrict__ part, int nslab, int rows,
                                                           int batch, float* __restrict__ y, float* __restrict__ pmax) {
     const int total_rows = MODE == kSwiglu ? 2 * rows : rows;
@@ -499,16 +499,37 @@ __global__ void __launch_bounds__(256) gemm_reduce_kernel(const float* __restric
     const int r = blockIdx.x * 256 + threadIdx.x;
     float v = -INFINITY;
     if (r < rows && b < batch) {
+        // every slab's value is loaded before the first add (see add_slabs)
         float s = 0.0f, s2 = 0.0f;
-        for (int k = 0; k < nslab; ++k) {
-            const float* p = part + ((int64_t)k * kMaxBatchTile + b) * total_rows;
-            if constexpr (MODE == kSwiglu) {
-                const float2 gu = *reinterpret_cast<const float2*>(p + 2 * r);
-                s += gu.x;
-                s2 += gu.y;
-            } else {
-                s += p[r];
+        const float* p0 = part + (int64_t)b * total_rows;
+        const int64_t ks = (int64_t)kMaxBatchTile * total_rows;
+        if constexpr (NS == 0) {
+            for (int k = 0; k < nslab; ++k) {
+                if constexpr (MODE == kSwiglu) {
+                    const float2 gu = *reinterpret_cast<const float2*>(p0 + k * ks + 2 * r);
+                    s += gu.x;
+                    s2 += gu.y;
+                } else {
+                    s += p0[k * ks + r];
+                }
             }
+        } else if constexpr (MODE == kSwiglu) {
+            float2 gu[NS];
+#pragma unroll
+            for (int k = 0; k < NS; ++k) gu[k] = *reinterpret_cast<const float2*>(p0 + min(k, nslab - 1) * ks + 2 * r);
+#pragma unroll
+            for (int k = 0; k < NS; ++k)
+                if (k < nslab) {
+                    s += gu[k].x;
+                    s2 += gu[k].y;
+                }
+        } else {
+            float t[NS];
+#pragma unroll
+            for (int k = 0; k < NS; ++k) t[k] = p0[min(k, nslab - 1) * ks + r];
+#pragma unroll
+            for (int k = 0; k < NS; ++k)
+                if (k < nslab) s += t[k];
         }
         float* out = y + (int64_t)b * rows + r;
         if constexpr (MODE == kStore || MODE == kLogits) *out = s;

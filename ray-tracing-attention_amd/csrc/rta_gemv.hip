@@ -367,6 +367,17 @@ static size_t projection_ws(int fmt, int rows, int cols, int batch, bool dual) {
     return a.x_bytes + (a.part_bytes > b.part_bytes ? a.part_bytes : b.part_bytes);
 }
 
+// The fixed-order slab reduce (gemm_reduce_kernel), its loads all in flight at once for
+// up to 16 slabs.
+template <int MODE>
+static void launch_reduce(dim3 grid, const float* part, int nslab, int rows, int batch, float* y, float* pmax,
+                          hipStream_t s) {
+    with_slab_count(nslab, [&](auto ns) {
+        hipLaunchKernelGGL((gemm_reduce_kernel<MODE, decltype(ns)::value>), grid, dim3(256), 0, s, part, nslab, rows,
+                           batch, y, pmax);
+    });
+}
+
 template <int FMT, int NBT, int MODE>
 static void launch_gemm(const MmaPlan& p, const Launch& l, const GemmX& xp, float* part, float* pmax,
                         hipStream_t s) {
@@ -396,8 +407,7 @@ static hipError_t run_mfma(int fmt, const Launch& l, void* ws, float* pmax, int*
     }
     if (p.nslab > 1) {
         const dim3 rg((l.rows + 255) / 256, l.batch);
-        hipLaunchKernelGGL((gemm_reduce_kernel<MODE>), rg, dim3(256), 0, s, part, p.nslab, l.rows, l.batch, l.y,
-                           pmax);
+        launch_reduce<MODE>(rg, part, p.nslab, l.rows, l.batch, l.y, pmax, s);
         if (ntasks_out) *ntasks_out = (int)rg.x;
         if (rpt_out) *rpt_out = 256;
     } else {
@@ -430,8 +440,7 @@ static hipError_t run_tiled(int fmt, const Launch& l, void* ws, float* pmax, int
     }
     if (p.nslab > 1) {
         const dim3 rg((l.rows + 255) / 256, l.batch);
-        hipLaunchKernelGGL((gemm_reduce_kernel<MODE>), rg, dim3(256), 0, s, part, p.nslab, l.rows, l.batch, l.y,
-                           pmax);
+        launch_reduce<MODE>(rg, part, p.nslab, l.rows, l.batch, l.y, pmax, s);
         if (ntasks_out) *ntasks_out = (int)rg.x;
         if (rpt_out) *rpt_out = 256;
     } else {
@@ -619,8 +628,7 @@ static int image_readout_mode(int fmt, const void* w, const void* w2, int rows, 
         else launch_packed<RTA_Q6_K, 2, MODE>(p, a, a2, rows, cols, img, batch, y, part, rn, s);
     }
     if (reduce && p.nslab > 1)
-        hipLaunchKernelGGL((gemm_reduce_kernel<MODE>), dim3((rows + 255) / 256, batch), dim3(256), 0, s, part, p.nslab,
-                           rows, batch, y, nullptr);
+        launch_reduce<MODE>(dim3((rows + 255) / 256, batch), part, p.nslab, rows, batch, y, nullptr, s);
     if (nslab) *nslab = reduce ? 1 : p.nslab;
     return hipGetLastError() == hipSuccess ? RTA_OK : RTA_ERR_LAUNCH;
 }
