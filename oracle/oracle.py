@@ -5,13 +5,15 @@ cpu_baseline leg of bench.py, always as the checker (or the timed CPU baseline),
 never as the product path.
 """
 import ctypes
+import os
 import subprocess
 from pathlib import Path
 
 import numpy as np
 
 HERE = Path(__file__).resolve().parent
-LIB_PATH = HERE / "lib" / "librta_oracle.so"
+# RTA_ORACLE_LIB: another build of the same sources (the sanitizer build of the tests)
+LIB_PATH = Path(os.environ["RTA_ORACLE_LIB"]) if os.environ.get("RTA_ORACLE_LIB") else HERE / "lib" / "librta_oracle.so"
 
 F32, F16, Q4_K, Q6_K, BF16 = 0, 1, 12, 14, 30
 
