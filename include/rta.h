@@ -235,6 +235,25 @@ int rta_decode_attention_noalloc(const float* q, int nseq, int hq, int hkv, int 
                                  int64_t n_slots, int max_ctx, const float* gate, float* out, float* m_out,
                                  float* z_out, rta_stream_t stream);
 
+/* Dense attention receipts, the per-group records the standard backend's attention
+ * writes for the diagnostic (resident_attention_dense.comp:190-300, layout
+ * attention_receipts.hpp:16-29 with compact false; the worker's op 14 returns them,
+ * rt_optical_resident.cpp attention_check).  Same q, packets, slot_base, ctx_len,
+ * capacity, n_slots and max_ctx as rta_decode_attention (rows = nseq).  Row r's
+ * min(ctx_len[r], capacity) newest positions form groups of block positions, newest
+ * first; record (groups of rows < r + g) * hq + h holds hd + 8 + block/32 uint32 words:
+ * m, Z = sum exp(s - m) (fp32 bits), count, exp evaluations, value runs, count, the
+ * traversal count (2 + ceil(count/16) on head 0, else 0), flags 3|4|8, the coverage
+ * bits, then U = sum exp(s - m) v (hd fp32 bits), in the reference's online order.
+ * block: a multiple of 32 in [32, 1024].  receipts holds n_records records
+ * (rta_attention_receipt_records); a record index past it sets RTA_DEVERR_HITS and is
+ * not written; a non-finite value sets RTA_DEVERR_DETECTOR. */
+int64_t rta_attention_receipt_records(const int32_t* ctx_len_host, int rows, int hq, int64_t capacity, int block);
+int rta_attention_receipts(const float* q, int rows, int hq, int hkv, int hd, const void* packets, int fmt_k,
+                           int fmt_v, const int64_t* slot_base, const int32_t* ctx_len, int64_t capacity,
+                           int64_t n_slots, int max_ctx, int block, uint32_t* receipts, int64_t n_records,
+                           rta_stream_t stream);
+
 /* ---------------- the rest of a decoder step (resident_math.comp ops 0, 1, 14, 15,
  * 18-21, 34); every call is stream ordered, allocates nothing, validates on the host. */
 

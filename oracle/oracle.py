@@ -39,6 +39,7 @@ _SIG = {
     "orc_pack_history": (_i, [_p, _p, _i, _i, _i, _p]),
     "orc_packet_value": (_f, [_p, _i, _i, _i, _i, _i]),
     "orc_decode_attention": (_i, [_p, _i, _i, _i, _i, _p, _i, _i, _p, _p, _i64, _p, _p, _p, _p]),
+    "orc_attention_receipts": (_i64, [_p, _i, _i, _i, _i, _p, _i, _i, _p, _p, _i64, _i, _i64, _p, _p, _p]),
     "orc_embed": (_i, [_i, _p, _i, _i, _p, _i, _p]),
     "orc_rmsnorm": (None, [_p, _p, _i, _i, _d, _p]),
     "orc_head_norm": (None, [_p, _i, _p, _p, _i, _i, _i, _i, _i, _d, _p]),
@@ -176,6 +177,25 @@ def decode_attention(q, packets, fmt_k, fmt_v, slot_base, ctx_len, capacity, hkv
                                     _p_(out), _p_(m), _p_(z))
     assert rc == 0, rc
     return out, m, z
+
+
+def attention_receipts(q, packets, fmt_k, fmt_v, slot_base, ctx_len, capacity, hkv, block):
+    """Expected dense receipts: (vals [n, 3 + hd] fp64 = m, Z, count, U; words [n, 8 + block//32]
+    uint32 with words 0 and 1 zero; tie [n] bool, records whose events may differ with the
+    fp32 summation order)."""
+    q = _c(q, np.float32)
+    rows, hq, hd = q.shape
+    ctx = _c(ctx_len, np.int32)
+    act = np.minimum(np.maximum(ctx.astype(np.int64), 0), capacity)
+    n = int(((act + block - 1) // block).sum()) * hq
+    vals = np.zeros((max(n, 1), 3 + hd), dtype=np.float64)
+    words = np.zeros((max(n, 1), 8 + block // 32), dtype=np.uint32)
+    tie = np.zeros(max(n, 1), dtype=np.uint8)
+    got = lib().orc_attention_receipts(_p_(q), rows, hq, hkv, hd, _p_(_c(packets, np.uint8)), fmt_k, fmt_v,
+                                       _p_(_c(slot_base, np.int64)), _p_(ctx), int(capacity), block, max(n, 1),
+                                       _p_(vals), _p_(words), _p_(tie))
+    assert got == n, (got, n)
+    return vals[:n], words[:n], tie[:n].astype(bool)
 
 
 # ---- the rest of a decoder step ----

@@ -465,6 +465,126 @@ int orc_decode_attention(const float* q, int nseq, int hq, int hkv, int hd,
     return 0;
 }
 
+/* ---- dense attention receipts --------------------------------------------
+ * Events (words 3, 4, 7) follow fusedAttention's online pass (resident_attention_dense.comp:
+ * 206-292): fp32 scores q.k / sqrt(hd), tiles of 4 positions raise the running maximum
+ * (one exp for the rescale when it moves and Z > 0), a weight is reused when the score
+ * and maximum repeat bit for bit, bit-equal consecutive value vectors form one run.
+ * Word 6 is traceGroup's count (resident_attention_dense.comp:108-126): two lens faces
+ * and one history ray per 16 positions, on head 0.  m, Z, U are the fp64 two-pass sums of
+ * verify_attention_receipts.py:117-139 over fp64 scores. */
+int64_t orc_attention_receipts(const float* q, int rows, int hq, int hkv, int hd, const uint8_t* packets, int fmt_k,
+                               int fmt_v, const int64_t* slot_base, const int32_t* ctx_len, int64_t capacity,
+                               int block, int64_t n_records, double* vals, uint32_t* words, uint8_t* tie) {
+    if (!q || !packets || !slot_base || !ctx_len || !vals || !words || !tie) return -1;
+    if (rows <= 0 || hq <= 0 || hkv <= 0 || hd <= 0 || hq % hkv || capacity <= 0 || block <= 0 || block % 32)
+        return -1;
+    const int kvw = hkv * hd, group = hq / hkv, cov = block / 32, nw = 8 + cov;
+    const int64_t stride = orc_history_bytes(kvw), padded = (kvw + 255) / 256 * 256;
+    float* kf = (float*)malloc(sizeof(float) * (size_t)padded * (size_t)block);
+    float* vf = (float*)malloc(sizeof(float) * (size_t)padded * (size_t)block);
+    float* sc = (float*)malloc(sizeof(float) * (size_t)block);
+    double* sd = (double*)malloc(sizeof(double) * (size_t)block);
+    if (!kf || !vf || !sc || !sd) { free(kf); free(vf); free(sc); free(sd); return -1; }
+    int64_t rec = 0;
+    for (int r = 0; r < rows; ++r) {
+        const int64_t L = ctx_len[r], active = L <= 0 ? 0 : (L < capacity ? L : capacity);
+        for (int64_t g = 0; g * block < active; ++g) {
+            const int count = (int)(active - g * block < block ? active - g * block : block);
+            for (int j = 0; j < count; ++j) {
+                const int64_t p = L - 1 - (g * block + j);
+                const uint8_t* pk = packets + (slot_base[r] + p % capacity) * stride;
+                decode_field(pk, kvw, fmt_k, fmt_v, 0, kf + (size_t)j * padded);
+                decode_field(pk, kvw, fmt_k, fmt_v, 1, vf + (size_t)j * padded);
+            }
+            for (int h = 0; h < hq; ++h, ++rec) {
+                if (rec >= n_records) { free(kf); free(vf); free(sc); free(sd); return -1; }
+                const int kvh = h / group;
+                const float* qh = q + ((int64_t)r * hq + h) * hd;
+                for (int j = 0; j < count; ++j) {
+                    float total = 0.0f;
+                    double exact = 0.0;
+                    for (int c = 0; c < hd; ++c) {
+                        float prod = qh[c] * kf[(size_t)j * padded + kvh * hd + c];
+                        total += prod;
+                        exact += (double)qh[c] * (double)kf[(size_t)j * padded + kvh * hd + c];
+                    }
+                    sc[j] = total / sqrtf((float)hd);
+                    sd[j] = exact / sqrt((double)hd);
+                }
+                /* the online events */
+                float maximum = -INFINITY, reference = 0.0f, prev_w = 0.0f;
+                uint32_t prev_score = 0, prev_max = 0, exps = 0, runs = 0;
+                int have_prev = 0, reused = 0, pending = 0, near = 0, prev_run = -1;
+                for (int t0 = 0; t0 < count; t0 += 4) {
+                    const int n = count - t0 < 4 ? count - t0 : 4;
+                    float local = -INFINITY;
+                    for (int j = 0; j < n; ++j) local = fmaxf(local, sc[t0 + j]);
+                    const float next = fmaxf(maximum, local);
+                    float scale = 0.0f;
+                    if (isfinite(maximum) && next != maximum && fabsf(next - maximum) <= 1e-5f * fmaxf(1.0f, fabsf(next))) near = 1;
+                    if (isfinite(maximum) && local < maximum && maximum - local <= 1e-5f * fmaxf(1.0f, fabsf(maximum))) near = 1;
+                    uint32_t nb, mb; memcpy(&nb, &next, 4); memcpy(&mb, &maximum, 4);
+                    if (reference > 0.0f) {
+                        if (nb == mb) scale = 1.0f;
+                        else { scale = expf(maximum - next); ++exps; }
+                    }
+                    reference *= scale;
+                    maximum = next;
+                    for (int j = 0; j < n; ++j) {
+                        const float s = sc[t0 + j];
+                        uint32_t sb; memcpy(&sb, &s, 4); memcpy(&mb, &maximum, 4);
+                        float w;
+                        if (have_prev && sb == prev_score && mb == prev_max) { w = prev_w; reused = 1; }
+                        else {
+                            float ps; memcpy(&ps, &prev_score, 4);
+                            if (have_prev && sb != prev_score && fabsf(s - ps) <= 1e-5f * fmaxf(1.0f, fabsf(s))) near = 1;
+                            w = expf(s - maximum); ++exps;
+                        }
+                        prev_score = sb; prev_max = mb; prev_w = w; have_prev = 1;
+                        reference += w;
+                        const float* v = vf + (size_t)(t0 + j) * padded + kvh * hd;
+                        int same = pending;
+                        if (same) {
+                            const float* pv = vf + (size_t)prev_run * padded + kvh * hd;
+                            same = memcmp(v, pv, sizeof(float) * (size_t)hd) == 0;
+                        }
+                        if (!same) {
+                            if (pending) ++runs;
+                            prev_run = t0 + j;
+                            pending = 1;
+                        }
+                    }
+                }
+                if (pending) ++runs;
+                /* the expected sums (two-pass, fp64) */
+                double* o = vals + rec * (3 + hd);
+                double mx = -INFINITY, z = 0.0;
+                for (int j = 0; j < count; ++j) if (sd[j] > mx) mx = sd[j];
+                for (int c = 0; c < hd; ++c) o[3 + c] = 0.0;
+                for (int j = 0; j < count; ++j) {
+                    const double w = exp(sd[j] - mx);
+                    z += w;
+                    for (int c = 0; c < hd; ++c) o[3 + c] += w * (double)vf[(size_t)j * padded + kvh * hd + c];
+                }
+                o[0] = mx; o[1] = z; o[2] = count;
+                uint32_t* wd = words + rec * nw;
+                wd[0] = wd[1] = 0u;
+                wd[2] = (uint32_t)count; wd[3] = exps; wd[4] = runs; wd[5] = (uint32_t)count;
+                wd[6] = h == 0 ? 2u + (uint32_t)(count + 15) / 16u : 0u;
+                wd[7] = 3u | (reused ? 4u : 0u) | (runs < (uint32_t)count ? 8u : 0u);
+                for (int k = 0; k < cov; ++k) {
+                    const int n = k * 32 < count ? (count - k * 32 < 32 ? count - k * 32 : 32) : 0;
+                    wd[8 + k] = n == 32 ? 0xFFFFFFFFu : n == 0 ? 0u : (1u << n) - 1u;
+                }
+                tie[rec] = (uint8_t)near;
+            }
+        }
+    }
+    free(kf); free(vf); free(sc); free(sd);
+    return rec;
+}
+
 /* ---- the rest of a decoder step ---- */
 
 /* resident_math.comp:30-32 (op 0): the embedding row, decoded like every weight. */

@@ -109,6 +109,18 @@ int orc_decode_attention(const float* q, int nseq, int hq, int hkv, int hd,
                          int64_t capacity, const float* gate,
                          double* out, double* m, double* z);
 
+/* Dense attention receipts (resident_attention_dense.comp:190-300): for each record
+ * (row, group, head) in the order (groups of rows < r + g) * hq + h, vals[rec] =
+ * {m, Z, count, U[0..hd)} in fp64 from the two-pass sums over fp64 scores that verify_attention_receipts.py:
+ * 117-139 expects, words[rec] = the integer words 2..7 and the coverage bits (words 0
+ * and 1 left 0), tie[rec] = 1 where an fp32 score lies within 1e-5 of the running
+ * maximum or of its neighbour without being bit-equal (events 3, 4, 7 may then differ
+ * with the summation order).  Returns the record count, or -1 on a bad argument or when
+ * more than n_records are needed. */
+int64_t orc_attention_receipts(const float* q, int rows, int hq, int hkv, int hd, const uint8_t* packets, int fmt_k,
+                               int fmt_v, const int64_t* slot_base, const int32_t* ctx_len, int64_t capacity,
+                               int block, int64_t n_records, double* vals, uint32_t* words, uint8_t* tie);
+
 /* ---- the rest of a decoder step (resident_math.comp ops 0, 1, 14, 15, 18-21) ----
  * Test infrastructure: restatements in fp64 (fp32 inputs, fp32 embedding values). */
 

@@ -2407,6 +2407,181 @@ static int scratch_address(void** out) {
     return RTA_OK;
 }
 
+
+// ------------------------------------------------------------ dense receipts ----
+// The standard backend's per-group attention records (resident_attention_dense.comp:
+// 190-300 fusedAttention and storeHead, 118-126 the traversal count; layout
+// attention_receipts.hpp:16-29, compact false).  Row r's history is its min(L, capacity)
+// newest positions (L = ctx_len[r]); group g covers the ages [g block, g block + count)
+// below its newest position, newest first.  Record (prefix(r) + g) hq + h, where
+// prefix(r) sums the groups of the rows before r, holds hd + 8 + block / 32 words:
+//   0 m, the group's maximum score q.k / sqrt(hd)      1 Z = sum exp(s - m)
+//   2 count   3 exp evaluations   4 value runs   5 count
+//   6 on head 0 the traversal count 2 + ceil(count / 16) that the reference's receipt
+//     tracer reports for a group (two lens faces, one history ray per 16 positions), a
+//     function of count alone; 0 on the other heads
+//   7 flags: 3 (scores and values complete) | 4 (a weight was reused) | 8 (runs < count)
+//   8 .. 8 + block / 32 the coverage bits (every position of the group is present)
+//   then U_d = sum exp(s - m) v_d, d < hd.
+// m, Z and U follow the reference's online order: tiles of four positions raise the
+// running maximum (rescaling Z and U by exp(old - new) when it moves), a weight is reused
+// when score and maximum repeat bit for bit, and consecutive bit-equal value vectors are
+// summed as one run (weight sum times the vector), so words 3, 4 and 7 count the same
+// events.  Block (head, group, row) of 256 threads: the four waves score the group's
+// positions into LDS, then wave 0 runs the ordered pass with two axes per lane.
+constexpr int kMaxReceiptBlock = 1024;
+constexpr int kReceiptTile = 4;
+
+__global__ void __launch_bounds__(256) attn_receipt_kernel(const float* __restrict__ q, int hq, int hkv,
+                                                           const uint8_t* __restrict__ packets, int fmt_k, int fmt_v,
+                                                           int64_t stride, int64_t v_offset,
+                                                           const int64_t* __restrict__ slot_base,
+                                                           const int32_t* __restrict__ ctx_len, int64_t capacity,
+                                                           int64_t n_slots, int block, uint32_t* __restrict__ rec,
+                                                           int64_t n_records) {
+#pragma clang fp contract(off)
+    __shared__ float s_q[kHd];
+    __shared__ float s_score[kMaxReceiptBlock];
+    __shared__ int64_t s_slot[kMaxReceiptBlock];
+    __shared__ int s_bad;
+    const int h = blockIdx.x, g = blockIdx.y, r = blockIdx.z, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int64_t L = ctx_len[r];
+    const int64_t active = L <= 0 ? 0 : (L < capacity ? L : capacity);
+    if ((int64_t)g * block >= active) return;   // uniform: this row has fewer groups
+    int64_t prefix = 0;
+    for (int rr = 0; rr < r; ++rr) {
+        const int64_t l = ctx_len[rr], a = l <= 0 ? 0 : (l < capacity ? l : capacity);
+        prefix += (a + block - 1) / block;
+    }
+    const int64_t record = (prefix + g) * hq + h;
+    if (record >= n_records) {
+        if (tid == 0) raise_error(RTA_DEVERR_HITS);
+        return;
+    }
+    const int count = (int)(active - (int64_t)g * block < block ? active - (int64_t)g * block : block);
+    const int kv = h / (hq / hkv);
+    if (tid == 0) s_bad = 0;
+    if (tid < kHd) s_q[tid] = q[((int64_t)r * hq + h) * kHd + tid];
+    __syncthreads();
+    for (int j = tid; j < count; j += 256) {
+        const int64_t p = L - 1 - ((int64_t)g * block + j);
+        const int64_t slot = slot_base[r] + p % capacity;
+        const bool bad = slot < 0 || slot >= n_slots;
+        if (bad) s_bad = 1;
+        s_slot[j] = bad ? 0 : slot;
+    }
+    __syncthreads();
+    if (s_bad) {
+        if (tid == 0) raise_error(RTA_DEVERR_HITS);
+        return;
+    }
+    // Scores: a wave per position, lane holds axes lane and lane + 64.
+    const float qa = s_q[lane], qb = s_q[lane + 64];
+    const bool q_ok = isfinite(qa) && isfinite(qb);
+    bool finite = q_ok;
+    const int64_t kbase = (int64_t)kv * kHd;
+    for (int j = wave; j < count; j += 4) {
+        const uint8_t* kf = packets + s_slot[j] * stride;
+        const float ka = dequant_value(fmt_k, kf, kbase + lane), kb = dequant_value(fmt_k, kf, kbase + lane + 64);
+        finite &= isfinite(ka) && isfinite(kb);
+        const float pa = qa * ka, pb = qb * kb;
+        float t = pa + pb;
+        for (int off = 32; off > 0; off >>= 1) t += __shfl_xor(t, off, kWave);
+        const float score = t / sqrtf((float)kHd);
+        finite &= isfinite(score);
+        if (lane == 0) s_score[j] = score;
+    }
+    if (!finite) raise_error(RTA_DEVERR_DETECTOR);
+    __syncthreads();
+    if (wave != 0) return;
+    float maximum = -INFINITY, reference = 0.0f, pending_w = 0.0f, prev_w = 0.0f;
+    float sig_a = 0.0f, sig_b = 0.0f, pv_a = 0.0f, pv_b = 0.0f;
+    uint32_t prev_score = 0u, prev_max = 0u, exps = 0u, runs = 0u;
+    bool pending = false, have_prev = false, reused = false, vfinite = true;
+    for (int t0 = 0; t0 < count; t0 += kReceiptTile) {
+        const int n = count - t0 < kReceiptTile ? count - t0 : kReceiptTile;
+        float local = -INFINITY;
+        for (int j = 0; j < n; ++j) local = fmaxf(local, s_score[t0 + j]);
+        const float next = fmaxf(maximum, local);
+        float scale = 0.0f;
+        if (reference > 0.0f) {
+            if (__float_as_uint(next) == __float_as_uint(maximum)) {
+                scale = 1.0f;
+            } else {
+                scale = expf(maximum - next);
+                ++exps;
+            }
+        }
+        reference *= scale;
+        pending_w *= scale;
+        sig_a *= scale;
+        sig_b *= scale;
+        maximum = next;
+        for (int j = 0; j < n; ++j) {
+            const float score = s_score[t0 + j];
+            float w;
+            if (have_prev && __float_as_uint(score) == prev_score && __float_as_uint(maximum) == prev_max) {
+                w = prev_w;
+                reused = true;
+            } else {
+                w = expf(score - maximum);
+                ++exps;
+            }
+            prev_score = __float_as_uint(score);
+            prev_max = __float_as_uint(maximum);
+            prev_w = w;
+            have_prev = true;
+            reference += w;
+            const uint8_t* vf = packets + s_slot[t0 + j] * stride + v_offset;
+            const float va = dequant_value(fmt_v, vf, kbase + lane), vb = dequant_value(fmt_v, vf, kbase + lane + 64);
+            vfinite &= isfinite(va) && isfinite(vb);
+            const bool same = pending && __float_as_uint(va) == __float_as_uint(pv_a) &&
+                              __float_as_uint(vb) == __float_as_uint(pv_b);
+            if (__all(same)) {
+                pending_w += w;
+            } else {
+                if (pending) {
+                    const float ca = pending_w * pv_a, cb = pending_w * pv_b;
+                    sig_a += ca;
+                    sig_b += cb;
+                    ++runs;
+                }
+                pv_a = va;
+                pv_b = vb;
+                pending_w = w;
+                pending = true;
+            }
+        }
+    }
+    if (pending) {
+        const float ca = pending_w * pv_a, cb = pending_w * pv_b;
+        sig_a += ca;
+        sig_b += cb;
+        ++runs;
+    }
+    if (!vfinite || !isfinite(reference) || !(reference > 0.0f) || !isfinite(maximum) || !isfinite(sig_a) ||
+        !isfinite(sig_b))
+        raise_error(RTA_DEVERR_DETECTOR);
+    uint32_t* out = rec + record * (int64_t)(kHd + 8 + block / 32);
+    const int cov = block / 32;
+    out[8 + cov + lane] = __float_as_uint(sig_a);
+    out[8 + cov + lane + 64] = __float_as_uint(sig_b);
+    for (int w = lane; w < cov; w += 64) {
+        const int first = 32 * w, nb = first < count ? (count - first < 32 ? count - first : 32) : 0;
+        out[8 + w] = nb == 32 ? 0xFFFFFFFFu : nb == 0 ? 0u : (1u << nb) - 1u;
+    }
+    if (lane == 0) {
+        out[0] = __float_as_uint(maximum);
+        out[1] = __float_as_uint(reference);
+        out[2] = (uint32_t)count;
+        out[3] = exps;
+        out[4] = runs;
+        out[5] = (uint32_t)count;
+        out[6] = h == 0 ? 2u + (uint32_t)(count + 15) / 16u : 0u;
+        out[7] = 3u | (reused ? 4u : 0u) | (runs < (uint32_t)count ? 8u : 0u);
+    }
+}
+
 }  // namespace rta
 
 using namespace rta;
@@ -2440,6 +2615,43 @@ size_t rta_decode_attention_workspace_bytes(int nseq, int hq, int hkv, int hd, i
     if (nseq <= 0 || hq <= 0 || hkv <= 0 || hd != kHd || max_ctx <= 0 || hq % hkv) return 0;
     return attn_record_bytes(nseq, hq, max_ctx) + (size_t)nseq * hkv * 6 * kWave * sizeof(uint4) +
            (((size_t)nseq + 1 + kMaxWg) * sizeof(int32_t) + 15) / 16 * 16;
+}
+
+int64_t rta_attention_receipt_records(const int32_t* ctx_len_host, int rows, int hq, int64_t capacity, int block) {
+    if (!ctx_len_host || rows <= 0 || hq <= 0 || capacity <= 0 || block <= 0) return -1;
+    int64_t n = 0;
+    for (int r = 0; r < rows; ++r) {
+        const int64_t L = ctx_len_host[r], active = L < capacity ? L : capacity;
+        if (active > 0) n += (active + block - 1) / block;
+    }
+    return n * hq;
+}
+
+int rta_attention_receipts(const float* q, int rows, int hq, int hkv, int hd, const void* packets, int fmt_k,
+                           int fmt_v, const int64_t* slot_base, const int32_t* ctx_len, int64_t capacity,
+                           int64_t n_slots, int max_ctx, int block, uint32_t* receipts, int64_t n_records,
+                           rta_stream_t stream) {
+    if (!q || !packets || !slot_base || !ctx_len || !receipts) return RTA_ERR_NULL;
+    if (rows <= 0 || hq <= 0 || hkv <= 0 || hq % hkv || capacity <= 0 || n_slots <= 0 || max_ctx <= 0 ||
+        n_records <= 0)
+        return RTA_ERR_SHAPE;
+    if ((fmt_k != RTA_Q4_K && fmt_k != RTA_Q6_K) || (fmt_v != RTA_Q4_K && fmt_v != RTA_Q6_K) ||
+        (fmt_k == RTA_Q6_K && fmt_v == RTA_Q6_K))
+        return RTA_ERR_FORMAT;
+    if (hd != kHd || block < 32 || block % 32 || block > kMaxReceiptBlock) return RTA_ERR_RANGE;
+    if (!host::aligned(q, 4) || !host::aligned(slot_base, 8) || !host::aligned(ctx_len, 4) ||
+        !host::aligned(receipts, 4))
+        return RTA_ERR_ALIGN;
+    const int64_t lim = (int64_t)max_ctx < capacity ? max_ctx : capacity;
+    const int64_t groups = (lim + block - 1) / block;
+    if (groups > 65535 || rows > 65535) return RTA_ERR_RANGE;
+    const int nkv2 = (hkv * kHd + 255) / 256;
+    const int64_t stride = host::history_bytes(hkv * kHd);
+    const int64_t v_offset = (int64_t)nkv2 * (fmt_k == RTA_Q4_K ? 144 : 210);
+    hipLaunchKernelGGL(attn_receipt_kernel, dim3(hq, (unsigned)groups, rows), dim3(256), 0, (hipStream_t)stream, q,
+                       hq, hkv, static_cast<const uint8_t*>(packets), fmt_k, fmt_v, stride, v_offset, slot_base,
+                       ctx_len, capacity, n_slots, block, receipts, n_records);
+    return hipGetLastError() == hipSuccess ? RTA_OK : RTA_ERR_LAUNCH;
 }
 
 int rta_decode_attention(const float* q, int nseq, int hq, int hkv, int hd, const void* packets, int fmt_k, int fmt_v,

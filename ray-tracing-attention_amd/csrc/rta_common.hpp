@@ -161,13 +161,18 @@ __device__ __forceinline__ float dequant_value(int fmt, const uint8_t* __restric
     if (fmt == RTA_F16) return (float)reinterpret_cast<const _Float16*>(src)[i];
     if (fmt == RTA_BF16) return __builtin_bit_cast(float, (uint32_t)reinterpret_cast<const uint16_t*>(src)[i] << 16);
     if (fmt == RTA_Q4_K) {
+        // A Q4_K field that follows a Q6_K field in a history packet starts 2 bytes past
+        // a word boundary (210-byte blocks), so the header is read in 16-bit halves: a
+        // 32-bit read there, when the address is wave-uniform, may be served by a scalar
+        // load, which drops the low address bits.
         const uint8_t* b = src + (i >> 8) * 144;
+        const uint16_t* hw = reinterpret_cast<const uint16_t*>(b);
         const int idx = (int)(i & 255), g = idx >> 5;
-        const float d = (float)*reinterpret_cast<const _Float16*>(b);
-        const float dmin = (float)*reinterpret_cast<const _Float16*>(b + 2);
+        const float d = (float)__builtin_bit_cast(_Float16, hw[0]);
+        const float dmin = (float)__builtin_bit_cast(_Float16, hw[1]);
         uint32_t sc, m;
-        const uint32_t* s = reinterpret_cast<const uint32_t*>(b + 4);
-        q4k_scale_min(s[0], s[1], s[2], g, sc, m);
+        q4k_scale_min(hw[2] | (uint32_t)hw[3] << 16, hw[4] | (uint32_t)hw[5] << 16, hw[6] | (uint32_t)hw[7] << 16, g,
+                      sc, m);
         const uint32_t q = (b[16 + (idx >> 6) * 32 + (idx & 31)] >> (((idx & 63) >> 5) * 4)) & 15u;
         const float ds = d * (float)sc;
         const float dq = ds * (float)q;

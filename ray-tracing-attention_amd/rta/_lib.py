@@ -72,6 +72,8 @@ SIGNATURES = {
                                   _p]),
     "rta_decode_attention_noalloc": (_i, [_p, _i, _i, _i, _i, _p, _i, _i, _p, _p, _i64, _i64, _i, _p, _p, _p, _p,
                                           _p]),
+    "rta_attention_receipt_records": (_i64, [_p, _i, _i, _i64, _i]),
+    "rta_attention_receipts": (_i, [_p, _i, _i, _i, _i, _p, _i, _i, _p, _p, _i64, _i64, _i, _i, _p, _i64, _p]),
     # host-only asset reader (rta.asset binds the structs)
     "rta_asset_open": (_i, [ctypes.c_char_p, ctypes.c_char_p, ctypes.POINTER(_p), ctypes.c_char_p, _sz]),
     "rta_asset_close": (None, [_p]),

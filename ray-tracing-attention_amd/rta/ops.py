@@ -250,6 +250,33 @@ def decode_attention_noalloc(q, packets, fmt_k, fmt_v, slot_base, ctx_len, capac
     return out, m, z
 
 
+def attention_receipt_records(ctx_len, hq, capacity, block):
+    """Number of dense receipt records for host context lengths ctx_len (a sequence)."""
+    lens = (ctypes.c_int32 * len(ctx_len))(*[int(x) for x in ctx_len])
+    n = int(_lib.load().rta_attention_receipt_records(lens, len(ctx_len), hq, capacity, block))
+    if n < 0:
+        raise ValueError("rta_attention_receipt_records: bad arguments")
+    return n
+
+
+def attention_receipts(q, packets, fmt_k, fmt_v, slot_base, ctx_len, capacity, max_ctx, hkv, block, n_records=None):
+    """Dense per-group attention receipts (rta_attention_receipts): uint32 tensor
+    [n_records, hd + 8 + block // 32] on q's device.  n_records defaults to the count
+    for ctx_len's values (read back to the host)."""
+    lib = _lib.load()
+    for t, n in ((q, "q"), (packets, "packets"), (slot_base, "slot_base"), (ctx_len, "ctx_len")):
+        _dev(t, n)
+    rows, hq, hd = q.shape
+    if n_records is None:
+        n_records = attention_receipt_records(ctx_len.cpu().tolist(), hq, capacity, block)
+    out = torch.zeros(max(n_records, 1), hd + 8 + block // 32, dtype=torch.int32, device=q.device)
+    n_slots = packets.numel() // history_bytes(hkv * hd)
+    check(lib.rta_attention_receipts(_ptr(q), rows, hq, hkv, hd, _ptr(packets), fmt_k, fmt_v, _ptr(slot_base),
+                                     _ptr(ctx_len), capacity, n_slots, max_ctx, block, _ptr(out), max(n_records, 1),
+                                     _stream()), "rta_attention_receipts")
+    return out[:n_records]
+
+
 def device_error(clear=True):
     """Sticky device error bits (RTA_DEVERR_*); synchronises the device."""
     bits = ctypes.c_uint32(0)

@@ -454,7 +454,7 @@ struct Worker {
     uint32_t control[8] = {0, 0, 1, 0, 0xffffffffu, 0xffffffffu, 0, 0};   // (resident_math.comp:130)
     uint64_t position = 0;                            // absolute position (emitted tokens count)
     std::map<int, std::unique_ptr<Device>> uploads;   // (layer, index) -> device payload
-    Device ws, x, act, y, logits, ids, rows, q, kbuf, vbuf, gate, out, m, z, packets, slots, ctx;
+    Device ws, x, act, y, logits, ids, rows, q, kbuf, vbuf, gate, out, m, z, packets, slots, ctx, rec;
 
     ~Worker() {
         if (asset) rta_asset_close(asset);
@@ -606,7 +606,7 @@ struct Worker {
     // op 14: pack the supplied K/V rows into history packets, then each query row r
     // attends causally to positions history_start .. query_start + r (all within
     // capacity); standard backend, dense receipts (resident_attention_runtime.inl:646-,
-    // attention_receipts.hpp:16-29).
+    // attention_receipts.hpp:16-29) written by rta_attention_receipts.
     void attention_check(uint32_t nrows, uint32_t layer) {
         uint32_t hdr[4];
         std::cin.read(reinterpret_cast<char*>(hdr), sizeof(hdr));
@@ -672,6 +672,15 @@ struct Worker {
                                        z.as<float>(), ws.p, wsb, stream),
                   "rta_decode_attention");
         const double fused = t.stop(stream);
+        // the per-group records of the same attention (index 1: every row has records)
+        const uint32_t stride = hd + 8 + block / 32;
+        const int64_t records = rta_attention_receipt_records(lens.data(), (int)nrows, (int)heads, capacity, (int)block);
+        if (records <= 0 || records > 0xFFFFFFFFll) throw std::runtime_error("Attention receipt count out of range");
+        rec.ensure((size_t)records * stride * 4);
+        rta_check(rta_attention_receipts(q.as<float>(), (int)nrows, (int)heads, (int)kv_heads, (int)hd, packets.p,
+                                         RTA_Q4_K, RTA_Q6_K, base_d.as<int64_t>(), ctx.as<int32_t>(), capacity, capacity,
+                                         max_ctx, (int)block, rec.as<uint32_t>(), records, stream),
+                  "rta_attention_receipts");
         uint32_t bits = 0;
         rta_check(rta_device_error(&bits, 1), "rta_device_error");
         std::vector<float> o_h(qs.size()), m_h((size_t)nrows * heads), z_h((size_t)nrows * heads);
@@ -685,13 +694,6 @@ struct Worker {
             phys[2 * i] = m_h[i] + 20.0f;   // the reported intensity m + 20 (resident_ray.comp:74)
             phys[2 * i + 1] = z_h[i];
         }
-        const uint32_t stride = hd + 8 + block / 32;
-        uint64_t records = 0;
-        for (uint32_t r = 0; r < nrows; ++r) {
-            const uint32_t active = std::min(qstart - hstart + r + 1, capacity);
-            records += (active + block - 1) / block;
-        }
-        records *= heads;
         const uint32_t legacy = hstart == 0 ? 1u : 0u;
         std::vector<char> o;
         const uint32_t header[12] = {0x41545231u, nrows, count, heads, kv_heads, hd, (uint32_t)pb,
@@ -710,8 +712,8 @@ struct Worker {
             append(o, zeros);
         }
         append(o, pk);
-        // receipts record ray-traversal evidence; no rays are traced here, so they are zero
-        const std::vector<uint32_t> receipts((size_t)records * stride, 0u);
+        std::vector<uint32_t> receipts((size_t)records * stride);
+        hip_check(hipMemcpy(receipts.data(), rec.p, receipts.size() * 4, hipMemcpyDeviceToHost), "read receipts");
         append(o, receipts);
         reply(o);
     }

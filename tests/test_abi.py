@@ -114,6 +114,17 @@ def test_argument_errors_are_reported_before_launch(lib):
     args[18] = 1 << 30
     args[11] = 0
     assert lib.rta_decode_attention(*args) == E["shape"]           # n_slots <= 0
+    # dense receipts: host refusals, and the record count of ragged rows
+    R = lambda **k: lib.rta_attention_receipts(
+        k.get("q", FAKE), 2, k.get("hq", 8), 2, k.get("hd", 128), FAKE, _lib.Q4_K, k.get("fv", _lib.Q6_K), FAKE,
+        FAKE, 300, 600, 300, k.get("block", 128), k.get("rec", FAKE), k.get("n", 64), None)
+    assert R(q=None) == E["null"] and R(hq=7) == E["shape"] and R(n=0) == E["shape"]
+    assert R(fv=_lib.F32) == E["format"] and R(hd=64) == E["range"]
+    assert R(block=96 + 1) == E["range"] and R(block=2048) == E["range"] and R(block=16) == E["range"]
+    assert R(rec=FAKE_ODD) == E["align"]
+    lens = (ctypes.c_int32 * 5)(1, 128, 129, 400, 0)
+    assert lib.rta_attention_receipt_records(lens, 5, 8, 300, 128) == 8 * (1 + 1 + 2 + 3 + 0)
+    assert lib.rta_attention_receipt_records(lens, 5, 8, 300, 0) == -1
 
 
 def test_missing_library_fails_loudly(tmp_path):

@@ -12,6 +12,7 @@ import pytest
 
 import asset_writer as aw
 import oracle as orc
+from receipt_check import compare as compare_receipts
 from conftest import tolerance_ok
 from resident_client import Worker
 from rta import synth
@@ -128,6 +129,10 @@ def test_attention_check(served, rows, count, hstart, gap):
         np.testing.assert_array_equal(r["legacy_output"], r["output"])
     else:
         assert not r["legacy_output"].any()
+    # dense receipts (attention_receipts.hpp:16-29) against the oracle's records
+    vals, words, tie = orc.attention_receipts(q, packets, orc.Q4_K, orc.Q6_K, np.zeros(rows, np.int64), ctx,
+                                              CAPACITY, kvh, block)
+    compare_receipts(r["receipts"], vals, words, tie, block, hd, "worker receipts")
 
 
 def test_resources(served):

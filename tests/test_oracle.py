@@ -443,3 +443,86 @@ def test_delta_rule_rank_one_closed_form():
     assert np.allclose(o[0], want, rtol=1e-12, atol=1e-13)
     wrong = (lam * a * (b @ q) + beta * (v - a * (b @ k)) * (k @ q)) / np.sqrt(hd)   # predict before decay
     assert not np.allclose(o[0], wrong, rtol=1e-6)
+
+
+# --------------------------------------------------------- dense receipts ----
+from receipt_check import bounds, merge, rows_heads   # noqa: E402
+
+
+def _receipts(q, packets, base, ctx, cap, hkv, block, fmts=(orc.Q4_K, orc.Q6_K)):
+    return orc.attention_receipts(q, packets, fmts[0], fmts[1], np.asarray(base, np.int64),
+                                  np.asarray(ctx, np.int32), cap, hkv, block)
+
+
+@pytest.mark.parametrize("fmts", [(orc.Q4_K, orc.Q6_K), (orc.Q6_K, orc.Q4_K)])
+def test_receipts_merge_to_attention(fmts):
+    """The records of each (row, head), merged as the reference's checker merges them
+    (max, rescaled Z and U), give the whole-history attention of decode_attention."""
+    rng = np.random.default_rng(40)
+    hq, hkv, hd, cap, block = 4, 2, 128, 70, 32
+    ctx = [1, 31, 32, 33, 70, 95]
+    base = [0, 100, 200, 300, 400, 500]
+    packets = _history(rng, 600, hkv, hd, *fmts)
+    q = rng.standard_normal((len(ctx), hq, hd)).astype(np.float32)
+    vals, words, tie = _receipts(q, packets, base, ctx, cap, hkv, block, fmts)
+    index = rows_heads(ctx, cap, block, hq)
+    assert len(vals) == len(index) == hq * sum((min(c, cap) + block - 1) // block for c in ctx)
+    out, M, Z = merge(vals[:, 0], vals[:, 1], vals[:, 3:], index, len(ctx), hq)
+    ref, m, z = orc.decode_attention(q, packets, fmts[0], fmts[1], base, ctx, cap, hkv)
+    np.testing.assert_allclose(out, ref, rtol=1e-10, atol=1e-12)
+    np.testing.assert_allclose(M, m, rtol=1e-12, atol=1e-12)
+    np.testing.assert_allclose(Z, z, rtol=1e-10)
+    bounds(words, index, block)
+    assert not tie.all()
+
+
+def test_receipts_groups_are_newest_first():
+    """A group of one position holds exactly that position's (score, 1, V): the record of
+    group g at block 32 for a history of 64 positions covers ages 32 g .. 32 g + 31."""
+    rng = np.random.default_rng(41)
+    hq, hkv, hd = 2, 1, 128
+    packets = _history(rng, 65, hkv, hd, orc.Q4_K, orc.Q6_K)
+    q = rng.standard_normal((1, hq, hd)).astype(np.float32)
+    vals, words, _ = _receipts(q, packets, [0], [65], 1 << 20, hkv, 32)
+    assert len(vals) == 3 * hq
+    # the last group holds age 64 alone: position 0
+    ref, m, z = orc.decode_attention(q, packets[:1], orc.Q4_K, orc.Q6_K, [0], [1], 1 << 20, hkv)
+    for h in range(hq):
+        np.testing.assert_allclose(vals[2 * hq + h, 3:], ref[0, h], rtol=1e-12)
+        assert vals[2 * hq + h, 1] == 1.0 and words[2 * hq + h, 2] == 1
+    # the first group: positions 64 .. 33 (newest first)
+    ring = np.empty((32, packets.shape[1]), np.uint8)
+    for p in range(33, 65):
+        ring[p % 32] = packets[p]
+    ref, m, z = orc.decode_attention(q, ring, orc.Q4_K, orc.Q6_K, [0], [65], 32, hkv)
+    np.testing.assert_allclose(vals[:hq, 3:] / vals[:hq, 1:2], ref[0], rtol=1e-10, atol=1e-12)
+
+
+def test_receipts_event_closed_forms():
+    rng = np.random.default_rng(42)
+    hq, hkv, hd, count = 1, 1, 128, 29
+    one = _history(rng, 1, hkv, hd, orc.Q4_K, orc.Q6_K)
+    q = rng.standard_normal((1, hq, hd)).astype(np.float32)
+    # identical packets: one exp (every later weight reused), one value run
+    _, words, tie = _receipts(q, np.repeat(one, count, 0), [0], [count], 1 << 20, hkv, 32)
+    assert list(words[0, 2:8]) == [count, 1, 1, count, 2 + 2, 3 | 4 | 8] and not tie[0]
+    # keys alpha_a * ones with alpha rising with age: each tile of four raises the running
+    # maximum, so every weight and every later tile's rescale costs an exp (the reference
+    # checker's upper bound count + ceil(count / 4) - 1); distinct values: count runs
+    e = np.ones((1, hd), np.float32)
+    k = [np.float32(1.0 + 0.25 * a) * e for a in range(count)][::-1]          # position p = count-1-age
+    v = [rng.standard_normal((1, hd)).astype(np.float32) for _ in range(count)]
+    pk = np.stack([orc.pack_history(k[p], v[p]) for p in range(count)])
+    qe = np.ones((1, hq, hd), np.float32)
+    vals, words, tie = _receipts(qe, pk, [0], [count], 1 << 20, hkv, 32)
+    assert not tie[0]
+    assert list(words[0, 2:8]) == [count, count + (count + 3) // 4 - 1, count, count, 4, 3]
+    # keys falling with age: the first tile sets the maximum for good, no rescales
+    pk2 = np.stack([orc.pack_history(k[count - 1 - p], v[p]) for p in range(count)])
+    _, words, tie = _receipts(qe, pk2, [0], [count], 1 << 20, hkv, 32)
+    assert not tie[0] and words[0, 3] == count
+    # values repeating in runs of three along the ages: ceil(count / 3) runs
+    vr = [v[(count - 1 - p) // 3] for p in range(count)]
+    pk3 = np.stack([orc.pack_history(k[p], vr[p]) for p in range(count)])
+    _, words, _ = _receipts(qe, pk3, [0], [count], 1 << 20, hkv, 32)
+    assert words[0, 4] == (count + 2) // 3 and words[0, 7] & 8
