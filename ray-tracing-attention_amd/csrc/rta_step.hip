@@ -401,6 +401,10 @@ __global__ void __launch_bounds__(64 * NW) recurrent_mix_kernel(
     float2 s[kRows];
 #pragma unroll
     for (int i = 0; i < kRows; ++i) s[i] = S[i * (hd / 2)];
+    // the updated state is stored non-temporally: it is read again only by the next
+    // step, after every other layer's weights have passed through the caches
+    using f2v = float __attribute__((ext_vector_type(2)));
+    f2v* Sv = reinterpret_cast<f2v*>(S);
 
     float y[3] = {0.0f, 0.0f, 0.0f};
     if (conv) {
@@ -468,7 +472,7 @@ __global__ void __launch_bounds__(64 * NW) recurrent_mix_kernel(
         const float delta = bt * (vv[i] - u[i]);
         s[i].x += delta * k.x;
         s[i].y += delta * k.y;
-        S[i * (hd / 2)] = s[i];
+        __builtin_nontemporal_store(f2v{s[i].x, s[i].y}, Sv + i * (hd / 2));
         o[i] = s[i].x * q.x + s[i].y * q.y;
     }
 #pragma unroll
