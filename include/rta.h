@@ -247,7 +247,8 @@ int rta_decode_attention_noalloc(const float* q, int nseq, int hq, int hkv, int 
  * bits, then U = sum exp(s - m) v (hd fp32 bits), in the reference's online order.
  * block: a multiple of 32 in [32, 1024].  receipts holds n_records records
  * (rta_attention_receipt_records); a record index past it sets RTA_DEVERR_HITS and is
- * not written; a non-finite value sets RTA_DEVERR_DETECTOR. */
+ * not written; a row with min(ctx_len, capacity) above max_ctx sets it too (that row's
+ * records are incomplete); a non-finite value sets RTA_DEVERR_DETECTOR. */
 int64_t rta_attention_receipt_records(const int32_t* ctx_len_host, int rows, int hq, int64_t capacity, int block);
 int rta_attention_receipts(const float* q, int rows, int hq, int hkv, int hd, const void* packets, int fmt_k,
                            int fmt_v, const int64_t* slot_base, const int32_t* ctx_len, int64_t capacity,

@@ -2448,6 +2448,11 @@ __global__ void __launch_bounds__(256) attn_receipt_kernel(const float* __restri
     const int64_t L = ctx_len[r];
     const int64_t active = L <= 0 ? 0 : (L < capacity ? L : capacity);
     if ((int64_t)g * block >= active) return;   // uniform: this row has fewer groups
+    // a row with more groups than the grid holds (max_ctx below its length) is refused
+    if (g == (int)gridDim.y - 1 && (int64_t)gridDim.y * block < active) {
+        if (tid == 0) raise_error(RTA_DEVERR_HITS);
+        return;
+    }
     int64_t prefix = 0;
     for (int rr = 0; rr < r; ++rr) {
         const int64_t l = ctx_len[rr], a = l <= 0 ? 0 : (l < capacity ? l : capacity);

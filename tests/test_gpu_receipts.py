@@ -122,6 +122,12 @@ def test_receipts_error_paths(torch_dev):
                            hkv, block)
     torch.cuda.synchronize()
     assert ops.device_error() & 8
+    # max_ctx below a row's length: that row's records are refused, the error bit set
+    ops.device_error(clear=True)
+    ops.attention_receipts(t(q), t(packets), orc.Q4_K, orc.Q6_K, t(np.zeros(2, np.int64)), ctx, cap, 32, hkv,
+                           block, n_records=need)
+    torch.cuda.synchronize()
+    assert ops.device_error() & 8
     # host refusals: nothing launched
     lib = _lib.load()
     buf = torch.zeros(need * (hd + 8 + block // 32), dtype=torch.int32, device=dev)
