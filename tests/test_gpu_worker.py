@@ -135,6 +135,34 @@ def test_attention_check(served, rows, count, hstart, gap):
     compare_receipts(r["receipts"], vals, words, tie, block, hd, "worker receipts")
 
 
+@pytest.mark.parametrize("block", [256, 512])
+def test_attention_check_receipt_blocks(served, tmp_path, block):
+    """The dense receipts at the worker's other attention blocks (RT_ATTENTION_BLOCK)."""
+    _, spec, _ = served
+    d = tmp_path / "asset"
+    d.mkdir()
+    rng = np.random.default_rng(12)
+    sp = copy.deepcopy(aw.SMALL_SPEC)
+    packed, floats = aw.random_model(rng, sp, lambda fmt, r, c: synth.random_matrix(rng, fmt, r, c))
+    aw.write(d, sp, packed, floats)
+    w = Worker(EXE, d, CAPACITY, env=dict(os.environ, RT_ATTENTION_BLOCK=str(block)))
+    heads, kvh, hd = sp["attention_heads"], sp["kv_heads"], sp["attention_head_dim"]
+    rows, count, hstart = 5, 290, 3
+    qstart = hstart + count - rows
+    q = rng.standard_normal((rows, heads, hd)).astype(np.float32)
+    k = rng.standard_normal((count, kvh, hd)).astype(np.float32)
+    v = rng.standard_normal((count, kvh, hd)).astype(np.float32)
+    print(f"worker: attention receipts block {block} rows {rows} count {count}", flush=True)
+    r = w.attention(q, k, v, None, sp["layer_types"].index("full"), qstart, hstart, heads, kvh, hd)
+    assert w.close() == 0, w.error_text()
+    assert r["error"] == 0 and r["block"] == block and r["stride"] == hd + 8 + block // 32
+    packets = np.stack([orc.pack_history(k[i], v[i]) for i in range(count)])
+    ctx = np.array([qstart - hstart + i + 1 for i in range(rows)], np.int32)
+    vals, words, tie = orc.attention_receipts(q, packets, orc.Q4_K, orc.Q6_K, np.zeros(rows, np.int64), ctx,
+                                              CAPACITY, kvh, block)
+    compare_receipts(r["receipts"], vals, words, tie, block, hd, f"worker receipts block {block}")
+
+
 def test_resources(served):
     w, _, _ = served
     v = w.resources()
