@@ -3,8 +3,8 @@ oracle's records: the standard backend's per-group (m, Z, U) and counters
 (resident_attention_dense.comp:190-300; layout attention_receipts.hpp:16-29).
 
 Cases: wrapped rings with several rows of ragged lengths (a single position, exact
-multiples of the block, one past, longer than the capacity), blocks 32 / 128 / 256 /
-512, both packet layouts and GQA ratios 1 / 4 / 8; histories of identical packets
+multiples of the block, one past, longer than the capacity), blocks 32 / 64 / 96 /
+128 / 256 / 512, both packet layouts, GQA ratios 1 / 2 / 4 / 8 and odd kv-head counts 3 and 5; histories of identical packets
 (every weight but the first reused, one value run); the error paths (too few records,
 a slot outside the packet array, arguments the host refuses).
 
@@ -46,6 +46,8 @@ CASES = [  # hq, hkv, capacity, block, ctx lengths
     (4, 4, 96, 32, [96, 97, 31]),
     (32, 8, 1024, 256, [1000, 257, 1, 4096]),
     (8, 1, 600, 512, [513, 600, 1200]),
+    (6, 3, 200, 64, [64, 65, 199, 450]),      # odd kv heads: packets with a padded superblock
+    (10, 5, 160, 96, [96, 97, 2, 161]),       # block not a power of two
 ]
 
 
