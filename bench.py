@@ -488,7 +488,7 @@ def w_proj(torch, args, orc):
 
 def step_kernels(torch, shape, batch, dev, packed):
     """The decode step's readouts and its attention as separate calls of the C ABI, at the
-    step's shapes, each over enough distinct (rotated) weight copies that every call
+    step's shapes (packed readouts as the step runs them: from the x image, K slabs left), each over enough distinct (rotated) weight copies that every call
     streams its weights from HBM, on the weight layout the step runs (packed tiles read by
     the matrix-core readout, or GGUF rows read by the vector-ALU one).  Returns [(name,
     calls per step, alg bytes, launch)]."""
@@ -524,22 +524,59 @@ def step_kernels(torch, shape, batch, dev, packed):
     rin = copies(Q4_K, 4 * S + 2 * shape.rec_heads, D)
     fin = copies(Q4_K, (hq + 2 * hkv) * hd, D)
     out = []
-    out.append((f"gate/up: {kern}<Q4_K,SwiGLU> (rta_swiglu, {lay} 2 x 12288x4096)", shape.layers,
-                2 * qb(Q4_K, FF, D) + 4 * batch * (D + FF),
-                lambda i: ops.swiglu(P4, gu[i % len(gu)][0], gu[i % len(gu)][1], D, FF, x_d, act=act, workspace=ws)))
-    out.append((f"down: {kern}<Q4_K,accumulate> + slab reduce (rta_gemv, {lay} 4096x12288)", shape.layers,
-                qb(Q4_K, D, FF) + 4 * batch * (FF + 2 * D),
-                lambda i: ops.gemv(P4, dn[i % len(dn)][0], D, FF, x_ff, y=y_d, accumulate=True, workspace=ws)))
+    if packed:
+        # the step's own readout kernel: gemm_packed_kernel over the x image (built once,
+        # outside the timed launches), K slabs left for the next kernel of the step
+        img_d, _ = ops.image_from_rows(P4, x_d)
+        ws_img = torch.empty(max(ops.image_readout_workspace_bytes(FF, D, True),
+                                 ops.image_readout_workspace_bytes(4 * S + 2 * shape.rec_heads, D, False),
+                                 ops.image_readout_workspace_bytes((hq + 2 * hkv) * hd, D, False)),
+                             dtype=torch.uint8, device=dev)
+        out.append(("gate/up: gemm_packed_kernel<Q4_K,SwiGLU> from the x image, K slabs left (rta_image_readout, "
+                    "packed 2 x 12288x4096)", shape.layers, 2 * qb(Q4_K, FF, D) + 4 * batch * (D + FF),
+                    lambda i: ops.image_readout(P4, ops.IMAGE_SWIGLU, gu[i % len(gu)][0], gu[i % len(gu)][1], FF, D,
+                                                img_d, batch, act, reduce=False, workspace=ws_img)))
+    else:
+        out.append((f"gate/up: {kern}<Q4_K,SwiGLU> (rta_swiglu, {lay} 2 x 12288x4096)", shape.layers,
+                    2 * qb(Q4_K, FF, D) + 4 * batch * (D + FF),
+                    lambda i: ops.swiglu(P4, gu[i % len(gu)][0], gu[i % len(gu)][1], D, FF, x_d, act=act,
+                                         workspace=ws)))
+    ns_gu = 0
+    if packed:   # the down projection's x image as the step builds it: SwiGLU of the gate/up slabs
+        ws_gu = torch.empty(ops.image_readout_workspace_bytes(FF, D, True), dtype=torch.uint8, device=dev)
+        ns_gu = ops.image_readout(P4, ops.IMAGE_SWIGLU, gu[0][0], gu[0][1], FF, D, img_d, batch, act,
+                                  reduce=False, workspace=ws_gu)
+    if ns_gu > 1:
+        img_ff = ops.image_from_swiglu(P4, ws_gu.view(torch.float32), ns_gu, FF, batch)
+        ws_dn = torch.empty(ops.image_readout_workspace_bytes(D, FF, False), dtype=torch.uint8, device=dev)
+        out.append(("down: gemm_packed_kernel<Q4_K,accumulate> from the SwiGLU image, K slabs left "
+                    "(rta_image_readout, packed 4096x12288)", shape.layers, qb(Q4_K, D, FF) + 4 * batch * (FF + 2 * D),
+                    lambda i: ops.image_readout(P4, 1, dn[i % len(dn)][0], None, D, FF, img_ff, batch, y_d,
+                                                reduce=False, workspace=ws_dn)))
+    else:
+        out.append((f"down: {kern}<Q4_K,accumulate> + slab reduce (rta_gemv, {lay} 4096x12288)", shape.layers,
+                    qb(Q4_K, D, FF) + 4 * batch * (FF + 2 * D),
+                    lambda i: ops.gemv(P4, dn[i % len(dn)][0], D, FF, x_ff, y=y_d, accumulate=True, workspace=ws)))
     out.append((f"O projection: {kern}<Q4_K,accumulate> + slab reduce (rta_gemv, {lay} 4096x4096)",
                 shape.layers, qb(Q4_K, D, hq * hd) + 4 * batch * (hq * hd + 2 * D),
                 lambda i: ops.gemv(P4, op[i % len(op)][0], D, hq * hd, x_d, y=y_d, accumulate=True, workspace=ws)))
-    out.append((f"recurrent in-projection: {kern}<Q4_K,store> + slab reduce (rta_gemv, {lay} 16448x4096)",
-                nrec, qb(Q4_K, 4 * S + 2 * shape.rec_heads, D) + 4 * batch * (D + 4 * S + 2 * shape.rec_heads),
-                lambda i: ops.gemv(P4, rin[i % len(rin)][0], 4 * S + 2 * shape.rec_heads, D, x_d, y=y_in,
-                                   workspace=ws)))
-    out.append((f"full in-projection: {kern}<Q4_K,store> + slab reduce (rta_gemv, {lay} 6144x4096)", nfull,
-                qb(Q4_K, (hq + 2 * hkv) * hd, D) + 4 * batch * (D + (hq + 2 * hkv) * hd),
-                lambda i: ops.gemv(P4, fin[i % len(fin)][0], (hq + 2 * hkv) * hd, D, x_d, y=y_full, workspace=ws)))
+    rw, fw = 4 * S + 2 * shape.rec_heads, (hq + 2 * hkv) * hd
+    if packed:
+        out.append(("recurrent in-projection: gemm_packed_kernel<Q4_K,store> from the x image, K slabs left "
+                    "(rta_image_readout, packed 16448x4096)", nrec, qb(Q4_K, rw, D) + 4 * batch * (D + rw),
+                    lambda i: ops.image_readout(P4, 0, rin[i % len(rin)][0], None, rw, D, img_d, batch, y_in,
+                                                reduce=False, workspace=ws_img)))
+        out.append(("full in-projection: gemm_packed_kernel<Q4_K,store> from the x image, K slabs left "
+                    "(rta_image_readout, packed 6144x4096)", nfull, qb(Q4_K, fw, D) + 4 * batch * (D + fw),
+                    lambda i: ops.image_readout(P4, 0, fin[i % len(fin)][0], None, fw, D, img_d, batch, y_full,
+                                                reduce=False, workspace=ws_img)))
+    else:
+        out.append((f"recurrent in-projection: {kern}<Q4_K,store> (rta_gemv, {lay} 16448x4096)", nrec,
+                    qb(Q4_K, rw, D) + 4 * batch * (D + rw),
+                    lambda i: ops.gemv(P4, rin[i % len(rin)][0], rw, D, x_d, y=y_in, workspace=ws)))
+        out.append((f"full in-projection: {kern}<Q4_K,store> (rta_gemv, {lay} 6144x4096)", nfull,
+                    qb(Q4_K, fw, D) + 4 * batch * (D + fw),
+                    lambda i: ops.gemv(P4, fin[i % len(fin)][0], fw, D, x_d, y=y_full, workspace=ws)))
     return out
 
 

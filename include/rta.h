@@ -162,6 +162,36 @@ int rta_mlp_swiglu(int fmt_g, const void* wg, int fmt_u, const void* wu,
 int rta_swiglu(int fmt, const void* wg, const void* wu, int hidden, int inter, const float* x, int batch,
                float* act, void* workspace, size_t workspace_bytes, rta_stream_t stream);
 
+/* The decode step's readout path for packed matrices at batch <= 32, split in its two
+ * stages (rta_hybrid_decode_step runs them inside the step; these expose them alone):
+ *  - rta_image_from_rows: img = the matrix-core image of x * w (x [batch, cols] fp32,
+ *    w [cols]; cols % 256 == 0, cols <= 4096) for packed format fmt (RTA_Q4_K | RTA_TILED
+ *    or RTA_Q6_K | RTA_TILED): per (row, 256-column superblock) a power-of-two scale,
+ *    binary16 hi and lo planes and group sums; ss [4 * batch] receives the rows' chunk sums
+ *    of x^2.  img holds rta_image_bytes(cols, batch) bytes, 256-byte aligned.
+ *  - rta_image_readout: y (=|+=) W x (mode RTA_EPI_STORE / RTA_EPI_ACCUMULATE) or, mode
+ *    RTA_IMAGE_SWIGLU, y = act of (W = wg, w2 = wu) as rta_swiglu, from img; with ss the
+ *    results take the RMSNorm factor 1 / sqrt(sum(ss of the row) / cols + eps) (x * w then
+ *    reads as rmsnorm(x) * w).  reduce != 0 adds the K slabs into y; reduce == 0 leaves
+ *    *nslab > 1 slabs in the workspace as [slab][32][rows] (SwiGLU: gate and up interleaved,
+ *    2 rows each) and writes y only when *nslab == 1.  Workspace:
+ *    rta_image_readout_workspace_bytes(rows, cols, dual = mode is SwiGLU).
+ * Replace op 1 + op 2 (resident_math.comp:33-38,39-75) as Resident::layer runs them for
+ * a batch of rows (optical_resident.cpp:455-491). */
+#define RTA_IMAGE_SWIGLU 2
+size_t rta_image_bytes(int cols, int batch);
+/* The image of act = swiglu(g, u) from the nslab K slabs a RTA_IMAGE_SWIGLU readout left
+ * with reduce == 0 (part = its workspace; width = its rows), slabs added in slab order:
+ * the x image of the down projection, as the decode step builds it. */
+int rta_image_from_swiglu(int fmt, const float* part, int nslab, int width, int batch, void* img,
+                          rta_stream_t stream);
+size_t rta_image_readout_workspace_bytes(int rows, int cols, int dual);
+int rta_image_from_rows(int fmt, const float* x, const float* w, int batch, int cols, float* ss, void* img,
+                        rta_stream_t stream);
+int rta_image_readout(int fmt, int mode, const void* w, const void* w2, int rows, int cols, const void* img,
+                      int batch, const float* ss, float eps, float* y, int reduce, void* workspace,
+                      size_t workspace_bytes, int* nslab, rta_stream_t stream);
+
 /* LM-head vocabulary readout with fused argmax.
  *   logits[b, v] = sum_k W[v, k] h[b, k]   (fp32, all v < vocab)
  *   ids[b] = lowest v with logits[b, v] >= M - margin*|M|, M = max_v logits[b, v]

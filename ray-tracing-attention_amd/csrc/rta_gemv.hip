@@ -1026,4 +1026,40 @@ int rta_pack_remap(int fmt, const void* src, int src_rows, int cols, const rta_r
     return pack_rows(fmt, src, rows, cols, m, dst, (hipStream_t)stream);
 }
 
+size_t rta_image_bytes(int cols, int batch) { return image_bytes(cols, batch); }
+
+size_t rta_image_readout_workspace_bytes(int rows, int cols, int dual) {
+    if (rows <= 0 || cols <= 0 || cols % 256) return 0;
+    return image_readout_ws_bytes(rows, cols, dual != 0);
+}
+
+int rta_image_from_rows(int fmt, const float* x, const float* w, int batch, int cols, float* ss, void* img,
+                        rta_stream_t stream) {
+    if (!x || !w || !ss || !img) return RTA_ERR_NULL;
+    // with no slabs the kernel reads x and never writes it
+    return residual_norm_image(fmt, const_cast<float*>(x), nullptr, 0, w, batch, cols, ss, nullptr, img,
+                               (hipStream_t)stream);
+}
+
+int rta_image_from_swiglu(int fmt, const float* part, int nslab, int width, int batch, void* img,
+                          rta_stream_t stream) {
+    if (!part || !img) return RTA_ERR_NULL;
+    if (nslab <= 0 || image_bytes(width, batch) == 0) return RTA_ERR_SHAPE;
+    if (!host::aligned(part, 16) || !host::aligned(img, 16)) return RTA_ERR_ALIGN;
+    return swiglu_image(fmt, part, nslab, width, batch, img, (hipStream_t)stream);
+}
+
+int rta_image_readout(int fmt, int mode, const void* w, const void* w2, int rows, int cols, const void* img,
+                      int batch, const float* ss, float eps, float* y, int reduce, void* workspace,
+                      size_t workspace_bytes, int* nslab, rta_stream_t stream) {
+    if (mode != RTA_EPI_STORE && mode != RTA_EPI_ACCUMULATE && mode != RTA_IMAGE_SWIGLU) return RTA_ERR_RANGE;
+    if (ss && !host::aligned(ss, 16)) return RTA_ERR_ALIGN;
+    if (image_bytes(cols, batch) == 0) return RTA_ERR_SHAPE;
+    RowNorm rn;
+    if (ss) rn = RowNorm{reinterpret_cast<const float4*>(ss), (float)cols, eps};
+    const int m = mode == RTA_EPI_STORE ? kReadStore : mode == RTA_EPI_ACCUMULATE ? kReadAccumulate : kReadSwiglu;
+    return image_readout(fmt, m, w, w2, rows, cols, img, batch, y, reduce != 0, workspace, workspace_bytes,
+                         (hipStream_t)stream, nslab, rn);
+}
+
 }  // extern "C"

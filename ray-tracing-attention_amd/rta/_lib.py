@@ -72,6 +72,11 @@ SIGNATURES = {
                                   _p]),
     "rta_decode_attention_noalloc": (_i, [_p, _i, _i, _i, _i, _p, _i, _i, _p, _p, _i64, _i64, _i, _p, _p, _p, _p,
                                           _p]),
+    "rta_image_bytes": (_sz, [_i, _i]),
+    "rta_image_readout_workspace_bytes": (_sz, [_i, _i, _i]),
+    "rta_image_from_swiglu": (_i, [_i, _p, _i, _i, _i, _p, _p]),
+    "rta_image_from_rows": (_i, [_i, _p, _p, _i, _i, _p, _p, _p]),
+    "rta_image_readout": (_i, [_i, _i, _p, _p, _i, _i, _p, _i, _p, _f, _p, _i, _p, _sz, ctypes.POINTER(_i), _p]),
     "rta_attention_receipt_records": (_i64, [_p, _i, _i, _i64, _i]),
     "rta_attention_receipts": (_i, [_p, _i, _i, _i, _i, _p, _i, _i, _p, _p, _i64, _i64, _i, _i, _p, _i64, _p]),
     # host-only asset reader (rta.asset binds the structs)

@@ -173,6 +173,57 @@ def swiglu(fmt, wg, wu, hidden, inter, x, act=None, workspace=None):
     return act
 
 
+IMAGE_SWIGLU = 2
+
+
+def image_readout_workspace_bytes(rows, cols, dual):
+    return int(_lib.load().rta_image_readout_workspace_bytes(rows, cols, 1 if dual else 0))
+
+
+def image_from_rows(fmt, x, w=None):
+    """(img, ss): the matrix-core image of x * w [batch <= 32, cols] for packed format fmt
+    and the rows' chunk sums of x^2 (rta_image_from_rows); w defaults to ones."""
+    lib = _lib.load()
+    _dev(x, "x")
+    batch, cols = x.shape
+    if w is None:
+        w = torch.ones(cols, dtype=torch.float32, device=x.device)
+    n = int(lib.rta_image_bytes(cols, batch))
+    if n == 0:
+        raise ValueError("rta_image_bytes: unsupported shape")
+    img = torch.empty(n, dtype=torch.uint8, device=x.device)
+    ss = torch.empty(4 * batch, dtype=torch.float32, device=x.device)
+    check(lib.rta_image_from_rows(fmt, _ptr(x), _ptr(w), batch, cols, _ptr(ss), _ptr(img), _stream()),
+          "rta_image_from_rows")
+    return img, ss
+
+
+def image_from_swiglu(fmt, part, nslab, width, batch):
+    """The down projection's x image from a SwiGLU image readout's K slabs (part: that
+    readout's workspace) (rta_image_from_swiglu)."""
+    lib = _lib.load()
+    n = int(lib.rta_image_bytes(width, batch))
+    if n == 0:
+        raise ValueError("rta_image_bytes: unsupported shape")
+    img = torch.empty(n, dtype=torch.uint8, device=part.device)
+    check(lib.rta_image_from_swiglu(fmt, _ptr(part), nslab, width, batch, _ptr(img), _stream()),
+          "rta_image_from_swiglu")
+    return img
+
+
+def image_readout(fmt, mode, w, w2, rows, cols, img, batch, y, ss=None, eps=1e-6, reduce=True, workspace=None):
+    """rta_image_readout into y [batch, rows]; returns the K-slab count left in the
+    workspace (1 when the slabs were added into y)."""
+    lib = _lib.load()
+    need = image_readout_workspace_bytes(rows, cols, mode == IMAGE_SWIGLU)
+    ws = _workspace(need, img.device, workspace)
+    ns = ctypes.c_int(0)
+    check(lib.rta_image_readout(fmt, mode, _ptr(w), _ptr(w2), rows, cols, _ptr(img), batch, _ptr(ss), eps, _ptr(y),
+                                1 if reduce else 0, _ptr(ws), ws.numel(), ctypes.byref(ns), _stream()),
+          "rta_image_readout")
+    return ns.value
+
+
 def lm_head_workspace_bytes(fmt, vocab, hidden, batch):
     return int(_lib.load().rta_lm_head_workspace_bytes(fmt, vocab, hidden, batch))
 

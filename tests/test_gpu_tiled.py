@@ -194,3 +194,69 @@ def test_swiglu_stage_alone(torch_dev, packed, batch):
     for b in range(batch):
         assert_close(act[b], ract[b], f"activation row {b}")
 
+
+
+@pytest.mark.parametrize("fmt", [orc.Q4_K, orc.Q6_K])
+@pytest.mark.parametrize("batch", [1, 5, 17, 32])
+def test_image_readout_matches_oracle(torch_dev, fmt, batch):
+    """rta_image_from_rows + rta_image_readout (the decode step's readout path) in every
+    mode, with the RMSNorm factor, against the oracle on rmsnorm(x) * w."""
+    torch, dev = torch_dev
+    rng = np.random.default_rng(900 + 7 * batch + fmt)
+    rows, cols, P = 300, 1024, fmt | TILED
+    print(f"image readout: fmt {fmt} batch {batch} rows {rows} cols {cols}", flush=True)
+    wg, wu = synth.random_matrix(rng, fmt, rows, cols), synth.random_matrix(rng, fmt, rows, cols)
+    x = rng.standard_normal((batch, cols)).astype(np.float32)
+    nw = (1.0 + 0.1 * rng.standard_normal(cols)).astype(np.float32)
+    pg = ops.pack(fmt, to_dev(torch, wg, dev), rows, cols)
+    pu = ops.pack(fmt, to_dev(torch, wu, dev), rows, cols)
+    img, ss = ops.image_from_rows(P, to_dev(torch, x, dev), to_dev(torch, nw, dev))
+    x64 = x.astype(np.float64)
+    xn = (x64 / np.sqrt((x64 * x64).mean(1, keepdims=True) + 1e-6) * nw).astype(np.float32)
+    g, u = orc.gemv_f64(fmt, wg, rows, cols, xn), orc.gemv_f64(fmt, wu, rows, cols, xn)
+    y = torch.zeros(batch, rows, device=dev)
+    assert ops.image_readout(P, 0, pg, None, rows, cols, img, batch, y, ss=ss) == 1
+    assert_close(y.cpu().numpy(), g, "store")
+    ops.image_readout(P, 1, pg, None, rows, cols, img, batch, y, ss=ss)
+    assert_close(y.cpu().numpy(), 2 * g, "accumulate")
+    act = torch.zeros(batch, rows, device=dev)
+    ops.image_readout(P, ops.IMAGE_SWIGLU, pg, pu, rows, cols, img, batch, act, ss=ss)
+    assert_close(act.cpu().numpy(), g * u / (1 + np.exp(-g)), "swiglu")
+    # without ss: W (x * w); K slabs left in the workspace as [slab][32][rows] add up to it
+    g0 = orc.gemv_f64(fmt, wg, rows, cols, (x * nw).astype(np.float32))
+    ops.image_readout(P, 0, pg, None, rows, cols, img, batch, y)
+    assert_close(y.cpu().numpy(), g0, "store, no norm")
+    ws = torch.zeros(ops.image_readout_workspace_bytes(rows, cols, False), dtype=torch.uint8, device=dev)
+    ns = ops.image_readout(P, 0, pg, None, rows, cols, img, batch, y, reduce=False, workspace=ws)
+    if ns > 1:
+        part = ws.view(torch.float32)[:ns * 32 * rows].view(ns, 32, rows)[:, :batch].sum(0)
+        assert_close(part.cpu().numpy(), g0, "slabs")
+    torch.cuda.synchronize()
+
+
+@pytest.mark.parametrize("batch", [3, 32])
+def test_swiglu_image_feeds_down_readout(torch_dev, batch):
+    """The decode step's MLP through the image path: gate/up readout with K slabs left ->
+    rta_image_from_swiglu -> down readout, against the oracle."""
+    torch, dev = torch_dev
+    rng = np.random.default_rng(950 + batch)
+    fmt, D, FF = orc.Q4_K, 512, 768
+    P = fmt | TILED
+    print(f"swiglu image: batch {batch} D {D} FF {FF}", flush=True)
+    wg, wu, wd = (synth.random_matrix(rng, fmt, FF, D), synth.random_matrix(rng, fmt, FF, D),
+                  synth.random_matrix(rng, fmt, D, FF))
+    x = rng.standard_normal((batch, D)).astype(np.float32)
+    pg, pu, pd = (ops.pack(fmt, to_dev(torch, w, dev), r, c) for w, r, c in ((wg, FF, D), (wu, FF, D), (wd, D, FF)))
+    img, _ = ops.image_from_rows(P, to_dev(torch, x, dev))
+    ws = torch.zeros(ops.image_readout_workspace_bytes(FF, D, True), dtype=torch.uint8, device=dev)
+    act = torch.zeros(batch, FF, device=dev)
+    ns = ops.image_readout(P, ops.IMAGE_SWIGLU, pg, pu, FF, D, img, batch, act, reduce=False, workspace=ws)
+    g, u = orc.gemv_f64(fmt, wg, FF, D, x), orc.gemv_f64(fmt, wu, FF, D, x)
+    a = (g * u / (1 + np.exp(-g))).astype(np.float32)
+    if ns == 1:
+        pytest.skip("one K slab at this shape: no slabs to turn into an image")
+    img2 = ops.image_from_swiglu(P, ws.view(torch.float32), ns, FF, batch)
+    y = torch.zeros(batch, D, device=dev)
+    ops.image_readout(P, 0, pd, None, D, FF, img2, batch, y)
+    assert_close(y.cpu().numpy(), orc.gemv_f64(fmt, wd, D, FF, a), "down from the SwiGLU image")
+    torch.cuda.synchronize()
