@@ -221,10 +221,14 @@ def cpu_time(fn, seconds):
 
 
 def close(got, ref):
+    """The float bar, max|got - ref| <= 1e-5 + 1e-3 max|ref| per tensor, and beside it the
+    fraction of elements passing the elementwise allclose(rtol=1e-3, atol=1e-5) test."""
     got, ref = np.asarray(got, np.float64), np.asarray(ref, np.float64)
     err = float(np.max(np.abs(got - ref)))
     peak = float(np.max(np.abs(ref)))
-    return {"max_abs_err": err, "peak": peak, "ok": bool(err <= 1e-5 + 1e-3 * peak)}
+    elem = float(np.mean(np.abs(got - ref) <= 1e-5 + 1e-3 * np.abs(ref)))
+    return {"max_abs_err": err, "peak": peak, "ok": bool(err <= 1e-5 + 1e-3 * peak),
+            "allclose_1e-3_1e-5_pass_fraction": elem}
 
 
 # ------------------------------------------------------------------ workloads ----

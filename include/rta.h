@@ -448,6 +448,27 @@ int rta_hybrid_decode_step(const rta_hybrid_shape* shape, const rta_hybrid_weigh
                            uint32_t* tokens, float* logits_out, void* workspace, size_t workspace_bytes,
                            rta_stream_t stream);
 
+/* What a step can copy out besides its tokens and logits (device pointers, NULL: not
+ * captured). */
+typedef struct rta_hybrid_capture {
+    float* residual;   /* [layers + 1][batch][hidden]: the embedding rows, then the residual
+                          stream after each layer's MLP -- the reference's layer capture
+                          (debug 1: the state snapshot after executeMLP,
+                          optical_resident.cpp:481, returned by prefill,
+                          resident_runtime.py:136-139) */
+    float* kv;         /* [full layer][batch][2][kv_heads * 128]: the normed, rotated key row
+                          and the value row each full layer quantises into its history
+                          packet (op 34's input, resident_history_quant.glsl:5) */
+} rta_hybrid_capture;
+
+/* rta_hybrid_decode_step that also fills the capture buffers (replaces the debug-1
+ * capture path of Resident::layer, optical_resident.cpp:481,609-686).  capture NULL or
+ * with both pointers NULL: exactly rta_hybrid_decode_step. */
+int rta_hybrid_decode_step_capture(const rta_hybrid_shape* shape, const rta_hybrid_weights* weights, int batch,
+                                   void* state, uint32_t* tokens, float* logits_out,
+                                   const rta_hybrid_capture* capture, void* workspace, size_t workspace_bytes,
+                                   rta_stream_t stream);
+
 /* ---------------- on-disk assets (host only: no device work, no GPU needed).
  * Reads the exporter's optical_model.bin (RTRES004), geometry_weights.bin and
  * vocabulary.bin (RTBASQ01) into host memory (ray_tracing/compiler/export.py:51-138),

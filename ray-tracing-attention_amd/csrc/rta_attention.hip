@@ -30,6 +30,7 @@
 #include "rta_common.hpp"
 #include "rta_host.hpp"
 #include "rta_internal.hpp"
+#include "rta_pack.hpp"
 
 namespace rta {
 
@@ -1847,8 +1848,9 @@ __global__ void __launch_bounds__(256, 2) attn_chunk_mma6_kernel(const AttnArgs 
 //                    q_out; with qop the head's rows of its kv head's matrix-core q
 //                    operands (make_qop's values); with a gate its summed rows to gate_out
 //   x < nqb + nkv2   kv heads 2j, 2j + 1 (j = x - nqb): K norm and RoPE (waves 0, 1), V
-//                    (waves 2, 3), then one superblock of each history field quantised with
-//                    pack_history_kernel's arithmetic and written to packet slot[b]
+//                    (waves 2, 3), then one superblock of each history field quantised by
+//                    the packer routine rta_pack_history runs (pack_superblock_pair) and
+//                    written to packet slot[b]; with kv_out the two rows as well
 //   x == nqb + nkv2  (b = 0, with a plan) the attention's tile plan.
 struct MiddleArgs {
     const float* proj;
@@ -1867,113 +1869,17 @@ struct MiddleArgs {
     const int64_t* slot;
     int64_t n_slots, stride, v_offset;
     uint8_t* packets;
+    float* kv_out;       // [nseq][2][hkv 128]: the key and value rows quantised, or null
     int nqb, nkv2;
     AttnArgs plan;       // plan.plan null: no tile plan
 };
-
-__device__ __forceinline__ float mid_glsl_min(float x, float y) { return y < x ? y : x; }
-__device__ __forceinline__ float mid_glsl_max(float x, float y) { return x < y ? y : x; }
-
-// One history field superblock (256 values in xs) quantised into out (144 or 210 bytes
-// in LDS) as pack_history_kernel quantises a field: 256 threads, LDS scratch st.
-struct FieldScratch {
-    float gscale[16], gmin[16], bd, bdm;
-    uint32_t sc[16], mn[16];
-};
-
-__device__ __forceinline__ void mid_stats(const float* xs, bool q4, FieldScratch& st, int t) {
-#pragma clang fp contract(off)
-    const int ng = q4 ? 8 : 16, width = q4 ? 32 : 16;
-    if (t < ng) {
-        float lo = 0.0f, hi = 0.0f;
-        for (int i = 0; i < width; ++i) {
-            const float v = xs[t * width + i];
-            if (q4) {
-                lo = mid_glsl_min(lo, v);
-                hi = mid_glsl_max(hi, v);
-            } else {
-                hi = mid_glsl_max(hi, fabsf(v));
-            }
-        }
-        st.gscale[t] = q4 ? (hi - lo) / 15.0f : hi / 31.0f;
-        st.gmin[t] = q4 ? -lo : 0.0f;
-    }
-}
-
-__device__ __forceinline__ void mid_scales(bool q4, FieldScratch& st, uint8_t* out) {
-#pragma clang fp contract(off)
-    const int ng = q4 ? 8 : 16;
-    float maxD = 0.0f, maxMin = 0.0f;
-    for (int g = 0; g < ng; ++g) {
-        maxD = mid_glsl_max(maxD, st.gscale[g]);
-        maxMin = mid_glsl_max(maxMin, st.gmin[g]);
-    }
-    const _Float16 hd16 = (_Float16)(maxD / (q4 ? 63.0f : 127.0f));
-    st.bd = (float)hd16;
-    const uint16_t hb = __builtin_bit_cast(uint16_t, hd16);
-    if (q4) {
-        const _Float16 hm16 = (_Float16)(maxMin / 63.0f);
-        st.bdm = (float)hm16;
-        const uint16_t hm = __builtin_bit_cast(uint16_t, hm16);
-        out[0] = hb & 255;
-        out[1] = hb >> 8;
-        out[2] = hm & 255;
-        out[3] = hm >> 8;
-    } else {
-        out[208] = hb & 255;
-        out[209] = hb >> 8;
-    }
-}
-
-__device__ __forceinline__ void mid_codes(bool q4, FieldScratch& st, uint8_t* out, int t) {
-#pragma clang fp contract(off)
-    const int ng = q4 ? 8 : 16;
-    if (t < ng) {
-        st.sc[t] = (uint32_t)fminf(fmaxf(rintf(st.gscale[t] / fmaxf(st.bd, 1e-30f)), 0.0f), q4 ? 63.0f : 127.0f);
-        if (q4) st.mn[t] = (uint32_t)fminf(fmaxf(rintf(st.gmin[t] / fmaxf(st.bdm, 1e-30f)), 0.0f), 63.0f);
-        else out[192 + t] = (uint8_t)st.sc[t];
-    }
-}
-
-__device__ __forceinline__ void mid_values(const float* xs, bool q4, const FieldScratch& st, uint8_t* out, int t) {
-#pragma clang fp contract(off)
-    if (q4 && t < 4) {
-        out[4 + t] = (uint8_t)(st.sc[t] | ((st.sc[t + 4] >> 4) << 6));
-        out[8 + t] = (uint8_t)(st.mn[t] | ((st.mn[t + 4] >> 4) << 6));
-        out[12 + t] = (uint8_t)((st.sc[t + 4] & 15u) | ((st.mn[t + 4] & 15u) << 4));
-    }
-    auto q4code = [&](int i) {
-        const int g = i >> 5;
-        const float num = xs[i] + st.bdm * (float)st.mn[g];
-        const float den = fmaxf(st.bd * (float)st.sc[g], 1e-30f);
-        return (uint32_t)fminf(fmaxf(rintf(num / den), 0.0f), 15.0f);
-    };
-    auto q6code = [&](int i) {
-        const int g = i >> 4;
-        const float den = fmaxf(st.bd * (float)st.sc[g], 1e-30f);
-        return (uint32_t)((int)fminf(fmaxf(rintf(xs[i] / den), -32.0f), 31.0f) + 32);
-    };
-    if (q4) {
-        if (t < 128) {   // qs byte t: value 64 (t/32) + t%32 (low nibble) and +32 (high)
-            const int i = 64 * (t >> 5) + (t & 31);
-            out[16 + t] = (uint8_t)(q4code(i) | (q4code(i + 32) << 4));
-        }
-    } else if (t < 128) {   // ql byte: value 128 (t/64) + t%64 (low) and +64 (high)
-        const int i = 128 * (t >> 6) + (t & 63);
-        out[t] = (uint8_t)((q6code(i) & 15u) | ((q6code(i + 64) & 15u) << 4));
-    } else if (t < 192) {   // qh byte: values 128 part + l + 32 k, two bits each
-        const int jj = t - 128, i = 128 * (jj >> 5) + (jj & 31);
-        out[t] = (uint8_t)(((q6code(i) >> 4) & 3u) | (((q6code(i + 32) >> 4) & 3u) << 2) |
-                           (((q6code(i + 64) >> 4) & 3u) << 4) | (((q6code(i + 96) >> 4) & 3u) << 6));
-    }
-}
 
 template <int NS>
 __global__ void __launch_bounds__(256) full_middle_kernel(const MiddleArgs p) {
     constexpr int hd = 128;
     __shared__ float xs[2][256];
     __shared__ float qsv[4][hd];
-    __shared__ FieldScratch st[2];
+    __shared__ PackScratch st[2];
     __shared__ uint8_t fb[2][212];
     const int x = blockIdx.x, b = blockIdx.y, tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -2110,20 +2016,16 @@ __global__ void __launch_bounds__(256) full_middle_kernel(const MiddleArgs p) {
             xs[1][(wave & 1) * hd + 2 * lane + 1] = v.y;
         }
         const bool q4[2] = {p.fmt_k == RTA_Q4_K, p.fmt_v == RTA_Q4_K};
-        for (int i = tid; i < 2 * 212; i += 256) fb[i / 212][i % 212] = 0;
         __syncthreads();
-        mid_stats(xs[0], q4[0], st[0], tid);
-        if (tid >= 64 && tid < 128) mid_stats(xs[1], q4[1], st[1], tid - 64);
-        __syncthreads();
-        if (tid == 0) mid_scales(q4[0], st[0], fb[0]);
-        if (tid == 64) mid_scales(q4[1], st[1], fb[1]);
-        __syncthreads();
-        mid_codes(q4[0], st[0], fb[0], tid);
-        if (tid >= 64 && tid < 128) mid_codes(q4[1], st[1], fb[1], tid - 64);
-        __syncthreads();
-        mid_values(xs[0], q4[0], st[0], fb[0], tid);
-        mid_values(xs[1], q4[1], st[1], fb[1], tid);
-        __syncthreads();
+        if (p.kv_out) {   // the rows this block quantises: key then value row of sequence b
+            const int kvw = p.hkv * hd, c = 256 * j + tid;
+            if (c < kvw) {
+                float* o = p.kv_out + (int64_t)b * 2 * kvw;
+                o[c] = xs[0][tid];
+                o[kvw + c] = xs[1][tid];
+            }
+        }
+        pack_superblock_pair(xs, q4, st, fb, tid);
         const int64_t sl = p.slot[b];
         if (sl < 0 || sl >= p.n_slots) {
             if (tid == 0) raise_error(RTA_DEVERR_HITS);
@@ -2672,14 +2574,8 @@ int rta_decode_attention(const float* q, int nseq, int hq, int hkv, int hd, cons
 
 namespace rta {
 
-int decode_attention_gate_stride(const float* q, int nseq, int hq, int hkv, int hd, const void* packets, int fmt_k,
-                                 int fmt_v, const int64_t* slot_base, const int32_t* ctx_len, int64_t capacity,
-                                 int64_t n_slots, int max_ctx, const float* gate, int64_t gate_stride, float* out,
-                                 float* m_out, float* z_out, void* workspace, size_t workspace_bytes,
-                                 rta_stream_t stream, int out_rotary, bool prepared) {
-    if (!q || !packets || !slot_base || !ctx_len || !out) return RTA_ERR_NULL;   // m_out, z_out optional
-    if (nseq <= 0 || hq <= 0 || hkv <= 0 || hd <= 0 || hq % hkv || capacity <= 0 || max_ctx <= 0 || n_slots <= 0)
-        return RTA_ERR_SHAPE;
+int attention_shape_check(int hq, int hkv, int hd, int fmt_k, int fmt_v) {
+    if (hq <= 0 || hkv <= 0 || hd <= 0 || hq % hkv) return RTA_ERR_SHAPE;
     if ((fmt_k != RTA_Q4_K && fmt_k != RTA_Q6_K) || (fmt_v != RTA_Q4_K && fmt_v != RTA_Q6_K)) return RTA_ERR_FORMAT;
     // a packet holds 354 bytes per 256 values (resident_dimensions.hpp:10): one Q4_K and one
     // Q6_K field, or two Q4_K fields; two Q6_K fields would overrun it
@@ -2689,8 +2585,22 @@ int decode_attention_gate_stride(const float* q, int nseq, int hq, int hkv, int 
     // phase B spreads every kv head over 128 / (8 or 16) threads of one 256-thread workgroup
     if (hkv * (G == 8 ? 16 : 8) > 256) return RTA_ERR_RANGE;
     const int nblk = (hkv * kHd + 255) / 256;
+    if (attn_lds_bytes(hq, hkv, nblk, fmt_v) > kMaxLds) return RTA_ERR_RANGE;
+    return RTA_OK;
+}
+
+int decode_attention_gate_stride(const float* q, int nseq, int hq, int hkv, int hd, const void* packets, int fmt_k,
+                                 int fmt_v, const int64_t* slot_base, const int32_t* ctx_len, int64_t capacity,
+                                 int64_t n_slots, int max_ctx, const float* gate, int64_t gate_stride, float* out,
+                                 float* m_out, float* z_out, void* workspace, size_t workspace_bytes,
+                                 rta_stream_t stream, int out_rotary, bool prepared) {
+    if (!q || !packets || !slot_base || !ctx_len || !out) return RTA_ERR_NULL;   // m_out, z_out optional
+    if (nseq <= 0 || capacity <= 0 || max_ctx <= 0 || n_slots <= 0) return RTA_ERR_SHAPE;
+    const int shape_rc = attention_shape_check(hq, hkv, hd, fmt_k, fmt_v);
+    if (shape_rc) return shape_rc;
+    const int G = hq / hkv;
+    const int nblk = (hkv * kHd + 255) / 256;
     const int lds = attn_lds_bytes(hq, hkv, nblk, fmt_v);
-    if (lds > kMaxLds) return RTA_ERR_RANGE;
     if (!host::aligned(q, 4) || !host::aligned(packets, 4) || !host::aligned(slot_base, 8) ||
         !host::aligned(ctx_len, 4) || !host::aligned(out, 4) || (gate && !host::aligned(gate, 4)))
         return RTA_ERR_ALIGN;
@@ -2745,7 +2655,7 @@ int full_layer_middle(const float* proj, int64_t slab_stride, int row_stride, in
                       const float* q_norm, const float* k_norm, float eps, const int64_t* positions, int rotary,
                       double theta, float* q_out, float* gate_out, int64_t gate_stride, int fmt_k, int fmt_v,
                       const int64_t* slots, int64_t n_slots, void* packets, const int32_t* ctx_len, int64_t capacity,
-                      int max_ctx, void* attn_ws, hipStream_t s) {
+                      int max_ctx, void* attn_ws, float* kv_out, hipStream_t s) {
     if (!proj || !positions || !q_out || !slots || !packets || !ctx_len || !attn_ws) return RTA_ERR_NULL;
     if (batch <= 0 || hq <= 0 || hkv <= 0 || hq % hkv || row_stride < (2 * hq + 2 * hkv) * kHd - (gate_out ? 0 : hq * kHd))
         return RTA_ERR_SHAPE;
@@ -2779,6 +2689,7 @@ int full_layer_middle(const float* proj, int64_t slab_stride, int row_stride, in
     p.nkv2 = (hkv * kHd + 255) / 256;
     p.v_offset = (int64_t)p.nkv2 * (fmt_k == RTA_Q4_K ? 144 : 210);
     p.packets = static_cast<uint8_t*>(packets);
+    p.kv_out = kv_out;
     p.nqb = (hq + 3) / 4;
     // the attention kernels for Q4_K keys of at most 8 kv heads read matrix-core q operands
     // (and, with Q6_K values, a tile plan) that rta_decode_attention keeps in its

@@ -1053,8 +1053,13 @@ int rta_image_readout(int fmt, int mode, const void* w, const void* w2, int rows
                       int batch, const float* ss, float eps, float* y, int reduce, void* workspace,
                       size_t workspace_bytes, int* nslab, rta_stream_t stream) {
     if (mode != RTA_EPI_STORE && mode != RTA_EPI_ACCUMULATE && mode != RTA_IMAGE_SWIGLU) return RTA_ERR_RANGE;
-    if (ss && !host::aligned(ss, 16)) return RTA_ERR_ALIGN;
     if (image_bytes(cols, batch) == 0) return RTA_ERR_SHAPE;
+    // ss holds the four 1024-column chunk sums rta_image_from_rows writes (cols <= 4096)
+    if (ss && cols > 4096) return RTA_ERR_SHAPE;
+    // img and the K slabs are read with 16-byte loads; y is written per element
+    if ((ss && !host::aligned(ss, 16)) || !host::aligned(img, 16) || !host::aligned(workspace, 16) ||
+        !host::aligned(y, 4))
+        return RTA_ERR_ALIGN;
     RowNorm rn;
     if (ss) rn = RowNorm{reinterpret_cast<const float4*>(ss), (float)cols, eps};
     const int m = mode == RTA_EPI_STORE ? kReadStore : mode == RTA_EPI_ACCUMULATE ? kReadAccumulate : kReadSwiglu;

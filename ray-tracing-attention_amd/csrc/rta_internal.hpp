@@ -67,6 +67,10 @@ int residual_rmsnorm(float* hidden, const float* part, int nslab, const float* w
 int residual_norm_deferred(float* hidden, const float* part, int nslab, const float* w, int batch, int width,
                            float* out, float* ss, hipStream_t s);
 
+// The head counts and field formats the attention kernels serve (rta_decode_attention's
+// own checks): RTA_OK, or the status it would return for them.
+int attention_shape_check(int hq, int hkv, int hd, int fmt_k, int fmt_v);
+
 // rta_decode_attention with the gate of sequence s at gate + s gate_stride (head h at
 // + h hd), gate_stride >= hq hd: the gate rows of a fused in-projection.  out_rotary R > 0:
 // output dim d < R of each head is written to column (d % 2)(R / 2) + d / 2 of the head.
@@ -80,7 +84,8 @@ int decode_attention_gate_stride(const float* q, int nseq, int hq, int hkv, int 
 // attention: in-projection rows (q | k | v | gate, hq / hkv / hkv / hq heads of 128) of
 // sequence b summed over nslab K slabs, proj[k slab_stride + b row_stride + r];
 // QK-norm + RoPE of q (to q_out, [batch][hq][128]) and k; k and v quantised into packet
-// slots[b] (fmt_k / fmt_v fields, as rta_pack_history); gate rows summed into gate_out
+// slots[b] (fmt_k / fmt_v fields, as rta_pack_history), and with kv_out those normed,
+// rotated k rows and v rows as well ([batch][2][hkv 128]); gate rows summed into gate_out
 // (row b at + b gate_stride; null: no gate).  For the layout whose attention runs on the
 // Q4_K-key matrix-core kernel it also writes that kernel's q operands and tile plan into
 // attn_ws (the workspace of the decode_attention_gate_stride call that follows with
@@ -89,7 +94,7 @@ int full_layer_middle(const float* proj, int64_t slab_stride, int row_stride, in
                       const float* q_norm, const float* k_norm, float eps, const int64_t* positions, int rotary,
                       double theta, float* q_out, float* gate_out, int64_t gate_stride, int fmt_k, int fmt_v,
                       const int64_t* slots, int64_t n_slots, void* packets, const int32_t* ctx_len, int64_t capacity,
-                      int max_ctx, void* attn_ws, hipStream_t s);
+                      int max_ctx, void* attn_ws, float* kv_out, hipStream_t s);
 
 // ---- the decode step's readouts of a staged x image (rta_packed.hpp) ----
 constexpr int kReadStore = 0, kReadAccumulate = 1, kReadSwiglu = 2;   // image_readout modes

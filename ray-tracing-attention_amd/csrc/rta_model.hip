@@ -10,6 +10,9 @@
 #include <string.h>
 
 #include <algorithm>
+#include <map>
+#include <mutex>
+#include <tuple>
 
 #include "rta_common.hpp"
 #include "rta_host.hpp"
@@ -107,6 +110,9 @@ int check_shape(const rta_hybrid_shape* s, int batch) {
         s->o_axis_remap < 0 || s->o_axis_remap > 1 ||
         s->rec_key_heads < 0 || s->rec_key_heads > s->rec_heads)
         return RTA_ERR_RANGE;
+    // the full layers' attention: refused here, before the step advances any state
+    if (s->full_every > 0 && s->layers >= s->full_every)
+        return attention_shape_check(s->q_heads, s->kv_heads, s->head_dim, s->fmt_k, s->fmt_v);
     return RTA_OK;
 }
 
@@ -138,6 +144,28 @@ struct Work {
     size_t attn_bytes, lm_bytes, gemm_bytes;
 };
 
+// The largest projection workspace of an in-projection part: parts may have any row
+// count up to the whole in-projection's, and a readout's workspace does not grow steadily
+// with its rows (fewer row tiles get more K slabs).  Within one run of row counts that
+// share a plan (the same number of 16- or 32-row tiles) the slab partials grow with the
+// rows, so the multiples of 16 bound every count.  Cached per (hidden, batch tile, rows).
+size_t parts_ws_bytes(int D, int B, int rows_max) {
+    static std::mutex mu;
+    static std::map<std::tuple<int, int, int>, size_t> memo;
+    const auto key = std::make_tuple(D, std::min(B, 32), rows_max);
+    {
+        std::lock_guard<std::mutex> g(mu);
+        const auto it = memo.find(key);
+        if (it != memo.end()) return it->second;
+    }
+    size_t m = 0;
+    for (const int f : {(int)RTA_Q4_K, (int)RTA_Q6_K, RTA_Q4_K | RTA_TILED, RTA_Q6_K | RTA_TILED})
+        for (int n = 16; n < rows_max + 16; n += 16) m = std::max(m, rta_gemv_workspace_bytes(f, n, D, B));
+    std::lock_guard<std::mutex> g(mu);
+    memo[key] = m;
+    return m;
+}
+
 // The projection workspace: enough for every format a layer may use (the shape alone
 // fixes the size), the K-quant and packed ones being the only that need any.
 size_t gemm_ws_bytes(const rta_hybrid_shape* s, const Dims& d) {
@@ -157,6 +185,8 @@ size_t gemm_ws_bytes(const rta_hybrid_shape* s, const Dims& d) {
     if (d.nrec) up(image_readout_ws_bytes(d.rows_rec, d.D, false));
     up(image_readout_ws_bytes(d.FF, d.D, true));
     up(image_readout_ws_bytes(d.D, d.FF, false));
+    if (s->layer_formats)   // in-projection parts of any row count (they need layer formats)
+        up(parts_ws_bytes(d.D, d.B, std::max(d.nfull ? d.rows_full : 0, d.nrec ? d.rows_rec : 0)));
     if (d.nrec && s->layer_formats) {   // separate a / b readouts behind a layer's pending K slabs
         size_t ab = 0;
         for (int f : {RTA_Q4_K, RTA_Q6_K}) ab = std::max(ab, rta_gemv_workspace_bytes(f, d.H, d.D, d.B));
@@ -254,6 +284,14 @@ int rta_hybrid_init(const rta_hybrid_shape* shape, int batch, void* state, const
 int rta_hybrid_decode_step(const rta_hybrid_shape* shape, const rta_hybrid_weights* weights, int batch, void* state,
                            uint32_t* tokens, float* logits_out, void* workspace, size_t workspace_bytes,
                            rta_stream_t stream) {
+    return rta_hybrid_decode_step_capture(shape, weights, batch, state, tokens, logits_out, nullptr, workspace,
+                                          workspace_bytes, stream);
+}
+
+int rta_hybrid_decode_step_capture(const rta_hybrid_shape* shape, const rta_hybrid_weights* weights, int batch,
+                                   void* state, uint32_t* tokens, float* logits_out,
+                                   const rta_hybrid_capture* capture, void* workspace, size_t workspace_bytes,
+                                   rta_stream_t stream) {
     int rc = check_shape(shape, batch);
     if (rc) return rc;
     if (!weights || !weights->layers || !weights->embed || !weights->lm_head || !weights->norm_final || !state ||
@@ -261,6 +299,7 @@ int rta_hybrid_decode_step(const rta_hybrid_shape* shape, const rta_hybrid_weigh
         return RTA_ERR_NULL;
     if (workspace_bytes < rta_hybrid_workspace_bytes(shape, batch)) return RTA_ERR_WORKSPACE;
     if (!host::aligned(state, 256) || !host::aligned(workspace, 256)) return RTA_ERR_ALIGN;
+    if (capture && !(host::aligned(capture->residual, 4) && host::aligned(capture->kv, 4))) return RTA_ERR_ALIGN;
     const Dims d = dims_of(shape, batch);
     const State st = carve_state(d, state, nullptr);
     Work w = carve_work(shape, d, workspace, nullptr);
@@ -279,6 +318,22 @@ int rta_hybrid_decode_step(const rta_hybrid_shape* shape, const rta_hybrid_weigh
                        (int64_t)d.cap, st.base, w.pos, w.visible, w.slots);
     if (hipGetLastError() != hipSuccess) return RTA_ERR_LAUNCH;
     RTA_TRY(rta_embed(shape->fmt_embed, weights->embed, d.V, d.D, tokens, B, w.hidden, stream));
+
+    // Layer capture: the residual stream after layer l is whole once the next norm has
+    // added the last projection's pending K slabs, so it is copied right after that norm.
+    float* cap_res = capture ? capture->residual : nullptr;
+    float* cap_kv = capture ? capture->kv : nullptr;
+    int cap_due = -1;   // residual row block still to copy (0: the embedding rows)
+    auto capture_residual = [&]() -> int {
+        if (!cap_res || cap_due < 0) return RTA_OK;
+        const size_t n = (size_t)B * d.D;
+        const hipError_t e = hipMemcpyAsync(cap_res + (size_t)cap_due * n, w.hidden, n * sizeof(float),
+                                            hipMemcpyDeviceToDevice, s);
+        cap_due = -1;
+        return e == hipSuccess ? RTA_OK : RTA_ERR_LAUNCH;
+    };
+    cap_due = 0;
+    RTA_TRY(capture_residual());
 
     // Per matrix: packed formats at one batch tile run on the fused paths.  The residual
     // projections (O and down) then leave their K slabs in the GEMM workspace and the
@@ -312,7 +367,7 @@ int rta_hybrid_decode_step(const rta_hybrid_shape* shape, const rta_hybrid_weigh
         int rc;
         if (!keep_fp32 && !pending && b1_norm_fusable(f, d.D, B)) {
             xn = XNorm{nw, eps};
-            return RTA_OK;
+            return capture_residual();
         }
         if (imaged(f)) {
             rc = residual_norm_image(f, w.hidden, part, pending, nw, B, d.D, w.rms, keep_fp32 ? w.normed : nullptr,
@@ -327,7 +382,7 @@ int rta_hybrid_decode_step(const rta_hybrid_shape* shape, const rta_hybrid_weigh
             rc = rta_rmsnorm(w.hidden, nw, B, d.D, eps, w.normed, stream);
         }
         pending = 0;
-        return rc;
+        return rc ? rc : capture_residual();
     };
 
     // An in-projection given in parts (formats of their own): each part is read into its
@@ -392,7 +447,8 @@ int rta_hybrid_decode_step(const rta_hybrid_shape* shape, const rta_hybrid_weigh
                                       (int64_t)kSlabBatch * d.rows_full, d.rows_full, ns, B, d.hq, d.hkv, lw.q_norm,
                                       lw.k_norm, eps, w.pos, shape->rope_rotary, shape->rope_theta, w.q, gate,
                                       d.rows_full, shape->fmt_k, shape->fmt_v, w.slots + (size_t)lf * B,
-                                      (int64_t)B * d.cap, packets, w.visible, d.cap, d.cap, w.attn_ws, s));
+                                      (int64_t)B * d.cap, packets, w.visible, d.cap, d.cap, w.attn_ws,
+                                      cap_kv ? cap_kv + (size_t)lf * B * 2 * d.kvw : nullptr, s));
             RTA_TRY(decode_attention_gate_stride(w.q, B, d.hq, d.hkv, d.hd, packets, shape->fmt_k, shape->fmt_v,
                                                  st.base + (size_t)lf * B, w.visible, d.cap, (int64_t)B * d.cap,
                                                  d.cap, gate, d.rows_full, w.mix, nullptr, nullptr, w.attn_ws,
@@ -471,6 +527,7 @@ int rta_hybrid_decode_step(const rta_hybrid_shape* shape, const rta_hybrid_weigh
                                       w.gemm_ws, w.gemm_bytes, s, rn, xn));
         }
         if (!down_done) RTA_TRY(residual_proj(fd, lw.w_down, d.FF, w.act));
+        cap_due = l + 1;
     }
     // op 1 index 2, then the readout (Resident::word): logits and the next tokens; the
     // packed LM head takes the row factor itself (never an image: it is read once)
@@ -490,6 +547,7 @@ int rta_hybrid_decode_step(const rta_hybrid_shape* shape, const rta_hybrid_weigh
             RTA_TRY(rta_rmsnorm(w.hidden, weights->norm_final, B, d.D, eps, w.normed, stream));
         }
         pending = 0;
+        RTA_TRY(capture_residual());
     }
     RTA_TRY(lm_head_rownorm(shape->fmt_lm, weights->lm_head, d.V, d.D, xn.w ? w.hidden : w.normed, B, shape->margin,
                             logits_out ? logits_out : w.logits, tokens, w.lm_ws, w.lm_bytes, s, rn, xn));

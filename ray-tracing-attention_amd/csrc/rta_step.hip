@@ -6,6 +6,7 @@
 #include "rta_common.hpp"
 #include "rta_host.hpp"
 #include "rta_internal.hpp"
+#include "rta_pack.hpp"
 
 namespace rta {
 
@@ -518,163 +519,41 @@ int recurrent_mix(const float* proj, int64_t slab_stride, int row_stride, int ns
 }
 
 // --------------------------------------------------------- history packer ----
-// op 34 (resident_history_quant.glsl:9-41): one block per sequence quantises its new
-// key and value rows into a history packet (a Q4_K or Q6_K field each) in LDS and
-// writes it to packet slot slot[b].  Every step follows the reference's fp32 order
-// (contraction off, IEEE division, round-half-even codes, fp16 block scales):
-//   Q4_K field: 32-value groups, span (max(0,x) - min(0,x)) / 15, minimum -min(0,x),
-//               d = fp16(max span / 63), dmin = fp16(max minimum / 63), 6-bit codes
-//   Q6_K field: 16-value groups, max|x| / 31, d = fp16(max / 127), 8-bit codes
+// op 34 (resident_history_quant.glsl:9-41): block (j, b) quantises superblock j (values
+// 256 j .. 256 j + 255) of sequence b's new key and value rows with the shared packer
+// routine (rta_pack.hpp, the arithmetic the decode step's middle kernel runs as well)
+// and writes it to packet slot slot[b]; block j = 0 also zeroes the packet's padding.
 constexpr int kPackMaxBlocks = 16;   // kvw <= 4096
-
-// GLSL min / max: x unless y is strictly smaller / larger.  They fix the sign of
-// zero where the packer compares +0 with -0 (the minimum -min(0, x) of an all-zero
-// group is -0), which the fp16 block minimum keeps.
-__device__ __forceinline__ float glsl_min(float x, float y) { return y < x ? y : x; }
-__device__ __forceinline__ float glsl_max(float x, float y) { return x < y ? y : x; }
 
 __global__ void __launch_bounds__(256) pack_history_kernel(const float* __restrict__ kin, int k_stride,
                                                            const float* __restrict__ vin, int v_stride, int kvw,
                                                            int fmt_k, int fmt_v, const int64_t* __restrict__ slot,
                                                            int64_t n_slots, int64_t stride,
                                                            uint8_t* __restrict__ packets) {
-#pragma clang fp contract(off)
-    __shared__ uint32_t pkt[kPackMaxBlocks * 2 * 210 / 4 + 4];
-    __shared__ float gscale[2][kPackMaxBlocks * 16], gmin[2][kPackMaxBlocks * 16];
-    __shared__ float bd[2][kPackMaxBlocks], bdm[2][kPackMaxBlocks];
-    __shared__ uint32_t sc[2][kPackMaxBlocks * 16], mn[2][kPackMaxBlocks * 16];
-    __shared__ float xs[2][kPackMaxBlocks * 256];   // the K and V rows, zero past kvw
-    uint8_t* pb = reinterpret_cast<uint8_t*>(pkt);
-    const int b = blockIdx.x, tid = threadIdx.x;
-    const int blocks = (kvw + 255) / 256;
-    const float* src[2] = {kin + (int64_t)b * k_stride, vin + (int64_t)b * v_stride};
-    const int fmt[2] = {fmt_k, fmt_v};
-    const int field_off[2] = {0, blocks * (fmt_k == RTA_Q4_K ? 144 : 210)};
-    // both rows into LDS once (every load issued before the first is used); the steps
-    // below read each value several times
-    {
-        float t[2][kPackMaxBlocks];
-#pragma unroll
-        for (int f = 0; f < 2; ++f)
-#pragma unroll
-            for (int k = 0; k < kPackMaxBlocks; ++k) {
-                const int i = tid + 256 * k;
-                t[f][k] = (k < blocks && i < kvw) ? src[f][i] : 0.0f;
-            }
-#pragma unroll
-        for (int f = 0; f < 2; ++f)
-#pragma unroll
-            for (int k = 0; k < kPackMaxBlocks; ++k)
-                if (k < blocks) xs[f][tid + 256 * k] = t[f][k];
-    }
-    auto value = [&](int f, int i) { return xs[f][i]; };
-    for (int i = tid; i < (int)(stride / 4); i += 256) pkt[i] = 0u;
+    __shared__ float xs[2][256];   // the superblock of the K and V rows, zero past kvw
+    __shared__ PackScratch st[2];
+    __shared__ uint8_t fb[2][212];
+    const int j = blockIdx.x, b = blockIdx.y, tid = threadIdx.x;
+    const int nsb = gridDim.x, c = 256 * j + tid;
+    const float k = c < kvw ? kin[(int64_t)b * k_stride + c] : 0.0f;
+    const float v = c < kvw ? vin[(int64_t)b * v_stride + c] : 0.0f;
+    xs[0][tid] = k;
+    xs[1][tid] = v;
     __syncthreads();
-    // 1. group statistics
-    for (int f = 0; f < 2; ++f) {
-        const bool q4 = fmt[f] == RTA_Q4_K;
-        const int ng = blocks * (q4 ? 8 : 16), width = q4 ? 32 : 16;
-        for (int g = tid; g < ng; g += 256) {
-            float lo = 0.0f, hi = 0.0f;
-            for (int i = 0; i < width; ++i) {
-                const float v = value(f, g * width + i);
-                if (q4) { lo = glsl_min(lo, v); hi = glsl_max(hi, v); }
-                else hi = glsl_max(hi, fabsf(v));
-            }
-            gscale[f][g] = q4 ? (hi - lo) / 15.0f : hi / 31.0f;
-            gmin[f][g] = q4 ? -lo : 0.0f;
-        }
-    }
-    __syncthreads();
-    // 2. block scales (fp16) and their header bytes
-    if (tid < 2 * blocks) {
-        const int f = tid / blocks, blk = tid - f * blocks;
-        const bool q4 = fmt[f] == RTA_Q4_K;
-        const int ng = q4 ? 8 : 16;
-        float maxD = 0.0f, maxMin = 0.0f;
-        for (int g = 0; g < ng; ++g) {
-            maxD = glsl_max(maxD, gscale[f][blk * ng + g]);
-            maxMin = glsl_max(maxMin, gmin[f][blk * ng + g]);
-        }
-        const _Float16 hd16 = (_Float16)(maxD / (q4 ? 63.0f : 127.0f));
-        bd[f][blk] = (float)hd16;
-        const uint16_t hb = __builtin_bit_cast(uint16_t, hd16);
-        uint8_t* base = pb + field_off[f] + blk * (q4 ? 144 : 210);
-        if (q4) {
-            const _Float16 hm16 = (_Float16)(maxMin / 63.0f);
-            bdm[f][blk] = (float)hm16;
-            const uint16_t hm = __builtin_bit_cast(uint16_t, hm16);
-            base[0] = hb & 255; base[1] = hb >> 8; base[2] = hm & 255; base[3] = hm >> 8;
-        } else {
-            base[208] = hb & 255; base[209] = hb >> 8;
-        }
-    }
-    __syncthreads();
-    // 3. group codes
-    for (int f = 0; f < 2; ++f) {
-        const bool q4 = fmt[f] == RTA_Q4_K;
-        const int ng = blocks * (q4 ? 8 : 16);
-        for (int g = tid; g < ng; g += 256) {
-            const int blk = g / (q4 ? 8 : 16);
-            const float d = bd[f][blk];
-            sc[f][g] = (uint32_t)fminf(fmaxf(rintf(gscale[f][g] / fmaxf(d, 1e-30f)), 0.0f), q4 ? 63.0f : 127.0f);
-            if (q4) mn[f][g] = (uint32_t)fminf(fmaxf(rintf(gmin[f][g] / fmaxf(bdm[f][blk], 1e-30f)), 0.0f), 63.0f);
-            else pb[field_off[f] + blk * 210 + 192 + (g & 15)] = (uint8_t)sc[f][g];
-        }
-    }
-    __syncthreads();
-    // 4. packed 6-bit Q4_K scales, then the quantised values, one output byte per thread
-    for (int f = 0; f < 2; ++f) {
-        if (fmt[f] != RTA_Q4_K) continue;
-        for (int t = tid; t < blocks * 4; t += 256) {
-            const int blk = t >> 2, g = t & 3, o = blk * 8;
-            uint8_t* base = pb + field_off[f] + blk * 144;
-            base[4 + g] = (uint8_t)(sc[f][o + g] | ((sc[f][o + g + 4] >> 4) << 6));
-            base[8 + g] = (uint8_t)(mn[f][o + g] | ((mn[f][o + g + 4] >> 4) << 6));
-            base[12 + g] = (uint8_t)((sc[f][o + g + 4] & 15u) | ((mn[f][o + g + 4] & 15u) << 4));
-        }
-    }
-    auto q4code = [&](int f, int i) {
-#pragma clang fp contract(off)
-        const int blk = i >> 8, g = i >> 5;
-        const float num = value(f, i) + bdm[f][blk] * (float)mn[f][g];
-        const float den = fmaxf(bd[f][blk] * (float)sc[f][g], 1e-30f);
-        return (uint32_t)fminf(fmaxf(rintf(num / den), 0.0f), 15.0f);
-    };
-    auto q6code = [&](int f, int i) {
-#pragma clang fp contract(off)
-        const int blk = i >> 8, g = i >> 4;
-        const float den = fmaxf(bd[f][blk] * (float)sc[f][g], 1e-30f);
-        return (uint32_t)((int)fminf(fmaxf(rintf(value(f, i) / den), -32.0f), 31.0f) + 32);
-    };
-    for (int f = 0; f < 2; ++f) {
-        const bool q4 = fmt[f] == RTA_Q4_K;
-        const int per = q4 ? 128 : 192;   // quant bytes per block
-        for (int t = tid; t < blocks * per; t += 256) {
-            const int blk = t / per, j = t - blk * per, v0 = blk * 256;
-            uint8_t byte;
-            if (q4) {   // qs byte j: value 64 (j/32) + j%32 (low nibble) and +32 (high)
-                const int i = v0 + 64 * (j >> 5) + (j & 31);
-                byte = (uint8_t)(q4code(f, i) | (q4code(f, i + 32) << 4));
-            } else if (j < 128) {   // ql byte: value 128 (j/64) + j%64 (low) and +64 (high)
-                const int i = v0 + 128 * (j >> 6) + (j & 63);
-                byte = (uint8_t)((q6code(f, i) & 15u) | ((q6code(f, i + 64) & 15u) << 4));
-            } else {                // qh byte: values 128 part + l + 32 k, two bits each
-                const int jj = j - 128, i = v0 + 128 * (jj >> 5) + (jj & 31);
-                byte = (uint8_t)(((q6code(f, i) >> 4) & 3u) | (((q6code(f, i + 32) >> 4) & 3u) << 2) |
-                                 (((q6code(f, i + 64) >> 4) & 3u) << 4) | (((q6code(f, i + 96) >> 4) & 3u) << 6));
-            }
-            pb[field_off[f] + blk * (q4 ? 144 : 210) + (q4 ? 16 + j : j)] = byte;
-        }
-    }
-    __syncthreads();
+    const bool q4[2] = {fmt_k == RTA_Q4_K, fmt_v == RTA_Q4_K};
+    pack_superblock_pair(xs, q4, st, fb, tid);
     const int64_t s = slot[b];
     if (s < 0 || s >= n_slots) {
-        if (tid == 0) raise_error(RTA_DEVERR_HITS);
+        if (tid == 0 && j == 0) raise_error(RTA_DEVERR_HITS);
         return;
     }
-    uint32_t* dst = reinterpret_cast<uint32_t*>(packets + s * stride);
-    for (int i = tid; i < (int)(stride / 4); i += 256) dst[i] = pkt[i];
+    uint8_t* pk = packets + s * stride;
+    const int kb = q4[0] ? 144 : 210, vb = q4[1] ? 144 : 210;
+    const int64_t v_offset = (int64_t)nsb * kb;
+    if (tid < kb) pk[(int64_t)j * kb + tid] = fb[0][tid];
+    if (tid < vb) pk[v_offset + (int64_t)j * vb + tid] = fb[1][tid];
+    if (j == 0)   // the packet's padding to 8 bytes
+        for (int64_t i = v_offset + (int64_t)nsb * vb + tid; i < stride; i += 256) pk[i] = 0;
 }
 
 }  // namespace rta
@@ -764,8 +643,9 @@ int rta_pack_history(const float* k, int k_stride, const float* v, int v_stride,
     if (kvw > 256 * kPackMaxBlocks) return RTA_ERR_RANGE;
     const int64_t stride = host::history_bytes(kvw);
     if (!host::aligned(packets, 8)) return RTA_ERR_ALIGN;
-    hipLaunchKernelGGL(pack_history_kernel, dim3(batch), dim3(256), 0, (hipStream_t)stream, k, k_stride, v, v_stride,
-                       kvw, fmt_k, fmt_v, slot, n_slots, stride, static_cast<uint8_t*>(packets));
+    hipLaunchKernelGGL(pack_history_kernel, dim3((kvw + 255) / 256, batch), dim3(256), 0, (hipStream_t)stream, k,
+                       k_stride, v, v_stride, kvw, fmt_k, fmt_v, slot, n_slots, stride,
+                       static_cast<uint8_t*>(packets));
     return hipGetLastError() == hipSuccess ? RTA_OK : RTA_ERR_LAUNCH;
 }
 

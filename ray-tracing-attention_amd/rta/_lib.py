@@ -54,6 +54,7 @@ SIGNATURES = {
     "rta_hybrid_layout": (_i, [_p, _i, _p, _p]),
     "rta_hybrid_init": (_i, [_p, _i, _p, _p, _p]),
     "rta_hybrid_decode_step": (_i, [_p, _p, _i, _p, _p, _p, _p, _sz, _p]),
+    "rta_hybrid_decode_step_capture": (_i, [_p, _p, _i, _p, _p, _p, _p, _p, _sz, _p]),
     "rta_pack": (_i, [_i, _p, _i, _i, _p, _p]),
     "rta_gemv_workspace_bytes": (_sz, [_i, _i, _i, _i]),
     "rta_gemv": (_i, [_i, _p, _i, _i, _p, _i, _p, _i, _p, _sz, _p]),

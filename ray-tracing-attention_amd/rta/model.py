@@ -42,6 +42,10 @@ class HybridViews(ctypes.Structure):
                 ("slots_per_layer", _i64)]
 
 
+class HybridCapture(ctypes.Structure):
+    _fields_ = [("residual", _p), ("kv", _p)]
+
+
 _SIGS = {
     "rta_hybrid_state_bytes": (ctypes.c_size_t, [ctypes.POINTER(HybridShape), _i]),
     "rta_hybrid_workspace_bytes": (ctypes.c_size_t, [ctypes.POINTER(HybridShape), _i]),
@@ -49,6 +53,8 @@ _SIGS = {
     "rta_hybrid_init": (_i, [ctypes.POINTER(HybridShape), _i, _p, _p, _p]),
     "rta_hybrid_decode_step": (_i, [ctypes.POINTER(HybridShape), ctypes.POINTER(HybridWeights), _i, _p, _p, _p, _p,
                                     ctypes.c_size_t, _p]),
+    "rta_hybrid_decode_step_capture": (_i, [ctypes.POINTER(HybridShape), ctypes.POINTER(HybridWeights), _i, _p, _p,
+                                            _p, ctypes.POINTER(HybridCapture), _p, ctypes.c_size_t, _p]),
 }
 
 
@@ -109,7 +115,8 @@ class DecodeModel:
     {"in", "o", "gate_up", "down", "ab"}; separate_ab keeps the delta-net a / b rows as
     matrices of their own (w_a, w_b); in_parts(l, full), when it returns a list of
     formats, splits the in-projection into that many parts of equal row counts
-    (matrices "<l>.w_in.<i>", each in its format).  self.fmts names each matrix's format."""
+    (matrices "<l>.w_in.<i>", each in its format), or, given (rows, format) pairs, into parts of
+    those row counts.  self.fmts names each matrix's format."""
 
     def __init__(self, shape, batch, ctx, seed=20261115, dev="cuda:0", keep_gguf=False, layer_fmts=None,
                  separate_ab=False, in_parts=None):
@@ -247,14 +254,20 @@ class DecodeModel:
         self.logits = None
 
     def _parts(self, L, l, fmts, rows, mat):
+        """fmts: a format per part (equal row counts) or (rows, format) pairs."""
         n = len(fmts)
-        assert 0 < n <= 4 and rows % (16 * n) == 0, (rows, n)
+        if all(isinstance(f, tuple) for f in fmts):
+            parts = list(fmts)
+        else:
+            assert rows % (16 * n) == 0, (rows, n)
+            parts = [(rows // n, f) for f in fmts]
+        assert 0 < n <= 4 and sum(r for r, _ in parts) == rows, (rows, parts)
         L.in_parts = n
         self.parts = getattr(self, "parts", {})
-        self.parts[l] = [(rows // n, f) for f in fmts]
-        for i, f in enumerate(fmts):
-            L.in_w[i] = mat(f, rows // n, self.shape.hidden, name=f"{l}.w_in.{i}").data_ptr()
-            L.in_rows[i], L.in_fmt[i] = rows // n, f
+        self.parts[l] = parts
+        for i, (r, f) in enumerate(parts):
+            L.in_w[i] = mat(f, r, self.shape.hidden, name=f"{l}.w_in.{i}").data_ptr()
+            L.in_rows[i], L.in_fmt[i] = r, f
 
     def _random_packets(self, pk, gen):
         """K (Q4_K) / V (Q6_K) history fields with random quants and sane block scales."""
@@ -279,15 +292,30 @@ class DecodeModel:
                     pk[:, o + 208:o + 210] = half()
         pk[:, nb * (kb + vb):] = 0   # the packet's padding to 8 bytes
 
-    def step(self, logits=False):
-        """One greedy decode step for every sequence (tokens and positions advance on the device)."""
+    def step(self, logits=False, capture=False):
+        """One greedy decode step for every sequence (tokens and positions advance on the device).
+        capture: also fill self.residual [layers + 1, B, hidden] (the embedding rows, then the
+        residual stream after each layer) and self.kv [full layers, B, 2, kv_heads * 128] (the
+        key and value rows each full layer packed into its history)."""
         if logits and self.logits is None:
             self.logits = torch.empty(self.batch, self.shape.vocab, dtype=torch.float32, device=self.dev)
-        check(self.lib.rta_hybrid_decode_step(ctypes.byref(self.shape), ctypes.byref(self.weights), self.batch,
-                                              self.state.data_ptr(), self.tokens.data_ptr(),
-                                              self.logits.data_ptr() if logits else None,
-                                              self.workspace.data_ptr(), self.ws_bytes, ops._stream()),
-              "rta_hybrid_decode_step")
+        lg = self.logits.data_ptr() if logits else None
+        if not capture:
+            check(self.lib.rta_hybrid_decode_step(ctypes.byref(self.shape), ctypes.byref(self.weights), self.batch,
+                                                  self.state.data_ptr(), self.tokens.data_ptr(), lg,
+                                                  self.workspace.data_ptr(), self.ws_bytes, ops._stream()),
+                  "rta_hybrid_decode_step")
+            return self.tokens
+        s = self.shape
+        nfull = s.layers // s.full_every if s.full_every else 0
+        self.residual = torch.full((s.layers + 1, self.batch, s.hidden), float("nan"), device=self.dev)
+        self.kv = torch.full((max(nfull, 1), self.batch, 2, s.kv_heads * s.head_dim), float("nan"), device=self.dev)
+        cap = HybridCapture(residual=self.residual.data_ptr(), kv=self.kv.data_ptr() if nfull else None)
+        check(self.lib.rta_hybrid_decode_step_capture(ctypes.byref(self.shape), ctypes.byref(self.weights),
+                                                      self.batch, self.state.data_ptr(), self.tokens.data_ptr(), lg,
+                                                      ctypes.byref(cap), self.workspace.data_ptr(), self.ws_bytes,
+                                                      ops._stream()),
+              "rta_hybrid_decode_step_capture")
         return self.tokens
 
     def weight_bytes(self):

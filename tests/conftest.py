@@ -42,6 +42,25 @@ def tolerance_ok(actual, expected, rel=1e-3, abs_=1e-5):
     return err <= abs_ + rel * peak, err / max(peak, 1e-30)
 
 
+def allclose_fraction(actual, expected, rel=1e-3, abs_=1e-5):
+    """Fraction of elements with |a - e| <= abs_ + rel |e| (numpy.allclose's test, per element),
+    reported beside the peak-relative bar."""
+    import numpy as np
+    a = np.asarray(actual, dtype=np.float64)
+    e = np.asarray(expected, dtype=np.float64)
+    if a.shape != e.shape or a.size == 0:
+        return 0.0 if a.shape != e.shape else 1.0
+    return float(np.mean(np.abs(a - e) <= abs_ + rel * np.abs(e)))
+
+
+def assert_close(got, ref, what, rel=1e-3, abs_=1e-5):
+    """The float bar of every GPU parity test (peak-relative, per tensor); the message also
+    gives the elementwise allclose(rel, abs_) pass fraction."""
+    ok, frac = tolerance_ok(got, ref, rel, abs_)
+    assert ok, (f"{what}: max|err|/peak = {frac:.3e}, elementwise allclose({rel:g}, {abs_:g}) pass fraction "
+                f"{allclose_fraction(got, ref, rel, abs_):.5f}")
+
+
 def check_margin_ids(logits_gpu, ids_gpu, logits_ref, margin):
     """ids equal the margin rule on the kernel's own logits, and the fp64 oracle's id unless
     a logit sits within rounding of the threshold."""

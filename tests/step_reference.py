@@ -1,23 +1,21 @@
 """The fp64 reference of one rta_hybrid_decode_step, composed from the oracle's
 restatements of every op, and the comparison of a model's steps with it.  Each step's
 reference starts from the GPU's state before that step, so float drift does not
-compound across steps; the new history packets are checked against the reference's
-keys and values to one quantisation step, the shifted conv windows bit exactly, the
-recurrent state, the new window entries, logits and next tokens to the float bar /
-the margin rule."""
+compound across steps.  The step runs with its capture on: the embedding rows are
+checked bit exactly and the residual stream after every layer to the float bar; the
+key and value rows each full layer quantised are checked against the reference's to
+the float bar, and the new history packets byte for byte against the oracle's packer
+(orc_pack_history, resident_history_quant.glsl:9-41) of those same rows.  The shifted
+conv windows are checked bit exactly; the recurrent state, the new window entries,
+logits and next tokens to the float bar / the margin rule."""
 import numpy as np
 
 import oracle as orc
-from conftest import tolerance_ok
+from conftest import assert_close
 
 REL, ABS = 1e-3, 1e-5
 f32 = np.float32
 Q4_K, Q6_K = orc.Q4_K, orc.Q6_K
-
-
-def assert_close(got, ref, what):
-    ok, frac = tolerance_ok(got, ref, REL, ABS)
-    assert ok, f"{what}: max|err|/peak = {frac:.3e}"
 
 
 def reference_step(m, tokens, ctx, rec, conv, packets_after):
@@ -35,6 +33,7 @@ def reference_step(m, tokens, ctx, rec, conv, packets_after):
         assert sum(r for r, _ in parts[l]) == rows
         return np.concatenate([gemv(f"{l}.w_in.{i}", r, D, x) for i, (r, _) in enumerate(parts[l])], axis=1)
     x = orc.embed(s.fmt_embed, g["embed"], s.vocab, D, tokens).astype(np.float64)
+    xs = [x.copy()]   # the residual stream: embedding rows, then after each layer
     new_rec, new_conv = rec.astype(np.float64).copy(), conv.copy()
     kv_new = []
     lf = lr = 0
@@ -87,24 +86,31 @@ def reference_step(m, tokens, ctx, rec, conv, packets_after):
         _, y = orc.mlp_swiglu((fmt(f"{l}.w_gate"), fmt(f"{l}.w_up"), fmt(f"{l}.w_down")), g[f"{l}.w_gate"],
                               g[f"{l}.w_up"], g[f"{l}.w_down"], D, s.ff, n.astype(f32))
         x = x + y
+        xs.append(x.copy())
     n = orc.rmsnorm(x.astype(f32), g["norm_final"], s.eps)
     logits = gemv("lm_head", s.vocab, D, n)
-    return logits, new_rec, new_conv, kv_new
+    return logits, new_rec, new_conv, kv_new, xs
 
 
 def check_steps(m, steps=2):
     shape, batch = m.shape, m.batch
     cap = shape.capacity
+    kvw = shape.kv_heads * 128
     for step in range(steps):
         tokens = m.tokens.cpu().numpy().view(np.uint32).copy()
         pos = m.state_view("ctx")
         rec, conv = m.state_view("recurrent"), m.state_view("conv")
-        m.step(logits=True)
+        m.step(logits=True, capture=True)
         got_tokens = m.tokens.cpu().numpy().view(np.uint32)
         got_logits = m.logits.cpu().numpy()
         packets = m.state_view("packets")
-        ref_logits, ref_rec, ref_conv, kv_new = reference_step(m, tokens, pos, rec, conv, packets)
+        ref_logits, ref_rec, ref_conv, kv_new, ref_x = reference_step(m, tokens, pos, rec, conv, packets)
         assert np.array_equal(m.state_view("ctx"), pos + 1)
+        res = m.residual.cpu().numpy()
+        assert np.array_equal(res[0], ref_x[0].astype(f32)), step   # embedding rows: exact
+        for l in range(1, shape.layers + 1):
+            for b in range(batch):
+                assert_close(res[l, b], ref_x[l][b], f"step {step} residual after layer {l - 1} row {b}")
         for b in range(batch):
             assert_close(got_logits[b], ref_logits[b], f"step {step} logits row {b}")
             assert int(got_tokens[b]) == orc.argmax_margin_f32(got_logits[b], 1e-4), (step, b)
@@ -112,14 +118,16 @@ def check_steps(m, steps=2):
         assert np.array_equal(got_conv[..., :2], ref_conv[..., :2]), step     # shifted window: exact
         assert_close(got_conv[..., 2], ref_conv[..., 2], f"step {step} conv window (new raw value)")
         assert_close(m.state_view("recurrent"), ref_rec, f"step {step} recurrent state")
-        # the new token's packet of each full layer holds the reference's k / v to one
-        # quantisation step of its group
-        kvw = shape.kv_heads * 128
+        # each full layer's new packet: the oracle's packer of the rows the step quantised,
+        # byte for byte; those rows: the reference's normed, rotated k and its v
+        kv = m.kv.cpu().numpy()
+        nb = orc.history_bytes(kvw)
         for lf, (k, v) in enumerate(kv_new):
             for b in range(batch):
-                pk = np.ascontiguousarray(packets[lf, b, pos[b] % cap])
-                kk = np.array([orc.lib().orc_packet_value(pk.ctypes.data, kvw, Q4_K, Q6_K, 0, c) for c in range(kvw)])
-                vv = np.array([orc.lib().orc_packet_value(pk.ctypes.data, kvw, Q4_K, Q6_K, 1, c) for c in range(kvw)])
-                for field, dec, q in ((k[b], kk, 15.0), (v[b], vv, 31.0)):
-                    step_ = 2.0 * np.abs(field).max() / q
-                    assert np.max(np.abs(dec - field)) <= step_ * 1.01, (step, lf, b)
+                assert_close(kv[lf, b, 0], k[b], f"step {step} full layer {lf} key row {b}")
+                assert_close(kv[lf, b, 1], v[b], f"step {step} full layer {lf} value row {b}")
+                want = orc.pack_history(kv[lf, b, 0], kv[lf, b, 1], shape.fmt_k, shape.fmt_v)
+                got = packets[lf, b, pos[b] % cap, :nb]
+                bad = np.flatnonzero(got != want)
+                assert bad.size == 0, (f"step {step} full layer {lf} row {b}: packet bytes differ at {bad[:8]} "
+                                       f"(got {got[bad[:8]]}, oracle {want[bad[:8]]})")

@@ -146,3 +146,59 @@ def test_read_ceiling_probe_loads_and_checks_arguments():
     assert f(FAKE_ODD, 1024, FAKE, 16, 0, None) == 2    # misaligned
     assert f(FAKE, 1024, FAKE, 0, 0, None) == 2         # no blocks
     assert f(FAKE, 1024, FAKE, 16, 4, None) == 2        # unknown variant
+
+
+def test_hybrid_shape_refuses_attention_the_kernels_do_not_serve(lib):
+    """The decode step checks its full layers' attention shape on the host, before it
+    advances any state: 16 query heads per kv head, a kv-head count whose thread split
+    exceeds a workgroup, and two Q6_K history fields (a packet holds one) are refused by
+    the size queries (0) and by the step itself with rta_decode_attention's codes."""
+    from rta import model
+    E = {"format": 3, "range": 7}
+    hybrid = model._lib_h()
+    cases = [({"kv_heads": 2}, E["range"]),                                   # G = 16
+             ({"q_heads": 64, "kv_heads": 64, "rec_heads": 64}, E["range"]),   # 64 x 8 threads > 256
+             ({"fmt_k": _lib.Q6_K, "fmt_v": _lib.Q6_K}, E["format"])]
+    for change, code in cases:
+        s = model.shape_9b(1024)
+        for k, v in change.items():
+            setattr(s, k, v)
+        assert hybrid.rta_hybrid_state_bytes(ctypes.byref(s), 4) == 0, change
+        assert hybrid.rta_hybrid_workspace_bytes(ctypes.byref(s), 4) == 0, change
+        w = model.HybridWeights(embed=FAKE.value, layers=ctypes.cast(FAKE.value, ctypes.POINTER(model.HybridLayer)),
+                                norm_final=FAKE.value, lm_head=FAKE.value)
+        assert hybrid.rta_hybrid_decode_step(ctypes.byref(s), ctypes.byref(w), 4, FAKE, FAKE, None, FAKE, 1 << 40,
+                                             None) == code, change
+    ok = model.shape_9b(1024)
+    assert hybrid.rta_hybrid_state_bytes(ctypes.byref(ok), 4) > 0
+    # a misaligned capture buffer is refused before any launch
+    cap = model.HybridCapture(residual=FAKE_ODD.value, kv=None)
+    need = hybrid.rta_hybrid_workspace_bytes(ctypes.byref(ok), 4)
+    w = model.HybridWeights(embed=FAKE.value, layers=ctypes.cast(FAKE.value, ctypes.POINTER(model.HybridLayer)),
+                            norm_final=FAKE.value, lm_head=FAKE.value)
+    assert hybrid.rta_hybrid_decode_step_capture(ctypes.byref(ok), ctypes.byref(w), 4, FAKE, FAKE, None,
+                                                 ctypes.byref(cap), FAKE, need, None) == 4
+
+
+def test_part_readout_workspace_is_not_monotonic_in_rows(lib):
+    """Why the decode step sizes its projection workspace over every in-projection part row
+    count: at 4096 columns and batch 32 a 7168-row Q4_K readout needs more workspace than
+    the whole 10240-row in-projection (fewer row tiles take more K slabs).  The step with
+    such parts runs in tests/test_gpu_sizes.py."""
+    assert lib.rta_gemv_workspace_bytes(_lib.Q4_K, 7168, 4096, 32) > lib.rta_gemv_workspace_bytes(_lib.Q4_K, 10240,
+                                                                                                    4096, 32)
+
+
+def test_image_readout_refusals(lib):
+    """rta_image_readout: the RMSNorm chunk sums cover at most 4096 columns; img and the
+    workspace must be 16-byte aligned, y 4-byte aligned (checked before any launch)."""
+    P = _lib.Q4_K | _lib.TILED
+    ns = ctypes.c_int(0)
+    R = lambda **k: lib.rta_image_readout(  # noqa: E731
+        P, 0, FAKE, None, 256, k.get("cols", 4096), k.get("img", FAKE), 4, k.get("ss", None), ctypes.c_float(1e-6),
+        k.get("y", FAKE), 1, k.get("ws", FAKE), 1 << 30, ctypes.byref(ns), None)
+    assert R(cols=8192, ss=FAKE) == 2          # shape: ss holds four 1024-column chunk sums
+    assert R(img=ctypes.c_void_p(FAKE.value + 8)) == 4
+    assert R(ws=ctypes.c_void_p(FAKE.value + 8)) == 4
+    assert R(y=FAKE_ODD) == 4
+    assert R(ss=ctypes.c_void_p(FAKE.value + 4)) == 4

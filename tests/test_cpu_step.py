@@ -65,7 +65,7 @@ def test_cpu_step_matches_fp64_composition():
         rec0, conv0, ctx0, tok0 = rec.copy(), conv.copy(), ctx.copy(), tokens.copy()
         logits = np.empty((B, shape.vocab), np.float32)
         cpu.step(B, rec, conv, packets, ctx, tokens, logits, threads=4)
-        ref_logits, ref_rec, ref_conv, _ = reference_step(m, tok0, ctx0, rec0, conv0, packets)
+        ref_logits, ref_rec, ref_conv, _, _ = reference_step(m, tok0, ctx0, rec0, conv0, packets)
         assert np.array_equal(ctx, ctx0 + 1)
         for b in range(B):
             ok, frac = tolerance_ok(logits[b], ref_logits[b])

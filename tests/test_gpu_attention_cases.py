@@ -21,7 +21,7 @@ import numpy as np
 import pytest
 
 import oracle as orc
-from conftest import tolerance_ok
+from conftest import assert_close
 from rta import ops, synth
 
 pytestmark = pytest.mark.gpu
@@ -38,11 +38,6 @@ def torch_dev():
 
 def to_dev(torch, a, dev):
     return torch.from_numpy(np.ascontiguousarray(a)).to(dev)
-
-
-def assert_close(got, ref, what):
-    ok, frac = tolerance_ok(got, ref, REL, ABS)
-    assert ok, f"{what}: max|err|/peak = {frac:.3e}"
 
 
 # ----------------------------------------------------- the verifier's cases ----
@@ -286,3 +281,25 @@ def test_ring_wrap_matrix_core_layout(torch_dev):
     """A ring of 300 slots below contexts of 600 / 1000 on the K Q4_K / V Q6_K kernel."""
     torch, dev = torch_dev
     _sized_case(torch, dev, 57, [600, 1000, 90, 4000], 16, 4, (orc.Q4_K, orc.Q6_K), capacity=300)
+
+
+@pytest.mark.parametrize("fmts", LAYOUTS)
+@pytest.mark.parametrize("nseq", [65, 200])
+def test_more_than_64_sequences(torch_dev, fmts, nseq):
+    """Above 64 sequences the matrix-core kernels read their tile list from the plan a
+    separate pass writes (Q6_K keys: attn_plan_kernel; Q4_K keys: the multi-wave scan of
+    attn_plan_wave) instead of the one each wave builds in registers.  Mixed contexts,
+    including 1, 64, 65 and several chunks."""
+    torch, dev = torch_dev
+    ctx = np.random.default_rng(60 + nseq).integers(1, 2500, nseq)
+    ctx[:5] = [1, 64, 65, 4097, 2]
+    ctx[-3:] = [1, 64, 65]
+    _sized_case(torch, dev, 61 + nseq, ctx, 16, 4, fmts, gate=True)
+
+
+def test_more_than_64_sequences_decode_step_heads(torch_dev):
+    """300 sequences at the decode step's 32 / 8 heads (K Q4_K / V Q6_K)."""
+    torch, dev = torch_dev
+    ctx = np.random.default_rng(62).integers(1, 900, 300)
+    ctx[:3] = [1, 64, 65]
+    _sized_case(torch, dev, 63, ctx, 32, 8, (orc.Q4_K, orc.Q6_K))

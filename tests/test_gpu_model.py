@@ -87,3 +87,21 @@ def test_hybrid_decode_steps_exported_layout(batch):
     m = model.DecodeModel(shape, batch, ctx, seed=11 + batch, keep_gguf=True, layer_fmts=_exporter_fmts,
                           separate_ab=True)
     check_steps(m, 2)
+
+
+# Both history field orders (the reference's K Q4_K / V Q6_K and the swapped K Q6_K / V
+# Q4_K) and an odd kv-head count (3 heads: the second superblock of each field half
+# zeros): every step's packets byte for byte against the oracle's packer of the rows the
+# step quantised (step_reference.check_steps).
+@pytest.mark.parametrize("fmt_k,hq,hkv", [("Q6_K", 4, 2), ("Q4_K", 6, 3), ("Q6_K", 6, 3)])
+def test_hybrid_decode_steps_history_layouts(fmt_k, hq, hkv):
+    from rta import model
+    from rta._lib import Q4_K, Q6_K, TILED
+    fk = Q4_K if fmt_k == "Q4_K" else Q6_K
+    fv = Q6_K if fk == Q4_K else Q4_K
+    shape = model.HybridShape(hidden=512, layers=4, full_every=2, q_heads=hq, kv_heads=hkv, head_dim=128,
+                              rec_heads=2, ff=512, vocab=3001, capacity=64, fmt_embed=Q4_K, fmt_proj=Q4_K | TILED,
+                              fmt_lm=Q6_K | TILED, fmt_k=fk, fmt_v=fv, rope_rotary=128, eps=1e-6, margin=1e-4,
+                              rope_theta=1e6)
+    m = model.DecodeModel(shape, 5, [3, 40, 64, 65, 100], seed=41 + hkv, keep_gguf=True)
+    check_steps(m, 2)

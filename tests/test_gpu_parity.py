@@ -6,7 +6,7 @@ import numpy as np
 import pytest
 
 import oracle as orc
-from conftest import check_margin_ids, tolerance_ok
+from conftest import assert_close, check_margin_ids
 from rta import ops, synth
 
 pytestmark = pytest.mark.gpu
@@ -21,11 +21,6 @@ def torch_dev():
 
 def to_dev(torch, a, dev):
     return torch.from_numpy(np.ascontiguousarray(a)).to(dev)
-
-
-def assert_close(got, ref, what):
-    ok, frac = tolerance_ok(got, ref, REL, ABS)
-    assert ok, f"{what}: max|err|/peak = {frac:.3e}"
 
 
 def _bits(a):

@@ -2,7 +2,10 @@
 151936-word vocabulary at batch 4 and 16 (row and packed layouts) and the packed
 151936 x 4096 LM head of the 9B decode step at batch 32; and the decode step itself at
 the 9B widths (hidden 4096, 32 / 8 heads, 32 delta-net heads, FF 12288, vocab 151936,
-batch 32, contexts U[256, 8192]) with four layers (three recurrent, one full).
+contexts U[256, 8192]) with four layers (three recurrent, one full): at batch 32 over
+packed weights, at batch 1 over GGUF rows (the RMSNorm fused into the readouts' x
+staging, the 151936 x 4096 LM head with its group maxima), and at batch 32 with the
+exporter's in-projection parts of uneven row counts.
 
 Bars: logits within max|gpu - ref| <= 1e-5 + 1e-3 max|ref| per row against the fp64
 oracle; ids exactly the margin rule on the kernel's logits and the oracle's id unless
@@ -11,7 +14,7 @@ import numpy as np
 import pytest
 
 import oracle as orc
-from conftest import check_margin_ids, tolerance_ok
+from conftest import assert_close, check_margin_ids
 from rta import model, ops
 from rta._lib import Q4_K, Q6_K, TILED
 from step_reference import check_steps
@@ -24,11 +27,6 @@ REL, ABS = 1e-3, 1e-5
 def torch_dev():
     import torch
     return torch, torch.device("cuda:0")
-
-
-def assert_close(got, ref, what):
-    ok, frac = tolerance_ok(got, ref, REL, ABS)
-    assert ok, f"{what}: max|err|/peak = {frac:.3e}"
 
 
 def _lm_head_case(torch, dev, vocab, hidden, batch, packed, seed):
@@ -64,3 +62,30 @@ def test_decode_step_9b_widths():
     ctx = np.random.default_rng(20261115).integers(256, 8193, 32)
     m = model.DecodeModel(shape, 32, ctx.tolist(), seed=20261115, keep_gguf=True)
     check_steps(m, 2)
+
+
+def test_decode_step_9b_widths_batch1():
+    """The batch-1 step as the metric runs it: GGUF-row readouts (gemv_b1_kernel with the
+    RMSNorm fused into x staging at 4096 columns, the 3-wave rows of the 12288-column down
+    projection with the accumulate epilogue, the 151936 x 4096 LM head)."""
+    shape = model.shape_9b(capacity=8448, packed=False)
+    shape.layers = 4
+    ctx = np.random.default_rng(20261116).integers(256, 8193, 1)
+    m = model.DecodeModel(shape, 1, ctx.tolist(), seed=20261116, keep_gguf=True)
+    check_steps(m, 2)
+
+
+def test_decode_step_9b_widths_uneven_in_projection_parts():
+    """In-projection parts of uneven row counts at the 9B widths and batch 32: the full
+    layers' q | k | v | gate rows as 7168 Q4_K rows and 3072 Q6_K rows.  A 7168-row readout
+    needs more workspace than the whole 10240-row one (fewer row tiles take more K slabs);
+    the step's workspace covers every part row count."""
+    shape = model.shape_9b(capacity=8448, packed=True)
+    shape.layers, shape.attn_gate, shape.layer_formats = 4, 1, 1
+    ctx = np.random.default_rng(20261117).integers(256, 8193, 32)
+    fmts = lambda l, full: {"in": Q4_K | TILED, "o": Q4_K | TILED, "gate_up": Q4_K | TILED,  # noqa: E731
+                            "down": Q4_K | TILED, "ab": Q4_K | TILED}
+    parts = lambda l, full: [(7168, Q4_K), (3072, Q6_K)] if full else None  # noqa: E731
+    m = model.DecodeModel(shape, 32, ctx.tolist(), seed=20261117, keep_gguf=True, layer_fmts=fmts,
+                          in_parts=parts)
+    check_steps(m, 1)

@@ -6,7 +6,7 @@ import numpy as np
 import pytest
 
 import oracle as orc
-from conftest import tolerance_ok
+from conftest import assert_close
 from rta import ops, synth
 
 pytestmark = pytest.mark.gpu
@@ -21,11 +21,6 @@ def torch_dev():
 
 def to_dev(torch, a, dev):
     return torch.from_numpy(np.ascontiguousarray(a)).to(dev)
-
-
-def assert_close(got, ref, what):
-    ok, frac = tolerance_ok(got, ref, REL, ABS)
-    assert ok, f"{what}: max|err|/peak = {frac:.3e}"
 
 
 @pytest.mark.parametrize("fmt", [orc.Q4_K, orc.Q6_K, orc.F16])
@@ -175,13 +170,15 @@ def test_pack_history_bad_slot(torch_dev):
     assert got[1].any() and not got[0].any() and not got[2].any()
 
 
+@pytest.mark.parametrize("which", ["mixed", "one_signed"])
 @pytest.mark.parametrize("fmts", [(orc.Q4_K, orc.Q6_K), (orc.Q6_K, orc.Q4_K)])
-def test_pack_history_known_answer(torch_dev, fmts):
+def test_pack_history_known_answer(torch_dev, fmts, which):
     """The HIP packer writes the hand-built packet bytes (exact d / dmin from /63 and /127,
-    scale code 127, round to nearest with .5 ties to even) in both field orders."""
-    from known_answers import known_answer_fields
+    scale code 127, round to nearest with .5 ties to even; Q4_K groups entirely above or
+    below zero with lo / hi started at 0) in both field orders."""
+    from known_answers import known_answer_fields, one_signed_fields
     torch, dev = torch_dev
-    k, v, expected = known_answer_fields()
+    k, v, expected = known_answer_fields() if which == "mixed" else one_signed_fields()
     if fmts[0] == orc.Q6_K:   # swapped: the Q6_K row is the K field
         k, v = v, k
         expected = np.concatenate([expected[144:354], expected[:144], expected[354:]])

@@ -6,7 +6,7 @@ import numpy as np
 import pytest
 
 import oracle as orc
-from conftest import tolerance_ok
+from conftest import assert_close
 from rta import ops, synth
 from rta._lib import TILED
 
@@ -22,11 +22,6 @@ def torch_dev():
 
 def to_dev(torch, a, dev):
     return torch.from_numpy(np.ascontiguousarray(a)).to(dev)
-
-
-def assert_close(got, ref, what):
-    ok, frac = tolerance_ok(got, ref, REL, ABS)
-    assert ok, f"{what}: max|err|/peak = {frac:.3e}"
 
 
 def np_pack(fmt, w, rows, cols):

@@ -309,6 +309,20 @@ def test_packer_known_answer_bytes():
     assert np.array_equal(sw[:210], expected[144:354]) and np.array_equal(sw[210:354], expected[:144])
 
 
+def test_packer_one_signed_groups_known_answer_bytes():
+    """Q4_K groups entirely above or below zero keep lo / hi started at 0
+    (resident_history_quant.glsl:14-15): all-positive groups get minimum code 0 and the span
+    [0, max], all-negative ones the span [min, 0].  A packer taking the true group min / max
+    changes the scale and minimum codes and fails."""
+    from known_answers import one_signed_fields
+    k, v, expected = one_signed_fields()
+    got = orc.pack_history(k, v, orc.Q4_K, orc.Q6_K)
+    diff = np.nonzero(got != expected)[0]
+    assert diff.size == 0, f"bytes differ at {diff[:16]}"
+    sw = orc.pack_history(v, k, orc.Q6_K, orc.Q4_K)
+    assert np.array_equal(sw[:210], expected[144:354]) and np.array_equal(sw[210:354], expected[:144])
+
+
 def test_packer_rounds_d_to_binary16_before_the_codes():
     """The block scale is rounded to binary16 before the group codes are formed
     (resident_history_quant.glsl:22 then :27): group ranges 1.0 and 0.5 give
