@@ -26,6 +26,7 @@ extern "C" {
 #endif
 
 typedef void* rta_stream_t; /* hipStream_t */
+typedef void* rta_event_t;  /* hipEvent_t */
 
 enum rta_status {
     RTA_OK = 0,
@@ -448,22 +449,34 @@ int rta_hybrid_decode_step(const rta_hybrid_shape* shape, const rta_hybrid_weigh
                            uint32_t* tokens, float* logits_out, void* workspace, size_t workspace_bytes,
                            rta_stream_t stream);
 
-/* What a step can copy out besides its tokens and logits (device pointers, NULL: not
- * captured). */
+/* What a step can copy out or mark besides its tokens and logits (NULL: not captured). */
 typedef struct rta_hybrid_capture {
-    float* residual;   /* [layers + 1][batch][hidden]: the embedding rows, then the residual
-                          stream after each layer's MLP -- the reference's layer capture
-                          (debug 1: the state snapshot after executeMLP,
-                          optical_resident.cpp:481, returned by prefill,
-                          resident_runtime.py:136-139) */
-    float* kv;         /* [full layer][batch][2][kv_heads * 128]: the normed, rotated key row
-                          and the value row each full layer quantises into its history
-                          packet (op 34's input, resident_history_quant.glsl:5) */
+    float* residual;    /* device [layers + 1 - residual_from][batch][hidden]: residual row
+                           blocks residual_from .. layers, block 0 being the embedding rows and
+                           block l + 1 the residual stream after layer l's MLP -- the
+                           reference's layer capture (debug 1: the state snapshot after
+                           executeMLP, optical_resident.cpp:481, returned by prefill and
+                           generation, resident_runtime.py:136-139,199) */
+    int residual_from;  /* 0 .. layers (layers: only the state after the last layer) */
+    float* kv;          /* device [full layer][batch][2][kv_heads * 128]: the normed, rotated key
+                           row and the value row each full layer quantises into its history
+                           packet (op 34's input, resident_history_quant.glsl:5) */
+    rta_event_t* marks; /* host array of layers * 7 + 4 events, recorded on the stream at the
+                           reference's profile points (debug 2, optical_resident.cpp:450,455-481,
+                           522-530): per layer l, marks 7l + 0 .. 6 = layer start | after the
+                           in-projection and (full) QK-norm, RoPE and history pack | (1-4 equal:
+                           no BVH update, trace or payload here) | after the detector (full:
+                           attention; recurrent: gates, conv, delta rule and gated norm, one
+                           kernel) | after the O projection and MLP; then 7 layers + 0 .. 3 =
+                           LM head start (after the final norm) | (same) | after the readout |
+                           after the argmax.  NULL entries are skipped; an event repeated at
+                           consecutive marks is recorded once (its stages then read 0 ms) */
 } rta_hybrid_capture;
 
-/* rta_hybrid_decode_step that also fills the capture buffers (replaces the debug-1
- * capture path of Resident::layer, optical_resident.cpp:481,609-686).  capture NULL or
- * with both pointers NULL: exactly rta_hybrid_decode_step. */
+/* rta_hybrid_decode_step that also fills the capture buffers and records the marks
+ * (replaces the debug-1 capture and debug-2 profile paths of Resident::layer / word,
+ * optical_resident.cpp:450,481,522,609-686,849-853).  capture NULL or with every pointer
+ * NULL: exactly rta_hybrid_decode_step. */
 int rta_hybrid_decode_step_capture(const rta_hybrid_shape* shape, const rta_hybrid_weights* weights, int batch,
                                    void* state, uint32_t* tokens, float* logits_out,
                                    const rta_hybrid_capture* capture, void* workspace, size_t workspace_bytes,

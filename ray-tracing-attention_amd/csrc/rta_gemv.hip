@@ -937,7 +937,7 @@ namespace rta {
 
 int lm_head_rownorm(int fmt, const void* w, int vocab, int hidden, const float* h, int batch, float margin,
                     float* logits, uint32_t* ids, void* workspace, size_t workspace_bytes, hipStream_t s,
-                    const RowNorm& rn, const XNorm& xn) {
+                    const RowNorm& rn, const XNorm& xn, hipEvent_t readout_done) {
     int rc = check_matrix(fmt, w, vocab, hidden);
     if (rc) return rc;
     if (!h || !logits || !ids) return RTA_ERR_NULL;
@@ -963,6 +963,7 @@ int lm_head_rownorm(int fmt, const void* w, int vocab, int hidden, const float* 
                                      logits + (int64_t)b0 * vocab, partial + (int64_t)b0 * vocab, &ntasks, &rpt,
                                      scratch, mma, s, batch, rc_rn, xn);
         if (rc) return rc;
+        if (readout_done && b0 + chunk == batch && hipEventRecord(readout_done, s) != hipSuccess) return RTA_ERR_LAUNCH;
         // many small tasks: their group maxima go into the maxima region after the tasks'
         // (the chunk's [chunk][ntasks] task maxima leave chunk x (vocab - ntasks) floats)
         const int ngroups = (ntasks + kWave - 1) / kWave;

@@ -32,10 +32,11 @@ bool b1_norm_fusable(int fmt, int cols, int batch);
 int projection_store(int fmt, const void* w, int rows, int cols, const float* x, int batch, float* y, void* ws,
                      size_t ws_bytes, hipStream_t s, const RowNorm& rn, const XNorm& xn = XNorm{});
 
-// rta_lm_head with a deferred RMSNorm factor per batch row.
+// rta_lm_head with a deferred RMSNorm factor per batch row; readout_done (optional) is
+// recorded after the last batch tile's readout, before its argmax.
 int lm_head_rownorm(int fmt, const void* w, int vocab, int hidden, const float* h, int batch, float margin,
                     float* logits, uint32_t* ids, void* workspace, size_t workspace_bytes, hipStream_t s,
-                    const RowNorm& rn, const XNorm& xn = XNorm{});
+                    const RowNorm& rn, const XNorm& xn = XNorm{}, hipEvent_t readout_done = nullptr);
 
 // The fused gate/up projection of the SwiGLU MLP alone: act = swiglu(Wg x, Wu x).
 int swiglu_activation(int fmt, const void* wg, const void* wu, int inter, int hidden, const float* x, int batch,

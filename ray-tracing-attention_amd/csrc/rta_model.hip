@@ -300,6 +300,8 @@ int rta_hybrid_decode_step_capture(const rta_hybrid_shape* shape, const rta_hybr
     if (workspace_bytes < rta_hybrid_workspace_bytes(shape, batch)) return RTA_ERR_WORKSPACE;
     if (!host::aligned(state, 256) || !host::aligned(workspace, 256)) return RTA_ERR_ALIGN;
     if (capture && !(host::aligned(capture->residual, 4) && host::aligned(capture->kv, 4))) return RTA_ERR_ALIGN;
+    if (capture && capture->residual && (capture->residual_from < 0 || capture->residual_from > shape->layers))
+        return RTA_ERR_RANGE;
     const Dims d = dims_of(shape, batch);
     const State st = carve_state(d, state, nullptr);
     Work w = carve_work(shape, d, workspace, nullptr);
@@ -322,15 +324,22 @@ int rta_hybrid_decode_step_capture(const rta_hybrid_shape* shape, const rta_hybr
     // Layer capture: the residual stream after layer l is whole once the next norm has
     // added the last projection's pending K slabs, so it is copied right after that norm.
     float* cap_res = capture ? capture->residual : nullptr;
+    const int cap_from = capture ? capture->residual_from : 0;
     float* cap_kv = capture ? capture->kv : nullptr;
     int cap_due = -1;   // residual row block still to copy (0: the embedding rows)
     auto capture_residual = [&]() -> int {
-        if (!cap_res || cap_due < 0) return RTA_OK;
+        if (!cap_res || cap_due < cap_from) return RTA_OK;
         const size_t n = (size_t)B * d.D;
-        const hipError_t e = hipMemcpyAsync(cap_res + (size_t)cap_due * n, w.hidden, n * sizeof(float),
+        const hipError_t e = hipMemcpyAsync(cap_res + (size_t)(cap_due - cap_from) * n, w.hidden, n * sizeof(float),
                                             hipMemcpyDeviceToDevice, s);
         cap_due = -1;
         return e == hipSuccess ? RTA_OK : RTA_ERR_LAUNCH;
+    };
+    // the profile marks (events recorded between the stages)
+    rta_event_t* marks = capture ? capture->marks : nullptr;
+    auto mark = [&](int i) -> int {   // an event repeated at consecutive marks is recorded once
+        if (!marks || !marks[i] || (i > 0 && marks[i] == marks[i - 1])) return RTA_OK;
+        return hipEventRecord((hipEvent_t)marks[i], s) == hipSuccess ? RTA_OK : RTA_ERR_LAUNCH;
     };
     cap_due = 0;
     RTA_TRY(capture_residual());
@@ -421,6 +430,7 @@ int rta_hybrid_decode_step_capture(const rta_hybrid_shape* shape, const rta_hybr
     int lf = 0, lr = 0;
     for (int l = 0; l < d.L; ++l) {
         const rta_hybrid_layer& lw = weights->layers[l];
+        RTA_TRY(mark(7 * l));
         const int fi = fmt_of(lw.fmt_in), fo = fmt_of(lw.fmt_o), fgu = fmt_of(lw.fmt_gate_up),
                   fd = fmt_of(lw.fmt_down);
         if (is_full(shape, l)) {
@@ -449,11 +459,13 @@ int rta_hybrid_decode_step_capture(const rta_hybrid_shape* shape, const rta_hybr
                                       d.rows_full, shape->fmt_k, shape->fmt_v, w.slots + (size_t)lf * B,
                                       (int64_t)B * d.cap, packets, w.visible, d.cap, d.cap, w.attn_ws,
                                       cap_kv ? cap_kv + (size_t)lf * B * 2 * d.kvw : nullptr, s));
+            for (int k = 1; k <= 4; ++k) RTA_TRY(mark(7 * l + k));
             RTA_TRY(decode_attention_gate_stride(w.q, B, d.hq, d.hkv, d.hd, packets, shape->fmt_k, shape->fmt_v,
                                                  st.base + (size_t)lf * B, w.visible, d.cap, (int64_t)B * d.cap,
                                                  d.cap, gate, d.rows_full, w.mix, nullptr, nullptr, w.attn_ws,
                                                  w.attn_bytes, stream, shape->o_axis_remap ? shape->rope_rotary : 0,
                                                  true));
+            RTA_TRY(mark(7 * l + 5));
             RTA_TRY(residual_proj(fo, lw.w_o, d.hq * d.hd, w.mix));
             ++lf;
         } else {
@@ -496,11 +508,13 @@ int rta_hybrid_decode_step_capture(const rta_hybrid_shape* shape, const rta_hybr
                 RTA_TRY(rta_gemv(fab, lw.w_a, d.H, d.D, w.normed, B, w.ext_a, RTA_EPI_STORE, ws2, ws2_bytes, stream));
                 RTA_TRY(rta_gemv(fab, lw.w_b, d.H, d.D, w.normed, B, w.ext_b, RTA_EPI_STORE, ws2, ws2_bytes, stream));
             }
+            for (int k = 1; k <= 4; ++k) RTA_TRY(mark(7 * l + k));
             RTA_TRY(recurrent_mix(slabs ? static_cast<const float*>(w.gemm_ws) : w.proj, (int64_t)kSlabBatch * rows,
                                   rows, slabs ? ns : 1, d.KH, ext ? w.ext_a : nullptr, ext ? w.ext_b : nullptr, d.H,
                                   rn, st.conv + (size_t)lr * B * 3 * d.S * 3, lw.conv_w, lw.a_log, lw.dt_bias,
                                   st.rec + (size_t)lr * B * d.H * d.hd * d.hd, lw.out_norm, B, d.H, eps, w.mix, d.S,
                                   s));
+            RTA_TRY(mark(7 * l + 5));
             RTA_TRY(residual_proj(fo, lw.w_o, d.S, w.mix));
             ++lr;
         }
@@ -527,6 +541,7 @@ int rta_hybrid_decode_step_capture(const rta_hybrid_shape* shape, const rta_hybr
                                       w.gemm_ws, w.gemm_bytes, s, rn, xn));
         }
         if (!down_done) RTA_TRY(residual_proj(fd, lw.w_down, d.FF, w.act));
+        RTA_TRY(mark(7 * l + 6));
         cap_due = l + 1;
     }
     // op 1 index 2, then the readout (Resident::word): logits and the next tokens; the
@@ -549,8 +564,13 @@ int rta_hybrid_decode_step_capture(const rta_hybrid_shape* shape, const rta_hybr
         pending = 0;
         RTA_TRY(capture_residual());
     }
+    RTA_TRY(mark(7 * d.L));
+    RTA_TRY(mark(7 * d.L + 1));
     RTA_TRY(lm_head_rownorm(shape->fmt_lm, weights->lm_head, d.V, d.D, xn.w ? w.hidden : w.normed, B, shape->margin,
-                            logits_out ? logits_out : w.logits, tokens, w.lm_ws, w.lm_bytes, s, rn, xn));
+                            logits_out ? logits_out : w.logits, tokens, w.lm_ws, w.lm_bytes, s, rn, xn,
+                            marks && marks[7 * d.L + 2] != marks[7 * d.L + 1] ? (hipEvent_t)marks[7 * d.L + 2]
+                                                                               : nullptr));
+    RTA_TRY(mark(7 * d.L + 3));
 #undef RTA_TRY
     return RTA_OK;
 }

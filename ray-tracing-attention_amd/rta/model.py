@@ -43,7 +43,7 @@ class HybridViews(ctypes.Structure):
 
 
 class HybridCapture(ctypes.Structure):
-    _fields_ = [("residual", _p), ("kv", _p)]
+    _fields_ = [("residual", _p), ("residual_from", _i), ("kv", _p), ("marks", ctypes.POINTER(_p))]
 
 
 _SIGS = {
@@ -310,7 +310,8 @@ class DecodeModel:
         nfull = s.layers // s.full_every if s.full_every else 0
         self.residual = torch.full((s.layers + 1, self.batch, s.hidden), float("nan"), device=self.dev)
         self.kv = torch.full((max(nfull, 1), self.batch, 2, s.kv_heads * s.head_dim), float("nan"), device=self.dev)
-        cap = HybridCapture(residual=self.residual.data_ptr(), kv=self.kv.data_ptr() if nfull else None)
+        cap = HybridCapture(residual=self.residual.data_ptr(), residual_from=0,
+                            kv=self.kv.data_ptr() if nfull else None, marks=None)
         check(self.lib.rta_hybrid_decode_step_capture(ctypes.byref(self.shape), ctypes.byref(self.weights),
                                                       self.batch, self.state.data_ptr(), self.tokens.data_ptr(), lg,
                                                       ctypes.byref(cap), self.workspace.data_ptr(), self.ws_bytes,

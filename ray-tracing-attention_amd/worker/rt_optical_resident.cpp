@@ -147,6 +147,57 @@ struct Timer {
     }
 };
 
+// The debug-2 profile of generation: events at the decode step's stage marks
+// (rta_hybrid_capture.marks: 7 per layer, then 4 around the LM head), read back after
+// each step into the reference's ten stage sums and two detector sums
+// (optical_resident.cpp:849-853; names at resident_runtime.py:195,229-231).
+struct Profile {
+    std::vector<hipEvent_t> ev;
+    std::vector<rta_event_t> marks;
+    double parts[10] = {};
+    double detector[2] = {};   // (attention, recurrent)
+    Profile() = default;
+    Profile(const Profile&) = delete;
+    Profile& operator=(const Profile&) = delete;
+    ~Profile() {
+        for (hipEvent_t e : ev) (void)hipEventDestroy(e);
+    }
+    // one event per distinct point: marks 1-4 of a layer and the LM head's first two
+    // coincide here (no BVH update, history trace, payload or vocabulary trace), and an
+    // event repeated at consecutive marks is recorded once, so those stages read 0
+    void start(int layers) {
+        if (ev.empty()) {
+            ev.resize((size_t)layers * 7 + 4);
+            for (hipEvent_t& e : ev) hip_check(hipEventCreate(&e), "hipEventCreate");
+            marks.assign(ev.begin(), ev.end());
+            for (int l = 0; l < layers; ++l)
+                for (int k = 2; k <= 4; ++k) marks[7 * l + k] = ev[7 * l + 1];
+            marks[7 * layers + 1] = ev[7 * layers];
+        }
+        std::fill(parts, parts + 10, 0.0);
+        detector[0] = detector[1] = 0.0;
+    }
+    double span(int a, int b) const {
+        if (marks[a] == marks[b]) return 0.0;
+        float ms = 0.0f;
+        hip_check(hipEventElapsedTime(&ms, (hipEvent_t)marks[a], (hipEvent_t)marks[b]), "hipEventElapsedTime");
+        return ms;
+    }
+    // one completed step: projection geometry, BVH update, history trace, coordinate
+    // restore, detector, output MLP per layer; the vocabulary and its three parts
+    void add(int layers, int full_every) {
+        for (int l = 0; l < layers; ++l) {
+            const int b = 7 * l;
+            for (int j = 0; j < 6; ++j) parts[j] += span(b + j, b + j + 1);
+            const bool full = full_every > 0 && l % full_every == full_every - 1;
+            detector[full ? 0 : 1] += span(b + 4, b + 5);
+        }
+        const int w = 7 * layers;
+        parts[6] += span(w, w + 3);
+        for (int j = 0; j < 3; ++j) parts[7 + j] += span(w + j, w + j + 1);
+    }
+};
+
 double wall_ms(std::chrono::steady_clock::time_point t0) {
     return std::chrono::duration<double, std::milli>(std::chrono::steady_clock::now() - t0).count();
 }
@@ -168,6 +219,7 @@ struct Decoder {
     std::vector<std::unique_ptr<Device>> mem;
     std::unique_ptr<Device> state;
     Device ws, tokens, prompt, zero_ctx;
+    Device last;   // the residual stream after the last layer of the latest step
     size_t ws_bytes = 0;
 
     const void* put(const void* host, size_t bytes) {
@@ -386,6 +438,7 @@ struct Decoder {
         weights.norm_final = vec(a, -1, 4, D);
         weights.layers = layers.data();
         tokens.ensure(256);
+        last.ensure((size_t)D * 4);
         int32_t zero = 0;
         zero_ctx.ensure(256);
         hip_check(hipMemcpy(zero_ctx.p, &zero, 4, hipMemcpyHostToDevice), "upload");
@@ -408,10 +461,22 @@ struct Decoder {
         rta_check(rta_hybrid_init(&shape, 1, state->p, zero_ctx.as<int32_t>(), s), "rta_hybrid_init");
     }
 
-    // one step: tokens[0] in, the greedy next token out
-    void step(hipStream_t s) {
-        rta_check(rta_hybrid_decode_step(&shape, &weights, 1, state->p, tokens.as<uint32_t>(), nullptr, ws.p, ws_bytes, s),
-                  "rta_hybrid_decode_step");
+    // one step: tokens[0] in, the greedy next token out.  The residual stream after the
+    // last layer goes to `last` (the state a debug-1 generation reply carries); with `all`
+    // every layer's as well ([layers + 1][hidden], the embedding first); with `marks` the
+    // stage events of a debug-2 profile are recorded.
+    void step(hipStream_t s, float* all = nullptr, rta_event_t* marks = nullptr) {
+        rta_hybrid_capture cap{};
+        cap.residual = all ? all : last.as<float>();
+        cap.residual_from = all ? 0 : shape.layers;
+        cap.marks = marks;
+        rta_check(rta_hybrid_decode_step_capture(&shape, &weights, 1, state->p, tokens.as<uint32_t>(), nullptr, &cap,
+                                                 ws.p, ws_bytes, s),
+                  "rta_hybrid_decode_step_capture");
+        if (all)
+            hip_check(hipMemcpyAsync(last.p, all + (size_t)shape.layers * shape.hidden, (size_t)shape.hidden * 4,
+                                     hipMemcpyDeviceToDevice, s),
+                      "copy state");
     }
 
     // the history ring grows to `next` slots; recurrent, conv and packet state are kept
@@ -454,7 +519,8 @@ struct Worker {
     uint32_t control[8] = {0, 0, 1, 0, 0xffffffffu, 0xffffffffu, 0, 0};   // (resident_math.comp:130)
     uint64_t position = 0;                            // absolute position (emitted tokens count)
     std::map<int, std::unique_ptr<Device>> uploads;   // (layer, index) -> device payload
-    Device ws, x, act, y, logits, ids, rows, q, kbuf, vbuf, gate, out, m, z, packets, slots, ctx, rec;
+    Device ws, x, act, y, logits, ids, rows, q, kbuf, vbuf, gate, out, m, z, packets, slots, ctx, rec, layers_cap;
+    Profile profile;
 
     ~Worker() {
         if (asset) rta_asset_close(asset);
@@ -507,11 +573,18 @@ struct Worker {
         y.ensure((size_t)count * D * 4);
         const size_t wsb = rta_mlp_workspace_bytes((int)g.fmt, (int)d.fmt, (int)D, (int)F, (int)count);
         ws.ensure(wsb);
+        if (g.fmt != u.fmt) throw std::runtime_error("ffn_gate and ffn_up differ in format");
+        // rta_mlp_swiglu's two passes as separate calls, timed one by one
         t.start(stream);
-        rta_check(rta_mlp_swiglu((int)g.fmt, wg, (int)u.fmt, wu, (int)d.fmt, wd, (int)D, (int)F, x.as<float>(),
-                                 (int)count, act.as<float>(), y.as<float>(), RTA_EPI_STORE, ws.p, wsb, stream),
-                  "rta_mlp_swiglu");
-        const double mlp = t.stop(stream);
+        rta_check(rta_swiglu((int)g.fmt, wg, wu, (int)D, (int)F, x.as<float>(), (int)count, act.as<float>(), ws.p, wsb,
+                             stream),
+                  "rta_swiglu");
+        const double gate_up = t.stop(stream);
+        t.start(stream);
+        rta_check(rta_gemv((int)d.fmt, wd, (int)D, (int)F, act.as<float>(), (int)count, y.as<float>(), RTA_EPI_STORE,
+                           ws.p, wsb, stream),
+                  "rta_gemv");
+        const double down = t.stop(stream);
         device_error_check("RT MLP transmission");
         std::vector<float> yo((size_t)count * D), ao((size_t)count * F);
         hip_check(hipMemcpy(yo.data(), y.p, yo.size() * 4, hipMemcpyDeviceToHost), "read output");
@@ -521,8 +594,7 @@ struct Worker {
         append(o, ao);
         const std::vector<uint32_t> hits(count, F);   // the full-matrix MLP reads every feature
         append(o, hits);
-        // (setup, gate_up, down): the gate/up and down passes run in one call here
-        const std::vector<double> times{setup, mlp, 0.0};
+        const std::vector<double> times{setup, gate_up, down};
         append(o, times);
         reply(o);
     }
@@ -639,9 +711,6 @@ struct Worker {
         hip_check(hipMemcpyAsync(kbuf.p, ks.data(), ks.size() * 4, hipMemcpyHostToDevice, stream), "upload keys");
         hip_check(hipMemcpyAsync(vbuf.p, vs.data(), vs.size() * 4, hipMemcpyHostToDevice, stream), "upload values");
         hip_check(hipMemcpyAsync(slots.p, sl.data(), (size_t)count * 8, hipMemcpyHostToDevice, stream), "upload slots");
-        rta_check(rta_pack_history(kbuf.as<float>(), (int)G, vbuf.as<float>(), (int)G, (int)count, (int)G, RTA_Q4_K,
-                                   RTA_Q6_K, slots.as<int64_t>(), capacity, packets.p, stream),
-                  "rta_pack_history");
         // one sequence per query row over the shared ring, each with its own length
         std::vector<int32_t> lens(nrows);
         std::vector<int64_t> bases(nrows, 0);
@@ -664,23 +733,30 @@ struct Worker {
         hip_check(hipMemcpyAsync(gate.p, gs.data(), gs.size() * 4, hipMemcpyHostToDevice, stream), "upload gate");
         const size_t wsb = rta_decode_attention_workspace_bytes((int)nrows, (int)heads, (int)kv_heads, (int)hd, max_ctx);
         ws.ensure(wsb);
-        Timer t;
-        t.start(stream);
+        const uint32_t stride = hd + 8 + block / 32;
+        const int64_t records = rta_attention_receipt_records(lens.data(), (int)nrows, (int)heads, capacity, (int)block);
+        if (records <= 0 || records > 0xFFFFFFFFll) throw std::runtime_error("Attention receipt count out of range");
+        rec.ensure((size_t)records * stride * 4);
+        // timed as the reference times the diagnostic (resident_attention_runtime.inl:707-726,752):
+        // the producer (history pack and the per-group records), then the attention output
+        // (the merge's place); the legacy output is the same computation, not run again
+        Timer producer, merge;
+        producer.start(stream);
+        rta_check(rta_pack_history(kbuf.as<float>(), (int)G, vbuf.as<float>(), (int)G, (int)count, (int)G, RTA_Q4_K,
+                                   RTA_Q6_K, slots.as<int64_t>(), capacity, packets.p, stream),
+                  "rta_pack_history");
+        rta_check(rta_attention_receipts(q.as<float>(), (int)nrows, (int)heads, (int)kv_heads, (int)hd, packets.p,
+                                         RTA_Q4_K, RTA_Q6_K, base_d.as<int64_t>(), ctx.as<int32_t>(), capacity, capacity,
+                                         max_ctx, (int)block, rec.as<uint32_t>(), records, stream),
+                  "rta_attention_receipts");
+        const double fused = producer.stop(stream);
+        merge.start(stream);
         rta_check(rta_decode_attention(q.as<float>(), (int)nrows, (int)heads, (int)kv_heads, (int)hd, packets.p, RTA_Q4_K,
                                        RTA_Q6_K, base_d.as<int64_t>(), ctx.as<int32_t>(), capacity, capacity, max_ctx,
                                        attention_gate ? gate.as<float>() : nullptr, out.as<float>(), m.as<float>(),
                                        z.as<float>(), ws.p, wsb, stream),
                   "rta_decode_attention");
-        const double fused = t.stop(stream);
-        // the per-group records of the same attention (index 1: every row has records)
-        const uint32_t stride = hd + 8 + block / 32;
-        const int64_t records = rta_attention_receipt_records(lens.data(), (int)nrows, (int)heads, capacity, (int)block);
-        if (records <= 0 || records > 0xFFFFFFFFll) throw std::runtime_error("Attention receipt count out of range");
-        rec.ensure((size_t)records * stride * 4);
-        rta_check(rta_attention_receipts(q.as<float>(), (int)nrows, (int)heads, (int)kv_heads, (int)hd, packets.p,
-                                         RTA_Q4_K, RTA_Q6_K, base_d.as<int64_t>(), ctx.as<int32_t>(), capacity, capacity,
-                                         max_ctx, (int)block, rec.as<uint32_t>(), records, stream),
-                  "rta_attention_receipts");
+        const double merged = merge.stop(stream);
         uint32_t bits = 0;
         rta_check(rta_device_error(&bits, 1), "rta_device_error");
         std::vector<float> o_h(qs.size()), m_h((size_t)nrows * heads), z_h((size_t)nrows * heads);
@@ -699,7 +775,7 @@ struct Worker {
         const uint32_t header[12] = {0x41545231u, nrows, count, heads, kv_heads, hd, (uint32_t)pb,
                                      block, stride, (uint32_t)records, legacy, bits};
         append(o, header, 12);
-        const std::vector<double> times{fused, 0.0, 0.0, wall_ms(t0)};
+        const std::vector<double> times{fused, merged, 0.0, wall_ms(t0)};
         append(o, times);
         append(o, o_h);
         append(o, phys);
@@ -729,7 +805,6 @@ struct Worker {
     // op 1 / 11 / 12: the prompt (at most capacity ids) from position 0, one decode step
     // per token; the last step leaves the first generated token pending on the device.
     void prefill(uint32_t count, uint32_t debug, uint32_t checkpoint_mode) {
-        if (debug == 1u) throw std::runtime_error("Layer capture is not provided by this worker");
         if (debug > 2u || !count || count > capacity) throw std::runtime_error("Invalid resident prefix");
         std::vector<uint32_t> ids;
         input(ids, count);
@@ -754,6 +829,15 @@ struct Worker {
             throw std::runtime_error("Invalid prefix word IDs or boundary");
         const auto t0 = std::chrono::steady_clock::now();
         Decoder& d = decoder();
+        // layer capture (debug 1, optical_resident.cpp:481,614-616,686): every position's
+        // residual stream after each layer, [count][depth + 1][hidden] on the device
+        const size_t D = info.hidden, depth = info.depth, per = (depth + 1) * D;
+        const bool capture = debug == 1u;
+        if (capture) {
+            if ((uint64_t)count * per * 4 > (1ull << 32))
+                throw std::runtime_error("Layer capture exceeds the device storage-buffer range; use a shorter prefix");
+            layers_cap.ensure((size_t)count * per * 4);
+        }
         d.prompt.ensure((size_t)count * 4);
         hip_check(hipMemcpyAsync(d.prompt.p, ids.data(), (size_t)count * 4, hipMemcpyHostToDevice, stream), "upload prompt");
         Timer t;
@@ -762,7 +846,7 @@ struct Worker {
         for (uint32_t i = 0; i < count; ++i) {
             hip_check(hipMemcpyAsync(d.tokens.p, d.prompt.as<uint32_t>() + i, 4, hipMemcpyDeviceToDevice, stream),
                       "prompt token");
-            d.step(stream);
+            d.step(stream, capture ? layers_cap.as<float>() + (size_t)i * per : nullptr);
         }
         const double gpu = t.stop(stream);
         uint32_t bits = 0;
@@ -777,6 +861,16 @@ struct Worker {
         const std::vector<double> times{0.0, gpu, 0.0, wall_ms(t0), 0.0, 0.0};
         append(o, times);
         append(o, control, 8);
+        if (capture) {   // the state after the last layer per position, then each layer's rows
+            std::vector<float> all((size_t)count * per), rows_out((size_t)count * D * (depth + 1));
+            hip_check(hipMemcpy(all.data(), layers_cap.p, all.size() * 4, hipMemcpyDeviceToHost), "read capture");
+            for (size_t i = 0; i < count; ++i) {
+                std::copy_n(&all[i * per + depth * D], D, &rows_out[i * D]);
+                for (size_t l = 0; l < depth; ++l)
+                    std::copy_n(&all[i * per + (l + 1) * D], D, &rows_out[((l + 1) * count + i) * D]);
+            }
+            append(o, rows_out);
+        }
         // (tokens per compute batch, batches, tree updates, query positions)
         const std::vector<uint64_t> footer{1u, count, 0u, count};
         append(o, footer);
@@ -788,17 +882,21 @@ struct Worker {
     bool generate(uint32_t count, uint32_t debug) {
         if (diagnostic_dirty) throw std::runtime_error("Attention diagnostics replace history; prefill again before generation");
         if (!prefilled || !count || count > 64) throw std::runtime_error("Resident generation expects 1..64 tokens after prefill");
-        if (debug == 1u) throw std::runtime_error("Layer capture is not provided by this worker");
         const auto t0 = std::chrono::steady_clock::now();
         Decoder& d = *dec;
         uint32_t ids[64] = {};
         uint32_t emitted = 0, computed = 0;
+        const bool profiled = debug == 2u;
+        if (profiled) profile.start(d.shape.layers);
+        bool marked = false;   // a profiled step whose marks are not read yet
         Timer t;
         t.start(stream);
         while (emitted < count && control[2]) {
             uint32_t id = 0;
             hip_check(hipMemcpyAsync(&id, d.tokens.p, 4, hipMemcpyDeviceToHost, stream), "read token");
             hip_check(hipStreamSynchronize(stream), "sync");
+            if (marked) profile.add(d.shape.layers, d.shape.full_every);
+            marked = false;
             if (id >= info.vocab) throw std::runtime_error("Resident decode optical error 2048");
             ids[emitted++] = id;
             control[0] = id;
@@ -807,10 +905,12 @@ struct Worker {
                 control[2] = 0;
                 break;
             }
-            d.step(stream);   // reads the pending id, leaves the next one
+            d.step(stream, nullptr, profiled ? profile.marks.data() : nullptr);   // reads the pending id, leaves the next one
+            marked = profiled;
             ++computed;
         }
         const double gpu = t.stop(stream);
+        if (marked) profile.add(d.shape.layers, d.shape.full_every);
         uint32_t bits = 0;
         rta_check(rta_device_error(&bits, 1), "rta_device_error");
         if (bits) throw std::runtime_error("Resident decode optical error " + std::to_string(bits));
@@ -822,6 +922,7 @@ struct Worker {
         timing[1] = wall_ms(t0);
         timing[2] = timing[3] = (double)std::max(computed, 1u);
         timing[6] = (double)position;
+        if (profiled) std::copy_n(profile.parts, 10, &timing[8]);
         std::vector<char> o;
         append(o, timing);
         append(o, control, 8);
@@ -829,12 +930,17 @@ struct Worker {
         const uint32_t mlp = computed * info.depth * info.middle;
         const uint32_t hits[5] = {mlp, mlp, emitted * info.vocab, 0u, 0xffffffffu};
         append(o, hits, 5);
+        if (debug == 1u) {   // the residual stream after the last layer of the latest step
+            std::vector<float> st(info.hidden);
+            hip_check(hipMemcpy(st.data(), d.last.p, st.size() * 4, hipMemcpyDeviceToHost), "read state");
+            append(o, st);
+        }
         append(o, std::vector<double>(4, 0.0));    // RT query time per kind
         append(o, std::vector<uint32_t>(4, 0u));   // cached tokens, cache queries, nodes, capacity
         append(o, std::vector<double>(2 + 3, 0.0));  // cache time; cached-state recovery
         append(o, std::vector<uint32_t>(2, 0u));   // cache candidates, rejected
         append(o, std::vector<uint64_t>(2, 0u));   // MLP route rows
-        if (debug == 2u) append(o, std::vector<double>(2, 0.0));   // detector time (attention, recurrent)
+        if (profiled) append(o, std::vector<double>{profile.detector[0], profile.detector[1]});
         reply(o);
         return control[2] != 0;
     }

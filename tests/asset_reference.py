@@ -27,6 +27,7 @@ class AssetReference:
         self.rec = {l: np.zeros((1, H, HD, HD)) for l, k in enumerate(self.kinds) if k != "full"}
         self.conv = {l: np.zeros((1, 3 * H * HD, 3), f32) for l, k in enumerate(self.kinds) if k != "full"}
         self.pos = 0
+        self.residual = []   # the residual stream after each layer of the last forward
 
     def _proj(self, tensor, rows, x, mode=0, first_row=0, key_rows=0, cols=None):
         fmt, raw = self.packed[tensor]   # uint8 [rows, row bytes]
@@ -43,6 +44,7 @@ class AssetReference:
         x = orc.embed(fe, te, sp["vocabulary_size"], d, [token]).astype(np.float64)
         # the exporter's q/k norm order (export.py:100-104): axis i of a head reads rot(i)
         perm = [orc.remap_row(3, HD, r, 0, i) for i in range(HD)]
+        self.residual = []
         for l, kind in enumerate(self.kinds):
             p = f"blk.{l}."
             n = orc.rmsnorm(x.astype(f32), self.floats[p + "attn_norm.weight"], eps)
@@ -91,6 +93,7 @@ class AssetReference:
             (fg, wg), (fu, wu), (fd, wd) = (self.packed[p + t + ".weight"] for t in ("ffn_gate", "ffn_up", "ffn_down"))
             _, y = orc.mlp_swiglu((fg, fu, fd), wg, wu, wd, d, sp["middle_size"], n.astype(f32))
             x = x + y
+            self.residual.append(x[0].copy())
         n = orc.rmsnorm(x.astype(f32), self.floats["output_norm.weight"], eps)
         fl, wl = self.packed["output.weight"]
         self.pos += 1

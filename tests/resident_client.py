@@ -124,7 +124,8 @@ class Worker:
         return np.frombuffer(self.request(8, 0), "<u8")
 
     # op 1 / 11 / 12
-    def prefill(self, ids, stops=(), checkpoint_tokens=None, boundaries=None, debug=0):
+    def prefill(self, ids, stops=(), checkpoint_tokens=None, boundaries=None, debug=0, hidden=0, depth=0):
+        """debug 1 (layer capture) needs hidden and depth to read the captured rows."""
         ids = np.asarray(ids, "<u4")
         stop = list(stops)[:2] + [0xFFFFFFFF] * 2
         body = ids.tobytes() + struct.pack("<2I", *stop[:2])
@@ -137,25 +138,41 @@ class Worker:
             op = 12
         pay = self.request(op, len(ids), debug, body)
         r = dict(times=np.frombuffer(pay, "<f8", count=6), control=np.frombuffer(pay, "<u4", count=8, offset=48))
-        if len(pay) >= 112:
-            r["footer"] = np.frombuffer(pay, "<u8", count=4, offset=80)
+        off = 80
+        if debug == 1:   # resident_runtime.py:136-139
+            n = len(ids) * hidden
+            r["state"] = np.frombuffer(pay, "<f4", count=n, offset=off).reshape(len(ids), hidden)
+            r["layers"] = np.frombuffer(pay, "<f4", count=depth * n, offset=off + 4 * n).reshape(depth, len(ids), hidden)
+            off += 4 * n * (depth + 1)
+        if len(pay) >= off + 32:
+            r["footer"] = np.frombuffer(pay, "<u8", count=4, offset=off)
         return r
 
+    PROFILE = ("projection_geometry", "bvh_update", "lens_history_trace", "coordinate_restore", "detector",
+               "output_mlp", "vocabulary", "vocabulary_rt", "vocabulary_coefficients", "vocabulary_reduce")
+
     @staticmethod
-    def generation(pay, profile=False):
-        """A GenerationPacket reply (resident_runtime.py:190-233)."""
+    def generation(pay, profile=False, state=0):
+        """A GenerationPacket reply (resident_runtime.py:190-233); state: hidden size of the
+        debug-1 state that follows the hits."""
         r = dict(timing=np.frombuffer(pay, "<f8", count=18), control=np.frombuffer(pay, "<u4", count=8, offset=144))
         r["ids"] = np.frombuffer(pay, "<u4", count=64, offset=176)[:int(r["control"][1])].copy()
         r["hits"] = np.frombuffer(pay, "<u4", count=5, offset=432)
         off = 452
+        if state:
+            r["state"] = np.frombuffer(pay, "<f4", count=state, offset=off)
+            off += 4 * state
         r["cache"] = np.frombuffer(pay, "<u4", count=4, offset=off + 32)
+        if profile:
+            r["profile"] = dict(zip(Worker.PROFILE, r["timing"][8:18]))
+            r["detector"] = np.frombuffer(pay, "<f8", count=2, offset=off + 112)
         r["size"] = len(pay)
         assert len(pay) == off + 112 + (16 if profile else 0), len(pay)
         return r
 
     # op 2
-    def generate(self, count, debug=0):
-        return self.generation(self.request(2, count, debug), debug == 2)
+    def generate(self, count, debug=0, hidden=0):
+        return self.generation(self.request(2, count, debug), debug == 2, hidden if debug == 1 else 0)
 
     # op 9: one reply per token until the count or a stop
     def stream(self, count, debug=0):

@@ -172,12 +172,16 @@ def test_hybrid_shape_refuses_attention_the_kernels_do_not_serve(lib):
     ok = model.shape_9b(1024)
     assert hybrid.rta_hybrid_state_bytes(ctypes.byref(ok), 4) > 0
     # a misaligned capture buffer is refused before any launch
-    cap = model.HybridCapture(residual=FAKE_ODD.value, kv=None)
+    cap = model.HybridCapture(residual=FAKE_ODD.value, residual_from=0, kv=None, marks=None)
     need = hybrid.rta_hybrid_workspace_bytes(ctypes.byref(ok), 4)
     w = model.HybridWeights(embed=FAKE.value, layers=ctypes.cast(FAKE.value, ctypes.POINTER(model.HybridLayer)),
                             norm_final=FAKE.value, lm_head=FAKE.value)
     assert hybrid.rta_hybrid_decode_step_capture(ctypes.byref(ok), ctypes.byref(w), 4, FAKE, FAKE, None,
                                                  ctypes.byref(cap), FAKE, need, None) == 4
+    # the first captured residual block lies in 0 .. layers
+    cap = model.HybridCapture(residual=FAKE.value, residual_from=33, kv=None, marks=None)
+    assert hybrid.rta_hybrid_decode_step_capture(ctypes.byref(ok), ctypes.byref(w), 4, FAKE, FAKE, None,
+                                                 ctypes.byref(cap), FAKE, need, None) == 7
 
 
 def test_part_readout_workspace_is_not_monotonic_in_rows(lib):

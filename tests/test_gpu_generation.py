@@ -17,6 +17,7 @@ import pytest
 
 import asset_writer as aw
 from asset_reference import AssetReference
+from conftest import assert_close
 from resident_client import Worker
 from rta import synth
 
@@ -147,3 +148,65 @@ def test_generation_errors(model):
     with pytest.raises(RuntimeError, match="prefill again before generation"):
         w.generate(1)
     assert w.close() == 1
+
+
+def test_layer_capture_matches_the_oracle(model):
+    """Layer capture (debug 1): prefill returns every position's residual stream after each
+    layer and the state after the last one (optical_resident.cpp:481,686;
+    resident_runtime.py:136-139); generation returns the state after its last step
+    (optical_resident.cpp:832,870; resident_runtime.py:199).  Each row against the fp64
+    composition fed the same ids, to the float bar."""
+    d, packed, floats = model
+    D, depth = SPEC["hidden_size"], len(SPEC["layer_types"])
+    prompt = np.arange(3, 3 + 12) * 53 % SPEC["vocabulary_size"]
+    w = _worker(d, 64)
+    try:
+        print("generation: layer capture", flush=True)
+        r = w.prefill(prompt, debug=1, hidden=D, depth=depth)
+        assert r["footer"].tolist() == [1, 12, 0, 12]
+        g = w.generate(3, debug=1, hidden=D)
+    finally:
+        assert w.close() == 0, w.error_text()
+    ref = AssetReference(SPEC, packed, floats)
+    for i, t in enumerate(prompt):
+        ref.last = ref.forward(int(t))
+        for l in range(depth):
+            assert_close(r["layers"][l, i], ref.residual[l], f"position {i} after layer {l}")
+        np.testing.assert_array_equal(r["state"][i], r["layers"][depth - 1, i])
+    assert len(g["ids"]) == 3
+    for t in g["ids"]:   # each emitted id is forwarded; the state is the last forward's
+        ref.last = ref.forward(int(t))
+    assert_close(g["state"], ref.residual[-1], "generation state")
+
+
+def test_generation_profile(model):
+    """debug 2: the GenerationPacket's stage sums (time[8:18], optical_resident.cpp:849-853;
+    resident_runtime.py:195) and detector sums (attention, recurrent; :229-231) from events
+    at the decode step's stage marks.  No BVH update, history trace, payload restore or
+    vocabulary trace runs here, so those stages are 0; the stages of a step cover its GPU
+    time but for the embedding, the final norm and the host's token read between steps."""
+    d, _, _ = model
+    prompt = np.arange(5, 5 + 20) * 29 % SPEC["vocabulary_size"]
+    w = _worker(d, 64)
+    try:
+        w.prefill(prompt)
+        plain = w.generate(6)["ids"].tolist()
+        w.prefill(prompt)
+        g = w.generate(6, debug=2)
+    finally:
+        assert w.close() == 0, w.error_text()
+    assert g["ids"].tolist() == plain
+    p = g["profile"]
+    print("generation profile (ms):", {k: round(v, 4) for k, v in p.items()}, "gpu", g["timing"][0],
+          "detector", g["detector"].tolist(), flush=True)
+    for k in ("projection_geometry", "detector", "output_mlp", "vocabulary", "vocabulary_coefficients",
+              "vocabulary_reduce"):
+        assert p[k] > 0, k
+    for k in ("bvh_update", "lens_history_trace", "coordinate_restore", "vocabulary_rt"):
+        assert p[k] == 0, k
+    assert g["detector"][0] > 0 and g["detector"][1] > 0
+    assert abs(g["detector"].sum() - p["detector"]) <= 1e-6 + 1e-4 * p["detector"]
+    parts = p["vocabulary_rt"] + p["vocabulary_coefficients"] + p["vocabulary_reduce"]
+    assert abs(parts - p["vocabulary"]) <= 1e-6 + 1e-4 * p["vocabulary"]
+    stages = sum(p[k] for k in Worker.PROFILE[:7])
+    assert 0.5 * g["timing"][0] <= stages <= g["timing"][0]

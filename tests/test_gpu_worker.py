@@ -64,7 +64,9 @@ def test_mlp_check(served, layer, rows):
     _close(r["activation"], act, "activation")
     _close(r["output"], y, "output")
     assert (r["feature_hits"] == f).all()
-    assert np.isfinite(r["times"]).all()
+    # (setup, gate_up, down) GPU ms (optical_resident.cpp:946; resident_runtime.py:259-262)
+    setup, gate_up, down = r["times"]
+    assert np.isfinite(r["times"]).all() and setup >= 0 and gate_up > 0 and down > 0
 
 
 @pytest.mark.parametrize("seed", [1, 2])
@@ -118,6 +120,10 @@ def test_attention_check(served, rows, count, hstart, gap):
     assert r["records"] == heads * sum((min(qstart - hstart + i + 1, CAPACITY) + block - 1) // block
                                        for i in range(rows))
     assert r["legacy"] == int(hstart == 0)
+    # (producer, merge, legacy, wall) ms (resident_attention_runtime.inl:707-726,752): the history
+    # pack and records, then the output; the legacy output is the same computation
+    fused, merge, legacy, wall = r["timing"]
+    assert fused > 0 and merge > 0 and legacy == 0 and wall >= fused + merge
     packets = np.stack([orc.pack_history(k[i], v[i]) for i in range(count)])
     np.testing.assert_array_equal(r["history_packets"], packets)
     ctx = np.array([qstart - hstart + i + 1 for i in range(rows)], np.int32)
