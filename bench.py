@@ -300,7 +300,8 @@ def w_mlp(torch, args, orc):
         ops.mlp_swiglu(kfm, g_, u_, d_, hidden, inter, xd, y=y, act=act, workspace=ws)
 
     alg = packed.nbytes + batch * (hidden * 4 + inter * 4 + hidden * 4)
-    res = {"alg_bytes": alg, "kernel": "gemv (gate+up fused SwiGLU) then gemv (down)", "step": step,
+    res = {"alg_bytes": alg, "kernel": "gate/up SwiGLU pair: " + readout_name("Q4_K", inter, hidden, batch, args.packed, True)
+           + "; down: " + readout_name("Q6_K", hidden, inter, batch, args.packed), "step": step,
            "kernel_launch": step, "unit": "GB/s", "value_from_ms": lambda ms: alg / (ms * 1e-3) / 1e9,
            "dtype": "q4_k/q6_k weights x fp32 activations, fp32 accumulate",
            "config": {"workload": f"SwiGLU MLP 2048->6144->2048 (gate/up Q4_K, down Q6_K), batch {batch}"
@@ -320,6 +321,21 @@ def w_mlp(torch, args, orc):
                 "sample": f"{n} calls of the oracle's fp64 SwiGLU MLP (batch {batch}) in {el:.1f} s on {cpu_model()}"}
     res["check"], res["cpu"] = check, cpu
     return res
+
+
+def readout_name(fmt_name, rows, cols, batch, packed, pair=False):
+    """The kernel a projection readout runs (the library's dispatch, for the bench line's
+    label): packed tiles on the matrix cores; GGUF rows on the batch-1 readout, the
+    vector-ALU batch readout, or the matrix cores from batch 5 (3 at 2^25+ weights, 2 at
+    2^27+ weights, a SwiGLU pair counting both matrices)."""
+    if packed:
+        return f"gemm_tiled_kernel<{fmt_name}> (packed tiles, matrix cores)"
+    if batch == 1:
+        return f"gemv_b1_kernel<{fmt_name}> (GGUF rows, vector ALUs)"
+    weights = rows * cols * (2 if pair else 1)
+    if batch >= 5 or (batch >= 3 and weights >= 1 << 25) or (batch >= 2 and weights >= 1 << 27):
+        return f"xprep_kernel + gemm_mfma_kernel<{fmt_name}> (GGUF rows, matrix cores)"
+    return f"gemv_kquant_kernel<{fmt_name}> (GGUF rows, vector ALUs)"
 
 
 def w_lm_head(torch, args, orc):
@@ -350,7 +366,8 @@ def w_lm_head(torch, args, orc):
 
     alg = w.nbytes + batch * (hidden * 4 + vocab * 4 + 4)
     alg_k = w.nbytes + batch * (hidden * 4 + vocab * 4)
-    res = {"alg_bytes": alg, "alg_bytes_kernel": alg_k, "kernel": "Q6_K logits GEMV (gemv_b1_kernel<Q6_K,R=2,store,KW=1>)",
+    res = {"alg_bytes": alg, "alg_bytes_kernel": alg_k,
+           "kernel": "Q6_K logits readout: " + readout_name("Q6_K", vocab, hidden, batch, args.packed),
            "step": step, "kernel_launch": readout, "unit": "GB/s", "value_from_ms": lambda ms: alg / (ms * 1e-3) / 1e9,
            "dtype": "q6_k weights x fp32 activations, fp32 accumulate",
            "config": {"workload": f"LM head 151936x2048 Q6_K + margin argmax, batch {batch}"
@@ -466,7 +483,7 @@ def w_proj(torch, args, orc):
         ops.gemv(kfmt, copies[i % len(copies)], rows, cols, xd, y=y, workspace=ws)
 
     alg = w.nbytes + batch * 4 * (cols + rows)
-    res = {"alg_bytes": alg, "kernel": "dequant-fused projection (MFMA path from batch 8)", "step": step,
+    res = {"alg_bytes": alg, "kernel": "dequant-fused projection (matrix cores from batch 5; 3 at 2^25+ weights, 2 at 2^27+)", "step": step,
            "kernel_launch": step, "unit": "GB/s", "value_from_ms": lambda ms: alg / (ms * 1e-3) / 1e9,
            "dtype": f"{args.fmt} weights x fp32 activations, fp32 accumulate",
            "config": {"workload": f"{args.fmt.upper()} projection {rows}x{cols}, batch {batch}"

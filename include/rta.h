@@ -91,8 +91,9 @@ int rta_pack(int fmt, const void* src, int rows, int cols, void* dst, rta_stream
 /* y[b, r] (=|+=) sum_c W[r, c] x[b, c],  b < batch, r < rows.
  *   x: [batch, cols] fp32 row-major, y: [batch, rows] fp32.
  *   K-quants need cols % 256 == 0; W 16-byte aligned (Q4_K) / 2-byte (Q6_K).
- *   Batch tiles of 8 or more K-quant rows, and packed matrices (fmt | RTA_TILED)
- *   at every batch, run on the matrix cores and need a workspace of
+ *   K-quant batches of 5 or more rows (3 or more when rows x cols >= 2^25, 2 or more
+ *   when >= 2^27; a SwiGLU pair counts both matrices), and packed matrices
+ *   (fmt | RTA_TILED) at every batch, run on the matrix cores and need a workspace of
  *   rta_gemv_workspace_bytes() (256-byte aligned); 0 bytes otherwise.
  * Replaces the projection detector, resident_math.comp:39-75 (op 2, indices
  * 0/1/2/4/6/8) dispatched by Resident::launch, optical_resident.cpp:304-347, and its

@@ -281,7 +281,24 @@ static int check_matrix(int fmt, const void* w, int rows, int cols) {
 }
 
 // ------------------------------------------------------------ MFMA path ----
-constexpr int kMfmaMinBatch = 8;   // batches from this size use the matrix cores
+// Whether a GGUF-row K-quant readout of `weights` values (rows x cols, both matrices of a
+// SwiGLU pair) over `batch` rows runs on the matrix cores rather than the vector ALUs.
+// Measured per call on MI355X against the vector-ALU kernel (gemv_kquant_kernel, batch
+// tiles of up to 8 rows), row layout:
+//   4096x4096 Q4_K      b2 9.5 / 19.6 us, b3 12.5 / 19.8, b4 14.3 / 20.0, b5 24.3 / 19.9
+//   12288x4096 Q4_K     b2 20.1 / 27.0, b3 27.4 / 27.3, b4 32.8 / 27.3, b5 61.2 / 27.5
+//   151936x2048 Q6_K LM head   b2 101.7 / 90.4, b4 154.5 / 90.7, b5 228.9 / 90.6,
+//                              b16 638.6 / 91.7 (vector ALUs: 135 M VALU instructions)
+//   SwiGLU MLP 2048x6144 (config 2)   b4 46.4 / 42.1, b8 78.7 / 43.8, b32 307.9 / 50.9
+// The vector path issues NB fma per weight and batch tile, so its time grows with the
+// batch; the matrix cores' does not up to 32 rows.
+constexpr int64_t kMmaAnyWeights = 0;               // from batch 5: every matrix
+constexpr int64_t kMmaMidWeights = 32ll << 20;      // from batch 3
+constexpr int64_t kMmaTallWeights = 128ll << 20;    // from batch 2
+__host__ __device__ constexpr bool mma_batch(int64_t weights, int batch) {
+    return (batch >= 5 && weights >= kMmaAnyWeights) || (batch >= 3 && weights >= kMmaMidWeights) ||
+           (batch >= 2 && weights >= kMmaTallWeights);
+}
 constexpr int kMfmaRT = 2;         // 16-row tiles per wave
 
 struct MmaPlan {
@@ -362,7 +379,7 @@ static size_t projection_ws(int fmt, int rows, int cols, int batch, bool dual) {
         const MmaPlan a = plan_tiled(rows, cols, 1, dual), b = plan_tiled(rows, cols, 2, dual);
         return a.x_bytes + (a.part_bytes > b.part_bytes ? a.part_bytes : b.part_bytes);
     }
-    if (!(fmt == RTA_Q4_K || fmt == RTA_Q6_K) || batch < kMfmaMinBatch) return 0;
+    if (!(fmt == RTA_Q4_K || fmt == RTA_Q6_K) || !mma_batch((int64_t)rows * cols * (dual ? 2 : 1), batch)) return 0;
     const MmaPlan a = plan_mfma(rows, cols, 1, dual), b = plan_mfma(rows, cols, 2, dual);
     return a.x_bytes + (a.part_bytes > b.part_bytes ? a.part_bytes : b.part_bytes);
 }
@@ -464,8 +481,10 @@ static int run_projection(int fmt, const void* w, const void* w2, int rows, int 
     const bool tiled = is_tiled(fmt);
     const int64_t row_bytes = tiled ? 0 : host::row_bytes(fmt, cols);
     int b0 = 0;
-    // The path depends on the whole batch, so a row's result never depends on tiling.
-    const bool mma = is_kquant(fmt) && (path_batch > 0 ? path_batch : batch) >= kMfmaMinBatch;
+    // The path depends on the whole batch (and the matrix), so a row's result never
+    // depends on tiling.
+    const bool mma = is_kquant(fmt) &&
+                     mma_batch((int64_t)rows * cols * (MODE == kSwiglu ? 2 : 1), path_batch > 0 ? path_batch : batch);
     while (b0 < batch) {
         const int cap = (mma || tiled) ? kMaxBatchTile : 8;
         const int chunk = batch - b0 < cap ? batch - b0 : cap;
@@ -954,7 +973,8 @@ int lm_head_rownorm(int fmt, const void* w, int vocab, int hidden, const float* 
     // Argmax per batch tile, with the plan that tile was written with.
     int b0 = 0;
     while (b0 < batch) {
-        const int cap = ((is_kquant(fmt) && batch >= kMfmaMinBatch) || is_tiled(fmt)) ? kMaxBatchTile : 8;
+        const bool cores = is_kquant(fmt) && mma_batch((int64_t)vocab * hidden, batch);
+        const int cap = (cores || is_tiled(fmt)) ? kMaxBatchTile : 8;
         const int chunk = batch - b0 < cap ? batch - b0 : cap;
         int ntasks = 0, rpt = 1;
         RowNorm rc_rn = rn;

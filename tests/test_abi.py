@@ -42,7 +42,15 @@ def test_host_queries(lib):
     assert lib.rta_row_bytes(_lib.F16, 10) == 20
     assert lib.rta_history_bytes(512) == 712          # resident_dimensions.hpp:10
     assert lib.rta_history_bytes(1024) == 1416
-    assert lib.rta_lm_head_workspace_bytes(_lib.Q6_K, 151936, 2048, 4) == 151936 * 4 * 4
+    # the LM head's task maxima; from batch 2 its 151936 x 2048 readout runs on the matrix cores
+    # (more than 2^27 weights), which add their scratch
+    assert lib.rta_lm_head_workspace_bytes(_lib.Q6_K, 151936, 2048, 1) == 151936 * 4
+    assert lib.rta_lm_head_workspace_bytes(_lib.Q6_K, 151936, 2048, 2) > 151936 * 2 * 4
+    # the 4096 x 4096 readout stays on the vector ALUs up to batch 4, the 12288 x 4096 one to 2
+    assert lib.rta_gemv_workspace_bytes(_lib.Q4_K, 4096, 4096, 4) == 0
+    assert lib.rta_gemv_workspace_bytes(_lib.Q4_K, 4096, 4096, 5) > 0
+    assert lib.rta_gemv_workspace_bytes(_lib.Q4_K, 12288, 4096, 2) == 0
+    assert lib.rta_gemv_workspace_bytes(_lib.Q4_K, 12288, 4096, 3) > 0
     assert lib.rta_gemv_workspace_bytes(_lib.Q4_K, 4096, 4096, 1) == 0
     assert lib.rta_gemv_workspace_bytes(_lib.Q4_K, 4096, 4096, 32) > 0
     assert lib.rta_mlp_workspace_bytes(_lib.Q4_K, _lib.Q6_K, 2048, 6144, 4) == 0

@@ -79,13 +79,13 @@ MMA_SHAPES = [(4096, 4096), (1000, 768), (37, 256), (300, 12288), (6144, 2048)]
 @pytest.mark.parametrize("fmt", [orc.Q4_K, orc.Q6_K])
 @pytest.mark.parametrize("rows,cols", MMA_SHAPES)
 def test_gemv_matrix_core_parity(torch_dev, fmt, rows, cols):
-    """Batch tiles of >= 8 rows run on the matrix cores (prepared fp16 hi/lo x, exact
-    integer weight operands, fixed-order K-slab reduce)."""
+    """Batches of >= 5 rows run on the matrix cores (prepared fp16 hi/lo x, exact integer
+    weight operands, fixed-order K-slab reduce)."""
     torch, dev = torch_dev
     rng = np.random.default_rng(rows * 13 + cols + fmt)
     w = synth.random_matrix(rng, fmt, rows, cols)
     wd = to_dev(torch, w, dev)
-    for batch in (8, 9, 16, 17, 32, 33, 40):
+    for batch in (5, 7, 8, 9, 16, 17, 32, 33, 40):
         x = rng.standard_normal((batch, cols)).astype(np.float32)
         x[0] *= 1e3          # rows of very different magnitude (per-row binary16 scaling)
         x[-1] *= 1e-3
@@ -93,6 +93,26 @@ def test_gemv_matrix_core_parity(torch_dev, fmt, rows, cols):
         ref = orc.gemv_f64(fmt, w, rows, cols, x)
         for b in range(batch):
             assert_close(got[b], ref[b], f"fmt {fmt} {rows}x{cols} batch {batch} row {b}")
+
+
+@pytest.mark.parametrize("fmt", [orc.Q4_K, orc.Q6_K])
+def test_gemv_small_batches_of_a_large_matrix(torch_dev, fmt):
+    """12288 x 4096 (more than 2^25 weights) runs on the matrix cores from batch 3, on the
+    vector ALUs at batch 2; both against the oracle, and the batch-3 rows bitwise equal to
+    the same rows inside a batch of 4 (one path for both)."""
+    torch, dev = torch_dev
+    rows, cols = 12288, 4096
+    rng = np.random.default_rng(92 + fmt)
+    w = synth.random_matrix(rng, fmt, rows, cols)
+    wd = to_dev(torch, w, dev)
+    x = rng.standard_normal((4, cols)).astype(np.float32)
+    ref = orc.gemv_f64(fmt, w, rows, cols, x)
+    got = {}
+    for batch in (2, 3, 4):
+        got[batch] = ops.gemv(fmt, wd, rows, cols, to_dev(torch, x[:batch], dev)).cpu().numpy()
+        for b in range(batch):
+            assert_close(got[batch][b], ref[b], f"fmt {fmt} batch {batch} row {b}")
+    assert np.array_equal(got[3], got[4][:3])
 
 
 def test_matrix_core_large_q6k_scales(torch_dev):
@@ -115,9 +135,9 @@ def test_matrix_core_large_q6k_scales(torch_dev):
 @pytest.mark.parametrize("fmt", [orc.Q4_K, orc.Q6_K])
 def test_gemv_invariants(torch_dev, fmt):
     """Zero row -> exact zero; batch-prefix bitwise invariance (verify_rt_mlp.py:95-98)
-    within each path: the VALU kernels (batch tiles of <= 7 rows) and the matrix-core
-    kernels (>= 8 rows) each compute a row independently of the other rows; across the
-    two paths results agree to tolerance.  x -> -x gives y -> -y exactly on the VALU
+    within each path: the VALU kernels (batches of <= 4 rows of this 512 x 4096 matrix)
+    and the matrix-core kernels (>= 5 rows) each compute a row independently of the other
+    rows; across the two paths results agree to tolerance.  x -> -x gives y -> -y exactly on the VALU
     path; on the matrix cores only to tolerance (the MFMA's multi-operand fp32
     accumulation is not sign-symmetric at the last bits)."""
     torch, dev = torch_dev
@@ -128,7 +148,7 @@ def test_gemv_invariants(torch_dev, fmt):
     x = rng.standard_normal((40, cols)).astype(np.float32)
     x[1] = 0.0
     x[2] = -x[0]
-    for n, prefixes, exact_sign in ((7, (1, 2, 4), True), (40, (8, 16, 33), False)):
+    for n, prefixes, exact_sign in ((4, (1, 2, 3), True), (40, (5, 8, 16, 33), False)):
         y = ops.gemv(fmt, w, rows, cols, to_dev(torch, x[:n], dev)).cpu().numpy()
         assert not y[1].any()                              # zero row -> exact zero
         if exact_sign:

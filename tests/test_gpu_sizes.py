@@ -1,5 +1,6 @@
 """GPU parity at the sizes the benchmarks run: the vocabulary readout over the full
-151936-word vocabulary at batch 4 and 16 (row and packed layouts) and the packed
+151936-word vocabulary at batch 2, 4 and 16 (row and packed layouts; the row layout on
+the matrix cores from batch 2 at this size) and the packed
 151936 x 4096 LM head of the 9B decode step at batch 32; and the decode step itself at
 the 9B widths (hidden 4096, 32 / 8 heads, 32 delta-net heads, FF 12288, vocab 151936,
 contexts U[256, 8192]) with four layers (three recurrent, one full): at batch 32 over
@@ -45,7 +46,7 @@ def _lm_head_case(torch, dev, vocab, hidden, batch, packed, seed):
 
 
 @pytest.mark.parametrize("packed", [False, True])
-@pytest.mark.parametrize("batch", [4, 16])
+@pytest.mark.parametrize("batch", [2, 4, 16])
 def test_lm_head_full_vocabulary(torch_dev, batch, packed):
     torch, dev = torch_dev
     _lm_head_case(torch, dev, 151936, 2048, batch, packed, 20261114 + batch)
