@@ -90,3 +90,43 @@ def test_decode_step_9b_widths_uneven_in_projection_parts():
     m = model.DecodeModel(shape, 32, ctx.tolist(), seed=20261117, keep_gguf=True, layer_fmts=fmts,
                           in_parts=parts)
     check_steps(m, 1)
+
+
+@pytest.mark.parametrize("batch", [1, 32])
+def test_decode_step_9b_full_depth_against_the_cpu_step(batch):
+    """All 32 layers of the 9B step, as the metric runs them (batch 32 on packed tiles, batch 1
+    on GGUF rows), one step against the oracle's fp32 CPU step (oracle/rta_cpu_step.c, itself
+    checked against the fp64 composition in tests/test_cpu_step.py) from the same state: the
+    logits of every row to the float bar, the next tokens under the margin rule (and equal to
+    the CPU step's unless a logit sits within rounding of the threshold), the updated
+    recurrent state to the float bar and the shifted conv windows bit exactly."""
+    shape = model.shape_9b(capacity=8448, packed=batch == 32)
+    ctx = np.random.default_rng(20261118 + batch).integers(256, 8193, batch)
+    m = model.DecodeModel(shape, batch, ctx.tolist(), seed=20261118 + batch, keep_gguf=True)
+    st = dict(rec=np.ascontiguousarray(m.state_view("recurrent")), conv=np.ascontiguousarray(m.state_view("conv")),
+              packets=np.ascontiguousarray(m.state_view("packets")), ctx=m.state_view("ctx"),
+              tokens=m.tokens.cpu().numpy().view(np.uint32).copy())
+    m.step(logits=True)
+    got = m.logits.cpu().numpy()
+    got_tokens = m.tokens.cpu().numpy().view(np.uint32)
+    assert ops.device_error() == 0
+    cpu = orc.CpuStep(shape, m.gguf)
+    ref = np.empty((batch, shape.vocab), np.float32)
+    cpu.step(batch, st["rec"], st["conv"], st["packets"], st["ctx"], st["tokens"], ref)
+    for b in range(batch):
+        assert_close(got[b], ref[b], f"logits row {b}")
+    check_margin_ids(got, got_tokens, ref, 1e-4)
+    conv = m.state_view("conv")
+    assert np.array_equal(conv[..., :2], st["conv"][..., :2])
+    assert_close(conv[..., 2], st["conv"][..., 2], "conv windows (new raw values)")
+    assert_close(m.state_view("recurrent"), st["rec"], "recurrent state")
+
+
+def test_decode_step_9b_full_depth_composition():
+    """The whole 32-layer 9B step at batch 32 against the fp64 composition (one step): every
+    layer's residual rows, the eight full layers' packed key / value rows and their history
+    packets byte for byte (step_reference.check_steps)."""
+    shape = model.shape_9b(capacity=8448, packed=True)
+    ctx = np.random.default_rng(20261119).integers(256, 8193, 32)
+    m = model.DecodeModel(shape, 32, ctx.tolist(), seed=20261119, keep_gguf=True)
+    check_steps(m, 1)
