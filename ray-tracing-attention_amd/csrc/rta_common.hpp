@@ -189,6 +189,15 @@ __device__ __forceinline__ float dequant_value(int fmt, const uint8_t* __restric
     return ds * (float)((int)(ql | (qh << 4)) - 32);
 }
 
+// op 0 (resident_math.comp:30-32): column c of table row id.  An id past the
+// vocabulary gives 0 and raises RTA_DEVERR_TOKEN (from column 0).
+__device__ __forceinline__ float embed_value(int fmt, const uint8_t* __restrict__ table, int64_t row_bytes,
+                                             int vocab, uint32_t id, int c) {
+    if (id < (uint32_t)vocab) return dequant_value(fmt, table + (int64_t)id * row_bytes, c);
+    if (c == 0) raise_error(RTA_DEVERR_TOKEN);
+    return 0.0f;
+}
+
 // Stable logistic of resident_common.glsl:138 (detectorSigmoid).
 __device__ __forceinline__ float detector_sigmoid(float v) {
     if (v >= 0.0f) return 1.0f / (1.0f + expf(-v));

@@ -34,5 +34,18 @@ inline int64_t history_bytes(int kvw) {
 
 inline bool aligned(const void* p, uintptr_t n) { return (reinterpret_cast<uintptr_t>(p) % n) == 0; }
 
+// Argument checks of a table lookup (op 0): RTA_OK and the table's row bytes in *rb, or
+// the error code.
+inline int embed_args(int fmt, const void* table, int vocab, int hidden, const uint32_t* ids, int batch,
+                      const float* out, int64_t* rb) {
+    if (!valid_format(fmt)) return RTA_ERR_FORMAT;
+    if (!table || !ids || !out) return RTA_ERR_NULL;
+    *rb = row_bytes(fmt, hidden);
+    if (vocab <= 0 || hidden <= 0 || batch <= 0 || *rb <= 0) return RTA_ERR_SHAPE;
+    if (!aligned(table, fmt == RTA_F32 || fmt == RTA_Q4_K ? 4 : 2) || !aligned(out, 4) || !aligned(ids, 4))
+        return RTA_ERR_ALIGN;
+    return RTA_OK;
+}
+
 }  // namespace host
 }  // namespace rta

@@ -20,20 +20,29 @@
 
 namespace rta {
 
-// Step prologue: the new token of sequence b sits at position pos = ctx[b]; it is
+// Step prologue and the token embedding (op 0) in one launch.  Block (x, b) decodes
+// columns 256 x .. 256 x + 255 of the table row tokens[b] into hidden[b]; thread 0 of
+// block (0, b) places sequence b's new token: it sits at position pos = ctx[b], is
 // written to ring slot base[l][b] + pos % capacity of every full layer l and sees
-// min(pos + 1, capacity) history entries.  ctx advances by one.
-__global__ void __launch_bounds__(256) step_prologue_kernel(int32_t* __restrict__ ctx, int batch, int n_full,
+// min(pos + 1, capacity) history entries (visible = pos + 1, the attention clamps it);
+// ctx advances by one.
+__global__ void __launch_bounds__(256) step_prologue_kernel(int32_t* __restrict__ ctx, int n_full,
                                                             int64_t capacity, const int64_t* __restrict__ base,
                                                             int64_t* __restrict__ pos64, int32_t* __restrict__ visible,
-                                                            int64_t* __restrict__ slots) {
-    const int b = blockIdx.x * 256 + threadIdx.x;
-    if (b >= batch) return;
-    const int32_t pos = ctx[b];
-    pos64[b] = pos;
-    visible[b] = pos + 1;
-    for (int l = 0; l < n_full; ++l) slots[(int64_t)l * batch + b] = base[(int64_t)l * batch + b] + pos % capacity;
-    ctx[b] = pos + 1;
+                                                            int64_t* __restrict__ slots, int fmt,
+                                                            const uint8_t* __restrict__ table, int64_t row_bytes,
+                                                            int vocab, int hidden, const uint32_t* __restrict__ tokens,
+                                                            float* __restrict__ out) {
+    const int b = blockIdx.y, batch = gridDim.y;
+    if (blockIdx.x == 0 && threadIdx.x == 0) {
+        const int32_t pos = ctx[b];
+        pos64[b] = pos;
+        visible[b] = pos + 1;
+        for (int l = 0; l < n_full; ++l) slots[(int64_t)l * batch + b] = base[(int64_t)l * batch + b] + pos % capacity;
+        ctx[b] = pos + 1;
+    }
+    const int c = blockIdx.x * 256 + threadIdx.x;
+    if (c < hidden) out[(int64_t)b * hidden + c] = embed_value(fmt, table, row_bytes, vocab, tokens[b], c);
 }
 
 // Ring bases (sequence b owns slots [b * capacity, (b + 1) * capacity) of every
@@ -305,6 +314,9 @@ int rta_hybrid_decode_step_capture(const rta_hybrid_shape* shape, const rta_hybr
     const Dims d = dims_of(shape, batch);
     const State st = carve_state(d, state, nullptr);
     Work w = carve_work(shape, d, workspace, nullptr);
+    int64_t embed_rb = 0;
+    rc = host::embed_args(shape->fmt_embed, weights->embed, d.V, d.D, tokens, d.B, w.hidden, &embed_rb);
+    if (rc) return rc;
     hipStream_t s = (hipStream_t)stream;
     const int pf = shape->fmt_proj;
     const float eps = shape->eps;
@@ -315,11 +327,11 @@ int rta_hybrid_decode_step_capture(const rta_hybrid_shape* shape, const rta_hybr
         if (e_) return e_;       \
     } while (0)
 
-    // prologue: positions, visible counts, ring slots; the token embedding (op 0)
-    hipLaunchKernelGGL(step_prologue_kernel, dim3((B + 255) / 256), dim3(256), 0, s, st.ctx, B, d.nfull,
-                       (int64_t)d.cap, st.base, w.pos, w.visible, w.slots);
+    // prologue: positions, visible counts, ring slots, and the token embedding (op 0)
+    hipLaunchKernelGGL(step_prologue_kernel, dim3((d.D + 255) / 256, B), dim3(256), 0, s, st.ctx, d.nfull,
+                       (int64_t)d.cap, st.base, w.pos, w.visible, w.slots, shape->fmt_embed,
+                       static_cast<const uint8_t*>(weights->embed), embed_rb, d.V, d.D, tokens, w.hidden);
     if (hipGetLastError() != hipSuccess) return RTA_ERR_LAUNCH;
-    RTA_TRY(rta_embed(shape->fmt_embed, weights->embed, d.V, d.D, tokens, B, w.hidden, stream));
 
     // Layer capture: the residual stream after layer l is whole once the next norm has
     // added the last projection's pending K slabs, so it is copied right after that norm.

@@ -39,11 +39,7 @@ __global__ void __launch_bounds__(256) embed_kernel(int fmt, const uint8_t* __re
                                                     float* __restrict__ out) {
     const int b = blockIdx.y, c = blockIdx.x * 256 + threadIdx.x;
     if (c >= hidden) return;
-    const uint32_t id = ids[b];
-    float v = 0.0f;
-    if (id < (uint32_t)vocab) v = dequant_value(fmt, table + (int64_t)id * row_bytes, c);
-    else if (c == 0) raise_error(RTA_DEVERR_TOKEN);
-    out[(int64_t)b * hidden + c] = v;
+    out[(int64_t)b * hidden + c] = embed_value(fmt, table, row_bytes, vocab, ids[b], c);
 }
 
 // --------------------------------------------------------------- RMSNorm ----
@@ -564,13 +560,9 @@ extern "C" {
 
 int rta_embed(int fmt, const void* table, int vocab, int hidden, const uint32_t* ids, int batch, float* out,
               rta_stream_t stream) {
-    if (!host::valid_format(fmt)) return RTA_ERR_FORMAT;
-    if (!table || !ids || !out) return RTA_ERR_NULL;
-    const int64_t rb = host::row_bytes(fmt, hidden);
-    if (vocab <= 0 || hidden <= 0 || batch <= 0 || rb <= 0) return RTA_ERR_SHAPE;
-    if (!host::aligned(table, fmt == RTA_F32 || fmt == RTA_Q4_K ? 4 : 2) || !host::aligned(out, 4) ||
-        !host::aligned(ids, 4))
-        return RTA_ERR_ALIGN;
+    int64_t rb = 0;
+    const int rc = host::embed_args(fmt, table, vocab, hidden, ids, batch, out, &rb);
+    if (rc) return rc;
     hipLaunchKernelGGL(embed_kernel, dim3((hidden + 255) / 256, batch), dim3(256), 0, (hipStream_t)stream, fmt,
                        static_cast<const uint8_t*>(table), rb, vocab, hidden, ids, out);
     return hipGetLastError() == hipSuccess ? RTA_OK : RTA_ERR_LAUNCH;
