@@ -17,7 +17,8 @@
 // balanced contiguous range of units of TPW tiles (kSwiglu: TPW/2 gate tiles and the
 // TPW/2 up tiles of the same rows) and, per superblock, reads the x operands of a
 // column offset from LDS once for all TPW tiles.  The weights of the next DEPTH - 1
-// superblocks are in flight in registers while one is multiplied.  Tile format and
+// superblocks are in flight in registers while one is multiplied.  The slab's images
+// reach LDS by direct global -> LDS loads (global_load_lds_dwordx4).  Tile format and
 // operand layouts are those of rta_tiled.hpp.
 #pragma once
 #include "rta_tiled.hpp"
@@ -233,42 +234,27 @@ __global__ void __launch_bounds__(64 * NWAVES) gemm_packed_kernel(
         }
     };
 
-    // the slab's x images: the first part's loads go out first (they complete before
-    // the weights issued behind them), then DEPTH - 1 superblocks of weights, then the
-    // stores; the rest of the slab follows in parts of kChunk loads per thread
+    // the slab's x images go to LDS by direct global -> LDS loads (lane l of a wave's
+    // instruction lands at the wave's LDS base + 16 l, so a wave moves 64 consecutive
+    // 16-byte words per instruction without a register round trip); all of them are in
+    // flight at once, with DEPTH - 1 superblocks of weights issued behind them
     constexpr int kThreads = 64 * NWAVES;
     constexpr int kPer = (kCap * (int)(sizeof(Img) / 16) + kThreads - 1) / kThreads;
-    constexpr int kParts = (kPer + 11) / 12;                  // at most 12 loads in flight per part
-    constexpr int kChunk = (kPer + kParts - 1) / kParts;
     const int n16 = nsb * (int)(sizeof(Img) / 16);
     const uint4* xsrc = reinterpret_cast<const uint4*>(xi + sb0);
     uint4* xdst = reinterpret_cast<uint4*>(sx);
-    // Loads and stores are both unconditional (indexes past the slab repeat its last
-    // chunk: the same bytes to the same place), so the compiler cannot sink a load into
-    // a guarded store, where it would wait for that one load on the spot.
-    auto copy_part = [&](int k0, bool prefetch_weights, Raw (*bufp)[TPW]) {
-        uint4 tmp[kChunk];
+    using lds_ptr = __attribute__((address_space(3))) void*;
 #pragma unroll
-        for (int k = 0; k < kChunk; ++k) {
-            const int i = tid + (k0 + k) * kThreads;
-            tmp[k] = xsrc[i < n16 ? i : n16 - 1];
-        }
-        if (prefetch_weights && nit > 0) {
-#pragma unroll
-            for (int d = 0; d < DEPTH - 1; ++d) load_next(bufp[d]);
-        }
-#pragma unroll
-        for (int k = 0; k < kChunk; ++k) {
-            const int i = tid + (k0 + k) * kThreads;
-            xdst[i < n16 ? i : n16 - 1] = tmp[k];
-        }
-    };
-    Raw buf[DEPTH][TPW];
-    copy_part(0, true, buf);
-    for (int k0 = kChunk; k0 < kPer; k0 += kChunk) {
-        if (k0 * kThreads >= n16) break;   // uniform
-        copy_part(k0, false, buf);
+    for (int k = 0; k < kPer; ++k) {
+        const int i0 = k * kThreads + wave * 64;   // the wave's first word (uniform)
+        if (i0 + lane < n16) __builtin_amdgcn_global_load_lds(xsrc + i0 + lane, (lds_ptr)(xdst + i0), 16, 0, 0);
     }
+    Raw buf[DEPTH][TPW];
+    if (nit > 0) {
+#pragma unroll
+        for (int d = 0; d < DEPTH - 1; ++d) load_next(buf[d]);
+    }
+    __builtin_amdgcn_s_waitcnt(0x0F70);   // vmcnt(0): the direct loads have landed
     __syncthreads();
 
     // the RMSNorm factor of each batch row this lane's results belong to
