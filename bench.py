@@ -26,6 +26,8 @@ step the dominant kernel is the one with the largest share of a step (calls per
 step x mean duration); every timed kernel is listed under "kernels".
 read_ceiling: the achievable HBM read rate (a streaming-read kernel over 1 GiB);
 roofline.frac_of_ceiling = achieved / that rate, beside frac = achieved / 8 TB/s.
+read_ceiling_at_size (gemv_q4k): the same kernel reading the GEMV's byte count once per
+launch, timed like the GEMV; roofline.frac_of_size_ceiling = achieved / its rate.
 """
 import argparse
 import json
@@ -113,6 +115,40 @@ def read_ceiling(torch, n_bytes=1 << 30):
     del buf
     return {"kernel": f"stream_read_kernel, {names[best[2]]} (lib/librta_ceiling.so)", "bytes": n_bytes,
             "gbs": best[0], "frac_of_peak": best[0] / HBM_PEAK_GBS, "blocks": best[1]}
+
+
+def read_ceiling_at(torch, n_bytes):
+    """What one launch that reads n_bytes once costs on this GPU: the streaming-read kernels of
+    lib/librta_ceiling.so over rotated n_bytes buffers (more than 3x the last-level cache in
+    all, one buffer per launch), 200 launches in a HIP graph timed as time_kernel times the
+    readouts; the best mean launch duration over the variants and grid sizes."""
+    import ctypes
+    path = ROOT / "ray-tracing-attention_amd" / "lib" / "librta_ceiling.so"
+    if not path.is_file():
+        return None
+    lib = ctypes.CDLL(str(path))
+    lib.rta_ceiling_stream_read.argtypes = [ctypes.c_void_p, ctypes.c_int64, ctypes.c_void_p, ctypes.c_int,
+                                            ctypes.c_int, ctypes.c_void_p]
+    lib.rta_ceiling_stream_read.restype = ctypes.c_int
+    dev = torch.device("cuda:0")
+    n = (n_bytes + 15) // 16 * 16
+    copies = [torch.empty(n, dtype=torch.uint8, device=dev).fill_(7)
+              for _ in range(int(min(256, max(2, 3 * CACHE_BYTES // n + 1))))]
+    out = torch.empty(65536, dtype=torch.int32, device=dev)
+    best = None
+    for variant in range(4):
+        for blocks in (256, 512, 1024, 2048, 4096):
+            def launch(i):
+                rc = lib.rta_ceiling_stream_read(copies[i % len(copies)].data_ptr(), n, out.data_ptr(), blocks,
+                                                 variant, torch.cuda.current_stream().cuda_stream)
+                if rc:
+                    raise RuntimeError(f"rta_ceiling_stream_read failed: {rc}")
+            ms = time_kernel(torch, launch)
+            if best is None or ms < best[0]:
+                best = (ms, blocks, variant)
+    del copies
+    return {"bytes": n, "us": best[0] * 1e3, "gbs": n / (best[0] * 1e-3) / 1e9, "blocks": best[1],
+            "variant": best[2]}
 
 
 def cpu_model():
@@ -761,6 +797,10 @@ def companions(torch, args, orc):
                                                        "unit": "GB/s", "frac": ach / HBM_PEAK_GBS,
                                                        "traffic": traffic_for("gemv_q4k")},
                        "kernel": g["kernel"], "kernel_ms_mean": k, "parity": pg, "config": g["config"]}
+    at = read_ceiling_at(torch, g["alg_bytes"])
+    if at:
+        out["gemv_q4k"]["read_ceiling_at_size"] = at
+        out["gemv_q4k"]["roofline"]["frac_of_size_ceiling"] = ach / at["gbs"]
     return out
 
 
@@ -827,6 +867,11 @@ def main():
         line["read_ceiling"] = ceil
         line["roofline"]["ceiling"] = ceil["gbs"]
         line["roofline"]["frac_of_ceiling"] = achieved / ceil["gbs"]
+    if args.workload == "gemv_q4k":
+        at = read_ceiling_at(torch, alg_k)
+        if at:
+            line["read_ceiling_at_size"] = at
+            line["roofline"]["frac_of_size_ceiling"] = achieved / at["gbs"]
     if args.workload == "decode" and not args.no_companions:
         line["companions"] = companions(torch, args, orc)
     print(json.dumps(line), flush=True)
