@@ -582,17 +582,20 @@ int residual_norm_image(int fmt, float* hidden, const float* part, int nslab, co
     const int nbt = batch > 16 ? 2 : 1;
     const dim3 g((width + 1023) / 1024, 16 * nbt), b(256);
     const bool q4 = (fmt & 0xff) == RTA_Q4_K;
-    if (nbt == 1) {
-        if (q4) hipLaunchKernelGGL((residual_norm_image_kernel<RTA_Q4_K, 1>), g, b, 0, s, hidden, part, nslab, w,
-                                   width, batch, ss, out, static_cast<XImage<1>*>(img));
-        else hipLaunchKernelGGL((residual_norm_image_kernel<RTA_Q6_K, 1>), g, b, 0, s, hidden, part, nslab, w, width,
-                                batch, ss, out, static_cast<XImage<1>*>(img));
-    } else {
-        if (q4) hipLaunchKernelGGL((residual_norm_image_kernel<RTA_Q4_K, 2>), g, b, 0, s, hidden, part, nslab, w,
-                                   width, batch, ss, out, static_cast<XImage<2>*>(img));
-        else hipLaunchKernelGGL((residual_norm_image_kernel<RTA_Q6_K, 2>), g, b, 0, s, hidden, part, nslab, w, width,
-                                batch, ss, out, static_cast<XImage<2>*>(img));
-    }
+    with_slab_count(nslab, [&](auto ns) {
+        constexpr int NS = decltype(ns)::value;
+        if (nbt == 1) {
+            if (q4) hipLaunchKernelGGL((residual_norm_image_kernel<RTA_Q4_K, 1, NS>), g, b, 0, s, hidden, part, nslab,
+                                       w, width, batch, ss, out, static_cast<XImage<1>*>(img));
+            else hipLaunchKernelGGL((residual_norm_image_kernel<RTA_Q6_K, 1, NS>), g, b, 0, s, hidden, part, nslab, w,
+                                    width, batch, ss, out, static_cast<XImage<1>*>(img));
+        } else {
+            if (q4) hipLaunchKernelGGL((residual_norm_image_kernel<RTA_Q4_K, 2, NS>), g, b, 0, s, hidden, part, nslab,
+                                       w, width, batch, ss, out, static_cast<XImage<2>*>(img));
+            else hipLaunchKernelGGL((residual_norm_image_kernel<RTA_Q6_K, 2, NS>), g, b, 0, s, hidden, part, nslab, w,
+                                    width, batch, ss, out, static_cast<XImage<2>*>(img));
+        }
+    });
     return hipGetLastError() == hipSuccess ? RTA_OK : RTA_ERR_LAUNCH;
 }
 
@@ -604,17 +607,20 @@ int swiglu_image(int fmt, const float* part, int nslab, int width, int batch, vo
     const int nbt = batch > 16 ? 2 : 1;
     const dim3 g((width + 1023) / 1024, 16 * nbt), b(256);
     const bool q4 = (fmt & 0xff) == RTA_Q4_K;
-    if (nbt == 1) {
-        if (q4) hipLaunchKernelGGL((swiglu_image_kernel<RTA_Q4_K, 1>), g, b, 0, s, part, nslab, width, batch,
-                                   static_cast<XImage<1>*>(img));
-        else hipLaunchKernelGGL((swiglu_image_kernel<RTA_Q6_K, 1>), g, b, 0, s, part, nslab, width, batch,
-                                static_cast<XImage<1>*>(img));
-    } else {
-        if (q4) hipLaunchKernelGGL((swiglu_image_kernel<RTA_Q4_K, 2>), g, b, 0, s, part, nslab, width, batch,
-                                   static_cast<XImage<2>*>(img));
-        else hipLaunchKernelGGL((swiglu_image_kernel<RTA_Q6_K, 2>), g, b, 0, s, part, nslab, width, batch,
-                                static_cast<XImage<2>*>(img));
-    }
+    with_slab_count(nslab, [&](auto ns) {
+        constexpr int NS = decltype(ns)::value;
+        if (nbt == 1) {
+            if (q4) hipLaunchKernelGGL((swiglu_image_kernel<RTA_Q4_K, 1, NS>), g, b, 0, s, part, nslab, width, batch,
+                                       static_cast<XImage<1>*>(img));
+            else hipLaunchKernelGGL((swiglu_image_kernel<RTA_Q6_K, 1, NS>), g, b, 0, s, part, nslab, width, batch,
+                                    static_cast<XImage<1>*>(img));
+        } else {
+            if (q4) hipLaunchKernelGGL((swiglu_image_kernel<RTA_Q4_K, 2, NS>), g, b, 0, s, part, nslab, width, batch,
+                                       static_cast<XImage<2>*>(img));
+            else hipLaunchKernelGGL((swiglu_image_kernel<RTA_Q6_K, 2, NS>), g, b, 0, s, part, nslab, width, batch,
+                                    static_cast<XImage<2>*>(img));
+        }
+    });
     return hipGetLastError() == hipSuccess ? RTA_OK : RTA_ERR_LAUNCH;
 }
 

@@ -95,7 +95,10 @@ __device__ __forceinline__ void image_row(XImage<NBT>& im, int b, bool live, flo
 // zeros.  For b < batch: hidden[b] += the K-slab partials [slab][32][width] (slab order)
 // and ss[4 b + c] = the chunk's sum of hidden^2 (entries past the chunks zero), as
 // residual_norm_deferred_kernel; out (may be null) = hidden * w in fp32 as well.
-template <int FMT, int NBT>
+// NS: the slab loads in flight, NS >= nslab (1, 2, 4, 8, 16; every slab's load issued at
+// once, indexes past the last slab clamped to it and not added), or 0 for a loop over more
+// than 16 slabs.  The partials are added in slab order either way.
+template <int FMT, int NBT, int NS>
 __global__ void __launch_bounds__(256) residual_norm_image_kernel(float* __restrict__ hidden,
                                                                   const float* __restrict__ part, int nslab,
                                                                   const float* __restrict__ w, int width, int batch,
@@ -112,15 +115,33 @@ __global__ void __launch_bounds__(256) residual_norm_image_kernel(float* __restr
     if (live && sb < nsbt) {
         float4* hr = reinterpret_cast<float4*>(hidden + (int64_t)b * width);
         v = hr[i];
+        if (nslab > 0) {   // uniform
+            const float4* pr = reinterpret_cast<const float4*>(part + (int64_t)b * width) + i;
+            const int64_t ps = (int64_t)32 * width / 4;   // float4s from one slab to the next
+            if constexpr (NS > 0) {
+                float4 p[NS];
+#pragma unroll
+                for (int k = 0; k < NS; ++k) p[k] = pr[(k < nslab ? k : nslab - 1) * ps];
+#pragma unroll
+                for (int k = 0; k < NS; ++k)
+                    if (k < nslab) {
+                        v.x += p[k].x;
+                        v.y += p[k].y;
+                        v.z += p[k].z;
+                        v.w += p[k].w;
+                    }
+            } else {
 #pragma unroll 4
-        for (int k = 0; k < nslab; ++k) {
-            const float4 p = reinterpret_cast<const float4*>(part + ((int64_t)k * 32 + b) * width)[i];
-            v.x += p.x;
-            v.y += p.y;
-            v.z += p.z;
-            v.w += p.w;
+                for (int k = 0; k < nslab; ++k) {
+                    const float4 p = pr[k * ps];
+                    v.x += p.x;
+                    v.y += p.y;
+                    v.z += p.z;
+                    v.w += p.w;
+                }
+            }
+            hr[i] = v;
         }
-        if (nslab > 0) hr[i] = v;
         sq = v.x * v.x + v.y * v.y + v.z * v.z + v.w * v.w;
         const float4 g = reinterpret_cast<const float4*>(w)[i];
         v = float4{v.x * g.x, v.y * g.y, v.z * g.z, v.w * g.w};
@@ -145,7 +166,8 @@ __global__ void __launch_bounds__(256) residual_norm_image_kernel(float* __restr
 // added in slab order as gemm_reduce_kernel adds them) written as the x image of the down
 // projection: block (c, b) as residual_norm_image_kernel, wave k = superblock 4 c + k of
 // row b (zeros past the batch), lane = 4 consecutive columns.
-template <int FMT, int NBT>
+// NS as in residual_norm_image_kernel.
+template <int FMT, int NBT, int NS>
 __global__ void __launch_bounds__(256) swiglu_image_kernel(const float* __restrict__ part, int nslab, int width,
                                                            int batch, XImage<NBT>* __restrict__ img) {
     const int c = blockIdx.x, b = blockIdx.y, lane = threadIdx.x & 63;
@@ -156,9 +178,9 @@ __global__ void __launch_bounds__(256) swiglu_image_kernel(const float* __restri
     if (live) {
         const int i = c * 256 + threadIdx.x;   // columns 4 i .. 4 i + 3
         float g[4] = {0.0f, 0.0f, 0.0f, 0.0f}, u[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-        for (int k = 0; k < nslab; ++k) {
-            const float4* p = reinterpret_cast<const float4*>(part + ((int64_t)k * 32 + b) * 2 * width) + 2 * i;
-            const float4 a = p[0], e = p[1];
+        const float4* pr = reinterpret_cast<const float4*>(part + (int64_t)b * 2 * width) + 2 * i;
+        const int64_t ps = (int64_t)32 * 2 * width / 4;   // float4s from one slab to the next
+        auto add = [&](float4 a, float4 e) {
             g[0] += a.x;
             u[0] += a.y;
             g[1] += a.z;
@@ -167,6 +189,20 @@ __global__ void __launch_bounds__(256) swiglu_image_kernel(const float* __restri
             u[2] += e.y;
             g[3] += e.z;
             u[3] += e.w;
+        };
+        if constexpr (NS > 0) {
+            float4 a[NS], e[NS];
+#pragma unroll
+            for (int k = 0; k < NS; ++k) {
+                const float4* p = pr + (k < nslab ? k : nslab - 1) * ps;
+                a[k] = p[0];
+                e[k] = p[1];
+            }
+#pragma unroll
+            for (int k = 0; k < NS; ++k)
+                if (k < nslab) add(a[k], e[k]);
+        } else {
+            for (int k = 0; k < nslab; ++k) add(pr[k * ps], pr[k * ps + 1]);
         }
         v = float4{swiglu(g[0], u[0]), swiglu(g[1], u[1]), swiglu(g[2], u[2]), swiglu(g[3], u[3])};
     }

@@ -126,6 +126,10 @@ int residual_rmsnorm(float* hidden, const float* part, int nslab, const float* w
 // 4096 columns spreads over up to 4 blocks.
 constexpr int kNormChunk = 1024;
 
+// NS: the slab loads in flight, NS >= nslab (1, 2, 4, 8, 16; every slab's load issued at
+// once, indexes past the last slab clamped to it and not added), or 0 for a loop over more
+// than 16 slabs.  The partials are added in slab order either way.
+template <int NS>
 __global__ void __launch_bounds__(256) residual_norm_deferred_kernel(float* __restrict__ hidden,
                                                                      const float* __restrict__ part, int nslab,
                                                                      const float* __restrict__ w, int width,
@@ -137,15 +141,33 @@ __global__ void __launch_bounds__(256) residual_norm_deferred_kernel(float* __re
     if (i < n4) {
         float4* hr = reinterpret_cast<float4*>(hidden + (int64_t)b * width);
         float4 v = hr[i];
+        if (nslab > 0) {   // uniform
+            const float4* pr = reinterpret_cast<const float4*>(part + (int64_t)b * width) + i;
+            const int64_t ps = (int64_t)32 * width / 4;   // float4s from one slab to the next
+            if constexpr (NS > 0) {
+                float4 p[NS];
+#pragma unroll
+                for (int k = 0; k < NS; ++k) p[k] = pr[(k < nslab ? k : nslab - 1) * ps];
+#pragma unroll
+                for (int k = 0; k < NS; ++k)
+                    if (k < nslab) {
+                        v.x += p[k].x;
+                        v.y += p[k].y;
+                        v.z += p[k].z;
+                        v.w += p[k].w;
+                    }
+            } else {
 #pragma unroll 4
-        for (int k = 0; k < nslab; ++k) {
-            const float4 p = reinterpret_cast<const float4*>(part + ((int64_t)k * 32 + b) * width)[i];
-            v.x += p.x;
-            v.y += p.y;
-            v.z += p.z;
-            v.w += p.w;
+                for (int k = 0; k < nslab; ++k) {
+                    const float4 p = pr[k * ps];
+                    v.x += p.x;
+                    v.y += p.y;
+                    v.z += p.z;
+                    v.w += p.w;
+                }
+            }
+            hr[i] = v;
         }
-        if (nslab > 0) hr[i] = v;
         sq = v.x * v.x + v.y * v.y + v.z * v.z + v.w * v.w;
         const float4 g = reinterpret_cast<const float4*>(w)[i];
         reinterpret_cast<float4*>(out + (int64_t)b * width)[i] = float4{v.x * g.x, v.y * g.y, v.z * g.z, v.w * g.w};
@@ -167,8 +189,11 @@ int residual_norm_deferred(float* hidden, const float* part, int nslab, const fl
     if (!host::aligned(hidden, 16) || !host::aligned(w, 16) || !host::aligned(out, 16) ||
         (part && !host::aligned(part, 16)))
         return RTA_ERR_ALIGN;
-    hipLaunchKernelGGL(residual_norm_deferred_kernel, dim3((width + kNormChunk - 1) / kNormChunk, batch),
-                       dim3(kNormChunk / 4), 0, s, hidden, part, nslab, w, width, out, ss);
+    with_slab_count(nslab, [&](auto ns) {
+        hipLaunchKernelGGL((residual_norm_deferred_kernel<decltype(ns)::value>),
+                           dim3((width + kNormChunk - 1) / kNormChunk, batch), dim3(kNormChunk / 4), 0, s, hidden,
+                           part, nslab, w, width, out, ss);
+    });
     return hipGetLastError() == hipSuccess ? RTA_OK : RTA_ERR_LAUNCH;
 }
 
