@@ -910,7 +910,6 @@ struct MmaWaveLds {                                         // one wave's region
     static constexpr int total = f + 16;
 };
 static_assert(MmaWaveLds::w % 4 == 0 && MmaWaveLds::total % 4 == 0, "16-byte aligned rows");
-constexpr int kMmaLdsBytes = 4 * MmaWaveLds::total * 4;
 
 // max / sum over the 16 lanes of each row (quad_perm [1,0,3,2], [2,3,0,1],
 // row_half_mirror, row_mirror)
@@ -934,8 +933,11 @@ __device__ __forceinline__ uint32_t pk_fms_f16(uint32_t a, uint32_t b, uint32_t 
                                                                   -__builtin_bit_cast(h2v_t, c)));
 }
 
-template <int G, int KPW>
-__global__ void __launch_bounds__(256, 2) attn_chunk_mma_kernel(const AttnArgs a) {
+// NWV waves per workgroup: 4 (two workgroups per CU), or 8 with one kv head per wave
+// (one workgroup per CU, when the whole tile list fits one tile per CU: each tile's
+// serial work is then halved).
+template <int G, int KPW, int NWV = 4>
+__global__ void __launch_bounds__(64 * NWV, 2) attn_chunk_mma_kernel(const AttnArgs a) {
     extern __shared__ __align__(16) float lds[];
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -958,12 +960,12 @@ __global__ void __launch_bounds__(256, 2) attn_chunk_mma_kernel(const AttnArgs a
     const int32_t* S = a.plan;
     const int64_t T = uni(S[a.nseq]);
     const int64_t P = a.nwg < T ? a.nwg : T;   // every workgroup below P has a tile
-    // v: this workgroup's place in the split.  Workgroups b and b + nwg / 2 are the two
-    // resident on one compute unit (dispatched in that order), so they take adjacent
-    // shares and every compute unit gets floor or ceil of 2 T / P tiles; the plain order
-    // would give both the same floor or ceil of T / P
+    // v: this workgroup's place in the split.  With two workgroups per CU, workgroups b
+    // and b + nwg / 2 are the two resident on one compute unit (dispatched in that
+    // order), so they take adjacent shares and every compute unit gets floor or ceil of
+    // 2 T / P tiles; the plain order would give both the same floor or ceil of T / P
     const int b = blockIdx.x, half = a.nwg / 2;
-    const int64_t v = (P == a.nwg && (a.nwg & 1) == 0) ? 2 * (b % half) + b / half : b;
+    const int64_t v = (a.per_cu == 2 && P == a.nwg && (a.nwg & 1) == 0) ? 2 * (b % half) + b / half : b;
     if (v >= P) return;   // (all of them when T = 0)
     const int64_t ta = v * T / P, tb = (v + 1) * T / P;
     int s = uni(S[a.nseq + 1 + v]);
@@ -2208,22 +2210,21 @@ static hipError_t launch_chunk(const AttnArgs& a, int lds, hipStream_t s) {
 
 // Q4_K keys of at most 8 kv heads are scored on the matrix cores, with q operands
 // prepared once per (sequence, kv head).
-template <int G, int KPW>
+template <int G, int KPW, int NWV = 4>
 static hipError_t launch_chunk_mma(const AttnArgs& a, hipStream_t s) {
+    constexpr int lds = NWV * MmaWaveLds::total * 4;
     static bool configured = false;
     if (!configured) {
-        const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&attn_chunk_mma_kernel<G, KPW>),
-                                                 hipFuncAttributeMaxDynamicSharedMemorySize, kMmaLdsBytes);
+        const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&attn_chunk_mma_kernel<G, KPW, NWV>),
+                                                 hipFuncAttributeMaxDynamicSharedMemorySize, lds);
         if (e != hipSuccess) return e;
         configured = true;
     }
-    hipLaunchKernelGGL((attn_chunk_mma_kernel<G, KPW>), dim3(a.nwg), dim3(256), kMmaLdsBytes, s, a);
+    hipLaunchKernelGGL((attn_chunk_mma_kernel<G, KPW, NWV>), dim3(a.nwg), dim3(64 * NWV), lds, s, a);
     return hipGetLastError();
 }
 
-// Workgroups of the matrix-core kernel: two per compute unit (its LDS and registers
-// admit two), all resident at once.
-static int attn_mma_workgroups(int per_cu) {
+static int compute_units() {
     static int cus = 0;
     if (cus == 0) {
         int dev = 0, n = 0;
@@ -2232,7 +2233,22 @@ static int attn_mma_workgroups(int per_cu) {
             n = 256;
         cus = n;
     }
+    return cus;
+}
+
+// Workgroups of the matrix-core kernels: per_cu per compute unit, all resident at once.
+static int attn_mma_workgroups(int per_cu) {
+    const int cus = compute_units();
     return per_cu * cus < kMaxWg ? per_cu * cus : kMaxWg;
+}
+
+// Workgroups per CU of attn_chunk_mma_kernel (Q4_K keys, Q6_K values): one 8-wave
+// workgroup (one kv head per wave) when more than 4 kv heads share a superblock pair and
+// the tile list cannot exceed one tile per CU (nseq x max_tiles <= CUs), else two 4-wave
+// workgroups.  The tile plan (attn_qprep_kernel, full_middle_kernel) and the merge follow
+// the same count.
+static int mma_per_cu(int nseq, int64_t max_tiles, int hkv) {
+    return (hkv > 4 && (int64_t)nseq * max_tiles <= compute_units()) ? 1 : 2;
 }
 
 // Q6_K keys with Q4_K values of at most 4 kv heads: scores and P V on the matrix cores.
@@ -2262,6 +2278,7 @@ static hipError_t launch_chunk_k(const AttnArgs& a, int lds, hipStream_t s) {
                 hipLaunchKernelGGL((attn_qprep_kernel<G>), dim3(a.hkv + (a.plan ? 1 : 0), a.nseq), dim3(kWave), 0, s, a);
             if constexpr (VF == RTA_Q6_K) {   // scores and P V on the matrix cores
                 if (a.hkv <= 4) return launch_chunk_mma<G, 1>(a, s);
+                if (a.per_cu == 1) return launch_chunk_mma<G, 1, 8>(a, s);
                 return launch_chunk_mma<G, 2>(a, s);
             }
             if (a.hkv <= 4) return launch_chunk<KF, VF, G, 1>(a, lds, s);
@@ -2637,7 +2654,7 @@ int decode_attention_gate_stride(const float* q, int nseq, int hq, int hkv, int 
     if ((fmt_k == RTA_Q4_K && fmt_v == RTA_Q6_K && hkv <= 8) ||
         (fmt_k == RTA_Q6_K && fmt_v == RTA_Q4_K && hkv <= 4)) {   // the matrix-core kernels' tile-list split
         a.plan = reinterpret_cast<int32_t*>(reinterpret_cast<uint8_t*>(a.qop) + (size_t)nseq * hkv * 6 * kWave * sizeof(uint4));
-        a.per_cu = fmt_k == RTA_Q6_K ? kMma6PerCu : 2;
+        a.per_cu = fmt_k == RTA_Q6_K ? kMma6PerCu : mma_per_cu(nseq, a.max_tiles, hkv);
         a.nwg = attn_mma_workgroups(a.per_cu);
         a.rstride = a.max_tiles;
     }
@@ -2702,7 +2719,7 @@ int full_layer_middle(const float* proj, int64_t slab_stride, int row_stride, in
         a.ctx_len = ctx_len;
         a.capacity = capacity;
         a.max_tiles = ((int64_t)max_ctx + kTile - 1) / kTile;
-        a.per_cu = 2;
+        a.per_cu = mma_per_cu(batch, a.max_tiles, hkv);
         a.nwg = attn_mma_workgroups(a.per_cu);
         a.plan = reinterpret_cast<int32_t*>(reinterpret_cast<uint8_t*>(p.qop) +
                                             (size_t)batch * hkv * 6 * kWave * sizeof(uint4));

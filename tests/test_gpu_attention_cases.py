@@ -253,6 +253,17 @@ def test_tile_split_64_sequences_8_2_heads(torch_dev):
     _sized_case(torch, dev, 54, ctx, 8, 2, (orc.Q4_K, orc.Q6_K))
 
 
+@pytest.mark.parametrize("ctx", [[8192, 8192], [8192, 1], [8192, 8100, 64]])
+def test_one_workgroup_per_cu_switch(torch_dev, ctx):
+    """32 / 8 heads, K Q4_K / V Q6_K.  A tile list that cannot exceed one tile per compute
+    unit (nseq x ceil(max_ctx / 64) <= 256 on MI355X) runs one 8-wave workgroup per CU, one
+    kv head per wave: [8192, 8192] gives each of the 256 workgroups exactly one tile,
+    [8192, 1] a ragged list of 129.  [8192, 8100, 64] (384 > 256) runs two 4-wave
+    workgroups per CU again."""
+    torch, dev = torch_dev
+    _sized_case(torch, dev, 57, ctx, 32, 8, (orc.Q4_K, orc.Q6_K), gate=True)
+
+
 def test_decode_step_attention_workload(torch_dev):
     """The attention call of one full layer of the 9B decode step at batch 32: 32 / 8 heads,
     contexts U[256, 8192] (2,200+ tiles, four or five per workgroup)."""
