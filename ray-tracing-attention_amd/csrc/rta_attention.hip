@@ -284,12 +284,10 @@ __device__ __forceinline__ QOp make_qop(const float* __restrict__ qg, int lane) 
             sum[kb] += v[kb][i];
         }
     }
-    mx = fmaxf(mx, __shfl_xor(mx, 16, kWave));
-    mx = fmaxf(mx, __shfl_xor(mx, 32, kWave));
+    mx = max_xor32(max_xor16(mx));
 #pragma unroll
     for (int kb = 0; kb < 4; ++kb) {   // fixed order: ((u0 + u1) + (u2 + u3))
-        sum[kb] += __shfl_xor(sum[kb], 16, kWave);
-        sum[kb] += __shfl_xor(sum[kb], 32, kWave);
+        sum[kb] = add_xor32(add_xor16(sum[kb]));
     }
     const int e = operand_exponent(mx);
     const float sg = ldexpf(1.0f, 14 - e);
@@ -1904,7 +1902,7 @@ __global__ void __launch_bounds__(256) full_middle_kernel(const MiddleArgs p) {
     auto norm_rope = [&](float2 v, const float* w) {
         if (w) {
             float ss = v.x * v.x + v.y * v.y;
-            for (int off = 32; off > 0; off >>= 1) ss += __shfl_xor(ss, off, kWave);
+            ss = wave_sum_dpp(ss);
             const float inv = 1.0f / sqrtf(ss / (float)hd + p.eps);
             v.x = v.x * inv * w[2 * lane];
             v.y = v.y * inv * w[2 * lane + 1];
@@ -1935,7 +1933,7 @@ __global__ void __launch_bounds__(256) full_middle_kernel(const MiddleArgs p) {
         qsv[wave][2 * lane] = v.x;
         qsv[wave][2 * lane + 1] = v.y;
         float mx = fmaxf(fabsf(v.x), fabsf(v.y));
-        for (int off = 32; off > 0; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off, kWave));
+        mx = wave_max_dpp(mx);
         const float sg = ldexpf(1.0f, 14 - operand_exponent(mx));
         __builtin_amdgcn_wave_barrier();
         uint4* dst = p.qop + ((int64_t)b * p.hkv + kvh) * 6 * kWave;

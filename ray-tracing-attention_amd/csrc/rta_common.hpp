@@ -48,34 +48,92 @@ __device__ __forceinline__ float group_sum(float v, int width) {
     return v;
 }
 
-__device__ __forceinline__ float group_max(float v, int width) {
-    for (int off = width >> 1; off > 0; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, kWave));
-    return v;
-}
+
 
 template <int CTRL>
 __device__ __forceinline__ float dpp_mov(float v) {
     return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), CTRL, 0xF, 0xF, true));
 }
 
+// The gfx950 row swaps with v as both operands (v_permlane16_swap / v_permlane32_swap):
+// every lane gets the value of its lane position in the even and the odd 16-lane row of
+// its row pair, or in the lower and the upper 32-lane half.  No LDS round trip.
+__device__ __forceinline__ void rows16_pair(float v, float& even, float& odd) {
+    const int b = __builtin_bit_cast(int, v);
+    const auto r = __builtin_amdgcn_permlane16_swap(b, b, false, false);
+    even = __builtin_bit_cast(float, (int)r[0]);
+    odd = __builtin_bit_cast(float, (int)r[1]);
+}
+__device__ __forceinline__ void halves32(float v, float& lo, float& hi) {
+    const int b = __builtin_bit_cast(int, v);
+    const auto r = __builtin_amdgcn_permlane32_swap(b, b, false, false);
+    lo = __builtin_bit_cast(float, (int)r[0]);
+    hi = __builtin_bit_cast(float, (int)r[1]);
+}
+// v + the value of lane ^ 16 (^ 32), as (even row + odd row) (lower + upper half) in
+// every lane: the sum a butterfly step forms, since addition commutes
+__device__ __forceinline__ float add_xor16(float v) {
+    float e, o;
+    rows16_pair(v, e, o);
+    return e + o;
+}
+__device__ __forceinline__ float add_xor32(float v) {
+    float l, h;
+    halves32(v, l, h);
+    return l + h;
+}
+__device__ __forceinline__ float max_xor16(float v) {
+    float e, o;
+    rows16_pair(v, e, o);
+    return fmaxf(e, o);
+}
+__device__ __forceinline__ float max_xor32(float v) {
+    float l, h;
+    halves32(v, l, h);
+    return fmaxf(l, h);
+}
+
 // Sum / max over the 64 lanes of a wave, every lane getting the same result: DPP
 // steps inside each 16-lane row (quad_perm [1,0,3,2], [2,3,0,1], row_half_mirror,
-// row_mirror), then two cross-row shuffles.
+// row_mirror), then the two row swaps.
 __device__ __forceinline__ float wave_sum_dpp(float v) {
     v += dpp_mov<0xB1>(v);
     v += dpp_mov<0x4E>(v);
     v += dpp_mov<0x141>(v);
     v += dpp_mov<0x140>(v);
-    v += __shfl_xor(v, 16, kWave);
-    return v + __shfl_xor(v, 32, kWave);
+    return add_xor32(add_xor16(v));
 }
 __device__ __forceinline__ float wave_max_dpp(float v) {
     v = fmaxf(v, dpp_mov<0xB1>(v));
     v = fmaxf(v, dpp_mov<0x4E>(v));
     v = fmaxf(v, dpp_mov<0x141>(v));
     v = fmaxf(v, dpp_mov<0x140>(v));
-    v = fmaxf(v, __shfl_xor(v, 16, kWave));
-    return fmaxf(v, __shfl_xor(v, 32, kWave));
+    return max_xor32(max_xor16(v));
+}
+
+// Integer minimum over the 64 lanes, every lane getting it (the same DPP steps and row
+// swaps as wave_max_dpp).
+__device__ __forceinline__ int wave_min_int(int v) {
+    v = min(v, __builtin_amdgcn_mov_dpp(v, 0xB1, 0xF, 0xF, true));
+    v = min(v, __builtin_amdgcn_mov_dpp(v, 0x4E, 0xF, 0xF, true));
+    v = min(v, __builtin_amdgcn_mov_dpp(v, 0x141, 0xF, 0xF, true));
+    v = min(v, __builtin_amdgcn_mov_dpp(v, 0x140, 0xF, 0xF, true));
+    const auto r = __builtin_amdgcn_permlane16_swap(v, v, false, false);
+    v = min((int)r[0], (int)r[1]);
+    const auto q = __builtin_amdgcn_permlane32_swap(v, v, false, false);
+    return min((int)q[0], (int)q[1]);
+}
+
+// Max over the lanes whose index differs only in the bits below `width` (a power of two
+// <= 64); every lane of the group ends with the group maximum (exact in any order).
+__device__ __forceinline__ float group_max(float v, int width) {
+    if (width >= 2) v = fmaxf(v, dpp_mov<0xB1>(v));
+    if (width >= 4) v = fmaxf(v, dpp_mov<0x4E>(v));
+    if (width >= 8) v = fmaxf(v, dpp_mov<0x141>(v));
+    if (width >= 16) v = fmaxf(v, dpp_mov<0x140>(v));
+    if (width >= 32) v = max_xor16(v);
+    if (width >= 64) v = max_xor32(v);
+    return v;
 }
 
 // Q4_K 6-bit scale/min codes of group g (0..7) from the scale dwords

@@ -85,7 +85,7 @@ __global__ void __launch_bounds__(64) xprep_kernel(const float* __restrict__ x, 
     float m = 0.0f;
 #pragma unroll
     for (int i = 0; i < 8; ++i) m = fmaxf(m, fabsf(v[i]));
-    for (int off = 16; off > 0; off >>= 1) m = fmaxf(m, __shfl_xor(m, off, kWave));   // within 32 lanes
+    m = group_max(m, 32);   // within 32 lanes
     const int e = operand_exponent(m);
     const float s = ldexpf(1.0f, 14 - e);        // m * s in [2^13, 2^14)
     if (t == 0) p.inv[(int64_t)b * nsb + sb] = b < batch ? ldexpf(1.0f, e - 14) : 0.0f;
@@ -103,8 +103,8 @@ __global__ void __launch_bounds__(64) xprep_kernel(const float* __restrict__ x, 
     *reinterpret_cast<h8_t*>(p.hi + at) = h8_t{hi[0], hi[1], hi[2], hi[3], hi[4], hi[5], hi[6], hi[7]};
     *reinterpret_cast<h8_t*>(p.lo + at) = h8_t{lo[0], lo[1], lo[2], lo[3], lo[4], lo[5], lo[6], lo[7]};
     _Float16* g = reinterpret_cast<_Float16*>(p.g + ((int64_t)b * nsb + sb) * 4);   // 32 f16
-    const float s16 = sum8 + __shfl_xor(sum8, 1, kWave);
-    const float s32 = s16 + __shfl_xor(s16, 2, kWave);
+    const float s16 = sum8 + dpp_mov<0xB1>(sum8);
+    const float s32 = s16 + dpp_mov<0x4E>(s16);
     if constexpr (LAYOUT == kXpQ6Row || LAYOUT == kXpQ6Tile) {
         if ((t & 1) == 0) {   // 16-group u = t / 2
             const int u = t >> 1;
@@ -445,7 +445,7 @@ __global__ void __launch_bounds__(64 * kGemmWaves) gemm_mfma_kernel(
                     if (nslab > 1) {
                         if (ok && b < batch) part[((int64_t)slab * kMaxBatchTile + b) * total_rows + v] = val;
                     } else if constexpr (MODE == kSwiglu) {
-                        const float up = __shfl_xor(val, 1, kWave);   // odd lane holds the up row
+                        const float up = dpp_mov<0xB1>(val);   // odd lane holds the up row
                         if (ok && b < batch && !(li & 1)) y[(int64_t)b * rows + (v >> 1)] = swiglu(val, up);
                     } else if constexpr (MODE == kAccumulate) {
                         if (ok && b < batch) y[(int64_t)b * rows + v] += val;
@@ -463,10 +463,7 @@ __global__ void __launch_bounds__(64 * kGemmWaves) gemm_mfma_kernel(
 #pragma unroll
                     for (int e = 0; e < 4; ++e) {
                         float m = tmax[bt][e];
-                        m = fmaxf(m, __shfl_xor(m, 1, kWave));
-                        m = fmaxf(m, __shfl_xor(m, 2, kWave));
-                        m = fmaxf(m, __shfl_xor(m, 4, kWave));
-                        m = fmaxf(m, __shfl_xor(m, 8, kWave));
+                        m = group_max(m, 16);
                         const int b = bt * 16 + 4 * s + e;
                         if (li == 0 && b < batch) pmax[(int64_t)b * ntg + tg] = m;
                     }
@@ -538,7 +535,7 @@ __global__ void __launch_bounds__(256) gemm_reduce_kernel(const float* __restric
         v = s;
     }
     if constexpr (MODE == kLogits) {
-        for (int off = 32; off > 0; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, kWave));
+        v = wave_max_dpp(v);
         __shared__ float red[4];
         if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
         __syncthreads();

@@ -82,7 +82,7 @@ __global__ void __launch_bounds__(kArgmaxThreads) argmax_margin_kernel(const flo
     int first = INT_MAX;   // branch-free so that the loads of a thread overlap
 #pragma unroll 8
     for (int t = tid; t < nscan; t += kArgmaxThreads) first = (gb[t] >= T && t < first) ? t : first;
-    for (int off = 32; off > 0; off >>= 1) first = min(first, __shfl_xor(first, off, kWave));
+    first = wave_min_int(first);
     if (lane == 0) red_i[wave] = first;
     __syncthreads();
     first = red_i[0];
@@ -104,7 +104,7 @@ __global__ void __launch_bounds__(kArgmaxThreads) argmax_margin_kernel(const flo
     int best = INT_MAX;
 #pragma unroll 4
     for (int r = r0 + tid; r < r1; r += kArgmaxThreads) best = (lb[r] >= T && r < best) ? r : best;
-    for (int off = 32; off > 0; off >>= 1) best = min(best, __shfl_xor(best, off, kWave));
+    best = wave_min_int(best);
     if (lane == 0) red_i[wave] = best;
     __syncthreads();
     if (tid == 0) {

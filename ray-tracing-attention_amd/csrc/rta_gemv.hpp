@@ -34,7 +34,10 @@ __device__ __forceinline__ float dpp(float v) {
 
 // Sum over aligned groups of `width` lanes (power of two, 4..64); every lane of
 // a group ends with the group sum.  quad_perm xor1/xor2, half-row and row
-// mirrors (DPP), then xor 16 / 32 through ds_bpermute.
+// mirrors (DPP), then xor 16 / 32 by the row swaps (v_permlane16/32_swap).
+// SWAPS false: xor 16 / 32 through ds_bpermute instead (the same sums; fewer registers
+// in the three-wave blocks, which the row swaps push past three waves per SIMD).
+template <bool SWAPS = true>
 __device__ __forceinline__ float lane_group_sum(float v, int width) {
     v += dpp<0xB1>(v);   // quad_perm [1,0,3,2]
     v += dpp<0x4E>(v);   // quad_perm [2,3,0,1]
@@ -43,9 +46,22 @@ __device__ __forceinline__ float lane_group_sum(float v, int width) {
     if (width == 8) return v;
     v += dpp<0x140>(v);  // row_mirror
     if (width == 16) return v;
-    v += __shfl_xor(v, 16, kWave);
+    v = SWAPS ? add_xor16(v) : v + __shfl_xor(v, 16, kWave);
     if (width == 32) return v;
-    return v + __shfl_xor(v, 32, kWave);
+    return SWAPS ? add_xor32(v) : v + __shfl_xor(v, 32, kWave);
+}
+
+// Max over the lanes that share lane % lpr (lpr a power of two <= 64): every lane ends
+// with the maximum of its class (exact in any order).  quad_perm xor1 / xor2, row_ror 4
+// and 8 (DPP; a class inside a row is closed under those rotations), then the row swaps.
+__device__ __forceinline__ float max_across_groups(float v, int lpr) {
+    if (lpr <= 1) v = fmaxf(v, dpp<0xB1>(v));
+    if (lpr <= 2) v = fmaxf(v, dpp<0x4E>(v));
+    if (lpr <= 4) v = fmaxf(v, dpp<0x124>(v));   // row_ror:4
+    if (lpr <= 8) v = fmaxf(v, dpp<0x128>(v));   // row_ror:8
+    if (lpr <= 16) v = max_xor16(v);
+    if (lpr <= 32) v = max_xor32(v);
+    return v;
 }
 
 // ---------------------------------------------------------------- Q4_K ----
@@ -261,8 +277,8 @@ __global__ void __launch_bounds__(256) gemv_b1_kernel(const uint8_t* __restrict_
         }
 #pragma unroll
         for (int r = 0; r < R; ++r) {
-            acc[r] = lane_group_sum(acc[r], lpr);
-            if constexpr (kDual) acc2[r] = lane_group_sum(acc2[r], lpr);
+            acc[r] = lane_group_sum<KW == 1>(acc[r], lpr);
+            if constexpr (kDual) acc2[r] = lane_group_sum<KW == 1>(acc2[r], lpr);
         }
         if constexpr (KW > 1) {   // lpr == 64 here: one row pass per wave
             if (lane == 0) {
@@ -302,7 +318,7 @@ __global__ void __launch_bounds__(256) gemv_b1_kernel(const uint8_t* __restrict_
             }
         }
         if constexpr (MODE == kLogits) {
-            for (int off = lpr; off < kWave; off <<= 1) local_max = fmaxf(local_max, __shfl_xor(local_max, off, kWave));
+            local_max = max_across_groups(local_max, lpr);
             if (lane == 0) partial[t] = local_max;
         }
     };
@@ -334,6 +350,8 @@ __global__ void __launch_bounds__(256) gemv_b1_kernel(const uint8_t* __restrict_
             const float4 v = xg[k];
             if ((int)threadIdx.x + k * (int)blockDim.x < nf) ss += v.x * v.x + v.y * v.y + v.z * v.z + v.w * v.w;
         }
+        // (a butterfly of shuffles: the DPP + row-swap sum here raised the register count of
+        // the three-wave blocks past three waves per SIMD)
         for (int off = 32; off > 0; off >>= 1) ss += __shfl_xor(ss, off, kWave);
         if (lane == 0) s_ss[wave] = ss;
         __syncthreads();
@@ -455,7 +473,7 @@ __global__ void __launch_bounds__(256) gemv_kquant_kernel(const uint8_t* __restr
 #pragma unroll
             for (int b = 0; b < NB; ++b) {
                 float m = local_max[b];
-                for (int off = lpr; off < kWave; off <<= 1) m = fmaxf(m, __shfl_xor(m, off, kWave));
+                m = max_across_groups(m, lpr);
                 if (lane == 0 && b < batch) partial[(int64_t)b * ntasks + task] = m;
             }
         }

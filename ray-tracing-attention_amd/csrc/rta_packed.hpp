@@ -47,7 +47,7 @@ constexpr int slab_capacity() {
 template <int FMT, int NBT>
 __device__ __forceinline__ void image_row(XImage<NBT>& im, int b, bool live, float4 v, int lane) {
     float m = fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
-    for (int off = 32; off > 0; off >>= 1) m = fmaxf(m, __shfl_xor(m, off, kWave));
+    m = wave_max_dpp(m);
     const int e = operand_exponent(m);
     const float sc = live ? ldexpf(1.0f, 14 - e) : 0.0f;
     if (lane == 0) im.inv[b] = live ? ldexpf(1.0f, e - 14) : 0.0f;
@@ -63,8 +63,10 @@ __device__ __forceinline__ void image_row(XImage<NBT>& im, int b, bool live, flo
     *reinterpret_cast<h4*>(&im.x[0][b][4 * lane]) = h4{hi[0], hi[1], hi[2], hi[3]};
     *reinterpret_cast<h4*>(&im.x[1][b][4 * lane]) = h4{lo[0], lo[1], lo[2], lo[3]};
     const float s4 = (t[0] + t[1]) + (t[2] + t[3]);
-    const float s8 = s4 + __shfl_xor(s4, 1, kWave);
-    const float s16 = s8 + __shfl_xor(s8, 2, kWave);
+    // (DPP quad_perm xor 1, xor 2, then row_half_mirror, which for a quad-uniform value
+    // reads the same partner value as xor 4)
+    const float s8 = s4 + dpp_mov<0xB1>(s4);
+    const float s16 = s8 + dpp_mov<0x4E>(s8);
     _Float16* g = reinterpret_cast<_Float16*>(&im.g[b][0]);   // 4 segments x 8
     if constexpr (FMT == RTA_Q6_K) {
         if ((lane & 3) == 0) {   // 16-group u = 8 hh + 2 q + sg -> segment 2 hh + sg, slot 2 q
@@ -76,7 +78,7 @@ __device__ __forceinline__ void image_row(XImage<NBT>& im, int b, bool live, flo
             g[8 * seg + 2 * q + 1] = l;
         }
     } else {
-        const float s32 = s16 + __shfl_xor(s16, 4, kWave);
+        const float s32 = s16 + dpp_mov<0x141>(s16);
         const int q = lane >> 3;   // 32-group: segment q / 2, slots 2 (q % 2), +1; zeros at +4, +5
         if ((lane & 7) == 0) {
             const float wv = s32 * (1.0f / 32.0f);
@@ -149,7 +151,7 @@ __global__ void __launch_bounds__(256) residual_norm_image_kernel(float* __restr
     }
     if (live) {
         // the block sum over every thread (threads past the row hold 0)
-        for (int off = 32; off > 0; off >>= 1) sq += __shfl_xor(sq, off, kWave);
+        sq = wave_sum_dpp(sq);
         if (lane == 0) red[wave] = sq;
         __syncthreads();
         if (threadIdx.x == 0) {

@@ -10,10 +10,7 @@
 
 namespace rta {
 
-__device__ __forceinline__ float wave_sum(float v) {
-    for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, kWave);
-    return v;
-}
+__device__ __forceinline__ float wave_sum(float v) { return wave_sum_dpp(v); }
 
 // Sum over a block of NW waves through LDS red[NW]; every thread gets the total.
 template <int NW>

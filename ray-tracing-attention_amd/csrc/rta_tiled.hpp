@@ -159,7 +159,7 @@ struct XStage {
             float m = 0.0f;
 #pragma unroll
             for (int i = 0; i < 8; ++i) m = fmaxf(m, fabsf(v[k][i]));
-            for (int off = 16; off > 0; off >>= 1) m = fmaxf(m, __shfl_xor(m, off, kWave));   // within 32 lanes
+            m = group_max(m, 32);   // within 32 lanes
             const int e = operand_exponent(m);
             const float sc = ldexpf(1.0f, 14 - e);
             if (t == 0) {
@@ -179,8 +179,8 @@ struct XStage {
             *reinterpret_cast<h8_t*>(&sm.x[sbl][0][r][8 * t]) = h8_t{hi[0], hi[1], hi[2], hi[3], hi[4], hi[5], hi[6], hi[7]};
             *reinterpret_cast<h8_t*>(&sm.x[sbl][1][r][8 * t]) = h8_t{lo[0], lo[1], lo[2], lo[3], lo[4], lo[5], lo[6], lo[7]};
             _Float16* g = reinterpret_cast<_Float16*>(&sm.g[sbl][r][0]);   // 4 segments x 8
-            const float s16 = sum8 + __shfl_xor(sum8, 1, kWave);
-            const float s32 = s16 + __shfl_xor(s16, 2, kWave);
+            const float s16 = sum8 + dpp_mov<0xB1>(sum8);
+            const float s32 = s16 + dpp_mov<0x4E>(s16);
             if constexpr (FMT == RTA_Q6_K) {
                 if ((t & 1) == 0) {   // 16-group u = 8 hh + 2 q + sg -> segment 2 hh + sg, slot 2 q
                     const int u = t >> 1;
@@ -462,10 +462,7 @@ __global__ void __launch_bounds__(64 * kGemmWaves) gemm_tiled_kernel(
 #pragma unroll
                         for (int e = 0; e < 4; ++e) {
                             float m = tmax[bt][e];
-                            m = fmaxf(m, __shfl_xor(m, 1, kWave));
-                            m = fmaxf(m, __shfl_xor(m, 2, kWave));
-                            m = fmaxf(m, __shfl_xor(m, 4, kWave));
-                            m = fmaxf(m, __shfl_xor(m, 8, kWave));
+                            m = group_max(m, 16);
                             const int b = bt * 16 + 4 * s + e;
                             if (li == 0 && b < batch) pmax[(int64_t)b * ntile + (t == 0 ? t0 : t1)] = m;
                         }
