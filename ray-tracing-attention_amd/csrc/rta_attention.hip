@@ -2048,8 +2048,11 @@ __global__ void __launch_bounds__(256) full_middle_kernel(const MiddleArgs p) {
 // coordinates; every thread keeps 8 chunk records in flight.  One pass: each group
 // folds its records into a running (m, Z, U), rescaled when m grows, and the groups
 // are combined at the end (the same sums as max-then-accumulate, in another order).
-__global__ void __launch_bounds__(256) attn_merge_kernel(const AttnArgs a) {
-    constexpr int kGroups = 8, kAhead = 8;
+// GROUPS groups of 32 threads, kAhead records in flight per group: 16 (512 threads) when
+// a sequence's records can number in the hundreds (few sequences share the grid), else 8.
+template <int GROUPS>
+__global__ void __launch_bounds__(32 * GROUPS) attn_merge_kernel(const AttnArgs a) {
+    constexpr int kGroups = GROUPS, kAhead = 8;
     __shared__ float4 s_u[kGroups][kHd / 4];
     __shared__ float s_zp[kGroups], s_mp[kGroups];
     const int sh = blockIdx.x;
@@ -2662,7 +2665,8 @@ int decode_attention_gate_stride(const float* q, int nseq, int hq, int hkv, int 
     else if (fmt_k == RTA_Q6_K && fmt_v == RTA_Q4_K) e = launch_chunks<RTA_Q6_K, RTA_Q4_K>(G, a, lds, s);
     else e = launch_chunks<RTA_Q4_K, RTA_Q4_K>(G, a, lds, s);
     if (e != hipSuccess) return RTA_ERR_LAUNCH;
-    hipLaunchKernelGGL(attn_merge_kernel, dim3(nseq * hq), dim3(256), 0, s, a);
+    if (nseq <= 16) hipLaunchKernelGGL((attn_merge_kernel<16>), dim3(nseq * hq), dim3(512), 0, s, a);
+    else hipLaunchKernelGGL((attn_merge_kernel<8>), dim3(nseq * hq), dim3(256), 0, s, a);
     return hipGetLastError() == hipSuccess ? RTA_OK : RTA_ERR_LAUNCH;
 }
 
