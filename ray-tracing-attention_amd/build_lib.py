@@ -24,6 +24,10 @@ FLAGS = [
     "--offload-arch=gfx950", "-O3", "-std=c++17", "-fPIC", "-fgpu-rdc",
     # keep the compiler from forming v_pk_{add,mul,fma}_f32
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    # the first 16 dwords of every kernel's arguments arrive preloaded in SGPRs, so a
+    # kernel's first loads need not wait on a scalar load of its arguments (a kernel
+    # starts with cold caches; batch-32 decode step 4.24 -> 4.19 ms)
+    "-mllvm", "-amdgpu-kernarg-preload-count=16",
     "-Wall", "-Wno-unused-function",
 ]
 

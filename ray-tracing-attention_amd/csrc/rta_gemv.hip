@@ -627,8 +627,8 @@ int swiglu_image(int fmt, const float* part, int nslab, int width, int batch, vo
 template <int FMT, int NBT, int MODE>
 static void launch_packed(const MmaPlan& p, const uint8_t* w, const uint8_t* w2, int rows, int cols, const void* img,
                           int batch, float* y, float* part, const RowNorm& rn, hipStream_t s) {
-    hipLaunchKernelGGL((gemm_packed_kernel<FMT, NBT, MODE, kPkTpw, kPkWaves, kPkDepth>), dim3(p.grid),
-                       dim3(64 * kPkWaves), 0, s, w, w2, rows, cols, static_cast<const XImage<NBT>*>(img), batch, y,
+    hipLaunchKernelGGL((gemm_packed_kernel<FMT, NBT, MODE, kPkTpw, kPkWaves, kPkDepth>),
+                       dim3(p.wgs_per_slab, p.nslab), dim3(64 * kPkWaves), 0, s, w, w2, rows, cols, static_cast<const XImage<NBT>*>(img), batch, y,
                        part, p.sb_per_slab, p.wgs_per_slab, rn);
 }
 

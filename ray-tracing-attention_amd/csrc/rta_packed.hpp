@@ -228,11 +228,30 @@ __global__ void __launch_bounds__(64 * NWAVES) gemm_packed_kernel(
 
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int slab = blockIdx.x / wgs_per_slab, pos = blockIdx.x - slab * wgs_per_slab;
-    const int nslab = gridDim.x / wgs_per_slab;
+    const int slab = blockIdx.y, pos = blockIdx.x;   // grid (wgs_per_slab, slabs)
+    const int nslab = gridDim.y;
     const int nsbt = cols >> 8;
     const int sb0 = slab * sb_per_slab;
     const int nsb = min(sb_per_slab, nsbt - sb0);
+
+    // The slab's x images go to LDS first, by direct global -> LDS loads (lane l of a
+    // wave's instruction lands at the wave's LDS base + 16 l, so a wave moves 64
+    // consecutive 16-byte words per instruction without a register round trip); all of
+    // them are in flight at once, with DEPTH - 1 superblocks of weights issued behind
+    // them.  They are issued before the work split is worked out: a kernel starts with
+    // cold instruction and scalar caches, and the loads are the long pole.
+    constexpr int kThreads = 64 * NWAVES;
+    constexpr int kPer = (kCap * (int)(sizeof(Img) / 16) + kThreads - 1) / kThreads;
+    const int n16 = nsb * (int)(sizeof(Img) / 16);
+    const uint4* xsrc = reinterpret_cast<const uint4*>(xi + sb0);
+    uint4* xdst = reinterpret_cast<uint4*>(sx);
+    using lds_ptr = __attribute__((address_space(3))) void*;
+#pragma unroll
+    for (int k = 0; k < kPer; ++k) {
+        const int i0 = k * kThreads + wave * 64;   // the wave's first word (uniform)
+        if (i0 + lane < n16) __builtin_amdgcn_global_load_lds(xsrc + i0 + lane, (lds_ptr)(xdst + i0), 16, 0, 0);
+    }
+
     const int s = lane >> 4, li = lane & 15;
     const int total_rows = kDual ? 2 * rows : rows;
     const int ntile = (rows + 15) >> 4;
@@ -243,8 +262,10 @@ __global__ void __launch_bounds__(64 * NWAVES) gemm_packed_kernel(
     // cut into (unit, superblock) items, shared out to the waves in balanced contiguous
     // ranges (so no wave carries a whole extra unit).  A unit whose items span several
     // waves belongs to the wave holding its first item; the later ones hand it their
-    // partial sums through LDS after the loop.
-    const int wa = (int)((int64_t)pos * nunits / wgs_per_slab), wb = (int)((int64_t)(pos + 1) * nunits / wgs_per_slab);
+    // partial sums through LDS after the loop.  floor(p nunits / wgs) in 32 bits:
+    // p (q wgs + r) / wgs = p q + floor(p r / wgs), p r < wgs^2.
+    const int uq = nunits / wgs_per_slab, ur = nunits - uq * wgs_per_slab;
+    const int wa = pos * uq + pos * ur / wgs_per_slab, wb = (pos + 1) * uq + (pos + 1) * ur / wgs_per_slab;
     const int items = (wb - wa) * nsb;
     auto item0 = [&](int wv) { return wv * items / NWAVES; };
     const int ia = item0(wave), nit = item0(wave + 1) - ia;
@@ -271,22 +292,6 @@ __global__ void __launch_bounds__(64 * NWAVES) gemm_packed_kernel(
             }
         }
     };
-
-    // the slab's x images go to LDS by direct global -> LDS loads (lane l of a wave's
-    // instruction lands at the wave's LDS base + 16 l, so a wave moves 64 consecutive
-    // 16-byte words per instruction without a register round trip); all of them are in
-    // flight at once, with DEPTH - 1 superblocks of weights issued behind them
-    constexpr int kThreads = 64 * NWAVES;
-    constexpr int kPer = (kCap * (int)(sizeof(Img) / 16) + kThreads - 1) / kThreads;
-    const int n16 = nsb * (int)(sizeof(Img) / 16);
-    const uint4* xsrc = reinterpret_cast<const uint4*>(xi + sb0);
-    uint4* xdst = reinterpret_cast<uint4*>(sx);
-    using lds_ptr = __attribute__((address_space(3))) void*;
-#pragma unroll
-    for (int k = 0; k < kPer; ++k) {
-        const int i0 = k * kThreads + wave * 64;   // the wave's first word (uniform)
-        if (i0 + lane < n16) __builtin_amdgcn_global_load_lds(xsrc + i0 + lane, (lds_ptr)(xdst + i0), 16, 0, 0);
-    }
     Raw buf[DEPTH][TPW];
     if (nit > 0) {
 #pragma unroll
