@@ -436,8 +436,9 @@ static hipError_t run_mfma(int fmt, const Launch& l, void* ws, float* pmax, int*
 
 template <int FMT, int NBT, int MODE>
 static void launch_tiled(const MmaPlan& p, const Launch& l, float* part, float* pmax, hipStream_t s) {
-    hipLaunchKernelGGL((gemm_tiled_kernel<FMT, NBT, MODE>), dim3(p.grid), dim3(64 * kGemmWaves), 0, s, l.w, l.w2,
-                       l.rows, l.cols, l.x, l.batch, l.y, part, pmax, p.sb_per_slab, p.wgs_per_slab, l.rn);
+    hipLaunchKernelGGL((gemm_tiled_kernel<FMT, NBT, MODE>), dim3(p.wgs_per_slab, p.nslab), dim3(64 * kGemmWaves), 0,
+                       s, l.w, l.w2, l.rows, l.cols, l.x, l.batch, l.y, part, pmax, p.sb_per_slab, p.wgs_per_slab,
+                       l.rn);
 }
 
 // One batch tile (<= 32 rows) over packed weights: the tiled GEMM prepares x in LDS

@@ -222,18 +222,28 @@ __global__ void __launch_bounds__(64 * kGemmWaves) gemm_tiled_kernel(
 
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int slab = blockIdx.x / wgs_per_slab, pos = blockIdx.x - slab * wgs_per_slab;
-    const int nslab = gridDim.x / wgs_per_slab;
+    const int slab = blockIdx.y, pos = blockIdx.x;   // grid (wgs_per_slab, slabs)
+    const int nslab = gridDim.y;
     const int nsbt = cols >> 8;
     const int sb0 = slab * sb_per_slab;
     const int nsb = min(sb_per_slab, nsbt - sb0);
+
+    // x loads first (vector-memory loads complete in order, so the x slab is not held
+    // up behind the weights; and a kernel starts with cold instruction and scalar
+    // caches, so nothing is worked out ahead of them that they do not need), then
+    // DEPTH - 1 superblocks of weights, then the x prep.
+    XStage<FMT, NBT> xs;
+    xs.load(x, cols, batch, sb0, nsb, rn);
+
     const int s = lane >> 4, li = lane & 15;
     const int total_rows = MODE == kSwiglu ? 2 * rows : rows;
     const int ntile = (rows + 15) >> 4;
 
-    // ---- balanced contiguous tile range of this wave
+    // ---- balanced contiguous tile range of this wave: floor(g ntile / nw) in 32 bits,
+    // g (q nw + r) / nw = g q + floor(g r / nw) with g r < nw^2
     const int gw = pos * kGemmWaves + wave, nw = wgs_per_slab * kGemmWaves;
-    const int ta = (int)((int64_t)gw * ntile / nw), tb = (int)((int64_t)(gw + 1) * ntile / nw);
+    const int tq = ntile / nw, tr = ntile - tq * nw;
+    const int ta = gw * tq + gw * tr / nw, tb = (gw + 1) * tq + (gw + 1) * tr / nw;
     const int nunit = MODE == kSwiglu ? tb - ta : (tb - ta + 1) >> 1;
     const int nit = nunit * nsb;
 
@@ -259,10 +269,6 @@ __global__ void __launch_bounds__(64 * kGemmWaves) gemm_tiled_kernel(
         }
     };
 
-    // x loads first (vector-memory loads complete in order, so the x slab is not held
-    // up behind the weights), then DEPTH - 1 superblocks of weights, then the x prep.
-    XStage<FMT, NBT> xs;
-    xs.load(x, cols, batch, sb0, nsb, rn);
     constexpr int DEPTH = 2;   // one superblock loads while the current one multiplies
     Raw buf[DEPTH][2];
     if (nit > 0) {
