@@ -251,8 +251,18 @@ __global__ void __launch_bounds__(64 * NWAVES) gemm_packed_kernel(
         const int i0 = k * kThreads + wave * 64;   // the wave's first word (uniform)
         if (i0 + lane < n16) __builtin_amdgcn_global_load_lds(xsrc + i0 + lane, (lds_ptr)(xdst + i0), 16, 0, 0);
     }
-
     const int s = lane >> 4, li = lane & 15;
+    // the sums of squares of the batch rows this lane's results belong to (RMSNorm
+    // factor): loaded with the x slab, every row clamped into the batch (no branch that
+    // would wait for each load on the spot), used once the slab has landed
+    float4 rnp[NBT][4];
+    if (rn.part) {   // uniform
+#pragma unroll
+        for (int bt = 0; bt < NBT; ++bt)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) rnp[bt][e] = rn.part[min(bt * 16 + 4 * s + e, batch - 1)];
+    }
+
     const int total_rows = kDual ? 2 * rows : rows;
     const int ntile = (rows + 15) >> 4;
     constexpr int kTpu = kDual ? TPW / 2 : TPW;   // row tiles per unit
@@ -305,10 +315,7 @@ __global__ void __launch_bounds__(64 * NWAVES) gemm_packed_kernel(
 #pragma unroll
     for (int bt = 0; bt < NBT; ++bt)
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-            const int bb = bt * 16 + 4 * s + e;
-            rowf[bt][e] = (rn.part && bb < batch) ? row_norm_factor(rn, rn.part[bb]) : 1.0f;
-        }
+        for (int e = 0; e < 4; ++e) rowf[bt][e] = rn.part ? row_norm_factor(rn, rnp[bt][e]) : 1.0f;
 
     f4_t acc[TPW][NBT];
 #pragma unroll
