@@ -252,6 +252,7 @@ __global__ void __launch_bounds__(64 * NWAVES) gemm_packed_kernel(
         if (i0 + lane < n16) __builtin_amdgcn_global_load_lds(xsrc + i0 + lane, (lds_ptr)(xdst + i0), 16, 0, 0);
     }
     const int s = lane >> 4, li = lane & 15;
+    const Q4kSegment seg(s);
     // the sums of squares of the batch rows this lane's results belong to (RMSNorm
     // factor): loaded with the x slab, every row clamped into the batch (no branch that
     // would wait for each load on the spot), used once the slab has landed
@@ -359,12 +360,10 @@ __global__ void __launch_bounds__(64 * NWAVES) gemm_packed_kernel(
                 dC[t] = half_lo(h.x) * 16384.0f;     // codes carry 2^-14
                 dM[t] = half_hi(h.x) * 32.0f;        // group sums are staged / 32
                 uint32_t sc0, m0, sc1, m1;
-                q4k_scale_min_lane(h.y, h.z, h.w, 2 * s, sc0, m0);
-                q4k_scale_min_lane(h.y, h.z, h.w, 2 * s + 1, sc1, m1);
-                slo[t] = h2dup((float)sc0 * 1024.0f);
-                shi[t] = h2dup((float)sc1 * 64.0f);
-                const _Float16 fm0 = (_Float16)(float)m0, fm1 = (_Float16)(float)m1, z = (_Float16)0.0f;
-                bm[t] = h8_t{fm0, fm0, fm1, fm1, z, z, z, z};
+                q4k_tile_scale_min(h, seg, sc0, sc1, m0, m1);
+                slo[t] = h2dup_scaled(sc0, 1024.0f);
+                shi[t] = h2dup_scaled(sc1, 64.0f);
+                bm[t] = __builtin_bit_cast(h8_t, uint4{h2dup_scaled(m0, 1.0f), h2dup_scaled(m1, 1.0f), 0u, 0u});
             }
             h8_t ah[NBT], al[NBT];
             xload(64 * s, ah, al);

@@ -9,7 +9,12 @@
 // whole contiguous lines that no other instruction needs.
 //
 //   Q4_K tile, 2304 bytes (16 x 144):
-//     [0, 256)      row r's 16-byte block header (d, dmin, 12 scale bytes) at 16 r
+//     [0, 256)      row r's 16-byte block header at 16 r: d and dmin as in the GGUF
+//                   block, then its eight 6-bit scales and minima regrouped per lane
+//                   segment: bits [24 s, 24 s + 24) of the 96-bit little-endian field in
+//                   bytes 4..15 hold sc(2 s), sc(2 s + 1), m(2 s), m(2 s + 1) at bit
+//                   offsets 0, 6, 12, 18 (the groups lane segment s multiplies; one
+//                   funnel shift and four field extracts decode them)
 //     [256, 1280)   lane l = 16 s + r: bytes [32 s, 32 s + 16) of row r's 128 quant bytes
 //     [1280, 2304)  lane l: bytes [32 s + 16, 32 s + 32)
 //   Q6_K tile, 3360 bytes (16 x 210):
@@ -50,9 +55,36 @@ struct TileFmt<RTA_Q4_K> {
         r.q0 = *reinterpret_cast<const uint4*>(c + 256 + 16 * lane);
         r.q1 = *reinterpret_cast<const uint4*>(c + 1280 + 16 * lane);
     }
-    // byte offset, inside row r's GGUF block, of tile byte o (o even)
+    // Bytes 4..15 of a tile row header from the GGUF block's 12 scale bytes q (the
+    // get_scale_min_k4 decoding of resident_quant.glsl:10-19): the 96-bit field of
+    // the layout above, as three little-endian words.
+    __host__ __device__ static inline void scale_field(const uint8_t* q, uint32_t f[3]) {
+        uint64_t lo = 0, hi = 0;   // bits [0, 64), [64, 96)
+        auto put = [](uint64_t& l, uint64_t& h, uint32_t v, int b) {   // 6-bit v at bit b
+            if (b >= 64) {
+                h |= (uint64_t)v << (b - 64);
+            } else {
+                l |= (uint64_t)v << b;
+                if (b > 58) h |= (uint64_t)v >> (64 - b);   // straddles bit 64
+            }
+        };
+        for (int g = 0; g < 8; ++g) {
+            const int j = g & 3;
+            const uint32_t sc = g < 4 ? (q[j] & 63u) : ((q[j + 8] & 15u) | ((q[j] >> 6) << 4));
+            const uint32_t m = g < 4 ? (q[j + 4] & 63u) : ((q[j + 8] >> 4) | ((q[j + 4] >> 6) << 4));
+            const int s = g >> 1, k = g & 1;
+            const int bs = 24 * s + 6 * k, bm = bs + 12;   // bit offsets of sc(g), m(g)
+            put(lo, hi, sc, bs);
+            put(lo, hi, m, bm);
+        }
+        f[0] = (uint32_t)lo;
+        f[1] = (uint32_t)(lo >> 32);
+        f[2] = (uint32_t)hi;
+    }
+    // byte offset, inside row r's GGUF block, of tile byte o (o even), or -1 for the
+    // regrouped scale bytes (header bytes 4..15, see scale_field)
     __host__ __device__ static inline int source(int o, int& r) {
-        if (o < 256) { r = o >> 4; return o & 15; }
+        if (o < 256) { r = o >> 4; return (o & 15) < 4 ? (o & 15) : -1; }
         const int k = o < 1280 ? 0 : 1, p = o - (k ? 1280 : 256), l = p >> 4;
         r = l & 15;
         return 16 + 32 * (l >> 4) + 16 * k + (p & 15);
@@ -99,8 +131,19 @@ __global__ void __launch_bounds__(256) pack_kernel(const uint8_t* __restrict__ s
     const int64_t row = tile * 16 + r;
     uint16_t v = 0;
     if (row < rows) {
-        const uint8_t* p = src + m.source_row(row) * (int64_t)nsb * F::kBlock + (int64_t)sb * F::kBlock + off;
-        v = (uint16_t)(p[0] | (p[1] << 8));
+        const uint8_t* blk = src + m.source_row(row) * (int64_t)nsb * F::kBlock + (int64_t)sb * F::kBlock;
+        if constexpr (FMT == RTA_Q4_K) {
+            if (off < 0) {   // regrouped scale bytes: half-word (within - 4) / 2 of the field
+                uint32_t f[3];
+                F::scale_field(blk + 4, f);
+                const int h = (within & 15) - 4;   // 0, 2, .., 10
+                v = (uint16_t)(f[h >> 2] >> (8 * (h & 3)));
+            } else {
+                v = (uint16_t)(blk[off] | (blk[off + 1] << 8));
+            }
+        } else {
+            v = (uint16_t)(blk[off] | (blk[off + 1] << 8));
+        }
     }
     *reinterpret_cast<uint16_t*>(dst + o) = v;
 }
@@ -108,6 +151,34 @@ __global__ void __launch_bounds__(256) pack_kernel(const uint8_t* __restrict__ s
 
 __device__ __forceinline__ uint32_t word_of(const uint4& v, int i) {
     return i == 0 ? v.x : i == 1 ? v.y : i == 2 ? v.z : v.w;
+}
+
+// Scales and minima of groups 2 s and 2 s + 1 from a packed Q4_K tile row header h (the
+// regrouped field of TileFmt<RTA_Q4_K>): the words holding segment s's 24 bits are
+// picked with the lane's masks (bit selects: an indexed pick among the header's words
+// would go through memory), one funnel shift brings the bits down, four field extracts
+// split them.
+struct Q4kSegment {
+    uint32_t m01, m2, shift;   // all-ones for segments 0-1, for segment 2; 24 s mod 32
+    __device__ explicit Q4kSegment(int s)
+        : m01(s < 2 ? ~0u : 0u), m2(s == 2 ? ~0u : 0u), shift((uint32_t)(24 * s) & 31u) {}
+};
+__device__ __forceinline__ void q4k_tile_scale_min(const uint4& h, const Q4kSegment& g, uint32_t& sc0, uint32_t& sc1,
+                                                   uint32_t& m0, uint32_t& m1) {
+    const uint32_t w23 = (h.z & g.m2) | (h.w & ~g.m2);      // segment 2: z, segment 3: w
+    const uint32_t lo = (h.y & g.m01) | (w23 & ~g.m01);
+    const uint32_t hi = (h.z & g.m01) | (h.w & ~g.m01);
+    const uint32_t f = __builtin_amdgcn_alignbit(hi, lo, g.shift);
+    sc0 = f & 63u;
+    sc1 = (f >> 6) & 63u;
+    m0 = (f >> 12) & 63u;
+    m1 = (f >> 18) & 63u;
+}
+
+// (f16(v), f16(v)) for an integer v < 2^11 times a power of two c (exact in binary16)
+__device__ __forceinline__ uint32_t h2dup_scaled(uint32_t v, float c) {
+    const float x = (float)v * c;
+    return __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(x, x));
 }
 
 // Prepares x rows [0, 16 NBT) over superblocks [sb0, sb0 + nsb) straight into LDS,
@@ -236,6 +307,7 @@ __global__ void __launch_bounds__(64 * kGemmWaves) gemm_tiled_kernel(
     xs.load(x, cols, batch, sb0, nsb, rn);
 
     const int s = lane >> 4, li = lane & 15;
+    const Q4kSegment seg(s);
     const int total_rows = MODE == kSwiglu ? 2 * rows : rows;
     const int ntile = (rows + 15) >> 4;
 
@@ -326,12 +398,10 @@ __global__ void __launch_bounds__(64 * kGemmWaves) gemm_tiled_kernel(
                 dC[t] = half_lo(h.x) * 16384.0f;     // codes carry 2^-14
                 dM[t] = half_hi(h.x) * 32.0f;        // group sums are staged / 32
                 uint32_t sc0, m0, sc1, m1;
-                q4k_scale_min_lane(h.y, h.z, h.w, 2 * s, sc0, m0);
-                q4k_scale_min_lane(h.y, h.z, h.w, 2 * s + 1, sc1, m1);
-                slo[t] = h2dup((float)sc0 * 1024.0f);
-                shi[t] = h2dup((float)sc1 * 64.0f);
-                const _Float16 fm0 = (_Float16)(float)m0, fm1 = (_Float16)(float)m1, z = (_Float16)0.0f;
-                bm[t] = h8_t{fm0, fm0, fm1, fm1, z, z, z, z};
+                q4k_tile_scale_min(h, seg, sc0, sc1, m0, m1);
+                slo[t] = h2dup_scaled(sc0, 1024.0f);
+                shi[t] = h2dup_scaled(sc1, 64.0f);
+                bm[t] = __builtin_bit_cast(h8_t, uint4{h2dup_scaled(m0, 1.0f), h2dup_scaled(m1, 1.0f), 0u, 0u});
             }
             h8_t ah[NBT], al[NBT];
             xload(64 * s, ah, al);

@@ -24,6 +24,27 @@ def to_dev(torch, a, dev):
     return torch.from_numpy(np.ascontiguousarray(a)).to(dev)
 
 
+def scale_fields(q):
+    """Bytes 4..15 of a packed Q4_K row header from the GGUF block's 12 scale bytes
+    (q [..., 12]): the 6-bit scales and minima decoded as resident_quant.glsl:10-19 does
+    and regrouped per lane segment s at bits 24 s + (0, 6, 12, 18) of a 96-bit field."""
+    q = q.astype(np.uint64)
+    field = np.zeros(q.shape[:-1], dtype=object)
+    for g in range(8):
+        j = g & 3
+        if g < 4:
+            sc, m = q[..., j] & 63, q[..., j + 4] & 63
+        else:
+            sc = (q[..., j + 8] & 15) | ((q[..., j] >> 6) << 4)
+            m = (q[..., j + 8] >> 4) | ((q[..., j + 4] >> 6) << 4)
+        s, k = g >> 1, g & 1
+        field = field + (sc.astype(object) << (24 * s + 6 * k)) + (m.astype(object) << (24 * s + 12 + 6 * k))
+    out = np.zeros(q.shape, np.uint8)
+    for b in range(12):
+        out[..., b] = np.vectorize(lambda f: (f >> (8 * b)) & 255, otypes=[np.uint8])(field)
+    return out
+
+
 def np_pack(fmt, w, rows, cols):
     """The tile layout, built field by field from the GGUF blocks (debugging aid;
     the parity tests below pin the packed path against the oracle)."""
@@ -33,7 +54,9 @@ def np_pack(fmt, w, rows, cols):
     g[:rows] = np.asarray(w, np.uint8).reshape(rows, nsb, blk)
     g = g.reshape(nt, 16, nsb, blk).transpose(0, 2, 1, 3)           # [tile][sb][row][block]
     if fmt == orc.Q4_K:
-        hdr = g[..., :16].reshape(nt, nsb, 256)
+        hdr = g[..., :16].copy()
+        hdr[..., 4:16] = scale_fields(g[..., 4:16])
+        hdr = hdr.reshape(nt, nsb, 256)
         qs = g[..., 16:].reshape(nt, nsb, 16, 4, 2, 16)               # [..][row][s][k][16]
         lanes = qs.transpose(0, 1, 4, 3, 2, 5).reshape(nt, nsb, 2048)  # [k][s][row][16]
         out = np.concatenate([hdr, lanes], axis=2)
