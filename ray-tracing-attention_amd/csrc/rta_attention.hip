@@ -1015,6 +1015,13 @@ __global__ void __launch_bounds__(64 * NWV, 2) attn_chunk_mma_kernel(const AttnA
         int S_cur = 0;
         for (int64_t tile = x - s_first; tile < seg_end - s_first; ++tile) {
             const bool first_tile = tile == x - s_first;
+            // the waves of the two workgroups on one compute unit share its SIMDs, whose
+            // arbiter issues for the older wave first; they take turns at the higher
+            // priority, tile by tile, so that neither runs its last tiles alone
+            if (((int)tile ^ (b >= half ? 1 : 0)) & 1)
+                __builtin_amdgcn_s_setprio(1);
+            else
+                __builtin_amdgcn_s_setprio(0);
             const int n = (int)(n_vis - tile * kTile < kTile ? n_vis - tile * kTile : kTile);
             // slot of the lane's position; past the tile's end the tile's last position
             // (its lines are read anyway), out of range slot 0

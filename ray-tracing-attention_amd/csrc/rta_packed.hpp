@@ -511,6 +511,7 @@ __global__ void __launch_bounds__(64 * NWAVES) gemm_packed_kernel(
             const int it = it0 + d;
             load_next(buf[(d + DEPTH - 1) % DEPTH]);
             if (it < nit) {
+                take_turns(wave, it);
                 compute(csb, buf[d]);
                 if (csb == nsb - 1) {
                     if (head_shared && cu == head) {

@@ -158,6 +158,17 @@ __device__ __forceinline__ uint32_t word_of(const uint4& v, int i) {
 // picked with the lane's masks (bit selects: an indexed pick among the header's words
 // would go through memory), one funnel shift brings the bits down, four field extracts
 // split them.
+// Waves w and w + 4 of an 8-wave workgroup share a SIMD, whose arbiter issues for the
+// older wave first: left to it, the older wave finishes its items ~3 us before the
+// younger one, which then runs alone on the SIMD.  The two take turns at the higher
+// issue priority, item by item (it: the wave's item index), and finish together.
+__device__ __forceinline__ void take_turns(int wave, int it) {
+    if (((wave >> 2) ^ it) & 1)
+        __builtin_amdgcn_s_setprio(1);
+    else
+        __builtin_amdgcn_s_setprio(0);
+}
+
 struct Q4kSegment {
     uint32_t m01, m2, shift;   // all-ones for segments 0-1, for segment 2; 24 s mod 32
     __device__ explicit Q4kSegment(int s)
@@ -558,6 +569,7 @@ __global__ void __launch_bounds__(64 * kGemmWaves) gemm_tiled_kernel(
             const int it = it0 + d;
             load_next(buf[(d + DEPTH - 1) % DEPTH]);
             if (it < nit) {
+                take_turns(wave, it);
                 compute(csb, buf[d]);
                 if (csb == nsb - 1) finish(cu);
                 if (++csb == nsb) {
