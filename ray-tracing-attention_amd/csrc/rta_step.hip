@@ -11,6 +11,46 @@
 namespace rta {
 
 __device__ __forceinline__ float wave_sum(float v) { return wave_sum_dpp(v); }
+// Sum over the 32 lanes of each half of a wave, every lane getting its half's sum: DPP
+// steps inside each 16-lane row, then the row swap (lane ^ 16).
+__device__ __forceinline__ float half_sum_dpp(float v) {
+    v += dpp_mov<0xB1>(v);
+    v += dpp_mov<0x4E>(v);
+    v += dpp_mov<0x141>(v);
+    v += dpp_mov<0x140>(v);
+    return add_xor16(v);
+}
+// The recurrent state's words held by one lane (float2 or float4 of one value row).
+__device__ __forceinline__ float dot(float2 a, float2 b) { return a.x * b.x + a.y * b.y; }
+__device__ __forceinline__ float dot(float4 a, float4 b) { return (a.x * b.x + a.y * b.y) + (a.z * b.z + a.w * b.w); }
+__device__ __forceinline__ void scale_by(float2& s, float c) {
+    s.x *= c;
+    s.y *= c;
+}
+__device__ __forceinline__ void scale_by(float4& s, float c) {
+    s.x *= c;
+    s.y *= c;
+    s.z *= c;
+    s.w *= c;
+}
+__device__ __forceinline__ void axpy(float2& s, float f, float2 k) {   // s += f k
+    s.x += f * k.x;
+    s.y += f * k.y;
+}
+__device__ __forceinline__ void axpy(float4& s, float f, float4 k) {
+    s.x += f * k.x;
+    s.y += f * k.y;
+    s.z += f * k.z;
+    s.w += f * k.w;
+}
+__device__ __forceinline__ void store_nt(float2* p, float2 v) {
+    using f2v = float __attribute__((ext_vector_type(2)));
+    __builtin_nontemporal_store(f2v{v.x, v.y}, reinterpret_cast<f2v*>(p));
+}
+__device__ __forceinline__ void store_nt(float4* p, float4 v) {
+    using f4v = float __attribute__((ext_vector_type(4)));
+    __builtin_nontemporal_store(f4v{v.x, v.y, v.z, v.w}, reinterpret_cast<f4v*>(p));
+}
 
 // Sum over a block of NW waves through LDS red[NW]; every thread gets the total.
 template <int NW>
@@ -366,7 +406,7 @@ __global__ void __launch_bounds__(64 * NW) recurrent_mix_kernel(
     const float* __restrict__ dt_bias, float* __restrict__ state, const float* __restrict__ norm_w, int heads,
     float eps, float* __restrict__ out, int out_stride) {
     constexpr int hd = 128, kRows = hd / NW;   // state rows per wave
-    __shared__ float qkv_s[3][hd];
+    __shared__ __align__(16) float qkv_s[3][hd];
     __shared__ float z_s[hd];
     __shared__ float gates_s[2];
     __shared__ float o_s[hd];
@@ -416,14 +456,21 @@ __global__ void __launch_bounds__(64 * NW) recurrent_mix_kernel(
         }
     }
     asm volatile("" ::: "memory");   // the state loads stay behind the loads above
-    float2* S = reinterpret_cast<float2*>(state + ((int64_t)b * heads + h) * hd * hd) + wave * kRows * (hd / 2) + lane;
-    float2 s[kRows];
+    // The wave's value rows: lane l holds keys 2 l, 2 l + 1 of every row (float2 words),
+    // or, with no K slabs to add (NS = 1: registers to spare within the 64 VGPRs of two
+    // blocks per CU), keys 4 (l % 32) .. + 3 of the rows 2 j + l / 32 (float4 words: one
+    // load covers two rows, and the row sums take half-wave reductions; batch-1 step
+    // 1.929 -> 1.899 ms, while at 4 K slabs the wider words cost 67 VGPRs and half the
+    // blocks per CU).  Word j of the lane is value row rbase + j rstep.
+    constexpr bool kWide = NS == 1;
+    using Word = typename std::conditional<kWide, float4, float2>::type;
+    constexpr int kWords = kWide ? kRows / 2 : kRows, rstep = kWide ? 2 : 1, kw = kWide ? 4 : 2;
+    const int half = kWide ? lane >> 5 : 0, cl = kWide ? lane & 31 : lane;
+    const int rbase = wave * kRows + half;
+    Word* S = reinterpret_cast<Word*>(state + ((int64_t)b * heads + h) * hd * hd + (int64_t)rbase * hd) + cl;
+    Word s[kWords];
 #pragma unroll
-    for (int i = 0; i < kRows; ++i) s[i] = S[i * (hd / 2)];
-    // the updated state is stored non-temporally: it is read again only by the next
-    // step, after every other layer's weights have passed through the caches
-    using f2v = float __attribute__((ext_vector_type(2)));
-    f2v* Sv = reinterpret_cast<f2v*>(S);
+    for (int j = 0; j < kWords; ++j) s[j] = S[j * (hd / 2)];   // (hd / 2 words: rstep rows)
 
     float y[3] = {0.0f, 0.0f, 0.0f};
     if (conv) {
@@ -472,33 +519,33 @@ __global__ void __launch_bounds__(64 * NW) recurrent_mix_kernel(
     }
     __syncthreads();
 
-    // op 21: NW waves x 128 / NW value rows; lane l holds keys 2l, 2l + 1
-    const float2 q = *reinterpret_cast<const float2*>(&qkv_s[0][2 * lane]);
-    const float2 k = *reinterpret_cast<const float2*>(&qkv_s[1][2 * lane]);
-    const float* vv = &qkv_s[2][wave * kRows];
+    // op 21 over the lane's words (the updated state is stored non-temporally: it is
+    // read again only by the next step, after every other layer's weights have passed
+    // through the caches)
+    const Word q = *reinterpret_cast<const Word*>(&qkv_s[0][kw * cl]);
+    const Word k = *reinterpret_cast<const Word*>(&qkv_s[1][kw * cl]);
+    const float* vv = &qkv_s[2][rbase];
     const float dc = gates_s[0], bt = gates_s[1];
     const float scale = 1.0f / sqrtf((float)hd);
-    float u[kRows];
+    auto row_sum = [](float v) { return kWide ? half_sum_dpp(v) : wave_sum_dpp(v); };
+    float u[kWords];
 #pragma unroll
-    for (int i = 0; i < kRows; ++i) {
-        s[i].x *= dc;
-        s[i].y *= dc;
-        u[i] = wave_sum_dpp(s[i].x * k.x + s[i].y * k.y);
+    for (int j = 0; j < kWords; ++j) {
+        scale_by(s[j], dc);
+        u[j] = row_sum(dot(s[j], k));
     }
-    float o[kRows];
+    float o[kWords];
 #pragma unroll
-    for (int i = 0; i < kRows; ++i) {
-        const float delta = bt * (vv[i] - u[i]);
-        s[i].x += delta * k.x;
-        s[i].y += delta * k.y;
-        __builtin_nontemporal_store(f2v{s[i].x, s[i].y}, Sv + i * (hd / 2));
-        o[i] = s[i].x * q.x + s[i].y * q.y;
+    for (int j = 0; j < kWords; ++j) {
+        axpy(s[j], bt * (vv[j * rstep] - u[j]), k);
+        store_nt(S + j * (hd / 2), s[j]);
+        o[j] = dot(s[j], q);
     }
 #pragma unroll
-    for (int i = 0; i < kRows; ++i) o[i] = wave_sum_dpp(o[i]);
-    if (lane == 0) {
+    for (int j = 0; j < kWords; ++j) o[j] = row_sum(o[j]);
+    if (cl == 0) {
 #pragma unroll
-        for (int i = 0; i < kRows; ++i) o_s[wave * kRows + i] = o[i] * scale;
+        for (int j = 0; j < kWords; ++j) o_s[rbase + j * rstep] = o[j] * scale;
     }
     __syncthreads();
     // op 15: gated RMSNorm of o
